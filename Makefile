@@ -1,0 +1,67 @@
+# Build of the MI355X (gfx950) tinytorch backend.
+#
+#   make lib      -> build/libtinytorch.so          (C ABI: tensor.h, autograd.h, tt_hip.h)
+#   make pybind   -> build/tinytorch_pybind<EXT>    (Node API, links libtinytorch.so)
+#   make oracle   -> oracle/build/liborc.so          (CPU restatement, test-only)
+#   make ref      -> oracle/_ref/libtinytorch_ref.so (reference sources, when present)
+# Target names and artefact names follow the reference Makefile:11-22.
+ROCM    ?= /opt/rocm
+HIPCC   ?= $(ROCM)/bin/hipcc
+CC      ?= gcc
+CXX     ?= g++
+ARCH    ?= gfx950
+BUILD   := build
+CSRC    := tinytorch_amd/csrc
+
+# -packed-fp32-ops off: no v_pk_*_f32 are generated ("build flags")
+HIPFLAGS := --offload-arch=$(ARCH) -O3 -fPIC -std=c++17 -Iinclude -I$(CSRC) \
+            -Xclang -target-feature -Xclang -packed-fp32-ops -Wno-unused-command-line-argument
+CFLAGS_HOST := -O2 -fPIC -std=c11 -Wall -Wextra -D__HIP_PLATFORM_AMD__ -I$(ROCM)/include \
+               -Iinclude -I$(CSRC)
+
+HOST_SRCS := $(CSRC)/runtime.c $(CSRC)/tensor.c $(CSRC)/ops.c $(CSRC)/autograd.c
+HIP_SRCS  := $(CSRC)/gemm.hip $(CSRC)/elementwise.hip $(CSRC)/spatial.hip
+HDRS      := $(wildcard include/*.h) $(wildcard $(CSRC)/*.h)
+HOST_OBJS := $(patsubst $(CSRC)/%.c,$(BUILD)/obj/%.o,$(HOST_SRCS))
+HIP_OBJS  := $(patsubst $(CSRC)/%.hip,$(BUILD)/obj/%.o,$(HIP_SRCS))
+
+PYBIND_INC := $(shell python3 -m pybind11 --includes 2>/dev/null)
+EXT_SUFFIX := $(shell python3-config --extension-suffix 2>/dev/null || echo ".so")
+
+all: lib pybind
+
+$(BUILD)/obj/%.o: $(CSRC)/%.c $(HDRS) | $(BUILD)/obj
+	$(CC) $(CFLAGS_HOST) -c $< -o $@
+
+# the GEMM may fuse multiply-adds (it is tolerance-checked); the bandwidth
+# kernels are compiled without contraction so their sums round like the
+# reference's separate multiply and add
+$(BUILD)/obj/gemm.o: $(CSRC)/gemm.hip $(HDRS) | $(BUILD)/obj
+	$(HIPCC) $(HIPFLAGS) -c $< -o $@
+
+$(BUILD)/obj/%.o: $(CSRC)/%.hip $(HDRS) | $(BUILD)/obj
+	$(HIPCC) $(HIPFLAGS) -ffp-contract=off -c $< -o $@
+
+$(BUILD)/libtinytorch.so: $(HOST_OBJS) $(HIP_OBJS)
+	$(HIPCC) --offload-arch=$(ARCH) -shared -fPIC -o $@ $^ -Wl,-Bsymbolic -Wl,-soname,libtinytorch.so
+
+$(BUILD)/tinytorch_pybind$(EXT_SUFFIX): $(CSRC)/bindings.cpp $(BUILD)/libtinytorch.so $(HDRS)
+	$(CXX) -O2 -fPIC -shared -std=c++17 $(PYBIND_INC) -Iinclude -o $@ $< \
+	    -L$(BUILD) -ltinytorch -Wl,-rpath,'$$ORIGIN'
+
+$(BUILD)/obj:
+	mkdir -p $@
+
+lib: $(BUILD)/libtinytorch.so
+pybind: $(BUILD)/tinytorch_pybind$(EXT_SUFFIX)
+
+oracle:
+	$(MAKE) -C oracle
+
+ref:
+	$(MAKE) -C oracle ref
+
+clean:
+	rm -rf $(BUILD)
+
+.PHONY: all lib pybind oracle ref clean

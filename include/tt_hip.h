@@ -1,0 +1,107 @@
+/* Device-level C ABI of the MI355X backend: runtime control and the HIP
+ * kernels behind tensor.h / autograd.h, callable on raw device pointers.
+ *
+ * All pointers named d* / the kernel operands are DEVICE pointers obtained
+ * from tth_malloc (or any hipMalloc'd memory of the current device); sizes
+ * are element counts unless stated.  Every kernel is enqueued on the
+ * library's single HIP stream (tth_stream) and returns 0 on a successful
+ * launch, negative on bad arguments or launch failure.  Completion is
+ * observed with tth_sync / tth_event_* or any copy back to the host.
+ *
+ * Each kernel cites the reference function it replaces. */
+#ifndef TINYTORCH_TT_HIP_H
+#define TINYTORCH_TT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- runtime ---- */
+int    tth_available(void);            /* 1 when a GPU is usable */
+int    tth_device_name(char *buf, int len);
+void  *tth_stream(void);               /* hipStream_t every kernel runs on */
+int    tth_sync(void);                 /* wait for the stream; 0 ok */
+int    tth_last_error(void);           /* last runtime error code (0 none) */
+void  *tth_malloc(size_t bytes);       /* cached device allocation; NULL on OOM */
+void   tth_free(void *d);
+void   tth_release_cache(void);
+size_t tth_bytes_in_use(void);
+int    tth_h2d(void *d, const void *h, size_t bytes);
+int    tth_d2h(void *h, const void *d, size_t bytes);
+/* device payload of a tensor (uploads a host-modified mirror first) */
+struct Tensor;
+float *tt_dev(struct Tensor *t);
+/* stream-ordered timing: events recorded on tth_stream */
+void  *tth_event_create(void);
+int    tth_event_record(void *ev);
+float  tth_event_elapsed_ms(void *start, void *stop);  /* syncs on stop */
+void   tth_event_destroy(void *ev);
+
+/* ---- GEMM (gemm.hip) ----
+ * C[M x N] = opA[M x K] * opB[K x N], fp32 in / fp32 MFMA accumulate / fp32 out.
+ *   transA = 0: A is M x K row-major, element (m,k) at A[m*lda + k]
+ *   transA = 1: A is K x M row-major, element (m,k) at A[k*lda + m]
+ *   transB = 0: B is K x N row-major, element (k,n) at B[k*ldb + n]
+ *   transB = 1: B is N x K row-major, element (k,n) at B[n*ldb + k]
+ * (0,0) replaces tt_sgemm_rowmajor   reference src/gemm.c:569-641
+ * (0,1) replaces matmul_nt (dA=dC*B^T) reference src/autograd.c:66-84
+ * (1,0) replaces matmul_tn (dB=A^T*dC) reference src/autograd.c:87-103 */
+int tt_k_gemm(int M, int N, int K,
+              const float *A, int lda, int transA,
+              const float *B, int ldb, int transB,
+              float *C, int ldc);
+
+/* Convolution GEMMs over the im2col matrix col[(c,kh,kw)][(n,ho,wo)]
+ * (Kc = C*HH*WW rows, Ncol = N*Ho*Wo columns, HW = Ho*Wo):
+ *   conv_fwd : out[n][f][hw] = sum_c W[f][c] col[c][p] + bias[f] (bias may be NULL)
+ *              reference src/ops_spatial.c:96-121 (GEMM + bias + NCHW permute)
+ *   conv_dw  : dW[f][c] = sum_p g[n][f][hw] col[c][p]
+ *              reference src/autograd.c:487-507 (g_perm + sgemm_A_Bt_local)
+ *   conv_dcol: dcol[c][p] = sum_f W[f][c] g[n][f][hw]
+ *              reference src/autograd.c:515-539 (W^T copy + g_perm + sgemm) */
+int tt_k_conv_fwd(int F, int Kc, long Ncol, int HW,
+                  const float *W, const float *col, const float *bias, float *out);
+int tt_k_conv_dw(int F, int Kc, long Ncol, int HW,
+                 const float *g, const float *col, float *dW);
+int tt_k_conv_dcol(int F, int Kc, long Ncol, int HW,
+                   const float *W, const float *g, float *dcol);
+
+/* ---- bandwidth kernels (elementwise.hip / spatial.hip) ---- */
+int tt_k_fill(float *x, long n, float v);
+int tt_k_copy(float *dst, const float *src, long n);
+int tt_k_add_inplace(float *dst, const float *src, long n);          /* accum: src/autograd.c:52-63 */
+int tt_k_relu_fwd(const float *x, float *y, long n);                  /* src/ops.c:104-106 */
+int tt_k_relu_bwd(const float *x, const float *g, float *dx, long n); /* src/autograd.c:318-327 */
+int tt_k_binary(const float *a, const float *b, float *y, long n, int op); /* 0 add, 1 mul: src/ops.c:26-52 */
+int tt_k_scalar(const float *a, float *y, long n, float s, int op);        /* 0 add, 1 mul: src/ops.c:71-78 */
+int tt_k_softmax_fwd(const float *x, float *y, long rows, int cols);       /* src/ops.c:108-145 */
+int tt_k_softmax_bwd(const float *s, const float *g, float *dx, long rows, int cols); /* src/autograd.c:329-346 */
+/* probs = softmax(logits); loss_rows[r] = -log(max(probs[r][y_r], 1e-12));
+ * seed = (probs - onehot(y)) * scale.  Harness math of
+ * reference tests/gate_cifar_cnn.py:175-181 on the device. */
+int tt_k_softmax_ce(const float *logits, const int32_t *labels, float *probs,
+                    float *loss_rows, float *seed, long rows, int cols, float scale);
+int tt_k_padones_fwd(const float *x, float *y, long M, long K);      /* src/autograd.c:195-212 */
+int tt_k_padones_bwd(const float *g, float *dx, long M, long K);     /* src/autograd.c:348-359 */
+int tt_k_im2col(const float *x, float *col, int N, int C, int H, int W,
+                int HH, int WW, int sh, int sw, int ph, int pw, int Ho, int Wo);  /* src/ops_spatial.c:37-69 */
+int tt_k_col2im(const float *col, float *x, int N, int C, int H, int W,
+                int HH, int WW, int sh, int sw, int ph, int pw, int Ho, int Wo);  /* src/autograd.c:406-434 */
+int tt_k_bias_grad(const float *g, float *db, int N, int F, int HW);              /* src/autograd.c:467-482 */
+int tt_k_maxpool_fwd(const float *x, float *y, int N, int C, int H, int W,
+                     int ph, int pw, int sh, int sw, int Ho, int Wo);             /* src/ops_spatial.c:129-164 */
+int tt_k_maxpool_bwd(const float *x, const float *g, float *dx, int N, int C, int H, int W,
+                     int ph, int pw, int sh, int sw, int Ho, int Wo);             /* src/autograd.c:555-594 */
+int tt_k_avgpool_fwd(const float *x, float *y, int N, int C, int H, int W,
+                     int ph, int pw, int sh, int sw, int Ho, int Wo);             /* src/ops_spatial.c:166-201 */
+int tt_k_avgpool_bwd(const float *g, float *dx, int N, int C, int H, int W,
+                     int ph, int pw, int sh, int sw, int Ho, int Wo);             /* src/autograd.c:596-628 */
+int tt_k_sgd(float *w, const float *g, long n, float lr);  /* harness SGD: tests/gate_mnist_mlp.py:121-124 */
+
+#ifdef __cplusplus
+}
+#endif
+#endif

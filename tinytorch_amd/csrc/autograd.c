@@ -1,0 +1,590 @@
+/* Reverse-mode autograd: host-side graph, device-side arithmetic.
+ *
+ * Follows the reference src/autograd.c:
+ *   node construction / ownership           :105-275
+ *   accum (first grad = copy, then +=)      :44-63
+ *   backward rules                          :283-628
+ *   iterative post-order topo sort          :649-680
+ *   reverse propagation                     :682-702
+ *   seeding and mismatch rule               :704-727
+ *
+ * Differences that do not change any observable value:
+ *   * A gradient a parent does not require is never computed (the reference
+ *     computes dA of every matmul and throws it away when A is a constant).
+ *   * A freshly computed gradient temporary is moved into an empty parent
+ *     grad instead of being copied (same bits, one copy fewer).
+ *   * conv2d keeps its forward im2col matrix for the backward pass instead
+ *     of recomputing it (reference :495 recomputes identical values).
+ *   * The NCHW <-> F x (N*Ho*Wo) permutes and W^T are folded into the GEMM
+ *     operand addressing instead of materialised (reference :498-533).
+ * Backward rules that fail to allocate skip silently, as in the reference. */
+#include "tt_internal.h"
+
+#include <stdlib.h>
+#include <string.h>
+
+typedef enum {
+    OP_LEAF, OP_ADD, OP_MUL, OP_ADDSCALAR, OP_MULSCALAR, OP_MATMUL, OP_RELU,
+    OP_SOFTMAX, OP_PADONES, OP_RESHAPE, OP_CONV2D, OP_MAXPOOL2D, OP_AVGPOOL2D,
+    OP_SOFTMAX_CE
+} OpKind;
+
+struct AGNode {
+    Tensor *val;
+    Tensor *grad;
+    AGNode *parents[3];
+    int     nparents;
+    OpKind  kind;
+    float   scalar;
+    int     params[4];
+    int     requires_grad;
+    int     mark;        /* DFS state: 0 new, 1 on stack, 2 done */
+    int     refcount;
+    float  *col;         /* conv2d: forward im2col matrix (device) */
+    Tensor *aux;         /* softmax_ce: probabilities */
+    Tensor *aux2;        /* softmax_ce: per-row seed (p - onehot)/rows */
+};
+
+/* ---------- gradient accumulation ---------- */
+
+/* p->grad += g, or p->grad = copy(g) if it has none (g is borrowed) */
+static void accum_copy(AGNode *p, Tensor *g) {
+    if (!p || !p->requires_grad || !g) return;
+    const float *gd = tt_dev(g);
+    if (!gd) return;
+    if (!p->grad) {
+        Tensor *c = tt_empty_like(g);
+        if (!c) return;
+        if (tt_k_copy(c->dev, gd, g->numel)) { tt_release(c); return; }
+        p->grad = c;
+        return;
+    }
+    float *pd = tt_dev(p->grad);
+    if (!pd) return;
+    tt_k_add_inplace(pd, gd, g->numel);
+    tt_mark_dev_written(p->grad);
+}
+
+/* same, but g is an owned temporary: moved in when p has no grad yet */
+static void accum_move(AGNode *p, Tensor *g) {
+    if (!g) return;
+    if (p && p->requires_grad && !p->grad) {
+        p->grad = g;
+        return;
+    }
+    accum_copy(p, g);
+    tt_release(g);
+}
+
+static int needs(const AGNode *p) { return p && p->requires_grad; }
+
+/* ---------- node construction ---------- */
+
+static AGNode *node_new(Tensor *val, int requires_grad) {
+    if (!val) return NULL;
+    AGNode *n = (AGNode *)calloc(1, sizeof(AGNode));
+    if (!n) { tt_release(val); return NULL; }
+    n->val = val;
+    n->requires_grad = requires_grad;
+    n->refcount = 1;
+    return n;
+}
+
+static AGNode *node_unary(AGNode *a, Tensor *val, OpKind k) {
+    AGNode *n = node_new(val, a->requires_grad);
+    if (!n) return NULL;
+    n->parents[0] = ag_retain(a);
+    n->nparents = 1;
+    n->kind = k;
+    return n;
+}
+
+static AGNode *node_binary(AGNode *a, AGNode *b, Tensor *val, OpKind k) {
+    AGNode *n = node_new(val, a->requires_grad || b->requires_grad);
+    if (!n) return NULL;
+    n->parents[0] = ag_retain(a);
+    n->parents[1] = ag_retain(b);
+    n->nparents = 2;
+    n->kind = k;
+    return n;
+}
+
+AGNode *ag_leaf(Tensor *t, int requires_grad) {
+    if (!t) return NULL;
+    AGNode *n = node_new(tt_retain(t), requires_grad);
+    if (n) n->kind = OP_LEAF;
+    return n;
+}
+
+AGNode *ag_add(AGNode *a, AGNode *b) {
+    if (!a || !b) return NULL;
+    return node_binary(a, b, tt_add(a->val, b->val), OP_ADD);
+}
+
+AGNode *ag_mul(AGNode *a, AGNode *b) {
+    if (!a || !b) return NULL;
+    return node_binary(a, b, tt_mul(a->val, b->val), OP_MUL);
+}
+
+AGNode *ag_addscalar(AGNode *a, float s) {
+    if (!a) return NULL;
+    AGNode *n = node_unary(a, tt_addscalar(a->val, s), OP_ADDSCALAR);
+    if (n) n->scalar = s;
+    return n;
+}
+
+AGNode *ag_mulscalar(AGNode *a, float s) {
+    if (!a) return NULL;
+    AGNode *n = node_unary(a, tt_mulscalar(a->val, s), OP_MULSCALAR);
+    if (n) n->scalar = s;
+    return n;
+}
+
+AGNode *ag_matmul(AGNode *a, AGNode *b) {
+    if (!a || !b) return NULL;
+    return node_binary(a, b, tt_matmul_omp(a->val, b->val, 0), OP_MATMUL);
+}
+
+AGNode *ag_relu(AGNode *a) {
+    if (!a) return NULL;
+    return node_unary(a, tt_relu(a->val), OP_RELU);
+}
+
+AGNode *ag_softmax(AGNode *a) {
+    if (!a) return NULL;
+    return node_unary(a, tt_softmax(a->val), OP_SOFTMAX);
+}
+
+AGNode *ag_padones(AGNode *a) {
+    if (!a || a->val->ndim != 2) return NULL;
+    const long M = a->val->shape[0], K = a->val->shape[1];
+    const long shp[2] = {M, K + 1};
+    const float *x = tt_dev(a->val);
+    if (!x) return NULL;
+    Tensor *v = tt_empty_dev(shp, 2);
+    if (!v) return NULL;
+    if (tt_k_padones_fwd(x, v->dev, M, K)) { tt_release(v); return NULL; }
+    return node_unary(a, v, OP_PADONES);
+}
+
+AGNode *ag_reshape(AGNode *a, const long *new_shape, int new_ndim) {
+    if (!a) return NULL;
+    Tensor *v = tt_reshape(a->val, new_shape, new_ndim);
+    if (!v) return NULL;
+    return node_unary(a, v, OP_RESHAPE);
+}
+
+AGNode *ag_conv2d(AGNode *a, AGNode *w, AGNode *b, int sh, int sw, int ph, int pw) {
+    if (!a || !w) return NULL;
+    const int keep = w->requires_grad;
+    float *col = NULL;
+    Tensor *v = tt_conv2d_keepcol(a->val, w->val, b ? b->val : NULL, sh, sw, ph, pw,
+                                  keep ? &col : NULL);
+    if (!v) return NULL;
+    int req = a->requires_grad || w->requires_grad || (b && b->requires_grad);
+    AGNode *n = node_new(v, req);
+    if (!n) { ttrt_free(col); return NULL; }
+    n->parents[0] = ag_retain(a);
+    n->parents[1] = ag_retain(w);
+    n->nparents = 2;
+    if (b) {
+        n->parents[2] = ag_retain(b);
+        n->nparents = 3;
+    }
+    n->kind = OP_CONV2D;
+    n->params[0] = sh; n->params[1] = sw;
+    n->params[2] = ph; n->params[3] = pw;
+    n->col = col;
+    return n;
+}
+
+static AGNode *pool_node(AGNode *a, Tensor *v, OpKind k, int ph, int pw, int sh, int sw) {
+    AGNode *n = node_unary(a, v, k);
+    if (!n) return NULL;
+    n->params[0] = ph; n->params[1] = pw;
+    n->params[2] = sh; n->params[3] = sw;
+    return n;
+}
+
+AGNode *ag_maxpool2d(AGNode *a, int ph, int pw, int sh, int sw) {
+    if (!a) return NULL;
+    Tensor *v = tt_maxpool2d(a->val, ph, pw, sh, sw);
+    if (!v) return NULL;
+    return pool_node(a, v, OP_MAXPOOL2D, ph, pw, sh, sw);
+}
+
+AGNode *ag_avgpool2d(AGNode *a, int ph, int pw, int sh, int sw) {
+    if (!a) return NULL;
+    Tensor *v = tt_avgpool2d(a->val, ph, pw, sh, sw);
+    if (!v) return NULL;
+    return pool_node(a, v, OP_AVGPOOL2D, ph, pw, sh, sw);
+}
+
+/* Fused softmax + mean cross-entropy (no reference counterpart: the
+ * reference harness does this in NumPy, tests/gate_cifar_cnn.py:175-181). */
+AGNode *ag_softmax_ce(AGNode *logits, const int *labels, long rows) {
+    if (!logits || !labels || logits->val->ndim != 2 || logits->val->shape[0] != rows ||
+        rows <= 0 || logits->val->shape[1] > 0x7fffffffL)
+        return NULL;
+    const int cols = (int)logits->val->shape[1];
+    const float *x = tt_dev(logits->val);
+    if (!x) return NULL;
+    const long one = 1;
+    Tensor *probs = tt_empty_like(logits->val);
+    Tensor *seed = tt_empty_like(logits->val);
+    Tensor *loss = tt_empty_dev(&one, 1);
+    int32_t *dlab = (int32_t *)ttrt_alloc(sizeof(int32_t) * (size_t)rows);
+    float *rowloss = (float *)ttrt_alloc(sizeof(float) * (size_t)rows);
+    int ok = probs && seed && loss && dlab && rowloss;
+    if (ok) {
+        int32_t *h = (int32_t *)malloc(sizeof(int32_t) * (size_t)rows);
+        ok = h != NULL;
+        if (ok) {
+            for (long r = 0; r < rows; r++) h[r] = (int32_t)labels[r];
+            ok = ttrt_h2d(dlab, h, sizeof(int32_t) * (size_t)rows) == 0;
+            free(h);
+        }
+    }
+    /* loss = mean of the per-row losses: a 1 x rows by rows x 1 GEMM with a
+     * vector of 1/rows keeps the reduction on the device */
+    float *inv = NULL;
+    if (ok) {
+        inv = (float *)ttrt_alloc(sizeof(float) * (size_t)rows);
+        ok = inv && tt_k_fill(inv, rows, 1.0f / (float)rows) == 0 &&
+             tt_k_softmax_ce(x, dlab, probs->dev, rowloss, seed->dev, rows, cols,
+                             1.0f / (float)rows) == 0 &&
+             tt_k_gemm(1, 1, (int)rows, rowloss, (int)rows, 0, inv, 1, 0, loss->dev, 1) == 0;
+    }
+    ttrt_free(dlab);
+    ttrt_free(rowloss);
+    ttrt_free(inv);
+    if (!ok) {
+        tt_release(probs); tt_release(seed); tt_release(loss);
+        return NULL;
+    }
+    AGNode *n = node_unary(logits, loss, OP_SOFTMAX_CE);
+    if (!n) { tt_release(probs); tt_release(seed); return NULL; }
+    n->aux = probs;
+    n->aux2 = seed;
+    return n;
+}
+
+Tensor *ag_softmax_ce_probs(const AGNode *n) {
+    return (n && n->kind == OP_SOFTMAX_CE) ? n->aux : NULL;
+}
+
+/* ---------- accessors ---------- */
+
+Tensor *ag_value(const AGNode *n) { return n ? n->val : NULL; }
+Tensor *ag_grad(const AGNode *n) { return n ? n->grad : NULL; }
+int ag_requires_grad(const AGNode *n) { return n ? n->requires_grad : 0; }
+
+/* ---------- backward rules ---------- */
+
+static void backward_add(AGNode *n) {
+    accum_copy(n->parents[0], n->grad);
+    accum_copy(n->parents[1], n->grad);
+}
+
+static void backward_mul(AGNode *n) {
+    AGNode *a = n->parents[0], *b = n->parents[1];
+    if (needs(a)) accum_move(a, tt_mul(n->grad, b->val));   /* g * b */
+    if (needs(b)) accum_move(b, tt_mul(n->grad, a->val));   /* g * a */
+}
+
+static void backward_addscalar(AGNode *n) { accum_copy(n->parents[0], n->grad); }
+
+static void backward_mulscalar(AGNode *n) {
+    if (needs(n->parents[0])) accum_move(n->parents[0], tt_mulscalar(n->grad, n->scalar));
+}
+
+static void backward_matmul(AGNode *n) {
+    AGNode *a = n->parents[0], *b = n->parents[1];
+    const int M = (int)a->val->shape[0], K = (int)a->val->shape[1], N = (int)b->val->shape[1];
+    const float *g = tt_dev(n->grad);
+    if (!g) return;
+    if (needs(a)) {  /* dA = g (MxN) * b^T (b is KxN) */
+        const float *bd = tt_dev(b->val);
+        Tensor *ga = bd ? tt_empty_like(a->val) : NULL;
+        if (ga && tt_k_gemm(M, K, N, g, N, 0, bd, N, 1, ga->dev, K) == 0) accum_move(a, ga);
+        else tt_release(ga);
+    }
+    if (needs(b)) {  /* dB = a^T (a is MxK) * g (MxN) */
+        const float *ad = tt_dev(a->val);
+        Tensor *gb = ad ? tt_empty_like(b->val) : NULL;
+        if (gb && tt_k_gemm(K, N, M, ad, K, 1, g, N, 0, gb->dev, N) == 0) accum_move(b, gb);
+        else tt_release(gb);
+    }
+}
+
+static void backward_relu(AGNode *n) {
+    AGNode *a = n->parents[0];
+    if (!needs(a)) return;
+    const float *x = tt_dev(a->val), *g = tt_dev(n->grad);
+    if (!x || !g) return;
+    Tensor *t = tt_empty_like(a->val);
+    if (!t) return;
+    if (tt_k_relu_bwd(x, g, t->dev, t->numel)) { tt_release(t); return; }
+    accum_move(a, t);
+}
+
+static void backward_softmax(AGNode *n) {
+    AGNode *a = n->parents[0];
+    if (!needs(a)) return;
+    const Tensor *s = n->val;
+    const long N = s->shape[s->ndim - 1];
+    const float *sd = tt_dev(n->val), *g = tt_dev(n->grad);
+    if (!sd || !g) return;
+    Tensor *t = tt_empty_like(s);
+    if (!t) return;
+    if (tt_k_softmax_bwd(sd, g, t->dev, s->numel / N, (int)N)) { tt_release(t); return; }
+    accum_move(a, t);
+}
+
+static void backward_padones(AGNode *n) {
+    AGNode *a = n->parents[0];
+    if (!needs(a)) return;
+    const float *g = tt_dev(n->grad);
+    if (!g) return;
+    Tensor *t = tt_empty_like(a->val);
+    if (!t) return;
+    if (tt_k_padones_bwd(g, t->dev, a->val->shape[0], a->val->shape[1])) {
+        tt_release(t);
+        return;
+    }
+    accum_move(a, t);
+}
+
+static void backward_reshape(AGNode *n) {
+    AGNode *a = n->parents[0];
+    if (!needs(a)) return;
+    accum_move(a, tt_reshape(n->grad, a->val->shape, a->val->ndim));
+}
+
+static void backward_conv2d(AGNode *n) {
+    AGNode *a = n->parents[0], *w = n->parents[1];
+    AGNode *b = n->nparents > 2 ? n->parents[2] : NULL;
+    const int sh = n->params[0], sw = n->params[1], ph = n->params[2], pw = n->params[3];
+    const Tensor *g = n->grad;
+    const int N = (int)a->val->shape[0], C = (int)a->val->shape[1], H = (int)a->val->shape[2],
+              W = (int)a->val->shape[3];
+    const int F = (int)w->val->shape[0], HH = (int)w->val->shape[2], WW = (int)w->val->shape[3];
+    const int Ho = (int)g->shape[2], Wo = (int)g->shape[3];
+    const int HW = Ho * Wo;
+    const int Kc = C * HH * WW;
+    const long Ncol = (long)N * HW;
+    const float *gd = tt_dev(n->grad);
+    if (!gd) return;
+
+    if (needs(b)) {
+        const long bshp[1] = {F};
+        Tensor *gb = tt_empty_dev(bshp, 1);
+        if (gb && tt_k_bias_grad(gd, gb->dev, N, F, HW) == 0) accum_move(b, gb);
+        else tt_release(gb);
+    }
+    if (needs(w)) {
+        float *col = n->col;
+        int own = 0;
+        if (!col) {
+            const float *x = tt_dev(a->val);
+            col = x ? (float *)ttrt_alloc(sizeof(float) * (size_t)Kc * (size_t)Ncol) : NULL;
+            if (col && tt_k_im2col(x, col, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo)) {
+                ttrt_free(col);
+                col = NULL;
+            }
+            own = 1;
+        }
+        Tensor *gw = col ? tt_empty_like(w->val) : NULL;
+        if (gw && tt_k_conv_dw(F, Kc, Ncol, HW, gd, col, gw->dev) == 0) accum_move(w, gw);
+        else tt_release(gw);
+        if (own) ttrt_free(col);
+    }
+    if (needs(a)) {
+        const float *wd = tt_dev(w->val);
+        float *dcol = wd ? (float *)ttrt_alloc(sizeof(float) * (size_t)Kc * (size_t)Ncol) : NULL;
+        Tensor *ga = dcol ? tt_empty_like(a->val) : NULL;
+        if (ga && tt_k_conv_dcol(F, Kc, Ncol, HW, wd, gd, dcol) == 0 &&
+            tt_k_col2im(dcol, ga->dev, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo) == 0)
+            accum_move(a, ga);
+        else
+            tt_release(ga);
+        ttrt_free(dcol);
+    }
+}
+
+static void backward_pool(AGNode *n, int is_max) {
+    AGNode *a = n->parents[0];
+    if (!needs(a)) return;
+    const int ph = n->params[0], pw = n->params[1], sh = n->params[2], sw = n->params[3];
+    const int N = (int)a->val->shape[0], C = (int)a->val->shape[1], H = (int)a->val->shape[2],
+              W = (int)a->val->shape[3];
+    const int Ho = (int)n->grad->shape[2], Wo = (int)n->grad->shape[3];
+    const float *g = tt_dev(n->grad);
+    const float *x = is_max ? tt_dev(a->val) : NULL;
+    if (!g || (is_max && !x)) return;
+    Tensor *t = tt_empty_like(a->val);
+    if (!t) return;
+    int rc = is_max ? tt_k_maxpool_bwd(x, g, t->dev, N, C, H, W, ph, pw, sh, sw, Ho, Wo)
+                    : tt_k_avgpool_bwd(g, t->dev, N, C, H, W, ph, pw, sh, sw, Ho, Wo);
+    if (rc) { tt_release(t); return; }
+    accum_move(a, t);
+}
+
+/* d logits = seed * dL (dL is the 1-element incoming gradient) */
+static void backward_softmax_ce(AGNode *n) {
+    AGNode *a = n->parents[0];
+    if (!needs(a)) return;
+    const float *seed = tt_dev(n->aux2), *gl = tt_dev(n->grad);
+    if (!seed || !gl) return;
+    Tensor *t = tt_empty_like(a->val);
+    if (!t) return;
+    /* outer product (rows*cols x 1) * (1 x 1) scales the seed by dL on device */
+    if (tt_k_gemm((int)t->numel, 1, 1, seed, 1, 0, gl, 1, 0, t->dev, 1)) {
+        tt_release(t);
+        return;
+    }
+    accum_move(a, t);
+}
+
+/* ---------- topological sort + propagation ---------- */
+
+typedef struct {
+    AGNode **items;
+    size_t len, cap;
+} NodeList;
+
+static int list_push(NodeList *l, AGNode *n) {
+    if (l->len == l->cap) {
+        size_t nc = l->cap ? l->cap * 2 : 64;
+        AGNode **ni = (AGNode **)realloc(l->items, nc * sizeof(AGNode *));
+        if (!ni) return 0;
+        l->items = ni;
+        l->cap = nc;
+    }
+    l->items[l->len++] = n;
+    return 1;
+}
+
+/* Iterative post-order DFS from root over parents (explicit stack, so a
+ * 1000-deep chain does not recurse); order ends with root. */
+static int topo_order(AGNode *root, NodeList *order) {
+    typedef struct { AGNode *n; int next; } Frame;
+    size_t cap = 64, top = 0;
+    Frame *st = (Frame *)malloc(cap * sizeof(Frame));
+    if (!st) return 0;
+    st[top].n = root; st[top].next = 0; top++;
+    root->mark = 1;
+    int ok = 1;
+    while (top > 0) {
+        Frame *f = &st[top - 1];
+        if (f->next < f->n->nparents) {
+            AGNode *c = f->n->parents[f->next++];
+            if (c->mark) continue;
+            if (top == cap) {
+                Frame *ns = (Frame *)realloc(st, 2 * cap * sizeof(Frame));
+                if (!ns) { ok = 0; break; }
+                st = ns;
+                cap *= 2;
+            }
+            c->mark = 1;
+            st[top].n = c; st[top].next = 0; top++;
+        } else {
+            f->n->mark = 2;
+            if (!list_push(order, f->n)) { ok = 0; break; }
+            top--;
+        }
+    }
+    free(st);
+    return ok;
+}
+
+static void propagate(NodeList *order) {
+    for (size_t i = order->len; i-- > 0;) {
+        AGNode *n = order->items[i];
+        if (!n->grad || n->nparents == 0) continue;
+        switch (n->kind) {
+            case OP_ADD:        backward_add(n); break;
+            case OP_MUL:        backward_mul(n); break;
+            case OP_ADDSCALAR:  backward_addscalar(n); break;
+            case OP_MULSCALAR:  backward_mulscalar(n); break;
+            case OP_MATMUL:     backward_matmul(n); break;
+            case OP_RELU:       backward_relu(n); break;
+            case OP_SOFTMAX:    backward_softmax(n); break;
+            case OP_PADONES:    backward_padones(n); break;
+            case OP_RESHAPE:    backward_reshape(n); break;
+            case OP_CONV2D:     backward_conv2d(n); break;
+            case OP_MAXPOOL2D:  backward_pool(n, 1); break;
+            case OP_AVGPOOL2D:  backward_pool(n, 0); break;
+            case OP_SOFTMAX_CE: backward_softmax_ce(n); break;
+            default: break;
+        }
+    }
+}
+
+/* seed_kind: 0 = ones, 1 = host floats, 2 = device tensor */
+static void backward_impl(AGNode *out, int seed_kind, const float *hseed, const Tensor *dseed) {
+    NodeList order = {0};
+    if (!topo_order(out, &order)) {
+        for (size_t i = 0; i < order.len; i++) order.items[i]->mark = 0;
+        free(order.items);
+        return;  /* marks of nodes still on the stack stay set only on OOM */
+    }
+    if (!out->grad) out->grad = tt_empty_like(out->val);
+    if (out->grad) {
+        int rc;
+        float *gd = out->grad->dev;
+        if (seed_kind == 1) rc = ttrt_h2d(gd, hseed, sizeof(float) * (size_t)out->val->numel);
+        else if (seed_kind == 2) {
+            const float *sd = tt_dev((Tensor *)dseed);
+            rc = sd ? tt_k_copy(gd, sd, out->val->numel) : -1;
+        } else rc = tt_k_fill(gd, out->grad->numel, 1.0f);
+        tt_mark_dev_written(out->grad);
+        if (rc == 0) propagate(&order);
+    }
+    for (size_t i = 0; i < order.len; i++) order.items[i]->mark = 0;
+    free(order.items);
+}
+
+void ag_backward_from(AGNode *out, const float *seed, size_t seed_numel) {
+    if (!out || !out->requires_grad) return;
+    if (seed && (!out->val || seed_numel != (size_t)out->val->numel)) return;
+    backward_impl(out, seed ? 1 : 0, seed, NULL);
+}
+
+void ag_backward(AGNode *out) { ag_backward_from(out, NULL, 0); }
+
+void ag_backward_from_tensor(AGNode *out, const Tensor *seed) {
+    if (!out || !out->requires_grad || !seed) return;
+    if (!out->val || seed->numel != out->val->numel) return;
+    backward_impl(out, 2, NULL, seed);
+}
+
+int ag_sgd_step(AGNode *leaf, float lr) {
+    if (!leaf || !leaf->grad) return 0;
+    float *w = tt_dev(leaf->val);
+    const float *g = tt_dev(leaf->grad);
+    if (!w || !g) return -1;
+    int rc = tt_k_sgd(w, g, leaf->val->numel, lr);
+    tt_mark_dev_written(leaf->val);
+    return rc;
+}
+
+/* ---------- lifecycle ---------- */
+
+AGNode *ag_retain(AGNode *n) {
+    if (!n) return NULL;
+    n->refcount++;
+    return n;
+}
+
+void ag_release(AGNode *n) {
+    if (!n) return;
+    if (--n->refcount > 0) return;
+    tt_release(n->val);
+    tt_release(n->grad);
+    tt_release(n->aux);
+    tt_release(n->aux2);
+    ttrt_free(n->col);
+    for (int i = 0; i < n->nparents; i++) ag_release(n->parents[i]);
+    free(n);
+}

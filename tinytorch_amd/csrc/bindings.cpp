@@ -1,0 +1,156 @@
+// pybind11 module `tinytorch_pybind`: the Node API of the reference bindings
+// (reference src/bindings.cpp:54-150) rebuilt against the GPU backend.
+//
+// Same class, method names, argument names and defaults; a NULL from the C
+// layer raises ValueError("tinytorch: invalid arguments or shape mismatch")
+// and a wrong-length backward seed raises ValueError before any gradient is
+// touched (reference src/bindings.cpp:22-30, 79-92).  value()/grad() return
+// fresh NumPy copies of the device data.  Additions of this backend:
+// softmax_ce(labels), probs(), backward_device(seed_node), sgd_step(lr) and
+// the module function available().
+#include <pybind11/numpy.h>
+#include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+
+#include <cstring>
+#include <memory>
+#include <vector>
+
+#include "autograd.h"
+#include "tensor.h"
+#include "tt_hip.h"
+
+namespace py = pybind11;
+
+namespace {
+
+using Arr = py::array_t<float, py::array::c_style | py::array::forcecast>;
+
+struct NodeRef {
+  AGNode *p;
+  explicit NodeRef(AGNode *n) : p(n) {}
+  ~NodeRef() { if (p) ag_release(p); }
+  NodeRef(const NodeRef &) = delete;
+  NodeRef &operator=(const NodeRef &) = delete;
+};
+
+[[noreturn]] void bad() { throw py::value_error("tinytorch: invalid arguments or shape mismatch"); }
+
+py::array_t<float> to_numpy(Tensor *t) {
+  if (!t) return py::array_t<float>();
+  const int nd = tt_ndim(t);
+  std::vector<long> shp(nd);
+  tt_shape(t, shp.data());
+  std::vector<py::ssize_t> shape(shp.begin(), shp.end());
+  const float *src = tt_data(t);
+  if (!src) throw std::runtime_error("tinytorch: device to host copy failed");
+  py::array_t<float> out(shape);
+  std::memcpy(out.mutable_data(), src, sizeof(float) * (size_t)tt_numel(t));
+  return out;
+}
+
+class PyNode {
+ public:
+  std::shared_ptr<NodeRef> ref;
+
+  explicit PyNode(AGNode *n) {
+    if (!n) bad();
+    ref = std::make_shared<NodeRef>(n);
+  }
+  AGNode *get() const { return ref->p; }
+
+  static PyNode leaf(Arr arr, bool requires_grad) {
+    py::buffer_info info = arr.request();
+    std::vector<long> shape(info.shape.begin(), info.shape.end());
+    Tensor *t = tt_fromdata(static_cast<const float *>(info.ptr), shape.data(), (int)info.ndim);
+    if (!t) bad();
+    AGNode *n = ag_leaf(t, requires_grad ? 1 : 0);
+    tt_release(t);  // the node holds its own reference
+    return PyNode(n);
+  }
+
+  py::array_t<float> value() const { return to_numpy(ag_value(get())); }
+
+  py::object grad() const {
+    Tensor *g = ag_grad(get());
+    if (!g) return py::none();
+    return to_numpy(g);
+  }
+
+  void backward(py::object seed) {
+    if (seed.is_none()) {
+      ag_backward(get());
+      return;
+    }
+    Arr arr = seed.cast<Arr>();
+    Tensor *v = ag_value(get());
+    const long need = v ? tt_numel(v) : -1;
+    if ((long)arr.size() != need) throw py::value_error("tinytorch: seed length mismatch");
+    ag_backward_from(get(), arr.data(), (size_t)arr.size());
+  }
+
+  PyNode add(const PyNode &o) { return PyNode(ag_add(get(), o.get())); }
+  PyNode mul(const PyNode &o) { return PyNode(ag_mul(get(), o.get())); }
+  PyNode addscalar(float s) { return PyNode(ag_addscalar(get(), s)); }
+  PyNode mulscalar(float s) { return PyNode(ag_mulscalar(get(), s)); }
+  PyNode matmul(const PyNode &o) { return PyNode(ag_matmul(get(), o.get())); }
+  PyNode relu() { return PyNode(ag_relu(get())); }
+  PyNode softmax() { return PyNode(ag_softmax(get())); }
+  PyNode padones() { return PyNode(ag_padones(get())); }
+  PyNode reshape(std::vector<long> shape) {
+    return PyNode(ag_reshape(get(), shape.data(), (int)shape.size()));
+  }
+  PyNode conv2d(const PyNode &w, py::object b, int sh, int sw, int ph, int pw) {
+    AGNode *bp = b.is_none() ? nullptr : b.cast<PyNode &>().get();
+    return PyNode(ag_conv2d(get(), w.get(), bp, sh, sw, ph, pw));
+  }
+  PyNode maxpool2d(int ph, int pw, int sh, int sw) { return PyNode(ag_maxpool2d(get(), ph, pw, sh, sw)); }
+  PyNode avgpool2d(int ph, int pw, int sh, int sw) { return PyNode(ag_avgpool2d(get(), ph, pw, sh, sw)); }
+
+  // ---- additions ----
+  PyNode softmax_ce(py::array_t<int, py::array::c_style | py::array::forcecast> labels) {
+    return PyNode(ag_softmax_ce(get(), labels.data(), (long)labels.size()));
+  }
+  py::object probs() const {
+    Tensor *p = ag_softmax_ce_probs(get());
+    if (!p) return py::none();
+    return to_numpy(p);
+  }
+  void sgd_step(float lr) {
+    if (ag_sgd_step(get(), lr) != 0) throw std::runtime_error("tinytorch: sgd step failed");
+  }
+};
+
+}  // namespace
+
+PYBIND11_MODULE(tinytorch_pybind, m) {
+  m.doc() = "tinytorch autograd Node API on the MI355X (gfx950) backend";
+  m.def("available", []() { return tth_available() == 1; });
+
+  py::class_<PyNode>(m, "Node")
+      .def_static("leaf", &PyNode::leaf, py::arg("arr"), py::arg("requires_grad") = true)
+      .def("value", &PyNode::value)
+      .def("grad", &PyNode::grad)
+      .def("backward", &PyNode::backward, py::arg("seed") = py::none())
+      .def("add", &PyNode::add)
+      .def("mul", &PyNode::mul)
+      .def("addscalar", &PyNode::addscalar)
+      .def("mulscalar", &PyNode::mulscalar)
+      .def("matmul", &PyNode::matmul)
+      .def("relu", &PyNode::relu)
+      .def("softmax", &PyNode::softmax)
+      .def("padones", &PyNode::padones)
+      .def("reshape", &PyNode::reshape)
+      .def("conv2d", &PyNode::conv2d, py::arg("w"), py::arg("b") = py::none(),
+           py::arg("stride_h") = 1, py::arg("stride_w") = 1, py::arg("pad_h") = 0,
+           py::arg("pad_w") = 0)
+      .def("maxpool2d", &PyNode::maxpool2d, py::arg("pool_h") = 2, py::arg("pool_w") = 2,
+           py::arg("stride_h") = 2, py::arg("stride_w") = 2)
+      .def("avgpool2d", &PyNode::avgpool2d, py::arg("pool_h") = 2, py::arg("pool_w") = 2,
+           py::arg("stride_h") = 2, py::arg("stride_w") = 2)
+      .def("softmax_ce", &PyNode::softmax_ce, py::arg("labels"))
+      .def("probs", &PyNode::probs)
+      .def("sgd_step", &PyNode::sgd_step, py::arg("lr"))
+      .def("__add__", &PyNode::add)
+      .def("__mul__", &PyNode::mul);
+}

@@ -1,0 +1,317 @@
+// Bandwidth-bound elementwise and row kernels (HBM roofline).
+//
+//   relu forward / backward    reference src/ops.c:104-106, src/autograd.c:318-327
+//   softmax forward / backward reference src/ops.c:108-145, src/autograd.c:329-346
+//   grad accumulation (accum)  reference src/autograd.c:52-63
+//   padones forward / backward reference src/autograd.c:195-212, 348-359
+//   add / mul / scalar ops     reference src/ops.c:26-78 (API completeness)
+//   softmax-cross-entropy seed reference harness tests/gate_cifar_cnn.py:175-181
+//
+// Flat kernels move 16 bytes per lane per access (float4) when the pointers
+// and the length allow it, with a scalar tail; a grid-stride loop sized to a
+// few waves per CU keeps every launch at one dispatch.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+#include "tt_rt.h"
+
+namespace {
+
+inline hipStream_t stream() { return (hipStream_t)ttrt_stream(); }
+
+inline bool a16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+inline int grid_for(long n, int per_thread) {
+  long blocks = (n / per_thread + 255) / 256;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 8192) blocks = 8192;
+  return (int)blocks;
+}
+
+inline int launched() { return hipGetLastError() == hipSuccess ? 0 : -3; }
+
+// Generic flat map over float4 groups with a scalar tail.
+template <typename F>
+__global__ void map4_kernel(long n4, long n, F f) {
+  const long stride = (long)gridDim.x * blockDim.x;
+  const long t0 = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  for (long i = t0; i < n4; i += stride) f.vec(i);
+  for (long i = n4 * 4 + t0; i < n; i += stride) f.one(i);
+}
+
+template <typename F>
+__global__ void map1_kernel(long n, F f) {
+  const long stride = (long)gridDim.x * blockDim.x;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) f.one(i);
+}
+
+template <typename F>
+int run_map(long n, bool vec, F f) {
+  if (n <= 0) return 0;
+  if (vec) {
+    long n4 = n / 4;
+    hipLaunchKernelGGL(map4_kernel<F>, dim3(grid_for(n, 4)), dim3(256), 0, stream(), n4, n, f);
+  } else {
+    hipLaunchKernelGGL(map1_kernel<F>, dim3(grid_for(n, 1)), dim3(256), 0, stream(), n, f);
+  }
+  return launched();
+}
+
+struct FillOp {
+  float *x; float v;
+  __device__ void vec(long i) const { reinterpret_cast<float4 *>(x)[i] = make_float4(v, v, v, v); }
+  __device__ void one(long i) const { x[i] = v; }
+};
+struct CopyOp {
+  float *d; const float *s;
+  __device__ void vec(long i) const { reinterpret_cast<float4 *>(d)[i] = reinterpret_cast<const float4 *>(s)[i]; }
+  __device__ void one(long i) const { d[i] = s[i]; }
+};
+struct AddInplaceOp {
+  float *d; const float *s;
+  __device__ void vec(long i) const {
+    float4 a = reinterpret_cast<float4 *>(d)[i];
+    const float4 b = reinterpret_cast<const float4 *>(s)[i];
+    a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+    reinterpret_cast<float4 *>(d)[i] = a;
+  }
+  __device__ void one(long i) const { d[i] += s[i]; }
+};
+__device__ __forceinline__ float relu1(float x) { return x > 0.0f ? x : 0.0f; }
+struct ReluFwdOp {
+  const float *x; float *y;
+  __device__ void vec(long i) const {
+    const float4 a = reinterpret_cast<const float4 *>(x)[i];
+    reinterpret_cast<float4 *>(y)[i] = make_float4(relu1(a.x), relu1(a.y), relu1(a.z), relu1(a.w));
+  }
+  __device__ void one(long i) const { y[i] = relu1(x[i]); }
+};
+struct ReluBwdOp {
+  const float *x; const float *g; float *dx;
+  __device__ void vec(long i) const {
+    const float4 a = reinterpret_cast<const float4 *>(x)[i];
+    const float4 b = reinterpret_cast<const float4 *>(g)[i];
+    reinterpret_cast<float4 *>(dx)[i] = make_float4(a.x > 0.0f ? b.x : 0.0f, a.y > 0.0f ? b.y : 0.0f,
+                                                    a.z > 0.0f ? b.z : 0.0f, a.w > 0.0f ? b.w : 0.0f);
+  }
+  __device__ void one(long i) const { dx[i] = x[i] > 0.0f ? g[i] : 0.0f; }
+};
+struct BinaryOp {
+  const float *a; const float *b; float *y; int op;
+  __device__ float f(float u, float v) const { return op == 0 ? u + v : u * v; }
+  __device__ void vec(long i) const {
+    const float4 u = reinterpret_cast<const float4 *>(a)[i];
+    const float4 v = reinterpret_cast<const float4 *>(b)[i];
+    reinterpret_cast<float4 *>(y)[i] = make_float4(f(u.x, v.x), f(u.y, v.y), f(u.z, v.z), f(u.w, v.w));
+  }
+  __device__ void one(long i) const { y[i] = f(a[i], b[i]); }
+};
+struct ScalarOp {
+  const float *a; float *y; float s; int op;
+  __device__ float f(float u) const { return op == 0 ? u + s : u * s; }
+  __device__ void vec(long i) const {
+    const float4 u = reinterpret_cast<const float4 *>(a)[i];
+    reinterpret_cast<float4 *>(y)[i] = make_float4(f(u.x), f(u.y), f(u.z), f(u.w));
+  }
+  __device__ void one(long i) const { y[i] = f(a[i]); }
+};
+struct SgdOp {
+  float *w; const float *g; float lr;
+  __device__ void vec(long i) const {
+    float4 a = reinterpret_cast<float4 *>(w)[i];
+    const float4 b = reinterpret_cast<const float4 *>(g)[i];
+    a.x -= lr * b.x; a.y -= lr * b.y; a.z -= lr * b.z; a.w -= lr * b.w;
+    reinterpret_cast<float4 *>(w)[i] = a;
+  }
+  __device__ void one(long i) const { w[i] -= lr * g[i]; }
+};
+
+// ---- row kernels ----
+// Rows of at most 64 columns run one row per lane with the reference's
+// sequential summation order; wider rows run one row per wavefront with a
+// butterfly reduction.
+
+// softmax, one row per thread (cols <= 64)
+__global__ void softmax_rowthread_kernel(const float *__restrict__ x, float *__restrict__ y,
+                                         long rows, int cols) {
+  const long r = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const float *xr = x + r * cols;
+  float *yr = y + r * cols;
+  float mx = -INFINITY;
+  for (int j = 0; j < cols; j++) { const float v = xr[j]; if (v > mx) mx = v; }
+  if (mx == -INFINITY) {
+    const float u = 1.0f / (float)cols;
+    for (int j = 0; j < cols; j++) yr[j] = u;
+    return;
+  }
+  float sum = 0.0f;
+  for (int j = 0; j < cols; j++) { const float e = expf(xr[j] - mx); yr[j] = e; sum += e; }
+  for (int j = 0; j < cols; j++) yr[j] = yr[j] / sum;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  for (int o = 32; o > 0; o >>= 1) { const float t = __shfl_xor(v, o, 64); v = t > v ? t : v; }
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// softmax, one row per wavefront (cols > 64)
+__global__ void softmax_rowwave_kernel(const float *__restrict__ x, float *__restrict__ y,
+                                       long rows, int cols) {
+  const long r = (long)blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
+  const int lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  const float *xr = x + r * cols;
+  float *yr = y + r * cols;
+  float mx = -INFINITY;
+  for (int j = lane; j < cols; j += 64) { const float v = xr[j]; if (v > mx) mx = v; }
+  mx = wave_max(mx);
+  if (mx == -INFINITY) {
+    const float u = 1.0f / (float)cols;
+    for (int j = lane; j < cols; j += 64) yr[j] = u;
+    return;
+  }
+  float sum = 0.0f;
+  for (int j = lane; j < cols; j += 64) { const float e = expf(xr[j] - mx); yr[j] = e; sum += e; }
+  sum = wave_sum(sum);
+  for (int j = lane; j < cols; j += 64) yr[j] = yr[j] / sum;
+}
+
+__global__ void softmax_bwd_rowthread_kernel(const float *__restrict__ s, const float *__restrict__ g,
+                                             float *__restrict__ dx, long rows, int cols) {
+  const long r = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const float *sr = s + r * cols, *gr = g + r * cols;
+  float dot = 0.0f;
+  for (int j = 0; j < cols; j++) dot += gr[j] * sr[j];
+  for (int j = 0; j < cols; j++) dx[r * cols + j] = sr[j] * (gr[j] - dot);
+}
+
+__global__ void softmax_bwd_rowwave_kernel(const float *__restrict__ s, const float *__restrict__ g,
+                                           float *__restrict__ dx, long rows, int cols) {
+  const long r = (long)blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
+  const int lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  const float *sr = s + r * cols, *gr = g + r * cols;
+  float dot = 0.0f;
+  for (int j = lane; j < cols; j += 64) dot += gr[j] * sr[j];
+  dot = wave_sum(dot);
+  for (int j = lane; j < cols; j += 64) dx[r * cols + j] = sr[j] * (gr[j] - dot);
+}
+
+// Fused softmax + cross-entropy: probs, per-row loss -log(max(p[y],1e-12))
+// and the logits gradient seed (p - onehot(y)) * scale, one row per thread.
+__global__ void softmax_ce_kernel(const float *__restrict__ x, const int32_t *__restrict__ lab,
+                                  float *__restrict__ probs, float *__restrict__ loss,
+                                  float *__restrict__ seed, long rows, int cols, float scale) {
+  const long r = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const float *xr = x + r * cols;
+  float *pr = probs + r * cols;
+  float mx = -INFINITY;
+  for (int j = 0; j < cols; j++) { const float v = xr[j]; if (v > mx) mx = v; }
+  if (mx == -INFINITY) {
+    for (int j = 0; j < cols; j++) pr[j] = 1.0f / (float)cols;
+  } else {
+    float sum = 0.0f;
+    for (int j = 0; j < cols; j++) { const float e = expf(xr[j] - mx); pr[j] = e; sum += e; }
+    for (int j = 0; j < cols; j++) pr[j] = pr[j] / sum;
+  }
+  const int y = lab[r];
+  const bool ok = y >= 0 && y < cols;
+  const float py = ok ? pr[y] : 0.0f;
+  loss[r] = -logf(fmaxf(py, 1e-12f));
+  for (int j = 0; j < cols; j++) seed[r * cols + j] = (pr[j] - (j == y ? 1.0f : 0.0f)) * scale;
+}
+
+__global__ void padones_fwd_kernel(const float *__restrict__ x, float *__restrict__ y, long M, long K) {
+  const long total = M * (K + 1);
+  const long stride = (long)gridDim.x * blockDim.x;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const long m = i / (K + 1), k = i - m * (K + 1);
+    y[i] = k < K ? x[m * K + k] : 1.0f;
+  }
+}
+
+__global__ void padones_bwd_kernel(const float *__restrict__ g, float *__restrict__ dx, long M, long K) {
+  const long total = M * K;
+  const long stride = (long)gridDim.x * blockDim.x;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const long m = i / K, k = i - m * K;
+    dx[i] = g[m * (K + 1) + k];
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int tt_k_fill(float *x, long n, float v) { return run_map(n, a16(x), FillOp{x, v}); }
+int tt_k_copy(float *d, const float *s, long n) { return run_map(n, a16(d) && a16(s), CopyOp{d, s}); }
+int tt_k_add_inplace(float *d, const float *s, long n) {
+  return run_map(n, a16(d) && a16(s), AddInplaceOp{d, s});
+}
+int tt_k_relu_fwd(const float *x, float *y, long n) { return run_map(n, a16(x) && a16(y), ReluFwdOp{x, y}); }
+int tt_k_relu_bwd(const float *x, const float *g, float *dx, long n) {
+  return run_map(n, a16(x) && a16(g) && a16(dx), ReluBwdOp{x, g, dx});
+}
+int tt_k_binary(const float *a, const float *b, float *y, long n, int op) {
+  return run_map(n, a16(a) && a16(b) && a16(y), BinaryOp{a, b, y, op});
+}
+int tt_k_scalar(const float *a, float *y, long n, float s, int op) {
+  return run_map(n, a16(a) && a16(y), ScalarOp{a, y, s, op});
+}
+int tt_k_sgd(float *w, const float *g, long n, float lr) {
+  return run_map(n, a16(w) && a16(g), SgdOp{w, g, lr});
+}
+
+int tt_k_softmax_fwd(const float *x, float *y, long rows, int cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  if (cols <= 64) {
+    hipLaunchKernelGGL(softmax_rowthread_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0,
+                       stream(), x, y, rows, cols);
+  } else {
+    hipLaunchKernelGGL(softmax_rowwave_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                       stream(), x, y, rows, cols);
+  }
+  return launched();
+}
+
+int tt_k_softmax_bwd(const float *s, const float *g, float *dx, long rows, int cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  if (cols <= 64) {
+    hipLaunchKernelGGL(softmax_bwd_rowthread_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256),
+                       0, stream(), s, g, dx, rows, cols);
+  } else {
+    hipLaunchKernelGGL(softmax_bwd_rowwave_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                       stream(), s, g, dx, rows, cols);
+  }
+  return launched();
+}
+
+int tt_k_softmax_ce(const float *logits, const int32_t *labels, float *probs, float *loss_rows,
+                    float *seed, long rows, int cols, float scale) {
+  if (rows <= 0 || cols <= 0) return 0;
+  hipLaunchKernelGGL(softmax_ce_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, stream(),
+                     logits, labels, probs, loss_rows, seed, rows, cols, scale);
+  return launched();
+}
+
+int tt_k_padones_fwd(const float *x, float *y, long M, long K) {
+  if (M <= 0 || K < 0) return 0;
+  hipLaunchKernelGGL(padones_fwd_kernel, dim3(grid_for(M * (K + 1), 1)), dim3(256), 0, stream(), x, y,
+                     M, K);
+  return launched();
+}
+
+int tt_k_padones_bwd(const float *g, float *dx, long M, long K) {
+  if (M <= 0 || K <= 0) return 0;
+  hipLaunchKernelGGL(padones_bwd_kernel, dim3(grid_for(M * K, 1)), dim3(256), 0, stream(), g, dx, M, K);
+  return launched();
+}
+
+}  // extern "C"

@@ -1,0 +1,419 @@
+// fp32 GEMM on the CDNA4 matrix cores (gfx950).
+//
+// Replaces, behind the same C ABI:
+//   tt_sgemm_rowmajor      reference src/gemm.c:569-641  (C = A*B, NN)
+//   matmul_nt              reference src/autograd.c:66-84 (dA = dC * B^T)
+//   matmul_tn              reference src/autograd.c:87-103 (dB = A^T * dC)
+//   conv forward GEMM      reference src/ops_spatial.c:96-121 (W*col, +bias, NCHW permute)
+//   sgemm_A_Bt_local       reference src/autograd.c:439-454 (conv dW = Gperm * col^T)
+//   conv dX GEMM           reference src/autograd.c:515-539 (dcol = W^T * Gperm)
+//
+// Design
+//   * v_mfma_f32_32x32x2_f32: one instruction multiplies a 32x2 by a 2x32
+//     fp32 block (2048 FMA, 16 passes).  Lane l feeds A[l%32][l/32] and
+//     B[l/32][l%32]; it receives D rows 8*(r/4) + 4*(l/32) + r%4, column l%32,
+//     in accumulator r = 0..15.
+//   * K is consumed 8 at a time per lane half: lane half g = l/32 holds the
+//     four k values kk+4g .. kk+4g+3 of each operand, so four MFMAs cover k
+//     kk..kk+7 (instruction s sums k = kk+s and kk+4+s).  With k-contiguous
+//     LDS rows that is one ds_read_b128 per 32-row block.
+//   * 256 threads = 4 waves in a 2x2 grid; wave tile (BM/2)x(BN/2) made of
+//     (BM/64)x(BN/64) 32x32 MFMA blocks whose accumulators stay in registers.
+//   * Global -> register prefetch of tile k+1 overlaps the MFMAs on tile k;
+//     LDS is double buffered so one barrier per K tile suffices.
+//   * LDS padding: k-contiguous rows are BK+4 floats (16-byte row skew, the
+//     b128 reads of 16 consecutive rows hit disjoint banks); m/n-contiguous
+//     rows are BM+8 floats (lane halves reading rows k and k+4 land 32 banks
+//     apart).
+//   * Out-of-range rows/cols/k are zero-filled in LDS, so any M, N, K works
+//     (the ragged 1000x1003x997 case); stores are predicated.
+//   * Tiles are remapped XCD-aware: the dispatcher deals workgroups round
+//     robin over the 8 XCDs, so consecutive logical tiles are gathered onto
+//     one XCD (shared L2) and grouped GROUP_M tile-rows at a time.
+//   * Split-K for small-MN / huge-K shapes (conv dW has K = N*Ho*Wo): each
+//     split writes a partial tile to a workspace and a second kernel sums the
+//     splits in a fixed order (deterministic, no atomics).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "tt_rt.h"
+
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int NT = 256;      // threads per workgroup
+constexpr int GROUP_M = 8;   // tile-row grouping for L2 reuse
+
+enum { EPI_STORE = 0, EPI_BIAS_NCHW = 1 };
+
+// Operand addressing.  The "contiguous" index of an operand is k for a
+// k-contiguous A or B^T layout, or m / n for an m/n-contiguous layout.  A
+// permuted operand splits its contiguous index i into (i / hw, i % hw) and
+// addresses  p[row*ld + (i/hw)*img + i%hw]  -- an NCHW gradient read as the
+// F x (N*Ho*Wo) matrix without materialising the permute.
+struct Opnd {
+  const float *p;
+  long ld;
+  long img;
+  int hw;
+};
+
+template <bool PERM>
+__device__ __forceinline__ long cidx(const Opnd &o, long i) {
+  if constexpr (PERM) {
+    long q = i / o.hw;
+    return q * o.img + (i - q * o.hw);
+  } else {
+    return i;
+  }
+}
+
+// Load 4 consecutive contiguous-index elements (i0 % 4 == 0) of stored row
+// `row`, zero-filling what lies outside [0, rows) x [0, ext).
+template <bool PERM, bool VEC>
+__device__ __forceinline__ float4 load4(const Opnd &o, long row, long rows, long i0, long ext) {
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (row >= rows) return v;
+  const float *base = o.p + row * o.ld;
+  if (VEC && i0 + 3 < ext) {
+    v = *reinterpret_cast<const float4 *>(base + cidx<PERM>(o, i0));
+  } else {
+    if (i0 + 0 < ext) v.x = base[cidx<PERM>(o, i0 + 0)];
+    if (i0 + 1 < ext) v.y = base[cidx<PERM>(o, i0 + 1)];
+    if (i0 + 2 < ext) v.z = base[cidx<PERM>(o, i0 + 2)];
+    if (i0 + 3 < ext) v.w = base[cidx<PERM>(o, i0 + 3)];
+  }
+  return v;
+}
+
+template <int BM, int BN, int BK, bool A_KC, bool A_PERM, bool B_NC, bool B_PERM,
+          bool VEC, int EPI>
+struct Cfg {
+  static constexpr int MI = BM / 64;            // 32x32 blocks per wave along m
+  static constexpr int NI = BN / 64;            // ... along n
+  static constexpr int A_ROWS = A_KC ? BM : BK; // stored rows of the LDS A tile
+  static constexpr int A_LD = A_KC ? BK + 4 : BM + 8;
+  static constexpr int B_ROWS = B_NC ? BK : BN;
+  static constexpr int B_LD = B_NC ? BN + 8 : BK + 4;
+  static constexpr int A_SZ = A_ROWS * A_LD;
+  static constexpr int B_SZ = B_ROWS * B_LD;
+  static constexpr int STAGE = A_SZ + B_SZ;
+  static constexpr int A_V4 = BM * BK / 4 / NT;  // float4 loads per thread
+  static constexpr int B_V4 = BN * BK / 4 / NT;
+  static_assert(A_V4 >= 1 && B_V4 >= 1, "tile too small for 256 threads");
+  static_assert(BM % 64 == 0 && BN % 64 == 0 && BK % 8 == 0, "tile shape");
+};
+
+template <int BM, int BN, int BK, bool A_KC, bool A_PERM, bool B_NC, bool B_PERM,
+          bool VEC, int EPI>
+__global__ void __launch_bounds__(NT)
+gemm_mfma_kernel(int M, int N, int K, Opnd A, Opnd B, float *__restrict__ C, long ldc,
+                 long split_stride, int kchunk, const float *__restrict__ bias, int HW) {
+  using G = Cfg<BM, BN, BK, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI>;
+  __shared__ __attribute__((aligned(16))) float smem[2 * G::STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+
+  // ---- XCD-aware tile mapping ----
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = (N + BN - 1) / BN;
+  const int ntiles = tiles_m * tiles_n;
+  int pid = blockIdx.x;
+  if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
+  const int group = GROUP_M * tiles_n;
+  const int first_m = (pid / group) * GROUP_M;
+  const int gsz = min(tiles_m - first_m, GROUP_M);
+  const int tm = first_m + (pid % group) % gsz;
+  const int tn = (pid % group) / gsz;
+  const long m0 = (long)tm * BM;
+  const long n0 = (long)tn * BN;
+
+  const int kbeg = blockIdx.z * kchunk;
+  const int kend = min(K, kbeg + kchunk);
+  const int nk = (kend - kbeg + BK - 1) / BK;
+  C += (long)blockIdx.z * split_stride;
+
+  const int wm = (wave >> 1) * (BM / 2);
+  const int wn = (wave & 1) * (BN / 2);
+
+  f32x16 acc[G::MI][G::NI];
+#pragma unroll
+  for (int i = 0; i < G::MI; i++)
+#pragma unroll
+    for (int j = 0; j < G::NI; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+  float4 ra[G::A_V4], rb[G::B_V4];
+
+  auto gload = [&](int kt) {
+    const long k0 = kbeg + (long)kt * BK;
+#pragma unroll
+    for (int v = 0; v < G::A_V4; v++) {
+      const int q = tid + v * NT;
+      if constexpr (A_KC) {  // stored row = m, contiguous = k
+        const int r = q / (BK / 4), c = (q % (BK / 4)) * 4;
+        ra[v] = load4<A_PERM, VEC>(A, m0 + r, M, k0 + c, kend);
+      } else {               // stored row = k, contiguous = m
+        const int r = q / (BM / 4), c = (q % (BM / 4)) * 4;
+        ra[v] = load4<false, VEC>(A, k0 + r, kend, m0 + c, M);
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < G::B_V4; v++) {
+      const int q = tid + v * NT;
+      if constexpr (B_NC) {  // stored row = k, contiguous = n
+        const int r = q / (BN / 4), c = (q % (BN / 4)) * 4;
+        rb[v] = load4<B_PERM, VEC>(B, k0 + r, kend, n0 + c, N);
+      } else {               // stored row = n, contiguous = k
+        const int r = q / (BK / 4), c = (q % (BK / 4)) * 4;
+        rb[v] = load4<false, VEC>(B, n0 + r, N, k0 + c, kend);
+      }
+    }
+  };
+
+  auto sstore = [&](int buf) {
+    float *sA = smem + buf * G::STAGE;
+    float *sB = sA + G::A_SZ;
+#pragma unroll
+    for (int v = 0; v < G::A_V4; v++) {
+      const int q = tid + v * NT;
+      int r, c;
+      if constexpr (A_KC) { r = q / (BK / 4); c = (q % (BK / 4)) * 4; }
+      else                { r = q / (BM / 4); c = (q % (BM / 4)) * 4; }
+      *reinterpret_cast<float4 *>(sA + r * G::A_LD + c) = ra[v];
+    }
+#pragma unroll
+    for (int v = 0; v < G::B_V4; v++) {
+      const int q = tid + v * NT;
+      int r, c;
+      if constexpr (B_NC) { r = q / (BN / 4); c = (q % (BN / 4)) * 4; }
+      else                { r = q / (BK / 4); c = (q % (BK / 4)) * 4; }
+      *reinterpret_cast<float4 *>(sB + r * G::B_LD + c) = rb[v];
+    }
+  };
+
+  auto compute = [&](int buf) {
+    const float *sA = smem + buf * G::STAGE;
+    const float *sB = sA + G::A_SZ;
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 8) {
+      float a[G::MI][4], b[G::NI][4];
+#pragma unroll
+      for (int i = 0; i < G::MI; i++) {
+        const int m = wm + 32 * i + l32;
+        if constexpr (A_KC) {
+          const float4 t = *reinterpret_cast<const float4 *>(sA + m * G::A_LD + kk + 4 * g);
+          a[i][0] = t.x; a[i][1] = t.y; a[i][2] = t.z; a[i][3] = t.w;
+        } else {
+#pragma unroll
+          for (int s = 0; s < 4; s++) a[i][s] = sA[(kk + 4 * g + s) * G::A_LD + m];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < G::NI; j++) {
+        const int n = wn + 32 * j + l32;
+        if constexpr (B_NC) {
+#pragma unroll
+          for (int s = 0; s < 4; s++) b[j][s] = sB[(kk + 4 * g + s) * G::B_LD + n];
+        } else {
+          const float4 t = *reinterpret_cast<const float4 *>(sB + n * G::B_LD + kk + 4 * g);
+          b[j][0] = t.x; b[j][1] = t.y; b[j][2] = t.z; b[j][3] = t.w;
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < 4; s++)
+#pragma unroll
+        for (int i = 0; i < G::MI; i++)
+#pragma unroll
+          for (int j = 0; j < G::NI; j++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  if (nk > 0) {
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+      const bool more = kt + 1 < nk;
+      if (more) gload(kt + 1);
+      compute(kt & 1);
+      if (more) sstore((kt + 1) & 1);
+      __syncthreads();
+    }
+  }
+
+  // ---- epilogue ----
+#pragma unroll
+  for (int i = 0; i < G::MI; i++)
+#pragma unroll
+    for (int j = 0; j < G::NI; j++) {
+      const long col = n0 + wn + 32 * j + l32;
+      if (col >= N) continue;
+      long img = 0, hw = 0;
+      if constexpr (EPI == EPI_BIAS_NCHW) { img = col / HW; hw = col - img * HW; }
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const long row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (row >= M) continue;
+        const float v = acc[i][j][r];
+        if constexpr (EPI == EPI_STORE) {
+          C[row * ldc + col] = v;
+        } else {
+          C[(img * M + row) * HW + hw] = v + (bias ? bias[row] : 0.f);
+        }
+      }
+    }
+}
+
+// Deterministic split-K reduction: out = sum_{z=0..S-1} ws[z] (+ epilogue).
+template <int EPI>
+__global__ void splitk_reduce_kernel(const float *__restrict__ ws, float *__restrict__ C,
+                                     int M, int N, int S, long ldc,
+                                     const float *__restrict__ bias, int HW) {
+  const long total = (long)M * N;
+  const long stride = (long)gridDim.x * blockDim.x;
+  for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += stride) {
+    float s = 0.f;
+    for (int z = 0; z < S; z++) s += ws[z * total + idx];
+    const long row = idx / N, col = idx - row * N;
+    if constexpr (EPI == EPI_STORE) {
+      C[row * ldc + col] = s;
+    } else {
+      const long img = col / HW, hw = col - img * HW;
+      C[(img * M + row) * HW + hw] = s + (bias ? bias[row] : 0.f);
+    }
+  }
+}
+
+inline hipStream_t stream() { return (hipStream_t)ttrt_stream(); }
+
+inline bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+struct Plan {
+  int bm, bn, splits, kchunk;
+};
+
+// Pick a tile and a split count so that the launch covers the 256 CUs.
+Plan plan(int M, int N, int K) {
+  const int CUS = 256;
+  Plan p{128, 128, 1, K};
+  const long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
+  if (N <= 64) {
+    p.bn = 64;  // skinny N: 128x64 tiles keep the whole tile useful
+    if ((long)((M + 127) / 128) < CUS) p.bm = 64;
+  } else if (t128 < CUS) {
+    p.bm = 64; p.bn = 64;
+  }
+  long tiles = (long)((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn);
+  // split K while the grid is under ~2 waves of CUs and each split keeps
+  // at least 256 k (8 K tiles of 32)
+  int s = 1;
+  while (tiles * s * 2 <= 2L * CUS && (long)K / (s * 2) >= 256 && s < 64) s *= 2;
+  p.splits = s;
+  int kc = (K + s - 1) / s;
+  kc = (kc + 31) / 32 * 32;
+  p.kchunk = kc;
+  p.splits = (K + kc - 1) / kc;
+  return p;
+}
+
+template <int BM, int BN, bool A_KC, bool A_PERM, bool B_NC, bool B_PERM, bool VEC, int EPI>
+void launch_tile(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ldc,
+                 long split_stride, int splits, int kchunk, const float *bias, int HW) {
+  const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  dim3 grid(tiles, 1, splits);
+  hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, 32, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI>),
+                     grid, dim3(NT), 0, stream(), M, N, K, A, B, C, ldc, split_stride, kchunk,
+                     bias, HW);
+}
+
+template <bool A_KC, bool A_PERM, bool B_NC, bool B_PERM, int EPI>
+int run(int M, int N, int K, Opnd A, Opnd B, float *C, long ldc, const float *bias, int HW,
+        bool vec) {
+  if (M <= 0 || N <= 0) return 0;
+  // K == 0 runs no K tiles: the epilogue stores zeros (plus bias)
+  Plan p = plan(M, N, K > 0 ? K : 1);
+  float *target = C;
+  long tgt_ld = ldc;
+  float *ws = nullptr;
+  int epi_direct = 1;
+  if (p.splits > 1) {
+    ws = (float *)ttrt_alloc(sizeof(float) * (size_t)M * N * p.splits);
+    if (!ws) return -2;
+    target = ws;
+    tgt_ld = N;
+    epi_direct = 0;
+  }
+  const long sstride = (long)M * N;
+#define TT_LAUNCH(BM_, BN_, VEC_, EPI_)                                                     \
+  launch_tile<BM_, BN_, A_KC, A_PERM, B_NC, B_PERM, VEC_, EPI_>(M, N, K, A, B, target,      \
+                                                                tgt_ld, sstride, p.splits, \
+                                                                p.kchunk, bias, HW)
+#define TT_SHAPES(EPI_)                                                          \
+  if (p.bm == 128 && p.bn == 128) {                                              \
+    if (vec) TT_LAUNCH(128, 128, true, EPI_); else TT_LAUNCH(128, 128, false, EPI_); \
+  } else if (p.bm == 128) {                                                      \
+    if (vec) TT_LAUNCH(128, 64, true, EPI_); else TT_LAUNCH(128, 64, false, EPI_);   \
+  } else {                                                                       \
+    if (vec) TT_LAUNCH(64, 64, true, EPI_); else TT_LAUNCH(64, 64, false, EPI_);     \
+  }
+  if (epi_direct) { TT_SHAPES(EPI) } else { TT_SHAPES(EPI_STORE) }
+#undef TT_SHAPES
+#undef TT_LAUNCH
+  if (hipGetLastError() != hipSuccess) { if (ws) ttrt_free(ws); return -3; }
+  if (ws) {
+    const long total = (long)M * N;
+    int blocks = (int)((total + 255) / 256);
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(splitk_reduce_kernel<EPI>, dim3(blocks), dim3(256), 0, stream(), ws, C,
+                       M, N, p.splits, ldc, bias, HW);
+    ttrt_free(ws);
+    if (hipGetLastError() != hipSuccess) return -3;
+  }
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int tt_k_gemm(int M, int N, int K, const float *A, int lda, int transA,
+                         const float *B, int ldb, int transB, float *C, int ldc) {
+  if (M < 0 || N < 0 || K < 0 || !A || !B || !C) return -1;
+  Opnd a{A, lda, 0, 1}, b{B, ldb, 0, 1};
+  const bool vec = aligned16(A) && aligned16(B) && (lda % 4 == 0) && (ldb % 4 == 0);
+  if (!transA && !transB) return run<true, false, true, false, EPI_STORE>(M, N, K, a, b, C, ldc, nullptr, 1, vec);
+  if (!transA && transB)  return run<true, false, false, false, EPI_STORE>(M, N, K, a, b, C, ldc, nullptr, 1, vec);
+  if (transA && !transB)  return run<false, false, true, false, EPI_STORE>(M, N, K, a, b, C, ldc, nullptr, 1, vec);
+  return run<false, false, false, false, EPI_STORE>(M, N, K, a, b, C, ldc, nullptr, 1, vec);
+}
+
+extern "C" int tt_k_conv_fwd(int F, int Kc, long Ncol, int HW, const float *W, const float *col,
+                             const float *bias, float *out) {
+  if (F <= 0 || Kc <= 0 || Ncol <= 0 || HW <= 0 || Ncol > 0x7fffffffL) return -1;
+  Opnd a{W, Kc, 0, 1}, b{col, Ncol, 0, 1};
+  const bool vec = aligned16(W) && aligned16(col) && (Kc % 4 == 0) && (Ncol % 4 == 0);
+  return run<true, false, true, false, EPI_BIAS_NCHW>(F, (int)Ncol, Kc, a, b, out, 0, bias, HW, vec);
+}
+
+extern "C" int tt_k_conv_dw(int F, int Kc, long Ncol, int HW, const float *g, const float *col,
+                            float *dW) {
+  if (F <= 0 || Kc <= 0 || Ncol <= 0 || HW <= 0 || Ncol > 0x7fffffffL) return -1;
+  // A = Gperm (m = f, k = p, permuted k), B = col^T (B stored Kc x Ncol = N x K)
+  Opnd a{g, HW, (long)F * HW, HW}, b{col, Ncol, 0, 1};
+  const bool vec = aligned16(g) && aligned16(col) && (HW % 4 == 0) && (Ncol % 4 == 0);
+  return run<true, true, false, false, EPI_STORE>(F, Kc, (int)Ncol, a, b, dW, Kc, nullptr, 1, vec);
+}
+
+extern "C" int tt_k_conv_dcol(int F, int Kc, long Ncol, int HW, const float *W, const float *g,
+                              float *dcol) {
+  if (F <= 0 || Kc <= 0 || Ncol <= 0 || HW <= 0 || Ncol > 0x7fffffffL) return -1;
+  // A = W^T (A stored F x Kc = K x M), B = Gperm (k = f, n = p, permuted n)
+  Opnd a{W, Kc, 0, 1}, b{g, HW, (long)F * HW, HW};
+  const bool vec = aligned16(W) && aligned16(g) && (Kc % 4 == 0) && (HW % 4 == 0);
+  return run<false, false, true, true, EPI_STORE>(Kc, (int)Ncol, F, a, b, dcol, Ncol, nullptr, 1, vec);
+}

@@ -1,0 +1,210 @@
+/* tt_* tensor ops on the GPU.
+ *
+ * Each op keeps the reference's argument validation and NULL-on-error
+ * behaviour and allocates a fresh output, but the arithmetic is one (or a
+ * few) kernel launches on the library stream:
+ *   elementwise / scalar / relu / softmax   reference src/ops.c:26-145
+ *   matmul (naive, fast, omp)               reference src/ops.c:84-102, src/gemm.c:644-671
+ *   reshape / conv2d / maxpool / avgpool     reference src/ops_spatial.c:12-201
+ * All three matmul entry points run the same MFMA GEMM; `nthreads` of
+ * tt_matmul_omp has no meaning on the GPU and is ignored. */
+#include "tt_internal.h"
+
+#include <stdlib.h>
+#include <string.h>
+
+static int same_shape(const Tensor *a, const Tensor *b) {
+    if (a->ndim != b->ndim) return 0;
+    for (int i = 0; i < a->ndim; i++)
+        if (a->shape[i] != b->shape[i]) return 0;
+    return 1;
+}
+
+static Tensor *fail(Tensor *out) {
+    tt_release(out);
+    return NULL;
+}
+
+static Tensor *binary(const Tensor *a, const Tensor *b, int op) {
+    if (!a || !b || !same_shape(a, b)) return NULL;
+    const float *x = tt_dev((Tensor *)a), *y = tt_dev((Tensor *)b);
+    if (!x || !y) return NULL;
+    Tensor *out = tt_empty_like(a);
+    if (!out) return NULL;
+    if (tt_k_binary(x, y, out->dev, a->numel, op)) return fail(out);
+    return out;
+}
+
+Tensor *tt_add(const Tensor *a, const Tensor *b) { return binary(a, b, 0); }
+Tensor *tt_mul(const Tensor *a, const Tensor *b) { return binary(a, b, 1); }
+
+static Tensor *scalar(const Tensor *a, float s, int op) {
+    if (!a) return NULL;
+    const float *x = tt_dev((Tensor *)a);
+    if (!x) return NULL;
+    Tensor *out = tt_empty_like(a);
+    if (!out) return NULL;
+    if (tt_k_scalar(x, out->dev, a->numel, s, op)) return fail(out);
+    return out;
+}
+
+Tensor *tt_addscalar(const Tensor *a, float s) { return scalar(a, s, 0); }
+Tensor *tt_mulscalar(const Tensor *a, float s) { return scalar(a, s, 1); }
+
+static Tensor *matmul2d(const Tensor *a, const Tensor *b) {
+    if (!a || !b || a->ndim != 2 || b->ndim != 2) return NULL;
+    if (a->shape[1] != b->shape[0]) return NULL;
+    if (a->shape[0] > 0x7fffffffL || a->shape[1] > 0x7fffffffL || b->shape[1] > 0x7fffffffL)
+        return NULL;
+    const int M = (int)a->shape[0], K = (int)a->shape[1], N = (int)b->shape[1];
+    const float *x = tt_dev((Tensor *)a), *y = tt_dev((Tensor *)b);
+    if (!x || !y) return NULL;
+    const long shp[2] = {M, N};
+    Tensor *out = tt_empty_dev(shp, 2);
+    if (!out) return NULL;
+    if (tt_k_gemm(M, N, K, x, K, 0, y, N, 0, out->dev, N)) return fail(out);
+    return out;
+}
+
+Tensor *tt_matmul(const Tensor *a, const Tensor *b) { return matmul2d(a, b); }
+Tensor *tt_matmul_fast(const Tensor *a, const Tensor *b) { return matmul2d(a, b); }
+Tensor *tt_matmul_omp(const Tensor *a, const Tensor *b, int nthreads) {
+    (void)nthreads;
+    return matmul2d(a, b);
+}
+
+int tt_sgemm_rowmajor(int M, int N, int K, const float *A, const float *B, float *C,
+                      int nthreads) {
+    (void)nthreads;
+    if (M <= 0 || N <= 0 || K < 0 || !C || (K > 0 && (!A || !B))) return -1;
+    const size_t sa = sizeof(float) * (size_t)M * (size_t)K;
+    const size_t sb = sizeof(float) * (size_t)K * (size_t)N;
+    const size_t sc = sizeof(float) * (size_t)M * (size_t)N;
+    float *dA = (float *)ttrt_alloc(sa ? sa : 4);
+    float *dB = (float *)ttrt_alloc(sb ? sb : 4);
+    float *dC = (float *)ttrt_alloc(sc);
+    int rc = -1;
+    if (dA && dB && dC && ttrt_h2d(dA, A, sa) == 0 && ttrt_h2d(dB, B, sb) == 0 &&
+        tt_k_gemm(M, N, K, dA, K, 0, dB, N, 0, dC, N) == 0 && ttrt_d2h(C, dC, sc) == 0)
+        rc = 0;
+    ttrt_free(dA);
+    ttrt_free(dB);
+    ttrt_free(dC);
+    return rc;
+}
+
+Tensor *tt_relu(const Tensor *a) {
+    if (!a) return NULL;
+    const float *x = tt_dev((Tensor *)a);
+    if (!x) return NULL;
+    Tensor *out = tt_empty_like(a);
+    if (!out) return NULL;
+    if (tt_k_relu_fwd(x, out->dev, a->numel)) return fail(out);
+    return out;
+}
+
+Tensor *tt_softmax(const Tensor *a) {
+    if (!a || a->ndim < 1) return NULL;
+    const long N = a->shape[a->ndim - 1];
+    if (N > 0x7fffffffL) return NULL;
+    const float *x = tt_dev((Tensor *)a);
+    if (!x) return NULL;
+    Tensor *out = tt_empty_like(a);
+    if (!out) return NULL;
+    if (tt_k_softmax_fwd(x, out->dev, a->numel / N, (int)N)) return fail(out);
+    return out;
+}
+
+/* ---- spatial ---- */
+
+static int valid_conv_params(int HH, int WW, int sh, int sw, int ph, int pw) {
+    return HH > 0 && WW > 0 && sh > 0 && sw > 0 && ph >= 0 && pw >= 0;
+}
+
+static int valid_pool_params(int ph, int pw, int sh, int sw) {
+    return ph > 0 && pw > 0 && sh > 0 && sw > 0;
+}
+
+Tensor *tt_reshape(const Tensor *a, const long *new_shape, int new_ndim) {
+    if (!a || !new_shape || new_ndim <= 0 || new_ndim > 8) return NULL;
+    long numel = 1;
+    for (int i = 0; i < new_ndim; i++) {
+        if (new_shape[i] <= 0) return NULL;
+        numel *= new_shape[i];
+    }
+    if (numel != a->numel) return NULL;
+    const float *x = tt_dev((Tensor *)a);
+    if (!x) return NULL;
+    Tensor *out = tt_empty_dev(new_shape, new_ndim);
+    if (!out) return NULL;
+    if (tt_k_copy(out->dev, x, numel)) return fail(out);
+    return out;
+}
+
+Tensor *tt_conv2d_keepcol(const Tensor *a, const Tensor *w, const Tensor *b, int sh, int sw,
+                          int ph, int pw, float **col_out) {
+    if (col_out) *col_out = NULL;
+    if (!a || !w || a->ndim != 4 || w->ndim != 4) return NULL;
+    const int N = (int)a->shape[0], C = (int)a->shape[1], H = (int)a->shape[2],
+              W = (int)a->shape[3];
+    const int F = (int)w->shape[0], Cw = (int)w->shape[1], HH = (int)w->shape[2],
+              WW = (int)w->shape[3];
+    if (C != Cw) return NULL;
+    if (b && (b->ndim != 1 || b->shape[0] != F)) return NULL;
+    if (!valid_conv_params(HH, WW, sh, sw, ph, pw)) return NULL;
+    const int Ho = (H + 2 * ph - HH) / sh + 1;
+    const int Wo = (W + 2 * pw - WW) / sw + 1;
+    if (Ho <= 0 || Wo <= 0) return NULL;
+
+    const float *x = tt_dev((Tensor *)a), *wd = tt_dev((Tensor *)w);
+    const float *bd = b ? tt_dev((Tensor *)b) : NULL;
+    if (!x || !wd || (b && !bd)) return NULL;
+
+    const long shp[4] = {N, F, Ho, Wo};
+    Tensor *out = tt_empty_dev(shp, 4);
+    if (!out) return NULL;
+    const int Kc = C * HH * WW;
+    const long Ncol = (long)N * Ho * Wo;
+    float *col = (float *)ttrt_alloc(sizeof(float) * (size_t)Kc * (size_t)Ncol);
+    if (!col) return fail(out);
+    if (tt_k_im2col(x, col, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo) ||
+        tt_k_conv_fwd(F, Kc, Ncol, Ho * Wo, wd, col, bd, out->dev)) {
+        ttrt_free(col);
+        return fail(out);
+    }
+    if (col_out) *col_out = col;
+    else ttrt_free(col);
+    return out;
+}
+
+Tensor *tt_conv2d(const Tensor *a, const Tensor *w, const Tensor *b, int sh, int sw, int ph,
+                  int pw) {
+    return tt_conv2d_keepcol(a, w, b, sh, sw, ph, pw, NULL);
+}
+
+static Tensor *pool(const Tensor *a, int ph, int pw, int sh, int sw, int is_max) {
+    if (!a || a->ndim != 4) return NULL;
+    if (!valid_pool_params(ph, pw, sh, sw)) return NULL;
+    const int N = (int)a->shape[0], C = (int)a->shape[1], H = (int)a->shape[2],
+              W = (int)a->shape[3];
+    const int Ho = (H - ph) / sh + 1;
+    const int Wo = (W - pw) / sw + 1;
+    if (Ho <= 0 || Wo <= 0 || ph > H || pw > W) return NULL;
+    const float *x = tt_dev((Tensor *)a);
+    if (!x) return NULL;
+    const long shp[4] = {N, C, Ho, Wo};
+    Tensor *out = tt_empty_dev(shp, 4);
+    if (!out) return NULL;
+    int rc = is_max ? tt_k_maxpool_fwd(x, out->dev, N, C, H, W, ph, pw, sh, sw, Ho, Wo)
+                    : tt_k_avgpool_fwd(x, out->dev, N, C, H, W, ph, pw, sh, sw, Ho, Wo);
+    if (rc) return fail(out);
+    return out;
+}
+
+Tensor *tt_maxpool2d(const Tensor *a, int ph, int pw, int sh, int sw) {
+    return pool(a, ph, pw, sh, sw, 1);
+}
+
+Tensor *tt_avgpool2d(const Tensor *a, int ph, int pw, int sh, int sw) {
+    return pool(a, ph, pw, sh, sw, 0);
+}

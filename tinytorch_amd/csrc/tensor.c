@@ -1,0 +1,191 @@
+/* Tensor lifecycle and accessors with device residency.
+ *
+ * Reference: src/tensor.c:1-75 (tt_alloc validation, calloc zero-fill,
+ * refcounting, accessors).  Validation is the same -- ndim in 1..8, every
+ * dim > 0, no long overflow, at most 2^40 elements -- so the hostile-shape
+ * cases return NULL before anything is allocated.
+ *
+ * Residency: the payload lives in `dev`.  `valid` records which copy is
+ * current (TT_V_DEV / TT_V_HOST).  tt_data() downloads into the host mirror
+ * and, because the caller may write through the returned pointer, leaves the
+ * HOST copy authoritative; tt_dev() (used by every op) uploads it again when
+ * needed.  Internal outputs are created with tt_empty_dev (no zero fill); the
+ * public tt_new keeps the reference's zero-filled contract. */
+#include "tt_internal.h"
+
+#include <hip/hip_runtime_api.h>
+#include <limits.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define TT_MAX_NUMEL (1L << 40)
+
+static Tensor *alloc_meta(const long *shape, int ndim) {
+    if (!shape || ndim <= 0 || ndim > 8) return NULL;
+    long numel = 1;
+    for (int i = 0; i < ndim; i++) {
+        if (shape[i] <= 0) return NULL;
+        if (numel > LONG_MAX / shape[i]) return NULL;
+        numel *= shape[i];
+    }
+    if (numel > TT_MAX_NUMEL) return NULL;
+    Tensor *t = (Tensor *)calloc(1, sizeof(Tensor));
+    if (!t) return NULL;
+    t->shape = (long *)malloc(sizeof(long) * (size_t)ndim);
+    t->strides = (long *)malloc(sizeof(long) * (size_t)ndim);
+    if (!t->shape || !t->strides) {
+        free(t->shape); free(t->strides); free(t);
+        return NULL;
+    }
+    long st = 1;
+    for (int i = ndim - 1; i >= 0; i--) {
+        t->shape[i] = shape[i];
+        t->strides[i] = st;
+        st *= shape[i];
+    }
+    t->ndim = ndim;
+    t->numel = numel;
+    t->refcount = 1;
+    return t;
+}
+
+static void free_meta(Tensor *t) {
+    free(t->data);
+    free(t->shape);
+    free(t->strides);
+    free(t);
+}
+
+Tensor *tt_empty_dev(const long *shape, int ndim) {
+    Tensor *t = alloc_meta(shape, ndim);
+    if (!t) return NULL;
+    t->dev = (float *)ttrt_alloc(sizeof(float) * (size_t)t->numel);
+    if (!t->dev) { free_meta(t); return NULL; }
+    t->valid = TT_V_DEV;
+    return t;
+}
+
+Tensor *tt_empty_like(const Tensor *a) { return tt_empty_dev(a->shape, a->ndim); }
+
+Tensor *tt_new(const long *shape, int ndim) {
+    Tensor *t = tt_empty_dev(shape, ndim);
+    if (!t) return NULL;
+    if (tt_k_fill(t->dev, t->numel, 0.0f) != 0) { tt_release(t); return NULL; }
+    return t;
+}
+
+Tensor *tt_fromdata(const float *data, const long *shape, int ndim) {
+    Tensor *t = alloc_meta(shape, ndim);
+    if (!t) return NULL;
+    if (!data) { free_meta(t); return NULL; }
+    t->dev = (float *)ttrt_alloc(sizeof(float) * (size_t)t->numel);
+    if (!t->dev) { free_meta(t); return NULL; }
+    if (ttrt_h2d(t->dev, data, sizeof(float) * (size_t)t->numel) != 0) {
+        tt_release(t);
+        return NULL;
+    }
+    t->valid = TT_V_DEV;
+    return t;
+}
+
+Tensor *tt_retain(Tensor *t) {
+    if (!t) return NULL;
+    t->refcount++;
+    return t;
+}
+
+void tt_release(Tensor *t) {
+    if (!t) return;
+    if (--t->refcount > 0) return;
+    ttrt_free(t->dev);
+    free_meta(t);
+}
+
+float *tt_dev(Tensor *t) {
+    if (!t || !t->dev) return NULL;
+    if (!(t->valid & TT_V_DEV)) {
+        if (!t->data || ttrt_h2d(t->dev, t->data, sizeof(float) * (size_t)t->numel) != 0)
+            return NULL;
+        t->valid |= TT_V_DEV;
+    }
+    return t->dev;
+}
+
+/* After the caller has been handed the host pointer, assume it may write:
+ * the device copy is re-uploaded before its next use. */
+float *tt_data(const Tensor *ct) {
+    Tensor *t = (Tensor *)ct;
+    if (!t) return NULL;
+    if (!(t->valid & TT_V_HOST)) {
+        if (!t->data) {
+            t->data = (float *)malloc(sizeof(float) * (size_t)t->numel);
+            if (!t->data) return NULL;
+        }
+        if (ttrt_d2h(t->data, t->dev, sizeof(float) * (size_t)t->numel) != 0) return NULL;
+    }
+    t->valid = TT_V_HOST;
+    return t->data;
+}
+
+/* device payload became the only current copy (a kernel wrote it) */
+void tt_mark_dev_written(Tensor *t) { t->valid = TT_V_DEV; }
+
+long tt_numel(const Tensor *t) { return t ? t->numel : 0; }
+int  tt_ndim(const Tensor *t) { return t ? t->ndim : 0; }
+
+void tt_shape(const Tensor *t, long *out) {
+    if (!t || !out) return;
+    for (int i = 0; i < t->ndim; i++) out[i] = t->shape[i];
+}
+
+void tt_strides(const Tensor *t, long *out) {
+    if (!t || !out) return;
+    for (int i = 0; i < t->ndim; i++) out[i] = t->strides[i];
+}
+
+/* ---- device-level runtime API (tt_hip.h) ---- */
+
+int tth_available(void) { return ttrt_init() == 0; }
+
+int tth_device_name(char *buf, int len) {
+    if (!buf || len <= 0 || ttrt_init() != 0) return -1;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, 0) != hipSuccess) return -1;
+    strncpy(buf, prop.gcnArchName, (size_t)len - 1);
+    buf[len - 1] = 0;
+    return 0;
+}
+
+void  *tth_stream(void) { return ttrt_init() == 0 ? ttrt_stream() : NULL; }
+int    tth_sync(void) { return ttrt_sync(); }
+int    tth_last_error(void) { return ttrt_last_error(); }
+void  *tth_malloc(size_t bytes) { return ttrt_alloc(bytes); }
+void   tth_free(void *d) { ttrt_free(d); }
+void   tth_release_cache(void) { ttrt_release_cache(); }
+size_t tth_bytes_in_use(void) { return ttrt_bytes_in_use(); }
+int    tth_h2d(void *d, const void *h, size_t bytes) { return ttrt_h2d(d, h, bytes); }
+int    tth_d2h(void *h, const void *d, size_t bytes) { return ttrt_d2h(h, d, bytes); }
+
+void *tth_event_create(void) {
+    if (ttrt_init() != 0) return NULL;
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return NULL;
+    return (void *)e;
+}
+
+int tth_event_record(void *ev) {
+    if (!ev) return -1;
+    return hipEventRecord((hipEvent_t)ev, (hipStream_t)ttrt_stream()) == hipSuccess ? 0 : -1;
+}
+
+float tth_event_elapsed_ms(void *start, void *stop) {
+    if (!start || !stop) return -1.0f;
+    if (hipEventSynchronize((hipEvent_t)stop) != hipSuccess) return -1.0f;
+    float ms = -1.0f;
+    if (hipEventElapsedTime(&ms, (hipEvent_t)start, (hipEvent_t)stop) != hipSuccess) return -1.0f;
+    return ms;
+}
+
+void tth_event_destroy(void *ev) {
+    if (ev) hipEventDestroy((hipEvent_t)ev);
+}

@@ -1,0 +1,23 @@
+/* Internal declarations shared by tensor.c, ops.c and autograd.c. */
+#ifndef TT_INTERNAL_H
+#define TT_INTERNAL_H
+
+#include "tensor.h"
+#include "autograd.h"
+#include "tt_hip.h"
+#include "tt_rt.h"
+
+#define TT_V_DEV  1
+#define TT_V_HOST 2
+
+/* device tensor without zero fill (the producing kernel writes every element) */
+Tensor *tt_empty_dev(const long *shape, int ndim);
+Tensor *tt_empty_like(const Tensor *a);
+void    tt_mark_dev_written(Tensor *t);
+
+/* conv2d forward that can hand back its im2col matrix (Kc x Ncol floats of
+ * device memory owned by the caller, release with ttrt_free) */
+Tensor *tt_conv2d_keepcol(const Tensor *a, const Tensor *w, const Tensor *b,
+                          int stride_h, int stride_w, int pad_h, int pad_w, float **col_out);
+
+#endif

@@ -1,0 +1,40 @@
+/* Internal runtime interface shared by the host C layer (tensor.c, ops.c,
+ * autograd.c) and the HIP kernel launchers (*.hip).  Everything here is
+ * C-ABI; nothing in this header is part of the public tensor.h/autograd.h
+ * surface.
+ *
+ * Execution model: one process, one GPU, one in-order HIP stream owned by
+ * the library.  Every kernel is launched on that stream, so a device buffer
+ * released back to the caching allocator may be handed out again at once:
+ * any later kernel that writes it is ordered after every earlier kernel that
+ * read it.  The host only waits on the stream when it copies results out
+ * (tt_data / ag_value readers) or when the caller asks (tth_sync). */
+#ifndef TT_RT_H
+#define TT_RT_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include "tt_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- runtime (alloc.c) ---- */
+int    ttrt_init(void);                 /* 0 ok, <0 no usable GPU */
+void  *ttrt_stream(void);               /* hipStream_t of the library */
+void  *ttrt_alloc(size_t bytes);        /* stream-ordered cached device alloc; NULL on OOM */
+void   ttrt_free(void *p);              /* return to cache (no sync) */
+void   ttrt_release_cache(void);        /* hipFree every cached block (syncs) */
+int    ttrt_sync(void);                 /* wait for the stream; 0 ok */
+int    ttrt_h2d(void *dst, const void *src, size_t bytes);   /* sync copy */
+int    ttrt_d2h(void *dst, const void *src, size_t bytes);   /* sync copy */
+void   ttrt_set_error(int code);
+int    ttrt_last_error(void);
+size_t ttrt_bytes_in_use(void);
+size_t ttrt_bytes_cached(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
