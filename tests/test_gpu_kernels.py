@@ -1,0 +1,301 @@
+"""GPU kernels vs the oracle, through the device-level C ABI (include/tt_hip.h).
+
+Bars:
+  * index / selection / copy work -- im2col, col2im, maxpool fwd/bwd,
+    avgpool, relu, padones, softmax backward -- bit-exact;
+  * GEMMs: max|C - C_oracle| / (sqrt(K) * max|A| * max|B|) <= 1e-4 and
+    max|C - C_oracle| / max|C_oracle| <= 1e-4;
+  * softmax forward (device expf vs libm expf) and the bias-grad reduction
+    (tree vs serial order): max relative error <= 1e-5.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import orc
+from tinytorch_amd.hip import DevBuf, check, sync
+
+pytestmark = pytest.mark.gpu
+rng = np.random.default_rng(99)
+
+GEMM_TOL = 1e-4
+
+
+def u(*s):
+    return rng.uniform(-1, 1, s).astype(np.float32)
+
+
+def bits_equal(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def gemm_err(C, ref, K, amax, bmax):
+    ref = np.asarray(ref, np.float64)
+    d = np.abs(np.asarray(C, np.float64) - ref).max() if C.size else 0.0
+    norm = d / (np.sqrt(max(K, 1)) * max(amax, 1e-30) * max(bmax, 1e-30))
+    rel = d / max(np.abs(ref).max(), 1e-30) if C.size else 0.0
+    return norm, rel
+
+
+def run_gemm(tlib, M, N, K, ta, tb, A, B):
+    dA, dB, dC = DevBuf.from_np(A), DevBuf.from_np(B), DevBuf(M * N)
+    lda = A.shape[1]
+    ldb = B.shape[1]
+    print(f"gemm M={M} N={N} K={K} ta={ta} tb={tb}", flush=True)
+    check(tlib.tt_k_gemm(M, N, K, dA.ptr, lda, ta, dB.ptr, ldb, tb, dC.ptr, N), "tt_k_gemm")
+    return dC.to_np((M, N))
+
+
+SHAPES = [(1, 1, 1), (3, 4, 5), (17, 13, 5), (5, 300, 3), (9, 33, 256), (64, 16, 512),
+          (128, 128, 32), (100, 70, 33), (1000, 1003, 997), (256, 512, 785), (256, 10, 257),
+          (513, 65, 1024), (31, 2000, 7)]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_gemm_nn_vs_oracle(tlib, M, N, K):
+    A, B = u(M, K), u(K, N)
+    C = run_gemm(tlib, M, N, K, 0, 0, A, B)
+    ref = orc.sgemm(A, B)
+    norm, rel = gemm_err(C, ref, K, np.abs(A).max(), np.abs(B).max())
+    assert norm <= GEMM_TOL and rel <= GEMM_TOL, (norm, rel)
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_gemm_nt_vs_oracle(tlib, M, N, K):
+    """dA = dC * B^T: opA = G (M x K), opB stored N x K (matmul_nt)."""
+    G, B = rng.standard_normal((M, K)).astype(np.float32), u(N, K)
+    C = run_gemm(tlib, M, N, K, 0, 1, G, B)
+    ref = orc.matmul_nt(G, B)
+    norm, rel = gemm_err(C, ref, K, np.abs(G).max(), np.abs(B).max())
+    assert norm <= GEMM_TOL and rel <= GEMM_TOL, (norm, rel)
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_gemm_tn_vs_oracle(tlib, M, N, K):
+    """dB = A^T * dC: opA stored K x M, opB = G (K x N) (matmul_tn)."""
+    A, G = u(K, M), rng.standard_normal((K, N)).astype(np.float32)
+    C = run_gemm(tlib, M, N, K, 1, 0, A, G)
+    ref = orc.matmul_tn(A, G)
+    norm, rel = gemm_err(C, ref, K, np.abs(A).max(), np.abs(G).max())
+    assert norm <= GEMM_TOL and rel <= GEMM_TOL, (norm, rel)
+
+
+@pytest.mark.parametrize("M,N,K", [(7, 9, 11), (130, 70, 300)])
+def test_gemm_tt_vs_float64(tlib, M, N, K):
+    A, B = u(K, M), u(N, K)
+    C = run_gemm(tlib, M, N, K, 1, 1, A, B)
+    ref = A.T.astype(np.float64) @ B.T.astype(np.float64)
+    norm, rel = gemm_err(C, ref, K, 1.0, 1.0)
+    assert norm <= GEMM_TOL and rel <= GEMM_TOL
+
+
+def test_gemm_k_zero_gives_zeros(tlib):
+    dA, dB, dC = DevBuf(4), DevBuf(4), DevBuf(6)
+    dC.fill(7.0)
+    check(tlib.tt_k_gemm(2, 3, 0, dA.ptr, 1, 0, dB.ptr, 3, 0, dC.ptr, 3), "gemm K=0")
+    assert np.all(dC.to_np() == 0.0)
+
+
+def test_gemm_rejects_bad_args(tlib):
+    d = DevBuf(4)
+    assert tlib.tt_k_gemm(-1, 2, 2, d.ptr, 2, 0, d.ptr, 2, 0, d.ptr, 2) != 0
+    assert tlib.tt_k_gemm(2, 2, 2, None, 2, 0, d.ptr, 2, 0, d.ptr, 2) != 0
+
+
+CONV_CASES = [  # (N, C, H, W, F, HH, WW, sh, sw, ph, pw)
+    (2, 3, 7, 7, 4, 3, 3, 1, 1, 1, 1), (2, 3, 7, 7, 4, 3, 3, 2, 2, 0, 0),
+    (3, 4, 9, 8, 5, 3, 2, 2, 1, 2, 1), (1, 1, 5, 5, 1, 1, 1, 1, 1, 0, 0),
+    (4, 32, 16, 16, 64, 3, 3, 1, 1, 1, 1), (8, 3, 32, 32, 32, 3, 3, 1, 1, 1, 1),
+    (2, 5, 6, 6, 3, 5, 5, 1, 1, 2, 2),
+]
+
+
+def conv_dims(N, C, H, W, F, HH, WW, sh, sw, ph, pw):
+    Ho, Wo = orc.conv_out(H, W, HH, WW, sh, sw, ph, pw)
+    return Ho, Wo, C * HH * WW, N * Ho * Wo
+
+
+@pytest.mark.parametrize("case", CONV_CASES)
+def test_im2col_col2im_bitexact(tlib, case):
+    N, C, H, W, F, HH, WW, sh, sw, ph, pw = case
+    Ho, Wo, Kc, Ncol = conv_dims(*case)
+    x = u(N, C, H, W)
+    dx, dcol = DevBuf.from_np(x), DevBuf(Kc * Ncol)
+    print("im2col", case, flush=True)
+    check(tlib.tt_k_im2col(dx.ptr, dcol.ptr, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo), "im2col")
+    assert bits_equal(dcol.to_np((Kc, Ncol)), orc.im2col(x, HH, WW, sh, sw, ph, pw))
+    col = u(Kc, Ncol)
+    dc, dimg = DevBuf.from_np(col), DevBuf(x.size)
+    print("col2im", case, flush=True)
+    check(tlib.tt_k_col2im(dc.ptr, dimg.ptr, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo), "col2im")
+    assert bits_equal(dimg.to_np(x.shape), orc.col2im(col, x.shape, HH, WW, sh, sw, ph, pw))
+
+
+@pytest.mark.parametrize("case", CONV_CASES)
+def test_conv_gemms_vs_oracle(tlib, case):
+    N, C, H, W, F, HH, WW, sh, sw, ph, pw = case
+    Ho, Wo, Kc, Ncol = conv_dims(*case)
+    x, w, b = u(N, C, H, W), u(F, C, HH, WW), u(F)
+    col = orc.im2col(x, HH, WW, sh, sw, ph, pw)
+    dcol, dw, db, dout = DevBuf.from_np(col), DevBuf.from_np(w), DevBuf.from_np(b), DevBuf(N * F * Ho * Wo)
+    print("conv_fwd", case, flush=True)
+    check(tlib.tt_k_conv_fwd(F, Kc, Ncol, Ho * Wo, dw.ptr, dcol.ptr, db.ptr, dout.ptr), "conv_fwd")
+    ref = orc.conv2d_fwd(x, w, b, sh, sw, ph, pw)
+    norm, rel = gemm_err(dout.to_np(ref.shape) - b[None, :, None, None],
+                         ref - b[None, :, None, None], Kc, np.abs(w).max(), np.abs(x).max())
+    assert norm <= GEMM_TOL and rel <= GEMM_TOL
+    g = rng.standard_normal((N, F, Ho, Wo)).astype(np.float32)
+    rdx, rdw, _ = orc.conv2d_bwd(x, w, g, sh, sw, ph, pw, need_db=False)
+    dg, ddw = DevBuf.from_np(g), DevBuf(w.size)
+    print("conv_dw", case, flush=True)
+    check(tlib.tt_k_conv_dw(F, Kc, Ncol, Ho * Wo, dg.ptr, dcol.ptr, ddw.ptr), "conv_dw")
+    norm, rel = gemm_err(ddw.to_np(w.shape), rdw, Ncol, np.abs(g).max(), np.abs(x).max())
+    assert norm <= GEMM_TOL and rel <= GEMM_TOL
+    ddc = DevBuf(Kc * Ncol)
+    print("conv_dcol", case, flush=True)
+    check(tlib.tt_k_conv_dcol(F, Kc, Ncol, Ho * Wo, dw.ptr, dg.ptr, ddc.ptr), "conv_dcol")
+    gp = g.transpose(1, 0, 2, 3).reshape(F, Ncol)
+    ref_dcol = orc.sgemm(np.ascontiguousarray(w.reshape(F, Kc).T), gp)
+    norm, rel = gemm_err(ddc.to_np((Kc, Ncol)), ref_dcol, F, np.abs(w).max(), np.abs(g).max())
+    assert norm <= GEMM_TOL and rel <= GEMM_TOL
+    # end to end dX = col2im(dcol) vs the oracle's conv backward
+    dimg = DevBuf(x.size)
+    check(tlib.tt_k_col2im(ddc.ptr, dimg.ptr, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo), "col2im")
+    got = dimg.to_np(x.shape)
+    assert np.abs(got - rdx).max() <= GEMM_TOL * max(np.abs(rdx).max(), 1e-30) * 4
+
+
+POOL_CASES = [(2, 2), (3, 2), (2, 1), (3, 3), (1, 1)]
+
+
+def pool_input(shape):
+    x = rng.integers(-3, 3, shape).astype(np.float32) * 0.5  # plenty of ties
+    x[0, 0, :3, :3] = -np.inf
+    x[0, 1, :3, :3] = np.nan
+    x[-1, -1, 0, 1] = np.nan
+    x[0, 2 % shape[1], 0, 0] = -2e30
+    return x
+
+
+@pytest.mark.parametrize("p,s", POOL_CASES)
+def test_maxpool_bitexact(tlib, p, s):
+    x = pool_input((3, 4, 9, 8))
+    N, C, H, W = x.shape
+    Ho, Wo = orc.pool_out(H, W, p, p, s, s)
+    dx_, dy = DevBuf.from_np(x), DevBuf(N * C * Ho * Wo)
+    print("maxpool", p, s, flush=True)
+    check(tlib.tt_k_maxpool_fwd(dx_.ptr, dy.ptr, N, C, H, W, p, p, s, s, Ho, Wo), "maxpool_fwd")
+    assert bits_equal(dy.to_np((N, C, Ho, Wo)), orc.maxpool_fwd(x, p, p, s, s))
+    g = u(N, C, Ho, Wo)
+    g[0, 0, 0, 0] = -0.0
+    dg, dgx = DevBuf.from_np(g), DevBuf(x.size)
+    check(tlib.tt_k_maxpool_bwd(dx_.ptr, dg.ptr, dgx.ptr, N, C, H, W, p, p, s, s, Ho, Wo), "maxpool_bwd")
+    assert bits_equal(dgx.to_np(x.shape), orc.maxpool_bwd(x, g, p, p, s, s))
+
+
+@pytest.mark.parametrize("p,s", POOL_CASES)
+def test_avgpool_bitexact(tlib, p, s):
+    x = u(2, 3, 9, 8)
+    N, C, H, W = x.shape
+    Ho, Wo = orc.pool_out(H, W, p, p, s, s)
+    dx_, dy = DevBuf.from_np(x), DevBuf(N * C * Ho * Wo)
+    check(tlib.tt_k_avgpool_fwd(dx_.ptr, dy.ptr, N, C, H, W, p, p, s, s, Ho, Wo), "avgpool_fwd")
+    assert bits_equal(dy.to_np((N, C, Ho, Wo)), orc.avgpool_fwd(x, p, p, s, s))
+    g = u(N, C, Ho, Wo)
+    dg, dgx = DevBuf.from_np(g), DevBuf(x.size)
+    check(tlib.tt_k_avgpool_bwd(dg.ptr, dgx.ptr, N, C, H, W, p, p, s, s, Ho, Wo), "avgpool_bwd")
+    assert bits_equal(dgx.to_np(x.shape), orc.avgpool_bwd(g, x.shape, p, p, s, s))
+
+
+@pytest.mark.parametrize("n", [0, 1, 3, 4, 1001, 1 << 20])
+def test_relu_bitexact(tlib, n):
+    x = rng.standard_normal(n).astype(np.float32)
+    if n >= 4:
+        x[:4] = [np.nan, np.inf, -np.inf, -0.0]
+    g = rng.standard_normal(n).astype(np.float32)
+    dx_, dg, dy, ddx = DevBuf.from_np(x), DevBuf.from_np(g), DevBuf(n), DevBuf(n)
+    check(tlib.tt_k_relu_fwd(dx_.ptr, dy.ptr, n), "relu_fwd")
+    check(tlib.tt_k_relu_bwd(dx_.ptr, dg.ptr, ddx.ptr, n), "relu_bwd")
+    assert bits_equal(dy.to_np(), orc.relu_fwd(x))
+    assert bits_equal(ddx.to_np(), orc.relu_bwd(x, g))
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (6, 10), (128, 10), (5, 64), (7, 65), (3, 1000)])
+def test_softmax(tlib, rows, cols):
+    x = (u(rows, cols) * 8).astype(np.float32)
+    if rows > 2:
+        x[1] = -np.inf
+        x[2] += 100.0
+    dx_, dy = DevBuf.from_np(x), DevBuf(x.size)
+    check(tlib.tt_k_softmax_fwd(dx_.ptr, dy.ptr, rows, cols), "softmax_fwd")
+    y = dy.to_np(x.shape)
+    ref = orc.softmax_fwd(x)
+    assert np.abs(y - ref).max() <= 1e-5 * max(np.abs(ref).max(), 1e-30)
+    if rows > 2:
+        assert np.all(y[1] == np.float32(1.0) / np.float32(cols))
+    g = u(rows, cols)
+    s = ref
+    ds, dg, ddx = DevBuf.from_np(s), DevBuf.from_np(g), DevBuf(x.size)
+    check(tlib.tt_k_softmax_bwd(ds.ptr, dg.ptr, ddx.ptr, rows, cols), "softmax_bwd")
+    got = ddx.to_np(x.shape)
+    want = orc.softmax_bwd(s, g)
+    if cols <= 64:  # one row per lane keeps the reference's serial dot order
+        assert bits_equal(got, want)
+    else:
+        assert np.abs(got - want).max() <= 1e-5 * max(np.abs(want).max(), 1e-30)
+
+
+@pytest.mark.parametrize("M,K", [(1, 1), (256, 784), (128, 4096), (3, 5)])
+def test_padones_bitexact(tlib, M, K):
+    x = u(M, K)
+    dx_, dy = DevBuf.from_np(x), DevBuf(M * (K + 1))
+    check(tlib.tt_k_padones_fwd(dx_.ptr, dy.ptr, M, K), "padones_fwd")
+    assert bits_equal(dy.to_np((M, K + 1)), orc.padones_fwd(x))
+    g = u(M, K + 1)
+    dg, ddx = DevBuf.from_np(g), DevBuf(M * K)
+    check(tlib.tt_k_padones_bwd(dg.ptr, ddx.ptr, M, K), "padones_bwd")
+    assert bits_equal(ddx.to_np((M, K)), orc.padones_bwd(g))
+
+
+@pytest.mark.parametrize("N,F,HW", [(1, 1, 1), (2, 4, 49), (128, 32, 1024), (128, 64, 256)])
+def test_bias_grad(tlib, N, F, HW):
+    g = rng.standard_normal((N, F, HW)).astype(np.float32)
+    dg, db = DevBuf.from_np(g), DevBuf(F)
+    check(tlib.tt_k_bias_grad(dg.ptr, db.ptr, N, F, HW), "bias_grad")
+    ref = orc.bias_grad(g)
+    exact = g.astype(np.float64).sum(axis=(0, 2))
+    got = db.to_np()
+    # serial fp32 (the reference) and tree fp32 (here) both sit near the exact sum
+    scale = np.abs(g).sum(axis=(0, 2)).max()
+    assert np.abs(got - exact).max() <= 1e-5 * scale + 1e-6
+    assert np.abs(got - ref).max() <= 2e-5 * scale + 1e-6
+
+
+def test_softmax_ce_closed_form(tlib):
+    rows, cols = 128, 10
+    x = (u(rows, cols) * 4).astype(np.float32)
+    y = rng.integers(0, cols, rows).astype(np.int32)
+    dx_, dlab = DevBuf.from_np(x), DevBuf.from_np(y)
+    dp, dl, ds = DevBuf(x.size), DevBuf(rows), DevBuf(x.size)
+    check(tlib.tt_k_softmax_ce(dx_.ptr, dlab.ptr, dp.ptr, dl.ptr, ds.ptr, rows, cols,
+                               ctypes.c_float(1.0 / rows)), "softmax_ce")
+    p = orc.softmax_fwd(x)
+    loss, seed = orc.ce_seed(p, y)
+    assert np.abs(dp.to_np(x.shape) - p).max() <= 1e-6
+    assert np.abs(ds.to_np(x.shape) - seed).max() <= 1e-7
+    assert abs(float(dl.to_np().astype(np.float64).mean()) - loss) <= 1e-5
+
+
+def test_copy_fill_add_sgd(tlib):
+    n = 12345
+    a, b = u(n), u(n)
+    da, db = DevBuf.from_np(a), DevBuf.from_np(b)
+    check(tlib.tt_k_add_inplace(da.ptr, db.ptr, n), "add_inplace")
+    assert bits_equal(da.to_np(), a + b)
+    check(tlib.tt_k_copy(da.ptr, db.ptr, n), "copy")
+    assert bits_equal(da.to_np(), b)
+    check(tlib.tt_k_fill(da.ptr, n, ctypes.c_float(2.5)), "fill")
+    assert np.all(da.to_np() == 2.5)
+    sync()
