@@ -1,0 +1,378 @@
+#!/usr/bin/env python3
+"""Benchmark of the tinytorch hot path on one MI355X.
+
+Headline (BASELINE.json metric): fp32 GEMM TFLOP/s at 4096^3 as a fraction
+of the fp32 MFMA peak, plus the CNN forward+backward step time.
+
+  * A "step" of the headline is one C = A*B at M = N = K = 4096, fp32 in,
+    fp32 MFMA accumulate, fp32 out, operands uniform[-1,1] from fixed seeds
+    and resident in HBM before timing.  W untimed steps, then exactly K
+    steps between two stream synchronisations; `value` = 2*4096^3*K / time.
+  * roofline.achieved uses HIP events recorded on the library's stream (the
+    stream the GEMM kernel runs on) around the K launches.
+  * extra.cnn_step_ms: config 4 (B=128, 3x32x32, conv32 -> relu -> pool ->
+    conv64 -> relu -> pool -> FC 4096->10, softmax-CE) forward + full
+    backward + an SGD update of every weight, inputs and weights resident,
+    graph rebuilt every step through the C ABI (ctypes), wall clock per step.
+  * extra.*: the other BASELINE configs (1024^3, 4096^3 NT/TN backward GEMMs,
+    8192^3, ragged, tall-skinny, MLP step).
+  * cpu_baseline: the reference's own AVX2+FMA OpenMP sgemm, compiled from
+    its sources into oracle/_ref (or the oracle restatement when that build
+    is missing), on this host's cores, on a bounded sample (median of 3 runs
+    of the same 4096^3 workload after one warmup).
+
+One JSON line on stdout.  --gpus N > 1 exits: this build targets one GPU.
+"""
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_FP32_MFMA_TFLOPS = 157.3   # MI355X dense fp32 matrix peak
+PEAK_HBM_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true", help="headline only")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="only run a plain 1 GiB device copy kernel 5 times (the known-size "
+                         "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    return ap.parse_args()
+
+
+# ---- seeded synthetic inputs; numpy only ----
+
+def uniform(shape, lo, hi, seed):
+    return np.random.default_rng(seed).uniform(lo, hi, shape).astype(np.float32)
+
+
+def he_normal(shape, fan_in, seed):
+    return (np.random.default_rng(seed).standard_normal(shape) *
+            np.sqrt(2.0 / fan_in)).astype(np.float32)
+
+
+def cnn_inputs(B=128, seed=0x5EED):
+    """config 4: x U[0,1] Bx3x32x32, labels U{0..9}, He-normal conv/FC, zero biases"""
+    x = uniform((B, 3, 32, 32), 0.0, 1.0, seed + 1)
+    y = np.random.default_rng(seed + 2).integers(0, 10, B).astype(np.int32)
+    wfc = he_normal((4097, 10), 4096, seed + 12)
+    wfc[4096] = 0.0
+    P = dict(w1=he_normal((32, 3, 3, 3), 27, seed + 10), b1=np.zeros(32, np.float32),
+             w2=he_normal((64, 32, 3, 3), 288, seed + 11), b2=np.zeros(64, np.float32), wfc=wfc)
+    return x, y, P
+
+
+def mlp_inputs(B=256, seed=0x5EED):
+    """config 2: x U[0,1] Bx784, labels U{0..9}, He-normal weights, zero bias rows"""
+    x = uniform((B, 784), 0.0, 1.0, seed + 1)
+    y = np.random.default_rng(seed + 2).integers(0, 10, B).astype(np.int32)
+    Ws = []
+    for i, (fi, fo) in enumerate(((784, 512), (512, 256), (256, 10))):
+        w = he_normal((fi + 1, fo), fi, seed + 10 + i)
+        w[fi] = 0.0
+        Ws.append(w)
+    return x, y, Ws
+
+
+def read_traffic():
+    """HBM bytes per launch of the 4096^3 GEMM from the committed rocprofv3
+    PMC summary (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated)."""
+    p = os.path.join(ROOT, "profiles", "sgemm_nn_4096_pmc.md")
+    if not os.path.exists(p):
+        return None
+    for line in open(p):
+        if line.strip().startswith("traffic_bytes_per_launch:"):
+            try:
+                return float(line.split(":", 1)[1].strip())
+            except ValueError:
+                return None
+    return None
+
+
+class Gemm:
+    def __init__(self, L, M, N, K, ta=0, tb=0, seed=0x5EED):
+        from tinytorch_amd.hip import DevBuf
+        self.L, self.M, self.N, self.K, self.ta, self.tb = L, M, N, K, ta, tb
+        A = uniform((K, M) if ta else (M, K), -1, 1, seed + 1)
+        B = uniform((N, K) if tb else (K, N), -1, 1, seed + 2)
+        self.dA, self.dB, self.dC = DevBuf.from_np(A), DevBuf.from_np(B), DevBuf(M * N)
+        self.lda = M if ta else K
+        self.ldb = K if tb else N
+
+    def launch(self):
+        rc = self.L.tt_k_gemm(self.M, self.N, self.K, self.dA.ptr, self.lda, self.ta,
+                              self.dB.ptr, self.ldb, self.tb, self.dC.ptr, self.N)
+        if rc != 0:
+            raise RuntimeError(f"tt_k_gemm failed: {rc}")
+
+    def flops(self):
+        return 2.0 * self.M * self.N * self.K
+
+    def free(self):
+        for b in (self.dA, self.dB, self.dC):
+            b.free()
+
+
+def time_gemm(L, g, steps, warmup):
+    from tinytorch_amd.hip import StreamTimer, sync
+    for _ in range(warmup):
+        g.launch()
+    sync()
+    tm = StreamTimer()
+    t0 = time.perf_counter()
+    tm.start()
+    for _ in range(steps):
+        g.launch()
+    ev_ms = tm.stop_ms()
+    sync()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    return wall_ms / steps, ev_ms / steps
+
+
+class CnnStep:
+    """Config 4 training step on device-resident tensors through the C ABI."""
+
+    def __init__(self, L, B=128):
+        self.L = L
+        x, y, P = cnn_inputs(B=B)
+        self.B = B
+        self.labels = np.ascontiguousarray(y, dtype=np.int32)
+        self.lab_p = self.labels.ctypes.data_as(ctypes.POINTER(ctypes.c_int))
+        self.t = {k: self._tensor(v) for k, v in dict(x=x, **P).items()}
+        self.flat = (ctypes.c_long * 2)(B, P["wfc"].shape[0] - 1)
+
+    def _tensor(self, a):
+        from tinytorch_amd import F32P
+        a = np.ascontiguousarray(a, np.float32)
+        shp = (ctypes.c_long * a.ndim)(*a.shape)
+        t = self.L.tt_fromdata(a.ctypes.data_as(F32P), shp, a.ndim)
+        assert t
+        return t
+
+    def step(self, lr=0.0):
+        L, t = self.L, self.t
+        nodes = []
+
+        def k(n):
+            assert n, "op returned NULL"
+            nodes.append(n)
+            return n
+        X = k(L.ag_leaf(t["x"], 0))
+        w1, b1, w2, b2, wfc = (k(L.ag_leaf(t[n], 1)) for n in ("w1", "b1", "w2", "b2", "wfc"))
+        h = k(L.ag_conv2d(X, w1, b1, 1, 1, 1, 1))
+        h = k(L.ag_maxpool2d(k(L.ag_relu(h)), 2, 2, 2, 2))
+        h = k(L.ag_conv2d(h, w2, b2, 1, 1, 1, 1))
+        h = k(L.ag_maxpool2d(k(L.ag_relu(h)), 2, 2, 2, 2))
+        h = k(L.ag_padones(k(L.ag_reshape(h, self.flat, 2))))
+        logits = k(L.ag_matmul(h, wfc))
+        loss = k(L.ag_softmax_ce(logits, self.lab_p, self.B))
+        L.ag_backward(loss)
+        for w in (w1, b1, w2, b2, wfc):
+            L.ag_sgd_step(w, ctypes.c_float(lr))
+        for n in nodes:
+            L.ag_release(n)
+
+
+class MlpStep:
+    """Config 2 training step (784->512->256->10, B=256) through the C ABI."""
+
+    def __init__(self, L, B=256):
+        self.L = L
+        x, y, Ws = mlp_inputs(B=B)
+        self.B = B
+        self.labels = np.ascontiguousarray(y, dtype=np.int32)
+        self.lab_p = self.labels.ctypes.data_as(ctypes.POINTER(ctypes.c_int))
+        from tinytorch_amd import F32P
+        self.t = []
+        for a in [x] + Ws:
+            shp = (ctypes.c_long * 2)(*a.shape)
+            self.t.append(L.tt_fromdata(np.ascontiguousarray(a).ctypes.data_as(F32P), shp, 2))
+
+    def step(self, lr=0.0):
+        L = self.L
+        nodes = []
+
+        def k(n):
+            assert n
+            nodes.append(n)
+            return n
+        X = k(L.ag_leaf(self.t[0], 0))
+        W = [k(L.ag_leaf(t, 1)) for t in self.t[1:]]
+        h = k(L.ag_relu(k(L.ag_matmul(k(L.ag_padones(X)), W[0]))))
+        h = k(L.ag_relu(k(L.ag_matmul(k(L.ag_padones(h)), W[1]))))
+        logits = k(L.ag_matmul(k(L.ag_padones(h)), W[2]))
+        loss = k(L.ag_softmax_ce(logits, self.lab_p, self.B))
+        L.ag_backward(loss)
+        for w in W:
+            L.ag_sgd_step(w, ctypes.c_float(lr))
+        for n in nodes:
+            L.ag_release(n)
+
+
+def time_steps(stepper, steps, warmup):
+    from tinytorch_amd.hip import sync
+    for _ in range(warmup):
+        stepper.step()
+    sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        stepper.step()
+    sync()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def cpu_threads():
+    n = os.environ.get("OMP_NUM_THREADS")
+    try:
+        n = int(n)
+    except (TypeError, ValueError):
+        n = len(os.sched_getaffinity(0))
+    return max(1, min(n, len(os.sched_getaffinity(0))))
+
+
+def cpu_baseline(threads):
+    """Reference CPU sgemm at 4096^3 and the reference CNN step, timed here."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import orc  # the CPU baseline leg is the only part of bench.py that uses oracle/
+    kind = "reference" if orc.ref_available() else "port"
+    n = 4096
+    A = uniform((n, n), -1, 1, 0x5EED + 1)
+    B = uniform((n, n), -1, 1, 0x5EED + 2)
+    C = np.zeros((n, n), np.float32)
+
+    def run():
+        if kind == "reference":
+            rc = orc.ref().tt_sgemm_rowmajor(n, n, n, A.ctypes.data, B.ctypes.data, C.ctypes.data,
+                                            threads)
+        else:
+            rc = orc.orc().orc_sgemm(n, n, n, A.ctypes.data, B.ctypes.data, C.ctypes.data, threads)
+        assert rc == 0
+    run()
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t0)
+    gflops = 2.0 * n ** 3 / statistics.median(ts) / 1e9
+    # CNN step on the reference autograd path (forward, softmax, NumPy CE seed, backward)
+    x, y, P = cnn_inputs()
+    step = (lambda: orc.ref_cnn_step(x, y, **P)) if kind == "reference" else \
+        (lambda: orc.cnn_step(x, y, nthreads=threads, **P))
+    step()
+    cts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        step()
+        cts.append(time.perf_counter() - t0)
+    return dict(value=round(gflops, 2), unit="GFLOP/s", cores=threads, kind=kind,
+                sample="sgemm 4096^3 NN fp32, 1 warmup + median of 3 runs; "
+                       "reference AVX2+FMA OpenMP kernel (src/gemm.c) built from its sources",
+                cnn_step_ms=round(statistics.median(cts) * 1e3, 2),
+                cnn_sample="config-4 CNN fwd+bwd on the reference autograd path, median of 3")
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on exactly one GPU; --gpus {args.gpus} is not supported "
+              "(see DESIGN.md: how the path would shard)", file=sys.stderr)
+        sys.exit(2)
+    import tinytorch_amd
+    tinytorch_amd.require_gpu()
+    L = tinytorch_amd.lib()
+    log("device", tinytorch_amd.device_name())
+    if args.copy_calib:
+        from tinytorch_amd.hip import DevBuf, check, sync
+        n = 256 << 20  # floats: 1 GiB read + 1 GiB written per launch (4x the MALL)
+        src, dst = DevBuf(n), DevBuf(n)
+        src.fill(1.0)
+        for _ in range(5):
+            check(L.tt_k_copy(dst.ptr, src.ptr, n), "tt_k_copy")
+        sync()
+        print(json.dumps({"copy_calib_bytes_each_way": n * 4, "launches": 5}))
+        return
+
+    g = Gemm(L, 4096, 4096, 4096)
+    wall_ms, ev_ms = time_gemm(L, g, args.steps, args.warmup)
+    value = g.flops() / (wall_ms * 1e-3) / 1e12
+    achieved = g.flops() / (ev_ms * 1e-3) / 1e12
+    g.free()
+    log(f"sgemm 4096^3: wall {wall_ms:.3f} ms/step ({value:.1f} TFLOP/s), "
+        f"events {ev_ms:.3f} ms/launch ({achieved:.1f} TFLOP/s)")
+    traffic = read_traffic()
+
+    extra = {}
+    if not args.no_extra:
+        for name, (M, N, K, ta, tb) in {
+                "sgemm_1024": (1024, 1024, 1024, 0, 0),
+                "sgemm_4096_nt_dA": (4096, 4096, 4096, 0, 1),
+                "sgemm_4096_tn_dB": (4096, 4096, 4096, 1, 0),
+                "sgemm_8192": (8192, 8192, 8192, 0, 0),
+                "sgemm_ragged_1000x1003x997": (1000, 1003, 997, 0, 0),
+                "sgemm_tall_65536x64x4096": (65536, 64, 4096, 0, 0)}.items():
+            gg = Gemm(L, M, N, K, ta, tb)
+            steps = max(3, min(args.steps, int(2e12 / gg.flops()) + 3))
+            _, ms = time_gemm(L, gg, steps, 2)
+            extra[name] = dict(tflops=round(gg.flops() / (ms * 1e-3) / 1e12, 2),
+                               ms=round(ms, 4),
+                               frac_of_peak=round(gg.flops() / (ms * 1e-3) / 1e12 /
+                                                  PEAK_FP32_MFMA_TFLOPS, 4))
+            gg.free()
+            log(name, extra[name])
+        cnn = CnnStep(L)
+        extra["cnn_step_ms"] = round(time_steps(cnn, 20, 5), 3)
+        log("cnn step ms", extra["cnn_step_ms"])
+        mlp = MlpStep(L)
+        extra["mlp_step_ms"] = round(time_steps(mlp, 50, 5), 3)
+        log("mlp step ms", extra["mlp_step_ms"])
+
+    cpu = None
+    if not args.no_cpu:
+        threads = cpu_threads()
+        log(f"cpu baseline on {threads} threads ...")
+        cpu = cpu_baseline(threads)
+        log("cpu", cpu)
+
+    out = {
+        "metric": "fp32 GEMM TFLOP/s @4096^3 (% MFMA peak) + CNN fwd+bwd step ms",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (uniform[-1,1] operands from fixed seeds)",
+        "config": {"workload": "sgemm C=A*B fp32 row-major, M=N=K=4096",
+                   "frac_of_fp32_mfma_peak": round(value / PEAK_FP32_MFMA_TFLOPS, 4)},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
+                     "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": traffic},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -241,7 +241,7 @@ AGNode *ag_softmax_ce(AGNode *logits, const int *labels, long rows) {
         ok = h != NULL;
         if (ok) {
             for (long r = 0; r < rows; r++) h[r] = (int32_t)labels[r];
-            ok = ttrt_h2d(dlab, h, sizeof(int32_t) * (size_t)rows) == 0;
+            ok = ttrt_h2d_async(dlab, h, sizeof(int32_t) * (size_t)rows) == 0;
             free(h);
         }
     }
@@ -533,7 +533,7 @@ static void backward_impl(AGNode *out, int seed_kind, const float *hseed, const 
     if (out->grad) {
         int rc;
         float *gd = out->grad->dev;
-        if (seed_kind == 1) rc = ttrt_h2d(gd, hseed, sizeof(float) * (size_t)out->val->numel);
+        if (seed_kind == 1) rc = ttrt_h2d_async(gd, hseed, sizeof(float) * (size_t)out->val->numel);
         else if (seed_kind == 2) {
             const float *sd = tt_dev((Tensor *)dseed);
             rc = sd ? tt_k_copy(gd, sd, out->val->numel) : -1;

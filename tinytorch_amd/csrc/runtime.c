@@ -215,6 +215,44 @@ int ttrt_h2d(void *dst, const void *src, size_t bytes) {
     return hipStreamSynchronize(g_stream) == hipSuccess ? 0 : -1;
 }
 
+/* Host-to-device copies of small buffers (tensor construction, backward
+ * seeds, labels) go through a ring of pinned staging slots: the bytes are
+ * copied into a slot on the host and the DMA is enqueued on the stream, so
+ * the caller neither waits for the GPU nor has to keep its buffer alive.  A
+ * slot is reused once the event recorded after its copy has completed. */
+#define TT_STAGE_SLOTS 8
+#define TT_STAGE_BYTES ((size_t)4 << 20)
+typedef struct { void *buf; hipEvent_t ev; int pending; } StageSlot;
+static StageSlot g_stage[TT_STAGE_SLOTS];
+static int g_stage_next = 0;
+
+int ttrt_h2d_async(void *dst, const void *src, size_t bytes) {
+    if (ttrt_init() != 0) return -1;
+    if (!bytes) return 0;
+    if (bytes > TT_STAGE_BYTES) return ttrt_h2d(dst, src, bytes);
+    StageSlot *s = &g_stage[g_stage_next];
+    if (!s->buf) {
+        if (hipHostMalloc(&s->buf, TT_STAGE_BYTES, hipHostMallocDefault) != hipSuccess) {
+            (void)hipGetLastError();
+            s->buf = NULL;
+            return ttrt_h2d(dst, src, bytes);
+        }
+        if (hipEventCreateWithFlags(&s->ev, hipEventDisableTiming) != hipSuccess) {
+            (void)hipGetLastError();
+            hipHostFree(s->buf);
+            s->buf = NULL;
+            return ttrt_h2d(dst, src, bytes);
+        }
+    }
+    g_stage_next = (g_stage_next + 1) % TT_STAGE_SLOTS;
+    if (s->pending && hipEventSynchronize(s->ev) != hipSuccess) return -1;
+    memcpy(s->buf, src, bytes);
+    if (hipMemcpyAsync(dst, s->buf, bytes, hipMemcpyHostToDevice, g_stream) != hipSuccess) return -1;
+    if (hipEventRecord(s->ev, g_stream) != hipSuccess) return -1;
+    s->pending = 1;
+    return 0;
+}
+
 int ttrt_d2h(void *dst, const void *src, size_t bytes) {
     if (ttrt_init() != 0) return -1;
     if (!bytes) return 0;

@@ -80,7 +80,7 @@ Tensor *tt_fromdata(const float *data, const long *shape, int ndim) {
     if (!data) { free_meta(t); return NULL; }
     t->dev = (float *)ttrt_alloc(sizeof(float) * (size_t)t->numel);
     if (!t->dev) { free_meta(t); return NULL; }
-    if (ttrt_h2d(t->dev, data, sizeof(float) * (size_t)t->numel) != 0) {
+    if (ttrt_h2d_async(t->dev, data, sizeof(float) * (size_t)t->numel) != 0) {
         tt_release(t);
         return NULL;
     }
@@ -104,7 +104,7 @@ void tt_release(Tensor *t) {
 float *tt_dev(Tensor *t) {
     if (!t || !t->dev) return NULL;
     if (!(t->valid & TT_V_DEV)) {
-        if (!t->data || ttrt_h2d(t->dev, t->data, sizeof(float) * (size_t)t->numel) != 0)
+        if (!t->data || ttrt_h2d_async(t->dev, t->data, sizeof(float) * (size_t)t->numel) != 0)
             return NULL;
         t->valid |= TT_V_DEV;
     }

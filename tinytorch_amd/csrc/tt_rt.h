@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-/* ---- runtime (alloc.c) ---- */
+/* ---- runtime (runtime.c) ---- */
 int    ttrt_init(void);                 /* 0 ok, <0 no usable GPU */
 void  *ttrt_stream(void);               /* hipStream_t of the library */
 void  *ttrt_alloc(size_t bytes);        /* stream-ordered cached device alloc; NULL on OOM */
@@ -29,6 +29,7 @@ void   ttrt_release_cache(void);        /* hipFree every cached block (syncs) */
 int    ttrt_sync(void);                 /* wait for the stream; 0 ok */
 int    ttrt_h2d(void *dst, const void *src, size_t bytes);   /* sync copy */
 int    ttrt_d2h(void *dst, const void *src, size_t bytes);   /* sync copy */
+int    ttrt_h2d_async(void *dst, const void *src, size_t bytes); /* stream-ordered, src reusable at return */
 void   ttrt_set_error(int code);
 int    ttrt_last_error(void);
 size_t ttrt_bytes_in_use(void);
