@@ -184,8 +184,8 @@ class CnnStep:
         logits = k(L.ag_matmul(h, wfc))
         loss = k(L.ag_softmax_ce(logits, self.lab_p, self.B))
         L.ag_backward(loss)
-        for w in (w1, b1, w2, b2, wfc):
-            L.ag_sgd_step(w, ctypes.c_float(lr))
+        ws = (ctypes.c_void_p * 5)(w1, b1, w2, b2, wfc)
+        assert L.ag_sgd_step_many(ws, 5, ctypes.c_float(lr)) == 0
         for n in nodes:
             L.ag_release(n)
 
@@ -220,8 +220,8 @@ class MlpStep:
         logits = k(L.ag_matmul(k(L.ag_padones(h)), W[2]))
         loss = k(L.ag_softmax_ce(logits, self.lab_p, self.B))
         L.ag_backward(loss)
-        for w in W:
-            L.ag_sgd_step(w, ctypes.c_float(lr))
+        ws = (ctypes.c_void_p * 3)(*W)
+        assert L.ag_sgd_step_many(ws, 3, ctypes.c_float(lr)) == 0
         for n in nodes:
             L.ag_release(n)
 

@@ -76,8 +76,11 @@ Tensor *ag_softmax_ce_probs(const AGNode *loss);
  * (no host round trip); same mismatch rule as ag_backward_from. */
 void    ag_backward_from_tensor(AGNode *out, const Tensor *seed);
 
-/* In-place SGD on a leaf value: value -= lr * grad (no-op without grad). */
+/* In-place SGD on a leaf value: value -= lr * grad (no-op without grad);
+ * the _many form updates `count` leaves in one kernel launch.  The update
+ * the reference harness does in NumPy (tests/gate_mnist_mlp.py:121-124). */
 int     ag_sgd_step(AGNode *leaf, float lr);
+int     ag_sgd_step_many(AGNode *const *leaves, int count, float lr);
 
 #ifdef __cplusplus
 }

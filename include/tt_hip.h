@@ -84,6 +84,13 @@ int tt_k_softmax_bwd(const float *s, const float *g, float *dx, long rows, int c
  * reference tests/gate_cifar_cnn.py:175-181 on the device. */
 int tt_k_softmax_ce(const float *logits, const int32_t *labels, float *probs,
                     float *loss_rows, float *seed, long rows, int cols, float scale);
+/* Same, for rows <= TT_CE_MEAN_MAX_ROWS, in one launch that also reduces the
+ * mean loss into loss_mean[0] (fixed reduction order). */
+#define TT_CE_MEAN_MAX_ROWS 8192
+int tt_k_softmax_ce_mean(const float *logits, const int32_t *labels, float *probs,
+                         float *loss_mean, float *seed, long rows, int cols, float scale);
+/* y = x * s[0], s a device scalar (chain rule through a scalar loss) */
+int tt_k_scale_by_dev(const float *x, const float *s, float *y, long n);
 int tt_k_padones_fwd(const float *x, float *y, long M, long K);      /* src/autograd.c:195-212 */
 int tt_k_padones_bwd(const float *g, float *dx, long M, long K);     /* src/autograd.c:348-359 */
 int tt_k_im2col(const float *x, float *col, int N, int C, int H, int W,
@@ -100,6 +107,9 @@ int tt_k_avgpool_fwd(const float *x, float *y, int N, int C, int H, int W,
 int tt_k_avgpool_bwd(const float *g, float *dx, int N, int C, int H, int W,
                      int ph, int pw, int sh, int sw, int Ho, int Wo);             /* src/autograd.c:596-628 */
 int tt_k_sgd(float *w, const float *g, long n, float lr);  /* harness SGD: tests/gate_mnist_mlp.py:121-124 */
+/* w[i] -= lr * g[i] for count <= TT_SGD_MAX tensors in one launch */
+#define TT_SGD_MAX 16
+int tt_k_sgd_multi(float *const *w, const float *const *g, const long *n, int count, float lr);
 
 #ifdef __cplusplus
 }

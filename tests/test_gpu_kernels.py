@@ -299,3 +299,40 @@ def test_copy_fill_add_sgd(tlib):
     check(tlib.tt_k_fill(da.ptr, n, ctypes.c_float(2.5)), "fill")
     assert np.all(da.to_np() == 2.5)
     sync()
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 3), (128, 10), (1000, 17), (8192, 10)])
+def test_softmax_ce_mean_one_launch(tlib, rows, cols):
+    x = (u(rows, cols) * 4).astype(np.float32)
+    y = rng.integers(0, cols, rows).astype(np.int32)
+    dx_, dlab = DevBuf.from_np(x), DevBuf.from_np(y)
+    dp, dl, ds = DevBuf(x.size), DevBuf(1), DevBuf(x.size)
+    check(tlib.tt_k_softmax_ce_mean(dx_.ptr, dlab.ptr, dp.ptr, dl.ptr, ds.ptr, rows, cols,
+                                    ctypes.c_float(1.0 / rows)), "softmax_ce_mean")
+    p = orc.softmax_fwd(x)
+    loss, seed = orc.ce_seed(p, y)
+    assert np.abs(dp.to_np(x.shape) - p).max() <= 1e-6
+    assert np.abs(ds.to_np(x.shape) - seed).max() <= 1e-7
+    assert abs(float(dl.to_np()[0]) - loss) <= 1e-5 * max(1.0, loss)
+    assert tlib.tt_k_softmax_ce_mean(dx_.ptr, dlab.ptr, dp.ptr, dl.ptr, ds.ptr, 8193, cols,
+                                     ctypes.c_float(1.0)) != 0  # above the one-workgroup limit
+
+
+def test_scale_by_dev_and_sgd_multi(tlib):
+    x = u(1000)
+    s = np.array([-1.75], np.float32)
+    dx_, ds, dy = DevBuf.from_np(x), DevBuf.from_np(s), DevBuf(1000)
+    check(tlib.tt_k_scale_by_dev(dx_.ptr, ds.ptr, dy.ptr, 1000), "scale_by_dev")
+    assert bits_equal(dy.to_np(), x * np.float32(-1.75))
+    sizes = [1, 7, 4096, 100003]
+    ws = [u(n) for n in sizes]
+    gs = [u(n) for n in sizes]
+    dws = [DevBuf.from_np(w) for w in ws]
+    dgs = [DevBuf.from_np(g) for g in gs]
+    W = (ctypes.c_void_p * 4)(*[d.ptr for d in dws])
+    G = (ctypes.c_void_p * 4)(*[d.ptr for d in dgs])
+    Nn = (ctypes.c_long * 4)(*sizes)
+    check(tlib.tt_k_sgd_multi(W, G, Nn, 4, ctypes.c_float(0.1)), "sgd_multi")
+    for w, g, d in zip(ws, gs, dws):
+        assert np.abs(d.to_np() - (w - np.float32(0.1) * g)).max() <= 1e-7
+    assert tlib.tt_k_sgd_multi(W, G, Nn, 17, ctypes.c_float(0.1)) != 0

@@ -74,6 +74,7 @@ SIGNATURES = [
     ("ag_softmax_ce_probs", VP, [VP]),
     ("ag_backward_from_tensor", None, [VP, VP]),
     ("ag_sgd_step", _I, [VP, _F]),
+    ("ag_sgd_step_many", _I, [ctypes.POINTER(VP), _I, _F]),
     # tt_hip.h: runtime
     ("tth_available", _I, []),
     ("tth_device_name", _I, [ctypes.c_char_p, _I]),
@@ -106,6 +107,8 @@ SIGNATURES = [
     ("tt_k_softmax_fwd", _I, [VP, VP, _L, _I]),
     ("tt_k_softmax_bwd", _I, [VP, VP, VP, _L, _I]),
     ("tt_k_softmax_ce", _I, [VP, VP, VP, VP, VP, _L, _I, _F]),
+    ("tt_k_softmax_ce_mean", _I, [VP, VP, VP, VP, VP, _L, _I, _F]),
+    ("tt_k_scale_by_dev", _I, [VP, VP, VP, _L]),
     ("tt_k_padones_fwd", _I, [VP, VP, _L, _L]),
     ("tt_k_padones_bwd", _I, [VP, VP, _L, _L]),
     ("tt_k_im2col", _I, [VP, VP] + [_I] * 12),
@@ -116,6 +119,7 @@ SIGNATURES = [
     ("tt_k_avgpool_fwd", _I, [VP, VP] + [_I] * 10),
     ("tt_k_avgpool_bwd", _I, [VP, VP] + [_I] * 10),
     ("tt_k_sgd", _I, [VP, VP, _L, _F]),
+    ("tt_k_sgd_multi", _I, [ctypes.POINTER(VP), ctypes.POINTER(VP), ctypes.POINTER(_L), _I, _F]),
 ]
 
 

@@ -234,8 +234,9 @@ AGNode *ag_softmax_ce(AGNode *logits, const int *labels, long rows) {
     Tensor *seed = tt_empty_like(logits->val);
     Tensor *loss = tt_empty_dev(&one, 1);
     int32_t *dlab = (int32_t *)ttrt_alloc(sizeof(int32_t) * (size_t)rows);
-    float *rowloss = (float *)ttrt_alloc(sizeof(float) * (size_t)rows);
-    int ok = probs && seed && loss && dlab && rowloss;
+    float *rowloss = rows > TT_CE_MEAN_MAX_ROWS ? (float *)ttrt_alloc(sizeof(float) * (size_t)rows)
+                                                : NULL;
+    int ok = probs && seed && loss && dlab && (rowloss || rows <= TT_CE_MEAN_MAX_ROWS);
     if (ok) {
         int32_t *h = (int32_t *)malloc(sizeof(int32_t) * (size_t)rows);
         ok = h != NULL;
@@ -245,10 +246,14 @@ AGNode *ag_softmax_ce(AGNode *logits, const int *labels, long rows) {
             free(h);
         }
     }
-    /* loss = mean of the per-row losses: a 1 x rows by rows x 1 GEMM with a
-     * vector of 1/rows keeps the reduction on the device */
+    /* small batches: one workgroup computes probabilities, seed and the mean
+     * loss; large ones reduce the per-row losses with a 1 x rows x 1 GEMM
+     * against a vector of 1/rows */
     float *inv = NULL;
-    if (ok) {
+    if (ok && rows <= TT_CE_MEAN_MAX_ROWS) {
+        ok = tt_k_softmax_ce_mean(x, dlab, probs->dev, loss->dev, seed->dev, rows, cols,
+                                  1.0f / (float)rows) == 0;
+    } else if (ok) {
         inv = (float *)ttrt_alloc(sizeof(float) * (size_t)rows);
         ok = inv && tt_k_fill(inv, rows, 1.0f / (float)rows) == 0 &&
              tt_k_softmax_ce(x, dlab, probs->dev, rowloss, seed->dev, rows, cols,
@@ -438,8 +443,7 @@ static void backward_softmax_ce(AGNode *n) {
     if (!seed || !gl) return;
     Tensor *t = tt_empty_like(a->val);
     if (!t) return;
-    /* outer product (rows*cols x 1) * (1 x 1) scales the seed by dL on device */
-    if (tt_k_gemm((int)t->numel, 1, 1, seed, 1, 0, gl, 1, 0, t->dev, 1)) {
+    if (tt_k_scale_by_dev(seed, gl, t->dev, t->numel)) {
         tt_release(t);
         return;
     }
@@ -557,6 +561,28 @@ void ag_backward_from_tensor(AGNode *out, const Tensor *seed) {
     if (!out || !out->requires_grad || !seed) return;
     if (!out->val || seed->numel != out->val->numel) return;
     backward_impl(out, 2, NULL, seed);
+}
+
+int ag_sgd_step_many(AGNode *const *leaves, int count, float lr) {
+    if (count < 0 || (count > 0 && !leaves)) return -1;
+    for (int base = 0; base < count; base += TT_SGD_MAX) {
+        float *w[TT_SGD_MAX];
+        const float *g[TT_SGD_MAX];
+        long n[TT_SGD_MAX];
+        int k = 0;
+        for (int i = base; i < count && i < base + TT_SGD_MAX; i++) {
+            AGNode *l = leaves[i];
+            if (!l || !l->grad) continue;
+            w[k] = tt_dev(l->val);
+            g[k] = tt_dev(l->grad);
+            if (!w[k] || !g[k]) return -1;
+            n[k] = l->val->numel;
+            tt_mark_dev_written(l->val);
+            k++;
+        }
+        if (tt_k_sgd_multi(w, g, n, k, lr)) return -1;
+    }
+    return 0;
 }
 
 int ag_sgd_step(AGNode *leaf, float lr) {

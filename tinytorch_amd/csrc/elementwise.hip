@@ -228,22 +228,85 @@ __global__ void softmax_ce_kernel(const float *__restrict__ x, const int32_t *__
   for (int j = 0; j < cols; j++) seed[r * cols + j] = (pr[j] - (j == y ? 1.0f : 0.0f)) * scale;
 }
 
+template <typename I>
 __global__ void padones_fwd_kernel(const float *__restrict__ x, float *__restrict__ y, long M, long K) {
-  const long total = M * (K + 1);
-  const long stride = (long)gridDim.x * blockDim.x;
-  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-    const long m = i / (K + 1), k = i - m * (K + 1);
-    y[i] = k < K ? x[m * K + k] : 1.0f;
+  const I total = (I)(M * (K + 1));
+  const I K1 = (I)(K + 1);
+  const I stride = (I)gridDim.x * blockDim.x;
+  for (I i = (I)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const I m = i / K1, k = i - m * K1;
+    y[i] = k < (I)K ? x[(long)m * K + k] : 1.0f;
   }
 }
 
+template <typename I>
 __global__ void padones_bwd_kernel(const float *__restrict__ g, float *__restrict__ dx, long M, long K) {
-  const long total = M * K;
-  const long stride = (long)gridDim.x * blockDim.x;
-  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-    const long m = i / K, k = i - m * K;
-    dx[i] = g[m * (K + 1) + k];
+  const I total = (I)(M * K);
+  const I stride = (I)gridDim.x * blockDim.x;
+  for (I i = (I)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const I m = i / (I)K, k = i - m * (I)K;
+    dx[i] = g[(long)m * (K + 1) + k];
   }
+}
+
+// Fused softmax + cross-entropy for up to a few thousand rows in ONE
+// workgroup: probabilities, the seed (p - onehot(y)) * scale and the mean
+// loss, reduced in a fixed order (per-thread row order, then the thread
+// partials through LDS in index order).
+__global__ void softmax_ce_mean_kernel(const float *__restrict__ x, const int32_t *__restrict__ lab,
+                                       float *__restrict__ probs, float *__restrict__ loss_mean,
+                                       float *__restrict__ seed, int rows, int cols, float scale) {
+  __shared__ float part[256];
+  float acc = 0.0f;
+  for (int r = threadIdx.x; r < rows; r += blockDim.x) {
+    const float *xr = x + (long)r * cols;
+    float *pr = probs + (long)r * cols;
+    float mx = -INFINITY;
+    for (int j = 0; j < cols; j++) { const float v = xr[j]; if (v > mx) mx = v; }
+    if (mx == -INFINITY) {
+      for (int j = 0; j < cols; j++) pr[j] = 1.0f / (float)cols;
+    } else {
+      float sum = 0.0f;
+      for (int j = 0; j < cols; j++) { const float e = expf(xr[j] - mx); pr[j] = e; sum += e; }
+      for (int j = 0; j < cols; j++) pr[j] = pr[j] / sum;
+    }
+    const int y = lab[r];
+    const float py = (y >= 0 && y < cols) ? pr[y] : 0.0f;
+    acc += -logf(fmaxf(py, 1e-12f));
+    for (int j = 0; j < cols; j++) seed[(long)r * cols + j] = (pr[j] - (j == y ? 1.0f : 0.0f)) * scale;
+  }
+  part[threadIdx.x] = acc;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) part[threadIdx.x] += part[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) loss_mean[0] = part[0] / (float)rows;
+}
+
+// y = x * s[0] with s a device scalar (the incoming gradient of a scalar loss)
+__global__ void scale_by_dev_kernel(const float *__restrict__ x, const float *__restrict__ s,
+                                    float *__restrict__ y, long n) {
+  const float k = s[0];
+  const long stride = (long)gridDim.x * blockDim.x;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) y[i] = x[i] * k;
+}
+
+// w_i -= lr * g_i for up to TT_SGD_MAX tensors in one launch: blockIdx.y
+// selects the tensor.
+struct SgdList {
+  float *w[TT_SGD_MAX];
+  const float *g[TT_SGD_MAX];
+  long n[TT_SGD_MAX];
+};
+
+__global__ void sgd_multi_kernel(SgdList L, float lr) {
+  const int t = blockIdx.y;
+  float *w = L.w[t];
+  const float *g = L.g[t];
+  const long n = L.n[t];
+  const long stride = (long)gridDim.x * blockDim.x;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) w[i] -= lr * g[i];
 }
 
 }  // namespace
@@ -303,14 +366,52 @@ int tt_k_softmax_ce(const float *logits, const int32_t *labels, float *probs, fl
 
 int tt_k_padones_fwd(const float *x, float *y, long M, long K) {
   if (M <= 0 || K < 0) return 0;
-  hipLaunchKernelGGL(padones_fwd_kernel, dim3(grid_for(M * (K + 1), 1)), dim3(256), 0, stream(), x, y,
-                     M, K);
+  const long total = M * (K + 1);
+  if (total < (1L << 31))
+    hipLaunchKernelGGL(padones_fwd_kernel<unsigned>, dim3(grid_for(total, 1)), dim3(256), 0, stream(), x, y, M, K);
+  else
+    hipLaunchKernelGGL(padones_fwd_kernel<unsigned long>, dim3(grid_for(total, 1)), dim3(256), 0, stream(), x, y, M, K);
   return launched();
 }
 
 int tt_k_padones_bwd(const float *g, float *dx, long M, long K) {
   if (M <= 0 || K <= 0) return 0;
-  hipLaunchKernelGGL(padones_bwd_kernel, dim3(grid_for(M * K, 1)), dim3(256), 0, stream(), g, dx, M, K);
+  const long total = M * K;
+  if (total < (1L << 31))
+    hipLaunchKernelGGL(padones_bwd_kernel<unsigned>, dim3(grid_for(total, 1)), dim3(256), 0, stream(), g, dx, M, K);
+  else
+    hipLaunchKernelGGL(padones_bwd_kernel<unsigned long>, dim3(grid_for(total, 1)), dim3(256), 0, stream(), g, dx, M, K);
+  return launched();
+}
+
+int tt_k_softmax_ce_mean(const float *logits, const int32_t *labels, float *probs, float *loss_mean,
+                         float *seed, long rows, int cols, float scale) {
+  if (rows <= 0 || cols <= 0 || rows > TT_CE_MEAN_MAX_ROWS) return -1;
+  hipLaunchKernelGGL(softmax_ce_mean_kernel, dim3(1), dim3(256), 0, stream(), logits, labels, probs,
+                     loss_mean, seed, (int)rows, cols, scale);
+  return launched();
+}
+
+int tt_k_scale_by_dev(const float *x, const float *s, float *y, long n) {
+  if (n <= 0) return 0;
+  hipLaunchKernelGGL(scale_by_dev_kernel, dim3(grid_for(n, 1)), dim3(256), 0, stream(), x, s, y, n);
+  return launched();
+}
+
+int tt_k_sgd_multi(float *const *w, const float *const *g, const long *n, int count, float lr) {
+  if (count < 0 || count > TT_SGD_MAX) return -1;
+  if (count == 0) return 0;
+  SgdList L;
+  long nmax = 0;
+  for (int i = 0; i < count; i++) {
+    L.w[i] = w[i];
+    L.g[i] = g[i];
+    L.n[i] = n[i];
+    if (n[i] > nmax) nmax = n[i];
+  }
+  for (int i = count; i < TT_SGD_MAX; i++) { L.w[i] = nullptr; L.g[i] = nullptr; L.n[i] = 0; }
+  if (nmax <= 0) return 0;
+  hipLaunchKernelGGL(sgd_multi_kernel, dim3(grid_for(nmax, 1), count), dim3(256), 0, stream(), L, lr);
   return launched();
 }
 

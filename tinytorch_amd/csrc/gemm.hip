@@ -35,6 +35,7 @@
 //     splits in a fixed order (deterministic, no atomics).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include "tt_rt.h"
 
 namespace {
@@ -58,11 +59,15 @@ struct Opnd {
   int hw;
 };
 
+// Contiguous indices are below 2^31 (checked at launch), so the permuted
+// split uses 32-bit unsigned division -- 64-bit division is a long software
+// sequence on the GPU.
 template <bool PERM>
 __device__ __forceinline__ long cidx(const Opnd &o, long i) {
   if constexpr (PERM) {
-    long q = i / o.hw;
-    return q * o.img + (i - q * o.hw);
+    const unsigned ui = (unsigned)i, hw = (unsigned)o.hw;
+    const unsigned q = ui / hw;
+    return (long)q * o.img + (long)(ui - q * hw);
   } else {
     return i;
   }
@@ -86,11 +91,12 @@ __device__ __forceinline__ float4 load4(const Opnd &o, long row, long rows, long
   return v;
 }
 
-template <int BM, int BN, int BK, bool A_KC, bool A_PERM, bool B_NC, bool B_PERM,
+template <int BM, int BN, int BK, int WM, bool A_KC, bool A_PERM, bool B_NC, bool B_PERM,
           bool VEC, int EPI>
 struct Cfg {
-  static constexpr int MI = BM / 64;            // 32x32 blocks per wave along m
-  static constexpr int NI = BN / 64;            // ... along n
+  static constexpr int WN = 4 / WM;             // wave grid WM x WN
+  static constexpr int MI = BM / (32 * WM);     // 32x32 blocks per wave along m
+  static constexpr int NI = BN / (32 * WN);     // ... along n
   static constexpr int A_ROWS = A_KC ? BM : BK; // stored rows of the LDS A tile
   static constexpr int A_LD = A_KC ? BK + 4 : BM + 8;
   static constexpr int B_ROWS = B_NC ? BK : BN;
@@ -101,15 +107,16 @@ struct Cfg {
   static constexpr int A_V4 = BM * BK / 4 / NT;  // float4 loads per thread
   static constexpr int B_V4 = BN * BK / 4 / NT;
   static_assert(A_V4 >= 1 && B_V4 >= 1, "tile too small for 256 threads");
-  static_assert(BM % 64 == 0 && BN % 64 == 0 && BK % 8 == 0, "tile shape");
+  static_assert(MI >= 1 && NI >= 1 && BM % (32 * WM) == 0 && BN % (32 * WN) == 0 && BK % 8 == 0,
+                "tile shape");
 };
 
-template <int BM, int BN, int BK, bool A_KC, bool A_PERM, bool B_NC, bool B_PERM,
+template <int BM, int BN, int BK, int WM, bool A_KC, bool A_PERM, bool B_NC, bool B_PERM,
           bool VEC, int EPI>
 __global__ void __launch_bounds__(NT)
 gemm_mfma_kernel(int M, int N, int K, Opnd A, Opnd B, float *__restrict__ C, long ldc,
                  long split_stride, int kchunk, const float *__restrict__ bias, int HW) {
-  using G = Cfg<BM, BN, BK, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI>;
+  using G = Cfg<BM, BN, BK, WM, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI>;
   __shared__ __attribute__((aligned(16))) float smem[2 * G::STAGE];
 
   const int tid = threadIdx.x;
@@ -137,8 +144,8 @@ gemm_mfma_kernel(int M, int N, int K, Opnd A, Opnd B, float *__restrict__ C, lon
   const int nk = (kend - kbeg + BK - 1) / BK;
   C += (long)blockIdx.z * split_stride;
 
-  const int wm = (wave >> 1) * (BM / 2);
-  const int wn = (wave & 1) * (BN / 2);
+  const int wm = (wave / G::WN) * (BM / WM);
+  const int wn = (wave % G::WN) * (BN / G::WN);
 
   f32x16 acc[G::MI][G::NI];
 #pragma unroll
@@ -256,7 +263,11 @@ gemm_mfma_kernel(int M, int N, int K, Opnd A, Opnd B, float *__restrict__ C, lon
       const long col = n0 + wn + 32 * j + l32;
       if (col >= N) continue;
       long img = 0, hw = 0;
-      if constexpr (EPI == EPI_BIAS_NCHW) { img = col / HW; hw = col - img * HW; }
+      if constexpr (EPI == EPI_BIAS_NCHW) {
+        const unsigned q = (unsigned)col / (unsigned)HW;
+        img = q;
+        hw = (long)((unsigned)col - q * (unsigned)HW);
+      }
 #pragma unroll
       for (int r = 0; r < 16; r++) {
         const long row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
@@ -285,7 +296,8 @@ __global__ void splitk_reduce_kernel(const float *__restrict__ ws, float *__rest
     if constexpr (EPI == EPI_STORE) {
       C[row * ldc + col] = s;
     } else {
-      const long img = col / HW, hw = col - img * HW;
+      const unsigned q = (unsigned)col / (unsigned)HW;
+      const long img = q, hw = (long)((unsigned)col - q * (unsigned)HW);
       C[(img * M + row) * HW + hw] = s + (bias ? bias[row] : 0.f);
     }
   }
@@ -295,27 +307,43 @@ inline hipStream_t stream() { return (hipStream_t)ttrt_stream(); }
 
 inline bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
+// Tile configurations (BM x BN, wave grid WM x 4/WM).
+enum Tile { T128x128 = 0, T128x64, T64x64, T32x256, T64x256, NTILE };
+constexpr int TILE_BM[NTILE] = {128, 128, 64, 32, 64};
+constexpr int TILE_BN[NTILE] = {128, 64, 64, 256, 256};
+
 struct Plan {
-  int bm, bn, splits, kchunk;
+  int tile, splits, kchunk;
 };
 
-// Pick a tile and a split count so that the launch covers the 256 CUs.
+inline long ntiles(int t, int M, int N) {
+  return (long)((M + TILE_BM[t] - 1) / TILE_BM[t]) * ((N + TILE_BN[t] - 1) / TILE_BN[t]);
+}
+
+// Pick a tile that wastes little of the output and a split count so that the
+// launch covers the 256 CUs.  TT_GEMM_TILE / TT_GEMM_SPLITS (environment)
+// force a choice, for tuning sweeps.
 Plan plan(int M, int N, int K) {
   const int CUS = 256;
-  Plan p{128, 128, 1, K};
-  const long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
-  if (N <= 64) {
-    p.bn = 64;  // skinny N: 128x64 tiles keep the whole tile useful
-    if ((long)((M + 127) / 128) < CUS) p.bm = 64;
-  } else if (t128 < CUS) {
-    p.bm = 64; p.bn = 64;
+  Plan p{T128x128, 1, K};
+  if (M <= 32 && N >= 1024) p.tile = T32x256;          // F x (N*Ho*Wo) conv shapes
+  else if (M <= 64 && N >= 2048) p.tile = T64x256;
+  else if (N <= 64) p.tile = ntiles(T128x64, M, N) >= CUS ? T128x64 : T64x64;
+  else if (ntiles(T128x128, M, N) < CUS) p.tile = T64x64;
+  static int force_tile = -2, force_splits = -2;
+  if (force_tile == -2) {
+    const char *e = getenv("TT_GEMM_TILE");
+    force_tile = (e && *e) ? atoi(e) : -1;
+    e = getenv("TT_GEMM_SPLITS");
+    force_splits = (e && *e) ? atoi(e) : -1;
   }
-  long tiles = (long)((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn);
-  // split K while the grid is under ~2 waves of CUs and each split keeps
-  // at least 256 k (8 K tiles of 32)
+  if (force_tile >= 0 && force_tile < NTILE) p.tile = force_tile;
+  const long tiles = ntiles(p.tile, M, N);
+  // split K while the grid holds fewer than ~2 workgroups per CU and every
+  // split keeps at least 128 k (4 K tiles)
   int s = 1;
-  while (tiles * s * 2 <= 2L * CUS && (long)K / (s * 2) >= 256 && s < 64) s *= 2;
-  p.splits = s;
+  while (tiles * s < 2L * CUS && (long)K / (s * 2) >= 128 && s < 256) s *= 2;
+  if (force_splits >= 1) s = force_splits;
   int kc = (K + s - 1) / s;
   kc = (kc + 31) / 32 * 32;
   p.kchunk = kc;
@@ -323,12 +351,13 @@ Plan plan(int M, int N, int K) {
   return p;
 }
 
-template <int BM, int BN, bool A_KC, bool A_PERM, bool B_NC, bool B_PERM, bool VEC, int EPI>
+template <int BM, int BN, int WM, bool A_KC, bool A_PERM, bool B_NC, bool B_PERM, bool VEC,
+          int EPI>
 void launch_tile(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ldc,
                  long split_stride, int splits, int kchunk, const float *bias, int HW) {
   const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   dim3 grid(tiles, 1, splits);
-  hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, 32, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI>),
+  hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, 32, WM, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI>),
                      grid, dim3(NT), 0, stream(), M, N, K, A, B, C, ldc, split_stride, kchunk,
                      bias, HW);
 }
@@ -351,20 +380,23 @@ int run(int M, int N, int K, Opnd A, Opnd B, float *C, long ldc, const float *bi
     epi_direct = 0;
   }
   const long sstride = (long)M * N;
-#define TT_LAUNCH(BM_, BN_, VEC_, EPI_)                                                     \
-  launch_tile<BM_, BN_, A_KC, A_PERM, B_NC, B_PERM, VEC_, EPI_>(M, N, K, A, B, target,      \
-                                                                tgt_ld, sstride, p.splits, \
-                                                                p.kchunk, bias, HW)
-#define TT_SHAPES(EPI_)                                                          \
-  if (p.bm == 128 && p.bn == 128) {                                              \
-    if (vec) TT_LAUNCH(128, 128, true, EPI_); else TT_LAUNCH(128, 128, false, EPI_); \
-  } else if (p.bm == 128) {                                                      \
-    if (vec) TT_LAUNCH(128, 64, true, EPI_); else TT_LAUNCH(128, 64, false, EPI_);   \
-  } else {                                                                       \
-    if (vec) TT_LAUNCH(64, 64, true, EPI_); else TT_LAUNCH(64, 64, false, EPI_);     \
+#define TT_LAUNCH(BM_, BN_, WM_, VEC_, EPI_)                                                  \
+  launch_tile<BM_, BN_, WM_, A_KC, A_PERM, B_NC, B_PERM, VEC_, EPI_>(                         \
+      M, N, K, A, B, target, tgt_ld, sstride, p.splits, p.kchunk, bias, HW)
+#define TT_VEC(BM_, BN_, WM_, EPI_)                 \
+  if (vec) TT_LAUNCH(BM_, BN_, WM_, true, EPI_);     \
+  else TT_LAUNCH(BM_, BN_, WM_, false, EPI_);
+#define TT_SHAPES(EPI_)                                     \
+  switch (p.tile) {                                         \
+    case T128x128: TT_VEC(128, 128, 2, EPI_) break;         \
+    case T128x64:  TT_VEC(128, 64, 2, EPI_) break;          \
+    case T64x64:   TT_VEC(64, 64, 2, EPI_) break;           \
+    case T32x256:  TT_VEC(32, 256, 1, EPI_) break;          \
+    default:       TT_VEC(64, 256, 1, EPI_) break;          \
   }
   if (epi_direct) { TT_SHAPES(EPI) } else { TT_SHAPES(EPI_STORE) }
 #undef TT_SHAPES
+#undef TT_VEC
 #undef TT_LAUNCH
   if (hipGetLastError() != hipSuccess) { if (ws) ttrt_free(ws); return -3; }
   if (ws) {
