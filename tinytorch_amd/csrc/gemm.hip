@@ -283,23 +283,32 @@ gemm_mfma_kernel(int M, int N, int K, Opnd A, Opnd B, float *__restrict__ C, lon
 }
 
 // Deterministic split-K reduction: out = sum_{z=0..S-1} ws[z] (+ epilogue).
-template <int EPI>
-__global__ void splitk_reduce_kernel(const float *__restrict__ ws, float *__restrict__ C,
-                                     int M, int N, int S, long ldc,
-                                     const float *__restrict__ bias, int HW) {
+// A workgroup is XL outputs x ZL split-lanes (XL*ZL = 256): lane ty adds
+// z = ty, ty+ZL, ... in order, then lane ty == 0 adds the ZL lane sums in
+// order.  Small outputs with many splits (conv dW, K = N*Ho*Wo) use wide ZL
+// so that hundreds of waves share the reduction.
+template <int EPI, int ZL>
+__global__ void __launch_bounds__(256)
+splitk_reduce_kernel(const float *__restrict__ ws, float *__restrict__ C, int M, int N, int S,
+                     long ldc, const float *__restrict__ bias, int HW) {
+  constexpr int XL = 256 / ZL;
+  __shared__ float part[ZL][XL];
+  const int tx = threadIdx.x % XL, ty = threadIdx.x / XL;
   const long total = (long)M * N;
-  const long stride = (long)gridDim.x * blockDim.x;
-  for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += stride) {
-    float s = 0.f;
-    for (int z = 0; z < S; z++) s += ws[z * total + idx];
-    const long row = idx / N, col = idx - row * N;
-    if constexpr (EPI == EPI_STORE) {
-      C[row * ldc + col] = s;
-    } else {
-      const unsigned q = (unsigned)col / (unsigned)HW;
-      const long img = q, hw = (long)((unsigned)col - q * (unsigned)HW);
-      C[(img * M + row) * HW + hw] = s + (bias ? bias[row] : 0.f);
-    }
+  const long idx = (long)blockIdx.x * XL + tx;
+  float s = 0.f;
+  if (idx < total)
+    for (int z = ty; z < S; z += ZL) s += ws[z * total + idx];
+  part[ty][tx] = s;
+  __syncthreads();
+  if (ty != 0 || idx >= total) return;
+  for (int j = 1; j < ZL; j++) s += part[j][tx];
+  const unsigned row = (unsigned)(idx / N), col = (unsigned)(idx - (long)row * N);
+  if constexpr (EPI == EPI_STORE) {
+    C[(long)row * ldc + col] = s;
+  } else {
+    const unsigned q = col / (unsigned)HW;
+    C[((long)q * M + row) * HW + (col - q * (unsigned)HW)] = s + (bias ? bias[row] : 0.f);
   }
 }
 
@@ -340,9 +349,10 @@ Plan plan(int M, int N, int K) {
   if (force_tile >= 0 && force_tile < NTILE) p.tile = force_tile;
   const long tiles = ntiles(p.tile, M, N);
   // split K while the grid holds fewer than ~2 workgroups per CU and every
-  // split keeps at least 128 k (4 K tiles)
+  // split keeps at least 256 k (8 K tiles): shorter splits cost more in the
+  // reduction than they gain
   int s = 1;
-  while (tiles * s < 2L * CUS && (long)K / (s * 2) >= 128 && s < 256) s *= 2;
+  while (tiles * s < 2L * CUS && (long)K / (s * 2) >= 256 && s < 256) s *= 2;
   if (force_splits >= 1) s = force_splits;
   int kc = (K + s - 1) / s;
   kc = (kc + 31) / 32 * 32;
@@ -401,10 +411,23 @@ int run(int M, int N, int K, Opnd A, Opnd B, float *C, long ldc, const float *bi
   if (hipGetLastError() != hipSuccess) { if (ws) ttrt_free(ws); return -3; }
   if (ws) {
     const long total = (long)M * N;
-    int blocks = (int)((total + 255) / 256);
-    if (blocks > 4096) blocks = 4096;
-    hipLaunchKernelGGL(splitk_reduce_kernel<EPI>, dim3(blocks), dim3(256), 0, stream(), ws, C,
-                       M, N, p.splits, ldc, bias, HW);
+    // as many split-lanes as keep >= ~512 waves busy (at most 32, at most S)
+    int zl = 1;
+    while (zl < 32 && zl < p.splits && (total * zl * 2) <= 512L * 64) zl *= 2;
+    if (zl < 4 && p.splits >= 4) zl = 4;
+#define TT_RED(ZL_)                                                                            \
+  hipLaunchKernelGGL((splitk_reduce_kernel<EPI, ZL_>), dim3((unsigned)((total + 256 / ZL_ - 1) / \
+                                                                      (256 / ZL_))),            \
+                     dim3(256), 0, stream(), ws, C, M, N, p.splits, ldc, bias, HW)
+    switch (zl) {
+      case 1: TT_RED(1); break;
+      case 2: TT_RED(2); break;
+      case 4: TT_RED(4); break;
+      case 8: TT_RED(8); break;
+      case 16: TT_RED(16); break;
+      default: TT_RED(32); break;
+    }
+#undef TT_RED
     ttrt_free(ws);
     if (hipGetLastError() != hipSuccess) return -3;
   }
