@@ -130,8 +130,20 @@ class Gemm:
             b.free()
 
 
+def prewarm(fn, seconds=0.3):
+    """Untimed device warm-up: the GPU leaves its idle clocks only after some
+    milliseconds of sustained work (first launches after idle run ~40% slower)."""
+    from tinytorch_amd.hip import sync
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(4):
+            fn()
+        sync()
+
+
 def time_gemm(L, g, steps, warmup):
     from tinytorch_amd.hip import StreamTimer, sync
+    prewarm(g.launch)
     for _ in range(warmup):
         g.launch()
     sync()
@@ -228,6 +240,7 @@ class MlpStep:
 
 def time_steps(stepper, steps, warmup):
     from tinytorch_amd.hip import sync
+    prewarm(stepper.step)
     for _ in range(warmup):
         stepper.step()
     sync()
@@ -328,7 +341,7 @@ def main():
                 "sgemm_ragged_1000x1003x997": (1000, 1003, 997, 0, 0),
                 "sgemm_tall_65536x64x4096": (65536, 64, 4096, 0, 0)}.items():
             gg = Gemm(L, M, N, K, ta, tb)
-            steps = max(3, min(args.steps, int(2e12 / gg.flops()) + 3))
+            steps = max(10, min(200, int(3e12 / gg.flops())))
             _, ms = time_gemm(L, gg, steps, 2)
             extra[name] = dict(tflops=round(gg.flops() / (ms * 1e-3) / 1e12, 2),
                                ms=round(ms, 4),

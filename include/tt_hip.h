@@ -54,6 +54,11 @@ int tt_k_gemm(int M, int N, int K,
               const float *B, int ldb, int transB,
               float *C, int ldc);
 
+/* Tuning hook: force the GEMM tile (0: 128x128, 1: 128x64, 2: 64x64, 3: 32x256,
+ * 4: 64x256, 5: 256x256, 6: 256x128) and/or split-K count for every later
+ * call; -1 restores the automatic choice. */
+int tth_gemm_config(int tile, int splits);
+
 /* Convolution GEMMs over the im2col matrix col[(c,kh,kw)][(n,ho,wo)]
  * (Kc = C*HH*WW rows, Ncol = N*Ho*Wo columns, HW = Ho*Wo):
  *   conv_fwd : out[n][f][hw] = sum_c W[f][c] col[c][p] + bias[f] (bias may be NULL)

@@ -91,6 +91,31 @@ __device__ __forceinline__ float4 load4(const Opnd &o, long row, long rows, long
   return v;
 }
 
+// W consecutive floats from LDS (16/8/4-byte aligned) into t[0..W-1]
+template <int W>
+__device__ __forceinline__ void ldsvec(float *t, const float *p) {
+  if constexpr (W == 4) {
+    const float4 v = *reinterpret_cast<const float4 *>(p);
+    t[0] = v.x; t[1] = v.y; t[2] = v.z; t[3] = v.w;
+  } else if constexpr (W == 2) {
+    const float2 v = *reinterpret_cast<const float2 *>(p);
+    t[0] = v.x; t[1] = v.y;
+  } else {
+    t[0] = p[0];
+  }
+}
+
+template <int W>
+__device__ __forceinline__ void stvec(float *p, const float *v) {
+  if constexpr (W == 4) {
+    *reinterpret_cast<float4 *>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  } else if constexpr (W == 2) {
+    *reinterpret_cast<float2 *>(p) = make_float2(v[0], v[1]);
+  } else {
+    p[0] = v[0];
+  }
+}
+
 template <int BM, int BN, int BK, int WM, bool A_KC, bool A_PERM, bool B_NC, bool B_PERM,
           bool VEC, int EPI>
 struct Cfg {
@@ -109,15 +134,17 @@ struct Cfg {
   static_assert(A_V4 >= 1 && B_V4 >= 1, "tile too small for 256 threads");
   static_assert(MI >= 1 && NI >= 1 && BM % (32 * WM) == 0 && BN % (32 * WN) == 0 && BK % 8 == 0,
                 "tile shape");
+  static_assert(MI == 1 || MI == 2 || MI == 4, "MI must be 1, 2 or 4");
+  static_assert(NI == 1 || NI == 2 || NI == 4, "NI must be 1, 2 or 4");
 };
 
 template <int BM, int BN, int BK, int WM, bool A_KC, bool A_PERM, bool B_NC, bool B_PERM,
           bool VEC, int EPI>
-__global__ void __launch_bounds__(NT)
-gemm_mfma_kernel(int M, int N, int K, Opnd A, Opnd B, float *__restrict__ C, long ldc,
-                 long split_stride, int kchunk, const float *__restrict__ bias, int HW) {
+__device__ __forceinline__ void gemm_body(float *smem, int M, int N, int K, const Opnd &A,
+                                          const Opnd &B, float *__restrict__ C, long ldc,
+                                          long split_stride, int kchunk,
+                                          const float *__restrict__ bias, int HW, bool cvec) {
   using G = Cfg<BM, BN, BK, WM, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI>;
-  __shared__ __attribute__((aligned(16))) float smem[2 * G::STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -157,8 +184,51 @@ gemm_mfma_kernel(int M, int N, int K, Opnd A, Opnd B, float *__restrict__ C, lon
 
   float4 ra[G::A_V4], rb[G::B_V4];
 
+  // Interior tiles of unpermuted, 16-byte aligned operands take a branch-free
+  // path: per-thread element offsets are fixed for the whole K loop and
+  // advance by a uniform stride per K tile.  Edge tiles and permuted
+  // operands use the bounds-checked loads.
+  constexpr bool FAST_OK = VEC && !A_PERM && !B_PERM;
+  const bool interior = FAST_OK && (m0 + BM <= M) && (n0 + BN <= N);
+  long aoff[G::A_V4], boff[G::B_V4];
+  if constexpr (FAST_OK) {
+#pragma unroll
+    for (int v = 0; v < G::A_V4; v++) {
+      const int q = tid + v * NT;
+      if constexpr (A_KC) {
+        const int r = q / (BK / 4), c = (q % (BK / 4)) * 4;
+        aoff[v] = (m0 + r) * A.ld + kbeg + c;
+      } else {
+        const int r = q / (BM / 4), c = (q % (BM / 4)) * 4;
+        aoff[v] = (long)(kbeg + r) * A.ld + m0 + c;
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < G::B_V4; v++) {
+      const int q = tid + v * NT;
+      if constexpr (B_NC) {
+        const int r = q / (BN / 4), c = (q % (BN / 4)) * 4;
+        boff[v] = (long)(kbeg + r) * B.ld + n0 + c;
+      } else {
+        const int r = q / (BK / 4), c = (q % (BK / 4)) * 4;
+        boff[v] = (n0 + r) * B.ld + kbeg + c;
+      }
+    }
+  }
+
   auto gload = [&](int kt) {
     const long k0 = kbeg + (long)kt * BK;
+    if (FAST_OK && interior && k0 + BK <= kend) {
+      const long astep = A_KC ? (long)kt * BK : (long)kt * BK * A.ld;
+      const long bstep = B_NC ? (long)kt * BK * B.ld : (long)kt * BK;
+#pragma unroll
+      for (int v = 0; v < G::A_V4; v++)
+        ra[v] = *reinterpret_cast<const float4 *>(A.p + aoff[v] + astep);
+#pragma unroll
+      for (int v = 0; v < G::B_V4; v++)
+        rb[v] = *reinterpret_cast<const float4 *>(B.p + boff[v] + bstep);
+      return;
+    }
 #pragma unroll
     for (int v = 0; v < G::A_V4; v++) {
       const int q = tid + v * NT;
@@ -204,31 +274,44 @@ gemm_mfma_kernel(int M, int N, int K, Opnd A, Opnd B, float *__restrict__ C, lon
     }
   };
 
+  // Operand fragments.  A k-contiguous operand is read as one float4 of 4 k
+  // per 32-row block.  An m- (n-) contiguous operand is read as one vector of
+  // MI (NI) consecutive m (n) per k: lane l32 then feeds row/column l32 of
+  // block i (j) with element MI*l32 + i (NI*l32 + j), i.e. the blocks are
+  // interleaved in m (n) and the epilogue maps them back.
   auto compute = [&](int buf) {
     const float *sA = smem + buf * G::STAGE;
     const float *sB = sA + G::A_SZ;
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 8) {
       float a[G::MI][4], b[G::NI][4];
+      if constexpr (A_KC) {
 #pragma unroll
-      for (int i = 0; i < G::MI; i++) {
-        const int m = wm + 32 * i + l32;
-        if constexpr (A_KC) {
-          const float4 t = *reinterpret_cast<const float4 *>(sA + m * G::A_LD + kk + 4 * g);
+        for (int i = 0; i < G::MI; i++) {
+          const float4 t = *reinterpret_cast<const float4 *>(sA + (wm + 32 * i + l32) * G::A_LD + kk + 4 * g);
           a[i][0] = t.x; a[i][1] = t.y; a[i][2] = t.z; a[i][3] = t.w;
-        } else {
+        }
+      } else {
 #pragma unroll
-          for (int s = 0; s < 4; s++) a[i][s] = sA[(kk + 4 * g + s) * G::A_LD + m];
+        for (int s = 0; s < 4; s++) {
+          float t[G::MI];
+          ldsvec<G::MI>(t, sA + (kk + 4 * g + s) * G::A_LD + wm + G::MI * l32);
+#pragma unroll
+          for (int i = 0; i < G::MI; i++) a[i][s] = t[i];
         }
       }
+      if constexpr (B_NC) {
 #pragma unroll
-      for (int j = 0; j < G::NI; j++) {
-        const int n = wn + 32 * j + l32;
-        if constexpr (B_NC) {
+        for (int s = 0; s < 4; s++) {
+          float t[G::NI];
+          ldsvec<G::NI>(t, sB + (kk + 4 * g + s) * G::B_LD + wn + G::NI * l32);
 #pragma unroll
-          for (int s = 0; s < 4; s++) b[j][s] = sB[(kk + 4 * g + s) * G::B_LD + n];
-        } else {
-          const float4 t = *reinterpret_cast<const float4 *>(sB + n * G::B_LD + kk + 4 * g);
+          for (int j = 0; j < G::NI; j++) b[j][s] = t[j];
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < G::NI; j++) {
+          const float4 t = *reinterpret_cast<const float4 *>(sB + (wn + 32 * j + l32) * G::B_LD + kk + 4 * g);
           b[j][0] = t.x; b[j][1] = t.y; b[j][2] = t.z; b[j][3] = t.w;
         }
       }
@@ -256,30 +339,87 @@ gemm_mfma_kernel(int M, int N, int K, Opnd A, Opnd B, float *__restrict__ C, lon
   }
 
   // ---- epilogue ----
+  // block i row rho (acc r: rho = 8*(r/4) + 4*g + r%4) is m = wm + 32*i + rho
+  // (k-contiguous A) or wm + MI*rho + i (interleaved A); block j column l32
+  // is n = wn + 32*j + l32 or wn + NI*l32 + j (interleaved B).  With
+  // interleaved B a lane owns NI adjacent columns and stores them as one vector.
 #pragma unroll
   for (int i = 0; i < G::MI; i++)
 #pragma unroll
-    for (int j = 0; j < G::NI; j++) {
-      const long col = n0 + wn + 32 * j + l32;
-      if (col >= N) continue;
-      long img = 0, hw = 0;
-      if constexpr (EPI == EPI_BIAS_NCHW) {
-        const unsigned q = (unsigned)col / (unsigned)HW;
-        img = q;
-        hw = (long)((unsigned)col - q * (unsigned)HW);
-      }
+    for (int r = 0; r < 16; r++) {
+      const int rho = 8 * (r >> 2) + 4 * g + (r & 3);
+      const long row = m0 + (A_KC ? wm + 32 * i + rho : wm + G::MI * rho + i);
+      if (row >= M) continue;
+      const float bv = (EPI == EPI_BIAS_NCHW && bias) ? bias[row] : 0.f;
+      if constexpr (B_NC) {
+        const long col0 = n0 + wn + G::NI * l32;
+        float v[G::NI];
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const long row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (row >= M) continue;
-        const float v = acc[i][j][r];
+        for (int j = 0; j < G::NI; j++) v[j] = acc[i][j][r] + bv;
         if constexpr (EPI == EPI_STORE) {
-          C[row * ldc + col] = v;
+          if (cvec && col0 + G::NI <= N) {
+            stvec<G::NI>(C + row * ldc + col0, v);
+          } else {
+#pragma unroll
+            for (int j = 0; j < G::NI; j++)
+              if (col0 + j < N) C[row * ldc + col0 + j] = v[j];
+          }
         } else {
-          C[(img * M + row) * HW + hw] = v + (bias ? bias[row] : 0.f);
+          const unsigned q = (unsigned)col0 / (unsigned)HW;
+          const long hw = (long)((unsigned)col0 - q * (unsigned)HW);
+          if (cvec && col0 + G::NI <= N && hw + G::NI <= HW) {
+            stvec<G::NI>(C + ((long)q * M + row) * HW + hw, v);
+          } else {
+#pragma unroll
+            for (int j = 0; j < G::NI; j++) {
+              const long col = col0 + j;
+              if (col >= N) continue;
+              const unsigned qq = (unsigned)col / (unsigned)HW;
+              C[((long)qq * M + row) * HW + ((unsigned)col - qq * (unsigned)HW)] = v[j];
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < G::NI; j++) {
+          const long col = n0 + wn + 32 * j + l32;
+          if (col >= N) continue;
+          const float v = acc[i][j][r] + bv;
+          if constexpr (EPI == EPI_STORE) {
+            C[row * ldc + col] = v;
+          } else {
+            const unsigned q = (unsigned)col / (unsigned)HW;
+            C[((long)q * M + row) * HW + ((unsigned)col - q * (unsigned)HW)] = v;
+          }
         }
       }
     }
+}
+
+template <int BM, int BN, int BK, int WM, bool A_KC, bool A_PERM, bool B_NC, bool B_PERM,
+          bool VEC, int EPI>
+__global__ void __launch_bounds__(NT)
+gemm_mfma_kernel(int M, int N, int K, Opnd A, Opnd B, float *__restrict__ C, long ldc,
+                 long split_stride, int kchunk, const float *__restrict__ bias, int HW,
+                 bool cvec) {
+  using G = Cfg<BM, BN, BK, WM, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI>;
+  __shared__ __attribute__((aligned(16))) float smem[2 * G::STAGE];
+  gemm_body<BM, BN, BK, WM, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI>(
+      smem, M, N, K, A, B, C, ldc, split_stride, kchunk, bias, HW, cvec);
+}
+
+// The 256x256 tile keeps 256 fp32 accumulators per lane: one wave per SIMD,
+// the whole register file.
+template <int BM, int BN, int BK, int WM, bool A_KC, bool A_PERM, bool B_NC, bool B_PERM,
+          bool VEC, int EPI>
+__global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1)))
+gemm_mfma_big_kernel(int M, int N, int K, Opnd A, Opnd B, float *__restrict__ C, long ldc,
+                     long split_stride, int kchunk, const float *__restrict__ bias, int HW,
+                     bool cvec) {
+  using G = Cfg<BM, BN, BK, WM, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI>;
+  __shared__ __attribute__((aligned(16))) float smem[2 * G::STAGE];
+  gemm_body<BM, BN, BK, WM, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI>(
+      smem, M, N, K, A, B, C, ldc, split_stride, kchunk, bias, HW, cvec);
 }
 
 // Deterministic split-K reduction: out = sum_{z=0..S-1} ws[z] (+ epilogue).
@@ -317,9 +457,12 @@ inline hipStream_t stream() { return (hipStream_t)ttrt_stream(); }
 inline bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 // Tile configurations (BM x BN, wave grid WM x 4/WM).
-enum Tile { T128x128 = 0, T128x64, T64x64, T32x256, T64x256, NTILE };
-constexpr int TILE_BM[NTILE] = {128, 128, 64, 32, 64};
-constexpr int TILE_BN[NTILE] = {128, 64, 64, 256, 256};
+enum Tile { T128x128 = 0, T128x64, T64x64, T32x256, T64x256, T256x256, T256x128, NTILE };
+constexpr int TILE_BM[NTILE] = {128, 128, 64, 32, 64, 256, 256};
+constexpr int TILE_BN[NTILE] = {128, 64, 64, 256, 256, 256, 128};
+
+// tuning override (tth_gemm_config): -1 = automatic
+int g_force_tile = -1, g_force_splits = -1;
 
 struct Plan {
   int tile, splits, kchunk;
@@ -330,30 +473,47 @@ inline long ntiles(int t, int M, int N) {
 }
 
 // Pick a tile that wastes little of the output and a split count so that the
-// launch covers the 256 CUs.  TT_GEMM_TILE / TT_GEMM_SPLITS (environment)
-// force a choice, for tuning sweeps.
+// launch covers the 256 CUs.  tth_gemm_config() forces a choice (tuning).
+// fraction of the padded tile grid that holds real output
+inline double fill(int t, int M, int N) {
+  const double pm = (double)((M + TILE_BM[t] - 1) / TILE_BM[t]) * TILE_BM[t];
+  const double pn = (double)((N + TILE_BN[t] - 1) / TILE_BN[t]) * TILE_BN[t];
+  return (double)M * N / (pm * pn);
+}
+
 Plan plan(int M, int N, int K) {
   const int CUS = 256;
-  Plan p{T128x128, 1, K};
-  if (M <= 32 && N >= 1024) p.tile = T32x256;          // F x (N*Ho*Wo) conv shapes
-  else if (M <= 64 && N >= 2048) p.tile = T64x256;
-  else if (N <= 64) p.tile = ntiles(T128x64, M, N) >= CUS ? T128x64 : T64x64;
-  else if (ntiles(T128x128, M, N) < CUS) p.tile = T64x64;
-  static int force_tile = -2, force_splits = -2;
-  if (force_tile == -2) {
-    const char *e = getenv("TT_GEMM_TILE");
-    force_tile = (e && *e) ? atoi(e) : -1;
-    e = getenv("TT_GEMM_SPLITS");
-    force_splits = (e && *e) ? atoi(e) : -1;
+  Plan p{T64x64, 1, K};
+  // Largest tile that still gives every CU a workgroup and wastes little of
+  // itself on padding; otherwise the small tile that fits the output best
+  // (F x N*Ho*Wo conv shapes have M = 32 or 64).
+  const int big[] = {T256x256, T256x128, T128x128};
+  int chosen = -1;
+  for (int t : big)
+    if (ntiles(t, M, N) >= CUS && fill(t, M, N) >= 0.87) { chosen = t; break; }
+  if (chosen < 0) {
+    const int small[] = {T128x64, T64x64, T32x256, T64x256};
+    double best = -1.0;
+    for (int t : small) {
+      if (t == T128x64 && (N > 64 || ntiles(t, M, N) < CUS)) continue;
+      if (t == T32x256 && M > 32) continue;
+      if (t == T64x256 && M > 64) continue;
+      const double f = fill(t, M, N);
+      if (f > best + 1e-9) { best = f; chosen = t; }
+    }
   }
-  if (force_tile >= 0 && force_tile < NTILE) p.tile = force_tile;
+  p.tile = chosen;
+  if (g_force_tile >= 0 && g_force_tile < NTILE) p.tile = g_force_tile;
   const long tiles = ntiles(p.tile, M, N);
-  // split K while the grid holds fewer than ~2 workgroups per CU and every
-  // split keeps at least 256 k (8 K tiles): shorter splits cost more in the
-  // reduction than they gain
+  // Split K (deterministically reduced afterwards) until the grid fills the
+  // CUs: each K tile of a small GEMM is latency-bound, so parallelism over K
+  // beats a long serial K loop.  Long reductions (conv dW, K = N*Ho*Wo) may
+  // go to ~4 workgroups per CU while each split keeps >= 256 k.
   int s = 1;
-  while (tiles * s < 2L * CUS && (long)K / (s * 2) >= 256 && s < 256) s *= 2;
-  if (force_splits >= 1) s = force_splits;
+  while (s < 256 && tiles * s * 2 <= CUS && (long)K / (s * 2) >= 32) s *= 2;
+  if (tiles < CUS)
+    while (s < 256 && tiles * s * 2 <= 4L * CUS && (long)K / (s * 2) >= 256) s *= 2;
+  if (g_force_splits >= 1) s = g_force_splits;
   int kc = (K + s - 1) / s;
   kc = (kc + 31) / 32 * 32;
   p.kchunk = kc;
@@ -367,9 +527,16 @@ void launch_tile(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, lo
                  long split_stride, int splits, int kchunk, const float *bias, int HW) {
   const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   dim3 grid(tiles, 1, splits);
-  hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, 32, WM, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI>),
-                     grid, dim3(NT), 0, stream(), M, N, K, A, B, C, ldc, split_stride, kchunk,
-                     bias, HW);
+  // vector epilogue stores need 16-byte aligned rows (NCHW: HW a multiple of 4)
+  const bool cvec = aligned16(C) && (EPI == EPI_STORE ? (ldc % 4 == 0) : (HW % 4 == 0));
+  if constexpr (BM * BN >= 256 * 256)
+    hipLaunchKernelGGL((gemm_mfma_big_kernel<BM, BN, 32, WM, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI>),
+                       grid, dim3(NT), 0, stream(), M, N, K, A, B, C, ldc, split_stride, kchunk,
+                       bias, HW, cvec);
+  else
+    hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, 32, WM, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI>),
+                       grid, dim3(NT), 0, stream(), M, N, K, A, B, C, ldc, split_stride, kchunk,
+                       bias, HW, cvec);
 }
 
 template <bool A_KC, bool A_PERM, bool B_NC, bool B_PERM, int EPI>
@@ -402,7 +569,9 @@ int run(int M, int N, int K, Opnd A, Opnd B, float *C, long ldc, const float *bi
     case T128x64:  TT_VEC(128, 64, 2, EPI_) break;          \
     case T64x64:   TT_VEC(64, 64, 2, EPI_) break;           \
     case T32x256:  TT_VEC(32, 256, 1, EPI_) break;          \
-    default:       TT_VEC(64, 256, 1, EPI_) break;          \
+    case T64x256:  TT_VEC(64, 256, 1, EPI_) break;          \
+    case T256x256: TT_VEC(256, 256, 2, EPI_) break;         \
+    default:       TT_VEC(256, 128, 2, EPI_) break;         \
   }
   if (epi_direct) { TT_SHAPES(EPI) } else { TT_SHAPES(EPI_STORE) }
 #undef TT_SHAPES
@@ -435,6 +604,13 @@ int run(int M, int N, int K, Opnd A, Opnd B, float *C, long ldc, const float *bi
 }
 
 }  // namespace
+
+extern "C" int tth_gemm_config(int tile, int splits) {
+  if (tile >= NTILE || splits > 1024) return -1;
+  g_force_tile = tile;
+  g_force_splits = splits;
+  return 0;
+}
 
 extern "C" int tt_k_gemm(int M, int N, int K, const float *A, int lda, int transA,
                          const float *B, int ldb, int transB, float *C, int ldc) {
