@@ -251,6 +251,62 @@ def time_steps(stepper, steps, warmup):
     return (time.perf_counter() - t0) * 1e3 / steps
 
 
+def bandwidth_kernels(L, reps=50):
+    """The HBM-bound kernels of the CNN step at config-4 sizes, each timed with
+    HIP events over `reps` launches; algorithmic bytes = every input element
+    read once + every output element written once."""
+    from tinytorch_amd.hip import DevBuf, StreamTimer, check, sync
+    rng = np.random.default_rng(7)
+    B = 128
+    out = {}
+
+    def run(name, fn, nbytes):
+        check(fn(), name)
+        prewarm(fn, 0.05)
+        tm = StreamTimer()
+        tm.start()
+        for _ in range(reps):
+            fn()
+        ms = tm.stop_ms() / reps
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = dict(us=round(ms * 1e3, 2), bytes=int(nbytes), gb_s=round(gbs, 1),
+                         frac_of_hbm_peak=round(gbs / PEAK_HBM_GBS, 4))
+
+    # conv1 / conv2 activations of config 4
+    for tag, (C, H, F) in (("conv1", (3, 32, 32)), ("conv2", (32, 16, 64))):
+        x = DevBuf.from_np(rng.uniform(0, 1, B * C * H * H).astype(np.float32))
+        Kc, Ncol = C * 9, B * H * H
+        col = DevBuf(Kc * Ncol)
+        run(f"im2col_{tag}", lambda: L.tt_k_im2col(x.ptr, col.ptr, B, C, H, H, 3, 3, 1, 1, 1, 1, H, H),
+            4 * (B * C * H * H + Kc * Ncol))
+        if tag == "conv2":
+            run("col2im_conv2", lambda: L.tt_k_col2im(col.ptr, x.ptr, B, C, H, H, 3, 3, 1, 1, 1, 1, H, H),
+                4 * (B * C * H * H + Kc * Ncol))
+        n = B * F * H * H  # conv output / relu / pool input
+        a = DevBuf.from_np(rng.standard_normal(n).astype(np.float32))
+        g = DevBuf.from_np(rng.standard_normal(n).astype(np.float32))
+        y = DevBuf(n)
+        run(f"relu_fwd_{tag}", lambda: L.tt_k_relu_fwd(a.ptr, y.ptr, n), 8 * n)
+        run(f"relu_bwd_{tag}", lambda: L.tt_k_relu_bwd(a.ptr, g.ptr, y.ptr, n), 12 * n)
+        Ho = H // 2
+        no = B * F * Ho * Ho
+        p = DevBuf(no)
+        run(f"maxpool_fwd_{tag}", lambda: L.tt_k_maxpool_fwd(a.ptr, p.ptr, B, F, H, H, 2, 2, 2, 2, Ho, Ho),
+            4 * (n + no))
+        run(f"maxpool_bwd_{tag}", lambda: L.tt_k_maxpool_bwd(a.ptr, p.ptr, y.ptr, B, F, H, H, 2, 2, 2, 2, Ho, Ho),
+            4 * (2 * n + no))
+        db = DevBuf(F)
+        run(f"bias_grad_{tag}", lambda: L.tt_k_bias_grad(g.ptr, db.ptr, B, F, H * H), 4 * (n + F))
+        for bb in (x, col, a, g, y, p, db):
+            bb.free()
+    D = 4096
+    h = DevBuf.from_np(rng.standard_normal(B * D).astype(np.float32))
+    hp = DevBuf(B * (D + 1))
+    run("padones_fwd_fc", lambda: L.tt_k_padones_fwd(h.ptr, hp.ptr, B, D), 4 * (B * D + B * (D + 1)))
+    sync()
+    return out
+
+
 def cpu_threads():
     n = os.environ.get("OMP_NUM_THREADS")
     try:
@@ -355,6 +411,9 @@ def main():
         mlp = MlpStep(L)
         extra["mlp_step_ms"] = round(time_steps(mlp, 50, 5), 3)
         log("mlp step ms", extra["mlp_step_ms"])
+        extra["hbm_kernels"] = bandwidth_kernels(L)
+        for k, v in extra["hbm_kernels"].items():
+            log(f"{k:22s} {v['us']:8.2f} us {v['gb_s']:8.1f} GB/s ({100 * v['frac_of_hbm_peak']:.1f}% of 8 TB/s)")
 
     cpu = None
     if not args.no_cpu:

@@ -73,6 +73,11 @@ int tt_k_conv_dw(int F, int Kc, long Ncol, int HW,
                  const float *g, const float *col, float *dW);
 int tt_k_conv_dcol(int F, int Kc, long Ncol, int HW,
                    const float *W, const float *g, float *dcol);
+/* conv_dw fused with the bias gradient (reference src/autograd.c:467-482):
+ * col1 is the im2col matrix with one extra row of ones (Kc + 1 rows, see
+ * tt_k_im2col_ones), db[f] = sum_p g[n][f][hw] comes out of the same GEMM. */
+int tt_k_conv_dw_bias(int F, int Kc, long Ncol, int HW,
+                      const float *g, const float *col1, float *dW, float *db);
 
 /* ---- bandwidth kernels (elementwise.hip / spatial.hip) ---- */
 int tt_k_fill(float *x, long n, float v);
@@ -100,6 +105,9 @@ int tt_k_padones_fwd(const float *x, float *y, long M, long K);      /* src/auto
 int tt_k_padones_bwd(const float *g, float *dx, long M, long K);     /* src/autograd.c:348-359 */
 int tt_k_im2col(const float *x, float *col, int N, int C, int H, int W,
                 int HH, int WW, int sh, int sw, int ph, int pw, int Ho, int Wo);  /* src/ops_spatial.c:37-69 */
+/* im2col followed by a row of Ncol ones (col has Kc + 1 rows) */
+int tt_k_im2col_ones(const float *x, float *col, int N, int C, int H, int W,
+                     int HH, int WW, int sh, int sw, int ph, int pw, int Ho, int Wo);
 int tt_k_col2im(const float *col, float *x, int N, int C, int H, int W,
                 int HH, int WW, int sh, int sw, int ph, int pw, int Ho, int Wo);  /* src/autograd.c:406-434 */
 int tt_k_bias_grad(const float *g, float *db, int N, int F, int HW);              /* src/autograd.c:467-482 */

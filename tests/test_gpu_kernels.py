@@ -336,3 +336,79 @@ def test_scale_by_dev_and_sgd_multi(tlib):
     for w, g, d in zip(ws, gs, dws):
         assert np.abs(d.to_np() - (w - np.float32(0.1) * g)).max() <= 1e-7
     assert tlib.tt_k_sgd_multi(W, G, Nn, 17, ctypes.c_float(0.1)) != 0
+
+
+TILE_IDS = range(7)  # 128x128, 128x64, 64x64, 32x256, 64x256, 256x256, 256x128
+
+
+@pytest.fixture
+def forced_config(tlib):
+    yield lambda t, s: check(tlib.tth_gemm_config(t, s), "tth_gemm_config")
+    tlib.tth_gemm_config(-1, -1)
+
+
+@pytest.mark.parametrize("tile", TILE_IDS)
+@pytest.mark.parametrize("splits", [1, 3])
+def test_every_tile_and_split_all_layouts(tlib, forced_config, tile, splits):
+    """Every tile configuration x split count, all four layouts, ragged edges
+    in M, N and K (so interior fast loads and bounds-checked edge loads both
+    run), against the oracle GEMM family."""
+    forced_config(tile, splits)
+    M, N, K = 300, 270, 161
+    A, B = u(M, K), u(K, N)
+    G = rng.standard_normal((M, N)).astype(np.float32)
+    for ta, tb, a, b, ref, k, am, bm in (
+            (0, 0, A, B, orc.sgemm(A, B), K, A, B),
+            (0, 1, G, B, orc.matmul_nt(G, B), N, G, B),
+            (1, 0, A, G, orc.matmul_tn(A, G), M, A, G),
+            (1, 1, np.ascontiguousarray(A.T), np.ascontiguousarray(B.T), orc.sgemm(A, B), K, A, B)):
+        Mo, No = ref.shape
+        C = run_gemm(tlib, Mo, No, k, ta, tb, a, b)
+        norm, rel = gemm_err(C, ref, k, np.abs(am).max(), np.abs(bm).max())
+        assert norm <= GEMM_TOL and rel <= GEMM_TOL, (tile, splits, ta, tb, norm, rel)
+
+
+@pytest.mark.parametrize("tile", TILE_IDS)
+def test_every_tile_conv_gemms(tlib, forced_config, tile):
+    forced_config(tile, 2)
+    N, C, H, W, F = 3, 5, 10, 9, 6
+    x, w, b = u(N, C, H, W), u(F, C, 3, 3), u(F)
+    Ho, Wo, Kc, Ncol = conv_dims(N, C, H, W, F, 3, 3, 1, 1, 1, 1)
+    col = orc.im2col(x, 3, 3, 1, 1, 1, 1)
+    dcol, dw, db = DevBuf.from_np(col), DevBuf.from_np(w), DevBuf.from_np(b)
+    dout = DevBuf(N * F * Ho * Wo)
+    check(tlib.tt_k_conv_fwd(F, Kc, Ncol, Ho * Wo, dw.ptr, dcol.ptr, db.ptr, dout.ptr), "conv_fwd")
+    ref = orc.conv2d_fwd(x, w, b, 1, 1, 1, 1)
+    assert np.abs(dout.to_np(ref.shape) - ref).max() <= GEMM_TOL * np.sqrt(Kc)
+    g = rng.standard_normal((N, F, Ho, Wo)).astype(np.float32)
+    rdx, rdw, _ = orc.conv2d_bwd(x, w, g, 1, 1, 1, 1, need_db=False)
+    dg, ddw, ddc = DevBuf.from_np(g), DevBuf(w.size), DevBuf(Kc * Ncol)
+    check(tlib.tt_k_conv_dw(F, Kc, Ncol, Ho * Wo, dg.ptr, dcol.ptr, ddw.ptr), "conv_dw")
+    norm, rel = gemm_err(ddw.to_np(w.shape), rdw, Ncol, np.abs(g).max(), 1.0)
+    assert norm <= GEMM_TOL and rel <= GEMM_TOL
+    check(tlib.tt_k_conv_dcol(F, Kc, Ncol, Ho * Wo, dw.ptr, dg.ptr, ddc.ptr), "conv_dcol")
+    gp = g.transpose(1, 0, 2, 3).reshape(F, Ncol)
+    ref_dcol = orc.sgemm(np.ascontiguousarray(w.reshape(F, Kc).T), gp)
+    norm, rel = gemm_err(ddc.to_np((Kc, Ncol)), ref_dcol, F, 1.0, np.abs(g).max())
+    assert norm <= GEMM_TOL and rel <= GEMM_TOL
+
+
+@pytest.mark.parametrize("case", CONV_CASES)
+def test_conv_dw_bias_fused(tlib, case):
+    """dW and db from one GEMM against [col; ones] vs the oracle's dW and
+    serial bias sum (reference src/autograd.c:467-507)."""
+    N, C, H, W, F, HH, WW, sh, sw, ph, pw = case
+    Ho, Wo, Kc, Ncol = conv_dims(*case)
+    x = u(N, C, H, W)
+    dx_, dcol = DevBuf.from_np(x), DevBuf((Kc + 1) * Ncol)
+    check(tlib.tt_k_im2col_ones(dx_.ptr, dcol.ptr, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo), "im2col_ones")
+    col1 = dcol.to_np((Kc + 1, Ncol))
+    assert bits_equal(col1[:Kc], orc.im2col(x, HH, WW, sh, sw, ph, pw)) and np.all(col1[Kc] == 1.0)
+    g = rng.standard_normal((N, F, Ho, Wo)).astype(np.float32)
+    _, rdw, rdb = orc.conv2d_bwd(x, u(F, C, HH, WW), g, sh, sw, ph, pw, need_dx=False)
+    dg, ddw, ddb = DevBuf.from_np(g), DevBuf(F * Kc), DevBuf(F)
+    check(tlib.tt_k_conv_dw_bias(F, Kc, Ncol, Ho * Wo, dg.ptr, dcol.ptr, ddw.ptr, ddb.ptr), "conv_dw_bias")
+    norm, rel = gemm_err(ddw.to_np(rdw.shape), rdw, Ncol, np.abs(g).max(), np.abs(x).max())
+    assert norm <= GEMM_TOL and rel <= GEMM_TOL
+    db = ddb.to_np()
+    assert np.abs(db - rdb).max() <= 1e-5 * np.abs(g).sum(axis=(0, 2, 3)).max() + 1e-6

@@ -98,6 +98,7 @@ SIGNATURES = [
     ("tt_k_conv_fwd", _I, [_I, _I, _L, _I, VP, VP, VP, VP]),
     ("tt_k_conv_dw", _I, [_I, _I, _L, _I, VP, VP, VP]),
     ("tt_k_conv_dcol", _I, [_I, _I, _L, _I, VP, VP, VP]),
+    ("tt_k_conv_dw_bias", _I, [_I, _I, _L, _I, VP, VP, VP, VP]),
     ("tt_k_fill", _I, [VP, _L, _F]),
     ("tt_k_copy", _I, [VP, VP, _L]),
     ("tt_k_add_inplace", _I, [VP, VP, _L]),
@@ -113,6 +114,7 @@ SIGNATURES = [
     ("tt_k_padones_fwd", _I, [VP, VP, _L, _L]),
     ("tt_k_padones_bwd", _I, [VP, VP, _L, _L]),
     ("tt_k_im2col", _I, [VP, VP] + [_I] * 12),
+    ("tt_k_im2col_ones", _I, [VP, VP] + [_I] * 12),
     ("tt_k_col2im", _I, [VP, VP] + [_I] * 12),
     ("tt_k_bias_grad", _I, [VP, VP, _I, _I, _I]),
     ("tt_k_maxpool_fwd", _I, [VP, VP] + [_I] * 10),

@@ -41,6 +41,7 @@ struct AGNode {
     int     mark;        /* DFS state: 0 new, 1 on stack, 2 done */
     int     refcount;
     float  *col;         /* conv2d: forward im2col matrix (device) */
+    int     col_ones;    /* conv2d: col carries the extra row of ones */
     Tensor *aux;         /* softmax_ce: probabilities */
     Tensor *aux2;        /* softmax_ce: per-row seed (p - onehot)/rows */
 };
@@ -177,9 +178,10 @@ AGNode *ag_reshape(AGNode *a, const long *new_shape, int new_ndim) {
 AGNode *ag_conv2d(AGNode *a, AGNode *w, AGNode *b, int sh, int sw, int ph, int pw) {
     if (!a || !w) return NULL;
     const int keep = w->requires_grad;
+    const int ones = keep && b && b->requires_grad;  /* fuse db into the dW GEMM */
     float *col = NULL;
     Tensor *v = tt_conv2d_keepcol(a->val, w->val, b ? b->val : NULL, sh, sw, ph, pw,
-                                  keep ? &col : NULL);
+                                  keep ? &col : NULL, ones);
     if (!v) return NULL;
     int req = a->requires_grad || w->requires_grad || (b && b->requires_grad);
     AGNode *n = node_new(v, req);
@@ -195,6 +197,7 @@ AGNode *ag_conv2d(AGNode *a, AGNode *w, AGNode *b, int sh, int sw, int ph, int p
     n->params[0] = sh; n->params[1] = sw;
     n->params[2] = ph; n->params[3] = pw;
     n->col = col;
+    n->col_ones = col && ones;
     return n;
 }
 
@@ -381,28 +384,41 @@ static void backward_conv2d(AGNode *n) {
     const float *gd = tt_dev(n->grad);
     if (!gd) return;
 
-    if (needs(b)) {
-        const long bshp[1] = {F};
-        Tensor *gb = tt_empty_dev(bshp, 1);
-        if (gb && tt_k_bias_grad(gd, gb->dev, N, F, HW) == 0) accum_move(b, gb);
-        else tt_release(gb);
-    }
-    if (needs(w)) {
-        float *col = n->col;
-        int own = 0;
-        if (!col) {
-            const float *x = tt_dev(a->val);
-            col = x ? (float *)ttrt_alloc(sizeof(float) * (size_t)Kc * (size_t)Ncol) : NULL;
-            if (col && tt_k_im2col(x, col, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo)) {
-                ttrt_free(col);
-                col = NULL;
-            }
-            own = 1;
+    const long bshp[1] = {F};
+    if (needs(b) && needs(w) && n->col && n->col_ones) {
+        /* dW and db from one GEMM against [col; ones] */
+        Tensor *gw = tt_empty_like(w->val);
+        Tensor *gb = gw ? tt_empty_dev(bshp, 1) : NULL;
+        if (gb && tt_k_conv_dw_bias(F, Kc, Ncol, HW, gd, n->col, gw->dev, gb->dev) == 0) {
+            accum_move(b, gb);
+            accum_move(w, gw);
+        } else {
+            tt_release(gw);
+            tt_release(gb);
         }
-        Tensor *gw = col ? tt_empty_like(w->val) : NULL;
-        if (gw && tt_k_conv_dw(F, Kc, Ncol, HW, gd, col, gw->dev) == 0) accum_move(w, gw);
-        else tt_release(gw);
-        if (own) ttrt_free(col);
+    } else {
+        if (needs(b)) {
+            Tensor *gb = tt_empty_dev(bshp, 1);
+            if (gb && tt_k_bias_grad(gd, gb->dev, N, F, HW) == 0) accum_move(b, gb);
+            else tt_release(gb);
+        }
+        if (needs(w)) {
+            float *col = n->col;
+            int own = 0;
+            if (!col) {
+                const float *x = tt_dev(a->val);
+                col = x ? (float *)ttrt_alloc(sizeof(float) * (size_t)Kc * (size_t)Ncol) : NULL;
+                if (col && tt_k_im2col(x, col, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo)) {
+                    ttrt_free(col);
+                    col = NULL;
+                }
+                own = 1;
+            }
+            Tensor *gw = col ? tt_empty_like(w->val) : NULL;
+            if (gw && tt_k_conv_dw(F, Kc, Ncol, HW, gd, col, gw->dev) == 0) accum_move(w, gw);
+            else tt_release(gw);
+            if (own) ttrt_free(col);
+        }
     }
     if (needs(a)) {
         const float *wd = tt_dev(w->val);

@@ -249,6 +249,24 @@ __global__ void padones_bwd_kernel(const float *__restrict__ g, float *__restric
   }
 }
 
+// padones by rows: workgroup (m, chunk) copies 1024 elements of row m with
+// no per-element division (grid.y indexes rows, so M < 65536 here)
+__global__ void padones_fwd_rows_kernel(const float *__restrict__ x, float *__restrict__ y, int K) {
+  const long m = blockIdx.y;
+  const float *xr = x + m * K;
+  float *yr = y + m * (K + 1);
+  for (int k = blockIdx.x * 1024 + threadIdx.x; k <= K && k < (int)(blockIdx.x + 1) * 1024; k += 256)
+    yr[k] = k < K ? xr[k] : 1.0f;
+}
+
+__global__ void padones_bwd_rows_kernel(const float *__restrict__ g, float *__restrict__ dx, int K) {
+  const long m = blockIdx.y;
+  const float *gr = g + m * (K + 1);
+  float *dr = dx + m * K;
+  for (int k = blockIdx.x * 1024 + threadIdx.x; k < K && k < (int)(blockIdx.x + 1) * 1024; k += 256)
+    dr[k] = gr[k];
+}
+
 // Fused softmax + cross-entropy for up to a few thousand rows in ONE
 // workgroup: probabilities, the seed (p - onehot(y)) * scale and the mean
 // loss, reduced in a fixed order (per-thread row order, then the thread
@@ -366,6 +384,11 @@ int tt_k_softmax_ce(const float *logits, const int32_t *labels, float *probs, fl
 
 int tt_k_padones_fwd(const float *x, float *y, long M, long K) {
   if (M <= 0 || K < 0) return 0;
+  if (M < 65536 && K < (1L << 30)) {
+    hipLaunchKernelGGL(padones_fwd_rows_kernel, dim3((unsigned)((K + 1 + 1023) / 1024), (unsigned)M), dim3(256), 0,
+                       stream(), x, y, (int)K);
+    return launched();
+  }
   const long total = M * (K + 1);
   if (total < (1L << 31))
     hipLaunchKernelGGL(padones_fwd_kernel<unsigned>, dim3(grid_for(total, 1)), dim3(256), 0, stream(), x, y, M, K);
@@ -376,6 +399,11 @@ int tt_k_padones_fwd(const float *x, float *y, long M, long K) {
 
 int tt_k_padones_bwd(const float *g, float *dx, long M, long K) {
   if (M <= 0 || K <= 0) return 0;
+  if (M < 65536 && K < (1L << 30)) {
+    hipLaunchKernelGGL(padones_bwd_rows_kernel, dim3((unsigned)((K + 1023) / 1024), (unsigned)M), dim3(256), 0,
+                       stream(), g, dx, (int)K);
+    return launched();
+  }
   const long total = M * K;
   if (total < (1L << 31))
     hipLaunchKernelGGL(padones_bwd_kernel<unsigned>, dim3(grid_for(total, 1)), dim3(256), 0, stream(), g, dx, M, K);

@@ -45,7 +45,12 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int NT = 256;      // threads per workgroup
 constexpr int GROUP_M = 8;   // tile-row grouping for L2 reuse
 
-enum { EPI_STORE = 0, EPI_BIAS_NCHW = 1 };
+// Epilogues: plain row-major store; conv forward (bias[row] added, column p
+// stored to out[p / HW][row][p % HW]); conv dW with its bias gradient (the
+// last of N columns holds sum_p g[row][p] against a row of ones appended to
+// the im2col matrix: it is written to db[row] = ((float *)bias)[row], the
+// first N-1 columns to C with leading dimension ldc).
+enum { EPI_STORE = 0, EPI_BIAS_NCHW = 1, EPI_DW_BIAS = 2 };
 
 // Operand addressing.  The "contiguous" index of an operand is k for a
 // k-contiguous A or B^T layout, or m / n for an m/n-contiguous layout.  A
@@ -364,6 +369,13 @@ __device__ __forceinline__ void gemm_body(float *smem, int M, int N, int K, cons
             for (int j = 0; j < G::NI; j++)
               if (col0 + j < N) C[row * ldc + col0 + j] = v[j];
           }
+        } else if constexpr (EPI == EPI_DW_BIAS) {
+#pragma unroll
+          for (int j = 0; j < G::NI; j++) {
+            const long col = col0 + j;
+            if (col < N - 1) C[row * ldc + col] = v[j];
+            else if (col == N - 1) const_cast<float *>(bias)[row] = v[j];
+          }
         } else {
           const unsigned q = (unsigned)col0 / (unsigned)HW;
           const long hw = (long)((unsigned)col0 - q * (unsigned)HW);
@@ -387,6 +399,9 @@ __device__ __forceinline__ void gemm_body(float *smem, int M, int N, int K, cons
           const float v = acc[i][j][r] + bv;
           if constexpr (EPI == EPI_STORE) {
             C[row * ldc + col] = v;
+          } else if constexpr (EPI == EPI_DW_BIAS) {
+            if (col < N - 1) C[row * ldc + col] = v;
+            else const_cast<float *>(bias)[row] = v;
           } else {
             const unsigned q = (unsigned)col / (unsigned)HW;
             C[((long)q * M + row) * HW + ((unsigned)col - q * (unsigned)HW)] = v;
@@ -446,6 +461,9 @@ splitk_reduce_kernel(const float *__restrict__ ws, float *__restrict__ C, int M,
   const unsigned row = (unsigned)(idx / N), col = (unsigned)(idx - (long)row * N);
   if constexpr (EPI == EPI_STORE) {
     C[(long)row * ldc + col] = s;
+  } else if constexpr (EPI == EPI_DW_BIAS) {
+    if ((int)col < N - 1) C[(long)row * ldc + col] = s;
+    else const_cast<float *>(bias)[row] = s;
   } else {
     const unsigned q = col / (unsigned)HW;
     C[((long)q * M + row) * HW + (col - q * (unsigned)HW)] = s + (bias ? bias[row] : 0.f);
@@ -638,6 +656,15 @@ extern "C" int tt_k_conv_dw(int F, int Kc, long Ncol, int HW, const float *g, co
   Opnd a{g, HW, (long)F * HW, HW}, b{col, Ncol, 0, 1};
   const bool vec = aligned16(g) && aligned16(col) && (HW % 4 == 0) && (Ncol % 4 == 0);
   return run<true, true, false, false, EPI_STORE>(F, Kc, (int)Ncol, a, b, dW, Kc, nullptr, 1, vec);
+}
+
+extern "C" int tt_k_conv_dw_bias(int F, int Kc, long Ncol, int HW, const float *g,
+                                 const float *col1, float *dW, float *db) {
+  if (F <= 0 || Kc <= 0 || Ncol <= 0 || HW <= 0 || Ncol > 0x7fffffffL || !db) return -1;
+  // B = [col; ones]^T: Kc + 1 stored rows of Ncol
+  Opnd a{g, HW, (long)F * HW, HW}, b{col1, Ncol, 0, 1};
+  const bool vec = aligned16(g) && aligned16(col1) && (HW % 4 == 0) && (Ncol % 4 == 0);
+  return run<true, true, false, false, EPI_DW_BIAS>(F, Kc + 1, (int)Ncol, a, b, dW, Kc, db, 1, vec);
 }
 
 extern "C" int tt_k_conv_dcol(int F, int Kc, long Ncol, int HW, const float *W, const float *g,

@@ -142,7 +142,7 @@ Tensor *tt_reshape(const Tensor *a, const long *new_shape, int new_ndim) {
 }
 
 Tensor *tt_conv2d_keepcol(const Tensor *a, const Tensor *w, const Tensor *b, int sh, int sw,
-                          int ph, int pw, float **col_out) {
+                          int ph, int pw, float **col_out, int ones_row) {
     if (col_out) *col_out = NULL;
     if (!a || !w || a->ndim != 4 || w->ndim != 4) return NULL;
     const int N = (int)a->shape[0], C = (int)a->shape[1], H = (int)a->shape[2],
@@ -165,9 +165,11 @@ Tensor *tt_conv2d_keepcol(const Tensor *a, const Tensor *w, const Tensor *b, int
     if (!out) return NULL;
     const int Kc = C * HH * WW;
     const long Ncol = (long)N * Ho * Wo;
-    float *col = (float *)ttrt_alloc(sizeof(float) * (size_t)Kc * (size_t)Ncol);
+    const int rows = (col_out && ones_row) ? Kc + 1 : Kc;
+    float *col = (float *)ttrt_alloc(sizeof(float) * (size_t)rows * (size_t)Ncol);
     if (!col) return fail(out);
-    if (tt_k_im2col(x, col, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo) ||
+    if ((rows > Kc ? tt_k_im2col_ones(x, col, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo)
+                   : tt_k_im2col(x, col, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo)) ||
         tt_k_conv_fwd(F, Kc, Ncol, Ho * Wo, wd, col, bd, out->dev)) {
         ttrt_free(col);
         return fail(out);
@@ -179,7 +181,7 @@ Tensor *tt_conv2d_keepcol(const Tensor *a, const Tensor *w, const Tensor *b, int
 
 Tensor *tt_conv2d(const Tensor *a, const Tensor *w, const Tensor *b, int sh, int sw, int ph,
                   int pw) {
-    return tt_conv2d_keepcol(a, w, b, sh, sw, ph, pw, NULL);
+    return tt_conv2d_keepcol(a, w, b, sh, sw, ph, pw, NULL, 0);
 }
 
 static Tensor *pool(const Tensor *a, int ph, int pw, int sh, int sw, int is_max) {

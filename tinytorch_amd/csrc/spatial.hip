@@ -111,6 +111,129 @@ __global__ void col2im_kernel(const float *__restrict__ col, float *__restrict__
   }
 }
 
+// im2col with one workgroup per (kernel tap c, 1024 consecutive columns p):
+// row c of the column matrix is contiguous in p, each lane writes 4 columns
+// with one 16-byte store, c comes from the grid and a lane divides only by
+// Ho*Wo and Wo.  Requires Ncol % 4 == 0.
+__global__ void __launch_bounds__(256)
+im2col_rows_kernel(const float *__restrict__ x, float *__restrict__ col, int N, int C, int H,
+                   int W, int HH, int WW, int sh, int sw, int ph, int pw, int Ho, int Wo) {
+  const int c = blockIdx.y;
+  const int kw = c % WW, kh = (c / WW) % HH, ci = c / (HH * WW);
+  const unsigned HoWo = (unsigned)(Ho * Wo);
+  const unsigned Ncol = (unsigned)N * HoWo;
+  const unsigned p0 = (blockIdx.x * 256u + threadIdx.x) * 4u;
+  if (p0 >= Ncol) return;
+  unsigned n = p0 / HoWo;
+  const unsigned rem = p0 - n * HoWo;
+  int ho = (int)(rem / (unsigned)Wo), wo = (int)(rem - (unsigned)ho * Wo);
+  float v[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int hi = ho * sh - ph + kh, wi = wo * sw - pw + kw;
+    v[j] = (hi >= 0 && hi < H && wi >= 0 && wi < W)
+               ? x[(((long)n * C + ci) * H + hi) * (long)W + wi] : 0.0f;
+    if (++wo == Wo) { wo = 0; if (++ho == Ho) { ho = 0; ++n; } }
+  }
+  *reinterpret_cast<float4 *>(col + (long)c * Ncol + p0) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
+// col2im with one workgroup per 1024 consecutive image pixels (n, ci, h, w):
+// each lane owns 4 consecutive pixels of one row and gathers their taps,
+// (kh, kw) ascending from +0.0f as the reference's scatter adds them.
+// Requires W % 4 == 0 and fewer than 2^32 pixels.
+__global__ void __launch_bounds__(256)
+col2im_rows_kernel(const float *__restrict__ col, float *__restrict__ x, int N, int C, int H,
+                   int W, int HH, int WW, int sh, int sw, int ph, int pw, int Ho, int Wo) {
+  const unsigned HW = (unsigned)(H * W);
+  const unsigned total = (unsigned)N * C * HW;
+  const unsigned i0 = (blockIdx.x * 256u + threadIdx.x) * 4u;
+  if (i0 >= total) return;
+  const unsigned plane = i0 / HW;
+  const unsigned pin = i0 - plane * HW;
+  const int h = (int)(pin / (unsigned)W), w0 = (int)(pin - (unsigned)h * W);
+  const int n = (int)(plane / (unsigned)C), ci = (int)(plane - (unsigned)n * C);
+  const long HoWo = (long)Ho * Wo, Ncol = (long)N * HoWo;
+  const float *cbase = col + (long)n * HoWo;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int kh = 0; kh < HH; kh++) {
+    const int t = h + ph - kh;
+    if (t < 0 || t % sh) continue;
+    const int ho = t / sh;
+    if (ho >= Ho) continue;
+    for (int kw = 0; kw < WW; kw++) {
+      const float *row = cbase + ((long)(ci * HH + kh) * WW + kw) * Ncol + (long)ho * Wo;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int u = w0 + j + pw - kw;
+        if (u < 0 || u % sw) continue;
+        const int wo = u / sw;
+        if (wo < Wo) acc[j] += row[wo];
+      }
+    }
+  }
+  *reinterpret_cast<float4 *>(x + i0) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+}
+
+// 2x2 / stride-2 max pool, two outputs per lane: two 16-byte loads (rows 2ho
+// and 2ho+1, columns 4q..4q+3) and one 8-byte store.  Requires W % 4 == 0.
+template <typename I>
+__global__ void maxpool2x2_fwd_kernel(const float *__restrict__ x, float *__restrict__ y, int H,
+                                      int W, int Ho, int Wo, I total) {
+  const int Wq = Wo / 2;
+  const I stride = (I)gridDim.x * blockDim.x;
+  for (I i = (I)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const I r = i / Wq;  // (nc, ho) row index
+    const int q = (int)(i - r * Wq);
+    const I nc = r / Ho;
+    const int ho = (int)(r - nc * Ho);
+    const float *xp = x + ((long)nc * H + 2 * ho) * W + 4 * q;
+    const float4 a = *reinterpret_cast<const float4 *>(xp);
+    const float4 b = *reinterpret_cast<const float4 *>(xp + W);
+    float m0 = -INFINITY, m1 = -INFINITY;
+    if (a.x > m0) m0 = a.x; if (a.y > m0) m0 = a.y; if (b.x > m0) m0 = b.x; if (b.y > m0) m0 = b.y;
+    if (a.z > m1) m1 = a.z; if (a.w > m1) m1 = a.w; if (b.z > m1) m1 = b.z; if (b.w > m1) m1 = b.w;
+    *reinterpret_cast<float2 *>(y + (long)r * Wo + 2 * q) = make_float2(m0, m1);
+  }
+}
+
+// matching backward: recompute each window's first strict maximum, write
+// 0.0f + g there and +0.0f elsewhere (rows below 2*Ho are zeroed separately)
+__device__ __forceinline__ void argmax4(float v0, float v1, float v2, float v3, int &am) {
+  float m = -INFINITY;
+  am = 0;
+  if (v0 > m) { m = v0; am = 0; }
+  if (v1 > m) { m = v1; am = 1; }
+  if (v2 > m) { m = v2; am = 2; }
+  if (v3 > m) { m = v3; am = 3; }
+}
+
+template <typename I>
+__global__ void maxpool2x2_bwd_kernel(const float *__restrict__ x, const float *__restrict__ g,
+                                      float *__restrict__ dx, int H, int W, int Ho, int Wo,
+                                      I total) {
+  const int Wq = Wo / 2;
+  const I stride = (I)gridDim.x * blockDim.x;
+  for (I i = (I)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const I r = i / Wq;
+    const int q = (int)(i - r * Wq);
+    const I nc = r / Ho;
+    const int ho = (int)(r - nc * Ho);
+    const long off = ((long)nc * H + 2 * ho) * W + 4 * q;
+    const float4 a = *reinterpret_cast<const float4 *>(x + off);
+    const float4 b = *reinterpret_cast<const float4 *>(x + off + W);
+    const float2 gv = *reinterpret_cast<const float2 *>(g + (long)r * Wo + 2 * q);
+    int am0, am1;
+    argmax4(a.x, a.y, b.x, b.y, am0);
+    argmax4(a.z, a.w, b.z, b.w, am1);
+    const float g0 = 0.0f + gv.x, g1 = 0.0f + gv.y;
+    float4 top = make_float4(am0 == 0 ? g0 : 0.0f, am0 == 1 ? g0 : 0.0f, am1 == 0 ? g1 : 0.0f, am1 == 1 ? g1 : 0.0f);
+    float4 bot = make_float4(am0 == 2 ? g0 : 0.0f, am0 == 3 ? g0 : 0.0f, am1 == 2 ? g1 : 0.0f, am1 == 3 ? g1 : 0.0f);
+    *reinterpret_cast<float4 *>(dx + off) = top;
+    *reinterpret_cast<float4 *>(dx + off + W) = bot;
+  }
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
@@ -313,6 +436,12 @@ int tt_k_im2col(const float *x, float *col, int N, int C, int H, int W, int HH, 
   const long Ncol = (long)N * Ho * Wo;
   const long total = (long)C * HH * WW * ((Ncol + 3) / 4);
   if (total <= 0 || Ncol <= 0) return 0;
+  const long Kc = (long)C * HH * WW;
+  if (Ncol % 4 == 0 && Kc <= 65535 && Ncol < (1L << 32) - 4096 && (((uintptr_t)col & 15) == 0)) {
+    hipLaunchKernelGGL(im2col_rows_kernel, dim3((unsigned)((Ncol / 4 + 255) / 256), (unsigned)Kc),
+                       dim3(256), 0, stream(), x, col, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo);
+    return launched();
+  }
   const bool vec = (Ncol % 4 == 0) && (((uintptr_t)col & 15) == 0);
   const bool small = (long)C * HH * WW * Ncol < (1L << 31);
   const dim3 g(blocks_for(total)), b(256);
@@ -327,10 +456,23 @@ int tt_k_im2col(const float *x, float *col, int N, int C, int H, int W, int HH, 
   return launched();
 }
 
+int tt_k_im2col_ones(const float *x, float *col, int N, int C, int H, int W, int HH, int WW,
+                     int sh, int sw, int ph, int pw, int Ho, int Wo) {
+  const int rc = tt_k_im2col(x, col, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo);
+  if (rc) return rc;
+  const long Ncol = (long)N * Ho * Wo;
+  return tt_k_fill(col + (long)C * HH * WW * Ncol, Ncol, 1.0f);
+}
+
 int tt_k_col2im(const float *col, float *x, int N, int C, int H, int W, int HH, int WW, int sh,
                 int sw, int ph, int pw, int Ho, int Wo) {
   const long total = (long)N * C * H * W;
   if (total <= 0) return 0;
+  if (W % 4 == 0 && (((uintptr_t)x & 15) == 0) && total < (1L << 32) - 4096) {
+    hipLaunchKernelGGL(col2im_rows_kernel, dim3((unsigned)((total / 4 + 255) / 256)), dim3(256), 0,
+                       stream(), col, x, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo);
+    return launched();
+  }
   TT_LAUNCH_I(col2im_kernel, total, col, x, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo);
   return launched();
 }
@@ -362,6 +504,15 @@ int tt_k_maxpool_fwd(const float *x, float *y, int N, int C, int H, int W, int p
                      int sw, int Ho, int Wo) {
   const long total = (long)N * C * Ho * Wo;
   if (total <= 0) return 0;
+  if (ph == 2 && pw == 2 && sh == 2 && sw == 2 && W % 4 == 0 && (((uintptr_t)x & 15) == 0) &&
+      (((uintptr_t)y & 7) == 0)) {
+    const long pairs = total / 2;  // Wo = W/2 is even
+    if (pairs < (1L << 31))
+      hipLaunchKernelGGL(maxpool2x2_fwd_kernel<unsigned>, dim3(blocks_for(pairs)), dim3(256), 0, stream(), x, y, H, W, Ho, Wo, (unsigned)pairs);
+    else
+      hipLaunchKernelGGL(maxpool2x2_fwd_kernel<unsigned long>, dim3(blocks_for(pairs)), dim3(256), 0, stream(), x, y, H, W, Ho, Wo, (unsigned long)pairs);
+    return launched();
+  }
   TT_LAUNCH_I(maxpool_fwd_kernel, total, x, y, N, C, H, W, ph, pw, sh, sw, Ho, Wo);
   return launched();
 }
@@ -370,7 +521,16 @@ int tt_k_maxpool_bwd(const float *x, const float *g, float *dx, int N, int C, in
                      int pw, int sh, int sw, int Ho, int Wo) {
   const long total = (long)N * C * H * W;
   if (total <= 0) return 0;
-  if (ph == sh && pw == sw) {
+  if (ph == 2 && pw == 2 && sh == 2 && sw == 2 && W % 4 == 0 && (((uintptr_t)x & 15) == 0) &&
+      (((uintptr_t)dx & 15) == 0) && (((uintptr_t)g & 7) == 0)) {
+    const long pairs = (long)N * C * Ho * Wo / 2;
+    if (pairs < (1L << 31))
+      hipLaunchKernelGGL(maxpool2x2_bwd_kernel<unsigned>, dim3(blocks_for(pairs)), dim3(256), 0, stream(), x, g, dx, H, W, Ho, Wo, (unsigned)pairs);
+    else
+      hipLaunchKernelGGL(maxpool2x2_bwd_kernel<unsigned long>, dim3(blocks_for(pairs)), dim3(256), 0, stream(), x, g, dx, H, W, Ho, Wo, (unsigned long)pairs);
+    if (2 * Ho < H)
+      TT_LAUNCH_I(pool_uncovered_zero_kernel, total, dx, N, C, H, W, 2 * Ho, 2 * Wo);
+  } else if (ph == sh && pw == sw) {
     const long nwin = (long)N * C * Ho * Wo;
     TT_LAUNCH_I(maxpool_bwd_tiled_kernel, nwin, x, g, dx, N, C, H, W, ph, pw, Ho, Wo);
     const int hcov = Ho * ph, wcov = Wo * pw;
