@@ -74,37 +74,46 @@ __global__ void im2col_kernel(const float *__restrict__ x, float *__restrict__ c
   }
 }
 
-// One thread per image pixel (n, c, h, w); sums col[(c,kh,kw)][(n,ho,wo)]
-// over the kernel taps that cover it, kh then kw ascending.
-template <typename I>
-__global__ void col2im_kernel(const float *__restrict__ col, float *__restrict__ x, int N, int C,
-                              int H, int W, int HH, int WW, int sh, int sw, int ph, int pw, int Ho,
-                              int Wo) {
-  const long HoWo = (long)Ho * Wo;
-  const long Ncol = (long)N * HoWo;
+// col2im, one pixel (n, ci, h, w) per lane with consecutive lanes on
+// consecutive pixels, so every tap's reads are contiguous across the wave.
+// The taps are summed kh then kw ascending from +0.0f, the reference's
+// scatter order, with no atomics.  S1 specialises stride 1 (no division per
+// tap); I is the index type.
+template <typename I, bool S1>
+__global__ void __launch_bounds__(256)
+col2im_px_kernel(const float *__restrict__ col, float *__restrict__ x, int N, int C, int H, int W,
+                 int HH, int WW, int sh, int sw, int ph, int pw, int Ho, int Wo) {
   const I total = (I)N * C * H * W;
+  const long HoWo = (long)Ho * Wo, Ncol = (long)N * HoWo;
   const I stride = (I)gridDim.x * blockDim.x;
   for (I i = (I)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-    const I iw = i / W;
-    const int w = (int)(i - iw * W);
-    const I ih = iw / H;
-    const int h = (int)(iw - ih * H);
-    const I ic = ih / C;
-    const int cim = (int)(ih - ic * C);
-    const long n = (long)ic;
+    const I q = i / (I)W;
+    const int w = (int)(i - q * (I)W);
+    const I plane = q / (I)H;
+    const int h = (int)(q - plane * (I)H);
+    const I n = plane / (I)C;
+    const int ci = (int)(plane - n * (I)C);
+    const float *cb = col + (long)n * HoWo + (long)ci * HH * WW * Ncol;
     float acc = 0.0f;
     for (int kh = 0; kh < HH; kh++) {
-      const int t = h + ph - kh;
-      if (t < 0 || t % sh) continue;
-      const int ho = t / sh;
-      if (ho >= Ho) continue;
+      int ho = h + ph - kh;
+      if constexpr (S1) {
+        if (ho < 0 || ho >= Ho) continue;
+      } else {
+        if (ho < 0 || ho % sh) continue;
+        ho /= sh;
+        if (ho >= Ho) continue;
+      }
       for (int kw = 0; kw < WW; kw++) {
-        const int u = w + pw - kw;
-        if (u < 0 || u % sw) continue;
-        const int wo = u / sw;
-        if (wo >= Wo) continue;
-        const long c = ((long)cim * HH + kh) * WW + kw;
-        acc += col[c * Ncol + n * HoWo + (long)ho * Wo + wo];
+        int wo = w + pw - kw;
+        if constexpr (S1) {
+          if (wo < 0 || wo >= Wo) continue;
+        } else {
+          if (wo < 0 || wo % sw) continue;
+          wo /= sw;
+          if (wo >= Wo) continue;
+        }
+        acc += cb[(long)(kh * WW + kw) * Ncol + (long)ho * Wo + wo];
       }
     }
     x[i] = acc;
@@ -138,41 +147,52 @@ im2col_rows_kernel(const float *__restrict__ x, float *__restrict__ col, int N, 
   *reinterpret_cast<float4 *>(col + (long)c * Ncol + p0) = make_float4(v[0], v[1], v[2], v[3]);
 }
 
-// col2im with one workgroup per 1024 consecutive image pixels (n, ci, h, w):
-// each lane owns 4 consecutive pixels of one row and gathers their taps,
-// (kh, kw) ascending from +0.0f as the reference's scatter adds them.
-// Requires W % 4 == 0 and fewer than 2^32 pixels.
+// im2col staged through LDS: one workgroup per (image n, channel ci) plane
+// reads the H x W plane once (16-byte loads), then writes the HH*WW column
+// rows it feeds, c = ci*HH*WW + kh*WW + kw, from LDS with 16-byte stores.
+// A lane owns the same 4 consecutive outputs (ho, wo..wo+3) of every tap.
+// Requires Wo % 4 == 0 (outputs of a lane stay in one row, stores aligned).
+// With ones_row, the channel-0 workgroup of image n also writes image n's
+// part of the extra (C*HH*WW)-th row of ones.
 __global__ void __launch_bounds__(256)
-col2im_rows_kernel(const float *__restrict__ col, float *__restrict__ x, int N, int C, int H,
-                   int W, int HH, int WW, int sh, int sw, int ph, int pw, int Ho, int Wo) {
-  const unsigned HW = (unsigned)(H * W);
-  const unsigned total = (unsigned)N * C * HW;
-  const unsigned i0 = (blockIdx.x * 256u + threadIdx.x) * 4u;
-  if (i0 >= total) return;
-  const unsigned plane = i0 / HW;
-  const unsigned pin = i0 - plane * HW;
-  const int h = (int)(pin / (unsigned)W), w0 = (int)(pin - (unsigned)h * W);
-  const int n = (int)(plane / (unsigned)C), ci = (int)(plane - (unsigned)n * C);
-  const long HoWo = (long)Ho * Wo, Ncol = (long)N * HoWo;
-  const float *cbase = col + (long)n * HoWo;
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int kh = 0; kh < HH; kh++) {
-    const int t = h + ph - kh;
-    if (t < 0 || t % sh) continue;
-    const int ho = t / sh;
-    if (ho >= Ho) continue;
-    for (int kw = 0; kw < WW; kw++) {
-      const float *row = cbase + ((long)(ci * HH + kh) * WW + kw) * Ncol + (long)ho * Wo;
+im2col_lds_kernel(const float *__restrict__ x, float *__restrict__ col, int N, int C, int H,
+                  int W, int HH, int WW, int sh, int sw, int ph, int pw, int Ho, int Wo,
+                  int ones_row) {
+  extern __shared__ float plane[];
+  const int n = blockIdx.x / C, ci = blockIdx.x - (blockIdx.x / C) * C;
+  const int HWi = H * W;
+  const float *src = x + (long)blockIdx.x * HWi;
+  if ((W & 3) == 0 && (((uintptr_t)src & 15) == 0)) {
+    for (int i = threadIdx.x * 4; i < HWi; i += 1024)
+      *reinterpret_cast<float4 *>(plane + i) = *reinterpret_cast<const float4 *>(src + i);
+  } else {
+    for (int i = threadIdx.x; i < HWi; i += 256) plane[i] = src[i];
+  }
+  __syncthreads();
+  const int HoWo = Ho * Wo;
+  const long Ncol = (long)N * HoWo;
+  const int taps = HH * WW;
+  float *dst0 = col + (long)ci * taps * Ncol + (long)n * HoWo;
+  for (int o = threadIdx.x * 4; o < HoWo; o += 1024) {
+    const int ho = o / Wo, wo = o - (o / Wo) * Wo;
+    for (int kh = 0; kh < HH; kh++) {
+      const int hi = ho * sh - ph + kh;
+      const bool hok = hi >= 0 && hi < H;
+      for (int kw = 0; kw < WW; kw++) {
+        float v[4];
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int u = w0 + j + pw - kw;
-        if (u < 0 || u % sw) continue;
-        const int wo = u / sw;
-        if (wo < Wo) acc[j] += row[wo];
+        for (int j = 0; j < 4; j++) {
+          const int wi = (wo + j) * sw - pw + kw;
+          v[j] = (hok && wi >= 0 && wi < W) ? plane[hi * W + wi] : 0.0f;
+        }
+        *reinterpret_cast<float4 *>(dst0 + (long)(kh * WW + kw) * Ncol + o) =
+            make_float4(v[0], v[1], v[2], v[3]);
       }
     }
+    if (ones_row && ci == 0)
+      *reinterpret_cast<float4 *>(col + (long)C * taps * Ncol + (long)n * HoWo + o) =
+          make_float4(1.0f, 1.0f, 1.0f, 1.0f);
   }
-  *reinterpret_cast<float4 *>(x + i0) = make_float4(acc[0], acc[1], acc[2], acc[3]);
 }
 
 // 2x2 / stride-2 max pool, two outputs per lane: two 16-byte loads (rows 2ho
@@ -418,6 +438,21 @@ __global__ void avgpool_bwd_kernel(const float *__restrict__ g, float *__restric
 
 }  // namespace
 
+// LDS-staged im2col: the input plane must fit in 64 KB of LDS and the
+// column rows must be 16-byte aligned.
+static bool im2col_lds_fits(int N, int C, int H, int W, int Wo, const float *col) {
+  return Wo % 4 == 0 && (long)H * W <= 16384 && (long)N * C < (1L << 31) &&
+         (((uintptr_t)col & 15) == 0);
+}
+
+static int im2col_lds(const float *x, float *col, int N, int C, int H, int W, int HH, int WW,
+                      int sh, int sw, int ph, int pw, int Ho, int Wo, int ones) {
+  hipLaunchKernelGGL(im2col_lds_kernel, dim3((unsigned)((long)N * C)), dim3(256),
+                     sizeof(float) * (size_t)H * W, stream(), x, col, N, C, H, W, HH, WW, sh, sw, ph,
+                     pw, Ho, Wo, ones);
+  return launched();
+}
+
 // Launch kernel template K<I> with I = unsigned when every index fits 32 bits.
 #define TT_LAUNCH_I(K_, total_, ...)                                                          \
   do {                                                                                        \
@@ -437,6 +472,8 @@ int tt_k_im2col(const float *x, float *col, int N, int C, int H, int W, int HH, 
   const long total = (long)C * HH * WW * ((Ncol + 3) / 4);
   if (total <= 0 || Ncol <= 0) return 0;
   const long Kc = (long)C * HH * WW;
+  if (im2col_lds_fits(N, C, H, W, Wo, col))
+    return im2col_lds(x, col, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo, 0);
   if (Ncol % 4 == 0 && Kc <= 65535 && Ncol < (1L << 32) - 4096 && (((uintptr_t)col & 15) == 0)) {
     hipLaunchKernelGGL(im2col_rows_kernel, dim3((unsigned)((Ncol / 4 + 255) / 256), (unsigned)Kc),
                        dim3(256), 0, stream(), x, col, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo);
@@ -458,6 +495,8 @@ int tt_k_im2col(const float *x, float *col, int N, int C, int H, int W, int HH, 
 
 int tt_k_im2col_ones(const float *x, float *col, int N, int C, int H, int W, int HH, int WW,
                      int sh, int sw, int ph, int pw, int Ho, int Wo) {
+  if (im2col_lds_fits(N, C, H, W, Wo, col))
+    return im2col_lds(x, col, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo, 1);
   const int rc = tt_k_im2col(x, col, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo);
   if (rc) return rc;
   const long Ncol = (long)N * Ho * Wo;
@@ -468,12 +507,15 @@ int tt_k_col2im(const float *col, float *x, int N, int C, int H, int W, int HH, 
                 int sw, int ph, int pw, int Ho, int Wo) {
   const long total = (long)N * C * H * W;
   if (total <= 0) return 0;
-  if (W % 4 == 0 && (((uintptr_t)x & 15) == 0) && total < (1L << 32) - 4096) {
-    hipLaunchKernelGGL(col2im_rows_kernel, dim3((unsigned)((total / 4 + 255) / 256)), dim3(256), 0,
-                       stream(), col, x, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo);
-    return launched();
+  const bool s1 = sh == 1 && sw == 1;
+  const dim3 g(blocks_for(total)), b(256);
+  if (total < (1L << 31)) {
+    if (s1) hipLaunchKernelGGL((col2im_px_kernel<unsigned, true>), g, b, 0, stream(), col, x, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo);
+    else    hipLaunchKernelGGL((col2im_px_kernel<unsigned, false>), g, b, 0, stream(), col, x, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo);
+  } else {
+    if (s1) hipLaunchKernelGGL((col2im_px_kernel<unsigned long, true>), g, b, 0, stream(), col, x, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo);
+    else    hipLaunchKernelGGL((col2im_px_kernel<unsigned long, false>), g, b, 0, stream(), col, x, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo);
   }
-  TT_LAUNCH_I(col2im_kernel, total, col, x, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo);
   return launched();
 }
 
