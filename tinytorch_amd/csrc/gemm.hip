@@ -193,18 +193,25 @@ __device__ __forceinline__ void gemm_body(float *smem, int M, int N, int K, cons
   // path: per-thread element offsets are fixed for the whole K loop and
   // advance by a uniform stride per K tile.  Edge tiles and permuted
   // operands use the bounds-checked loads.
-  constexpr bool FAST_OK = VEC && !A_PERM && !B_PERM;
+  // A permuted operand (an NCHW gradient read as F x N*Ho*Wo) is 16 bytes
+  // contiguous per float4 when hw % 4 == 0, which VEC guarantees: its fixed
+  // part is precomputed, its K-dependent split (one 32-bit division per
+  // float4) is done per K tile.
+  constexpr bool FAST_OK = VEC;
   const bool interior = FAST_OK && (m0 + BM <= M) && (n0 + BN <= N);
   long aoff[G::A_V4], boff[G::B_V4];
+  int acol[G::A_V4];
   if constexpr (FAST_OK) {
 #pragma unroll
     for (int v = 0; v < G::A_V4; v++) {
       const int q = tid + v * NT;
       if constexpr (A_KC) {
         const int r = q / (BK / 4), c = (q % (BK / 4)) * 4;
-        aoff[v] = (m0 + r) * A.ld + kbeg + c;
+        acol[v] = c;
+        aoff[v] = A_PERM ? (m0 + r) * A.ld : (m0 + r) * A.ld + kbeg + c;
       } else {
         const int r = q / (BM / 4), c = (q % (BM / 4)) * 4;
+        acol[v] = c;
         aoff[v] = (long)(kbeg + r) * A.ld + m0 + c;
       }
     }
@@ -213,7 +220,7 @@ __device__ __forceinline__ void gemm_body(float *smem, int M, int N, int K, cons
       const int q = tid + v * NT;
       if constexpr (B_NC) {
         const int r = q / (BN / 4), c = (q % (BN / 4)) * 4;
-        boff[v] = (long)(kbeg + r) * B.ld + n0 + c;
+        boff[v] = (long)(kbeg + r) * B.ld + cidx<B_PERM>(B, n0 + c);
       } else {
         const int r = q / (BK / 4), c = (q % (BK / 4)) * 4;
         boff[v] = (n0 + r) * B.ld + kbeg + c;
@@ -221,17 +228,21 @@ __device__ __forceinline__ void gemm_body(float *smem, int M, int N, int K, cons
     }
   }
 
-  auto gload = [&](int kt) {
+  auto gload = [&](int kt, float4 *xa, float4 *xb) {
     const long k0 = kbeg + (long)kt * BK;
     if (FAST_OK && interior && k0 + BK <= kend) {
       const long astep = A_KC ? (long)kt * BK : (long)kt * BK * A.ld;
       const long bstep = B_NC ? (long)kt * BK * B.ld : (long)kt * BK;
 #pragma unroll
-      for (int v = 0; v < G::A_V4; v++)
-        ra[v] = *reinterpret_cast<const float4 *>(A.p + aoff[v] + astep);
+      for (int v = 0; v < G::A_V4; v++) {
+        if constexpr (A_PERM)
+          xa[v] = *reinterpret_cast<const float4 *>(A.p + aoff[v] + cidx<true>(A, k0 + acol[v]));
+        else
+          xa[v] = *reinterpret_cast<const float4 *>(A.p + aoff[v] + astep);
+      }
 #pragma unroll
       for (int v = 0; v < G::B_V4; v++)
-        rb[v] = *reinterpret_cast<const float4 *>(B.p + boff[v] + bstep);
+        xb[v] = *reinterpret_cast<const float4 *>(B.p + boff[v] + bstep);
       return;
     }
 #pragma unroll
@@ -239,10 +250,10 @@ __device__ __forceinline__ void gemm_body(float *smem, int M, int N, int K, cons
       const int q = tid + v * NT;
       if constexpr (A_KC) {  // stored row = m, contiguous = k
         const int r = q / (BK / 4), c = (q % (BK / 4)) * 4;
-        ra[v] = load4<A_PERM, VEC>(A, m0 + r, M, k0 + c, kend);
+        xa[v] = load4<A_PERM, VEC>(A, m0 + r, M, k0 + c, kend);
       } else {               // stored row = k, contiguous = m
         const int r = q / (BM / 4), c = (q % (BM / 4)) * 4;
-        ra[v] = load4<false, VEC>(A, k0 + r, kend, m0 + c, M);
+        xa[v] = load4<false, VEC>(A, k0 + r, kend, m0 + c, M);
       }
     }
 #pragma unroll
@@ -250,15 +261,15 @@ __device__ __forceinline__ void gemm_body(float *smem, int M, int N, int K, cons
       const int q = tid + v * NT;
       if constexpr (B_NC) {  // stored row = k, contiguous = n
         const int r = q / (BN / 4), c = (q % (BN / 4)) * 4;
-        rb[v] = load4<B_PERM, VEC>(B, k0 + r, kend, n0 + c, N);
+        xb[v] = load4<B_PERM, VEC>(B, k0 + r, kend, n0 + c, N);
       } else {               // stored row = n, contiguous = k
         const int r = q / (BK / 4), c = (q % (BK / 4)) * 4;
-        rb[v] = load4<false, VEC>(B, n0 + r, N, k0 + c, kend);
+        xb[v] = load4<false, VEC>(B, n0 + r, N, k0 + c, kend);
       }
     }
   };
 
-  auto sstore = [&](int buf) {
+  auto sstore = [&](int buf, const float4 *xa, const float4 *xb) {
     float *sA = smem + buf * G::STAGE;
     float *sB = sA + G::A_SZ;
 #pragma unroll
@@ -267,7 +278,7 @@ __device__ __forceinline__ void gemm_body(float *smem, int M, int N, int K, cons
       int r, c;
       if constexpr (A_KC) { r = q / (BK / 4); c = (q % (BK / 4)) * 4; }
       else                { r = q / (BM / 4); c = (q % (BM / 4)) * 4; }
-      *reinterpret_cast<float4 *>(sA + r * G::A_LD + c) = ra[v];
+      *reinterpret_cast<float4 *>(sA + r * G::A_LD + c) = xa[v];
     }
 #pragma unroll
     for (int v = 0; v < G::B_V4; v++) {
@@ -275,7 +286,7 @@ __device__ __forceinline__ void gemm_body(float *smem, int M, int N, int K, cons
       int r, c;
       if constexpr (B_NC) { r = q / (BN / 4); c = (q % (BN / 4)) * 4; }
       else                { r = q / (BK / 4); c = (q % (BK / 4)) * 4; }
-      *reinterpret_cast<float4 *>(sB + r * G::B_LD + c) = rb[v];
+      *reinterpret_cast<float4 *>(sB + r * G::B_LD + c) = xb[v];
     }
   };
 
@@ -331,14 +342,14 @@ __device__ __forceinline__ void gemm_body(float *smem, int M, int N, int K, cons
   };
 
   if (nk > 0) {
-    gload(0);
-    sstore(0);
+    gload(0, ra, rb);
+    sstore(0, ra, rb);
     __syncthreads();
     for (int kt = 0; kt < nk; kt++) {
       const bool more = kt + 1 < nk;
-      if (more) gload(kt + 1);
+      if (more) gload(kt + 1, ra, rb);
       compute(kt & 1);
-      if (more) sstore((kt + 1) & 1);
+      if (more) sstore((kt + 1) & 1, ra, rb);
       __syncthreads();
     }
   }
@@ -347,7 +358,30 @@ __device__ __forceinline__ void gemm_body(float *smem, int M, int N, int K, cons
   // block i row rho (acc r: rho = 8*(r/4) + 4*g + r%4) is m = wm + 32*i + rho
   // (k-contiguous A) or wm + MI*rho + i (interleaved A); block j column l32
   // is n = wn + 32*j + l32 or wn + NI*l32 + j (interleaved B).  With
-  // interleaved B a lane owns NI adjacent columns and stores them as one vector.
+  // interleaved B a lane owns NI adjacent columns and stores them as one
+  // vector.  Everything that depends only on the column (the NCHW split of
+  // the conv epilogue) is computed once per lane, outside the row loops.
+  constexpr int NC = B_NC ? 1 : G::NI;  // column groups per lane
+  constexpr int NW = B_NC ? G::NI : 1;  // adjacent columns per group
+  long cbase[NC];     // element offset of the group's first column, row 0
+  long cstride;       // offset between consecutive rows
+  bool cok[NC], cvok[NC];
+  if constexpr (EPI == EPI_BIAS_NCHW) cstride = HW;
+  else cstride = ldc;
+#pragma unroll
+  for (int j = 0; j < NC; j++) {
+    const long col = n0 + wn + (B_NC ? G::NI * l32 : 32 * j + l32);
+    cok[j] = col < N;
+    cvok[j] = cvec && col + NW <= N;
+    if constexpr (EPI == EPI_BIAS_NCHW) {
+      const unsigned q = (unsigned)col / (unsigned)HW;
+      const unsigned hw = (unsigned)col - q * (unsigned)HW;
+      cbase[j] = (long)q * M * HW + hw;
+      cvok[j] = cvok[j] && hw + NW <= (unsigned)HW;
+    } else {
+      cbase[j] = col;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < G::MI; i++)
 #pragma unroll
@@ -356,55 +390,32 @@ __device__ __forceinline__ void gemm_body(float *smem, int M, int N, int K, cons
       const long row = m0 + (A_KC ? wm + 32 * i + rho : wm + G::MI * rho + i);
       if (row >= M) continue;
       const float bv = (EPI == EPI_BIAS_NCHW && bias) ? bias[row] : 0.f;
-      if constexpr (B_NC) {
-        const long col0 = n0 + wn + G::NI * l32;
-        float v[G::NI];
 #pragma unroll
-        for (int j = 0; j < G::NI; j++) v[j] = acc[i][j][r] + bv;
-        if constexpr (EPI == EPI_STORE) {
-          if (cvec && col0 + G::NI <= N) {
-            stvec<G::NI>(C + row * ldc + col0, v);
-          } else {
+      for (int j = 0; j < NC; j++) {
+        if (!cok[j]) continue;
+        float v[NW];
 #pragma unroll
-            for (int j = 0; j < G::NI; j++)
-              if (col0 + j < N) C[row * ldc + col0 + j] = v[j];
+        for (int w = 0; w < NW; w++) v[w] = acc[i][B_NC ? w : j][r] + bv;
+        const long col = n0 + wn + (B_NC ? G::NI * l32 : 32 * j + l32);
+        if constexpr (EPI == EPI_DW_BIAS) {
+#pragma unroll
+          for (int w = 0; w < NW; w++) {
+            if (col + w < N - 1) C[row * ldc + col + w] = v[w];
+            else if (col + w == N - 1) const_cast<float *>(bias)[row] = v[w];
           }
-        } else if constexpr (EPI == EPI_DW_BIAS) {
+        } else if (cvok[j]) {
+          stvec<NW>(C + row * cstride + cbase[j], v);
+        } else if constexpr (EPI == EPI_STORE) {
 #pragma unroll
-          for (int j = 0; j < G::NI; j++) {
-            const long col = col0 + j;
-            if (col < N - 1) C[row * ldc + col] = v[j];
-            else if (col == N - 1) const_cast<float *>(bias)[row] = v[j];
-          }
+          for (int w = 0; w < NW; w++)
+            if (col + w < N) C[row * ldc + col + w] = v[w];
         } else {
-          const unsigned q = (unsigned)col0 / (unsigned)HW;
-          const long hw = (long)((unsigned)col0 - q * (unsigned)HW);
-          if (cvec && col0 + G::NI <= N && hw + G::NI <= HW) {
-            stvec<G::NI>(C + ((long)q * M + row) * HW + hw, v);
-          } else {
 #pragma unroll
-            for (int j = 0; j < G::NI; j++) {
-              const long col = col0 + j;
-              if (col >= N) continue;
-              const unsigned qq = (unsigned)col / (unsigned)HW;
-              C[((long)qq * M + row) * HW + ((unsigned)col - qq * (unsigned)HW)] = v[j];
-            }
-          }
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < G::NI; j++) {
-          const long col = n0 + wn + 32 * j + l32;
-          if (col >= N) continue;
-          const float v = acc[i][j][r] + bv;
-          if constexpr (EPI == EPI_STORE) {
-            C[row * ldc + col] = v;
-          } else if constexpr (EPI == EPI_DW_BIAS) {
-            if (col < N - 1) C[row * ldc + col] = v;
-            else const_cast<float *>(bias)[row] = v;
-          } else {
-            const unsigned q = (unsigned)col / (unsigned)HW;
-            C[((long)q * M + row) * HW + ((unsigned)col - q * (unsigned)HW)] = v;
+          for (int w = 0; w < NW; w++) {
+            const long cc = col + w;
+            if (cc >= N) continue;
+            const unsigned q = (unsigned)cc / (unsigned)HW;
+            C[((long)q * M + row) * HW + ((unsigned)cc - q * (unsigned)HW)] = v[w];
           }
         }
       }
