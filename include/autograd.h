@@ -82,6 +82,27 @@ void    ag_backward_from_tensor(AGNode *out, const Tensor *seed);
 int     ag_sgd_step(AGNode *leaf, float lr);
 int     ag_sgd_step_many(AGNode *const *leaves, int count, float lr);
 
+/* Optimizers whose state (velocity / Adam moments) stays on the device.
+ * State slot i belongs to position i of the `params` list given to
+ * ag_optim_step; the first step fixes the list length and each slot's
+ * element count (a later mismatch returns -1 without updating anything).
+ * Parameters without a gradient are skipped.  Each call updates the leaf
+ * values in place in one launch per TT_SGD_MAX parameters.
+ *   sgd_momentum: v = momentum*v - lr*g; w += v
+ *                 (reference tests/gate_mnist_mlp.py:121-124)
+ *   adam:         t += 1; lr_t = lr*sqrt(1-b2^t)/(1-b1^t);
+ *                 m = b1*m + (1-b1)*g; v = b2*v + (1-b2)*g*g;
+ *                 w -= lr_t*m/(sqrt(v)+eps)
+ *                 (reference tests/gate_cifar_cnn.py:81-98)
+ * Arithmetic matches NumPy's on float32 arrays with Python-float
+ * hyperparameters.  Returns NULL / -1 on bad arguments or OOM. */
+typedef struct AGOptim AGOptim;
+AGOptim *ag_optim_sgd_momentum(double lr, double momentum);
+AGOptim *ag_optim_adam(double lr, double beta1, double beta2, double eps);
+int      ag_optim_step(AGOptim *opt, AGNode *const *params, int count);
+long     ag_optim_steps(const AGOptim *opt);     /* Adam's t; -1 for NULL */
+void     ag_optim_release(AGOptim *opt);
+
 #ifdef __cplusplus
 }
 #endif

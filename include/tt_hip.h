@@ -123,6 +123,18 @@ int tt_k_sgd(float *w, const float *g, long n, float lr);  /* harness SGD: tests
 /* w[i] -= lr * g[i] for count <= TT_SGD_MAX tensors in one launch */
 #define TT_SGD_MAX 16
 int tt_k_sgd_multi(float *const *w, const float *const *g, const long *n, int count, float lr);
+/* SGD with momentum, per tensor i (count <= TT_SGD_MAX, one launch), fp32 as
+ * NumPy evaluates tests/gate_mnist_mlp.py:121-124:
+ *   v = (mu * v) - (lr * g);  w = w + v                                  */
+int tt_k_momentum_multi(float *const *w, const float *const *g, float *const *v, const long *n,
+                        int count, float lr, float mu);
+/* Adam, per tensor i (count <= TT_SGD_MAX, one launch), as NumPy evaluates
+ * tests/gate_cifar_cnn.py:92-98 (fp32 moments, fp64 step):
+ *   m = b1*m + omb1*g;  v = b2*v + omb2*(g*g)          (fp32)
+ *   w = fp32( fp64(w) - (lr_t * fp64(m)) / fp64(sqrtf(v) + eps) )         */
+int tt_k_adam_multi(float *const *w, const float *const *g, float *const *m, float *const *v,
+                    const long *n, int count, float b1, float omb1, float b2, float omb2,
+                    float eps, double lr_t);
 
 #ifdef __cplusplus
 }

@@ -7,6 +7,7 @@ oracle/Makefile).  Imported only by tests/, __graft_entry__.smoke() and
 bench.py's cpu_baseline leg; never by the product package.
 """
 import ctypes
+import math
 import os
 
 import numpy as np
@@ -291,6 +292,40 @@ def ce_seed(p, labels):
     seed = np.empty_like(p)
     loss = orc().orc_ce_seed(_p(p), _p(lab), rows, cols, _p(seed))
     return loss, seed
+
+
+def momentum_step(w, v, g, lr, mu):
+    """SGD with momentum of the reference MNIST harness (reference
+    tests/gate_mnist_mlp.py:121-124): v = mu*v - lr*g, then w = w + v, on
+    float32 arrays with Python-float hyperparameters.  NumPy 2 rounds a
+    Python float to float32 against a float32 array, and every product is
+    rounded before the subtraction.  Updates w and v in place."""
+    assert w.dtype == v.dtype == g.dtype == np.float32
+    v[:] = np.float32(mu) * v - np.float32(lr) * g
+    w[:] = w + v
+
+
+def adam_lr_t(lr, b1, b2, t):
+    """Bias-corrected step size of step t (reference tests/gate_cifar_cnn.py:93-94),
+    a float64."""
+    return lr * (math.sqrt(1.0 - b2 ** t) / (1.0 - b1 ** t))
+
+
+def adam_step(params, grads, m, v, t, lr=0.003, b1=0.9, b2=0.999, eps=1e-8):
+    """Step t (1-based) of the reference CIFAR harness's Adam (reference
+    tests/gate_cifar_cnn.py:81-98) with its dtypes written out: the moments
+    are float32 (the Python-float betas rounded to float32), the step
+    lr_t*m/(sqrt(v)+eps) is float64 because lr_t is a NumPy float64 scalar,
+    and the in-place subtraction rounds the float64 result into the float32
+    parameter once.  Updates params, m and v in place."""
+    lr_t = adam_lr_t(lr, b1, b2, t)
+    c1, d1 = np.float32(b1), np.float32(1.0 - b1)
+    c2, d2 = np.float32(b2), np.float32(1.0 - b2)
+    for p, g, mi, vi in zip(params, grads, m, v):
+        mi[:] = c1 * mi + d1 * g
+        vi[:] = c2 * vi + d2 * (g * g)
+        den = (np.sqrt(vi) + np.float32(eps)).astype(np.float64)
+        p[:] = (p.astype(np.float64) - (lr_t * mi.astype(np.float64)) / den).astype(np.float32)
 
 
 def mlp_step(x, labels, W1, W2, W3, nthreads=8):

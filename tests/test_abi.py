@@ -86,8 +86,10 @@ def test_pybind_module_imports():
         sys.path.pop(0)
     for meth in ("leaf", "value", "grad", "backward", "add", "mul", "addscalar", "mulscalar",
                  "matmul", "relu", "softmax", "padones", "reshape", "conv2d", "maxpool2d",
-                 "avgpool2d", "__add__", "__mul__", "softmax_ce", "sgd_step"):
+                 "avgpool2d", "__add__", "__mul__", "softmax_ce", "sgd_step", "detach"):
         assert hasattr(m.Node, meth), meth
+    for meth in ("sgd_momentum", "adam", "step", "t"):
+        assert hasattr(m.Optim, meth), meth
 
 
 @pytest.mark.skipif(os.path.exists("/dev/kfd"), reason="a GPU device node is present")

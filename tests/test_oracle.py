@@ -299,3 +299,82 @@ def test_ce_seed_closed_form():
     oh = np.eye(10, dtype=np.float32)[y]
     assert same(seed, (p - oh) / np.float32(6))
     assert abs(loss + np.mean(np.log(p[np.arange(6), y].astype(np.float64)))) < 1e-6
+
+
+# ---- optimizers of the reference harnesses (SGD-momentum, Adam) ----
+# The reference has no compiled optimizer: its harnesses run them in NumPy.
+# The oracle writes the NumPy dtype rules out explicitly; these pins check
+# them against closed-form trajectories (constant gradient) and against
+# NumPy's own promotion of Python-float / NumPy-float64 scalars.
+
+def test_momentum_constant_gradient_closed_form():
+    w0 = u(300)
+    g = u(300)
+    lr, mu, k = 0.1, 0.9, 12
+    w, v = w0.copy(), np.zeros_like(w0)
+    for _ in range(k):
+        orc.momentum_step(w, v, g, lr, mu)
+    # v_k = -lr g (1 - mu^k)/(1 - mu);  w_k = w0 + sum_j v_j
+    g64 = g.astype(np.float64)
+    vk = -lr * g64 * (1 - mu ** k) / (1 - mu)
+    wk = w0 + sum(-lr * g64 * (1 - mu ** j) / (1 - mu) for j in range(1, k + 1))
+    assert np.abs(v - vk).max() <= 1e-5 * np.abs(vk).max()
+    assert np.abs(w - wk).max() <= 1e-5 * np.abs(wk).max()
+
+
+def test_adam_constant_gradient_closed_form():
+    """With a constant g the bias-corrected moments are exactly g and g^2, so
+    step t moves w by lr*g*s_t/(|g|*s_t + eps), s_t = sqrt(1-b2^t).  eps is
+    chosen comparable to |g| so a misplaced eps or bias correction shows."""
+    g = np.concatenate([u(200), np.float32(1e-3) * u(200)])
+    w0 = u(400)
+    lr, b1, b2, eps = 0.003, 0.9, 0.999, 1e-3
+    p, m, v = [w0.copy()], [np.zeros_like(w0)], [np.zeros_like(w0)]
+    w = w0.astype(np.float64)
+    g64 = g.astype(np.float64)
+    for t in range(1, 9):
+        orc.adam_step(p, [g], m, v, t, lr, b1, b2, eps)
+        s = np.sqrt(1 - b2 ** t)
+        w = w - lr * g64 * s / (np.abs(g64) * s + eps)
+        assert np.abs(m[0] - g64 * (1 - b1 ** t)).max() <= 1e-6
+        assert np.abs(v[0] - g64 ** 2 * (1 - b2 ** t)).max() <= 1e-8
+        assert np.abs(p[0] - w).max() <= 2e-6, t
+
+
+def test_adam_first_step_is_signed_lr():
+    """t = 1 with eps -> 0: w1 = w0 - lr*sign(g) (the classic Adam first step)."""
+    g = u(500)
+    g[np.abs(g) < 1e-3] = 0.5
+    w0 = u(500)
+    p, m, v = [w0.copy()], [np.zeros_like(w0)], [np.zeros_like(w0)]
+    orc.adam_step(p, [g], m, v, 1, lr=0.01, eps=1e-12)
+    assert np.abs(p[0] - (w0.astype(np.float64) - 0.01 * np.sign(g))).max() <= 1e-6
+
+
+def test_optimizer_dtype_rules_match_numpy_promotion():
+    """The explicit float32/float64 steps of the oracle equal what NumPy does
+    when the harness's expressions mix float32 arrays with a Python float
+    (weak: rounded to float32) and with a NumPy float64 scalar (strong:
+    promotes the array expression to float64, rounded by the in-place -=)."""
+    w, v, g = u(1000), u(1000), u(1000)
+    w1, v1 = w.copy(), v.copy()
+    orc.momentum_step(w1, v1, g, 0.1, 0.9)
+    v2 = 0.9 * v - 0.1 * g
+    w2 = w.copy()
+    w2 += v2
+    assert v2.dtype == np.float32
+    assert np.array_equal(v1, v2) and np.array_equal(w1, w2)
+
+    p, m, vv = u(1000), u(1000) * np.float32(0.1), np.abs(u(1000)) * np.float32(0.01)
+    P1, M1, V1 = [p.copy()], [m.copy()], [vv.copy()]
+    orc.adam_step(P1, [g], M1, V1, 3)
+    lr_t = 0.003 * (np.sqrt(1.0 - 0.999 ** 3) / (1.0 - 0.9 ** 3))
+    assert isinstance(lr_t, np.float64)
+    m2 = 0.9 * m + (1.0 - 0.9) * g
+    v3 = 0.999 * vv + (1.0 - 0.999) * (g * g)
+    step = lr_t * m2 / (np.sqrt(v3) + 1e-8)
+    assert m2.dtype == np.float32 and step.dtype == np.float64
+    p2 = p.copy()
+    p2 -= step
+    assert np.array_equal(M1[0], m2) and np.array_equal(V1[0], v3)
+    assert np.array_equal(P1[0], p2)

@@ -75,6 +75,11 @@ SIGNATURES = [
     ("ag_backward_from_tensor", None, [VP, VP]),
     ("ag_sgd_step", _I, [VP, _F]),
     ("ag_sgd_step_many", _I, [ctypes.POINTER(VP), _I, _F]),
+    ("ag_optim_sgd_momentum", VP, [ctypes.c_double, ctypes.c_double]),
+    ("ag_optim_adam", VP, [ctypes.c_double] * 4),
+    ("ag_optim_step", _I, [VP, ctypes.POINTER(VP), _I]),
+    ("ag_optim_steps", _L, [VP]),
+    ("ag_optim_release", None, [VP]),
     # tt_hip.h: runtime
     ("tth_available", _I, []),
     ("tth_device_name", _I, [ctypes.c_char_p, _I]),
@@ -123,6 +128,9 @@ SIGNATURES = [
     ("tt_k_avgpool_bwd", _I, [VP, VP] + [_I] * 10),
     ("tt_k_sgd", _I, [VP, VP, _L, _F]),
     ("tt_k_sgd_multi", _I, [ctypes.POINTER(VP), ctypes.POINTER(VP), ctypes.POINTER(_L), _I, _F]),
+    ("tt_k_momentum_multi", _I, [ctypes.POINTER(VP)] * 3 + [ctypes.POINTER(_L), _I, _F, _F]),
+    ("tt_k_adam_multi", _I, [ctypes.POINTER(VP)] * 4 + [ctypes.POINTER(_L), _I] + [_F] * 5
+     + [ctypes.c_double]),
 ]
 
 

@@ -20,6 +20,7 @@
  * Backward rules that fail to allocate skip silently, as in the reference. */
 #include "tt_internal.h"
 
+#include <math.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -609,6 +610,138 @@ int ag_sgd_step(AGNode *leaf, float lr) {
     int rc = tt_k_sgd(w, g, leaf->val->numel, lr);
     tt_mark_dev_written(leaf->val);
     return rc;
+}
+
+/* ---------- optimizers with device-resident state ---------- */
+
+/* One state slot per position in the parameter list handed to
+ * ag_optim_step: leaves are rebuilt every step around the same tensors, so
+ * the slot, not the node, owns the moments.  Hyperparameters are doubles
+ * because the reference harness keeps them as Python floats: the fp32
+ * factors are the doubles rounded once, as NumPy rounds a Python scalar
+ * against a float32 array, and Adam's bias-corrected rate stays a double. */
+enum { OPT_MOMENTUM = 1, OPT_ADAM = 2 };
+
+struct AGOptim {
+    int kind;
+    double lr, mu, b1, b2, eps;
+    long t;            /* Adam steps taken */
+    int nslots;        /* fixed by the first step */
+    long *numel;       /* per slot */
+    float **m, **v;    /* per-slot device state (v: Adam only) */
+};
+
+static AGOptim *optim_new(int kind) {
+    if (ttrt_init() != 0) return NULL;
+    AGOptim *o = (AGOptim *)calloc(1, sizeof(AGOptim));
+    if (o) o->kind = kind;
+    return o;
+}
+
+AGOptim *ag_optim_sgd_momentum(double lr, double momentum) {
+    AGOptim *o = optim_new(OPT_MOMENTUM);
+    if (!o) return NULL;
+    o->lr = lr;
+    o->mu = momentum;
+    return o;
+}
+
+AGOptim *ag_optim_adam(double lr, double beta1, double beta2, double eps) {
+    if (!(beta1 >= 0.0 && beta1 < 1.0) || !(beta2 >= 0.0 && beta2 < 1.0)) return NULL;
+    AGOptim *o = optim_new(OPT_ADAM);
+    if (!o) return NULL;
+    o->lr = lr;
+    o->b1 = beta1;
+    o->b2 = beta2;
+    o->eps = eps;
+    return o;
+}
+
+void ag_optim_release(AGOptim *o) {
+    if (!o) return;
+    for (int i = 0; i < o->nslots; i++) {
+        ttrt_free(o->m ? o->m[i] : NULL);
+        ttrt_free(o->v ? o->v[i] : NULL);
+    }
+    free(o->numel);
+    free(o->m);
+    free(o->v);
+    free(o);
+}
+
+long ag_optim_steps(const AGOptim *o) { return o ? o->t : -1; }
+
+/* zero-filled per-slot state on the first step */
+static int optim_bind(AGOptim *o, AGNode *const *params, int count) {
+    o->numel = (long *)calloc((size_t)count, sizeof(long));
+    o->m = (float **)calloc((size_t)count, sizeof(float *));
+    o->v = (float **)calloc((size_t)count, sizeof(float *));
+    if (!o->numel || !o->m || !o->v) return -1;
+    o->nslots = count;
+    for (int i = 0; i < count; i++) {
+        if (!params[i]) return -1;
+        const long n = params[i]->val->numel;
+        o->numel[i] = n;
+        const size_t bytes = sizeof(float) * (size_t)n;
+        o->m[i] = (float *)ttrt_alloc(bytes);
+        if (!o->m[i] || tt_k_fill(o->m[i], n, 0.0f)) return -1;
+        if (o->kind == OPT_ADAM) {
+            o->v[i] = (float *)ttrt_alloc(bytes);
+            if (!o->v[i] || tt_k_fill(o->v[i], n, 0.0f)) return -1;
+        }
+    }
+    return 0;
+}
+
+int ag_optim_step(AGOptim *o, AGNode *const *params, int count) {
+    if (!o || count < 0 || (count > 0 && !params)) return -1;
+    if (o->nslots == 0 && count > 0) {
+        if (optim_bind(o, params, count)) {
+            for (int i = 0; i < o->nslots; i++) {
+                ttrt_free(o->m[i]);
+                ttrt_free(o->v[i]);
+            }
+            free(o->numel); free(o->m); free(o->v);
+            o->numel = NULL; o->m = o->v = NULL; o->nslots = 0;
+            return -1;
+        }
+    }
+    if (count != o->nslots) return -1;
+    for (int i = 0; i < count; i++)
+        if (!params[i] || params[i]->val->numel != o->numel[i]) return -1;
+
+    double lr_t = 0.0;
+    if (o->kind == OPT_ADAM) {
+        /* tests/gate_cifar_cnn.py:93-94 */
+        o->t++;
+        lr_t = o->lr * (sqrt(1.0 - pow(o->b2, (double)o->t)) / (1.0 - pow(o->b1, (double)o->t)));
+    }
+    for (int base = 0; base < count; base += TT_SGD_MAX) {
+        float *w[TT_SGD_MAX], *m[TT_SGD_MAX], *v[TT_SGD_MAX];
+        const float *g[TT_SGD_MAX];
+        long n[TT_SGD_MAX];
+        int k = 0;
+        for (int i = base; i < count && i < base + TT_SGD_MAX; i++) {
+            AGNode *l = params[i];
+            if (!l->grad) continue;   /* no gradient reached it: state untouched */
+            w[k] = tt_dev(l->val);
+            g[k] = tt_dev(l->grad);
+            if (!w[k] || !g[k]) return -1;
+            m[k] = o->m[i];
+            v[k] = o->v[i];
+            n[k] = o->numel[i];
+            tt_mark_dev_written(l->val);
+            k++;
+        }
+        int rc;
+        if (o->kind == OPT_MOMENTUM)
+            rc = tt_k_momentum_multi(w, g, m, n, k, (float)o->lr, (float)o->mu);
+        else
+            rc = tt_k_adam_multi(w, g, m, v, n, k, (float)o->b1, (float)(1.0 - o->b1),
+                                 (float)o->b2, (float)(1.0 - o->b2), (float)o->eps, lr_t);
+        if (rc) return -1;
+    }
+    return 0;
 }
 
 /* ---------- lifecycle ---------- */

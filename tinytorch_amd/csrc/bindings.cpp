@@ -5,9 +5,11 @@
 // layer raises ValueError("tinytorch: invalid arguments or shape mismatch")
 // and a wrong-length backward seed raises ValueError before any gradient is
 // touched (reference src/bindings.cpp:22-30, 79-92).  value()/grad() return
-// fresh NumPy copies of the device data.  Additions of this backend:
-// softmax_ce(labels), probs(), backward_device(seed_node), sgd_step(lr) and
-// the module function available().
+// fresh NumPy copies of the device data, as the reference's do; with
+// copy=False they return a view of the pinned host mirror instead.
+// detach() re-enters a device-resident parameter into a new graph.  Additions of this backend:
+// softmax_ce(labels), probs(), backward_device(seed_node), sgd_step(lr), the
+// Optim class (SGD-momentum, Adam) and the module function available().
 #include <pybind11/numpy.h>
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
@@ -49,6 +51,24 @@ py::array_t<float> to_numpy(Tensor *t) {
   return out;
 }
 
+// Zero-copy form: a NumPy array over the tensor's pinned host mirror that
+// keeps the tensor alive.  The mirror is refreshed in place by every later
+// value()/grad()/tt_data() of the same tensor, and writes through the array
+// reach the device before the tensor's next use (the host copy stays
+// authoritative until then).
+py::array_t<float> view_numpy(Tensor *t) {
+  if (!t) return py::array_t<float>();
+  const int nd = tt_ndim(t);
+  std::vector<long> shp(nd);
+  tt_shape(t, shp.data());
+  std::vector<py::ssize_t> shape(shp.begin(), shp.end());
+  float *src = tt_data(t);
+  if (!src) throw std::runtime_error("tinytorch: device to host copy failed");
+  tt_retain(t);
+  py::capsule owner(t, [](void *p) { tt_release(static_cast<Tensor *>(p)); });
+  return py::array_t<float>(shape, src, owner);
+}
+
 class PyNode {
  public:
   std::shared_ptr<NodeRef> ref;
@@ -69,12 +89,19 @@ class PyNode {
     return PyNode(n);
   }
 
-  py::array_t<float> value() const { return to_numpy(ag_value(get())); }
+  py::array_t<float> value(bool copy) const {
+    return copy ? to_numpy(ag_value(get())) : view_numpy(ag_value(get()));
+  }
 
-  py::object grad() const {
+  py::object grad(bool copy) const {
     Tensor *g = ag_grad(get());
     if (!g) return py::none();
-    return to_numpy(g);
+    return copy ? to_numpy(g) : view_numpy(g);
+  }
+
+  // a new leaf around this node's value tensor (shared, not copied)
+  PyNode detach(bool requires_grad) const {
+    return PyNode(ag_leaf(ag_value(get()), requires_grad ? 1 : 0));
   }
 
   void backward(py::object seed) {
@@ -121,6 +148,31 @@ class PyNode {
   }
 };
 
+// Optimizer with device-resident state; step() takes the parameter nodes in
+// the same order every call (state slot i follows position i).
+class PyOptim {
+ public:
+  std::shared_ptr<AGOptim> opt;
+  explicit PyOptim(AGOptim *o) {
+    if (!o) bad();
+    opt.reset(o, ag_optim_release);
+  }
+  static PyOptim sgd_momentum(double lr, double momentum) {
+    return PyOptim(ag_optim_sgd_momentum(lr, momentum));
+  }
+  static PyOptim adam(double lr, double b1, double b2, double eps) {
+    return PyOptim(ag_optim_adam(lr, b1, b2, eps));
+  }
+  void step(const std::vector<PyNode> &params) {
+    std::vector<AGNode *> ps;
+    ps.reserve(params.size());
+    for (const auto &p : params) ps.push_back(p.get());
+    if (ag_optim_step(opt.get(), ps.data(), (int)ps.size()) != 0)
+      throw py::value_error("tinytorch: optimizer step failed (parameter list or sizes changed?)");
+  }
+  long steps() const { return ag_optim_steps(opt.get()); }
+};
+
 }  // namespace
 
 PYBIND11_MODULE(tinytorch_pybind, m) {
@@ -129,8 +181,9 @@ PYBIND11_MODULE(tinytorch_pybind, m) {
 
   py::class_<PyNode>(m, "Node")
       .def_static("leaf", &PyNode::leaf, py::arg("arr"), py::arg("requires_grad") = true)
-      .def("value", &PyNode::value)
-      .def("grad", &PyNode::grad)
+      .def("value", &PyNode::value, py::arg("copy") = true)
+      .def("grad", &PyNode::grad, py::arg("copy") = true)
+      .def("detach", &PyNode::detach, py::arg("requires_grad") = true)
       .def("backward", &PyNode::backward, py::arg("seed") = py::none())
       .def("add", &PyNode::add)
       .def("mul", &PyNode::mul)
@@ -153,4 +206,11 @@ PYBIND11_MODULE(tinytorch_pybind, m) {
       .def("sgd_step", &PyNode::sgd_step, py::arg("lr"))
       .def("__add__", &PyNode::add)
       .def("__mul__", &PyNode::mul);
+
+  py::class_<PyOptim>(m, "Optim")
+      .def_static("sgd_momentum", &PyOptim::sgd_momentum, py::arg("lr"), py::arg("momentum"))
+      .def_static("adam", &PyOptim::adam, py::arg("lr") = 0.003, py::arg("beta1") = 0.9,
+                  py::arg("beta2") = 0.999, py::arg("eps") = 1e-8)
+      .def("step", &PyOptim::step, py::arg("params"))
+      .def_property_readonly("t", &PyOptim::steps);
 }

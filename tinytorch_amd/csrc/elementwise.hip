@@ -327,6 +327,57 @@ __global__ void sgd_multi_kernel(SgdList L, float lr) {
   for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) w[i] -= lr * g[i];
 }
 
+// SGD with momentum on up to TT_SGD_MAX tensors (blockIdx.y selects one).
+// The file is compiled with -ffp-contract=off, so each product is rounded
+// before the subtraction exactly as NumPy's separate array operations are.
+struct MomList {
+  float *w[TT_SGD_MAX];
+  const float *g[TT_SGD_MAX];
+  float *v[TT_SGD_MAX];
+  long n[TT_SGD_MAX];
+};
+
+__global__ void momentum_multi_kernel(MomList L, float lr, float mu) {
+  const int t = blockIdx.y;
+  float *w = L.w[t], *v = L.v[t];
+  const float *g = L.g[t];
+  const long n = L.n[t];
+  const long stride = (long)gridDim.x * blockDim.x;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float vn = mu * v[i] - lr * g[i];
+    v[i] = vn;
+    w[i] = w[i] + vn;
+  }
+}
+
+// Adam on up to TT_SGD_MAX tensors.  Moments are fp32; the parameter step
+// is formed in fp64 (lr_t is a double) and rounded once when stored.
+struct AdamList {
+  float *w[TT_SGD_MAX];
+  const float *g[TT_SGD_MAX];
+  float *m[TT_SGD_MAX];
+  float *v[TT_SGD_MAX];
+  long n[TT_SGD_MAX];
+};
+
+__global__ void adam_multi_kernel(AdamList L, float b1, float omb1, float b2, float omb2, float eps,
+                                  double lr_t) {
+  const int t = blockIdx.y;
+  float *w = L.w[t], *m = L.m[t], *v = L.v[t];
+  const float *g = L.g[t];
+  const long n = L.n[t];
+  const long stride = (long)gridDim.x * blockDim.x;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float gi = g[i];
+    const float mn = b1 * m[i] + omb1 * gi;
+    const float vn = b2 * v[i] + omb2 * (gi * gi);
+    m[i] = mn;
+    v[i] = vn;
+    const float den = sqrtf(vn) + eps;
+    w[i] = (float)((double)w[i] - (lr_t * (double)mn) / (double)den);
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -440,6 +491,46 @@ int tt_k_sgd_multi(float *const *w, const float *const *g, const long *n, int co
   for (int i = count; i < TT_SGD_MAX; i++) { L.w[i] = nullptr; L.g[i] = nullptr; L.n[i] = 0; }
   if (nmax <= 0) return 0;
   hipLaunchKernelGGL(sgd_multi_kernel, dim3(grid_for(nmax, 1), count), dim3(256), 0, stream(), L, lr);
+  return launched();
+}
+
+int tt_k_momentum_multi(float *const *w, const float *const *g, float *const *v, const long *n,
+                        int count, float lr, float mu) {
+  if (count < 0 || count > TT_SGD_MAX) return -1;
+  if (count == 0) return 0;
+  MomList L{};
+  long nmax = 0;
+  for (int i = 0; i < count; i++) {
+    L.w[i] = w[i];
+    L.g[i] = g[i];
+    L.v[i] = v[i];
+    L.n[i] = n[i];
+    if (n[i] > nmax) nmax = n[i];
+  }
+  if (nmax <= 0) return 0;
+  hipLaunchKernelGGL(momentum_multi_kernel, dim3(grid_for(nmax, 1), count), dim3(256), 0, stream(),
+                     L, lr, mu);
+  return launched();
+}
+
+int tt_k_adam_multi(float *const *w, const float *const *g, float *const *m, float *const *v,
+                    const long *n, int count, float b1, float omb1, float b2, float omb2,
+                    float eps, double lr_t) {
+  if (count < 0 || count > TT_SGD_MAX) return -1;
+  if (count == 0) return 0;
+  AdamList L{};
+  long nmax = 0;
+  for (int i = 0; i < count; i++) {
+    L.w[i] = w[i];
+    L.g[i] = g[i];
+    L.m[i] = m[i];
+    L.v[i] = v[i];
+    L.n[i] = n[i];
+    if (n[i] > nmax) nmax = n[i];
+  }
+  if (nmax <= 0) return 0;
+  hipLaunchKernelGGL(adam_multi_kernel, dim3(grid_for(nmax, 1), count), dim3(256), 0, stream(), L,
+                     b1, omb1, b2, omb2, eps, lr_t);
   return launched();
 }
 

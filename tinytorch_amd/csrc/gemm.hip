@@ -463,8 +463,10 @@ splitk_reduce_kernel(const float *__restrict__ ws, float *__restrict__ C, int M,
   const long total = (long)M * N;
   const long idx = (long)blockIdx.x * XL + tx;
   float s = 0.f;
-  if (idx < total)
+  if (idx < total) {
+#pragma unroll 4
     for (int z = ty; z < S; z += ZL) s += ws[z * total + idx];
+  }
   part[ty][tx] = s;
   __syncthreads();
   if (ty != 0 || idx >= total) return;
@@ -609,9 +611,11 @@ int run(int M, int N, int K, Opnd A, Opnd B, float *C, long ldc, const float *bi
   if (hipGetLastError() != hipSuccess) { if (ws) ttrt_free(ws); return -3; }
   if (ws) {
     const long total = (long)M * N;
-    // as many split-lanes as keep >= ~512 waves busy (at most 32, at most S)
+    // widen the split-lanes until ~2048 workgroups share the reduction (at
+    // most 32 lanes, at most S): each lane's loads are independent, so more
+    // lanes means more loads in flight for the few outputs of a conv dW
     int zl = 1;
-    while (zl < 32 && zl < p.splits && (total * zl * 2) <= 512L * 64) zl *= 2;
+    while (zl < 32 && zl < p.splits && (total * zl * 2) <= 2048L * 256) zl *= 2;
     if (zl < 4 && p.splits >= 4) zl = 4;
 #define TT_RED(ZL_)                                                                            \
   hipLaunchKernelGGL((splitk_reduce_kernel<EPI, ZL_>), dim3((unsigned)((total + 256 / ZL_ - 1) / \

@@ -253,6 +253,87 @@ int ttrt_h2d_async(void *dst, const void *src, size_t bytes) {
     return 0;
 }
 
+/* Pinned host mirrors.  tt_data() hands the caller a host copy of a device
+ * tensor; when that copy lives in page-locked memory the device-to-host DMA
+ * writes it directly instead of bouncing through the driver's staging
+ * buffers, and NumPy views of it (pybind value(copy=False)) cost nothing.
+ * Page-locking is slow (a syscall and page pinning per hipHostMalloc), so
+ * freed mirrors go to per-size free lists like device blocks, up to
+ * TT_HOST_CACHE_MAX bytes.  A 64-byte header in front of the payload keeps
+ * the rounded size and whether the block is pinned (a failed hipHostMalloc
+ * falls back to malloc). */
+#define TT_HOST_HDR 64
+#define TT_HOST_CACHE_MAX ((size_t)1 << 30)
+typedef struct { size_t sz; int pinned; } HostHdr;
+static Bin *g_hbins = NULL;
+static int g_nhbins = 0, g_hbins_cap = 0;
+static size_t g_hcached = 0;
+
+static Bin *hbin_for(size_t sz, int create) {
+    for (int i = 0; i < g_nhbins; i++)
+        if (g_hbins[i].sz == sz) return &g_hbins[i];
+    if (!create) return NULL;
+    if (g_nhbins == g_hbins_cap) {
+        int nc = g_hbins_cap ? g_hbins_cap * 2 : 32;
+        Bin *nb = (Bin *)realloc(g_hbins, sizeof(Bin) * (size_t)nc);
+        if (!nb) return NULL;
+        g_hbins = nb;
+        g_hbins_cap = nc;
+    }
+    Bin *b = &g_hbins[g_nhbins++];
+    memset(b, 0, sizeof(*b));
+    b->sz = sz;
+    return b;
+}
+
+static void host_block_free(void *base) {
+    HostHdr *h = (HostHdr *)base;
+    if (h->pinned) hipHostFree(base);
+    else free(base);
+}
+
+void *ttrt_host_alloc(size_t bytes) {
+    size_t sz = round_size(bytes + TT_HOST_HDR);
+    if (sz < 4096) sz = 4096;
+    Bin *b = hbin_for(sz, 0);
+    void *base = NULL;
+    if (b && b->n > 0) {
+        base = b->ptrs[--b->n];
+        g_hcached -= sz;
+    } else {
+        int pinned = 0;
+        if (ttrt_init() == 0 && hipHostMalloc(&base, sz, hipHostMallocDefault) == hipSuccess) {
+            pinned = 1;
+        } else {
+            (void)hipGetLastError();
+            base = malloc(sz);
+            if (!base) return NULL;
+        }
+        ((HostHdr *)base)->sz = sz;
+        ((HostHdr *)base)->pinned = pinned;
+    }
+    return (char *)base + TT_HOST_HDR;
+}
+
+void ttrt_host_free(void *p) {
+    if (!p) return;
+    void *base = (char *)p - TT_HOST_HDR;
+    const size_t sz = ((HostHdr *)base)->sz;
+    Bin *b = g_hcached + sz <= TT_HOST_CACHE_MAX ? hbin_for(sz, 1) : NULL;
+    if (b && b->n == b->cap) {
+        int nc = b->cap ? b->cap * 2 : 8;
+        void **np = (void **)realloc(b->ptrs, sizeof(void *) * (size_t)nc);
+        if (np) { b->ptrs = np; b->cap = nc; } else b = NULL;
+    }
+    if (!b) { host_block_free(base); return; }
+    b->ptrs[b->n++] = base;
+    g_hcached += sz;
+}
+
+int ttrt_host_is_pinned(const void *p) {
+    return p ? ((const HostHdr *)((const char *)p - TT_HOST_HDR))->pinned : 0;
+}
+
 int ttrt_d2h(void *dst, const void *src, size_t bytes) {
     if (ttrt_init() != 0) return -1;
     if (!bytes) return 0;

@@ -9,7 +9,8 @@
  * current (TT_V_DEV / TT_V_HOST).  tt_data() downloads into the host mirror
  * and, because the caller may write through the returned pointer, leaves the
  * HOST copy authoritative; tt_dev() (used by every op) uploads it again when
- * needed.  Internal outputs are created with tt_empty_dev (no zero fill); the
+ * needed.  The host mirror is a pinned block from the runtime's host cache
+ * (direct DMA on download).  Internal outputs are created with tt_empty_dev (no zero fill); the
  * public tt_new keeps the reference's zero-filled contract. */
 #include "tt_internal.h"
 
@@ -50,7 +51,7 @@ static Tensor *alloc_meta(const long *shape, int ndim) {
 }
 
 static void free_meta(Tensor *t) {
-    free(t->data);
+    ttrt_host_free(t->data);
     free(t->shape);
     free(t->strides);
     free(t);
@@ -118,7 +119,7 @@ float *tt_data(const Tensor *ct) {
     if (!t) return NULL;
     if (!(t->valid & TT_V_HOST)) {
         if (!t->data) {
-            t->data = (float *)malloc(sizeof(float) * (size_t)t->numel);
+            t->data = (float *)ttrt_host_alloc(sizeof(float) * (size_t)t->numel);
             if (!t->data) return NULL;
         }
         if (ttrt_d2h(t->data, t->dev, sizeof(float) * (size_t)t->numel) != 0) return NULL;

@@ -30,6 +30,9 @@ int    ttrt_sync(void);                 /* wait for the stream; 0 ok */
 int    ttrt_h2d(void *dst, const void *src, size_t bytes);   /* sync copy */
 int    ttrt_d2h(void *dst, const void *src, size_t bytes);   /* sync copy */
 int    ttrt_h2d_async(void *dst, const void *src, size_t bytes); /* stream-ordered, src reusable at return */
+void  *ttrt_host_alloc(size_t bytes);   /* pinned (cached) host block, 64-B aligned; NULL on OOM */
+void   ttrt_host_free(void *p);         /* only for ttrt_host_alloc blocks */
+int    ttrt_host_is_pinned(const void *p);
 void   ttrt_set_error(int code);
 int    ttrt_last_error(void);
 size_t ttrt_bytes_in_use(void);

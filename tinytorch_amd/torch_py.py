@@ -69,6 +69,12 @@ class Node:
         t.release()  # the node holds its own reference
         return n
 
+    def detach(self, requires_grad=True):
+        """A new leaf sharing this node's value tensor (no copy, fresh grad):
+        how device-resident parameters are re-entered into each step's graph."""
+        return Node(_checked(LIB.ag_leaf(LIB.ag_value(self.ptr), 1 if requires_grad else 0),
+                             "ag_leaf"))
+
     def value(self):
         return Tensor(LIB.ag_value(self.ptr), owned=False).to_np()
 
@@ -149,3 +155,46 @@ class Node:
         if self.ptr:
             LIB.ag_release(self.ptr)
             self.ptr = None
+
+
+class Optim:
+    """Optimizer with device-resident state (SGD-momentum or Adam).
+
+    The update rules are the reference harness's NumPy optimizers
+    (reference tests/gate_mnist_mlp.py:121-124, tests/gate_cifar_cnn.py:81-98)
+    run on the GPU; step(params) takes the parameter nodes in the same order
+    on every call."""
+
+    def __init__(self, ptr):
+        if not ptr:
+            raise ValueError("tinytorch: invalid optimizer arguments")
+        self.ptr = ptr
+
+    @classmethod
+    def sgd_momentum(cls, lr, momentum):
+        return cls(LIB.ag_optim_sgd_momentum(lr, momentum))
+
+    @classmethod
+    def adam(cls, lr=0.003, beta1=0.9, beta2=0.999, eps=1e-8):
+        return cls(LIB.ag_optim_adam(lr, beta1, beta2, eps))
+
+    def step(self, params):
+        arr = (ctypes.c_void_p * len(params))(*[p.ptr for p in params])
+        if LIB.ag_optim_step(self.ptr, arr, len(params)) != 0:
+            raise ValueError("tinytorch: optimizer step failed (parameter list or sizes changed?)")
+
+    @property
+    def t(self):
+        return LIB.ag_optim_steps(self.ptr)
+
+    def release(self):
+        if self.ptr:
+            LIB.ag_optim_release(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
+
