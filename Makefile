@@ -19,7 +19,7 @@ HIPFLAGS := --offload-arch=$(ARCH) -O3 -fPIC -std=c++17 -Iinclude -I$(CSRC) \
 CFLAGS_HOST := -O2 -fPIC -std=c11 -Wall -Wextra -D__HIP_PLATFORM_AMD__ -I$(ROCM)/include \
                -Iinclude -I$(CSRC)
 
-HOST_SRCS := $(CSRC)/runtime.c $(CSRC)/tensor.c $(CSRC)/ops.c $(CSRC)/autograd.c
+HOST_SRCS := $(CSRC)/runtime.c $(CSRC)/tensor.c $(CSRC)/ops.c $(CSRC)/autograd.c $(CSRC)/dataset.c
 HIP_SRCS  := $(CSRC)/gemm.hip $(CSRC)/elementwise.hip $(CSRC)/spatial.hip
 HDRS      := $(wildcard include/*.h) $(wildcard $(CSRC)/*.h)
 HOST_OBJS := $(patsubst $(CSRC)/%.c,$(BUILD)/obj/%.o,$(HOST_SRCS))
@@ -43,7 +43,7 @@ $(BUILD)/obj/%.o: $(CSRC)/%.hip $(HDRS) | $(BUILD)/obj
 	$(HIPCC) $(HIPFLAGS) -ffp-contract=off -c $< -o $@
 
 $(BUILD)/libtinytorch.so: $(HOST_OBJS) $(HIP_OBJS)
-	$(HIPCC) --offload-arch=$(ARCH) -shared -fPIC -o $@ $^ -Wl,-Bsymbolic -Wl,-soname,libtinytorch.so
+	$(HIPCC) --offload-arch=$(ARCH) -shared -fPIC -o $@ $^ -Wl,-Bsymbolic -Wl,-soname,libtinytorch.so -lz
 
 $(BUILD)/tinytorch_pybind$(EXT_SUFFIX): $(CSRC)/bindings.cpp $(BUILD)/libtinytorch.so $(HDRS)
 	$(CXX) -O2 -fPIC -shared -std=c++17 $(PYBIND_INC) -Iinclude -o $@ $< \

@@ -101,6 +101,10 @@ AGOptim *ag_optim_sgd_momentum(double lr, double momentum);
 AGOptim *ag_optim_adam(double lr, double beta1, double beta2, double eps);
 int      ag_optim_step(AGOptim *opt, AGNode *const *params, int count);
 long     ag_optim_steps(const AGOptim *opt);     /* Adam's t; -1 for NULL */
+/* learning-rate schedule: the CIFAR harness decays Adam's lr between epochs
+ * (reference tests/gate_cifar_cnn.py:159-160); takes effect at the next step */
+int      ag_optim_set_lr(AGOptim *opt, double lr);
+double   ag_optim_lr(const AGOptim *opt);
 void     ag_optim_release(AGOptim *opt);
 
 #ifdef __cplusplus

@@ -135,6 +135,13 @@ int tt_k_momentum_multi(float *const *w, const float *const *g, float *const *v,
 int tt_k_adam_multi(float *const *w, const float *const *g, float *const *m, float *const *v,
                     const long *n, int count, float b1, float omb1, float b2, float omb2,
                     float eps, double lr_t);
+/* Dataset batch gather + normalisation (see tt_data.h):
+ * out[r, j] = ((float)src[idx[r]*sample + j] / 255 - mean[c]) / stdv[c],
+ * c = j / plane, channels = sample / plane <= 4.  idx values must be in
+ * [0, nsrc): the caller checks them (the kernel trusts them). */
+int tt_k_gather_u8_norm(const uint8_t *src, long nsrc, long sample, long plane, int channels,
+                        const int64_t *idx, long n, const float *mean, const float *stdv,
+                        float *out);
 
 #ifdef __cplusplus
 }

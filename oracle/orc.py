@@ -328,6 +328,39 @@ def adam_step(params, grads, m, v, t, lr=0.003, b1=0.9, b2=0.999, eps=1e-8):
         p[:] = (p.astype(np.float64) - (lr_t * mi.astype(np.float64)) / den).astype(np.float32)
 
 
+def read_idx(path):
+    """uint8 idx file (gzip'd or plain) -> ndarray of its dims.  The MNIST
+    harness's parse (reference tests/gate_mnist_mlp.py:44-53): big-endian
+    header (0, 0, type 0x08, ndim) then ndim uint32 dims, data after."""
+    import gzip
+    with open(path, "rb") as f:
+        raw = f.read()
+    if raw[:2] == b"\x1f\x8b":
+        raw = gzip.decompress(raw)
+    assert raw[0] == 0 and raw[1] == 0 and raw[2] == 0x08, "not a uint8 idx file"
+    nd = raw[3]
+    dims = [int.from_bytes(raw[4 + 4 * i: 8 + 4 * i], "big") for i in range(nd)]
+    off = 4 + 4 * nd
+    return np.frombuffer(raw, np.uint8, count=int(np.prod(dims)), offset=off).reshape(dims)
+
+
+def read_cifar_bin(paths):
+    """CIFAR-10 binary batches -> (uint8 (n, 3, 32, 32), int32 labels): records
+    of 1 label byte + 3072 channel-major pixels, files concatenated."""
+    recs = np.concatenate([np.fromfile(p, np.uint8).reshape(-1, 3073) for p in paths])
+    return recs[:, 1:].reshape(-1, 3, 32, 32).copy(), recs[:, 0].astype(np.int32)
+
+
+def normalize_u8(x, mean, std):
+    """((x / 255) - mean[c]) / std[c] in float32, channel axis 1 -- the
+    harnesses' normalisation (reference tests/gate_mnist_mlp.py:85,
+    tests/gate_cifar_cnn.py:165) with the float32 scalars written out."""
+    x = x.astype(np.float32) / np.float32(255.0)
+    m = np.asarray(mean, np.float32).reshape((1, -1) + (1,) * (x.ndim - 2))
+    s = np.asarray(std, np.float32).reshape((1, -1) + (1,) * (x.ndim - 2))
+    return (x - m) / s
+
+
 def mlp_step(x, labels, W1, W2, W3, nthreads=8):
     x, W1, W2, W3 = f32(x), f32(W1), f32(W2), f32(W3)
     lab = np.ascontiguousarray(labels, dtype=np.int32)

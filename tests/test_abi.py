@@ -11,7 +11,13 @@ import pytest
 import tinytorch_amd
 
 ROOT = tinytorch_amd.ROOT
-HEADERS = [os.path.join(ROOT, "include", h) for h in ("tensor.h", "autograd.h", "tt_hip.h")]
+HEADERS = [os.path.join(ROOT, "include", h)
+           for h in ("tensor.h", "autograd.h", "tt_hip.h", "tt_data.h")]
+
+
+def test_every_header_is_checked():
+    assert sorted(os.listdir(os.path.join(ROOT, "include"))) == sorted(
+        os.path.basename(h) for h in HEADERS)
 
 
 def declared_functions(path):

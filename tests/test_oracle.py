@@ -378,3 +378,68 @@ def test_optimizer_dtype_rules_match_numpy_promotion():
     p2 -= step
     assert np.array_equal(M1[0], m2) and np.array_equal(V1[0], v3)
     assert np.array_equal(P1[0], p2)
+
+
+# ---- dataset formats and normalisation ----
+
+def _write_idx(path, arr, gz):
+    import gzip
+    import struct
+    arr = np.ascontiguousarray(arr, np.uint8)
+    raw = struct.pack(">BBBB", 0, 0, 0x08, arr.ndim) + struct.pack(">" + "I" * arr.ndim, *arr.shape)
+    raw += arr.tobytes()
+    with (gzip.open(path, "wb") if gz else open(path, "wb")) as f:
+        f.write(raw)
+
+
+@pytest.mark.parametrize("gz", [False, True])
+def test_idx_reader_and_probe(tmp_path, gz):
+    """the oracle reader and the library's host-side header parser agree with
+    a file written from the format's definition"""
+    import ctypes
+    import tinytorch_amd
+    img = rng.integers(0, 256, (7, 28, 28), dtype=np.uint8)
+    p = str(tmp_path / ("img.idx.gz" if gz else "img.idx"))
+    _write_idx(p, img, gz)
+    assert np.array_equal(orc.read_idx(p), img)
+    L = tinytorch_amd.lib()
+    nd = ctypes.c_int()
+    dims = (ctypes.c_long * 8)()
+    assert L.tt_idx_probe(p.encode(), ctypes.byref(nd), dims) == 0
+    assert tuple(dims[: nd.value]) == (7, 28, 28)
+    bad = str(tmp_path / "bad.idx")
+    with open(bad, "wb") as f:
+        f.write(bytes([0, 0, 0x0D, 1, 0, 0, 0, 4]) + b"\0" * 16)  # float32 idx: rejected
+    assert L.tt_idx_probe(bad.encode(), ctypes.byref(nd), dims) != 0
+    assert L.tt_idx_probe(str(tmp_path / "missing").encode(), ctypes.byref(nd), dims) != 0
+
+
+def test_cifar_bin_reader(tmp_path):
+    ims = [rng.integers(0, 256, (n, 3, 32, 32), dtype=np.uint8) for n in (3, 5)]
+    labs = [rng.integers(0, 10, n).astype(np.int32) for n in (3, 5)]
+    paths = []
+    for i, (im, lb) in enumerate(zip(ims, labs)):
+        p = str(tmp_path / f"b{i}.bin")
+        with open(p, "wb") as f:
+            for k in range(len(lb)):
+                f.write(bytes([lb[k]]) + im[k].tobytes())  # label byte, then R, G, B planes
+        paths.append(p)
+    x, y = orc.read_cifar_bin(paths)
+    assert np.array_equal(x, np.concatenate(ims)) and np.array_equal(y, np.concatenate(labs))
+
+
+def test_normalize_matches_numpy_harness_forms_and_float64():
+    x = np.arange(256, dtype=np.uint8).reshape(1, 1, 16, 16)
+    # MNIST form: Python-float mean/std against a float32 array
+    got = orc.normalize_u8(x, [0.1307], [0.3081])
+    harness = ((x.astype(np.float32) / 255.0) - 0.1307) / 0.3081
+    assert harness.dtype == np.float32 and np.array_equal(got, harness)
+    # CIFAR form: float32 (1, 3, 1, 1) arrays
+    x3 = rng.integers(0, 256, (4, 3, 8, 8), dtype=np.uint8)
+    mean = np.array([0.4914, 0.4822, 0.4465], dtype=np.float32).reshape(1, 3, 1, 1)
+    std = np.array([0.2023, 0.1994, 0.2010], dtype=np.float32).reshape(1, 3, 1, 1)
+    got3 = orc.normalize_u8(x3, mean.ravel(), std.ravel())
+    assert np.array_equal(got3, (x3.astype(np.float32) / 255.0 - mean) / std)
+    # and within float32 rounding of the exact value
+    exact = (x3 / 255.0 - mean.astype(np.float64)) / std.astype(np.float64)
+    assert np.abs(got3 - exact).max() <= 4e-7 * np.abs(exact).max()

@@ -80,6 +80,18 @@ SIGNATURES = [
     ("ag_optim_step", _I, [VP, ctypes.POINTER(VP), _I]),
     ("ag_optim_steps", _L, [VP]),
     ("ag_optim_release", None, [VP]),
+    ("ag_optim_set_lr", _I, [VP, ctypes.c_double]),
+    ("ag_optim_lr", ctypes.c_double, [VP]),
+    # tt_data.h: device-resident datasets
+    ("tt_idx_probe", _I, [ctypes.c_char_p, ctypes.POINTER(_I), ctypes.POINTER(_L)]),
+    ("tt_dataset_idx", VP, [ctypes.c_char_p, ctypes.c_char_p]),
+    ("tt_dataset_cifar10_bin", VP, [ctypes.POINTER(ctypes.c_char_p), _I]),
+    ("tt_dataset_from_u8", VP, [VP, VP, _L, _I, _I, _I]),
+    ("tt_dataset_len", _L, [VP]),
+    ("tt_dataset_shape", _I, [VP, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I)]),
+    ("tt_dataset_labels", _I, [VP, VP]),
+    ("tt_dataset_batch", VP, [VP, VP, _L, F32P, F32P, _I, VP]),
+    ("tt_dataset_release", None, [VP]),
     # tt_hip.h: runtime
     ("tth_available", _I, []),
     ("tth_device_name", _I, [ctypes.c_char_p, _I]),
@@ -128,6 +140,7 @@ SIGNATURES = [
     ("tt_k_avgpool_bwd", _I, [VP, VP] + [_I] * 10),
     ("tt_k_sgd", _I, [VP, VP, _L, _F]),
     ("tt_k_sgd_multi", _I, [ctypes.POINTER(VP), ctypes.POINTER(VP), ctypes.POINTER(_L), _I, _F]),
+    ("tt_k_gather_u8_norm", _I, [VP, _L, _L, _L, _I, VP, _L, F32P, F32P, VP]),
     ("tt_k_momentum_multi", _I, [ctypes.POINTER(VP)] * 3 + [ctypes.POINTER(_L), _I, _F, _F]),
     ("tt_k_adam_multi", _I, [ctypes.POINTER(VP)] * 4 + [ctypes.POINTER(_L), _I] + [_F] * 5
      + [ctypes.c_double]),

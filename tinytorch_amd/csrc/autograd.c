@@ -671,6 +671,14 @@ void ag_optim_release(AGOptim *o) {
 
 long ag_optim_steps(const AGOptim *o) { return o ? o->t : -1; }
 
+int ag_optim_set_lr(AGOptim *o, double lr) {
+    if (!o) return -1;
+    o->lr = lr;
+    return 0;
+}
+
+double ag_optim_lr(const AGOptim *o) { return o ? o->lr : 0.0; }
+
 /* zero-filled per-slot state on the first step */
 static int optim_bind(AGOptim *o, AGNode *const *params, int count) {
     o->numel = (long *)calloc((size_t)count, sizeof(long));

@@ -9,7 +9,8 @@
 // copy=False they return a view of the pinned host mirror instead.
 // detach() re-enters a device-resident parameter into a new graph.  Additions of this backend:
 // softmax_ce(labels), probs(), backward_device(seed_node), sgd_step(lr), the
-// Optim class (SGD-momentum, Adam) and the module function available().
+// Optim class (SGD-momentum, Adam), the Dataset class (device-resident
+// MNIST / CIFAR-10) and the module function available().
 #include <pybind11/numpy.h>
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
@@ -20,6 +21,7 @@
 
 #include "autograd.h"
 #include "tensor.h"
+#include "tt_data.h"
 #include "tt_hip.h"
 
 namespace py = pybind11;
@@ -171,6 +173,44 @@ class PyOptim {
       throw py::value_error("tinytorch: optimizer step failed (parameter list or sizes changed?)");
   }
   long steps() const { return ag_optim_steps(opt.get()); }
+  double lr() const { return ag_optim_lr(opt.get()); }
+  void set_lr(double v) { ag_optim_set_lr(opt.get(), v); }
+};
+
+// Device-resident uint8 dataset; batch(idx) returns (leaf Node, labels).
+class PyDataset {
+ public:
+  std::shared_ptr<TTDataset> d;
+  std::vector<float> mean, stdv;
+  PyDataset(TTDataset *p, std::vector<float> m, std::vector<float> s) : mean(m), stdv(s) {
+    if (!p) throw py::value_error("tinytorch: dataset load failed (missing or malformed file?)");
+    d.reset(p, tt_dataset_release);
+    int c, h, w;
+    tt_dataset_shape(p, &c, &h, &w);
+    if ((int)mean.size() != c || (int)stdv.size() != c)
+      throw py::value_error("tinytorch: mean/std need one value per channel");
+  }
+  static PyDataset mnist(const std::string &img, const std::string &lab, std::vector<float> m,
+                         std::vector<float> s) {
+    return PyDataset(tt_dataset_idx(img.c_str(), lab.c_str()), m, s);
+  }
+  static PyDataset cifar10(const std::vector<std::string> &paths, std::vector<float> m,
+                           std::vector<float> s) {
+    std::vector<const char *> ps;
+    for (const auto &p : paths) ps.push_back(p.c_str());
+    return PyDataset(tt_dataset_cifar10_bin(ps.data(), (int)ps.size()), m, s);
+  }
+  long len() const { return tt_dataset_len(d.get()); }
+  py::tuple batch(py::array_t<long, py::array::c_style | py::array::forcecast> idx, bool flat,
+                  bool requires_grad) {
+    py::array_t<int32_t> lab(idx.size());
+    Tensor *t = tt_dataset_batch(d.get(), idx.data(), (long)idx.size(), mean.data(), stdv.data(),
+                                 flat ? 1 : 0, lab.mutable_data());
+    if (!t) bad();
+    AGNode *n = ag_leaf(t, requires_grad ? 1 : 0);
+    tt_release(t);
+    return py::make_tuple(PyNode(n), lab);
+  }
 };
 
 }  // namespace
@@ -207,10 +247,22 @@ PYBIND11_MODULE(tinytorch_pybind, m) {
       .def("__add__", &PyNode::add)
       .def("__mul__", &PyNode::mul);
 
+  py::class_<PyDataset>(m, "Dataset")
+      .def_static("mnist", &PyDataset::mnist, py::arg("images"), py::arg("labels"),
+                  py::arg("mean") = std::vector<float>{0.1307f},
+                  py::arg("std") = std::vector<float>{0.3081f})
+      .def_static("cifar10", &PyDataset::cifar10, py::arg("paths"),
+                  py::arg("mean") = std::vector<float>{0.4914f, 0.4822f, 0.4465f},
+                  py::arg("std") = std::vector<float>{0.2023f, 0.1994f, 0.2010f})
+      .def("__len__", &PyDataset::len)
+      .def("batch", &PyDataset::batch, py::arg("idx"), py::arg("flat") = false,
+           py::arg("requires_grad") = false);
+
   py::class_<PyOptim>(m, "Optim")
       .def_static("sgd_momentum", &PyOptim::sgd_momentum, py::arg("lr"), py::arg("momentum"))
       .def_static("adam", &PyOptim::adam, py::arg("lr") = 0.003, py::arg("beta1") = 0.9,
                   py::arg("beta2") = 0.999, py::arg("eps") = 1e-8)
       .def("step", &PyOptim::step, py::arg("params"))
-      .def_property_readonly("t", &PyOptim::steps);
+      .def_property_readonly("t", &PyOptim::steps)
+      .def_property("lr", &PyOptim::lr, &PyOptim::set_lr);
 }

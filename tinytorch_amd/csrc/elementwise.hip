@@ -378,6 +378,44 @@ __global__ void adam_multi_kernel(AdamList L, float b1, float omb1, float b2, fl
   }
 }
 
+// Dataset batch: out[r, j] = ((float)src[idx[r], j] / 255 - mean[c]) / std[c]
+// with c = j / plane.  Division is IEEE (correctly rounded) and nothing is
+// contracted, so the result equals NumPy's float32 evaluation.  blockIdx.y
+// strides over rows; the vector path moves 4 bytes in and 16 bytes out per
+// lane (needs sample and plane sizes that are multiples of 4).
+struct NormParams {
+  float mean[4], stdv[4];
+};
+
+__device__ __forceinline__ float norm_u8(unsigned v, float m, float s) {
+  return ((float)v / 255.0f - m) / s;
+}
+
+template <bool VEC>
+__global__ void gather_u8_norm_kernel(const uint8_t *__restrict__ src, long S, long plane,
+                                      const int64_t *__restrict__ idx, long n, NormParams P,
+                                      float *__restrict__ out) {
+  const long per = VEC ? S / 4 : S;
+  for (long r = blockIdx.y; r < n; r += gridDim.y) {
+    const uint8_t *row = src + idx[r] * S;
+    float *orow = out + r * S;
+    for (long j = (long)blockIdx.x * blockDim.x + threadIdx.x; j < per;
+         j += (long)gridDim.x * blockDim.x) {
+      if constexpr (VEC) {
+        const uchar4 v = *reinterpret_cast<const uchar4 *>(row + 4 * j);
+        const int c = (int)((4 * j) / plane);
+        const float m = P.mean[c], sd = P.stdv[c];
+        *reinterpret_cast<float4 *>(orow + 4 * j) =
+            make_float4(norm_u8(v.x, m, sd), norm_u8(v.y, m, sd), norm_u8(v.z, m, sd),
+                        norm_u8(v.w, m, sd));
+      } else {
+        const int c = (int)(j / plane);
+        orow[j] = norm_u8(row[j], P.mean[c], P.stdv[c]);
+      }
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -531,6 +569,32 @@ int tt_k_adam_multi(float *const *w, const float *const *g, float *const *m, flo
   if (nmax <= 0) return 0;
   hipLaunchKernelGGL(adam_multi_kernel, dim3(grid_for(nmax, 1), count), dim3(256), 0, stream(), L,
                      b1, omb1, b2, omb2, eps, lr_t);
+  return launched();
+}
+
+int tt_k_gather_u8_norm(const uint8_t *src, long nsrc, long sample, long plane, int channels,
+                        const int64_t *idx, long n, const float *mean, const float *stdv,
+                        float *out) {
+  if (n <= 0) return 0;
+  if (!src || !idx || !out || !mean || !stdv || nsrc <= 0 || sample <= 0 || plane <= 0 ||
+      channels < 1 || channels > 4 || plane * channels != sample)
+    return -1;
+  NormParams P{};
+  for (int c = 0; c < channels; c++) {
+    P.mean[c] = mean[c];
+    P.stdv[c] = stdv[c];
+  }
+  const bool vec = sample % 4 == 0 && plane % 4 == 0 && a16(out);
+  const long per = vec ? sample / 4 : sample;
+  long gx = (per + 255) / 256;
+  if (gx > 64) gx = 64;
+  const long gy = n < 65535 ? n : 65535;
+  if (vec)
+    hipLaunchKernelGGL(gather_u8_norm_kernel<true>, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0,
+                       stream(), src, sample, plane, idx, n, P, out);
+  else
+    hipLaunchKernelGGL(gather_u8_norm_kernel<false>, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0,
+                       stream(), src, sample, plane, idx, n, P, out);
   return launched();
 }
 

@@ -187,6 +187,14 @@ class Optim:
     def t(self):
         return LIB.ag_optim_steps(self.ptr)
 
+    @property
+    def lr(self):
+        return LIB.ag_optim_lr(self.ptr)
+
+    @lr.setter
+    def lr(self, value):
+        LIB.ag_optim_set_lr(self.ptr, float(value))
+
     def release(self):
         if self.ptr:
             LIB.ag_optim_release(self.ptr)
