@@ -135,6 +135,28 @@ int tt_k_momentum_multi(float *const *w, const float *const *g, float *const *v,
 int tt_k_adam_multi(float *const *w, const float *const *g, float *const *m, float *const *v,
                     const long *n, int count, float b1, float omb1, float b2, float omb2,
                     float eps, double lr_t);
+/* Implicit-GEMM convolution: the im2col matrix is never formed; the GEMM's
+ * B operand reads x (or the output gradient) directly.  Same results as the
+ * explicit im2col + GEMM forms above, to GEMM rounding.  Return -1 (nothing
+ * launched) for shapes they do not cover: tensors of 2^31 elements or more;
+ * for dX, stride != 1 or padding > kernel-1.
+ *   fwd: out (N,F,Ho,Wo) = conv(x, w) + bias        src/ops_spatial.c:71-127
+ *   dw:  dw (F, C*HH*WW), db (F, optional)         src/autograd.c:467-513
+ *   dx:  dx (N,C,H,W) = conv_transpose(g, w)       src/autograd.c:515-539,406-434 */
+/* Convolutions whose im2col matrix would take at least implicit_min_bytes
+ * use these implicit forms inside tt_conv2d / ag_conv2d (default 256 MiB;
+ * a negative value restores it, 0 uses them wherever they apply). */
+int tth_conv_config(long implicit_min_bytes);
+int tt_k_conv2d_fwd_implicit(const float *x, const float *w, const float *bias, float *out,
+                             int N, int C, int H, int W, int F, int HH, int WW,
+                             int sh, int sw, int ph, int pw, int Ho, int Wo);
+int tt_k_conv2d_dw_implicit(const float *g, const float *x, float *dw, float *db,
+                            int N, int C, int H, int W, int F, int HH, int WW,
+                            int sh, int sw, int ph, int pw, int Ho, int Wo);
+int tt_k_conv2d_dx_implicit(const float *g, const float *w, float *dx,
+                            int N, int C, int H, int W, int F, int HH, int WW,
+                            int sh, int sw, int ph, int pw, int Ho, int Wo);
+
 /* Dataset batch gather + normalisation (see tt_data.h):
  * out[r, j] = ((float)src[idx[r]*sample + j] / 255 - mean[c]) / stdv[c],
  * c = j / plane, channels = sample / plane <= 4.  idx values must be in

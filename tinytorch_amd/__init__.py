@@ -140,6 +140,10 @@ SIGNATURES = [
     ("tt_k_avgpool_bwd", _I, [VP, VP] + [_I] * 10),
     ("tt_k_sgd", _I, [VP, VP, _L, _F]),
     ("tt_k_sgd_multi", _I, [ctypes.POINTER(VP), ctypes.POINTER(VP), ctypes.POINTER(_L), _I, _F]),
+    ("tth_conv_config", _I, [_L]),
+    ("tt_k_conv2d_fwd_implicit", _I, [VP, VP, VP, VP] + [_I] * 13),
+    ("tt_k_conv2d_dw_implicit", _I, [VP, VP, VP, VP] + [_I] * 13),
+    ("tt_k_conv2d_dx_implicit", _I, [VP, VP, VP] + [_I] * 13),
     ("tt_k_gather_u8_norm", _I, [VP, _L, _L, _L, _I, VP, _L, F32P, F32P, VP]),
     ("tt_k_momentum_multi", _I, [ctypes.POINTER(VP)] * 3 + [ctypes.POINTER(_L), _I, _F, _F]),
     ("tt_k_adam_multi", _I, [ctypes.POINTER(VP)] * 4 + [ctypes.POINTER(_L), _I] + [_F] * 5

@@ -397,6 +397,20 @@ static void backward_conv2d(AGNode *n) {
             tt_release(gw);
             tt_release(gb);
         }
+    } else if (needs(w) && !n->col && tt_conv_use_implicit(sizeof(float) * (long)Kc * Ncol)) {
+        /* implicit forward kept no col: dW (and db, from the ones row) read x */
+        const float *x = tt_dev(a->val);
+        Tensor *gw = x ? tt_empty_like(w->val) : NULL;
+        Tensor *gb = gw && needs(b) ? tt_empty_dev(bshp, 1) : NULL;
+        if (gw && (gb || !needs(b)) &&
+            tt_k_conv2d_dw_implicit(gd, x, gw->dev, gb ? gb->dev : NULL, N, C, H, W, F, HH, WW,
+                                    sh, sw, ph, pw, Ho, Wo) == 0) {
+            if (gb) accum_move(b, gb);
+            accum_move(w, gw);
+        } else {
+            tt_release(gw);
+            tt_release(gb);
+        }
     } else {
         if (needs(b)) {
             Tensor *gb = tt_empty_dev(bshp, 1);
@@ -420,6 +434,17 @@ static void backward_conv2d(AGNode *n) {
             else tt_release(gw);
             if (own) ttrt_free(col);
         }
+    }
+    if (needs(a) && tt_conv_use_implicit(sizeof(float) * (long)Kc * Ncol)) {
+        /* stride-1 dX as one implicit GEMM; other strides keep dcol + col2im */
+        const float *wd = tt_dev(w->val);
+        Tensor *ga = wd ? tt_empty_like(a->val) : NULL;
+        if (ga && tt_k_conv2d_dx_implicit(gd, wd, ga->dev, N, C, H, W, F, HH, WW, sh, sw, ph, pw,
+                                          Ho, Wo) == 0) {
+            accum_move(a, ga);
+            return;
+        }
+        tt_release(ga);
     }
     if (needs(a)) {
         const float *wd = tt_dev(w->val);

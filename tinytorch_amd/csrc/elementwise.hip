@@ -271,9 +271,62 @@ __global__ void padones_bwd_rows_kernel(const float *__restrict__ g, float *__re
 // workgroup: probabilities, the seed (p - onehot(y)) * scale and the mean
 // loss, reduced in a fixed order (per-thread row order, then the thread
 // partials through LDS in index order).
+template <int MAXC>
 __global__ void softmax_ce_mean_kernel(const float *__restrict__ x, const int32_t *__restrict__ lab,
                                        float *__restrict__ probs, float *__restrict__ loss_mean,
                                        float *__restrict__ seed, int rows, int cols, float scale) {
+  __shared__ float part[256];
+  float acc = 0.0f;
+  for (int r = threadIdx.x; r < rows; r += blockDim.x) {
+    const float *xr = x + (long)r * cols;
+    float *pr = probs + (long)r * cols;
+    float *sr = seed + (long)r * cols;
+    // the row stays in registers (cols <= MAXC): no global round trips
+    // between the max, exp, normalise and seed passes
+    float v[MAXC];
+#pragma unroll
+    for (int j = 0; j < MAXC; j++) v[j] = j < cols ? xr[j] : -INFINITY;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < MAXC; j++) if (j < cols && v[j] > mx) mx = v[j];
+    if (mx == -INFINITY) {
+#pragma unroll
+      for (int j = 0; j < MAXC; j++) v[j] = 1.0f / (float)cols;
+    } else {
+      float sum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < MAXC; j++)
+        if (j < cols) { v[j] = expf(v[j] - mx); sum += v[j]; }
+#pragma unroll
+      for (int j = 0; j < MAXC; j++) v[j] = v[j] / sum;
+    }
+    const int y = lab[r];
+    float py = 0.0f;
+#pragma unroll
+    for (int j = 0; j < MAXC; j++)
+      if (j < cols) {
+        pr[j] = v[j];
+        sr[j] = (v[j] - (j == y ? 1.0f : 0.0f)) * scale;
+        if (j == y) py = v[j];
+      }
+    acc += -logf(fmaxf(py, 1e-12f));
+  }
+  part[threadIdx.x] = acc;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) part[threadIdx.x] += part[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) loss_mean[0] = part[0] / (float)rows;
+}
+
+// general width: the same passes over global memory
+__global__ void softmax_ce_mean_wide_kernel(const float *__restrict__ x,
+                                            const int32_t *__restrict__ lab,
+                                            float *__restrict__ probs,
+                                            float *__restrict__ loss_mean,
+                                            float *__restrict__ seed, int rows, int cols,
+                                            float scale) {
   __shared__ float part[256];
   float acc = 0.0f;
   for (int r = threadIdx.x; r < rows; r += blockDim.x) {
@@ -504,8 +557,15 @@ int tt_k_padones_bwd(const float *g, float *dx, long M, long K) {
 int tt_k_softmax_ce_mean(const float *logits, const int32_t *labels, float *probs, float *loss_mean,
                          float *seed, long rows, int cols, float scale) {
   if (rows <= 0 || cols <= 0 || rows > TT_CE_MEAN_MAX_ROWS) return -1;
-  hipLaunchKernelGGL(softmax_ce_mean_kernel, dim3(1), dim3(256), 0, stream(), logits, labels, probs,
-                     loss_mean, seed, (int)rows, cols, scale);
+  if (cols <= 16)
+    hipLaunchKernelGGL(softmax_ce_mean_kernel<16>, dim3(1), dim3(256), 0, stream(), logits, labels,
+                       probs, loss_mean, seed, (int)rows, cols, scale);
+  else if (cols <= 32)
+    hipLaunchKernelGGL(softmax_ce_mean_kernel<32>, dim3(1), dim3(256), 0, stream(), logits, labels,
+                       probs, loss_mean, seed, (int)rows, cols, scale);
+  else
+    hipLaunchKernelGGL(softmax_ce_mean_wide_kernel, dim3(1), dim3(256), 0, stream(), logits, labels,
+                       probs, loss_mean, seed, (int)rows, cols, scale);
   return launched();
 }
 

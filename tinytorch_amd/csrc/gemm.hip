@@ -64,6 +64,68 @@ struct Opnd {
   int hw;
 };
 
+// Implicit im2col operand: element (kc, p) of the (C*HH*WW [+1]) x
+// (N*Ho*Wo) im2col matrix of the NCHW tensor x -- x[n][c][ho*sh-ph+kh]
+// [wo*sw-pw+kw] or 0 in the padding, with kc = (c*HH + kh)*WW + kw and
+// p = (n*Ho + ho)*Wo + wo (the reference layout, src/ops_spatial.c:48-67),
+// and, when `ones`, a last row kc = Kc of ones.  The GEMM reads it straight
+// from x: no im2col matrix is written or read.  Element offsets fit in 32
+// bits (checked at launch).
+struct I2C {
+  const float *x;
+  int C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo, Kc, ones;
+};
+
+// Per-kc entry of the workgroup's LDS table: .x = c*H*W + kh*W + kw, .y =
+// kh << 16 | kw, or a negative .y for a row of ones / an empty row.
+constexpr int I2C_ONES = -1, I2C_EMPTY = -2;
+constexpr int I2C_TAB = 1024;  // k entries per workgroup (forward / dX form)
+
+__device__ __forceinline__ int2 i2c_entry(const I2C &cv, int kc, int lim) {
+  if (kc >= lim) return make_int2(0, I2C_EMPTY);
+  if (kc >= cv.Kc) return make_int2(0, cv.ones ? I2C_ONES : I2C_EMPTY);
+  const unsigned taps = (unsigned)(cv.HH * cv.WW);
+  const unsigned c = (unsigned)kc / taps;
+  const unsigned r = (unsigned)kc - c * taps;
+  const unsigned kh = r / (unsigned)cv.WW;
+  const unsigned kw = r - kh * (unsigned)cv.WW;
+  return make_int2((int)(c * (unsigned)(cv.H * cv.W) + kh * (unsigned)cv.W + kw),
+                   (int)((kh << 16) | kw));
+}
+
+// Origin of output pixel p: offset of x[n][0][hi0][wi0] and (hi0, wi0); a
+// pixel at or past `lim` gets an origin that no tap can bring in range.
+struct I2CPix {
+  int base, hi0, wi0;
+};
+
+__device__ __forceinline__ I2CPix i2c_pixel(const I2C &cv, long p, long lim) {
+  I2CPix o{0, -(1 << 30), 0};
+  if (p >= lim) return o;
+  const unsigned hw = (unsigned)(cv.Ho * cv.Wo);
+  const unsigned n = (unsigned)p / hw;
+  const unsigned r = (unsigned)p - n * hw;
+  const unsigned ho = r / (unsigned)cv.Wo;
+  const unsigned wo = r - ho * (unsigned)cv.Wo;
+  o.hi0 = (int)ho * cv.sh - cv.ph;
+  o.wi0 = (int)wo * cv.sw - cv.pw;
+  o.base = (int)(n * (unsigned)(cv.C * cv.H * cv.W)) + o.hi0 * cv.W + o.wi0;
+  return o;
+}
+
+// Branch-free: the load is always issued (from x[0] when the tap falls in
+// the padding) and the value selected afterwards.  A load under a divergent
+// branch makes the compiler wait for it before the branches rejoin, which
+// serialises every element's memory latency.
+__device__ __forceinline__ float i2c_value(const I2C &cv, const I2CPix &px, int2 en) {
+  const int hi = px.hi0 + (en.y >> 16);
+  const int wi = px.wi0 + (en.y & 0xffff);
+  const bool inb = en.y >= 0 && (unsigned)hi < (unsigned)cv.H && (unsigned)wi < (unsigned)cv.W;
+  const float v = cv.x[inb ? px.base + en.x : 0];
+  const float other = (en.y == I2C_ONES && px.hi0 > -(1 << 29)) ? 1.0f : 0.0f;
+  return inb ? v : other;
+}
+
 // Contiguous indices are below 2^31 (checked at launch), so the permuted
 // split uses 32-bit unsigned division -- 64-bit division is a long software
 // sequence on the GPU.
@@ -144,11 +206,12 @@ struct Cfg {
 };
 
 template <int BM, int BN, int BK, int WM, bool A_KC, bool A_PERM, bool B_NC, bool B_PERM,
-          bool VEC, int EPI>
+          bool VEC, int EPI, bool B_I2C>
 __device__ __forceinline__ void gemm_body(float *smem, int M, int N, int K, const Opnd &A,
                                           const Opnd &B, float *__restrict__ C, long ldc,
                                           long split_stride, int kchunk,
-                                          const float *__restrict__ bias, int HW, bool cvec) {
+                                          const float *__restrict__ bias, int HW, bool cvec,
+                                          const I2C &cv) {
   using G = Cfg<BM, BN, BK, WM, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI>;
 
   const int tid = threadIdx.x;
@@ -189,6 +252,48 @@ __device__ __forceinline__ void gemm_body(float *smem, int M, int N, int K, cons
 
   float4 ra[G::A_V4], rb[G::B_V4];
 
+  // ---- implicit im2col B: LDS table of kc decompositions, pixel origins ----
+  // Forward / dX form (B_NC): the table covers this split's k range; each
+  // thread owns one column p (fixed) and 4*B_V4 rows.  dW form (!B_NC): the
+  // table covers the tile's BN rows kc; each thread owns one k column
+  // (p = k0 + tid % BK, decomposed per K tile) and 4*B_V4 rows.
+  static_assert(!B_I2C || (B_NC ? NT % BN == 0 : BN % 32 == 0), "I2C tile shape");
+  constexpr int I2C_RSTEP = B_NC ? (NT / BN) * 4 : (NT / BK) * 4;  // row step between v
+  int2 *tab = reinterpret_cast<int2 *>(smem + 2 * G::STAGE);
+  const int i2c_c = B_NC ? tid % BN : tid % BK;        // owned column in the LDS tile
+  const int i2c_r = B_NC ? (tid / BN) * 4 : (tid / BK) * 4;  // first owned row
+  I2CPix px{0, -(1 << 30), 0};
+  if constexpr (B_I2C) {
+    if constexpr (B_NC) {
+      for (int i = tid; i < nk * BK; i += NT) tab[i] = i2c_entry(cv, kbeg + i, kend);
+      px = i2c_pixel(cv, n0 + i2c_c, N);
+    } else {
+      for (int i = tid; i < BN; i += NT) tab[i] = i2c_entry(cv, (int)n0 + i, N);
+    }
+    __syncthreads();
+  }
+  auto i2c_load = [&](int kt, float4 *xb) {
+    if constexpr (B_I2C) {
+      if constexpr (!B_NC) px = i2c_pixel(cv, kbeg + (long)kt * BK + i2c_c, kend);
+      // all table entries first (one LDS wait), then every load
+      int4 en[G::B_V4][2];
+#pragma unroll
+      for (int v = 0; v < G::B_V4; v++) {
+        const int r = i2c_r + v * I2C_RSTEP;
+        const int4 *tp = reinterpret_cast<const int4 *>(tab + (B_NC ? kt * BK + r : r));
+        en[v][0] = tp[0];
+        en[v][1] = tp[1];
+      }
+#pragma unroll
+      for (int v = 0; v < G::B_V4; v++) {
+        xb[v] = make_float4(i2c_value(cv, px, make_int2(en[v][0].x, en[v][0].y)),
+                            i2c_value(cv, px, make_int2(en[v][0].z, en[v][0].w)),
+                            i2c_value(cv, px, make_int2(en[v][1].x, en[v][1].y)),
+                            i2c_value(cv, px, make_int2(en[v][1].z, en[v][1].w)));
+      }
+    }
+  };
+
   // Interior tiles of unpermuted, 16-byte aligned operands take a branch-free
   // path: per-thread element offsets are fixed for the whole K loop and
   // advance by a uniform stride per K tile.  Edge tiles and permuted
@@ -218,7 +323,9 @@ __device__ __forceinline__ void gemm_body(float *smem, int M, int N, int K, cons
 #pragma unroll
     for (int v = 0; v < G::B_V4; v++) {
       const int q = tid + v * NT;
-      if constexpr (B_NC) {
+      if constexpr (B_I2C) {
+        boff[v] = 0;
+      } else if constexpr (B_NC) {
         const int r = q / (BN / 4), c = (q % (BN / 4)) * 4;
         boff[v] = (long)(kbeg + r) * B.ld + cidx<B_PERM>(B, n0 + c);
       } else {
@@ -240,9 +347,13 @@ __device__ __forceinline__ void gemm_body(float *smem, int M, int N, int K, cons
         else
           xa[v] = *reinterpret_cast<const float4 *>(A.p + aoff[v] + astep);
       }
+      if constexpr (B_I2C) {
+        i2c_load(kt, xb);
+      } else {
 #pragma unroll
-      for (int v = 0; v < G::B_V4; v++)
-        xb[v] = *reinterpret_cast<const float4 *>(B.p + boff[v] + bstep);
+        for (int v = 0; v < G::B_V4; v++)
+          xb[v] = *reinterpret_cast<const float4 *>(B.p + boff[v] + bstep);
+      }
       return;
     }
 #pragma unroll
@@ -255,6 +366,10 @@ __device__ __forceinline__ void gemm_body(float *smem, int M, int N, int K, cons
         const int r = q / (BM / 4), c = (q % (BM / 4)) * 4;
         xa[v] = load4<false, VEC>(A, k0 + r, kend, m0 + c, M);
       }
+    }
+    if constexpr (B_I2C) {
+      i2c_load(kt, xb);
+      return;
     }
 #pragma unroll
     for (int v = 0; v < G::B_V4; v++) {
@@ -279,6 +394,18 @@ __device__ __forceinline__ void gemm_body(float *smem, int M, int N, int K, cons
       if constexpr (A_KC) { r = q / (BK / 4); c = (q % (BK / 4)) * 4; }
       else                { r = q / (BM / 4); c = (q % (BM / 4)) * 4; }
       *reinterpret_cast<float4 *>(sA + r * G::A_LD + c) = xa[v];
+    }
+    if constexpr (B_I2C) {
+      // one column, four consecutive rows per v: scalar LDS writes
+#pragma unroll
+      for (int v = 0; v < G::B_V4; v++) {
+        float *d = sB + (i2c_r + v * I2C_RSTEP) * G::B_LD + i2c_c;
+        d[0] = xb[v].x;
+        d[G::B_LD] = xb[v].y;
+        d[2 * G::B_LD] = xb[v].z;
+        d[3 * G::B_LD] = xb[v].w;
+      }
+      return;
     }
 #pragma unroll
     for (int v = 0; v < G::B_V4; v++) {
@@ -423,15 +550,17 @@ __device__ __forceinline__ void gemm_body(float *smem, int M, int N, int K, cons
 }
 
 template <int BM, int BN, int BK, int WM, bool A_KC, bool A_PERM, bool B_NC, bool B_PERM,
-          bool VEC, int EPI>
+          bool VEC, int EPI, bool B_I2C>
 __global__ void __launch_bounds__(NT)
 gemm_mfma_kernel(int M, int N, int K, Opnd A, Opnd B, float *__restrict__ C, long ldc,
                  long split_stride, int kchunk, const float *__restrict__ bias, int HW,
-                 bool cvec) {
+                 bool cvec, I2C cv) {
   using G = Cfg<BM, BN, BK, WM, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI>;
-  __shared__ __attribute__((aligned(16))) float smem[2 * G::STAGE];
-  gemm_body<BM, BN, BK, WM, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI>(
-      smem, M, N, K, A, B, C, ldc, split_stride, kchunk, bias, HW, cvec);
+  // implicit im2col adds its int2 table (2 floats per entry)
+  constexpr int TAB = B_I2C ? 2 * (B_NC ? I2C_TAB : BN) : 0;
+  __shared__ __attribute__((aligned(16))) float smem[2 * G::STAGE + TAB];
+  gemm_body<BM, BN, BK, WM, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI, B_I2C>(
+      smem, M, N, K, A, B, C, ldc, split_stride, kchunk, bias, HW, cvec, cv);
 }
 
 // The 256x256 tile keeps 256 fp32 accumulators per lane: one wave per SIMD,
@@ -444,8 +573,8 @@ gemm_mfma_big_kernel(int M, int N, int K, Opnd A, Opnd B, float *__restrict__ C,
                      bool cvec) {
   using G = Cfg<BM, BN, BK, WM, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI>;
   __shared__ __attribute__((aligned(16))) float smem[2 * G::STAGE];
-  gemm_body<BM, BN, BK, WM, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI>(
-      smem, M, N, K, A, B, C, ldc, split_stride, kchunk, bias, HW, cvec);
+  gemm_body<BM, BN, BK, WM, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI, false>(
+      smem, M, N, K, A, B, C, ldc, split_stride, kchunk, bias, HW, cvec, I2C{});
 }
 
 // Deterministic split-K reduction: out = sum_{z=0..S-1} ws[z] (+ epilogue).
@@ -488,9 +617,13 @@ inline hipStream_t stream() { return (hipStream_t)ttrt_stream(); }
 inline bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 // Tile configurations (BM x BN, wave grid WM x 4/WM).
-enum Tile { T128x128 = 0, T128x64, T64x64, T32x256, T64x256, T256x256, T256x128, NTILE };
-constexpr int TILE_BM[NTILE] = {128, 128, 64, 32, 64, 256, 256};
-constexpr int TILE_BN[NTILE] = {128, 64, 64, 256, 256, 256, 128};
+// (the K64 tiles take 64 k per LDS stage: half the K iterations and twice
+// the loads in flight per iteration, for latency-bound skinny GEMMs)
+enum Tile { T128x128 = 0, T128x64, T64x64, T32x256, T64x256, T256x256, T256x128, T64x128,
+            T32x128, T64x64K64, T32x128K64, NTILE };
+constexpr int TILE_BM[NTILE] = {128, 128, 64, 32, 64, 256, 256, 64, 32, 64, 32};
+constexpr int TILE_BN[NTILE] = {128, 64, 64, 256, 256, 256, 128, 128, 128, 64, 128};
+constexpr int TILE_BK[NTILE] = {32, 32, 32, 32, 32, 32, 32, 32, 32, 64, 64};
 
 // tuning override (tth_gemm_config): -1 = automatic
 int g_force_tile = -1, g_force_splits = -1;
@@ -523,14 +656,25 @@ Plan plan(int M, int N, int K) {
   for (int t : big)
     if (ntiles(t, M, N) >= CUS && fill(t, M, N) >= 0.87) { chosen = t; break; }
   if (chosen < 0) {
-    const int small[] = {T128x64, T64x64, T32x256, T64x256};
+    // small tiles: the best output fill first; among tiles within 2 % of it,
+    // the one with the most workgroups.  These GEMMs are bound by memory
+    // latency, which several workgroups per CU hide better than one larger
+    // one (measured: 2 x 64x64 per CU beat 1 x 64x128 on the conv GEMMs).
+    const int small[] = {T128x64, T64x64, T32x256, T64x256, T64x128, T32x128};
+    auto allowed = [&](int t) {
+      if (t == T128x64 && (N > 64 || ntiles(t, M, N) < CUS)) return false;
+      if ((t == T32x256 || t == T32x128) && M > 32) return false;
+      if ((t == T64x256 || t == T64x128) && M > 64) return false;
+      return true;
+    };
     double best = -1.0;
+    for (int t : small)
+      if (allowed(t)) best = fmax(best, fill(t, M, N));
+    long most = -1;
     for (int t : small) {
-      if (t == T128x64 && (N > 64 || ntiles(t, M, N) < CUS)) continue;
-      if (t == T32x256 && M > 32) continue;
-      if (t == T64x256 && M > 64) continue;
-      const double f = fill(t, M, N);
-      if (f > best + 1e-9) { best = f; chosen = t; }
+      if (!allowed(t) || fill(t, M, N) < best - 0.02) continue;
+      const long nt = ntiles(t, M, N);
+      if (nt > most) { most = nt; chosen = t; }
     }
   }
   p.tile = chosen;
@@ -546,36 +690,50 @@ Plan plan(int M, int N, int K) {
     while (s < 256 && tiles * s * 2 <= 4L * CUS && (long)K / (s * 2) >= 256) s *= 2;
   if (g_force_splits >= 1) s = g_force_splits;
   int kc = (K + s - 1) / s;
-  kc = (kc + 31) / 32 * 32;
+  const int bk = TILE_BK[p.tile];
+  kc = (kc + bk - 1) / bk * bk;
   p.kchunk = kc;
   p.splits = (K + kc - 1) / kc;
   return p;
 }
 
-template <int BM, int BN, int WM, bool A_KC, bool A_PERM, bool B_NC, bool B_PERM, bool VEC,
-          int EPI>
+template <int BM, int BN, int BK, int WM, bool A_KC, bool A_PERM, bool B_NC, bool B_PERM,
+          bool VEC, int EPI, bool B_I2C>
 void launch_tile(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ldc,
-                 long split_stride, int splits, int kchunk, const float *bias, int HW) {
+                 long split_stride, int splits, int kchunk, const float *bias, int HW,
+                 const I2C &cv) {
   const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   dim3 grid(tiles, 1, splits);
   // vector epilogue stores need 16-byte aligned rows (NCHW: HW a multiple of 4)
   const bool cvec = aligned16(C) && (EPI == EPI_STORE ? (ldc % 4 == 0) : (HW % 4 == 0));
-  if constexpr (BM * BN >= 256 * 256)
-    hipLaunchKernelGGL((gemm_mfma_big_kernel<BM, BN, 32, WM, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI>),
+  if constexpr (BM * BN >= 256 * 256) {
+    static_assert(!B_I2C, "implicit im2col is not built for the 256x256 tile");
+    hipLaunchKernelGGL((gemm_mfma_big_kernel<BM, BN, BK, WM, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI>),
                        grid, dim3(NT), 0, stream(), M, N, K, A, B, C, ldc, split_stride, kchunk,
                        bias, HW, cvec);
-  else
-    hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, 32, WM, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI>),
-                       grid, dim3(NT), 0, stream(), M, N, K, A, B, C, ldc, split_stride, kchunk,
-                       bias, HW, cvec);
+  } else {
+    hipLaunchKernelGGL(
+        (gemm_mfma_kernel<BM, BN, BK, WM, A_KC, A_PERM, B_NC, B_PERM, VEC, EPI, B_I2C>), grid,
+        dim3(NT), 0, stream(), M, N, K, A, B, C, ldc, split_stride, kchunk, bias, HW, cvec, cv);
+  }
 }
 
-template <bool A_KC, bool A_PERM, bool B_NC, bool B_PERM, int EPI>
+template <bool A_KC, bool A_PERM, bool B_NC, bool B_PERM, int EPI, bool B_I2C = false>
 int run(int M, int N, int K, Opnd A, Opnd B, float *C, long ldc, const float *bias, int HW,
-        bool vec) {
+        bool vec, const I2C &cv = I2C{}) {
   if (M <= 0 || N <= 0) return 0;
   // K == 0 runs no K tiles: the epilogue stores zeros (plus bias)
   Plan p = plan(M, N, K > 0 ? K : 1);
+  if constexpr (B_I2C) {
+    // no 256-wide big tile; a split's k range must fit the LDS kc table
+    if (p.tile == T256x256 || p.tile == T256x128) p.tile = T128x128;
+    if (B_NC && p.kchunk > I2C_TAB) {
+      const int s = (K + I2C_TAB - 1) / I2C_TAB;
+      const int bk = TILE_BK[p.tile];
+      p.kchunk = ((K + s - 1) / s + bk - 1) / bk * bk;
+      p.splits = (K + p.kchunk - 1) / p.kchunk;
+    }
+  }
   float *target = C;
   long tgt_ld = ldc;
   float *ws = nullptr;
@@ -588,12 +746,13 @@ int run(int M, int N, int K, Opnd A, Opnd B, float *C, long ldc, const float *bi
     epi_direct = 0;
   }
   const long sstride = (long)M * N;
-#define TT_LAUNCH(BM_, BN_, WM_, VEC_, EPI_)                                                  \
-  launch_tile<BM_, BN_, WM_, A_KC, A_PERM, B_NC, B_PERM, VEC_, EPI_>(                         \
-      M, N, K, A, B, target, tgt_ld, sstride, p.splits, p.kchunk, bias, HW)
-#define TT_VEC(BM_, BN_, WM_, EPI_)                 \
-  if (vec) TT_LAUNCH(BM_, BN_, WM_, true, EPI_);     \
-  else TT_LAUNCH(BM_, BN_, WM_, false, EPI_);
+#define TT_LAUNCH(BM_, BN_, BK_, WM_, VEC_, EPI_)                                             \
+  launch_tile<BM_, BN_, BK_, WM_, A_KC, A_PERM, B_NC, B_PERM, VEC_, EPI_, B_I2C>(             \
+      M, N, K, A, B, target, tgt_ld, sstride, p.splits, p.kchunk, bias, HW, cv)
+#define TT_VECK(BM_, BN_, BK_, WM_, EPI_)                 \
+  if (vec) TT_LAUNCH(BM_, BN_, BK_, WM_, true, EPI_);      \
+  else TT_LAUNCH(BM_, BN_, BK_, WM_, false, EPI_);
+#define TT_VEC(BM_, BN_, WM_, EPI_) TT_VECK(BM_, BN_, 32, WM_, EPI_)
 #define TT_SHAPES(EPI_)                                     \
   switch (p.tile) {                                         \
     case T128x128: TT_VEC(128, 128, 2, EPI_) break;         \
@@ -601,12 +760,17 @@ int run(int M, int N, int K, Opnd A, Opnd B, float *C, long ldc, const float *bi
     case T64x64:   TT_VEC(64, 64, 2, EPI_) break;           \
     case T32x256:  TT_VEC(32, 256, 1, EPI_) break;          \
     case T64x256:  TT_VEC(64, 256, 1, EPI_) break;          \
-    case T256x256: TT_VEC(256, 256, 2, EPI_) break;         \
-    default:       TT_VEC(256, 128, 2, EPI_) break;         \
+    case T64x128:  TT_VEC(64, 128, 1, EPI_) break;          \
+    case T32x128:  TT_VEC(32, 128, 1, EPI_) break;          \
+    case T64x64K64:  TT_VECK(64, 64, 64, 2, EPI_) break;    \
+    case T32x128K64: TT_VECK(32, 128, 64, 1, EPI_) break;   \
+    case T256x256: if constexpr (!B_I2C) { TT_VEC(256, 256, 2, EPI_) } break; \
+    default:       if constexpr (!B_I2C) { TT_VEC(256, 128, 2, EPI_) } break; \
   }
   if (epi_direct) { TT_SHAPES(EPI) } else { TT_SHAPES(EPI_STORE) }
 #undef TT_SHAPES
 #undef TT_VEC
+#undef TT_VECK
 #undef TT_LAUNCH
   if (hipGetLastError() != hipSuccess) { if (ws) ttrt_free(ws); return -3; }
   if (ws) {
@@ -689,4 +853,95 @@ extern "C" int tt_k_conv_dcol(int F, int Kc, long Ncol, int HW, const float *W, 
   Opnd a{W, Kc, 0, 1}, b{g, HW, (long)F * HW, HW};
   const bool vec = aligned16(W) && aligned16(g) && (Kc % 4 == 0) && (HW % 4 == 0);
   return run<false, false, true, true, EPI_STORE>(Kc, (int)Ncol, F, a, b, dcol, Ncol, nullptr, 1, vec);
+}
+
+// ---- implicit-GEMM convolution (im2col folded into the B operand) ----
+
+namespace {
+
+// Kernel taps of the transposed convolution: wt[c][(f*HH + kh)*WW + kw] =
+// w[f][c][HH-1-kh][WW-1-kw] (C x F*HH*WW, k-contiguous rows).
+__global__ void conv_flip_weights_kernel(const float *__restrict__ w, float *__restrict__ wt, int F,
+                                         int C, int HH, int WW) {
+  const int taps = HH * WW;
+  const long total = (long)F * C * taps;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (long)gridDim.x * blockDim.x) {
+    const int t = (int)(i % taps);
+    const long fc = i / taps;
+    const int c = (int)(fc % C), f = (int)(fc / C);
+    const int kh = t / WW, kw = t - kh * WW;
+    wt[((long)c * F + f) * taps + (HH - 1 - kh) * WW + (WW - 1 - kw)] = w[i];
+  }
+}
+
+bool i2c_fits(long xnumel, long ncol) { return xnumel < 0x7fffffffL && ncol < 0x7fffffffL; }
+
+}  // namespace
+
+// out = conv(x, w) + bias in NCHW: the conv forward GEMM W (F x Kc) times the
+// implicit im2col of x (reference src/ops_spatial.c:71-127).
+extern "C" int tt_k_conv2d_fwd_implicit(const float *x, const float *w, const float *bias,
+                                        float *out, int N, int C, int H, int W, int F, int HH,
+                                        int WW, int sh, int sw, int ph, int pw, int Ho, int Wo) {
+  if (!x || !w || !out || N <= 0 || C <= 0 || F <= 0 || HH <= 0 || WW <= 0 || Ho <= 0 || Wo <= 0)
+    return -1;
+  const long ncol = (long)N * Ho * Wo;
+  const long kc = (long)C * HH * WW;
+  if (!i2c_fits((long)N * C * H * W, ncol) || kc > 0x7fffffffL) return -1;
+  I2C cv{x, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo, (int)kc, 0};
+  Opnd a{w, kc, 0, 1}, b{nullptr, 0, 0, 1};
+  const bool vec = aligned16(w) && kc % 4 == 0;
+  return run<true, false, true, false, EPI_BIAS_NCHW, true>(F, (int)ncol, (int)kc, a, b, out, 0,
+                                                            bias, Ho * Wo, vec, cv);
+}
+
+// dW (F x Kc) = Gperm (F x N*Ho*Wo) times the implicit im2col of x,
+// transposed; with db, the ones row gives db in the same GEMM (reference
+// src/autograd.c:467-513).
+extern "C" int tt_k_conv2d_dw_implicit(const float *g, const float *x, float *dw, float *db,
+                                       int N, int C, int H, int W, int F, int HH, int WW, int sh,
+                                       int sw, int ph, int pw, int Ho, int Wo) {
+  if (!g || !x || !dw || N <= 0 || C <= 0 || F <= 0 || HH <= 0 || WW <= 0 || Ho <= 0 || Wo <= 0)
+    return -1;
+  const long ncol = (long)N * Ho * Wo;
+  const long kc = (long)C * HH * WW;
+  if (!i2c_fits((long)N * C * H * W, ncol) || kc >= 0x7fffffffL) return -1;
+  const int HWo = Ho * Wo;
+  I2C cv{x, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo, (int)kc, db ? 1 : 0};
+  Opnd a{g, HWo, (long)F * HWo, HWo}, b{nullptr, 0, 0, 1};
+  const bool vec = aligned16(g) && HWo % 4 == 0;
+  if (db)
+    return run<true, true, false, false, EPI_DW_BIAS, true>(F, (int)kc + 1, (int)ncol, a, b, dw,
+                                                            kc, db, 1, vec, cv);
+  return run<true, true, false, false, EPI_STORE, true>(F, (int)kc, (int)ncol, a, b, dw, kc,
+                                                        nullptr, 1, vec, cv);
+}
+
+// dX of a stride-1 convolution as the convolution of the output gradient g
+// with the flipped, transposed kernel and padding HH-1-ph / WW-1-pw: the
+// reference's dcol = W^T * Gperm followed by col2im (src/autograd.c:515-539,
+// 406-434) in one implicit GEMM, M = C, K = F*HH*WW, N = N*H*W.
+extern "C" int tt_k_conv2d_dx_implicit(const float *g, const float *w, float *dx, int N, int C,
+                                       int H, int W, int F, int HH, int WW, int sh, int sw, int ph,
+                                       int pw, int Ho, int Wo) {
+  if (!g || !w || !dx || N <= 0 || C <= 0 || F <= 0 || HH <= 0 || WW <= 0) return -1;
+  if (sh != 1 || sw != 1 || ph > HH - 1 || pw > WW - 1) return -1;
+  if (Ho != H + 2 * ph - HH + 1 || Wo != W + 2 * pw - WW + 1) return -1;
+  const long kt = (long)F * HH * WW;
+  const long npix = (long)N * H * W;
+  if (!i2c_fits((long)N * F * Ho * Wo, npix) || kt > 0x7fffffffL) return -1;
+  float *wt = (float *)ttrt_alloc(sizeof(float) * (size_t)kt * C);
+  if (!wt) return -2;
+  long blocks = (kt * C + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(conv_flip_weights_kernel, dim3((unsigned)blocks), dim3(256), 0, stream(), w,
+                     wt, F, C, HH, WW);
+  I2C cv{g, F, Ho, Wo, HH, WW, 1, 1, HH - 1 - ph, WW - 1 - pw, H, W, (int)kt, 0};
+  Opnd a{wt, kt, 0, 1}, b{nullptr, 0, 0, 1};
+  const bool vec = kt % 4 == 0;
+  const int rc = run<true, false, true, false, EPI_BIAS_NCHW, true>(
+      C, (int)npix, (int)kt, a, b, dx, 0, nullptr, H * W, vec, cv);
+  ttrt_free(wt);  // stream-ordered: the GEMM above is queued before any reuse
+  return rc;
 }

@@ -141,6 +141,19 @@ Tensor *tt_reshape(const Tensor *a, const long *new_shape, int new_ndim) {
     return out;
 }
 
+/* Convolutions whose im2col matrix would reach this many bytes run as
+ * implicit GEMMs (the matrix is never formed); below it the explicit
+ * im2col + GEMM is as fast or faster at the sizes measured, and the forward
+ * matrix is kept for the weight gradient. */
+static long g_implicit_min_bytes = 256L << 20;
+
+int tth_conv_config(long implicit_min_bytes) {
+    g_implicit_min_bytes = implicit_min_bytes < 0 ? (256L << 20) : implicit_min_bytes;
+    return 0;
+}
+
+int tt_conv_use_implicit(long col_bytes) { return col_bytes >= g_implicit_min_bytes; }
+
 Tensor *tt_conv2d_keepcol(const Tensor *a, const Tensor *w, const Tensor *b, int sh, int sw,
                           int ph, int pw, float **col_out, int ones_row) {
     if (col_out) *col_out = NULL;
@@ -165,6 +178,10 @@ Tensor *tt_conv2d_keepcol(const Tensor *a, const Tensor *w, const Tensor *b, int
     if (!out) return NULL;
     const int Kc = C * HH * WW;
     const long Ncol = (long)N * Ho * Wo;
+    if (tt_conv_use_implicit(sizeof(float) * (long)Kc * Ncol) &&
+        tt_k_conv2d_fwd_implicit(x, wd, bd, out->dev, N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho,
+                                 Wo) == 0)
+        return out;  /* no col: the backward pass reads x directly too */
     const int rows = (col_out && ones_row) ? Kc + 1 : Kc;
     float *col = (float *)ttrt_alloc(sizeof(float) * (size_t)rows * (size_t)Ncol);
     if (!col) return fail(out);

@@ -18,6 +18,7 @@ void    tt_mark_dev_written(Tensor *t);
 /* conv2d forward that can hand back its im2col matrix (Kc x Ncol floats of
  * device memory owned by the caller, release with ttrt_free); with ones_row
  * the matrix gets a (Kc+1)-th row of ones for the fused bias gradient */
+int tt_conv_use_implicit(long col_bytes);
 Tensor *tt_conv2d_keepcol(const Tensor *a, const Tensor *w, const Tensor *b,
                           int stride_h, int stride_w, int pad_h, int pad_w, float **col_out,
                           int ones_row);
