@@ -55,9 +55,13 @@ int tt_k_gemm(int M, int N, int K,
               float *C, int ldc);
 
 /* Tuning hook: force the GEMM tile (0: 128x128, 1: 128x64, 2: 64x64, 3: 32x256,
- * 4: 64x256, 5: 256x256, 6: 256x128) and/or split-K count for every later
+ * 4: 64x256, 5: 256x256, 6: 256x128, 7: 64x128, 8: 32x128, 9: 64x64 with 64-k
+ * stages, 10: 32x128 with 64-k stages) and/or split-K count for every later
  * call; -1 restores the automatic choice. */
 int tth_gemm_config(int tile, int splits);
+/* Tuning hook: 0 disables, 1 (default) enables the direct-to-LDS kernel used
+ * for plain NN GEMMs on whole 256x256 tiles. */
+int tth_gemm_direct(int on);
 
 /* Convolution GEMMs over the im2col matrix col[(c,kh,kw)][(n,ho,wo)]
  * (Kc = C*HH*WW rows, Ncol = N*Ho*Wo columns, HW = Ho*Wo):

@@ -612,6 +612,177 @@ splitk_reduce_kernel(const float *__restrict__ ws, float *__restrict__ C, int M,
   }
 }
 
+// ---- 256x256 NN tile with direct global->LDS loads ----
+// gfx950's global_load_lds_dwordx4 moves 16 bytes per lane from global memory
+// straight into LDS (lane i of a wave writes bytes [16i, 16i+16) after the
+// wave-uniform LDS address), so the next K tile needs no staging registers:
+// the 64 VGPRs the register-staged kernel spends on it go to fragment
+// buffers, and the ds_write pass disappears.  Layout:
+//   B (rows k, 256 n): one wave load fills one padded LDS row, as before;
+//   A (rows m, 32 k, unpadded 128-byte rows): a wave load fills 8 rows, and
+//     16-byte chunk c of row R sits in slot c ^ ((R >> 1) & 7), so the
+//     fragment reads (32 rows at one chunk per half-wave) spread over all
+//     banks; each lane loads the global chunk that belongs in its slot.
+// Interior-only: the host uses it when M and N are multiples of 256, the K
+// range of every split a multiple of 32, and all rows 16-byte aligned.
+constexpr int D_BM = 256, D_BN = 256, D_BK = 32;
+constexpr int D_A_LD = D_BK;
+constexpr int D_B_LD = D_BN + 8;
+constexpr int D_A_SZ = D_BM * D_A_LD;
+constexpr int D_B_SZ = D_BK * D_B_LD;
+constexpr int D_STAGE = D_A_SZ + D_B_SZ;
+
+// One wave-wide direct load.  Issued from inline assembly on purpose: the
+// compiler's own LDS-DMA builtin makes it assume the DMA may alias every
+// later LDS read, and it then waits for the next tile's loads before the
+// current tile's fragment reads, serialising the pipeline.  Here the kernel
+// orders them itself: s_waitcnt vmcnt(0) + barrier before a tile is read.
+// M0 holds the wave-uniform LDS byte address of lane 0's 16 bytes.
+__device__ __forceinline__ void g2lds16(const float *src, const float *lds) {
+  const unsigned addr = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(addr), "v"(src)
+               : "memory", "m0");
+}
+
+__device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+__global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1)))
+gemm_nn_direct_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
+                      const float *__restrict__ B, long ldb, float *__restrict__ C, long ldc,
+                      long split_stride, int kchunk) {
+  __shared__ __attribute__((aligned(16))) float smem[2 * D_STAGE];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+
+  const int tiles_m = M / D_BM, tiles_n = N / D_BN;
+  const int ntiles = tiles_m * tiles_n;
+  int pid = blockIdx.x;
+  if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
+  const int group = GROUP_M * tiles_n;
+  const int first_m = (pid / group) * GROUP_M;
+  const int gsz = min(tiles_m - first_m, GROUP_M);
+  const int tm = first_m + (pid % group) % gsz;
+  const int tn = (pid % group) / gsz;
+  const long m0 = (long)tm * D_BM;
+  const long n0 = (long)tn * D_BN;
+  const int kbeg = blockIdx.z * kchunk;
+  const int nk = (min(K, kbeg + kchunk) - kbeg) / D_BK;
+  C += (long)blockIdx.z * split_stride;
+
+  const int wm = (wave >> 1) * 128;
+  const int wn = (wave & 1) * 128;
+
+  // per-lane global sources of the 8 + 8 wave loads of one K tile
+  const int arow = wave * 64 + (lane >> 3);  // + 8j
+  const float *asrc[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const int R = arow + 8 * j;
+    const int c = (lane & 7) ^ ((R >> 1) & 7);
+    asrc[j] = A + (m0 + R) * lda + kbeg + 4 * c;
+  }
+  const float *bsrc = B + (long)(kbeg + wave * 8) * ldb + n0 + 4 * lane;
+
+  auto issue = [&](int kt, int buf) {
+    float *sA = smem + buf * D_STAGE;
+    float *sB = sA + D_A_SZ;
+    const long ka = (long)kt * D_BK;
+#pragma unroll
+    for (int j = 0; j < 8; j++) g2lds16(asrc[j] + ka, sA + (wave * 64 + 8 * j) * D_A_LD);
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      g2lds16(bsrc + (ka + j) * ldb, sB + (wave * 8 + j) * D_B_LD);
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+  // fragments of k-step kk (8 k): a[i][s] for the 4 row blocks, b[j][s]
+  // for the 4 interleaved column blocks
+  auto frags = [&](const float *sA, const float *sB, int kk, float (*a)[4], float (*b)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int R = wm + 32 * i + l32;
+      const int slot = ((kk >> 2) + g) ^ ((R >> 1) & 7);
+      const float4 t = *reinterpret_cast<const float4 *>(sA + R * D_A_LD + 4 * slot);
+      a[i][0] = t.x; a[i][1] = t.y; a[i][2] = t.z; a[i][3] = t.w;
+    }
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      const float4 t =
+          *reinterpret_cast<const float4 *>(sB + (kk + 4 * g + s) * D_B_LD + wn + 4 * l32);
+      b[0][s] = t.x; b[1][s] = t.y; b[2][s] = t.z; b[3][s] = t.w;
+    }
+  };
+  // the fragments of step kk+8 are read while the MFMAs of step kk run
+  auto compute = [&](int buf) {
+    const float *sA = smem + buf * D_STAGE;
+    const float *sB = sA + D_A_SZ;
+    float a[2][4][4], b[2][4][4];
+    frags(sA, sB, 0, a[0], b[0]);
+#pragma unroll
+    for (int q = 0; q < D_BK / 8; q++) {
+      if (q + 1 < D_BK / 8) frags(sA, sB, 8 * (q + 1), a[(q + 1) & 1], b[(q + 1) & 1]);
+#pragma unroll
+      for (int s = 0; s < 4; s++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+          for (int j = 0; j < 4; j++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[q & 1][i][s], b[q & 1][j][s],
+                                                             acc[i][j], 0, 0, 0);
+    }
+    // Schedule (the compiler otherwise sinks each fragment read to just
+    // before its first MFMA and waits on it): the first step's 8 reads, then
+    // per step the next step's 8 reads spread over the first 16 MFMAs.
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // DS reads
+#pragma unroll
+    for (int q = 0; q + 1 < D_BK / 8; q++) {
+#pragma unroll
+      for (int r = 0; r < 8; r++) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 48, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 64, 0);
+  };
+
+  if (nk > 0) {
+    issue(0, 0);
+    wait_vm_all();
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+      if (kt + 1 < nk) issue(kt + 1, (kt + 1) & 1);
+      compute(kt & 1);
+      wait_vm_all();
+      __syncthreads();
+    }
+  }
+
+  // epilogue: block i row rho (acc r: rho = 8*(r/4) + 4*g + r%4), columns
+  // wn + 4*l32 .. +3 (the interleaved B blocks j = 0..3)
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int rho = 8 * (r >> 2) + 4 * g + (r & 3);
+      const long row = m0 + wm + 32 * i + rho;
+      *reinterpret_cast<float4 *>(C + row * ldc + n0 + wn + 4 * l32) =
+          make_float4(acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]);
+    }
+}
+
 inline hipStream_t stream() { return (hipStream_t)ttrt_stream(); }
 
 inline bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
@@ -627,6 +798,7 @@ constexpr int TILE_BK[NTILE] = {32, 32, 32, 32, 32, 32, 32, 32, 32, 64, 64};
 
 // tuning override (tth_gemm_config): -1 = automatic
 int g_force_tile = -1, g_force_splits = -1;
+int g_direct = 1;  // direct-to-LDS NN kernel enabled (tth_gemm_direct)
 
 struct Plan {
   int tile, splits, kchunk;
@@ -767,7 +939,19 @@ int run(int M, int N, int K, Opnd A, Opnd B, float *C, long ldc, const float *bi
     case T256x256: if constexpr (!B_I2C) { TT_VEC(256, 256, 2, EPI_) } break; \
     default:       if constexpr (!B_I2C) { TT_VEC(256, 128, 2, EPI_) } break; \
   }
-  if (epi_direct) { TT_SHAPES(EPI) } else { TT_SHAPES(EPI_STORE) }
+  bool done = false;
+  if constexpr (A_KC && !A_PERM && B_NC && !B_PERM && !B_I2C && EPI == EPI_STORE) {
+    // plain NN GEMM on whole 256x256 tiles: the direct-to-LDS kernel
+    if (g_direct && p.tile == T256x256 && vec && M % D_BM == 0 && N % D_BN == 0 &&
+        K % D_BK == 0 && p.kchunk % D_BK == 0 && aligned16(target) && tgt_ld % 4 == 0) {
+      const dim3 grid((M / D_BM) * (N / D_BN), 1, p.splits);
+      hipLaunchKernelGGL(gemm_nn_direct_kernel, grid, dim3(NT), 0, stream(), M, N, K, A.p, A.ld,
+                         B.p, B.ld, target, tgt_ld, sstride, p.kchunk);
+      done = true;
+    }
+  }
+  if (done) {
+  } else if (epi_direct) { TT_SHAPES(EPI) } else { TT_SHAPES(EPI_STORE) }
 #undef TT_SHAPES
 #undef TT_VEC
 #undef TT_VECK
@@ -801,6 +985,11 @@ int run(int M, int N, int K, Opnd A, Opnd B, float *C, long ldc, const float *bi
 }
 
 }  // namespace
+
+extern "C" int tth_gemm_direct(int on) {
+  g_direct = on ? 1 : 0;
+  return 0;
+}
 
 extern "C" int tth_gemm_config(int tile, int splits) {
   if (tile >= NTILE || splits > 1024) return -1;
