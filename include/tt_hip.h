@@ -60,7 +60,7 @@ int tt_k_gemm(int M, int N, int K,
  * call; -1 restores the automatic choice. */
 int tth_gemm_config(int tile, int splits);
 /* Tuning hook: 0 disables, 1 (default) enables the direct-to-LDS kernel used
- * for plain NN GEMMs on whole 256x256 tiles. */
+ * for plain GEMMs (any transposition) on whole 256x256 tiles. */
 int tth_gemm_direct(int on);
 
 /* Convolution GEMMs over the im2col matrix col[(c,kh,kw)][(n,ho,wo)]

@@ -414,22 +414,25 @@ def test_conv_dw_bias_fused(tlib, case):
     assert np.abs(db - rdb).max() <= 1e-5 * np.abs(g).sum(axis=(0, 2, 3)).max() + 1e-6
 
 
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("M,N,K,splits", [(512, 768, 1056, 1), (512, 768, 1056, 3),
                                           (256, 256, 32, 1), (768, 512, 4096, 4)])
-def test_gemm_direct_lds_kernel(tlib, M, N, K, splits):
-    """The direct-to-LDS 256x256 NN kernel (forced: tile 5) against float64,
-    and bit for bit against the register-staged 256x256 kernel, which sums
-    in the same order; with split-K the deterministic reduction follows."""
-    A, B = u(M, K), u(K, N)
+def test_gemm_direct_lds_kernel(tlib, M, N, K, splits, ta, tb):
+    """The direct-to-LDS 256x256 kernel (forced: tile 5) in every
+    transposition layout against float64, and bit for bit against the
+    register-staged 256x256 kernel, which sums in the same order; with
+    split-K the deterministic reduction follows."""
+    A = u(K, M) if ta else u(M, K)
+    B = u(N, K) if tb else u(K, N)
     try:
         tlib.tth_gemm_config(5, splits)
-        C = run_gemm(tlib, M, N, K, 0, 0, A, B)
+        C = run_gemm(tlib, M, N, K, ta, tb, A, B)
         tlib.tth_gemm_direct(0)
-        C_staged = run_gemm(tlib, M, N, K, 0, 0, A, B)
+        C_staged = run_gemm(tlib, M, N, K, ta, tb, A, B)
     finally:
         tlib.tth_gemm_direct(1)
         tlib.tth_gemm_config(-1, -1)
-    ref = A.astype(np.float64) @ B.astype(np.float64)
+    ref = (A.T if ta else A).astype(np.float64) @ (B.T if tb else B).astype(np.float64)
     norm, rel = gemm_err(C, ref, K, np.abs(A).max(), np.abs(B).max())
     assert norm <= GEMM_TOL and rel <= GEMM_TOL, (norm, rel)
     assert bits_equal(C, C_staged)

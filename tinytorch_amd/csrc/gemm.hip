@@ -612,25 +612,27 @@ splitk_reduce_kernel(const float *__restrict__ ws, float *__restrict__ C, int M,
   }
 }
 
-// ---- 256x256 NN tile with direct global->LDS loads ----
+// ---- 256x256 tile with direct global->LDS loads ----
 // gfx950's global_load_lds_dwordx4 moves 16 bytes per lane from global memory
 // straight into LDS (lane i of a wave writes bytes [16i, 16i+16) after the
 // wave-uniform LDS address), so the next K tile needs no staging registers:
 // the 64 VGPRs the register-staged kernel spends on it go to fragment
-// buffers, and the ds_write pass disappears.  Layout:
-//   B (rows k, 256 n): one wave load fills one padded LDS row, as before;
-//   A (rows m, 32 k, unpadded 128-byte rows): a wave load fills 8 rows, and
-//     16-byte chunk c of row R sits in slot c ^ ((R >> 1) & 7), so the
-//     fragment reads (32 rows at one chunk per half-wave) spread over all
-//     banks; each lane loads the global chunk that belongs in its slot.
+// buffers, and the ds_write pass disappears.  Operand layouts in LDS:
+//   m/n-contiguous (NN's B, TN's A; rows k of 256 floats): one wave load
+//     fills one padded row, fragments read as 4 consecutive m/n per lane
+//     (interleaved blocks, as in the register-staged kernel);
+//   k-contiguous (NN's A, NT's B; rows m/n of 32 k, unpadded 128-byte rows):
+//     a wave load fills 8 rows, and 16-byte chunk c of row R sits in slot
+//     c ^ ((R >> 1) & 7), so the fragment reads (32 rows at one chunk per
+//     half-wave) spread over all banks; each lane loads the global chunk
+//     that belongs in its slot.
 // Interior-only: the host uses it when M and N are multiples of 256, the K
 // range of every split a multiple of 32, and all rows 16-byte aligned.
 constexpr int D_BM = 256, D_BN = 256, D_BK = 32;
-constexpr int D_A_LD = D_BK;
-constexpr int D_B_LD = D_BN + 8;
-constexpr int D_A_SZ = D_BM * D_A_LD;
-constexpr int D_B_SZ = D_BK * D_B_LD;
-constexpr int D_STAGE = D_A_SZ + D_B_SZ;
+constexpr int D_KC_LD = D_BK;        // k-contiguous rows (swizzled)
+constexpr int D_NC_LD = D_BN + 8;    // m/n-contiguous rows (padded)
+constexpr int D_KC_SZ = D_BM * D_KC_LD;
+constexpr int D_NC_SZ = D_BK * D_NC_LD;
 
 // One wave-wide direct load.  Issued from inline assembly on purpose: the
 // compiler's own LDS-DMA builtin makes it assume the DMA may alias every
@@ -648,11 +650,67 @@ __device__ __forceinline__ void g2lds16(const float *src, const float *lds) {
 
 __device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Per-lane sources and wave-uniform destinations of one operand's 8 wave
+// loads per K tile.  KC: rows r = wave*64 + 8j + lane/8 of 32 k (swizzled);
+// NC: rows k = wave*8 + j of 256 floats.
+template <bool KC>
+struct DirectOperand {
+  const float *src[KC ? 8 : 1];
+  long ld;
+  __device__ __forceinline__ void init(const float *p, long ld_, long r0, int kbeg, int wave,
+                                       int lane) {
+    ld = ld_;
+    if constexpr (KC) {
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int R = wave * 64 + 8 * j + (lane >> 3);
+        const int c = (lane & 7) ^ ((R >> 1) & 7);
+        src[j] = p + (r0 + R) * ld + kbeg + 4 * c;
+      }
+    } else {
+      src[0] = p + (long)(kbeg + wave * 8) * ld + r0 + 4 * lane;
+    }
+  }
+  __device__ __forceinline__ void issue(int kt, float *lds, int wave) const {
+    const long k = (long)kt * D_BK;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      if constexpr (KC) g2lds16(src[j] + k, lds + (wave * 64 + 8 * j) * D_KC_LD);
+      else g2lds16(src[0] + (k + j) * ld, lds + (wave * 8 + j) * D_NC_LD);
+    }
+  }
+  // fragment v[x][s] (x = 32-row block, s = k within the 8-step) for rows
+  // base + 32x + l32 (KC) or m/n base + 4*l32 + x (NC, interleaved)
+  __device__ __forceinline__ static void frag(const float *lds, int base, int kk, int l32, int g,
+                                              float (*v)[4]) {
+    if constexpr (KC) {
+#pragma unroll
+      for (int x = 0; x < 4; x++) {
+        const int R = base + 32 * x + l32;
+        const int slot = ((kk >> 2) + g) ^ ((R >> 1) & 7);
+        const float4 t = *reinterpret_cast<const float4 *>(lds + R * D_KC_LD + 4 * slot);
+        v[x][0] = t.x; v[x][1] = t.y; v[x][2] = t.z; v[x][3] = t.w;
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        const float4 t =
+            *reinterpret_cast<const float4 *>(lds + (kk + 4 * g + s) * D_NC_LD + base + 4 * l32);
+        v[0][s] = t.x; v[1][s] = t.y; v[2][s] = t.z; v[3][s] = t.w;
+      }
+    }
+  }
+};
+
+template <bool A_KC, bool B_NC>
 __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1)))
-gemm_nn_direct_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
-                      const float *__restrict__ B, long ldb, float *__restrict__ C, long ldc,
-                      long split_stride, int kchunk) {
-  __shared__ __attribute__((aligned(16))) float smem[2 * D_STAGE];
+gemm_direct_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
+                   const float *__restrict__ B, long ldb, float *__restrict__ C, long ldc,
+                   long split_stride, int kchunk) {
+  constexpr int A_SZ = A_KC ? D_KC_SZ : D_NC_SZ;
+  constexpr int B_SZ = B_NC ? D_NC_SZ : D_KC_SZ;
+  constexpr int STAGE = A_SZ + B_SZ;
+  __shared__ __attribute__((aligned(16))) float smem[2 * STAGE];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -677,27 +735,12 @@ gemm_nn_direct_kernel(int M, int N, int K, const float *__restrict__ A, long lda
   const int wm = (wave >> 1) * 128;
   const int wn = (wave & 1) * 128;
 
-  // per-lane global sources of the 8 + 8 wave loads of one K tile
-  const int arow = wave * 64 + (lane >> 3);  // + 8j
-  const float *asrc[8];
-#pragma unroll
-  for (int j = 0; j < 8; j++) {
-    const int R = arow + 8 * j;
-    const int c = (lane & 7) ^ ((R >> 1) & 7);
-    asrc[j] = A + (m0 + R) * lda + kbeg + 4 * c;
-  }
-  const float *bsrc = B + (long)(kbeg + wave * 8) * ldb + n0 + 4 * lane;
-
-  auto issue = [&](int kt, int buf) {
-    float *sA = smem + buf * D_STAGE;
-    float *sB = sA + D_A_SZ;
-    const long ka = (long)kt * D_BK;
-#pragma unroll
-    for (int j = 0; j < 8; j++) g2lds16(asrc[j] + ka, sA + (wave * 64 + 8 * j) * D_A_LD);
-#pragma unroll
-    for (int j = 0; j < 8; j++)
-      g2lds16(bsrc + (ka + j) * ldb, sB + (wave * 8 + j) * D_B_LD);
-  };
+  // A k-contiguous: rows m of A (M x K); else rows k of A (K x M).
+  // B m/n-contiguous: rows k of B (K x N); else rows n of B (N x K).
+  DirectOperand<A_KC> opa;
+  DirectOperand<!B_NC> opb;
+  opa.init(A, lda, m0, kbeg, wave, lane);
+  opb.init(B, ldb, n0, kbeg, wave, lane);
 
   f32x16 acc[4][4];
 #pragma unroll
@@ -707,32 +750,19 @@ gemm_nn_direct_kernel(int M, int N, int K, const float *__restrict__ A, long lda
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
-  // fragments of k-step kk (8 k): a[i][s] for the 4 row blocks, b[j][s]
-  // for the 4 interleaved column blocks
-  auto frags = [&](const float *sA, const float *sB, int kk, float (*a)[4], float (*b)[4]) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int R = wm + 32 * i + l32;
-      const int slot = ((kk >> 2) + g) ^ ((R >> 1) & 7);
-      const float4 t = *reinterpret_cast<const float4 *>(sA + R * D_A_LD + 4 * slot);
-      a[i][0] = t.x; a[i][1] = t.y; a[i][2] = t.z; a[i][3] = t.w;
-    }
-#pragma unroll
-    for (int s = 0; s < 4; s++) {
-      const float4 t =
-          *reinterpret_cast<const float4 *>(sB + (kk + 4 * g + s) * D_B_LD + wn + 4 * l32);
-      b[0][s] = t.x; b[1][s] = t.y; b[2][s] = t.z; b[3][s] = t.w;
-    }
-  };
   // the fragments of step kk+8 are read while the MFMAs of step kk run
   auto compute = [&](int buf) {
-    const float *sA = smem + buf * D_STAGE;
-    const float *sB = sA + D_A_SZ;
+    const float *sA = smem + buf * STAGE;
+    const float *sB = sA + A_SZ;
     float a[2][4][4], b[2][4][4];
-    frags(sA, sB, 0, a[0], b[0]);
+    DirectOperand<A_KC>::frag(sA, wm, 0, l32, g, a[0]);
+    DirectOperand<!B_NC>::frag(sB, wn, 0, l32, g, b[0]);
 #pragma unroll
     for (int q = 0; q < D_BK / 8; q++) {
-      if (q + 1 < D_BK / 8) frags(sA, sB, 8 * (q + 1), a[(q + 1) & 1], b[(q + 1) & 1]);
+      if (q + 1 < D_BK / 8) {
+        DirectOperand<A_KC>::frag(sA, wm, 8 * (q + 1), l32, g, a[(q + 1) & 1]);
+        DirectOperand<!B_NC>::frag(sB, wn, 8 * (q + 1), l32, g, b[(q + 1) & 1]);
+      }
 #pragma unroll
       for (int s = 0; s < 4; s++)
 #pragma unroll
@@ -759,27 +789,40 @@ gemm_nn_direct_kernel(int M, int N, int K, const float *__restrict__ A, long lda
   };
 
   if (nk > 0) {
-    issue(0, 0);
+    opa.issue(0, smem, wave);
+    opb.issue(0, smem + A_SZ, wave);
     wait_vm_all();
     __syncthreads();
     for (int kt = 0; kt < nk; kt++) {
-      if (kt + 1 < nk) issue(kt + 1, (kt + 1) & 1);
+      if (kt + 1 < nk) {
+        float *nb = smem + ((kt + 1) & 1) * STAGE;
+        opa.issue(kt + 1, nb, wave);
+        opb.issue(kt + 1, nb + A_SZ, wave);
+      }
       compute(kt & 1);
       wait_vm_all();
       __syncthreads();
     }
   }
 
-  // epilogue: block i row rho (acc r: rho = 8*(r/4) + 4*g + r%4), columns
-  // wn + 4*l32 .. +3 (the interleaved B blocks j = 0..3)
+  // epilogue: block i row rho (acc r: rho = 8*(r/4) + 4*g + r%4) is
+  // m = wm + 32i + rho (k-contiguous A) or wm + 4*rho + i (interleaved A);
+  // block j column l32 is n = wn + 4*l32 + j (interleaved B: one float4 per
+  // row) or wn + 32j + l32.
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       const int rho = 8 * (r >> 2) + 4 * g + (r & 3);
-      const long row = m0 + wm + 32 * i + rho;
-      *reinterpret_cast<float4 *>(C + row * ldc + n0 + wn + 4 * l32) =
-          make_float4(acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]);
+      const long row = m0 + (A_KC ? wm + 32 * i + rho : wm + 4 * rho + i);
+      float *crow = C + row * ldc + n0 + wn;
+      if constexpr (B_NC) {
+        *reinterpret_cast<float4 *>(crow + 4 * l32) =
+            make_float4(acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++) crow[32 * j + l32] = acc[i][j][r];
+      }
     }
 }
 
@@ -798,7 +841,7 @@ constexpr int TILE_BK[NTILE] = {32, 32, 32, 32, 32, 32, 32, 32, 32, 64, 64};
 
 // tuning override (tth_gemm_config): -1 = automatic
 int g_force_tile = -1, g_force_splits = -1;
-int g_direct = 1;  // direct-to-LDS NN kernel enabled (tth_gemm_direct)
+int g_direct = 1;  // direct-to-LDS 256x256 kernel enabled (tth_gemm_direct)
 
 struct Plan {
   int tile, splits, kchunk;
@@ -940,13 +983,13 @@ int run(int M, int N, int K, Opnd A, Opnd B, float *C, long ldc, const float *bi
     default:       if constexpr (!B_I2C) { TT_VEC(256, 128, 2, EPI_) } break; \
   }
   bool done = false;
-  if constexpr (A_KC && !A_PERM && B_NC && !B_PERM && !B_I2C && EPI == EPI_STORE) {
-    // plain NN GEMM on whole 256x256 tiles: the direct-to-LDS kernel
+  if constexpr (!A_PERM && !B_PERM && !B_I2C && EPI == EPI_STORE) {
+    // plain GEMM on whole 256x256 tiles: the direct-to-LDS kernel
     if (g_direct && p.tile == T256x256 && vec && M % D_BM == 0 && N % D_BN == 0 &&
         K % D_BK == 0 && p.kchunk % D_BK == 0 && aligned16(target) && tgt_ld % 4 == 0) {
       const dim3 grid((M / D_BM) * (N / D_BN), 1, p.splits);
-      hipLaunchKernelGGL(gemm_nn_direct_kernel, grid, dim3(NT), 0, stream(), M, N, K, A.p, A.ld,
-                         B.p, B.ld, target, tgt_ld, sstride, p.kchunk);
+      hipLaunchKernelGGL((gemm_direct_kernel<A_KC, B_NC>), grid, dim3(NT), 0, stream(), M, N, K,
+                         A.p, A.ld, B.p, B.ld, target, tgt_ld, sstride, p.kchunk);
       done = true;
     }
   }
