@@ -20,7 +20,7 @@ CFLAGS_HOST := -O2 -fPIC -std=c11 -Wall -Wextra -D__HIP_PLATFORM_AMD__ -I$(ROCM)
                -Iinclude -I$(CSRC)
 
 HOST_SRCS := $(CSRC)/runtime.c $(CSRC)/tensor.c $(CSRC)/ops.c $(CSRC)/autograd.c $(CSRC)/dataset.c
-HIP_SRCS  := $(CSRC)/gemm.hip $(CSRC)/elementwise.hip $(CSRC)/spatial.hip
+HIP_SRCS  := $(CSRC)/gemm.hip $(CSRC)/conv.hip $(CSRC)/elementwise.hip $(CSRC)/spatial.hip
 HDRS      := $(wildcard include/*.h) $(wildcard $(CSRC)/*.h)
 HOST_OBJS := $(patsubst $(CSRC)/%.c,$(BUILD)/obj/%.o,$(HOST_SRCS))
 HIP_OBJS  := $(patsubst $(CSRC)/%.hip,$(BUILD)/obj/%.o,$(HIP_SRCS))
@@ -38,6 +38,11 @@ $(BUILD)/obj/%.o: $(CSRC)/%.c $(HDRS) | $(BUILD)/obj
 # reference's separate multiply and add
 $(BUILD)/obj/gemm.o: $(CSRC)/gemm.hip $(HDRS) | $(BUILD)/obj
 	$(HIPCC) $(HIPFLAGS) -c $< -o $@
+
+# direct convolution: MFMA accumulators in VGPRs (the AGPR form made the
+# compiler copy accumulators between register files every loop iteration)
+$(BUILD)/obj/conv.o: $(CSRC)/conv.hip $(HDRS) | $(BUILD)/obj
+	$(HIPCC) $(HIPFLAGS) -ffp-contract=off -mllvm -amdgpu-mfma-vgpr-form=1 -c $< -o $@
 
 $(BUILD)/obj/%.o: $(CSRC)/%.hip $(HDRS) | $(BUILD)/obj
 	$(HIPCC) $(HIPFLAGS) -ffp-contract=off -c $< -o $@

@@ -51,6 +51,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline only")
+    ap.add_argument("--cnn-only", action="store_true",
+                    help="only time the config-4 CNN training step (for kernel traces of it)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 1 GiB device copy kernel 5 times (the known-size "
                          "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -367,6 +369,10 @@ def main():
     tinytorch_amd.require_gpu()
     L = tinytorch_amd.lib()
     log("device", tinytorch_amd.device_name())
+    if args.cnn_only:
+        ms = time_steps(CnnStep(L), args.steps, args.warmup)
+        print(json.dumps({"cnn_step_ms": round(ms, 4), "steps": args.steps, "warmup": args.warmup}))
+        return
     if args.copy_calib:
         from tinytorch_amd.hip import DevBuf, check, sync
         n = 256 << 20  # floats: 1 GiB read + 1 GiB written per launch (4x the MALL)

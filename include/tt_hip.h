@@ -161,6 +161,34 @@ int tt_k_conv2d_dx_implicit(const float *g, const float *w, float *dx,
                             int N, int C, int H, int W, int F, int HH, int WW,
                             int sh, int sw, int ph, int pw, int Ho, int Wo);
 
+/* Direct convolution with the image rows staged in LDS (conv.hip): the
+ * MFMA operands are read through im2col addressing of the staged slab, so
+ * no im2col matrix is formed.  Used by tt_conv2d / ag_conv2d wherever
+ * tt_k_conv2d_lds_plan reports coverage (bit 0 forward, bit 1 dW/db, bit 2
+ * dX; dX needs stride 1 and padding <= kernel-1).  Each entry returns -1
+ * (nothing launched) for shapes it does not cover, -2 out of memory, -3
+ * launch failure.  tth_conv_lds(0) switches them off (1 on, <0 query); the
+ * previous setting is returned.
+ *   fwd: out (N,F,Ho,Wo) = conv(x, w) + bias        src/ops_spatial.c:71-127
+ *   dw:  dw (F, C*HH*WW), db (F, optional)         src/autograd.c:456-513
+ *   dx:  dx (N,C,H,W)                              src/autograd.c:515-539,406-434 */
+int tth_conv_lds(int on);
+/* Profiling aid for the LDS-staged kernels: bit 0 skips staging the
+ * activations, bit 1 the weights / output gradient, bit 2 the MFMA loop,
+ * bit 3 the result stores (results are then wrong).  0 = normal. */
+int tth_conv_dbg(int mask);
+int tt_k_conv2d_lds_plan(int N, int C, int H, int W, int F, int HH, int WW,
+                         int sh, int sw, int ph, int pw, int Ho, int Wo);
+int tt_k_conv2d_fwd_lds(const float *x, const float *w, const float *bias, float *out,
+                        int N, int C, int H, int W, int F, int HH, int WW,
+                        int sh, int sw, int ph, int pw, int Ho, int Wo);
+int tt_k_conv2d_dw_lds(const float *g, const float *x, float *dw, float *db,
+                       int N, int C, int H, int W, int F, int HH, int WW,
+                       int sh, int sw, int ph, int pw, int Ho, int Wo);
+int tt_k_conv2d_dx_lds(const float *g, const float *w, float *dx,
+                       int N, int C, int H, int W, int F, int HH, int WW,
+                       int sh, int sw, int ph, int pw, int Ho, int Wo);
+
 /* Dataset batch gather + normalisation (see tt_data.h):
  * out[r, j] = ((float)src[idx[r]*sample + j] / 255 - mean[c]) / stdv[c],
  * c = j / plane, channels = sample / plane <= 4.  idx values must be in

@@ -94,6 +94,7 @@ def test_autograd_conv_through_implicit_path(tlib, case):
     b = rng.uniform(-1, 1, F).astype(np.float32)
     g = rng.standard_normal((N, F, Ho, Wo)).astype(np.float32)
     tlib.tth_conv_config(0)
+    prev = tlib.tth_conv_lds(0)  # the LDS-staged kernels would take these shapes first
     try:
         X, Wn, Bn = Node.leaf(x), Node.leaf(w), Node.leaf(b)
         out = X.conv2d(Wn, Bn, (sh, sw), (ph, pw))
@@ -109,3 +110,4 @@ def test_autograd_conv_through_implicit_path(tlib, case):
             n.release()
     finally:
         tlib.tth_conv_config(-1)
+        tlib.tth_conv_lds(prev)

@@ -1,0 +1,158 @@
+"""LDS-staged direct convolution (image rows in LDS, MFMA operands read
+through im2col addressing) against the oracle's conv2d forward / backward
+(reference src/ops_spatial.c:71-127, src/autograd.c:456-553), at the GEMM
+bar max|err| / (sqrt(K) * max|A| * max|B|) <= 1e-4, K the summed length."""
+import numpy as np
+import pytest
+
+import orc
+from tinytorch_amd.hip import DevBuf, check
+
+pytestmark = pytest.mark.gpu
+rng = np.random.default_rng(5151)
+TOL = 1e-4
+
+CASES = [  # (N, C, H, W, F, HH, WW, sh, sw, ph, pw)
+    (2, 3, 7, 7, 4, 3, 3, 1, 1, 1, 1), (2, 3, 7, 7, 4, 3, 3, 2, 2, 0, 0),
+    (3, 4, 9, 8, 5, 3, 2, 2, 1, 2, 1), (1, 1, 5, 5, 1, 1, 1, 1, 1, 0, 0),
+    (2, 5, 6, 6, 3, 5, 5, 1, 1, 2, 2), (3, 6, 11, 5, 7, 3, 3, 1, 1, 0, 0),
+    (2, 2, 9, 13, 3, 3, 5, 1, 1, 1, 2), (5, 7, 10, 10, 9, 4, 4, 2, 2, 1, 1),
+    (2, 3, 33, 31, 33, 3, 3, 1, 1, 1, 1),   # F = 33: a second, mostly empty filter block
+    (2, 16, 12, 12, 70, 3, 3, 1, 1, 1, 1),  # K = 144, F = 70
+    (2, 64, 8, 8, 20, 3, 3, 1, 1, 1, 1),    # K = 576: one 16-filter block, 36 tap blocks
+    (3, 3, 17, 19, 8, 3, 3, 3, 3, 1, 1),    # stride 3, pixel count not a multiple of 4
+    (2, 4, 40, 40, 6, 3, 3, 1, 1, 0, 0),    # 38 x 38 output: chunks that straddle rows
+    (2, 1, 70, 70, 4, 3, 3, 1, 1, 1, 1),    # wide rows (Wp > 64)
+    (8, 3, 32, 32, 32, 3, 3, 1, 1, 1, 1), (16, 32, 16, 16, 64, 3, 3, 1, 1, 1, 1),
+    (128, 3, 32, 32, 32, 3, 3, 1, 1, 1, 1), (128, 32, 16, 16, 64, 3, 3, 1, 1, 1, 1),  # config 4
+]
+
+
+def err(got, ref, K, amax, bmax):
+    d = np.abs(got.astype(np.float64) - ref).max()
+    return d / (np.sqrt(K) * amax * bmax)
+
+
+def _inputs(case):
+    N, C, H, W, F, HH, WW, sh, sw, ph, pw = case
+    Ho, Wo = orc.conv_out(H, W, HH, WW, sh, sw, ph, pw)
+    x = rng.uniform(-1, 1, (N, C, H, W)).astype(np.float32)
+    w = rng.uniform(-1, 1, (F, C, HH, WW)).astype(np.float32)
+    b = rng.uniform(-1, 1, F).astype(np.float32)
+    g = rng.standard_normal((N, F, Ho, Wo)).astype(np.float32)
+    return x, w, b, g, (N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo)
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_lds_conv_vs_oracle(tlib, case):
+    x, w, b, g, geo = _inputs(case)
+    N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo = geo
+    print("lds conv", case, flush=True)
+    bits = tlib.tt_k_conv2d_lds_plan(*geo)
+    assert bits & 3 == 3, f"plan {bits}"
+    stride1 = sh == 1 and sw == 1 and ph <= HH - 1 and pw <= WW - 1
+    assert bool(bits & 4) == stride1
+    dx_, dw_, db_, dg_ = DevBuf.from_np(x), DevBuf.from_np(w), DevBuf.from_np(b), DevBuf.from_np(g)
+
+    out = DevBuf(N * F * Ho * Wo)
+    check(tlib.tt_k_conv2d_fwd_lds(dx_.ptr, dw_.ptr, db_.ptr, out.ptr, *geo), "fwd")
+    ref = orc.conv2d_fwd(x, w, b, sh, sw, ph, pw)
+    Kc = C * HH * WW
+    bb = b[None, :, None, None]
+    assert err(out.to_np(ref.shape) - bb, ref - bb, Kc, 1.0, 1.0) <= TOL
+    out0 = DevBuf(N * F * Ho * Wo)  # no bias
+    check(tlib.tt_k_conv2d_fwd_lds(dx_.ptr, dw_.ptr, None, out0.ptr, *geo), "fwd nobias")
+    assert err(out0.to_np(ref.shape), ref - bb, Kc, 1.0, 1.0) <= TOL
+
+    rdx, rdw, rdb = orc.conv2d_bwd(x, w, g, sh, sw, ph, pw)
+    Ncol = N * Ho * Wo
+    gmax = float(np.abs(g).max())
+    dW, dB = DevBuf(w.size), DevBuf(F)
+    check(tlib.tt_k_conv2d_dw_lds(dg_.ptr, dx_.ptr, dW.ptr, dB.ptr, *geo), "dw+db")
+    assert err(dW.to_np(w.shape), rdw, Ncol, gmax, 1.0) <= TOL
+    assert err(dB.to_np((F,)), rdb, Ncol, gmax, 1.0) <= TOL
+    dW2 = DevBuf(w.size)
+    check(tlib.tt_k_conv2d_dw_lds(dg_.ptr, dx_.ptr, dW2.ptr, None, *geo), "dw")
+    assert np.array_equal(dW2.to_np(w.shape), dW.to_np(w.shape))  # deterministic
+
+    dX = DevBuf(x.size)
+    rc = tlib.tt_k_conv2d_dx_lds(dg_.ptr, dw_.ptr, dX.ptr, *geo)
+    if stride1:
+        check(rc, "dx")
+        assert err(dX.to_np(x.shape), rdx, F * HH * WW, gmax, 1.0) <= TOL
+    else:
+        assert rc == -1  # not covered: nothing launched
+    for bf in (dx_, dw_, db_, dg_, out, out0, dW, dB, dW2, dX):
+        bf.free()
+
+
+@pytest.mark.parametrize("case", [(2, 3, 12, 12, 5, 3, 3, 1, 1, 1, 1),
+                                  (2, 9, 10, 10, 4, 3, 3, 1, 1, 1, 1)])
+def test_lds_conv_nonfinite_stays_local(tlib, case):
+    """An Inf in the input reaches only the outputs whose window holds it:
+    padded taps (past K) read a zero plane, never an input value times 0."""
+    x, w, b, g, geo = _inputs(case)
+    N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo = geo
+    x[1, C - 1, H // 2, W // 3] = np.inf
+    g[0, F - 1, 0, Wo - 1] = -np.inf
+    ref = orc.conv2d_fwd(x, w, b, sh, sw, ph, pw)
+    rdx, _, _ = orc.conv2d_bwd(x, w, g, sh, sw, ph, pw)
+    dx_, dw_, db_, dg_ = DevBuf.from_np(x), DevBuf.from_np(w), DevBuf.from_np(b), DevBuf.from_np(g)
+    out, dX = DevBuf(ref.size), DevBuf(x.size)
+    check(tlib.tt_k_conv2d_fwd_lds(dx_.ptr, dw_.ptr, db_.ptr, out.ptr, *geo), "fwd")
+    check(tlib.tt_k_conv2d_dx_lds(dg_.ptr, dw_.ptr, dX.ptr, *geo), "dx")
+    o, d = out.to_np(ref.shape), dX.to_np(x.shape)
+    assert np.array_equal(np.isfinite(o), np.isfinite(ref))
+    assert np.array_equal(np.isfinite(d), np.isfinite(rdx))
+    m = np.isfinite(ref)
+    assert np.abs(o[m] - ref[m]).max() <= TOL * np.sqrt(C * HH * WW) * 2
+    m = np.isfinite(rdx)
+    assert np.abs(d[m] - rdx[m]).max() <= TOL * np.sqrt(F * HH * WW) * 4 * np.abs(g[np.isfinite(g)]).max()
+    for bf in (dx_, dw_, db_, dg_, out, dX):
+        bf.free()
+
+
+def test_lds_conv_rejects_uncovered(tlib):
+    buf = DevBuf(1 << 16)
+    geo = (2, 3, 7, 7, 4, 3, 3, 1, 1, 1, 1, 7, 7)
+    assert tlib.tt_k_conv2d_fwd_lds(None, None, None, None, *geo) == -1
+    bad = (2, 3, 7, 7, 4, 3, 3, 1, 1, 1, 1, 6, 7)   # Ho inconsistent with the geometry
+    assert tlib.tt_k_conv2d_lds_plan(*bad) == 0
+    assert tlib.tt_k_conv2d_fwd_lds(buf.ptr, buf.ptr, None, buf.ptr, *bad) == -1
+    # a 1 x 4096 x 4 x 4 input with a 3x3 kernel: the staged slab does not fit
+    big = (1, 4096, 4, 4, 8, 3, 3, 1, 1, 1, 1, 4, 4)
+    assert tlib.tt_k_conv2d_lds_plan(*big) & 1 == 0
+    assert tlib.tt_k_conv2d_fwd_lds(buf.ptr, buf.ptr, None, buf.ptr, *big) == -1
+    prev = tlib.tth_conv_lds(0)
+    try:
+        assert tlib.tt_k_conv2d_lds_plan(*geo) == 0
+    finally:
+        tlib.tth_conv_lds(prev)
+    buf.free()
+
+
+@pytest.mark.parametrize("lds", [1, 0])
+@pytest.mark.parametrize("case", [(4, 3, 9, 9, 5, 3, 3, 1, 1, 1, 1), (3, 4, 9, 8, 5, 3, 2, 2, 1, 2, 1),
+                                  (128, 32, 16, 16, 64, 3, 3, 1, 1, 1, 1)])
+def test_autograd_conv_lds_on_off(tlib, case, lds):
+    """ag_conv2d forward + backward (dX, dW, db) with the LDS kernels on (the
+    default) and off (im2col + GEMM) against the oracle."""
+    from tinytorch_amd.torch_py import Node
+    x, w, b, g, geo = _inputs(case)
+    N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo = geo
+    prev = tlib.tth_conv_lds(lds)
+    try:
+        X, Wn, Bn = Node.leaf(x), Node.leaf(w), Node.leaf(b)
+        out = X.conv2d(Wn, Bn, (sh, sw), (ph, pw))
+        out.backward(g)
+        ref = orc.conv2d_fwd(x, w, b, sh, sw, ph, pw)
+        rdx, rdw, rdb = orc.conv2d_bwd(x, w, g, sh, sw, ph, pw)
+        gmax = float(np.abs(g).max())
+        assert err(out.value(), ref, C * HH * WW, 1.0, 1.0) <= TOL
+        assert err(Wn.grad(), rdw, N * Ho * Wo, gmax, 1.0) <= TOL
+        assert err(Bn.grad(), rdb, N * Ho * Wo, gmax, 1.0) <= TOL
+        assert err(X.grad(), rdx, F * HH * WW, gmax, 1.0) <= TOL
+        for n in (out, X, Wn, Bn):
+            n.release()
+    finally:
+        tlib.tth_conv_lds(prev)

@@ -145,6 +145,11 @@ SIGNATURES = [
     ("tt_k_conv2d_fwd_implicit", _I, [VP, VP, VP, VP] + [_I] * 13),
     ("tt_k_conv2d_dw_implicit", _I, [VP, VP, VP, VP] + [_I] * 13),
     ("tt_k_conv2d_dx_implicit", _I, [VP, VP, VP] + [_I] * 13),
+    ("tth_conv_lds", _I, [_I]),
+    ("tt_k_conv2d_lds_plan", _I, [_I] * 13),
+    ("tt_k_conv2d_fwd_lds", _I, [VP, VP, VP, VP] + [_I] * 13),
+    ("tt_k_conv2d_dw_lds", _I, [VP, VP, VP, VP] + [_I] * 13),
+    ("tt_k_conv2d_dx_lds", _I, [VP, VP, VP] + [_I] * 13),
     ("tt_k_gather_u8_norm", _I, [VP, _L, _L, _L, _I, VP, _L, F32P, F32P, VP]),
     ("tt_k_momentum_multi", _I, [ctypes.POINTER(VP)] * 3 + [ctypes.POINTER(_L), _I, _F, _F]),
     ("tt_k_adam_multi", _I, [ctypes.POINTER(VP)] * 4 + [ctypes.POINTER(_L), _I] + [_F] * 5

@@ -386,7 +386,26 @@ static void backward_conv2d(AGNode *n) {
     if (!gd) return;
 
     const long bshp[1] = {F};
-    if (needs(b) && needs(w) && n->col && n->col_ones) {
+    const int lds = tt_k_conv2d_lds_plan(N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo);
+    int w_done = 0;
+    if (needs(w) && !n->col && (lds & 2)) {
+        /* LDS-staged forward kept no col: dW (and db) read x */
+        const float *x = tt_dev(a->val);
+        Tensor *gw = x ? tt_empty_like(w->val) : NULL;
+        Tensor *gb = gw && needs(b) ? tt_empty_dev(bshp, 1) : NULL;
+        if (gw && (gb || !needs(b)) &&
+            tt_k_conv2d_dw_lds(gd, x, gw->dev, gb ? gb->dev : NULL, N, C, H, W, F, HH, WW, sh,
+                               sw, ph, pw, Ho, Wo) == 0) {
+            if (gb) accum_move(b, gb);
+            accum_move(w, gw);
+            w_done = 1;
+        } else {
+            tt_release(gw);
+            tt_release(gb);
+        }
+    }
+    if (w_done) {
+    } else if (needs(b) && needs(w) && n->col && n->col_ones) {
         /* dW and db from one GEMM against [col; ones] */
         Tensor *gw = tt_empty_like(w->val);
         Tensor *gb = gw ? tt_empty_dev(bshp, 1) : NULL;
@@ -434,6 +453,16 @@ static void backward_conv2d(AGNode *n) {
             else tt_release(gw);
             if (own) ttrt_free(col);
         }
+    }
+    if (needs(a) && (lds & 4)) {
+        const float *wd = tt_dev(w->val);
+        Tensor *ga = wd ? tt_empty_like(a->val) : NULL;
+        if (ga && tt_k_conv2d_dx_lds(gd, wd, ga->dev, N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho,
+                                     Wo) == 0) {
+            accum_move(a, ga);
+            return;
+        }
+        tt_release(ga);
     }
     if (needs(a) && tt_conv_use_implicit(sizeof(float) * (long)Kc * Ncol)) {
         /* stride-1 dX as one implicit GEMM; other strides keep dcol + col2im */

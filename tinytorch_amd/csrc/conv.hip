@@ -1,0 +1,1107 @@
+// Direct convolution on the matrix cores with the image staged in LDS
+// (gfx950).  Replaces, for convolutions whose per-image row slab fits in LDS,
+// the reference's im2col + GEMM sequence behind tt_conv2d / ag_conv2d:
+//
+//   forward  out = W * im2col(x) + bias, NCHW     reference src/ops_spatial.c:71-127
+//   dW, db   dW = Gperm * im2col(x)^T, db = sum g reference src/autograd.c:456-513
+//   dX       col2im(W^T * Gperm), stride 1         reference src/autograd.c:515-539,406-434
+//
+// The im2col matrix is never written.  A workgroup copies the input rows its
+// output pixels need (all channels, R rows of W floats each, rows outside the
+// image as zeros) from HBM into LDS once, and the MFMA operand for im2col
+// element (k, p), k = (c*HH + kh)*WW + kw, p = ho*Wo + wo, is read from LDS at
+//     koff[k] + pix[p],  koff = (c*R + kh)*W + kw - pw,  pix = (ho-ho0)*sh*W + wo*sw
+// and replaced by 0 when the column wo*sw + kw - pw falls outside [0, W) --
+// the horizontal zero padding is applied on read, so each channel's rows are
+// one contiguous block of x and are staged with 16-byte direct global->LDS
+// loads.  Every staged element feeds up to HH*WW im2col entries: HBM sees the
+// input about once per workgroup instead of an HH*WW-fold im2col matrix being
+// written and read back.
+//
+//   forward / dX: v_mfma_f32_32x32x2_f32, A = weights (32 output channels,
+//     LDS [k][f], 32 floats a row), B = the slab.  Lane l feeds A[l%32][l/32]
+//     and B[l/32][l%32]; accumulator r of lane l holds row 8(r/4) + 4(l/32) +
+//     r%4, column l%32.  Each wave owns PB blocks of 32 consecutive output
+//     pixels.  Taps past K read a zero plane after the slab, so no operand is
+//     ever 0 * (input value) for a tap that does not exist.
+//   dX of a stride-1 convolution is the forward convolution of the output
+//     gradient with the kernel flipped in (kh, kw) and channels swapped,
+//     padding HH-1-ph: the flip is applied while staging the weights.
+//   dW: v_mfma_f32_16x16x4_f32, A = the output gradient (16 filters x 4
+//     pixels, staged in LDS), B = the slab (4 pixels x 16 taps).  Lane l
+//     feeds A[l%16][l/16], B[l/16][l%16]; accumulator r holds row 4(l/16)+r,
+//     column l%16.  The sum over a workgroup's pixels goes to a partial
+//     (F x (K+1), last column = the bias gradient summed on the VALU), and a
+//     second kernel adds the partials in index order: deterministic, no
+//     atomics.
+//
+// Staging: activations and output gradients with direct loads
+// (global_load_lds_dwordx4 when rows are 16-byte aligned, else _dword);
+// weights through registers (coalesced reads of the weight tensor, transposed
+// LDS writes).  Measured on MI355X, linear 16-byte direct loads fill LDS about
+// 10x faster than per-lane scattered 4-byte ones.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "tt_rt.h"
+
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+inline hipStream_t stream() { return (hipStream_t)ttrt_stream(); }
+
+constexpr int NT = 256;                    // threads per workgroup (4 waves)
+constexpr long LDS_MAX = 160L * 1024;      // bytes of LDS per workgroup on gfx950
+constexpr int GUARD = 64;                  // floats before the slab (reads at -pw are masked)
+
+// Convolution geometry as the kernels see it: input C x H x W, kernel
+// HH x WW, stride, padding, output Ho x Wo, F output channels, K = C*HH*WW.
+struct Geo {
+  int C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo, F, K;
+};
+
+// Slab of one workgroup: output pixels [p0, p1) of image n cover output rows
+// ho0..; input rows ho0*sh-ph .. +R-1 are staged as R rows of W floats per
+// channel, then a zero plane of R*W floats.
+struct Slab {
+  int ho0, R;
+};
+
+__device__ __forceinline__ Slab slab_of(const Geo &g, int p0, int p1) {
+  Slab s;
+  s.ho0 = p0 / g.Wo;
+  const int ho1 = (p1 - 1) / g.Wo;
+  s.R = (ho1 - s.ho0) * g.sh + g.HH;
+  return s;
+}
+
+// n / d for 0 <= n < 2^24, 0 < d < 2^16 through the float reciprocal, with
+// one correction step each way (the estimate is within 1 of the quotient).
+__device__ __forceinline__ int fdiv(int n, int d, float rcp) {
+  int q = (int)((float)n * rcp);
+  const int r = n - q * d;
+  q += (r >= d) - (r < 0);
+  return q;
+}
+
+// Every padding element of a staged operand is loaded from here.
+__device__ __attribute__((aligned(16))) float g_zero_src[4];
+
+// Direct loads: lane i's 4 (or 16) bytes from `src` go to LDS at lds_wave +
+// 4i (16i); M0 holds the wave-uniform LDS byte address.  Nothing lands in
+// registers, so a wave issues all of its staging loads back to back and the
+// kernel waits for them once (vmcnt(0) and a barrier).
+__device__ __forceinline__ void dma_dword(const float *src, const float *lds_wave) {
+  const unsigned addr = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_wave);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off"
+               :
+               : "s"(addr), "v"(src)
+               : "memory", "m0");
+}
+
+__device__ __forceinline__ void dma_dwordx4(const float *src, const float *lds_wave) {
+  const unsigned addr = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_wave);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(addr), "v"(src)
+               : "memory", "m0");
+}
+
+__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+inline __host__ __device__ int round_up(int v, int m) { return (v + m - 1) / m * m; }
+
+// Copy T floats into LDS at dst, viewed as blocks of B floats: element j of
+// block b is src[b * bstride + j] when b < nb and jlo <= j < jhi, else 0.
+// VEC: 16-byte loads (B, bstride, jlo, jhi multiples of 4, src 16-byte
+// aligned); dst is then filled in whole 256-float runs.
+template <bool VEC>
+__device__ __forceinline__ void stage_blocks(float *dst, const float *__restrict__ src, int T,
+                                             int B, int nb, long bstride, int jlo, int jhi) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const float rcpB = 1.0f / (float)B;
+  constexpr int E = VEC ? 4 : 1;   // floats per lane per load
+  for (int base = wave * 64 * E; base < T; base += NT * E) {
+    const int i = base + lane * E;
+    const int b = fdiv(i, B, rcpB), j = i - b * B;
+    const bool ok = i < T && b < nb && j >= jlo && j < jhi;
+    const float *p = ok ? src + b * bstride + j : g_zero_src;
+    if constexpr (VEC) dma_dwordx4(p, dst + base);
+    else dma_dword(p, dst + base);
+  }
+}
+
+// Slab of image n: channel blocks of R*W floats (rows hs..hs+R-1 of x, those
+// outside [0, H) as zeros), then the zero plane.
+template <bool VEC>
+__device__ __forceinline__ void stage_slab(float *xs, const float *__restrict__ x, const Geo &g,
+                                           const Slab &s, int n) {
+  const int hs = s.ho0 * g.sh - g.ph;
+  const int RW = s.R * g.W;
+  const int rlo = hs < 0 ? -hs : 0;
+  const int rhi = g.H - hs < s.R ? g.H - hs : s.R;
+  const float *xn = x + (long)n * g.C * g.H * g.W + (long)hs * g.W;
+  stage_blocks<VEC>(xs, xn, (g.C + 1) * RW, RW, g.C, (long)g.H * g.W, rlo * g.W, rhi * g.W);
+}
+
+// im2col row k -> (LDS offset of the tap inside the slab, kw - pw, offset of
+// the flipped tap in the FLIP weight layout); taps past K -> the zero plane,
+// never masked (their weight offset is 0: a finite weight times zero).
+__device__ __forceinline__ int4 tap_entry(const Geo &g, const Slab &s, int k) {
+  if (k >= g.K) return make_int4(g.C * s.R * g.W, 0, 0, 0);
+  const int taps = g.HH * g.WW;
+  const int c = fdiv(k, taps, 1.0f / (float)taps), t = k - c * taps;
+  const int kh = fdiv(t, g.WW, 1.0f / (float)g.WW), kw = t - kh * g.WW;
+  return make_int4((c * s.R + kh) * g.W + kw - g.pw, kw - g.pw, c * 32 * taps + taps - 1 - t, 0);
+}
+
+// output pixel p -> (LDS offset inside the slab, wo*sw)
+__device__ __forceinline__ int2 pixel_entry(const Geo &g, const Slab &s, int p) {
+  const int ho = fdiv(p, g.Wo, 1.0f / (float)g.Wo), wo = p - ho * g.Wo;
+  return make_int2((ho - s.ho0) * g.sh * g.W + wo * g.sw, wo * g.sw);
+}
+
+// B operand: slab element at tap + pixel, 0 in the horizontal padding
+__device__ __forceinline__ float slab_read(const float *xs, int4 tap, int2 pix, int W) {
+  const float v = xs[tap.x + pix.x];
+  return (unsigned)(pix.y + tap.y) < (unsigned)W ? v : 0.0f;
+}
+
+// Row stride of the forward weights in LDS: whole 16-byte reads, and
+// 8 lanes reading rows f..f+7 at one k cover all 32 banks (stride = 4 mod 32).
+__host__ __device__ inline int wrow_stride(int Kp) { return round_up(Kp, 32) + 4; }
+
+// Weights of one block of 32 output channels into LDS with direct loads.
+//   forward: ws[f][KST] = W[f0+f][0..K) (zeros past K and past F): rows of
+//     the weight tensor, so each row is one contiguous copy;
+//   FLIP (the dX convolution; w is the forward kernel, C_in x F_out x HH x
+//     WW in this geometry's terms): ws[fi][c][t] = w[fi][f0+c][t] for c < 32
+//     (zeros past F), the tensor's own order; the tap flip is applied when
+//     the operand is read (tap_entry's .z).
+template <bool FLIP, bool VEC>
+__device__ __forceinline__ void stage_weights(float *ws, const float *__restrict__ w,
+                                              const Geo &g, int f0, int Kp) {
+  const int nf = g.F - f0 < 32 ? g.F - f0 : 32;
+  const int taps = g.HH * g.WW;
+  if constexpr (FLIP)
+    stage_blocks<VEC>(ws, w + (long)f0 * taps, g.C * 32 * taps, 32 * taps, g.C,
+                      (long)g.F * taps, 0, nf * taps);
+  else
+    stage_blocks<VEC>(ws, w + (long)f0 * g.K, 32 * wrow_stride(Kp), wrow_stride(Kp), nf,
+                      g.K, 0, g.K);
+}
+
+// ---- forward (and stride-1 dX with FLIP) ----
+//
+// Grid: x = image * chunks + chunk (chunks of 128*PB output pixels), y =
+// block of 32 output channels.
+template <int PB, bool FLIP, bool VEC>
+__global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2)))
+conv_fwd_lds_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                    const float *__restrict__ bias, float *__restrict__ out, Geo g, int chunks,
+                    int dbg) {
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  constexpr int CHUNK = 128 * PB;
+  const int n = blockIdx.x / chunks, chunk = blockIdx.x - n * chunks;
+  const int P = g.Ho * g.Wo;
+  const int p0 = chunk * CHUNK;
+  const int p1 = min(p0 + CHUNK, P);
+  const int f0 = blockIdx.y * 32;
+  const int Kp = (g.K + 7) & ~7;  // whole groups of 4 k-steps per lane half
+  const int Kh = Kp >> 1;         // lane half h takes k = h*Kh + step
+  const int KST = wrow_stride(Kp);
+  const int taps = g.HH * g.WW;
+  const Slab s = slab_of(g, p0, p1);
+
+  float *ws = smem;                                  // forward: 32 x KST; FLIP: C x 32 x taps
+  int4 *tab = (int4 *)(ws + (FLIP ? round_up(g.K * 32, 256) : round_up(32 * KST, 256)));
+  float *bs = (float *)(tab + Kp);                   // 32 (+pad): bias of the block
+  float *xs = bs + 64 + GUARD;                       // (C+1) x R x W (whole 16-byte loads)
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  if (!(dbg & 1)) stage_slab<VEC>(xs, x, g, s, n);
+  if (!(dbg & 2)) stage_weights<FLIP, VEC>(ws, w, g, f0, Kp);
+  for (int k = tid; k < Kp; k += NT) tab[k] = tap_entry(g, s, k);
+  if (tid < 32) bs[tid] = (bias && f0 + tid < g.F) ? bias[f0 + tid] : 0.0f;
+  dma_wait();
+  __syncthreads();
+
+  const int l32 = lane & 31, half = lane >> 5;
+  int2 pix[PB];
+#pragma unroll
+  for (int j = 0; j < PB; j++) {
+    const int p = p0 + (wave * PB + j) * 32 + l32;
+    pix[j] = p < p1 ? pixel_entry(g, s, p) : make_int2(0, -(1 << 20));  // masked
+  }
+  f32x16 acc[PB];
+#pragma unroll
+  for (int j = 0; j < PB; j++)
+    for (int r = 0; r < 16; r++) acc[j][r] = 0.0f;
+
+  // Software pipeline over groups of U = 4 k-steps: while the MFMAs of group
+  // i run, the operands of group i+1 and the tap entries of group i+2 are
+  // read from LDS, so no MFMA waits on an LDS round trip.  Lane half h
+  // covers k = h*Kh + step (A and B agree on the order, so the sum is the
+  // same); the forward weights of 4 steps are one 16-byte read.
+  constexpr int U = 4;
+  const float *wa = FLIP ? ws + l32 * taps : ws + l32 * KST + half * Kh;
+  const int4 *tb = tab + half * Kh;
+  const int groups = (dbg & 4) ? 0 : Kh / U;
+  float a_c[U], b_c[U][PB];
+  int4 t_c[U], t_n[U];
+#pragma unroll
+  for (int u = 0; u < U; u++) t_c[u] = tb[u];
+  if constexpr (FLIP) {
+#pragma unroll
+    for (int u = 0; u < U; u++) a_c[u] = wa[t_c[u].z];
+  } else {
+    const float4 a4 = *(const float4 *)wa;
+    a_c[0] = a4.x; a_c[1] = a4.y; a_c[2] = a4.z; a_c[3] = a4.w;
+  }
+#pragma unroll
+  for (int u = 0; u < U; u++)
+#pragma unroll
+    for (int j = 0; j < PB; j++) b_c[u][j] = slab_read(xs, t_c[u], pix[j], g.W);
+  {
+    const int g1 = groups > 1 ? 1 : 0;
+#pragma unroll
+    for (int u = 0; u < U; u++) t_n[u] = tb[g1 * U + u];
+  }
+  for (int gi = 0; gi < groups; gi++) {
+    const int g1 = gi + 1 < groups ? gi + 1 : gi;
+    const int g2 = gi + 2 < groups ? gi + 2 : g1;
+    float a_n[U], b_n[U][PB];
+    int4 t_nn[U];
+    if constexpr (FLIP) {
+#pragma unroll
+      for (int u = 0; u < U; u++) a_n[u] = wa[t_n[u].z];
+    } else {
+      const float4 a4 = *(const float4 *)(wa + g1 * U);
+      a_n[0] = a4.x; a_n[1] = a4.y; a_n[2] = a4.z; a_n[3] = a4.w;
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+#pragma unroll
+      for (int j = 0; j < PB; j++) b_n[u][j] = slab_read(xs, t_n[u], pix[j], g.W);
+      t_nn[u] = tb[g2 * U + u];
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++)
+#pragma unroll
+      for (int j = 0; j < PB; j++)
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a_c[u], b_c[u][j], acc[j], 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      a_c[u] = a_n[u];
+      t_n[u] = t_nn[u];
+#pragma unroll
+      for (int j = 0; j < PB; j++) b_c[u][j] = b_n[u][j];
+    }
+  }
+
+  float bv[16];  // bias of this lane's 16 rows (zeros when there is none)
+#pragma unroll
+  for (int r = 0; r < 16; r++) bv[r] = bs[8 * (r >> 2) + 4 * half + (r & 3)];
+  float *on = out + (long)n * g.F * P;
+#pragma unroll
+  for (int j = 0; j < PB; j++) {
+    const int p = p0 + (wave * PB + j) * 32 + l32;
+    if (p >= p1 || (dbg & 8)) continue;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int f = f0 + 8 * (r >> 2) + 4 * half + (r & 3);
+      if (f < g.F) on[(long)f * P + p] = acc[j][r] + bv[r];
+    }
+  }
+}
+
+// ---- forward / dX for KH x KW kernels known at compile time ----
+//
+// Lane half h of the 32x32x2 MFMA takes input channels [h*CH2, (h+1)*CH2)
+// (CH2 = ceil(C/2); an odd C borrows the zero plane as channel C), so both
+// halves use the same tap (kh, kw) at every step: the tap is a loop
+// constant, the slab address is a per-lane base (advanced once per channel)
+// plus an immediate, and the horizontal padding is one of KW lane masks
+// computed once.  The main loop reads no tables and does almost no VALU
+// work.  Weights as in the generic kernel (forward rows of KST floats, FLIP
+// in the tensor's order).
+template <int PB, bool FLIP, bool VEC, int KH, int KW>
+__global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2)))
+conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                  const float *__restrict__ bias, float *__restrict__ out, Geo g, int chunks,
+                  int dbg) {
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  constexpr int CHUNK = 128 * PB, TAPS = KH * KW;
+  const int n = blockIdx.x / chunks, chunk = blockIdx.x - n * chunks;
+  const int P = g.Ho * g.Wo;
+  const int p0 = chunk * CHUNK;
+  const int p1 = min(p0 + CHUNK, P);
+  const int f0 = blockIdx.y * 32;
+  const int CH2 = (g.C + 1) >> 1;
+  const int KST = wrow_stride(2 * CH2 * TAPS);
+  const Slab s = slab_of(g, p0, p1);
+  const int RW = s.R * g.W;
+  const int nf = g.F - f0 < 32 ? g.F - f0 : 32;
+
+  float *ws = smem;  // forward: 32 x KST; FLIP: 2*CH2 x 32 x TAPS
+  float *bs = ws + (FLIP ? round_up(2 * CH2 * 32 * TAPS, 256) : round_up(32 * KST, 256));
+  float *xs = bs + 64 + GUARD;                       // (C+1) x R x W
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  if (!(dbg & 1)) stage_slab<VEC>(xs, x, g, s, n);
+  if (!(dbg & 2)) {
+    if constexpr (FLIP)
+      stage_blocks<VEC>(ws, w + (long)f0 * TAPS, 2 * CH2 * 32 * TAPS, 32 * TAPS, g.C,
+                        (long)g.F * TAPS, 0, nf * TAPS);
+    else
+      stage_blocks<VEC>(ws, w + (long)f0 * g.K, 32 * KST, KST, nf, g.K, 0, g.K);
+  }
+  if (tid < 32) bs[tid] = (bias && f0 + tid < g.F) ? bias[f0 + tid] : 0.0f;
+  dma_wait();
+  __syncthreads();
+
+  const int l32 = lane & 31, half = lane >> 5;
+  const int hoff = half * CH2 * RW - g.pw;
+  int bj[PB];
+  bool mk[PB][KW];
+#pragma unroll
+  for (int j = 0; j < PB; j++) {
+    const int p = p0 + (wave * PB + j) * 32 + l32;
+    int2 e = make_int2(0, -(1 << 20));  // past the chunk: every tap masked
+    if (p < p1) e = pixel_entry(g, s, p);
+    bj[j] = e.x + hoff;
+#pragma unroll
+    for (int kw = 0; kw < KW; kw++) mk[j][kw] = (unsigned)(e.y + kw - g.pw) < (unsigned)g.W;
+  }
+  f32x16 acc[PB];
+#pragma unroll
+  for (int j = 0; j < PB; j++)
+    for (int r = 0; r < 16; r++) acc[j][r] = 0.0f;
+
+  const float *wa = FLIP ? ws + l32 * TAPS + half * CH2 * 32 * TAPS
+                         : ws + l32 * KST + half * CH2 * TAPS;
+  constexpr int WSTEP_FLIP = 32 * TAPS;
+  const int steps = (dbg & 4) ? 0 : CH2;
+  // operands of channel c+1 are read before the MFMAs of channel c
+  auto load = [&](int c, float (&a)[TAPS], float (&b)[TAPS][PB]) {
+    const float *wc = wa + c * (FLIP ? WSTEP_FLIP : TAPS);
+    const int cb = c * RW;
+#pragma unroll
+    for (int t = 0; t < TAPS; t++) a[t] = FLIP ? wc[TAPS - 1 - t] : wc[t];
+#pragma unroll
+    for (int j = 0; j < PB; j++)
+#pragma unroll
+      for (int kh = 0; kh < KH; kh++) {
+        const float *row = xs + bj[j] + cb + kh * g.W;
+#pragma unroll
+        for (int kw = 0; kw < KW; kw++) b[kh * KW + kw][j] = row[kw];  // raw: masked at use
+      }
+  };
+  float a_c[TAPS], b_c[TAPS][PB];
+  if (steps > 0) load(0, a_c, b_c);
+  for (int c = 0; c < steps; c++) {
+    float a_n[TAPS], b_n[TAPS][PB];
+    load(c + 1 < steps ? c + 1 : c, a_n, b_n);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < TAPS; t++)
+#pragma unroll
+      for (int j = 0; j < PB; j++) {
+        const float b = mk[j][t % KW] ? b_c[t][j] : 0.0f;
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a_c[t], b, acc[j], 0, 0, 0);
+      }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < TAPS; t++) {
+      a_c[t] = a_n[t];
+#pragma unroll
+      for (int j = 0; j < PB; j++) b_c[t][j] = b_n[t][j];
+    }
+  }
+
+  float bv[16];
+#pragma unroll
+  for (int r = 0; r < 16; r++) bv[r] = bs[8 * (r >> 2) + 4 * half + (r & 3)];
+  float *on = out + (long)n * g.F * P;
+#pragma unroll
+  for (int j = 0; j < PB; j++) {
+    const int p = p0 + (wave * PB + j) * 32 + l32;
+    if (p >= p1 || (dbg & 8)) continue;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int f = f0 + 8 * (r >> 2) + 4 * half + (r & 3);
+      if (f < g.F) on[(long)f * P + p] = acc[j][r] + bv[r];
+    }
+  }
+}
+
+// ---- weight gradient partials ----
+//
+// Grid: x = image * chunks + chunk (chunk = CH output pixels), y = block of
+// FB filters (FB = 16 * FS).  Waves: KS of them split the chunk's pixels
+// (4-pixel steps, interleaved), 4/KS groups split the FS x JB grid of 16x16
+// output blocks as (FS/MF) x (JB/JW) rectangles of MF x JW blocks.  Partial
+// z = blockIdx.x gets part[z][f][k] (k < K) and part[z][f][K] = sum of g.
+template <int MF, int JW, int KS, bool VEC, bool ROWS>
+__global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2)))
+conv_dw_lds_kernel(const float *__restrict__ gr, const float *__restrict__ x,
+                   float *__restrict__ part, Geo g, int chunks, int CH, int FS, int dbg) {
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  const int n = blockIdx.x / chunks, chunk = blockIdx.x - n * chunks;
+  const int P = g.Ho * g.Wo;
+  const int p0 = chunk * CH;
+  const int p1 = min(p0 + CH, P);
+  const int np = p1 - p0;
+  const int npp = (np + 3) & ~3;
+  const int GS = ((npp + 31) & ~31) + 4;   // g row stride: 16 rows x 4 pixels hit distinct banks
+  const int FB = 16 * FS;
+  const int f0 = blockIdx.y * FB;
+  const int JB16 = ((g.K + 15) >> 4) << 4;
+  const Slab s = slab_of(g, p0, p1);
+
+  float *gs = smem;                                    // FB x GS (whole 16-byte loads)
+  int2 *pixt = (int2 *)(gs + round_up(FB * GS, 256));  // npp pixel entries
+  int4 *ktab = (int4 *)(pixt + npp);                   // JB16 tap entries
+  float *xs = (float *)(ktab + JB16) + GUARD;          // (C+1) x R x W
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const float *gn = gr + (long)n * g.F * P + (long)f0 * P + p0;
+  const int nf = g.F - f0 < FB ? g.F - f0 : FB;
+  if (!(dbg & 2)) stage_blocks<VEC>(gs, gn, FB * GS, GS, nf, P, 0, np);
+  if (!(dbg & 1)) stage_slab<VEC>(xs, x, g, s, n);
+  for (int q = tid; q < npp; q += NT)
+    pixt[q] = q < np ? pixel_entry(g, s, p0 + q) : make_int2(0, -(1 << 20));  // masked
+  for (int k = tid; k < JB16; k += NT) ktab[k] = tap_entry(g, s, k);
+  dma_wait();
+  __syncthreads();
+
+  // bias gradient partial: TPR consecutive lanes per filter row
+  {
+    const int TPR = NT / FB;
+    const int f = tid / TPR, sub = tid - f * TPR;
+    float sum = 0.0f;
+    for (int q = sub; q < np; q += TPR) sum += gs[f * GS + q];
+    for (int o = 1; o < TPR; o <<= 1) sum += __shfl_xor(sum, o, 64);
+    const int fo = f0 + f;
+    if (sub == 0 && fo < g.F) part[((long)blockIdx.x * g.F + fo) * (g.K + 1) + g.K] = sum;
+  }
+
+  const int JB = (g.K + 15) >> 4;
+  const int ks = wave % KS, grp = wave / KS;
+  const int fgroups = FS / MF;
+  const int fs0 = (grp % fgroups) * MF, jb0 = (grp / fgroups) * JW;
+  const int l16 = lane & 15, q4 = lane >> 4;
+
+  int4 kof[JW];
+#pragma unroll
+  for (int jw = 0; jw < JW; jw++) {
+    const int k = (jb0 + jw) * 16 + l16;
+    kof[jw] = k < JB16 ? ktab[k] : make_int4(g.C * s.R * g.W, 0, 0, 0);  // past JB: zero plane
+  }
+
+  f32x4 acc[MF][JW];
+#pragma unroll
+  for (int m = 0; m < MF; m++)
+#pragma unroll
+    for (int jw = 0; jw < JW; jw++) acc[m][jw] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const bool active = jb0 < JB && !(dbg & 4);   // wave-uniform
+  if constexpr (ROWS) {
+    // Whole output rows (Wo a multiple of 16, chunk = whole rows): wave ks
+    // takes rows ks, ks+KS, ...; a row is walked in 16-pixel segments of 4
+    // steps whose pixel offsets are immediates.  Lane (tap l16, pixel q4):
+    // slab column of step s in a segment at wo0 = (wo0 + 4s + q4)*sw + kw - pw.
+    if (active) {
+      const int rows = np / g.Wo;
+      int cq[JW], bb[JW];
+#pragma unroll
+      for (int jw = 0; jw < JW; jw++) {
+        cq[jw] = q4 * g.sw + kof[jw].y;
+        bb[jw] = kof[jw].x + q4 * g.sw;
+      }
+      const float *ga = gs + (fs0 * 16 + l16) * GS + q4;
+      for (int r = ks; r < rows; r += KS) {
+        const int pr = r * g.sh * g.W;   // chunk rows start at s.ho0
+        for (int wo0 = 0; wo0 < g.Wo; wo0 += 16) {
+          const int qb = r * g.Wo + wo0;
+          const int pb = pr + wo0 * g.sw;
+#pragma unroll
+          for (int st = 0; st < 4; st++) {
+            float a[MF];
+#pragma unroll
+            for (int m = 0; m < MF; m++) a[m] = ga[m * 16 * GS + qb + 4 * st];
+#pragma unroll
+            for (int jw = 0; jw < JW; jw++) {
+              const float v = xs[bb[jw] + pb + 4 * st * g.sw];
+              const bool ok = (unsigned)(cq[jw] + (wo0 + 4 * st) * g.sw) < (unsigned)g.W;
+              const float b = ok ? v : 0.0f;
+#pragma unroll
+              for (int m = 0; m < MF; m++)
+                acc[m][jw] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[m], b, acc[m][jw], 0, 0, 0);
+            }
+          }
+        }
+      }
+    }
+  } else {
+  const int nst = npp >> 2;
+  const int T = active && nst > ks ? (nst - ks + KS - 1) / KS : 0;
+  if (T > 0) {
+    // step t covers pixels (ks + t*KS)*4 .. +3 of the chunk
+    const float *ga = gs + (fs0 * 16 + l16) * GS + q4;
+#pragma unroll 2
+    for (int t = 0; t < T; t++) {
+      const int st = ks + t * KS;
+      const int2 px = pixt[st * 4 + q4];
+      float a[MF];
+#pragma unroll
+      for (int m = 0; m < MF; m++) a[m] = ga[m * 16 * GS + st * 4];
+#pragma unroll
+      for (int jw = 0; jw < JW; jw++) {
+        const float b = slab_read(xs, kof[jw], px, g.W);
+#pragma unroll
+        for (int m = 0; m < MF; m++)
+          acc[m][jw] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[m], b, acc[m][jw], 0, 0, 0);
+      }
+    }
+  }
+  }
+
+  if constexpr (KS > 1) {
+    // the KS pixel-split waves of a group add their accumulators in order
+    __syncthreads();  // every wave is done reading the slab: reuse it
+    float *red = xs;
+    constexpr int PER = MF * JW * 4;
+    if (ks > 0) {
+#pragma unroll
+      for (int m = 0; m < MF; m++)
+#pragma unroll
+        for (int jw = 0; jw < JW; jw++)
+#pragma unroll
+          for (int r = 0; r < 4; r++)
+            red[(((grp * (KS - 1) + ks - 1) * PER) + (m * JW + jw) * 4 + r) * 64 + lane] =
+                acc[m][jw][r];
+    }
+    __syncthreads();
+    if (ks != 0) return;
+#pragma unroll
+    for (int o = 1; o < KS; o++)
+#pragma unroll
+      for (int m = 0; m < MF; m++)
+#pragma unroll
+        for (int jw = 0; jw < JW; jw++)
+#pragma unroll
+          for (int r = 0; r < 4; r++)
+            acc[m][jw][r] +=
+                red[(((grp * (KS - 1) + o - 1) * PER) + (m * JW + jw) * 4 + r) * 64 + lane];
+  }
+  if (jb0 >= JB || (dbg & 8)) return;
+
+  float *pz = part + (long)blockIdx.x * g.F * (g.K + 1);
+#pragma unroll
+  for (int jw = 0; jw < JW; jw++) {
+    const int k = (jb0 + jw) * 16 + l16;
+    if (k >= g.K) continue;
+#pragma unroll
+    for (int m = 0; m < MF; m++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int f = f0 + (fs0 + m) * 16 + 4 * q4 + r;
+        if (f < g.F) pz[(long)f * (g.K + 1) + k] = acc[m][jw][r];
+      }
+  }
+}
+
+// ---- weight gradient partials on 32x32x2 MFMAs (even Wo, whole rows) ----
+//
+// Block (32 filters) x (32 taps) per MFMA, two output pixels per step: lane
+// l feeds A[f = l%32][pixel h = l/32] = g and B[pixel h][tap l%32] = the
+// slab; accumulator r holds filter 8(r/4) + 4h + r%4, tap l%32.  Grid: x =
+// image * chunks + chunk (chunk = whole output rows), y = block of 32
+// filters.  Waves: 4/KS groups take JW tap blocks each, the KS waves of a
+// group take rows ks, ks+KS, ...; each row is walked two pixels a step with
+// the pixel offsets as immediates (4 steps unrolled).  Measured on gfx950
+// the 32x32x2 form runs ~20% faster than 16x16x4.
+template <int JW, int KS, bool VEC>
+__global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2)))
+conv_dw32_kernel(const float *__restrict__ gr, const float *__restrict__ x,
+                 float *__restrict__ part, Geo g, int chunks, int CH, int dbg) {
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  constexpr int FB = 32;
+  const int n = blockIdx.x / chunks, chunk = blockIdx.x - n * chunks;
+  const int P = g.Ho * g.Wo;
+  const int p0 = chunk * CH;
+  const int p1 = min(p0 + CH, P);
+  const int np = p1 - p0;
+  const int GS = ((np + 31) & ~31) + 4;
+  const int f0 = blockIdx.y * FB;
+  const int JB = (g.K + 31) >> 5;                  // 32-tap blocks
+  const Slab s = slab_of(g, p0, p1);
+
+  float *gs = smem;                                       // FB x GS
+  int4 *ktab = (int4 *)(gs + round_up(FB * GS, 256));     // 32*JB tap entries
+  float *xs = (float *)(ktab + 32 * JB) + GUARD;          // (C+1) x R x W
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const float *gn = gr + (long)n * g.F * P + (long)f0 * P + p0;
+  const int nf = g.F - f0 < FB ? g.F - f0 : FB;
+  if (!(dbg & 2)) stage_blocks<VEC>(gs, gn, FB * GS, GS, nf, P, 0, np);
+  if (!(dbg & 1)) stage_slab<VEC>(xs, x, g, s, n);
+  for (int k = tid; k < 32 * JB; k += NT) ktab[k] = tap_entry(g, s, k);
+  dma_wait();
+  __syncthreads();
+
+  {  // bias gradient partial: 8 consecutive lanes per filter row
+    const int f = tid >> 3, sub = tid & 7;
+    float sum = 0.0f;
+    for (int q = sub; q < np; q += 8) sum += gs[f * GS + q];
+    for (int o = 1; o < 8; o <<= 1) sum += __shfl_xor(sum, o, 64);
+    const int fo = f0 + f;
+    if (sub == 0 && fo < g.F) part[((long)blockIdx.x * g.F + fo) * (g.K + 1) + g.K] = sum;
+  }
+
+  const int ks = wave % KS, grp = wave / KS;
+  const int jb0 = grp * JW;
+  const int l32 = lane & 31, h = lane >> 5;
+  int bb[JW], cq[JW];
+#pragma unroll
+  for (int jw = 0; jw < JW; jw++) {
+    const int k = (jb0 + jw) * 32 + l32;
+    const int4 t = k < 32 * JB ? ktab[k] : make_int4(g.C * s.R * g.W, 0, 0, 0);
+    bb[jw] = t.x + h * g.sw;      // slab offset of (tap, pixel h) at the row start
+    cq[jw] = t.y + h * g.sw;      // its column relative to wo*sw
+  }
+  f32x16 acc[JW];
+#pragma unroll
+  for (int jw = 0; jw < JW; jw++)
+    for (int r = 0; r < 16; r++) acc[jw][r] = 0.0f;
+
+  if (jb0 < JB && !(dbg & 4)) {
+    // this wave's steps: rows ks, ks+KS, ... of the chunk, Wo/2 steps a row;
+    // the operands of step t+1 are read before the MFMAs of step t
+    const int rows = np / g.Wo;
+    const int half_w = g.Wo >> 1;
+    const int T = rows > ks ? ((rows - ks + KS - 1) / KS) * half_w : 0;
+    const float *ga = gs + l32 * GS + h;
+    auto load = [&](int r, int st, float &a, float (&b)[JW]) {  // raw: masked at use
+      a = ga[r * g.Wo + 2 * st];
+      const int off = r * g.sh * g.W + 2 * st * g.sw;
+#pragma unroll
+      for (int jw = 0; jw < JW; jw++) b[jw] = xs[bb[jw] + off];
+    };
+    int r = ks, st = 0;
+    float a_c, b_c[JW];
+    if (T > 0) load(r, st, a_c, b_c);
+    for (int t = 0; t < T; t++) {
+      int st1 = st + 1, r1 = r;
+      if (st1 == half_w) { st1 = 0; r1 += KS; }
+      float a_n, b_n[JW];
+      load(t + 1 < T ? r1 : r, t + 1 < T ? st1 : st, a_n, b_n);
+      __builtin_amdgcn_sched_barrier(0);
+      const int col = 2 * st * g.sw;
+#pragma unroll
+      for (int jw = 0; jw < JW; jw++) {
+        const float b = (unsigned)(cq[jw] + col) < (unsigned)g.W ? b_c[jw] : 0.0f;
+        acc[jw] = __builtin_amdgcn_mfma_f32_32x32x2f32(a_c, b, acc[jw], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      a_c = a_n;
+#pragma unroll
+      for (int jw = 0; jw < JW; jw++) b_c[jw] = b_n[jw];
+      r = r1;
+      st = st1;
+    }
+  }
+
+  if constexpr (KS > 1) {
+    // the KS row-split waves of a group add their accumulators in order
+    __syncthreads();  // operands no longer read: reuse the whole LDS
+    float *red = smem;
+    constexpr int PER = JW * 16;
+    if (ks > 0) {
+#pragma unroll
+      for (int jw = 0; jw < JW; jw++)
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+          red[((grp * (KS - 1) + ks - 1) * PER + jw * 16 + r) * 64 + lane] = acc[jw][r];
+    }
+    __syncthreads();
+    if (ks != 0) return;
+#pragma unroll
+    for (int o = 1; o < KS; o++)
+#pragma unroll
+      for (int jw = 0; jw < JW; jw++)
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+          acc[jw][r] += red[((grp * (KS - 1) + o - 1) * PER + jw * 16 + r) * 64 + lane];
+  }
+  if (jb0 >= JB || (dbg & 8)) return;
+
+  float *pz = part + (long)blockIdx.x * g.F * (g.K + 1);
+#pragma unroll
+  for (int jw = 0; jw < JW; jw++) {
+    const int k = (jb0 + jw) * 32 + l32;
+    if (k >= g.K) continue;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int f = f0 + 8 * (r >> 2) + 4 * h + (r & 3);
+      if (f < g.F) pz[(long)f * (g.K + 1) + k] = acc[jw][r];
+    }
+  }
+}
+
+// dw[f][k] = sum_z part[z][f][k] (k < K), db[f] = sum_z part[z][f][K]; ZL
+// lanes per output each add every ZL-th partial in order, then lane 0 adds
+// the ZL sums in order.
+template <int ZL>
+__global__ void __launch_bounds__(NT)
+conv_dw_reduce_kernel(const float *__restrict__ part, float *__restrict__ dw,
+                      float *__restrict__ db, int Z, int F, int K) {
+  constexpr int XL = NT / ZL;
+  __shared__ float sums[ZL][XL];
+  const int tx = threadIdx.x % XL, ty = threadIdx.x / XL;
+  const int total = F * (K + 1);
+  const int idx = blockIdx.x * XL + tx;
+  float s = 0.0f;
+  if (idx < total)
+    for (int z = ty; z < Z; z += ZL) s += part[(long)z * total + idx];
+  sums[ty][tx] = s;
+  __syncthreads();
+  if (ty != 0 || idx >= total) return;
+  for (int j = 1; j < ZL; j++) s += sums[j][tx];
+  const int f = idx / (K + 1), k = idx - f * (K + 1);
+  if (k < K) dw[(long)f * K + k] = s;
+  else if (db) db[f] = s;
+}
+
+// ---- host-side planning ----
+
+bool geo_ok(long N, long C, long H, long W, long F, long HH, long WW, long sh, long sw, long ph,
+            long pw, long Ho, long Wo) {
+  if (N <= 0 || C <= 0 || H <= 0 || W <= 0 || F <= 0 || HH <= 0 || WW <= 0 || sh <= 0 ||
+      sw <= 0 || ph < 0 || pw < 0 || Ho <= 0 || Wo <= 0)
+    return false;
+  if (Ho != (H + 2 * ph - HH) / sh + 1 || Wo != (W + 2 * pw - WW) / sw + 1) return false;
+  const long lim = 0x7fffffffL;
+  // pixel and tap indices go through a float-reciprocal division (< 2^24);
+  // reads at column -pw stay inside the guard before the slab
+  return N * C * H * W < lim && N * F * Ho * Wo < lim && C * HH * WW < 65536 &&
+         Ho * Wo < (1L << 24) && N < 65536L * 16 && pw < GUARD;
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+// Most output rows a run of L consecutive pixels can touch.
+inline int rows_spanned(int L, int Wo) { return (L + Wo - 2) / Wo + 1; }
+
+// LDS floats of the slab for L consecutive output pixels, rounded to whole
+// 256-float runs of 16-byte loads (LDS_MAX / 4 + 1 when it cannot fit)
+inline long slab_floats(const Geo &g, int L) {
+  const long R = (long)(rows_spanned(L, g.Wo) - 1) * g.sh + g.HH;
+  const long f = (long)(g.C + 1) * R * g.W;
+  if (f > LDS_MAX / 4) return LDS_MAX / 4 + 1;
+  return round_up((int)f, 256);
+}
+
+int g_dbg = 0;
+
+struct FwdPlan {
+  int pb = 0, chunks = 0;
+  size_t lds = 0;
+};
+
+inline bool is_k3(const Geo &g) { return g.HH == 3 && g.WW == 3; }
+
+FwdPlan plan_fwd(const Geo &g, int N, bool flip) {
+  FwdPlan best;
+  const int P = g.Ho * g.Wo;
+  const int Kp = (g.K + 7) & ~7;
+  const int fblocks = (g.F + 31) / 32;
+  const int K2 = 2 * ((g.C + 1) / 2) * g.HH * g.WW;  // 3x3 kernel: channels padded to even
+  for (int pb = 2; pb >= 1; pb--) {
+    const int chunk = 128 * pb;
+    const int chunks = (P + chunk - 1) / chunk;
+    const long sf = slab_floats(g, chunk < P ? chunk : P);
+    long wsz, tabsz;
+    if (is_k3(g)) {
+      wsz = flip ? round_up(K2 * 32, 256) : round_up(32 * wrow_stride(K2), 256);
+      tabsz = 0;
+    } else {
+      wsz = flip ? round_up(g.K * 32, 256) : round_up(32 * wrow_stride(Kp), 256);
+      tabsz = 4L * Kp;
+    }
+    const long lds = 4L * (wsz + tabsz + 64 + GUARD + sf);
+    if (lds > LDS_MAX) continue;
+    best.pb = pb;
+    best.chunks = chunks;
+    best.lds = (size_t)lds;
+    // the wider chunk amortises the slab halo; take it while the grid still
+    // gives every CU two workgroups
+    if ((long)N * chunks * fblocks >= 512) break;
+  }
+  return best;
+}
+
+template <int PB, bool FLIP, bool VEC>
+int launch_fwd(const float *x, const float *w, const float *bias, float *out, const Geo &g, int N,
+               const FwdPlan &pl) {
+  auto kern = is_k3(g) ? conv_fwd_k_kernel<PB, FLIP, VEC, 3, 3> : conv_fwd_lds_kernel<PB, FLIP, VEC>;
+  if (pl.lds > 64 * 1024 &&
+      hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)pl.lds) != hipSuccess)
+    return -1;
+  const dim3 grid((unsigned)(N * pl.chunks), (unsigned)((g.F + 31) / 32));
+  hipLaunchKernelGGL(kern, grid, dim3(NT), pl.lds, stream(), x, w, bias, out, g, pl.chunks, g_dbg);
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+template <bool FLIP>
+int run_fwd(const float *x, const float *w, const float *bias, float *out, const Geo &g, int N,
+            bool dry) {
+  const FwdPlan pl = plan_fwd(g, N, FLIP);
+  if (!pl.pb) return -1;
+  if (dry) return 0;
+  // 16-byte loads: 4-aligned rows of x and of the weight blocks
+  const int taps = g.HH * g.WW;
+  const bool wvec = FLIP ? (g.F * taps) % 4 == 0 && ((g.F % 32) * taps) % 4 == 0 &&
+                               (32 * taps) % 4 == 0
+                         : g.K % 4 == 0;
+  const bool vec = g.W % 4 == 0 && aligned16(x) && wvec && aligned16(w);
+  if (pl.pb == 2)
+    return vec ? launch_fwd<2, FLIP, true>(x, w, bias, out, g, N, pl)
+               : launch_fwd<2, FLIP, false>(x, w, bias, out, g, N, pl);
+  return vec ? launch_fwd<1, FLIP, true>(x, w, bias, out, g, N, pl)
+             : launch_fwd<1, FLIP, false>(x, w, bias, out, g, N, pl);
+}
+
+// dW kernel variants: (MF, JW, KS) with FS = filters/16 per workgroup.
+//   V0 (1, 9, 1): FS = 1 -> 1 x 4 groups, K <= 576
+//   V1 (2, 2, 4): FS = 2, one group, K <= 32, waves split the pixels
+//   V2 (1, 4, 2): FS = 2, 2 x 1 groups, K <= 64, pairs of waves split the pixels
+//   V3 (1, 9, 2): FS = 1, 1 x 2 groups, K <= 288, pairs of waves split the pixels
+struct DwPlan {
+  int var = -1, fs = 0, ch = 0, chunks = 0;
+  size_t lds = 0;
+};
+
+// 32x32x2 dW variants (JW, KS): 4/KS groups of JW 32-tap blocks.
+//   W0 (1, 4): K <= 32      W1 (2, 2): K <= 128
+//   W2 (5, 2): K <= 320     W3 (9, 1): K <= 1152
+DwPlan plan_dw32(const Geo &g, int N) {
+  DwPlan pl;
+  const int JB = (g.K + 31) / 32;
+  const int P = g.Ho * g.Wo;
+  if (g.Wo % 2 != 0) return pl;
+  int groups;
+  if (JB <= 1) { pl.var = 10; groups = 1; }
+  else if (JB <= 4) { pl.var = 11; groups = 2; }
+  else if (JB <= 10) { pl.var = 12; groups = 2; }
+  else if (JB <= 36) { pl.var = 13; groups = 4; }
+  else return pl;
+  (void)groups;
+  const int fblocks = (g.F + 31) / 32;
+  // whole rows per chunk: whole images, halved while the grid gives a CU
+  // fewer than two workgroups and the partials stay small (each halving
+  // doubles the partial traffic)
+  int rows = g.Ho;
+  while (rows > 1 && (long)N * ((g.Ho + rows - 1) / rows) * fblocks < 512 &&
+         (long)N * ((g.Ho + rows / 2 - 1) / (rows / 2)) * g.F * (g.K + 1) * 4 <= (8L << 20))
+    rows = (rows + 1) / 2;
+  for (;; rows = (rows + 1) / 2) {
+    const int ch = rows * g.Wo;
+    const int GS = ((ch + 31) & ~31) + 4;
+    const int JWv = pl.var == 10 ? 1 : pl.var == 11 ? 2 : pl.var == 12 ? 5 : 9;
+    const int KSv = pl.var == 10 ? 4 : pl.var == 13 ? 1 : 2;
+    const long red = (long)(4 / KSv) * (KSv - 1) * JWv * 16 * 64;
+    long xs = slab_floats(g, ch < P ? ch : P);
+    const long main = round_up(32 * GS, 256) + 4L * 32 * JB + GUARD + xs;
+    const long lds = 4L * (main > red ? main : red);
+    if (lds <= LDS_MAX) {
+      pl.ch = ch;
+      pl.chunks = (P + ch - 1) / ch;
+      pl.fs = 2;
+      pl.lds = (size_t)lds;
+      return pl;
+    }
+    if (rows == 1) break;
+  }
+  pl.var = -1;
+  return pl;
+}
+
+DwPlan plan_dw(const Geo &g, int N) {
+  DwPlan pl = plan_dw32(g, N);
+  if (pl.var >= 0) return pl;
+  const int JB = (g.K + 15) / 16;
+  const int P = g.Ho * g.Wo;
+  if (JB <= 2) { pl.var = 1; pl.fs = 2; }
+  else if (JB <= 4) { pl.var = 2; pl.fs = 2; }
+  else if (JB <= 18) { pl.var = 3; pl.fs = 1; }
+  else if (JB <= 36) { pl.var = 0; pl.fs = 1; }
+  else return pl;
+  const int fblocks = (g.F + 16 * pl.fs - 1) / (16 * pl.fs);
+  // pixels per workgroup: whole images down to 64-pixel chunks, until the
+  // grid gives every CU two workgroups (one wave per SIMD leaves the LDS
+  // latency of each step exposed); more chunks mean more partial traffic
+  int ch = (P + 3) & ~3;
+  while (ch > 64 && (long)N * ((P + ch - 1) / ch) * fblocks < 512) ch = ((ch / 2) + 3) & ~3;
+  for (;; ch = ((ch / 2) + 3) & ~3) {
+    const int npp = (ch + 3) & ~3;
+    const int GS = ((npp + 31) & ~31) + 4;
+    // the pixel-split variants add their waves' accumulators through a buffer
+    // that reuses the slab: groups * (KS-1) * MF*JW*4 floats per lane
+    const long red = pl.var == 1   ? 1L * 3 * 2 * 2 * 4 * 64
+                     : pl.var == 2 ? 2L * 1 * 1 * 4 * 4 * 64
+                     : pl.var == 3 ? 2L * 1 * 1 * 9 * 4 * 64
+                                   : 0;
+    long xs = slab_floats(g, ch < P ? ch : P);
+    if (xs < red) xs = red;
+    const long lds =
+        4L * (round_up(16 * pl.fs * GS, 256) + 2L * npp + 4L * JB * 16 + GUARD + xs);
+    if (lds <= LDS_MAX) {
+      pl.ch = ch;
+      pl.chunks = (P + ch - 1) / ch;
+      pl.lds = (size_t)lds;
+      return pl;
+    }
+    if (ch <= 4) break;
+  }
+  pl.var = -1;
+  return pl;
+}
+
+template <int MF, int JW, int KS, bool VEC>
+int launch_dw(const float *gr, const float *x, float *part, const Geo &g, int N, const DwPlan &pl) {
+  // whole-row walk when rows are whole 16-pixel segments and chunks whole rows
+  const bool rows = g.Wo % 16 == 0 && pl.ch % g.Wo == 0;
+  auto kern = rows ? conv_dw_lds_kernel<MF, JW, KS, VEC, true>
+                   : conv_dw_lds_kernel<MF, JW, KS, VEC, false>;
+  if (pl.lds > 64 * 1024 &&
+      hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)pl.lds) != hipSuccess)
+    return -1;
+  const dim3 grid((unsigned)(N * pl.chunks), (unsigned)((g.F + 16 * pl.fs - 1) / (16 * pl.fs)));
+  hipLaunchKernelGGL(kern, grid, dim3(NT), pl.lds, stream(), gr, x, part, g, pl.chunks, pl.ch,
+                     pl.fs, g_dbg);
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+template <int JW, int KS, bool VEC>
+int launch_dw32(const float *gr, const float *x, float *part, const Geo &g, int N,
+                const DwPlan &pl) {
+  auto kern = conv_dw32_kernel<JW, KS, VEC>;
+  if (pl.lds > 64 * 1024 &&
+      hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)pl.lds) != hipSuccess)
+    return -1;
+  const dim3 grid((unsigned)(N * pl.chunks), (unsigned)((g.F + 31) / 32));
+  hipLaunchKernelGGL(kern, grid, dim3(NT), pl.lds, stream(), gr, x, part, g, pl.chunks, pl.ch,
+                     g_dbg);
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+template <bool VEC>
+int launch_dw_var(const float *gr, const float *x, float *part, const Geo &g, int N,
+                  const DwPlan &pl) {
+  switch (pl.var) {
+    case 10: return launch_dw32<1, 4, VEC>(gr, x, part, g, N, pl);
+    case 11: return launch_dw32<2, 2, VEC>(gr, x, part, g, N, pl);
+    case 12: return launch_dw32<5, 2, VEC>(gr, x, part, g, N, pl);
+    case 13: return launch_dw32<9, 1, VEC>(gr, x, part, g, N, pl);
+    case 0: return launch_dw<1, 9, 1, VEC>(gr, x, part, g, N, pl);
+    case 1: return launch_dw<2, 2, 4, VEC>(gr, x, part, g, N, pl);
+    case 2: return launch_dw<1, 4, 2, VEC>(gr, x, part, g, N, pl);
+    default: return launch_dw<1, 9, 2, VEC>(gr, x, part, g, N, pl);
+  }
+}
+
+int g_lds_conv = 1;  // tth_conv_lds
+
+}  // namespace
+
+extern "C" int tth_conv_dbg(int v) { g_dbg = v; return 0; }
+
+extern "C" int tth_conv_lds(int on) {
+  const int prev = g_lds_conv;
+  if (on >= 0) g_lds_conv = on ? 1 : 0;
+  return prev;
+}
+
+// Which LDS-staged kernels cover this convolution: bit 0 forward, bit 1
+// weight gradient, bit 2 input gradient.  0 when switched off.
+extern "C" int tt_k_conv2d_lds_plan(int N, int C, int H, int W, int F, int HH, int WW, int sh,
+                                    int sw, int ph, int pw, int Ho, int Wo) {
+  if (!g_lds_conv || !geo_ok(N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo)) return 0;
+  int bits = 0;
+  const Geo g{C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo, F, C * HH * WW};
+  if (run_fwd<false>(nullptr, nullptr, nullptr, nullptr, g, N, true) == 0) bits |= 1;
+  if (plan_dw(g, N).var >= 0) bits |= 2;
+  if (sh == 1 && sw == 1 && ph <= HH - 1 && pw <= WW - 1) {
+    const Geo gx{F, Ho, Wo, HH, WW, 1, 1, HH - 1 - ph, WW - 1 - pw, H, W, C, F * HH * WW};
+    if (run_fwd<true>(nullptr, nullptr, nullptr, nullptr, gx, N, true) == 0) bits |= 4;
+  }
+  return bits;
+}
+
+// out (N,F,Ho,Wo) = conv(x, w) + bias (bias may be NULL).  -1: not covered.
+extern "C" int tt_k_conv2d_fwd_lds(const float *x, const float *w, const float *bias, float *out,
+                                   int N, int C, int H, int W, int F, int HH, int WW, int sh,
+                                   int sw, int ph, int pw, int Ho, int Wo) {
+  if (!x || !w || !out || !geo_ok(N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo)) return -1;
+  const Geo g{C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo, F, C * HH * WW};
+  return run_fwd<false>(x, w, bias, out, g, N, false);
+}
+
+// dw (F, C*HH*WW) and, when db is given, db (F) from the output gradient g
+// (N,F,Ho,Wo) and the input x.  -1: not covered; -2: out of memory.
+extern "C" int tt_k_conv2d_dw_lds(const float *gr, const float *x, float *dw, float *db, int N,
+                                  int C, int H, int W, int F, int HH, int WW, int sh, int sw,
+                                  int ph, int pw, int Ho, int Wo) {
+  if (!gr || !x || !dw || !geo_ok(N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo)) return -1;
+  const Geo g{C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo, F, C * HH * WW};
+  const DwPlan pl = plan_dw(g, N);
+  if (pl.var < 0) return -1;
+  const long Z = (long)N * pl.chunks;
+  const long total = (long)F * (g.K + 1);
+  if (Z * total >= 0x7fffffffL) return -1;
+  float *part = (float *)ttrt_alloc(sizeof(float) * (size_t)(Z * total));
+  if (!part) return -2;
+  // 16-byte loads need 4-aligned rows of x and of the output gradient
+  const int P = Ho * Wo;
+  const bool vec = W % 4 == 0 && P % 4 == 0 && aligned16(x) && aligned16(gr);
+  int rc = vec ? launch_dw_var<true>(gr, x, part, g, N, pl)
+               : launch_dw_var<false>(gr, x, part, g, N, pl);
+  if (rc == 0) {
+    // lanes per output: enough workgroups to spread the partial reads
+    int zl = 1;
+    while (zl < 32 && zl < Z && total * zl * 2 <= 2048L * NT) zl *= 2;
+#define TT_RED(ZL_)                                                                       \
+  hipLaunchKernelGGL(conv_dw_reduce_kernel<ZL_>,                                          \
+                     dim3((unsigned)((total + NT / ZL_ - 1) / (NT / ZL_))), dim3(NT), 0,  \
+                     stream(), part, dw, db, (int)Z, F, g.K)
+    switch (zl) {
+      case 1: TT_RED(1); break;
+      case 2: TT_RED(2); break;
+      case 4: TT_RED(4); break;
+      case 8: TT_RED(8); break;
+      case 16: TT_RED(16); break;
+      default: TT_RED(32); break;
+    }
+#undef TT_RED
+    rc = hipGetLastError() == hipSuccess ? 0 : -3;
+  }
+  ttrt_free(part);  // stream-ordered: the kernels above run before any reuse
+  return rc;
+}
+
+// dx (N,C,H,W) of a stride-1 convolution from the output gradient g
+// (N,F,Ho,Wo) and the weights w (F,C,HH,WW).  -1: not covered.
+extern "C" int tt_k_conv2d_dx_lds(const float *gr, const float *w, float *dx, int N, int C, int H,
+                                  int W, int F, int HH, int WW, int sh, int sw, int ph, int pw,
+                                  int Ho, int Wo) {
+  if (!gr || !w || !dx || !geo_ok(N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo)) return -1;
+  if (sh != 1 || sw != 1 || ph > HH - 1 || pw > WW - 1) return -1;
+  const Geo gx{F, Ho, Wo, HH, WW, 1, 1, HH - 1 - ph, WW - 1 - pw, H, W, C, F * HH * WW};
+  return run_fwd<true>(gr, w, nullptr, dx, gx, N, false);
+}

@@ -178,6 +178,13 @@ Tensor *tt_conv2d_keepcol(const Tensor *a, const Tensor *w, const Tensor *b, int
     if (!out) return NULL;
     const int Kc = C * HH * WW;
     const long Ncol = (long)N * Ho * Wo;
+    /* LDS-staged direct convolution: taken when it also covers the weight
+     * gradient the caller will ask for (that reads x, so no col is kept) */
+    const int lds = tt_k_conv2d_lds_plan(N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo);
+    if ((lds & 1) && (!col_out || (lds & 2)) &&
+        tt_k_conv2d_fwd_lds(x, wd, bd, out->dev, N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho,
+                            Wo) == 0)
+        return out;
     if (tt_conv_use_implicit(sizeof(float) * (long)Kc * Ncol) &&
         tt_k_conv2d_fwd_implicit(x, wd, bd, out->dev, N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho,
                                  Wo) == 0)
