@@ -119,7 +119,7 @@ inline __host__ __device__ int round_up(int v, int m) { return (v + m - 1) / m *
 template <bool VEC>
 __device__ __forceinline__ void stage_blocks(float *dst, const float *__restrict__ src, int T,
                                              int B, int nb, long bstride, int jlo, int jhi) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const float rcpB = 1.0f / (float)B;
   constexpr int E = VEC ? 4 : 1;   // floats per lane per load
   for (int base = wave * 64 * E; base < T; base += NT * E) {
@@ -132,28 +132,36 @@ __device__ __forceinline__ void stage_blocks(float *dst, const float *__restrict
   }
 }
 
-// Slab of image n: channel blocks of R*W floats (rows hs..hs+R-1 of x, those
-// outside [0, H) as zeros), then the zero plane.
+// Channel stride of the slab in LDS: R rows of W floats plus 4 floats of
+// padding.  The pad moves consecutive channels to other banks: the 32 taps
+// of a weight-gradient operand read (3 to 4 channels of 3x3 taps) would
+// otherwise fall on a handful of banks whenever R*W is a multiple of 32
+// (16-way conflicts at W = 16); with it, 4-way at worst.
+__host__ __device__ inline int slab_cs(int R, int W) { return R * W + 4; }
+
+// Slab of image n: channel blocks of CS floats (rows hs..hs+R-1 of x, those
+// outside [0, H) as zeros, then the pad), then the zero plane.
 template <bool VEC>
 __device__ __forceinline__ void stage_slab(float *xs, const float *__restrict__ x, const Geo &g,
                                            const Slab &s, int n) {
   const int hs = s.ho0 * g.sh - g.ph;
-  const int RW = s.R * g.W;
+  const int CS = slab_cs(s.R, g.W);
   const int rlo = hs < 0 ? -hs : 0;
   const int rhi = g.H - hs < s.R ? g.H - hs : s.R;
   const float *xn = x + (long)n * g.C * g.H * g.W + (long)hs * g.W;
-  stage_blocks<VEC>(xs, xn, (g.C + 1) * RW, RW, g.C, (long)g.H * g.W, rlo * g.W, rhi * g.W);
+  stage_blocks<VEC>(xs, xn, (g.C + 1) * CS, CS, g.C, (long)g.H * g.W, rlo * g.W, rhi * g.W);
 }
 
 // im2col row k -> (LDS offset of the tap inside the slab, kw - pw, offset of
 // the flipped tap in the FLIP weight layout); taps past K -> the zero plane,
 // never masked (their weight offset is 0: a finite weight times zero).
 __device__ __forceinline__ int4 tap_entry(const Geo &g, const Slab &s, int k) {
-  if (k >= g.K) return make_int4(g.C * s.R * g.W, 0, 0, 0);
+  const int CS = slab_cs(s.R, g.W);
+  if (k >= g.K) return make_int4(g.C * CS, 0, 0, 0);
   const int taps = g.HH * g.WW;
   const int c = fdiv(k, taps, 1.0f / (float)taps), t = k - c * taps;
   const int kh = fdiv(t, g.WW, 1.0f / (float)g.WW), kw = t - kh * g.WW;
-  return make_int4((c * s.R + kh) * g.W + kw - g.pw, kw - g.pw, c * 32 * taps + taps - 1 - t, 0);
+  return make_int4(c * CS + kh * g.W + kw - g.pw, kw - g.pw, c * 32 * taps + taps - 1 - t, 0);
 }
 
 // output pixel p -> (LDS offset inside the slab, wo*sw)
@@ -219,7 +227,8 @@ conv_fwd_lds_kernel(const float *__restrict__ x, const float *__restrict__ w,
   float *bs = (float *)(tab + Kp);                   // 32 (+pad): bias of the block
   float *xs = bs + 64 + GUARD;                       // (C+1) x R x W (whole 16-byte loads)
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
   if (!(dbg & 1)) stage_slab<VEC>(xs, x, g, s, n);
   if (!(dbg & 2)) stage_weights<FLIP, VEC>(ws, w, g, f0, Kp);
   for (int k = tid; k < Kp; k += NT) tab[k] = tap_entry(g, s, k);
@@ -341,14 +350,15 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
   const int CH2 = (g.C + 1) >> 1;
   const int KST = wrow_stride(2 * CH2 * TAPS);
   const Slab s = slab_of(g, p0, p1);
-  const int RW = s.R * g.W;
+  const int RW = slab_cs(s.R, g.W);  // channel stride of the slab
   const int nf = g.F - f0 < 32 ? g.F - f0 : 32;
 
   float *ws = smem;  // forward: 32 x KST; FLIP: 2*CH2 x 32 x TAPS
   float *bs = ws + (FLIP ? round_up(2 * CH2 * 32 * TAPS, 256) : round_up(32 * KST, 256));
   float *xs = bs + 64 + GUARD;                       // (C+1) x R x W
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
   if (!(dbg & 1)) stage_slab<VEC>(xs, x, g, s, n);
   if (!(dbg & 2)) {
     if constexpr (FLIP)
@@ -465,7 +475,8 @@ conv_dw_lds_kernel(const float *__restrict__ gr, const float *__restrict__ x,
   int4 *ktab = (int4 *)(pixt + npp);                   // JB16 tap entries
   float *xs = (float *)(ktab + JB16) + GUARD;          // (C+1) x R x W
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
   const float *gn = gr + (long)n * g.F * P + (long)f0 * P + p0;
   const int nf = g.F - f0 < FB ? g.F - f0 : FB;
   if (!(dbg & 2)) stage_blocks<VEC>(gs, gn, FB * GS, GS, nf, P, 0, np);
@@ -497,7 +508,7 @@ conv_dw_lds_kernel(const float *__restrict__ gr, const float *__restrict__ x,
 #pragma unroll
   for (int jw = 0; jw < JW; jw++) {
     const int k = (jb0 + jw) * 16 + l16;
-    kof[jw] = k < JB16 ? ktab[k] : make_int4(g.C * s.R * g.W, 0, 0, 0);  // past JB: zero plane
+    kof[jw] = k < JB16 ? ktab[k] : make_int4(g.C * slab_cs(s.R, g.W), 0, 0, 0);  // past JB: zero plane
   }
 
   f32x4 acc[MF][JW];
@@ -643,7 +654,8 @@ conv_dw32_kernel(const float *__restrict__ gr, const float *__restrict__ x,
   int4 *ktab = (int4 *)(gs + round_up(FB * GS, 256));     // 32*JB tap entries
   float *xs = (float *)(ktab + 32 * JB) + GUARD;          // (C+1) x R x W
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
   const float *gn = gr + (long)n * g.F * P + (long)f0 * P + p0;
   const int nf = g.F - f0 < FB ? g.F - f0 : FB;
   if (!(dbg & 2)) stage_blocks<VEC>(gs, gn, FB * GS, GS, nf, P, 0, np);
@@ -652,13 +664,16 @@ conv_dw32_kernel(const float *__restrict__ gr, const float *__restrict__ x,
   dma_wait();
   __syncthreads();
 
+  // this workgroup's partial: JB blocks of 16 x 64 accumulators (the MFMA
+  // register layout, so every store is 256 contiguous bytes), then the 32
+  // bias sums
+  float *pz = part + ((long)blockIdx.x * gridDim.y + blockIdx.y) * (JB * 1024 + 32);
   {  // bias gradient partial: 8 consecutive lanes per filter row
     const int f = tid >> 3, sub = tid & 7;
     float sum = 0.0f;
     for (int q = sub; q < np; q += 8) sum += gs[f * GS + q];
     for (int o = 1; o < 8; o <<= 1) sum += __shfl_xor(sum, o, 64);
-    const int fo = f0 + f;
-    if (sub == 0 && fo < g.F) part[((long)blockIdx.x * g.F + fo) * (g.K + 1) + g.K] = sum;
+    if (sub == 0) pz[JB * 1024 + f] = sum;
   }
 
   const int ks = wave % KS, grp = wave / KS;
@@ -668,7 +683,7 @@ conv_dw32_kernel(const float *__restrict__ gr, const float *__restrict__ x,
 #pragma unroll
   for (int jw = 0; jw < JW; jw++) {
     const int k = (jb0 + jw) * 32 + l32;
-    const int4 t = k < 32 * JB ? ktab[k] : make_int4(g.C * s.R * g.W, 0, 0, 0);
+    const int4 t = k < 32 * JB ? ktab[k] : make_int4(g.C * slab_cs(s.R, g.W), 0, 0, 0);
     bb[jw] = t.x + h * g.sw;      // slab offset of (tap, pixel h) at the row start
     cq[jw] = t.y + h * g.sw;      // its column relative to wo*sw
   }
@@ -684,20 +699,22 @@ conv_dw32_kernel(const float *__restrict__ gr, const float *__restrict__ x,
     const int half_w = g.Wo >> 1;
     const int T = rows > ks ? ((rows - ks + KS - 1) / KS) * half_w : 0;
     const float *ga = gs + l32 * GS + h;
-    auto load = [&](int r, int st, float &a, float (&b)[JW]) {  // raw: masked at use
-      a = ga[r * g.Wo + 2 * st];
-      const int off = r * g.sh * g.W + 2 * st * g.sw;
+    // (scalar) offsets of the current step: g column qa, slab offset xo,
+    // column col; a step adds 2 pixels, a row end jumps KS rows ahead
+    const int qstep_row = KS * g.Wo - 2 * half_w, xstep_row = KS * g.sh * g.W - 2 * half_w * g.sw;
+    auto load = [&](int qa, int xo, float &a, float (&b)[JW]) {  // raw: masked at use
+      a = ga[qa];
 #pragma unroll
-      for (int jw = 0; jw < JW; jw++) b[jw] = xs[bb[jw] + off];
+      for (int jw = 0; jw < JW; jw++) b[jw] = xs[bb[jw] + xo];
     };
-    int r = ks, st = 0;
+    int qa = ks * g.Wo, xo = ks * g.sh * g.W, st = 0;
     float a_c, b_c[JW];
-    if (T > 0) load(r, st, a_c, b_c);
+    if (T > 0) load(qa, xo, a_c, b_c);
     for (int t = 0; t < T; t++) {
-      int st1 = st + 1, r1 = r;
-      if (st1 == half_w) { st1 = 0; r1 += KS; }
+      int qa1 = qa + 2, xo1 = xo + 2 * g.sw, st1 = st + 1;
+      if (st1 == half_w) { st1 = 0; qa1 += qstep_row; xo1 += xstep_row; }
       float a_n, b_n[JW];
-      load(t + 1 < T ? r1 : r, t + 1 < T ? st1 : st, a_n, b_n);
+      load(t + 1 < T ? qa1 : qa, t + 1 < T ? xo1 : xo, a_n, b_n);
       __builtin_amdgcn_sched_barrier(0);
       const int col = 2 * st * g.sw;
 #pragma unroll
@@ -709,7 +726,8 @@ conv_dw32_kernel(const float *__restrict__ gr, const float *__restrict__ x,
       a_c = a_n;
 #pragma unroll
       for (int jw = 0; jw < JW; jw++) b_c[jw] = b_n[jw];
-      r = r1;
+      qa = qa1;
+      xo = xo1;
       st = st1;
     }
   }
@@ -737,18 +755,49 @@ conv_dw32_kernel(const float *__restrict__ gr, const float *__restrict__ x,
           acc[jw][r] += red[((grp * (KS - 1) + o - 1) * PER + jw * 16 + r) * 64 + lane];
   }
   if (jb0 >= JB || (dbg & 8)) return;
-
-  float *pz = part + (long)blockIdx.x * g.F * (g.K + 1);
 #pragma unroll
   for (int jw = 0; jw < JW; jw++) {
-    const int k = (jb0 + jw) * 32 + l32;
-    if (k >= g.K) continue;
+    if (jb0 + jw >= JB) break;
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int f = f0 + 8 * (r >> 2) + 4 * h + (r & 3);
-      if (f < g.F) pz[(long)f * (g.K + 1) + k] = acc[jw][r];
-    }
+    for (int r = 0; r < 16; r++) pz[((jb0 + jw) * 16 + r) * 64 + lane] = acc[jw][r];
   }
+}
+
+// Sum of the dw32 partials.  A workgroup takes XL consecutive partial
+// elements (coalesced) x ZL lanes: lane ty adds partials z = ty, ty+ZL, ...
+// in order, lane 0 adds the ZL sums in order, and writes the gradient entry
+// the element holds: block jb, accumulator r, lane l -> filter fb*32 +
+// 8(r/4) + 4(l/32) + r%4, tap jb*32 + l%32; the last 32 of a block -> bias.
+template <int ZL>
+__global__ void __launch_bounds__(NT)
+conv_dw32_reduce_kernel(const float *__restrict__ part, float *__restrict__ dw,
+                        float *__restrict__ db, int Z, int FBLK, int JB, int F, int K) {
+  constexpr int XL = NT / ZL;
+  __shared__ float sums[ZL][XL];
+  const int tx = threadIdx.x % XL, ty = threadIdx.x / XL;
+  const int S = JB * 1024 + 32;
+  const long total = (long)FBLK * S;
+  const long e = (long)blockIdx.x * XL + tx;
+  float sum = 0.0f;
+  if (e < total) {
+    const float *p = part + e;
+#pragma unroll 4
+    for (int z = ty; z < Z; z += ZL) sum += p[(long)z * total];
+  }
+  sums[ty][tx] = sum;
+  __syncthreads();
+  if (ty != 0 || e >= total) return;
+  for (int j = 1; j < ZL; j++) sum += sums[j][tx];
+  const int fb = (int)(e / S), i = (int)(e - (long)fb * S);
+  if (i >= JB * 1024) {
+    const int f = fb * 32 + (i - JB * 1024);
+    if (db && f < F) db[f] = sum;
+    return;
+  }
+  const int jb = i >> 10, r = (i >> 6) & 15, l = i & 63;
+  const int f = fb * 32 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+  const int k = jb * 32 + (l & 31);
+  if (f < F && k < K) dw[(long)f * K + k] = sum;
 }
 
 // dw[f][k] = sum_z part[z][f][k] (k < K), db[f] = sum_z part[z][f][K]; ZL
@@ -799,9 +848,23 @@ inline int rows_spanned(int L, int Wo) { return (L + Wo - 2) / Wo + 1; }
 // 256-float runs of 16-byte loads (LDS_MAX / 4 + 1 when it cannot fit)
 inline long slab_floats(const Geo &g, int L) {
   const long R = (long)(rows_spanned(L, g.Wo) - 1) * g.sh + g.HH;
-  const long f = (long)(g.C + 1) * R * g.W;
+  const long f = (long)(g.C + 1) * (R * g.W + 4);
   if (f > LDS_MAX / 4) return LDS_MAX / 4 + 1;
   return round_up((int)f, 256);
+}
+
+// Kernels that take more than 64 KB of dynamic LDS need the limit raised
+// once per function (the runtime call is slow enough to show up per launch).
+bool allow_big_lds(const void *fn) {
+  static const void *done[32];
+  static int ndone = 0;
+  for (int i = 0; i < ndone; i++)
+    if (done[i] == fn) return true;
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_MAX) !=
+      hipSuccess)
+    return false;
+  if (ndone < 32) done[ndone++] = fn;
+  return true;
 }
 
 int g_dbg = 0;
@@ -847,10 +910,7 @@ template <int PB, bool FLIP, bool VEC>
 int launch_fwd(const float *x, const float *w, const float *bias, float *out, const Geo &g, int N,
                const FwdPlan &pl) {
   auto kern = is_k3(g) ? conv_fwd_k_kernel<PB, FLIP, VEC, 3, 3> : conv_fwd_lds_kernel<PB, FLIP, VEC>;
-  if (pl.lds > 64 * 1024 &&
-      hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)pl.lds) != hipSuccess)
-    return -1;
+  if (pl.lds > 64 * 1024 && !allow_big_lds((const void *)kern)) return -1;
   const dim3 grid((unsigned)(N * pl.chunks), (unsigned)((g.F + 31) / 32));
   hipLaunchKernelGGL(kern, grid, dim3(NT), pl.lds, stream(), x, w, bias, out, g, pl.chunks, g_dbg);
   return hipGetLastError() == hipSuccess ? 0 : -3;
@@ -977,10 +1037,7 @@ int launch_dw(const float *gr, const float *x, float *part, const Geo &g, int N,
   const bool rows = g.Wo % 16 == 0 && pl.ch % g.Wo == 0;
   auto kern = rows ? conv_dw_lds_kernel<MF, JW, KS, VEC, true>
                    : conv_dw_lds_kernel<MF, JW, KS, VEC, false>;
-  if (pl.lds > 64 * 1024 &&
-      hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)pl.lds) != hipSuccess)
-    return -1;
+  if (pl.lds > 64 * 1024 && !allow_big_lds((const void *)kern)) return -1;
   const dim3 grid((unsigned)(N * pl.chunks), (unsigned)((g.F + 16 * pl.fs - 1) / (16 * pl.fs)));
   hipLaunchKernelGGL(kern, grid, dim3(NT), pl.lds, stream(), gr, x, part, g, pl.chunks, pl.ch,
                      pl.fs, g_dbg);
@@ -991,10 +1048,7 @@ template <int JW, int KS, bool VEC>
 int launch_dw32(const float *gr, const float *x, float *part, const Geo &g, int N,
                 const DwPlan &pl) {
   auto kern = conv_dw32_kernel<JW, KS, VEC>;
-  if (pl.lds > 64 * 1024 &&
-      hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)pl.lds) != hipSuccess)
-    return -1;
+  if (pl.lds > 64 * 1024 && !allow_big_lds((const void *)kern)) return -1;
   const dim3 grid((unsigned)(N * pl.chunks), (unsigned)((g.F + 31) / 32));
   hipLaunchKernelGGL(kern, grid, dim3(NT), pl.lds, stream(), gr, x, part, g, pl.chunks, pl.ch,
                      g_dbg);
@@ -1063,7 +1117,9 @@ extern "C" int tt_k_conv2d_dw_lds(const float *gr, const float *x, float *dw, fl
   const DwPlan pl = plan_dw(g, N);
   if (pl.var < 0) return -1;
   const long Z = (long)N * pl.chunks;
-  const long total = (long)F * (g.K + 1);
+  const bool d32 = pl.var >= 10;
+  const int FBLK = (F + 31) / 32, JB32 = (g.K + 31) / 32;
+  const long total = d32 ? (long)FBLK * (JB32 * 1024 + 32) : (long)F * (g.K + 1);
   if (Z * total >= 0x7fffffffL) return -1;
   float *part = (float *)ttrt_alloc(sizeof(float) * (size_t)(Z * total));
   if (!part) return -2;
@@ -1077,9 +1133,14 @@ extern "C" int tt_k_conv2d_dw_lds(const float *gr, const float *x, float *dw, fl
     int zl = 1;
     while (zl < 32 && zl < Z && total * zl * 2 <= 2048L * NT) zl *= 2;
 #define TT_RED(ZL_)                                                                       \
-  hipLaunchKernelGGL(conv_dw_reduce_kernel<ZL_>,                                          \
-                     dim3((unsigned)((total + NT / ZL_ - 1) / (NT / ZL_))), dim3(NT), 0,  \
-                     stream(), part, dw, db, (int)Z, F, g.K)
+  if (d32)                                                                                \
+    hipLaunchKernelGGL(conv_dw32_reduce_kernel<ZL_>,                                      \
+                       dim3((unsigned)((total + NT / ZL_ - 1) / (NT / ZL_))), dim3(NT), 0, \
+                       stream(), part, dw, db, (int)Z, FBLK, JB32, F, g.K);               \
+  else                                                                                    \
+    hipLaunchKernelGGL(conv_dw_reduce_kernel<ZL_>,                                        \
+                       dim3((unsigned)((total + NT / ZL_ - 1) / (NT / ZL_))), dim3(NT), 0, \
+                       stream(), part, dw, db, (int)Z, F, g.K)
     switch (zl) {
       case 1: TT_RED(1); break;
       case 2: TT_RED(2); break;
