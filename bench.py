@@ -15,7 +15,10 @@ of the fp32 MFMA peak, plus the CNN forward+backward step time.
     backward + an SGD update of every weight, inputs and weights resident,
     graph rebuilt every step through the C ABI (ctypes), wall clock per step.
   * extra.*: the other BASELINE configs (1024^3, 4096^3 NT/TN backward GEMMs,
-    8192^3, ragged, tall-skinny, MLP step).
+    8192^3, ragged, tall-skinny, MLP step); extra.conv_kernels: the direct
+    convolution kernels of the CNN step alone (TFLOP/s vs the MFMA peak);
+    extra.hbm_kernels: the bandwidth kernels (im2col/col2im serve only the
+    convolutions whose input slab does not fit LDS).
   * cpu_baseline: the reference's own AVX2+FMA OpenMP sgemm, compiled from
     its sources into oracle/_ref (or the oracle restatement when that build
     is missing), on this host's cores, on a bounded sample (median of 3 runs
@@ -309,6 +312,49 @@ def bandwidth_kernels(L, reps=50):
     return out
 
 
+def conv_kernels(L, reps=50):
+    """The direct (LDS-staged) convolution kernels of the CNN step at config-4
+    shapes, each timed with HIP events over `reps` calls (a call of dW includes
+    its partial reduction).  Algorithmic work: 2*F*C*HH*WW*N*Ho*Wo flops; bytes:
+    every input element read once + every output element written once."""
+    from tinytorch_amd.hip import DevBuf, StreamTimer, check, sync
+    rng = np.random.default_rng(9)
+    B = 128
+    out = {}
+    for tag, (C, H, F) in (("conv1", (3, 32, 32)), ("conv2", (32, 16, 64))):
+        x = DevBuf.from_np(rng.uniform(0, 1, B * C * H * H).astype(np.float32))
+        w = DevBuf.from_np(rng.uniform(-1, 1, F * C * 9).astype(np.float32))
+        b = DevBuf.from_np(np.zeros(F, np.float32))
+        g = DevBuf.from_np(rng.standard_normal(B * F * H * H).astype(np.float32))
+        y, dx, dw, db = DevBuf(B * F * H * H), DevBuf(B * C * H * H), DevBuf(F * C * 9), DevBuf(F)
+        geo = (B, C, H, H, F, 3, 3, 1, 1, 1, 1, H, H)
+        flops = 2.0 * F * C * 9 * B * H * H
+        nx, ny, nw = B * C * H * H, B * F * H * H, F * C * 9
+        ops = {f"fwd_{tag}": (lambda: L.tt_k_conv2d_fwd_lds(x.ptr, w.ptr, b.ptr, y.ptr, *geo),
+                              4 * (nx + nw + F + ny)),
+               f"dw_db_{tag}": (lambda: L.tt_k_conv2d_dw_lds(g.ptr, x.ptr, dw.ptr, db.ptr, *geo),
+                                4 * (ny + nx + nw + F))}
+        if tag == "conv2":  # conv1's input is the image: no dX in the training step
+            ops[f"dx_{tag}"] = (lambda: L.tt_k_conv2d_dx_lds(g.ptr, w.ptr, dx.ptr, *geo),
+                                4 * (ny + nw + nx))
+        for name, (fn, nbytes) in ops.items():
+            check(fn(), name)
+            prewarm(fn, 0.05)
+            tm = StreamTimer()
+            tm.start()
+            for _ in range(reps):
+                fn()
+            ms = tm.stop_ms() / reps
+            tf = flops / (ms * 1e-3) / 1e12
+            out[name] = dict(us=round(ms * 1e3, 2), gflop=round(flops / 1e9, 3),
+                             tflops=round(tf, 1), frac_of_mfma_peak=round(tf / PEAK_FP32_MFMA_TFLOPS, 3),
+                             bytes=int(nbytes), gb_s=round(nbytes / (ms * 1e-3) / 1e9, 1))
+        for bb in (x, w, b, g, y, dx, dw, db):
+            bb.free()
+    sync()
+    return out
+
+
 def cpu_threads():
     n = os.environ.get("OMP_NUM_THREADS")
     try:
@@ -417,6 +463,9 @@ def main():
         mlp = MlpStep(L)
         extra["mlp_step_ms"] = round(time_steps(mlp, 50, 5), 3)
         log("mlp step ms", extra["mlp_step_ms"])
+        extra["conv_kernels"] = conv_kernels(L)
+        for k, v in extra["conv_kernels"].items():
+            log(f"{k:22s} {v['us']:8.2f} us {v['tflops']:6.1f} TFLOP/s ({100 * v['frac_of_mfma_peak']:.1f}% of fp32 MFMA)")
         extra["hbm_kernels"] = bandwidth_kernels(L)
         for k, v in extra["hbm_kernels"].items():
             log(f"{k:22s} {v['us']:8.2f} us {v['gb_s']:8.1f} GB/s ({100 * v['frac_of_hbm_peak']:.1f}% of 8 TB/s)")

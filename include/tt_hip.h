@@ -173,10 +173,6 @@ int tt_k_conv2d_dx_implicit(const float *g, const float *w, float *dx,
  *   dw:  dw (F, C*HH*WW), db (F, optional)         src/autograd.c:456-513
  *   dx:  dx (N,C,H,W)                              src/autograd.c:515-539,406-434 */
 int tth_conv_lds(int on);
-/* Profiling aid for the LDS-staged kernels: bit 0 skips staging the
- * activations, bit 1 the weights / output gradient, bit 2 the MFMA loop,
- * bit 3 the result stores (results are then wrong).  0 = normal. */
-int tth_conv_dbg(int mask);
 int tt_k_conv2d_lds_plan(int N, int C, int H, int W, int F, int HH, int WW,
                          int sh, int sw, int ph, int pw, int Ho, int Wo);
 int tt_k_conv2d_fwd_lds(const float *x, const float *w, const float *bias, float *out,

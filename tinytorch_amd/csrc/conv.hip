@@ -207,8 +207,7 @@ __device__ __forceinline__ void stage_weights(float *ws, const float *__restrict
 template <int PB, bool FLIP, bool VEC>
 __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2)))
 conv_fwd_lds_kernel(const float *__restrict__ x, const float *__restrict__ w,
-                    const float *__restrict__ bias, float *__restrict__ out, Geo g, int chunks,
-                    int dbg) {
+                    const float *__restrict__ bias, float *__restrict__ out, Geo g, int chunks) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   constexpr int CHUNK = 128 * PB;
   const int n = blockIdx.x / chunks, chunk = blockIdx.x - n * chunks;
@@ -229,8 +228,8 @@ conv_fwd_lds_kernel(const float *__restrict__ x, const float *__restrict__ w,
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
-  if (!(dbg & 1)) stage_slab<VEC>(xs, x, g, s, n);
-  if (!(dbg & 2)) stage_weights<FLIP, VEC>(ws, w, g, f0, Kp);
+  stage_slab<VEC>(xs, x, g, s, n);
+  stage_weights<FLIP, VEC>(ws, w, g, f0, Kp);
   for (int k = tid; k < Kp; k += NT) tab[k] = tap_entry(g, s, k);
   if (tid < 32) bs[tid] = (bias && f0 + tid < g.F) ? bias[f0 + tid] : 0.0f;
   dma_wait();
@@ -256,7 +255,7 @@ conv_fwd_lds_kernel(const float *__restrict__ x, const float *__restrict__ w,
   constexpr int U = 4;
   const float *wa = FLIP ? ws + l32 * taps : ws + l32 * KST + half * Kh;
   const int4 *tb = tab + half * Kh;
-  const int groups = (dbg & 4) ? 0 : Kh / U;
+  const int groups = Kh / U;
   float a_c[U], b_c[U][PB];
   int4 t_c[U], t_n[U];
 #pragma unroll
@@ -316,7 +315,7 @@ conv_fwd_lds_kernel(const float *__restrict__ x, const float *__restrict__ w,
 #pragma unroll
   for (int j = 0; j < PB; j++) {
     const int p = p0 + (wave * PB + j) * 32 + l32;
-    if (p >= p1 || (dbg & 8)) continue;
+    if (p >= p1) continue;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       const int f = f0 + 8 * (r >> 2) + 4 * half + (r & 3);
@@ -338,8 +337,7 @@ conv_fwd_lds_kernel(const float *__restrict__ x, const float *__restrict__ w,
 template <int PB, bool FLIP, bool VEC, int KH, int KW>
 __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2)))
 conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
-                  const float *__restrict__ bias, float *__restrict__ out, Geo g, int chunks,
-                  int dbg) {
+                  const float *__restrict__ bias, float *__restrict__ out, Geo g, int chunks) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   constexpr int CHUNK = 128 * PB, TAPS = KH * KW;
   const int n = blockIdx.x / chunks, chunk = blockIdx.x - n * chunks;
@@ -359,8 +357,8 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
-  if (!(dbg & 1)) stage_slab<VEC>(xs, x, g, s, n);
-  if (!(dbg & 2)) {
+  stage_slab<VEC>(xs, x, g, s, n);
+  {
     if constexpr (FLIP)
       stage_blocks<VEC>(ws, w + (long)f0 * TAPS, 2 * CH2 * 32 * TAPS, 32 * TAPS, g.C,
                         (long)g.F * TAPS, 0, nf * TAPS);
@@ -392,7 +390,7 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
   const float *wa = FLIP ? ws + l32 * TAPS + half * CH2 * 32 * TAPS
                          : ws + l32 * KST + half * CH2 * TAPS;
   constexpr int WSTEP_FLIP = 32 * TAPS;
-  const int steps = (dbg & 4) ? 0 : CH2;
+  const int steps = CH2;
   // operands of channel c+1 are read before the MFMAs of channel c
   auto load = [&](int c, float (&a)[TAPS], float (&b)[TAPS][PB]) {
     const float *wc = wa + c * (FLIP ? WSTEP_FLIP : TAPS);
@@ -437,7 +435,7 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
 #pragma unroll
   for (int j = 0; j < PB; j++) {
     const int p = p0 + (wave * PB + j) * 32 + l32;
-    if (p >= p1 || (dbg & 8)) continue;
+    if (p >= p1) continue;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       const int f = f0 + 8 * (r >> 2) + 4 * half + (r & 3);
@@ -456,7 +454,7 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
 template <int MF, int JW, int KS, bool VEC, bool ROWS>
 __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2)))
 conv_dw_lds_kernel(const float *__restrict__ gr, const float *__restrict__ x,
-                   float *__restrict__ part, Geo g, int chunks, int CH, int FS, int dbg) {
+                   float *__restrict__ part, Geo g, int chunks, int CH, int FS) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   const int n = blockIdx.x / chunks, chunk = blockIdx.x - n * chunks;
   const int P = g.Ho * g.Wo;
@@ -479,8 +477,8 @@ conv_dw_lds_kernel(const float *__restrict__ gr, const float *__restrict__ x,
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
   const float *gn = gr + (long)n * g.F * P + (long)f0 * P + p0;
   const int nf = g.F - f0 < FB ? g.F - f0 : FB;
-  if (!(dbg & 2)) stage_blocks<VEC>(gs, gn, FB * GS, GS, nf, P, 0, np);
-  if (!(dbg & 1)) stage_slab<VEC>(xs, x, g, s, n);
+  stage_blocks<VEC>(gs, gn, FB * GS, GS, nf, P, 0, np);
+  stage_slab<VEC>(xs, x, g, s, n);
   for (int q = tid; q < npp; q += NT)
     pixt[q] = q < np ? pixel_entry(g, s, p0 + q) : make_int2(0, -(1 << 20));  // masked
   for (int k = tid; k < JB16; k += NT) ktab[k] = tap_entry(g, s, k);
@@ -517,7 +515,7 @@ conv_dw_lds_kernel(const float *__restrict__ gr, const float *__restrict__ x,
 #pragma unroll
     for (int jw = 0; jw < JW; jw++) acc[m][jw] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  const bool active = jb0 < JB && !(dbg & 4);   // wave-uniform
+  const bool active = jb0 < JB;   // wave-uniform
   if constexpr (ROWS) {
     // Whole output rows (Wo a multiple of 16, chunk = whole rows): wave ks
     // takes rows ks, ks+KS, ...; a row is walked in 16-pixel segments of 4
@@ -607,7 +605,7 @@ conv_dw_lds_kernel(const float *__restrict__ gr, const float *__restrict__ x,
             acc[m][jw][r] +=
                 red[(((grp * (KS - 1) + o - 1) * PER) + (m * JW + jw) * 4 + r) * 64 + lane];
   }
-  if (jb0 >= JB || (dbg & 8)) return;
+  if (jb0 >= JB) return;
 
   float *pz = part + (long)blockIdx.x * g.F * (g.K + 1);
 #pragma unroll
@@ -637,7 +635,7 @@ conv_dw_lds_kernel(const float *__restrict__ gr, const float *__restrict__ x,
 template <int JW, int KS, bool VEC>
 __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2)))
 conv_dw32_kernel(const float *__restrict__ gr, const float *__restrict__ x,
-                 float *__restrict__ part, Geo g, int chunks, int CH, int dbg) {
+                 float *__restrict__ part, Geo g, int chunks, int CH) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   constexpr int FB = 32;
   const int n = blockIdx.x / chunks, chunk = blockIdx.x - n * chunks;
@@ -658,8 +656,8 @@ conv_dw32_kernel(const float *__restrict__ gr, const float *__restrict__ x,
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
   const float *gn = gr + (long)n * g.F * P + (long)f0 * P + p0;
   const int nf = g.F - f0 < FB ? g.F - f0 : FB;
-  if (!(dbg & 2)) stage_blocks<VEC>(gs, gn, FB * GS, GS, nf, P, 0, np);
-  if (!(dbg & 1)) stage_slab<VEC>(xs, x, g, s, n);
+  stage_blocks<VEC>(gs, gn, FB * GS, GS, nf, P, 0, np);
+  stage_slab<VEC>(xs, x, g, s, n);
   for (int k = tid; k < 32 * JB; k += NT) ktab[k] = tap_entry(g, s, k);
   dma_wait();
   __syncthreads();
@@ -692,7 +690,7 @@ conv_dw32_kernel(const float *__restrict__ gr, const float *__restrict__ x,
   for (int jw = 0; jw < JW; jw++)
     for (int r = 0; r < 16; r++) acc[jw][r] = 0.0f;
 
-  if (jb0 < JB && !(dbg & 4)) {
+  if (jb0 < JB) {
     // this wave's steps: rows ks, ks+KS, ... of the chunk, Wo/2 steps a row;
     // the operands of step t+1 are read before the MFMAs of step t
     const int rows = np / g.Wo;
@@ -754,7 +752,7 @@ conv_dw32_kernel(const float *__restrict__ gr, const float *__restrict__ x,
         for (int r = 0; r < 16; r++)
           acc[jw][r] += red[((grp * (KS - 1) + o - 1) * PER + jw * 16 + r) * 64 + lane];
   }
-  if (jb0 >= JB || (dbg & 8)) return;
+  if (jb0 >= JB) return;
 #pragma unroll
   for (int jw = 0; jw < JW; jw++) {
     if (jb0 + jw >= JB) break;
@@ -867,8 +865,6 @@ bool allow_big_lds(const void *fn) {
   return true;
 }
 
-int g_dbg = 0;
-
 struct FwdPlan {
   int pb = 0, chunks = 0;
   size_t lds = 0;
@@ -912,7 +908,7 @@ int launch_fwd(const float *x, const float *w, const float *bias, float *out, co
   auto kern = is_k3(g) ? conv_fwd_k_kernel<PB, FLIP, VEC, 3, 3> : conv_fwd_lds_kernel<PB, FLIP, VEC>;
   if (pl.lds > 64 * 1024 && !allow_big_lds((const void *)kern)) return -1;
   const dim3 grid((unsigned)(N * pl.chunks), (unsigned)((g.F + 31) / 32));
-  hipLaunchKernelGGL(kern, grid, dim3(NT), pl.lds, stream(), x, w, bias, out, g, pl.chunks, g_dbg);
+  hipLaunchKernelGGL(kern, grid, dim3(NT), pl.lds, stream(), x, w, bias, out, g, pl.chunks);
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
@@ -1040,7 +1036,7 @@ int launch_dw(const float *gr, const float *x, float *part, const Geo &g, int N,
   if (pl.lds > 64 * 1024 && !allow_big_lds((const void *)kern)) return -1;
   const dim3 grid((unsigned)(N * pl.chunks), (unsigned)((g.F + 16 * pl.fs - 1) / (16 * pl.fs)));
   hipLaunchKernelGGL(kern, grid, dim3(NT), pl.lds, stream(), gr, x, part, g, pl.chunks, pl.ch,
-                     pl.fs, g_dbg);
+                     pl.fs);
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
@@ -1050,8 +1046,7 @@ int launch_dw32(const float *gr, const float *x, float *part, const Geo &g, int 
   auto kern = conv_dw32_kernel<JW, KS, VEC>;
   if (pl.lds > 64 * 1024 && !allow_big_lds((const void *)kern)) return -1;
   const dim3 grid((unsigned)(N * pl.chunks), (unsigned)((g.F + 31) / 32));
-  hipLaunchKernelGGL(kern, grid, dim3(NT), pl.lds, stream(), gr, x, part, g, pl.chunks, pl.ch,
-                     g_dbg);
+  hipLaunchKernelGGL(kern, grid, dim3(NT), pl.lds, stream(), gr, x, part, g, pl.chunks, pl.ch);
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
@@ -1073,8 +1068,6 @@ int launch_dw_var(const float *gr, const float *x, float *part, const Geo &g, in
 int g_lds_conv = 1;  // tth_conv_lds
 
 }  // namespace
-
-extern "C" int tth_conv_dbg(int v) { g_dbg = v; return 0; }
 
 extern "C" int tth_conv_lds(int on) {
   const int prev = g_lds_conv;
