@@ -672,9 +672,14 @@ struct DirectOperand {
     }
   }
   __device__ __forceinline__ void issue(int kt, float *lds, int wave) const {
+    issue_part<0, 8>(kt, lds, wave);
+  }
+  // loads J0 .. J0+NJ-1 of the 8
+  template <int J0, int NJ>
+  __device__ __forceinline__ void issue_part(int kt, float *lds, int wave) const {
     const long k = (long)kt * D_BK;
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
+    for (int j = J0; j < J0 + NJ; j++) {
       if constexpr (KC) g2lds16(src[j] + k, lds + (wave * 64 + 8 * j) * D_KC_LD);
       else g2lds16(src[0] + (k + j) * ld, lds + (wave * 8 + j) * D_NC_LD);
     }
@@ -750,42 +755,63 @@ gemm_direct_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
-  // the fragments of step kk+8 are read while the MFMAs of step kk run
-  auto compute = [&](int buf) {
+  // The fragments of step kk+8 are read while the MFMAs of step kk run.
+  // mid(c), c = 0..3, runs after the c-th group of 16 MFMAs of the tile's
+  // first step: the next tile's loads go out a quarter at a time, each chunk
+  // in the shadow of queued MFMAs, instead of as one block the matrix pipe
+  // waits through.  After the third step the wave waits for those loads and
+  // meets the others at the barrier (the next tile is then complete in LDS
+  // and this tile's last fragments are already in registers), so the last
+  // step's MFMAs cover the reads of the next tile's first fragments.
+  float a[2][4][4], b[2][4][4];
+  auto compute = [&](int buf, bool more, auto mid) {
     const float *sA = smem + buf * STAGE;
     const float *sB = sA + A_SZ;
-    float a[2][4][4], b[2][4][4];
-    DirectOperand<A_KC>::frag(sA, wm, 0, l32, g, a[0]);
-    DirectOperand<!B_NC>::frag(sB, wn, 0, l32, g, b[0]);
+    const float *nA = smem + (buf ^ 1) * STAGE;
+    const float *nB = nA + A_SZ;
 #pragma unroll
     for (int q = 0; q < D_BK / 8; q++) {
-      if (q + 1 < D_BK / 8) {
+      const bool last = q + 1 == D_BK / 8;
+      if (!last) {
         DirectOperand<A_KC>::frag(sA, wm, 8 * (q + 1), l32, g, a[(q + 1) & 1]);
         DirectOperand<!B_NC>::frag(sB, wn, 8 * (q + 1), l32, g, b[(q + 1) & 1]);
+      } else if (more) {
+        DirectOperand<A_KC>::frag(nA, wm, 0, l32, g, a[0]);
+        DirectOperand<!B_NC>::frag(nB, wn, 0, l32, g, b[0]);
       }
 #pragma unroll
-      for (int s = 0; s < 4; s++)
+      for (int s = 0; s < 4; s++) {
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
           for (int j = 0; j < 4; j++)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[q & 1][i][s], b[q & 1][j][s],
                                                              acc[i][j], 0, 0, 0);
-    }
-    // Schedule (the compiler otherwise sinks each fragment read to just
-    // before its first MFMA and waits on it): the first step's 8 reads, then
-    // per step the next step's 8 reads spread over the first 16 MFMAs.
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // DS reads
+        // Schedule (the compiler otherwise sinks each fragment read to just
+        // before its first MFMA and waits on it): the step's first group
+        // carries the 8 reads for the following step, one per 2 MFMAs.
+        if (s == 0) {
 #pragma unroll
-    for (int q = 0; q + 1 < D_BK / 8; q++) {
-#pragma unroll
-      for (int r = 0; r < 8; r++) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+          for (int r = 0; r < 8; r++) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+          }
+        } else {
+          __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+        }
+        if (q == 0) {
+          __builtin_amdgcn_sched_barrier(0);
+          mid(s);
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
-      __builtin_amdgcn_sched_group_barrier(0x008, 48, 0);
+      if (q + 2 == D_BK / 8) {
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vm_all();
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 64, 0);
   };
 
   if (nk > 0) {
@@ -793,15 +819,18 @@ gemm_direct_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
     opb.issue(0, smem + A_SZ, wave);
     wait_vm_all();
     __syncthreads();
+    DirectOperand<A_KC>::frag(smem, wm, 0, l32, g, a[0]);
+    DirectOperand<!B_NC>::frag(smem + A_SZ, wn, 0, l32, g, b[0]);
     for (int kt = 0; kt < nk; kt++) {
-      if (kt + 1 < nk) {
-        float *nb = smem + ((kt + 1) & 1) * STAGE;
-        opa.issue(kt + 1, nb, wave);
-        opb.issue(kt + 1, nb + A_SZ, wave);
-      }
-      compute(kt & 1);
-      wait_vm_all();
-      __syncthreads();
+      float *nb = smem + ((kt + 1) & 1) * STAGE;
+      const bool more = kt + 1 < nk;
+      compute(kt & 1, more, [&](int c) {
+        if (!more) return;
+        if (c == 0) opa.template issue_part<0, 4>(kt + 1, nb, wave);
+        else if (c == 1) opa.template issue_part<4, 4>(kt + 1, nb, wave);
+        else if (c == 2) opb.template issue_part<0, 4>(kt + 1, nb + A_SZ, wave);
+        else opb.template issue_part<4, 4>(kt + 1, nb + A_SZ, wave);
+      });
     }
   }
 
