@@ -718,7 +718,7 @@ gemm_direct_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
   __shared__ __attribute__((aligned(16))) float smem[2 * STAGE];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: LDS addresses in SGPRs
   const int l32 = lane & 31;
   const int g = lane >> 5;
 
