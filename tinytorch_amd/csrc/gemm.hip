@@ -216,7 +216,7 @@ __device__ __forceinline__ void gemm_body(float *smem, int M, int N, int K, cons
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
   const int l32 = lane & 31;
   const int g = lane >> 5;
 
@@ -845,12 +845,14 @@ gemm_direct_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
       const int rho = 8 * (r >> 2) + 4 * g + (r & 3);
       const long row = m0 + (A_KC ? wm + 32 * i + rho : wm + 4 * rho + i);
       float *crow = C + row * ldc + n0 + wn;
+      // streaming stores: C is not read again by this kernel
       if constexpr (B_NC) {
-        *reinterpret_cast<float4 *>(crow + 4 * l32) =
-            make_float4(acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]);
+        typedef float f32x4v __attribute__((ext_vector_type(4)));
+        const f32x4v v = {acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]};
+        __builtin_nontemporal_store(v, reinterpret_cast<f32x4v *>(crow + 4 * l32));
       } else {
 #pragma unroll
-        for (int j = 0; j < 4; j++) crow[32 * j + l32] = acc[i][j][r];
+        for (int j = 0; j < 4; j++) __builtin_nontemporal_store(acc[i][j][r], crow + 32 * j + l32);
       }
     }
 }
