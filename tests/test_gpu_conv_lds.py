@@ -156,3 +156,57 @@ def test_autograd_conv_lds_on_off(tlib, case, lds):
             n.release()
     finally:
         tlib.tth_conv_lds(prev)
+
+
+def _random_cases(n=40, seed=777):
+    """Seeded random shapes spread over the kernel variants: 3x3 and other
+    kernels, strides 1-3, paddings 0..k-1, odd/even widths (16-byte and 4-byte
+    staging), channel counts from 1 to 48 (dW tap-block variants up to
+    K = 432), filter counts across block boundaries."""
+    r = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        HH = int(r.choice([1, 2, 3, 3, 3, 5]))
+        WW = HH if r.random() < 0.8 else int(r.choice([1, 2, 3]))
+        sh, sw = int(r.integers(1, 4)), int(r.integers(1, 3))
+        ph, pw = int(r.integers(0, HH)), int(r.integers(0, WW))
+        H, W = int(r.integers(max(HH, 3), 24)), int(r.integers(max(WW, 3), 24))
+        C, F, N = int(r.integers(1, 49)), int(r.integers(1, 70)), int(r.integers(1, 5))
+        Ho = (H + 2 * ph - HH) // sh + 1
+        Wo = (W + 2 * pw - WW) // sw + 1
+        if Ho <= 0 or Wo <= 0:
+            continue
+        out.append((N, C, H, W, F, HH, WW, sh, sw, ph, pw))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_cases())
+def test_lds_conv_random_shapes(tlib, case):
+    """Every entry the plan reports as covered, against the oracle."""
+    x, w, b, g, geo = _inputs(case)
+    N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo = geo
+    print("lds conv random", case, flush=True)
+    bits = tlib.tt_k_conv2d_lds_plan(*geo)
+    dx_, dw_, db_, dg_ = DevBuf.from_np(x), DevBuf.from_np(w), DevBuf.from_np(b), DevBuf.from_np(g)
+    gmax = float(np.abs(g).max())
+    if bits & 1:
+        out = DevBuf(N * F * Ho * Wo)
+        check(tlib.tt_k_conv2d_fwd_lds(dx_.ptr, dw_.ptr, db_.ptr, out.ptr, *geo), "fwd")
+        ref = orc.conv2d_fwd(x, w, b, sh, sw, ph, pw)
+        bb = b[None, :, None, None]
+        assert err(out.to_np(ref.shape) - bb, ref - bb, C * HH * WW, 1.0, 1.0) <= TOL
+        out.free()
+    rdx, rdw, rdb = orc.conv2d_bwd(x, w, g, sh, sw, ph, pw)
+    if bits & 2:
+        dW, dB = DevBuf(w.size), DevBuf(F)
+        check(tlib.tt_k_conv2d_dw_lds(dg_.ptr, dx_.ptr, dW.ptr, dB.ptr, *geo), "dw")
+        assert err(dW.to_np(w.shape), rdw, N * Ho * Wo, gmax, 1.0) <= TOL
+        assert err(dB.to_np((F,)), rdb, N * Ho * Wo, gmax, 1.0) <= TOL
+        dW.free(); dB.free()
+    if bits & 4:
+        dX = DevBuf(x.size)
+        check(tlib.tt_k_conv2d_dx_lds(dg_.ptr, dw_.ptr, dX.ptr, *geo), "dx")
+        assert err(dX.to_np(x.shape), rdx, F * HH * WW, gmax, 1.0) <= TOL
+        dX.free()
+    for bf in (dx_, dw_, db_, dg_):
+        bf.free()
