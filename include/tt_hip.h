@@ -62,6 +62,10 @@ int tth_gemm_config(int tile, int splits);
 /* Tuning hook: 0 disables, 1 (default) enables the direct-to-LDS kernel used
  * for plain GEMMs (any transposition) on whole 256x256 tiles. */
 int tth_gemm_direct(int on);
+/* Tuning hook: 0 disables, 1 (default) enables the 64x64 direct-load kernel
+ * used for plain GEMMs too small for 128x128 tiles on every CU (and for
+ * ragged or unaligned operands); a forced tile (tth_gemm_config) bypasses it. */
+int tth_gemm_mid(int on);
 
 /* Convolution GEMMs over the im2col matrix col[(c,kh,kw)][(n,ho,wo)]
  * (Kc = C*HH*WW rows, Ncol = N*Ho*Wo columns, HW = Ho*Wo):

@@ -436,3 +436,32 @@ def test_gemm_direct_lds_kernel(tlib, M, N, K, splits, ta, tb):
     norm, rel = gemm_err(C, ref, K, np.abs(A).max(), np.abs(B).max())
     assert norm <= GEMM_TOL and rel <= GEMM_TOL, (norm, rel)
     assert bits_equal(C, C_staged)
+
+
+# Shapes for the 64x64 direct-load kernel (16-byte aligned rows, K and the
+# m/n-contiguous extents multiples of 4): edge tiles in M and N, K tails
+# inside a 64-k tile, split-K (few tiles, long K), the 8-wave variant (at
+# most one workgroup per CU) and the 4-wave one (more tiles than CUs).
+MID_SHAPES = [(4, 4, 4), (100, 68, 36), (130, 196, 260), (60, 4, 1028), (64, 64, 64),
+              (1024, 1024, 1024), (200, 64, 4100), (2052, 1024, 132), (68, 2000, 516)]
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+@pytest.mark.parametrize("M,N,K", MID_SHAPES)
+def test_gemm_mid_kernel(tlib, M, N, K, ta, tb):
+    A = u(K, M) if ta else u(M, K)
+    B = u(N, K) if tb else u(K, N)
+    Am = A.T if ta else A
+    Bm = B.T if tb else B
+    ref = Am.astype(np.float64) @ Bm.astype(np.float64)
+    C = run_gemm(tlib, M, N, K, ta, tb, A, B)
+    norm, rel = gemm_err(C, ref, K, 1.0, 1.0)
+    assert norm <= GEMM_TOL and rel <= GEMM_TOL, (norm, rel)
+    # the other kernels agree to the same bar
+    check(tlib.tth_gemm_mid(0), "mid off")
+    try:
+        C2 = run_gemm(tlib, M, N, K, ta, tb, A, B)
+    finally:
+        check(tlib.tth_gemm_mid(1), "mid on")
+    norm2, _ = gemm_err(C, C2, K, 1.0, 1.0)
+    assert norm2 <= GEMM_TOL, norm2

@@ -142,6 +142,7 @@ SIGNATURES = [
     ("tt_k_sgd_multi", _I, [ctypes.POINTER(VP), ctypes.POINTER(VP), ctypes.POINTER(_L), _I, _F]),
     ("tth_conv_config", _I, [_L]),
     ("tth_gemm_direct", _I, [_I]),
+    ("tth_gemm_mid", _I, [_I]),
     ("tt_k_conv2d_fwd_implicit", _I, [VP, VP, VP, VP] + [_I] * 13),
     ("tt_k_conv2d_dw_implicit", _I, [VP, VP, VP, VP] + [_I] * 13),
     ("tt_k_conv2d_dx_implicit", _I, [VP, VP, VP] + [_I] * 13),

@@ -857,6 +857,316 @@ gemm_direct_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
     }
 }
 
+// ---- 64x64 tile with direct loads, a deep LDS pipeline and in-workgroup split-K ----
+// For GEMMs too small to give every CU a 256x256 tile (1024^3 has 16 of
+// them).  A 64x64 tile per CU needs four times the loads per MFMA of the
+// 256x256 tile, so the kernel keeps several K tiles of loads in flight
+// (global->LDS DMA, no staging registers) and splits each K tile over its NW
+// waves: wave w multiplies the whole 64x64 tile over its BK/NW k of the tile
+// with four independent 32x32 accumulators, and the NW wave sums are added in
+// LDS at the end in wave order (deterministic).  With NW = 8 two waves share
+// each SIMD, so one wave's MFMAs run while the other issues its loads.
+// Operands are 16-byte aligned with leading dimensions and contiguous extents
+// multiples of 4; any M, N, K otherwise.
+// LDS layouts (per stage):
+//   k-contiguous operand: 64 rows of BK k, 16-byte chunk c of row R in slot
+//     c ^ swz(R) (the b128 fragment reads of 32 rows at one chunk spread
+//     over all banks);
+//   m/n-contiguous operand: BK rows k of 64 floats; fragments are read as
+//     float2, so block x of a wave holds m/n = 2*l32 + x (interleaved).
+constexpr int M_T = 64;
+constexpr int M_RLD = M_T + 4;  // row stride of the wave-sum area
+
+__device__ __attribute__((aligned(16))) float g_gemm_zero[4];
+
+// DMA with a wave-uniform base address in SGPRs and a per-lane 32-bit byte
+// offset: the K loop advances only the scalar base, so issuing a tile's
+// loads takes no vector instructions (vector ALU work between MFMAs stalls
+// the matrix pipe).
+__device__ __forceinline__ void g2lds16s(const float *sbase, unsigned voff, const float *lds) {
+  const unsigned addr = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(addr), "v"(voff), "s"(sbase)
+               : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N) for a compile-time N (capped at the counter's 63)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  constexpr int n = N > 63 ? 63 : N;
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
+}
+
+// One operand's loads (16 bytes per lane; a load fills 256 floats of LDS).
+// KC: rows r0+R of a row-major (rows x K) matrix, BK k per tile.  NC: rows k
+// of a row-major (K x cols) matrix, columns r0 .. r0+63.  lim = rows (KC) or
+// cols (NC).  Rows / columns past lim load row / columns lim-1 / lim-4
+// instead (they only feed outputs that are not stored), so a tile's loads
+// need no range test; only k past the end of the K range (the last tile)
+// must read zeros.  Each lane keeps the byte offset of its element in every
+// load relative to the tile origin (row r0 at k0 for KC, row k0 at column r0
+// for NC); the host keeps these below 2^32 (64 rows of the leading
+// dimension).
+template <bool KC, int BK, int NW>
+struct MidOperand {
+  static constexpr int CPR = BK / 4;       // 16-byte chunks per KC row
+  static constexpr int NL = BK / (4 * NW); // loads per wave per tile
+  static_assert(NL >= 1, "tile too shallow for the waves");
+  __device__ __forceinline__ static int swz(int R) { return BK == 32 ? (R >> 1) & 7 : R & 15; }
+  unsigned voff[NL];
+  const float *p;
+  long ld, r0;
+  int wave, lane;
+  __device__ __forceinline__ void init(const float *p_, long ld_, long r0_, int lim, int wave_,
+                                       int lane_) {
+    p = p_;
+    ld = ld_;
+    r0 = r0_;
+    wave = wave_;
+    lane = lane_;
+#pragma unroll
+    for (int j = 0; j < NL; j++) {
+      long e;  // element offset from the tile origin
+      if constexpr (KC) {
+        const int R = (wave * NL + j) * (256 / BK) + lane / CPR;
+        e = (min(r0 + R, (long)lim - 1) - r0) * ld + koff(j);
+      } else {
+        e = (long)koff(j) * ld + (min(r0 + 4 * (lane & 15), (long)lim - 4) - r0);
+      }
+      voff[j] = (unsigned)(e * 4);
+    }
+  }
+  // k of load j's lane relative to the tile's first k
+  __device__ __forceinline__ int koff(int j) const {
+    const int q = wave * NL + j;
+    if constexpr (KC) {
+      const int R = q * (256 / BK) + lane / CPR;
+      return 4 * ((lane % CPR) ^ swz(R));
+    } else {
+      return 4 * q + (lane >> 4);
+    }
+  }
+  // LDS float offset of load j's first lane
+  __device__ __forceinline__ int dst(int j) const { return (wave * NL + j) * 256; }
+  // tile origin for the tile starting at absolute k = k0 (wave-uniform; made
+  // scalar explicitly, as the DMA takes it in SGPRs)
+  __device__ __forceinline__ const float *origin(int k0) const {
+    const float *o = KC ? p + r0 * ld + k0 : p + (long)k0 * ld + r0;
+    const uintptr_t u = (uintptr_t)o;
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)u);
+    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(u >> 32));
+    return reinterpret_cast<const float *>(((uintptr_t)hi << 32) | lo);
+  }
+  __device__ __forceinline__ void issue(int j, const float *org, float *lds) const {
+    g2lds16s(org, voff[j], lds + dst(j));
+  }
+  // the last tile: k >= kend reads zeros
+  __device__ __forceinline__ void issue_tail(int j, const float *org, int k0, int kend,
+                                             float *lds) const {
+    const float *sp =
+        (k0 + koff(j) < kend)
+            ? reinterpret_cast<const float *>(reinterpret_cast<const char *>(org) + voff[j])
+            : g_gemm_zero;
+    g2lds16(sp, lds + dst(j));
+  }
+  // fragments of wave `wave`'s k slice, sub-slice h (8 k): v[x][s] for
+  // k = wave*BK/NW + 8h + 4g + s and row 32x + l32 (KC) or m/n 2*l32 + x (NC)
+  __device__ __forceinline__ static void frag(const float *lds, int wave, int h, int l32, int g,
+                                              float (*v)[4]) {
+    if constexpr (KC) {
+#pragma unroll
+      for (int x = 0; x < 2; x++) {
+        const int R = 32 * x + l32;
+        const int slot = (wave * (BK / (4 * NW)) + 2 * h + g) ^ swz(R);
+        const float4 t = *reinterpret_cast<const float4 *>(lds + R * BK + 4 * slot);
+        v[x][0] = t.x; v[x][1] = t.y; v[x][2] = t.z; v[x][3] = t.w;
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        const float2 t = *reinterpret_cast<const float2 *>(
+            lds + (wave * (BK / NW) + 8 * h + 4 * g + s) * M_T + 2 * l32);
+        v[0][s] = t.x; v[1][s] = t.y;
+      }
+    }
+  }
+};
+
+template <bool A_KC, bool B_NC, int BK, int S, int NW>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4, 2)))
+gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
+                const float *__restrict__ B, long ldb, float *__restrict__ C, long ldc,
+                long split_stride, int kchunk, bool cvec) {
+  static_assert(S >= 3, "the pipeline needs three stages");
+  constexpr int NTH = 64 * NW;
+  constexpr int OPS = M_T * BK;  // floats per operand per stage
+  constexpr int STAGE = 2 * OPS;
+  constexpr int PIPE = S * STAGE, RED = NW * M_T * M_RLD;
+  constexpr int KSUB = BK / (8 * NW);  // 8-k sub-slices per wave per tile
+  static_assert(KSUB >= 1, "tile too shallow for the waves");
+  __shared__ __attribute__((aligned(16))) float smem[PIPE > RED ? PIPE : RED];
+  using OA = MidOperand<A_KC, BK, NW>;
+  using OB = MidOperand<!B_NC, BK, NW>;
+  constexpr int NL = OA::NL + OB::NL;  // loads per wave per tile
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+
+  const int tiles_m = (M + M_T - 1) / M_T, tiles_n = (N + M_T - 1) / M_T;
+  const int ntiles = tiles_m * tiles_n;
+  int pid = blockIdx.x;
+  if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
+  const int group = GROUP_M * tiles_n;
+  const int first_m = (pid / group) * GROUP_M;
+  const int gsz = min(tiles_m - first_m, GROUP_M);
+  const int tm = first_m + (pid % group) % gsz;
+  const int tn = (pid % group) / gsz;
+  const long m0 = (long)tm * M_T;
+  const long n0 = (long)tn * M_T;
+  const int kbeg = blockIdx.z * kchunk;
+  const int kend = min(K, kbeg + kchunk);
+  const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+  C += (long)blockIdx.z * split_stride;
+
+  OA opa;
+  OB opb;
+  // A k-contiguous: rows m of A (M x K); else rows k of A (K x M), columns m.
+  // B m/n-contiguous: rows k of B (K x N); else rows n of B (N x K).
+  opa.init(A, lda, m0, M, wave, lane);
+  opb.init(B, ldb, n0, N, wave, lane);
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+  // loads J0 .. J0+NJ-1 of the NL of tile kt (A's first, then B's)
+  auto issue_part = [&](int kt, int j0, int nj) {
+    float *st = smem + (kt % S) * STAGE;
+    const int k0 = kbeg + kt * BK;
+    const float *oa = opa.origin(k0), *ob = opb.origin(k0);
+    if (k0 + BK <= kend) {
+#pragma unroll
+      for (int j = 0; j < NL; j++) {
+        if (j < j0 || j >= j0 + nj) continue;
+        if (j < OA::NL) opa.issue(j, oa, st);
+        else opb.issue(j - OA::NL, ob, st + OPS);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NL; j++) {
+        if (j < j0 || j >= j0 + nj) continue;
+        if (j < OA::NL) opa.issue_tail(j, oa, k0, kend, st);
+        else opb.issue_tail(j - OA::NL, ob, k0, kend, st + OPS);
+      }
+    }
+  };
+  auto frags = [&](int kt, float (*a)[2][4], float (*b)[2][4]) {
+    const float *st = smem + (kt % S) * STAGE;
+#pragma unroll
+    for (int h = 0; h < KSUB; h++) {
+      OA::frag(st, wave, h, l32, g, a[h]);
+      OB::frag(st + OPS, wave, h, l32, g, b[h]);
+    }
+  };
+  auto mfma4 = [&](float (*ca)[2][4], float (*cb)[2][4], int h, int s) {
+#pragma unroll
+    for (int x = 0; x < 2; x++)
+#pragma unroll
+      for (int y = 0; y < 2; y++)
+        acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(ca[h][x][s], cb[h][y][s], acc[x][y], 0, 0, 0);
+  };
+  // Tile kt: wait for tile kt+1 (tiles up to kt+S-2 are issued; S-3 may stay
+  // in flight, all of them near the end) and meet the other waves; read tile
+  // kt+1's fragments (they land under the MFMAs), then the MFMAs on the
+  // current fragments in groups of 4, each group followed by an equal share
+  // of the loads of tile kt+S-1 (into the stage tile kt-1 left, which every
+  // wave finished reading before the previous barrier).  The barrier and the
+  // reads are unconditional (on the last tile they read a stale stage nobody
+  // uses): under a branch the compiler's wait-count merge makes the MFMAs
+  // wait for the new reads instead of only for the previous tile's.
+  auto step = [&](int kt, float (*ca)[2][4], float (*cb)[2][4], float (*na)[2][4],
+                  float (*nb)[2][4]) {
+    if (kt + S - 2 < nk) wait_vm<NL *(S - 3)>();
+    else wait_vm<0>();
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    frags(kt + 1, na, nb);
+    __builtin_amdgcn_sched_barrier(0);
+    const bool more = kt + S - 1 < nk;
+    constexpr int G = 4 * KSUB;  // groups of 4 MFMAs
+    constexpr int PER = (NL + G - 1) / G;
+#pragma unroll
+    for (int q = 0; q < G; q++) {
+      mfma4(ca, cb, q / 4, q % 4);
+      __builtin_amdgcn_sched_barrier(0);
+      if (more && q * PER < NL) issue_part(kt + S - 1, q * PER, PER);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  if (nk > 0) {
+    for (int t = 0; t < S - 1 && t < nk; t++) issue_part(t, 0, NL);
+    if (nk >= S - 1) wait_vm<NL *(S - 2)>();
+    else wait_vm<0>();
+    __syncthreads();
+    float a0[KSUB][2][4], b0[KSUB][2][4], a1[KSUB][2][4], b1[KSUB][2][4];
+    frags(0, a0, b0);
+    for (int kt = 0; kt < nk; kt += 2) {
+      step(kt, a0, b0, a1, b1);
+      if (kt + 1 < nk) step(kt + 1, a1, b1, a0, b0);
+    }
+  }
+
+  // wave sums -> LDS (acc r of block (x, y): row 8*(r/4) + 4g + r%4 of the
+  // block), then each thread adds the NW wave sums of its outputs in order
+  __syncthreads();
+  float *red = smem + wave * (M_T * M_RLD);
+#pragma unroll
+  for (int x = 0; x < 2; x++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int i = 8 * (r >> 2) + 4 * g + (r & 3);
+      const int m = A_KC ? 32 * x + i : 2 * i + x;
+      if constexpr (B_NC) {
+        *reinterpret_cast<float2 *>(red + m * M_RLD + 2 * l32) = make_float2(acc[x][0][r], acc[x][1][r]);
+      } else {
+        red[m * M_RLD + l32] = acc[x][0][r];
+        red[m * M_RLD + 32 + l32] = acc[x][1][r];
+      }
+    }
+  __syncthreads();
+#pragma unroll
+  for (int f0 = 0; f0 < M_T * M_T / 4; f0 += NTH) {
+    const int f = f0 + tid;  // float4 index: row f / 16, columns 4 * (f % 16) ..
+    const int m = f >> 4, n = 4 * (f & 15);
+    const long row = m0 + m;
+    if (row >= M) continue;
+    float4 v = *reinterpret_cast<const float4 *>(smem + m * M_RLD + n);
+#pragma unroll
+    for (int w = 1; w < NW; w++) {
+      const float4 t = *reinterpret_cast<const float4 *>(smem + w * (M_T * M_RLD) + m * M_RLD + n);
+      v.x += t.x; v.y += t.y; v.z += t.z; v.w += t.w;
+    }
+    float *crow = C + row * ldc;
+    const long col = n0 + n;
+    if (cvec && col + 3 < N) {
+      *reinterpret_cast<float4 *>(crow + col) = v;
+    } else {
+      if (col < N) crow[col] = v.x;
+      if (col + 1 < N) crow[col + 1] = v.y;
+      if (col + 2 < N) crow[col + 2] = v.z;
+      if (col + 3 < N) crow[col + 3] = v.w;
+    }
+  }
+}
+
 inline hipStream_t stream() { return (hipStream_t)ttrt_stream(); }
 
 inline bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
@@ -873,6 +1183,7 @@ constexpr int TILE_BK[NTILE] = {32, 32, 32, 32, 32, 32, 32, 32, 32, 64, 64};
 // tuning override (tth_gemm_config): -1 = automatic
 int g_force_tile = -1, g_force_splits = -1;
 int g_direct = 1;  // direct-to-LDS 256x256 kernel enabled (tth_gemm_direct)
+int g_mid = 1;     // 64x64 direct-load kernel for plain GEMMs (tth_gemm_mid)
 
 struct Plan {
   int tile, splits, kchunk;
@@ -964,12 +1275,97 @@ void launch_tile(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, lo
   }
 }
 
+// Sum the S partial products of a split-K launch into C (+ epilogue).
+template <int EPI>
+int reduce_splits(const float *ws, float *C, int M, int N, int S, long ldc, const float *bias,
+                  int HW) {
+  const long total = (long)M * N;
+  // widen the split-lanes until ~2048 workgroups share the reduction (at
+  // most 32 lanes, at most S): each lane's loads are independent, so more
+  // lanes means more loads in flight for the few outputs of a conv dW
+  int zl = 1;
+  while (zl < 32 && zl < S && (total * zl * 2) <= 2048L * 256) zl *= 2;
+  if (zl < 4 && S >= 4) zl = 4;
+#define TT_RED(ZL_)                                                                            \
+  hipLaunchKernelGGL((splitk_reduce_kernel<EPI, ZL_>), dim3((unsigned)((total + 256 / ZL_ - 1) / \
+                                                                      (256 / ZL_))),            \
+                     dim3(256), 0, stream(), ws, C, M, N, S, ldc, bias, HW)
+  switch (zl) {
+    case 1: TT_RED(1); break;
+    case 2: TT_RED(2); break;
+    case 4: TT_RED(4); break;
+    case 8: TT_RED(8); break;
+    case 16: TT_RED(16); break;
+    default: TT_RED(32); break;
+  }
+#undef TT_RED
+  return hipGetLastError() != hipSuccess ? -3 : 0;
+}
+
+// Plain GEMM on 64x64 tiles (gemm_mid_kernel), split over K until the grid
+// covers the CUs.  Operands 16-byte aligned, leading dimensions multiples of
+// 4 (and at most 2^22), K % 4 == 0 for k-contiguous operands, M / N % 4 == 0
+// for m/n-contiguous ones (mid_ok).
+template <bool A_KC, bool B_NC>
+bool mid_ok(int M, int N, int K, const Opnd &A, const Opnd &B, bool vec) {
+  const bool kc_ops = A_KC || !B_NC;
+  return g_mid && vec && A.ld <= (1L << 22) && B.ld <= (1L << 22) && (!kc_ops || K % 4 == 0) &&
+         (A_KC || M % 4 == 0) && (!B_NC || N % 4 == 0);
+}
+
+template <bool A_KC, bool B_NC>
+int run_mid(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ldc) {
+  const int CUS = 256;
+  const long tiles = (long)((M + M_T - 1) / M_T) * ((N + M_T - 1) / M_T);
+  int s = 1;
+  while (s < 64 && tiles * s * 2 <= CUS && K / (s * 2) >= 128) s *= 2;
+  if (g_force_splits >= 1) s = g_force_splits;
+  // a split's k range is a whole number of 64-k tiles (the 32-k kernel
+  // takes the same ranges)
+  int kc = ((K + s - 1) / s + 63) / 64 * 64;
+  if (kc < 64) kc = 64;
+  const int splits = K > 0 ? (K + kc - 1) / kc : 1;
+  float *target = C;
+  long tld = ldc;
+  float *ws = nullptr;
+  if (splits > 1) {
+    ws = (float *)ttrt_alloc(sizeof(float) * (size_t)M * N * splits);
+    if (!ws) return -2;
+    target = ws;
+    tld = N;
+  }
+  const bool cvec = aligned16(target) && tld % 4 == 0;
+  const dim3 grid((unsigned)tiles, 1, splits);
+  const long sstride = (long)M * N;
+  // at most one workgroup per CU: 8 waves (two per SIMD) over 4 stages of
+  // 64 k (139 KB of LDS); more: 4 waves over 5 stages of 32 k (80 KB), two
+  // workgroups per CU
+  if (tiles * splits <= CUS)
+    hipLaunchKernelGGL((gemm_mid_kernel<A_KC, B_NC, 64, 4, 8>), grid, dim3(512), 0, stream(), M,
+                       N, K, A.p, A.ld, B.p, B.ld, target, tld, sstride, kc, cvec);
+  else
+    hipLaunchKernelGGL((gemm_mid_kernel<A_KC, B_NC, 32, 5, 4>), grid, dim3(256), 0, stream(), M,
+                       N, K, A.p, A.ld, B.p, B.ld, target, tld, sstride, kc, cvec);
+  if (hipGetLastError() != hipSuccess) { if (ws) ttrt_free(ws); return -3; }
+  if (ws) {
+    const int rc = reduce_splits<EPI_STORE>(ws, C, M, N, splits, ldc, nullptr, 1);
+    ttrt_free(ws);
+    if (rc) return rc;
+  }
+  return 0;
+}
+
 template <bool A_KC, bool A_PERM, bool B_NC, bool B_PERM, int EPI, bool B_I2C = false>
 int run(int M, int N, int K, Opnd A, Opnd B, float *C, long ldc, const float *bias, int HW,
         bool vec, const I2C &cv = I2C{}) {
   if (M <= 0 || N <= 0) return 0;
   // K == 0 runs no K tiles: the epilogue stores zeros (plus bias)
   Plan p = plan(M, N, K > 0 ? K : 1);
+  if constexpr (!A_PERM && !B_PERM && !B_I2C && EPI == EPI_STORE) {
+    if (p.tile != T256x256 && p.tile != T256x128 && p.tile != T128x128 && g_force_tile < 0 &&
+        mid_ok<A_KC, B_NC>(M, N, K, A, B, vec))
+      return run_mid<A_KC, B_NC>(M, N, K, A, B, C, ldc);
+  }
   if constexpr (B_I2C) {
     // no 256-wide big tile; a split's k range must fit the LDS kc table
     if (p.tile == T256x256 || p.tile == T256x128) p.tile = T128x128;
@@ -1032,28 +1428,9 @@ int run(int M, int N, int K, Opnd A, Opnd B, float *C, long ldc, const float *bi
 #undef TT_LAUNCH
   if (hipGetLastError() != hipSuccess) { if (ws) ttrt_free(ws); return -3; }
   if (ws) {
-    const long total = (long)M * N;
-    // widen the split-lanes until ~2048 workgroups share the reduction (at
-    // most 32 lanes, at most S): each lane's loads are independent, so more
-    // lanes means more loads in flight for the few outputs of a conv dW
-    int zl = 1;
-    while (zl < 32 && zl < p.splits && (total * zl * 2) <= 2048L * 256) zl *= 2;
-    if (zl < 4 && p.splits >= 4) zl = 4;
-#define TT_RED(ZL_)                                                                            \
-  hipLaunchKernelGGL((splitk_reduce_kernel<EPI, ZL_>), dim3((unsigned)((total + 256 / ZL_ - 1) / \
-                                                                      (256 / ZL_))),            \
-                     dim3(256), 0, stream(), ws, C, M, N, p.splits, ldc, bias, HW)
-    switch (zl) {
-      case 1: TT_RED(1); break;
-      case 2: TT_RED(2); break;
-      case 4: TT_RED(4); break;
-      case 8: TT_RED(8); break;
-      case 16: TT_RED(16); break;
-      default: TT_RED(32); break;
-    }
-#undef TT_RED
+    const int rc = reduce_splits<EPI>(ws, C, M, N, p.splits, ldc, bias, HW);
     ttrt_free(ws);
-    if (hipGetLastError() != hipSuccess) return -3;
+    if (rc) return rc;
   }
   return 0;
 }
@@ -1062,6 +1439,11 @@ int run(int M, int N, int K, Opnd A, Opnd B, float *C, long ldc, const float *bi
 
 extern "C" int tth_gemm_direct(int on) {
   g_direct = on ? 1 : 0;
+  return 0;
+}
+
+extern "C" int tth_gemm_mid(int on) {
+  g_mid = on ? 1 : 0;
   return 0;
 }
 
