@@ -465,3 +465,21 @@ def test_gemm_mid_kernel(tlib, M, N, K, ta, tb):
         check(tlib.tth_gemm_mid(1), "mid on")
     norm2, _ = gemm_err(C, C2, K, 1.0, 1.0)
     assert norm2 <= GEMM_TOL, norm2
+
+
+# Large GEMMs with unaligned operands take aligned, zero-padded copies into
+# the 64x64 kernel: ragged leading dimensions, K % 4 != 0, odd M / N.
+PAD_SHAPES = [(1000, 1003, 997), (1001, 1024, 1000), (1024, 999, 1024), (515, 1025, 1023)]
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+@pytest.mark.parametrize("M,N,K", PAD_SHAPES)
+def test_gemm_padded_operands(tlib, M, N, K, ta, tb):
+    A = u(K, M) if ta else u(M, K)
+    B = u(N, K) if tb else u(K, N)
+    Am = A.T if ta else A
+    Bm = B.T if tb else B
+    ref = Am.astype(np.float64) @ Bm.astype(np.float64)
+    C = run_gemm(tlib, M, N, K, ta, tb, A, B)
+    norm, rel = gemm_err(C, ref, K, 1.0, 1.0)
+    assert norm <= GEMM_TOL and rel <= GEMM_TOL, (norm, rel)

@@ -901,10 +901,10 @@ __device__ __forceinline__ void wait_vm() {
 // One operand's loads (16 bytes per lane; a load fills 256 floats of LDS).
 // KC: rows r0+R of a row-major (rows x K) matrix, BK k per tile.  NC: rows k
 // of a row-major (K x cols) matrix, columns r0 .. r0+63.  lim = rows (KC) or
-// cols (NC).  Rows / columns past lim load row / columns lim-1 / lim-4
-// instead (they only feed outputs that are not stored), so a tile's loads
-// need no range test; only k past the end of the K range (the last tile)
-// must read zeros.  Each lane keeps the byte offset of its element in every
+// the columns that may be read (NC: a multiple of 4, at least cols).  Rows /
+// columns past lim load row / columns lim-1 / lim-4 instead (they only feed
+// outputs that are not stored), so a tile's loads need no range test; only k
+// past the end of the K range (the last tile) must read zeros.  Each lane keeps the byte offset of its element in every
 // load relative to the tile origin (row r0 at k0 for KC, row k0 at column r0
 // for NC); the host keeps these below 2^32 (64 rows of the leading
 // dimension).
@@ -997,7 +997,7 @@ template <bool A_KC, bool B_NC, int BK, int S, int NW>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4, 2)))
 gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
                 const float *__restrict__ B, long ldb, float *__restrict__ C, long ldc,
-                long split_stride, int kchunk, bool cvec) {
+                long split_stride, int kchunk, bool cvec, int alim, int blim) {
   static_assert(S >= 3, "the pipeline needs three stages");
   constexpr int NTH = 64 * NW;
   constexpr int OPS = M_T * BK;  // floats per operand per stage
@@ -1035,8 +1035,9 @@ gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
   OB opb;
   // A k-contiguous: rows m of A (M x K); else rows k of A (K x M), columns m.
   // B m/n-contiguous: rows k of B (K x N); else rows n of B (N x K).
-  opa.init(A, lda, m0, M, wave, lane);
-  opb.init(B, ldb, n0, N, wave, lane);
+  // (alim / blim: the rows of a KC operand, the readable columns of an NC one)
+  opa.init(A, lda, m0, alim, wave, lane);
+  opb.init(B, ldb, n0, blim, wave, lane);
 
   f32x16 acc[2][2];
 #pragma unroll
@@ -1302,6 +1303,47 @@ int reduce_splits(const float *ws, float *C, int M, int N, int S, long ldc, cons
   return hipGetLastError() != hipSuccess ? -3 : 0;
 }
 
+// dst (rows x ldp, ldp a multiple of 4) = src (rows x cols, leading dimension
+// ld) with columns cols .. ldp-1 zero: a 16-byte aligned copy of an operand
+// whose rows are not.
+struct PadJob {
+  const float *src;
+  long ld;
+  int rows, cols;
+  float *dst;
+  int ldp;
+};
+
+// Both operands' copies in one launch: workgroups [0, ga) take job a's rows,
+// the rest job b's (a job with no rows is skipped); a workgroup copies whole
+// rows, consecutive lanes on consecutive floats (the source rows are not
+// 16-byte aligned, so wider per-lane loads would stride the cache lines).
+__global__ void __launch_bounds__(256) pad_rows_kernel(PadJob a, PadJob b, int ga) {
+  const bool first = (int)blockIdx.x < ga;
+  const PadJob &j = first ? a : b;
+  const int b0 = first ? blockIdx.x : blockIdx.x - ga;
+  const int nb = first ? ga : gridDim.x - ga;
+  for (int r = b0; r < j.rows; r += nb) {
+    const float *__restrict__ sr = j.src + (long)r * j.ld;
+    float *__restrict__ dr = j.dst + (long)r * j.ldp;
+    // four loads issued before their stores (one memory round trip per 1024
+    // floats, not one per 256)
+    for (int c0 = 0; c0 < j.ldp; c0 += 1024) {
+      float v[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int c = c0 + 256 * u + threadIdx.x;
+        v[u] = c < j.cols ? sr[c] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int c = c0 + 256 * u + threadIdx.x;
+        if (c < j.ldp) dr[c] = v[u];
+      }
+    }
+  }
+}
+
 // Plain GEMM on 64x64 tiles (gemm_mid_kernel), split over K until the grid
 // covers the CUs.  Operands 16-byte aligned, leading dimensions multiples of
 // 4 (and at most 2^22), K % 4 == 0 for k-contiguous operands, M / N % 4 == 0
@@ -1313,8 +1355,11 @@ bool mid_ok(int M, int N, int K, const Opnd &A, const Opnd &B, bool vec) {
          (A_KC || M % 4 == 0) && (!B_NC || N % 4 == 0);
 }
 
+// pad_a / pad_b: the operand is a padded copy whose rows may be read up to
+// the next multiple of 4 columns.
 template <bool A_KC, bool B_NC>
-int run_mid(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ldc) {
+int run_mid(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ldc,
+            bool pad_a = false, bool pad_b = false) {
   const int CUS = 256;
   const long tiles = (long)((M + M_T - 1) / M_T) * ((N + M_T - 1) / M_T);
   int s = 1;
@@ -1340,12 +1385,14 @@ int run_mid(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ld
   // at most one workgroup per CU: 8 waves (two per SIMD) over 4 stages of
   // 64 k (139 KB of LDS); more: 4 waves over 5 stages of 32 k (80 KB), two
   // workgroups per CU
+  const int alim = A_KC ? M : (pad_a ? (M + 3) / 4 * 4 : M);
+  const int blim = !B_NC ? N : (pad_b ? (N + 3) / 4 * 4 : N);
   if (tiles * splits <= CUS)
     hipLaunchKernelGGL((gemm_mid_kernel<A_KC, B_NC, 64, 4, 8>), grid, dim3(512), 0, stream(), M,
-                       N, K, A.p, A.ld, B.p, B.ld, target, tld, sstride, kc, cvec);
+                       N, K, A.p, A.ld, B.p, B.ld, target, tld, sstride, kc, cvec, alim, blim);
   else
     hipLaunchKernelGGL((gemm_mid_kernel<A_KC, B_NC, 32, 5, 4>), grid, dim3(256), 0, stream(), M,
-                       N, K, A.p, A.ld, B.p, B.ld, target, tld, sstride, kc, cvec);
+                       N, K, A.p, A.ld, B.p, B.ld, target, tld, sstride, kc, cvec, alim, blim);
   if (hipGetLastError() != hipSuccess) { if (ws) ttrt_free(ws); return -3; }
   if (ws) {
     const int rc = reduce_splits<EPI_STORE>(ws, C, M, N, splits, ldc, nullptr, 1);
@@ -1355,6 +1402,42 @@ int run_mid(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ld
   return 0;
 }
 
+// A GEMM large enough to amortise two copies whose operands are not
+// 16-byte aligned (ragged leading dimensions, K % 4 != 0 with k-contiguous
+// rows): copy the operands that need it into aligned, zero-padded buffers and
+// run the 64x64 kernel on those.
+template <bool A_KC, bool B_NC>
+int run_mid_padded(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ldc) {
+  // stored rows x cols of each operand
+  const int ar = A_KC ? M : K, ac = A_KC ? K : M;
+  const int br = B_NC ? K : N, bc = B_NC ? N : K;
+  // a copy is needed for unaligned rows, and for a partial last 16-byte chunk
+  // (K % 4 for k-contiguous rows, M / N % 4 for m/n-contiguous ones)
+  auto needs = [&](const Opnd &o, bool kc, int ext) {
+    return !aligned16(o.p) || o.ld % 4 != 0 || (kc ? K : ext) % 4 != 0;
+  };
+  const bool pa = needs(A, A_KC, M), pb = needs(B, !B_NC, N);
+  const int lda = (ac + 3) / 4 * 4, ldb = (bc + 3) / 4 * 4;
+  if (lda > (1 << 22) || ldb > (1 << 22)) return -1;
+  const size_t na = pa ? (size_t)ar * lda : 0, nb = pb ? (size_t)br * ldb : 0;
+  float *buf = (float *)ttrt_alloc(sizeof(float) * (na + nb));
+  if (!buf) return -2;
+  Opnd a2 = A, b2 = B;
+  PadJob ja{A.p, A.ld, pa ? ar : 0, ac, buf, lda}, jb{B.p, B.ld, pb ? br : 0, bc, buf + na, ldb};
+  // a workgroup per row (all loads in flight at once) up to 16384, split
+  // between the jobs by rows
+  const long rows = (long)ja.rows + jb.rows;
+  const long cap = min(rows, 16384L);
+  const int ga = ja.rows ? (int)max(1L, cap * ja.rows / rows) : 0;
+  const int gb = jb.rows ? (int)max(1L, cap * jb.rows / rows) : 0;
+  hipLaunchKernelGGL(pad_rows_kernel, dim3(ga + gb), dim3(256), 0, stream(), ja, jb, ga);
+  if (pa) a2 = Opnd{buf, lda, 0, 1};
+  if (pb) b2 = Opnd{buf + na, ldb, 0, 1};
+  const int rc = run_mid<A_KC, B_NC>(M, N, K, a2, b2, C, ldc, pa, pb);
+  ttrt_free(buf);  // stream-ordered: the GEMM above is queued before any reuse
+  return rc;
+}
+
 template <bool A_KC, bool A_PERM, bool B_NC, bool B_PERM, int EPI, bool B_I2C = false>
 int run(int M, int N, int K, Opnd A, Opnd B, float *C, long ldc, const float *bias, int HW,
         bool vec, const I2C &cv = I2C{}) {
@@ -1362,9 +1445,10 @@ int run(int M, int N, int K, Opnd A, Opnd B, float *C, long ldc, const float *bi
   // K == 0 runs no K tiles: the epilogue stores zeros (plus bias)
   Plan p = plan(M, N, K > 0 ? K : 1);
   if constexpr (!A_PERM && !B_PERM && !B_I2C && EPI == EPI_STORE) {
-    if (p.tile != T256x256 && p.tile != T256x128 && p.tile != T128x128 && g_force_tile < 0 &&
-        mid_ok<A_KC, B_NC>(M, N, K, A, B, vec))
-      return run_mid<A_KC, B_NC>(M, N, K, A, B, C, ldc);
+    if (p.tile != T256x256 && p.tile != T256x128 && p.tile != T128x128 && g_force_tile < 0) {
+      if (mid_ok<A_KC, B_NC>(M, N, K, A, B, vec)) return run_mid<A_KC, B_NC>(M, N, K, A, B, C, ldc);
+      if (g_mid && 2.0 * M * N * K >= 1e9) return run_mid_padded<A_KC, B_NC>(M, N, K, A, B, C, ldc);
+    }
   }
   if constexpr (B_I2C) {
     // no 256-wide big tile; a split's k range must fit the LDS kc table
