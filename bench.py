@@ -56,6 +56,9 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="headline only")
     ap.add_argument("--cnn-only", action="store_true",
                     help="only time the config-4 CNN training step (for kernel traces of it)")
+    ap.add_argument("--gemm-shapes", action="store_true",
+                    help="only time the secondary GEMM shapes (configs 1, 3, 5; for kernel "
+                         "traces of them)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 1 GiB device copy kernel 5 times (the known-size "
                          "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -405,6 +408,29 @@ def cpu_baseline(threads):
                 cnn_sample="config-4 CNN fwd+bwd on the reference autograd path, median of 3")
 
 
+# secondary GEMM shapes (3 and 5): name -> (M, N, K, transA, transB)
+GEMM_SHAPES = {"sgemm_1024": (1024, 1024, 1024, 0, 0),
+               "sgemm_4096_nt_dA": (4096, 4096, 4096, 0, 1),
+               "sgemm_4096_tn_dB": (4096, 4096, 4096, 1, 0),
+               "sgemm_8192": (8192, 8192, 8192, 0, 0),
+               "sgemm_ragged_1000x1003x997": (1000, 1003, 997, 0, 0),
+               "sgemm_tall_65536x64x4096": (65536, 64, 4096, 0, 0)}
+
+
+def gemm_shapes(L):
+    out = {}
+    for name, (M, N, K, ta, tb) in GEMM_SHAPES.items():
+        gg = Gemm(L, M, N, K, ta, tb)
+        steps = max(10, min(200, int(3e12 / gg.flops())))
+        _, ms = time_gemm(L, gg, steps, 2)
+        out[name] = dict(tflops=round(gg.flops() / (ms * 1e-3) / 1e12, 2), ms=round(ms, 4),
+                         frac_of_peak=round(gg.flops() / (ms * 1e-3) / 1e12 /
+                                            PEAK_FP32_MFMA_TFLOPS, 4))
+        gg.free()
+        log(name, out[name])
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -418,6 +444,9 @@ def main():
     if args.cnn_only:
         ms = time_steps(CnnStep(L), args.steps, args.warmup)
         print(json.dumps({"cnn_step_ms": round(ms, 4), "steps": args.steps, "warmup": args.warmup}))
+        return
+    if args.gemm_shapes:
+        print(json.dumps(gemm_shapes(L)))
         return
     if args.copy_calib:
         from tinytorch_amd.hip import DevBuf, check, sync
@@ -441,22 +470,7 @@ def main():
 
     extra = {}
     if not args.no_extra:
-        for name, (M, N, K, ta, tb) in {
-                "sgemm_1024": (1024, 1024, 1024, 0, 0),
-                "sgemm_4096_nt_dA": (4096, 4096, 4096, 0, 1),
-                "sgemm_4096_tn_dB": (4096, 4096, 4096, 1, 0),
-                "sgemm_8192": (8192, 8192, 8192, 0, 0),
-                "sgemm_ragged_1000x1003x997": (1000, 1003, 997, 0, 0),
-                "sgemm_tall_65536x64x4096": (65536, 64, 4096, 0, 0)}.items():
-            gg = Gemm(L, M, N, K, ta, tb)
-            steps = max(10, min(200, int(3e12 / gg.flops())))
-            _, ms = time_gemm(L, gg, steps, 2)
-            extra[name] = dict(tflops=round(gg.flops() / (ms * 1e-3) / 1e12, 2),
-                               ms=round(ms, 4),
-                               frac_of_peak=round(gg.flops() / (ms * 1e-3) / 1e12 /
-                                                  PEAK_FP32_MFMA_TFLOPS, 4))
-            gg.free()
-            log(name, extra[name])
+        extra.update(gemm_shapes(L))
         cnn = CnnStep(L)
         extra["cnn_step_ms"] = round(time_steps(cnn, 20, 5), 3)
         log("cnn step ms", extra["cnn_step_ms"])
