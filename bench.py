@@ -56,6 +56,8 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="headline only")
     ap.add_argument("--cnn-only", action="store_true",
                     help="only time the config-4 CNN training step (for kernel traces of it)")
+    ap.add_argument("--mlp-only", action="store_true",
+                    help="only time the config-2 MLP training step (for kernel traces of it)")
     ap.add_argument("--gemm-shapes", action="store_true",
                     help="only time the secondary GEMM shapes (configs 1, 3, 5; for kernel "
                          "traces of them)")
@@ -444,6 +446,10 @@ def main():
     if args.cnn_only:
         ms = time_steps(CnnStep(L), args.steps, args.warmup)
         print(json.dumps({"cnn_step_ms": round(ms, 4), "steps": args.steps, "warmup": args.warmup}))
+        return
+    if args.mlp_only:
+        ms = time_steps(MlpStep(L), args.steps, args.warmup)
+        print(json.dumps({"mlp_step_ms": round(ms, 4), "steps": args.steps, "warmup": args.warmup}))
         return
     if args.gemm_shapes:
         print(json.dumps(gemm_shapes(L)))

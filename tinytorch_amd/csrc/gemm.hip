@@ -1351,7 +1351,10 @@ __global__ void __launch_bounds__(256) pad_rows_kernel(PadJob a, PadJob b, int g
 template <bool A_KC, bool B_NC>
 bool mid_ok(int M, int N, int K, const Opnd &A, const Opnd &B, bool vec) {
   const bool kc_ops = A_KC || !B_NC;
-  return g_mid && vec && A.ld <= (1L << 22) && B.ld <= (1L << 22) && (!kc_ops || K % 4 == 0) &&
+  // below ~0.5 GFLOP the per-launch cost of the deep pipeline and the wave
+  // sums outweighs its faster K loop (measured: 512^3 and the MLP GEMMs are
+  // faster on the register-staged 64x64 kernel)
+  return g_mid && vec && 2.0 * M * N * K >= (double)(1L << 29) && A.ld <= (1L << 22) && B.ld <= (1L << 22) && (!kc_ops || K % 4 == 0) &&
          (A_KC || M % 4 == 0) && (!B_NC || N % 4 == 0);
 }
 
