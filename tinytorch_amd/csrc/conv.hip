@@ -152,6 +152,51 @@ __device__ __forceinline__ void stage_slab(float *xs, const float *__restrict__ 
   stage_blocks<VEC>(xs, xn, (g.C + 1) * CS, CS, g.C, (long)g.H * g.W, rlo * g.W, rhi * g.W);
 }
 
+// Gapped slab (weight gradient, 16-byte staging): every row of W floats sits
+// in a slot of W + G floats behind G zeros, G a multiple of 4 covering the
+// left padding and the right overhang of the widest tap, so a tap read past
+// either end of a row lands in a gap and reads zero -- no mask per read.
+// Channel stride R*(W+G) + 4, then a zero plane.  The DMA still fills LDS in
+// whole 16-byte runs: a lane whose chunk falls in a gap loads the zero source.
+__host__ __device__ inline int gslab_gap(const Geo &g) {
+  const int ro = (g.Wo - 1) * g.sw - g.pw + g.WW - g.W;  // right overhang
+  int need = g.pw > ro ? g.pw : ro;
+  if (need < 1) need = 1;
+  return round_up(need, 4);
+}
+__host__ __device__ inline int gslab_rw(const Geo &g) { return g.W + gslab_gap(g); }
+__host__ __device__ inline int gslab_cs(int R, const Geo &g) { return R * gslab_rw(g) + 4; }
+
+__device__ __forceinline__ void stage_gslab(float *xs, const float *__restrict__ x, const Geo &g,
+                                            const Slab &s, int n) {
+  const int hs = s.ho0 * g.sh - g.ph;
+  const int G = gslab_gap(g), RW = g.W + G;
+  const int CS = gslab_cs(s.R, g);
+  const int T = (g.C + 1) * CS;
+  const float rcpC = 1.0f / (float)CS, rcpR = 1.0f / (float)RW;
+  const float *xn = x + (long)n * g.C * g.H * g.W;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  for (int base = wave * 256; base < T; base += NT * 4) {
+    const int i = base + lane * 4;
+    const int c = fdiv(i, CS, rcpC), rem = i - c * CS;
+    const int slot = fdiv(rem, RW, rcpR), j = rem - slot * RW;
+    const int row = hs + slot;
+    const bool ok = i < T && c < g.C && slot < s.R && j >= G && row >= 0 && row < g.H;
+    const float *p = ok ? xn + ((long)c * g.H + row) * g.W + (j - G) : g_zero_src;
+    dma_dwordx4(p, xs + base);
+  }
+}
+
+// tap k of the gapped slab -> LDS offset (taps past K -> the zero plane)
+__device__ __forceinline__ int gslab_tap(const Geo &g, const Slab &s, int k) {
+  const int CS = gslab_cs(s.R, g), RW = gslab_rw(g);
+  if (k >= g.K) return g.C * CS;
+  const int taps = g.HH * g.WW;
+  const int c = fdiv(k, taps, 1.0f / (float)taps), t = k - c * taps;
+  const int kh = fdiv(t, g.WW, 1.0f / (float)g.WW), kw = t - kh * g.WW;
+  return c * CS + kh * RW + gslab_gap(g) + kw - g.pw;
+}
+
 // im2col row k -> (LDS offset of the tap inside the slab, kw - pw, offset of
 // the flipped tap in the FLIP weight layout); taps past K -> the zero plane,
 // never masked (their weight offset is 0: a finite weight times zero).
@@ -657,8 +702,14 @@ conv_dw32_kernel(const float *__restrict__ gr, const float *__restrict__ x,
   const float *gn = gr + (long)n * g.F * P + (long)f0 * P + p0;
   const int nf = g.F - f0 < FB ? g.F - f0 : FB;
   stage_blocks<VEC>(gs, gn, FB * GS, GS, nf, P, 0, np);
-  stage_slab<VEC>(xs, x, g, s, n);
-  for (int k = tid; k < 32 * JB; k += NT) ktab[k] = tap_entry(g, s, k);
+  // 16-byte staging: the gapped slab (no masks in the loop)
+  if constexpr (VEC) {
+    stage_gslab(xs, x, g, s, n);
+    for (int k = tid; k < 32 * JB; k += NT) ktab[k] = make_int4(gslab_tap(g, s, k), 0, 0, 0);
+  } else {
+    stage_slab<VEC>(xs, x, g, s, n);
+    for (int k = tid; k < 32 * JB; k += NT) ktab[k] = tap_entry(g, s, k);
+  }
   dma_wait();
   __syncthreads();
 
@@ -681,7 +732,8 @@ conv_dw32_kernel(const float *__restrict__ gr, const float *__restrict__ x,
 #pragma unroll
   for (int jw = 0; jw < JW; jw++) {
     const int k = (jb0 + jw) * 32 + l32;
-    const int4 t = k < 32 * JB ? ktab[k] : make_int4(g.C * slab_cs(s.R, g.W), 0, 0, 0);
+    const int zplane = g.C * (VEC ? gslab_cs(s.R, g) : slab_cs(s.R, g.W));
+    const int4 t = k < 32 * JB ? ktab[k] : make_int4(zplane, 0, 0, 0);
     bb[jw] = t.x + h * g.sw;      // slab offset of (tap, pixel h) at the row start
     cq[jw] = t.y + h * g.sw;      // its column relative to wo*sw
   }
@@ -699,35 +751,51 @@ conv_dw32_kernel(const float *__restrict__ gr, const float *__restrict__ x,
     const float *ga = gs + l32 * GS + h;
     // (scalar) offsets of the current step: g column qa, slab offset xo,
     // column col; a step adds 2 pixels, a row end jumps KS rows ahead
-    const int qstep_row = KS * g.Wo - 2 * half_w, xstep_row = KS * g.sh * g.W - 2 * half_w * g.sw;
+    const int RS = VEC ? gslab_rw(g) : g.W;  // slab row stride
+    const int qstep_row = KS * g.Wo - 2 * half_w, xstep_row = KS * g.sh * RS - 2 * half_w * g.sw;
     auto load = [&](int qa, int xo, float &a, float (&b)[JW]) {  // raw: masked at use
       a = ga[qa];
 #pragma unroll
       for (int jw = 0; jw < JW; jw++) b[jw] = xs[bb[jw] + xo];
     };
-    int qa = ks * g.Wo, xo = ks * g.sh * g.W, st = 0;
-    float a_c, b_c[JW];
-    if (T > 0) load(qa, xo, a_c, b_c);
-    for (int t = 0; t < T; t++) {
-      int qa1 = qa + 2, xo1 = xo + 2 * g.sw, st1 = st + 1;
-      if (st1 == half_w) { st1 = 0; qa1 += qstep_row; xo1 += xstep_row; }
-      float a_n, b_n[JW];
-      load(t + 1 < T ? qa1 : qa, t + 1 < T ? xo1 : xo, a_n, b_n);
-      __builtin_amdgcn_sched_barrier(0);
-      const int col = 2 * st * g.sw;
+    auto advance = [&](int &qa_, int &xo_, int &st_) {
+      qa_ += 2;
+      xo_ += 2 * g.sw;
+      if (++st_ == half_w) { st_ = 0; qa_ += qstep_row; xo_ += xstep_row; }
+    };
+    auto mfmas = [&](float a, const float (&b)[JW], int st_) {
+      const int col = 2 * st_ * g.sw;
 #pragma unroll
       for (int jw = 0; jw < JW; jw++) {
-        const float b = (unsigned)(cq[jw] + col) < (unsigned)g.W ? b_c[jw] : 0.0f;
-        acc[jw] = __builtin_amdgcn_mfma_f32_32x32x2f32(a_c, b, acc[jw], 0, 0, 0);
+        const float bm = VEC || (unsigned)(cq[jw] + col) < (unsigned)g.W ? b[jw] : 0.0f;
+        acc[jw] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bm, acc[jw], 0, 0, 0);
       }
+    };
+    // two operand sets in turn: a step's operands are read a whole step
+    // before its MFMAs (a read past the last step re-reads the last one)
+    int qa = ks * g.Wo, xo = ks * g.sh * RS, st = 0;
+    float a0 = 0.0f, b0[JW], a1, b1[JW];
+    if (T > 0) load(qa, xo, a0, b0);
+    int t = 0;
+    for (; t + 1 < T; t += 2) {
+      int qa1 = qa, xo1 = xo, st1 = st;
+      advance(qa1, xo1, st1);
+      load(qa1, xo1, a1, b1);
       __builtin_amdgcn_sched_barrier(0);
-      a_c = a_n;
-#pragma unroll
-      for (int jw = 0; jw < JW; jw++) b_c[jw] = b_n[jw];
-      qa = qa1;
-      xo = xo1;
-      st = st1;
+      mfmas(a0, b0, st);
+      __builtin_amdgcn_sched_barrier(0);
+      int qa2 = qa1, xo2 = xo1, st2 = st1;
+      advance(qa2, xo2, st2);
+      const bool more = t + 2 < T;
+      load(more ? qa2 : qa1, more ? xo2 : xo1, a0, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(a1, b1, st1);
+      __builtin_amdgcn_sched_barrier(0);
+      qa = qa2;
+      xo = xo2;
+      st = st2;
     }
+    if (t < T) mfmas(a0, b0, st);
   }
 
   if constexpr (KS > 1) {
@@ -971,6 +1039,11 @@ DwPlan plan_dw32(const Geo &g, int N) {
     const int KSv = pl.var == 10 ? 4 : pl.var == 13 ? 1 : 2;
     const long red = (long)(4 / KSv) * (KSv - 1) * JWv * 16 * 64;
     long xs = slab_floats(g, ch < P ? ch : P);
+    if (g.W % 4 == 0) {  // 16-byte staging takes the gapped slab (larger)
+      const long R = (long)(rows_spanned(ch < P ? ch : P, g.Wo) - 1) * g.sh + g.HH;
+      const long gx = round_up((int)min((long)(g.C + 1) * (R * gslab_rw(g) + 4), (long)LDS_MAX), 256);
+      if (gx > xs) xs = gx;
+    }
     const long main = round_up(32 * GS, 256) + 4L * 32 * JB + GUARD + xs;
     const long lds = 4L * (main > red ? main : red);
     if (lds <= LDS_MAX) {
