@@ -187,6 +187,13 @@ __device__ __forceinline__ void stage_gslab(float *xs, const float *__restrict__
   }
 }
 
+// output pixel p -> (LDS offset of its first tap's row start inside the
+// gapped slab, wo*sw): rows of gslab_rw floats, data behind the gap
+__device__ __forceinline__ int2 gslab_pixel(const Geo &g, const Slab &s, int p) {
+  const int ho = fdiv(p, g.Wo, 1.0f / (float)g.Wo), wo = p - ho * g.Wo;
+  return make_int2((ho - s.ho0) * g.sh * gslab_rw(g) + wo * g.sw + gslab_gap(g), wo * g.sw);
+}
+
 // tap k of the gapped slab -> LDS offset (taps past K -> the zero plane)
 __device__ __forceinline__ int gslab_tap(const Geo &g, const Slab &s, int k) {
   const int CS = gslab_cs(s.R, g), RW = gslab_rw(g);
@@ -393,7 +400,10 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
   const int CH2 = (g.C + 1) >> 1;
   const int KST = wrow_stride(2 * CH2 * TAPS);
   const Slab s = slab_of(g, p0, p1);
-  const int RW = slab_cs(s.R, g.W);  // channel stride of the slab
+  // 16-byte staging: the gapped slab (reads past a row end hit zeros, no
+  // masks); otherwise rows of W floats and a select per read
+  const int RW = VEC ? gslab_cs(s.R, g) : slab_cs(s.R, g.W);  // channel stride of the slab
+  const int RS = VEC ? gslab_rw(g) : g.W;                     // row stride of the slab
   const int nf = g.F - f0 < 32 ? g.F - f0 : 32;
 
   float *ws = smem;  // forward: 32 x KST; FLIP: 2*CH2 x 32 x TAPS
@@ -402,7 +412,8 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
-  stage_slab<VEC>(xs, x, g, s, n);
+  if constexpr (VEC) stage_gslab(xs, x, g, s, n);
+  else stage_slab<VEC>(xs, x, g, s, n);
   {
     if constexpr (FLIP)
       stage_blocks<VEC>(ws, w + (long)f0 * TAPS, 2 * CH2 * 32 * TAPS, 32 * TAPS, g.C,
@@ -421,8 +432,10 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
 #pragma unroll
   for (int j = 0; j < PB; j++) {
     const int p = p0 + (wave * PB + j) * 32 + l32;
-    int2 e = make_int2(0, -(1 << 20));  // past the chunk: every tap masked
-    if (p < p1) e = pixel_entry(g, s, p);
+    // past the chunk: every tap masked (gapped: any in-slab pixel, the
+    // output is not stored)
+    int2 e = make_int2(VEC ? g.pw : 0, -(1 << 20));
+    if (p < p1) e = VEC ? gslab_pixel(g, s, p) : pixel_entry(g, s, p);
     bj[j] = e.x + hoff;
 #pragma unroll
     for (int kw = 0; kw < KW; kw++) mk[j][kw] = (unsigned)(e.y + kw - g.pw) < (unsigned)g.W;
@@ -446,32 +459,36 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
     for (int j = 0; j < PB; j++)
 #pragma unroll
       for (int kh = 0; kh < KH; kh++) {
-        const float *row = xs + bj[j] + cb + kh * g.W;
+        const float *row = xs + bj[j] + cb + kh * RS;
 #pragma unroll
         for (int kw = 0; kw < KW; kw++) b[kh * KW + kw][j] = row[kw];  // raw: masked at use
       }
   };
-  float a_c[TAPS], b_c[TAPS][PB];
-  if (steps > 0) load(0, a_c, b_c);
-  for (int c = 0; c < steps; c++) {
-    float a_n[TAPS], b_n[TAPS][PB];
-    load(c + 1 < steps ? c + 1 : c, a_n, b_n);
-    __builtin_amdgcn_sched_barrier(0);
+  auto mfmas = [&](const float (&a)[TAPS], const float (&b)[TAPS][PB]) {
 #pragma unroll
     for (int t = 0; t < TAPS; t++)
 #pragma unroll
       for (int j = 0; j < PB; j++) {
-        const float b = mk[j][t % KW] ? b_c[t][j] : 0.0f;
-        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a_c[t], b, acc[j], 0, 0, 0);
+        const float bm = VEC || mk[j][t % KW] ? b[t][j] : 0.0f;
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t], bm, acc[j], 0, 0, 0);
       }
+  };
+  // two operand sets in turn: a channel's operands are read a whole channel
+  // before its MFMAs (a read past the last channel re-reads the last one)
+  float a0[TAPS], b0[TAPS][PB], a1[TAPS], b1[TAPS][PB];
+  if (steps > 0) load(0, a0, b0);
+  int c = 0;
+  for (; c + 1 < steps; c += 2) {
+    load(c + 1, a1, b1);
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int t = 0; t < TAPS; t++) {
-      a_c[t] = a_n[t];
-#pragma unroll
-      for (int j = 0; j < PB; j++) b_c[t][j] = b_n[t][j];
-    }
+    mfmas(a0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    load(c + 2 < steps ? c + 2 : c + 1, a0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(a1, b1);
+    __builtin_amdgcn_sched_barrier(0);
   }
+  if (c < steps) mfmas(a0, b0);
 
   float bv[16];
 #pragma unroll
@@ -949,7 +966,12 @@ FwdPlan plan_fwd(const Geo &g, int N, bool flip) {
   for (int pb = 2; pb >= 1; pb--) {
     const int chunk = 128 * pb;
     const int chunks = (P + chunk - 1) / chunk;
-    const long sf = slab_floats(g, chunk < P ? chunk : P);
+    long sf = slab_floats(g, chunk < P ? chunk : P);
+    if (is_k3(g) && g.W % 4 == 0) {  // 16-byte staging takes the gapped slab (larger)
+      const long R = (long)(rows_spanned(chunk < P ? chunk : P, g.Wo) - 1) * g.sh + g.HH;
+      const long gx = round_up((int)min((long)(g.C + 1) * (R * gslab_rw(g) + 4), (long)LDS_MAX), 256);
+      if (gx > sf) sf = gx;
+    }
     long wsz, tabsz;
     if (is_k3(g)) {
       wsz = flip ? round_up(K2 * 32, 256) : round_up(32 * wrow_stride(K2), 256);
