@@ -418,8 +418,10 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
     if constexpr (FLIP)
       stage_blocks<VEC>(ws, w + (long)f0 * TAPS, 2 * CH2 * 32 * TAPS, 32 * TAPS, g.C,
                         (long)g.F * TAPS, 0, nf * TAPS);
-    else
-      stage_blocks<VEC>(ws, w + (long)f0 * g.K, 32 * KST, KST, nf, g.K, 0, g.K);
+    else if (VEC && g.K % 4 == 0)
+      stage_blocks<true>(ws, w + (long)f0 * g.K, 32 * KST, KST, nf, g.K, 0, g.K);
+    else  // rows of K floats not 16-byte aligned (K % 4 != 0): 4-byte loads
+      stage_blocks<false>(ws, w + (long)f0 * g.K, 32 * KST, KST, nf, g.K, 0, g.K);
   }
   if (tid < 32) bs[tid] = (bias && f0 + tid < g.F) ? bias[f0 + tid] : 0.0f;
   dma_wait();
@@ -1008,12 +1010,16 @@ int run_fwd(const float *x, const float *w, const float *bias, float *out, const
   const FwdPlan pl = plan_fwd(g, N, FLIP);
   if (!pl.pb) return -1;
   if (dry) return 0;
-  // 16-byte loads: 4-aligned rows of x and of the weight blocks
+  // 16-byte loads: 4-aligned rows of x and of the weight blocks (the 3x3
+  // forward kernel stages weight rows that are not 16-byte aligned with
+  // 4-byte loads whatever VEC is)
   const int taps = g.HH * g.WW;
-  const bool wvec = FLIP ? (g.F * taps) % 4 == 0 && ((g.F % 32) * taps) % 4 == 0 &&
-                               (32 * taps) % 4 == 0
-                         : g.K % 4 == 0;
-  const bool vec = g.W % 4 == 0 && aligned16(x) && wvec && aligned16(w);
+  bool wok;  // the weights can be staged under this VEC choice
+  if (is_k3(g) && !FLIP) wok = g.K % 4 != 0 || aligned16(w);  // else 4-byte loads
+  else wok = aligned16(w) && (FLIP ? (g.F * taps) % 4 == 0 && ((g.F % 32) * taps) % 4 == 0 &&
+                                         (32 * taps) % 4 == 0
+                                   : g.K % 4 == 0);
+  const bool vec = g.W % 4 == 0 && aligned16(x) && wok;
   if (pl.pb == 2)
     return vec ? launch_fwd<2, FLIP, true>(x, w, bias, out, g, N, pl)
                : launch_fwd<2, FLIP, false>(x, w, bias, out, g, N, pl);
