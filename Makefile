@@ -13,7 +13,8 @@ ARCH    ?= gfx950
 BUILD   := build
 CSRC    := tinytorch_amd/csrc
 
-# -packed-fp32-ops off: no v_pk_*_f32 are generated ("build flags")
+# -packed-fp32-ops off: the compiler generates no packed fp32 instructions
+# (v_pk_*_f32); some of their forms have given wrong results on this hardware
 HIPFLAGS := --offload-arch=$(ARCH) -O3 -fPIC -std=c++17 -Iinclude -I$(CSRC) \
             -Xclang -target-feature -Xclang -packed-fp32-ops -Wno-unused-command-line-argument
 CFLAGS_HOST := -O2 -fPIC -std=c11 -Wall -Wextra -D__HIP_PLATFORM_AMD__ -I$(ROCM)/include \

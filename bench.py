@@ -437,7 +437,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU; --gpus {args.gpus} is not supported "
-              "(see DESIGN.md: how the path would shard)", file=sys.stderr)
+              "(a multi-GPU run would be data parallel: one process per GPU, each with B/N "
+              "images, and one all-reduce of the weight gradients per step)", file=sys.stderr)
         sys.exit(2)
     import tinytorch_amd
     tinytorch_amd.require_gpu()
