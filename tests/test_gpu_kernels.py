@@ -483,3 +483,22 @@ def test_gemm_padded_operands(tlib, M, N, K, ta, tb):
     C = run_gemm(tlib, M, N, K, ta, tb, A, B)
     norm, rel = gemm_err(C, ref, K, 1.0, 1.0)
     assert norm <= GEMM_TOL and rel <= GEMM_TOL, (norm, rel)
+
+
+# Tall GEMMs with few columns (N <= 64, at least 256 tiles of 256 rows) take
+# the 256-row tiles of the 64x64 kernel: edge rows and columns, a K tail,
+# all three transposition layouts, whole result against float64.
+TALL_SHAPES = [(65536, 64, 256), (65600, 48, 200), (70000, 60, 132)]
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+@pytest.mark.parametrize("M,N,K", TALL_SHAPES)
+def test_gemm_tall_rows(tlib, M, N, K, ta, tb):
+    A = u(K, M) if ta else u(M, K)
+    B = u(N, K) if tb else u(K, N)
+    Am = A.T if ta else A
+    Bm = B.T if tb else B
+    ref = Am.astype(np.float64) @ Bm.astype(np.float64)
+    C = run_gemm(tlib, M, N, K, ta, tb, A, B)
+    norm, rel = gemm_err(C, ref, K, 1.0, 1.0)
+    assert norm <= GEMM_TOL and rel <= GEMM_TOL, (norm, rel)

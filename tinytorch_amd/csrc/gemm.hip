@@ -908,11 +908,13 @@ __device__ __forceinline__ void wait_vm() {
 // load relative to the tile origin (row r0 at k0 for KC, row k0 at column r0
 // for NC); the host keeps these below 2^32 (64 rows of the leading
 // dimension).
-template <bool KC, int BK, int NW>
+template <bool KC, int BK, int NW, int T = M_T, int KSL = NW>
 struct MidOperand {
-  static constexpr int CPR = BK / 4;       // 16-byte chunks per KC row
-  static constexpr int NL = BK / (4 * NW); // loads per wave per tile
-  static_assert(NL >= 1, "tile too shallow for the waves");
+  // T: the tile's extent in this operand (rows for KC, columns for NC);
+  // KSL: waves sharing one K tile (its k slices)
+  static constexpr int CPR = BK / 4;               // 16-byte chunks per KC row
+  static constexpr int NL = T * BK / (256 * NW);   // loads per wave per tile
+  static_assert(NL >= 1 && NL * 256 * NW == T * BK, "tile too small for the waves");
   __device__ __forceinline__ static int swz(int R) { return BK == 32 ? (R >> 1) & 7 : R & 15; }
   unsigned voff[NL];
   const float *p;
@@ -932,19 +934,20 @@ struct MidOperand {
         const int R = (wave * NL + j) * (256 / BK) + lane / CPR;
         e = (min(r0 + R, (long)lim - 1) - r0) * ld + koff(j);
       } else {
-        e = (long)koff(j) * ld + (min(r0 + 4 * (lane & 15), (long)lim - 4) - r0);
+        e = (long)koff(j) * ld + (min(r0 + 4 * (lane % (T / 4)), (long)lim - 4) - r0);
       }
       voff[j] = (unsigned)(e * 4);
     }
   }
-  // k of load j's lane relative to the tile's first k
+  // k of load j's lane relative to the tile's first k (NC: a load fills
+  // 256/T rows k of T floats)
   __device__ __forceinline__ int koff(int j) const {
     const int q = wave * NL + j;
     if constexpr (KC) {
       const int R = q * (256 / BK) + lane / CPR;
       return 4 * ((lane % CPR) ^ swz(R));
     } else {
-      return 4 * q + (lane >> 4);
+      return q * (256 / T) + lane / (T / 4);
     }
   }
   // LDS float offset of load j's first lane
@@ -970,15 +973,16 @@ struct MidOperand {
             : g_gemm_zero;
     g2lds16(sp, lds + dst(j));
   }
-  // fragments of wave `wave`'s k slice, sub-slice h (8 k): v[x][s] for
-  // k = wave*BK/NW + 8h + 4g + s and row 32x + l32 (KC) or m/n 2*l32 + x (NC)
-  __device__ __forceinline__ static void frag(const float *lds, int wave, int h, int l32, int g,
-                                              float (*v)[4]) {
+  // fragments of k slice ks, sub-slice h (8 k): v[x][s] for
+  // k = ks*BK/KSL + 8h + 4g + s and row base + 32x + l32 (KC) or m/n
+  // base + 2*l32 + x (NC)
+  __device__ __forceinline__ static void frag(const float *lds, int ks, int base, int h, int l32,
+                                              int g, float (*v)[4]) {
     if constexpr (KC) {
 #pragma unroll
       for (int x = 0; x < 2; x++) {
-        const int R = 32 * x + l32;
-        const int slot = (wave * (BK / (4 * NW)) + 2 * h + g) ^ swz(R);
+        const int R = base + 32 * x + l32;
+        const int slot = (ks * (BK / (4 * KSL)) + 2 * h + g) ^ swz(R);
         const float4 t = *reinterpret_cast<const float4 *>(lds + R * BK + 4 * slot);
         v[x][0] = t.x; v[x][1] = t.y; v[x][2] = t.z; v[x][3] = t.w;
       }
@@ -986,36 +990,41 @@ struct MidOperand {
 #pragma unroll
       for (int s = 0; s < 4; s++) {
         const float2 t = *reinterpret_cast<const float2 *>(
-            lds + (wave * (BK / NW) + 8 * h + 4 * g + s) * M_T + 2 * l32);
+            lds + (ks * (BK / KSL) + 8 * h + 4 * g + s) * T + base + 2 * l32);
         v[0][s] = t.x; v[1][s] = t.y;
       }
     }
   }
 };
 
-template <bool A_KC, bool B_NC, int BK, int S, int NW>
+// ROWS: rows of A per tile (64, or 256 for tall operands with few columns:
+// four 64-row blocks share each tile of B); NWK: waves per K tile.  Wave w
+// owns row block w / NWK and k slice w % NWK.
+template <bool A_KC, bool B_NC, int BK, int S, int NW, int ROWS = M_T, int NWK = NW>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4, 2)))
 gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
                 const float *__restrict__ B, long ldb, float *__restrict__ C, long ldc,
                 long split_stride, int kchunk, bool cvec, int alim, int blim) {
   static_assert(S >= 3, "the pipeline needs three stages");
   constexpr int NTH = 64 * NW;
-  constexpr int OPS = M_T * BK;  // floats per operand per stage
-  constexpr int STAGE = 2 * OPS;
+  static_assert(ROWS % M_T == 0 && NW == (ROWS / M_T) * NWK, "waves = row blocks x k slices");
+  constexpr int OPA = ROWS * BK, OPB = M_T * BK;  // floats per operand per stage
+  constexpr int STAGE = OPA + OPB;
   constexpr int PIPE = S * STAGE, RED = NW * M_T * M_RLD;
-  constexpr int KSUB = BK / (8 * NW);  // 8-k sub-slices per wave per tile
+  constexpr int KSUB = BK / (8 * NWK);  // 8-k sub-slices per wave per tile
   static_assert(KSUB >= 1, "tile too shallow for the waves");
   __shared__ __attribute__((aligned(16))) float smem[PIPE > RED ? PIPE : RED];
-  using OA = MidOperand<A_KC, BK, NW>;
-  using OB = MidOperand<!B_NC, BK, NW>;
+  using OA = MidOperand<A_KC, BK, NW, ROWS, NWK>;
+  using OB = MidOperand<!B_NC, BK, NW, M_T, NWK>;
   constexpr int NL = OA::NL + OB::NL;  // loads per wave per tile
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int g = lane >> 5;
+  const int rb = wave / NWK, ks = wave % NWK;  // row block, k slice
 
-  const int tiles_m = (M + M_T - 1) / M_T, tiles_n = (N + M_T - 1) / M_T;
+  const int tiles_m = (M + ROWS - 1) / ROWS, tiles_n = (N + M_T - 1) / M_T;
   const int ntiles = tiles_m * tiles_n;
   int pid = blockIdx.x;
   if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
@@ -1024,7 +1033,7 @@ gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
   const int gsz = min(tiles_m - first_m, GROUP_M);
   const int tm = first_m + (pid % group) % gsz;
   const int tn = (pid % group) / gsz;
-  const long m0 = (long)tm * M_T;
+  const long m0 = (long)tm * ROWS;
   const long n0 = (long)tn * M_T;
   const int kbeg = blockIdx.z * kchunk;
   const int kend = min(K, kbeg + kchunk);
@@ -1057,14 +1066,14 @@ gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
       for (int j = 0; j < NL; j++) {
         if (j < j0 || j >= j0 + nj) continue;
         if (j < OA::NL) opa.issue(j, oa, st);
-        else opb.issue(j - OA::NL, ob, st + OPS);
+        else opb.issue(j - OA::NL, ob, st + OPA);
       }
     } else {
 #pragma unroll
       for (int j = 0; j < NL; j++) {
         if (j < j0 || j >= j0 + nj) continue;
         if (j < OA::NL) opa.issue_tail(j, oa, k0, kend, st);
-        else opb.issue_tail(j - OA::NL, ob, k0, kend, st + OPS);
+        else opb.issue_tail(j - OA::NL, ob, k0, kend, st + OPA);
       }
     }
   };
@@ -1072,8 +1081,8 @@ gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
     const float *st = smem + (kt % S) * STAGE;
 #pragma unroll
     for (int h = 0; h < KSUB; h++) {
-      OA::frag(st, wave, h, l32, g, a[h]);
-      OB::frag(st + OPS, wave, h, l32, g, b[h]);
+      OA::frag(st, ks, rb * M_T, h, l32, g, a[h]);
+      OB::frag(st + OPA, ks, 0, h, l32, g, b[h]);
     }
   };
   auto mfma4 = [&](float (*ca)[2][4], float (*cb)[2][4], int h, int s) {
@@ -1126,7 +1135,8 @@ gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
   }
 
   // wave sums -> LDS (acc r of block (x, y): row 8*(r/4) + 4g + r%4 of the
-  // block), then each thread adds the NW wave sums of its outputs in order
+  // block), then each thread adds the NWK k-slice sums of its outputs in
+  // order
   __syncthreads();
   float *red = smem + wave * (M_T * M_RLD);
 #pragma unroll
@@ -1144,15 +1154,17 @@ gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
     }
   __syncthreads();
 #pragma unroll
-  for (int f0 = 0; f0 < M_T * M_T / 4; f0 += NTH) {
+  for (int f0 = 0; f0 < ROWS * M_T / 4; f0 += NTH) {
     const int f = f0 + tid;  // float4 index: row f / 16, columns 4 * (f % 16) ..
-    const int m = f >> 4, n = 4 * (f & 15);
-    const long row = m0 + m;
+    const int mr = f >> 4, n = 4 * (f & 15);
+    const int fb = mr / M_T, m = mr - fb * M_T;  // row block, row in it
+    const long row = m0 + mr;
     if (row >= M) continue;
-    float4 v = *reinterpret_cast<const float4 *>(smem + m * M_RLD + n);
+    const float *rb0 = smem + (fb * NWK) * (M_T * M_RLD) + m * M_RLD + n;
+    float4 v = *reinterpret_cast<const float4 *>(rb0);
 #pragma unroll
-    for (int w = 1; w < NW; w++) {
-      const float4 t = *reinterpret_cast<const float4 *>(smem + w * (M_T * M_RLD) + m * M_RLD + n);
+    for (int w = 1; w < NWK; w++) {
+      const float4 t = *reinterpret_cast<const float4 *>(rb0 + w * (M_T * M_RLD));
       v.x += t.x; v.y += t.y; v.z += t.z; v.w += t.w;
     }
     float *crow = C + row * ldc;
@@ -1390,7 +1402,13 @@ int run_mid(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ld
   // workgroups per CU
   const int alim = A_KC ? M : (pad_a ? (M + 3) / 4 * 4 : M);
   const int blim = !B_NC ? N : (pad_b ? (N + 3) / 4 * 4 : N);
-  if (tiles * splits <= CUS)
+  const long tiles256 = (long)((M + 255) / 256) * ((N + M_T - 1) / M_T);
+  if (N <= M_T && splits == 1 && tiles256 >= CUS)
+    // tall: 256-row tiles, the 64 columns of B loaded once for four row blocks
+    hipLaunchKernelGGL((gemm_mid_kernel<A_KC, B_NC, 32, 4, 8, 256, 2>), dim3((unsigned)tiles256),
+                       dim3(512), 0, stream(), M, N, K, A.p, A.ld, B.p, B.ld, target, tld,
+                       sstride, kc, cvec, alim, blim);
+  else if (tiles * splits <= CUS)
     hipLaunchKernelGGL((gemm_mid_kernel<A_KC, B_NC, 64, 4, 8>), grid, dim3(512), 0, stream(), M,
                        N, K, A.p, A.ld, B.p, B.ld, target, tld, sstride, kc, cvec, alim, blim);
   else
