@@ -475,22 +475,100 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
         acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t], bm, acc[j], 0, 0, 0);
       }
   };
-  // two operand sets in turn: a channel's operands are read a whole channel
-  // before its MFMAs (a read past the last channel re-reads the last one)
-  float a0[TAPS], b0[TAPS][PB], a1[TAPS], b1[TAPS][PB];
-  if (steps > 0) load(0, a0, b0);
-  int c = 0;
-  for (; c + 1 < steps; c += 2) {
-    load(c + 1, a1, b1);
-    __builtin_amdgcn_sched_barrier(0);
-    mfmas(a0, b0);
-    __builtin_amdgcn_sched_barrier(0);
-    load(c + 2 < steps ? c + 2 : c + 1, a0, b0);
-    __builtin_amdgcn_sched_barrier(0);
-    mfmas(a1, b1);
-    __builtin_amdgcn_sched_barrier(0);
+  if (!FLIP && steps % 4 == 0) {
+    // Forward weights of four channels at a time: 4*TAPS floats per lane as
+    // 16-byte reads (row stride KST = 4 mod 32: eight lanes cover all banks,
+    // where single-float reads of 32 rows fall on 8 banks), a quad ahead.
+    // The slab operands alternate two sets a channel ahead as below.
+    constexpr int NV = TAPS;  // 16-byte vectors per quad (4 * TAPS floats)
+    const int quads = steps / 4;
+    auto loadw = [&](int q, f32x4 (&wv)[NV]) {
+      const f32x4 *p = (const f32x4 *)(wa + q * 4 * TAPS);
+#pragma unroll
+      for (int i = 0; i < NV; i++) wv[i] = p[i];
+    };
+    auto loadb = [&](int c, float (&b)[TAPS][PB]) {
+      const int cb = c * RW;
+#pragma unroll
+      for (int j = 0; j < PB; j++)
+#pragma unroll
+        for (int kh = 0; kh < KH; kh++) {
+          const float *row = xs + bj[j] + cb + kh * RS;
+#pragma unroll
+          for (int kw = 0; kw < KW; kw++) b[kh * KW + kw][j] = row[kw];
+        }
+    };
+    auto mfq = [&](const f32x4 (&wv)[NV], const int cc, const float (&b)[TAPS][PB]) {
+#pragma unroll
+      for (int t = 0; t < TAPS; t++)
+#pragma unroll
+        for (int j = 0; j < PB; j++) {
+          const int e = cc * TAPS + t;
+          const float bm = VEC || mk[j][t % KW] ? b[t][j] : 0.0f;
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(wv[e >> 2][e & 3], bm, acc[j], 0, 0, 0);
+        }
+    };
+    f32x4 w0[NV], w1[NV];
+    float b0[TAPS][PB], b1[TAPS][PB];
+    loadw(0, w0);
+    loadb(0, b0);
+    for (int q = 0; q < quads; q += 2) {
+      const int c = 4 * q;
+      const int cl = steps - 1;
+      loadw(q + 1 < quads ? q + 1 : q, w1);
+      loadb(c + 1, b1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfq(w0, 0, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      loadb(c + 2, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      mfq(w0, 1, b1);
+      __builtin_amdgcn_sched_barrier(0);
+      loadb(c + 3, b1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfq(w0, 2, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      loadb(c + 4 < cl ? c + 4 : cl, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      mfq(w0, 3, b1);
+      __builtin_amdgcn_sched_barrier(0);
+      if (q + 1 >= quads) break;
+      loadw(q + 2 < quads ? q + 2 : q + 1, w0);
+      loadb(c + 5, b1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfq(w1, 0, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      loadb(c + 6, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      mfq(w1, 1, b1);
+      __builtin_amdgcn_sched_barrier(0);
+      loadb(c + 7, b1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfq(w1, 2, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      loadb(c + 8 < cl ? c + 8 : cl, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      mfq(w1, 3, b1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+    // two operand sets in turn: a channel's operands are read a whole channel
+    // before its MFMAs (a read past the last channel re-reads the last one)
+    float a0[TAPS], b0[TAPS][PB], a1[TAPS], b1[TAPS][PB];
+    if (steps > 0) load(0, a0, b0);
+    int c = 0;
+    for (; c + 1 < steps; c += 2) {
+      load(c + 1, a1, b1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(a0, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      load(c + 2 < steps ? c + 2 : c + 1, a0, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(a1, b1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (c < steps) mfmas(a0, b0);
   }
-  if (c < steps) mfmas(a0, b0);
 
   float bv[16];
 #pragma unroll
