@@ -115,14 +115,14 @@ inline __host__ __device__ int round_up(int v, int m) { return (v + m - 1) / m *
 // Copy T floats into LDS at dst, viewed as blocks of B floats: element j of
 // block b is src[b * bstride + j] when b < nb and jlo <= j < jhi, else 0.
 // VEC: 16-byte loads (B, bstride, jlo, jhi multiples of 4, src 16-byte
-// aligned); dst is then filled in whole 256-float runs.
-template <bool VEC>
+// aligned); dst is then filled in whole 256-float runs.  NTH threads take part.
+template <bool VEC, int NTH = NT>
 __device__ __forceinline__ void stage_blocks(float *dst, const float *__restrict__ src, int T,
                                              int B, int nb, long bstride, int jlo, int jhi) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const float rcpB = 1.0f / (float)B;
   constexpr int E = VEC ? 4 : 1;   // floats per lane per load
-  for (int base = wave * 64 * E; base < T; base += NT * E) {
+  for (int base = wave * 64 * E; base < T; base += NTH * E) {
     const int i = base + lane * E;
     const int b = fdiv(i, B, rcpB), j = i - b * B;
     const bool ok = i < T && b < nb && j >= jlo && j < jhi;
@@ -141,7 +141,7 @@ __host__ __device__ inline int slab_cs(int R, int W) { return R * W + 4; }
 
 // Slab of image n: channel blocks of CS floats (rows hs..hs+R-1 of x, those
 // outside [0, H) as zeros, then the pad), then the zero plane.
-template <bool VEC>
+template <bool VEC, int NTH = NT>
 __device__ __forceinline__ void stage_slab(float *xs, const float *__restrict__ x, const Geo &g,
                                            const Slab &s, int n) {
   const int hs = s.ho0 * g.sh - g.ph;
@@ -149,7 +149,7 @@ __device__ __forceinline__ void stage_slab(float *xs, const float *__restrict__ 
   const int rlo = hs < 0 ? -hs : 0;
   const int rhi = g.H - hs < s.R ? g.H - hs : s.R;
   const float *xn = x + (long)n * g.C * g.H * g.W + (long)hs * g.W;
-  stage_blocks<VEC>(xs, xn, (g.C + 1) * CS, CS, g.C, (long)g.H * g.W, rlo * g.W, rhi * g.W);
+  stage_blocks<VEC, NTH>(xs, xn, (g.C + 1) * CS, CS, g.C, (long)g.H * g.W, rlo * g.W, rhi * g.W);
 }
 
 // Gapped slab (weight gradient, 16-byte staging): every row of W floats sits
@@ -167,6 +167,7 @@ __host__ __device__ inline int gslab_gap(const Geo &g) {
 __host__ __device__ inline int gslab_rw(const Geo &g) { return g.W + gslab_gap(g); }
 __host__ __device__ inline int gslab_cs(int R, const Geo &g) { return R * gslab_rw(g) + 4; }
 
+template <int NTH = NT>
 __device__ __forceinline__ void stage_gslab(float *xs, const float *__restrict__ x, const Geo &g,
                                             const Slab &s, int n) {
   const int hs = s.ho0 * g.sh - g.ph;
@@ -176,7 +177,7 @@ __device__ __forceinline__ void stage_gslab(float *xs, const float *__restrict__
   const float rcpC = 1.0f / (float)CS, rcpR = 1.0f / (float)RW;
   const float *xn = x + (long)n * g.C * g.H * g.W;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  for (int base = wave * 256; base < T; base += NT * 4) {
+  for (int base = wave * 256; base < T; base += NTH * 4) {
     const int i = base + lane * 4;
     const int c = fdiv(i, CS, rcpC), rem = i - c * CS;
     const int slot = fdiv(rem, RW, rcpR), j = rem - slot * RW;
@@ -386,8 +387,12 @@ conv_fwd_lds_kernel(const float *__restrict__ x, const float *__restrict__ w,
 // computed once.  The main loop reads no tables and does almost no VALU
 // work.  Weights as in the generic kernel (forward rows of KST floats, FLIP
 // in the tensor's order).
-template <int PB, bool FLIP, bool VEC, int KH, int KW>
-__global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2)))
+//
+// KS = 2: eight waves, the second four taking the upper half of the channel
+// steps of the same pixels; their sums are added in LDS (the waves of a
+// workgroup that fills a CU's LDS then share each SIMD two ways).
+template <int PB, bool FLIP, bool VEC, int KH, int KW, int KS = 1>
+__global__ void __launch_bounds__(NT * KS) __attribute__((amdgpu_waves_per_eu(1, 2)))
 conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
                   const float *__restrict__ bias, float *__restrict__ out, Geo g, int chunks) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
@@ -412,16 +417,18 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
-  if constexpr (VEC) stage_gslab(xs, x, g, s, n);
-  else stage_slab<VEC>(xs, x, g, s, n);
+  const int pw4 = wave & 3, grp = wave >> 2;  // pixel blocks, channel-step group
+  constexpr int NTH = NT * KS;
+  if constexpr (VEC) stage_gslab<NTH>(xs, x, g, s, n);
+  else stage_slab<VEC, NTH>(xs, x, g, s, n);
   {
     if constexpr (FLIP)
-      stage_blocks<VEC>(ws, w + (long)f0 * TAPS, 2 * CH2 * 32 * TAPS, 32 * TAPS, g.C,
+      stage_blocks<VEC, NTH>(ws, w + (long)f0 * TAPS, 2 * CH2 * 32 * TAPS, 32 * TAPS, g.C,
                         (long)g.F * TAPS, 0, nf * TAPS);
     else if (VEC && g.K % 4 == 0)
-      stage_blocks<true>(ws, w + (long)f0 * g.K, 32 * KST, KST, nf, g.K, 0, g.K);
+      stage_blocks<true, NTH>(ws, w + (long)f0 * g.K, 32 * KST, KST, nf, g.K, 0, g.K);
     else  // rows of K floats not 16-byte aligned (K % 4 != 0): 4-byte loads
-      stage_blocks<false>(ws, w + (long)f0 * g.K, 32 * KST, KST, nf, g.K, 0, g.K);
+      stage_blocks<false, NTH>(ws, w + (long)f0 * g.K, 32 * KST, KST, nf, g.K, 0, g.K);
   }
   if (tid < 32) bs[tid] = (bias && f0 + tid < g.F) ? bias[f0 + tid] : 0.0f;
   dma_wait();
@@ -433,7 +440,7 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
   bool mk[PB][KW];
 #pragma unroll
   for (int j = 0; j < PB; j++) {
-    const int p = p0 + (wave * PB + j) * 32 + l32;
+    const int p = p0 + (pw4 * PB + j) * 32 + l32;
     // past the chunk: every tap masked (gapped: any in-slab pixel, the
     // output is not stored)
     int2 e = make_int2(VEC ? g.pw : 0, -(1 << 20));
@@ -450,7 +457,10 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
   const float *wa = FLIP ? ws + l32 * TAPS + half * CH2 * 32 * TAPS
                          : ws + l32 * KST + half * CH2 * TAPS;
   constexpr int WSTEP_FLIP = 32 * TAPS;
-  const int steps = CH2;
+  // this wave's channel steps [cs0, cs1): all of them, or one half each
+  // (KS = 2 needs CH2 even)
+  const int cs0 = grp * (CH2 / KS), cs1 = cs0 + CH2 / KS;
+  const int steps = cs1 - cs0;
   // operands of channel c+1 are read before the MFMAs of channel c
   auto load = [&](int c, float (&a)[TAPS], float (&b)[TAPS][PB]) {
     const float *wc = wa + c * (FLIP ? WSTEP_FLIP : TAPS);
@@ -475,13 +485,13 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
         acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t], bm, acc[j], 0, 0, 0);
       }
   };
-  if (!FLIP && steps % 4 == 0) {
+  if (!FLIP && steps % 4 == 0 && cs0 % 4 == 0) {
     // Forward weights of four channels at a time: 4*TAPS floats per lane as
     // 16-byte reads (row stride KST = 4 mod 32: eight lanes cover all banks,
     // where single-float reads of 32 rows fall on 8 banks), a quad ahead.
     // The slab operands alternate two sets a channel ahead as below.
     constexpr int NV = TAPS;  // 16-byte vectors per quad (4 * TAPS floats)
-    const int quads = steps / 4;
+    const int q0 = cs0 / 4, quads = cs1 / 4;
     auto loadw = [&](int q, f32x4 (&wv)[NV]) {
       const f32x4 *p = (const f32x4 *)(wa + q * 4 * TAPS);
 #pragma unroll
@@ -510,11 +520,11 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
     };
     f32x4 w0[NV], w1[NV];
     float b0[TAPS][PB], b1[TAPS][PB];
-    loadw(0, w0);
-    loadb(0, b0);
-    for (int q = 0; q < quads; q += 2) {
+    loadw(q0, w0);
+    loadb(cs0, b0);
+    for (int q = q0; q < quads; q += 2) {
       const int c = 4 * q;
-      const int cl = steps - 1;
+      const int cl = cs1 - 1;
       loadw(q + 1 < quads ? q + 1 : q, w1);
       loadb(c + 1, b1);
       __builtin_amdgcn_sched_barrier(0);
@@ -555,28 +565,47 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
     // two operand sets in turn: a channel's operands are read a whole channel
     // before its MFMAs (a read past the last channel re-reads the last one)
     float a0[TAPS], b0[TAPS][PB], a1[TAPS], b1[TAPS][PB];
-    if (steps > 0) load(0, a0, b0);
-    int c = 0;
-    for (; c + 1 < steps; c += 2) {
+    if (steps > 0) load(cs0, a0, b0);
+    int c = cs0;
+    for (; c + 1 < cs1; c += 2) {
       load(c + 1, a1, b1);
       __builtin_amdgcn_sched_barrier(0);
       mfmas(a0, b0);
       __builtin_amdgcn_sched_barrier(0);
-      load(c + 2 < steps ? c + 2 : c + 1, a0, b0);
+      load(c + 2 < cs1 ? c + 2 : c + 1, a0, b0);
       __builtin_amdgcn_sched_barrier(0);
       mfmas(a1, b1);
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (c < steps) mfmas(a0, b0);
+    if (c < cs1) mfmas(a0, b0);
   }
 
   float bv[16];
 #pragma unroll
   for (int r = 0; r < 16; r++) bv[r] = bs[8 * (r >> 2) + 4 * half + (r & 3)];
+  if constexpr (KS == 2) {
+    // the upper group's sums through LDS (every wave is past its last read
+    // of the operands at the first barrier), added in a fixed order
+    float *red = smem + pw4 * (PB * 16 * 64) + lane;
+    __syncthreads();
+    if (grp == 1) {
+#pragma unroll
+      for (int j = 0; j < PB; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) red[(j * 16 + r) * 64] = acc[j][r];
+    }
+    __syncthreads();
+    if (grp == 1) return;
+#pragma unroll
+    for (int j = 0; j < PB; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[j][r] += red[(j * 16 + r) * 64];
+  }
+
   float *on = out + (long)n * g.F * P;
 #pragma unroll
   for (int j = 0; j < PB; j++) {
-    const int p = p0 + (wave * PB + j) * 32 + l32;
+    const int p = p0 + (pw4 * PB + j) * 32 + l32;
     if (p >= p1) continue;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
@@ -1031,7 +1060,7 @@ bool allow_big_lds(const void *fn) {
 }
 
 struct FwdPlan {
-  int pb = 0, chunks = 0;
+  int pb = 0, chunks = 0, ks = 1;
   size_t lds = 0;
 };
 
@@ -1069,16 +1098,25 @@ FwdPlan plan_fwd(const Geo &g, int N, bool flip) {
     // gives every CU two workgroups
     if ((long)N * chunks * fblocks >= 512) break;
   }
+  // a workgroup that takes more than half the LDS runs alone on its CU: the
+  // 3x3 kernel then splits the channel steps over eight waves (two per SIMD)
+  // and adds the halves through LDS (PB x 16 KB, reusing the operands' space)
+  if (best.pb && is_k3(g) && ((g.C + 1) / 2) % 2 == 0 && best.lds > (size_t)LDS_MAX / 2 &&
+      best.lds >= (size_t)best.pb * 16384)
+    best.ks = 2;
   return best;
 }
 
 template <int PB, bool FLIP, bool VEC>
 int launch_fwd(const float *x, const float *w, const float *bias, float *out, const Geo &g, int N,
                const FwdPlan &pl) {
-  auto kern = is_k3(g) ? conv_fwd_k_kernel<PB, FLIP, VEC, 3, 3> : conv_fwd_lds_kernel<PB, FLIP, VEC>;
+  auto kern = !is_k3(g)     ? conv_fwd_lds_kernel<PB, FLIP, VEC>
+              : pl.ks == 2 ? conv_fwd_k_kernel<PB, FLIP, VEC, 3, 3, 2>
+                           : conv_fwd_k_kernel<PB, FLIP, VEC, 3, 3, 1>;
   if (pl.lds > 64 * 1024 && !allow_big_lds((const void *)kern)) return -1;
   const dim3 grid((unsigned)(N * pl.chunks), (unsigned)((g.F + 31) / 32));
-  hipLaunchKernelGGL(kern, grid, dim3(NT), pl.lds, stream(), x, w, bias, out, g, pl.chunks);
+  hipLaunchKernelGGL(kern, grid, dim3(NT * pl.ks), pl.lds, stream(), x, w, bias, out, g,
+                     pl.chunks);
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
