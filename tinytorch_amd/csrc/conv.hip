@@ -955,41 +955,46 @@ conv_dw32_kernel(const float *__restrict__ gr, const float *__restrict__ x,
   }
 }
 
-// Sum of the dw32 partials.  A workgroup takes XL consecutive partial
-// elements (coalesced) x ZL lanes: lane ty adds partials z = ty, ty+ZL, ...
-// in order, lane 0 adds the ZL sums in order, and writes the gradient entry
-// the element holds: block jb, accumulator r, lane l -> filter fb*32 +
-// 8(r/4) + 4(l/32) + r%4, tap jb*32 + l%32; the last 32 of a block -> bias.
+// Sum of the dw32 partials.  A workgroup takes XL consecutive groups of 4
+// partial elements (16-byte loads) x ZL lanes: lane ty adds partials z = ty,
+// ty+ZL, ... in order, lane 0 adds the ZL sums in order, and writes the
+// gradient entries the elements hold: block jb, accumulator r, lane l ->
+// filter fb*32 + 8(r/4) + 4(l/32) + r%4, tap jb*32 + l%32; the last 32 of a
+// block -> bias.  Partials are JB*1024 + 32 floats (a multiple of 4).
 template <int ZL>
 __global__ void __launch_bounds__(NT)
 conv_dw32_reduce_kernel(const float *__restrict__ part, float *__restrict__ dw,
                         float *__restrict__ db, int Z, int FBLK, int JB, int F, int K) {
   constexpr int XL = NT / ZL;
-  __shared__ float sums[ZL][XL];
+  __shared__ f32x4 sums[ZL][XL];
   const int tx = threadIdx.x % XL, ty = threadIdx.x / XL;
   const int S = JB * 1024 + 32;
-  const long total = (long)FBLK * S;
-  const long e = (long)blockIdx.x * XL + tx;
-  float sum = 0.0f;
-  if (e < total) {
-    const float *p = part + e;
-#pragma unroll 4
-    for (int z = ty; z < Z; z += ZL) sum += p[(long)z * total];
+  const long total4 = (long)FBLK * S / 4;
+  const long e4 = (long)blockIdx.x * XL + tx;
+  f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (e4 < total4) {
+    const f32x4 *p = (const f32x4 *)part + e4;
+#pragma unroll 8
+    for (int z = ty; z < Z; z += ZL) sum += p[(long)z * total4];
   }
   sums[ty][tx] = sum;
   __syncthreads();
-  if (ty != 0 || e >= total) return;
+  if (ty != 0 || e4 >= total4) return;
   for (int j = 1; j < ZL; j++) sum += sums[j][tx];
-  const int fb = (int)(e / S), i = (int)(e - (long)fb * S);
-  if (i >= JB * 1024) {
-    const int f = fb * 32 + (i - JB * 1024);
-    if (db && f < F) db[f] = sum;
-    return;
+#pragma unroll
+  for (int u = 0; u < 4; u++) {
+    const long e = e4 * 4 + u;
+    const int fb = (int)(e / S), i = (int)(e - (long)fb * S);
+    if (i >= JB * 1024) {
+      const int f = fb * 32 + (i - JB * 1024);
+      if (db && f < F) db[f] = sum[u];
+      continue;
+    }
+    const int jb = i >> 10, r = (i >> 6) & 15, l = i & 63;
+    const int f = fb * 32 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+    const int k = jb * 32 + (l & 31);
+    if (f < F && k < K) dw[(long)f * K + k] = sum[u];
   }
-  const int jb = i >> 10, r = (i >> 6) & 15, l = i & 63;
-  const int f = fb * 32 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-  const int k = jb * 32 + (l & 31);
-  if (f < F && k < K) dw[(long)f * K + k] = sum;
 }
 
 // dw[f][k] = sum_z part[z][f][k] (k < K), db[f] = sum_z part[z][f][K]; ZL
@@ -1340,13 +1345,16 @@ extern "C" int tt_k_conv2d_dw_lds(const float *gr, const float *x, float *dw, fl
                : launch_dw_var<false>(gr, x, part, g, N, pl);
   if (rc == 0) {
     // lanes per output: enough workgroups to spread the partial reads
+    // (the dw32 reduction reads 4 floats a lane and keeps at least 8
+    // partials per lane: measured faster than more lanes with fewer loads)
     int zl = 1;
-    while (zl < 32 && zl < Z && total * zl * 2 <= 2048L * NT) zl *= 2;
+    const long units = d32 ? total / 4 : total;
+    while (zl < 32 && zl < Z && units * zl * 2 <= 2048L * NT && (!d32 || zl * 16 <= Z)) zl *= 2;
 #define TT_RED(ZL_)                                                                       \
   if (d32)                                                                                \
     hipLaunchKernelGGL(conv_dw32_reduce_kernel<ZL_>,                                      \
-                       dim3((unsigned)((total + NT / ZL_ - 1) / (NT / ZL_))), dim3(NT), 0, \
-                       stream(), part, dw, db, (int)Z, FBLK, JB32, F, g.K);               \
+                       dim3((unsigned)((total / 4 + NT / ZL_ - 1) / (NT / ZL_))), dim3(NT), \
+                       0, stream(), part, dw, db, (int)Z, FBLK, JB32, F, g.K);            \
   else                                                                                    \
     hipLaunchKernelGGL(conv_dw_reduce_kernel<ZL_>,                                        \
                        dim3((unsigned)((total + NT / ZL_ - 1) / (NT / ZL_))), dim3(NT), 0, \
