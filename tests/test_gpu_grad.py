@@ -214,6 +214,32 @@ def test_rules_vs_oracle_larger(Node):
     for n in (ny, nx, nw, nb_):
         n.release()
 
+    # relu -> 2x2 max pool: one fused backward when the relu feeds only the
+    # pool (the first call), the two separate steps when the relu feeds two
+    # pools or already holds a gradient (a second call accumulates, and the
+    # relu's backward then sees the accumulated gradient, as in the reference)
+    x = rng.integers(-2, 3, (3, 4, 9, 8)).astype(np.float32)
+    g = rng.standard_normal((3, 4, 4, 4)).astype(np.float32)
+    dr = orc.maxpool_bwd(orc.relu_fwd(x), g, 2, 2, 2, 2)
+    nx = Node.leaf(x)
+    nr = nx.relu()
+    ny = nr.maxpool2d(pool_size=2, stride=2)
+    ny.backward(g)
+    assert np.array_equal(nr.grad(), dr) and np.array_equal(nx.grad(), orc.relu_bwd(x, dr))
+    ny.backward(g)
+    dx2 = orc.relu_bwd(x, dr) + orc.relu_bwd(x, dr + dr)
+    assert np.array_equal(nr.grad(), dr + dr) and np.array_equal(nx.grad(), dx2)
+    for n in (ny, nr, nx):
+        n.release()
+    nx = Node.leaf(x)
+    nr = nx.relu()
+    n1, n2 = nr.maxpool2d(pool_size=2, stride=2), nr.maxpool2d(pool_size=2, stride=2)
+    ns = n1 + n2
+    ns.backward(g)
+    assert np.array_equal(nr.grad(), dr + dr) and np.array_equal(nx.grad(), orc.relu_bwd(x, dr + dr))
+    for n in (ns, n1, n2, nr, nx):
+        n.release()
+
     x = rng.integers(-2, 2, (3, 4, 9, 9)).astype(np.float32)
     nx = Node.leaf(x)
     acc = np.zeros_like(x)

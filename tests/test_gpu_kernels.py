@@ -195,6 +195,29 @@ def test_maxpool_bitexact(tlib, p, s):
     assert bits_equal(dgx.to_np(x.shape), orc.maxpool_bwd(x, g, p, p, s, s))
 
 
+@pytest.mark.parametrize("shape", [(3, 4, 9, 8), (2, 3, 8, 12)])
+def test_maxpool_relu_fused_bitexact(tlib, shape):
+    """The fused 2x2 pool + relu backward against the reference's two steps:
+    the pool's input r is relu(x); dr = maxpool backward, dx = relu backward
+    of dr evaluated on x (NaN, -0.0 and exact zeros in x; odd H leaves a row
+    the pool does not cover)."""
+    x = pool_input(shape)
+    x[0, 0, 4, :4] = [0.0, -0.0, 1e-30, -1e-30]
+    N, C, H, W = shape
+    Ho, Wo = orc.pool_out(H, W, 2, 2, 2, 2)
+    r = orc.relu_fwd(x)
+    g = u(N, C, Ho, Wo)
+    g[0, 0, 0, 0] = -0.0
+    dr_ref = orc.maxpool_bwd(r, g, 2, 2, 2, 2)
+    dx_ref = orc.relu_bwd(x, dr_ref)
+    dr_, dg, ddr, ddx = DevBuf.from_np(r), DevBuf.from_np(g), DevBuf(x.size), DevBuf(x.size)
+    print("maxpool+relu bwd", shape, flush=True)
+    check(tlib.tt_k_maxpool2x2_relu_bwd(dr_.ptr, dg.ptr, ddr.ptr, ddx.ptr, N, C, H, W, Ho, Wo),
+          "maxpool2x2_relu_bwd")
+    assert bits_equal(ddr.to_np(shape), dr_ref)
+    assert bits_equal(ddx.to_np(shape), dx_ref)
+
+
 @pytest.mark.parametrize("p,s", POOL_CASES)
 def test_avgpool_bitexact(tlib, p, s):
     x = u(2, 3, 9, 8)

@@ -136,6 +136,7 @@ SIGNATURES = [
     ("tt_k_bias_grad", _I, [VP, VP, _I, _I, _I]),
     ("tt_k_maxpool_fwd", _I, [VP, VP] + [_I] * 10),
     ("tt_k_maxpool_bwd", _I, [VP, VP, VP] + [_I] * 10),
+    ("tt_k_maxpool2x2_relu_bwd", _I, [VP, VP, VP, VP] + [_I] * 6),
     ("tt_k_avgpool_fwd", _I, [VP, VP] + [_I] * 10),
     ("tt_k_avgpool_bwd", _I, [VP, VP] + [_I] * 10),
     ("tt_k_sgd", _I, [VP, VP, _L, _F]),

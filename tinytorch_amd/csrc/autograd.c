@@ -40,6 +40,8 @@ struct AGNode {
     int     params[4];
     int     requires_grad;
     int     mark;        /* DFS state: 0 new, 1 on stack, 2 done */
+    int     uses;        /* backward: edges from nodes of this pass to this node */
+    int     grad_done;   /* backward: this relu's backward already ran fused */
     int     refcount;
     float  *col;         /* conv2d: forward im2col matrix (device) */
     int     col_ones;    /* conv2d: col carries the extra row of ones */
@@ -488,6 +490,31 @@ static void backward_conv2d(AGNode *n) {
     }
 }
 
+/* A 2x2 / stride-2 max pool whose input is a relu used by nothing else
+ * (whose gradient is therefore complete after the pool's backward) runs
+ * both backwards in one pass: the relu's gradient is written as usual and
+ * its input's gradient from the same registers, so the relu node's own step
+ * is skipped.  Only when the relu's gradient starts empty and its input has
+ * no other consumer, so every gradient gets the same sums in the same order
+ * as with the two steps. */
+static int backward_maxpool_relu(AGNode *n, AGNode *r, const float *g, const float *x, int N,
+                                 int C, int H, int W, int Ho, int Wo) {
+    AGNode *in = r->parents[0];
+    if (r->kind != OP_RELU || r->uses != 1 || r->grad || !needs(in) || in->uses != 1 ||
+        n->params[0] != 2 || n->params[1] != 2 || n->params[2] != 2 || n->params[3] != 2)
+        return 0;
+    Tensor *t = tt_empty_like(r->val), *u = t ? tt_empty_like(in->val) : NULL;
+    if (!u || tt_k_maxpool2x2_relu_bwd(x, g, t->dev, u->dev, N, C, H, W, Ho, Wo)) {
+        tt_release(t);
+        tt_release(u);
+        return 0;
+    }
+    accum_move(r, t);
+    accum_move(in, u);
+    r->grad_done = 1;
+    return 1;
+}
+
 static void backward_pool(AGNode *n, int is_max) {
     AGNode *a = n->parents[0];
     if (!needs(a)) return;
@@ -498,6 +525,7 @@ static void backward_pool(AGNode *n, int is_max) {
     const float *g = tt_dev(n->grad);
     const float *x = is_max ? tt_dev(a->val) : NULL;
     if (!g || (is_max && !x)) return;
+    if (is_max && backward_maxpool_relu(n, a, g, x, N, C, H, W, Ho, Wo)) return;
     Tensor *t = tt_empty_like(a->val);
     if (!t) return;
     int rc = is_max ? tt_k_maxpool_bwd(x, g, t->dev, N, C, H, W, ph, pw, sh, sw, Ho, Wo)
@@ -583,7 +611,10 @@ static void propagate(NodeList *order) {
             case OP_ADDSCALAR:  backward_addscalar(n); break;
             case OP_MULSCALAR:  backward_mulscalar(n); break;
             case OP_MATMUL:     backward_matmul(n); break;
-            case OP_RELU:       backward_relu(n); break;
+            case OP_RELU:
+                if (n->grad_done) n->grad_done = 0;
+                else backward_relu(n);
+                break;
             case OP_SOFTMAX:    backward_softmax(n); break;
             case OP_PADONES:    backward_padones(n); break;
             case OP_RESHAPE:    backward_reshape(n); break;
@@ -604,6 +635,9 @@ static void backward_impl(AGNode *out, int seed_kind, const float *hseed, const 
         free(order.items);
         return;  /* marks of nodes still on the stack stay set only on OOM */
     }
+    for (size_t i = 0; i < order.len; i++) order.items[i]->uses = 0;
+    for (size_t i = 0; i < order.len; i++)
+        for (int j = 0; j < order.items[i]->nparents; j++) order.items[i]->parents[j]->uses++;
     if (!out->grad) out->grad = tt_empty_like(out->val);
     if (out->grad) {
         int rc;
@@ -616,7 +650,7 @@ static void backward_impl(AGNode *out, int seed_kind, const float *hseed, const 
         tt_mark_dev_written(out->grad);
         if (rc == 0) propagate(&order);
     }
-    for (size_t i = 0; i < order.len; i++) order.items[i]->mark = 0;
+    for (size_t i = 0; i < order.len; i++) order.items[i]->mark = order.items[i]->grad_done = 0;
     free(order.items);
 }
 

@@ -228,10 +228,13 @@ __device__ __forceinline__ void argmax4(float v0, float v1, float v2, float v3, 
   if (v3 > m) { m = v3; am = 3; }
 }
 
-template <typename I>
+// RELU: x is the output of a relu whose only consumer is this pool; dxr =
+// relu backward of dx (dx where x > 0, else +0.0f) is written in the same
+// pass (x > 0 exactly when the relu's input is > 0).
+template <typename I, bool RELU = false>
 __global__ void maxpool2x2_bwd_kernel(const float *__restrict__ x, const float *__restrict__ g,
                                       float *__restrict__ dx, int H, int W, int Ho, int Wo,
-                                      I total) {
+                                      I total, float *__restrict__ dxr = nullptr) {
   const int Wq = Wo / 2;
   const I stride = (I)gridDim.x * blockDim.x;
   for (I i = (I)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
@@ -251,6 +254,14 @@ __global__ void maxpool2x2_bwd_kernel(const float *__restrict__ x, const float *
     float4 bot = make_float4(am0 == 2 ? g0 : 0.0f, am0 == 3 ? g0 : 0.0f, am1 == 2 ? g1 : 0.0f, am1 == 3 ? g1 : 0.0f);
     *reinterpret_cast<float4 *>(dx + off) = top;
     *reinterpret_cast<float4 *>(dx + off + W) = bot;
+    if constexpr (RELU) {
+      const float4 rt = make_float4(a.x > 0.0f ? top.x : 0.0f, a.y > 0.0f ? top.y : 0.0f,
+                                    a.z > 0.0f ? top.z : 0.0f, a.w > 0.0f ? top.w : 0.0f);
+      const float4 rb = make_float4(b.x > 0.0f ? bot.x : 0.0f, b.y > 0.0f ? bot.y : 0.0f,
+                                    b.z > 0.0f ? bot.z : 0.0f, b.w > 0.0f ? bot.w : 0.0f);
+      *reinterpret_cast<float4 *>(dxr + off) = rt;
+      *reinterpret_cast<float4 *>(dxr + off + W) = rb;
+    }
   }
 }
 
@@ -556,6 +567,31 @@ int tt_k_maxpool_fwd(const float *x, float *y, int N, int C, int H, int W, int p
     return launched();
   }
   TT_LAUNCH_I(maxpool_fwd_kernel, total, x, y, N, C, H, W, ph, pw, sh, sw, Ho, Wo);
+  return launched();
+}
+
+// 2x2 / stride-2 max pool backward fused with the backward of the relu that
+// produced its input: dx = pool backward (as tt_k_maxpool_bwd), dxr = dx
+// where x > 0 else +0.0f.  -1 when the shape or alignment does not fit the
+// 2x2 kernel (the caller then runs the two backwards separately).
+int tt_k_maxpool2x2_relu_bwd(const float *x, const float *g, float *dx, float *dxr, int N, int C,
+                             int H, int W, int Ho, int Wo) {
+  const long total = (long)N * C * H * W;
+  if (total <= 0) return 0;
+  if (W % 4 != 0 || Ho != H / 2 || Wo != W / 2 || (((uintptr_t)x & 15) != 0) ||
+      (((uintptr_t)dx & 15) != 0) || (((uintptr_t)dxr & 15) != 0) || (((uintptr_t)g & 7) != 0))
+    return -1;
+  const long pairs = (long)N * C * Ho * Wo / 2;
+  if (pairs < (1L << 31))
+    hipLaunchKernelGGL((maxpool2x2_bwd_kernel<unsigned, true>), dim3(blocks_for(pairs)), dim3(256),
+                       0, stream(), x, g, dx, H, W, Ho, Wo, (unsigned)pairs, dxr);
+  else
+    hipLaunchKernelGGL((maxpool2x2_bwd_kernel<unsigned long, true>), dim3(blocks_for(pairs)),
+                       dim3(256), 0, stream(), x, g, dx, H, W, Ho, Wo, (unsigned long)pairs, dxr);
+  if (2 * Ho < H) {
+    TT_LAUNCH_I(pool_uncovered_zero_kernel, total, dx, N, C, H, W, 2 * Ho, 2 * Wo);
+    TT_LAUNCH_I(pool_uncovered_zero_kernel, total, dxr, N, C, H, W, 2 * Ho, 2 * Wo);
+  }
   return launched();
 }
 
