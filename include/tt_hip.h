@@ -111,6 +111,11 @@ int tt_k_softmax_ce_mean(const float *logits, const int32_t *labels, float *prob
 int tt_k_scale_by_dev(const float *x, const float *s, float *y, long n);
 int tt_k_padones_fwd(const float *x, float *y, long M, long K);      /* src/autograd.c:195-212 */
 int tt_k_padones_bwd(const float *g, float *dx, long M, long K);     /* src/autograd.c:348-359 */
+/* padones backward and the backward of the relu whose output r (M x K) was
+ * padded, in one pass: dr = g without its last column, dx = dr where r > 0
+ * else +0.0f (src/autograd.c:348-359 followed by src/autograd.c:318-327 of
+ * the reference).  -1: M >= 65536 (the caller runs the two steps). */
+int tt_k_padones_relu_bwd(const float *g, const float *r, float *dr, float *dx, long M, long K);
 int tt_k_im2col(const float *x, float *col, int N, int C, int H, int W,
                 int HH, int WW, int sh, int sw, int ph, int pw, int Ho, int Wo);  /* src/ops_spatial.c:37-69 */
 /* im2col followed by a row of Ncol ones (col has Kc + 1 rows) */

@@ -240,6 +240,21 @@ def test_rules_vs_oracle_larger(Node):
     for n in (ns, n1, n2, nr, nx):
         n.release()
 
+    # relu -> padones: fused backward on the first call, two steps after
+    x = rng.integers(-2, 3, (6, 7)).astype(np.float32)
+    g = rng.standard_normal((6, 8)).astype(np.float32)
+    dr = orc.padones_bwd(g)
+    nx = Node.leaf(x)
+    nr = nx.relu()
+    ny = nr.padones()
+    ny.backward(g)
+    assert np.array_equal(nr.grad(), dr) and np.array_equal(nx.grad(), orc.relu_bwd(x, dr))
+    ny.backward(g)
+    dx2 = orc.relu_bwd(x, dr) + orc.relu_bwd(x, dr + dr)
+    assert np.array_equal(nr.grad(), dr + dr) and np.array_equal(nx.grad(), dx2)
+    for n in (ny, nr, nx):
+        n.release()
+
     x = rng.integers(-2, 2, (3, 4, 9, 9)).astype(np.float32)
     nx = Node.leaf(x)
     acc = np.zeros_like(x)

@@ -282,6 +282,21 @@ def test_padones_bitexact(tlib, M, K):
     assert bits_equal(ddx.to_np((M, K)), orc.padones_bwd(g))
 
 
+@pytest.mark.parametrize("M,K", [(1, 1), (256, 512), (3, 1030)])
+def test_padones_relu_fused_bitexact(tlib, M, K):
+    """The fused padones + relu backward against the reference's two steps
+    (relu backward evaluated on the relu's input x: NaN, -0.0, exact zeros)."""
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x.flat[: min(4, x.size)] = [0.0, -0.0, np.nan, 1e-38][: min(4, x.size)]
+    r = orc.relu_fwd(x)
+    g = u(M, K + 1)
+    dr_ref = orc.padones_bwd(g)
+    dr_, dg, ddr, ddx = DevBuf.from_np(r), DevBuf.from_np(g), DevBuf(M * K), DevBuf(M * K)
+    check(tlib.tt_k_padones_relu_bwd(dg.ptr, dr_.ptr, ddr.ptr, ddx.ptr, M, K), "padones_relu_bwd")
+    assert bits_equal(ddr.to_np((M, K)), dr_ref)
+    assert bits_equal(ddx.to_np((M, K)), orc.relu_bwd(x, dr_ref))
+
+
 @pytest.mark.parametrize("N,F,HW", [(1, 1, 1), (2, 4, 49), (128, 32, 1024), (128, 64, 256)])
 def test_bias_grad(tlib, N, F, HW):
     g = rng.standard_normal((N, F, HW)).astype(np.float32)

@@ -352,11 +352,39 @@ static void backward_softmax(AGNode *n) {
     accum_move(a, t);
 }
 
+/* A node whose backward can also run the backward of the relu r feeding it
+ * in the same pass: r is used by nothing else in this pass (its gradient is
+ * complete once this node's backward has run), starts with no gradient, and
+ * its input needs one and has no other consumer -- so every gradient gets
+ * the same sums in the same order as with two separate steps. */
+static int relu_fusable(const AGNode *r) {
+    return r->kind == OP_RELU && r->uses == 1 && !r->grad && needs(r->parents[0]) &&
+           r->parents[0]->uses == 1;
+}
+
+/* hand the fused pass's two gradients to the relu and its input */
+static void fused_relu_done(AGNode *r, Tensor *dr, Tensor *dx) {
+    accum_move(r, dr);
+    accum_move(r->parents[0], dx);
+    r->grad_done = 1;
+}
+
 static void backward_padones(AGNode *n) {
     AGNode *a = n->parents[0];
     if (!needs(a)) return;
     const float *g = tt_dev(n->grad);
     if (!g) return;
+    if (relu_fusable(a)) {
+        const float *r = tt_dev(a->val);
+        Tensor *t = r ? tt_empty_like(a->val) : NULL, *u = t ? tt_empty_like(a->val) : NULL;
+        if (u && tt_k_padones_relu_bwd(g, r, t->dev, u->dev, a->val->shape[0],
+                                       a->val->shape[1]) == 0) {
+            fused_relu_done(a, t, u);
+            return;
+        }
+        tt_release(t);
+        tt_release(u);
+    }
     Tensor *t = tt_empty_like(a->val);
     if (!t) return;
     if (tt_k_padones_bwd(g, t->dev, a->val->shape[0], a->val->shape[1])) {
@@ -490,28 +518,20 @@ static void backward_conv2d(AGNode *n) {
     }
 }
 
-/* A 2x2 / stride-2 max pool whose input is a relu used by nothing else
- * (whose gradient is therefore complete after the pool's backward) runs
- * both backwards in one pass: the relu's gradient is written as usual and
- * its input's gradient from the same registers, so the relu node's own step
- * is skipped.  Only when the relu's gradient starts empty and its input has
- * no other consumer, so every gradient gets the same sums in the same order
- * as with the two steps. */
+/* A 2x2 / stride-2 max pool whose input is a fusable relu (relu_fusable)
+ * runs both backwards in one pass; the relu node's own step is skipped. */
 static int backward_maxpool_relu(AGNode *n, AGNode *r, const float *g, const float *x, int N,
                                  int C, int H, int W, int Ho, int Wo) {
-    AGNode *in = r->parents[0];
-    if (r->kind != OP_RELU || r->uses != 1 || r->grad || !needs(in) || in->uses != 1 ||
-        n->params[0] != 2 || n->params[1] != 2 || n->params[2] != 2 || n->params[3] != 2)
+    if (!relu_fusable(r) || n->params[0] != 2 || n->params[1] != 2 || n->params[2] != 2 ||
+        n->params[3] != 2)
         return 0;
-    Tensor *t = tt_empty_like(r->val), *u = t ? tt_empty_like(in->val) : NULL;
+    Tensor *t = tt_empty_like(r->val), *u = t ? tt_empty_like(r->parents[0]->val) : NULL;
     if (!u || tt_k_maxpool2x2_relu_bwd(x, g, t->dev, u->dev, N, C, H, W, Ho, Wo)) {
         tt_release(t);
         tt_release(u);
         return 0;
     }
-    accum_move(r, t);
-    accum_move(in, u);
-    r->grad_done = 1;
+    fused_relu_done(r, t, u);
     return 1;
 }
 

@@ -267,6 +267,21 @@ __global__ void padones_bwd_rows_kernel(const float *__restrict__ g, float *__re
     dr[k] = gr[k];
 }
 
+// padones backward fused with the backward of the relu whose output r is
+// the padded tensor: dr = g without its last column, dx = dr where r > 0
+// (r > 0 exactly when the relu's input is > 0), else +0.0f.
+__global__ void padones_relu_bwd_rows_kernel(const float *__restrict__ g, const float *__restrict__ r,
+                                             float *__restrict__ dr, float *__restrict__ dx, int K) {
+  const long m = blockIdx.y;
+  const float *gr = g + m * (K + 1);
+  const long o = m * K;
+  for (int k = blockIdx.x * 1024 + threadIdx.x; k < K && k < (int)(blockIdx.x + 1) * 1024; k += 256) {
+    const float v = gr[k];
+    dr[o + k] = v;
+    dx[o + k] = r[o + k] > 0.0f ? v : 0.0f;
+  }
+}
+
 // Fused softmax + cross-entropy for up to a few thousand rows in ONE
 // workgroup: probabilities, the seed (p - onehot(y)) * scale and the mean
 // loss, reduced in a fixed order (per-thread row order, then the thread
@@ -536,6 +551,14 @@ int tt_k_padones_fwd(const float *x, float *y, long M, long K) {
     hipLaunchKernelGGL(padones_fwd_kernel<unsigned>, dim3(grid_for(total, 1)), dim3(256), 0, stream(), x, y, M, K);
   else
     hipLaunchKernelGGL(padones_fwd_kernel<unsigned long>, dim3(grid_for(total, 1)), dim3(256), 0, stream(), x, y, M, K);
+  return launched();
+}
+
+int tt_k_padones_relu_bwd(const float *g, const float *r, float *dr, float *dx, long M, long K) {
+  if (M <= 0 || K <= 0) return 0;
+  if (M >= 65536 || K >= (1L << 30)) return -1;
+  hipLaunchKernelGGL(padones_relu_bwd_rows_kernel, dim3((unsigned)((K + 1023) / 1024), (unsigned)M),
+                     dim3(256), 0, stream(), g, r, dr, dx, (int)K);
   return launched();
 }
 
