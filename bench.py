@@ -18,7 +18,8 @@ of the fp32 MFMA peak, plus the CNN forward+backward step time.
     8192^3, ragged, tall-skinny, MLP step); extra.conv_kernels: the direct
     convolution kernels of the CNN step alone (TFLOP/s vs the MFMA peak);
     extra.hbm_kernels: the bandwidth kernels (im2col/col2im serve only the
-    convolutions whose input slab does not fit LDS).
+    convolutions whose input slab does not fit LDS; the step runs the pool
+    and relu backwards as the one maxpool_relu_bwd pass).
   * cpu_baseline: the reference's own AVX2+FMA OpenMP sgemm, compiled from
     its sources into oracle/_ref (or the oracle restatement when that build
     is missing), on this host's cores, on a bounded sample (median of 3 runs
@@ -305,6 +306,12 @@ def bandwidth_kernels(L, reps=50):
             4 * (n + no))
         run(f"maxpool_bwd_{tag}", lambda: L.tt_k_maxpool_bwd(a.ptr, p.ptr, y.ptr, B, F, H, H, 2, 2, 2, 2, Ho, Ho),
             4 * (2 * n + no))
+        # the step's form: pool and relu backward in one pass (a = relu output)
+        y2 = DevBuf(n)
+        run(f"maxpool_relu_bwd_{tag}",
+            lambda: L.tt_k_maxpool2x2_relu_bwd(a.ptr, p.ptr, y.ptr, y2.ptr, B, F, H, H, Ho, Ho),
+            4 * (3 * n + no))
+        y2.free()
         db = DevBuf(F)
         run(f"bias_grad_{tag}", lambda: L.tt_k_bias_grad(g.ptr, db.ptr, B, F, H * H), 4 * (n + F))
         for bb in (x, col, a, g, y, p, db):
