@@ -66,6 +66,11 @@ int tth_gemm_direct(int on);
  * used for plain GEMMs too small for 128x128 tiles on every CU (and for
  * ragged or unaligned operands); a forced tile (tth_gemm_config) bypasses it. */
 int tth_gemm_mid(int on);
+/* Tuning hook: 0 disables, 1 (default) enables the 32x32-tile register
+ * kernel (K split over the waves of a workgroup, no split-K workspace) used
+ * for plain GEMMs below 2^29 flops with at least 128 output tiles whose
+ * k-contiguous operands have 16-byte aligned rows. */
+int tth_gemm_small(int on);
 
 /* Convolution GEMMs over the im2col matrix col[(c,kh,kw)][(n,ho,wo)]
  * (Kc = C*HH*WW rows, Ncol = N*Ho*Wo columns, HW = Ho*Wo):

@@ -505,6 +505,34 @@ def test_gemm_mid_kernel(tlib, M, N, K, ta, tb):
     assert norm2 <= GEMM_TOL, norm2
 
 
+# Small GEMMs (2MNK < 2^29, >= 128 tiles of 32x32) run the register kernel
+# that splits K over the waves of one workgroup: edges in M / N, K not a
+# multiple of 8 or below 8, every layout (k-contiguous operands with aligned
+# rows take 16-byte loads; the unaligned K = 5 / 13 cases run the layouts
+# whose operands are m/n-contiguous).
+SMALL_SHAPES = [(300, 500, 36), (257, 513, 256), (4097, 10, 128), (33, 4100, 5), (512, 512, 512),
+                (600, 300, 13), (1000, 40, 1000)]
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", SMALL_SHAPES)
+def test_gemm_small_kernel(tlib, M, N, K, ta, tb):
+    A = u(K, M) if ta else u(M, K)
+    B = u(N, K) if tb else u(K, N)
+    ref = (A.T if ta else A).astype(np.float64) @ (B.T if tb else B).astype(np.float64)
+    print("gemm small", M, N, K, ta, tb, flush=True)
+    C = run_gemm(tlib, M, N, K, ta, tb, A, B)
+    norm, rel = gemm_err(C, ref, K, 1.0, 1.0)
+    assert norm <= GEMM_TOL and rel <= GEMM_TOL, (norm, rel)
+    check(tlib.tth_gemm_small(0), "small off")
+    try:
+        C2 = run_gemm(tlib, M, N, K, ta, tb, A, B)
+    finally:
+        check(tlib.tth_gemm_small(1), "small on")
+    norm2, _ = gemm_err(C, C2, K, 1.0, 1.0)
+    assert norm2 <= GEMM_TOL, norm2
+
+
 # Large GEMMs with unaligned operands take aligned, zero-padded copies into
 # the 64x64 kernel: ragged leading dimensions, K % 4 != 0, odd M / N.
 PAD_SHAPES = [(1000, 1003, 997), (1001, 1024, 1000), (1024, 999, 1024), (515, 1025, 1023)]

@@ -1197,6 +1197,7 @@ constexpr int TILE_BK[NTILE] = {32, 32, 32, 32, 32, 32, 32, 32, 32, 64, 64};
 int g_force_tile = -1, g_force_splits = -1;
 int g_direct = 1;  // direct-to-LDS 256x256 kernel enabled (tth_gemm_direct)
 int g_mid = 1;     // 64x64 direct-load kernel for plain GEMMs (tth_gemm_mid)
+int g_small = 1;   // 32x32 register kernel for small plain GEMMs (tth_gemm_small)
 
 struct Plan {
   int tile, splits, kchunk;
@@ -1356,6 +1357,124 @@ __global__ void __launch_bounds__(256) pad_rows_kernel(PadJob a, PadJob b, int g
   }
 }
 
+// Small plain GEMM: one 32x32 tile of C per workgroup, its K range split over
+// SW waves, each multiplying its k slice with operands loaded straight into
+// registers (no LDS staging, no split-K workspace); the wave sums are added
+// through LDS in wave order (deterministic).  Lane l of v_mfma_f32_32x32x2
+// feeds A[l%32][k] and B[k][l%32]; lane half h takes k = 4h..4h+3 of each
+// 8-k group, one per MFMA, so the four MFMAs of a group cover its 8 k.
+// Loads run a chunk of SG groups ahead of the MFMAs (two register sets).
+// VA / VB: the operand is k-contiguous with 16-byte aligned rows, so a lane
+// reads its 4 k as one 16-byte load.  Rows / columns past the matrix load
+// the last valid one (their outputs are not stored); k past the slice loads
+// zeros.
+constexpr int SW = 8;  // waves per small-GEMM workgroup
+constexpr int SG = 4;  // 8-k groups per pipelined chunk
+template <bool A_KC, bool B_NC, bool VA, bool VB>
+__global__ void __launch_bounds__(64 * SW)
+gemm_small_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
+                  const float *__restrict__ B, long ldb, float *__restrict__ C, long ldc, int kc) {
+  __shared__ float red[(SW - 1) * 16 * 64];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l32 = lane & 31, h = lane >> 5;
+  const int m0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
+  const int mr = min(m0 + l32, M - 1), nr = min(n0 + l32, N - 1);
+  // this lane's A row / B column: element k at base + k * step
+  const float *ap = A_KC ? A + (long)mr * lda : A + mr;
+  const long as = A_KC ? 1 : lda;
+  const float *bp = B_NC ? B + nr : B + (long)nr * ldb;
+  const long bs = B_NC ? ldb : 1;
+  const int k0 = w * kc, k1 = min(K, k0 + kc);
+  f32x16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+  auto load = [&](int kb, float (&a)[SG][4], float (&b)[SG][4]) {
+#pragma unroll
+    for (int g = 0; g < SG; g++) {
+      const int kq = kb + 8 * g + 4 * h;
+      if (VA && kq + 3 < k1) {
+        const float4 v = *(const float4 *)(ap + kq);
+        a[g][0] = v.x; a[g][1] = v.y; a[g][2] = v.z; a[g][3] = v.w;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) a[g][i] = kq + i < k1 ? ap[(long)(kq + i) * as] : 0.0f;
+      }
+      if (VB && kq + 3 < k1) {
+        const float4 v = *(const float4 *)(bp + kq);
+        b[g][0] = v.x; b[g][1] = v.y; b[g][2] = v.z; b[g][3] = v.w;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) b[g][i] = kq + i < k1 ? bp[(long)(kq + i) * bs] : 0.0f;
+      }
+    }
+  };
+  auto mfmas = [&](const float (&a)[SG][4], const float (&b)[SG][4]) {
+#pragma unroll
+    for (int g = 0; g < SG; g++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[g][i], b[g][i], acc, 0, 0, 0);
+  };
+  constexpr int CK = 8 * SG;  // k per chunk
+  float a0[SG][4], b0[SG][4], a1[SG][4], b1[SG][4];
+  if (k0 < k1) load(k0, a0, b0);
+  for (int kb = k0; kb < k1; kb += 2 * CK) {
+    const bool more = kb + CK < k1;
+    if (more) load(kb + CK, a1, b1);
+    mfmas(a0, b0);
+    if (!more) break;
+    if (kb + 2 * CK < k1) load(kb + 2 * CK, a0, b0);
+    mfmas(a1, b1);
+  }
+  if (w > 0) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) red[((w - 1) * 16 + r) * 64 + lane] = acc[r];
+  }
+  __syncthreads();
+  if (w > 0) return;
+  for (int o = 0; o < SW - 1; o++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] += red[(o * 16 + r) * 64 + lane];
+  const int n = n0 + l32;
+  if (n >= N) return;
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    const int m = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
+    if (m < M) C[(long)m * ldc + n] = acc[r];
+  }
+}
+
+// small_ok: below the 64x64 kernel's range (2MNK < 2^29) with at least 128
+// tiles to spread, and every k-contiguous operand 16-byte aligned (rows read
+// by 32 lanes one float at a time bound the address path: measured slower
+// than the split-K register kernel).
+template <bool A_KC, bool B_NC>
+bool small_ok(int M, int N, int K, const Opnd &A, const Opnd &B) {
+  const long tiles = (long)((M + 31) / 32) * ((N + 31) / 32);
+  const bool va = !A_KC || (aligned16(A.p) && A.ld % 4 == 0);
+  const bool vb = B_NC || (aligned16(B.p) && B.ld % 4 == 0);
+  return g_small && K > 0 && 2.0 * M * N * K < (double)(1L << 29) && tiles >= 128 &&
+         (M + 31) / 32 <= 65535 && va && vb;
+}
+
+template <bool A_KC, bool B_NC>
+int run_small(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ldc) {
+  const int kc = ((K + SW - 1) / SW + 7) / 8 * 8;
+  const dim3 grid((unsigned)((N + 31) / 32), (unsigned)((M + 31) / 32));
+  // 16-byte loads of a k-contiguous operand whose rows are 16-byte aligned
+  const bool va = A_KC && aligned16(A.p) && A.ld % 4 == 0;
+  const bool vb = !B_NC && aligned16(B.p) && B.ld % 4 == 0;
+#define TT_SMALL(VA_, VB_)                                                                      \
+  hipLaunchKernelGGL((gemm_small_kernel<A_KC, B_NC, VA_, VB_>), grid, dim3(64 * SW), 0, stream(), \
+                     M, N, K, A.p, A.ld, B.p, B.ld, C, ldc, kc)
+  if (va && vb) TT_SMALL(A_KC, !B_NC);
+  else if (va) TT_SMALL(A_KC, false);
+  else if (vb) TT_SMALL(false, !B_NC);
+  else TT_SMALL(false, false);
+#undef TT_SMALL
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
 // Plain GEMM on 64x64 tiles (gemm_mid_kernel), split over K until the grid
 // covers the CUs.  Operands 16-byte aligned, leading dimensions multiples of
 // 4 (and at most 2^22), K % 4 == 0 for k-contiguous operands, M / N % 4 == 0
@@ -1467,6 +1586,7 @@ int run(int M, int N, int K, Opnd A, Opnd B, float *C, long ldc, const float *bi
   Plan p = plan(M, N, K > 0 ? K : 1);
   if constexpr (!A_PERM && !B_PERM && !B_I2C && EPI == EPI_STORE) {
     if (p.tile != T256x256 && p.tile != T256x128 && p.tile != T128x128 && g_force_tile < 0) {
+      if (small_ok<A_KC, B_NC>(M, N, K, A, B)) return run_small<A_KC, B_NC>(M, N, K, A, B, C, ldc);
       if (mid_ok<A_KC, B_NC>(M, N, K, A, B, vec)) return run_mid<A_KC, B_NC>(M, N, K, A, B, C, ldc);
       if (g_mid && 2.0 * M * N * K >= 1e9) return run_mid_padded<A_KC, B_NC>(M, N, K, A, B, C, ldc);
     }
@@ -1549,6 +1669,11 @@ extern "C" int tth_gemm_direct(int on) {
 
 extern "C" int tth_gemm_mid(int on) {
   g_mid = on ? 1 : 0;
+  return 0;
+}
+
+extern "C" int tth_gemm_small(int on) {
+  g_small = on ? 1 : 0;
   return 0;
 }
 
