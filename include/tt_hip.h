@@ -194,11 +194,24 @@ int tt_k_conv2d_dx_implicit(const float *g, const float *w, float *dx,
  *   dw:  dw (F, C*HH*WW), db (F, optional)         src/autograd.c:456-513
  *   dx:  dx (N,C,H,W)                              src/autograd.c:515-539,406-434 */
 int tth_conv_lds(int on);
+/* 1 (default): ag_conv2d leaves its direct-convolution launch pending until
+ * the next library call, and an ag_relu on its output computes both in one
+ * launch (tt_k_conv2d_relu_fwd_lds); 0: every convolution launches at once.
+ * <0 queries; the previous setting is returned. */
+int tth_conv_relu_fuse(int on);
 int tt_k_conv2d_lds_plan(int N, int C, int H, int W, int F, int HH, int WW,
                          int sh, int sw, int ph, int pw, int Ho, int Wo);
 int tt_k_conv2d_fwd_lds(const float *x, const float *w, const float *bias, float *out,
                         int N, int C, int H, int W, int F, int HH, int WW,
                         int sh, int sw, int ph, int pw, int Ho, int Wo);
+/* Forward convolution and the relu applied to its output in one launch:
+ * out = conv(x, w) + bias as tt_k_conv2d_fwd_lds, rout = out > 0 ? out : 0
+ * (NaN -> 0), bit-identical to tt_k_conv2d_fwd_lds + tt_k_relu_fwd.
+ * Replaces tt_conv2d followed by tt_relu (src/ops_spatial.c:71-127,
+ * src/ops.c:55-69,104-106) when the relu consumes the convolution. */
+int tt_k_conv2d_relu_fwd_lds(const float *x, const float *w, const float *bias, float *out,
+                             float *rout, int N, int C, int H, int W, int F, int HH, int WW,
+                             int sh, int sw, int ph, int pw, int Ho, int Wo);
 int tt_k_conv2d_dw_lds(const float *g, const float *x, float *dw, float *db,
                        int N, int C, int H, int W, int F, int HH, int WW,
                        int sh, int sw, int ph, int pw, int Ho, int Wo);

@@ -210,3 +210,75 @@ def test_lds_conv_random_shapes(tlib, case):
         dX.free()
     for bf in (dx_, dw_, db_, dg_):
         bf.free()
+
+
+def _bits_equal(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_conv_relu_fused_kernel_bitexact(tlib, case):
+    """tt_k_conv2d_relu_fwd_lds: both outputs bit for bit equal to the
+    convolution alone followed by the relu kernel (reference
+    src/ops_spatial.c:71-127 then src/ops.c:104-106), NaN and -0 included."""
+    x, w, b, _, geo = _inputs(case)
+    N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo = geo
+    x.flat[:: max(1, x.size // 7)] = np.nan  # NaN outputs: the relu gives +0
+    print("conv relu fused", case, flush=True)
+    n_out = N * F * Ho * Wo
+    dx_, dw_, db_ = DevBuf.from_np(x), DevBuf.from_np(w), DevBuf.from_np(b)
+    for bias in (db_.ptr, None):
+        o1, r1, o2, r2 = DevBuf(n_out), DevBuf(n_out), DevBuf(n_out), DevBuf(n_out)
+        check(tlib.tt_k_conv2d_relu_fwd_lds(dx_.ptr, dw_.ptr, bias, o1.ptr, r1.ptr, *geo), "fused")
+        check(tlib.tt_k_conv2d_fwd_lds(dx_.ptr, dw_.ptr, bias, o2.ptr, *geo), "conv")
+        check(tlib.tt_k_relu_fwd(o2.ptr, r2.ptr, n_out), "relu")
+        shp = (N, F, Ho, Wo)
+        assert _bits_equal(o1.to_np(shp), o2.to_np(shp))
+        assert _bits_equal(r1.to_np(shp), r2.to_np(shp))
+    assert tlib.tt_k_conv2d_relu_fwd_lds(dx_.ptr, dw_.ptr, None, o1.ptr, o1.ptr, *geo) == -1
+
+
+@pytest.mark.parametrize("case", CASES[-4:] + CASES[:3])
+def test_autograd_conv_relu_deferred(tlib, case):
+    """ag_conv2d followed by ag_relu (one fused launch) against the same graph
+    with every convolution launched at once: values and gradients bit for bit
+    equal.  Reading the convolution's value before the relu, releasing it
+    before the relu, and a relu on another tensor in between all launch the
+    pending convolution first."""
+    from tinytorch_amd.torch_py import Node
+    x, w, b, _, geo = _inputs(case)
+    N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo = geo
+    g = rng.standard_normal((N, F, Ho, Wo)).astype(np.float32)
+    print("deferred conv relu", case, flush=True)
+
+    def run(mode):
+        X, Wn, Bn = Node.leaf(x), Node.leaf(w), Node.leaf(b)
+        c = X.conv2d(Wn, Bn, (sh, sw), (ph, pw))
+        if mode == "peek":
+            cv = c.value()          # launches the pending convolution
+        if mode == "other":
+            o = Bn.relu()           # a relu of another node: flushes, then runs alone
+            o.release()
+        r = c.relu()
+        vals = [c.value(), r.value()]
+        if mode == "release":
+            c.release()             # r keeps the convolution node alive
+        r.backward(g)
+        out = vals + [X.grad(), Wn.grad(), Bn.grad()]
+        if mode == "peek":
+            assert _bits_equal(cv, vals[0])
+        for n in ([r, X, Wn, Bn] if mode == "release" else [r, c, X, Wn, Bn]):
+            n.release()
+        return out
+
+    prev = tlib.tth_conv_relu_fuse(0)
+    try:
+        ref = run("plain")
+    finally:
+        tlib.tth_conv_relu_fuse(prev)
+    assert tlib.tth_conv_relu_fuse(-1) == 1
+    for mode in ("fused", "peek", "other", "release"):
+        got = run(mode)
+        for a, e in zip(got, ref):
+            assert _bits_equal(a, e), mode

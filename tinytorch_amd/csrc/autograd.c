@@ -151,6 +151,22 @@ AGNode *ag_matmul(AGNode *a, AGNode *b) {
 
 AGNode *ag_relu(AGNode *a) {
     if (!a) return NULL;
+    if (tt_pend.active && tt_pend.out == a->val) {
+        /* the convolution producing a is still pending: one launch writes
+         * it and its relu (same values as tt_relu of the stored output) */
+        Tensor *r = tt_empty_like(a->val);
+        if (r) {
+            const TTPendConv p = tt_pend;
+            const int *q = p.geo;
+            tt_pend.active = 0;
+            if (tt_k_conv2d_relu_fwd_lds(p.x, p.w, p.b, p.out->dev, r->dev, q[0], q[1], q[2],
+                                         q[3], q[4], q[5], q[6], q[7], q[8], q[9], q[10], q[11],
+                                         q[12]) == 0)
+                return node_unary(a, r, OP_RELU);
+            tt_pend = p;  /* not launched: the plain convolution runs below */
+            tt_release(r);
+        }
+    }
     return node_unary(a, tt_relu(a->val), OP_RELU);
 }
 
@@ -183,12 +199,16 @@ AGNode *ag_conv2d(AGNode *a, AGNode *w, AGNode *b, int sh, int sw, int ph, int p
     const int keep = w->requires_grad;
     const int ones = keep && b && b->requires_grad;  /* fuse db into the dW GEMM */
     float *col = NULL;
-    Tensor *v = tt_conv2d_keepcol(a->val, w->val, b ? b->val : NULL, sh, sw, ph, pw,
-                                  keep ? &col : NULL, ones);
+    Tensor *v = tt_conv2d_keepcol_ex(a->val, w->val, b ? b->val : NULL, sh, sw, ph, pw,
+                                     keep ? &col : NULL, ones, 1);
     if (!v) return NULL;
     int req = a->requires_grad || w->requires_grad || (b && b->requires_grad);
     AGNode *n = node_new(v, req);
-    if (!n) { ttrt_free(col); return NULL; }
+    if (!n) {
+        if (tt_pend.active && tt_pend.out == v) tt_pend.active = 0;  /* v was released */
+        ttrt_free(col);
+        return NULL;
+    }
     n->parents[0] = ag_retain(a);
     n->parents[1] = ag_retain(w);
     n->nparents = 2;
@@ -871,6 +891,7 @@ AGNode *ag_retain(AGNode *n) {
 void ag_release(AGNode *n) {
     if (!n) return;
     if (--n->refcount > 0) return;
+    if (tt_pend.active && tt_pend.out == n->val) tt_flush_pending();
     tt_release(n->val);
     tt_release(n->grad);
     tt_release(n->aux);

@@ -41,6 +41,7 @@
 // LDS writes).  Measured on MI355X, linear 16-byte direct loads fill LDS about
 // 10x faster than per-lane scattered 4-byte ones.
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <stdint.h>
 #include "tt_rt.h"
 
@@ -260,7 +261,8 @@ __device__ __forceinline__ void stage_weights(float *ws, const float *__restrict
 template <int PB, bool FLIP, bool VEC>
 __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2)))
 conv_fwd_lds_kernel(const float *__restrict__ x, const float *__restrict__ w,
-                    const float *__restrict__ bias, float *__restrict__ out, Geo g, int chunks) {
+                    const float *__restrict__ bias, float *__restrict__ out,
+                    float *__restrict__ rout, Geo g, int chunks) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   constexpr int CHUNK = 128 * PB;
   const int n = blockIdx.x / chunks, chunk = blockIdx.x - n * chunks;
@@ -365,16 +367,27 @@ conv_fwd_lds_kernel(const float *__restrict__ x, const float *__restrict__ w,
 #pragma unroll
   for (int r = 0; r < 16; r++) bv[r] = bs[8 * (r >> 2) + 4 * half + (r & 3)];
   float *on = out + (long)n * g.F * P;
+  // rout: the relu of the output as well (x > 0 ? x : +0, NaN -> +0)
+  float *rn = rout ? rout + (long)n * g.F * P : nullptr;
+  // one unrolled store loop per form (a branch on rn inside it defeats the unroll)
+  auto store = [&](auto relu) {
 #pragma unroll
-  for (int j = 0; j < PB; j++) {
-    const int p = p0 + (wave * PB + j) * 32 + l32;
-    if (p >= p1) continue;
+    for (int j = 0; j < PB; j++) {
+      const int p = p0 + (wave * PB + j) * 32 + l32;
+      if (p >= p1) continue;
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int f = f0 + 8 * (r >> 2) + 4 * half + (r & 3);
-      if (f < g.F) on[(long)f * P + p] = acc[j][r] + bv[r];
+      for (int r = 0; r < 16; r++) {
+        const int f = f0 + 8 * (r >> 2) + 4 * half + (r & 3);
+        if (f < g.F) {
+          const float v = acc[j][r] + bv[r];
+          on[(long)f * P + p] = v;
+          if constexpr (decltype(relu)::value) rn[(long)f * P + p] = v > 0.0f ? v : 0.0f;
+        }
+      }
     }
-  }
+  };
+  if (rn) store(std::true_type{});
+  else store(std::false_type{});
 }
 
 // ---- forward / dX for KH x KW kernels known at compile time ----
@@ -394,7 +407,8 @@ conv_fwd_lds_kernel(const float *__restrict__ x, const float *__restrict__ w,
 template <int PB, bool FLIP, bool VEC, int KH, int KW, int KS = 1>
 __global__ void __launch_bounds__(NT * KS) __attribute__((amdgpu_waves_per_eu(1, 2)))
 conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
-                  const float *__restrict__ bias, float *__restrict__ out, Geo g, int chunks) {
+                  const float *__restrict__ bias, float *__restrict__ out,
+                  float *__restrict__ rout, Geo g, int chunks) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   constexpr int CHUNK = 128 * PB, TAPS = KH * KW;
   const int n = blockIdx.x / chunks, chunk = blockIdx.x - n * chunks;
@@ -603,16 +617,27 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
   }
 
   float *on = out + (long)n * g.F * P;
+  // rout: the relu of the output as well (x > 0 ? x : +0, NaN -> +0)
+  float *rn = rout ? rout + (long)n * g.F * P : nullptr;
+  // one unrolled store loop per form (a branch on rn inside it defeats the unroll)
+  auto store = [&](auto relu) {
 #pragma unroll
-  for (int j = 0; j < PB; j++) {
-    const int p = p0 + (pw4 * PB + j) * 32 + l32;
-    if (p >= p1) continue;
+    for (int j = 0; j < PB; j++) {
+      const int p = p0 + (pw4 * PB + j) * 32 + l32;
+      if (p >= p1) continue;
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int f = f0 + 8 * (r >> 2) + 4 * half + (r & 3);
-      if (f < g.F) on[(long)f * P + p] = acc[j][r] + bv[r];
+      for (int r = 0; r < 16; r++) {
+        const int f = f0 + 8 * (r >> 2) + 4 * half + (r & 3);
+        if (f < g.F) {
+          const float v = acc[j][r] + bv[r];
+          on[(long)f * P + p] = v;
+          if constexpr (decltype(relu)::value) rn[(long)f * P + p] = v > 0.0f ? v : 0.0f;
+        }
+      }
     }
-  }
+  };
+  if (rn) store(std::true_type{});
+  else store(std::false_type{});
 }
 
 // ---- weight gradient partials ----
@@ -1113,21 +1138,21 @@ FwdPlan plan_fwd(const Geo &g, int N, bool flip) {
 }
 
 template <int PB, bool FLIP, bool VEC>
-int launch_fwd(const float *x, const float *w, const float *bias, float *out, const Geo &g, int N,
-               const FwdPlan &pl) {
+int launch_fwd(const float *x, const float *w, const float *bias, float *out, float *rout,
+               const Geo &g, int N, const FwdPlan &pl) {
   auto kern = !is_k3(g)     ? conv_fwd_lds_kernel<PB, FLIP, VEC>
               : pl.ks == 2 ? conv_fwd_k_kernel<PB, FLIP, VEC, 3, 3, 2>
                            : conv_fwd_k_kernel<PB, FLIP, VEC, 3, 3, 1>;
   if (pl.lds > 64 * 1024 && !allow_big_lds((const void *)kern)) return -1;
   const dim3 grid((unsigned)(N * pl.chunks), (unsigned)((g.F + 31) / 32));
-  hipLaunchKernelGGL(kern, grid, dim3(NT * pl.ks), pl.lds, stream(), x, w, bias, out, g,
+  hipLaunchKernelGGL(kern, grid, dim3(NT * pl.ks), pl.lds, stream(), x, w, bias, out, rout, g,
                      pl.chunks);
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
 template <bool FLIP>
 int run_fwd(const float *x, const float *w, const float *bias, float *out, const Geo &g, int N,
-            bool dry) {
+            bool dry, float *rout = nullptr) {
   const FwdPlan pl = plan_fwd(g, N, FLIP);
   if (!pl.pb) return -1;
   if (dry) return 0;
@@ -1142,10 +1167,10 @@ int run_fwd(const float *x, const float *w, const float *bias, float *out, const
                                    : g.K % 4 == 0);
   const bool vec = g.W % 4 == 0 && aligned16(x) && wok;
   if (pl.pb == 2)
-    return vec ? launch_fwd<2, FLIP, true>(x, w, bias, out, g, N, pl)
-               : launch_fwd<2, FLIP, false>(x, w, bias, out, g, N, pl);
-  return vec ? launch_fwd<1, FLIP, true>(x, w, bias, out, g, N, pl)
-             : launch_fwd<1, FLIP, false>(x, w, bias, out, g, N, pl);
+    return vec ? launch_fwd<2, FLIP, true>(x, w, bias, out, rout, g, N, pl)
+               : launch_fwd<2, FLIP, false>(x, w, bias, out, rout, g, N, pl);
+  return vec ? launch_fwd<1, FLIP, true>(x, w, bias, out, rout, g, N, pl)
+             : launch_fwd<1, FLIP, false>(x, w, bias, out, rout, g, N, pl);
 }
 
 // dW kernel variants: (MF, JW, KS) with FS = filters/16 per workgroup.
@@ -1320,6 +1345,20 @@ extern "C" int tt_k_conv2d_fwd_lds(const float *x, const float *w, const float *
   if (!x || !w || !out || !geo_ok(N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo)) return -1;
   const Geo g{C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo, F, C * HH * WW};
   return run_fwd<false>(x, w, bias, out, g, N, false);
+}
+
+// The same convolution with its relu: out as above and rout = relu(out)
+// from the same values in one launch (bit-identical to tt_k_conv2d_fwd_lds
+// followed by tt_k_relu_fwd).  -1: not covered.
+extern "C" int tt_k_conv2d_relu_fwd_lds(const float *x, const float *w, const float *bias,
+                                        float *out, float *rout, int N, int C, int H, int W,
+                                        int F, int HH, int WW, int sh, int sw, int ph, int pw,
+                                        int Ho, int Wo) {
+  if (!x || !w || !out || !rout || out == rout ||
+      !geo_ok(N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo))
+    return -1;
+  const Geo g{C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo, F, C * HH * WW};
+  return run_fwd<false>(x, w, bias, out, g, N, false, rout);
 }
 
 // dw (F, C*HH*WW) and, when db is given, db (F) from the output gradient g

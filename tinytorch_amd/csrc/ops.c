@@ -154,8 +154,35 @@ int tth_conv_config(long implicit_min_bytes) {
 
 int tt_conv_use_implicit(long col_bytes) { return col_bytes >= g_implicit_min_bytes; }
 
+TTPendConv tt_pend;
+static int g_conv_relu = 1;   /* defer ag_conv2d launches so a relu can fuse */
+
+int tth_conv_relu_fuse(int on) {
+    const int prev = g_conv_relu;
+    if (on >= 0) {
+        tt_flush_pending();
+        g_conv_relu = on ? 1 : 0;
+    }
+    return prev;
+}
+
+void tt_flush_pending(void) {
+    if (!tt_pend.active) return;
+    tt_pend.active = 0;
+    const int *q = tt_pend.geo;
+    if (tt_k_conv2d_fwd_lds(tt_pend.x, tt_pend.w, tt_pend.b, tt_pend.out->dev, q[0], q[1], q[2],
+                            q[3], q[4], q[5], q[6], q[7], q[8], q[9], q[10], q[11], q[12]) != 0)
+        ttrt_set_error(-3);
+}
+
 Tensor *tt_conv2d_keepcol(const Tensor *a, const Tensor *w, const Tensor *b, int sh, int sw,
                           int ph, int pw, float **col_out, int ones_row) {
+    return tt_conv2d_keepcol_ex(a, w, b, sh, sw, ph, pw, col_out, ones_row, 0);
+}
+
+/* defer: the direct-convolution launch may be left pending in tt_pend */
+Tensor *tt_conv2d_keepcol_ex(const Tensor *a, const Tensor *w, const Tensor *b, int sh, int sw,
+                             int ph, int pw, float **col_out, int ones_row, int defer) {
     if (col_out) *col_out = NULL;
     if (!a || !w || a->ndim != 4 || w->ndim != 4) return NULL;
     const int N = (int)a->shape[0], C = (int)a->shape[1], H = (int)a->shape[2],
@@ -181,10 +208,20 @@ Tensor *tt_conv2d_keepcol(const Tensor *a, const Tensor *w, const Tensor *b, int
     /* LDS-staged direct convolution: taken when it also covers the weight
      * gradient the caller will ask for (that reads x, so no col is kept) */
     const int lds = tt_k_conv2d_lds_plan(N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo);
-    if ((lds & 1) && (!col_out || (lds & 2)) &&
-        tt_k_conv2d_fwd_lds(x, wd, bd, out->dev, N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho,
-                            Wo) == 0)
-        return out;
+    if ((lds & 1) && (!col_out || (lds & 2))) {
+        if (defer && g_conv_relu) {
+            tt_flush_pending();
+            const int q[13] = {N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo};
+            tt_pend.out = out;
+            tt_pend.x = x; tt_pend.w = wd; tt_pend.b = bd;
+            for (int i = 0; i < 13; i++) tt_pend.geo[i] = q[i];
+            tt_pend.active = 1;
+            return out;
+        }
+        if (tt_k_conv2d_fwd_lds(x, wd, bd, out->dev, N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho,
+                                Wo) == 0)
+            return out;
+    }
     if (tt_conv_use_implicit(sizeof(float) * (long)Kc * Ncol) &&
         tt_k_conv2d_fwd_implicit(x, wd, bd, out->dev, N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho,
                                  Wo) == 0)

@@ -103,6 +103,7 @@ void tt_release(Tensor *t) {
 }
 
 float *tt_dev(Tensor *t) {
+    if (tt_pend.active) tt_flush_pending();
     if (!t || !t->dev) return NULL;
     if (!(t->valid & TT_V_DEV)) {
         if (!t->data || ttrt_h2d_async(t->dev, t->data, sizeof(float) * (size_t)t->numel) != 0)
@@ -116,6 +117,7 @@ float *tt_dev(Tensor *t) {
  * the device copy is re-uploaded before its next use. */
 float *tt_data(const Tensor *ct) {
     Tensor *t = (Tensor *)ct;
+    if (tt_pend.active) tt_flush_pending();
     if (!t) return NULL;
     if (!(t->valid & TT_V_HOST)) {
         if (!t->data) {
@@ -158,14 +160,23 @@ int tth_device_name(char *buf, int len) {
 }
 
 void  *tth_stream(void) { return ttrt_init() == 0 ? ttrt_stream() : NULL; }
-int    tth_sync(void) { return ttrt_sync(); }
+int    tth_sync(void) {
+    tt_flush_pending();
+    return ttrt_sync();
+}
 int    tth_last_error(void) { return ttrt_last_error(); }
 void  *tth_malloc(size_t bytes) { return ttrt_alloc(bytes); }
 void   tth_free(void *d) { ttrt_free(d); }
 void   tth_release_cache(void) { ttrt_release_cache(); }
 size_t tth_bytes_in_use(void) { return ttrt_bytes_in_use(); }
-int    tth_h2d(void *d, const void *h, size_t bytes) { return ttrt_h2d(d, h, bytes); }
-int    tth_d2h(void *h, const void *d, size_t bytes) { return ttrt_d2h(h, d, bytes); }
+int    tth_h2d(void *d, const void *h, size_t bytes) {
+    tt_flush_pending();
+    return ttrt_h2d(d, h, bytes);
+}
+int    tth_d2h(void *h, const void *d, size_t bytes) {
+    tt_flush_pending();
+    return ttrt_d2h(h, d, bytes);
+}
 
 void *tth_event_create(void) {
     if (ttrt_init() != 0) return NULL;
@@ -176,6 +187,7 @@ void *tth_event_create(void) {
 
 int tth_event_record(void *ev) {
     if (!ev) return -1;
+    tt_flush_pending();
     return hipEventRecord((hipEvent_t)ev, (hipStream_t)ttrt_stream()) == hipSuccess ? 0 : -1;
 }
 

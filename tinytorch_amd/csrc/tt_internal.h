@@ -23,4 +23,21 @@ Tensor *tt_conv2d_keepcol(const Tensor *a, const Tensor *w, const Tensor *b,
                           int stride_h, int stride_w, int pad_h, int pad_w, float **col_out,
                           int ones_row);
 
+/* A forward convolution of ag_conv2d whose launch waits for the next call
+ * into the library: when that call is ag_relu on its output, the relu is
+ * computed by the same launch (tt_k_conv2d_relu_fwd_lds); any other call
+ * launches it first (tt_flush_pending from tt_dev, tt_data, tth_sync and
+ * ag_release), so every later kernel is still enqueued after it. */
+typedef struct {
+    int active;
+    Tensor *out;              /* the convolution's output (owned by its node) */
+    const float *x, *w, *b;   /* device operands, retained by the node's parents */
+    int geo[13];              /* N C H W F HH WW sh sw ph pw Ho Wo */
+} TTPendConv;
+extern TTPendConv tt_pend;
+void tt_flush_pending(void);
+Tensor *tt_conv2d_keepcol_ex(const Tensor *a, const Tensor *w, const Tensor *b,
+                             int stride_h, int stride_w, int pad_h, int pad_w, float **col_out,
+                             int ones_row, int defer);
+
 #endif
