@@ -112,6 +112,12 @@ int tt_k_softmax_ce(const float *logits, const int32_t *labels, float *probs,
 #define TT_CE_MEAN_MAX_ROWS 8192
 int tt_k_softmax_ce_mean(const float *logits, const int32_t *labels, float *probs,
                          float *loss_mean, float *seed, long rows, int cols, float scale);
+/* Same, with the labels read from HOST memory at the call and handed to the
+ * kernel inside its launch arguments (no device label buffer, no copy before
+ * the launch); rows <= TT_CE_ARG_ROWS. */
+#define TT_CE_ARG_ROWS 512
+int tt_k_softmax_ce_mean_hostlab(const float *logits, const int32_t *host_labels, float *probs,
+                                 float *loss_mean, float *seed, long rows, int cols, float scale);
 /* y = x * s[0], s a device scalar (chain rule through a scalar loss) */
 int tt_k_scale_by_dev(const float *x, const float *s, float *y, long n);
 int tt_k_padones_fwd(const float *x, float *y, long M, long K);      /* src/autograd.c:195-212 */

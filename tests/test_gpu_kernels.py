@@ -568,3 +568,56 @@ def test_gemm_tall_rows(tlib, M, N, K, ta, tb):
     C = run_gemm(tlib, M, N, K, ta, tb, A, B)
     norm, rel = gemm_err(C, ref, K, 1.0, 1.0)
     assert norm <= GEMM_TOL and rel <= GEMM_TOL, (norm, rel)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 10), (128, 10), (256, 10), (512, 33), (300, 7)])
+def test_softmax_ce_mean_host_labels(tlib, rows, cols):
+    """Labels in the launch arguments: bit for bit the device-label kernel,
+    out-of-range labels included."""
+    x = (rng.standard_normal((rows, cols)) * 4).astype(np.float32)
+    y = rng.integers(0, cols, rows).astype(np.int32)
+    y[:: 17] = cols + 3
+    outs = []
+    for host in (False, True):
+        dx_, dp, ds, dl = DevBuf.from_np(x), DevBuf(rows * cols), DevBuf(rows * cols), DevBuf(1)
+        if host:
+            check(tlib.tt_k_softmax_ce_mean_hostlab(dx_.ptr, y.ctypes.data, dp.ptr, dl.ptr, ds.ptr, rows,
+                                                    cols, ctypes.c_float(1.0 / rows)), "hostlab")
+        else:
+            dlab = DevBuf.from_np(y)
+            check(tlib.tt_k_softmax_ce_mean(dx_.ptr, dlab.ptr, dp.ptr, dl.ptr, ds.ptr, rows, cols,
+                                            ctypes.c_float(1.0 / rows)), "devlab")
+        outs.append([dp.to_np((rows, cols)), ds.to_np((rows, cols)), dl.to_np((1,))])
+    for a, b in zip(*outs):
+        assert bits_equal(a, b)
+    assert tlib.tt_k_softmax_ce_mean_hostlab(dx_.ptr, y.ctypes.data, dp.ptr, dl.ptr, ds.ptr, 513, cols,
+                                             ctypes.c_float(1.0)) == -1
+
+
+def test_autograd_softmax_ce_seed_moves_and_recomputes(tlib):
+    """ag_softmax_ce backward: the first backward with the default seed hands
+    the logits the per-row seed (p - onehot)/rows; a second backward adds the
+    recomputed seed (exactly twice the first); a seed of 2 scales it."""
+    from tinytorch_amd.torch_py import Node
+    rows, cols = 128, 10
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    y = rng.integers(0, cols, rows).astype(np.int32)
+    X = Node.leaf(x)
+    loss = X.softmax_ce(y)
+    p = loss.probs()
+    onehot = np.eye(cols, dtype=np.float32)[y]
+    seed = (p - onehot) * np.float32(1.0 / rows)
+    loss.backward(None)
+    g1 = X.grad()
+    assert bits_equal(g1, seed)
+    assert bits_equal(loss.grad(), np.ones(1, np.float32))
+    loss.backward(None)
+    assert bits_equal(X.grad(), seed + seed)
+    loss.release()
+    X.release()
+    X2 = Node.leaf(x)
+    loss2 = X2.softmax_ce(y)
+    loss2.backward(np.array([2.0], np.float32))
+    assert bits_equal(X2.grad(), seed * np.float32(2.0))
+    loss2.release()
+    X2.release()

@@ -46,7 +46,9 @@ struct AGNode {
     float  *col;         /* conv2d: forward im2col matrix (device) */
     int     col_ones;    /* conv2d: col carries the extra row of ones */
     Tensor *aux;         /* softmax_ce: probabilities */
-    Tensor *aux2;        /* softmax_ce: per-row seed (p - onehot)/rows */
+    Tensor *aux2;        /* softmax_ce: per-row seed (p - onehot)/rows; NULL once
+                            moved into the logits' gradient */
+    int32_t *labels;     /* softmax_ce: host copy of the labels (seed recompute) */
 };
 
 /* ---------- gradient accumulation ---------- */
@@ -259,6 +261,21 @@ AGNode *ag_softmax_ce(AGNode *logits, const int *labels, long rows) {
     Tensor *probs = tt_empty_like(logits->val);
     Tensor *seed = tt_empty_like(logits->val);
     Tensor *loss = tt_empty_dev(&one, 1);
+    int32_t *hlab = (int32_t *)malloc(sizeof(int32_t) * (size_t)rows);
+    if (hlab)
+        for (long r = 0; r < rows; r++) hlab[r] = (int32_t)labels[r];
+    /* small batches: the labels travel inside the kernel's arguments */
+    if (probs && seed && loss && hlab && rows <= TT_CE_ARG_ROWS &&
+        tt_k_softmax_ce_mean_hostlab(x, hlab, probs->dev, loss->dev, seed->dev, rows, cols,
+                                     1.0f / (float)rows) == 0) {
+        AGNode *n = node_unary(logits, loss, OP_SOFTMAX_CE);
+        if (!n) { tt_release(probs); tt_release(seed); free(hlab); return NULL; }
+        n->aux = probs;
+        n->aux2 = seed;
+        n->labels = hlab;
+        return n;
+    }
+    free(hlab);
     int32_t *dlab = (int32_t *)ttrt_alloc(sizeof(int32_t) * (size_t)rows);
     float *rowloss = rows > TT_CE_MEAN_MAX_ROWS ? (float *)ttrt_alloc(sizeof(float) * (size_t)rows)
                                                 : NULL;
@@ -574,10 +591,43 @@ static void backward_pool(AGNode *n, int is_max) {
     accum_move(a, t);
 }
 
-/* d logits = seed * dL (dL is the 1-element incoming gradient) */
+/* the tensor's current copy is the host one and holds exactly 1.0f (the
+ * default seed of ag_backward, see backward_impl) */
+static int is_host_one(const Tensor *t) {
+    return t && t->numel == 1 && t->valid == TT_V_HOST && t->data && t->data[0] == 1.0f;
+}
+
+/* d logits = seed * dL (dL is the 1-element incoming gradient).  With dL
+ * exactly 1 the product is the seed itself: the first backward moves the
+ * seed tensor into the logits' gradient (no kernel); a later one recomputes
+ * it (same kernel, same inputs, same bits) from the kept host labels. */
 static void backward_softmax_ce(AGNode *n) {
     AGNode *a = n->parents[0];
     if (!needs(a)) return;
+    if (!n->aux2 && n->labels) {
+        const float *x = tt_dev(a->val);
+        const long rows = a->val->shape[0];
+        const int cols = (int)a->val->shape[1];
+        Tensor *p = tt_empty_like(a->val), *s = tt_empty_like(a->val);
+        float *l = (float *)ttrt_alloc(sizeof(float));
+        const int ok = x && p && s && l &&
+                       tt_k_softmax_ce_mean_hostlab(x, n->labels, p->dev, l, s->dev, rows, cols,
+                                                    1.0f / (float)rows) == 0;
+        tt_release(p);
+        ttrt_free(l);
+        if (!ok) { tt_release(s); return; }
+        n->aux2 = s;
+    }
+    if (!n->aux2) return;
+    if (is_host_one(n->grad)) {
+        if (n->labels && !a->grad) {
+            a->grad = n->aux2;
+            n->aux2 = NULL;
+        } else {
+            accum_copy(a, n->aux2);
+        }
+        return;
+    }
     const float *seed = tt_dev(n->aux2), *gl = tt_dev(n->grad);
     if (!seed || !gl) return;
     Tensor *t = tt_empty_like(a->val);
@@ -679,6 +729,21 @@ static void backward_impl(AGNode *out, int seed_kind, const float *hseed, const 
     for (size_t i = 0; i < order.len; i++)
         for (int j = 0; j < order.items[i]->nparents; j++) order.items[i]->parents[j]->uses++;
     if (!out->grad) out->grad = tt_empty_like(out->val);
+    if (out->grad && seed_kind == 0 && out->grad->numel == 1) {
+        /* a scalar ones seed is written to the host copy: no kernel, and a
+         * rule that only needs to know it is 1 (softmax-CE) reads no device
+         * memory; tt_dev uploads it for any rule that does */
+        Tensor *t = out->grad;
+        if (!t->data) t->data = (float *)ttrt_host_alloc(sizeof(float));
+        if (t->data) {
+            t->data[0] = 1.0f;
+            t->valid = TT_V_HOST;
+            propagate(&order);
+            for (size_t i = 0; i < order.len; i++) order.items[i]->mark = order.items[i]->grad_done = 0;
+            free(order.items);
+            return;
+        }
+    }
     if (out->grad) {
         int rc;
         float *gd = out->grad->dev;
@@ -896,6 +961,7 @@ void ag_release(AGNode *n) {
     tt_release(n->grad);
     tt_release(n->aux);
     tt_release(n->aux2);
+    free(n->labels);
     ttrt_free(n->col);
     for (int i = 0; i < n->nparents; i++) ag_release(n->parents[i]);
     free(n);

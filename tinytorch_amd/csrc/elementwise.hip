@@ -286,8 +286,16 @@ __global__ void padones_relu_bwd_rows_kernel(const float *__restrict__ g, const 
 // workgroup: probabilities, the seed (p - onehot(y)) * scale and the mean
 // loss, reduced in a fixed order (per-thread row order, then the thread
 // partials through LDS in index order).
-template <int MAXC>
-__global__ void softmax_ce_mean_kernel(const float *__restrict__ x, const int32_t *__restrict__ lab,
+// Labels handed over inside the kernel arguments (no copy to device memory
+// before the launch): up to TT_CE_ARG_ROWS of them.
+struct LabArg {
+  int32_t v[TT_CE_ARG_ROWS];
+  __device__ int32_t operator[](int r) const { return v[r]; }
+};
+
+// LAB: a device pointer to the labels or a LabArg
+template <int MAXC, class LAB>
+__global__ void softmax_ce_mean_kernel(const float *__restrict__ x, const LAB lab,
                                        float *__restrict__ probs, float *__restrict__ loss_mean,
                                        float *__restrict__ seed, int rows, int cols, float scale) {
   __shared__ float part[256];
@@ -336,8 +344,8 @@ __global__ void softmax_ce_mean_kernel(const float *__restrict__ x, const int32_
 }
 
 // general width: the same passes over global memory
-__global__ void softmax_ce_mean_wide_kernel(const float *__restrict__ x,
-                                            const int32_t *__restrict__ lab,
+template <class LAB>
+__global__ void softmax_ce_mean_wide_kernel(const float *__restrict__ x, const LAB lab,
                                             float *__restrict__ probs,
                                             float *__restrict__ loss_mean,
                                             float *__restrict__ seed, int rows, int cols,
@@ -577,18 +585,34 @@ int tt_k_padones_bwd(const float *g, float *dx, long M, long K) {
   return launched();
 }
 
+extern "C++" template <class LAB>
+static void launch_ce_mean(const float *logits, const LAB &labels, float *probs, float *loss_mean,
+                           float *seed, long rows, int cols, float scale) {
+  if (cols <= 16)
+    hipLaunchKernelGGL((softmax_ce_mean_kernel<16, LAB>), dim3(1), dim3(256), 0, stream(), logits,
+                       labels, probs, loss_mean, seed, (int)rows, cols, scale);
+  else if (cols <= 32)
+    hipLaunchKernelGGL((softmax_ce_mean_kernel<32, LAB>), dim3(1), dim3(256), 0, stream(), logits,
+                       labels, probs, loss_mean, seed, (int)rows, cols, scale);
+  else
+    hipLaunchKernelGGL((softmax_ce_mean_wide_kernel<LAB>), dim3(1), dim3(256), 0, stream(), logits,
+                       labels, probs, loss_mean, seed, (int)rows, cols, scale);
+}
+
 int tt_k_softmax_ce_mean(const float *logits, const int32_t *labels, float *probs, float *loss_mean,
                          float *seed, long rows, int cols, float scale) {
   if (rows <= 0 || cols <= 0 || rows > TT_CE_MEAN_MAX_ROWS) return -1;
-  if (cols <= 16)
-    hipLaunchKernelGGL(softmax_ce_mean_kernel<16>, dim3(1), dim3(256), 0, stream(), logits, labels,
-                       probs, loss_mean, seed, (int)rows, cols, scale);
-  else if (cols <= 32)
-    hipLaunchKernelGGL(softmax_ce_mean_kernel<32>, dim3(1), dim3(256), 0, stream(), logits, labels,
-                       probs, loss_mean, seed, (int)rows, cols, scale);
-  else
-    hipLaunchKernelGGL(softmax_ce_mean_wide_kernel, dim3(1), dim3(256), 0, stream(), logits, labels,
-                       probs, loss_mean, seed, (int)rows, cols, scale);
+  launch_ce_mean(logits, labels, probs, loss_mean, seed, rows, cols, scale);
+  return launched();
+}
+
+int tt_k_softmax_ce_mean_hostlab(const float *logits, const int32_t *host_labels, float *probs,
+                                 float *loss_mean, float *seed, long rows, int cols, float scale) {
+  if (rows <= 0 || cols <= 0 || rows > TT_CE_ARG_ROWS || !host_labels) return -1;
+  LabArg la;
+  for (long r = 0; r < rows; r++) la.v[r] = host_labels[r];
+  for (long r = rows; r < TT_CE_ARG_ROWS; r++) la.v[r] = 0;
+  launch_ce_mean(logits, la, probs, loss_mean, seed, rows, cols, scale);
   return launched();
 }
 
