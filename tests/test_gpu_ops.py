@@ -272,3 +272,66 @@ def test_allocator_reuses_blocks(L):
         L.tt_release(t)
     assert L.tth_bytes_in_use() == before
     assert tinytorch_amd.device_name().startswith("gfx950")
+
+
+def _bits(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("M,K", [(1, 1), (128, 4096), (3, 1023), (7, 1024), (5, 3000)])
+def test_copy_padones_kernel_bitexact(tlib, M, K):
+    """tt_k_copy_padones_fwd: the copy and the padded tensor bit for bit
+    equal to tt_k_copy + tt_k_padones_fwd (reference src/ops_spatial.c:22-34,
+    src/autograd.c:195-212)."""
+    from tinytorch_amd.hip import DevBuf, check
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x.flat[::5] = np.nan
+    dx_, c1, y1, c2, y2 = (DevBuf.from_np(x), DevBuf(M * K), DevBuf(M * (K + 1)), DevBuf(M * K),
+                           DevBuf(M * (K + 1)))
+    check(tlib.tt_k_copy_padones_fwd(dx_.ptr, c1.ptr, y1.ptr, M, K), "copy_padones")
+    check(tlib.tt_k_copy(c2.ptr, dx_.ptr, M * K), "copy")
+    check(tlib.tt_k_padones_fwd(dx_.ptr, y2.ptr, M, K), "padones")
+    assert _bits(c1.to_np((M, K)), c2.to_np((M, K)))
+    assert _bits(y1.to_np((M, K + 1)), y2.to_np((M, K + 1)))
+    assert _bits(y1.to_np((M, K + 1))[:, K], np.ones(M, np.float32))
+
+
+@pytest.mark.parametrize("mode", ["fused", "peek", "other"])
+def test_autograd_reshape_padones_deferred(tlib, mode):
+    """ag_reshape followed by ag_padones (one launch) against the same graph
+    with deferral off: values and gradients bit for bit equal; reading the
+    reshape's value first, or another op in between, launches the pending
+    copy first."""
+    from tinytorch_amd.torch_py import Node
+    x = rng.standard_normal((16, 8, 4, 4)).astype(np.float32)
+    w = rng.standard_normal((129, 10)).astype(np.float32)
+    g = rng.standard_normal((16, 10)).astype(np.float32)
+
+    def run(m):
+        X, Wn = Node.leaf(x), Node.leaf(w)
+        r = X.reshape((16, 128))
+        if m == "peek":
+            rv = r.value()
+        if m == "other":
+            o = Wn.relu()
+            o.release()
+        p = r.padones()
+        out = p.matmul(Wn)
+        vals = [r.value(), p.value(), out.value()]
+        out.backward(g)
+        res = vals + [X.grad(), Wn.grad()]
+        if m == "peek":
+            assert _bits(rv, vals[0])
+        for n in (out, p, r, X, Wn):
+            n.release()
+        return res
+
+    prev = tlib.tth_conv_relu_fuse(0)
+    try:
+        ref = run("plain")
+    finally:
+        tlib.tth_conv_relu_fuse(prev)
+    for a, e in zip(run(mode), ref):
+        assert _bits(a, e), mode
+    assert _bits(ref[0], x.reshape(16, 128))

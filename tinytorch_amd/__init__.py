@@ -130,6 +130,7 @@ SIGNATURES = [
     ("tt_k_softmax_ce_mean_hostlab", _I, [VP, VP, VP, VP, VP, _L, _I, _F]),
     ("tt_k_scale_by_dev", _I, [VP, VP, VP, _L]),
     ("tt_k_padones_fwd", _I, [VP, VP, _L, _L]),
+    ("tt_k_copy_padones_fwd", _I, [VP, VP, VP, _L, _L]),
     ("tt_k_padones_bwd", _I, [VP, VP, _L, _L]),
     ("tt_k_padones_relu_bwd", _I, [VP, VP, VP, VP, _L, _L]),
     ("tt_k_im2col", _I, [VP, VP] + [_I] * 12),

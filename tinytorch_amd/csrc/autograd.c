@@ -153,7 +153,7 @@ AGNode *ag_matmul(AGNode *a, AGNode *b) {
 
 AGNode *ag_relu(AGNode *a) {
     if (!a) return NULL;
-    if (tt_pend.active && tt_pend.out == a->val) {
+    if (tt_pend.active == TT_PEND_CONV && tt_pend.out == a->val) {
         /* the convolution producing a is still pending: one launch writes
          * it and its relu (same values as tt_relu of the stored output) */
         Tensor *r = tt_empty_like(a->val);
@@ -181,6 +181,19 @@ AGNode *ag_padones(AGNode *a) {
     if (!a || a->val->ndim != 2) return NULL;
     const long M = a->val->shape[0], K = a->val->shape[1];
     const long shp[2] = {M, K + 1};
+    if (tt_pend.active == TT_PEND_COPY && tt_pend.out == a->val) {
+        /* a is a reshape whose copy is still pending: one pass writes the
+         * copy and the padded tensor */
+        Tensor *v = tt_empty_dev(shp, 2);
+        if (v) {
+            const TTPendConv p = tt_pend;
+            tt_pend.active = 0;
+            if (tt_k_copy_padones_fwd(p.x, p.out->dev, v->dev, M, K) == 0)
+                return node_unary(a, v, OP_PADONES);
+            tt_pend = p;  /* not launched: the plain copy runs below */
+            tt_release(v);
+        }
+    }
     const float *x = tt_dev(a->val);
     if (!x) return NULL;
     Tensor *v = tt_empty_dev(shp, 2);
@@ -191,9 +204,11 @@ AGNode *ag_padones(AGNode *a) {
 
 AGNode *ag_reshape(AGNode *a, const long *new_shape, int new_ndim) {
     if (!a) return NULL;
-    Tensor *v = tt_reshape(a->val, new_shape, new_ndim);
+    Tensor *v = tt_reshape_ex(a->val, new_shape, new_ndim, 1);
     if (!v) return NULL;
-    return node_unary(a, v, OP_RESHAPE);
+    AGNode *n = node_unary(a, v, OP_RESHAPE);
+    if (!n && tt_pend.active && tt_pend.out == v) tt_pend.active = 0;  /* v was released */
+    return n;
 }
 
 AGNode *ag_conv2d(AGNode *a, AGNode *w, AGNode *b, int sh, int sw, int ph, int pw) {

@@ -259,6 +259,25 @@ __global__ void padones_fwd_rows_kernel(const float *__restrict__ x, float *__re
     yr[k] = k < K ? xr[k] : 1.0f;
 }
 
+// padones of a tensor that is itself a fresh copy of x (reshape then
+// padones): writes the copy c = x and y = padones(x) from one read of x
+__global__ void copy_padones_rows_kernel(const float *__restrict__ x, float *__restrict__ c,
+                                         float *__restrict__ y, int K) {
+  const long m = blockIdx.y;
+  const float *xr = x + m * K;
+  float *cr = c + m * K;
+  float *yr = y + m * (K + 1);
+  for (int k = blockIdx.x * 1024 + threadIdx.x; k <= K && k < (int)(blockIdx.x + 1) * 1024; k += 256) {
+    if (k < K) {
+      const float v = xr[k];
+      cr[k] = v;
+      yr[k] = v;
+    } else {
+      yr[k] = 1.0f;
+    }
+  }
+}
+
 __global__ void padones_bwd_rows_kernel(const float *__restrict__ g, float *__restrict__ dx, int K) {
   const long m = blockIdx.y;
   const float *gr = g + m * (K + 1);
@@ -544,6 +563,14 @@ int tt_k_softmax_ce(const float *logits, const int32_t *labels, float *probs, fl
   if (rows <= 0 || cols <= 0) return 0;
   hipLaunchKernelGGL(softmax_ce_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, stream(),
                      logits, labels, probs, loss_rows, seed, rows, cols, scale);
+  return launched();
+}
+
+int tt_k_copy_padones_fwd(const float *x, float *c, float *y, long M, long K) {
+  if (M <= 0 || K < 0) return 0;
+  if (M >= 65536 || K >= (1L << 30) || !x || !c || !y) return -1;
+  hipLaunchKernelGGL(copy_padones_rows_kernel, dim3((unsigned)((K + 1 + 1023) / 1024), (unsigned)M),
+                     dim3(256), 0, stream(), x, c, y, (int)K);
   return launched();
 }
 

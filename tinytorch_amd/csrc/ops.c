@@ -125,7 +125,16 @@ static int valid_pool_params(int ph, int pw, int sh, int sw) {
     return ph > 0 && pw > 0 && sh > 0 && sw > 0;
 }
 
+TTPendConv tt_pend;
+/* defer ag_conv2d / ag_reshape launches so a relu / padones can fuse */
+static int g_conv_relu = 1;
+
 Tensor *tt_reshape(const Tensor *a, const long *new_shape, int new_ndim) {
+    return tt_reshape_ex(a, new_shape, new_ndim, 0);
+}
+
+/* defer: the copy may be left pending in tt_pend (ag_reshape) */
+Tensor *tt_reshape_ex(const Tensor *a, const long *new_shape, int new_ndim, int defer) {
     if (!a || !new_shape || new_ndim <= 0 || new_ndim > 8) return NULL;
     long numel = 1;
     for (int i = 0; i < new_ndim; i++) {
@@ -137,6 +146,13 @@ Tensor *tt_reshape(const Tensor *a, const long *new_shape, int new_ndim) {
     if (!x) return NULL;
     Tensor *out = tt_empty_dev(new_shape, new_ndim);
     if (!out) return NULL;
+    if (defer && g_conv_relu) {
+        tt_flush_pending();
+        tt_pend.out = out;
+        tt_pend.x = x;
+        tt_pend.active = TT_PEND_COPY;
+        return out;
+    }
     if (tt_k_copy(out->dev, x, numel)) return fail(out);
     return out;
 }
@@ -154,8 +170,6 @@ int tth_conv_config(long implicit_min_bytes) {
 
 int tt_conv_use_implicit(long col_bytes) { return col_bytes >= g_implicit_min_bytes; }
 
-TTPendConv tt_pend;
-static int g_conv_relu = 1;   /* defer ag_conv2d launches so a relu can fuse */
 
 int tth_conv_relu_fuse(int on) {
     const int prev = g_conv_relu;
@@ -168,7 +182,12 @@ int tth_conv_relu_fuse(int on) {
 
 void tt_flush_pending(void) {
     if (!tt_pend.active) return;
+    const int kind = tt_pend.active;
     tt_pend.active = 0;
+    if (kind == TT_PEND_COPY) {
+        if (tt_k_copy(tt_pend.out->dev, tt_pend.x, tt_pend.out->numel) != 0) ttrt_set_error(-3);
+        return;
+    }
     const int *q = tt_pend.geo;
     if (tt_k_conv2d_fwd_lds(tt_pend.x, tt_pend.w, tt_pend.b, tt_pend.out->dev, q[0], q[1], q[2],
                             q[3], q[4], q[5], q[6], q[7], q[8], q[9], q[10], q[11], q[12]) != 0)
@@ -215,7 +234,7 @@ Tensor *tt_conv2d_keepcol_ex(const Tensor *a, const Tensor *w, const Tensor *b, 
             tt_pend.out = out;
             tt_pend.x = x; tt_pend.w = wd; tt_pend.b = bd;
             for (int i = 0; i < 13; i++) tt_pend.geo[i] = q[i];
-            tt_pend.active = 1;
+            tt_pend.active = TT_PEND_CONV;
             return out;
         }
         if (tt_k_conv2d_fwd_lds(x, wd, bd, out->dev, N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho,

@@ -23,19 +23,24 @@ Tensor *tt_conv2d_keepcol(const Tensor *a, const Tensor *w, const Tensor *b,
                           int stride_h, int stride_w, int pad_h, int pad_w, float **col_out,
                           int ones_row);
 
-/* A forward convolution of ag_conv2d whose launch waits for the next call
- * into the library: when that call is ag_relu on its output, the relu is
- * computed by the same launch (tt_k_conv2d_relu_fwd_lds); any other call
+/* A forward convolution of ag_conv2d (or the copy of ag_reshape) whose
+ * launch waits for the next call into the library: when that call is ag_relu
+ * on the convolution's output, the relu is computed by the same launch
+ * (tt_k_conv2d_relu_fwd_lds); ag_padones on the copy's output likewise
+ * (tt_k_copy_padones_fwd); any other call
  * launches it first (tt_flush_pending from tt_dev, tt_data, tth_sync and
  * ag_release), so every later kernel is still enqueued after it. */
+#define TT_PEND_CONV 1
+#define TT_PEND_COPY 2        /* ag_reshape's copy; ag_padones of it fuses */
 typedef struct {
-    int active;
-    Tensor *out;              /* the convolution's output (owned by its node) */
+    int active;               /* 0, TT_PEND_CONV or TT_PEND_COPY */
+    Tensor *out;              /* the pending output (owned by its node) */
     const float *x, *w, *b;   /* device operands, retained by the node's parents */
-    int geo[13];              /* N C H W F HH WW sh sw ph pw Ho Wo */
+    int geo[13];              /* conv: N C H W F HH WW sh sw ph pw Ho Wo */
 } TTPendConv;
 extern TTPendConv tt_pend;
 void tt_flush_pending(void);
+Tensor *tt_reshape_ex(const Tensor *a, const long *new_shape, int new_ndim, int defer);
 Tensor *tt_conv2d_keepcol_ex(const Tensor *a, const Tensor *w, const Tensor *b,
                              int stride_h, int stride_w, int pad_h, int pad_w, float **col_out,
                              int ones_row, int defer);
