@@ -125,6 +125,10 @@ int tt_k_padones_fwd(const float *x, float *y, long M, long K);      /* src/auto
  * reshape (src/ops_spatial.c:22-34, a copy) followed by ag_padones
  * (src/autograd.c:195-212).  M < 65536, K < 2^30, else -1. */
 int tt_k_copy_padones_fwd(const float *x, float *c, float *y, long M, long K);
+/* r = relu(x) (M*K floats) and y = padones(r) (M x K+1) from one read of x:
+ * ag_relu (src/ops.c:104-106) followed by ag_padones (src/autograd.c:195-212).
+ * M < 65536, K < 2^30, else -1. */
+int tt_k_relu_padones_fwd(const float *x, float *r, float *y, long M, long K);
 int tt_k_padones_bwd(const float *g, float *dx, long M, long K);     /* src/autograd.c:348-359 */
 /* padones backward and the backward of the relu whose output r (M x K) was
  * padded, in one pass: dr = g without its last column, dx = dr where r > 0
@@ -206,9 +210,10 @@ int tt_k_conv2d_dx_implicit(const float *g, const float *w, float *dx,
 int tth_conv_lds(int on);
 /* 1 (default): ag_conv2d leaves its direct-convolution launch pending until
  * the next library call, and an ag_relu on its output computes both in one
- * launch (tt_k_conv2d_relu_fwd_lds); ag_reshape's copy likewise, fused with
- * an ag_padones of its output (tt_k_copy_padones_fwd); 0: every convolution
- * and reshape launches at once.
+ * launch (tt_k_conv2d_relu_fwd_lds); ag_reshape's copy and any other
+ * ag_relu likewise, fused with an ag_padones of their output
+ * (tt_k_copy_padones_fwd, tt_k_relu_padones_fwd); 0: every convolution,
+ * reshape and relu launches at once.
  * <0 queries; the previous setting is returned. */
 int tth_conv_relu_fuse(int on);
 int tt_k_conv2d_lds_plan(int N, int C, int H, int W, int F, int HH, int WW,

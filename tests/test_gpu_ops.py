@@ -335,3 +335,65 @@ def test_autograd_reshape_padones_deferred(tlib, mode):
     for a, e in zip(run(mode), ref):
         assert _bits(a, e), mode
     assert _bits(ref[0], x.reshape(16, 128))
+
+
+@pytest.mark.parametrize("M,K", [(1, 1), (256, 512), (3, 1023), (5, 3000)])
+def test_relu_padones_kernel_bitexact(tlib, M, K):
+    """tt_k_relu_padones_fwd: relu output and padded tensor bit for bit equal
+    to tt_k_relu_fwd + tt_k_padones_fwd, NaN and -0 included."""
+    from tinytorch_amd.hip import DevBuf, check
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x.flat[::5] = np.nan
+    x.flat[1::7] = -0.0
+    dx_, r1, y1, r2, y2 = (DevBuf.from_np(x), DevBuf(M * K), DevBuf(M * (K + 1)), DevBuf(M * K),
+                           DevBuf(M * (K + 1)))
+    check(tlib.tt_k_relu_padones_fwd(dx_.ptr, r1.ptr, y1.ptr, M, K), "relu_padones")
+    check(tlib.tt_k_relu_fwd(dx_.ptr, r2.ptr, M * K), "relu")
+    check(tlib.tt_k_padones_fwd(r2.ptr, y2.ptr, M, K), "padones")
+    assert _bits(r1.to_np((M, K)), r2.to_np((M, K)))
+    assert _bits(y1.to_np((M, K + 1)), y2.to_np((M, K + 1)))
+
+
+@pytest.mark.parametrize("mode", ["fused", "peek", "other", "no_padones"])
+def test_autograd_relu_padones_deferred(tlib, mode):
+    """ag_relu followed by ag_padones (one launch) against deferral off, for
+    a two-layer MLP fragment: values and gradients bit for bit equal."""
+    from tinytorch_amd.torch_py import Node
+    x = rng.standard_normal((32, 20)).astype(np.float32)
+    w1 = rng.standard_normal((21, 16)).astype(np.float32)
+    w2 = rng.standard_normal((17, 4)).astype(np.float32)
+    g = rng.standard_normal((32, 4)).astype(np.float32)
+
+    def run(m):
+        X, W1, W2 = Node.leaf(x), Node.leaf(w1), Node.leaf(w2)
+        h = X.padones().matmul(W1)
+        r = h.relu()
+        if m == "peek":
+            rv = r.value()
+        if m == "other":
+            o = W2.relu()
+            o.release()
+        if m == "no_padones":
+            s_ = r * 2.0            # a consumer other than padones launches the relu first
+            sv = s_.value()
+            s_.release()
+        p = r.padones()
+        out = p.matmul(W2)
+        vals = [h.value(), r.value(), p.value(), out.value()]
+        out.backward(g)
+        res = vals + [X.grad(), W1.grad(), W2.grad()]
+        if m == "peek":
+            assert _bits(rv, vals[1])
+        if m == "no_padones":
+            assert _bits(sv, vals[1] * np.float32(2.0))
+        for n in (out, p, r, h, X, W1, W2):
+            n.release()
+        return res
+
+    prev = tlib.tth_conv_relu_fuse(0)
+    try:
+        ref = run("plain")
+    finally:
+        tlib.tth_conv_relu_fuse(prev)
+    for a, e in zip(run(mode), ref):
+        assert _bits(a, e), mode

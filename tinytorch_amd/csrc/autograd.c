@@ -169,6 +169,19 @@ AGNode *ag_relu(AGNode *a) {
             tt_release(r);
         }
     }
+    if (tt_defer_enabled() && a->val->ndim == 2) {
+        /* a relu that a padones may consume (the MLP's hidden layers): left
+         * pending like the convolution above */
+        const float *x = tt_dev(a->val);
+        Tensor *r = x ? tt_empty_like(a->val) : NULL;
+        if (!r) return NULL;
+        AGNode *n = node_unary(a, r, OP_RELU);
+        if (!n) return NULL;
+        tt_pend.out = r;
+        tt_pend.x = x;
+        tt_pend.active = TT_PEND_RELU;
+        return n;
+    }
     return node_unary(a, tt_relu(a->val), OP_RELU);
 }
 
@@ -191,6 +204,17 @@ AGNode *ag_padones(AGNode *a) {
             if (tt_k_copy_padones_fwd(p.x, p.out->dev, v->dev, M, K) == 0)
                 return node_unary(a, v, OP_PADONES);
             tt_pend = p;  /* not launched: the plain copy runs below */
+            tt_release(v);
+        }
+    }
+    if (tt_pend.active == TT_PEND_RELU && tt_pend.out == a->val) {
+        Tensor *v = tt_empty_dev(shp, 2);
+        if (v) {
+            const TTPendConv p = tt_pend;
+            tt_pend.active = 0;
+            if (tt_k_relu_padones_fwd(p.x, p.out->dev, v->dev, M, K) == 0)
+                return node_unary(a, v, OP_PADONES);
+            tt_pend = p;  /* not launched: the plain relu runs below */
             tt_release(v);
         }
     }

@@ -278,6 +278,26 @@ __global__ void copy_padones_rows_kernel(const float *__restrict__ x, float *__r
   }
 }
 
+// padones of a relu output that is computed in the same pass: r = relu(x)
+// (x > 0 ? x : +0, NaN -> +0) and y = padones(r) from one read of x
+__global__ void relu_padones_rows_kernel(const float *__restrict__ x, float *__restrict__ r,
+                                         float *__restrict__ y, int K) {
+  const long m = blockIdx.y;
+  const float *xr = x + m * K;
+  float *rr = r + m * K;
+  float *yr = y + m * (K + 1);
+  for (int k = blockIdx.x * 1024 + threadIdx.x; k <= K && k < (int)(blockIdx.x + 1) * 1024; k += 256) {
+    if (k < K) {
+      const float v = xr[k];
+      const float o = v > 0.0f ? v : 0.0f;
+      rr[k] = o;
+      yr[k] = o;
+    } else {
+      yr[k] = 1.0f;
+    }
+  }
+}
+
 __global__ void padones_bwd_rows_kernel(const float *__restrict__ g, float *__restrict__ dx, int K) {
   const long m = blockIdx.y;
   const float *gr = g + m * (K + 1);
@@ -571,6 +591,14 @@ int tt_k_copy_padones_fwd(const float *x, float *c, float *y, long M, long K) {
   if (M >= 65536 || K >= (1L << 30) || !x || !c || !y) return -1;
   hipLaunchKernelGGL(copy_padones_rows_kernel, dim3((unsigned)((K + 1 + 1023) / 1024), (unsigned)M),
                      dim3(256), 0, stream(), x, c, y, (int)K);
+  return launched();
+}
+
+int tt_k_relu_padones_fwd(const float *x, float *r, float *y, long M, long K) {
+  if (M <= 0 || K < 0) return 0;
+  if (M >= 65536 || K >= (1L << 30) || !x || !r || !y) return -1;
+  hipLaunchKernelGGL(relu_padones_rows_kernel, dim3((unsigned)((K + 1 + 1023) / 1024), (unsigned)M),
+                     dim3(256), 0, stream(), x, r, y, (int)K);
   return launched();
 }
 

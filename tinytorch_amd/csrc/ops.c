@@ -129,6 +129,8 @@ TTPendConv tt_pend;
 /* defer ag_conv2d / ag_reshape launches so a relu / padones can fuse */
 static int g_conv_relu = 1;
 
+int tt_defer_enabled(void) { return g_conv_relu; }
+
 Tensor *tt_reshape(const Tensor *a, const long *new_shape, int new_ndim) {
     return tt_reshape_ex(a, new_shape, new_ndim, 0);
 }
@@ -184,8 +186,11 @@ void tt_flush_pending(void) {
     if (!tt_pend.active) return;
     const int kind = tt_pend.active;
     tt_pend.active = 0;
-    if (kind == TT_PEND_COPY) {
-        if (tt_k_copy(tt_pend.out->dev, tt_pend.x, tt_pend.out->numel) != 0) ttrt_set_error(-3);
+    if (kind == TT_PEND_COPY || kind == TT_PEND_RELU) {
+        const int rc = kind == TT_PEND_COPY
+                           ? tt_k_copy(tt_pend.out->dev, tt_pend.x, tt_pend.out->numel)
+                           : tt_k_relu_fwd(tt_pend.x, tt_pend.out->dev, tt_pend.out->numel);
+        if (rc != 0) ttrt_set_error(-3);
         return;
     }
     const int *q = tt_pend.geo;

@@ -32,6 +32,7 @@ Tensor *tt_conv2d_keepcol(const Tensor *a, const Tensor *w, const Tensor *b,
  * ag_release), so every later kernel is still enqueued after it. */
 #define TT_PEND_CONV 1
 #define TT_PEND_COPY 2        /* ag_reshape's copy; ag_padones of it fuses */
+#define TT_PEND_RELU 3        /* ag_relu; ag_padones of it fuses */
 typedef struct {
     int active;               /* 0, TT_PEND_CONV or TT_PEND_COPY */
     Tensor *out;              /* the pending output (owned by its node) */
@@ -40,6 +41,7 @@ typedef struct {
 } TTPendConv;
 extern TTPendConv tt_pend;
 void tt_flush_pending(void);
+int tt_defer_enabled(void);
 Tensor *tt_reshape_ex(const Tensor *a, const long *new_shape, int new_ndim, int defer);
 Tensor *tt_conv2d_keepcol_ex(const Tensor *a, const Tensor *w, const Tensor *b,
                              int stride_h, int stride_w, int pad_h, int pad_w, float **col_out,
