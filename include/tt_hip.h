@@ -129,6 +129,12 @@ int tt_k_copy_padones_fwd(const float *x, float *c, float *y, long M, long K);
  * ag_relu (src/ops.c:104-106) followed by ag_padones (src/autograd.c:195-212).
  * M < 65536, K < 2^30, else -1. */
 int tt_k_relu_padones_fwd(const float *x, float *r, float *y, long M, long K);
+/* padones backward (src/autograd.c:348-359) written to two buffers: d1 and
+ * d2 both get g without its last column; the backward pass uses it when the
+ * padded tensor is a reshape (src/autograd.c:361-369, a copy of the
+ * gradient) so the reshape's input gradient needs no second pass.
+ * M < 65536, K < 2^30, else -1. */
+int tt_k_padones_bwd2(const float *g, float *d1, float *d2, long M, long K);
 int tt_k_padones_bwd(const float *g, float *dx, long M, long K);     /* src/autograd.c:348-359 */
 /* padones backward and the backward of the relu whose output r (M x K) was
  * padded, in one pass: dr = g without its last column, dx = dr where r > 0

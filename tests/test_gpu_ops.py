@@ -397,3 +397,40 @@ def test_autograd_relu_padones_deferred(tlib, mode):
         tlib.tth_conv_relu_fuse(prev)
     for a, e in zip(run(mode), ref):
         assert _bits(a, e), mode
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_padones_backward_through_reshape(tlib, shared):
+    """reshape -> padones -> matmul: the reshape's gradient is the padones
+    backward (g without its last column) and its input's gradient the same
+    values in the input's shape, bit for bit, whether written by the one-pass
+    form (reshape used once) or by the separate passes (reshape shared)."""
+    from tinytorch_amd.torch_py import Node
+    x = rng.standard_normal((8, 4, 2, 3)).astype(np.float32)
+    w = rng.standard_normal((25, 5)).astype(np.float32)
+    g = rng.standard_normal((8, 5)).astype(np.float32)
+    X, Wn = Node.leaf(x), Node.leaf(w)
+    r = X.reshape((8, 24))
+    p = r.padones()
+    out = p.matmul(Wn)
+    if shared:
+        # r also feeds a second consumer: the separate passes run
+        s_ = r * 1.0
+        Z = Node.leaf(np.zeros((5, 24), np.float32), False)
+        z = out.matmul(Z)
+        tot = z + s_
+        G = rng.standard_normal((8, 24)).astype(np.float32)
+        tot.backward(G)
+        assert _bits(r.grad(), G)
+        assert _bits(X.grad(), G.reshape(x.shape))
+        for n in (tot, z, Z, s_, out, p, r, X, Wn):
+            n.release()
+        return
+    out.backward(g)
+    gp = p.grad()
+    assert _bits(r.grad(), gp[:, :24])
+    assert _bits(X.grad(), gp[:, :24].reshape(x.shape))
+    ref = (g.astype(np.float64) @ w.T.astype(np.float64))[:, :24]
+    assert np.abs(r.grad() - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
+    for n in (out, p, r, X, Wn):
+        n.release()

@@ -41,7 +41,7 @@ struct AGNode {
     int     requires_grad;
     int     mark;        /* DFS state: 0 new, 1 on stack, 2 done */
     int     uses;        /* backward: edges from nodes of this pass to this node */
-    int     grad_done;   /* backward: this relu's backward already ran fused */
+    int     grad_done;   /* backward: this relu's / reshape's backward already ran fused */
     int     refcount;
     float  *col;         /* conv2d: forward im2col matrix (device) */
     int     col_ones;    /* conv2d: col carries the extra row of ones */
@@ -461,6 +461,21 @@ static void backward_padones(AGNode *n) {
         tt_release(t);
         tt_release(u);
     }
+    if (a->kind == OP_RESHAPE && a->uses == 1 && !a->grad && needs(a->parents[0]) &&
+        a->parents[0]->uses == 1) {
+        /* a reshape (a copy) feeds only this padones: its gradient and its
+         * input's gradient are the same values, written by one pass */
+        AGNode *x = a->parents[0];
+        Tensor *t = tt_empty_like(a->val), *u = t ? tt_empty_like(x->val) : NULL;
+        if (u && tt_k_padones_bwd2(g, t->dev, u->dev, a->val->shape[0], a->val->shape[1]) == 0) {
+            accum_move(a, t);
+            accum_move(x, u);
+            a->grad_done = 1;
+            return;
+        }
+        tt_release(t);
+        tt_release(u);
+    }
     Tensor *t = tt_empty_like(a->val);
     if (!t) return;
     if (tt_k_padones_bwd(g, t->dev, a->val->shape[0], a->val->shape[1])) {
@@ -746,7 +761,10 @@ static void propagate(NodeList *order) {
                 break;
             case OP_SOFTMAX:    backward_softmax(n); break;
             case OP_PADONES:    backward_padones(n); break;
-            case OP_RESHAPE:    backward_reshape(n); break;
+            case OP_RESHAPE:
+                if (n->grad_done) n->grad_done = 0;
+                else backward_reshape(n);
+                break;
             case OP_CONV2D:     backward_conv2d(n); break;
             case OP_MAXPOOL2D:  backward_pool(n, 1); break;
             case OP_AVGPOOL2D:  backward_pool(n, 0); break;

@@ -298,6 +298,20 @@ __global__ void relu_padones_rows_kernel(const float *__restrict__ x, float *__r
   }
 }
 
+// padones backward whose result is also the gradient of a reshape's input
+// (same data, another shape): both copies from one read of g
+__global__ void padones_bwd2_rows_kernel(const float *__restrict__ g, float *__restrict__ d1,
+                                         float *__restrict__ d2, int K) {
+  const long m = blockIdx.y;
+  const float *gr = g + m * (K + 1);
+  const long o = m * K;
+  for (int k = blockIdx.x * 1024 + threadIdx.x; k < K && k < (int)(blockIdx.x + 1) * 1024; k += 256) {
+    const float v = gr[k];
+    d1[o + k] = v;
+    d2[o + k] = v;
+  }
+}
+
 __global__ void padones_bwd_rows_kernel(const float *__restrict__ g, float *__restrict__ dx, int K) {
   const long m = blockIdx.y;
   const float *gr = g + m * (K + 1);
@@ -599,6 +613,14 @@ int tt_k_relu_padones_fwd(const float *x, float *r, float *y, long M, long K) {
   if (M >= 65536 || K >= (1L << 30) || !x || !r || !y) return -1;
   hipLaunchKernelGGL(relu_padones_rows_kernel, dim3((unsigned)((K + 1 + 1023) / 1024), (unsigned)M),
                      dim3(256), 0, stream(), x, r, y, (int)K);
+  return launched();
+}
+
+int tt_k_padones_bwd2(const float *g, float *d1, float *d2, long M, long K) {
+  if (M <= 0 || K <= 0) return 0;
+  if (M >= 65536 || K >= (1L << 30) || !g || !d1 || !d2) return -1;
+  hipLaunchKernelGGL(padones_bwd2_rows_kernel, dim3((unsigned)((K + 1023) / 1024), (unsigned)M),
+                     dim3(256), 0, stream(), g, d1, d2, (int)K);
   return launched();
 }
 
