@@ -195,7 +195,30 @@ def test_maxpool_bitexact(tlib, p, s):
     assert bits_equal(dgx.to_np(x.shape), orc.maxpool_bwd(x, g, p, p, s, s))
 
 
-@pytest.mark.parametrize("shape", [(3, 4, 9, 8), (2, 3, 8, 12)])
+CONFIG4_POOLS = [(128, 32, 32, 32), (128, 64, 16, 16)]
+
+
+@pytest.mark.parametrize("shape", CONFIG4_POOLS)
+def test_maxpool2x2_config4_bitexact(tlib, shape):
+    """The 2x2/s2 fast kernels at the CNN config's activation shapes: forward
+    values and backward argmax routing bit-exact against the oracle (ties,
+    NaN, -Inf, -2e30 and -0.0 gradients included)."""
+    x = pool_input(shape)
+    N, C, H, W = shape
+    Ho, Wo = H // 2, W // 2
+    dx_, dy = DevBuf.from_np(x), DevBuf(N * C * Ho * Wo)
+    print("maxpool config4", shape, flush=True)
+    check(tlib.tt_k_maxpool_fwd(dx_.ptr, dy.ptr, N, C, H, W, 2, 2, 2, 2, Ho, Wo), "maxpool_fwd")
+    assert bits_equal(dy.to_np((N, C, Ho, Wo)), orc.maxpool_fwd(x, 2, 2, 2, 2))
+    g = u(N, C, Ho, Wo)
+    g[0, 0, 0, 0] = -0.0
+    dg, dgx = DevBuf.from_np(g), DevBuf(x.size)
+    check(tlib.tt_k_maxpool_bwd(dx_.ptr, dg.ptr, dgx.ptr, N, C, H, W, 2, 2, 2, 2, Ho, Wo),
+          "maxpool_bwd")
+    assert bits_equal(dgx.to_np(x.shape), orc.maxpool_bwd(x, g, 2, 2, 2, 2))
+
+
+@pytest.mark.parametrize("shape", [(3, 4, 9, 8), (2, 3, 8, 12)] + CONFIG4_POOLS)
 def test_maxpool_relu_fused_bitexact(tlib, shape):
     """The fused 2x2 pool + relu backward against the reference's two steps:
     the pool's input r is relu(x); dr = maxpool backward, dx = relu backward
