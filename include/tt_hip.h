@@ -54,6 +54,27 @@ int tt_k_gemm(int M, int N, int K,
               const float *B, int ldb, int transB,
               float *C, int ldc);
 
+/* tt_k_gemm without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, kernels and results as tt_k_gemm (bit-identical), but the
+ * workspace some shapes need (split-K partials, 16-byte aligned copies of
+ * ragged operands) comes from one static device array of
+ * TT_GEMM_SCRATCH_BYTES per GPU, held until the process ends, instead of the
+ * caching allocator.  A shape whose workspace exceeds it returns
+ * TT_E_SCRATCH with nothing launched (also reported by tth_last_error).
+ * Every call on a GPU shares that GPU's array and leaves its contents behind
+ * (the kernels write every workspace element before reading it, so nothing
+ * needs clearing).  Calls that could overlap on one GPU race on the array:
+ * the library enqueues all of them on its one stream, which orders them; do
+ * not run them from several threads or processes on one GPU at once. */
+#define TT_GEMM_SCRATCH_BYTES (32L << 20)
+#define TT_E_SCRATCH (-4)
+int tt_k_gemm_noalloc(int M, int N, int K,
+                      const float *A, int lda, int transA,
+                      const float *B, int ldb, int transB,
+                      float *C, int ldc);
+
 /* Tuning hook: force the GEMM tile (0: 128x128, 1: 128x64, 2: 64x64, 3: 32x256,
  * 4: 64x256, 5: 256x256, 6: 256x128, 7: 64x128, 8: 32x128, 9: 64x64 with 64-k
  * stages, 10: 32x128 with 64-k stages) and/or split-K count for every later

@@ -1182,6 +1182,31 @@ gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
 
 inline hipStream_t stream() { return (hipStream_t)ttrt_stream(); }
 
+// Workspace of a GEMM call (split-K partials, aligned operand copies).  By
+// default it comes from the caching allocator; inside tt_k_gemm_noalloc it is
+// carved out of the static device array `scratch` (bump allocation, nothing
+// returned until the call ends).  Every path requests all of its workspace
+// before its first launch, so a request the scratch cannot hold fails with
+// nothing enqueued.
+struct WsArena {
+  char *base;
+  size_t cap, used;
+};
+WsArena *g_arena = nullptr;
+
+float *ws_alloc(size_t bytes) {
+  if (!g_arena) return (float *)ttrt_alloc(bytes);
+  const size_t b = (bytes + 255) / 256 * 256;
+  if (g_arena->used + b > g_arena->cap) return nullptr;
+  float *p = (float *)(g_arena->base + g_arena->used);
+  g_arena->used += b;
+  return p;
+}
+
+void ws_free(void *p) {
+  if (!g_arena) ttrt_free(p);
+}
+
 inline bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 // Tile configurations (BM x BN, wave grid WM x 4/WM).
@@ -1489,26 +1514,35 @@ bool mid_ok(int M, int N, int K, const Opnd &A, const Opnd &B, bool vec) {
          (A_KC || M % 4 == 0) && (!B_NC || N % 4 == 0);
 }
 
-// pad_a / pad_b: the operand is a padded copy whose rows may be read up to
-// the next multiple of 4 columns.
-template <bool A_KC, bool B_NC>
-int run_mid(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ldc,
-            bool pad_a = false, bool pad_b = false) {
+// Split-K count of the 64x64 kernel: split until the grid covers the CUs;
+// a split's k range is a whole number of 64-k tiles (the 32-k kernel takes
+// the same ranges).  *kc_out receives the k range of one split.
+int mid_splits(int M, int N, int K, int *kc_out) {
   const int CUS = 256;
   const long tiles = (long)((M + M_T - 1) / M_T) * ((N + M_T - 1) / M_T);
   int s = 1;
   while (s < 64 && tiles * s * 2 <= CUS && K / (s * 2) >= 128) s *= 2;
   if (g_force_splits >= 1) s = g_force_splits;
-  // a split's k range is a whole number of 64-k tiles (the 32-k kernel
-  // takes the same ranges)
   int kc = ((K + s - 1) / s + 63) / 64 * 64;
   if (kc < 64) kc = 64;
-  const int splits = K > 0 ? (K + kc - 1) / kc : 1;
+  *kc_out = kc;
+  return K > 0 ? (K + kc - 1) / kc : 1;
+}
+
+// pad_a / pad_b: the operand is a padded copy whose rows may be read up to
+// the next multiple of 4 columns.
+template <bool A_KC, bool B_NC>
+int run_mid(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ldc,
+            bool pad_a = false, bool pad_b = false, float *ws_given = nullptr) {
+  const int CUS = 256;
+  const long tiles = (long)((M + M_T - 1) / M_T) * ((N + M_T - 1) / M_T);
+  int kc;
+  const int splits = mid_splits(M, N, K, &kc);
   float *target = C;
   long tld = ldc;
   float *ws = nullptr;
   if (splits > 1) {
-    ws = (float *)ttrt_alloc(sizeof(float) * (size_t)M * N * splits);
+    ws = ws_given ? ws_given : ws_alloc(sizeof(float) * (size_t)M * N * splits);
     if (!ws) return -2;
     target = ws;
     tld = N;
@@ -1533,10 +1567,11 @@ int run_mid(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ld
   else
     hipLaunchKernelGGL((gemm_mid_kernel<A_KC, B_NC, 32, 5, 4>), grid, dim3(256), 0, stream(), M,
                        N, K, A.p, A.ld, B.p, B.ld, target, tld, sstride, kc, cvec, alim, blim);
-  if (hipGetLastError() != hipSuccess) { if (ws) ttrt_free(ws); return -3; }
+  const bool own = ws && !ws_given;
+  if (hipGetLastError() != hipSuccess) { if (own) ws_free(ws); return -3; }
   if (ws) {
     const int rc = reduce_splits<EPI_STORE>(ws, C, M, N, splits, ldc, nullptr, 1);
-    ttrt_free(ws);
+    if (own) ws_free(ws);
     if (rc) return rc;
   }
   return 0;
@@ -1560,7 +1595,13 @@ int run_mid_padded(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, 
   const int lda = (ac + 3) / 4 * 4, ldb = (bc + 3) / 4 * 4;
   if (lda > (1 << 22) || ldb > (1 << 22)) return -1;
   const size_t na = pa ? (size_t)ar * lda : 0, nb = pb ? (size_t)br * ldb : 0;
-  float *buf = (float *)ttrt_alloc(sizeof(float) * (na + nb));
+  // the copies and the 64x64 kernel's split-K partials in one request, made
+  // before anything is launched
+  int kc;
+  const int splits = mid_splits(M, N, K, &kc);
+  const size_t nws = splits > 1 ? (size_t)M * N * splits : 0;
+  const size_t nab = (na + nb + 63) / 64 * 64;
+  float *buf = ws_alloc(sizeof(float) * (nab + nws));
   if (!buf) return -2;
   Opnd a2 = A, b2 = B;
   PadJob ja{A.p, A.ld, pa ? ar : 0, ac, buf, lda}, jb{B.p, B.ld, pb ? br : 0, bc, buf + na, ldb};
@@ -1573,8 +1614,8 @@ int run_mid_padded(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, 
   hipLaunchKernelGGL(pad_rows_kernel, dim3(ga + gb), dim3(256), 0, stream(), ja, jb, ga);
   if (pa) a2 = Opnd{buf, lda, 0, 1};
   if (pb) b2 = Opnd{buf + na, ldb, 0, 1};
-  const int rc = run_mid<A_KC, B_NC>(M, N, K, a2, b2, C, ldc, pa, pb);
-  ttrt_free(buf);  // stream-ordered: the GEMM above is queued before any reuse
+  const int rc = run_mid<A_KC, B_NC>(M, N, K, a2, b2, C, ldc, pa, pb, nws ? buf + nab : nullptr);
+  ws_free(buf);  // stream-ordered: the GEMM above is queued before any reuse
   return rc;
 }
 
@@ -1606,7 +1647,7 @@ int run(int M, int N, int K, Opnd A, Opnd B, float *C, long ldc, const float *bi
   float *ws = nullptr;
   int epi_direct = 1;
   if (p.splits > 1) {
-    ws = (float *)ttrt_alloc(sizeof(float) * (size_t)M * N * p.splits);
+    ws = ws_alloc(sizeof(float) * (size_t)M * N * p.splits);
     if (!ws) return -2;
     target = ws;
     tgt_ld = N;
@@ -1651,10 +1692,10 @@ int run(int M, int N, int K, Opnd A, Opnd B, float *C, long ldc, const float *bi
 #undef TT_VEC
 #undef TT_VECK
 #undef TT_LAUNCH
-  if (hipGetLastError() != hipSuccess) { if (ws) ttrt_free(ws); return -3; }
+  if (hipGetLastError() != hipSuccess) { if (ws) ws_free(ws); return -3; }
   if (ws) {
     const int rc = reduce_splits<EPI>(ws, C, M, N, p.splits, ldc, bias, HW);
-    ttrt_free(ws);
+    ws_free(ws);
     if (rc) return rc;
   }
   return 0;
@@ -1693,6 +1734,49 @@ extern "C" int tt_k_gemm(int M, int N, int K, const float *A, int lda, int trans
   if (!transA && transB)  return run<true, false, false, false, EPI_STORE>(M, N, K, a, b, C, ldc, nullptr, 1, vec);
   if (transA && !transB)  return run<false, false, true, false, EPI_STORE>(M, N, K, a, b, C, ldc, nullptr, 1, vec);
   return run<false, false, false, false, EPI_STORE>(M, N, K, a, b, C, ldc, nullptr, 1, vec);
+}
+
+// ---- the GEMM without allocation (tt_k_gemm_noalloc) ----
+// Its workspace lives in this fixed device array; each GPU holds its own copy
+// for the life of the process.  In host code the name `scratch` is only a
+// stand-in for the device symbol: its device address is looked up once per
+// device (ttg_scratch_setup, called from the runtime's initialisation) and
+// only that address is handed to kernels.
+static __device__ __align__(256) char scratch[TT_GEMM_SCRATCH_BYTES];
+namespace {
+constexpr int MAX_DEV = 64;
+char *g_scratch_dev[MAX_DEV];  // device address of `scratch`, per device
+}  // namespace
+
+extern "C" int ttg_scratch_setup(void) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) return -1;
+  if (g_scratch_dev[dev]) return 0;
+  void *ptr = nullptr;
+  if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) {
+    (void)hipGetLastError();
+    return -1;
+  }
+  g_scratch_dev[dev] = (char *)ptr;
+  return 0;
+}
+
+extern "C" int tt_k_gemm_noalloc(int M, int N, int K, const float *A, int lda, int transA,
+                                 const float *B, int ldb, int transB, float *C, int ldc) {
+  if (M < 0 || N < 0 || K < 0 || !A || !B || !C) return -1;
+  if (ttrt_init() != 0) return -3;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) return -3;
+  if (!g_scratch_dev[dev] && ttg_scratch_setup() != 0) return -3;
+  WsArena arena{g_scratch_dev[dev], (size_t)TT_GEMM_SCRATCH_BYTES, 0};
+  g_arena = &arena;
+  int rc = tt_k_gemm(M, N, K, A, lda, transA, B, ldb, transB, C, ldc);
+  g_arena = nullptr;
+  if (rc == -2) {  // the workspace this shape needs exceeds the scratch: nothing was launched
+    ttrt_set_error(TT_E_SCRATCH);
+    rc = TT_E_SCRATCH;
+  }
+  return rc;
 }
 
 extern "C" int tt_k_conv_fwd(int F, int Kc, long Ncol, int HW, const float *W, const float *col,

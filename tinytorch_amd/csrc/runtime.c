@@ -135,6 +135,8 @@ int ttrt_init(void) {
     if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) { (void)hipGetLastError(); return -1; }
     if (hipSetDevice(0) != hipSuccess) return -1;
     if (hipStreamCreate(&g_stream) != hipSuccess) return -1;
+    /* device address of the no-allocation GEMM's scratch array (gemm.hip) */
+    if (ttg_scratch_setup() != 0) return -1;
     const char *fa = getenv("TT_FAIL_ALLOC_AFTER");
     if (fa && *fa) g_fail_after = atol(fa);
     g_state = 1;

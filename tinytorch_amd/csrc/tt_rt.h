@@ -37,6 +37,9 @@ void   ttrt_set_error(int code);
 int    ttrt_last_error(void);
 size_t ttrt_bytes_in_use(void);
 size_t ttrt_bytes_cached(void);
+/* gemm.hip: look up, on the current device, the device address of the
+ * static scratch array behind tt_k_gemm_noalloc; 0 ok */
+int    ttg_scratch_setup(void);
 
 #ifdef __cplusplus
 }
