@@ -70,8 +70,10 @@ Tensor *tt_avgpool2d(const Tensor *a, int pool_h, int pool_w,
                      int stride_h, int stride_w);
 
 /* Row-major C = A*B on host pointers (A MxK, B KxN, C MxN), computed on the
- * GPU; C is overwritten.  Exported without a header by the reference
- * (src/gemm.c:569); returns 0, or -1 on allocation/launch failure.
+ * GPU.  As in the reference, C is overwritten on the leading
+ * (M/6*6) x (N/16*16) block when K > 0 and that block is not empty, and the
+ * product is added into C everywhere else.  Exported without a header by the
+ * reference (src/gemm.c:569-641); returns 0, or -1 on allocation/launch failure.
  * nthreads is accepted for ABI compatibility and ignored. */
 int tt_sgemm_rowmajor(int M, int N, int K, const float *A, const float *B,
                       float *C, int nthreads);

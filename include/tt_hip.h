@@ -28,6 +28,10 @@ int    tth_last_error(void);           /* last runtime error code (0 none) */
 void  *tth_malloc(size_t bytes);       /* cached device allocation; NULL on OOM */
 void   tth_free(void *d);
 void   tth_release_cache(void);
+/* Test hook: every device allocation after the next n fails (n < 0: none
+ * fails), as TT_FAIL_ALLOC_AFTER=n in the environment does from the first
+ * allocation; exercises the NULL-on-out-of-memory paths of the C ABI. */
+int    tth_fail_alloc_after(long n);
 size_t tth_bytes_in_use(void);
 int    tth_h2d(void *d, const void *h, size_t bytes);
 int    tth_d2h(void *h, const void *d, size_t bytes);
@@ -185,6 +189,11 @@ int tt_k_avgpool_fwd(const float *x, float *y, int N, int C, int H, int W,
                      int ph, int pw, int sh, int sw, int Ho, int Wo);             /* src/ops_spatial.c:166-201 */
 int tt_k_avgpool_bwd(const float *g, float *dx, int N, int C, int H, int W,
                      int ph, int pw, int sh, int sw, int Ho, int Wo);             /* src/autograd.c:596-628 */
+/* C (M x N) = A (M x K) * B (K x N), row-major, with the arithmetic of the
+ * reference's naive tt_matmul (src/ops.c:84-101): per output, +0.0 plus
+ * a*b for k ascending, terms with a == 0 skipped (a NaN or Inf in B meets a
+ * zero of A without reaching C); bit-identical to it. */
+int tt_k_matmul_naive(const float *A, const float *B, float *C, int M, int N, int K);
 int tt_k_sgd(float *w, const float *g, long n, float lr);  /* harness SGD: tests/gate_mnist_mlp.py:121-124 */
 /* w[i] -= lr * g[i] for count <= TT_SGD_MAX tensors in one launch */
 #define TT_SGD_MAX 16

@@ -120,6 +120,27 @@ def sgemm(A, B, nthreads=8):
     return C
 
 
+def matmul_naive(A, B):
+    """reference tt_matmul (src/ops.c:84-101): serial k, zeros of A skipped"""
+    A, B = f32(A), f32(B)
+    M, K = A.shape
+    N = B.shape[1]
+    C = np.empty((M, N), np.float32)
+    orc().orc_matmul_naive(M, N, K, _p(A), _p(B), _p(C))
+    return C
+
+
+def ref_matmul(A, B):
+    """the reference's own tt_matmul, built from its sources"""
+    ta, tb = _rt(A), _rt(B)
+    o = ref().tt_matmul(ta, tb)
+    assert o, "reference tt_matmul returned NULL"
+    out = _rnp(o, (A.shape[0], B.shape[1]))
+    for t in (ta, tb, o):
+        ref().tt_release(t)
+    return out
+
+
 def matmul_nt(X, Y):
     X, Y = f32(X), f32(Y)
     M, K = X.shape

@@ -125,3 +125,74 @@ def test_hostile_shapes_rejected_before_any_device_call():
     assert not L.tt_fromdata(None, big, 2)
     nine = (ctypes.c_long * 9)(*([1] * 9))
     assert not L.tt_new(nine, 9)
+
+
+REF_INCLUDE = "/root/reference/include"
+
+
+def prototypes(path):
+    """name -> (return type, [parameter types]) with parameter names and
+    whitespace normalised away."""
+    src = open(path).read()
+    src = re.sub(r"/\*.*?\*/", " ", src, flags=re.S)
+    src = re.sub(r"//[^\n]*", " ", src)
+    src = re.sub(r"#[^\n]*", " ", src)
+    src = re.sub(r"typedef struct \w+ \{.*?\} \w+;", " ", src, flags=re.S)
+    out = {}
+    for ret, name, params in re.findall(
+            r"([A-Za-z_][\w\s\*]*?)\s*\b([A-Za-z_]\w*)\s*\(([^;{}()]*)\)\s*;", src):
+        ret = re.sub(r"\s+", " ", ret.replace("*", " * ")).strip().split(" ")
+        ret = " ".join(t for t in ret if t not in ("typedef", "extern", '"C"', "{", "}"))
+        types = []
+        for p in params.split(","):
+            p = re.sub(r"\s+", " ", p.replace("*", " * ")).strip()
+            if not p or p == "void":
+                continue
+            toks = p.split(" ")
+            if len(toks) > 1 and re.fullmatch(r"[A-Za-z_]\w*", toks[-1]) and toks[-1] not in (
+                    "int", "long", "float", "double", "char", "size_t"):
+                toks = toks[:-1]  # drop the parameter name
+            types.append(" ".join(toks))
+        out[name] = (ret, types)
+    return out
+
+
+@pytest.mark.skipif(not os.path.isdir(REF_INCLUDE), reason="reference headers not present")
+@pytest.mark.parametrize("header", ["tensor.h", "autograd.h"])
+def test_prototypes_match_reference(header):
+    """Every reference prototype (include/tensor.h:20-50, include/autograd.h:
+    14-48) is declared here with the same return and parameter types."""
+    ref = prototypes(os.path.join(REF_INCLUDE, header))
+    ours = prototypes(os.path.join(ROOT, "include", header))
+    assert len(ref) >= 20
+    diff = {n: (ref[n], ours.get(n)) for n in ref if ours.get(n) != ref[n]}
+    assert not diff, diff
+
+
+@pytest.mark.skipif(not os.path.isdir(REF_INCLUDE), reason="reference headers not present")
+def test_tensor_struct_prefix_matches_reference():
+    """The Tensor struct keeps the reference's fields, types and order as its
+    prefix (include/tensor.h:10-17)."""
+    def fields(path):
+        src = re.sub(r"/\*.*?\*/", " ", open(path).read(), flags=re.S)
+        body = re.search(r"typedef struct Tensor \{(.*?)\} Tensor;", src, flags=re.S).group(1)
+        return [re.sub(r"\s+", " ", f.replace("*", " * ")).strip()
+                for f in body.split(";") if f.strip()]
+    ref = fields(os.path.join(REF_INCLUDE, "tensor.h"))
+    ours = fields(os.path.join(ROOT, "include", "tensor.h"))
+    assert ours[:len(ref)] == ref
+
+
+@pytest.mark.skipif(not os.path.isdir("/root/reference/src"), reason="reference sources not present")
+def test_sgemm_rowmajor_prototype_matches_reference():
+    """tt_sgemm_rowmajor (reference src/gemm.c:569, exported without a header)."""
+    src = open("/root/reference/src/gemm.c").read()
+    m = re.search(r"\bint\s+tt_sgemm_rowmajor\s*\(([^)]*)\)", src)
+    assert m
+    ref_decl = "int tt_sgemm_rowmajor(" + m.group(1) + ");"
+    tmp = os.path.join(ROOT, "build", "_ref_sgemm_proto.h")
+    os.makedirs(os.path.dirname(tmp), exist_ok=True)
+    with open(tmp, "w") as f:
+        f.write(ref_decl)
+    assert prototypes(os.path.join(ROOT, "include", "tensor.h"))["tt_sgemm_rowmajor"] == \
+        prototypes(tmp)["tt_sgemm_rowmajor"]

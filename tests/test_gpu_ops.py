@@ -86,14 +86,50 @@ def test_matmul_variants(L, sa, sb):
     L.tt_release(tb)
 
 
-def test_sgemm_rowmajor_host_pointers(L):
-    M, N, K = 37, 45, 29
+@pytest.mark.parametrize("M,N,K", [(37, 45, 29), (36, 48, 29), (5, 40, 9), (40, 15, 9),
+                                   (12, 32, 0), (1, 1, 3)])
+def test_sgemm_rowmajor_host_pointers(L, M, N, K):
+    """C on entry is overwritten on the reference's main block and
+    accumulated into everywhere else (src/gemm.c:569-641): compared with the
+    reference build itself where it exists, else with the oracle."""
     A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
     B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
-    C = np.full((M, N), 3.0, np.float32)  # overwritten, not accumulated
+    C0 = rng.uniform(2, 3, (M, N)).astype(np.float32)
+    C = C0.copy()
     assert L.tt_sgemm_rowmajor(M, N, K, A.ctypes.data_as(F32P), B.ctypes.data_as(F32P),
                                C.ctypes.data_as(F32P), 6) == 0
-    assert np.abs(C - orc.sgemm(A, B)).max() <= 1e-4 * np.sqrt(K)
+    mb, nb = M // 6 * 6, N // 16 * 16
+    keep = np.ones((M, N))
+    if K > 0 and mb and nb:   # main block overwritten, the rest accumulated
+        keep[:mb, :nb] = 0.0
+    want = A.astype(np.float64) @ B + keep * C0
+    assert np.abs(C - want).max() <= 1e-4 * np.sqrt(max(K, 1)) * 4
+    if K == 0:
+        assert np.array_equal(C, C0)
+    if orc.ref_available():   # the reference build on the same C
+        R = C0.copy()
+        assert orc.ref().tt_sgemm_rowmajor(M, N, K, A.ctypes.data, B.ctypes.data, R.ctypes.data,
+                                           1) == 0
+        assert np.abs(C - R).max() <= 1e-4 * np.sqrt(max(K, 1)) * 4
+
+
+def test_matmul_naive_bitexact_and_zero_skip(L):
+    """tt_matmul keeps the reference's naive arithmetic (src/ops.c:84-101):
+    bit-identical to the oracle, a zero of A masks NaN / Inf in B."""
+    M, N, K = 37, 300, 23
+    A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    A[A < -0.6] = 0.0
+    A[1, 2] = -0.0
+    A[3, 2] = 0.5
+    B[2, :5] = [np.nan, np.inf, -np.inf, np.nan, 1.0]
+    ta, tb = make(L, A), make(L, B)
+    o = L.tt_matmul(ta, tb)
+    got = to_np(L, o, (M, N))
+    assert bits_equal(got, orc.matmul_naive(A, B))
+    assert np.isfinite(got[1]).all() and np.isnan(got[3, 0])
+    for t in (o, ta, tb):
+        L.tt_release(t)
 
 
 def softmax_ref(x):

@@ -43,6 +43,46 @@ def test_sgemm_bitexact_vs_ref(M, N, K):
     assert same(orc.sgemm(A, B), orc.ref_sgemm(A, B))
 
 
+def naive_case(M=37, N=29, K=23):
+    A, B = u(M, K), u(K, N)
+    A[A < -0.6] = 0.0
+    A[1, 2] = -0.0
+    B[2, :5] = [np.nan, np.inf, -np.inf, np.nan, 1.0]   # row k=2 meets A[1,2] = -0.0
+    A[3, 2] = 0.5                                       # ... and a non-zero: NaN/Inf reach row 3
+    return A, B
+
+
+@needs_ref
+def test_matmul_naive_bitexact_vs_ref():
+    """reference tt_matmul (src/ops.c:84-101) including its a == 0 skip"""
+    A, B = naive_case()
+    assert same(orc.matmul_naive(A, B), orc.ref_matmul(A, B))
+
+
+def test_matmul_naive_zero_skip_and_float64():
+    """A zero of A masks NaN / Inf in the matching row of B (the skip); a
+    non-zero lets them through; finite entries equal the float64 product
+    summed in k order with float32 rounding, which for small integers is
+    exact."""
+    A, B = naive_case()
+    C = orc.matmul_naive(A, B)
+    rows_hit = np.nonzero(A[:, 2] != 0)[0]
+    assert 1 not in rows_hit and 3 in rows_hit
+    assert np.isfinite(C[1]).all()
+    assert np.isnan(C[3, 0]) and np.isnan(C[3, 3])
+    assert C[3, 1] == np.inf and C[3, 2] == -np.inf
+    # finite case: serial float32 accumulation
+    Ai = rng.integers(-3, 4, (9, 11)).astype(np.float32)
+    Bi = rng.integers(-3, 4, (11, 7)).astype(np.float32)
+    assert same(orc.matmul_naive(Ai, Bi), (Ai.astype(np.float64) @ Bi).astype(np.float32))
+    Af, Bf = u(8, 50), u(50, 6)
+    ref = np.zeros((8, 6), np.float32)
+    for k in range(50):
+        nz = Af[:, k] != 0
+        ref[nz] = ref[nz] + (Af[nz, k:k + 1] * Bf[k:k + 1, :])
+    assert same(orc.matmul_naive(Af, Bf), ref)
+
+
 @needs_ref
 def test_matmul_grads_bitexact_vs_ref():
     A, B, G = u(33, 21), u(21, 19), u(33, 19)

@@ -102,6 +102,7 @@ SIGNATURES = [
     ("tth_free", None, [VP]),
     ("tth_release_cache", None, []),
     ("tth_bytes_in_use", _SZ, []),
+    ("tth_fail_alloc_after", _I, [ctypes.c_long]),
     ("tth_h2d", _I, [VP, VP, _SZ]),
     ("tth_d2h", _I, [VP, VP, _SZ]),
     ("tt_dev", VP, [VP]),
@@ -112,6 +113,7 @@ SIGNATURES = [
     # tt_hip.h: kernels (device pointers)
     ("tth_gemm_config", _I, [_I, _I]),
     ("tt_k_gemm", _I, [_I, _I, _I, VP, _I, _I, VP, _I, _I, VP, _I]),
+    ("tt_k_matmul_naive", _I, [VP, VP, VP, _I, _I, _I]),
     ("tt_k_gemm_noalloc", _I, [_I, _I, _I, VP, _I, _I, VP, _I, _I, VP, _I]),
     ("tt_k_conv_fwd", _I, [_I, _I, _L, _I, VP, VP, VP, VP]),
     ("tt_k_conv_dw", _I, [_I, _I, _L, _I, VP, VP, VP]),

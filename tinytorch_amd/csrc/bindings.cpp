@@ -218,6 +218,11 @@ class PyDataset {
 PYBIND11_MODULE(tinytorch_pybind, m) {
   m.doc() = "tinytorch autograd Node API on the MI355X (gfx950) backend";
   m.def("available", []() { return tth_available() == 1; });
+  // waits for every queued kernel; raises when a launch (also one that an op
+  // left pending) failed
+  m.def("sync", []() {
+    if (tth_sync() != 0) throw std::runtime_error("tinytorch: device work failed");
+  });
 
   py::class_<PyNode>(m, "Node")
       .def_static("leaf", &PyNode::leaf, py::arg("arr"), py::arg("requires_grad") = true)

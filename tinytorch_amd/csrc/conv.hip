@@ -43,6 +43,7 @@
 #include <hip/hip_runtime.h>
 #include <type_traits>
 #include <stdint.h>
+#include <stdlib.h>
 #include "tt_rt.h"
 
 namespace {
@@ -1075,6 +1076,18 @@ inline long slab_floats(const Geo &g, int L) {
   return round_up((int)f, 256);
 }
 
+// TT_FAIL_DIRECT_CONV=1 (environment, read once): every launch of the direct
+// forward / dX kernels reports a launch failure although the planner covers
+// the shape, so the callers' fallbacks can be tested.
+bool fail_direct() {
+  static int v = -1;
+  if (v < 0) {
+    const char *e = getenv("TT_FAIL_DIRECT_CONV");
+    v = (e && *e && *e != '0') ? 1 : 0;
+  }
+  return v == 1;
+}
+
 // Kernels that take more than 64 KB of dynamic LDS need the limit raised
 // once per function (the runtime call is slow enough to show up per launch).
 bool allow_big_lds(const void *fn) {
@@ -1156,6 +1169,7 @@ int run_fwd(const float *x, const float *w, const float *bias, float *out, const
   const FwdPlan pl = plan_fwd(g, N, FLIP);
   if (!pl.pb) return -1;
   if (dry) return 0;
+  if (fail_direct()) return -3;
   // 16-byte loads: 4-aligned rows of x and of the weight blocks (the 3x3
   // forward kernel stages weight rows that are not 16-byte aligned with
   // 4-byte loads whatever VEC is)

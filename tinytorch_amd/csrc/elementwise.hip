@@ -545,6 +545,42 @@ __global__ void gather_u8_norm_kernel(const uint8_t *__restrict__ src, long S, l
   }
 }
 
+// Naive matmul with the reference's arithmetic: C[m][n] starts at +0.0 and
+// adds a*B[k][n] for k ascending, skipping every k where a = A[m][k] is zero
+// (so 0 * NaN / 0 * Inf in B never reach C), one multiply and one add each
+// (this file is compiled without contraction).  One lane per output; the
+// lanes of a wave take consecutive n of one row, so B's rows are read
+// coalesced and A[m][k] is one broadcast load.
+__global__ void __launch_bounds__(256)
+matmul_naive_kernel(const float *__restrict__ A, const float *__restrict__ B,
+                    float *__restrict__ C, int M, int N, int K) {
+  const int n = blockIdx.x * 256 + threadIdx.x;
+  if (n >= N) return;
+  for (int m = blockIdx.y; m < M; m += gridDim.y) {
+    const float *a = A + (long)m * K;
+    float acc = 0.0f;
+    for (int k = 0; k < K; k++) {
+      const float av = a[k];
+      if (av == 0.0f) continue;
+      acc += av * B[(long)k * N + n];
+    }
+    C[(long)m * N + n] = acc;
+  }
+}
+
+// c[m][n] += cin[m][n] for every (m, n) outside the leading mb x nb block
+// (tt_sgemm_rowmajor's accumulating tails).
+__global__ void __launch_bounds__(256)
+add_outside_kernel(float *__restrict__ c, const float *__restrict__ cin, int M, int N, int mb,
+                   int nb) {
+  const long total = (long)M * N;
+  const long stride = (long)gridDim.x * blockDim.x;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int m = (int)(i / N), n = (int)(i % N);
+    if (m >= mb || n >= nb) c[i] = cin[i] + c[i];
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -563,6 +599,19 @@ int tt_k_binary(const float *a, const float *b, float *y, long n, int op) {
 }
 int tt_k_scalar(const float *a, float *y, long n, float s, int op) {
   return run_map(n, a16(a) && a16(y), ScalarOp{a, y, s, op});
+}
+int tt_k_matmul_naive(const float *A, const float *B, float *C, int M, int N, int K) {
+  if (M < 0 || N < 0 || K < 0 || (M && N && (!A || !B || !C))) return -1;
+  if (M == 0 || N == 0) return 0;
+  const dim3 grid((unsigned)((N + 255) / 256), (unsigned)(M < 65535 ? M : 65535));
+  hipLaunchKernelGGL(matmul_naive_kernel, grid, dim3(256), 0, stream(), A, B, C, M, N, K);
+  return launched();
+}
+int ttk_add_outside(float *c, const float *cin, int M, int N, int mb, int nb) {
+  if (M <= 0 || N <= 0) return 0;
+  hipLaunchKernelGGL(add_outside_kernel, dim3(grid_for((long)M * N, 1)), dim3(256), 0, stream(),
+                     c, cin, M, N, mb, nb);
+  return launched();
 }
 int tt_k_sgd(float *w, const float *g, long n, float lr) {
   return run_map(n, a16(w) && a16(g), SgdOp{w, g, lr});

@@ -66,30 +66,62 @@ static Tensor *matmul2d(const Tensor *a, const Tensor *b) {
     return out;
 }
 
-Tensor *tt_matmul(const Tensor *a, const Tensor *b) { return matmul2d(a, b); }
+/* The reference's naive matmul (src/ops.c:84-101) keeps its own arithmetic
+ * here -- serial k order, zeros of a skipped -- so its results, NaN masking
+ * included, are the reference's bit for bit; the fast entries below run the
+ * MFMA GEMM. */
+Tensor *tt_matmul(const Tensor *a, const Tensor *b) {
+    if (!a || !b || a->ndim != 2 || b->ndim != 2) return NULL;
+    if (a->shape[1] != b->shape[0]) return NULL;
+    if (a->shape[0] > 0x7fffffffL || a->shape[1] > 0x7fffffffL || b->shape[1] > 0x7fffffffL)
+        return NULL;
+    const int M = (int)a->shape[0], K = (int)a->shape[1], N = (int)b->shape[1];
+    const float *x = tt_dev((Tensor *)a), *y = tt_dev((Tensor *)b);
+    if (!x || !y) return NULL;
+    const long shp[2] = {M, N};
+    Tensor *out = tt_empty_dev(shp, 2);
+    if (!out) return NULL;
+    if (tt_k_matmul_naive(x, y, out->dev, M, N, K)) return fail(out);
+    return out;
+}
 Tensor *tt_matmul_fast(const Tensor *a, const Tensor *b) { return matmul2d(a, b); }
 Tensor *tt_matmul_omp(const Tensor *a, const Tensor *b, int nthreads) {
     (void)nthreads;
     return matmul2d(a, b);
 }
 
+/* Host pointers in and out, as the reference (src/gemm.c:569-641).  The
+ * reference overwrites C only on its main block -- the leading
+ * (M/6*6) x (N/16*16) rows and columns, when K > 0 and that block is not
+ * empty -- and ADDS the product into C everywhere else (its scalar tails
+ * accumulate; with K == 0 or fewer than 16 columns nothing is overwritten).
+ * The same contract here: C is uploaded when any element accumulates and
+ * added to the product outside the overwritten block. */
 int tt_sgemm_rowmajor(int M, int N, int K, const float *A, const float *B, float *C,
                       int nthreads) {
     (void)nthreads;
     if (M <= 0 || N <= 0 || K < 0 || !C || (K > 0 && (!A || !B))) return -1;
+    const int Nfull = N / 16 * 16, Msfx = M / 6 * 6;
+    const int over = Nfull > 0 && K > 0 && Msfx > 0;
+    const int mb = over ? Msfx : 0, nb = over ? Nfull : 0;
+    const int accum = !(mb == M && nb == N);
     const size_t sa = sizeof(float) * (size_t)M * (size_t)K;
     const size_t sb = sizeof(float) * (size_t)K * (size_t)N;
     const size_t sc = sizeof(float) * (size_t)M * (size_t)N;
     float *dA = (float *)ttrt_alloc(sa ? sa : 4);
     float *dB = (float *)ttrt_alloc(sb ? sb : 4);
     float *dC = (float *)ttrt_alloc(sc);
+    float *dCin = accum ? (float *)ttrt_alloc(sc) : NULL;
     int rc = -1;
-    if (dA && dB && dC && ttrt_h2d(dA, A, sa) == 0 && ttrt_h2d(dB, B, sb) == 0 &&
-        tt_k_gemm(M, N, K, dA, K, 0, dB, N, 0, dC, N) == 0 && ttrt_d2h(C, dC, sc) == 0)
+    if (dA && dB && dC && (dCin || !accum) && ttrt_h2d(dA, A, sa) == 0 &&
+        ttrt_h2d(dB, B, sb) == 0 && (!accum || ttrt_h2d(dCin, C, sc) == 0) &&
+        tt_k_gemm(M, N, K, dA, K, 0, dB, N, 0, dC, N) == 0 &&
+        (!accum || ttk_add_outside(dC, dCin, M, N, mb, nb) == 0) && ttrt_d2h(C, dC, sc) == 0)
         rc = 0;
     ttrt_free(dA);
     ttrt_free(dB);
     ttrt_free(dC);
+    ttrt_free(dCin);
     return rc;
 }
 
@@ -182,21 +214,52 @@ int tth_conv_relu_fuse(int on) {
     return prev;
 }
 
-void tt_flush_pending(void) {
-    if (!tt_pend.active) return;
+/* The forward convolution without the LDS-staged kernel: the implicit GEMM
+ * where it applies (no im2col matrix), else im2col + GEMM.  q holds
+ * N C H W F HH WW sh sw ph pw Ho Wo.  0 ok. */
+static int conv_fwd_gemm(const float *x, const float *wd, const float *bd, float *out,
+                         const int *q) {
+    const int N = q[0], C = q[1], H = q[2], W = q[3], F = q[4], HH = q[5], WW = q[6];
+    const int sh = q[7], sw = q[8], ph = q[9], pw = q[10], Ho = q[11], Wo = q[12];
+    const int Kc = C * HH * WW;
+    const long Ncol = (long)N * Ho * Wo;
+    if (tt_k_conv2d_fwd_implicit(x, wd, bd, out, N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho,
+                                 Wo) == 0)
+        return 0;
+    float *col = (float *)ttrt_alloc(sizeof(float) * (size_t)Kc * (size_t)Ncol);
+    if (!col) return -2;
+    const int rc = tt_k_im2col(x, col, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo) ||
+                   tt_k_conv_fwd(F, Kc, Ncol, Ho * Wo, wd, col, bd, out);
+    ttrt_free(col);
+    return rc ? -3 : 0;
+}
+
+/* Launch the pending kernel.  A convolution whose direct kernel cannot be
+ * launched after all runs through conv_fwd_gemm instead.  When nothing can
+ * produce the output, the output tensor is marked as holding no valid data,
+ * so tt_dev / tt_data on it return NULL (and every op reading it returns
+ * NULL), as an op failing at its call would have. */
+int tt_flush_pending(void) {
+    if (!tt_pend.active) return 0;
     const int kind = tt_pend.active;
     tt_pend.active = 0;
+    int rc;
     if (kind == TT_PEND_COPY || kind == TT_PEND_RELU) {
-        const int rc = kind == TT_PEND_COPY
-                           ? tt_k_copy(tt_pend.out->dev, tt_pend.x, tt_pend.out->numel)
-                           : tt_k_relu_fwd(tt_pend.x, tt_pend.out->dev, tt_pend.out->numel);
-        if (rc != 0) ttrt_set_error(-3);
-        return;
+        rc = kind == TT_PEND_COPY ? tt_k_copy(tt_pend.out->dev, tt_pend.x, tt_pend.out->numel)
+                                  : tt_k_relu_fwd(tt_pend.x, tt_pend.out->dev, tt_pend.out->numel);
+    } else {
+        const int *q = tt_pend.geo;
+        rc = tt_k_conv2d_fwd_lds(tt_pend.x, tt_pend.w, tt_pend.b, tt_pend.out->dev, q[0], q[1],
+                                 q[2], q[3], q[4], q[5], q[6], q[7], q[8], q[9], q[10], q[11],
+                                 q[12]);
+        if (rc != 0) rc = conv_fwd_gemm(tt_pend.x, tt_pend.w, tt_pend.b, tt_pend.out->dev, q);
     }
-    const int *q = tt_pend.geo;
-    if (tt_k_conv2d_fwd_lds(tt_pend.x, tt_pend.w, tt_pend.b, tt_pend.out->dev, q[0], q[1], q[2],
-                            q[3], q[4], q[5], q[6], q[7], q[8], q[9], q[10], q[11], q[12]) != 0)
+    if (rc != 0) {
+        tt_pend.out->valid = 0;
         ttrt_set_error(-3);
+        return -3;
+    }
+    return 0;
 }
 
 Tensor *tt_conv2d_keepcol(const Tensor *a, const Tensor *w, const Tensor *b, int sh, int sw,

@@ -146,6 +146,12 @@ int ttrt_init(void) {
 void *ttrt_stream(void) { return (void *)g_stream; }
 
 void ttrt_set_error(int code) { g_err = code; }
+
+int tth_fail_alloc_after(long n) {
+    if (ttrt_init() != 0) return -1;
+    g_fail_after = n < 0 ? -1 : g_alloc_count + n;
+    return 0;
+}
 int ttrt_last_error(void) { return g_err; }
 size_t ttrt_bytes_in_use(void) { return g_in_use; }
 size_t ttrt_bytes_cached(void) { return g_cached; }

@@ -9,7 +9,8 @@
  * current (TT_V_DEV / TT_V_HOST).  tt_data() downloads into the host mirror
  * and, because the caller may write through the returned pointer, leaves the
  * HOST copy authoritative; tt_dev() (used by every op) uploads it again when
- * needed.  The host mirror is a pinned block from the runtime's host cache
+ * needed.  valid == 0 marks a tensor whose producing kernel failed to
+ * launch: both accessors return NULL for it.  The host mirror is a pinned block from the runtime's host cache
  * (direct DMA on download).  Internal outputs are created with tt_empty_dev (no zero fill); the
  * public tt_new keeps the reference's zero-filled contract. */
 #include "tt_internal.h"
@@ -104,7 +105,7 @@ void tt_release(Tensor *t) {
 
 float *tt_dev(Tensor *t) {
     if (tt_pend.active) tt_flush_pending();
-    if (!t || !t->dev) return NULL;
+    if (!t || !t->dev || !t->valid) return NULL;
     if (!(t->valid & TT_V_DEV)) {
         if (!t->data || ttrt_h2d_async(t->dev, t->data, sizeof(float) * (size_t)t->numel) != 0)
             return NULL;
@@ -118,7 +119,7 @@ float *tt_dev(Tensor *t) {
 float *tt_data(const Tensor *ct) {
     Tensor *t = (Tensor *)ct;
     if (tt_pend.active) tt_flush_pending();
-    if (!t) return NULL;
+    if (!t || !t->valid) return NULL;
     if (!(t->valid & TT_V_HOST)) {
         if (!t->data) {
             t->data = (float *)ttrt_host_alloc(sizeof(float) * (size_t)t->numel);
@@ -161,8 +162,9 @@ int tth_device_name(char *buf, int len) {
 
 void  *tth_stream(void) { return ttrt_init() == 0 ? ttrt_stream() : NULL; }
 int    tth_sync(void) {
-    tt_flush_pending();
-    return ttrt_sync();
+    const int rc = tt_flush_pending();
+    const int rs = ttrt_sync();
+    return rc ? rc : rs;
 }
 int    tth_last_error(void) { return ttrt_last_error(); }
 void  *tth_malloc(size_t bytes) { return ttrt_alloc(bytes); }

@@ -9,6 +9,7 @@
 
 #define TT_V_DEV  1
 #define TT_V_HOST 2
+/* valid == 0: no copy is current (the kernel that was to write it failed) */
 
 /* device tensor without zero fill (the producing kernel writes every element) */
 Tensor *tt_empty_dev(const long *shape, int ndim);
@@ -40,7 +41,7 @@ typedef struct {
     int geo[13];              /* conv: N C H W F HH WW sh sw ph pw Ho Wo */
 } TTPendConv;
 extern TTPendConv tt_pend;
-void tt_flush_pending(void);
+int tt_flush_pending(void);   /* 0 ok; <0 the pending output is invalid */
 int tt_defer_enabled(void);
 Tensor *tt_reshape_ex(const Tensor *a, const long *new_shape, int new_ndim, int defer);
 Tensor *tt_conv2d_keepcol_ex(const Tensor *a, const Tensor *w, const Tensor *b,

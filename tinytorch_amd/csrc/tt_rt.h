@@ -37,6 +37,9 @@ void   ttrt_set_error(int code);
 int    ttrt_last_error(void);
 size_t ttrt_bytes_in_use(void);
 size_t ttrt_bytes_cached(void);
+/* elementwise.hip: c[m][n] = cin[m][n] + c[m][n] for every (m, n) of the
+ * M x N matrices outside the leading mb x nb block */
+int    ttk_add_outside(float *c, const float *cin, int M, int N, int mb, int nb);
 /* gemm.hip: look up, on the current device, the device address of the
  * static scratch array behind tt_k_gemm_noalloc; 0 ok */
 int    ttg_scratch_setup(void);
