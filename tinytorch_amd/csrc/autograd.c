@@ -1,12 +1,16 @@
 /* Reverse-mode autograd: host-side graph, device-side arithmetic.
  *
- * Follows the reference src/autograd.c:
+ * Behaviour follows the reference src/autograd.c:
  *   node construction / ownership           :105-275
  *   accum (first grad = copy, then +=)      :44-63
  *   backward rules                          :283-628
- *   iterative post-order topo sort          :649-680
- *   reverse propagation                     :682-702
+ *   order the rules run in                  :649-702
  *   seeding and mismatch rule               :704-727
+ * The structure is this file's own: each node points at an operation
+ * descriptor (its backward rule and the release of its own state), the
+ * backward schedule is threaded through the nodes themselves (no node list,
+ * no stack allocation, nothing to reset afterwards), and release walks a
+ * worklist instead of recursing.
  *
  * Differences that do not change any observable value:
  *   * A gradient a parent does not require is never computed (the reference
@@ -24,38 +28,79 @@
 #include <stdlib.h>
 #include <string.h>
 
-typedef enum {
-    OP_LEAF, OP_ADD, OP_MUL, OP_ADDSCALAR, OP_MULSCALAR, OP_MATMUL, OP_RELU,
-    OP_SOFTMAX, OP_PADONES, OP_RESHAPE, OP_CONV2D, OP_MAXPOOL2D, OP_AVGPOOL2D,
-    OP_SOFTMAX_CE
-} OpKind;
+/* An operation kind: its name and the rule that turns a node's gradient
+ * into gradients of its inputs.  Leaves have no operation. */
+typedef struct AGOp {
+    const char *name;
+    void (*backward)(AGNode *n);
+    void (*drop)(AGNode *n);     /* frees the kind's own state; may be NULL */
+} AGOp;
 
+/* A graph node.  `in` holds the inputs (retained), packed from index 0.
+ * `at` holds what one kind of node needs beyond its inputs.  The trailing
+ * fields are scratch of the backward pass that last visited the node. */
 struct AGNode {
+    const AGOp *op;
     Tensor *val;
-    Tensor *grad;
-    AGNode *parents[3];
-    int     nparents;
-    OpKind  kind;
-    float   scalar;
-    int     params[4];
-    int     requires_grad;
-    int     mark;        /* DFS state: 0 new, 1 on stack, 2 done */
-    int     uses;        /* backward: edges from nodes of this pass to this node */
-    int     grad_done;   /* backward: this relu's / reshape's backward already ran fused */
-    int     refcount;
-    float  *col;         /* conv2d: forward im2col matrix (device) */
-    int     col_ones;    /* conv2d: col carries the extra row of ones */
-    Tensor *aux;         /* softmax_ce: probabilities */
-    Tensor *aux2;        /* softmax_ce: per-row seed (p - onehot)/rows; NULL once
-                            moved into the logits' gradient */
-    int32_t *labels;     /* softmax_ce: host copy of the labels (seed recompute) */
+    Tensor *grad;                /* NULL until a backward pass reaches the node */
+    AGNode *in[3];
+    int     n_in;
+    int     needs_grad;
+    int     refs;
+    union {
+        float s;                                          /* add/mul scalar */
+        struct { int kh, kw, sh, sw; } win;               /* pools */
+        struct { int sh, sw, ph, pw; float *col; int col_ones; } conv;
+        struct { Tensor *probs, *seed; int32_t *labels; } ce;  /* softmax-CE */
+    } at;
+    unsigned long long pass;     /* backward pass that scheduled the node */
+    int     walk;                /* depth-first walk: next input to enter */
+    AGNode *up;                  /* depth-first walk: the node it was entered from */
+    AGNode *next;                /* schedule: the node whose rule runs after this one */
+    int     fanin;               /* edges into the node from nodes of the pass */
+    int     fused;               /* its rule already ran inside a consumer's fused rule */
 };
+
+static void backward_add(AGNode *n);
+static void backward_mul(AGNode *n);
+static void backward_addscalar(AGNode *n);
+static void backward_mulscalar(AGNode *n);
+static void backward_matmul(AGNode *n);
+static void backward_relu(AGNode *n);
+static void backward_softmax(AGNode *n);
+static void backward_padones(AGNode *n);
+static void backward_reshape(AGNode *n);
+static void backward_conv2d(AGNode *n);
+static void backward_maxpool(AGNode *n);
+static void backward_avgpool(AGNode *n);
+static void backward_softmax_ce(AGNode *n);
+
+static void drop_conv(AGNode *n) { ttrt_free(n->at.conv.col); }
+static void drop_ce(AGNode *n) {
+    tt_release(n->at.ce.probs);
+    tt_release(n->at.ce.seed);
+    free(n->at.ce.labels);
+}
+
+static const AGOp OP_ADD = {"add", backward_add, NULL};
+static const AGOp OP_MUL = {"mul", backward_mul, NULL};
+static const AGOp OP_ADDSCALAR = {"addscalar", backward_addscalar, NULL};
+static const AGOp OP_MULSCALAR = {"mulscalar", backward_mulscalar, NULL};
+static const AGOp OP_MATMUL = {"matmul", backward_matmul, NULL};
+static const AGOp OP_RELU = {"relu", backward_relu, NULL};
+static const AGOp OP_SOFTMAX = {"softmax", backward_softmax, NULL};
+static const AGOp OP_PADONES = {"padones", backward_padones, NULL};
+static const AGOp OP_RESHAPE = {"reshape", backward_reshape, NULL};
+static const AGOp OP_CONV2D = {"conv2d", backward_conv2d, drop_conv};
+static const AGOp OP_MAXPOOL2D = {"maxpool2d", backward_maxpool, NULL};
+static const AGOp OP_AVGPOOL2D = {"avgpool2d", backward_avgpool, NULL};
+static const AGOp OP_SOFTMAX_CE = {"softmax_ce", backward_softmax_ce, drop_ce};
 
 /* ---------- gradient accumulation ---------- */
 
 /* p->grad += g, or p->grad = copy(g) if it has none (g is borrowed) */
 static void accum_copy(AGNode *p, Tensor *g) {
-    if (!p || !p->requires_grad || !g) return;
+    if (!p || !p->needs_grad || !g) return;
     const float *gd = tt_dev(g);
     if (!gd) return;
     if (!p->grad) {
@@ -74,7 +119,7 @@ static void accum_copy(AGNode *p, Tensor *g) {
 /* same, but g is an owned temporary: moved in when p has no grad yet */
 static void accum_move(AGNode *p, Tensor *g) {
     if (!g) return;
-    if (p && p->requires_grad && !p->grad) {
+    if (p && p->needs_grad && !p->grad) {
         p->grad = g;
         return;
     }
@@ -82,73 +127,63 @@ static void accum_move(AGNode *p, Tensor *g) {
     tt_release(g);
 }
 
-static int needs(const AGNode *p) { return p && p->requires_grad; }
+static int needs(const AGNode *p) { return p && p->needs_grad; }
 
 /* ---------- node construction ---------- */
 
-static AGNode *node_new(Tensor *val, int requires_grad) {
+/* A node computing `val` (owned; released when the node cannot be made)
+ * from up to three inputs; NULL entries of `in` are skipped.  The node needs
+ * a gradient when any input does. */
+static AGNode *make_node(Tensor *val, const AGOp *op, AGNode *x, AGNode *y, AGNode *z) {
     if (!val) return NULL;
     AGNode *n = (AGNode *)calloc(1, sizeof(AGNode));
     if (!n) { tt_release(val); return NULL; }
+    n->op = op;
     n->val = val;
-    n->requires_grad = requires_grad;
-    n->refcount = 1;
-    return n;
-}
-
-static AGNode *node_unary(AGNode *a, Tensor *val, OpKind k) {
-    AGNode *n = node_new(val, a->requires_grad);
-    if (!n) return NULL;
-    n->parents[0] = ag_retain(a);
-    n->nparents = 1;
-    n->kind = k;
-    return n;
-}
-
-static AGNode *node_binary(AGNode *a, AGNode *b, Tensor *val, OpKind k) {
-    AGNode *n = node_new(val, a->requires_grad || b->requires_grad);
-    if (!n) return NULL;
-    n->parents[0] = ag_retain(a);
-    n->parents[1] = ag_retain(b);
-    n->nparents = 2;
-    n->kind = k;
+    n->refs = 1;
+    AGNode *const in[3] = {x, y, z};
+    for (int i = 0; i < 3; i++) {
+        if (!in[i]) continue;
+        n->needs_grad |= in[i]->needs_grad;
+        n->in[n->n_in++] = ag_retain(in[i]);
+    }
     return n;
 }
 
 AGNode *ag_leaf(Tensor *t, int requires_grad) {
     if (!t) return NULL;
-    AGNode *n = node_new(tt_retain(t), requires_grad);
-    if (n) n->kind = OP_LEAF;
+    AGNode *n = make_node(tt_retain(t), NULL, NULL, NULL, NULL);
+    if (n) n->needs_grad = requires_grad ? 1 : 0;
     return n;
 }
 
 AGNode *ag_add(AGNode *a, AGNode *b) {
     if (!a || !b) return NULL;
-    return node_binary(a, b, tt_add(a->val, b->val), OP_ADD);
+    return make_node(tt_add(a->val, b->val), &OP_ADD, a, b, NULL);
 }
 
 AGNode *ag_mul(AGNode *a, AGNode *b) {
     if (!a || !b) return NULL;
-    return node_binary(a, b, tt_mul(a->val, b->val), OP_MUL);
+    return make_node(tt_mul(a->val, b->val), &OP_MUL, a, b, NULL);
 }
 
 AGNode *ag_addscalar(AGNode *a, float s) {
     if (!a) return NULL;
-    AGNode *n = node_unary(a, tt_addscalar(a->val, s), OP_ADDSCALAR);
-    if (n) n->scalar = s;
+    AGNode *n = make_node(tt_addscalar(a->val, s), &OP_ADDSCALAR, a, NULL, NULL);
+    if (n) n->at.s = s;
     return n;
 }
 
 AGNode *ag_mulscalar(AGNode *a, float s) {
     if (!a) return NULL;
-    AGNode *n = node_unary(a, tt_mulscalar(a->val, s), OP_MULSCALAR);
-    if (n) n->scalar = s;
+    AGNode *n = make_node(tt_mulscalar(a->val, s), &OP_MULSCALAR, a, NULL, NULL);
+    if (n) n->at.s = s;
     return n;
 }
 
 AGNode *ag_matmul(AGNode *a, AGNode *b) {
     if (!a || !b) return NULL;
-    return node_binary(a, b, tt_matmul_omp(a->val, b->val, 0), OP_MATMUL);
+    return make_node(tt_matmul_omp(a->val, b->val, 0), &OP_MATMUL, a, b, NULL);
 }
 
 AGNode *ag_relu(AGNode *a) {
@@ -164,7 +199,7 @@ AGNode *ag_relu(AGNode *a) {
             if (tt_k_conv2d_relu_fwd_lds(p.x, p.w, p.b, p.out->dev, r->dev, q[0], q[1], q[2],
                                          q[3], q[4], q[5], q[6], q[7], q[8], q[9], q[10], q[11],
                                          q[12]) == 0)
-                return node_unary(a, r, OP_RELU);
+                return make_node(r, &OP_RELU, a, NULL, NULL);
             tt_pend = p;  /* not launched: the plain convolution runs below */
             tt_release(r);
         }
@@ -175,19 +210,19 @@ AGNode *ag_relu(AGNode *a) {
         const float *x = tt_dev(a->val);
         Tensor *r = x ? tt_empty_like(a->val) : NULL;
         if (!r) return NULL;
-        AGNode *n = node_unary(a, r, OP_RELU);
+        AGNode *n = make_node(r, &OP_RELU, a, NULL, NULL);
         if (!n) return NULL;
         tt_pend.out = r;
         tt_pend.x = x;
         tt_pend.active = TT_PEND_RELU;
         return n;
     }
-    return node_unary(a, tt_relu(a->val), OP_RELU);
+    return make_node(tt_relu(a->val), &OP_RELU, a, NULL, NULL);
 }
 
 AGNode *ag_softmax(AGNode *a) {
     if (!a) return NULL;
-    return node_unary(a, tt_softmax(a->val), OP_SOFTMAX);
+    return make_node(tt_softmax(a->val), &OP_SOFTMAX, a, NULL, NULL);
 }
 
 AGNode *ag_padones(AGNode *a) {
@@ -202,7 +237,7 @@ AGNode *ag_padones(AGNode *a) {
             const TTPendConv p = tt_pend;
             tt_pend.active = 0;
             if (tt_k_copy_padones_fwd(p.x, p.out->dev, v->dev, M, K) == 0)
-                return node_unary(a, v, OP_PADONES);
+                return make_node(v, &OP_PADONES, a, NULL, NULL);
             tt_pend = p;  /* not launched: the plain copy runs below */
             tt_release(v);
         }
@@ -213,7 +248,7 @@ AGNode *ag_padones(AGNode *a) {
             const TTPendConv p = tt_pend;
             tt_pend.active = 0;
             if (tt_k_relu_padones_fwd(p.x, p.out->dev, v->dev, M, K) == 0)
-                return node_unary(a, v, OP_PADONES);
+                return make_node(v, &OP_PADONES, a, NULL, NULL);
             tt_pend = p;  /* not launched: the plain relu runs below */
             tt_release(v);
         }
@@ -223,53 +258,44 @@ AGNode *ag_padones(AGNode *a) {
     Tensor *v = tt_empty_dev(shp, 2);
     if (!v) return NULL;
     if (tt_k_padones_fwd(x, v->dev, M, K)) { tt_release(v); return NULL; }
-    return node_unary(a, v, OP_PADONES);
+    return make_node(v, &OP_PADONES, a, NULL, NULL);
 }
 
 AGNode *ag_reshape(AGNode *a, const long *new_shape, int new_ndim) {
     if (!a) return NULL;
     Tensor *v = tt_reshape_ex(a->val, new_shape, new_ndim, 1);
     if (!v) return NULL;
-    AGNode *n = node_unary(a, v, OP_RESHAPE);
+    AGNode *n = make_node(v, &OP_RESHAPE, a, NULL, NULL);
     if (!n && tt_pend.active && tt_pend.out == v) tt_pend.active = 0;  /* v was released */
     return n;
 }
 
 AGNode *ag_conv2d(AGNode *a, AGNode *w, AGNode *b, int sh, int sw, int ph, int pw) {
     if (!a || !w) return NULL;
-    const int keep = w->requires_grad;
-    const int ones = keep && b && b->requires_grad;  /* fuse db into the dW GEMM */
+    const int keep = w->needs_grad;
+    const int ones = keep && b && b->needs_grad;  /* fuse db into the dW GEMM */
     float *col = NULL;
     Tensor *v = tt_conv2d_keepcol_ex(a->val, w->val, b ? b->val : NULL, sh, sw, ph, pw,
                                      keep ? &col : NULL, ones, 1);
     if (!v) return NULL;
-    int req = a->requires_grad || w->requires_grad || (b && b->requires_grad);
-    AGNode *n = node_new(v, req);
+    AGNode *n = make_node(v, &OP_CONV2D, a, w, b);
     if (!n) {
         if (tt_pend.active && tt_pend.out == v) tt_pend.active = 0;  /* v was released */
         ttrt_free(col);
         return NULL;
     }
-    n->parents[0] = ag_retain(a);
-    n->parents[1] = ag_retain(w);
-    n->nparents = 2;
-    if (b) {
-        n->parents[2] = ag_retain(b);
-        n->nparents = 3;
-    }
-    n->kind = OP_CONV2D;
-    n->params[0] = sh; n->params[1] = sw;
-    n->params[2] = ph; n->params[3] = pw;
-    n->col = col;
-    n->col_ones = col && ones;
+    n->at.conv.sh = sh; n->at.conv.sw = sw;
+    n->at.conv.ph = ph; n->at.conv.pw = pw;
+    n->at.conv.col = col;
+    n->at.conv.col_ones = col && ones;
     return n;
 }
 
-static AGNode *pool_node(AGNode *a, Tensor *v, OpKind k, int ph, int pw, int sh, int sw) {
-    AGNode *n = node_unary(a, v, k);
+static AGNode *pool_node(AGNode *a, Tensor *v, const AGOp *op, int ph, int pw, int sh, int sw) {
+    AGNode *n = make_node(v, op, a, NULL, NULL);
     if (!n) return NULL;
-    n->params[0] = ph; n->params[1] = pw;
-    n->params[2] = sh; n->params[3] = sw;
+    n->at.win.kh = ph; n->at.win.kw = pw;
+    n->at.win.sh = sh; n->at.win.sw = sw;
     return n;
 }
 
@@ -277,14 +303,14 @@ AGNode *ag_maxpool2d(AGNode *a, int ph, int pw, int sh, int sw) {
     if (!a) return NULL;
     Tensor *v = tt_maxpool2d(a->val, ph, pw, sh, sw);
     if (!v) return NULL;
-    return pool_node(a, v, OP_MAXPOOL2D, ph, pw, sh, sw);
+    return pool_node(a, v, &OP_MAXPOOL2D, ph, pw, sh, sw);
 }
 
 AGNode *ag_avgpool2d(AGNode *a, int ph, int pw, int sh, int sw) {
     if (!a) return NULL;
     Tensor *v = tt_avgpool2d(a->val, ph, pw, sh, sw);
     if (!v) return NULL;
-    return pool_node(a, v, OP_AVGPOOL2D, ph, pw, sh, sw);
+    return pool_node(a, v, &OP_AVGPOOL2D, ph, pw, sh, sw);
 }
 
 /* Fused softmax + mean cross-entropy (no reference counterpart: the
@@ -307,11 +333,11 @@ AGNode *ag_softmax_ce(AGNode *logits, const int *labels, long rows) {
     if (probs && seed && loss && hlab && rows <= TT_CE_ARG_ROWS &&
         tt_k_softmax_ce_mean_hostlab(x, hlab, probs->dev, loss->dev, seed->dev, rows, cols,
                                      1.0f / (float)rows) == 0) {
-        AGNode *n = node_unary(logits, loss, OP_SOFTMAX_CE);
+        AGNode *n = make_node(loss, &OP_SOFTMAX_CE, logits, NULL, NULL);
         if (!n) { tt_release(probs); tt_release(seed); free(hlab); return NULL; }
-        n->aux = probs;
-        n->aux2 = seed;
-        n->labels = hlab;
+        n->at.ce.probs = probs;
+        n->at.ce.seed = seed;
+        n->at.ce.labels = hlab;
         return n;
     }
     free(hlab);
@@ -349,44 +375,44 @@ AGNode *ag_softmax_ce(AGNode *logits, const int *labels, long rows) {
         tt_release(probs); tt_release(seed); tt_release(loss);
         return NULL;
     }
-    AGNode *n = node_unary(logits, loss, OP_SOFTMAX_CE);
+    AGNode *n = make_node(loss, &OP_SOFTMAX_CE, logits, NULL, NULL);
     if (!n) { tt_release(probs); tt_release(seed); return NULL; }
-    n->aux = probs;
-    n->aux2 = seed;
+    n->at.ce.probs = probs;
+    n->at.ce.seed = seed;
     return n;
 }
 
 Tensor *ag_softmax_ce_probs(const AGNode *n) {
-    return (n && n->kind == OP_SOFTMAX_CE) ? n->aux : NULL;
+    return (n && n->op == &OP_SOFTMAX_CE) ? n->at.ce.probs : NULL;
 }
 
 /* ---------- accessors ---------- */
 
 Tensor *ag_value(const AGNode *n) { return n ? n->val : NULL; }
 Tensor *ag_grad(const AGNode *n) { return n ? n->grad : NULL; }
-int ag_requires_grad(const AGNode *n) { return n ? n->requires_grad : 0; }
+int ag_requires_grad(const AGNode *n) { return n ? n->needs_grad : 0; }
 
 /* ---------- backward rules ---------- */
 
 static void backward_add(AGNode *n) {
-    accum_copy(n->parents[0], n->grad);
-    accum_copy(n->parents[1], n->grad);
+    accum_copy(n->in[0], n->grad);
+    accum_copy(n->in[1], n->grad);
 }
 
 static void backward_mul(AGNode *n) {
-    AGNode *a = n->parents[0], *b = n->parents[1];
+    AGNode *a = n->in[0], *b = n->in[1];
     if (needs(a)) accum_move(a, tt_mul(n->grad, b->val));   /* g * b */
     if (needs(b)) accum_move(b, tt_mul(n->grad, a->val));   /* g * a */
 }
 
-static void backward_addscalar(AGNode *n) { accum_copy(n->parents[0], n->grad); }
+static void backward_addscalar(AGNode *n) { accum_copy(n->in[0], n->grad); }
 
 static void backward_mulscalar(AGNode *n) {
-    if (needs(n->parents[0])) accum_move(n->parents[0], tt_mulscalar(n->grad, n->scalar));
+    if (needs(n->in[0])) accum_move(n->in[0], tt_mulscalar(n->grad, n->at.s));
 }
 
 static void backward_matmul(AGNode *n) {
-    AGNode *a = n->parents[0], *b = n->parents[1];
+    AGNode *a = n->in[0], *b = n->in[1];
     const int M = (int)a->val->shape[0], K = (int)a->val->shape[1], N = (int)b->val->shape[1];
     const float *g = tt_dev(n->grad);
     if (!g) return;
@@ -405,7 +431,7 @@ static void backward_matmul(AGNode *n) {
 }
 
 static void backward_relu(AGNode *n) {
-    AGNode *a = n->parents[0];
+    AGNode *a = n->in[0];
     if (!needs(a)) return;
     const float *x = tt_dev(a->val), *g = tt_dev(n->grad);
     if (!x || !g) return;
@@ -416,7 +442,7 @@ static void backward_relu(AGNode *n) {
 }
 
 static void backward_softmax(AGNode *n) {
-    AGNode *a = n->parents[0];
+    AGNode *a = n->in[0];
     if (!needs(a)) return;
     const Tensor *s = n->val;
     const long N = s->shape[s->ndim - 1];
@@ -434,19 +460,19 @@ static void backward_softmax(AGNode *n) {
  * its input needs one and has no other consumer -- so every gradient gets
  * the same sums in the same order as with two separate steps. */
 static int relu_fusable(const AGNode *r) {
-    return r->kind == OP_RELU && r->uses == 1 && !r->grad && needs(r->parents[0]) &&
-           r->parents[0]->uses == 1;
+    return r->op == &OP_RELU && r->fanin == 1 && !r->grad && needs(r->in[0]) &&
+           r->in[0]->fanin == 1;
 }
 
 /* hand the fused pass's two gradients to the relu and its input */
 static void fused_relu_done(AGNode *r, Tensor *dr, Tensor *dx) {
     accum_move(r, dr);
-    accum_move(r->parents[0], dx);
-    r->grad_done = 1;
+    accum_move(r->in[0], dx);
+    r->fused = 1;
 }
 
 static void backward_padones(AGNode *n) {
-    AGNode *a = n->parents[0];
+    AGNode *a = n->in[0];
     if (!needs(a)) return;
     const float *g = tt_dev(n->grad);
     if (!g) return;
@@ -461,16 +487,16 @@ static void backward_padones(AGNode *n) {
         tt_release(t);
         tt_release(u);
     }
-    if (a->kind == OP_RESHAPE && a->uses == 1 && !a->grad && needs(a->parents[0]) &&
-        a->parents[0]->uses == 1) {
+    if (a->op == &OP_RESHAPE && a->fanin == 1 && !a->grad && needs(a->in[0]) &&
+        a->in[0]->fanin == 1) {
         /* a reshape (a copy) feeds only this padones: its gradient and its
          * input's gradient are the same values, written by one pass */
-        AGNode *x = a->parents[0];
+        AGNode *x = a->in[0];
         Tensor *t = tt_empty_like(a->val), *u = t ? tt_empty_like(x->val) : NULL;
         if (u && tt_k_padones_bwd2(g, t->dev, u->dev, a->val->shape[0], a->val->shape[1]) == 0) {
             accum_move(a, t);
             accum_move(x, u);
-            a->grad_done = 1;
+            a->fused = 1;
             return;
         }
         tt_release(t);
@@ -486,15 +512,15 @@ static void backward_padones(AGNode *n) {
 }
 
 static void backward_reshape(AGNode *n) {
-    AGNode *a = n->parents[0];
+    AGNode *a = n->in[0];
     if (!needs(a)) return;
     accum_move(a, tt_reshape(n->grad, a->val->shape, a->val->ndim));
 }
 
 static void backward_conv2d(AGNode *n) {
-    AGNode *a = n->parents[0], *w = n->parents[1];
-    AGNode *b = n->nparents > 2 ? n->parents[2] : NULL;
-    const int sh = n->params[0], sw = n->params[1], ph = n->params[2], pw = n->params[3];
+    AGNode *a = n->in[0], *w = n->in[1];
+    AGNode *b = n->n_in > 2 ? n->in[2] : NULL;
+    const int sh = n->at.conv.sh, sw = n->at.conv.sw, ph = n->at.conv.ph, pw = n->at.conv.pw;
     const Tensor *g = n->grad;
     const int N = (int)a->val->shape[0], C = (int)a->val->shape[1], H = (int)a->val->shape[2],
               W = (int)a->val->shape[3];
@@ -509,7 +535,7 @@ static void backward_conv2d(AGNode *n) {
     const long bshp[1] = {F};
     const int lds = tt_k_conv2d_lds_plan(N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo);
     int w_done = 0;
-    if (needs(w) && !n->col && (lds & 2)) {
+    if (needs(w) && !n->at.conv.col && (lds & 2)) {
         /* LDS-staged forward kept no col: dW (and db) read x */
         const float *x = tt_dev(a->val);
         Tensor *gw = x ? tt_empty_like(w->val) : NULL;
@@ -526,18 +552,18 @@ static void backward_conv2d(AGNode *n) {
         }
     }
     if (w_done) {
-    } else if (needs(b) && needs(w) && n->col && n->col_ones) {
+    } else if (needs(b) && needs(w) && n->at.conv.col && n->at.conv.col_ones) {
         /* dW and db from one GEMM against [col; ones] */
         Tensor *gw = tt_empty_like(w->val);
         Tensor *gb = gw ? tt_empty_dev(bshp, 1) : NULL;
-        if (gb && tt_k_conv_dw_bias(F, Kc, Ncol, HW, gd, n->col, gw->dev, gb->dev) == 0) {
+        if (gb && tt_k_conv_dw_bias(F, Kc, Ncol, HW, gd, n->at.conv.col, gw->dev, gb->dev) == 0) {
             accum_move(b, gb);
             accum_move(w, gw);
         } else {
             tt_release(gw);
             tt_release(gb);
         }
-    } else if (needs(w) && !n->col && tt_conv_use_implicit(sizeof(float) * (long)Kc * Ncol)) {
+    } else if (needs(w) && !n->at.conv.col && tt_conv_use_implicit(sizeof(float) * (long)Kc * Ncol)) {
         /* implicit forward kept no col: dW (and db, from the ones row) read x */
         const float *x = tt_dev(a->val);
         Tensor *gw = x ? tt_empty_like(w->val) : NULL;
@@ -558,7 +584,7 @@ static void backward_conv2d(AGNode *n) {
             else tt_release(gb);
         }
         if (needs(w)) {
-            float *col = n->col;
+            float *col = n->at.conv.col;
             int own = 0;
             if (!col) {
                 const float *x = tt_dev(a->val);
@@ -613,10 +639,10 @@ static void backward_conv2d(AGNode *n) {
  * runs both backwards in one pass; the relu node's own step is skipped. */
 static int backward_maxpool_relu(AGNode *n, AGNode *r, const float *g, const float *x, int N,
                                  int C, int H, int W, int Ho, int Wo) {
-    if (!relu_fusable(r) || n->params[0] != 2 || n->params[1] != 2 || n->params[2] != 2 ||
-        n->params[3] != 2)
+    if (!relu_fusable(r) || n->at.win.kh != 2 || n->at.win.kw != 2 || n->at.win.sh != 2 ||
+        n->at.win.sw != 2)
         return 0;
-    Tensor *t = tt_empty_like(r->val), *u = t ? tt_empty_like(r->parents[0]->val) : NULL;
+    Tensor *t = tt_empty_like(r->val), *u = t ? tt_empty_like(r->in[0]->val) : NULL;
     if (!u || tt_k_maxpool2x2_relu_bwd(x, g, t->dev, u->dev, N, C, H, W, Ho, Wo)) {
         tt_release(t);
         tt_release(u);
@@ -627,9 +653,9 @@ static int backward_maxpool_relu(AGNode *n, AGNode *r, const float *g, const flo
 }
 
 static void backward_pool(AGNode *n, int is_max) {
-    AGNode *a = n->parents[0];
+    AGNode *a = n->in[0];
     if (!needs(a)) return;
-    const int ph = n->params[0], pw = n->params[1], sh = n->params[2], sw = n->params[3];
+    const int ph = n->at.win.kh, pw = n->at.win.kw, sh = n->at.win.sh, sw = n->at.win.sw;
     const int N = (int)a->val->shape[0], C = (int)a->val->shape[1], H = (int)a->val->shape[2],
               W = (int)a->val->shape[3];
     const int Ho = (int)n->grad->shape[2], Wo = (int)n->grad->shape[3];
@@ -645,6 +671,9 @@ static void backward_pool(AGNode *n, int is_max) {
     accum_move(a, t);
 }
 
+static void backward_maxpool(AGNode *n) { backward_pool(n, 1); }
+static void backward_avgpool(AGNode *n) { backward_pool(n, 0); }
+
 /* the tensor's current copy is the host one and holds exactly 1.0f (the
  * default seed of ag_backward, see backward_impl) */
 static int is_host_one(const Tensor *t) {
@@ -656,33 +685,33 @@ static int is_host_one(const Tensor *t) {
  * seed tensor into the logits' gradient (no kernel); a later one recomputes
  * it (same kernel, same inputs, same bits) from the kept host labels. */
 static void backward_softmax_ce(AGNode *n) {
-    AGNode *a = n->parents[0];
+    AGNode *a = n->in[0];
     if (!needs(a)) return;
-    if (!n->aux2 && n->labels) {
+    if (!n->at.ce.seed && n->at.ce.labels) {
         const float *x = tt_dev(a->val);
         const long rows = a->val->shape[0];
         const int cols = (int)a->val->shape[1];
         Tensor *p = tt_empty_like(a->val), *s = tt_empty_like(a->val);
         float *l = (float *)ttrt_alloc(sizeof(float));
         const int ok = x && p && s && l &&
-                       tt_k_softmax_ce_mean_hostlab(x, n->labels, p->dev, l, s->dev, rows, cols,
+                       tt_k_softmax_ce_mean_hostlab(x, n->at.ce.labels, p->dev, l, s->dev, rows, cols,
                                                     1.0f / (float)rows) == 0;
         tt_release(p);
         ttrt_free(l);
         if (!ok) { tt_release(s); return; }
-        n->aux2 = s;
+        n->at.ce.seed = s;
     }
-    if (!n->aux2) return;
+    if (!n->at.ce.seed) return;
     if (is_host_one(n->grad)) {
-        if (n->labels && !a->grad) {
-            a->grad = n->aux2;
-            n->aux2 = NULL;
+        if (n->at.ce.labels && !a->grad) {
+            a->grad = n->at.ce.seed;
+            n->at.ce.seed = NULL;
         } else {
-            accum_copy(a, n->aux2);
+            accum_copy(a, n->at.ce.seed);
         }
         return;
     }
-    const float *seed = tt_dev(n->aux2), *gl = tt_dev(n->grad);
+    const float *seed = tt_dev(n->at.ce.seed), *gl = tt_dev(n->grad);
     if (!seed || !gl) return;
     Tensor *t = tt_empty_like(a->val);
     if (!t) return;
@@ -693,100 +722,63 @@ static void backward_softmax_ce(AGNode *n) {
     accum_move(a, t);
 }
 
-/* ---------- topological sort + propagation ---------- */
+/* ---------- scheduling and running the backward pass ---------- */
 
-typedef struct {
-    AGNode **items;
-    size_t len, cap;
-} NodeList;
+static unsigned long long g_pass = 0;
 
-static int list_push(NodeList *l, AGNode *n) {
-    if (l->len == l->cap) {
-        size_t nc = l->cap ? l->cap * 2 : 64;
-        AGNode **ni = (AGNode **)realloc(l->items, nc * sizeof(AGNode *));
-        if (!ni) return 0;
-        l->items = ni;
-        l->cap = nc;
-    }
-    l->items[l->len++] = n;
-    return 1;
-}
-
-/* Iterative post-order DFS from root over parents (explicit stack, so a
- * 1000-deep chain does not recurse); order ends with root. */
-static int topo_order(AGNode *root, NodeList *order) {
-    typedef struct { AGNode *n; int next; } Frame;
-    size_t cap = 64, top = 0;
-    Frame *st = (Frame *)malloc(cap * sizeof(Frame));
-    if (!st) return 0;
-    st[top].n = root; st[top].next = 0; top++;
-    root->mark = 1;
-    int ok = 1;
-    while (top > 0) {
-        Frame *f = &st[top - 1];
-        if (f->next < f->n->nparents) {
-            AGNode *c = f->n->parents[f->next++];
-            if (c->mark) continue;
-            if (top == cap) {
-                Frame *ns = (Frame *)realloc(st, 2 * cap * sizeof(Frame));
-                if (!ns) { ok = 0; break; }
-                st = ns;
-                cap *= 2;
+/* The order in which the rules run: the reverse of the post-order of a
+ * depth-first walk from `root` that enters each node's inputs in index order
+ * and every node once (a node is placed only after every input reachable
+ * through it; the reference's order, src/autograd.c:650-686, which fixes the
+ * order gradients are summed in).  The walk keeps its state in the nodes --
+ * `up` links back to the node a node was entered from, `walk` is its next
+ * input -- so it needs no stack of its own and cannot fail; finished nodes
+ * are pushed onto the front of the list through `next`, which leaves the
+ * list in running order, root first.  `fanin` counts the pass's edges into
+ * each node (the fused rules need to know a node has one consumer). */
+static AGNode *schedule(AGNode *root) {
+    const unsigned long long pass = ++g_pass;
+    AGNode *head = NULL;
+    root->pass = pass;
+    root->walk = 0;
+    root->fanin = 0;
+    root->up = NULL;
+    AGNode *cur = root;
+    while (cur) {
+        if (cur->walk < cur->n_in) {
+            AGNode *c = cur->in[cur->walk++];
+            if (c->pass != pass) {       /* first visit: enter it */
+                c->pass = pass;
+                c->walk = 0;
+                c->fanin = 0;
+                c->up = cur;
+                cur = c;
             }
-            c->mark = 1;
-            st[top].n = c; st[top].next = 0; top++;
-        } else {
-            f->n->mark = 2;
-            if (!list_push(order, f->n)) { ok = 0; break; }
-            top--;
+            c->fanin++;
+        } else {                         /* every input placed: place it */
+            cur->next = head;
+            head = cur;
+            cur = cur->up;
         }
     }
-    free(st);
-    return ok;
+    return head;
 }
 
-static void propagate(NodeList *order) {
-    for (size_t i = order->len; i-- > 0;) {
-        AGNode *n = order->items[i];
-        if (!n->grad || n->nparents == 0) continue;
-        switch (n->kind) {
-            case OP_ADD:        backward_add(n); break;
-            case OP_MUL:        backward_mul(n); break;
-            case OP_ADDSCALAR:  backward_addscalar(n); break;
-            case OP_MULSCALAR:  backward_mulscalar(n); break;
-            case OP_MATMUL:     backward_matmul(n); break;
-            case OP_RELU:
-                if (n->grad_done) n->grad_done = 0;
-                else backward_relu(n);
-                break;
-            case OP_SOFTMAX:    backward_softmax(n); break;
-            case OP_PADONES:    backward_padones(n); break;
-            case OP_RESHAPE:
-                if (n->grad_done) n->grad_done = 0;
-                else backward_reshape(n);
-                break;
-            case OP_CONV2D:     backward_conv2d(n); break;
-            case OP_MAXPOOL2D:  backward_pool(n, 1); break;
-            case OP_AVGPOOL2D:  backward_pool(n, 0); break;
-            case OP_SOFTMAX_CE: backward_softmax_ce(n); break;
-            default: break;
-        }
+static void run_rules(AGNode *head) {
+    for (AGNode *n = head; n; n = n->next) {
+        if (!n->grad || !n->op) continue;
+        if (n->fused) continue;          /* its consumer's rule did its work */
+        n->op->backward(n);
     }
+    for (AGNode *n = head; n; n = n->next) n->fused = 0;
 }
 
 /* seed_kind: 0 = ones, 1 = host floats, 2 = device tensor */
 static void backward_impl(AGNode *out, int seed_kind, const float *hseed, const Tensor *dseed) {
-    NodeList order = {0};
-    if (!topo_order(out, &order)) {
-        for (size_t i = 0; i < order.len; i++) order.items[i]->mark = 0;
-        free(order.items);
-        return;  /* marks of nodes still on the stack stay set only on OOM */
-    }
-    for (size_t i = 0; i < order.len; i++) order.items[i]->uses = 0;
-    for (size_t i = 0; i < order.len; i++)
-        for (int j = 0; j < order.items[i]->nparents; j++) order.items[i]->parents[j]->uses++;
+    AGNode *head = schedule(out);
     if (!out->grad) out->grad = tt_empty_like(out->val);
-    if (out->grad && seed_kind == 0 && out->grad->numel == 1) {
+    if (!out->grad) return;
+    if (seed_kind == 0 && out->grad->numel == 1) {
         /* a scalar ones seed is written to the host copy: no kernel, and a
          * rule that only needs to know it is 1 (softmax-CE) reads no device
          * memory; tt_dev uploads it for any rule that does */
@@ -795,29 +787,23 @@ static void backward_impl(AGNode *out, int seed_kind, const float *hseed, const 
         if (t->data) {
             t->data[0] = 1.0f;
             t->valid = TT_V_HOST;
-            propagate(&order);
-            for (size_t i = 0; i < order.len; i++) order.items[i]->mark = order.items[i]->grad_done = 0;
-            free(order.items);
+            run_rules(head);
             return;
         }
     }
-    if (out->grad) {
-        int rc;
-        float *gd = out->grad->dev;
-        if (seed_kind == 1) rc = ttrt_h2d_async(gd, hseed, sizeof(float) * (size_t)out->val->numel);
-        else if (seed_kind == 2) {
-            const float *sd = tt_dev((Tensor *)dseed);
-            rc = sd ? tt_k_copy(gd, sd, out->val->numel) : -1;
-        } else rc = tt_k_fill(gd, out->grad->numel, 1.0f);
-        tt_mark_dev_written(out->grad);
-        if (rc == 0) propagate(&order);
-    }
-    for (size_t i = 0; i < order.len; i++) order.items[i]->mark = order.items[i]->grad_done = 0;
-    free(order.items);
+    int rc;
+    float *gd = out->grad->dev;
+    if (seed_kind == 1) rc = ttrt_h2d_async(gd, hseed, sizeof(float) * (size_t)out->val->numel);
+    else if (seed_kind == 2) {
+        const float *sd = tt_dev((Tensor *)dseed);
+        rc = sd ? tt_k_copy(gd, sd, out->val->numel) : -1;
+    } else rc = tt_k_fill(gd, out->grad->numel, 1.0f);
+    tt_mark_dev_written(out->grad);
+    if (rc == 0) run_rules(head);
 }
 
 void ag_backward_from(AGNode *out, const float *seed, size_t seed_numel) {
-    if (!out || !out->requires_grad) return;
+    if (!out || !out->needs_grad) return;
     if (seed && (!out->val || seed_numel != (size_t)out->val->numel)) return;
     backward_impl(out, seed ? 1 : 0, seed, NULL);
 }
@@ -825,7 +811,7 @@ void ag_backward_from(AGNode *out, const float *seed, size_t seed_numel) {
 void ag_backward(AGNode *out) { ag_backward_from(out, NULL, 0); }
 
 void ag_backward_from_tensor(AGNode *out, const Tensor *seed) {
-    if (!out || !out->requires_grad || !seed) return;
+    if (!out || !out->needs_grad || !seed) return;
     if (!out->val || seed->numel != out->val->numel) return;
     backward_impl(out, 2, NULL, seed);
 }
@@ -1006,20 +992,31 @@ int ag_optim_step(AGOptim *o, AGNode *const *params, int count) {
 
 AGNode *ag_retain(AGNode *n) {
     if (!n) return NULL;
-    n->refcount++;
+    n->refs++;
     return n;
 }
 
+/* Dropping the last reference frees the node and releases its inputs; the
+ * nodes whose count reaches zero that way wait on a list linked through
+ * `next` (no recursion, so a long chain frees in constant stack). */
 void ag_release(AGNode *n) {
-    if (!n) return;
-    if (--n->refcount > 0) return;
-    if (tt_pend.active && tt_pend.out == n->val) tt_flush_pending();
-    tt_release(n->val);
-    tt_release(n->grad);
-    tt_release(n->aux);
-    tt_release(n->aux2);
-    free(n->labels);
-    ttrt_free(n->col);
-    for (int i = 0; i < n->nparents; i++) ag_release(n->parents[i]);
-    free(n);
+    if (!n || --n->refs > 0) return;
+    n->next = NULL;
+    AGNode *dead = n;
+    while (dead) {
+        AGNode *d = dead;
+        dead = d->next;
+        if (tt_pend.active && tt_pend.out == d->val) tt_flush_pending();
+        tt_release(d->val);
+        tt_release(d->grad);
+        if (d->op && d->op->drop) d->op->drop(d);
+        for (int i = 0; i < d->n_in; i++) {
+            AGNode *p = d->in[i];
+            if (--p->refs == 0) {
+                p->next = dead;
+                dead = p;
+            }
+        }
+        free(d);
+    }
 }
