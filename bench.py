@@ -10,10 +10,14 @@ of the fp32 MFMA peak, plus the CNN forward+backward step time.
     steps between two stream synchronisations; `value` = 2*4096^3*K / time.
   * roofline.achieved uses HIP events recorded on the library's stream (the
     stream the GEMM kernel runs on) around the K launches.
-  * extra.cnn_step_ms: config 4 (B=128, 3x32x32, conv32 -> relu -> pool ->
+  * extra.cnn_step: config 4 (B=128, 3x32x32, conv32 -> relu -> pool ->
     conv64 -> relu -> pool -> FC 4096->10, softmax-CE) forward + full
     backward + an SGD update of every weight, inputs and weights resident,
-    graph rebuilt every step through the C ABI (ctypes), wall clock per step.
+    graph rebuilt every step through the C ABI (ctypes): ms per step over K
+    back-to-back steps, the reference protocol's median (5 warmup, median of
+    20 synced steps), TFLOP/s on the step's 4.11 GFLOP against the fp32 MFMA
+    peak, and the reference CPU step beside it.  extra.mlp_step: the same
+    for config 2.
   * extra.*: the other BASELINE configs (1024^3, 4096^3 NT/TN backward GEMMs,
     8192^3, ragged, tall-skinny, MLP step); extra.conv_kernels: the direct
     convolution kernels of the CNN step alone (TFLOP/s vs the MFMA peak);
@@ -22,8 +26,10 @@ of the fp32 MFMA peak, plus the CNN forward+backward step time.
     and relu backwards as the one maxpool_relu_bwd pass).
   * cpu_baseline: the reference's own AVX2+FMA OpenMP sgemm, compiled from
     its sources into oracle/_ref (or the oracle restatement when that build
-    is missing), on this host's cores, on a bounded sample (median of 3 runs
-    of the same 4096^3 workload after one warmup).
+    is missing), on this host's cores, on a bounded sample (median of 9 runs
+    of the same 4096^3 workload after 2 warmups); beside it the reference
+    CNN and MLP steps (5 warmup + median of 20) and one 4096^3 matmul
+    backward on the reference autograd (config 3).
 
 One JSON line on stdout.  --gpus N > 1 exits: this build targets one GPU.
 """
@@ -62,6 +68,8 @@ def parse():
     ap.add_argument("--gemm-shapes", action="store_true",
                     help="only time the secondary GEMM shapes (configs 1, 3, 5; for kernel "
                          "traces of them)")
+    ap.add_argument("--gemm-shape", choices=None, default=None,
+                    help="only time one secondary GEMM shape, by its extra.* name")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 1 GiB device copy kernel 5 times (the known-size "
                          "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -249,6 +257,31 @@ class MlpStep:
             L.ag_release(n)
 
 
+# Algorithmic work of one training step (SURVEY 8(d) counts): the CNN's
+# convolution and classifier GEMMs forward + backward (conv1 dX is not part
+# of the step: its input is the image), and the MLP's minimal 617 MFLOP
+# (2*256*(785*512 + 513*256 + 257*10) forward, twice that backward without
+# the first layer's input gradient).
+CNN_STEP_GFLOP = 4.11
+MLP_STEP_GFLOP = 0.617
+
+
+def step_figures(stepper, gflop, steps):
+    """ms: K back-to-back steps between two syncs (throughput); median_ms:
+    the reference protocol, 5 warmup steps then the median of 20 steps each
+    bracketed by a sync (bench/bench_cpu.py:74-82)."""
+    from tinytorch_amd.hip import sync
+    ms = time_steps(stepper, steps, 5)
+
+    def one():
+        stepper.step()
+        sync()
+    med_ms = median_time(one, 5, 20) * 1e3
+    tf = gflop / (ms * 1e-3) / 1e3
+    return dict(ms=round(ms, 4), median_ms=round(med_ms, 4), gflop=gflop, tflops=round(tf, 2),
+                frac_of_fp32_mfma_peak=round(tf / PEAK_FP32_MFMA_TFLOPS, 4))
+
+
 def time_steps(stepper, steps, warmup):
     from tinytorch_amd.hip import sync
     prewarm(stepper.step)
@@ -376,8 +409,23 @@ def cpu_threads():
     return max(1, min(n, len(os.sched_getaffinity(0))))
 
 
+def median_time(fn, warmup, reps):
+    """the reference's timing protocol (bench/bench_cpu.py:74-82): `warmup`
+    untimed calls, then the median of `reps` timed ones, in seconds"""
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
 def cpu_baseline(threads):
-    """Reference CPU sgemm at 4096^3 and the reference CNN step, timed here."""
+    """The reference CPU path on this host: its AVX2 OpenMP sgemm at 4096^3,
+    its autograd CNN and MLP training steps, and its 4096^3 matmul backward
+    (dA = dC B^T and dB = A^T dC, the naive loops of src/autograd.c:66-103)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import orc  # the CPU baseline leg is the only part of bench.py that uses oracle/
     kind = "reference" if orc.ref_available() else "port"
@@ -393,28 +441,42 @@ def cpu_baseline(threads):
         else:
             rc = orc.orc().orc_sgemm(n, n, n, A.ctypes.data, B.ctypes.data, C.ctypes.data, threads)
         assert rc == 0
-    run()
-    ts = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        run()
-        ts.append(time.perf_counter() - t0)
-    gflops = 2.0 * n ** 3 / statistics.median(ts) / 1e9
-    # CNN step on the reference autograd path (forward, softmax, NumPy CE seed, backward)
+    gflops = 2.0 * n ** 3 / median_time(run, 2, 9) / 1e9
+    # CNN and MLP steps on the reference autograd path (forward, softmax,
+    # NumPy CE seed, backward), warmup 5 + median of 20
     x, y, P = cnn_inputs()
     step = (lambda: orc.ref_cnn_step(x, y, **P)) if kind == "reference" else \
         (lambda: orc.cnn_step(x, y, nthreads=threads, **P))
-    step()
-    cts = []
-    for _ in range(3):
+    cnn_s = median_time(step, 5, 20)
+    xm, ym, Ws = mlp_inputs()
+    mstep = (lambda: orc.ref_mlp_step(xm, ym, *Ws)) if kind == "reference" else \
+        (lambda: orc.mlp_step(xm, ym, *Ws, nthreads=threads))
+    mlp_s = median_time(mstep, 5, 20)
+    out = dict(value=round(gflops, 2), unit="GFLOP/s", cores=threads, kind=kind,
+               sample="sgemm 4096^3 NN fp32 (config 3 shape), 2 warmup + median of 9 runs; "
+                      "reference AVX2+FMA OpenMP kernel (src/gemm.c) built from its sources",
+               cnn_step_ms=round(cnn_s * 1e3, 2),
+               mlp_step_ms=round(mlp_s * 1e3, 3),
+               steps_sample="config-4 CNN and config-2 MLP fwd+bwd on the reference autograd "
+                            "path, 5 warmup + median of 20 (bench/bench_cpu.py:74-82)")
+    if kind == "reference":
+        # config 3 on the reference autograd: one forward and one backward of a
+        # 4096^3 matmul whose seed is dC ~ N(0,1); backward = dA + dB
+        G = np.random.default_rng(0x5EED + 3).standard_normal((n, n)).astype(np.float32)
+        g = orc.RefGraph()
+        nA, nB = g.leaf(A), g.leaf(B)
         t0 = time.perf_counter()
-        step()
-        cts.append(time.perf_counter() - t0)
-    return dict(value=round(gflops, 2), unit="GFLOP/s", cores=threads, kind=kind,
-                sample="sgemm 4096^3 NN fp32, 1 warmup + median of 3 runs; "
-                       "reference AVX2+FMA OpenMP kernel (src/gemm.c) built from its sources",
-                cnn_step_ms=round(statistics.median(cts) * 1e3, 2),
-                cnn_sample="config-4 CNN fwd+bwd on the reference autograd path, median of 3")
+        out_n = g.add(orc.ref().ag_matmul(nA, nB))
+        t1 = time.perf_counter()
+        g.backward(out_n, G)
+        t2 = time.perf_counter()
+        g.release()
+        out["matmul_bwd_4096_s"] = round(t2 - t1, 3)
+        out["matmul_bwd_4096_gflops"] = round(2 * 2.0 * n ** 3 / (t2 - t1) / 1e9, 2)
+        out["matmul_fwd_4096_s"] = round(t1 - t0, 3)
+        out["bwd_sample"] = ("config 3: one ag_matmul forward + one backward (dA and dB, "
+                             "the reference's naive matmul_nt / matmul_tn) at 4096^3, 1 run")
+    return out
 
 
 # secondary GEMM shapes (3 and 5): name -> (M, N, K, transA, transB)
@@ -426,9 +488,11 @@ GEMM_SHAPES = {"sgemm_1024": (1024, 1024, 1024, 0, 0),
                "sgemm_tall_65536x64x4096": (65536, 64, 4096, 0, 0)}
 
 
-def gemm_shapes(L):
+def gemm_shapes(L, only=None):
     out = {}
     for name, (M, N, K, ta, tb) in GEMM_SHAPES.items():
+        if only and name != only:
+            continue
         gg = Gemm(L, M, N, K, ta, tb)
         steps = max(10, min(200, int(3e12 / gg.flops())))
         _, ms = time_gemm(L, gg, steps, 2)
@@ -459,8 +523,10 @@ def main():
         ms = time_steps(MlpStep(L), args.steps, args.warmup)
         print(json.dumps({"mlp_step_ms": round(ms, 4), "steps": args.steps, "warmup": args.warmup}))
         return
-    if args.gemm_shapes:
-        print(json.dumps(gemm_shapes(L)))
+    if args.gemm_shapes or args.gemm_shape:
+        if args.gemm_shape and args.gemm_shape not in GEMM_SHAPES:
+            sys.exit(f"bench.py: unknown --gemm-shape {args.gemm_shape}; one of {list(GEMM_SHAPES)}")
+        print(json.dumps(gemm_shapes(L, args.gemm_shape)))
         return
     if args.copy_calib:
         from tinytorch_amd.hip import DevBuf, check, sync
@@ -486,11 +552,13 @@ def main():
     if not args.no_extra:
         extra.update(gemm_shapes(L))
         cnn = CnnStep(L)
-        extra["cnn_step_ms"] = round(time_steps(cnn, 20, 5), 3)
-        log("cnn step ms", extra["cnn_step_ms"])
+        extra["cnn_step"] = step_figures(cnn, CNN_STEP_GFLOP, 20)
+        extra["cnn_step_ms"] = extra["cnn_step"]["ms"]
+        log("cnn step", extra["cnn_step"])
         mlp = MlpStep(L)
-        extra["mlp_step_ms"] = round(time_steps(mlp, 50, 5), 3)
-        log("mlp step ms", extra["mlp_step_ms"])
+        extra["mlp_step"] = step_figures(mlp, MLP_STEP_GFLOP, 50)
+        extra["mlp_step_ms"] = extra["mlp_step"]["ms"]
+        log("mlp step", extra["mlp_step"])
         extra["conv_kernels"] = conv_kernels(L)
         for k, v in extra["conv_kernels"].items():
             log(f"{k:22s} {v['us']:8.2f} us {v['tflops']:6.1f} TFLOP/s ({100 * v['frac_of_mfma_peak']:.1f}% of fp32 MFMA)")
@@ -504,6 +572,16 @@ def main():
         log(f"cpu baseline on {threads} threads ...")
         cpu = cpu_baseline(threads)
         log("cpu", cpu)
+
+    if cpu and extra.get("cnn_step"):
+        for key, cpu_key in (("cnn_step", "cnn_step_ms"), ("mlp_step", "mlp_step_ms")):
+            extra[key]["cpu_ms"] = cpu[cpu_key]
+            extra[key]["speedup_vs_cpu"] = round(cpu[cpu_key] / extra[key]["ms"], 1)
+        if "matmul_bwd_4096_s" in cpu:
+            gpu_ms = extra["sgemm_4096_nt_dA"]["ms"] + extra["sgemm_4096_tn_dB"]["ms"]
+            extra["matmul_bwd_4096"] = dict(ms=round(gpu_ms, 4), cpu_ms=round(
+                cpu["matmul_bwd_4096_s"] * 1e3, 1), speedup_vs_cpu=round(
+                cpu["matmul_bwd_4096_s"] * 1e3 / gpu_ms, 1))
 
     out = {
         "metric": "fp32 GEMM TFLOP/s @4096^3 (% MFMA peak) + CNN fwd+bwd step ms",
