@@ -21,7 +21,8 @@ CFLAGS_HOST := -O2 -fPIC -std=c11 -Wall -Wextra -D__HIP_PLATFORM_AMD__ -I$(ROCM)
                -Iinclude -I$(CSRC)
 
 HOST_SRCS := $(CSRC)/runtime.c $(CSRC)/tensor.c $(CSRC)/ops.c $(CSRC)/autograd.c $(CSRC)/dataset.c
-HIP_SRCS  := $(CSRC)/gemm.hip $(CSRC)/conv.hip $(CSRC)/elementwise.hip $(CSRC)/spatial.hip
+HIP_SRCS  := $(CSRC)/gemm.hip $(CSRC)/conv.hip $(CSRC)/elementwise.hip $(CSRC)/spatial.hip \
+             $(CSRC)/head.hip
 HDRS      := $(wildcard include/*.h) $(wildcard $(CSRC)/*.h)
 HOST_OBJS := $(patsubst $(CSRC)/%.c,$(BUILD)/obj/%.o,$(HOST_SRCS))
 HIP_OBJS  := $(patsubst $(CSRC)/%.hip,$(BUILD)/obj/%.o,$(HIP_SRCS))

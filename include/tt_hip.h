@@ -143,6 +143,16 @@ int tt_k_softmax_ce_mean(const float *logits, const int32_t *labels, float *prob
 #define TT_CE_ARG_ROWS 512
 int tt_k_softmax_ce_mean_hostlab(const float *logits, const int32_t *host_labels, float *probs,
                                  float *loss_mean, float *seed, long rows, int cols, float scale);
+/* Backward of a classifier layer, one launch: dW (K x N) = A^T * G summed over m
+ * ascending (reference matmul_tn, src/autograd.c:87-103) and dA (M x K) =
+ * G * W^T summed over j ascending (reference matmul_nt, :66-84), both
+ * bit-identical to the reference loops; either may be NULL.  d1 / d2
+ * (optional, need dA): dA without its last column (M x (K-1)) -- the
+ * padones backward (:348-359); d2 is masked by R > 0 when R is given (the
+ * relu backward through the relu output R, :318-327).  N <= 32 and, with
+ * dW, M <= 480 (a block of A is staged in LDS), else -1. */
+int tt_k_head_bwd(const float *A, int M, int K, const float *W, int N, const float *G,
+                  float *dW, float *dA, float *d1, float *d2, const float *R);
 /* y = x * s[0], s a device scalar (chain rule through a scalar loss) */
 int tt_k_scale_by_dev(const float *x, const float *s, float *y, long n);
 int tt_k_padones_fwd(const float *x, float *y, long M, long K);      /* src/autograd.c:195-212 */

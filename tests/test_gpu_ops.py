@@ -341,8 +341,10 @@ def test_autograd_reshape_padones_deferred(tlib, mode):
     copy first."""
     from tinytorch_amd.torch_py import Node
     x = rng.standard_normal((16, 8, 4, 4)).astype(np.float32)
-    w = rng.standard_normal((129, 10)).astype(np.float32)
-    g = rng.standard_normal((16, 10)).astype(np.float32)
+    # 40 columns: above the fused classifier head's limit (32), whose
+    # backward sums in another order than the GEMM path this compares with
+    w = rng.standard_normal((129, 40)).astype(np.float32)
+    g = rng.standard_normal((16, 40)).astype(np.float32)
 
     def run(m):
         X, Wn = Node.leaf(x), Node.leaf(w)
@@ -396,9 +398,11 @@ def test_autograd_relu_padones_deferred(tlib, mode):
     a two-layer MLP fragment: values and gradients bit for bit equal."""
     from tinytorch_amd.torch_py import Node
     x = rng.standard_normal((32, 20)).astype(np.float32)
-    w1 = rng.standard_normal((21, 16)).astype(np.float32)
-    w2 = rng.standard_normal((17, 4)).astype(np.float32)
-    g = rng.standard_normal((32, 4)).astype(np.float32)
+    # 40 columns: above the fused classifier head's limit (32), whose
+    # backward sums in another order than the GEMM path this compares with
+    w1 = rng.standard_normal((21, 40)).astype(np.float32)
+    w2 = rng.standard_normal((41, 40)).astype(np.float32)
+    g = rng.standard_normal((32, 40)).astype(np.float32)
 
     def run(m):
         X, W1, W2 = Node.leaf(x), Node.leaf(w1), Node.leaf(w2)

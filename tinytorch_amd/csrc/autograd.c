@@ -181,6 +181,10 @@ AGNode *ag_mulscalar(AGNode *a, float s) {
     return n;
 }
 
+/* The backward of a matmul with at most this many output columns (a
+ * classifier layer) runs as one launch (backward_matmul_head). */
+#define HEAD_MAX_N 32
+
 AGNode *ag_matmul(AGNode *a, AGNode *b) {
     if (!a || !b) return NULL;
     return make_node(tt_matmul_omp(a->val, b->val, 0), &OP_MATMUL, a, b, NULL);
@@ -411,11 +415,57 @@ static void backward_mulscalar(AGNode *n) {
     if (needs(n->in[0])) accum_move(n->in[0], tt_mulscalar(n->grad, n->at.s));
 }
 
+static int relu_fusable(const AGNode *r);
+
+/* The backward of a matmul with at most HEAD_MAX_N columns in one launch
+ * (tt_k_head_bwd): dA and dB and, when A is a padones used only here whose
+ * input is used only by it, that input's gradient too -- and, when the
+ * input is a reshape or a fusable relu, the gradient of the node before it.
+ * The nodes whose rules this covers are marked `fused`.  0 when done. */
+static int backward_matmul_head(AGNode *n, const float *g) {
+    AGNode *a = n->in[0], *b = n->in[1];
+    const int M = (int)a->val->shape[0], K = (int)a->val->shape[1], N = (int)b->val->shape[1];
+    if (N > HEAD_MAX_N) return -1;
+    const float *ad = needs(b) ? tt_dev(a->val) : NULL;
+    const float *bd = needs(a) ? tt_dev(b->val) : NULL;
+    if ((needs(b) && !ad) || (needs(a) && !bd)) return -1;
+    AGNode *x = NULL, *y = NULL;
+    const float *R = NULL;
+    if (needs(a) && a->op == &OP_PADONES && a->fanin == 1 && !a->grad && needs(a->in[0]) &&
+        a->in[0]->fanin == 1 && !a->in[0]->grad) {
+        x = a->in[0];
+        AGNode *z = x->in[0];
+        if (x->op == &OP_RESHAPE && needs(z) && z->fanin == 1 && !z->grad) {
+            y = z;
+        } else if (relu_fusable(x)) {
+            y = z;
+            R = tt_dev(x->val);
+            if (!R) return -1;
+        }
+    }
+    Tensor *gb = needs(b) ? tt_empty_like(b->val) : NULL;
+    Tensor *ga = needs(a) ? tt_empty_like(a->val) : NULL;
+    Tensor *tx = x ? tt_empty_like(x->val) : NULL;
+    Tensor *ty = y ? tt_empty_like(y->val) : NULL;
+    if ((needs(b) && !gb) || (needs(a) && !ga) || (x && !tx) || (y && !ty) ||
+        tt_k_head_bwd(ad, M, K, bd, N, g, gb ? gb->dev : NULL, ga ? ga->dev : NULL,
+                      tx ? tx->dev : NULL, ty ? ty->dev : NULL, R) != 0) {
+        tt_release(gb); tt_release(ga); tt_release(tx); tt_release(ty);
+        return -1;
+    }
+    if (gb) accum_move(b, gb);
+    if (ga) accum_move(a, ga);
+    if (tx) { accum_move(x, tx); a->fused = 1; }
+    if (ty) { accum_move(y, ty); x->fused = 1; }
+    return 0;
+}
+
 static void backward_matmul(AGNode *n) {
     AGNode *a = n->in[0], *b = n->in[1];
     const int M = (int)a->val->shape[0], K = (int)a->val->shape[1], N = (int)b->val->shape[1];
     const float *g = tt_dev(n->grad);
     if (!g) return;
+    if (tt_defer_enabled() && backward_matmul_head(n, g) == 0) return;
     if (needs(a)) {  /* dA = g (MxN) * b^T (b is KxN) */
         const float *bd = tt_dev(b->val);
         Tensor *ga = bd ? tt_empty_like(a->val) : NULL;

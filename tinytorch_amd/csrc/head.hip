@@ -1,0 +1,195 @@
+// Backward of a classifier layer on gfx950 in one launch: a matmul with few
+// output columns (N <= 32) together with the backward of the padones (and
+// the reshape or relu before it) that feeds it.
+//
+// Replaces, for the last layer of the reference's training steps:
+//   dW = h_pad^T * dlogits      reference src/autograd.c:87-103 (matmul_tn)
+//   dh_pad = dlogits * W^T      reference src/autograd.c:66-84  (matmul_nt)
+//   padones backward, reshape backward (a copy) or relu backward
+//                               reference src/autograd.c:318-327,348-369
+// which the general path runs as three launches (two GEMMs of a few MFLOP
+// and the padones backward).  Kernels this small are bound by latency on
+// MI355X, so the kernel spreads its work over hundreds of waves with short
+// per-lane loops, issues its global loads unconditionally (addresses
+// clamped, values selected) and in batches, so a batch costs one memory
+// round trip, and stages shared operands in LDS once per workgroup.
+//
+// Two kinds of workgroups in one grid:
+//   dW blocks: 64 rows k of W x 4 columns j (32 x 8 for large M), one
+//     output per lane, summed over m ascending from LDS -- the reference
+//     matmul_tn order (+0.0, then one multiply and one add per m);
+//   dA blocks: 64 columns k x 32 rows m, each lane's 8 outputs summed over j
+//     ascending -- the reference matmul_nt order.
+// Both are bit-identical to the reference's loops (this file is compiled
+// without contraction).  dh is written whole (the padones node's gradient)
+// and, without its last column, once or twice more: the gradient of the
+// padones' input and, when that input is a reshape (a copy) or a relu used
+// only here, the gradient of the node before it (for a relu, masked by
+// relu output > 0, which equals relu input > 0).
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+#include "tt_rt.h"
+
+namespace {
+
+inline hipStream_t stream() { return (hipStream_t)ttrt_stream(); }
+inline int launched() { return hipGetLastError() == hipSuccess ? 0 : -3; }
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int NT = 256;
+
+
+// Every padding element of a staged block is loaded from here.
+__device__ float g_head_zero[4];
+
+// Stage a rows x COLS block (COLS a power of two <= 64) into LDS:
+// dst[r * dstride + c] = src[r * sstride + c] for r < nr and c < nc, else 0,
+// for r < rows.  Lane t takes column t % COLS of rows t / COLS + (NT/COLS) u;
+// U loads per lane per batch, all issued before the first LDS store.
+template <int COLS, int U>
+__device__ __forceinline__ void stage(float *dst, int dstride, const float *__restrict__ src,
+                                      long sstride, int rows, int nr, int nc) {
+  constexpr int RPB = NT / COLS;             // rows per pass of the workgroup
+  const int c = threadIdx.x % COLS, r0 = threadIdx.x / COLS;
+  for (int base = 0; base < rows; base += RPB * U) {
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int r = base + r0 + RPB * u;
+      const bool ok = r < nr && c < nc;
+      v[u] = *(ok ? src + r * sstride + c : g_head_zero);
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int r = base + r0 + RPB * u;
+      if (r < rows) dst[r * dstride + c] = v[u];
+    }
+  }
+}
+
+
+// ---- backward ----
+constexpr int DA_M = 32;  // rows m per dA workgroup (8 per lane)
+template <int NC>
+__global__ void __launch_bounds__(NT)
+head_bwd_kernel(const float *__restrict__ A, int M, int K, const float *__restrict__ W, int N,
+                const float *__restrict__ G, float *__restrict__ dW, float *__restrict__ dA,
+                float *__restrict__ d1, float *__restrict__ d2, const float *__restrict__ R,
+                int nbw, int KW, int nkw) {
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nkb = (K + 63) / 64;
+  if ((int)blockIdx.x < nbw) {
+    // dW[k][j] for KW rows k and JW = 256 / KW columns j: lane t takes
+    // k = k0 + t % KW, j = j0 + t / KW.  As (M x KW), Gs (M x JW)
+    const int JW = NT / KW;
+    const int kb = blockIdx.x % nkw, jb = blockIdx.x / nkw;
+    const int k0 = kb * KW, j0 = jb * JW;
+    float *As = lds, *Gs = lds + M * KW;
+    if (KW == 64) {
+      stage<64, 16>(As, 64, A + k0, K, M, M, min(64, K - k0));
+      stage<4, 8>(Gs, 4, G + j0, N, M, M, min(4, N - j0));
+    } else {
+      stage<32, 16>(As, 32, A + k0, K, M, M, min(32, K - k0));
+      stage<8, 8>(Gs, 8, G + j0, N, M, M, min(8, N - j0));
+    }
+    __syncthreads();
+    const int kl = tid % KW, jl = tid / KW;
+    const int k = k0 + kl, j = j0 + jl;
+    if (j >= N || k >= K) return;
+    const float *ac = As + kl, *gc = Gs + jl;
+    float acc = 0.0f;
+    int m = 0;
+    for (; m + 16 <= M; m += 16) {
+      float a[16], g[16];
+#pragma unroll
+      for (int u = 0; u < 16; u++) { a[u] = ac[(m + u) * KW]; g[u] = gc[(m + u) * JW]; }
+#pragma unroll
+      for (int u = 0; u < 16; u++) acc += a[u] * g[u];
+    }
+    for (; m < M; m++) acc += ac[m * KW] * gc[m * JW];
+    dW[(long)k * N + j] = acc;
+    return;
+  }
+  // dA block: columns [k0, k0 + 64) x rows [m0, m0 + DA_M); Ws, Gs (64 / DA_M x NC)
+  const int blk = blockIdx.x - nbw;
+  const int k0 = (blk % nkb) * 64, m0 = (blk / nkb) * DA_M;
+  float *Ws = lds, *Gs = lds + 64 * NC;
+  stage<NC, 4>(Ws, NC, W + (long)k0 * N, N, 64, min(64, K - k0), N);
+  stage<NC, 4>(Gs, NC, G + (long)m0 * N, N, DA_M, min(DA_M, M - m0), N);
+  const int kl = lane, mg = wave;
+  const int k = k0 + kl;
+  const int K1 = K - 1;
+  constexpr int MI = DA_M / 4;  // rows per lane: m0 + mg + 4 i
+  float rv[MI];
+  if (R && d2) {
+    const int kc = k < K1 ? k : K1 - 1;
+#pragma unroll
+    for (int i = 0; i < MI; i++) {
+      const int m = m0 + mg + 4 * i;
+      rv[i] = R[(long)(m < M ? m : M - 1) * K1 + kc];
+    }
+  }
+  __syncthreads();
+  if (k >= K) return;
+  f32x4 w4[NC / 4];
+#pragma unroll
+  for (int v = 0; v < NC / 4; v++) w4[v] = *(const f32x4 *)(Ws + kl * NC + 4 * v);
+#pragma unroll
+  for (int i = 0; i < MI; i++) {
+    const int m = m0 + mg + 4 * i;
+    if (m < M) {
+      const f32x4 *gr = (const f32x4 *)(Gs + (mg + 4 * i) * NC);
+      float s = 0.0f;
+#pragma unroll
+      for (int v = 0; v < NC / 4; v++) {
+        const f32x4 g4 = gr[v];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float t = s + g4[e] * w4[v][e];
+          s = 4 * v + e < N ? t : s;
+        }
+      }
+      dA[(long)m * K + k] = s;
+      if (k < K1) {
+        const long o = (long)m * K1 + k;
+        if (d1) d1[o] = s;
+        if (d2) d2[o] = R ? (rv[i] > 0.0f ? s : 0.0f) : s;
+      }
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int tt_k_head_bwd(const float *A, int M, int K, const float *W, int N, const float *G,
+                  float *dW, float *dA, float *d1, float *d2, const float *R) {
+  if (M <= 0 || K <= 0 || N <= 0 || N > 32 || !G || (!dW && !dA) || (dW && !A) ||
+      (dA && !W) || ((d1 || d2) && (!dA || K < 2)))
+    return -1;
+  const int NC = N <= 16 ? 16 : 32;
+  const int KW = (size_t)M * (64 + 4) * sizeof(float) <= 64 * 1024 ? 64 : 32;
+  const size_t lds_w = dW ? sizeof(float) * (size_t)M * (KW + NT / KW) : 0;
+  const size_t lds_a = dA ? sizeof(float) * (size_t)(64 + DA_M) * NC : 0;
+  const size_t lds = lds_w > lds_a ? lds_w : lds_a;
+  if (lds > 64 * 1024) return -1;
+  const long nkb = (K + 63) / 64, nkw = (K + KW - 1) / KW;
+  const long nbw = dW ? nkw * ((N + NT / KW - 1) / (NT / KW)) : 0;
+  const long nba = dA ? nkb * ((M + DA_M - 1) / DA_M) : 0;
+  if (nbw + nba > 0x7fffffffL) return -1;
+  const dim3 grid((unsigned)(nbw + nba));
+  if (NC == 16)
+    hipLaunchKernelGGL(head_bwd_kernel<16>, grid, dim3(NT), lds, stream(), A, M, K, W, N, G, dW,
+                       dA, d1, d2, R, (int)nbw, KW, (int)nkw);
+  else
+    hipLaunchKernelGGL(head_bwd_kernel<32>, grid, dim3(NT), lds, stream(), A, M, K, W, N, G, dW,
+                       dA, d1, d2, R, (int)nbw, KW, (int)nkw);
+  return launched();
+}
+
+}  // extern "C"
