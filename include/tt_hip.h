@@ -254,6 +254,12 @@ int tt_k_conv2d_dx_implicit(const float *g, const float *w, float *dx,
  *   dw:  dw (F, C*HH*WW), db (F, optional)         src/autograd.c:456-513
  *   dx:  dx (N,C,H,W)                              src/autograd.c:515-539,406-434 */
 int tth_conv_lds(int on);
+/* 1 (default): tt_k_conv2d_dw_lds uses the tiled, pipelined weight-gradient
+ * kernel (blocks of filters x taps x pixels, the next unit staged while the
+ * current one multiplies) where it applies (W % 4 == 0, Wo % 8 == 0, 16-byte
+ * aligned operands); 0: the per-image kernel.  <0 queries; returns the
+ * previous setting. */
+int tth_conv_dwt(int on);
 /* 1 (default): ag_conv2d leaves its direct-convolution launch pending until
  * the next library call, and an ag_relu on its output computes both in one
  * launch (tt_k_conv2d_relu_fwd_lds); ag_reshape's copy and any other

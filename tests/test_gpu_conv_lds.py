@@ -282,3 +282,40 @@ def test_autograd_conv_relu_deferred(tlib, case):
         got = run(mode)
         for a, e in zip(got, ref):
             assert _bits_equal(a, e), mode
+
+
+DWT_CASES = CASES + [
+    (4, 8, 16, 16, 40, 5, 5, 1, 1, 2, 2),   # 5x5 taps, F = 40: two filter blocks
+    (3, 5, 20, 24, 7, 3, 3, 2, 2, 1, 1),    # stride 2
+    (2, 64, 8, 8, 20, 3, 3, 1, 1, 1, 1),    # K = 576: six tap groups
+    (1, 2, 4, 4, 3, 1, 1, 1, 1, 0, 0),      # 1x1, a single unit
+    (9, 16, 12, 12, 33, 3, 3, 1, 1, 1, 1),  # units not a multiple of the groups
+]
+
+
+@pytest.mark.parametrize("case", DWT_CASES)
+def test_conv_dw_tiled_vs_oracle(tlib, case):
+    """The tiled weight gradient (where it applies) and the per-image kernel,
+    each against the oracle, each deterministic run to run."""
+    x, w, b, g, geo = _inputs(case)
+    N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo = geo
+    if not tlib.tt_k_conv2d_lds_plan(*geo) & 2:
+        pytest.skip("weight gradient not covered by the LDS kernels")
+    rdx, rdw, rdb = orc.conv2d_bwd(x, w, g, sh, sw, ph, pw)
+    dx_, dg_ = DevBuf.from_np(x), DevBuf.from_np(g)
+    gmax = float(np.abs(g).max())
+    prev = tlib.tth_conv_dwt(-1)
+    try:
+        for on in (1, 0):
+            tlib.tth_conv_dwt(on)
+            print("conv dw tiled", on, case, flush=True)
+            outs = []
+            for _ in range(2):
+                dW, dB = DevBuf(w.size), DevBuf(F)
+                check(tlib.tt_k_conv2d_dw_lds(dg_.ptr, dx_.ptr, dW.ptr, dB.ptr, *geo), "dw")
+                outs.append((dW.to_np(w.shape), dB.to_np((F,))))
+            assert err(outs[0][0], rdw, N * Ho * Wo, gmax, 1.0) <= TOL
+            assert err(outs[0][1], rdb, N * Ho * Wo, gmax, 1.0) <= TOL
+            assert _bits_equal(outs[0][0], outs[1][0]) and _bits_equal(outs[0][1], outs[1][1])
+    finally:
+        tlib.tth_conv_dwt(prev)

@@ -159,6 +159,7 @@ SIGNATURES = [
     ("tt_k_conv2d_dx_implicit", _I, [VP, VP, VP] + [_I] * 13),
     ("tth_conv_lds", _I, [_I]),
     ("tth_conv_relu_fuse", _I, [_I]),
+    ("tth_conv_dwt", _I, [_I]),
     ("tt_k_conv2d_lds_plan", _I, [_I] * 13),
     ("tt_k_conv2d_fwd_lds", _I, [VP, VP, VP, VP] + [_I] * 13),
     ("tt_k_conv2d_relu_fwd_lds", _I, [VP, VP, VP, VP, VP] + [_I] * 13),

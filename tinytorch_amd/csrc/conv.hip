@@ -1023,6 +1023,245 @@ conv_dw32_reduce_kernel(const float *__restrict__ part, float *__restrict__ dw,
   }
 }
 
+// ---- weight gradient, one workgroup per (output rows of one image, taps, filters) ----
+//
+// Workgroup (u, ts, fb) computes the dW contribution of unit u (RC output
+// rows of one image) for filters [32 fb, 32 fb + 32) and the taps of tap
+// set ts (NTGW groups of TG blocks of 32 taps).  It stages the unit's output
+// gradient rows (32 filters) and the input rows they need (the channels of
+// the tap set, gapped slab) once, with 16-byte direct loads.  Wave w takes
+// tap group w / 4 of the set and the rows pq, pq + 4, ... (pq = w % 4) of
+// the unit, so the 4 SIMDs of a CU get equal shares and g and x are read
+// once per workgroup.  (Staging in two phases, the first phase's MFMAs
+// running while the second's loads are in flight, measured slower: the
+// loads of all workgroups are bandwidth-bound together.)
+// The 4 waves of a tap group add their accumulators through LDS
+// ((0 + 2) + (1 + 3)) and wave pq = 0 writes the unit's partial block, which
+// conv_dwt_reduce_kernel sums over the units in unit order.  MFMA operands
+// as conv_dw32_kernel: lane l feeds A[f = l%32][pixel h = l/32] = g and
+// B[pixel h][tap l%32] = the gapped slab; accumulator r of block jb holds
+// filter 8(r/4) + 4h + r%4, tap 32 jb + l%32.  The bias gradient is summed
+// on the VALU from the same A operands (first group of the first tap set).
+constexpr int DWT_NPQ = 4;  // waves sharing a tap group (pixel quarters)
+
+template <int TG, int NTGW>
+__global__ void __launch_bounds__(64 * DWT_NPQ * NTGW)
+conv_dwt_kernel(const float *__restrict__ gr, const float *__restrict__ x,
+                float *__restrict__ part, Geo g, int RC, int nch, int GS, int CS, int jbp) {
+  constexpr int NTH = 64 * DWT_NPQ * NTGW;
+  constexpr int SLOT = TG * 1024 + 64;  // one wave's accumulators and bias in LDS
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  const int u = blockIdx.x, ts = blockIdx.y, fb = blockIdx.z;
+  const int n = u / nch, ho0 = (u - n * nch) * RC;
+  const int rows = min(g.Ho, ho0 + RC) - ho0;
+  const int P = g.Ho * g.Wo;
+  const int f0 = fb * 32;
+  const int nf = g.F - f0 < 32 ? g.F - f0 : 32;
+  const int taps = g.HH * g.WW;
+  const int kts = ts * NTGW * TG * 32;  // first tap of the set
+  const int c0 = kts / taps;
+  const int c1 = min(g.C, (min(g.K, kts + NTGW * TG * 32) + taps - 1) / taps);
+  const int nc = c1 - c0;
+  const int G = gslab_gap(g), RW = g.W + G;
+  const int R = (rows - 1) * g.sh + g.HH;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tgw = wave / DWT_NPQ, pq = wave - tgw * DWT_NPQ;
+  const int l32 = lane & 31, h = lane >> 5;
+  const float *gs = smem;
+  const float *xs = smem + round_up(32 * GS, 256);
+
+  // stage g rows (32 x GS), the gapped slab of channels [c0, c1), a zero plane
+  stage_blocks<true, NTH>(smem, gr + (long)n * g.F * P + (long)f0 * P + (long)ho0 * g.Wo,
+                          32 * GS, GS, nf, P, 0, rows * g.Wo);
+  {
+    const int hs = ho0 * g.sh - g.ph;
+    const int T = (nc + 1) * CS;
+    const float rcpC = 1.0f / (float)CS, rcpR = 1.0f / (float)RW;
+    const float *xn = x + ((long)n * g.C + c0) * g.H * g.W;
+    for (int base = wave * 256; base < T; base += NTH * 4) {
+      const int i = base + lane * 4;
+      const int c = fdiv(i, CS, rcpC), rem = i - c * CS;
+      const int slot = fdiv(rem, RW, rcpR), j = rem - slot * RW;
+      const int row = hs + slot;
+      const bool ok = i < T && c < nc && slot < R && j >= G && row >= 0 && row < g.H;
+      dma_dwordx4(ok ? xn + ((long)c * g.H + row) * g.W + (j - G) : g_zero_src,
+                  xs + base);
+    }
+  }
+
+  // this lane's tap offsets inside the slab (taps past K: the zero plane)
+  const int kt0 = kts + tgw * TG * 32;
+  int bb[TG];
+#pragma unroll
+  for (int jw = 0; jw < TG; jw++) {
+    const int k = kt0 + jw * 32 + l32;
+    int off = nc * CS;
+    if (k < g.K) {
+      const int c = k / taps - c0, t = k % taps;
+      const int kh = t / g.WW, kw = t - kh * g.WW;
+      off = c * CS + kh * RW + G + kw - g.pw;
+    }
+    bb[jw] = off;
+  }
+  f32x16 acc[TG];
+#pragma unroll
+  for (int jw = 0; jw < TG; jw++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[jw][r] = 0.0f;
+  float bsum = 0.0f;
+  dma_wait();
+  __syncthreads();
+
+  // items (row, quad): rows pq, pq+4, ... of the unit; lane half h takes
+  // the pixels [h*Wo/2, h*Wo/2 + Wo/2) of a row, four at a time: one 16-byte
+  // read of g (rows of GS = 4 mod 32 floats: eight lanes of a read cover the
+  // 32 banks) feeds four MFMA steps.  The next item's operands are read
+  // before the current item's MFMAs.
+  const int half_w = g.Wo >> 1;
+  const int quads = half_w >> 2;
+  const int xh = h * half_w * g.sw;
+  const int xstep = DWT_NPQ * g.sh * RW - quads * 4 * g.sw;  // next row, first quad
+  const int gstep = DWT_NPQ * g.Wo - quads * 4;
+  const int nrow = kt0 < g.K && rows > pq ? (rows - pq + DWT_NPQ - 1) / DWT_NPQ : 0;
+  const int nit = nrow * quads;
+  const float *ga = gs + l32 * GS + h * half_w;
+  {
+    int go = pq * g.Wo, xo = pq * g.sh * RW + xh;  // item offsets into g and the slab
+    int qd = 0;
+    f32x4 a4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    float bv[4][TG];
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+#pragma unroll
+      for (int jw = 0; jw < TG; jw++) bv[e][jw] = 0.0f;
+    if (nit > 0) {
+      a4 = *(const f32x4 *)(ga + go);
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+#pragma unroll
+        for (int jw = 0; jw < TG; jw++) bv[e][jw] = xs[bb[jw] + xo + e * g.sw];
+    }
+#pragma unroll 1
+    for (int it = 0; it < nit; it++) {
+      // advance to the next item (the last item re-reads itself)
+      if (it + 1 < nit) {
+        if (++qd == quads) {
+          qd = 0;
+          go += gstep + 4;
+          xo += xstep + 4 * g.sw;
+        } else {
+          go += 4;
+          xo += 4 * g.sw;
+        }
+      }
+      // this item's operands were consumed by the previous iteration's
+      // copies: with no LDS read in flight here, the reads below are the
+      // only ones outstanding while the MFMAs issue
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      const f32x4 a4n = *(const f32x4 *)(ga + go);
+      float bn[4][TG];
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+#pragma unroll
+        for (int jw = 0; jw < TG; jw++) bn[e][jw] = xs[bb[jw] + xo + e * g.sw];
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+#pragma unroll
+        for (int jw = 0; jw < TG; jw++)
+          acc[jw] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[e], bv[e][jw], acc[jw], 0, 0, 0);
+      bsum += (a4[0] + a4[1]) + (a4[2] + a4[3]);
+      __builtin_amdgcn_sched_barrier(0);
+      a4 = a4n;
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+#pragma unroll
+        for (int jw = 0; jw < TG; jw++) bv[e][jw] = bn[e][jw];
+    }
+  }
+  bsum += __shfl_xor(bsum, 32, 64);  // both halves of filter l32
+
+  // add the DWT_NPQ waves of each tap group: (0 + 2) + (1 + 3), through LDS
+#pragma unroll
+  for (int s = DWT_NPQ / 2; s >= 1; s >>= 1) {
+    __syncthreads();
+    if (pq >= s && pq < 2 * s) {
+      float *d = smem + (tgw * s + pq - s) * SLOT;
+#pragma unroll
+      for (int jw = 0; jw < TG; jw++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) d[(jw * 16 + r) * 64 + lane] = acc[jw][r];
+      d[TG * 1024 + lane] = bsum;
+    }
+    __syncthreads();
+    if (pq < s) {
+      const float *d = smem + (tgw * s + pq) * SLOT;
+#pragma unroll
+      for (int jw = 0; jw < TG; jw++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[jw][r] += d[(jw * 16 + r) * 64 + lane];
+      bsum += d[TG * 1024 + lane];
+    }
+  }
+  if (pq != 0) return;
+  float *pz = part + ((long)fb * gridDim.x + u) * ((long)jbp * 1024 + 32);
+  const int jb0 = (ts * NTGW + tgw) * TG;
+#pragma unroll
+  for (int jw = 0; jw < TG; jw++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) pz[((jb0 + jw) * 16 + r) * 64 + lane] = acc[jw][r];
+  if (ts == 0 && tgw == 0 && lane < 32) pz[jbp * 1024 + lane] = bsum;
+}
+
+// dW / db from the dwt partials: each lane owns 4 consecutive elements of a
+// filter block's partial (16-byte loads; a wave's loads cover whole 1 KB
+// runs) and adds the units z, z+ZL, ... in order, 8 loads in flight; the ZL
+// lanes of an element are then added in lane order.
+template <int ZL>
+__global__ void __launch_bounds__(NT)
+conv_dwt_reduce_kernel(const float *__restrict__ part, float *__restrict__ dw,
+                       float *__restrict__ db, int nu, int nfb, int jbp, int F, int K) {
+  constexpr int XL = NT / ZL;  // 4-element columns per workgroup
+  const int S4 = (jbp * 1024 + 32) / 4;
+  __shared__ f32x4 sums[ZL][XL];
+  const int tx = threadIdx.x % XL, ty = threadIdx.x / XL;
+  const long e4 = (long)blockIdx.x * XL + tx;
+  const bool in = e4 < (long)nfb * S4;
+  const long ec = in ? e4 : 0;
+  const int fb = (int)(ec / S4), i4 = (int)(ec - (long)fb * S4);
+  const f32x4 *p = (const f32x4 *)part + (long)fb * nu * S4 + i4;
+  f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int q0 = ty; q0 < nu; q0 += 8 * ZL) {
+    f32x4 t[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) t[k] = p[(long)min(q0 + k * ZL, nu - 1) * S4];
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+      if (q0 + k * ZL < nu) v += t[k];
+  }
+  sums[ty][tx] = v;
+  __syncthreads();
+  if (ty != 0 || !in) return;
+  for (int z = 1; z < ZL; z++) v += sums[z][tx];
+  const int i = i4 * 4;
+  if (i >= jbp * 1024) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int f = fb * 32 + (i + e - jbp * 1024);
+      if (db && f < F) db[f] = v[e];
+    }
+    return;
+  }
+  const int jb = i >> 10, r = (i >> 6) & 15, l = i & 63;
+  const int f = fb * 32 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+  const int k = jb * 32 + (l & 31);
+  if (f >= F) return;
+#pragma unroll
+  for (int e = 0; e < 4; e++)
+    if (k + e < K) dw[(long)f * K + k + e] = v[e];
+}
+
 // dw[f][k] = sum_z part[z][f][k] (k < K), db[f] = sum_z part[z][f][K]; ZL
 // lanes per output each add every ZL-th partial in order, then lane 0 adds
 // the ZL sums in order.
@@ -1326,9 +1565,142 @@ int launch_dw_var(const float *gr, const float *x, float *part, const Geo &g, in
   }
 }
 
+int g_dwt = 1;  // tiled weight gradient enabled (tth_conv_dwt)
+
+// ---- dwt planning ----
+struct DwtPlan {
+  int tg = 0, ntgw = 0, nts = 0, nfb = 0, rc = 0, nch = 0, units = 0, gs = 0, cs = 0, jbp = 0;
+  size_t lds = 0;
+};
+
+// Channel stride of the dwt slab: R rows of gslab_rw floats plus a pad (a
+// multiple of 4 below 32) chosen so that the 32 taps of an MFMA operand read
+// fall on as few shared banks as possible (32 banks of 4 bytes).
+int dwt_channel_stride(const Geo &g, int R, int TG) {
+  const int RW = gslab_rw(g), taps = g.HH * g.WW;
+  int best = R * RW, best_worst = 1 << 30;
+  for (int pad = 0; pad < 32; pad += 4) {
+    const int cs = R * RW + pad;
+    int worst = 0;
+    for (int jb = 0; jb < (g.K + 31) / 32 && jb < 64; jb++) {
+      const int k0 = (jb / TG) * TG * 32, c0 = k0 / taps;
+      int cnt[32] = {0};
+      for (int l = 0; l < 32; l++) {
+        const int k = jb * 32 + l;
+        if (k >= g.K) break;
+        const int c = k / taps - c0, t = k % taps, kh = t / g.WW, kw = t % g.WW;
+        const int b = ((c * cs + kh * RW + kw) % 32 + 32) % 32;
+        if (++cnt[b] > worst) worst = cnt[b];
+      }
+    }
+    if (worst < best_worst) { best_worst = worst; best = cs; }
+  }
+  return best;
+}
+
+// The tiled weight gradient covers 16-byte staged (W % 4 == 0) convolutions
+// with Wo % 8 == 0.  Tap blocks of 32 go in groups of TG <= 3 (one wave's
+// accumulators), up to 4 groups per workgroup (16 waves); the unit is the
+// largest number of output rows whose staging fits the LDS while the grid
+// still has about 2048 waves (8 per SIMD) to spread.
+DwtPlan plan_dwt(const Geo &g, int N) {
+  DwtPlan pl;
+  if (g.W % 4 != 0 || g.Wo % 8 != 0) return pl;
+  const int JB = (g.K + 31) / 32;
+  const int TG = JB < 3 ? JB : 3;
+  const int NTG = (JB + TG - 1) / TG;
+  const int nts = (NTG + 3) / 4, ntgw = (NTG + nts - 1) / nts;
+  const int taps = g.HH * g.WW;
+  const int ncmax = min(g.C, (ntgw * TG * 32 + taps - 1) / taps + 1);  // channels a set spans
+  const int nfb = (g.F + 31) / 32;
+  const int nw = DWT_NPQ * ntgw;
+  const long red = 4L * ntgw * (DWT_NPQ / 2) * (TG * 1024 + 64);
+  for (int rc = g.Ho;; rc = (rc + 1) / 2) {
+    const int R = (rc - 1) * g.sh + g.HH;
+    const int cs = dwt_channel_stride(g, R, TG);
+    const int gs = ((rc * g.Wo + 31) & ~31) + 4;
+    const long stage = 4L * (round_up(32 * gs, 256) + round_up((ncmax + 1) * cs, 256));
+    const long lds = stage > red ? stage : red;
+    const int nch = (g.Ho + rc - 1) / rc;
+    const long waves = (long)N * nch * nts * nfb * nw;
+    if (lds > LDS_MAX || (waves < 2048 && rc > DWT_NPQ)) {
+      if (rc == 1) break;
+      continue;
+    }
+    if ((long)N * nch > 0x7fffffffL) break;
+    pl.tg = TG;
+    pl.ntgw = ntgw;
+    pl.nts = nts;
+    pl.nfb = nfb;
+    pl.rc = rc;
+    pl.nch = nch;
+    pl.units = N * nch;
+    pl.gs = gs;
+    pl.cs = cs;
+    pl.jbp = nts * ntgw * TG;
+    pl.lds = (size_t)lds;
+    return pl;
+  }
+  pl.tg = 0;
+  return pl;
+}
+
+template <int TG, int NTGW>
+int launch_dwt(const float *gr, const float *x, float *dw, float *db, const Geo &g,
+               const DwtPlan &pl) {
+  auto kern = conv_dwt_kernel<TG, NTGW>;
+  if (pl.lds > 64 * 1024 && !allow_big_lds((const void *)kern)) return -1;
+  const long S = (long)pl.jbp * 1024 + 32;
+  float *part = (float *)ttrt_alloc(sizeof(float) * (size_t)(S * pl.units * pl.nfb));
+  if (!part) return -2;
+  hipLaunchKernelGGL(kern, dim3((unsigned)pl.units, (unsigned)pl.nts, (unsigned)pl.nfb),
+                     dim3(64 * DWT_NPQ * NTGW), pl.lds, stream(), gr, x, part, g, pl.rc, pl.nch,
+                     pl.gs, pl.cs, pl.jbp);
+  int rc = hipGetLastError() == hipSuccess ? 0 : -3;
+  if (rc == 0) {
+    const long cols = (long)pl.nfb * (S / 4);
+    // lanes per element: about 16 units each
+    int zl = 1;
+    while (zl < 64 && zl * 16 < pl.units) zl *= 2;
+#define TT_DWR(ZL_)                                                                          \
+  case ZL_:                                                                                  \
+    hipLaunchKernelGGL(conv_dwt_reduce_kernel<ZL_>,                                          \
+                       dim3((unsigned)((cols + NT / ZL_ - 1) / (NT / ZL_))), dim3(NT), 0,    \
+                       stream(), part, dw, db, pl.units, pl.nfb, pl.jbp, g.F, g.K);          \
+    break;
+    switch (zl) {
+      TT_DWR(1) TT_DWR(2) TT_DWR(4) TT_DWR(8) TT_DWR(16) TT_DWR(32) TT_DWR(64)
+    }
+#undef TT_DWR
+    rc = hipGetLastError() == hipSuccess ? 0 : -3;
+  }
+  ttrt_free(part);  // stream-ordered: the kernels above run before any reuse
+  return rc;
+}
+
+int launch_dwt_plan(const float *gr, const float *x, float *dw, float *db, const Geo &g,
+                    const DwtPlan &pl) {
+  if (pl.tg == 1) return launch_dwt<1, 1>(gr, x, dw, db, g, pl);
+  if (pl.tg == 2) return launch_dwt<2, 1>(gr, x, dw, db, g, pl);
+  if (pl.tg != 3) return -1;
+  switch (pl.ntgw) {
+    case 1: return launch_dwt<3, 1>(gr, x, dw, db, g, pl);
+    case 2: return launch_dwt<3, 2>(gr, x, dw, db, g, pl);
+    case 3: return launch_dwt<3, 3>(gr, x, dw, db, g, pl);
+    case 4: return launch_dwt<3, 4>(gr, x, dw, db, g, pl);
+  }
+  return -1;
+}
+
 int g_lds_conv = 1;  // tth_conv_lds
 
 }  // namespace
+
+extern "C" int tth_conv_dwt(int on) {
+  const int prev = g_dwt;
+  if (on >= 0) g_dwt = on ? 1 : 0;
+  return prev;
+}
 
 extern "C" int tth_conv_lds(int on) {
   const int prev = g_lds_conv;
@@ -1382,6 +1754,10 @@ extern "C" int tt_k_conv2d_dw_lds(const float *gr, const float *x, float *dw, fl
                                   int ph, int pw, int Ho, int Wo) {
   if (!gr || !x || !dw || !geo_ok(N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo)) return -1;
   const Geo g{C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo, F, C * HH * WW};
+  if (g_dwt && aligned16(x) && aligned16(gr)) {
+    const DwtPlan tp = plan_dwt(g, N);
+    if (tp.tg) return launch_dwt_plan(gr, x, dw, db, g, tp);
+  }
   const DwPlan pl = plan_dw(g, N);
   if (pl.var < 0) return -1;
   const long Z = (long)N * pl.chunks;
