@@ -164,6 +164,13 @@ int tt_k_copy_padones_fwd(const float *x, float *c, float *y, long M, long K);
  * ag_relu (src/ops.c:104-106) followed by ag_padones (src/autograd.c:195-212).
  * M < 65536, K < 2^30, else -1. */
 int tt_k_relu_padones_fwd(const float *x, float *r, float *y, long M, long K);
+/* C = A * B (row-major, contiguous; ag_matmul, reference
+ * src/autograd.c:168-171) with the relu and padones that follow it in an MLP
+ * layer (src/autograd.c:173-193, src/autograd.c:195-212): R = relu(C), P = [R, 1]
+ * (M x N+1).  The three outputs of tt_k_gemm then tt_k_relu_padones_fwd,
+ * bit for bit, written by the GEMM's split-K reduction when it has one. */
+int tt_k_gemm_relu_pad(int M, int N, int K, const float *A, const float *B, float *C, float *R,
+                       float *P);
 /* padones backward (src/autograd.c:348-359) written to two buffers: d1 and
  * d2 both get g without its last column; the backward pass uses it when the
  * padded tensor is a reshape (src/autograd.c:361-369, a copy of the

@@ -1,0 +1,78 @@
+"""A matmul and the layer after it in one GEMM + reduction pass.
+
+tt_k_gemm_relu_pad must give exactly what tt_k_gemm followed by
+tt_k_relu_padones_fwd gives (C, relu(C) and [relu(C), 1]), and those values
+must be the oracle's relu / padones of C.  Shapes cover the split-K path
+(the reduction carries the epilogue) and the paths without a reduction (the
+epilogue runs as its own pass).  Also the softmax-CE with one-byte labels in
+the launch arguments against the oracle.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import orc
+from tinytorch_amd.hip import DevBuf, check
+
+pytestmark = pytest.mark.gpu
+rng = np.random.default_rng(4242)
+
+
+def bits_equal(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+RELU_SHAPES = [(256, 785, 512), (256, 513, 256), (64, 3000, 100), (7, 9, 5), (1, 1, 1),
+               (300, 4096, 1000)]
+
+
+@pytest.mark.parametrize("M,K,N", RELU_SHAPES)
+def test_gemm_relu_pad_matches_unfused(tlib, M, K, N):
+    A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    B = (rng.standard_normal((K, N)) / np.sqrt(K)).astype(np.float32)
+    dA, dB = DevBuf.from_np(A), DevBuf.from_np(B)
+    C1, R1, P1 = DevBuf(M * N), DevBuf(M * N), DevBuf(M * (N + 1))
+    C2, R2, P2 = DevBuf(M * N), DevBuf(M * N), DevBuf(M * (N + 1))
+    print("gemm_relu_pad", M, K, N, flush=True)
+    check(tlib.tt_k_gemm_relu_pad(M, N, K, dA.ptr, dB.ptr, C1.ptr, R1.ptr, P1.ptr), "fused")
+    check(tlib.tt_k_gemm(M, N, K, dA.ptr, K, 0, dB.ptr, N, 0, C2.ptr, N), "gemm")
+    check(tlib.tt_k_relu_padones_fwd(C2.ptr, R2.ptr, P2.ptr, M, N), "relu_padones")
+    c = C1.to_np((M, N))
+    assert bits_equal(c, C2.to_np((M, N)))
+    assert bits_equal(R1.to_np((M, N)), R2.to_np((M, N)))
+    assert bits_equal(P1.to_np((M, N + 1)), P2.to_np((M, N + 1)))
+    # and what the values are: relu and a column of ones
+    assert bits_equal(R1.to_np((M, N)), orc.relu_fwd(c))
+    assert bits_equal(P1.to_np((M, N + 1)), orc.padones_fwd(orc.relu_fwd(c)))
+
+
+def test_gemm_relu_pad_rejects(tlib):
+    d = DevBuf(64)
+    assert tlib.tt_k_gemm_relu_pad(0, 1, 1, d.ptr, d.ptr, d.ptr, d.ptr, d.ptr) == -1
+    assert tlib.tt_k_gemm_relu_pad(1, 1, 1, d.ptr, d.ptr, d.ptr, None, d.ptr) == -1
+
+
+CE_CASES = [(128, 10), (256, 10), (33, 17), (512, 32), (5, 3), (300, 300)]
+
+
+@pytest.mark.parametrize("rows,cols", CE_CASES)
+def test_softmax_ce_hostlab_u8_labels(tlib, rows, cols):
+    """Labels travel inside the launch arguments, one byte each for up to 255
+    columns: labels outside [0, cols) (-1, cols, 300) must still give the
+    loss -log(1e-12) and no one-hot term, as with 4-byte labels."""
+    x = rng.standard_normal((rows, cols)).astype(np.float32) * 3
+    y = rng.integers(0, cols, rows).astype(np.int32)
+    if rows >= 4:
+        y[:4] = [-1, cols, 300, cols - 1]
+    yp = y.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+    dx, p, s, l = DevBuf.from_np(x), DevBuf(rows * cols), DevBuf(rows * cols), DevBuf(1)
+    print("ce hostlab", rows, cols, flush=True)
+    check(tlib.tt_k_softmax_ce_mean_hostlab(dx.ptr, yp, p.ptr, l.ptr, s.ptr, rows, cols,
+                                            ctypes.c_float(1.0 / rows)), "ce")
+    probs = orc.softmax_fwd(x)
+    loss, seed = orc.ce_seed(probs, y)
+    assert np.abs(p.to_np((rows, cols)) - probs).max() <= 1e-6
+    assert abs(float(l.to_np((1,))[0]) - loss) <= 1e-5 * max(1.0, abs(loss))
+    assert np.abs(s.to_np((rows, cols)) - seed).max() <= 1e-6

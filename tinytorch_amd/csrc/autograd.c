@@ -187,11 +187,46 @@ AGNode *ag_mulscalar(AGNode *a, float s) {
 
 AGNode *ag_matmul(AGNode *a, AGNode *b) {
     if (!a || !b) return NULL;
+    const Tensor *av = a->val, *bv = b->val;
+    if (tt_defer_enabled() && av->ndim == 2 && bv->ndim == 2 && av->shape[1] == bv->shape[0] &&
+        av->shape[0] > 0 && av->shape[1] > 0 && bv->shape[1] > 0 &&
+        av->shape[0] <= 0x7fffffffL && av->shape[1] <= 0x7fffffffL &&
+        bv->shape[1] <= 0x7fffffffL) {
+        /* left pending: a relu + padones of the product is then computed
+         * by the GEMM's own reduction pass */
+        const float *x = tt_dev(a->val), *y = tt_dev(b->val);
+        if (!x || !y) return NULL;
+        const long shp[2] = {av->shape[0], bv->shape[1]};
+        Tensor *out = tt_empty_dev(shp, 2);
+        if (!out) return NULL;
+        AGNode *n = make_node(out, &OP_MATMUL, a, b, NULL);
+        if (!n) return NULL;
+        tt_pend.out = out;
+        tt_pend.r = NULL;
+        tt_pend.x = x;
+        tt_pend.w = y;
+        tt_pend.geo[0] = (int)av->shape[0];
+        tt_pend.geo[1] = (int)bv->shape[1];
+        tt_pend.geo[2] = (int)av->shape[1];
+        tt_pend.active = TT_PEND_MATMUL;
+        return n;
+    }
     return make_node(tt_matmul_omp(a->val, b->val, 0), &OP_MATMUL, a, b, NULL);
 }
 
 AGNode *ag_relu(AGNode *a) {
     if (!a) return NULL;
+    if (tt_pend.active == TT_PEND_MATMUL && tt_pend.out == a->val) {
+        /* the matmul producing a is still pending: its relu waits with it
+         * (a padones of the relu then fuses all three) */
+        Tensor *r = tt_empty_like(a->val);
+        if (!r) return NULL;
+        AGNode *n = make_node(r, &OP_RELU, a, NULL, NULL);
+        if (!n) return NULL;
+        tt_pend.r = r;
+        tt_pend.active = TT_PEND_MATMUL_RELU;
+        return n;
+    }
     if (tt_pend.active == TT_PEND_CONV && tt_pend.out == a->val) {
         /* the convolution producing a is still pending: one launch writes
          * it and its relu (same values as tt_relu of the stored output) */
@@ -243,6 +278,19 @@ AGNode *ag_padones(AGNode *a) {
             if (tt_k_copy_padones_fwd(p.x, p.out->dev, v->dev, M, K) == 0)
                 return make_node(v, &OP_PADONES, a, NULL, NULL);
             tt_pend = p;  /* not launched: the plain copy runs below */
+            tt_release(v);
+        }
+    }
+    if (tt_pend.active == TT_PEND_MATMUL_RELU && tt_pend.r == a->val) {
+        /* matmul, relu and padones in one GEMM + reduction */
+        Tensor *v = tt_empty_dev(shp, 2);
+        if (v) {
+            const TTPendConv p = tt_pend;
+            tt_pend.active = 0;
+            if (tt_k_gemm_relu_pad(p.geo[0], p.geo[1], p.geo[2], p.x, p.w, p.out->dev,
+                                   p.r->dev, v->dev) == 0)
+                return make_node(v, &OP_PADONES, a, NULL, NULL);
+            tt_pend = p;  /* not launched: the plain matmul and relu run below */
             tt_release(v);
         }
     }
@@ -324,8 +372,6 @@ AGNode *ag_softmax_ce(AGNode *logits, const int *labels, long rows) {
         rows <= 0 || logits->val->shape[1] > 0x7fffffffL)
         return NULL;
     const int cols = (int)logits->val->shape[1];
-    const float *x = tt_dev(logits->val);
-    if (!x) return NULL;
     const long one = 1;
     Tensor *probs = tt_empty_like(logits->val);
     Tensor *seed = tt_empty_like(logits->val);
@@ -333,6 +379,11 @@ AGNode *ag_softmax_ce(AGNode *logits, const int *labels, long rows) {
     int32_t *hlab = (int32_t *)malloc(sizeof(int32_t) * (size_t)rows);
     if (hlab)
         for (long r = 0; r < rows; r++) hlab[r] = (int32_t)labels[r];
+    const float *x = tt_dev(logits->val);
+    if (!x) {
+        tt_release(probs); tt_release(seed); tt_release(loss); free(hlab);
+        return NULL;
+    }
     /* small batches: the labels travel inside the kernel's arguments */
     if (probs && seed && loss && hlab && rows <= TT_CE_ARG_ROWS &&
         tt_k_softmax_ce_mean_hostlab(x, hlab, probs->dev, loss->dev, seed->dev, rows, cols,

@@ -14,6 +14,7 @@
 #include <math.h>
 #include <stdint.h>
 #include "tt_rt.h"
+#include "ce_rows.h"
 
 namespace {
 
@@ -336,64 +337,23 @@ __global__ void padones_relu_bwd_rows_kernel(const float *__restrict__ g, const 
 }
 
 // Fused softmax + cross-entropy for up to a few thousand rows in ONE
-// workgroup: probabilities, the seed (p - onehot(y)) * scale and the mean
-// loss, reduced in a fixed order (per-thread row order, then the thread
-// partials through LDS in index order).
-// Labels handed over inside the kernel arguments (no copy to device memory
-// before the launch): up to TT_CE_ARG_ROWS of them.
+// workgroup (ce_rows_block): probabilities, the seed (p - onehot(y)) * scale
+// and the mean loss.  Labels from device memory or, up to TT_CE_ARG_ROWS of
+// them, inside the kernel arguments (LabArg: 4 bytes a label; LabU8: one byte,
+// for cols <= 255).
 struct LabArg {
   int32_t v[TT_CE_ARG_ROWS];
   __device__ int32_t operator[](int r) const { return v[r]; }
 };
 
-// LAB: a device pointer to the labels or a LabArg
+// LAB: a device pointer to the labels, a LabArg or a LabU8
 template <int MAXC, class LAB>
-__global__ void softmax_ce_mean_kernel(const float *__restrict__ x, const LAB lab,
-                                       float *__restrict__ probs, float *__restrict__ loss_mean,
-                                       float *__restrict__ seed, int rows, int cols, float scale) {
+__global__ void __launch_bounds__(256)
+softmax_ce_mean_kernel(const float *__restrict__ x, const LAB lab, float *__restrict__ probs,
+                       float *__restrict__ loss_mean, float *__restrict__ seed, int rows,
+                       int cols, float scale) {
   __shared__ float part[256];
-  float acc = 0.0f;
-  for (int r = threadIdx.x; r < rows; r += blockDim.x) {
-    const float *xr = x + (long)r * cols;
-    float *pr = probs + (long)r * cols;
-    float *sr = seed + (long)r * cols;
-    // the row stays in registers (cols <= MAXC): no global round trips
-    // between the max, exp, normalise and seed passes
-    float v[MAXC];
-#pragma unroll
-    for (int j = 0; j < MAXC; j++) v[j] = j < cols ? xr[j] : -INFINITY;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < MAXC; j++) if (j < cols && v[j] > mx) mx = v[j];
-    if (mx == -INFINITY) {
-#pragma unroll
-      for (int j = 0; j < MAXC; j++) v[j] = 1.0f / (float)cols;
-    } else {
-      float sum = 0.0f;
-#pragma unroll
-      for (int j = 0; j < MAXC; j++)
-        if (j < cols) { v[j] = expf(v[j] - mx); sum += v[j]; }
-#pragma unroll
-      for (int j = 0; j < MAXC; j++) v[j] = v[j] / sum;
-    }
-    const int y = lab[r];
-    float py = 0.0f;
-#pragma unroll
-    for (int j = 0; j < MAXC; j++)
-      if (j < cols) {
-        pr[j] = v[j];
-        sr[j] = (v[j] - (j == y ? 1.0f : 0.0f)) * scale;
-        if (j == y) py = v[j];
-      }
-    acc += -logf(fmaxf(py, 1e-12f));
-  }
-  part[threadIdx.x] = acc;
-  __syncthreads();
-  for (int o = 128; o > 0; o >>= 1) {
-    if ((int)threadIdx.x < o) part[threadIdx.x] += part[threadIdx.x + o];
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) loss_mean[0] = part[0] / (float)rows;
+  ce_rows_block<MAXC>(x, lab, probs, loss_mean, seed, rows, cols, scale, part);
 }
 
 // general width: the same passes over global memory
@@ -735,6 +695,12 @@ int tt_k_softmax_ce_mean(const float *logits, const int32_t *labels, float *prob
 int tt_k_softmax_ce_mean_hostlab(const float *logits, const int32_t *host_labels, float *probs,
                                  float *loss_mean, float *seed, long rows, int cols, float scale) {
   if (rows <= 0 || cols <= 0 || rows > TT_CE_ARG_ROWS || !host_labels) return -1;
+  if (cols <= 255) {
+    LabU8 lu;
+    lab_u8_fill(lu, host_labels, rows, cols);
+    launch_ce_mean(logits, lu, probs, loss_mean, seed, rows, cols, scale);
+    return launched();
+  }
   LabArg la;
   for (long r = 0; r < rows; r++) la.v[r] = host_labels[r];
   for (long r = rows; r < TT_CE_ARG_ROWS; r++) la.v[r] = 0;

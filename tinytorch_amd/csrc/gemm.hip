@@ -612,6 +612,49 @@ splitk_reduce_kernel(const float *__restrict__ ws, float *__restrict__ C, int M,
   }
 }
 
+// The split-K reduction of a row-major C = A*B (ldc = N) with the relu +
+// padones that follow it in an MLP layer fused in: R = relu(C) and
+// P = [R, 1] (M x (N+1)) as well as C, the values relu_padones_rows_kernel
+// writes from C.
+struct ReluPadEx {
+  float *r, *p;
+};
+
+template <int ZL>
+__device__ __forceinline__ float reduce_one(const float *__restrict__ ws, int S, long total,
+                                            long idx, int ty, float (*part)[256 / ZL], int tx) {
+  float s = 0.f;
+  if (idx < total) {
+#pragma unroll 4
+    for (int z = ty; z < S; z += ZL) s += ws[z * total + idx];
+  }
+  part[ty][tx] = s;
+  __syncthreads();
+  if (ty == 0)
+    for (int j = 1; j < ZL; j++) s += part[j][tx];
+  return s;
+}
+
+template <int ZL>
+__global__ void __launch_bounds__(256)
+splitk_reduce_relu_pad_kernel(const float *__restrict__ ws, float *__restrict__ C, int M, int N,
+                              int S, ReluPadEx ex) {
+  constexpr int XL = 256 / ZL;
+  __shared__ float part[ZL][XL];
+  const int tx = threadIdx.x % XL, ty = threadIdx.x / XL;
+  const long total = (long)M * N;
+  const long idx = (long)blockIdx.x * XL + tx;
+  const float s = reduce_one<ZL>(ws, S, total, idx, ty, part, tx);
+  if (ty != 0 || idx >= total) return;
+  const unsigned row = (unsigned)(idx / N), col = (unsigned)(idx - (long)row * N);
+  const float o = s > 0.0f ? s : 0.0f;
+  C[idx] = s;
+  ex.r[idx] = o;
+  float *pr = ex.p + (long)row * (N + 1);
+  pr[col] = o;
+  if ((int)col == N - 1) pr[N] = 1.0f;
+}
+
 // ---- 256x256 tile with direct global->LDS loads ----
 // gfx950's global_load_lds_dwordx4 moves 16 bytes per lane from global memory
 // straight into LDS (lane i of a wave writes bytes [16i, 16i+16) after the
@@ -1314,11 +1357,49 @@ void launch_tile(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, lo
   }
 }
 
+// The epilogue that tt_k_gemm_relu_pad asks of the split-K reduction writing
+// its C; `applied` tells it whether the GEMM took a split-K path (else it
+// launches the epilogue on its own).
+enum { HOOK_RELU_PAD = 1 };
+struct RedHook {
+  int kind;
+  const float *C;
+  ReluPadEx rp;
+  int applied;
+};
+RedHook *g_red_hook = nullptr;
+
+int reduce_hooked(const float *ws, int M, int N, int S) {
+  RedHook &h = *g_red_hook;
+  float *C = const_cast<float *>(h.C);
+  const long total = (long)M * N;
+  int zl = 1;
+  while (zl < 32 && zl < S && (total * zl * 2) <= 2048L * 256) zl *= 2;
+  if (zl < 4 && S >= 4) zl = 4;
+#define TT_HK(ZL_)                                                                            \
+  case ZL_:                                                                                   \
+    hipLaunchKernelGGL((splitk_reduce_relu_pad_kernel<ZL_>),                                  \
+                       dim3((unsigned)((total + 256 / ZL_ - 1) / (256 / ZL_))), dim3(256), 0,  \
+                       stream(), ws, C, M, N, S, h.rp);                                       \
+    break;
+  switch (zl) {
+    TT_HK(1) TT_HK(2) TT_HK(4) TT_HK(8) TT_HK(16)
+    default: TT_HK(32)
+  }
+#undef TT_HK
+  if (hipGetLastError() != hipSuccess) return -3;
+  h.applied = 1;
+  return 0;
+}
+
 // Sum the S partial products of a split-K launch into C (+ epilogue).
 template <int EPI>
 int reduce_splits(const float *ws, float *C, int M, int N, int S, long ldc, const float *bias,
                   int HW) {
   const long total = (long)M * N;
+  if constexpr (EPI == EPI_STORE) {
+    if (g_red_hook && g_red_hook->C == C && ldc == N) return reduce_hooked(ws, M, N, S);
+  }
   // widen the split-lanes until ~2048 workgroups share the reduction (at
   // most 32 lanes, at most S): each lane's loads are independent, so more
   // lanes means more loads in flight for the few outputs of a conv dW
@@ -1734,6 +1815,23 @@ extern "C" int tt_k_gemm(int M, int N, int K, const float *A, int lda, int trans
   if (!transA && transB)  return run<true, false, false, false, EPI_STORE>(M, N, K, a, b, C, ldc, nullptr, 1, vec);
   if (transA && !transB)  return run<false, false, true, false, EPI_STORE>(M, N, K, a, b, C, ldc, nullptr, 1, vec);
   return run<false, false, false, false, EPI_STORE>(M, N, K, a, b, C, ldc, nullptr, 1, vec);
+}
+
+// C = A * B (row-major, contiguous) and the relu + padones that follow it:
+// R = relu(C), P = [R, 1].  Fused into the split-K reduction when the GEMM
+// takes a split-K path, else a separate pass; the same values either way.
+extern "C" int tt_k_gemm_relu_pad(int M, int N, int K, const float *A, const float *B, float *C,
+                                  float *R, float *P) {
+  if (M <= 0 || N <= 0 || K < 0 || !A || !B || !C || !R || !P) return -1;
+  RedHook h{};
+  h.kind = HOOK_RELU_PAD;
+  h.C = C;
+  h.rp = ReluPadEx{R, P};
+  g_red_hook = &h;
+  const int rc = tt_k_gemm(M, N, K, A, K, 0, B, N, 0, C, N);
+  g_red_hook = nullptr;
+  if (rc) return rc;
+  return h.applied ? 0 : tt_k_relu_padones_fwd(C, R, P, M, N);
 }
 
 // ---- the GEMM without allocation (tt_k_gemm_noalloc) ----

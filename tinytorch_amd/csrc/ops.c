@@ -247,6 +247,13 @@ int tt_flush_pending(void) {
     if (kind == TT_PEND_COPY || kind == TT_PEND_RELU) {
         rc = kind == TT_PEND_COPY ? tt_k_copy(tt_pend.out->dev, tt_pend.x, tt_pend.out->numel)
                                   : tt_k_relu_fwd(tt_pend.x, tt_pend.out->dev, tt_pend.out->numel);
+    } else if (kind == TT_PEND_MATMUL || kind == TT_PEND_MATMUL_RELU) {
+        const int M = tt_pend.geo[0], N = tt_pend.geo[1], K = tt_pend.geo[2];
+        rc = tt_k_gemm(M, N, K, tt_pend.x, K, 0, tt_pend.w, N, 0, tt_pend.out->dev, N);
+        if (kind == TT_PEND_MATMUL_RELU) {
+            if (rc == 0) rc = tt_k_relu_fwd(tt_pend.out->dev, tt_pend.r->dev, tt_pend.r->numel);
+            if (rc != 0) tt_pend.r->valid = 0;
+        }
     } else {
         const int *q = tt_pend.geo;
         rc = tt_k_conv2d_fwd_lds(tt_pend.x, tt_pend.w, tt_pend.b, tt_pend.out->dev, q[0], q[1],
