@@ -153,6 +153,14 @@ int tt_k_softmax_ce_mean_hostlab(const float *logits, const int32_t *host_labels
  * dW, M <= 480 (a block of A is staged in LDS), else -1. */
 int tt_k_head_bwd(const float *A, int M, int K, const float *W, int N, const float *G,
                   float *dW, float *dA, float *d1, float *d2, const float *R);
+/* Both gradients of a matmul C = A * B (A M x K, B K x N; reference
+ * src/autograd.c:66-103, matmul_nt for dA = G * B^T and matmul_tn for
+ * dB = A^T * G) in ONE launch, when tt_k_gemm would compute each with its
+ * small-GEMM kernel -- the same values as the two tt_k_gemm calls -- with
+ * the d1 / d2 / R epilogue of tt_k_head_bwd on dA.  -1: not covered,
+ * nothing launched. */
+int tt_k_matmul_bwd_small(const float *A, int M, int K, const float *B, int N, const float *G,
+                          float *dB, float *dA, float *d1, float *d2, const float *R);
 /* y = x * s[0], s a device scalar (chain rule through a scalar loss) */
 int tt_k_scale_by_dev(const float *x, const float *s, float *y, long n);
 int tt_k_padones_fwd(const float *x, float *y, long M, long K);      /* src/autograd.c:195-212 */

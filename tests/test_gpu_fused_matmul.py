@@ -76,3 +76,51 @@ def test_softmax_ce_hostlab_u8_labels(tlib, rows, cols):
     assert np.abs(p.to_np((rows, cols)) - probs).max() <= 1e-6
     assert abs(float(l.to_np((1,))[0]) - loss) <= 1e-5 * max(1.0, abs(loss))
     assert np.abs(s.to_np((rows, cols)) - seed).max() <= 1e-6
+
+
+PAIR_SHAPES = [(256, 513, 256), (128, 1025, 160), (384, 417, 352)]
+
+
+@pytest.mark.parametrize("M,K,N", PAIR_SHAPES)
+@pytest.mark.parametrize("mode", ["plain", "copy", "relu"])
+def test_matmul_bwd_small_matches_two_gemms(tlib, M, K, N, mode):
+    """Both gradients in one launch: dA and dB bit-identical to the two
+    tt_k_gemm calls of the unfused rule, d1 / d2 the padones (relu) backward
+    of dA exactly; within tolerance of the oracle's matmul_nt / matmul_tn."""
+    A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    B = (rng.standard_normal((K, N)) / np.sqrt(K)).astype(np.float32)
+    G = (rng.standard_normal((M, N)) / M).astype(np.float32)
+    R = np.maximum(rng.standard_normal((M, K - 1)).astype(np.float32), 0.0)
+    dA_, dB_, dG, dR = DevBuf.from_np(A), DevBuf.from_np(B), DevBuf.from_np(G), DevBuf.from_np(R)
+    gb, ga, d1, d2 = DevBuf(K * N), DevBuf(M * K), DevBuf(M * (K - 1)), DevBuf(M * (K - 1))
+    rb, ra = DevBuf(K * N), DevBuf(M * K)
+    print("matmul_bwd_small", M, K, N, mode, flush=True)
+    rc = tlib.tt_k_matmul_bwd_small(dA_.ptr, M, K, dB_.ptr, N, dG.ptr, gb.ptr, ga.ptr,
+                                    d1.ptr if mode != "plain" else None,
+                                    d2.ptr if mode != "plain" else None,
+                                    dR.ptr if mode == "relu" else None)
+    if rc == -1:
+        pytest.skip("tt_k_gemm takes another kernel for this shape")
+    check(rc, "tt_k_matmul_bwd_small")
+    check(tlib.tt_k_gemm(M, K, N, dG.ptr, N, 0, dB_.ptr, N, 1, ra.ptr, K), "dA")
+    check(tlib.tt_k_gemm(K, N, M, dA_.ptr, K, 1, dG.ptr, N, 0, rb.ptr, N), "dB")
+    a, b = ga.to_np((M, K)), gb.to_np((K, N))
+    assert bits_equal(a, ra.to_np((M, K)))
+    assert bits_equal(b, rb.to_np((K, N)))
+    if mode != "plain":
+        assert bits_equal(d1.to_np((M, K - 1)), a[:, :-1])
+        want2 = orc.relu_bwd(R, a[:, :-1]) if mode == "relu" else a[:, :-1]
+        assert bits_equal(d2.to_np((M, K - 1)), want2)
+    ea = orc.matmul_nt(G, B)
+    eb = orc.matmul_tn(A, G)
+    assert np.abs(a - ea).max() <= 1e-5 * max(1.0, np.abs(ea).max())
+    assert np.abs(b - eb).max() <= 1e-5 * max(1.0, np.abs(eb).max())
+
+
+def test_matmul_bwd_small_shapes_taken(tlib):
+    """The MLP's middle layer (config 2: 256 x 513 x 256) is covered."""
+    d = DevBuf(256 * 513)
+    g = DevBuf(256 * 256)
+    w = DevBuf(513 * 256)
+    assert tlib.tt_k_matmul_bwd_small(d.ptr, 256, 513, w.ptr, 256, g.ptr, DevBuf(513 * 256).ptr,
+                                      DevBuf(256 * 513).ptr, None, None, None) == 0

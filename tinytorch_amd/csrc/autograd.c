@@ -182,7 +182,7 @@ AGNode *ag_mulscalar(AGNode *a, float s) {
 }
 
 /* The backward of a matmul with at most this many output columns (a
- * classifier layer) runs as one launch (backward_matmul_head). */
+ * classifier layer) runs as one launch of tt_k_head_bwd. */
 #define HEAD_MAX_N 32
 
 AGNode *ag_matmul(AGNode *a, AGNode *b) {
@@ -468,15 +468,19 @@ static void backward_mulscalar(AGNode *n) {
 
 static int relu_fusable(const AGNode *r);
 
-/* The backward of a matmul with at most HEAD_MAX_N columns in one launch
- * (tt_k_head_bwd): dA and dB and, when A is a padones used only here whose
- * input is used only by it, that input's gradient too -- and, when the
- * input is a reshape or a fusable relu, the gradient of the node before it.
- * The nodes whose rules this covers are marked `fused`.  0 when done. */
-static int backward_matmul_head(AGNode *n, const float *g) {
+/* Both gradients of matmul n in one launch and, when A is a padones used
+ * only here whose input is used only by it, that input's gradient too --
+ * and, when the input is a reshape or a fusable relu, the gradient of the
+ * node before it: the classifier-layer kernel (tt_k_head_bwd) for at most
+ * HEAD_MAX_N output columns, else the paired small-GEMM kernel
+ * (tt_k_matmul_bwd_small, which needs both gradients).  The nodes whose
+ * rules this covers are marked `fused`.  0 when done; -1: not taken,
+ * nothing launched. */
+static int backward_matmul_fused(AGNode *n, const float *g) {
     AGNode *a = n->in[0], *b = n->in[1];
     const int M = (int)a->val->shape[0], K = (int)a->val->shape[1], N = (int)b->val->shape[1];
-    if (N > HEAD_MAX_N) return -1;
+    const int head = N <= HEAD_MAX_N;
+    if (!head && !(needs(a) && needs(b))) return -1;
     const float *ad = needs(b) ? tt_dev(a->val) : NULL;
     const float *bd = needs(a) ? tt_dev(b->val) : NULL;
     if ((needs(b) && !ad) || (needs(a) && !bd)) return -1;
@@ -498,9 +502,14 @@ static int backward_matmul_head(AGNode *n, const float *g) {
     Tensor *ga = needs(a) ? tt_empty_like(a->val) : NULL;
     Tensor *tx = x ? tt_empty_like(x->val) : NULL;
     Tensor *ty = y ? tt_empty_like(y->val) : NULL;
-    if ((needs(b) && !gb) || (needs(a) && !ga) || (x && !tx) || (y && !ty) ||
-        tt_k_head_bwd(ad, M, K, bd, N, g, gb ? gb->dev : NULL, ga ? ga->dev : NULL,
-                      tx ? tx->dev : NULL, ty ? ty->dev : NULL, R) != 0) {
+    int rc = -1;
+    if ((!needs(b) || gb) && (!needs(a) || ga) && (!x || tx) && (!y || ty)) {
+        float *dB = gb ? gb->dev : NULL, *dA = ga ? ga->dev : NULL;
+        float *d1 = tx ? tx->dev : NULL, *d2 = ty ? ty->dev : NULL;
+        rc = head ? tt_k_head_bwd(ad, M, K, bd, N, g, dB, dA, d1, d2, R)
+                  : tt_k_matmul_bwd_small(ad, M, K, bd, N, g, dB, dA, d1, d2, R);
+    }
+    if (rc != 0) {
         tt_release(gb); tt_release(ga); tt_release(tx); tt_release(ty);
         return -1;
     }
@@ -516,7 +525,7 @@ static void backward_matmul(AGNode *n) {
     const int M = (int)a->val->shape[0], K = (int)a->val->shape[1], N = (int)b->val->shape[1];
     const float *g = tt_dev(n->grad);
     if (!g) return;
-    if (tt_defer_enabled() && backward_matmul_head(n, g) == 0) return;
+    if (tt_defer_enabled() && backward_matmul_fused(n, g) == 0) return;
     if (needs(a)) {  /* dA = g (MxN) * b^T (b is KxN) */
         const float *bd = tt_dev(b->val);
         Tensor *ga = bd ? tt_empty_like(a->val) : NULL;

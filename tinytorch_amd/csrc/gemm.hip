@@ -1476,15 +1476,26 @@ __global__ void __launch_bounds__(256) pad_rows_kernel(PadJob a, PadJob b, int g
 // zeros.
 constexpr int SW = 8;  // waves per small-GEMM workgroup
 constexpr int SG = 4;  // 8-k groups per pipelined chunk
+// Where a small-GEMM tile's outputs go: C (ldc), and for the dA of a
+// matmul whose input is a padones (of a relu output R), also the padones
+// input's gradient d1 = C[:, :-1] and d2 = d1 masked by R > 0 (d2 = d1
+// without R); d1 / d2 are (M x (N-1)) row-major.
+struct SmallOut {
+  float *C;
+  long ldc;
+  float *d1, *d2;
+  const float *R;
+};
+
 template <bool A_KC, bool B_NC, bool VA, bool VB>
-__global__ void __launch_bounds__(64 * SW)
-gemm_small_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
-                  const float *__restrict__ B, long ldb, float *__restrict__ C, long ldc, int kc) {
-  __shared__ float red[(SW - 1) * 16 * 64];
+__device__ __forceinline__ void small_tile(int M, int N, int K, const float *__restrict__ A,
+                                           long lda, const float *__restrict__ B, long ldb,
+                                           const SmallOut &out, int kc, int bx, int by,
+                                           float *red) {
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l32 = lane & 31, h = lane >> 5;
-  const int m0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
+  const int m0 = by * 32, n0 = bx * 32;
   const int mr = min(m0 + l32, M - 1), nr = min(n0 + l32, N - 1);
   // this lane's A row / B column: element k at base + k * step
   const float *ap = A_KC ? A + (long)mr * lda : A + mr;
@@ -1543,11 +1554,55 @@ gemm_small_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
     for (int r = 0; r < 16; r++) acc[r] += red[(o * 16 + r) * 64 + lane];
   const int n = n0 + l32;
   if (n >= N) return;
+  const bool pad = out.d1 || out.d2;
 #pragma unroll
   for (int r = 0; r < 16; r++) {
     const int m = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
-    if (m < M) C[(long)m * ldc + n] = acc[r];
+    if (m < M) {
+      out.C[(long)m * out.ldc + n] = acc[r];
+      if (pad && n < N - 1) {
+        const long o = (long)m * (N - 1) + n;
+        if (out.d1) out.d1[o] = acc[r];
+        if (out.d2) out.d2[o] = out.R ? (out.R[o] > 0.0f ? acc[r] : 0.0f) : acc[r];
+      }
+    }
   }
+}
+
+template <bool A_KC, bool B_NC, bool VA, bool VB>
+__global__ void __launch_bounds__(64 * SW)
+gemm_small_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
+                  const float *__restrict__ B, long ldb, float *__restrict__ C, long ldc, int kc) {
+  __shared__ float red[(SW - 1) * 16 * 64];
+  small_tile<A_KC, B_NC, VA, VB>(M, N, K, A, lda, B, ldb, SmallOut{C, ldc, nullptr, nullptr, nullptr},
+                                 kc, blockIdx.x, blockIdx.y, red);
+}
+
+// Both gradients of a matmul C = A * B in one launch of small-GEMM tiles:
+// dA = G * B^T (the tiles of tt_k_gemm(M, K, N, G, N, 0, B, N, 1, ...)) in
+// workgroups [0, nba), dB = A^T * G (tt_k_gemm(K, N, M, A, K, 1, G, N, 0, ...))
+// after them; each tile is computed exactly as its own launch computes it.
+struct SmallJob {
+  int M, N, K;
+  const float *A;
+  long lda;
+  const float *B;
+  long ldb;
+  SmallOut out;
+  int kc, nbx;
+};
+
+template <bool VDA>
+__global__ void __launch_bounds__(64 * SW)
+gemm_small_pair_kernel(SmallJob da, SmallJob db, int nba) {
+  __shared__ float red[(SW - 1) * 16 * 64];
+  const int i = blockIdx.x;
+  if (i < nba)
+    small_tile<true, false, VDA, VDA>(da.M, da.N, da.K, da.A, da.lda, da.B, da.ldb, da.out, da.kc,
+                                      i % da.nbx, i / da.nbx, red);
+  else
+    small_tile<false, true, false, false>(db.M, db.N, db.K, db.A, db.lda, db.B, db.ldb, db.out,
+                                          db.kc, (i - nba) % db.nbx, (i - nba) / db.nbx, red);
 }
 
 // small_ok: below the 64x64 kernel's range (2MNK < 2^29) with at least 128
@@ -1832,6 +1887,42 @@ extern "C" int tt_k_gemm_relu_pad(int M, int N, int K, const float *A, const flo
   g_red_hook = nullptr;
   if (rc) return rc;
   return h.applied ? 0 : tt_k_relu_padones_fwd(C, R, P, M, N);
+}
+
+// Both gradients of C = A * B (A M x K, B K x N, row-major) in one launch,
+// when tt_k_gemm would compute each of them with its small-GEMM kernel:
+// the same tiles, so the same values as two tt_k_gemm calls.  d1 / d2: the
+// padones (and relu) backward fused into dA's stores, as in tt_k_head_bwd.
+// -1: not covered (nothing launched).
+extern "C" int tt_k_matmul_bwd_small(const float *A, int M, int K, const float *B, int N,
+                                     const float *G, float *dB, float *dA, float *d1, float *d2,
+                                     const float *R) {
+  if (M <= 0 || K <= 0 || N <= 0 || !A || !B || !G || !dA || !dB || ((d1 || d2) && K < 2) ||
+      g_force_tile >= 0)
+    return -1;
+  const Opnd g{G, N, 0, 1}, b{B, N, 0, 1}, a{A, K, 0, 1};
+  auto big = [](const Plan &p) {
+    return p.tile == T256x256 || p.tile == T256x128 || p.tile == T128x128;
+  };
+  // run()'s choice for dA = G * B^T (M, K, N) and dB = A^T * G (K, N, M)
+  if (big(plan(M, K, N)) || big(plan(K, N, M)) || !small_ok<true, false>(M, K, N, g, b) ||
+      !small_ok<false, true>(K, N, M, a, g))
+    return -1;
+  SmallJob da{M, K, N, G, N, B, N, SmallOut{dA, K, d1, d2, R}, ((N + SW - 1) / SW + 7) / 8 * 8,
+              (K + 31) / 32};
+  SmallJob db{K, N, M, A, K, G, N, SmallOut{dB, N, nullptr, nullptr, nullptr},
+              ((M + SW - 1) / SW + 7) / 8 * 8, (N + 31) / 32};
+  const long nba = (long)da.nbx * ((M + 31) / 32), nbb = (long)db.nbx * ((K + 31) / 32);
+  if (nba + nbb > 0x7fffffffL) return -1;
+  // 16-byte loads of G's and B's k-contiguous rows (the loads only, not the values)
+  const bool vec = aligned16(G) && aligned16(B) && N % 4 == 0;
+  if (vec)
+    hipLaunchKernelGGL(gemm_small_pair_kernel<true>, dim3((unsigned)(nba + nbb)), dim3(64 * SW), 0,
+                       stream(), da, db, (int)nba);
+  else
+    hipLaunchKernelGGL(gemm_small_pair_kernel<false>, dim3((unsigned)(nba + nbb)), dim3(64 * SW),
+                       0, stream(), da, db, (int)nba);
+  return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
 // ---- the GEMM without allocation (tt_k_gemm_noalloc) ----
