@@ -49,24 +49,78 @@ __device__ float g_head_zero[4];
 // for r < rows.  Lane t takes column t % COLS of rows t / COLS + (NT/COLS) u;
 // U loads per lane per batch, all issued before the first LDS store.
 template <int COLS, int U>
-__device__ __forceinline__ void stage(float *dst, int dstride, const float *__restrict__ src,
-                                      long sstride, int rows, int nr, int nc) {
-  constexpr int RPB = NT / COLS;             // rows per pass of the workgroup
+__device__ __forceinline__ void stage_load(float (&v)[U], const float *__restrict__ src,
+                                           long sstride, int base, int nr, int nc) {
+  constexpr int RPB = NT / COLS;  // rows per pass of the workgroup
   const int c = threadIdx.x % COLS, r0 = threadIdx.x / COLS;
-  for (int base = 0; base < rows; base += RPB * U) {
-    float v[U];
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-      const int r = base + r0 + RPB * u;
-      const bool ok = r < nr && c < nc;
-      v[u] = *(ok ? src + r * sstride + c : g_head_zero);
-    }
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-      const int r = base + r0 + RPB * u;
-      if (r < rows) dst[r * dstride + c] = v[u];
-    }
+  for (int u = 0; u < U; u++) {
+    const int r = base + r0 + RPB * u;
+    const bool ok = r < nr && c < nc;
+    v[u] = *(ok ? src + r * sstride + c : g_head_zero);
   }
+}
+
+template <int COLS, int U>
+__device__ __forceinline__ void stage_store(const float (&v)[U], float *dst, int dstride, int base,
+                                            int rows) {
+  constexpr int RPB = NT / COLS;
+  const int c = threadIdx.x % COLS, r0 = threadIdx.x / COLS;
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const int r = base + r0 + RPB * u;
+    if (r < rows) dst[r * dstride + c] = v[u];
+  }
+}
+
+// Two blocks of M rows staged together: both blocks' loads of a batch of
+// rows are issued before either's LDS stores (one memory round trip per
+// batch).  (NT / CA) * UA == (NT / CB) * UB rows per batch.
+template <int CA, int UA, int CB, int UB>
+__device__ __forceinline__ void stage_pair(float *da, const float *__restrict__ sa, long lda,
+                                           int nca, float *db, const float *__restrict__ sb,
+                                           long ldb, int ncb, int M) {
+  static_assert((NT / CA) * UA == (NT / CB) * UB, "batches of the two blocks differ");
+  for (int base = 0; base < M; base += (NT / CA) * UA) {
+    float va[UA], vb[UB];
+    stage_load<CA, UA>(va, sa, lda, base, M, nca);
+    stage_load<CB, UB>(vb, sb, ldb, base, M, ncb);
+    stage_store<CA, UA>(va, da, CA, base, M);
+    stage_store<CB, UB>(vb, db, CB, base, M);
+  }
+}
+
+// dW[k][j] for KW rows k and JW = NT / KW columns j of one workgroup: lane t
+// takes k = k0 + t % KW, j = j0 + t / KW and sums over m ascending from LDS
+// (As: M x KW, Gs: M x JW; the strides are constants, so every LDS read of
+// the loop carries its offset in the instruction).
+template <int KW>
+__device__ __forceinline__ void head_dw_block(const float *__restrict__ A, int M, int K,
+                                              const float *__restrict__ G, int N,
+                                              float *__restrict__ dW, int k0, int j0,
+                                              float *lds) {
+  constexpr int JW = NT / KW;
+  const int tid = threadIdx.x;
+  float *As = lds, *Gs = lds + M * KW;
+  // batches of 32 * NT / KW rows (128 or 256)
+  stage_pair<KW, 32, JW, 32 * JW / KW>(As, A + k0, K, min(KW, K - k0), Gs, G + j0, N,
+                                       min(JW, N - j0), M);
+  __syncthreads();
+  const int kl = tid % KW, jl = tid / KW;
+  const int k = k0 + kl, j = j0 + jl;
+  if (j >= N || k >= K) return;
+  const float *ac = As + kl, *gc = Gs + jl;
+  float acc = 0.0f;
+  int m = 0;
+  for (; m + 16 <= M; m += 16) {
+    float a[16], g[16];
+#pragma unroll
+    for (int u = 0; u < 16; u++) { a[u] = ac[(m + u) * KW]; g[u] = gc[(m + u) * JW]; }
+#pragma unroll
+    for (int u = 0; u < 16; u++) acc += a[u] * g[u];
+  }
+  for (; m < M; m++) acc += ac[m * KW] * gc[m * JW];
+  dW[(long)k * N + j] = acc;
 }
 
 
@@ -83,43 +137,25 @@ head_bwd_kernel(const float *__restrict__ A, int M, int K, const float *__restri
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nkb = (K + 63) / 64;
   if ((int)blockIdx.x < nbw) {
-    // dW[k][j] for KW rows k and JW = 256 / KW columns j: lane t takes
-    // k = k0 + t % KW, j = j0 + t / KW.  As (M x KW), Gs (M x JW)
+    // dW blocks: KW rows k x NT / KW columns j
     const int JW = NT / KW;
     const int kb = blockIdx.x % nkw, jb = blockIdx.x / nkw;
-    const int k0 = kb * KW, j0 = jb * JW;
-    float *As = lds, *Gs = lds + M * KW;
-    if (KW == 64) {
-      stage<64, 16>(As, 64, A + k0, K, M, M, min(64, K - k0));
-      stage<4, 8>(Gs, 4, G + j0, N, M, M, min(4, N - j0));
-    } else {
-      stage<32, 16>(As, 32, A + k0, K, M, M, min(32, K - k0));
-      stage<8, 8>(Gs, 8, G + j0, N, M, M, min(8, N - j0));
-    }
-    __syncthreads();
-    const int kl = tid % KW, jl = tid / KW;
-    const int k = k0 + kl, j = j0 + jl;
-    if (j >= N || k >= K) return;
-    const float *ac = As + kl, *gc = Gs + jl;
-    float acc = 0.0f;
-    int m = 0;
-    for (; m + 16 <= M; m += 16) {
-      float a[16], g[16];
-#pragma unroll
-      for (int u = 0; u < 16; u++) { a[u] = ac[(m + u) * KW]; g[u] = gc[(m + u) * JW]; }
-#pragma unroll
-      for (int u = 0; u < 16; u++) acc += a[u] * g[u];
-    }
-    for (; m < M; m++) acc += ac[m * KW] * gc[m * JW];
-    dW[(long)k * N + j] = acc;
+    if (KW == 64) head_dw_block<64>(A, M, K, G, N, dW, kb * 64, jb * JW, lds);
+    else head_dw_block<32>(A, M, K, G, N, dW, kb * 32, jb * JW, lds);
     return;
   }
   // dA block: columns [k0, k0 + 64) x rows [m0, m0 + DA_M); Ws, Gs (64 / DA_M x NC)
   const int blk = blockIdx.x - nbw;
   const int k0 = (blk % nkb) * 64, m0 = (blk / nkb) * DA_M;
   float *Ws = lds, *Gs = lds + 64 * NC;
-  stage<NC, 4>(Ws, NC, W + (long)k0 * N, N, 64, min(64, K - k0), N);
-  stage<NC, 4>(Gs, NC, G + (long)m0 * N, N, DA_M, min(DA_M, M - m0), N);
+  {  // both blocks' loads in flight before either's LDS stores
+    constexpr int UW = 64 / (NT / NC), UG = DA_M / (NT / NC);
+    float vw[UW], vg[UG];
+    stage_load<NC, UW>(vw, W + (long)k0 * N, N, 0, min(64, K - k0), N);
+    stage_load<NC, UG>(vg, G + (long)m0 * N, N, 0, min(DA_M, M - m0), N);
+    stage_store<NC, UW>(vw, Ws, NC, 0, 64);
+    stage_store<NC, UG>(vg, Gs, NC, 0, DA_M);
+  }
   const int kl = lane, mg = wave;
   const int k = k0 + kl;
   const int K1 = K - 1;
