@@ -1446,13 +1446,15 @@ __global__ void __launch_bounds__(256) pad_rows_kernel(PadJob a, PadJob b, int g
     const float *__restrict__ sr = j.src + (long)r * j.ld;
     float *__restrict__ dr = j.dst + (long)r * j.ldp;
     // four loads issued before their stores (one memory round trip per 1024
-    // floats, not one per 256)
+    // floats, not one per 256); the loads are unconditional (the column
+    // clamped, the value selected), so none waits on a branch
     for (int c0 = 0; c0 < j.ldp; c0 += 1024) {
       float v[4];
 #pragma unroll
       for (int u = 0; u < 4; u++) {
         const int c = c0 + 256 * u + threadIdx.x;
-        v[u] = c < j.cols ? sr[c] : 0.f;
+        const float t = sr[min(c, j.cols - 1)];
+        v[u] = c < j.cols ? t : 0.f;
       }
 #pragma unroll
       for (int u = 0; u < 4; u++) {
