@@ -319,3 +319,90 @@ def test_conv_dw_tiled_vs_oracle(tlib, case):
             assert _bits_equal(outs[0][0], outs[1][0]) and _bits_equal(outs[0][1], outs[1][1])
     finally:
         tlib.tth_conv_dwt(prev)
+
+
+POOL_CASES = [
+    (128, 3, 32, 32, 32, 3, 3, 1, 1, 1, 1), (128, 32, 16, 16, 64, 3, 3, 1, 1, 1, 1),  # config 4
+    (128, 4, 32, 32, 8, 3, 3, 1, 1, 1, 1),  # Wo = 32 pairs blocks: needs two blocks a wave (N >= 128)
+    (4, 16, 8, 8, 40, 3, 3, 1, 1, 1, 1), (2, 4, 4, 4, 8, 3, 3, 1, 1, 1, 1),
+    (3, 5, 16, 16, 33, 3, 3, 1, 1, 1, 1),
+]
+
+
+@pytest.mark.parametrize("case", POOL_CASES)
+def test_conv_relu_pool_fused_kernel_bitexact(tlib, case):
+    """tt_k_conv2d_relu_pool_fwd_lds: convolution, relu and 2x2 / stride-2
+    max pool bit for bit equal to the convolution + relu kernel followed by
+    the pool kernel, and the pool equal to the oracle's max pool of the relu
+    (reference src/ops_spatial.c:129-164), NaN inputs included."""
+    x, w, b, _, geo = _inputs(case)
+    N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo = geo
+    x.flat[:: max(1, x.size // 5)] = np.nan
+    print("conv relu pool fused", case, flush=True)
+    n_out, n_pool = N * F * Ho * Wo, N * F * (Ho // 2) * (Wo // 2)
+    dx_, dw_, db_ = DevBuf.from_np(x), DevBuf.from_np(w), DevBuf.from_np(b)
+    o1, r1, p1 = DevBuf(n_out), DevBuf(n_out), DevBuf(n_pool)
+    o2, r2, p2 = DevBuf(n_out), DevBuf(n_out), DevBuf(n_pool)
+    check(tlib.tt_k_conv2d_relu_pool_fwd_lds(dx_.ptr, dw_.ptr, db_.ptr, o1.ptr, r1.ptr, p1.ptr,
+                                             *geo), "fused")
+    check(tlib.tt_k_conv2d_relu_fwd_lds(dx_.ptr, dw_.ptr, db_.ptr, o2.ptr, r2.ptr, *geo), "conv")
+    check(tlib.tt_k_maxpool_fwd(r2.ptr, p2.ptr, N, F, Ho, Wo, 2, 2, 2, 2, Ho // 2, Wo // 2), "pool")
+    shp, pshp = (N, F, Ho, Wo), (N, F, Ho // 2, Wo // 2)
+    assert _bits_equal(o1.to_np(shp), o2.to_np(shp))
+    assert _bits_equal(r1.to_np(shp), r2.to_np(shp))
+    pool = p1.to_np(pshp)
+    assert _bits_equal(pool, p2.to_np(pshp))
+    assert _bits_equal(pool, orc.maxpool_fwd(r1.to_np(shp), 2, 2, 2, 2))
+
+
+@pytest.mark.parametrize("case", [(2, 3, 24, 24, 4, 3, 3, 1, 1, 1, 1),   # 32 % Wo != 0
+                                  (2, 3, 7, 7, 4, 3, 3, 1, 1, 1, 1),     # odd Ho, Wo
+                                  (2, 3, 8, 8, 4, 5, 5, 1, 1, 2, 2),     # not 3x3
+                                  (8, 3, 32, 32, 32, 3, 3, 1, 1, 1, 1)])  # Wo = 32, one block a wave
+def test_conv_relu_pool_fused_rejects(tlib, case):
+    x, w, b, _, geo = _inputs(case)
+    N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo = geo
+    dx_, dw_ = DevBuf.from_np(x), DevBuf.from_np(w)
+    o, r, p = DevBuf(N * F * Ho * Wo), DevBuf(N * F * Ho * Wo), DevBuf(N * F * Ho * Wo)
+    assert tlib.tt_k_conv2d_relu_pool_fwd_lds(dx_.ptr, dw_.ptr, None, o.ptr, r.ptr, p.ptr,
+                                              *geo) == -1
+
+
+@pytest.mark.parametrize("case", [POOL_CASES[3], POOL_CASES[5], (2, 3, 24, 24, 4, 3, 3, 1, 1, 1, 1)])
+def test_autograd_conv_relu_pool_deferred(tlib, case):
+    """ag_conv2d, ag_relu, ag_maxpool2d(2x2) in one launch against the same
+    graph with every launch made at once: values and gradients bit for bit
+    equal.  Reading the relu's value first, or a 3x3 pool, launches the
+    pending convolution + relu alone (the pool then runs by itself)."""
+    from tinytorch_amd.torch_py import Node
+    x, w, b, _, geo = _inputs(case)
+    N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo = geo
+    print("deferred conv relu pool", case, flush=True)
+
+    def run(mode):
+        X, Wn, Bn = Node.leaf(x), Node.leaf(w), Node.leaf(b)
+        c = X.conv2d(Wn, Bn, (sh, sw), (ph, pw))
+        r = c.relu()
+        if mode == "peek":
+            rv = r.value()
+        k = 3 if mode == "pool3" else 2
+        m = r.maxpool2d(k, k)
+        vals = [c.value(), r.value(), m.value()]
+        gm = np.ascontiguousarray(np.cos(np.arange(vals[2].size, dtype=np.float32)).reshape(vals[2].shape))
+        m.backward(gm)
+        out = vals + [X.grad(), Wn.grad(), Bn.grad()]
+        if mode == "peek":
+            assert _bits_equal(rv, vals[1])
+        for nd in (m, r, c, X, Wn, Bn):
+            nd.release()
+        return out
+
+    for mode in ("fused", "peek", "pool3"):
+        prev = tlib.tth_conv_relu_fuse(0)
+        try:
+            ref = run(mode)
+        finally:
+            tlib.tth_conv_relu_fuse(prev)
+        got = run(mode)
+        for a, e in zip(got, ref):
+            assert _bits_equal(a, e), mode

@@ -228,20 +228,17 @@ AGNode *ag_relu(AGNode *a) {
         return n;
     }
     if (tt_pend.active == TT_PEND_CONV && tt_pend.out == a->val) {
-        /* the convolution producing a is still pending: one launch writes
-         * it and its relu (same values as tt_relu of the stored output) */
+        /* the convolution producing a is still pending: its relu waits with
+         * it, and one launch writes both (same values as tt_relu of the
+         * stored output) -- with a 2x2 max pool of the relu too when that is
+         * the next call */
         Tensor *r = tt_empty_like(a->val);
-        if (r) {
-            const TTPendConv p = tt_pend;
-            const int *q = p.geo;
-            tt_pend.active = 0;
-            if (tt_k_conv2d_relu_fwd_lds(p.x, p.w, p.b, p.out->dev, r->dev, q[0], q[1], q[2],
-                                         q[3], q[4], q[5], q[6], q[7], q[8], q[9], q[10], q[11],
-                                         q[12]) == 0)
-                return make_node(r, &OP_RELU, a, NULL, NULL);
-            tt_pend = p;  /* not launched: the plain convolution runs below */
-            tt_release(r);
-        }
+        if (!r) return NULL;
+        AGNode *n = make_node(r, &OP_RELU, a, NULL, NULL);
+        if (!n) return NULL;
+        tt_pend.r = r;
+        tt_pend.active = TT_PEND_CONV_RELU;
+        return n;
     }
     if (tt_defer_enabled() && a->val->ndim == 2) {
         /* a relu that a padones may consume (the MLP's hidden layers): left
@@ -353,6 +350,25 @@ static AGNode *pool_node(AGNode *a, Tensor *v, const AGOp *op, int ph, int pw, i
 
 AGNode *ag_maxpool2d(AGNode *a, int ph, int pw, int sh, int sw) {
     if (!a) return NULL;
+    if (tt_pend.active == TT_PEND_CONV_RELU && tt_pend.r == a->val && ph == 2 && pw == 2 &&
+        sh == 2 && sw == 2 && a->val->ndim == 4 && a->val->shape[2] % 2 == 0 &&
+        a->val->shape[3] % 2 == 0) {
+        /* convolution, relu and this pool in one launch */
+        const long shp[4] = {a->val->shape[0], a->val->shape[1], a->val->shape[2] / 2,
+                             a->val->shape[3] / 2};
+        Tensor *v = tt_empty_dev(shp, 4);
+        if (v) {
+            const TTPendConv p = tt_pend;
+            const int *q = p.geo;
+            tt_pend.active = 0;
+            if (tt_k_conv2d_relu_pool_fwd_lds(p.x, p.w, p.b, p.out->dev, p.r->dev, v->dev, q[0],
+                                              q[1], q[2], q[3], q[4], q[5], q[6], q[7], q[8],
+                                              q[9], q[10], q[11], q[12]) == 0)
+                return pool_node(a, v, &OP_MAXPOOL2D, ph, pw, sh, sw);
+            tt_pend = p;  /* not launched: convolution + relu, then the pool below */
+            tt_release(v);
+        }
+    }
     Tensor *v = tt_maxpool2d(a->val, ph, pw, sh, sw);
     if (!v) return NULL;
     return pool_node(a, v, &OP_MAXPOOL2D, ph, pw, sh, sw);

@@ -263,7 +263,8 @@ template <int PB, bool FLIP, bool VEC>
 __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2)))
 conv_fwd_lds_kernel(const float *__restrict__ x, const float *__restrict__ w,
                     const float *__restrict__ bias, float *__restrict__ out,
-                    float *__restrict__ rout, Geo g, int chunks) {
+                    float *__restrict__ rout, float *__restrict__ /*pout: 3x3 kernel only*/,
+                    Geo g, int chunks) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   constexpr int CHUNK = 128 * PB;
   const int n = blockIdx.x / chunks, chunk = blockIdx.x - n * chunks;
@@ -409,7 +410,7 @@ template <int PB, bool FLIP, bool VEC, int KH, int KW, int KS = 1>
 __global__ void __launch_bounds__(NT * KS) __attribute__((amdgpu_waves_per_eu(1, 2)))
 conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
                   const float *__restrict__ bias, float *__restrict__ out,
-                  float *__restrict__ rout, Geo g, int chunks) {
+                  float *__restrict__ rout, float *__restrict__ pout, Geo g, int chunks) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   constexpr int CHUNK = 128 * PB, TAPS = KH * KW;
   const int n = blockIdx.x / chunks, chunk = blockIdx.x - n * chunks;
@@ -637,8 +638,65 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
       }
     }
   };
-  if (rn) store(std::true_type{});
-  else store(std::false_type{});
+  if (pout) {
+    // relu and the 2x2 / stride-2 max pool of it as well (pout, N x F x
+    // Ho/2 x Wo/2; the host checks that Ho and Wo are even, chunks start on
+    // even rows and a row pair is either inside one 32-pixel block
+    // (32 % Wo == 0, 32 / Wo even) or two consecutive blocks (Wo == 32, PB
+    // even)).  The relu values are >= +0 and never NaN, so their max does
+    // not depend on the order of the comparisons: the pool's output bit for
+    // bit.  Every lane takes part in the shuffles; stores are masked.
+    float o[PB][16];
+#pragma unroll
+    for (int j = 0; j < PB; j++) {
+      const int p = p0 + (pw4 * PB + j) * 32 + l32;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int f = f0 + 8 * (r >> 2) + 4 * half + (r & 3);
+        const float v = acc[j][r] + bv[r];
+        o[j][r] = v > 0.0f ? v : 0.0f;
+        if (f < g.F && p < p1) {
+          on[(long)f * P + p] = v;
+          rn[(long)f * P + p] = o[j][r];
+        }
+      }
+    }
+    const int P4 = P >> 2, Wo2 = g.Wo >> 1;
+    float *pn = pout + (long)n * g.F * P4;
+    if (g.Wo == 32) {  // rows 2i, 2i+1 are blocks j, j+1
+#pragma unroll
+      for (int j = 0; j + 1 < PB; j += 2) {
+        const int pj = p0 + (pw4 * PB + j) * 32;
+        const int prow = pj >> 6;
+        const bool lead = (l32 & 1) == 0 && pj < p1;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const float m0 = fmaxf(o[j][r], o[j + 1][r]);
+          const float m = fmaxf(m0, __shfl_xor(m0, 1, 64));
+          const int f = f0 + 8 * (r >> 2) + 4 * half + (r & 3);
+          if (lead && f < g.F) pn[(long)f * P4 + prow * Wo2 + (l32 >> 1)] = m;
+        }
+      }
+    } else {  // rows 2i, 2i+1 are lanes l and l ^ Wo of one block
+#pragma unroll
+      for (int j = 0; j < PB; j++) {
+        const int p = p0 + (pw4 * PB + j) * 32 + l32;
+        const int row = p / g.Wo, col = p - row * g.Wo;
+        const bool lead = (col & 1) == 0 && (row & 1) == 0 && p < p1;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const float m0 = fmaxf(o[j][r], __shfl_xor(o[j][r], 1, 64));
+          const float m = fmaxf(m0, __shfl_xor(m0, g.Wo, 64));
+          const int f = f0 + 8 * (r >> 2) + 4 * half + (r & 3);
+          if (lead && f < g.F) pn[(long)f * P4 + (row >> 1) * Wo2 + (col >> 1)] = m;
+        }
+      }
+    }
+  } else if (rn) {
+    store(std::true_type{});
+  } else {
+    store(std::false_type{});
+  }
 }
 
 // ---- weight gradient partials ----
@@ -1389,24 +1447,36 @@ FwdPlan plan_fwd(const Geo &g, int N, bool flip) {
   return best;
 }
 
+// The 3x3 forward kernel can also write the 2x2 / stride-2 max pool of its
+// relu: even Ho and Wo, chunks starting on even rows, and a row pair inside one
+// 32-pixel block (32 % Wo == 0, 32 / Wo even) or two consecutive blocks
+// (Wo == 32, two blocks per wave).
+bool pool_fusable(const Geo &g, const FwdPlan &pl) {
+  const int chunk = 128 * pl.pb;
+  if (!is_k3(g) || g.Ho % 2 || g.Wo % 2 || chunk % (2 * g.Wo)) return false;
+  if (g.Wo == 32) return pl.pb % 2 == 0;
+  return g.Wo < 32 && 32 % g.Wo == 0 && (32 / g.Wo) % 2 == 0;
+}
+
 template <int PB, bool FLIP, bool VEC>
 int launch_fwd(const float *x, const float *w, const float *bias, float *out, float *rout,
-               const Geo &g, int N, const FwdPlan &pl) {
+               float *pout, const Geo &g, int N, const FwdPlan &pl) {
   auto kern = !is_k3(g)     ? conv_fwd_lds_kernel<PB, FLIP, VEC>
               : pl.ks == 2 ? conv_fwd_k_kernel<PB, FLIP, VEC, 3, 3, 2>
                            : conv_fwd_k_kernel<PB, FLIP, VEC, 3, 3, 1>;
   if (pl.lds > 64 * 1024 && !allow_big_lds((const void *)kern)) return -1;
   const dim3 grid((unsigned)(N * pl.chunks), (unsigned)((g.F + 31) / 32));
-  hipLaunchKernelGGL(kern, grid, dim3(NT * pl.ks), pl.lds, stream(), x, w, bias, out, rout, g,
-                     pl.chunks);
+  hipLaunchKernelGGL(kern, grid, dim3(NT * pl.ks), pl.lds, stream(), x, w, bias, out, rout, pout,
+                     g, pl.chunks);
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
 template <bool FLIP>
 int run_fwd(const float *x, const float *w, const float *bias, float *out, const Geo &g, int N,
-            bool dry, float *rout = nullptr) {
+            bool dry, float *rout = nullptr, float *pout = nullptr) {
   const FwdPlan pl = plan_fwd(g, N, FLIP);
   if (!pl.pb) return -1;
+  if (pout && !(rout && !FLIP && pool_fusable(g, pl))) return -1;
   if (dry) return 0;
   if (fail_direct()) return -3;
   // 16-byte loads: 4-aligned rows of x and of the weight blocks (the 3x3
@@ -1420,10 +1490,10 @@ int run_fwd(const float *x, const float *w, const float *bias, float *out, const
                                    : g.K % 4 == 0);
   const bool vec = g.W % 4 == 0 && aligned16(x) && wok;
   if (pl.pb == 2)
-    return vec ? launch_fwd<2, FLIP, true>(x, w, bias, out, rout, g, N, pl)
-               : launch_fwd<2, FLIP, false>(x, w, bias, out, rout, g, N, pl);
-  return vec ? launch_fwd<1, FLIP, true>(x, w, bias, out, rout, g, N, pl)
-             : launch_fwd<1, FLIP, false>(x, w, bias, out, rout, g, N, pl);
+    return vec ? launch_fwd<2, FLIP, true>(x, w, bias, out, rout, pout, g, N, pl)
+               : launch_fwd<2, FLIP, false>(x, w, bias, out, rout, pout, g, N, pl);
+  return vec ? launch_fwd<1, FLIP, true>(x, w, bias, out, rout, pout, g, N, pl)
+             : launch_fwd<1, FLIP, false>(x, w, bias, out, rout, pout, g, N, pl);
 }
 
 // dW kernel variants: (MF, JW, KS) with FS = filters/16 per workgroup.
@@ -1745,6 +1815,21 @@ extern "C" int tt_k_conv2d_relu_fwd_lds(const float *x, const float *w, const fl
     return -1;
   const Geo g{C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo, F, C * HH * WW};
   return run_fwd<false>(x, w, bias, out, g, N, false, rout);
+}
+
+// The same convolution with its relu and the 2x2 / stride-2 max pool of the
+// relu: out, rout as above and pout (N x F x Ho/2 x Wo/2) in one launch
+// (bit-identical to tt_k_conv2d_relu_fwd_lds followed by the max pool).
+// -1: not covered (see pool_fusable).
+extern "C" int tt_k_conv2d_relu_pool_fwd_lds(const float *x, const float *w, const float *bias,
+                                             float *out, float *rout, float *pout, int N, int C,
+                                             int H, int W, int F, int HH, int WW, int sh, int sw,
+                                             int ph, int pw, int Ho, int Wo) {
+  if (!x || !w || !out || !rout || !pout || out == rout ||
+      !geo_ok(N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo))
+    return -1;
+  const Geo g{C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo, F, C * HH * WW};
+  return run_fwd<false>(x, w, bias, out, g, N, false, rout, pout);
 }
 
 // dw (F, C*HH*WW) and, when db is given, db (F) from the output gradient g

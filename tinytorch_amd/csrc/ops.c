@@ -254,6 +254,16 @@ int tt_flush_pending(void) {
             if (rc == 0) rc = tt_k_relu_fwd(tt_pend.out->dev, tt_pend.r->dev, tt_pend.r->numel);
             if (rc != 0) tt_pend.r->valid = 0;
         }
+    } else if (kind == TT_PEND_CONV_RELU) {
+        const int *q = tt_pend.geo;
+        rc = tt_k_conv2d_relu_fwd_lds(tt_pend.x, tt_pend.w, tt_pend.b, tt_pend.out->dev,
+                                      tt_pend.r->dev, q[0], q[1], q[2], q[3], q[4], q[5], q[6],
+                                      q[7], q[8], q[9], q[10], q[11], q[12]);
+        if (rc != 0) {
+            rc = conv_fwd_gemm(tt_pend.x, tt_pend.w, tt_pend.b, tt_pend.out->dev, q);
+            if (rc == 0) rc = tt_k_relu_fwd(tt_pend.out->dev, tt_pend.r->dev, tt_pend.r->numel);
+        }
+        if (rc != 0) tt_pend.r->valid = 0;
     } else {
         const int *q = tt_pend.geo;
         rc = tt_k_conv2d_fwd_lds(tt_pend.x, tt_pend.w, tt_pend.b, tt_pend.out->dev, q[0], q[1],
