@@ -299,13 +299,16 @@ int tt_k_conv2d_relu_fwd_lds(const float *x, const float *w, const float *bias, 
 /* The same convolution, its relu and the 2x2 / stride-2 max pool of the relu
  * (reference src/ops_spatial.c:129-164) in one launch: out, rout as in
  * tt_k_conv2d_relu_fwd_lds and pout (N x F x Ho/2 x Wo/2), bit-identical to
- * the three separate steps.  3x3 kernels with even Ho, Wo whose output rows
- * pair up inside the kernel's pixel blocks (Wo = 32, or 32 % Wo == 0 with
- * 32 / Wo even); -1 otherwise, nothing launched. */
+ * the three separate steps; cout / dout (may be NULL): the pool output
+ * flattened per image once more, as a copy (a reshape to N x F*Ho*Wo/4,
+ * src/ops_spatial.c:22-34) and padded with a last column of ones (padones
+ * of that, src/autograd.c:195-212).  3x3 kernels with even Ho, Wo whose
+ * output rows pair up inside the kernel's pixel blocks (Wo = 32, or
+ * 32 % Wo == 0 with 32 / Wo even); -1 otherwise, nothing launched. */
 int tt_k_conv2d_relu_pool_fwd_lds(const float *x, const float *w, const float *bias, float *out,
-                                  float *rout, float *pout, int N, int C, int H, int W, int F,
-                                  int HH, int WW, int sh, int sw, int ph, int pw, int Ho,
-                                  int Wo);
+                                  float *rout, float *pout, float *cout, float *dout, int N,
+                                  int C, int H, int W, int F, int HH, int WW, int sh, int sw,
+                                  int ph, int pw, int Ho, int Wo);
 int tt_k_conv2d_dw_lds(const float *g, const float *x, float *dw, float *db,
                        int N, int C, int H, int W, int F, int HH, int WW,
                        int sh, int sw, int ph, int pw, int Ho, int Wo);

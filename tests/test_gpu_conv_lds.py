@@ -343,8 +343,10 @@ def test_conv_relu_pool_fused_kernel_bitexact(tlib, case):
     dx_, dw_, db_ = DevBuf.from_np(x), DevBuf.from_np(w), DevBuf.from_np(b)
     o1, r1, p1 = DevBuf(n_out), DevBuf(n_out), DevBuf(n_pool)
     o2, r2, p2 = DevBuf(n_out), DevBuf(n_out), DevBuf(n_pool)
+    K1 = F * (Ho // 2) * (Wo // 2)
+    c1, d1 = DevBuf(n_pool), DevBuf(N * (K1 + 1))
     check(tlib.tt_k_conv2d_relu_pool_fwd_lds(dx_.ptr, dw_.ptr, db_.ptr, o1.ptr, r1.ptr, p1.ptr,
-                                             *geo), "fused")
+                                             c1.ptr, d1.ptr, *geo), "fused")
     check(tlib.tt_k_conv2d_relu_fwd_lds(dx_.ptr, dw_.ptr, db_.ptr, o2.ptr, r2.ptr, *geo), "conv")
     check(tlib.tt_k_maxpool_fwd(r2.ptr, p2.ptr, N, F, Ho, Wo, 2, 2, 2, 2, Ho // 2, Wo // 2), "pool")
     shp, pshp = (N, F, Ho, Wo), (N, F, Ho // 2, Wo // 2)
@@ -353,6 +355,9 @@ def test_conv_relu_pool_fused_kernel_bitexact(tlib, case):
     pool = p1.to_np(pshp)
     assert _bits_equal(pool, p2.to_np(pshp))
     assert _bits_equal(pool, orc.maxpool_fwd(r1.to_np(shp), 2, 2, 2, 2))
+    flat = pool.reshape(N, K1)
+    assert _bits_equal(c1.to_np((N, K1)), flat)
+    assert _bits_equal(d1.to_np((N, K1 + 1)), orc.padones_fwd(flat))
 
 
 @pytest.mark.parametrize("case", [(2, 3, 24, 24, 4, 3, 3, 1, 1, 1, 1),   # 32 % Wo != 0
@@ -365,7 +370,7 @@ def test_conv_relu_pool_fused_rejects(tlib, case):
     dx_, dw_ = DevBuf.from_np(x), DevBuf.from_np(w)
     o, r, p = DevBuf(N * F * Ho * Wo), DevBuf(N * F * Ho * Wo), DevBuf(N * F * Ho * Wo)
     assert tlib.tt_k_conv2d_relu_pool_fwd_lds(dx_.ptr, dw_.ptr, None, o.ptr, r.ptr, p.ptr,
-                                              *geo) == -1
+                                              None, None, *geo) == -1
 
 
 @pytest.mark.parametrize("case", [POOL_CASES[3], POOL_CASES[5], (2, 3, 24, 24, 4, 3, 3, 1, 1, 1, 1)])
@@ -406,3 +411,52 @@ def test_autograd_conv_relu_pool_deferred(tlib, case):
         got = run(mode)
         for a, e in zip(got, ref):
             assert _bits_equal(a, e), mode
+
+
+@pytest.mark.parametrize("mode", ["fused", "peek_pool", "reshape3d", "no_padones"])
+def test_autograd_conv_pool_flatten_deferred(tlib, mode):
+    """The classifier's input chain conv -> relu -> 2x2 pool -> reshape ->
+    padones (config 4's second convolution) as one launch, against the same
+    graph with every launch made at once: values and gradients bit for bit
+    equal.  Reading the pool first, a reshape that is not a flattening to 2-D,
+    or a reshape not followed by a padones run the pending chain without the
+    later steps."""
+    from tinytorch_amd.torch_py import Node
+    case = (16, 32, 16, 16, 64, 3, 3, 1, 1, 1, 1)
+    x, w, b, _, geo = _inputs(case)
+    N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo = geo
+    K1 = F * (Ho // 2) * (Wo // 2)
+    print("deferred conv pool flatten", mode, flush=True)
+
+    def run():
+        X, Wn, Bn = Node.leaf(x), Node.leaf(w), Node.leaf(b)
+        m = X.conv2d(Wn, Bn, (sh, sw), (ph, pw)).relu().maxpool2d(2, 2)
+        if mode == "peek_pool":
+            m.value()
+        nodes = [m]
+        shape = (N, F, 1, K1 // F) if mode == "reshape3d" else (N, K1)
+        rs = m.reshape(shape)
+        nodes.append(rs)
+        if mode == "reshape3d":
+            rs = rs.reshape((N, K1))
+            nodes.append(rs)
+        top = rs
+        if mode != "no_padones":
+            top = rs.padones()
+            nodes.append(top)
+        v = top.value()
+        gt = np.ascontiguousarray(np.sin(np.arange(v.size, dtype=np.float32)).reshape(v.shape))
+        top.backward(gt)
+        out = [v, m.value(), X.grad(), Wn.grad(), Bn.grad()]
+        for nd in nodes[::-1] + [X, Wn, Bn]:
+            nd.release()
+        return out
+
+    prev = tlib.tth_conv_relu_fuse(0)
+    try:
+        ref = run()
+    finally:
+        tlib.tth_conv_relu_fuse(prev)
+    got = run()
+    for a, e in zip(got, ref):
+        assert _bits_equal(a, e), mode

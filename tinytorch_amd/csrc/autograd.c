@@ -265,6 +265,23 @@ AGNode *ag_padones(AGNode *a) {
     if (!a || a->val->ndim != 2) return NULL;
     const long M = a->val->shape[0], K = a->val->shape[1];
     const long shp[2] = {M, K + 1};
+    if (tt_pend.active == TT_PEND_CONV_RELU_POOL_COPY && tt_pend.c == a->val) {
+        /* convolution, relu, pool, flattening copy and this padones in one
+         * launch */
+        Tensor *v = tt_empty_dev(shp, 2);
+        if (v) {
+            const TTPendConv p = tt_pend;
+            const int *q = p.geo;
+            tt_pend.active = 0;
+            if (tt_k_conv2d_relu_pool_fwd_lds(p.x, p.w, p.b, p.out->dev, p.r->dev, p.p->dev,
+                                              p.c->dev, v->dev, q[0], q[1], q[2], q[3], q[4],
+                                              q[5], q[6], q[7], q[8], q[9], q[10], q[11],
+                                              q[12]) == 0)
+                return make_node(v, &OP_PADONES, a, NULL, NULL);
+            tt_pend = p;  /* not launched: the chain runs below, then the padones */
+            tt_release(v);
+        }
+    }
     if (tt_pend.active == TT_PEND_COPY && tt_pend.out == a->val) {
         /* a is a reshape whose copy is still pending: one pass writes the
          * copy and the padded tensor */
@@ -312,6 +329,19 @@ AGNode *ag_padones(AGNode *a) {
 
 AGNode *ag_reshape(AGNode *a, const long *new_shape, int new_ndim) {
     if (!a) return NULL;
+    if (tt_pend.active == TT_PEND_CONV_RELU_POOL && tt_pend.p == a->val && new_shape &&
+        new_ndim == 2 && new_shape[0] == a->val->shape[0] &&
+        new_shape[0] > 0 && new_shape[1] == a->val->numel / new_shape[0] &&
+        new_shape[0] * new_shape[1] == a->val->numel) {
+        /* a flattening reshape of a pending pool output: its copy waits too */
+        Tensor *v = tt_empty_dev(new_shape, 2);
+        if (!v) return NULL;
+        AGNode *n = make_node(v, &OP_RESHAPE, a, NULL, NULL);
+        if (!n) return NULL;
+        tt_pend.c = v;
+        tt_pend.active = TT_PEND_CONV_RELU_POOL_COPY;
+        return n;
+    }
     Tensor *v = tt_reshape_ex(a->val, new_shape, new_ndim, 1);
     if (!v) return NULL;
     AGNode *n = make_node(v, &OP_RESHAPE, a, NULL, NULL);
@@ -353,21 +383,18 @@ AGNode *ag_maxpool2d(AGNode *a, int ph, int pw, int sh, int sw) {
     if (tt_pend.active == TT_PEND_CONV_RELU && tt_pend.r == a->val && ph == 2 && pw == 2 &&
         sh == 2 && sw == 2 && a->val->ndim == 4 && a->val->shape[2] % 2 == 0 &&
         a->val->shape[3] % 2 == 0) {
-        /* convolution, relu and this pool in one launch */
+        /* the convolution and relu producing a are still pending: this pool
+         * waits with them (one launch writes all three, and a flattening
+         * reshape + padones of the pool's output can join it) */
         const long shp[4] = {a->val->shape[0], a->val->shape[1], a->val->shape[2] / 2,
                              a->val->shape[3] / 2};
         Tensor *v = tt_empty_dev(shp, 4);
-        if (v) {
-            const TTPendConv p = tt_pend;
-            const int *q = p.geo;
-            tt_pend.active = 0;
-            if (tt_k_conv2d_relu_pool_fwd_lds(p.x, p.w, p.b, p.out->dev, p.r->dev, v->dev, q[0],
-                                              q[1], q[2], q[3], q[4], q[5], q[6], q[7], q[8],
-                                              q[9], q[10], q[11], q[12]) == 0)
-                return pool_node(a, v, &OP_MAXPOOL2D, ph, pw, sh, sw);
-            tt_pend = p;  /* not launched: convolution + relu, then the pool below */
-            tt_release(v);
-        }
+        if (!v) return NULL;
+        AGNode *n = pool_node(a, v, &OP_MAXPOOL2D, ph, pw, sh, sw);
+        if (!n) return NULL;
+        tt_pend.p = v;
+        tt_pend.active = TT_PEND_CONV_RELU_POOL;
+        return n;
     }
     Tensor *v = tt_maxpool2d(a->val, ph, pw, sh, sw);
     if (!v) return NULL;

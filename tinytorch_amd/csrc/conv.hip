@@ -264,7 +264,8 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2)))
 conv_fwd_lds_kernel(const float *__restrict__ x, const float *__restrict__ w,
                     const float *__restrict__ bias, float *__restrict__ out,
                     float *__restrict__ rout, float *__restrict__ /*pout: 3x3 kernel only*/,
-                    Geo g, int chunks) {
+                    float *__restrict__ /*cout*/, float *__restrict__ /*dout*/, Geo g,
+                    int chunks) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   constexpr int CHUNK = 128 * PB;
   const int n = blockIdx.x / chunks, chunk = blockIdx.x - n * chunks;
@@ -410,7 +411,8 @@ template <int PB, bool FLIP, bool VEC, int KH, int KW, int KS = 1>
 __global__ void __launch_bounds__(NT * KS) __attribute__((amdgpu_waves_per_eu(1, 2)))
 conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
                   const float *__restrict__ bias, float *__restrict__ out,
-                  float *__restrict__ rout, float *__restrict__ pout, Geo g, int chunks) {
+                  float *__restrict__ rout, float *__restrict__ pout, float *__restrict__ cout,
+                  float *__restrict__ dout, Geo g, int chunks) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   constexpr int CHUNK = 128 * PB, TAPS = KH * KW;
   const int n = blockIdx.x / chunks, chunk = blockIdx.x - n * chunks;
@@ -645,7 +647,10 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
     // (32 % Wo == 0, 32 / Wo even) or two consecutive blocks (Wo == 32, PB
     // even)).  The relu values are >= +0 and never NaN, so their max does
     // not depend on the order of the comparisons: the pool's output bit for
-    // bit.  Every lane takes part in the shuffles; stores are masked.
+    // bit.  Every lane takes part in the shuffles; stores are masked.  cout /
+    // dout (optional): the pool output once more (a flattening reshape's copy,
+    // the same layout) and padded -- rows of F*Ho*Wo/4 + 1 floats per image,
+    // the last one 1 (a padones after the reshape).
     float o[PB][16];
 #pragma unroll
     for (int j = 0; j < PB; j++) {
@@ -663,6 +668,15 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
     }
     const int P4 = P >> 2, Wo2 = g.Wo >> 1;
     float *pn = pout + (long)n * g.F * P4;
+    float *cn = cout ? cout + (long)n * g.F * P4 : nullptr;
+    const long drow = (long)g.F * P4 + 1;
+    float *dn = dout ? dout + (long)n * drow : nullptr;
+    if (dn && blockIdx.y == 0 && chunk == 0 && tid == 0) dn[drow - 1] = 1.0f;
+    auto put = [&](long o, float m) {
+      pn[o] = m;
+      if (cn) cn[o] = m;
+      if (dn) dn[o] = m;
+    };
     if (g.Wo == 32) {  // rows 2i, 2i+1 are blocks j, j+1
 #pragma unroll
       for (int j = 0; j + 1 < PB; j += 2) {
@@ -674,7 +688,7 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
           const float m0 = fmaxf(o[j][r], o[j + 1][r]);
           const float m = fmaxf(m0, __shfl_xor(m0, 1, 64));
           const int f = f0 + 8 * (r >> 2) + 4 * half + (r & 3);
-          if (lead && f < g.F) pn[(long)f * P4 + prow * Wo2 + (l32 >> 1)] = m;
+          if (lead && f < g.F) put((long)f * P4 + prow * Wo2 + (l32 >> 1), m);
         }
       }
     } else {  // rows 2i, 2i+1 are lanes l and l ^ Wo of one block
@@ -688,7 +702,7 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
           const float m0 = fmaxf(o[j][r], __shfl_xor(o[j][r], 1, 64));
           const float m = fmaxf(m0, __shfl_xor(m0, g.Wo, 64));
           const int f = f0 + 8 * (r >> 2) + 4 * half + (r & 3);
-          if (lead && f < g.F) pn[(long)f * P4 + (row >> 1) * Wo2 + (col >> 1)] = m;
+          if (lead && f < g.F) put((long)f * P4 + (row >> 1) * Wo2 + (col >> 1), m);
         }
       }
     }
@@ -1460,23 +1474,25 @@ bool pool_fusable(const Geo &g, const FwdPlan &pl) {
 
 template <int PB, bool FLIP, bool VEC>
 int launch_fwd(const float *x, const float *w, const float *bias, float *out, float *rout,
-               float *pout, const Geo &g, int N, const FwdPlan &pl) {
+               float *pout, float *cout, float *dout, const Geo &g, int N, const FwdPlan &pl) {
   auto kern = !is_k3(g)     ? conv_fwd_lds_kernel<PB, FLIP, VEC>
               : pl.ks == 2 ? conv_fwd_k_kernel<PB, FLIP, VEC, 3, 3, 2>
                            : conv_fwd_k_kernel<PB, FLIP, VEC, 3, 3, 1>;
   if (pl.lds > 64 * 1024 && !allow_big_lds((const void *)kern)) return -1;
   const dim3 grid((unsigned)(N * pl.chunks), (unsigned)((g.F + 31) / 32));
   hipLaunchKernelGGL(kern, grid, dim3(NT * pl.ks), pl.lds, stream(), x, w, bias, out, rout, pout,
-                     g, pl.chunks);
+                     cout, dout, g, pl.chunks);
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
 template <bool FLIP>
 int run_fwd(const float *x, const float *w, const float *bias, float *out, const Geo &g, int N,
-            bool dry, float *rout = nullptr, float *pout = nullptr) {
+            bool dry, float *rout = nullptr, float *pout = nullptr, float *cout = nullptr,
+            float *dout = nullptr) {
   const FwdPlan pl = plan_fwd(g, N, FLIP);
   if (!pl.pb) return -1;
   if (pout && !(rout && !FLIP && pool_fusable(g, pl))) return -1;
+  if ((cout || dout) && !pout) return -1;
   if (dry) return 0;
   if (fail_direct()) return -3;
   // 16-byte loads: 4-aligned rows of x and of the weight blocks (the 3x3
@@ -1490,10 +1506,10 @@ int run_fwd(const float *x, const float *w, const float *bias, float *out, const
                                    : g.K % 4 == 0);
   const bool vec = g.W % 4 == 0 && aligned16(x) && wok;
   if (pl.pb == 2)
-    return vec ? launch_fwd<2, FLIP, true>(x, w, bias, out, rout, pout, g, N, pl)
-               : launch_fwd<2, FLIP, false>(x, w, bias, out, rout, pout, g, N, pl);
-  return vec ? launch_fwd<1, FLIP, true>(x, w, bias, out, rout, pout, g, N, pl)
-             : launch_fwd<1, FLIP, false>(x, w, bias, out, rout, pout, g, N, pl);
+    return vec ? launch_fwd<2, FLIP, true>(x, w, bias, out, rout, pout, cout, dout, g, N, pl)
+               : launch_fwd<2, FLIP, false>(x, w, bias, out, rout, pout, cout, dout, g, N, pl);
+  return vec ? launch_fwd<1, FLIP, true>(x, w, bias, out, rout, pout, cout, dout, g, N, pl)
+             : launch_fwd<1, FLIP, false>(x, w, bias, out, rout, pout, cout, dout, g, N, pl);
 }
 
 // dW kernel variants: (MF, JW, KS) with FS = filters/16 per workgroup.
@@ -1819,17 +1835,20 @@ extern "C" int tt_k_conv2d_relu_fwd_lds(const float *x, const float *w, const fl
 
 // The same convolution with its relu and the 2x2 / stride-2 max pool of the
 // relu: out, rout as above and pout (N x F x Ho/2 x Wo/2) in one launch
-// (bit-identical to tt_k_conv2d_relu_fwd_lds followed by the max pool).
+// (bit-identical to tt_k_conv2d_relu_fwd_lds followed by the max pool);
+// cout / dout (optional): the pool output flattened per image, as a copy and
+// padded with a last column of ones (a reshape and a padones after it).
 // -1: not covered (see pool_fusable).
 extern "C" int tt_k_conv2d_relu_pool_fwd_lds(const float *x, const float *w, const float *bias,
-                                             float *out, float *rout, float *pout, int N, int C,
-                                             int H, int W, int F, int HH, int WW, int sh, int sw,
-                                             int ph, int pw, int Ho, int Wo) {
+                                             float *out, float *rout, float *pout, float *cout,
+                                             float *dout, int N, int C, int H, int W, int F,
+                                             int HH, int WW, int sh, int sw, int ph, int pw,
+                                             int Ho, int Wo) {
   if (!x || !w || !out || !rout || !pout || out == rout ||
       !geo_ok(N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo))
     return -1;
   const Geo g{C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo, F, C * HH * WW};
-  return run_fwd<false>(x, w, bias, out, g, N, false, rout, pout);
+  return run_fwd<false>(x, w, bias, out, g, N, false, rout, pout, cout, dout);
 }
 
 // dw (F, C*HH*WW) and, when db is given, db (F) from the output gradient g

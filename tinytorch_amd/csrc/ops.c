@@ -254,16 +254,35 @@ int tt_flush_pending(void) {
             if (rc == 0) rc = tt_k_relu_fwd(tt_pend.out->dev, tt_pend.r->dev, tt_pend.r->numel);
             if (rc != 0) tt_pend.r->valid = 0;
         }
-    } else if (kind == TT_PEND_CONV_RELU) {
+    } else if (kind == TT_PEND_CONV_RELU || kind == TT_PEND_CONV_RELU_POOL ||
+               kind == TT_PEND_CONV_RELU_POOL_COPY) {
         const int *q = tt_pend.geo;
-        rc = tt_k_conv2d_relu_fwd_lds(tt_pend.x, tt_pend.w, tt_pend.b, tt_pend.out->dev,
-                                      tt_pend.r->dev, q[0], q[1], q[2], q[3], q[4], q[5], q[6],
-                                      q[7], q[8], q[9], q[10], q[11], q[12]);
-        if (rc != 0) {
-            rc = conv_fwd_gemm(tt_pend.x, tt_pend.w, tt_pend.b, tt_pend.out->dev, q);
-            if (rc == 0) rc = tt_k_relu_fwd(tt_pend.out->dev, tt_pend.r->dev, tt_pend.r->numel);
+        Tensor *p = kind != TT_PEND_CONV_RELU ? tt_pend.p : NULL;
+        Tensor *c = kind == TT_PEND_CONV_RELU_POOL_COPY ? tt_pend.c : NULL;
+        rc = p ? tt_k_conv2d_relu_pool_fwd_lds(tt_pend.x, tt_pend.w, tt_pend.b, tt_pend.out->dev,
+                                               tt_pend.r->dev, p->dev, c ? c->dev : NULL, NULL,
+                                               q[0], q[1], q[2], q[3], q[4], q[5], q[6], q[7],
+                                               q[8], q[9], q[10], q[11], q[12])
+               : -1;
+        if (rc != 0) {  /* the convolution + relu, then the pool and the copy by themselves */
+            rc = tt_k_conv2d_relu_fwd_lds(tt_pend.x, tt_pend.w, tt_pend.b, tt_pend.out->dev,
+                                          tt_pend.r->dev, q[0], q[1], q[2], q[3], q[4], q[5],
+                                          q[6], q[7], q[8], q[9], q[10], q[11], q[12]);
+            if (rc != 0) {
+                rc = conv_fwd_gemm(tt_pend.x, tt_pend.w, tt_pend.b, tt_pend.out->dev, q);
+                if (rc == 0)
+                    rc = tt_k_relu_fwd(tt_pend.out->dev, tt_pend.r->dev, tt_pend.r->numel);
+            }
+            if (rc == 0 && p)
+                rc = tt_k_maxpool_fwd(tt_pend.r->dev, p->dev, q[0], q[4], q[11], q[12], 2, 2, 2,
+                                      2, q[11] / 2, q[12] / 2);
+            if (rc == 0 && c) rc = tt_k_copy(c->dev, p->dev, c->numel);
         }
-        if (rc != 0) tt_pend.r->valid = 0;
+        if (rc != 0) {
+            tt_pend.r->valid = 0;
+            if (p) p->valid = 0;
+            if (c) c->valid = 0;
+        }
     } else {
         const int *q = tt_pend.geo;
         rc = tt_k_conv2d_fwd_lds(tt_pend.x, tt_pend.w, tt_pend.b, tt_pend.out->dev, q[0], q[1],

@@ -36,11 +36,14 @@ Tensor *tt_conv2d_keepcol(const Tensor *a, const Tensor *w, const Tensor *b,
 #define TT_PEND_RELU 3        /* ag_relu; ag_padones of it fuses */
 #define TT_PEND_MATMUL 4      /* ag_matmul (x * w); ag_relu of it waits with it */
 #define TT_PEND_MATMUL_RELU 5 /* ag_matmul and ag_relu of it (r); ag_padones of r fuses */
-#define TT_PEND_CONV_RELU 6   /* ag_conv2d and ag_relu of it (r); a 2x2 ag_maxpool2d of r fuses */
+#define TT_PEND_CONV_RELU 6   /* ag_conv2d and ag_relu of it (r); a 2x2 ag_maxpool2d of r waits too */
+#define TT_PEND_CONV_RELU_POOL 7  /* ... and the 2x2 max pool of r (p); ag_reshape of p waits too */
+#define TT_PEND_CONV_RELU_POOL_COPY 8  /* ... and that reshape's copy (c); ag_padones of c fuses */
 typedef struct {
     int active;               /* 0 or one of TT_PEND_* */
     Tensor *out;              /* the pending output (owned by its node) */
-    Tensor *r;                /* *_RELU kinds: the relu output (owned by its node) */
+    Tensor *r;                /* *_RELU* kinds: the relu output (owned by its node) */
+    Tensor *p, *c;            /* the pool output, the reshape's copy (owned by their nodes) */
     const float *x, *w, *b;   /* device operands, retained by the node's parents */
     int geo[13];              /* conv: N C H W F HH WW sh sw ph pw Ho Wo; matmul: M N K */
 } TTPendConv;
