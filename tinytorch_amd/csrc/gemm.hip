@@ -1557,6 +1557,18 @@ __device__ __forceinline__ void small_tile(int M, int N, int K, const float *__r
   const int n = n0 + l32;
   if (n >= N) return;
   const bool pad = out.d1 || out.d2;
+  // the relu outputs of this lane's 16 elements, loaded up front and
+  // unconditionally (clamped to the matrix): a load under the store's
+  // branches would wait for its own round trip
+  float rv[16];
+  if (out.R) {
+    const int nc = n < N - 1 ? n : (N > 1 ? N - 2 : 0);
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int m = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
+      rv[r] = out.R[(long)(m < M ? m : M - 1) * (N - 1) + nc];
+    }
+  }
 #pragma unroll
   for (int r = 0; r < 16; r++) {
     const int m = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
@@ -1565,7 +1577,7 @@ __device__ __forceinline__ void small_tile(int M, int N, int K, const float *__r
       if (pad && n < N - 1) {
         const long o = (long)m * (N - 1) + n;
         if (out.d1) out.d1[o] = acc[r];
-        if (out.d2) out.d2[o] = out.R ? (out.R[o] > 0.0f ? acc[r] : 0.0f) : acc[r];
+        if (out.d2) out.d2[o] = out.R ? (rv[r] > 0.0f ? acc[r] : 0.0f) : acc[r];
       }
     }
   }
