@@ -1188,8 +1188,9 @@ conv_dwt_kernel(const float *__restrict__ gr, const float *__restrict__ x,
   // items (row, quad): rows pq, pq+4, ... of the unit; lane half h takes
   // the pixels [h*Wo/2, h*Wo/2 + Wo/2) of a row, four at a time: one 16-byte
   // read of g (rows of GS = 4 mod 32 floats: eight lanes of a read cover the
-  // 32 banks) feeds four MFMA steps.  The next item's operands are read
-  // before the current item's MFMAs.
+  // 32 banks) feeds four MFMA steps.  Two operand sets in turn: the next
+  // item's operands are read into one while the current item's MFMAs use
+  // the other (no register copies in the loop).
   const int half_w = g.Wo >> 1;
   const int quads = half_w >> 2;
   const int xh = h * half_w * g.sw;
@@ -1200,56 +1201,51 @@ conv_dwt_kernel(const float *__restrict__ gr, const float *__restrict__ x,
   const float *ga = gs + l32 * GS + h * half_w;
   {
     int go = pq * g.Wo, xo = pq * g.sh * RW + xh;  // item offsets into g and the slab
-    int qd = 0;
-    f32x4 a4 = {0.0f, 0.0f, 0.0f, 0.0f};
-    float bv[4][TG];
-#pragma unroll
-    for (int e = 0; e < 4; e++)
-#pragma unroll
-      for (int jw = 0; jw < TG; jw++) bv[e][jw] = 0.0f;
-    if (nit > 0) {
+    int qd = 0, left = nit;
+    // step to the next item (the last item stays put, so a read past the
+    // end re-reads it)
+    auto advance = [&]() {
+      if (--left <= 0) return;
+      if (++qd == quads) {
+        qd = 0;
+        go += gstep + 4;
+        xo += xstep + 4 * g.sw;
+      } else {
+        go += 4;
+        xo += 4 * g.sw;
+      }
+    };
+    auto load = [&](f32x4 &a4, float (&bv)[4][TG]) {
       a4 = *(const f32x4 *)(ga + go);
 #pragma unroll
       for (int e = 0; e < 4; e++)
 #pragma unroll
         for (int jw = 0; jw < TG; jw++) bv[e][jw] = xs[bb[jw] + xo + e * g.sw];
-    }
-#pragma unroll 1
-    for (int it = 0; it < nit; it++) {
-      // advance to the next item (the last item re-reads itself)
-      if (it + 1 < nit) {
-        if (++qd == quads) {
-          qd = 0;
-          go += gstep + 4;
-          xo += xstep + 4 * g.sw;
-        } else {
-          go += 4;
-          xo += 4 * g.sw;
-        }
-      }
-      // this item's operands were consumed by the previous iteration's
-      // copies: with no LDS read in flight here, the reads below are the
-      // only ones outstanding while the MFMAs issue
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-      const f32x4 a4n = *(const f32x4 *)(ga + go);
-      float bn[4][TG];
-#pragma unroll
-      for (int e = 0; e < 4; e++)
-#pragma unroll
-        for (int jw = 0; jw < TG; jw++) bn[e][jw] = xs[bb[jw] + xo + e * g.sw];
-      __builtin_amdgcn_sched_barrier(0);
+    };
+    auto mfmas = [&](const f32x4 &a4, const float (&bv)[4][TG]) {
 #pragma unroll
       for (int e = 0; e < 4; e++)
 #pragma unroll
         for (int jw = 0; jw < TG; jw++)
           acc[jw] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[e], bv[e][jw], acc[jw], 0, 0, 0);
       bsum += (a4[0] + a4[1]) + (a4[2] + a4[3]);
+    };
+    f32x4 a0, a1;
+    float b0[4][TG], b1[4][TG];
+    if (nit > 0) load(a0, b0);
+#pragma unroll 1
+    for (int it = 0; it < nit; it += 2) {
+      advance();
+      load(a1, b1);  // item it+1 (or it again)
       __builtin_amdgcn_sched_barrier(0);
-      a4 = a4n;
-#pragma unroll
-      for (int e = 0; e < 4; e++)
-#pragma unroll
-        for (int jw = 0; jw < TG; jw++) bv[e][jw] = bn[e][jw];
+      mfmas(a0, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (it + 1 >= nit) break;
+      advance();
+      load(a0, b0);  // item it+2
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(a1, b1);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   bsum += __shfl_xor(bsum, 32, 64);  // both halves of filter l32
