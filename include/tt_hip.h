@@ -179,6 +179,14 @@ int tt_k_relu_padones_fwd(const float *x, float *r, float *y, long M, long K);
  * bit for bit, written by the GEMM's split-K reduction when it has one. */
 int tt_k_gemm_relu_pad(int M, int N, int K, const float *A, const float *B, float *C, float *R,
                        float *P);
+/* C = A * B + bias (A M x K, B K x N row-major, contiguous; bias a row of N
+ * added to every row of C), and when R, P are given R = relu(C),
+ * P = [R, 1]: ag_matmul of a padones output (src/autograd.c:168-171,
+ * 195-212) computed from the padones input X and the weights W, as
+ * X * W[:K] + W[K] -- the same sum as the padded product, not the same
+ * rounding order.  R and P both or neither. */
+int tt_k_gemm_bias_relu_pad(int M, int N, int K, const float *A, const float *B,
+                            const float *bias, float *C, float *R, float *P);
 /* padones backward (src/autograd.c:348-359) written to two buffers: d1 and
  * d2 both get g without its last column; the backward pass uses it when the
  * padded tensor is a reshape (src/autograd.c:361-369, a copy of the

@@ -124,3 +124,30 @@ def test_matmul_bwd_small_shapes_taken(tlib):
     w = DevBuf(513 * 256)
     assert tlib.tt_k_matmul_bwd_small(d.ptr, 256, 513, w.ptr, 256, g.ptr, DevBuf(513 * 256).ptr,
                                       DevBuf(256 * 513).ptr, None, None, None) == 0
+
+
+BIAS_SHAPES = [(256, 784, 512), (256, 512, 256), (256, 256, 10), (128, 4096, 10), (7, 9, 5),
+               (300, 1000, 96), (64, 3, 40)]
+
+
+@pytest.mark.parametrize("M,K,N", BIAS_SHAPES)
+@pytest.mark.parametrize("epi", [False, True])
+def test_gemm_bias_relu_pad_vs_padded_product(tlib, M, K, N, epi):
+    """tt_k_gemm_bias_relu_pad (X * W[:K] + W[K], the matmul of a padones
+    output from the padones input): C within the GEMM bar of the oracle's
+    product of the padded matrix, and R / P exactly relu(C) / [relu(C), 1]."""
+    X = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    W = (rng.standard_normal((K + 1, N)) / np.sqrt(K)).astype(np.float32)
+    dX, dW = DevBuf.from_np(X), DevBuf.from_np(W)
+    bias_ptr = dW.ptr + 4 * K * N
+    C, R, P = DevBuf(M * N), DevBuf(M * N), DevBuf(M * (N + 1))
+    print("gemm_bias_relu_pad", M, K, N, epi, flush=True)
+    check(tlib.tt_k_gemm_bias_relu_pad(M, N, K, dX.ptr, dW.ptr, bias_ptr, C.ptr,
+                                       R.ptr if epi else None, P.ptr if epi else None), "bias")
+    c = C.to_np((M, N))
+    ref = orc.sgemm(orc.padones_fwd(X), W)
+    amax = max(1.0, float(np.abs(W).max()))
+    assert np.abs(c - ref).max() / (np.sqrt(K + 1) * amax) <= 1e-4
+    if epi:
+        assert bits_equal(R.to_np((M, N)), orc.relu_fwd(c))
+        assert bits_equal(P.to_np((M, N + 1)), orc.padones_fwd(orc.relu_fwd(c)))

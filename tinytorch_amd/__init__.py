@@ -138,6 +138,7 @@ SIGNATURES = [
     ("tt_k_copy_padones_fwd", _I, [VP, VP, VP, _L, _L]),
     ("tt_k_relu_padones_fwd", _I, [VP, VP, VP, _L, _L]),
     ("tt_k_gemm_relu_pad", _I, [_I, _I, _I, VP, VP, VP, VP, VP]),
+    ("tt_k_gemm_bias_relu_pad", _I, [_I, _I, _I, VP, VP, VP, VP, VP, VP]),
     ("tt_k_padones_bwd2", _I, [VP, VP, VP, _L, _L]),
     ("tt_k_padones_bwd", _I, [VP, VP, _L, _L]),
     ("tt_k_padones_relu_bwd", _I, [VP, VP, VP, VP, _L, _L]),

@@ -185,30 +185,53 @@ AGNode *ag_mulscalar(AGNode *a, float s) {
  * classifier layer) runs as one launch of tt_k_head_bwd. */
 #define HEAD_MAX_N 32
 
+/* The input of a padones node, when a is one: a matmul of a padones output
+ * [X, 1] * W is X * W[:K-1] + W[K-1] (the weights' last row added to every
+ * row), computed from X's aligned rows without reading the ones column. */
+static const Tensor *padones_input(const AGNode *a) {
+    if (a->op != &OP_PADONES || !a->in[0]) return NULL;
+    const Tensor *x = a->in[0]->val;
+    return x && x->ndim == 2 && x->shape[1] >= 1 && a->val->shape[1] == x->shape[1] + 1 ? x
+                                                                                       : NULL;
+}
+
 AGNode *ag_matmul(AGNode *a, AGNode *b) {
     if (!a || !b) return NULL;
     const Tensor *av = a->val, *bv = b->val;
-    if (tt_defer_enabled() && av->ndim == 2 && bv->ndim == 2 && av->shape[1] == bv->shape[0] &&
-        av->shape[0] > 0 && av->shape[1] > 0 && bv->shape[1] > 0 &&
-        av->shape[0] <= 0x7fffffffL && av->shape[1] <= 0x7fffffffL &&
-        bv->shape[1] <= 0x7fffffffL) {
-        /* left pending: a relu + padones of the product is then computed
-         * by the GEMM's own reduction pass */
-        const float *x = tt_dev(a->val), *y = tt_dev(b->val);
+    if (av->ndim == 2 && bv->ndim == 2 && av->shape[1] == bv->shape[0] && av->shape[0] > 0 &&
+        av->shape[1] > 0 && bv->shape[1] > 0 && av->shape[0] <= 0x7fffffffL &&
+        av->shape[1] <= 0x7fffffffL && bv->shape[1] <= 0x7fffffffL) {
+        const Tensor *xv = padones_input(a);
+        const int M = (int)av->shape[0], N = (int)bv->shape[1], K = (int)av->shape[1];
+        const float *x = tt_dev((Tensor *)(xv ? xv : av)), *y = tt_dev(b->val);
         if (!x || !y) return NULL;
-        const long shp[2] = {av->shape[0], bv->shape[1]};
+        const float *bias = xv ? y + (long)(K - 1) * N : NULL;
+        const int Kx = xv ? K - 1 : K;
+        const long shp[2] = {M, N};
         Tensor *out = tt_empty_dev(shp, 2);
         if (!out) return NULL;
         AGNode *n = make_node(out, &OP_MATMUL, a, b, NULL);
         if (!n) return NULL;
-        tt_pend.out = out;
-        tt_pend.r = NULL;
-        tt_pend.x = x;
-        tt_pend.w = y;
-        tt_pend.geo[0] = (int)av->shape[0];
-        tt_pend.geo[1] = (int)bv->shape[1];
-        tt_pend.geo[2] = (int)av->shape[1];
-        tt_pend.active = TT_PEND_MATMUL;
+        if (tt_defer_enabled()) {
+            /* left pending: a relu + padones of the product is then computed
+             * by the GEMM's own epilogue */
+            tt_pend.out = out;
+            tt_pend.r = NULL;
+            tt_pend.x = x;
+            tt_pend.w = y;
+            tt_pend.b = bias;
+            tt_pend.geo[0] = M;
+            tt_pend.geo[1] = N;
+            tt_pend.geo[2] = Kx;
+            tt_pend.active = TT_PEND_MATMUL;
+            return n;
+        }
+        const int rc = bias ? tt_k_gemm_bias_relu_pad(M, N, Kx, x, y, bias, out->dev, NULL, NULL)
+                            : tt_k_gemm(M, N, K, x, K, 0, y, N, 0, out->dev, N);
+        if (rc != 0) {
+            ag_release(n);
+            return NULL;
+        }
         return n;
     }
     return make_node(tt_matmul_omp(a->val, b->val, 0), &OP_MATMUL, a, b, NULL);
@@ -301,8 +324,10 @@ AGNode *ag_padones(AGNode *a) {
         if (v) {
             const TTPendConv p = tt_pend;
             tt_pend.active = 0;
-            if (tt_k_gemm_relu_pad(p.geo[0], p.geo[1], p.geo[2], p.x, p.w, p.out->dev,
-                                   p.r->dev, v->dev) == 0)
+            if ((p.b ? tt_k_gemm_bias_relu_pad(p.geo[0], p.geo[1], p.geo[2], p.x, p.w, p.b,
+                                               p.out->dev, p.r->dev, v->dev)
+                     : tt_k_gemm_relu_pad(p.geo[0], p.geo[1], p.geo[2], p.x, p.w, p.out->dev,
+                                          p.r->dev, v->dev)) == 0)
                 return make_node(v, &OP_PADONES, a, NULL, NULL);
             tt_pend = p;  /* not launched: the plain matmul and relu run below */
             tt_release(v);

@@ -685,6 +685,34 @@ static void launch_ce_mean(const float *logits, const LAB &labels, float *probs,
                        labels, probs, loss_mean, seed, (int)rows, cols, scale);
 }
 
+// c[m][n] += bias[n]; r = relu(c), p = [r, 1] when given (a row per
+// blockIdx.y, 1024 columns per blockIdx.x)
+__global__ void bias_relu_pad_rows_kernel(float *__restrict__ c, const float *__restrict__ bias,
+                                          float *__restrict__ r, float *__restrict__ p, int N) {
+  const long m = blockIdx.y;
+  float *cr = c + m * N;
+  for (int k = blockIdx.x * 1024 + threadIdx.x; k <= N && k < (int)(blockIdx.x + 1) * 1024;
+       k += 256) {
+    if (k < N) {
+      const float v = cr[k] + bias[k];
+      cr[k] = v;
+      const float o = v > 0.0f ? v : 0.0f;
+      if (r) r[m * N + k] = o;
+      if (p) p[m * (N + 1) + k] = o;
+    } else if (p) {
+      p[m * (N + 1) + N] = 1.0f;
+    }
+  }
+}
+
+extern "C" int ttk_bias_relu_pad(float *c, const float *bias, float *r, float *p, int M, int N) {
+  if (M <= 0 || N <= 0) return 0;
+  if (M >= 65536) return -1;
+  hipLaunchKernelGGL(bias_relu_pad_rows_kernel, dim3((unsigned)((N + 1 + 1023) / 1024), (unsigned)M),
+                     dim3(256), 0, stream(), c, bias, r, p, N);
+  return launched();
+}
+
 int tt_k_softmax_ce_mean(const float *logits, const int32_t *labels, float *probs, float *loss_mean,
                          float *seed, long rows, int cols, float scale) {
   if (rows <= 0 || cols <= 0 || rows > TT_CE_MEAN_MAX_ROWS) return -1;

@@ -617,7 +617,8 @@ splitk_reduce_kernel(const float *__restrict__ ws, float *__restrict__ C, int M,
 // P = [R, 1] (M x (N+1)) as well as C, the values relu_padones_rows_kernel
 // writes from C.
 struct ReluPadEx {
-  float *r, *p;
+  float *r, *p;         // may be null (the bias-only form)
+  const float *bias;    // row added to every output row, or null
 };
 
 template <int ZL>
@@ -647,12 +648,15 @@ splitk_reduce_relu_pad_kernel(const float *__restrict__ ws, float *__restrict__ 
   const float s = reduce_one<ZL>(ws, S, total, idx, ty, part, tx);
   if (ty != 0 || idx >= total) return;
   const unsigned row = (unsigned)(idx / N), col = (unsigned)(idx - (long)row * N);
-  const float o = s > 0.0f ? s : 0.0f;
-  C[idx] = s;
-  ex.r[idx] = o;
-  float *pr = ex.p + (long)row * (N + 1);
-  pr[col] = o;
-  if ((int)col == N - 1) pr[N] = 1.0f;
+  const float v = ex.bias ? s + ex.bias[col] : s;
+  const float o = v > 0.0f ? v : 0.0f;
+  C[idx] = v;
+  if (ex.r) ex.r[idx] = o;
+  if (ex.p) {
+    float *pr = ex.p + (long)row * (N + 1);
+    pr[col] = o;
+    if ((int)col == N - 1) pr[N] = 1.0f;
+  }
 }
 
 // ---- 256x256 tile with direct global->LDS loads ----
@@ -1487,6 +1491,10 @@ struct SmallOut {
   long ldc;
   float *d1, *d2;
   const float *R;
+  // forward epilogue (C = A * B + bias row): bias[n] added to every row;
+  // relu = relu(C) and pad = [relu, 1] (M x (N+1)) when given
+  const float *bias = nullptr;
+  float *relu = nullptr, *pad = nullptr;
 };
 
 template <bool A_KC, bool B_NC, bool VA, bool VB>
@@ -1569,6 +1577,25 @@ __device__ __forceinline__ void small_tile(int M, int N, int K, const float *__r
       rv[r] = out.R[(long)(m < M ? m : M - 1) * (N - 1) + nc];
     }
   }
+  if (out.bias) {  // forward: C = acc + bias[n], and its relu / padded relu
+    const float bn = out.bias[n];
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int m = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
+      if (m < M) {
+        const float v = acc[r] + bn;
+        out.C[(long)m * out.ldc + n] = v;
+        const float o = v > 0.0f ? v : 0.0f;
+        if (out.relu) out.relu[(long)m * N + n] = o;
+        if (out.pad) {
+          float *pr = out.pad + (long)m * (N + 1);
+          pr[n] = o;
+          if (n == N - 1) pr[N] = 1.0f;
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int r = 0; r < 16; r++) {
     const int m = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
@@ -1590,6 +1617,15 @@ gemm_small_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
   __shared__ float red[(SW - 1) * 16 * 64];
   small_tile<A_KC, B_NC, VA, VB>(M, N, K, A, lda, B, ldb, SmallOut{C, ldc, nullptr, nullptr, nullptr},
                                  kc, blockIdx.x, blockIdx.y, red);
+}
+
+// The same tiles with a forward epilogue (SmallOut::bias / relu / pad).
+template <bool VA, bool VB>
+__global__ void __launch_bounds__(64 * SW)
+gemm_small_epi_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
+                      const float *__restrict__ B, long ldb, SmallOut out, int kc) {
+  __shared__ float red[(SW - 1) * 16 * 64];
+  small_tile<true, true, VA, VB>(M, N, K, A, lda, B, ldb, out, kc, blockIdx.x, blockIdx.y, red);
 }
 
 // Both gradients of a matmul C = A * B in one launch of small-GEMM tiles:
@@ -1620,7 +1656,9 @@ gemm_small_pair_kernel(SmallJob da, SmallJob db, int nba) {
 }
 
 // small_ok: below the 64x64 kernel's range (2MNK < 2^29) with at least 128
-// tiles to spread, and every k-contiguous operand 16-byte aligned (rows read
+// tiles to spread -- 256 unless K <= 512 (a long K on half the CUs measured
+// slower than the split-K kernel: 256x512x784 16.2 vs 10.6 us) -- and
+// every k-contiguous operand 16-byte aligned (rows read
 // by 32 lanes one float at a time bound the address path: measured slower
 // than the split-K register kernel).
 template <bool A_KC, bool B_NC>
@@ -1629,7 +1667,7 @@ bool small_ok(int M, int N, int K, const Opnd &A, const Opnd &B) {
   const bool va = !A_KC || (aligned16(A.p) && A.ld % 4 == 0);
   const bool vb = B_NC || (aligned16(B.p) && B.ld % 4 == 0);
   return g_small && K > 0 && 2.0 * M * N * K < (double)(1L << 29) && tiles >= 128 &&
-         (M + 31) / 32 <= 65535 && va && vb;
+         (tiles >= 256 || K <= 512) && (M + 31) / 32 <= 65535 && va && vb;
 }
 
 template <bool A_KC, bool B_NC>
@@ -1895,7 +1933,7 @@ extern "C" int tt_k_gemm_relu_pad(int M, int N, int K, const float *A, const flo
   RedHook h{};
   h.kind = HOOK_RELU_PAD;
   h.C = C;
-  h.rp = ReluPadEx{R, P};
+  h.rp = ReluPadEx{R, P, nullptr};
   g_red_hook = &h;
   const int rc = tt_k_gemm(M, N, K, A, K, 0, B, N, 0, C, N);
   g_red_hook = nullptr;
@@ -1937,6 +1975,46 @@ extern "C" int tt_k_matmul_bwd_small(const float *A, int M, int K, const float *
     hipLaunchKernelGGL(gemm_small_pair_kernel<false>, dim3((unsigned)(nba + nbb)), dim3(64 * SW),
                        0, stream(), da, db, (int)nba);
   return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+// C = A * B + bias (A M x K, B K x N row-major and contiguous; bias a row of
+// N added to every row of C), optionally with R = relu(C) and P = [R, 1]:
+// the matmul of a padones output computed from the padones input (its
+// aligned rows) and the weights' last row.  Small GEMMs store the epilogue
+// from their tiles, split-K GEMMs from their reduction, the rest in a pass
+// after the GEMM.
+extern "C" int tt_k_gemm_bias_relu_pad(int M, int N, int K, const float *A, const float *B,
+                                       const float *bias, float *C, float *R, float *P) {
+  if (M <= 0 || N <= 0 || K < 0 || !A || !B || !bias || !C || (!R && P) || (R && !P))
+    return -1;
+  const Opnd a{A, K, 0, 1}, b{B, N, 0, 1};
+  auto big = [](const Plan &p) {
+    return p.tile == T256x256 || p.tile == T256x128 || p.tile == T128x128;
+  };
+  if (K > 0 && g_force_tile < 0 && !big(plan(M, N, K)) && small_ok<true, true>(M, N, K, a, b)) {
+    const int kc = ((K + SW - 1) / SW + 7) / 8 * 8;
+    const dim3 grid((unsigned)((N + 31) / 32), (unsigned)((M + 31) / 32));
+    SmallOut out{C, N, nullptr, nullptr, nullptr};
+    out.bias = bias;
+    out.relu = R;
+    out.pad = P;
+    if (aligned16(A) && K % 4 == 0)
+      hipLaunchKernelGGL((gemm_small_epi_kernel<true, false>), grid, dim3(64 * SW), 0, stream(),
+                         M, N, K, A, (long)K, B, (long)N, out, kc);
+    else
+      hipLaunchKernelGGL((gemm_small_epi_kernel<false, false>), grid, dim3(64 * SW), 0, stream(),
+                         M, N, K, A, (long)K, B, (long)N, out, kc);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+  }
+  RedHook h{};
+  h.kind = HOOK_RELU_PAD;
+  h.C = C;
+  h.rp = ReluPadEx{R, P, bias};
+  g_red_hook = &h;
+  const int rc = tt_k_gemm(M, N, K, A, K, 0, B, N, 0, C, N);
+  g_red_hook = nullptr;
+  if (rc) return rc;
+  return h.applied ? 0 : ttk_bias_relu_pad(C, bias, R, P, M, N);
 }
 
 // ---- the GEMM without allocation (tt_k_gemm_noalloc) ----

@@ -249,7 +249,9 @@ int tt_flush_pending(void) {
                                   : tt_k_relu_fwd(tt_pend.x, tt_pend.out->dev, tt_pend.out->numel);
     } else if (kind == TT_PEND_MATMUL || kind == TT_PEND_MATMUL_RELU) {
         const int M = tt_pend.geo[0], N = tt_pend.geo[1], K = tt_pend.geo[2];
-        rc = tt_k_gemm(M, N, K, tt_pend.x, K, 0, tt_pend.w, N, 0, tt_pend.out->dev, N);
+        rc = tt_pend.b ? tt_k_gemm_bias_relu_pad(M, N, K, tt_pend.x, tt_pend.w, tt_pend.b,
+                                                 tt_pend.out->dev, NULL, NULL)
+                       : tt_k_gemm(M, N, K, tt_pend.x, K, 0, tt_pend.w, N, 0, tt_pend.out->dev, N);
         if (kind == TT_PEND_MATMUL_RELU) {
             if (rc == 0) rc = tt_k_relu_fwd(tt_pend.out->dev, tt_pend.r->dev, tt_pend.r->numel);
             if (rc != 0) tt_pend.r->valid = 0;

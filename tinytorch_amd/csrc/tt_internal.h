@@ -44,7 +44,8 @@ typedef struct {
     Tensor *out;              /* the pending output (owned by its node) */
     Tensor *r;                /* *_RELU* kinds: the relu output (owned by its node) */
     Tensor *p, *c;            /* the pool output, the reshape's copy (owned by their nodes) */
-    const float *x, *w, *b;   /* device operands, retained by the node's parents */
+    const float *x, *w, *b;   /* device operands, retained by the node's parents (matmul: b is
+                                 the weights' last row when x is a padones input) */
     int geo[13];              /* conv: N C H W F HH WW sh sw ph pw Ho Wo; matmul: M N K */
 } TTPendConv;
 extern TTPendConv tt_pend;

@@ -40,6 +40,9 @@ size_t ttrt_bytes_cached(void);
 /* elementwise.hip: c[m][n] = cin[m][n] + c[m][n] for every (m, n) of the
  * M x N matrices outside the leading mb x nb block */
 int    ttk_add_outside(float *c, const float *cin, int M, int N, int mb, int nb);
+/* elementwise.hip: c[m][n] += bias[n] for the M x N matrix c, and when r / p
+ * are given r = relu(c), p = [r, 1] (M x N+1) */
+int    ttk_bias_relu_pad(float *c, const float *bias, float *r, float *p, int M, int N);
 /* gemm.hip: look up, on the current device, the device address of the
  * static scratch array behind tt_k_gemm_noalloc; 0 ok */
 int    ttg_scratch_setup(void);
