@@ -214,8 +214,8 @@ int tt_k_maxpool_bwd(const float *x, const float *g, float *dx, int N, int C, in
 /* 2x2 / stride-2 max pool backward and the backward of the relu whose output
  * x is the pool's input, in one pass: dx as tt_k_maxpool_bwd, dxr = dx where
  * x > 0 else +0.0f (src/autograd.c:555-594 followed by src/autograd.c:318-327
- * of the reference, which runs them as two steps).  -1: shape or alignment
- * outside the 2x2 kernel. */
+ * of the reference, which runs them as two steps).  dx may be NULL: then only
+ * dxr is written.  -1: shape or alignment outside the 2x2 kernel. */
 int tt_k_maxpool2x2_relu_bwd(const float *x, const float *g, float *dx, float *dxr, int N, int C,
                              int H, int W, int Ho, int Wo);
 int tt_k_avgpool_fwd(const float *x, float *y, int N, int C, int H, int W,

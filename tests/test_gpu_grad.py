@@ -239,6 +239,24 @@ def test_rules_vs_oracle_larger(Node):
     assert np.array_equal(nr.grad(), dr + dr) and np.array_equal(nx.grad(), orc.relu_bwd(x, dr + dr))
     for n in (ns, n1, n2, nr, nx):
         n.release()
+    # the fused backward leaves the relu's own gradient unwritten until it is
+    # asked for: a second pass before any read, a read of the pool's gradient
+    # first, and a release without a read all keep the values above
+    for order in ("twice_unread", "pool_first", "unread"):
+        nx = Node.leaf(x)
+        nr = nx.relu()
+        ny = nr.maxpool2d(pool_size=2, stride=2)
+        ny.backward(g)
+        if order == "twice_unread":
+            ny.backward(g)
+            assert np.array_equal(nx.grad(), dx2) and np.array_equal(nr.grad(), dr + dr)
+        elif order == "pool_first":
+            assert np.array_equal(ny.grad(), g)
+            assert np.array_equal(nr.grad(), dr) and np.array_equal(nx.grad(), orc.relu_bwd(x, dr))
+        else:
+            assert np.array_equal(nx.grad(), orc.relu_bwd(x, dr))
+        for n in (ny, nr, nx) if order != "unread" else (nr, ny, nx):
+            n.release()
 
     # relu -> padones: fused backward on the first call, two steps after
     x = rng.integers(-2, 3, (6, 7)).astype(np.float32)

@@ -59,7 +59,15 @@ struct AGNode {
     AGNode *next;                /* schedule: the node whose rule runs after this one */
     int     fanin;               /* edges into the node from nodes of the pass */
     int     fused;               /* its rule already ran inside a consumer's fused rule */
+    /* A relu whose gradient the fused 2x2 max pool + relu backward did not
+     * write: lazy_g (retained) is the pool's output gradient, from which
+     * materialise computes it on first need; lazy_next links the
+     * nodes that hold one. */
+    Tensor *lazy_g;
+    AGNode *lazy_next;
 };
+
+static AGNode *g_lazy;           /* nodes whose gradient is still a recipe */
 
 static void backward_add(AGNode *n);
 static void backward_mul(AGNode *n);
@@ -128,6 +136,48 @@ static void accum_move(AGNode *p, Tensor *g) {
 }
 
 static int needs(const AGNode *p) { return p && p->needs_grad; }
+
+/* Write the gradient of a node that holds a recipe: the max pool backward
+ * of the relu's output with the pool's output gradient (the reference's
+ * src/autograd.c:555-594), run on first need -- before ag_grad hands out the
+ * node's gradient or the pool's, and before a backward pass that may add
+ * into the pool's gradient -- so the recipe's operands are unchanged. */
+static void materialise(AGNode *n) {
+    for (AGNode **pp = &g_lazy; *pp; pp = &(*pp)->lazy_next)
+        if (*pp == n) { *pp = n->lazy_next; break; }
+    n->lazy_next = NULL;
+    Tensor *g = n->lazy_g;
+    n->lazy_g = NULL;
+    const Tensor *v = n->val;
+    const float *x = tt_dev(v), *gd = tt_dev(g);
+    Tensor *t = (x && gd) ? tt_empty_like(v) : NULL;
+    if (t && tt_k_maxpool_bwd(x, gd, t->dev, (int)v->shape[0], (int)v->shape[1],
+                              (int)v->shape[2], (int)v->shape[3], 2, 2, 2, 2,
+                              (int)g->shape[2], (int)g->shape[3]) == 0)
+        accum_move(n, t);
+    else
+        tt_release(t);
+    tt_release(g);
+}
+
+/* materialise every recipe that is n's gradient or reads it */
+static void materialise_for(const AGNode *n) {
+    AGNode *l = g_lazy;
+    while (l) {
+        AGNode *next = l->lazy_next;
+        if (l == n || (n->grad && l->lazy_g == n->grad)) materialise(l);
+        l = next;
+    }
+}
+
+static void lazy_drop(AGNode *n) {
+    if (!n->lazy_g) return;
+    for (AGNode **pp = &g_lazy; *pp; pp = &(*pp)->lazy_next)
+        if (*pp == n) { *pp = n->lazy_next; break; }
+    tt_release(n->lazy_g);
+    n->lazy_g = NULL;
+    n->lazy_next = NULL;
+}
 
 /* ---------- node construction ---------- */
 
@@ -512,7 +562,11 @@ Tensor *ag_softmax_ce_probs(const AGNode *n) {
 /* ---------- accessors ---------- */
 
 Tensor *ag_value(const AGNode *n) { return n ? n->val : NULL; }
-Tensor *ag_grad(const AGNode *n) { return n ? n->grad : NULL; }
+Tensor *ag_grad(const AGNode *n) {
+    if (!n) return NULL;
+    if (g_lazy) materialise_for(n);
+    return n->grad;
+}
 int ag_requires_grad(const AGNode *n) { return n ? n->needs_grad : 0; }
 
 /* ---------- backward rules ---------- */
@@ -638,7 +692,7 @@ static void backward_softmax(AGNode *n) {
  * its input needs one and has no other consumer -- so every gradient gets
  * the same sums in the same order as with two separate steps. */
 static int relu_fusable(const AGNode *r) {
-    return r->op == &OP_RELU && r->fanin == 1 && !r->grad && needs(r->in[0]) &&
+    return r->op == &OP_RELU && r->fanin == 1 && !r->grad && !r->lazy_g && needs(r->in[0]) &&
            r->in[0]->fanin == 1;
 }
 
@@ -820,13 +874,19 @@ static int backward_maxpool_relu(AGNode *n, AGNode *r, const float *g, const flo
     if (!relu_fusable(r) || n->at.win.kh != 2 || n->at.win.kw != 2 || n->at.win.sh != 2 ||
         n->at.win.sw != 2)
         return 0;
-    Tensor *t = tt_empty_like(r->val), *u = t ? tt_empty_like(r->in[0]->val) : NULL;
-    if (!u || tt_k_maxpool2x2_relu_bwd(x, g, t->dev, u->dev, N, C, H, W, Ho, Wo)) {
-        tt_release(t);
+    /* the relu's own gradient is left as a recipe (nothing in the pass reads
+     * it: the relu feeds only this pool and its rule is skipped); the pool's
+     * gradient is complete here, as every consumer's rule has run */
+    Tensor *u = tt_empty_like(r->in[0]->val);
+    if (!u || tt_k_maxpool2x2_relu_bwd(x, g, NULL, u->dev, N, C, H, W, Ho, Wo)) {
         tt_release(u);
         return 0;
     }
-    fused_relu_done(r, t, u);
+    r->lazy_g = tt_retain(n->grad);
+    r->lazy_next = g_lazy;
+    g_lazy = r;
+    accum_move(r->in[0], u);
+    r->fused = 1;
     return 1;
 }
 
@@ -954,6 +1014,8 @@ static void run_rules(AGNode *head) {
 /* seed_kind: 0 = ones, 1 = host floats, 2 = device tensor */
 static void backward_impl(AGNode *out, int seed_kind, const float *hseed, const Tensor *dseed) {
     AGNode *head = schedule(out);
+    if (g_lazy)
+        for (AGNode *n = head; n && g_lazy; n = n->next) materialise_for(n);
     if (!out->grad) out->grad = tt_empty_like(out->val);
     if (!out->grad) return;
     if (seed_kind == 0 && out->grad->numel == 1) {
@@ -1187,6 +1249,7 @@ void ag_release(AGNode *n) {
         if (tt_pend.active && tt_pend.out == d->val) tt_flush_pending();
         tt_release(d->val);
         tt_release(d->grad);
+        lazy_drop(d);
         if (d->op && d->op->drop) d->op->drop(d);
         for (int i = 0; i < d->n_in; i++) {
             AGNode *p = d->in[i];

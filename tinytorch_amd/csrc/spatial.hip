@@ -230,7 +230,8 @@ __device__ __forceinline__ void argmax4(float v0, float v1, float v2, float v3, 
 
 // RELU: x is the output of a relu whose only consumer is this pool; dxr =
 // relu backward of dx (dx where x > 0, else +0.0f) is written in the same
-// pass (x > 0 exactly when the relu's input is > 0).
+// pass (x > 0 exactly when the relu's input is > 0); dx may then be null,
+// and only dxr is written.
 template <typename I, bool RELU = false>
 __global__ void maxpool2x2_bwd_kernel(const float *__restrict__ x, const float *__restrict__ g,
                                       float *__restrict__ dx, int H, int W, int Ho, int Wo,
@@ -252,8 +253,10 @@ __global__ void maxpool2x2_bwd_kernel(const float *__restrict__ x, const float *
     const float g0 = 0.0f + gv.x, g1 = 0.0f + gv.y;
     float4 top = make_float4(am0 == 0 ? g0 : 0.0f, am0 == 1 ? g0 : 0.0f, am1 == 0 ? g1 : 0.0f, am1 == 1 ? g1 : 0.0f);
     float4 bot = make_float4(am0 == 2 ? g0 : 0.0f, am0 == 3 ? g0 : 0.0f, am1 == 2 ? g1 : 0.0f, am1 == 3 ? g1 : 0.0f);
-    *reinterpret_cast<float4 *>(dx + off) = top;
-    *reinterpret_cast<float4 *>(dx + off + W) = bot;
+    if (!RELU || dx) {
+      *reinterpret_cast<float4 *>(dx + off) = top;
+      *reinterpret_cast<float4 *>(dx + off + W) = bot;
+    }
     if constexpr (RELU) {
       const float4 rt = make_float4(a.x > 0.0f ? top.x : 0.0f, a.y > 0.0f ? top.y : 0.0f,
                                     a.z > 0.0f ? top.z : 0.0f, a.w > 0.0f ? top.w : 0.0f);
@@ -579,7 +582,8 @@ int tt_k_maxpool2x2_relu_bwd(const float *x, const float *g, float *dx, float *d
   const long total = (long)N * C * H * W;
   if (total <= 0) return 0;
   if (W % 4 != 0 || Ho != H / 2 || Wo != W / 2 || (((uintptr_t)x & 15) != 0) ||
-      (((uintptr_t)dx & 15) != 0) || (((uintptr_t)dxr & 15) != 0) || (((uintptr_t)g & 7) != 0))
+      (((uintptr_t)dx & 15) != 0) || !dxr || (((uintptr_t)dxr & 15) != 0) ||
+      (((uintptr_t)g & 7) != 0))
     return -1;
   const long pairs = (long)N * C * Ho * Wo / 2;
   if (pairs < (1L << 31))
@@ -589,7 +593,7 @@ int tt_k_maxpool2x2_relu_bwd(const float *x, const float *g, float *dx, float *d
     hipLaunchKernelGGL((maxpool2x2_bwd_kernel<unsigned long, true>), dim3(blocks_for(pairs)),
                        dim3(256), 0, stream(), x, g, dx, H, W, Ho, Wo, (unsigned long)pairs, dxr);
   if (2 * Ho < H) {
-    TT_LAUNCH_I(pool_uncovered_zero_kernel, total, dx, N, C, H, W, 2 * Ho, 2 * Wo);
+    if (dx) TT_LAUNCH_I(pool_uncovered_zero_kernel, total, dx, N, C, H, W, 2 * Ho, 2 * Wo);
     TT_LAUNCH_I(pool_uncovered_zero_kernel, total, dxr, N, C, H, W, 2 * Ho, 2 * Wo);
   }
   return launched();
