@@ -62,10 +62,9 @@ int tt_k_gemm(int M, int N, int K,
  * reference: it is for callers that cannot allocate (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
  * arguments, kernels and results as tt_k_gemm (bit-identical), but the
- * workspace some shapes need (split-K partials, 16-byte aligned copies of
- * ragged operands) comes from one static device array of
- * TT_GEMM_SCRATCH_BYTES per GPU, held until the process ends, instead of the
- * caching allocator.  A shape whose workspace exceeds it returns
+ * workspace some shapes need (split-K partials) comes from one static
+ * device array of TT_GEMM_SCRATCH_BYTES per GPU, held until the process
+ * ends, instead of the caching allocator.  A shape whose workspace exceeds it returns
  * TT_E_SCRATCH with nothing launched (also reported by tth_last_error).
  * Every call on a GPU shares that GPU's array and leaves its contents behind
  * (the kernels write every workspace element before reading it, so nothing

@@ -556,12 +556,12 @@ def test_gemm_small_kernel(tlib, M, N, K, ta, tb):
     assert norm2 <= GEMM_TOL, norm2
 
 
-# Large GEMMs with unaligned operands take aligned, zero-padded copies into
-# the 64x64 kernel: ragged leading dimensions, K % 4 != 0, odd M / N.
+# Large GEMMs with unaligned operands are read in place by the 64x64 kernel's
+# 4-byte loads: ragged leading dimensions, K % 4 != 0, odd M / N.
 PAD_SHAPES = [(1000, 1003, 997), (1001, 1024, 1000), (1024, 999, 1024), (515, 1025, 1023)]
 
 
-@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("M,N,K", PAD_SHAPES)
 def test_gemm_padded_operands(tlib, M, N, K, ta, tb):
     A = u(K, M) if ta else u(M, K)
@@ -571,6 +571,53 @@ def test_gemm_padded_operands(tlib, M, N, K, ta, tb):
     ref = Am.astype(np.float64) @ Bm.astype(np.float64)
     C = run_gemm(tlib, M, N, K, ta, tb, A, B)
     norm, rel = gemm_err(C, ref, K, 1.0, 1.0)
+    assert norm <= GEMM_TOL and rel <= GEMM_TOL, (norm, rel)
+
+
+# The same 4-byte-load path for each of the kernel's three tilings (one
+# workgroup per CU; more tiles than CUs; tall 256-row tiles), and for
+# operands whose first element is not 16-byte aligned.
+DW_SHAPES = [(2000, 1999, 1001, 0), (65537, 63, 255, 0), (1024, 1024, 1024, 1), (768, 1000, 1003, 3)]
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K,shift", DW_SHAPES)
+def test_gemm_unaligned_in_place(tlib, M, N, K, shift, ta, tb):
+    A = u(K, M) if ta else u(M, K)
+    B = u(N, K) if tb else u(K, N)
+    Am = A.T if ta else A
+    Bm = B.T if tb else B
+    ref = Am.astype(np.float64) @ Bm.astype(np.float64)
+    # operands start `shift` floats into their buffers
+    pa = np.concatenate([np.zeros(shift, np.float32), A.ravel()])
+    pb = np.concatenate([np.zeros(shift, np.float32), B.ravel()])
+    dA, dB, dC = DevBuf.from_np(pa), DevBuf.from_np(pb), DevBuf(M * N)
+    print(f"gemm in place M={M} N={N} K={K} shift={shift} ta={ta} tb={tb}", flush=True)
+    check(tlib.tt_k_gemm(M, N, K, dA.ptr + 4 * shift, A.shape[1], ta, dB.ptr + 4 * shift,
+                         B.shape[1], tb, dC.ptr, N), "tt_k_gemm")
+    C = dC.to_np((M, N))
+    norm, rel = gemm_err(C, ref, K, 1.0, 1.0)
+    assert norm <= GEMM_TOL and rel <= GEMM_TOL, (norm, rel)
+
+
+def test_gemm_unaligned_nonfinite_isolation(tlib):
+    """In-place reads of ragged rows touch no element outside the operand's
+    own rows / columns: an Inf at the start of a row of A and a NaN at the
+    end of the last row of B reach only their own row / column of C."""
+    M, N, K = 1000, 997, 1003
+    A, B = u(M, K), u(K, N)
+    A[5, 0] = np.inf
+    A[6, K - 1] = np.inf
+    B[K - 1, N - 1] = np.nan
+    C = run_gemm(tlib, M, N, K, 0, 0, A, B)
+    bad = ~np.isfinite(C)
+    expect = np.zeros_like(bad)
+    expect[5, :] = expect[6, :] = True
+    expect[:, N - 1] = True
+    assert np.array_equal(bad, expect)
+    ref = A.astype(np.float64) @ B.astype(np.float64)
+    keep = ~expect
+    norm, rel = gemm_err(C[keep], ref[keep], K, 1.0, 1.0)
     assert norm <= GEMM_TOL and rel <= GEMM_TOL, (norm, rel)
 
 

@@ -3,8 +3,8 @@
 Its results are checked bit-for-bit against tt_k_gemm (the same kernels, the
 workspace taken from the static scratch array instead of the caching
 allocator) on two calls in a row, the second with a smaller input, with
-shapes that need workspace (aligned copies of ragged operands, split-K
-partials).  A child process whose every library allocation after the
+shapes that need workspace (split-K partials, with ragged and with aligned
+operands).  A child process whose every library allocation after the
 operands fails (TT_FAIL_ALLOC_AFTER) shows that the entry point allocates
 nothing: tt_k_gemm fails there, tt_k_gemm_noalloc does not.  A shape whose
 workspace exceeds the scratch is refused with TT_E_SCRATCH and C untouched.
@@ -23,9 +23,9 @@ pytestmark = pytest.mark.gpu
 TT_E_SCRATCH = -4
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
-# (M, N, K): ragged 1000x1003x997 takes aligned operand copies; 128x128x8192
-# takes 64 split-K partials (4 MiB); both smaller than the first call
-CALLS = [(1000, 1003, 997), (128, 128, 8192)]
+# (M, N, K): ragged 256x251x8191 takes 16 split-K partials read in place
+# (4 MiB); 128x128x8192 takes 64 (4 MiB) of a smaller output
+CALLS = [(256, 251, 8191), (128, 128, 8192)]
 
 
 def operands(M, N, K, seed):

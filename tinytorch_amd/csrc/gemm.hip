@@ -938,6 +938,23 @@ __device__ __forceinline__ void g2lds16s(const float *sbase, unsigned voff, cons
                : "memory", "m0");
 }
 
+// The 4-byte forms: lane l's float goes to M0 + 4l.  A source needs only
+// 4-byte alignment, so rows of any length are read in place.
+__device__ __forceinline__ void g2lds4s(const float *sbase, unsigned voff, const float *lds) {
+  const unsigned addr = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2"
+               :
+               : "s"(addr), "v"(voff), "s"(sbase)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void g2lds4(const float *src, const float *lds) {
+  const unsigned addr = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off"
+               :
+               : "s"(addr), "v"(src)
+               : "memory", "m0");
+}
+
 // s_waitcnt vmcnt(N) for a compile-time N (capped at the counter's 63)
 template <int N>
 __device__ __forceinline__ void wait_vm() {
@@ -945,28 +962,40 @@ __device__ __forceinline__ void wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
 }
 
-// One operand's loads (16 bytes per lane; a load fills 256 floats of LDS).
-// KC: rows r0+R of a row-major (rows x K) matrix, BK k per tile.  NC: rows k
-// of a row-major (K x cols) matrix, columns r0 .. r0+63.  lim = rows (KC) or
-// the columns that may be read (NC: a multiple of 4, at least cols).  Rows /
-// columns past lim load row / columns lim-1 / lim-4 instead (they only feed
-// outputs that are not stored), so a tile's loads need no range test; only k
-// past the end of the K range (the last tile) must read zeros.  Each lane keeps the byte offset of its element in every
-// load relative to the tile origin (row r0 at k0 for KC, row k0 at column r0
-// for NC); the host keeps these below 2^32 (64 rows of the leading
-// dimension).
-template <bool KC, int BK, int NW, int T = M_T, int KSL = NW>
+// One operand's loads.  x4 form (DW false): 16 bytes a lane, a load fills
+// 256 floats of LDS.  DW form: 4 bytes a lane, a load fills 64 floats; the
+// same LDS layout, element by element, so any row length and alignment is
+// read in place (no aligned copy).  KC: rows r0+R of a row-major (rows x K)
+// matrix, BK k per tile.  NC: rows k of a row-major (K x cols) matrix,
+// columns r0 .. r0+63.  lim = rows (KC) or the columns that may be read (NC:
+// x4 form a multiple of 4, at least cols; DW form cols).  Rows / columns past
+// lim load row / column lim-1 (x4 NC: the 4 columns from lim-4) instead (they
+// only feed outputs that are not stored), so a tile's loads need no range
+// test; only k past the end of the K range (the last tile) must read zeros.
+// Each lane keeps the byte offset of its element in every load relative to
+// the tile origin (row r0 at k0 for KC, row k0 at column r0 for NC); the host
+// keeps these below 2^32 (64 rows of the leading dimension).
+template <bool KC, int BK, int NW, int T = M_T, int KSL = NW, bool DW = false>
 struct MidOperand {
   // T: the tile's extent in this operand (rows for KC, columns for NC);
   // KSL: waves sharing one K tile (its k slices)
   static constexpr int CPR = BK / 4;               // 16-byte chunks per KC row
-  static constexpr int NL = T * BK / (256 * NW);   // loads per wave per tile
-  static_assert(NL >= 1 && NL * 256 * NW == T * BK, "tile too small for the waves");
+  static constexpr int LF = DW ? 64 : 256;         // floats of LDS per load
+  static constexpr int NL = T * BK / (LF * NW);    // loads per wave per tile
+  static_assert(NL >= 1 && NL * LF * NW == T * BK, "tile too small for the waves");
   __device__ __forceinline__ static int swz(int R) { return BK == 32 ? (R >> 1) & 7 : R & 15; }
   unsigned voff[NL];
   const float *p;
   long ld, r0;
   int wave, lane;
+  // the tile float that load j's lane fills, as (x4 load q4, its lane l4,
+  // float e of the lane's 16 bytes)
+  __device__ __forceinline__ void pos(int j, int &q4, int &l4, int &e) const {
+    const int f = (wave * NL + j) * LF + (DW ? lane : 4 * lane);
+    q4 = f >> 8;
+    l4 = (f & 255) >> 2;
+    e = f & 3;
+  }
   __device__ __forceinline__ void init(const float *p_, long ld_, long r0_, int lim, int wave_,
                                        int lane_) {
     p = p_;
@@ -976,29 +1005,34 @@ struct MidOperand {
     lane = lane_;
 #pragma unroll
     for (int j = 0; j < NL; j++) {
-      long e;  // element offset from the tile origin
+      int q4, l4, e;
+      pos(j, q4, l4, e);
+      long off;  // element offset from the tile origin
       if constexpr (KC) {
-        const int R = (wave * NL + j) * (256 / BK) + lane / CPR;
-        e = (min(r0 + R, (long)lim - 1) - r0) * ld + koff(j);
+        const int R = q4 * (256 / BK) + l4 / CPR;
+        off = (min(r0 + R, (long)lim - 1) - r0) * ld + koff(j);
       } else {
-        e = (long)koff(j) * ld + (min(r0 + 4 * (lane % (T / 4)), (long)lim - 4) - r0);
+        const long c = DW ? min(r0 + 4 * (l4 % (T / 4)) + e, (long)lim - 1)
+                          : min(r0 + 4 * (l4 % (T / 4)), (long)lim - 4);
+        off = (long)koff(j) * ld + (c - r0);
       }
-      voff[j] = (unsigned)(e * 4);
+      voff[j] = (unsigned)(off * 4);
     }
   }
-  // k of load j's lane relative to the tile's first k (NC: a load fills
+  // k of load j's lane relative to the tile's first k (NC: an x4 load fills
   // 256/T rows k of T floats)
   __device__ __forceinline__ int koff(int j) const {
-    const int q = wave * NL + j;
+    int q4, l4, e;
+    pos(j, q4, l4, e);
     if constexpr (KC) {
-      const int R = q * (256 / BK) + lane / CPR;
-      return 4 * ((lane % CPR) ^ swz(R));
+      const int R = q4 * (256 / BK) + l4 / CPR;
+      return 4 * ((l4 % CPR) ^ swz(R)) + e;
     } else {
-      return q * (256 / T) + lane / (T / 4);
+      return q4 * (256 / T) + l4 / (T / 4);
     }
   }
   // LDS float offset of load j's first lane
-  __device__ __forceinline__ int dst(int j) const { return (wave * NL + j) * 256; }
+  __device__ __forceinline__ int dst(int j) const { return (wave * NL + j) * LF; }
   // tile origin for the tile starting at absolute k = k0 (wave-uniform; made
   // scalar explicitly, as the DMA takes it in SGPRs)
   __device__ __forceinline__ const float *origin(int k0) const {
@@ -1009,7 +1043,8 @@ struct MidOperand {
     return reinterpret_cast<const float *>(((uintptr_t)hi << 32) | lo);
   }
   __device__ __forceinline__ void issue(int j, const float *org, float *lds) const {
-    g2lds16s(org, voff[j], lds + dst(j));
+    if constexpr (DW) g2lds4s(org, voff[j], lds + dst(j));
+    else g2lds16s(org, voff[j], lds + dst(j));
   }
   // the last tile: k >= kend reads zeros
   __device__ __forceinline__ void issue_tail(int j, const float *org, int k0, int kend,
@@ -1018,7 +1053,8 @@ struct MidOperand {
         (k0 + koff(j) < kend)
             ? reinterpret_cast<const float *>(reinterpret_cast<const char *>(org) + voff[j])
             : g_gemm_zero;
-    g2lds16(sp, lds + dst(j));
+    if constexpr (DW) g2lds4(sp, lds + dst(j));
+    else g2lds16(sp, lds + dst(j));
   }
   // fragments of k slice ks, sub-slice h (8 k): v[x][s] for
   // k = ks*BK/KSL + 8h + 4g + s and row base + 32x + l32 (KC) or m/n
@@ -1047,7 +1083,8 @@ struct MidOperand {
 // ROWS: rows of A per tile (64, or 256 for tall operands with few columns:
 // four 64-row blocks share each tile of B); NWK: waves per K tile.  Wave w
 // owns row block w / NWK and k slice w % NWK.
-template <bool A_KC, bool B_NC, int BK, int S, int NW, int ROWS = M_T, int NWK = NW>
+template <bool A_KC, bool B_NC, int BK, int S, int NW, int ROWS = M_T, int NWK = NW,
+          bool DW = false>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4, 2)))
 gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
                 const float *__restrict__ B, long ldb, float *__restrict__ C, long ldc,
@@ -1061,8 +1098,8 @@ gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
   constexpr int KSUB = BK / (8 * NWK);  // 8-k sub-slices per wave per tile
   static_assert(KSUB >= 1, "tile too shallow for the waves");
   __shared__ __attribute__((aligned(16))) float smem[PIPE > RED ? PIPE : RED];
-  using OA = MidOperand<A_KC, BK, NW, ROWS, NWK>;
-  using OB = MidOperand<!B_NC, BK, NW, M_T, NWK>;
+  using OA = MidOperand<A_KC, BK, NW, ROWS, NWK, DW>;
+  using OB = MidOperand<!B_NC, BK, NW, M_T, NWK, DW>;
   constexpr int NL = OA::NL + OB::NL;  // loads per wave per tile
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1429,46 +1466,6 @@ int reduce_splits(const float *ws, float *C, int M, int N, int S, long ldc, cons
 // dst (rows x ldp, ldp a multiple of 4) = src (rows x cols, leading dimension
 // ld) with columns cols .. ldp-1 zero: a 16-byte aligned copy of an operand
 // whose rows are not.
-struct PadJob {
-  const float *src;
-  long ld;
-  int rows, cols;
-  float *dst;
-  int ldp;
-};
-
-// Both operands' copies in one launch: workgroups [0, ga) take job a's rows,
-// the rest job b's (a job with no rows is skipped); a workgroup copies whole
-// rows, consecutive lanes on consecutive floats (the source rows are not
-// 16-byte aligned, so wider per-lane loads would stride the cache lines).
-__global__ void __launch_bounds__(256) pad_rows_kernel(PadJob a, PadJob b, int ga) {
-  const bool first = (int)blockIdx.x < ga;
-  const PadJob &j = first ? a : b;
-  const int b0 = first ? blockIdx.x : blockIdx.x - ga;
-  const int nb = first ? ga : gridDim.x - ga;
-  for (int r = b0; r < j.rows; r += nb) {
-    const float *__restrict__ sr = j.src + (long)r * j.ld;
-    float *__restrict__ dr = j.dst + (long)r * j.ldp;
-    // four loads issued before their stores (one memory round trip per 1024
-    // floats, not one per 256); the loads are unconditional (the column
-    // clamped, the value selected), so none waits on a branch
-    for (int c0 = 0; c0 < j.ldp; c0 += 1024) {
-      float v[4];
-#pragma unroll
-      for (int u = 0; u < 4; u++) {
-        const int c = c0 + 256 * u + threadIdx.x;
-        const float t = sr[min(c, j.cols - 1)];
-        v[u] = c < j.cols ? t : 0.f;
-      }
-#pragma unroll
-      for (int u = 0; u < 4; u++) {
-        const int c = c0 + 256 * u + threadIdx.x;
-        if (c < j.ldp) dr[c] = v[u];
-      }
-    }
-  }
-}
-
 // Small plain GEMM: one 32x32 tile of C per workgroup, its K range split over
 // SW waves, each multiplying its k slice with operands loaded straight into
 // registers (no LDS staging, no split-K workspace); the wave sums are added
@@ -1717,11 +1714,9 @@ int mid_splits(int M, int N, int K, int *kc_out) {
   return K > 0 ? (K + kc - 1) / kc : 1;
 }
 
-// pad_a / pad_b: the operand is a padded copy whose rows may be read up to
-// the next multiple of 4 columns.
-template <bool A_KC, bool B_NC>
-int run_mid(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ldc,
-            bool pad_a = false, bool pad_b = false, float *ws_given = nullptr) {
+// DW: 4-byte loads (operands of any alignment and row length, read in place).
+template <bool A_KC, bool B_NC, bool DW = false>
+int run_mid(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ldc) {
   const int CUS = 256;
   const long tiles = (long)((M + M_T - 1) / M_T) * ((N + M_T - 1) / M_T);
   int kc;
@@ -1730,7 +1725,7 @@ int run_mid(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ld
   long tld = ldc;
   float *ws = nullptr;
   if (splits > 1) {
-    ws = ws_given ? ws_given : ws_alloc(sizeof(float) * (size_t)M * N * splits);
+    ws = ws_alloc(sizeof(float) * (size_t)M * N * splits);
     if (!ws) return -2;
     target = ws;
     tld = N;
@@ -1741,21 +1736,22 @@ int run_mid(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ld
   // at most one workgroup per CU: 8 waves (two per SIMD) over 4 stages of
   // 64 k (139 KB of LDS); more: 4 waves over 5 stages of 32 k (80 KB), two
   // workgroups per CU
-  const int alim = A_KC ? M : (pad_a ? (M + 3) / 4 * 4 : M);
-  const int blim = !B_NC ? N : (pad_b ? (N + 3) / 4 * 4 : N);
+  const int alim = M, blim = N;
   const long tiles256 = (long)((M + 255) / 256) * ((N + M_T - 1) / M_T);
   if (N <= M_T && splits == 1 && tiles256 >= CUS)
     // tall: 256-row tiles, the 64 columns of B loaded once for four row blocks
-    hipLaunchKernelGGL((gemm_mid_kernel<A_KC, B_NC, 32, 4, 8, 256, 2>), dim3((unsigned)tiles256),
-                       dim3(512), 0, stream(), M, N, K, A.p, A.ld, B.p, B.ld, target, tld,
-                       sstride, kc, cvec, alim, blim);
+    hipLaunchKernelGGL((gemm_mid_kernel<A_KC, B_NC, 32, 4, 8, 256, 2, DW>),
+                       dim3((unsigned)tiles256), dim3(512), 0, stream(), M, N, K, A.p, A.ld, B.p,
+                       B.ld, target, tld, sstride, kc, cvec, alim, blim);
   else if (tiles * splits <= CUS)
-    hipLaunchKernelGGL((gemm_mid_kernel<A_KC, B_NC, 64, 4, 8>), grid, dim3(512), 0, stream(), M,
-                       N, K, A.p, A.ld, B.p, B.ld, target, tld, sstride, kc, cvec, alim, blim);
+    hipLaunchKernelGGL((gemm_mid_kernel<A_KC, B_NC, 64, 4, 8, M_T, 8, DW>), grid, dim3(512), 0,
+                       stream(), M, N, K, A.p, A.ld, B.p, B.ld, target, tld, sstride, kc, cvec,
+                       alim, blim);
   else
-    hipLaunchKernelGGL((gemm_mid_kernel<A_KC, B_NC, 32, 5, 4>), grid, dim3(256), 0, stream(), M,
-                       N, K, A.p, A.ld, B.p, B.ld, target, tld, sstride, kc, cvec, alim, blim);
-  const bool own = ws && !ws_given;
+    hipLaunchKernelGGL((gemm_mid_kernel<A_KC, B_NC, 32, 5, 4, M_T, 4, DW>), grid, dim3(256), 0,
+                       stream(), M, N, K, A.p, A.ld, B.p, B.ld, target, tld, sstride, kc, cvec,
+                       alim, blim);
+  const bool own = ws != nullptr;
   if (hipGetLastError() != hipSuccess) { if (own) ws_free(ws); return -3; }
   if (ws) {
     const int rc = reduce_splits<EPI_STORE>(ws, C, M, N, splits, ldc, nullptr, 1);
@@ -1763,48 +1759,6 @@ int run_mid(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ld
     if (rc) return rc;
   }
   return 0;
-}
-
-// A GEMM large enough to amortise two copies whose operands are not
-// 16-byte aligned (ragged leading dimensions, K % 4 != 0 with k-contiguous
-// rows): copy the operands that need it into aligned, zero-padded buffers and
-// run the 64x64 kernel on those.
-template <bool A_KC, bool B_NC>
-int run_mid_padded(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ldc) {
-  // stored rows x cols of each operand
-  const int ar = A_KC ? M : K, ac = A_KC ? K : M;
-  const int br = B_NC ? K : N, bc = B_NC ? N : K;
-  // a copy is needed for unaligned rows, and for a partial last 16-byte chunk
-  // (K % 4 for k-contiguous rows, M / N % 4 for m/n-contiguous ones)
-  auto needs = [&](const Opnd &o, bool kc, int ext) {
-    return !aligned16(o.p) || o.ld % 4 != 0 || (kc ? K : ext) % 4 != 0;
-  };
-  const bool pa = needs(A, A_KC, M), pb = needs(B, !B_NC, N);
-  const int lda = (ac + 3) / 4 * 4, ldb = (bc + 3) / 4 * 4;
-  if (lda > (1 << 22) || ldb > (1 << 22)) return -1;
-  const size_t na = pa ? (size_t)ar * lda : 0, nb = pb ? (size_t)br * ldb : 0;
-  // the copies and the 64x64 kernel's split-K partials in one request, made
-  // before anything is launched
-  int kc;
-  const int splits = mid_splits(M, N, K, &kc);
-  const size_t nws = splits > 1 ? (size_t)M * N * splits : 0;
-  const size_t nab = (na + nb + 63) / 64 * 64;
-  float *buf = ws_alloc(sizeof(float) * (nab + nws));
-  if (!buf) return -2;
-  Opnd a2 = A, b2 = B;
-  PadJob ja{A.p, A.ld, pa ? ar : 0, ac, buf, lda}, jb{B.p, B.ld, pb ? br : 0, bc, buf + na, ldb};
-  // a workgroup per row (all loads in flight at once) up to 16384, split
-  // between the jobs by rows
-  const long rows = (long)ja.rows + jb.rows;
-  const long cap = min(rows, 16384L);
-  const int ga = ja.rows ? (int)max(1L, cap * ja.rows / rows) : 0;
-  const int gb = jb.rows ? (int)max(1L, cap * jb.rows / rows) : 0;
-  hipLaunchKernelGGL(pad_rows_kernel, dim3(ga + gb), dim3(256), 0, stream(), ja, jb, ga);
-  if (pa) a2 = Opnd{buf, lda, 0, 1};
-  if (pb) b2 = Opnd{buf + na, ldb, 0, 1};
-  const int rc = run_mid<A_KC, B_NC>(M, N, K, a2, b2, C, ldc, pa, pb, nws ? buf + nab : nullptr);
-  ws_free(buf);  // stream-ordered: the GEMM above is queued before any reuse
-  return rc;
 }
 
 template <bool A_KC, bool A_PERM, bool B_NC, bool B_PERM, int EPI, bool B_I2C = false>
@@ -1817,7 +1771,10 @@ int run(int M, int N, int K, Opnd A, Opnd B, float *C, long ldc, const float *bi
     if (p.tile != T256x256 && p.tile != T256x128 && p.tile != T128x128 && g_force_tile < 0) {
       if (small_ok<A_KC, B_NC>(M, N, K, A, B)) return run_small<A_KC, B_NC>(M, N, K, A, B, C, ldc);
       if (mid_ok<A_KC, B_NC>(M, N, K, A, B, vec)) return run_mid<A_KC, B_NC>(M, N, K, A, B, C, ldc);
-      if (g_mid && 2.0 * M * N * K >= 1e9) return run_mid_padded<A_KC, B_NC>(M, N, K, A, B, C, ldc);
+      // operands that are not 16-byte aligned (ragged leading dimensions,
+      // K % 4 != 0 with k-contiguous rows): the same kernel with 4-byte loads
+      if (g_mid && 2.0 * M * N * K >= 1e9 && A.ld <= (1L << 22) && B.ld <= (1L << 22))
+        return run_mid<A_KC, B_NC, true>(M, N, K, A, B, C, ldc);
     }
   }
   if constexpr (B_I2C) {
