@@ -217,6 +217,12 @@ int tt_k_maxpool_bwd(const float *x, const float *g, float *dx, int N, int C, in
  * dxr is written.  -1: shape or alignment outside the 2x2 kernel. */
 int tt_k_maxpool2x2_relu_bwd(const float *x, const float *g, float *dx, float *dxr, int N, int C,
                              int H, int W, int Ho, int Wo);
+/* The same from the relu's INPUT xpre: the relu (xpre > 0 ? xpre : +0) is
+ * taken as each value is read, so the results are bit for bit those of
+ * tt_k_maxpool2x2_relu_bwd on the relu's output (for callers that did not
+ * store that output). */
+int tt_k_maxpool2x2_prerelu_bwd(const float *xpre, const float *g, float *dx, float *dxr, int N,
+                                int C, int H, int W, int Ho, int Wo);
 int tt_k_avgpool_fwd(const float *x, float *y, int N, int C, int H, int W,
                      int ph, int pw, int sh, int sw, int Ho, int Wo);             /* src/ops_spatial.c:166-201 */
 int tt_k_avgpool_bwd(const float *g, float *dx, int N, int C, int H, int W,

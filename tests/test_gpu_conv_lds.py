@@ -392,17 +392,24 @@ def test_autograd_conv_relu_pool_deferred(tlib, case):
             rv = r.value()
         k = 3 if mode == "pool3" else 2
         m = r.maxpool2d(k, k)
-        vals = [c.value(), r.value(), m.value()]
-        gm = np.ascontiguousarray(np.cos(np.arange(vals[2].size, dtype=np.float32)).reshape(vals[2].shape))
-        m.backward(gm)
-        out = vals + [X.grad(), Wn.grad(), Bn.grad()]
+        mv = m.value()
+        gm = np.ascontiguousarray(np.cos(np.arange(mv.size, dtype=np.float32)).reshape(mv.shape))
+        if mode == "late":
+            # the relu output is first read after the backward (which then
+            # took the pool backward from the convolution output)
+            m.backward(gm)
+            vals = [c.value(), r.value(), mv]
+        else:
+            vals = [c.value(), r.value(), mv]
+            m.backward(gm)
+        out = vals + [X.grad(), Wn.grad(), Bn.grad(), r.grad()]
         if mode == "peek":
             assert _bits_equal(rv, vals[1])
         for nd in (m, r, c, X, Wn, Bn):
             nd.release()
         return out
 
-    for mode in ("fused", "peek", "pool3"):
+    for mode in ("fused", "peek", "pool3", "late"):
         prev = tlib.tth_conv_relu_fuse(0)
         try:
             ref = run(mode)
@@ -430,7 +437,8 @@ def test_autograd_conv_pool_flatten_deferred(tlib, mode):
 
     def run():
         X, Wn, Bn = Node.leaf(x), Node.leaf(w), Node.leaf(b)
-        m = X.conv2d(Wn, Bn, (sh, sw), (ph, pw)).relu().maxpool2d(2, 2)
+        m_relu = X.conv2d(Wn, Bn, (sh, sw), (ph, pw)).relu()
+        m = m_relu.maxpool2d(2, 2)
         if mode == "peek_pool":
             m.value()
         nodes = [m]
@@ -448,6 +456,9 @@ def test_autograd_conv_pool_flatten_deferred(tlib, mode):
         gt = np.ascontiguousarray(np.sin(np.arange(v.size, dtype=np.float32)).reshape(v.shape))
         top.backward(gt)
         out = [v, m.value(), X.grad(), Wn.grad(), Bn.grad()]
+        if mode == "fused":
+            # read last: the relu output and its gradient, both still recipes
+            out += [m_relu.value(), m_relu.grad()]
         for nd in nodes[::-1] + [X, Wn, Bn]:
             nd.release()
         return out

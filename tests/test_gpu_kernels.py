@@ -239,6 +239,16 @@ def test_maxpool_relu_fused_bitexact(tlib, shape):
           "maxpool2x2_relu_bwd")
     assert bits_equal(ddr.to_np(shape), dr_ref)
     assert bits_equal(ddx.to_np(shape), dx_ref)
+    # from the relu's input (the relu taken on load), and without dr
+    dxp, ddr2, ddx2 = DevBuf.from_np(x), DevBuf(x.size), DevBuf(x.size)
+    check(tlib.tt_k_maxpool2x2_prerelu_bwd(dxp.ptr, dg.ptr, ddr2.ptr, ddx2.ptr, N, C, H, W, Ho, Wo),
+          "maxpool2x2_prerelu_bwd")
+    assert bits_equal(ddr2.to_np(shape), dr_ref)
+    assert bits_equal(ddx2.to_np(shape), dx_ref)
+    ddx3 = DevBuf(x.size)
+    check(tlib.tt_k_maxpool2x2_prerelu_bwd(dxp.ptr, dg.ptr, None, ddx3.ptr, N, C, H, W, Ho, Wo),
+          "maxpool2x2_prerelu_bwd dx only")
+    assert bits_equal(ddx3.to_np(shape), dx_ref)
 
 
 @pytest.mark.parametrize("p,s", POOL_CASES)

@@ -149,6 +149,7 @@ SIGNATURES = [
     ("tt_k_maxpool_fwd", _I, [VP, VP] + [_I] * 10),
     ("tt_k_maxpool_bwd", _I, [VP, VP, VP] + [_I] * 10),
     ("tt_k_maxpool2x2_relu_bwd", _I, [VP, VP, VP, VP] + [_I] * 6),
+    ("tt_k_maxpool2x2_prerelu_bwd", _I, [VP, VP, VP, VP] + [_I] * 6),
     ("tt_k_avgpool_fwd", _I, [VP, VP] + [_I] * 10),
     ("tt_k_avgpool_bwd", _I, [VP, VP] + [_I] * 10),
     ("tt_k_sgd", _I, [VP, VP, _L, _F]),

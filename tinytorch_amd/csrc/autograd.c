@@ -346,11 +346,16 @@ AGNode *ag_padones(AGNode *a) {
             const TTPendConv p = tt_pend;
             const int *q = p.geo;
             tt_pend.active = 0;
-            if (tt_k_conv2d_relu_pool_fwd_lds(p.x, p.w, p.b, p.out->dev, p.r->dev, p.p->dev,
+            /* the relu output is not stored: a recipe run on first use */
+            if (tt_k_conv2d_relu_pool_fwd_lds(p.x, p.w, p.b, p.out->dev, NULL, p.p->dev,
                                               p.c->dev, v->dev, q[0], q[1], q[2], q[3], q[4],
                                               q[5], q[6], q[7], q[8], q[9], q[10], q[11],
-                                              q[12]) == 0)
+                                              q[12]) == 0) {
+                if (tt_lazy_relu(p.r, p.out) != 0 &&
+                    tt_k_relu_fwd(p.out->dev, p.r->dev, p.r->numel) != 0)
+                    p.r->valid = 0;
                 return make_node(v, &OP_PADONES, a, NULL, NULL);
+            }
             tt_pend = p;  /* not launched: the chain runs below, then the padones */
             tt_release(v);
         }
@@ -869,16 +874,22 @@ static void backward_conv2d(AGNode *n) {
 
 /* A 2x2 / stride-2 max pool whose input is a fusable relu (relu_fusable)
  * runs both backwards in one pass; the relu node's own step is skipped. */
-static int backward_maxpool_relu(AGNode *n, AGNode *r, const float *g, const float *x, int N,
-                                 int C, int H, int W, int Ho, int Wo) {
+static int backward_maxpool_relu(AGNode *n, AGNode *r, const float *g, int N, int C, int H,
+                                 int W, int Ho, int Wo) {
     if (!relu_fusable(r) || n->at.win.kh != 2 || n->at.win.kw != 2 || n->at.win.sh != 2 ||
         n->at.win.sw != 2)
         return 0;
+    /* a relu output still unwritten (a recipe of its input): the kernel reads
+     * the relu's input and takes the relu on load */
+    Tensor *pre = tt_lazy_relu_src(r->val);
+    const float *x = pre ? tt_dev(pre) : tt_dev(r->val);
+    if (!x) return 0;
     /* the relu's own gradient is left as a recipe (nothing in the pass reads
      * it: the relu feeds only this pool and its rule is skipped); the pool's
      * gradient is complete here, as every consumer's rule has run */
     Tensor *u = tt_empty_like(r->in[0]->val);
-    if (!u || tt_k_maxpool2x2_relu_bwd(x, g, NULL, u->dev, N, C, H, W, Ho, Wo)) {
+    if (!u || (pre ? tt_k_maxpool2x2_prerelu_bwd(x, g, NULL, u->dev, N, C, H, W, Ho, Wo)
+                   : tt_k_maxpool2x2_relu_bwd(x, g, NULL, u->dev, N, C, H, W, Ho, Wo))) {
         tt_release(u);
         return 0;
     }
@@ -898,9 +909,10 @@ static void backward_pool(AGNode *n, int is_max) {
               W = (int)a->val->shape[3];
     const int Ho = (int)n->grad->shape[2], Wo = (int)n->grad->shape[3];
     const float *g = tt_dev(n->grad);
+    if (!g) return;
+    if (is_max && backward_maxpool_relu(n, a, g, N, C, H, W, Ho, Wo)) return;
     const float *x = is_max ? tt_dev(a->val) : NULL;
-    if (!g || (is_max && !x)) return;
-    if (is_max && backward_maxpool_relu(n, a, g, x, N, C, H, W, Ho, Wo)) return;
+    if (is_max && !x) return;
     Tensor *t = tt_empty_like(a->val);
     if (!t) return;
     int rc = is_max ? tt_k_maxpool_bwd(x, g, t->dev, N, C, H, W, ph, pw, sh, sw, Ho, Wo)

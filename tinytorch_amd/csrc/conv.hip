@@ -662,7 +662,7 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
         o[j][r] = v > 0.0f ? v : 0.0f;
         if (f < g.F && p < p1) {
           on[(long)f * P + p] = v;
-          rn[(long)f * P + p] = o[j][r];
+          if (rn) rn[(long)f * P + p] = o[j][r];
         }
       }
     }
@@ -1487,7 +1487,7 @@ int run_fwd(const float *x, const float *w, const float *bias, float *out, const
             float *dout = nullptr) {
   const FwdPlan pl = plan_fwd(g, N, FLIP);
   if (!pl.pb) return -1;
-  if (pout && !(rout && !FLIP && pool_fusable(g, pl))) return -1;
+  if (pout && !(!FLIP && pool_fusable(g, pl))) return -1;
   if ((cout || dout) && !pout) return -1;
   if (dry) return 0;
   if (fail_direct()) return -3;
@@ -1833,14 +1833,15 @@ extern "C" int tt_k_conv2d_relu_fwd_lds(const float *x, const float *w, const fl
 // relu: out, rout as above and pout (N x F x Ho/2 x Wo/2) in one launch
 // (bit-identical to tt_k_conv2d_relu_fwd_lds followed by the max pool);
 // cout / dout (optional): the pool output flattened per image, as a copy and
-// padded with a last column of ones (a reshape and a padones after it).
+// padded with a last column of ones (a reshape and a padones after it);
+// rout may be NULL (the relu is then only pooled, not stored).
 // -1: not covered (see pool_fusable).
 extern "C" int tt_k_conv2d_relu_pool_fwd_lds(const float *x, const float *w, const float *bias,
                                              float *out, float *rout, float *pout, float *cout,
                                              float *dout, int N, int C, int H, int W, int F,
                                              int HH, int WW, int sh, int sw, int ph, int pw,
                                              int Ho, int Wo) {
-  if (!x || !w || !out || !rout || !pout || out == rout ||
+  if (!x || !w || !out || !pout || out == rout ||
       !geo_ok(N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo))
     return -1;
   const Geo g{C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo, F, C * HH * WW};

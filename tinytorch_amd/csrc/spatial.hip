@@ -231,8 +231,9 @@ __device__ __forceinline__ void argmax4(float v0, float v1, float v2, float v3, 
 // RELU: x is the output of a relu whose only consumer is this pool; dxr =
 // relu backward of dx (dx where x > 0, else +0.0f) is written in the same
 // pass (x > 0 exactly when the relu's input is > 0); dx may then be null,
-// and only dxr is written.
-template <typename I, bool RELU = false>
+// and only dxr is written.  PRE: x is the relu's input instead (its relu,
+// x > 0 ? x : +0, is taken on load: the same values, so the same argmax).
+template <typename I, bool RELU = false, bool PRE = false>
 __global__ void maxpool2x2_bwd_kernel(const float *__restrict__ x, const float *__restrict__ g,
                                       float *__restrict__ dx, int H, int W, int Ho, int Wo,
                                       I total, float *__restrict__ dxr = nullptr) {
@@ -244,8 +245,14 @@ __global__ void maxpool2x2_bwd_kernel(const float *__restrict__ x, const float *
     const I nc = r / Ho;
     const int ho = (int)(r - nc * Ho);
     const long off = ((long)nc * H + 2 * ho) * W + 4 * q;
-    const float4 a = *reinterpret_cast<const float4 *>(x + off);
-    const float4 b = *reinterpret_cast<const float4 *>(x + off + W);
+    float4 a = *reinterpret_cast<const float4 *>(x + off);
+    float4 b = *reinterpret_cast<const float4 *>(x + off + W);
+    if constexpr (PRE) {
+      a = make_float4(a.x > 0.0f ? a.x : 0.0f, a.y > 0.0f ? a.y : 0.0f, a.z > 0.0f ? a.z : 0.0f,
+                      a.w > 0.0f ? a.w : 0.0f);
+      b = make_float4(b.x > 0.0f ? b.x : 0.0f, b.y > 0.0f ? b.y : 0.0f, b.z > 0.0f ? b.z : 0.0f,
+                      b.w > 0.0f ? b.w : 0.0f);
+    }
     const float2 gv = *reinterpret_cast<const float2 *>(g + (long)r * Wo + 2 * q);
     int am0, am1;
     argmax4(a.x, a.y, b.x, b.y, am0);
@@ -577,8 +584,12 @@ int tt_k_maxpool_fwd(const float *x, float *y, int N, int C, int H, int W, int p
 // produced its input: dx = pool backward (as tt_k_maxpool_bwd), dxr = dx
 // where x > 0 else +0.0f.  -1 when the shape or alignment does not fit the
 // 2x2 kernel (the caller then runs the two backwards separately).
-int tt_k_maxpool2x2_relu_bwd(const float *x, const float *g, float *dx, float *dxr, int N, int C,
-                             int H, int W, int Ho, int Wo) {
+}  // extern "C"
+
+namespace {
+template <bool PRE>
+int maxpool2x2_relu_bwd(const float *x, const float *g, float *dx, float *dxr, int N, int C,
+                        int H, int W, int Ho, int Wo) {
   const long total = (long)N * C * H * W;
   if (total <= 0) return 0;
   if (W % 4 != 0 || Ho != H / 2 || Wo != W / 2 || (((uintptr_t)x & 15) != 0) ||
@@ -587,16 +598,30 @@ int tt_k_maxpool2x2_relu_bwd(const float *x, const float *g, float *dx, float *d
     return -1;
   const long pairs = (long)N * C * Ho * Wo / 2;
   if (pairs < (1L << 31))
-    hipLaunchKernelGGL((maxpool2x2_bwd_kernel<unsigned, true>), dim3(blocks_for(pairs)), dim3(256),
+    hipLaunchKernelGGL((maxpool2x2_bwd_kernel<unsigned, true, PRE>), dim3(blocks_for(pairs)), dim3(256),
                        0, stream(), x, g, dx, H, W, Ho, Wo, (unsigned)pairs, dxr);
   else
-    hipLaunchKernelGGL((maxpool2x2_bwd_kernel<unsigned long, true>), dim3(blocks_for(pairs)),
+    hipLaunchKernelGGL((maxpool2x2_bwd_kernel<unsigned long, true, PRE>), dim3(blocks_for(pairs)),
                        dim3(256), 0, stream(), x, g, dx, H, W, Ho, Wo, (unsigned long)pairs, dxr);
   if (2 * Ho < H) {
     if (dx) TT_LAUNCH_I(pool_uncovered_zero_kernel, total, dx, N, C, H, W, 2 * Ho, 2 * Wo);
     TT_LAUNCH_I(pool_uncovered_zero_kernel, total, dxr, N, C, H, W, 2 * Ho, 2 * Wo);
   }
   return launched();
+}
+
+}  // namespace
+
+extern "C" {
+
+int tt_k_maxpool2x2_relu_bwd(const float *x, const float *g, float *dx, float *dxr, int N, int C,
+                             int H, int W, int Ho, int Wo) {
+  return maxpool2x2_relu_bwd<false>(x, g, dx, dxr, N, C, H, W, Ho, Wo);
+}
+
+int tt_k_maxpool2x2_prerelu_bwd(const float *xpre, const float *g, float *dx, float *dxr, int N,
+                                int C, int H, int W, int Ho, int Wo) {
+  return maxpool2x2_relu_bwd<true>(xpre, g, dx, dxr, N, C, H, W, Ho, Wo);
 }
 
 int tt_k_maxpool_bwd(const float *x, const float *g, float *dx, int N, int C, int H, int W, int ph,

@@ -96,15 +96,64 @@ Tensor *tt_retain(Tensor *t) {
     return t;
 }
 
+/* Tensors whose payload is a recipe not yet run: t = relu(src), written by
+ * the first accessor that needs it (tt_dev / tt_data of t), or before the
+ * host may write src (tt_data of src).  src is retained meanwhile; a tensor
+ * released unread is never written.  The fused convolution + relu + pool
+ * forward registers its relu output this way: the pool is computed from
+ * the relu values in registers and the pool backward reads the convolution
+ * output, so the relu tensor is needed only when someone asks for it. */
+typedef struct TTLazyVal {
+    Tensor *t, *src;
+    struct TTLazyVal *next;
+} TTLazyVal;
+static TTLazyVal *g_lazy_vals;
+
+int tt_lazy_relu(Tensor *t, Tensor *src) {
+    TTLazyVal *l = (TTLazyVal *)malloc(sizeof(TTLazyVal));
+    if (!l) return -1;
+    l->t = t;
+    l->src = tt_retain(src);
+    l->next = g_lazy_vals;
+    g_lazy_vals = l;
+    return 0;
+}
+
+Tensor *tt_lazy_relu_src(const Tensor *t) {
+    for (TTLazyVal *l = g_lazy_vals; l; l = l->next)
+        if (l->t == t) return l->src;
+    return NULL;
+}
+
+/* unlink the entries of t (as the recipe's output, or every entry computed
+ * from t when `from`), running their recipes unless `drop` */
+static void lazy_take(const Tensor *t, int from, int drop) {
+    TTLazyVal **pp = &g_lazy_vals;
+    while (*pp) {
+        TTLazyVal *l = *pp;
+        if ((from ? l->src : l->t) != t) { pp = &l->next; continue; }
+        *pp = l->next;
+        if (!drop) {
+            const float *x = tt_dev(l->src);
+            if (!x || tt_k_relu_fwd(x, l->t->dev, l->t->numel) != 0) l->t->valid = 0;
+            else tt_mark_dev_written(l->t);
+        }
+        tt_release(l->src);
+        free(l);
+    }
+}
+
 void tt_release(Tensor *t) {
     if (!t) return;
     if (--t->refcount > 0) return;
+    if (g_lazy_vals) lazy_take(t, 0, 1);
     ttrt_free(t->dev);
     free_meta(t);
 }
 
 float *tt_dev(Tensor *t) {
     if (tt_pend.active) tt_flush_pending();
+    if (g_lazy_vals && t) lazy_take(t, 0, 0);
     if (!t || !t->dev || !t->valid) return NULL;
     if (!(t->valid & TT_V_DEV)) {
         if (!t->data || ttrt_h2d_async(t->dev, t->data, sizeof(float) * (size_t)t->numel) != 0)
@@ -119,6 +168,10 @@ float *tt_dev(Tensor *t) {
 float *tt_data(const Tensor *ct) {
     Tensor *t = (Tensor *)ct;
     if (tt_pend.active) tt_flush_pending();
+    if (g_lazy_vals && t) {
+        lazy_take(t, 0, 0);
+        lazy_take(t, 1, 0);  /* the host may write t: recipes reading it run now */
+    }
     if (!t || !t->valid) return NULL;
     if (!(t->valid & TT_V_HOST)) {
         if (!t->data) {

@@ -50,6 +50,9 @@ typedef struct {
 } TTPendConv;
 extern TTPendConv tt_pend;
 int tt_flush_pending(void);   /* 0 ok; <0 the pending output is invalid */
+/* t (allocated, unwritten) = relu(src), written on first use (tensor.c) */
+int tt_lazy_relu(Tensor *t, Tensor *src);
+Tensor *tt_lazy_relu_src(const Tensor *t);  /* src while t is still unwritten */
 int tt_defer_enabled(void);
 Tensor *tt_reshape_ex(const Tensor *a, const long *new_shape, int new_ndim, int defer);
 Tensor *tt_conv2d_keepcol_ex(const Tensor *a, const Tensor *w, const Tensor *b,
