@@ -223,6 +223,12 @@ int tt_k_maxpool2x2_relu_bwd(const float *x, const float *g, float *dx, float *d
  * store that output). */
 int tt_k_maxpool2x2_prerelu_bwd(const float *xpre, const float *g, float *dx, float *dxr, int N,
                                 int C, int H, int W, int Ho, int Wo);
+/* dxr of tt_k_maxpool2x2_relu_bwd from the pool windows' codes of
+ * tt_k_conv2d_relu_pool_fwd_lds instead of the relu output (H = 2 Ho,
+ * W = 2 Wo, W % 4 == 0): bit for bit the same, reading a byte per window
+ * instead of four floats.  -1: shape or alignment outside the kernel. */
+int tt_k_maxpool2x2_code_relu_bwd(const unsigned char *codes, const float *g, float *dxr, int N,
+                                  int C, int H, int W, int Ho, int Wo);
 int tt_k_avgpool_fwd(const float *x, float *y, int N, int C, int H, int W,
                      int ph, int pw, int sh, int sw, int Ho, int Wo);             /* src/ops_spatial.c:166-201 */
 int tt_k_avgpool_bwd(const float *g, float *dx, int N, int C, int H, int W,
@@ -317,14 +323,30 @@ int tt_k_conv2d_relu_fwd_lds(const float *x, const float *w, const float *bias, 
  * src/ops_spatial.c:22-34) and padded with a last column of ones (padones
  * of that, src/autograd.c:195-212).  3x3 kernels with even Ho, Wo whose
  * output rows pair up inside the kernel's pixel blocks (Wo = 32, or
- * 32 % Wo == 0 with 32 / Wo even); -1 otherwise, nothing launched. */
+ * 32 % Wo == 0 with 32 / Wo even); -1 otherwise, nothing launched.  rout
+ * may be NULL (the relu is pooled but not stored); codes (optional): one
+ * byte per pool window, N x F x Ho/2 x Wo/2 -- bits 0-1 the window's argmax
+ * (first maximum in top-left, top-right, bottom-left, bottom-right order, as
+ * src/autograd.c:555-594 scans), bits 2-5 which relu values are > 0 -- for
+ * tt_k_maxpool2x2_code_relu_bwd. */
 int tt_k_conv2d_relu_pool_fwd_lds(const float *x, const float *w, const float *bias, float *out,
-                                  float *rout, float *pout, float *cout, float *dout, int N,
-                                  int C, int H, int W, int F, int HH, int WW, int sh, int sw,
-                                  int ph, int pw, int Ho, int Wo);
+                                  float *rout, float *pout, float *cout, float *dout,
+                                  unsigned char *codes, int N, int C, int H, int W, int F, int HH,
+                                  int WW, int sh, int sw, int ph, int pw, int Ho, int Wo);
 int tt_k_conv2d_dw_lds(const float *g, const float *x, float *dw, float *db,
                        int N, int C, int H, int W, int F, int HH, int WW,
                        int sh, int sw, int ph, int pw, int Ho, int Wo);
+/* dw / db of tt_k_conv2d_dw_lds when the output gradient is that of a relu
+ * followed by a 2x2 / stride-2 max pool: computed from the pool's gradient
+ * gp (N x F x Ho/2 x Wo/2) and the windows' codes of
+ * tt_k_conv2d_relu_pool_fwd_lds, the output gradient decoded in LDS and
+ * never stored -- bit for bit tt_k_maxpool2x2_code_relu_bwd followed by
+ * tt_k_conv2d_dw_lds (the reference's src/autograd.c:555-594, 318-327 and
+ * src/ops_spatial.c:71-127 backward in one step).  dw == NULL: 0 when the
+ * shape is covered, -1 when not (nothing launched). */
+int tt_k_conv2d_dw_lds_pooled(const float *gp, const unsigned char *codes, const float *x,
+                              float *dw, float *db, int N, int C, int H, int W, int F, int HH,
+                              int WW, int sh, int sw, int ph, int pw, int Ho, int Wo);
 int tt_k_conv2d_dx_lds(const float *g, const float *w, float *dx,
                        int N, int C, int H, int W, int F, int HH, int WW,
                        int sh, int sw, int ph, int pw, int Ho, int Wo);

@@ -345,8 +345,9 @@ def test_conv_relu_pool_fused_kernel_bitexact(tlib, case):
     o2, r2, p2 = DevBuf(n_out), DevBuf(n_out), DevBuf(n_pool)
     K1 = F * (Ho // 2) * (Wo // 2)
     c1, d1 = DevBuf(n_pool), DevBuf(N * (K1 + 1))
+    codes = DevBuf(n_pool, np.uint8)
     check(tlib.tt_k_conv2d_relu_pool_fwd_lds(dx_.ptr, dw_.ptr, db_.ptr, o1.ptr, r1.ptr, p1.ptr,
-                                             c1.ptr, d1.ptr, *geo), "fused")
+                                             c1.ptr, d1.ptr, codes.ptr, *geo), "fused")
     check(tlib.tt_k_conv2d_relu_fwd_lds(dx_.ptr, dw_.ptr, db_.ptr, o2.ptr, r2.ptr, *geo), "conv")
     check(tlib.tt_k_maxpool_fwd(r2.ptr, p2.ptr, N, F, Ho, Wo, 2, 2, 2, 2, Ho // 2, Wo // 2), "pool")
     shp, pshp = (N, F, Ho, Wo), (N, F, Ho // 2, Wo // 2)
@@ -358,6 +359,36 @@ def test_conv_relu_pool_fused_kernel_bitexact(tlib, case):
     flat = pool.reshape(N, K1)
     assert _bits_equal(c1.to_np((N, K1)), flat)
     assert _bits_equal(d1.to_np((N, K1 + 1)), orc.padones_fwd(flat))
+    # the windows' codes: first argmax (top-left, top-right, bottom-left,
+    # bottom-right) in bits 0-1, relu > 0 of the four in bits 2-5
+    r = r1.to_np(shp)
+    win = np.stack([r[:, :, 0::2, 0::2], r[:, :, 0::2, 1::2], r[:, :, 1::2, 0::2],
+                    r[:, :, 1::2, 1::2]])
+    want = np.argmax(win, axis=0).astype(np.uint8)
+    for k in range(4):
+        want |= ((win[k] > 0).astype(np.uint8) << (2 + k))
+    assert np.array_equal(codes.to_np(pshp), want)
+    # the pool + relu backward from the codes: bit for bit the one from the
+    # relu values (the convolution output's gradient)
+    gp = np.random.default_rng(3).standard_normal(pshp).astype(np.float32)
+    gp.flat[::7] = -0.0
+    dg = DevBuf.from_np(gp)
+    e1, e2 = DevBuf(n_out), DevBuf(n_out)
+    check(tlib.tt_k_maxpool2x2_code_relu_bwd(codes.ptr, dg.ptr, e1.ptr, N, F, Ho, Wo, Ho // 2,
+                                             Wo // 2), "code bwd")
+    check(tlib.tt_k_maxpool2x2_relu_bwd(r1.ptr, dg.ptr, None, e2.ptr, N, F, Ho, Wo, Ho // 2,
+                                        Wo // 2), "relu bwd")
+    assert _bits_equal(e1.to_np(shp), e2.to_np(shp))
+    # the weight gradient from the pool gradient and the codes: bit for bit
+    # the one from the decoded output gradient
+    dw1, db1, dw2, db2 = DevBuf(w.size), DevBuf(F), DevBuf(w.size), DevBuf(F)
+    covered = tlib.tt_k_conv2d_dw_lds_pooled(None, None, None, None, None, *geo) == 0
+    if covered:
+        check(tlib.tt_k_conv2d_dw_lds_pooled(dg.ptr, codes.ptr, dx_.ptr, dw1.ptr, db1.ptr, *geo),
+              "pooled dw")
+        check(tlib.tt_k_conv2d_dw_lds(e1.ptr, dx_.ptr, dw2.ptr, db2.ptr, *geo), "dw")
+        assert _bits_equal(dw1.to_np(w.shape), dw2.to_np(w.shape))
+        assert _bits_equal(db1.to_np((F,)), db2.to_np((F,)))
 
 
 @pytest.mark.parametrize("case", [(2, 3, 24, 24, 4, 3, 3, 1, 1, 1, 1),   # 32 % Wo != 0
@@ -370,7 +401,7 @@ def test_conv_relu_pool_fused_rejects(tlib, case):
     dx_, dw_ = DevBuf.from_np(x), DevBuf.from_np(w)
     o, r, p = DevBuf(N * F * Ho * Wo), DevBuf(N * F * Ho * Wo), DevBuf(N * F * Ho * Wo)
     assert tlib.tt_k_conv2d_relu_pool_fwd_lds(dx_.ptr, dw_.ptr, None, o.ptr, r.ptr, p.ptr,
-                                              None, None, *geo) == -1
+                                              None, None, None, *geo) == -1
 
 
 @pytest.mark.parametrize("case", [POOL_CASES[3], POOL_CASES[5], (2, 3, 24, 24, 4, 3, 3, 1, 1, 1, 1)])
@@ -385,7 +416,7 @@ def test_autograd_conv_relu_pool_deferred(tlib, case):
     print("deferred conv relu pool", case, flush=True)
 
     def run(mode):
-        X, Wn, Bn = Node.leaf(x), Node.leaf(w), Node.leaf(b)
+        X, Wn, Bn = Node.leaf(x, mode != "nograd"), Node.leaf(w), Node.leaf(b)
         c = X.conv2d(Wn, Bn, (sh, sw), (ph, pw))
         r = c.relu()
         if mode == "peek":
@@ -402,14 +433,16 @@ def test_autograd_conv_relu_pool_deferred(tlib, case):
         else:
             vals = [c.value(), r.value(), mv]
             m.backward(gm)
-        out = vals + [X.grad(), Wn.grad(), Bn.grad(), r.grad()]
+        out = vals + [Wn.grad(), Bn.grad(), r.grad(), c.grad()]
+        if mode != "nograd":
+            out.append(X.grad())
         if mode == "peek":
             assert _bits_equal(rv, vals[1])
         for nd in (m, r, c, X, Wn, Bn):
             nd.release()
         return out
 
-    for mode in ("fused", "peek", "pool3", "late"):
+    for mode in ("fused", "peek", "pool3", "late", "nograd"):
         prev = tlib.tth_conv_relu_fuse(0)
         try:
             ref = run(mode)
@@ -420,7 +453,7 @@ def test_autograd_conv_relu_pool_deferred(tlib, case):
             assert _bits_equal(a, e), mode
 
 
-@pytest.mark.parametrize("mode", ["fused", "peek_pool", "reshape3d", "no_padones"])
+@pytest.mark.parametrize("mode", ["fused", "peek_pool", "reshape3d", "no_padones", "x_nograd"])
 def test_autograd_conv_pool_flatten_deferred(tlib, mode):
     """The classifier's input chain conv -> relu -> 2x2 pool -> reshape ->
     padones (config 4's second convolution) as one launch, against the same
@@ -436,7 +469,7 @@ def test_autograd_conv_pool_flatten_deferred(tlib, mode):
     print("deferred conv pool flatten", mode, flush=True)
 
     def run():
-        X, Wn, Bn = Node.leaf(x), Node.leaf(w), Node.leaf(b)
+        X, Wn, Bn = Node.leaf(x, mode != "x_nograd"), Node.leaf(w), Node.leaf(b)
         m_relu = X.conv2d(Wn, Bn, (sh, sw), (ph, pw)).relu()
         m = m_relu.maxpool2d(2, 2)
         if mode == "peek_pool":
@@ -455,8 +488,10 @@ def test_autograd_conv_pool_flatten_deferred(tlib, mode):
         v = top.value()
         gt = np.ascontiguousarray(np.sin(np.arange(v.size, dtype=np.float32)).reshape(v.shape))
         top.backward(gt)
-        out = [v, m.value(), X.grad(), Wn.grad(), Bn.grad()]
-        if mode == "fused":
+        out = [v, m.value(), Wn.grad(), Bn.grad()]
+        if mode != "x_nograd":
+            out.append(X.grad())
+        if mode in ("fused", "x_nograd"):
             # read last: the relu output and its gradient, both still recipes
             out += [m_relu.value(), m_relu.grad()]
         for nd in nodes[::-1] + [X, Wn, Bn]:

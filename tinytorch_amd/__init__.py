@@ -150,6 +150,7 @@ SIGNATURES = [
     ("tt_k_maxpool_bwd", _I, [VP, VP, VP] + [_I] * 10),
     ("tt_k_maxpool2x2_relu_bwd", _I, [VP, VP, VP, VP] + [_I] * 6),
     ("tt_k_maxpool2x2_prerelu_bwd", _I, [VP, VP, VP, VP] + [_I] * 6),
+    ("tt_k_maxpool2x2_code_relu_bwd", _I, [VP, VP, VP] + [_I] * 6),
     ("tt_k_avgpool_fwd", _I, [VP, VP] + [_I] * 10),
     ("tt_k_avgpool_bwd", _I, [VP, VP] + [_I] * 10),
     ("tt_k_sgd", _I, [VP, VP, _L, _F]),
@@ -167,8 +168,9 @@ SIGNATURES = [
     ("tt_k_conv2d_lds_plan", _I, [_I] * 13),
     ("tt_k_conv2d_fwd_lds", _I, [VP, VP, VP, VP] + [_I] * 13),
     ("tt_k_conv2d_relu_fwd_lds", _I, [VP, VP, VP, VP, VP] + [_I] * 13),
-    ("tt_k_conv2d_relu_pool_fwd_lds", _I, [VP] * 8 + [_I] * 13),
+    ("tt_k_conv2d_relu_pool_fwd_lds", _I, [VP] * 9 + [_I] * 13),
     ("tt_k_conv2d_dw_lds", _I, [VP, VP, VP, VP] + [_I] * 13),
+    ("tt_k_conv2d_dw_lds_pooled", _I, [VP] * 5 + [_I] * 13),
     ("tt_k_conv2d_dx_lds", _I, [VP, VP, VP] + [_I] * 13),
     ("tt_k_gather_u8_norm", _I, [VP, _L, _L, _L, _I, VP, _L, F32P, F32P, VP]),
     ("tt_k_momentum_multi", _I, [ctypes.POINTER(VP)] * 3 + [ctypes.POINTER(_L), _I, _F, _F]),

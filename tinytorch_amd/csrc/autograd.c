@@ -49,7 +49,8 @@ struct AGNode {
     int     refs;
     union {
         float s;                                          /* add/mul scalar */
-        struct { int kh, kw, sh, sw; } win;               /* pools */
+        struct { int kh, kw, sh, sw; Tensor *codes; } win;  /* pools (codes: one byte a
+                                                      2x2 window, or NULL) */
         struct { int sh, sw, ph, pw; float *col; int col_ones; } conv;
         struct { Tensor *probs, *seed; int32_t *labels; } ce;  /* softmax-CE */
     } at;
@@ -59,11 +60,14 @@ struct AGNode {
     AGNode *next;                /* schedule: the node whose rule runs after this one */
     int     fanin;               /* edges into the node from nodes of the pass */
     int     fused;               /* its rule already ran inside a consumer's fused rule */
-    /* A relu whose gradient the fused 2x2 max pool + relu backward did not
-     * write: lazy_g (retained) is the pool's output gradient, from which
-     * materialise computes it on first need; lazy_next links the
-     * nodes that hold one. */
-    Tensor *lazy_g;
+    /* A gradient the fused 2x2 max pool + relu backward did not write,
+     * computed by materialise on first need from lazy_g (retained), the
+     * pool's output gradient: the relu's own gradient (lazy_codes NULL), or
+     * the gradient of the convolution feeding the relu (lazy_codes, retained:
+     * the pool windows' codes), whose weight gradient is then computed from
+     * lazy_g and the codes directly.  lazy_next links the nodes that hold
+     * one. */
+    Tensor *lazy_g, *lazy_codes;
     AGNode *lazy_next;
 };
 
@@ -79,11 +83,13 @@ static void backward_softmax(AGNode *n);
 static void backward_padones(AGNode *n);
 static void backward_reshape(AGNode *n);
 static void backward_conv2d(AGNode *n);
+static int conv_pooled_dw(AGNode *n);
 static void backward_maxpool(AGNode *n);
 static void backward_avgpool(AGNode *n);
 static void backward_softmax_ce(AGNode *n);
 
 static void drop_conv(AGNode *n) { ttrt_free(n->at.conv.col); }
+static void drop_pool(AGNode *n) { tt_release(n->at.win.codes); }
 static void drop_ce(AGNode *n) {
     tt_release(n->at.ce.probs);
     tt_release(n->at.ce.seed);
@@ -100,7 +106,7 @@ static const AGOp OP_SOFTMAX = {"softmax", backward_softmax, NULL};
 static const AGOp OP_PADONES = {"padones", backward_padones, NULL};
 static const AGOp OP_RESHAPE = {"reshape", backward_reshape, NULL};
 static const AGOp OP_CONV2D = {"conv2d", backward_conv2d, drop_conv};
-static const AGOp OP_MAXPOOL2D = {"maxpool2d", backward_maxpool, NULL};
+static const AGOp OP_MAXPOOL2D = {"maxpool2d", backward_maxpool, drop_pool};
 static const AGOp OP_AVGPOOL2D = {"avgpool2d", backward_avgpool, NULL};
 static const AGOp OP_SOFTMAX_CE = {"softmax_ce", backward_softmax_ce, drop_ce};
 
@@ -139,25 +145,31 @@ static int needs(const AGNode *p) { return p && p->needs_grad; }
 
 /* Write the gradient of a node that holds a recipe: the max pool backward
  * of the relu's output with the pool's output gradient (the reference's
- * src/autograd.c:555-594), run on first need -- before ag_grad hands out the
- * node's gradient or the pool's, and before a backward pass that may add
- * into the pool's gradient -- so the recipe's operands are unchanged. */
+ * src/autograd.c:555-594), or for the convolution before the relu that
+ * followed by the relu backward (src/autograd.c:318-327) from the windows'
+ * codes.  Run on first need -- before ag_grad hands out the node's gradient
+ * or the pool's, before a rule other than the convolution's reads it, and
+ * before a backward pass that may add into the pool's gradient -- so the
+ * recipe's operands are unchanged. */
 static void materialise(AGNode *n) {
     for (AGNode **pp = &g_lazy; *pp; pp = &(*pp)->lazy_next)
         if (*pp == n) { *pp = n->lazy_next; break; }
     n->lazy_next = NULL;
-    Tensor *g = n->lazy_g;
-    n->lazy_g = NULL;
+    Tensor *g = n->lazy_g, *codes = n->lazy_codes;
+    n->lazy_g = n->lazy_codes = NULL;
     const Tensor *v = n->val;
-    const float *x = tt_dev(v), *gd = tt_dev(g);
-    Tensor *t = (x && gd) ? tt_empty_like(v) : NULL;
-    if (t && tt_k_maxpool_bwd(x, gd, t->dev, (int)v->shape[0], (int)v->shape[1],
-                              (int)v->shape[2], (int)v->shape[3], 2, 2, 2, 2,
-                              (int)g->shape[2], (int)g->shape[3]) == 0)
+    const int N = (int)v->shape[0], C = (int)v->shape[1], H = (int)v->shape[2],
+              W = (int)v->shape[3], Ho = (int)g->shape[2], Wo = (int)g->shape[3];
+    const float *x = codes ? NULL : tt_dev((Tensor *)v), *gd = tt_dev(g);
+    const unsigned char *cd = codes ? (const unsigned char *)tt_dev(codes) : NULL;
+    Tensor *t = ((x || cd) && gd) ? tt_empty_like(v) : NULL;
+    if (t && (cd ? tt_k_maxpool2x2_code_relu_bwd(cd, gd, t->dev, N, C, H, W, Ho, Wo)
+                 : tt_k_maxpool_bwd(x, gd, t->dev, N, C, H, W, 2, 2, 2, 2, Ho, Wo)) == 0)
         accum_move(n, t);
     else
         tt_release(t);
     tt_release(g);
+    tt_release(codes);
 }
 
 /* materialise every recipe that is n's gradient or reads it */
@@ -175,8 +187,16 @@ static void lazy_drop(AGNode *n) {
     for (AGNode **pp = &g_lazy; *pp; pp = &(*pp)->lazy_next)
         if (*pp == n) { *pp = n->lazy_next; break; }
     tt_release(n->lazy_g);
-    n->lazy_g = NULL;
+    tt_release(n->lazy_codes);
+    n->lazy_g = n->lazy_codes = NULL;
     n->lazy_next = NULL;
+}
+
+static void lazy_set(AGNode *n, Tensor *g, Tensor *codes) {
+    n->lazy_g = tt_retain(g);
+    n->lazy_codes = codes ? tt_retain(codes) : NULL;
+    n->lazy_next = g_lazy;
+    g_lazy = n;
 }
 
 /* ---------- node construction ---------- */
@@ -348,9 +368,12 @@ AGNode *ag_padones(AGNode *a) {
             tt_pend.active = 0;
             /* the relu output is not stored: a recipe run on first use */
             if (tt_k_conv2d_relu_pool_fwd_lds(p.x, p.w, p.b, p.out->dev, NULL, p.p->dev,
-                                              p.c->dev, v->dev, q[0], q[1], q[2], q[3], q[4],
-                                              q[5], q[6], q[7], q[8], q[9], q[10], q[11],
+                                              p.c->dev, v->dev,
+                                              p.codes ? (unsigned char *)p.codes->dev : NULL,
+                                              q[0], q[1], q[2], q[3],
+                                              q[4], q[5], q[6], q[7], q[8], q[9], q[10], q[11],
                                               q[12]) == 0) {
+                if (p.codes) *p.codes_dst = p.codes;
                 if (tt_lazy_relu(p.r, p.out) != 0 &&
                     tt_k_relu_fwd(p.out->dev, p.r->dev, p.r->numel) != 0)
                     p.r->valid = 0;
@@ -473,6 +496,11 @@ AGNode *ag_maxpool2d(AGNode *a, int ph, int pw, int sh, int sw) {
         AGNode *n = pool_node(a, v, &OP_MAXPOOL2D, ph, pw, sh, sw);
         if (!n) return NULL;
         tt_pend.p = v;
+        /* the launch also writes each window's argmax + relu mask (a byte),
+         * from which the backward runs without reading the relu values */
+        const long cshp[1] = {(v->numel + 3) / 4};
+        tt_pend.codes = tt_empty_dev(cshp, 1);
+        tt_pend.codes_dst = &n->at.win.codes;
         tt_pend.active = TT_PEND_CONV_RELU_POOL;
         return n;
     }
@@ -755,6 +783,11 @@ static void backward_reshape(AGNode *n) {
 }
 
 static void backward_conv2d(AGNode *n) {
+    if (n->lazy_codes) {
+        if (conv_pooled_dw(n)) return;
+        materialise(n);
+        if (!n->grad) return;  /* could not be written (out of memory) */
+    }
     AGNode *a = n->in[0], *w = n->in[1];
     AGNode *b = n->n_in > 2 ? n->in[2] : NULL;
     const int sh = n->at.conv.sh, sw = n->at.conv.sw, ph = n->at.conv.ph, pw = n->at.conv.pw;
@@ -874,28 +907,90 @@ static void backward_conv2d(AGNode *n) {
 
 /* A 2x2 / stride-2 max pool whose input is a fusable relu (relu_fusable)
  * runs both backwards in one pass; the relu node's own step is skipped. */
+/* geometry of a convolution node: N C H W F HH WW sh sw ph pw Ho Wo */
+static void conv_geo(const AGNode *c, int q[13]) {
+    const Tensor *x = c->in[0]->val, *w = c->in[1]->val;
+    const int v[13] = {(int)x->shape[0], (int)x->shape[1], (int)x->shape[2], (int)x->shape[3],
+                       (int)w->shape[0], (int)w->shape[2], (int)w->shape[3], c->at.conv.sh,
+                       c->at.conv.sw, c->at.conv.ph, c->at.conv.pw, (int)c->val->shape[2],
+                       (int)c->val->shape[3]};
+    for (int i = 0; i < 13; i++) q[i] = v[i];
+}
+
+/* A convolution whose rule can take its output gradient as (pool gradient,
+ * pool codes): only its weight (and bias) gradient is wanted -- its input
+ * needs none -- on the LDS path the pooled form covers. */
+static int conv_takes_pooled(const AGNode *c) {
+    if (c->op != &OP_CONV2D || c->fanin != 1 || c->grad || c->lazy_g || needs(c->in[0]) ||
+        !needs(c->in[1]) || c->at.conv.col)
+        return 0;
+    int q[13];
+    conv_geo(c, q);
+    return (tt_k_conv2d_lds_plan(q[0], q[1], q[2], q[3], q[4], q[5], q[6], q[7], q[8], q[9],
+                                 q[10], q[11], q[12]) & 2) &&
+           tt_k_conv2d_dw_lds_pooled(NULL, NULL, NULL, NULL, NULL, q[0], q[1], q[2], q[3], q[4],
+                                     q[5], q[6], q[7], q[8], q[9], q[10], q[11], q[12]) == 0;
+}
+
+/* The rule of such a convolution: dW (and db) from the pool gradient and
+ * codes; its own gradient stays a recipe.  0: not done (the caller
+ * materialises the gradient and takes the ordinary rule). */
+static int conv_pooled_dw(AGNode *n) {
+    AGNode *a = n->in[0], *w = n->in[1];
+    AGNode *b = n->n_in > 2 ? n->in[2] : NULL;
+    if (needs(a) || !needs(w)) return 0;
+    int q[13];
+    conv_geo(n, q);
+    const long bshp[1] = {q[4]};
+    const float *x = tt_dev(a->val), *gp = tt_dev(n->lazy_g);
+    const unsigned char *cd = (const unsigned char *)tt_dev(n->lazy_codes);
+    Tensor *gw = x && gp && cd ? tt_empty_like(w->val) : NULL;
+    Tensor *gb = gw && needs(b) ? tt_empty_dev(bshp, 1) : NULL;
+    if (gw && (gb || !needs(b)) &&
+        tt_k_conv2d_dw_lds_pooled(gp, cd, x, gw->dev, gb ? gb->dev : NULL, q[0], q[1], q[2],
+                                  q[3], q[4], q[5], q[6], q[7], q[8], q[9], q[10], q[11],
+                                  q[12]) == 0) {
+        if (gb) accum_move(b, gb);
+        accum_move(w, gw);
+        return 1;
+    }
+    tt_release(gw);
+    tt_release(gb);
+    return 0;
+}
+
 static int backward_maxpool_relu(AGNode *n, AGNode *r, const float *g, int N, int C, int H,
                                  int W, int Ho, int Wo) {
     if (!relu_fusable(r) || n->at.win.kh != 2 || n->at.win.kw != 2 || n->at.win.sh != 2 ||
         n->at.win.sw != 2)
         return 0;
-    /* a relu output still unwritten (a recipe of its input): the kernel reads
-     * the relu's input and takes the relu on load */
-    Tensor *pre = tt_lazy_relu_src(r->val);
-    const float *x = pre ? tt_dev(pre) : tt_dev(r->val);
-    if (!x) return 0;
+    /* from the windows' codes written by the fused forward; else, a relu
+     * output still unwritten (a recipe of its input): the kernel reads the
+     * relu's input and takes the relu on load */
+    const unsigned char *codes =
+        n->at.win.codes ? (const unsigned char *)tt_dev(n->at.win.codes) : NULL;
+    if (codes && conv_takes_pooled(r->in[0])) {
+        /* the convolution's weight gradient reads the pool's gradient and
+         * the codes itself: neither gradient is written here */
+        lazy_set(r, n->grad, NULL);
+        lazy_set(r->in[0], n->grad, n->at.win.codes);
+        r->fused = 1;
+        return 1;
+    }
+    Tensor *pre = codes ? NULL : tt_lazy_relu_src(r->val);
+    const float *x = codes ? NULL : pre ? tt_dev(pre) : tt_dev(r->val);
+    if (!codes && !x) return 0;
     /* the relu's own gradient is left as a recipe (nothing in the pass reads
      * it: the relu feeds only this pool and its rule is skipped); the pool's
      * gradient is complete here, as every consumer's rule has run */
     Tensor *u = tt_empty_like(r->in[0]->val);
-    if (!u || (pre ? tt_k_maxpool2x2_prerelu_bwd(x, g, NULL, u->dev, N, C, H, W, Ho, Wo)
-                   : tt_k_maxpool2x2_relu_bwd(x, g, NULL, u->dev, N, C, H, W, Ho, Wo))) {
+    if (!u || (codes ? tt_k_maxpool2x2_code_relu_bwd(codes, g, u->dev, N, C, H, W, Ho, Wo)
+               : pre ? tt_k_maxpool2x2_prerelu_bwd(x, g, NULL, u->dev, N, C, H, W, Ho, Wo)
+                     : tt_k_maxpool2x2_relu_bwd(x, g, NULL, u->dev, N, C, H, W, Ho, Wo))) {
         tt_release(u);
         return 0;
     }
-    r->lazy_g = tt_retain(n->grad);
-    r->lazy_next = g_lazy;
-    g_lazy = r;
+    lazy_set(r, n->grad, NULL);
     accum_move(r->in[0], u);
     r->fused = 1;
     return 1;
@@ -1016,8 +1111,13 @@ static AGNode *schedule(AGNode *root) {
 
 static void run_rules(AGNode *head) {
     for (AGNode *n = head; n; n = n->next) {
-        if (!n->grad || !n->op) continue;
+        if ((!n->grad && !n->lazy_g) || !n->op) continue;
         if (n->fused) continue;          /* its consumer's rule did its work */
+        /* a gradient still a recipe: only the convolution's rule reads one */
+        if (n->lazy_g && n->op != &OP_CONV2D) {
+            materialise(n);
+            if (!n->grad) continue;  /* could not be written (out of memory) */
+        }
         n->op->backward(n);
     }
     for (AGNode *n = head; n; n = n->next) n->fused = 0;
@@ -1258,7 +1358,9 @@ void ag_release(AGNode *n) {
     while (dead) {
         AGNode *d = dead;
         dead = d->next;
-        if (tt_pend.active && tt_pend.out == d->val) tt_flush_pending();
+        if (tt_pend.active && (tt_pend.out == d->val || tt_pend.r == d->val ||
+                               tt_pend.p == d->val || tt_pend.c == d->val))
+            tt_flush_pending();  /* the launch writes into d's tensors */
         tt_release(d->val);
         tt_release(d->grad);
         lazy_drop(d);

@@ -264,8 +264,8 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2)))
 conv_fwd_lds_kernel(const float *__restrict__ x, const float *__restrict__ w,
                     const float *__restrict__ bias, float *__restrict__ out,
                     float *__restrict__ rout, float *__restrict__ /*pout: 3x3 kernel only*/,
-                    float *__restrict__ /*cout*/, float *__restrict__ /*dout*/, Geo g,
-                    int chunks) {
+                    float *__restrict__ /*cout*/, float *__restrict__ /*dout*/,
+                    unsigned char *__restrict__ /*aout*/, Geo g, int chunks) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   constexpr int CHUNK = 128 * PB;
   const int n = blockIdx.x / chunks, chunk = blockIdx.x - n * chunks;
@@ -393,6 +393,24 @@ conv_fwd_lds_kernel(const float *__restrict__ x, const float *__restrict__ w,
   else store(std::false_type{});
 }
 
+// A 2x2 pool window of relu values (>= +0, never NaN) at top-left, top-right,
+// bottom-left, bottom-right: returns its max, and its code -- bits 0-1 the
+// first position holding the max in that order (the order the pool backward
+// scans: maxpool2x2_bwd_kernel), bits 2-5 which of the four are > 0 (the
+// relu backward's mask).  Bit for bit, the pool backward and the relu
+// backward after it need nothing else (maxpool2x2_code_bwd_kernel).
+__device__ __forceinline__ float pool_code(float tl, float tr, float bl, float br,
+                                           unsigned &code) {
+  float m = tl;
+  unsigned am = 0;
+  if (tr > m) { m = tr; am = 1; }
+  if (bl > m) { m = bl; am = 2; }
+  if (br > m) { m = br; am = 3; }
+  code = am | (tl > 0.0f ? 4u : 0u) | (tr > 0.0f ? 8u : 0u) | (bl > 0.0f ? 16u : 0u) |
+         (br > 0.0f ? 32u : 0u);
+  return m;
+}
+
 // ---- forward / dX for KH x KW kernels known at compile time ----
 //
 // Lane half h of the 32x32x2 MFMA takes input channels [h*CH2, (h+1)*CH2)
@@ -412,7 +430,7 @@ __global__ void __launch_bounds__(NT * KS) __attribute__((amdgpu_waves_per_eu(1,
 conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
                   const float *__restrict__ bias, float *__restrict__ out,
                   float *__restrict__ rout, float *__restrict__ pout, float *__restrict__ cout,
-                  float *__restrict__ dout, Geo g, int chunks) {
+                  float *__restrict__ dout, unsigned char *__restrict__ aout, Geo g, int chunks) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   constexpr int CHUNK = 128 * PB, TAPS = KH * KW;
   const int n = blockIdx.x / chunks, chunk = blockIdx.x - n * chunks;
@@ -677,18 +695,36 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
       if (cn) cn[o] = m;
       if (dn) dn[o] = m;
     };
+    // aout (optional): each window's code (pool_code), N x F x Ho/2 x Wo/2 bytes
+    unsigned char *an = aout ? aout + (long)n * g.F * P4 : nullptr;
     if (g.Wo == 32) {  // rows 2i, 2i+1 are blocks j, j+1
 #pragma unroll
       for (int j = 0; j + 1 < PB; j += 2) {
         const int pj = p0 + (pw4 * PB + j) * 32;
         const int prow = pj >> 6;
         const bool lead = (l32 & 1) == 0 && pj < p1;
+        if (an) {
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const float m0 = fmaxf(o[j][r], o[j + 1][r]);
-          const float m = fmaxf(m0, __shfl_xor(m0, 1, 64));
-          const int f = f0 + 8 * (r >> 2) + 4 * half + (r & 3);
-          if (lead && f < g.F) put((long)f * P4 + prow * Wo2 + (l32 >> 1), m);
+          for (int r = 0; r < 16; r++) {
+            const float a = o[j][r], b = o[j + 1][r];
+            const float a1 = __shfl_xor(a, 1, 64), b1 = __shfl_xor(b, 1, 64);
+            unsigned code;
+            const float m = pool_code(a, a1, b, b1, code);
+            const int f = f0 + 8 * (r >> 2) + 4 * half + (r & 3);
+            const long po = (long)f * P4 + prow * Wo2 + (l32 >> 1);
+            if (lead && f < g.F) {
+              put(po, m);
+              an[po] = (unsigned char)code;
+            }
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; r++) {
+            const float m0 = fmaxf(o[j][r], o[j + 1][r]);
+            const float m = fmaxf(m0, __shfl_xor(m0, 1, 64));
+            const int f = f0 + 8 * (r >> 2) + 4 * half + (r & 3);
+            if (lead && f < g.F) put((long)f * P4 + prow * Wo2 + (l32 >> 1), m);
+          }
         }
       }
     } else {  // rows 2i, 2i+1 are lanes l and l ^ Wo of one block
@@ -697,12 +733,29 @@ conv_fwd_k_kernel(const float *__restrict__ x, const float *__restrict__ w,
         const int p = p0 + (pw4 * PB + j) * 32 + l32;
         const int row = p / g.Wo, col = p - row * g.Wo;
         const bool lead = (col & 1) == 0 && (row & 1) == 0 && p < p1;
+        if (an) {
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const float m0 = fmaxf(o[j][r], __shfl_xor(o[j][r], 1, 64));
-          const float m = fmaxf(m0, __shfl_xor(m0, g.Wo, 64));
-          const int f = f0 + 8 * (r >> 2) + 4 * half + (r & 3);
-          if (lead && f < g.F) put((long)f * P4 + (row >> 1) * Wo2 + (col >> 1), m);
+          for (int r = 0; r < 16; r++) {
+            const float a = o[j][r];
+            const float a1 = __shfl_xor(a, 1, 64), b = __shfl_xor(a, g.Wo, 64);
+            const float b1 = __shfl_xor(a, g.Wo ^ 1, 64);
+            unsigned code;
+            const float m = pool_code(a, a1, b, b1, code);
+            const int f = f0 + 8 * (r >> 2) + 4 * half + (r & 3);
+            const long po = (long)f * P4 + (row >> 1) * Wo2 + (col >> 1);
+            if (lead && f < g.F) {
+              put(po, m);
+              an[po] = (unsigned char)code;
+            }
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; r++) {
+            const float m0 = fmaxf(o[j][r], __shfl_xor(o[j][r], 1, 64));
+            const float m = fmaxf(m0, __shfl_xor(m0, g.Wo, 64));
+            const int f = f0 + 8 * (r >> 2) + 4 * half + (r & 3);
+            if (lead && f < g.F) put((long)f * P4 + (row >> 1) * Wo2 + (col >> 1), m);
+          }
         }
       }
     }
@@ -1115,11 +1168,19 @@ conv_dw32_reduce_kernel(const float *__restrict__ part, float *__restrict__ dw,
 // filter 8(r/4) + 4h + r%4, tap 32 jb + l%32.  The bias gradient is summed
 // on the VALU from the same A operands (first group of the first tap set).
 constexpr int DWT_NPQ = 4;  // waves sharing a tap group (pixel quarters)
+constexpr int DWT_UB = 8;   // pooled-gradient items a lane decodes per batch
 
-template <int TG, int NTGW>
+// CODE: gr is the gradient of a 2x2 / stride-2 max pool of the relu of this
+// convolution's output (N x F x Ho/2 x Wo/2) and codes its windows' codes
+// (pool_code): the output gradient rows are decoded into LDS as the pool +
+// relu backward would have written them (maxpool2x2_code_bwd_kernel), so
+// that gradient is never stored.  Needs even RC (or one unit per image),
+// even Ho and Wo % 8 == 0.
+template <int TG, int NTGW, bool CODE = false>
 __global__ void __launch_bounds__(64 * DWT_NPQ * NTGW)
 conv_dwt_kernel(const float *__restrict__ gr, const float *__restrict__ x,
-                float *__restrict__ part, Geo g, int RC, int nch, int GS, int CS, int jbp) {
+                float *__restrict__ part, Geo g, int RC, int nch, int GS, int CS, int jbp,
+                const unsigned char *__restrict__ codes) {
   constexpr int NTH = 64 * DWT_NPQ * NTGW;
   constexpr int SLOT = TG * 1024 + 64;  // one wave's accumulators and bias in LDS
   extern __shared__ __attribute__((aligned(16))) float smem[];
@@ -1144,8 +1205,50 @@ conv_dwt_kernel(const float *__restrict__ gr, const float *__restrict__ x,
   const float *xs = smem + round_up(32 * GS, 256);
 
   // stage g rows (32 x GS), the gapped slab of channels [c0, c1), a zero plane
-  stage_blocks<true, NTH>(smem, gr + (long)n * g.F * P + (long)f0 * P + (long)ho0 * g.Wo,
-                          32 * GS, GS, nf, P, 0, rows * g.Wo);
+  if constexpr (CODE) {
+    // four pixels of one row a lane: two pool windows (a 2-byte code pair,
+    // a float2 of the pooled gradient), written with one 16-byte LDS store;
+    // DWT_UB items a lane at a time, all their loads issued (unconditional,
+    // out-of-range items read window 0) before any is decoded
+    const int Ho2 = g.Ho >> 1, Wo2 = g.Wo >> 1, RWo = rows * g.Wo;
+    const int q4 = GS >> 2, T4 = 32 * q4;
+    const float rcpQ = 1.0f / (float)q4, rcpW = 1.0f / (float)(g.Wo >> 2);
+    const long wbase = ((long)(n * g.F + f0) * Ho2 + (ho0 >> 1)) * Wo2;
+    for (int base = tid; base < T4; base += NTH * DWT_UB) {
+      unsigned c2[DWT_UB], kk[DWT_UB];
+      float2 gv[DWT_UB];
+      bool ok[DWT_UB];
+#pragma unroll
+      for (int u = 0; u < DWT_UB; u++) {
+        const int i = base + u * NTH;
+        const int b = fdiv(i, q4, rcpQ), j = (i - b * q4) * 4;
+        ok[u] = i < T4 && b < nf && j < RWo;
+        const int hr = fdiv(j >> 2, g.Wo >> 2, rcpW);  // row within the unit
+        const int wo = j - hr * g.Wo;
+        const long w2 = ok[u] ? wbase + ((long)b * Ho2 + (hr >> 1)) * Wo2 + (wo >> 1) : 0;
+        kk[u] = ((ho0 + hr) & 1) * 2;
+        c2[u] = *reinterpret_cast<const unsigned short *>(codes + w2);
+        gv[u] = *reinterpret_cast<const float2 *>(gr + w2);
+      }
+#pragma unroll
+      for (int u = 0; u < DWT_UB; u++) {
+        const int i = base + u * NTH;
+        if (i >= T4) break;
+        const float g0 = 0.0f + gv[u].x, g1 = 0.0f + gv[u].y;
+        const unsigned k = kk[u], ca = c2[u] & 0xff, cb = c2[u] >> 8;
+        auto at = [](unsigned c, unsigned kq, float val) {
+          return ((c & 3) == kq && ((c >> (2 + kq)) & 1)) ? val : 0.0f;
+        };
+        const float4 v = ok[u] ? make_float4(at(ca, k, g0), at(ca, k + 1, g0), at(cb, k, g1),
+                                             at(cb, k + 1, g1))
+                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        *reinterpret_cast<float4 *>(smem + i * 4) = v;
+      }
+    }
+  } else {
+    stage_blocks<true, NTH>(smem, gr + (long)n * g.F * P + (long)f0 * P + (long)ho0 * g.Wo,
+                            32 * GS, GS, nf, P, 0, rows * g.Wo);
+  }
   {
     const int hs = ho0 * g.sh - g.ph;
     const int T = (nc + 1) * CS;
@@ -1470,25 +1573,26 @@ bool pool_fusable(const Geo &g, const FwdPlan &pl) {
 
 template <int PB, bool FLIP, bool VEC>
 int launch_fwd(const float *x, const float *w, const float *bias, float *out, float *rout,
-               float *pout, float *cout, float *dout, const Geo &g, int N, const FwdPlan &pl) {
+               float *pout, float *cout, float *dout, unsigned char *aout, const Geo &g, int N,
+               const FwdPlan &pl) {
   auto kern = !is_k3(g)     ? conv_fwd_lds_kernel<PB, FLIP, VEC>
               : pl.ks == 2 ? conv_fwd_k_kernel<PB, FLIP, VEC, 3, 3, 2>
                            : conv_fwd_k_kernel<PB, FLIP, VEC, 3, 3, 1>;
   if (pl.lds > 64 * 1024 && !allow_big_lds((const void *)kern)) return -1;
   const dim3 grid((unsigned)(N * pl.chunks), (unsigned)((g.F + 31) / 32));
   hipLaunchKernelGGL(kern, grid, dim3(NT * pl.ks), pl.lds, stream(), x, w, bias, out, rout, pout,
-                     cout, dout, g, pl.chunks);
+                     cout, dout, aout, g, pl.chunks);
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
 template <bool FLIP>
 int run_fwd(const float *x, const float *w, const float *bias, float *out, const Geo &g, int N,
             bool dry, float *rout = nullptr, float *pout = nullptr, float *cout = nullptr,
-            float *dout = nullptr) {
+            float *dout = nullptr, unsigned char *aout = nullptr) {
   const FwdPlan pl = plan_fwd(g, N, FLIP);
   if (!pl.pb) return -1;
   if (pout && !(!FLIP && pool_fusable(g, pl))) return -1;
-  if ((cout || dout) && !pout) return -1;
+  if ((cout || dout || aout) && !pout) return -1;
   if (dry) return 0;
   if (fail_direct()) return -3;
   // 16-byte loads: 4-aligned rows of x and of the weight blocks (the 3x3
@@ -1502,10 +1606,11 @@ int run_fwd(const float *x, const float *w, const float *bias, float *out, const
                                    : g.K % 4 == 0);
   const bool vec = g.W % 4 == 0 && aligned16(x) && wok;
   if (pl.pb == 2)
-    return vec ? launch_fwd<2, FLIP, true>(x, w, bias, out, rout, pout, cout, dout, g, N, pl)
-               : launch_fwd<2, FLIP, false>(x, w, bias, out, rout, pout, cout, dout, g, N, pl);
-  return vec ? launch_fwd<1, FLIP, true>(x, w, bias, out, rout, pout, cout, dout, g, N, pl)
-             : launch_fwd<1, FLIP, false>(x, w, bias, out, rout, pout, cout, dout, g, N, pl);
+    return vec ? launch_fwd<2, FLIP, true>(x, w, bias, out, rout, pout, cout, dout, aout, g, N, pl)
+               : launch_fwd<2, FLIP, false>(x, w, bias, out, rout, pout, cout, dout, aout, g, N,
+                                            pl);
+  return vec ? launch_fwd<1, FLIP, true>(x, w, bias, out, rout, pout, cout, dout, aout, g, N, pl)
+             : launch_fwd<1, FLIP, false>(x, w, bias, out, rout, pout, cout, dout, aout, g, N, pl);
 }
 
 // dW kernel variants: (MF, JW, KS) with FS = filters/16 per workgroup.
@@ -1727,17 +1832,17 @@ DwtPlan plan_dwt(const Geo &g, int N) {
   return pl;
 }
 
-template <int TG, int NTGW>
+template <int TG, int NTGW, bool CODE = false>
 int launch_dwt(const float *gr, const float *x, float *dw, float *db, const Geo &g,
-               const DwtPlan &pl) {
-  auto kern = conv_dwt_kernel<TG, NTGW>;
+               const DwtPlan &pl, const unsigned char *codes = nullptr) {
+  auto kern = conv_dwt_kernel<TG, NTGW, CODE>;
   if (pl.lds > 64 * 1024 && !allow_big_lds((const void *)kern)) return -1;
   const long S = (long)pl.jbp * 1024 + 32;
   float *part = (float *)ttrt_alloc(sizeof(float) * (size_t)(S * pl.units * pl.nfb));
   if (!part) return -2;
   hipLaunchKernelGGL(kern, dim3((unsigned)pl.units, (unsigned)pl.nts, (unsigned)pl.nfb),
                      dim3(64 * DWT_NPQ * NTGW), pl.lds, stream(), gr, x, part, g, pl.rc, pl.nch,
-                     pl.gs, pl.cs, pl.jbp);
+                     pl.gs, pl.cs, pl.jbp, codes);
   int rc = hipGetLastError() == hipSuccess ? 0 : -3;
   if (rc == 0) {
     const long cols = (long)pl.nfb * (S / 4);
@@ -1760,16 +1865,17 @@ int launch_dwt(const float *gr, const float *x, float *dw, float *db, const Geo 
   return rc;
 }
 
+template <bool CODE>
 int launch_dwt_plan(const float *gr, const float *x, float *dw, float *db, const Geo &g,
-                    const DwtPlan &pl) {
-  if (pl.tg == 1) return launch_dwt<1, 1>(gr, x, dw, db, g, pl);
-  if (pl.tg == 2) return launch_dwt<2, 1>(gr, x, dw, db, g, pl);
+                    const DwtPlan &pl, const unsigned char *codes = nullptr) {
+  if (pl.tg == 1) return launch_dwt<1, 1, CODE>(gr, x, dw, db, g, pl, codes);
+  if (pl.tg == 2) return launch_dwt<2, 1, CODE>(gr, x, dw, db, g, pl, codes);
   if (pl.tg != 3) return -1;
   switch (pl.ntgw) {
-    case 1: return launch_dwt<3, 1>(gr, x, dw, db, g, pl);
-    case 2: return launch_dwt<3, 2>(gr, x, dw, db, g, pl);
-    case 3: return launch_dwt<3, 3>(gr, x, dw, db, g, pl);
-    case 4: return launch_dwt<3, 4>(gr, x, dw, db, g, pl);
+    case 1: return launch_dwt<3, 1, CODE>(gr, x, dw, db, g, pl, codes);
+    case 2: return launch_dwt<3, 2, CODE>(gr, x, dw, db, g, pl, codes);
+    case 3: return launch_dwt<3, 3, CODE>(gr, x, dw, db, g, pl, codes);
+    case 4: return launch_dwt<3, 4, CODE>(gr, x, dw, db, g, pl, codes);
   }
   return -1;
 }
@@ -1834,18 +1940,19 @@ extern "C" int tt_k_conv2d_relu_fwd_lds(const float *x, const float *w, const fl
 // (bit-identical to tt_k_conv2d_relu_fwd_lds followed by the max pool);
 // cout / dout (optional): the pool output flattened per image, as a copy and
 // padded with a last column of ones (a reshape and a padones after it);
-// rout may be NULL (the relu is then only pooled, not stored).
+// rout may be NULL (the relu is then only pooled, not stored); codes
+// (optional): one byte per pool window for tt_k_maxpool2x2_code_relu_bwd.
 // -1: not covered (see pool_fusable).
 extern "C" int tt_k_conv2d_relu_pool_fwd_lds(const float *x, const float *w, const float *bias,
                                              float *out, float *rout, float *pout, float *cout,
-                                             float *dout, int N, int C, int H, int W, int F,
-                                             int HH, int WW, int sh, int sw, int ph, int pw,
-                                             int Ho, int Wo) {
+                                             float *dout, unsigned char *codes, int N, int C,
+                                             int H, int W, int F, int HH, int WW, int sh, int sw,
+                                             int ph, int pw, int Ho, int Wo) {
   if (!x || !w || !out || !pout || out == rout ||
       !geo_ok(N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo))
     return -1;
   const Geo g{C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo, F, C * HH * WW};
-  return run_fwd<false>(x, w, bias, out, g, N, false, rout, pout, cout, dout);
+  return run_fwd<false>(x, w, bias, out, g, N, false, rout, pout, cout, dout, codes);
 }
 
 // dw (F, C*HH*WW) and, when db is given, db (F) from the output gradient g
@@ -1857,7 +1964,7 @@ extern "C" int tt_k_conv2d_dw_lds(const float *gr, const float *x, float *dw, fl
   const Geo g{C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo, F, C * HH * WW};
   if (g_dwt && aligned16(x) && aligned16(gr)) {
     const DwtPlan tp = plan_dwt(g, N);
-    if (tp.tg) return launch_dwt_plan(gr, x, dw, db, g, tp);
+    if (tp.tg) return launch_dwt_plan<false>(gr, x, dw, db, g, tp);
   }
   const DwPlan pl = plan_dw(g, N);
   if (pl.var < 0) return -1;
@@ -1902,6 +2009,27 @@ extern "C" int tt_k_conv2d_dw_lds(const float *gr, const float *x, float *dw, fl
   }
   ttrt_free(part);  // stream-ordered: the kernels above run before any reuse
   return rc;
+}
+
+// dw / db as tt_k_conv2d_dw_lds from the gradient gp of the 2x2 / stride-2
+// max pool of the relu of this convolution's output and the pool windows'
+// codes (tt_k_conv2d_relu_pool_fwd_lds): the output gradient is decoded
+// while it is staged, never stored (bit for bit tt_k_maxpool2x2_code_relu_bwd
+// followed by tt_k_conv2d_dw_lds on its result).  dw == NULL: only reports
+// whether the shape is covered (0) or not (-1).
+extern "C" int tt_k_conv2d_dw_lds_pooled(const float *gp, const unsigned char *codes,
+                                         const float *x, float *dw, float *db, int N, int C,
+                                         int H, int W, int F, int HH, int WW, int sh, int sw,
+                                         int ph, int pw, int Ho, int Wo) {
+  if (!geo_ok(N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo) || Ho % 2 || Wo % 2 || !g_dwt)
+    return -1;
+  const Geo g{C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo, F, C * HH * WW};
+  const DwtPlan tp = plan_dwt(g, N);
+  if (!tp.tg || (tp.rc % 2 && tp.nch > 1)) return -1;
+  if (!dw) return 0;
+  if (!gp || !codes || !x || !aligned16(x) || ((uintptr_t)gp & 7) || ((uintptr_t)codes & 1))
+    return -1;
+  return launch_dwt_plan<true>(gp, x, dw, db, g, tp, codes);
 }
 
 // dx (N,C,H,W) of a stride-1 convolution from the output gradient g

@@ -263,11 +263,18 @@ int tt_flush_pending(void) {
         Tensor *c = kind == TT_PEND_CONV_RELU_POOL_COPY ? tt_pend.c : NULL;
         /* with the pool, the relu output is not stored: it becomes a recipe
          * (relu of the convolution output) run on first use */
+        Tensor *codes = p ? tt_pend.codes : NULL;
         rc = p ? tt_k_conv2d_relu_pool_fwd_lds(tt_pend.x, tt_pend.w, tt_pend.b, tt_pend.out->dev,
-                                               NULL, p->dev, c ? c->dev : NULL, NULL, q[0], q[1],
-                                               q[2], q[3], q[4], q[5], q[6], q[7], q[8], q[9],
-                                               q[10], q[11], q[12])
+                                               NULL, p->dev, c ? c->dev : NULL, NULL,
+                                               codes ? (unsigned char *)codes->dev : NULL,
+                                               q[0], q[1], q[2], q[3], q[4], q[5], q[6], q[7],
+                                               q[8], q[9], q[10], q[11], q[12])
                : -1;
+        if (rc == 0 && codes) {
+            *tt_pend.codes_dst = codes;  /* the pool node owns them now */
+            codes = NULL;
+        }
+        tt_release(codes);  /* not written: the backward reads the relu values */
         if (rc == 0 && tt_lazy_relu(tt_pend.r, tt_pend.out) != 0)
             rc = tt_k_relu_fwd(tt_pend.out->dev, tt_pend.r->dev, tt_pend.r->numel) ? -2 : 0;
         if (rc != 0) {  /* the convolution + relu, then the pool and the copy by themselves */

@@ -228,6 +228,35 @@ __device__ __forceinline__ void argmax4(float v0, float v1, float v2, float v3, 
   if (v3 > m) { m = v3; am = 3; }
 }
 
+// dxr of the 2x2 pool + relu backward from the windows' codes (bits 0-1 the
+// argmax, bits 2-5 the relu mask; pool_code in conv.hip): a thread takes two
+// windows, as maxpool2x2_bwd_kernel, and writes the same values -- the
+// incoming gradient (+0 added, as there) where the argmax is and the relu
+// value is > 0, +0 elsewhere.
+template <typename I>
+__global__ void maxpool2x2_code_bwd_kernel(const unsigned char *__restrict__ codes,
+                                           const float *__restrict__ g, float *__restrict__ dxr,
+                                           int H, int W, int Ho, int Wo, I total) {
+  const int Wq = Wo / 2;
+  const I stride = (I)gridDim.x * blockDim.x;
+  for (I i = (I)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const I r = i / Wq;
+    const int q = (int)(i - r * Wq);
+    const I nc = r / Ho;
+    const int ho = (int)(r - nc * Ho);
+    const long off = ((long)nc * H + 2 * ho) * W + 4 * q;
+    const unsigned c2 = *reinterpret_cast<const unsigned short *>(codes + (long)r * Wo + 2 * q);
+    const float2 gv = *reinterpret_cast<const float2 *>(g + (long)r * Wo + 2 * q);
+    const float g0 = 0.0f + gv.x, g1 = 0.0f + gv.y;
+    const unsigned c0 = c2 & 0xff, c1 = c2 >> 8;
+    auto at = [](unsigned c, unsigned k, float v) {
+      return ((c & 3) == k && ((c >> (2 + k)) & 1)) ? v : 0.0f;
+    };
+    *reinterpret_cast<float4 *>(dxr + off) = make_float4(at(c0, 0, g0), at(c0, 1, g0), at(c1, 0, g1), at(c1, 1, g1));
+    *reinterpret_cast<float4 *>(dxr + off + W) = make_float4(at(c0, 2, g0), at(c0, 3, g0), at(c1, 2, g1), at(c1, 3, g1));
+  }
+}
+
 // RELU: x is the output of a relu whose only consumer is this pool; dxr =
 // relu backward of dx (dx where x > 0, else +0.0f) is written in the same
 // pass (x > 0 exactly when the relu's input is > 0); dx may then be null,
@@ -622,6 +651,22 @@ int tt_k_maxpool2x2_relu_bwd(const float *x, const float *g, float *dx, float *d
 int tt_k_maxpool2x2_prerelu_bwd(const float *xpre, const float *g, float *dx, float *dxr, int N,
                                 int C, int H, int W, int Ho, int Wo) {
   return maxpool2x2_relu_bwd<true>(xpre, g, dx, dxr, N, C, H, W, Ho, Wo);
+}
+
+int tt_k_maxpool2x2_code_relu_bwd(const unsigned char *codes, const float *g, float *dxr, int N,
+                                  int C, int H, int W, int Ho, int Wo) {
+  const long pairs = (long)N * C * Ho * Wo / 2;
+  if (pairs <= 0) return 0;
+  if (W % 4 != 0 || H != 2 * Ho || W != 2 * Wo || !codes || !g || !dxr ||
+      (((uintptr_t)codes & 1) != 0) || (((uintptr_t)dxr & 15) != 0) || (((uintptr_t)g & 7) != 0))
+    return -1;
+  if (pairs < (1L << 31))
+    hipLaunchKernelGGL(maxpool2x2_code_bwd_kernel<unsigned>, dim3(blocks_for(pairs)), dim3(256), 0,
+                       stream(), codes, g, dxr, H, W, Ho, Wo, (unsigned)pairs);
+  else
+    hipLaunchKernelGGL(maxpool2x2_code_bwd_kernel<unsigned long>, dim3(blocks_for(pairs)),
+                       dim3(256), 0, stream(), codes, g, dxr, H, W, Ho, Wo, (unsigned long)pairs);
+  return launched();
 }
 
 int tt_k_maxpool_bwd(const float *x, const float *g, float *dx, int N, int C, int H, int W, int ph,

@@ -47,6 +47,9 @@ typedef struct {
     const float *x, *w, *b;   /* device operands, retained by the node's parents (matmul: b is
                                  the weights' last row when x is a padones input) */
     int geo[13];              /* conv: N C H W F HH WW sh sw ph pw Ho Wo; matmul: M N K */
+    Tensor *codes;            /* *_POOL* kinds: the pool windows' codes (bytes in a float */
+    Tensor **codes_dst;       /* tensor, or NULL), handed to the pool node's field here
+                                 once written */
 } TTPendConv;
 extern TTPendConv tt_pend;
 int tt_flush_pending(void);   /* 0 ok; <0 the pending output is invalid */
