@@ -116,6 +116,14 @@ int tt_k_conv_dcol(int F, int Kc, long Ncol, int HW,
 int tt_k_conv_dw_bias(int F, int Kc, long Ncol, int HW,
                       const float *g, const float *col1, float *dW, float *db);
 
+/* dW = [X, 1]^T * G ((Kx+1) x N) for X (rows x Kx) and G (rows x N): the
+ * weight gradient of a matmul of padones(X) (reference src/autograd.c:168-171
+ * on src/autograd.c:195-212's output) computed from X itself, the ones
+ * column taken as a row of ones in the MFMA tiles -- bit for bit tt_k_gemm on
+ * the padded matrix, where that takes the small-GEMM kernel; -1 elsewhere,
+ * nothing launched. */
+int tt_k_gemm_tn_padones(int rows, int Kx, int N, const float *X, const float *G, float *dW);
+
 /* ---- bandwidth kernels (elementwise.hip / spatial.hip) ---- */
 int tt_k_fill(float *x, long n, float v);
 int tt_k_copy(float *dst, const float *src, long n);

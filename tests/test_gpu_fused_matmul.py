@@ -151,3 +151,78 @@ def test_gemm_bias_relu_pad_vs_padded_product(tlib, M, K, N, epi):
     if epi:
         assert bits_equal(R.to_np((M, N)), orc.relu_fwd(c))
         assert bits_equal(P.to_np((M, N + 1)), orc.padones_fwd(orc.relu_fwd(c)))
+
+
+# (rows, Kx, N, taken): the MLP's first layer (784 -> 512 at batch 256),
+# ragged widths, and a shape the small-GEMM tiles do not take (too few
+# tiles: -1, nothing launched)
+TN_PAD_SHAPES = [(256, 784, 512, True), (200, 1023, 300, True), (512, 390, 700, True),
+                 (300, 33, 257, False)]
+
+
+@pytest.mark.parametrize("rows,Kx,N,taken", TN_PAD_SHAPES)
+def test_gemm_tn_padones_bitexact(tlib, rows, Kx, N, taken):
+    """[X, 1]^T G from X: bit for bit tt_k_gemm on the padded matrix (the
+    ones row is the column sums of G), and within tolerance of float64."""
+    x = np.random.default_rng(5).uniform(-1, 1, (rows, Kx)).astype(np.float32)
+    g = np.random.default_rng(6).standard_normal((rows, N)).astype(np.float32)
+    xp = orc.padones_fwd(x)
+    dx_, dxp, dg = DevBuf.from_np(x), DevBuf.from_np(xp), DevBuf.from_np(g)
+    d1, d2 = DevBuf((Kx + 1) * N), DevBuf((Kx + 1) * N)
+    print("gemm_tn_padones", rows, Kx, N, flush=True)
+    rc = tlib.tt_k_gemm_tn_padones(rows, Kx, N, dx_.ptr, dg.ptr, d1.ptr)
+    if not taken:
+        assert rc == -1
+        return
+    check(rc, "gemm_tn_padones")
+    check(tlib.tt_k_gemm(Kx + 1, N, rows, dxp.ptr, Kx + 1, 1, dg.ptr, N, 0, d2.ptr, N), "gemm")
+    got = d1.to_np((Kx + 1, N))
+    assert np.array_equal(got.view(np.uint32), d2.to_np((Kx + 1, N)).view(np.uint32))
+    ref = xp.astype(np.float64).T @ g.astype(np.float64)
+    assert np.abs(got - ref).max() / np.sqrt(rows) <= 1e-4 * np.abs(g).max()
+
+
+def test_gemm_tn_padones_rejects(tlib):
+    d = DevBuf(16)
+    assert tlib.tt_k_gemm_tn_padones(0, 4, 4, d.ptr, d.ptr, d.ptr) == -1
+    # 4096-row output: the big tiles, not the small-GEMM kernel (buffers of
+    # the full sizes all the same)
+    x, g, dw = DevBuf(4096 * 4095), DevBuf(4096 * 4096), DevBuf(4096 * 4096)
+    assert tlib.tt_k_gemm_tn_padones(4096, 4095, 4096, x.ptr, g.ptr, dw.ptr) == -1
+
+
+@pytest.mark.parametrize("read_first", [False, True])
+def test_autograd_padones_input_unpadded(tlib, read_first):
+    """padones of an input that needs no gradient feeding a matmul (the
+    MLP's first layer): the padded copy is written only when read, the
+    weight gradient comes from the input itself -- values and gradients bit
+    for bit those of the graph with every launch made at once."""
+    from tinytorch_amd.torch_py import Node
+    rng = np.random.default_rng(8)
+    x = rng.uniform(0, 1, (256, 784)).astype(np.float32)
+    w = (rng.standard_normal((785, 512)) * 0.05).astype(np.float32)
+    gy = rng.standard_normal((256, 512)).astype(np.float32)
+
+    def run():
+        X, Wn = Node.leaf(x, False), Node.leaf(w)
+        P = X.padones()
+        pv = P.value() if read_first else None
+        Y = P.matmul(Wn)
+        yv = Y.value()
+        Y.backward(gy)
+        out = [yv, Wn.grad(), P.value()]
+        if read_first:
+            assert np.array_equal(pv, out[2])
+        for nd in (Y, P, X, Wn):
+            nd.release()
+        return out
+
+    prev = tlib.tth_conv_relu_fuse(0)
+    try:
+        ref = run()
+    finally:
+        tlib.tth_conv_relu_fuse(prev)
+    got = run()
+    for a, e in zip(got, ref):
+        assert np.array_equal(a.view(np.uint32), e.view(np.uint32))
+    assert np.array_equal(got[2], orc.padones_fwd(x))

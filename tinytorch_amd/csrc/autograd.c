@@ -426,7 +426,15 @@ AGNode *ag_padones(AGNode *a) {
     if (!x) return NULL;
     Tensor *v = tt_empty_dev(shp, 2);
     if (!v) return NULL;
-    if (tt_k_padones_fwd(x, v->dev, M, K)) { tt_release(v); return NULL; }
+    /* an input that needs no gradient (never changed in place by the
+     * library): the padded copy is a recipe, written when first read -- a
+     * matmul of it reads the input itself, forward (ag_matmul) and for its
+     * weight gradient (tt_k_gemm_tn_padones) */
+    if (!(tt_defer_enabled() && !needs(a) && tt_lazy_padones(v, a->val) == 0) &&
+        tt_k_padones_fwd(x, v->dev, M, K)) {
+        tt_release(v);
+        return NULL;
+    }
     return make_node(v, &OP_PADONES, a, NULL, NULL);
 }
 
@@ -681,6 +689,16 @@ static void backward_matmul(AGNode *n) {
     const float *g = tt_dev(n->grad);
     if (!g) return;
     if (tt_defer_enabled() && backward_matmul_fused(n, g) == 0) return;
+    if (needs(b) && !needs(a) && a->op == &OP_PADONES && K > 1) {
+        /* dB from the padones input: the padded copy is not read */
+        const float *xd = tt_dev(a->in[0]->val);
+        Tensor *gb = xd ? tt_empty_like(b->val) : NULL;
+        if (gb && tt_k_gemm_tn_padones(M, K - 1, N, xd, g, gb->dev) == 0) {
+            accum_move(b, gb);
+            return;
+        }
+        tt_release(gb);
+    }
     if (needs(a)) {  /* dA = g (MxN) * b^T (b is KxN) */
         const float *bd = tt_dev(b->val);
         Tensor *ga = bd ? tt_empty_like(a->val) : NULL;

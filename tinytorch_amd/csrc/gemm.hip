@@ -1492,6 +1492,9 @@ struct SmallOut {
   // relu = relu(C) and pad = [relu, 1] (M x (N+1)) when given
   const float *bias = nullptr;
   float *relu = nullptr, *pad = nullptr;
+  // row ones_m of op(A) is all ones instead of A's (A, m-contiguous, then
+  // has ones_m columns: the padones column [X, 1] of a matrix X)
+  int ones_m = -1;
 };
 
 template <bool A_KC, bool B_NC, bool VA, bool VB>
@@ -1503,7 +1506,9 @@ __device__ __forceinline__ void small_tile(int M, int N, int K, const float *__r
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l32 = lane & 31, h = lane >> 5;
   const int m0 = by * 32, n0 = bx * 32;
-  const int mr = min(m0 + l32, M - 1), nr = min(n0 + l32, N - 1);
+  const bool one = m0 + l32 == out.ones_m;
+  const int mr = min(m0 + l32, out.ones_m >= 0 ? out.ones_m - 1 : M - 1);
+  const int nr = min(n0 + l32, N - 1);
   // this lane's A row / B column: element k at base + k * step
   const float *ap = A_KC ? A + (long)mr * lda : A + mr;
   const long as = A_KC ? 1 : lda;
@@ -1523,6 +1528,10 @@ __device__ __forceinline__ void small_tile(int M, int N, int K, const float *__r
       } else {
 #pragma unroll
         for (int i = 0; i < 4; i++) a[g][i] = kq + i < k1 ? ap[(long)(kq + i) * as] : 0.0f;
+      }
+      if (!A_KC && one) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) a[g][i] = kq + i < k1 ? 1.0f : 0.0f;
       }
       if (VB && kq + 3 < k1) {
         const float4 v = *(const float4 *)(bp + kq);
@@ -1610,10 +1619,12 @@ __device__ __forceinline__ void small_tile(int M, int N, int K, const float *__r
 template <bool A_KC, bool B_NC, bool VA, bool VB>
 __global__ void __launch_bounds__(64 * SW)
 gemm_small_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
-                  const float *__restrict__ B, long ldb, float *__restrict__ C, long ldc, int kc) {
+                  const float *__restrict__ B, long ldb, float *__restrict__ C, long ldc, int kc,
+                  int ones_m) {
   __shared__ float red[(SW - 1) * 16 * 64];
-  small_tile<A_KC, B_NC, VA, VB>(M, N, K, A, lda, B, ldb, SmallOut{C, ldc, nullptr, nullptr, nullptr},
-                                 kc, blockIdx.x, blockIdx.y, red);
+  SmallOut out{C, ldc, nullptr, nullptr, nullptr};
+  out.ones_m = ones_m;
+  small_tile<A_KC, B_NC, VA, VB>(M, N, K, A, lda, B, ldb, out, kc, blockIdx.x, blockIdx.y, red);
 }
 
 // The same tiles with a forward epilogue (SmallOut::bias / relu / pad).
@@ -1676,7 +1687,7 @@ int run_small(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long 
   const bool vb = !B_NC && aligned16(B.p) && B.ld % 4 == 0;
 #define TT_SMALL(VA_, VB_)                                                                      \
   hipLaunchKernelGGL((gemm_small_kernel<A_KC, B_NC, VA_, VB_>), grid, dim3(64 * SW), 0, stream(), \
-                     M, N, K, A.p, A.ld, B.p, B.ld, C, ldc, kc)
+                     M, N, K, A.p, A.ld, B.p, B.ld, C, ldc, kc, -1)
   if (va && vb) TT_SMALL(A_KC, !B_NC);
   else if (va) TT_SMALL(A_KC, false);
   else if (vb) TT_SMALL(false, !B_NC);
@@ -1931,6 +1942,29 @@ extern "C" int tt_k_matmul_bwd_small(const float *A, int M, int K, const float *
   else
     hipLaunchKernelGGL(gemm_small_pair_kernel<false>, dim3((unsigned)(nba + nbb)), dim3(64 * SW),
                        0, stream(), da, db, (int)nba);
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+// dW = [X, 1]^T * G ((Kx + 1) x N; X rows x Kx, G rows x N, row-major and
+// contiguous): the weight gradient of a matmul whose input is padones(X),
+// without the padded copy -- row Kx of the product is the column sums of G,
+// taken by the same MFMA tiles from a row of ones.  Bit for bit
+// tt_k_gemm(Kx + 1, N, rows, [X, 1], Kx + 1, 1, G, N, 0, dW, N), on the
+// shapes where that call takes the small-GEMM tiles; -1 elsewhere (nothing
+// launched).
+extern "C" int tt_k_gemm_tn_padones(int rows, int Kx, int N, const float *X, const float *G,
+                                    float *dW) {
+  if (rows <= 0 || Kx <= 0 || N <= 0 || !X || !G || !dW || g_force_tile >= 0) return -1;
+  const int M = Kx + 1;
+  const Opnd a{X, Kx, 0, 1}, g{G, N, 0, 1};
+  const Plan p = plan(M, N, rows);
+  if (p.tile == T256x256 || p.tile == T256x128 || p.tile == T128x128 ||
+      !small_ok<false, true>(M, N, rows, a, g) || (M + 31) / 32 > 65535)
+    return -1;
+  const int kc = ((rows + SW - 1) / SW + 7) / 8 * 8;
+  const dim3 grid((unsigned)((N + 31) / 32), (unsigned)((M + 31) / 32));
+  hipLaunchKernelGGL((gemm_small_kernel<false, true, false, false>), grid, dim3(64 * SW), 0,
+                     stream(), M, N, rows, X, (long)Kx, G, (long)N, dW, (long)N, kc, Kx);
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
