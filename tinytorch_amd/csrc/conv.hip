@@ -1204,7 +1204,24 @@ conv_dwt_kernel(const float *__restrict__ gr, const float *__restrict__ x,
   const float *gs = smem;
   const float *xs = smem + round_up(32 * GS, 256);
 
-  // stage g rows (32 x GS), the gapped slab of channels [c0, c1), a zero plane
+  // stage the gapped slab of channels [c0, c1) and a zero plane, then g
+  {
+    const int hs = ho0 * g.sh - g.ph;
+    const int T = (nc + 1) * CS;
+    const float rcpC = 1.0f / (float)CS, rcpR = 1.0f / (float)RW;
+    const float *xn = x + ((long)n * g.C + c0) * g.H * g.W;
+    for (int base = wave * 256; base < T; base += NTH * 4) {
+      const int i = base + lane * 4;
+      const int c = fdiv(i, CS, rcpC), rem = i - c * CS;
+      const int slot = fdiv(rem, RW, rcpR), j = rem - slot * RW;
+      const int row = hs + slot;
+      const bool ok = i < T && c < nc && slot < R && j >= G && row >= 0 && row < g.H;
+      dma_dwordx4(ok ? xn + ((long)c * g.H + row) * g.W + (j - G) : g_zero_src,
+                  xs + base);
+    }
+  }
+  // stage g rows (32 x GS) -- after the slab's DMA is issued, so a decode
+  // (CODE) waits on its own loads while the slab is in flight
   if constexpr (CODE) {
     // four pixels of one row a lane: two pool windows (a 2-byte code pair,
     // a float2 of the pooled gradient), written with one 16-byte LDS store;
@@ -1248,21 +1265,6 @@ conv_dwt_kernel(const float *__restrict__ gr, const float *__restrict__ x,
   } else {
     stage_blocks<true, NTH>(smem, gr + (long)n * g.F * P + (long)f0 * P + (long)ho0 * g.Wo,
                             32 * GS, GS, nf, P, 0, rows * g.Wo);
-  }
-  {
-    const int hs = ho0 * g.sh - g.ph;
-    const int T = (nc + 1) * CS;
-    const float rcpC = 1.0f / (float)CS, rcpR = 1.0f / (float)RW;
-    const float *xn = x + ((long)n * g.C + c0) * g.H * g.W;
-    for (int base = wave * 256; base < T; base += NTH * 4) {
-      const int i = base + lane * 4;
-      const int c = fdiv(i, CS, rcpC), rem = i - c * CS;
-      const int slot = fdiv(rem, RW, rcpR), j = rem - slot * RW;
-      const int row = hs + slot;
-      const bool ok = i < T && c < nc && slot < R && j >= G && row >= 0 && row < g.H;
-      dma_dwordx4(ok ? xn + ((long)c * g.H + row) * g.W + (j - G) : g_zero_src,
-                  xs + base);
-    }
   }
 
   // this lane's tap offsets inside the slab (taps past K: the zero plane)
