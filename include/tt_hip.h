@@ -58,6 +58,23 @@ int tt_k_gemm(int M, int N, int K,
               const float *B, int ldb, int transB,
               float *C, int ldc);
 
+/* C = A * B + bias (row-major; bias a row of N) with the softmax-CE of C's
+ * rows in the GEMM's split-K reduction: probs, seed = (p - onehot(label)) *
+ * scale and rowloss[r] = -log max(p[label], 1e-12), labels on the host
+ * (M <= TT_CE_ARG_ROWS, N <= 32) -- the matmul of the classifier and
+ * softmax-CE of the reference harness (tests/gate_cifar_cnn.py:175-181)
+ * in one pass over the partial products, bit for bit the GEMM followed by
+ * tt_k_softmax_ce_mean_hostlab (whose mean the row losses give, summed in
+ * its order, by tt_k_ce_mean_rows).  0: all written; 1: only C (the GEMM
+ * took no split-K path; run the softmax-CE); < 0: error. */
+int tt_k_gemm_bias_ce(int M, int N, int K, const float *A, const float *B, const float *bias,
+                      float *C, const int32_t *host_labels, float *probs, float *seed,
+                      float *rowloss, float scale);
+/* loss[0] = the mean of rowloss (rows floats) summed as
+ * tt_k_softmax_ce_mean_hostlab sums its row losses (the loss of a
+ * tt_k_gemm_bias_ce pass) */
+int tt_k_ce_mean_rows(const float *rowloss, float *loss, int rows);
+
 /* tt_k_gemm without any device allocation.  No counterpart in the
  * reference: it is for callers that cannot allocate (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  Same

@@ -226,3 +226,88 @@ def test_autograd_padones_input_unpadded(tlib, read_first):
     for a, e in zip(got, ref):
         assert np.array_equal(a.view(np.uint32), e.view(np.uint32))
     assert np.array_equal(got[2], orc.padones_fwd(x))
+
+
+# (M, N, K): the CNN classifier (128 x 4096 -> 10), the MLP's last layer
+# (256 x 256 -> 10), wider rows, and a shape whose GEMM takes no split-K path
+CE_SHAPES = [(128, 10, 4096), (256, 10, 256), (100, 32, 2000), (7, 3, 4100), (512, 10, 64)]
+
+
+@pytest.mark.parametrize("M,N,K", CE_SHAPES)
+def test_gemm_bias_ce_matches_unfused(tlib, M, N, K):
+    """The softmax-CE inside the classifier GEMM's split-K reduction: logits,
+    probabilities, seed and (through tt_k_ce_mean_rows) the mean loss bit for
+    bit those of the GEMM followed by the one-workgroup softmax-CE kernel;
+    labels out of range included.  Return 1 (a GEMM without split-K): the
+    logits only."""
+    r = np.random.default_rng(11)
+    a = r.uniform(-1, 1, (M, K)).astype(np.float32)
+    b = (r.standard_normal((K, N)) * 0.1).astype(np.float32)
+    bias = r.standard_normal(N).astype(np.float32)
+    y = r.integers(0, N, M).astype(np.int32)
+    y[::13] = N + 2
+    da, db, dbias = DevBuf.from_np(a), DevBuf.from_np(b), DevBuf.from_np(bias)
+    c1, p1, s1, rl, l1 = DevBuf(M * N), DevBuf(M * N), DevBuf(M * N), DevBuf(M), DevBuf(1)
+    c2, p2, s2, l2 = DevBuf(M * N), DevBuf(M * N), DevBuf(M * N), DevBuf(1)
+    scale = ctypes.c_float(1.0 / M)
+    print("gemm_bias_ce", M, N, K, flush=True)
+    rc = tlib.tt_k_gemm_bias_ce(M, N, K, da.ptr, db.ptr, dbias.ptr, c1.ptr, y.ctypes.data,
+                                p1.ptr, s1.ptr, rl.ptr, scale)
+    assert rc in (0, 1), rc
+    check(tlib.tt_k_gemm_bias_relu_pad(M, N, K, da.ptr, db.ptr, dbias.ptr, c2.ptr, None, None),
+          "gemm bias")
+    assert bits_equal(c1.to_np((M, N)), c2.to_np((M, N)))
+    if (M, N, K) in ((128, 10, 4096), (256, 10, 256)):
+        assert rc == 0  # the two configs' classifiers take split-K
+    if rc == 1:
+        return
+    check(tlib.tt_k_softmax_ce_mean_hostlab(c2.ptr, y.ctypes.data, p2.ptr, l2.ptr, s2.ptr, M, N,
+                                            scale), "ce")
+    check(tlib.tt_k_ce_mean_rows(rl.ptr, l1.ptr, M), "mean")
+    assert bits_equal(p1.to_np((M, N)), p2.to_np((M, N)))
+    assert bits_equal(s1.to_np((M, N)), s2.to_np((M, N)))
+    assert bits_equal(l1.to_np((1,)), l2.to_np((1,)))
+
+
+@pytest.mark.parametrize("read_loss", ["before", "after", "never"])
+def test_autograd_classifier_ce_in_reduction(tlib, read_loss):
+    """padones -> matmul -> softmax_ce (the classifier layer): the CE joins
+    the pending GEMM's reduction and the mean loss is written when read --
+    loss, logits, probabilities and gradients bit for bit those of the same
+    graph whose logits are read before the softmax-CE (the GEMM then runs by
+    itself and the one-workgroup CE kernel after it)."""
+    from tinytorch_amd.torch_py import Node
+    r = np.random.default_rng(12)
+    x = r.uniform(0, 1, (128, 4096)).astype(np.float32)
+    w = (r.standard_normal((4097, 10)) * 0.02).astype(np.float32)
+    y = r.integers(0, 10, 128)
+
+    def run(join):
+        X, Wn = Node.leaf(x), Node.leaf(w)
+        P = X.padones()
+        Z = P.matmul(Wn)
+        if not join:
+            Z.value()
+        L = Z.softmax_ce(y)
+        out = []
+        if read_loss == "before":
+            out.append(L.value())
+        L.backward(None)
+        if read_loss == "after":
+            out.append(L.value())
+        out += [Z.value(), Wn.grad(), X.grad()]
+        for nd in (L, Z, P, X, Wn):
+            nd.release()
+        return out
+
+    ref = run(False)
+    got = run(True)
+    for g, e in zip(got, ref):
+        assert bits_equal(g, e)
+    wp = np.concatenate([x, np.ones((128, 1), np.float32)], 1)
+    z = wp.astype(np.float64) @ w.astype(np.float64)
+    p = np.exp(z - z.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    if read_loss != "never":
+        loss = -np.log(p[np.arange(128), y]).mean()
+        assert abs(float(got[0][0]) - loss) <= 1e-4 * max(1.0, abs(loss))

@@ -115,6 +115,8 @@ SIGNATURES = [
     ("tt_k_gemm", _I, [_I, _I, _I, VP, _I, _I, VP, _I, _I, VP, _I]),
     ("tt_k_head_bwd", _I, [VP, _I, _I, VP, _I, VP, VP, VP, VP, VP, VP]),
     ("tt_k_gemm_tn_padones", _I, [_I, _I, _I, VP, VP, VP]),
+    ("tt_k_gemm_bias_ce", _I, [_I, _I, _I, VP, VP, VP, VP, VP, VP, VP, VP, ctypes.c_float]),
+    ("tt_k_ce_mean_rows", _I, [VP, VP, _I]),
     ("tt_k_matmul_bwd_small", _I, [VP, _I, _I, VP, _I, VP, VP, VP, VP, VP, VP]),
     ("tt_k_matmul_naive", _I, [VP, VP, VP, _I, _I, _I]),
     ("tt_k_gemm_noalloc", _I, [_I, _I, _I, VP, _I, _I, VP, _I, _I, VP, _I]),

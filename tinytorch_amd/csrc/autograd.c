@@ -538,6 +538,32 @@ AGNode *ag_softmax_ce(AGNode *logits, const int *labels, long rows) {
     int32_t *hlab = (int32_t *)malloc(sizeof(int32_t) * (size_t)rows);
     if (hlab)
         for (long r = 0; r < rows; r++) hlab[r] = (int32_t)labels[r];
+    if (tt_pend.active == TT_PEND_MATMUL && tt_pend.out == logits->val && tt_pend.b && probs &&
+        seed && loss && hlab && rows <= TT_CE_ARG_ROWS && cols <= 32) {
+        /* the classifier's GEMM is still pending: the softmax-CE runs in its
+         * split-K reduction, and the mean loss becomes a recipe of the row
+         * losses (nothing in the backward reads it) */
+        Tensor *rl = tt_empty_dev(&rows, 1);
+        const TTPendConv p = tt_pend;
+        tt_pend.active = 0;
+        const int rc = rl ? tt_k_gemm_bias_ce(p.geo[0], p.geo[1], p.geo[2], p.x, p.w, p.b,
+                                              p.out->dev, hlab, probs->dev, seed->dev, rl->dev,
+                                              1.0f / (float)rows)
+                          : -1;
+        if (rc == 0 && (tt_lazy_ce_mean(loss, rl) == 0 ||
+                        tt_k_ce_mean_rows(rl->dev, loss->dev, (int)rows) == 0)) {
+            tt_release(rl);
+            AGNode *n = make_node(loss, &OP_SOFTMAX_CE, logits, NULL, NULL);
+            if (!n) { tt_release(probs); tt_release(seed); free(hlab); return NULL; }
+            n->at.ce.probs = probs;
+            n->at.ce.seed = seed;
+            n->at.ce.labels = hlab;
+            return n;
+        }
+        tt_release(rl);
+        if (rc < 0) tt_pend = p;  /* not run: the pending GEMM is launched below */
+        /* else the GEMM wrote the logits: the softmax-CE runs below */
+    }
     const float *x = tt_dev(logits->val);
     if (!x) {
         tt_release(probs); tt_release(seed); tt_release(loss); free(hlab);

@@ -543,6 +543,58 @@ add_outside_kernel(float *__restrict__ c, const float *__restrict__ cin, int M, 
 
 }  // namespace
 
+// The split-K reduction of a GEMM whose rows go straight into softmax-CE
+// (the classifier): each element summed exactly as gemm.hip's reduce_one
+// (lanes ty = 0..ZL-1 add partials z = ty, ty + ZL, ... in order, then lane
+// 0 adds the lanes' sums in lane order) plus bias, stored to C; a workgroup
+// holds rpb whole rows (ZL x rpb*N threads), so after a barrier thread r
+// runs ce_row on row r from LDS.  The same bits as the reduction followed by
+// softmax_ce_mean_kernel (whose per-row losses ttk_ce_mean_rows adds).
+template <int ZL, int MAXC>
+__global__ void __launch_bounds__(1024)
+splitk_reduce_ce_kernel(const float *__restrict__ ws, float *__restrict__ C, int M, int N, int S,
+                        int rpb, const float *__restrict__ bias, LabU8 lab,
+                        float *__restrict__ probs, float *__restrict__ seed,
+                        float *__restrict__ rowloss, float scale) {
+  extern __shared__ float sm[];
+  const int XL = rpb * N;
+  float *part = sm, *lv = sm + ZL * XL;
+  const int tx = threadIdx.x % XL, ty = threadIdx.x / XL;
+  const long total = (long)M * N;
+  const long idx = (long)blockIdx.x * XL + tx;
+  float s = 0.f;
+  if (idx < total) {
+#pragma unroll 4
+    for (int z = ty; z < S; z += ZL) s += ws[z * total + idx];
+  }
+  part[ty * XL + tx] = s;
+  __syncthreads();
+  if (ty == 0) {
+    for (int j = 1; j < ZL; j++) s += part[j * XL + tx];
+    if (idx < total) {
+      const float v = bias ? s + bias[tx % N] : s;
+      C[idx] = v;
+      lv[tx] = v;
+    }
+  }
+  __syncthreads();
+  const int r = threadIdx.x;
+  const long row = (long)blockIdx.x * rpb + r;
+  if (r < rpb && row < M)
+    rowloss[row] = ce_row<MAXC>(lv + r * N, lab[(int)row], probs + row * N, seed + row * N, N,
+                                scale);
+}
+
+// loss[0] = the mean of rowloss as softmax_ce_mean_kernel forms it (thread t
+// adds rows t, t + 256, ... in order, then ce_mean_tree)
+__global__ void __launch_bounds__(256)
+ce_mean_rows_kernel(const float *__restrict__ rowloss, float *__restrict__ loss, int rows) {
+  __shared__ float part[256];
+  float acc = 0.0f;
+  for (int r = threadIdx.x; r < rows; r += 256) acc += rowloss[r];
+  ce_mean_tree(acc, part, loss, rows);
+}
+
 extern "C" {
 
 int tt_k_fill(float *x, long n, float v) { return run_map(n, a16(x), FillOp{x, v}); }
@@ -710,6 +762,39 @@ extern "C" int ttk_bias_relu_pad(float *c, const float *bias, float *r, float *p
   if (M >= 65536) return -1;
   hipLaunchKernelGGL(bias_relu_pad_rows_kernel, dim3((unsigned)((N + 1 + 1023) / 1024), (unsigned)M),
                      dim3(256), 0, stream(), c, bias, r, p, N);
+  return launched();
+}
+
+extern "C" int ttk_reduce_ce(const float *ws, float *C, int M, int N, int S, int zl,
+                             const TTCeHook *h) {
+  if (M <= 0 || N <= 0 || N > 32 || M > TT_CE_ARG_ROWS || N * zl > 1024 || !h->host_labels)
+    return 1;
+  LabU8 lu;
+  lab_u8_fill(lu, h->host_labels, M, N);
+  const int rpb = 1024 / (zl * N);
+  const int XL = rpb * N;
+  const size_t lds = sizeof(float) * (size_t)(zl * XL + XL);
+  const dim3 grid((unsigned)((M + rpb - 1) / rpb));
+#define TT_RCE(ZL_, MC_)                                                                    \
+  hipLaunchKernelGGL((splitk_reduce_ce_kernel<ZL_, MC_>), grid, dim3(ZL_ * XL), lds, stream(), \
+                     ws, C, M, N, S, rpb, h->bias, lu, h->probs, h->seed, h->rowloss, h->scale)
+#define TT_RCE2(ZL_)                  \
+  case ZL_:                           \
+    if (N <= 16) TT_RCE(ZL_, 16);     \
+    else TT_RCE(ZL_, 32);             \
+    break;
+  switch (zl) {
+    TT_RCE2(1) TT_RCE2(2) TT_RCE2(4) TT_RCE2(8) TT_RCE2(16) TT_RCE2(32)
+    default: return 1;
+  }
+#undef TT_RCE2
+#undef TT_RCE
+  return launched();
+}
+
+extern "C" int tt_k_ce_mean_rows(const float *rowloss, float *loss, int rows) {
+  if (rows <= 0) return -1;
+  hipLaunchKernelGGL(ce_mean_rows_kernel, dim3(1), dim3(256), 0, stream(), rowloss, loss, rows);
   return launched();
 }
 

@@ -1401,12 +1401,13 @@ void launch_tile(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, lo
 // The epilogue that tt_k_gemm_relu_pad asks of the split-K reduction writing
 // its C; `applied` tells it whether the GEMM took a split-K path (else it
 // launches the epilogue on its own).
-enum { HOOK_RELU_PAD = 1 };
+enum { HOOK_RELU_PAD = 1, HOOK_CE = 2 };
 struct RedHook {
   int kind;
   const float *C;
   ReluPadEx rp;
-  int applied;
+  const TTCeHook *ce;  // HOOK_CE: the softmax-CE that follows (rp.bias is the bias)
+  int applied;         // 1: the epilogue ran in the reduction; 2: the CE too
 };
 RedHook *g_red_hook = nullptr;
 
@@ -1417,6 +1418,14 @@ int reduce_hooked(const float *ws, int M, int N, int S) {
   int zl = 1;
   while (zl < 32 && zl < S && (total * zl * 2) <= 2048L * 256) zl *= 2;
   if (zl < 4 && S >= 4) zl = 4;
+  if (h.kind == HOOK_CE) {
+    const int rc = ttk_reduce_ce(ws, C, M, N, S, zl, h.ce);
+    if (rc < 0) return rc;
+    if (rc == 0) {
+      h.applied = 2;
+      return 0;
+    }
+  }
 #define TT_HK(ZL_)                                                                            \
   case ZL_:                                                                                   \
     hipLaunchKernelGGL((splitk_reduce_relu_pad_kernel<ZL_>),                                  \
@@ -2006,6 +2015,40 @@ extern "C" int tt_k_gemm_bias_relu_pad(int M, int N, int K, const float *A, cons
   g_red_hook = nullptr;
   if (rc) return rc;
   return h.applied ? 0 : ttk_bias_relu_pad(C, bias, R, P, M, N);
+}
+
+// C = A * B + bias as tt_k_gemm_bias_relu_pad (C only) and, when the GEMM
+// takes a split-K path, the softmax-CE of C's rows in its reduction
+// (ttk_reduce_ce: probs, seed, rowloss).  0: all written; 1: only C (the
+// caller runs the softmax-CE); < 0: error.
+extern "C" int tt_k_gemm_bias_ce(int M, int N, int K, const float *A, const float *B,
+                                 const float *bias, float *C, const int32_t *host_labels,
+                                 float *probs, float *seed, float *rowloss, float scale) {
+  if (M <= 0 || N <= 0 || K < 0 || !A || !B || !bias || !C || !host_labels || !probs || !seed ||
+      !rowloss)
+    return -1;
+  const Opnd a{A, K, 0, 1}, b{B, N, 0, 1};
+  auto big = [](const Plan &p) {
+    return p.tile == T256x256 || p.tile == T256x128 || p.tile == T128x128;
+  };
+  if (K > 0 && g_force_tile < 0 && !big(plan(M, N, K)) && small_ok<true, true>(M, N, K, a, b)) {
+    const int rc = tt_k_gemm_bias_relu_pad(M, N, K, A, B, bias, C, nullptr, nullptr);
+    return rc ? rc : 1;
+  }
+  const TTCeHook ce{bias, host_labels, probs, seed, rowloss, scale};
+  RedHook h{};
+  h.kind = HOOK_CE;
+  h.C = C;
+  h.rp = ReluPadEx{nullptr, nullptr, bias};
+  h.ce = &ce;
+  g_red_hook = &h;
+  const int rc = tt_k_gemm(M, N, K, A, K, 0, B, N, 0, C, N);
+  g_red_hook = nullptr;
+  if (rc) return rc;
+  if (h.applied == 2) return 0;
+  if (h.applied == 1) return 1;
+  const int rb = ttk_bias_relu_pad(C, bias, nullptr, nullptr, M, N);
+  return rb ? rb : 1;
 }
 
 // ---- the GEMM without allocation (tt_k_gemm_noalloc) ----

@@ -96,28 +96,30 @@ Tensor *tt_retain(Tensor *t) {
     return t;
 }
 
-/* Tensors whose payload is a recipe not yet run: t = relu(src) or
- * t = padones(src), written by the first accessor that needs it (tt_dev /
+/* Tensors whose payload is a recipe not yet run: t = relu(src),
+ * t = padones(src) or t = the mean loss of the row losses src, written by the first accessor that needs it (tt_dev /
  * tt_data of t), or before the host may write src (tt_data of src).  src is
  * retained meanwhile; a tensor released unread is never written.  The fused
  * convolution + relu + pool forward registers its relu output this way (the
  * pool is computed from the relu values in registers and the pool backward
- * reads the convolution output or the windows' codes), and ag_padones the
+ * reads the convolution output or the windows' codes), ag_padones the
  * padded copy of an input that needs no gradient (the matmul reads the
- * input itself, forward and backward). */
+ * input itself, forward and backward), and ag_softmax_ce the loss of a
+ * softmax-CE computed in its classifier's GEMM (the backward reads only
+ * the seed). */
 typedef struct TTLazyVal {
     Tensor *t, *src;
-    int padones;               /* 0: relu(src); 1: padones(src) */
+    int kind;                  /* 0: relu(src); 1: padones(src); 2: mean of src */
     struct TTLazyVal *next;
 } TTLazyVal;
 static TTLazyVal *g_lazy_vals;
 
-static int lazy_add(Tensor *t, Tensor *src, int padones) {
+static int lazy_add(Tensor *t, Tensor *src, int kind) {
     TTLazyVal *l = (TTLazyVal *)malloc(sizeof(TTLazyVal));
     if (!l) return -1;
     l->t = t;
     l->src = tt_retain(src);
-    l->padones = padones;
+    l->kind = kind;
     l->next = g_lazy_vals;
     g_lazy_vals = l;
     return 0;
@@ -125,10 +127,11 @@ static int lazy_add(Tensor *t, Tensor *src, int padones) {
 
 int tt_lazy_relu(Tensor *t, Tensor *src) { return lazy_add(t, src, 0); }
 int tt_lazy_padones(Tensor *t, Tensor *src) { return lazy_add(t, src, 1); }
+int tt_lazy_ce_mean(Tensor *t, Tensor *src) { return lazy_add(t, src, 2); }
 
 Tensor *tt_lazy_relu_src(const Tensor *t) {
     for (TTLazyVal *l = g_lazy_vals; l; l = l->next)
-        if (l->t == t && !l->padones) return l->src;
+        if (l->t == t && l->kind == 0) return l->src;
     return NULL;
 }
 
@@ -143,9 +146,10 @@ static void lazy_take(const Tensor *t, int from, int drop) {
         if (!drop) {
             const float *x = tt_dev(l->src);
             const int rc = !x ? -1
-                           : l->padones ? tt_k_padones_fwd(x, l->t->dev, l->t->shape[0],
-                                                           l->t->shape[1] - 1)
-                                        : tt_k_relu_fwd(x, l->t->dev, l->t->numel);
+                           : l->kind == 1 ? tt_k_padones_fwd(x, l->t->dev, l->t->shape[0],
+                                                             l->t->shape[1] - 1)
+                           : l->kind == 2 ? tt_k_ce_mean_rows(x, l->t->dev, (int)l->src->numel)
+                                          : tt_k_relu_fwd(x, l->t->dev, l->t->numel);
             if (rc != 0) l->t->valid = 0;
             else tt_mark_dev_written(l->t);
         }

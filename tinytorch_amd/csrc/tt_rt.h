@@ -43,6 +43,20 @@ int    ttk_add_outside(float *c, const float *cin, int M, int N, int mb, int nb)
 /* elementwise.hip: c[m][n] += bias[n] for the M x N matrix c, and when r / p
  * are given r = relu(c), p = [r, 1] (M x N+1) */
 int    ttk_bias_relu_pad(float *c, const float *bias, float *r, float *p, int M, int N);
+/* elementwise.hip: the split-K reduction of a GEMM (ws: S partial M x N
+ * products, summed as gemm.hip's reduce_one does with zl lanes an element)
+ * plus bias into C, and the softmax-CE of C's rows in the same launch:
+ * probs, seed = (p - onehot(label)) * scale, rowloss[r] = -log p[label];
+ * labels on the host (rows <= TT_CE_ARG_ROWS).  1: shape not covered
+ * (N * zl > 1024, N > 32), nothing launched. */
+typedef struct {
+    const float *bias;
+    const int32_t *host_labels;
+    float *probs, *seed, *rowloss;
+    float scale;
+} TTCeHook;
+int    ttk_reduce_ce(const float *ws, float *C, int M, int N, int S, int zl, const TTCeHook *h);
+
 /* gemm.hip: look up, on the current device, the device address of the
  * static scratch array behind tt_k_gemm_noalloc; 0 ok */
 int    ttg_scratch_setup(void);
