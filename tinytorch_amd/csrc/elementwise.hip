@@ -595,6 +595,64 @@ ce_mean_rows_kernel(const float *__restrict__ rowloss, float *__restrict__ loss,
   ce_mean_tree(acc, part, loss, rows);
 }
 
+// C = A * B + bias for a skinny B (N <= MAXN columns): one workgroup per
+// row of A.  Thread t forms the N dot-product pieces over k = t, t + 256, ...
+// (fused multiply-adds, in k order), the 256 pieces of each column are added
+// in a fixed tree through LDS, and the row's epilogue follows in the same
+// launch: relu / padded relu (R, P), or the softmax-CE of the row (CE:
+// probabilities, seed, the row's loss).  The classifier layer (N = 10),
+// where a 64-wide MFMA tile would be 84 % padding and a split-K reduction a
+// second launch.
+template <int MAXN, bool CE>
+__global__ void __launch_bounds__(256)
+gemm_rows_kernel(const float *__restrict__ A, const float *__restrict__ B,
+                 const float *__restrict__ bias, float *__restrict__ C, float *__restrict__ R,
+                 float *__restrict__ P, int N, int K, LabU8 lab, float *__restrict__ probs,
+                 float *__restrict__ seed, float *__restrict__ rowloss, float scale) {
+  __shared__ float part[MAXN][256];
+  __shared__ float lv[MAXN];
+  const int t = threadIdx.x;
+  const long m = blockIdx.x;
+  const float *__restrict__ a = A + m * K;
+  float acc[MAXN];
+#pragma unroll
+  for (int n = 0; n < MAXN; n++) acc[n] = 0.0f;
+#pragma unroll 4
+  for (int k = t; k < K; k += 256) {
+    const float av = a[k];
+    const float *__restrict__ b = B + (long)k * N;
+#pragma unroll
+    for (int n = 0; n < MAXN; n++)
+      if (n < N) acc[n] = fmaf(av, b[n], acc[n]);
+  }
+#pragma unroll
+  for (int n = 0; n < MAXN; n++) part[n][t] = acc[n];
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (t < o) {
+#pragma unroll
+      for (int n = 0; n < MAXN; n++) part[n][t] += part[n][t + o];
+    }
+    __syncthreads();
+  }
+  if (t < N) {
+    const float v = part[t][0] + bias[t];
+    C[m * N + t] = v;
+    const float o = v > 0.0f ? v : 0.0f;
+    if (R) R[m * N + t] = o;
+    if (P) {
+      P[m * (N + 1) + t] = o;
+      if (t == 0) P[m * (N + 1) + N] = 1.0f;
+    }
+    lv[t] = v;
+  }
+  if constexpr (CE) {
+    __syncthreads();
+    if (t == 0)
+      rowloss[m] = ce_row<MAXN>(lv, lab[(int)m], probs + m * N, seed + m * N, N, scale);
+  }
+}
+
 extern "C" {
 
 int tt_k_fill(float *x, long n, float v) { return run_map(n, a16(x), FillOp{x, v}); }
@@ -762,6 +820,24 @@ extern "C" int ttk_bias_relu_pad(float *c, const float *bias, float *r, float *p
   if (M >= 65536) return -1;
   hipLaunchKernelGGL(bias_relu_pad_rows_kernel, dim3((unsigned)((N + 1 + 1023) / 1024), (unsigned)M),
                      dim3(256), 0, stream(), c, bias, r, p, N);
+  return launched();
+}
+
+extern "C" int ttk_gemm_rows(const float *A, const float *B, const float *bias, float *C,
+                             float *R, float *P, int M, int N, int K, const TTCeHook *ce) {
+  // K <= 1024: four k a thread at most (at the CNN classifier's K = 4096
+  // with 128 rows, one workgroup a row measured slower than split-K)
+  if (M <= 0 || N <= 0 || N > 16 || K < 0 || K > 1024 || !bias || (ce && (M > TT_CE_ARG_ROWS ||
+                                                             !ce->host_labels)))
+    return 1;
+  LabU8 lu;
+  if (ce) lab_u8_fill(lu, ce->host_labels, M, N);
+  if (ce)
+    hipLaunchKernelGGL((gemm_rows_kernel<16, true>), dim3((unsigned)M), dim3(256), 0, stream(), A,
+                       B, bias, C, R, P, N, K, lu, ce->probs, ce->seed, ce->rowloss, ce->scale);
+  else
+    hipLaunchKernelGGL((gemm_rows_kernel<16, false>), dim3((unsigned)M), dim3(256), 0, stream(),
+                       A, B, bias, C, R, P, N, K, lu, nullptr, nullptr, nullptr, 0.0f);
   return launched();
 }
 

@@ -1987,6 +1987,10 @@ extern "C" int tt_k_gemm_bias_relu_pad(int M, int N, int K, const float *A, cons
                                        const float *bias, float *C, float *R, float *P) {
   if (M <= 0 || N <= 0 || K < 0 || !A || !B || !bias || !C || (!R && P) || (R && !P))
     return -1;
+  if (g_force_tile < 0) {  // skinny outputs (a classifier): a workgroup per row
+    const int rr = ttk_gemm_rows(A, B, bias, C, R, P, M, N, K, nullptr);
+    if (rr != 1) return rr;
+  }
   const Opnd a{A, K, 0, 1}, b{B, N, 0, 1};
   auto big = [](const Plan &p) {
     return p.tile == T256x256 || p.tile == T256x128 || p.tile == T128x128;
@@ -2028,6 +2032,15 @@ extern "C" int tt_k_gemm_bias_ce(int M, int N, int K, const float *A, const floa
       !rowloss)
     return -1;
   const Opnd a{A, K, 0, 1}, b{B, N, 0, 1};
+  const TTCeHook ce{bias, host_labels, probs, seed, rowloss, scale};
+  if (g_force_tile < 0) {  // skinny outputs: a workgroup per row, the CE in its epilogue
+    const int rr = ttk_gemm_rows(A, B, bias, C, nullptr, nullptr, M, N, K, &ce);
+    if (rr != 1) return rr;
+    // too many rows for the CE's labels: the logits as tt_k_gemm_bias_relu_pad
+    // forms them, the CE the caller's
+    const int rc = ttk_gemm_rows(A, B, bias, C, nullptr, nullptr, M, N, K, nullptr);
+    if (rc != 1) return rc ? rc : 1;
+  }
   auto big = [](const Plan &p) {
     return p.tile == T256x256 || p.tile == T256x128 || p.tile == T128x128;
   };
@@ -2035,7 +2048,6 @@ extern "C" int tt_k_gemm_bias_ce(int M, int N, int K, const float *A, const floa
     const int rc = tt_k_gemm_bias_relu_pad(M, N, K, A, B, bias, C, nullptr, nullptr);
     return rc ? rc : 1;
   }
-  const TTCeHook ce{bias, host_labels, probs, seed, rowloss, scale};
   RedHook h{};
   h.kind = HOOK_CE;
   h.C = C;

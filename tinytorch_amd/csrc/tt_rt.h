@@ -56,6 +56,13 @@ typedef struct {
     float scale;
 } TTCeHook;
 int    ttk_reduce_ce(const float *ws, float *C, int M, int N, int S, int zl, const TTCeHook *h);
+/* elementwise.hip: C = A * B + bias (A M x K, B K x N row-major) for N <= 16,
+ * one workgroup per row, with R = relu(C) / P = [relu(C), 1] when given, or
+ * with the softmax-CE of each row when ce is given (ce->bias unused).  1:
+ * not covered (N > 16, K > 1024; with ce, M > TT_CE_ARG_ROWS), nothing
+ * launched. */
+int    ttk_gemm_rows(const float *A, const float *B, const float *bias, float *C, float *R,
+                     float *P, int M, int N, int K, const TTCeHook *ce);
 
 /* gemm.hip: look up, on the current device, the device address of the
  * static scratch array behind tt_k_gemm_noalloc; 0 ok */
