@@ -506,3 +506,30 @@ def test_autograd_conv_pool_flatten_deferred(tlib, mode):
     got = run()
     for a, e in zip(got, ref):
         assert _bits_equal(a, e), mode
+
+
+def test_relu_recipe_survives_host_write_of_its_input(tlib):
+    """The fused conv + relu + pool forward leaves the relu output as a
+    recipe of the convolution output; writing the convolution output through
+    its host pointer runs the recipe first, so the relu output keeps the
+    values of the original convolution."""
+    import ctypes
+    from tinytorch_amd.torch_py import Node
+    case = POOL_CASES[3]
+    x, w, b, _, geo = _inputs(case)
+    N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo = geo
+    X, Wn, Bn = Node.leaf(x, False), Node.leaf(w), Node.leaf(b)
+    c = X.conv2d(Wn, Bn, (sh, sw), (ph, pw))
+    r = c.relu()
+    m = r.maxpool2d(2, 2)
+    m.value()  # launches the fused chain: the relu output is not stored
+    ct = tlib.ag_value(c.ptr)
+    hp = tlib.tt_data(ct)
+    assert hp
+    n = N * F * Ho * Wo
+    buf = np.ctypeslib.as_array(ctypes.cast(hp, ctypes.POINTER(ctypes.c_float)), shape=(n,))
+    orig = buf.copy().reshape(N, F, Ho, Wo)
+    buf[:] = -3.0
+    assert _bits_equal(r.value(), orc.relu_fwd(orig))
+    for nd in (m, r, c, X, Wn, Bn):
+        nd.release()

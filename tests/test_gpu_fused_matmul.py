@@ -311,3 +311,23 @@ def test_autograd_classifier_ce_in_reduction(tlib, read_loss):
     if read_loss != "never":
         loss = -np.log(p[np.arange(128), y]).mean()
         assert abs(float(got[0][0]) - loss) <= 1e-4 * max(1.0, abs(loss))
+
+
+def test_recipe_source_written_through_host_pointer(tlib):
+    """A tensor left as a recipe (the padded copy of a no-grad input) is
+    written before the host may change its source: tt_data of the source
+    runs the recipe first, so the padded copy keeps the values the input had
+    when ag_padones was called."""
+    from tinytorch_amd.torch_py import Node
+    x = np.random.default_rng(21).uniform(-1, 1, (64, 96)).astype(np.float32)
+    X = Node.leaf(x, False)
+    P = X.padones()
+    xt = tlib.ag_value(X.ptr)
+    hp = tlib.tt_data(xt)
+    assert hp
+    buf = np.ctypeslib.as_array(ctypes.cast(hp, ctypes.POINTER(ctypes.c_float)), shape=(x.size,))
+    buf[:] = 5.0  # the caller writes the input through the host pointer
+    assert np.array_equal(P.value(), orc.padones_fwd(x))
+    assert np.all(X.value() == 5.0)
+    for nd in (P, X):
+        nd.release()
