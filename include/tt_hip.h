@@ -177,6 +177,15 @@ int tt_k_softmax_ce_mean_hostlab(const float *logits, const int32_t *host_labels
  * dW, M <= 480 (a block of A is staged in LDS), else -1. */
 int tt_k_head_bwd(const float *A, int M, int K, const float *W, int N, const float *G,
                   float *dW, float *dA, float *d1, float *d2, const float *R);
+/* tt_k_head_bwd (R = NULL) where d2 is the gradient of a 2x2 / stride-2 max
+ * pool (F x Ho2 x Wo2 per row, K - 1 = F * Ho2 * Wo2) of a relu output whose
+ * windows' codes are given (tt_k_conv2d_relu_pool_fwd_lds): dc (N x F x
+ * 2Ho2 x 2Wo2) gets the pool + relu backward of d2 in the same launch (the
+ * reference's src/autograd.c:555-594 then :318-327), bit for bit
+ * tt_k_maxpool2x2_code_relu_bwd of d2.  -1: shapes or alignment outside it. */
+int tt_k_head_bwd_pool(const float *A, int M, int K, const float *W, int N, const float *G,
+                       float *dW, float *dA, float *d1, float *d2, const unsigned char *codes,
+                       float *dc, int F, int Ho2, int Wo2);
 /* Both gradients of a matmul C = A * B (A M x K, B K x N; reference
  * src/autograd.c:66-103, matmul_nt for dA = G * B^T and matmul_tn for
  * dB = A^T * G) in ONE launch, when tt_k_gemm would compute each with its

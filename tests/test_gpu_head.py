@@ -104,3 +104,36 @@ def test_head_fusion_in_steps_on_off(tlib):
             assert abs(gm["loss"] - refm["loss"]) <= 1e-5 * max(1.0, refm["loss"])
     finally:
         tlib.tth_conv_relu_fuse(prev)
+
+
+@pytest.mark.parametrize("M,F,H2,W2", [(128, 64, 8, 8), (5, 3, 4, 6), (33, 16, 2, 2)])
+def test_head_bwd_pool_bitexact(tlib, M, F, H2, W2):
+    """tt_k_head_bwd_pool: the classifier backward also writing the pool +
+    relu backward of its reshape's gradient from the pool windows' codes --
+    dW, dA, d1, d2 bit for bit tt_k_head_bwd's, dc bit for bit
+    tt_k_maxpool2x2_code_relu_bwd of d2 (codes with ties, zero masks and
+    every argmax)."""
+    K, N = F * H2 * W2 + 1, 10
+    A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    W = rng.standard_normal((K, N)).astype(np.float32)
+    G = (rng.standard_normal((M, N)) / M).astype(np.float32)
+    codes = rng.integers(0, 64, (M, F, H2, W2)).astype(np.uint8)
+    dA_, dW_, dG = DevBuf.from_np(A), DevBuf.from_np(W), DevBuf.from_np(G)
+    dcodes = DevBuf.from_np(codes)
+    outs = []
+    for pooled in (True, False):
+        dw, da = DevBuf(K * N), DevBuf(M * K)
+        d1, d2 = DevBuf(M * (K - 1)), DevBuf(M * (K - 1))
+        dc = DevBuf(M * F * 4 * H2 * W2)
+        print("head_bwd_pool", M, F, H2, W2, pooled, flush=True)
+        if pooled:
+            check(tlib.tt_k_head_bwd_pool(dA_.ptr, M, K, dW_.ptr, N, dG.ptr, dw.ptr, da.ptr, d1.ptr,
+                                          d2.ptr, dcodes.ptr, dc.ptr, F, H2, W2), "head pool")
+        else:
+            check(tlib.tt_k_head_bwd(dA_.ptr, M, K, dW_.ptr, N, dG.ptr, dw.ptr, da.ptr, d1.ptr,
+                                     d2.ptr, None), "head")
+            check(tlib.tt_k_maxpool2x2_code_relu_bwd(dcodes.ptr, d2.ptr, dc.ptr, M, F, 2 * H2,
+                                                     2 * W2, H2, W2), "code bwd")
+        outs.append([b.to_np() for b in (dw, da, d1, d2, dc)])
+    for a, b in zip(*outs):
+        assert bits_equal(a, b)

@@ -114,6 +114,7 @@ SIGNATURES = [
     ("tth_gemm_config", _I, [_I, _I]),
     ("tt_k_gemm", _I, [_I, _I, _I, VP, _I, _I, VP, _I, _I, VP, _I]),
     ("tt_k_head_bwd", _I, [VP, _I, _I, VP, _I, VP, VP, VP, VP, VP, VP]),
+    ("tt_k_head_bwd_pool", _I, [VP, _I, _I, VP, _I, VP, VP, VP, VP, VP, VP, VP, _I, _I, _I]),
     ("tt_k_gemm_tn_padones", _I, [_I, _I, _I, VP, VP, VP]),
     ("tt_k_gemm_bias_ce", _I, [_I, _I, _I, VP, VP, VP, VP, VP, VP, VP, VP, ctypes.c_float]),
     ("tt_k_ce_mean_rows", _I, [VP, VP, _I]),

@@ -687,25 +687,54 @@ static int backward_matmul_fused(AGNode *n, const float *g) {
             if (!R) return -1;
         }
     }
+    /* y a 2x2 max pool (with its windows' codes) of a fusable relu: the head
+     * kernel writes the relu input's gradient too (the pool and relu rules
+     * are covered; the relu's own gradient stays a recipe) */
+    AGNode *pr = NULL;
+    const unsigned char *codes = NULL;
+    if (head && y && !R && x->op == &OP_RESHAPE && y->op == &OP_MAXPOOL2D && y->at.win.codes &&
+        y->at.win.kh == 2 && y->at.win.kw == 2 && y->at.win.sh == 2 && y->at.win.sw == 2 &&
+        y->val->ndim == 4 && relu_fusable(y->in[0]) &&
+        y->in[0]->val->shape[2] == 2 * y->val->shape[2] &&
+        y->in[0]->val->shape[3] == 2 * y->val->shape[3]) {
+        codes = (const unsigned char *)tt_dev(y->at.win.codes);
+        if (codes) pr = y->in[0];
+    }
     Tensor *gb = needs(b) ? tt_empty_like(b->val) : NULL;
     Tensor *ga = needs(a) ? tt_empty_like(a->val) : NULL;
     Tensor *tx = x ? tt_empty_like(x->val) : NULL;
     Tensor *ty = y ? tt_empty_like(y->val) : NULL;
+    Tensor *tc = pr ? tt_empty_like(pr->in[0]->val) : NULL;
     int rc = -1;
-    if ((!needs(b) || gb) && (!needs(a) || ga) && (!x || tx) && (!y || ty)) {
+    if ((!needs(b) || gb) && (!needs(a) || ga) && (!x || tx) && (!y || ty) && (!pr || tc)) {
         float *dB = gb ? gb->dev : NULL, *dA = ga ? ga->dev : NULL;
         float *d1 = tx ? tx->dev : NULL, *d2 = ty ? ty->dev : NULL;
-        rc = head ? tt_k_head_bwd(ad, M, K, bd, N, g, dB, dA, d1, d2, R)
-                  : tt_k_matmul_bwd_small(ad, M, K, bd, N, g, dB, dA, d1, d2, R);
+        if (pr)
+            rc = tt_k_head_bwd_pool(ad, M, K, bd, N, g, dB, dA, d1, d2, codes, tc->dev,
+                                    (int)y->val->shape[1], (int)y->val->shape[2],
+                                    (int)y->val->shape[3]);
+        if (rc != 0) {
+            tt_release(tc);
+            tc = NULL;
+            pr = NULL;
+            rc = head ? tt_k_head_bwd(ad, M, K, bd, N, g, dB, dA, d1, d2, R)
+                      : tt_k_matmul_bwd_small(ad, M, K, bd, N, g, dB, dA, d1, d2, R);
+        }
     }
     if (rc != 0) {
-        tt_release(gb); tt_release(ga); tt_release(tx); tt_release(ty);
+        tt_release(gb); tt_release(ga); tt_release(tx); tt_release(ty); tt_release(tc);
         return -1;
     }
     if (gb) accum_move(b, gb);
     if (ga) accum_move(a, ga);
     if (tx) { accum_move(x, tx); a->fused = 1; }
     if (ty) { accum_move(y, ty); x->fused = 1; }
+    if (pr) {
+        lazy_set(pr, y->grad, NULL);
+        accum_move(pr->in[0], tc);
+        y->fused = 1;
+        pr->fused = 1;
+    }
     return 0;
 }
 

@@ -131,7 +131,8 @@ __global__ void __launch_bounds__(NT)
 head_bwd_kernel(const float *__restrict__ A, int M, int K, const float *__restrict__ W, int N,
                 const float *__restrict__ G, float *__restrict__ dW, float *__restrict__ dA,
                 float *__restrict__ d1, float *__restrict__ d2, const float *__restrict__ R,
-                int nbw, int KW, int nkw) {
+                int nbw, int KW, int nkw, const unsigned char *__restrict__ codes,
+                float *__restrict__ dc, int P2, int Wo2) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -194,6 +195,20 @@ head_bwd_kernel(const float *__restrict__ A, int M, int K, const float *__restri
         const long o = (long)m * K1 + k;
         if (d1) d1[o] = s;
         if (d2) d2[o] = R ? (rv[i] > 0.0f ? s : 0.0f) : s;
+        if (dc) {
+          // d2 is a 2x2 max pool's output gradient (K1 = F x Ho2 x Wo2 per
+          // row) whose input was a relu: its pool + relu backward from the
+          // window's code (bits 0-1 argmax, 2-5 relu mask), as
+          // maxpool2x2_code_bwd_kernel writes it
+          const int fc = k / P2, rem = k - fc * P2, h2 = rem / Wo2, w2 = rem - h2 * Wo2;
+          const unsigned c = codes[o];
+          const float g0 = 0.0f + s;
+          auto at = [&](unsigned q) { return ((c & 3) == q && ((c >> (2 + q)) & 1)) ? g0 : 0.0f; };
+          float *dr = dc + ((long)(m * (K1 / P2) + fc) * (2 * (P2 / Wo2)) + 2 * h2) * (2 * Wo2) +
+                      2 * w2;
+          *reinterpret_cast<float2 *>(dr) = make_float2(at(0), at(1));
+          *reinterpret_cast<float2 *>(dr + 2 * Wo2) = make_float2(at(2), at(3));
+        }
       }
     }
   }
@@ -203,8 +218,9 @@ head_bwd_kernel(const float *__restrict__ A, int M, int K, const float *__restri
 
 extern "C" {
 
-int tt_k_head_bwd(const float *A, int M, int K, const float *W, int N, const float *G,
-                  float *dW, float *dA, float *d1, float *d2, const float *R) {
+static int head_bwd(const float *A, int M, int K, const float *W, int N, const float *G,
+                    float *dW, float *dA, float *d1, float *d2, const float *R,
+                    const unsigned char *codes, float *dc, int P2, int Wo2) {
   if (M <= 0 || K <= 0 || N <= 0 || N > 32 || !G || (!dW && !dA) || (dW && !A) ||
       (dA && !W) || ((d1 || d2) && (!dA || K < 2)))
     return -1;
@@ -221,11 +237,25 @@ int tt_k_head_bwd(const float *A, int M, int K, const float *W, int N, const flo
   const dim3 grid((unsigned)(nbw + nba));
   if (NC == 16)
     hipLaunchKernelGGL(head_bwd_kernel<16>, grid, dim3(NT), lds, stream(), A, M, K, W, N, G, dW,
-                       dA, d1, d2, R, (int)nbw, KW, (int)nkw);
+                       dA, d1, d2, R, (int)nbw, KW, (int)nkw, codes, dc, P2, Wo2);
   else
     hipLaunchKernelGGL(head_bwd_kernel<32>, grid, dim3(NT), lds, stream(), A, M, K, W, N, G, dW,
-                       dA, d1, d2, R, (int)nbw, KW, (int)nkw);
+                       dA, d1, d2, R, (int)nbw, KW, (int)nkw, codes, dc, P2, Wo2);
   return launched();
+}
+
+int tt_k_head_bwd(const float *A, int M, int K, const float *W, int N, const float *G,
+                  float *dW, float *dA, float *d1, float *d2, const float *R) {
+  return head_bwd(A, M, K, W, N, G, dW, dA, d1, d2, R, nullptr, nullptr, 1, 1);
+}
+
+int tt_k_head_bwd_pool(const float *A, int M, int K, const float *W, int N, const float *G,
+                       float *dW, float *dA, float *d1, float *d2, const unsigned char *codes,
+                       float *dc, int F, int Ho2, int Wo2) {
+  if (!codes || !dc || !d2 || F <= 0 || Ho2 <= 0 || Wo2 <= 0 ||
+      (long)F * Ho2 * Wo2 != (long)K - 1 || ((uintptr_t)dc & 7))
+    return -1;
+  return head_bwd(A, M, K, W, N, G, dW, dA, d1, d2, nullptr, codes, dc, Ho2 * Wo2, Wo2);
 }
 
 }  // extern "C"
