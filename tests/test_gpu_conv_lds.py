@@ -533,3 +533,52 @@ def test_relu_recipe_survives_host_write_of_its_input(tlib):
     assert _bits_equal(r.value(), orc.relu_fwd(orig))
     for nd in (m, r, c, X, Wn, Bn):
         nd.release()
+
+
+@pytest.mark.parametrize("order", ["read_all", "drop_first"])
+def test_deferred_weight_gradient_reductions(tlib, order):
+    """Two convolutions' weight-gradient reductions are left pending by the
+    backward pass and run together when the first gradient is read; a
+    pending reduction whose gradients are released unread writes nothing.
+    The gradients are the oracle's (within tolerance) and the same bits in
+    either order."""
+    from tinytorch_amd.torch_py import Node
+    r = np.random.default_rng(31)
+    x = r.uniform(-1, 1, (4, 16, 8, 8)).astype(np.float32)
+    w1 = r.uniform(-0.3, 0.3, (40, 16, 3, 3)).astype(np.float32)
+    b1 = r.uniform(-1, 1, 40).astype(np.float32)
+    w2 = r.uniform(-0.3, 0.3, (24, 40, 3, 3)).astype(np.float32)
+    b2 = r.uniform(-1, 1, 24).astype(np.float32)
+    g = r.standard_normal((4, 24, 8, 8)).astype(np.float32)
+
+    def run(drop_first):
+        X = Node.leaf(x, False)
+        W1, B1, W2, B2 = Node.leaf(w1), Node.leaf(b1), Node.leaf(w2), Node.leaf(b2)
+        c1 = X.conv2d(W1, B1, (1, 1), (1, 1))
+        c2 = c1.conv2d(W2, B2, (1, 1), (1, 1))
+        c2.backward(g)
+        out = {}
+        if drop_first:
+            for nd in (W1, B1, c2, c1):  # W1's and B1's gradients released unread
+                nd.release()
+            out["w2"], out["b2"] = W2.grad(), B2.grad()
+            for nd in (X, W2, B2):
+                nd.release()
+        else:
+            out["w2"], out["b2"] = W2.grad(), B2.grad()
+            out["w1"], out["b1"] = W1.grad(), B1.grad()
+            for nd in (c2, c1, X, W1, B1, W2, B2):
+                nd.release()
+        return out
+
+    got = run(order == "drop_first")
+    ref = run(False)
+    for k in got:
+        assert _bits_equal(got[k], ref[k]), k
+    y1 = orc.conv2d_fwd(x, w1, b1, 1, 1, 1, 1)
+    dx1, dw2, db2 = orc.conv2d_bwd(y1, w2, g, 1, 1, 1, 1)
+    _, dw1, db1 = orc.conv2d_bwd(x, w1, dx1, 1, 1, 1, 1)
+    for k, want in (("w2", dw2), ("b2", db2), ("w1", dw1), ("b1", db1)):
+        if k in got:
+            e = np.abs(got[k] - want).max() / max(np.abs(want).max(), 1e-30)
+            assert e <= 1e-4, (k, e)

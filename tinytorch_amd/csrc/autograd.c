@@ -84,6 +84,8 @@ static void backward_padones(AGNode *n);
 static void backward_reshape(AGNode *n);
 static void backward_conv2d(AGNode *n);
 static int conv_pooled_dw(AGNode *n);
+static int conv_dw_deferred(const float *gd, const unsigned char *codes, const float *x,
+                            Tensor *gw, Tensor *gb, const int q[13]);
 static void backward_maxpool(AGNode *n);
 static void backward_avgpool(AGNode *n);
 static void backward_softmax_ce(AGNode *n);
@@ -883,9 +885,11 @@ static void backward_conv2d(AGNode *n) {
         const float *x = tt_dev(a->val);
         Tensor *gw = x ? tt_empty_like(w->val) : NULL;
         Tensor *gb = gw && needs(b) ? tt_empty_dev(bshp, 1) : NULL;
+        const int q[13] = {N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo};
         if (gw && (gb || !needs(b)) &&
-            tt_k_conv2d_dw_lds(gd, x, gw->dev, gb ? gb->dev : NULL, N, C, H, W, F, HH, WW, sh,
-                               sw, ph, pw, Ho, Wo) == 0) {
+            (conv_dw_deferred(gd, NULL, x, gw, gb, q) == 0 ||
+             tt_k_conv2d_dw_lds(gd, x, gw->dev, gb ? gb->dev : NULL, N, C, H, W, F, HH, WW, sh,
+                                sw, ph, pw, Ho, Wo) == 0)) {
             if (gb) accum_move(b, gb);
             accum_move(w, gw);
             w_done = 1;
@@ -980,6 +984,19 @@ static void backward_conv2d(AGNode *n) {
 
 /* A 2x2 / stride-2 max pool whose input is a fusable relu (relu_fusable)
  * runs both backwards in one pass; the relu node's own step is skipped. */
+/* dW (and db) on the tiled LDS path with the reduction deferred: gw and gb
+ * become recipes, and every pending reduction runs in one launch when the
+ * first of them is read (the optimizer's step, ag_grad, ...).  codes: gd is
+ * the pool gradient of tt_k_conv2d_dw_lds_pooled.  0 done; -1 not covered. */
+static int conv_dw_deferred(const float *gd, const unsigned char *codes, const float *x,
+                            Tensor *gw, Tensor *gb, const int q[13]) {
+    TTDwtJob job;
+    const int rc = ttk_conv2d_dwt_defer(gd, codes, x, gw->dev, gb ? gb->dev : NULL, q, &job);
+    if (rc != 0) return rc < -1 ? rc : -1;
+    if (tt_lazy_dwt(gw, gb, &job) != 0) return ttk_dwt_reduce_jobs(&job, 1);
+    return 0;
+}
+
 /* geometry of a convolution node: N C H W F HH WW sh sw ph pw Ho Wo */
 static void conv_geo(const AGNode *c, int q[13]) {
     const Tensor *x = c->in[0]->val, *w = c->in[1]->val;
@@ -1020,9 +1037,10 @@ static int conv_pooled_dw(AGNode *n) {
     Tensor *gw = x && gp && cd ? tt_empty_like(w->val) : NULL;
     Tensor *gb = gw && needs(b) ? tt_empty_dev(bshp, 1) : NULL;
     if (gw && (gb || !needs(b)) &&
-        tt_k_conv2d_dw_lds_pooled(gp, cd, x, gw->dev, gb ? gb->dev : NULL, q[0], q[1], q[2],
-                                  q[3], q[4], q[5], q[6], q[7], q[8], q[9], q[10], q[11],
-                                  q[12]) == 0) {
+        (conv_dw_deferred(gp, cd, x, gw, gb, q) == 0 ||
+         tt_k_conv2d_dw_lds_pooled(gp, cd, x, gw->dev, gb ? gb->dev : NULL, q[0], q[1], q[2],
+                                   q[3], q[4], q[5], q[6], q[7], q[8], q[9], q[10], q[11],
+                                   q[12]) == 0)) {
         if (gb) accum_move(b, gb);
         accum_move(w, gw);
         return 1;

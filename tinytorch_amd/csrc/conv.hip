@@ -1391,15 +1391,17 @@ conv_dwt_kernel(const float *__restrict__ gr, const float *__restrict__ x,
 // filter block's partial (16-byte loads; a wave's loads cover whole 1 KB
 // runs) and adds the units z, z+ZL, ... in order, 8 loads in flight; the ZL
 // lanes of an element are then added in lane order.
+// One workgroup's share of the reduction: block blk of the columns (dw or
+// db NULL: that output is not written).
 template <int ZL>
-__global__ void __launch_bounds__(NT)
-conv_dwt_reduce_kernel(const float *__restrict__ part, float *__restrict__ dw,
-                       float *__restrict__ db, int nu, int nfb, int jbp, int F, int K) {
+__device__ __forceinline__ void dwt_reduce_block(int blk, f32x4 *sums,
+                                                 const float *__restrict__ part,
+                                                 float *__restrict__ dw, float *__restrict__ db,
+                                                 int nu, int nfb, int jbp, int F, int K) {
   constexpr int XL = NT / ZL;  // 4-element columns per workgroup
   const int S4 = (jbp * 1024 + 32) / 4;
-  __shared__ f32x4 sums[ZL][XL];
   const int tx = threadIdx.x % XL, ty = threadIdx.x / XL;
-  const long e4 = (long)blockIdx.x * XL + tx;
+  const long e4 = (long)blk * XL + tx;
   const bool in = e4 < (long)nfb * S4;
   const long ec = in ? e4 : 0;
   const int fb = (int)(ec / S4), i4 = (int)(ec - (long)fb * S4);
@@ -1413,10 +1415,10 @@ conv_dwt_reduce_kernel(const float *__restrict__ part, float *__restrict__ dw,
     for (int k = 0; k < 8; k++)
       if (q0 + k * ZL < nu) v += t[k];
   }
-  sums[ty][tx] = v;
+  sums[ty * XL + tx] = v;
   __syncthreads();
   if (ty != 0 || !in) return;
-  for (int z = 1; z < ZL; z++) v += sums[z][tx];
+  for (int z = 1; z < ZL; z++) v += sums[z * XL + tx];
   const int i = i4 * 4;
   if (i >= jbp * 1024) {
 #pragma unroll
@@ -1429,10 +1431,42 @@ conv_dwt_reduce_kernel(const float *__restrict__ part, float *__restrict__ dw,
   const int jb = i >> 10, r = (i >> 6) & 15, l = i & 63;
   const int f = fb * 32 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
   const int k = jb * 32 + (l & 31);
-  if (f >= F) return;
+  if (f >= F || !dw) return;
 #pragma unroll
   for (int e = 0; e < 4; e++)
     if (k + e < K) dw[(long)f * K + k + e] = v[e];
+}
+
+template <int ZL>
+__global__ void __launch_bounds__(NT)
+conv_dwt_reduce_kernel(const float *__restrict__ part, float *__restrict__ dw,
+                       float *__restrict__ db, int nu, int nfb, int jbp, int F, int K) {
+  __shared__ f32x4 sums[NT];
+  dwt_reduce_block<ZL>(blockIdx.x, sums, part, dw, db, nu, nfb, jbp, F, K);
+}
+
+// Up to DWT_JOBS deferred reductions in one launch: blocks [start[q],
+// start[q+1]) take job q, each exactly as its own conv_dwt_reduce_kernel.
+constexpr int DWT_JOBS = 4;
+struct DwtJobs {
+  TTDwtJob j[DWT_JOBS];
+  int start[DWT_JOBS + 1];
+  int n;
+};
+__global__ void __launch_bounds__(NT) conv_dwt_reduce_multi_kernel(DwtJobs js) {
+  __shared__ f32x4 sums[NT];
+  int q = 0;
+  while (q + 1 < js.n && (int)blockIdx.x >= js.start[q + 1]) q++;
+  const TTDwtJob &j = js.j[q];
+  const int blk = blockIdx.x - js.start[q];
+  switch (j.zl) {
+#define TT_DJ(ZL_)                                                                         \
+  case ZL_:                                                                                \
+    dwt_reduce_block<ZL_>(blk, sums, j.part, j.dw, j.db, j.nu, j.nfb, j.jbp, j.F, j.K);    \
+    break;
+    TT_DJ(1) TT_DJ(2) TT_DJ(4) TT_DJ(8) TT_DJ(16) TT_DJ(32) TT_DJ(64)
+#undef TT_DJ
+  }
 }
 
 // dw[f][k] = sum_z part[z][f][k] (k < K), db[f] = sum_z part[z][f][K]; ZL
@@ -1834,9 +1868,12 @@ DwtPlan plan_dwt(const Geo &g, int N) {
   return pl;
 }
 
+// defer: the reduction is not launched but described there (its partials
+// then belong to the job)
 template <int TG, int NTGW, bool CODE = false>
 int launch_dwt(const float *gr, const float *x, float *dw, float *db, const Geo &g,
-               const DwtPlan &pl, const unsigned char *codes = nullptr) {
+               const DwtPlan &pl, const unsigned char *codes = nullptr,
+               TTDwtJob *defer = nullptr) {
   auto kern = conv_dwt_kernel<TG, NTGW, CODE>;
   if (pl.lds > 64 * 1024 && !allow_big_lds((const void *)kern)) return -1;
   const long S = (long)pl.jbp * 1024 + 32;
@@ -1851,6 +1888,11 @@ int launch_dwt(const float *gr, const float *x, float *dw, float *db, const Geo 
     // lanes per element: about 16 units each
     int zl = 1;
     while (zl < 64 && zl * 16 < pl.units) zl *= 2;
+    if (defer) {
+      *defer = TTDwtJob{part, dw, db, pl.units, pl.nfb, pl.jbp, g.F, g.K, zl,
+                        (int)((cols + NT / zl - 1) / (NT / zl))};
+      return 0;
+    }
 #define TT_DWR(ZL_)                                                                          \
   case ZL_:                                                                                  \
     hipLaunchKernelGGL(conv_dwt_reduce_kernel<ZL_>,                                          \
@@ -1869,15 +1911,16 @@ int launch_dwt(const float *gr, const float *x, float *dw, float *db, const Geo 
 
 template <bool CODE>
 int launch_dwt_plan(const float *gr, const float *x, float *dw, float *db, const Geo &g,
-                    const DwtPlan &pl, const unsigned char *codes = nullptr) {
-  if (pl.tg == 1) return launch_dwt<1, 1, CODE>(gr, x, dw, db, g, pl, codes);
-  if (pl.tg == 2) return launch_dwt<2, 1, CODE>(gr, x, dw, db, g, pl, codes);
+                    const DwtPlan &pl, const unsigned char *codes = nullptr,
+                    TTDwtJob *defer = nullptr) {
+  if (pl.tg == 1) return launch_dwt<1, 1, CODE>(gr, x, dw, db, g, pl, codes, defer);
+  if (pl.tg == 2) return launch_dwt<2, 1, CODE>(gr, x, dw, db, g, pl, codes, defer);
   if (pl.tg != 3) return -1;
   switch (pl.ntgw) {
-    case 1: return launch_dwt<3, 1, CODE>(gr, x, dw, db, g, pl, codes);
-    case 2: return launch_dwt<3, 2, CODE>(gr, x, dw, db, g, pl, codes);
-    case 3: return launch_dwt<3, 3, CODE>(gr, x, dw, db, g, pl, codes);
-    case 4: return launch_dwt<3, 4, CODE>(gr, x, dw, db, g, pl, codes);
+    case 1: return launch_dwt<3, 1, CODE>(gr, x, dw, db, g, pl, codes, defer);
+    case 2: return launch_dwt<3, 2, CODE>(gr, x, dw, db, g, pl, codes, defer);
+    case 3: return launch_dwt<3, 3, CODE>(gr, x, dw, db, g, pl, codes, defer);
+    case 4: return launch_dwt<3, 4, CODE>(gr, x, dw, db, g, pl, codes, defer);
   }
   return -1;
 }
@@ -2043,4 +2086,51 @@ extern "C" int tt_k_conv2d_dx_lds(const float *gr, const float *w, float *dx, in
   if (sh != 1 || sw != 1 || ph > HH - 1 || pw > WW - 1) return -1;
   const Geo gx{F, Ho, Wo, HH, WW, 1, 1, HH - 1 - ph, WW - 1 - pw, H, W, C, F * HH * WW};
   return run_fwd<true>(gr, w, nullptr, dx, gx, N, false);
+}
+
+extern "C" int ttk_conv2d_dwt_defer(const float *gr, const unsigned char *codes, const float *x,
+                                    float *dw, float *db, const int q[13], TTDwtJob *job) {
+  const int N = q[0], C = q[1], H = q[2], W = q[3], F = q[4], HH = q[5], WW = q[6], sh = q[7],
+            sw = q[8], ph = q[9], pw = q[10], Ho = q[11], Wo = q[12];
+  if (!gr || !x || !dw || !job || !g_dwt || !geo_ok(N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo))
+    return -1;
+  const Geo g{C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo, F, C * HH * WW};
+  const DwtPlan tp = plan_dwt(g, N);
+  if (!tp.tg || !aligned16(x)) return -1;
+  if (codes) {
+    if (Ho % 2 || Wo % 2 || (tp.rc % 2 && tp.nch > 1) || ((uintptr_t)gr & 7) ||
+        ((uintptr_t)codes & 1))
+      return -1;
+    return launch_dwt_plan<true>(gr, x, dw, db, g, tp, codes, job);
+  }
+  if (!aligned16(gr)) return -1;
+  return launch_dwt_plan<false>(gr, x, dw, db, g, tp, nullptr, job);
+}
+
+extern "C" int ttk_dwt_reduce_jobs(const TTDwtJob *jobs, int n) {
+  int rc = 0;
+  for (int b = 0; b < n; b += DWT_JOBS) {
+    DwtJobs js{};
+    js.n = n - b < DWT_JOBS ? n - b : DWT_JOBS;
+    long tot = 0;
+    for (int q = 0; q < js.n; q++) {
+      js.j[q] = jobs[b + q];
+      js.start[q] = (int)tot;
+      tot += jobs[b + q].nblk;
+    }
+    js.start[js.n] = (int)tot;
+    if (tot > 0) {
+      hipLaunchKernelGGL(conv_dwt_reduce_multi_kernel, dim3((unsigned)tot), dim3(NT), 0,
+                         stream(), js);
+      if (hipGetLastError() != hipSuccess) rc = -3;
+    }
+    for (int q = 0; q < js.n; q++) ttrt_free(js.j[q].part);  // stream-ordered
+  }
+  return rc;
+}
+
+extern "C" void ttk_dwt_job_drop(TTDwtJob *job) {
+  if (!job) return;
+  ttrt_free(job->part);
+  job->part = nullptr;
 }

@@ -107,9 +107,18 @@ Tensor *tt_retain(Tensor *t) {
  * input itself, forward and backward), and ag_softmax_ce the loss of a
  * softmax-CE computed in its classifier's GEMM (the backward reads only
  * the seed). */
+/* a deferred weight-gradient reduction, shared by its dw and db tensors */
+typedef struct {
+    TTDwtJob job;
+    int refs;
+} TTDwtShared;
+
 typedef struct TTLazyVal {
     Tensor *t, *src;
-    int kind;                  /* 0: relu(src); 1: padones(src); 2: mean of src */
+    int kind;                  /* 0: relu(src); 1: padones(src); 2: mean of src;
+                                  3: the reduction `dwt` (every pending one runs
+                                  in the same launch) */
+    TTDwtShared *dwt;
     struct TTLazyVal *next;
 } TTLazyVal;
 static TTLazyVal *g_lazy_vals;
@@ -120,6 +129,7 @@ static int lazy_add(Tensor *t, Tensor *src, int kind) {
     l->t = t;
     l->src = tt_retain(src);
     l->kind = kind;
+    l->dwt = NULL;
     l->next = g_lazy_vals;
     g_lazy_vals = l;
     return 0;
@@ -135,13 +145,85 @@ Tensor *tt_lazy_relu_src(const Tensor *t) {
     return NULL;
 }
 
+int tt_lazy_dwt(Tensor *dw, Tensor *db, const TTDwtJob *job) {
+    TTDwtShared *sh = (TTDwtShared *)malloc(sizeof(TTDwtShared));
+    TTLazyVal *a = (TTLazyVal *)malloc(sizeof(TTLazyVal));
+    TTLazyVal *b = db ? (TTLazyVal *)malloc(sizeof(TTLazyVal)) : NULL;
+    if (!sh || !a || (db && !b)) {
+        free(sh); free(a); free(b);
+        return -1;
+    }
+    sh->job = *job;
+    sh->refs = db ? 2 : 1;
+    a->t = dw; a->src = NULL; a->kind = 3; a->dwt = sh;
+    a->next = g_lazy_vals;
+    g_lazy_vals = a;
+    if (b) {
+        b->t = db; b->src = NULL; b->kind = 3; b->dwt = sh;
+        b->next = g_lazy_vals;
+        g_lazy_vals = b;
+    }
+    return 0;
+}
+
+/* every pending reduction (up to 32 at a time) in one launch; their tensors
+ * become current */
+static void dwt_flush_all(void) {
+    for (;;) {
+        TTDwtShared *sh[32];
+        TTDwtJob jobs[32];
+        int n = 0;
+        for (TTLazyVal *l = g_lazy_vals; l && n < 32; l = l->next) {
+            if (l->kind != 3) continue;
+            int seen = 0;
+            for (int i = 0; i < n; i++) seen |= sh[i] == l->dwt;
+            if (!seen) { sh[n] = l->dwt; jobs[n] = l->dwt->job; n++; }
+        }
+        if (!n) return;
+        const int rc = ttk_dwt_reduce_jobs(jobs, n);  /* frees the partials */
+        TTLazyVal **pp = &g_lazy_vals;
+        while (*pp) {
+            TTLazyVal *l = *pp;
+            int mine = 0;
+            for (int i = 0; l->kind == 3 && i < n; i++) mine |= sh[i] == l->dwt;
+            if (!mine) { pp = &l->next; continue; }
+            *pp = l->next;
+            if (rc != 0) l->t->valid = 0;
+            else tt_mark_dev_written(l->t);
+            free(l);
+        }
+        for (int i = 0; i < n; i++) free(sh[i]);
+    }
+}
+
+/* a pending reduction's output released unread: the reduction skips it (and
+ * is dropped when nothing of it is left) */
+static void dwt_drop_entry(TTLazyVal **pp) {
+    TTLazyVal *l = *pp;
+    TTDwtShared *sh = l->dwt;
+    *pp = l->next;
+    if (sh->job.dw == l->t->dev) sh->job.dw = NULL;
+    if (sh->job.db == l->t->dev) sh->job.db = NULL;
+    if (--sh->refs == 0) {
+        ttk_dwt_job_drop(&sh->job);
+        free(sh);
+    }
+    free(l);
+}
+
 /* unlink the entries of t (as the recipe's output, or every entry computed
- * from t when `from`), running their recipes unless `drop` */
+ * from t when `from`), running their recipes unless `drop`; a recipe's run
+ * may change the list, so the walk restarts after each */
 static void lazy_take(const Tensor *t, int from, int drop) {
-    TTLazyVal **pp = &g_lazy_vals;
-    while (*pp) {
+restart:
+    for (TTLazyVal **pp = &g_lazy_vals; *pp; pp = &(*pp)->next) {
         TTLazyVal *l = *pp;
-        if ((from ? l->src : l->t) != t) { pp = &l->next; continue; }
+        if ((from ? l->src : l->t) != t) continue;
+        if (l->kind == 3) {
+            if (drop) dwt_drop_entry(pp);
+            else dwt_flush_all();
+            goto restart;
+        }
         *pp = l->next;
         if (!drop) {
             const float *x = tt_dev(l->src);
@@ -155,6 +237,7 @@ static void lazy_take(const Tensor *t, int from, int drop) {
         }
         tt_release(l->src);
         free(l);
+        goto restart;
     }
 }
 

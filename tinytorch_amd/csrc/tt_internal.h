@@ -57,6 +57,9 @@ int tt_flush_pending(void);   /* 0 ok; <0 the pending output is invalid */
 int tt_lazy_relu(Tensor *t, Tensor *src);
 int tt_lazy_padones(Tensor *t, Tensor *src);  /* t (M x K+1) = padones(src (M x K)) */
 int tt_lazy_ce_mean(Tensor *t, Tensor *src);  /* t (1) = mean of the row losses src */
+/* dw, db (db may be NULL) = the pending reduction job; 0 ok, -1 (no memory):
+ * run the job now */
+int tt_lazy_dwt(Tensor *dw, Tensor *db, const TTDwtJob *job);
 Tensor *tt_lazy_relu_src(const Tensor *t);  /* src while t is still unwritten */
 int tt_defer_enabled(void);
 Tensor *tt_reshape_ex(const Tensor *a, const long *new_shape, int new_ndim, int defer);

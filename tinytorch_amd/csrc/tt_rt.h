@@ -56,6 +56,24 @@ typedef struct {
     float scale;
 } TTCeHook;
 int    ttk_reduce_ce(const float *ws, float *C, int M, int N, int S, int zl, const TTCeHook *h);
+/* conv.hip: a weight gradient whose tiled kernel ran but whose reduction is
+ * still to run: the partial sums (owned), the outputs (dw, db; either may
+ * be NULL: not written) and the reduction's shape */
+typedef struct {
+    float *part;
+    float *dw, *db;
+    int nu, nfb, jbp, F, K, zl, nblk;
+} TTDwtJob;
+/* conv.hip: tt_k_conv2d_dw_lds (codes NULL) or tt_k_conv2d_dw_lds_pooled
+ * (gr the pool gradient) without the reduction, described in *job.  0:
+ * launched; -1: not covered (nothing launched); < -1: error. */
+int    ttk_conv2d_dwt_defer(const float *gr, const unsigned char *codes, const float *x,
+                            float *dw, float *db, const int geo[13], TTDwtJob *job);
+/* conv.hip: the reductions of n jobs in one launch (the same values as
+ * each job's own reduction), then their partials freed; 0 ok */
+int    ttk_dwt_reduce_jobs(const TTDwtJob *jobs, int n);
+/* conv.hip: free a job's partials without reducing them */
+void   ttk_dwt_job_drop(TTDwtJob *job);
 /* elementwise.hip: C = A * B + bias (A M x K, B K x N row-major) for N <= 16,
  * one workgroup per row, with R = relu(C) / P = [relu(C), 1] when given, or
  * with the softmax-CE of each row when ce is given (ce->bias unused).  1:
