@@ -582,3 +582,41 @@ def test_deferred_weight_gradient_reductions(tlib, order):
         if k in got:
             e = np.abs(got[k] - want).max() / max(np.abs(want).max(), 1e-30)
             assert e <= 1e-4, (k, e)
+
+
+def test_sgd_step_runs_pending_reductions(tlib):
+    """ag_sgd_step_many on weights whose gradients are pending reductions:
+    the reductions and the step in one launch give the same weights and
+    gradients, bit for bit, as reading the gradients first (which runs the
+    reductions) and stepping the plain way; a leaf without a pending
+    reduction (the second bias is given no gradient path change) rides along."""
+    import ctypes
+    from tinytorch_amd.torch_py import Node
+    r = np.random.default_rng(41)
+    x = r.uniform(-1, 1, (4, 16, 8, 8)).astype(np.float32)
+    ps = [r.uniform(-0.3, 0.3, (40, 16, 3, 3)), r.uniform(-1, 1, 40),
+          r.uniform(-0.3, 0.3, (24, 40, 3, 3)), r.uniform(-1, 1, 24),
+          r.uniform(-1, 1, (4, 24, 8, 8))]
+    ps = [p.astype(np.float32) for p in ps]
+    g = r.standard_normal((4, 24, 8, 8)).astype(np.float32)
+
+    def run(read_first):
+        X = Node.leaf(x, False)
+        P = [Node.leaf(p) for p in ps]
+        c1 = X.conv2d(P[0], P[1], (1, 1), (1, 1))
+        c2 = c1.conv2d(P[2], P[3], (1, 1), (1, 1))
+        y = c2 * P[4]  # a leaf whose gradient is an ordinary tensor
+        y.backward(g)
+        if read_first:
+            for p in P:
+                p.grad()
+        arr = (ctypes.c_void_p * 5)(*[p.ptr for p in P])
+        assert tlib.ag_sgd_step_many(arr, 5, ctypes.c_float(0.1)) == 0
+        out = [p.value() for p in P] + [p.grad() for p in P]
+        for nd in [y, c2, c1, X] + P:
+            nd.release()
+        return out
+
+    fused, plain = run(False), run(True)
+    for a, b in zip(fused, plain):
+        assert _bits_equal(a, b)

@@ -1264,19 +1264,29 @@ int ag_sgd_step_many(AGNode *const *leaves, int count, float lr) {
     for (int base = 0; base < count; base += TT_SGD_MAX) {
         float *w[TT_SGD_MAX];
         const float *g[TT_SGD_MAX];
+        Tensor *gt[TT_SGD_MAX];
         long n[TT_SGD_MAX];
         int k = 0;
         for (int i = base; i < count && i < base + TT_SGD_MAX; i++) {
             AGNode *l = leaves[i];
             if (!l || !l->grad) continue;
             w[k] = tt_dev(l->val);
-            g[k] = tt_dev(l->grad);
-            if (!w[k] || !g[k]) return -1;
+            if (!w[k]) return -1;
+            gt[k] = l->grad;
             n[k] = l->val->numel;
-            tt_mark_dev_written(l->val);
             k++;
         }
-        if (tt_k_sgd_multi(w, g, n, k, lr)) return -1;
+        /* gradients whose reduction is still pending: the reductions and
+         * the step in one launch */
+        const int rc = tt_lazy_dwt_sgd(w, gt, n, k, lr);
+        if (rc < 0) return -1;
+        if (rc == 1) {
+            for (int i = 0; i < k; i++)
+                if (!(g[i] = tt_dev(gt[i]))) return -1;
+            if (tt_k_sgd_multi(w, g, n, k, lr)) return -1;
+        }
+        for (int i = base; i < count && i < base + TT_SGD_MAX; i++)
+            if (leaves[i] && leaves[i]->grad) tt_mark_dev_written(leaves[i]->val);
     }
     return 0;
 }

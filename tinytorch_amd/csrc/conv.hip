@@ -1393,11 +1393,17 @@ conv_dwt_kernel(const float *__restrict__ gr, const float *__restrict__ x,
 // lanes of an element are then added in lane order.
 // One workgroup's share of the reduction: block blk of the columns (dw or
 // db NULL: that output is not written).
+// wdw / wdb (optional): the weights and bias dw / db are the gradients of;
+// each gets the SGD step w -= lr * g from the value just stored (the same
+// arithmetic as sgd_multi_kernel, without contraction).
 template <int ZL>
 __device__ __forceinline__ void dwt_reduce_block(int blk, f32x4 *sums,
                                                  const float *__restrict__ part,
                                                  float *__restrict__ dw, float *__restrict__ db,
-                                                 int nu, int nfb, int jbp, int F, int K) {
+                                                 int nu, int nfb, int jbp, int F, int K,
+                                                 float *__restrict__ wdw = nullptr,
+                                                 float *__restrict__ wdb = nullptr,
+                                                 float lr = 0.0f) {
   constexpr int XL = NT / ZL;  // 4-element columns per workgroup
   const int S4 = (jbp * 1024 + 32) / 4;
   const int tx = threadIdx.x % XL, ty = threadIdx.x / XL;
@@ -1425,6 +1431,7 @@ __device__ __forceinline__ void dwt_reduce_block(int blk, f32x4 *sums,
     for (int e = 0; e < 4; e++) {
       const int f = fb * 32 + (i + e - jbp * 1024);
       if (db && f < F) db[f] = v[e];
+      if (wdb && f < F) wdb[f] -= lr * v[e];
     }
     return;
   }
@@ -1434,7 +1441,10 @@ __device__ __forceinline__ void dwt_reduce_block(int blk, f32x4 *sums,
   if (f >= F || !dw) return;
 #pragma unroll
   for (int e = 0; e < 4; e++)
-    if (k + e < K) dw[(long)f * K + k + e] = v[e];
+    if (k + e < K) {
+      dw[(long)f * K + k + e] = v[e];
+      if (wdw) wdw[(long)f * K + k + e] -= lr * v[e];
+    }
 }
 
 template <int ZL>
@@ -2126,6 +2136,83 @@ extern "C" int ttk_dwt_reduce_jobs(const TTDwtJob *jobs, int n) {
     }
     for (int q = 0; q < js.n; q++) ttrt_free(js.j[q].part);  // stream-ordered
   }
+  return rc;
+}
+
+// The pending reductions of an SGD step's gradients and the step itself in
+// one launch: blocks [0, start[n]) reduce job q (writing its dw / db and
+// stepping wdw[q] / wdb[q] when given), the rest step the plain tensors
+// (a thread an element).
+struct DwtSgd {
+  TTDwtJob j[DWT_JOBS];
+  float *wdw[DWT_JOBS], *wdb[DWT_JOBS];
+  int start[DWT_JOBS + 1];
+  int n;
+  float *pw[TT_SGD_MAX];
+  const float *pg[TT_SGD_MAX];
+  long pn[TT_SGD_MAX];
+  long pstart[TT_SGD_MAX + 1];
+  int np;
+  float lr;
+};
+__global__ void __launch_bounds__(NT) conv_dwt_reduce_sgd_kernel(DwtSgd js) {
+  __shared__ f32x4 sums[NT];
+  const int bx = blockIdx.x;
+  if (bx >= js.start[js.n]) {
+    const long b = bx - js.start[js.n];
+    int t = 0;
+    while (t + 1 < js.np && b >= js.pstart[t + 1]) t++;
+    const long i = (b - js.pstart[t]) * NT + threadIdx.x;
+    if (i < js.pn[t]) js.pw[t][i] -= js.lr * js.pg[t][i];
+    return;
+  }
+  int q = 0;
+  while (q + 1 < js.n && bx >= js.start[q + 1]) q++;
+  const TTDwtJob &j = js.j[q];
+  const int blk = bx - js.start[q];
+  switch (j.zl) {
+#define TT_DJ(ZL_)                                                                         \
+  case ZL_:                                                                                \
+    dwt_reduce_block<ZL_>(blk, sums, j.part, j.dw, j.db, j.nu, j.nfb, j.jbp, j.F, j.K,     \
+                          js.wdw[q], js.wdb[q], js.lr);                                    \
+    break;
+    TT_DJ(1) TT_DJ(2) TT_DJ(4) TT_DJ(8) TT_DJ(16) TT_DJ(32) TT_DJ(64)
+#undef TT_DJ
+  }
+}
+
+extern "C" int ttk_dwt_reduce_sgd(const TTDwtJob *jobs, float *const *wdw, float *const *wdb,
+                                  int nj, float *const *pw, const float *const *pg,
+                                  const long *pn, int np, float lr) {
+  if (nj < 1 || nj > DWT_JOBS || np < 0 || np > TT_SGD_MAX) return 1;
+  DwtSgd js{};
+  js.n = nj;
+  js.np = np;
+  js.lr = lr;
+  long tot = 0;
+  for (int q = 0; q < nj; q++) {
+    js.j[q] = jobs[q];
+    js.wdw[q] = wdw[q];
+    js.wdb[q] = wdb[q];
+    js.start[q] = (int)tot;
+    tot += jobs[q].nblk;
+  }
+  js.start[nj] = (int)tot;
+  long ptot = 0;
+  for (int t = 0; t < np; t++) {
+    js.pw[t] = pw[t];
+    js.pg[t] = pg[t];
+    js.pn[t] = pn[t];
+    js.pstart[t] = ptot;
+    ptot += (pn[t] + NT - 1) / NT;
+  }
+  js.pstart[np] = ptot;
+  if (tot + ptot > 0x7fffffffL) return 1;
+  if (tot + ptot > 0)
+    hipLaunchKernelGGL(conv_dwt_reduce_sgd_kernel, dim3((unsigned)(tot + ptot)), dim3(NT), 0,
+                       stream(), js);
+  const int rc = hipGetLastError() == hipSuccess ? 0 : -3;
+  for (int q = 0; q < nj; q++) ttrt_free(js.j[q].part);  // stream-ordered
   return rc;
 }
 

@@ -196,6 +196,75 @@ static void dwt_flush_all(void) {
     }
 }
 
+static TTLazyVal *dwt_entry(const Tensor *t) {
+    for (TTLazyVal *l = g_lazy_vals; l; l = l->next)
+        if (l->kind == 3 && l->t == t) return l;
+    return NULL;
+}
+
+int tt_lazy_dwt_sgd(float *const *w, Tensor *const *g, const long *n, int count, float lr) {
+    if (count <= 0 || count > TT_SGD_MAX || !g_lazy_vals) return 1;
+    int any = 0;
+    for (int i = 0; i < count; i++) {
+        if (dwt_entry(g[i])) any = 1;
+        for (int k = 0; k < i; k++)
+            if (g[k] == g[i] || w[k] == w[i]) return 1;  /* a tensor twice: the plain way */
+    }
+    if (!any) return 1;
+    /* every pending job (the step reads the gradients they write) */
+    TTDwtShared *sh[4];
+    TTDwtJob jobs[4];
+    float *wdw[4], *wdb[4];
+    int nj = 0;
+    for (TTLazyVal *l = g_lazy_vals; l; l = l->next) {
+        if (l->kind != 3) continue;
+        int seen = 0;
+        for (int q = 0; q < nj; q++) seen |= sh[q] == l->dwt;
+        if (seen) continue;
+        if (nj == 4) return 1;
+        sh[nj] = l->dwt;
+        jobs[nj] = l->dwt->job;
+        wdw[nj] = wdb[nj] = NULL;
+        nj++;
+    }
+    float *pw[TT_SGD_MAX];
+    const float *pg[TT_SGD_MAX];
+    long pn[TT_SGD_MAX];
+    int np = 0;
+    for (int i = 0; i < count; i++) {
+        TTLazyVal *l = dwt_entry(g[i]);
+        if (!l) {
+            pw[np] = w[i];
+            pn[np] = n[i];
+            pg[np] = tt_dev(g[i]);  /* no pending reduction: nothing flushed */
+            if (!pg[np]) return -1;
+            np++;
+            continue;
+        }
+        for (int q = 0; q < nj; q++) {
+            if (sh[q] != l->dwt) continue;
+            if (g[i]->dev == jobs[q].dw) wdw[q] = w[i];
+            else if (g[i]->dev == jobs[q].db) wdb[q] = w[i];
+        }
+    }
+    const int rc = ttk_dwt_reduce_sgd(jobs, wdw, wdb, nj, pw, pg, pn, np, lr);
+    if (rc == 1) return 1;
+    /* the jobs ran (or failed): their tensors leave the registry */
+    TTLazyVal **pp = &g_lazy_vals;
+    while (*pp) {
+        TTLazyVal *l = *pp;
+        int mine = 0;
+        for (int q = 0; l->kind == 3 && q < nj; q++) mine |= sh[q] == l->dwt;
+        if (!mine) { pp = &l->next; continue; }
+        *pp = l->next;
+        if (rc != 0) l->t->valid = 0;
+        else tt_mark_dev_written(l->t);
+        free(l);
+    }
+    for (int q = 0; q < nj; q++) free(sh[q]);
+    return rc;
+}
+
 /* a pending reduction's output released unread: the reduction skips it (and
  * is dropped when nothing of it is left) */
 static void dwt_drop_entry(TTLazyVal **pp) {

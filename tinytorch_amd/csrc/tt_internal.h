@@ -60,6 +60,10 @@ int tt_lazy_ce_mean(Tensor *t, Tensor *src);  /* t (1) = mean of the row losses 
 /* dw, db (db may be NULL) = the pending reduction job; 0 ok, -1 (no memory):
  * run the job now */
 int tt_lazy_dwt(Tensor *dw, Tensor *db, const TTDwtJob *job);
+/* w[i] -= lr * g[i] (count <= TT_SGD_MAX) with every pending reduction in the
+ * same launch when some g[i] is one's output; 1: none is (or the step does
+ * not fit one launch) -- take the plain way, nothing done; 0 ok; < 0 error */
+int tt_lazy_dwt_sgd(float *const *w, Tensor *const *g, const long *n, int count, float lr);
 Tensor *tt_lazy_relu_src(const Tensor *t);  /* src while t is still unwritten */
 int tt_defer_enabled(void);
 Tensor *tt_reshape_ex(const Tensor *a, const long *new_shape, int new_ndim, int defer);

@@ -72,6 +72,14 @@ int    ttk_conv2d_dwt_defer(const float *gr, const unsigned char *codes, const f
 /* conv.hip: the reductions of n jobs in one launch (the same values as
  * each job's own reduction), then their partials freed; 0 ok */
 int    ttk_dwt_reduce_jobs(const TTDwtJob *jobs, int n);
+/* conv.hip: the reductions of nj <= 4 jobs and an SGD step (w -= lr * g) in
+ * one launch: job q's dw / db are written and, when wdw[q] / wdb[q] are
+ * given, those weights stepped with them; the np plain tensors pw are
+ * stepped with pg.  Then the jobs' partials are freed.  0 ok; 1: too many
+ * jobs or tensors, nothing launched. */
+int    ttk_dwt_reduce_sgd(const TTDwtJob *jobs, float *const *wdw, float *const *wdb, int nj,
+                          float *const *pw, const float *const *pg, const long *pn, int np,
+                          float lr);
 /* conv.hip: free a job's partials without reducing them */
 void   ttk_dwt_job_drop(TTDwtJob *job);
 /* elementwise.hip: C = A * B + bias (A M x K, B K x N row-major) for N <= 16,
