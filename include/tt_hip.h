@@ -138,7 +138,7 @@ int tt_k_conv_dw_bias(int F, int Kc, long Ncol, int HW,
  * on src/autograd.c:195-212's output) computed from X itself, the ones
  * column taken as a row of ones in the MFMA tiles -- bit for bit tt_k_gemm on
  * the padded matrix, where that takes the small-GEMM kernel; -1 elsewhere,
- * nothing launched. */
+ * nothing launched.  dW == NULL: 0 when the shape is covered, -1 when not. */
 int tt_k_gemm_tn_padones(int rows, int Kx, int N, const float *X, const float *G, float *dW);
 
 /* ---- bandwidth kernels (elementwise.hip / spatial.hip) ---- */

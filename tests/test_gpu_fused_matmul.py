@@ -331,3 +331,50 @@ def test_recipe_source_written_through_host_pointer(tlib):
     assert np.all(X.value() == 5.0)
     for nd in (P, X):
         nd.release()
+
+
+@pytest.mark.parametrize("second_pass", [False, True])
+def test_mlp_first_layer_grad_pending_into_sgd(tlib, second_pass):
+    """The first layer's weight gradient of padones(X) -> matmul (X without
+    gradient) is left pending and computed inside the SGD step's launch (the
+    step of its weights in the same threads): the stepped weights and the
+    gradients bit for bit those of reading the gradients first; a second
+    backward pass before the step (which adds into the layer's output
+    gradient the recipe reads) gives the same bits both ways too."""
+    from tinytorch_amd.torch_py import Node
+    r = np.random.default_rng(51)
+    x = r.uniform(0, 1, (256, 784)).astype(np.float32)
+    w1 = (r.standard_normal((785, 512)) * 0.05).astype(np.float32)
+    w2 = (r.standard_normal((513, 10)) * 0.05).astype(np.float32)
+    gy = r.standard_normal((256, 10)).astype(np.float32)
+
+    def run(read_first):
+        X, W1, W2 = Node.leaf(x, False), Node.leaf(w1), Node.leaf(w2)
+        P1 = X.padones()
+        H = P1.matmul(W1).relu()
+        P2 = H.padones()
+        Y = P2.matmul(W2)
+        Y.backward(gy)
+        if second_pass:
+            Y.backward(gy)
+        if read_first:
+            W1.grad()
+        arr = (ctypes.c_void_p * 2)(W1.ptr, W2.ptr)
+        assert tlib.ag_sgd_step_many(arr, 2, ctypes.c_float(0.05)) == 0
+        out = [W1.value(), W2.value(), W1.grad(), W2.grad()]
+        for nd in (Y, P2, H, P1, X, W1, W2):
+            nd.release()
+        return out
+
+    fused, plain = run(False), run(True)
+    for a, b in zip(fused, plain):
+        assert bits_equal(a, b)
+    if second_pass:
+        return  # (a second pass re-propagates the accumulated intermediate gradients)
+    # the gradient itself against float64
+    xp = orc.padones_fwd(x).astype(np.float64)
+    h = np.maximum(xp @ w1, 0.0)
+    gh = (gy.astype(np.float64) @ w2[:512].astype(np.float64).T) * (h > 0)
+    want = xp.T @ gh
+    e = np.abs(fused[2] - want).max() / np.abs(want).max()
+    assert e <= 1e-4, e

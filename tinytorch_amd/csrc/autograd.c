@@ -126,6 +126,7 @@ static void accum_copy(AGNode *p, Tensor *g) {
         p->grad = c;
         return;
     }
+    tt_lazy_before_write(p->grad);  /* a recipe may read this gradient */
     float *pd = tt_dev(p->grad);
     if (!pd) return;
     tt_k_add_inplace(pd, gd, g->numel);
@@ -747,7 +748,18 @@ static void backward_matmul(AGNode *n) {
     if (!g) return;
     if (tt_defer_enabled() && backward_matmul_fused(n, g) == 0) return;
     if (needs(b) && !needs(a) && a->op == &OP_PADONES && K > 1) {
-        /* dB from the padones input: the padded copy is not read */
+        /* dB from the padones input: the padded copy is not read; with the
+         * deferral, dB is a recipe that the optimizer's step runs in its own
+         * launch (or the first read runs by itself) */
+        if (tt_defer_enabled() &&
+            tt_k_gemm_tn_padones(M, K - 1, N, NULL, NULL, NULL) == 0) {
+            Tensor *gb = tt_empty_like(b->val);
+            if (gb && tt_lazy_gemm_tn_padones(gb, a->in[0]->val, n->grad, M, K - 1, N) == 0) {
+                accum_move(b, gb);
+                return;
+            }
+            tt_release(gb);
+        }
         const float *xd = tt_dev(a->in[0]->val);
         Tensor *gb = xd ? tt_empty_like(b->val) : NULL;
         if (gb && tt_k_gemm_tn_padones(M, K - 1, N, xd, g, gb->dev) == 0) {
@@ -1219,6 +1231,7 @@ static void backward_impl(AGNode *out, int seed_kind, const float *hseed, const 
     AGNode *head = schedule(out);
     if (g_lazy)
         for (AGNode *n = head; n && g_lazy; n = n->next) materialise_for(n);
+    tt_lazy_before_write(out->grad);  /* the seed overwrites it below */
     if (!out->grad) out->grad = tt_empty_like(out->val);
     if (!out->grad) return;
     if (seed_kind == 0 && out->grad->numel == 1) {
@@ -1278,7 +1291,8 @@ int ag_sgd_step_many(AGNode *const *leaves, int count, float lr) {
         }
         /* gradients whose reduction is still pending: the reductions and
          * the step in one launch */
-        const int rc = tt_lazy_dwt_sgd(w, gt, n, k, lr);
+        int rc = tt_lazy_dwt_sgd(w, gt, n, k, lr);
+        if (rc == 1) rc = tt_lazy_gemm_sgd(w, gt, n, k, lr);
         if (rc < 0) return -1;
         if (rc == 1) {
             for (int i = 0; i < k; i++)

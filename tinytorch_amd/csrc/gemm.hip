@@ -1494,6 +1494,15 @@ constexpr int SG = 4;  // 8-k groups per pipelined chunk
 // matmul whose input is a padones (of a relu output R), also the padones
 // input's gradient d1 = C[:, :-1] and d2 = d1 masked by R > 0 (d2 = d1
 // without R); d1 / d2 are (M x (N-1)) row-major.
+// w - lr * g with the product rounded on its own (this file is compiled with
+// contraction; the empty asm hides the product from the multiply-add
+// combiner), as the SGD kernels compute it
+__device__ __forceinline__ float sgd_sub(float w, float lr, float g) {
+  float p = lr * g;
+  asm volatile("" : "+v"(p));
+  return w - p;
+}
+
 struct SmallOut {
   float *C;
   long ldc;
@@ -1506,6 +1515,11 @@ struct SmallOut {
   // row ones_m of op(A) is all ones instead of A's (A, m-contiguous, then
   // has ones_m columns: the padones column [X, 1] of a matrix X)
   int ones_m = -1;
+  // C is a gradient: the weights wsgd (laid out as C) get the SGD step
+  // w -= lr * C from the stored value (multiply rounded on its own, as the
+  // SGD kernel computes it)
+  float *wsgd = nullptr;
+  float lr = 0.0f;
 };
 
 template <bool A_KC, bool B_NC, bool VA, bool VB>
@@ -1613,11 +1627,20 @@ __device__ __forceinline__ void small_tile(int M, int N, int K, const float *__r
     }
     return;
   }
+  float wv[16];
+  if (out.wsgd) {  // loaded up front, clamped, as rv
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int m = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
+      wv[r] = out.wsgd[(long)(m < M ? m : M - 1) * out.ldc + n];
+    }
+  }
 #pragma unroll
   for (int r = 0; r < 16; r++) {
     const int m = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
     if (m < M) {
       out.C[(long)m * out.ldc + n] = acc[r];
+      if (out.wsgd) out.wsgd[(long)m * out.ldc + n] = sgd_sub(wv[r], out.lr, acc[r]);
       if (pad && n < N - 1) {
         const long o = (long)m * (N - 1) + n;
         if (out.d1) out.d1[o] = acc[r];
@@ -1636,6 +1659,40 @@ gemm_small_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
   SmallOut out{C, ldc, nullptr, nullptr, nullptr};
   out.ones_m = ones_m;
   small_tile<A_KC, B_NC, VA, VB>(M, N, K, A, lda, B, ldb, out, kc, blockIdx.x, blockIdx.y, red);
+}
+
+// The weight gradient [X, 1]^T G of tt_k_gemm_tn_padones and an SGD step in
+// one launch: workgroups [0, gblocks) are the GEMM's tiles (gx across),
+// each also stepping its tile of wsgd; the rest step the plain tensors of
+// P, a thread an element (sgd_sub, as sgd_multi_kernel).
+struct SgdPlain {
+  float *w[TT_SGD_MAX];
+  const float *g[TT_SGD_MAX];
+  long n[TT_SGD_MAX];
+  long start[TT_SGD_MAX + 1];
+  int np;
+  float lr;
+};
+__global__ void __launch_bounds__(64 * SW)
+gemm_tn_padones_sgd_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
+                           const float *__restrict__ B, long ldb, float *__restrict__ C,
+                           long ldc, int kc, int ones_m, float *__restrict__ wsgd, int gx,
+                           int gblocks, SgdPlain P) {
+  __shared__ float red[(SW - 1) * 16 * 64];
+  if ((int)blockIdx.x >= gblocks) {
+    const long b = blockIdx.x - gblocks;
+    int t = 0;
+    while (t + 1 < P.np && b >= P.start[t + 1]) t++;
+    const long i = (b - P.start[t]) * (64 * SW) + threadIdx.x;
+    if (i < P.n[t]) P.w[t][i] = sgd_sub(P.w[t][i], P.lr, P.g[t][i]);
+    return;
+  }
+  SmallOut out{C, ldc, nullptr, nullptr, nullptr};
+  out.ones_m = ones_m;
+  out.wsgd = wsgd;
+  out.lr = P.lr;
+  small_tile<false, true, false, false>(M, N, K, A, lda, B, ldb, out, kc, blockIdx.x % gx,
+                                        blockIdx.x / gx, red);
 }
 
 // The same tiles with a forward epilogue (SmallOut::bias / relu / pad).
@@ -1965,17 +2022,50 @@ extern "C" int tt_k_matmul_bwd_small(const float *A, int M, int K, const float *
 // launched).
 extern "C" int tt_k_gemm_tn_padones(int rows, int Kx, int N, const float *X, const float *G,
                                     float *dW) {
-  if (rows <= 0 || Kx <= 0 || N <= 0 || !X || !G || !dW || g_force_tile >= 0) return -1;
+  if (rows <= 0 || Kx <= 0 || N <= 0 || g_force_tile >= 0) return -1;
   const int M = Kx + 1;
   const Opnd a{X, Kx, 0, 1}, g{G, N, 0, 1};
   const Plan p = plan(M, N, rows);
   if (p.tile == T256x256 || p.tile == T256x128 || p.tile == T128x128 ||
       !small_ok<false, true>(M, N, rows, a, g) || (M + 31) / 32 > 65535)
     return -1;
+  if (!dW) return 0;  // only asked whether the shape is covered
+  if (!X || !G) return -1;
   const int kc = ((rows + SW - 1) / SW + 7) / 8 * 8;
   const dim3 grid((unsigned)((N + 31) / 32), (unsigned)((M + 31) / 32));
   hipLaunchKernelGGL((gemm_small_kernel<false, true, false, false>), grid, dim3(64 * SW), 0,
                      stream(), M, N, rows, X, (long)Kx, G, (long)N, dW, (long)N, kc, Kx);
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+// tt_k_gemm_tn_padones and the SGD step wsgd -= lr * dW plus the plain
+// steps pw -= lr * pg, in one launch.  1: not covered, nothing launched.
+extern "C" int ttk_gemm_tn_padones_sgd(int rows, int Kx, int N, const float *X, const float *G,
+                                       float *dW, float *wsgd, float lr, float *const *pw,
+                                       const float *const *pg, const long *pn, int np) {
+  if (!X || !G || !dW || !wsgd || np < 0 || np > TT_SGD_MAX ||
+      tt_k_gemm_tn_padones(rows, Kx, N, nullptr, nullptr, nullptr) != 0)
+    return 1;
+  const int M = Kx + 1;
+  const int kc = ((rows + SW - 1) / SW + 7) / 8 * 8;
+  const int gx = (N + 31) / 32, gy = (M + 31) / 32;
+  const long gblocks = (long)gx * gy;
+  SgdPlain P{};
+  P.np = np;
+  P.lr = lr;
+  long tot = 0;
+  for (int t = 0; t < np; t++) {
+    P.w[t] = pw[t];
+    P.g[t] = pg[t];
+    P.n[t] = pn[t];
+    P.start[t] = tot;
+    tot += (pn[t] + 64 * SW - 1) / (64 * SW);
+  }
+  P.start[np] = tot;
+  if (gblocks + tot > 0x7fffffffL) return 1;
+  hipLaunchKernelGGL(gemm_tn_padones_sgd_kernel, dim3((unsigned)(gblocks + tot)), dim3(64 * SW),
+                     0, stream(), M, N, rows, X, (long)Kx, G, (long)N, dW, (long)N, kc, Kx, wsgd,
+                     gx, (int)gblocks, P);
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 

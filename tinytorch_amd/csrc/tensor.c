@@ -117,8 +117,12 @@ typedef struct TTLazyVal {
     Tensor *t, *src;
     int kind;                  /* 0: relu(src); 1: padones(src); 2: mean of src;
                                   3: the reduction `dwt` (every pending one runs
-                                  in the same launch) */
+                                  in the same launch); 4: [src, 1]^T src2, the
+                                  weight gradient of a matmul of padones(src)
+                                  (tt_k_gemm_tn_padones, dims rows Kx N) */
     TTDwtShared *dwt;
+    Tensor *src2;
+    int dims[3];
     struct TTLazyVal *next;
 } TTLazyVal;
 static TTLazyVal *g_lazy_vals;
@@ -130,6 +134,7 @@ static int lazy_add(Tensor *t, Tensor *src, int kind) {
     l->src = tt_retain(src);
     l->kind = kind;
     l->dwt = NULL;
+    l->src2 = NULL;
     l->next = g_lazy_vals;
     g_lazy_vals = l;
     return 0;
@@ -138,6 +143,15 @@ static int lazy_add(Tensor *t, Tensor *src, int kind) {
 int tt_lazy_relu(Tensor *t, Tensor *src) { return lazy_add(t, src, 0); }
 int tt_lazy_padones(Tensor *t, Tensor *src) { return lazy_add(t, src, 1); }
 int tt_lazy_ce_mean(Tensor *t, Tensor *src) { return lazy_add(t, src, 2); }
+
+int tt_lazy_gemm_tn_padones(Tensor *dw, Tensor *x, Tensor *g, int rows, int Kx, int N) {
+    if (lazy_add(dw, x, 4) != 0) return -1;
+    g_lazy_vals->src2 = tt_retain(g);
+    g_lazy_vals->dims[0] = rows;
+    g_lazy_vals->dims[1] = Kx;
+    g_lazy_vals->dims[2] = N;
+    return 0;
+}
 
 Tensor *tt_lazy_relu_src(const Tensor *t) {
     for (TTLazyVal *l = g_lazy_vals; l; l = l->next)
@@ -155,11 +169,11 @@ int tt_lazy_dwt(Tensor *dw, Tensor *db, const TTDwtJob *job) {
     }
     sh->job = *job;
     sh->refs = db ? 2 : 1;
-    a->t = dw; a->src = NULL; a->kind = 3; a->dwt = sh;
+    a->t = dw; a->src = NULL; a->kind = 3; a->dwt = sh; a->src2 = NULL;
     a->next = g_lazy_vals;
     g_lazy_vals = a;
     if (b) {
-        b->t = db; b->src = NULL; b->kind = 3; b->dwt = sh;
+        b->t = db; b->src = NULL; b->kind = 3; b->dwt = sh; b->src2 = NULL;
         b->next = g_lazy_vals;
         g_lazy_vals = b;
     }
@@ -265,6 +279,47 @@ int tt_lazy_dwt_sgd(float *const *w, Tensor *const *g, const long *n, int count,
     return rc;
 }
 
+int tt_lazy_gemm_sgd(float *const *w, Tensor *const *g, const long *n, int count, float lr) {
+    if (count <= 0 || count > TT_SGD_MAX || !g_lazy_vals) return 1;
+    TTLazyVal *pend = NULL;
+    int at = -1;
+    for (int i = 0; i < count; i++) {
+        for (TTLazyVal *l = g_lazy_vals; l; l = l->next)
+            if (l->kind == 4 && l->t == g[i]) {
+                if (pend) return 1;  /* one such gradient a launch */
+                pend = l;
+                at = i;
+            }
+        for (int k = 0; k < i; k++)
+            if (g[k] == g[i] || w[k] == w[i]) return 1;
+    }
+    if (!pend) return 1;
+    const float *x = tt_dev(pend->src), *gg = tt_dev(pend->src2);
+    if (!x || !gg) return -1;
+    float *pw[TT_SGD_MAX];
+    const float *pg[TT_SGD_MAX];
+    long pn[TT_SGD_MAX];
+    int np = 0;
+    for (int i = 0; i < count; i++) {
+        if (i == at) continue;
+        pw[np] = w[i];
+        pn[np] = n[i];
+        if (!(pg[np] = tt_dev(g[i]))) return -1;
+        np++;
+    }
+    const int rc = ttk_gemm_tn_padones_sgd(pend->dims[0], pend->dims[1], pend->dims[2], x, gg,
+                                           pend->t->dev, w[at], lr, pw, pg, pn, np);
+    if (rc == 1) return 1;
+    for (TTLazyVal **pp = &g_lazy_vals; *pp; pp = &(*pp)->next)
+        if (*pp == pend) { *pp = pend->next; break; }
+    if (rc != 0) pend->t->valid = 0;
+    else tt_mark_dev_written(pend->t);
+    tt_release(pend->src);
+    tt_release(pend->src2);
+    free(pend);
+    return rc;
+}
+
 /* a pending reduction's output released unread: the reduction skips it (and
  * is dropped when nothing of it is left) */
 static void dwt_drop_entry(TTLazyVal **pp) {
@@ -287,7 +342,7 @@ static void lazy_take(const Tensor *t, int from, int drop) {
 restart:
     for (TTLazyVal **pp = &g_lazy_vals; *pp; pp = &(*pp)->next) {
         TTLazyVal *l = *pp;
-        if ((from ? l->src : l->t) != t) continue;
+        if (from ? (l->src != t && l->src2 != t) : l->t != t) continue;
         if (l->kind == 3) {
             if (drop) dwt_drop_entry(pp);
             else dwt_flush_all();
@@ -296,18 +351,26 @@ restart:
         *pp = l->next;
         if (!drop) {
             const float *x = tt_dev(l->src);
-            const int rc = !x ? -1
+            const float *x2 = l->src2 ? tt_dev(l->src2) : NULL;
+            const int rc = !x || (l->src2 && !x2) ? -1
                            : l->kind == 1 ? tt_k_padones_fwd(x, l->t->dev, l->t->shape[0],
                                                              l->t->shape[1] - 1)
                            : l->kind == 2 ? tt_k_ce_mean_rows(x, l->t->dev, (int)l->src->numel)
+                           : l->kind == 4 ? tt_k_gemm_tn_padones(l->dims[0], l->dims[1],
+                                                                 l->dims[2], x, x2, l->t->dev)
                                           : tt_k_relu_fwd(x, l->t->dev, l->t->numel);
             if (rc != 0) l->t->valid = 0;
             else tt_mark_dev_written(l->t);
         }
         tt_release(l->src);
+        tt_release(l->src2);
         free(l);
         goto restart;
     }
+}
+
+void tt_lazy_before_write(Tensor *t) {
+    if (g_lazy_vals && t) lazy_take(t, 1, 0);
 }
 
 void tt_release(Tensor *t) {

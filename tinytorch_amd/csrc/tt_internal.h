@@ -64,6 +64,14 @@ int tt_lazy_dwt(Tensor *dw, Tensor *db, const TTDwtJob *job);
  * same launch when some g[i] is one's output; 1: none is (or the step does
  * not fit one launch) -- take the plain way, nothing done; 0 ok; < 0 error */
 int tt_lazy_dwt_sgd(float *const *w, Tensor *const *g, const long *n, int count, float lr);
+/* dw (Kx+1 x N) = [x, 1]^T g, the weight gradient of a matmul of padones(x)
+ * (x rows x Kx, g rows x N), written on first use; 0 ok, -1 no memory */
+int tt_lazy_gemm_tn_padones(Tensor *dw, Tensor *x, Tensor *g, int rows, int Kx, int N);
+/* as tt_lazy_dwt_sgd, for one pending tt_lazy_gemm_tn_padones gradient: the
+ * GEMM (stepping its weights) and the other tensors' steps in one launch */
+int tt_lazy_gemm_sgd(float *const *w, Tensor *const *g, const long *n, int count, float lr);
+/* t is about to be changed in place: run the recipes that read it */
+void tt_lazy_before_write(Tensor *t);
 Tensor *tt_lazy_relu_src(const Tensor *t);  /* src while t is still unwritten */
 int tt_defer_enabled(void);
 Tensor *tt_reshape_ex(const Tensor *a, const long *new_shape, int new_ndim, int defer);

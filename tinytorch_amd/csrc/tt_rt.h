@@ -80,6 +80,12 @@ int    ttk_dwt_reduce_jobs(const TTDwtJob *jobs, int n);
 int    ttk_dwt_reduce_sgd(const TTDwtJob *jobs, float *const *wdw, float *const *wdb, int nj,
                           float *const *pw, const float *const *pg, const long *pn, int np,
                           float lr);
+/* gemm.hip: tt_k_gemm_tn_padones (dW) with the SGD step wsgd -= lr * dW and
+ * the plain steps pw -= lr * pg (np <= TT_SGD_MAX) in one launch; 1: not
+ * covered, nothing launched. */
+int    ttk_gemm_tn_padones_sgd(int rows, int Kx, int N, const float *X, const float *G,
+                               float *dW, float *wsgd, float lr, float *const *pw,
+                               const float *const *pg, const long *pn, int np);
 /* conv.hip: free a job's partials without reducing them */
 void   ttk_dwt_job_drop(TTDwtJob *job);
 /* elementwise.hip: C = A * B + bias (A M x K, B K x N row-major) for N <= 16,
