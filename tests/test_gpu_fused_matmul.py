@@ -126,8 +126,10 @@ def test_matmul_bwd_small_shapes_taken(tlib):
                                       DevBuf(256 * 513).ptr, None, None, None) == 0
 
 
+# (the first two and the last three take the 16x16-tile kernel: ragged M and
+# N, K not a multiple of a wave's slice, waves with no k at all)
 BIAS_SHAPES = [(256, 784, 512), (256, 512, 256), (256, 256, 10), (128, 4096, 10), (7, 9, 5),
-               (300, 1000, 96), (64, 3, 40)]
+               (300, 1000, 96), (64, 3, 40), (250, 780, 500), (256, 20, 300), (1000, 64, 250)]
 
 
 @pytest.mark.parametrize("M,K,N", BIAS_SHAPES)

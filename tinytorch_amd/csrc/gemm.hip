@@ -1307,6 +1307,7 @@ int g_force_tile = -1, g_force_splits = -1;
 int g_direct = 1;  // direct-to-LDS 256x256 kernel enabled (tth_gemm_direct)
 int g_mid = 1;     // 64x64 direct-load kernel for plain GEMMs (tth_gemm_mid)
 int g_small = 1;   // 32x32 register kernel for small plain GEMMs (tth_gemm_small)
+int g_t16 = 1;     // 16x16 forward kernel for GEMMs below a full 32x32 grid (tth_gemm_t16)
 
 struct Plan {
   int tile, splits, kchunk;
@@ -1704,6 +1705,119 @@ gemm_small_epi_kernel(int M, int N, int K, const float *__restrict__ A, long lda
   small_tile<true, true, VA, VB>(M, N, K, A, lda, B, ldb, out, kc, blockIdx.x, blockIdx.y, red);
 }
 
+// C = A * B + bias (and relu / padded relu) on 16x16 tiles for GEMMs too
+// small to fill the chip with 32x32 tiles (the MLP's hidden layers: 256 x
+// 512 x 784, 256 x 256 x 512).  A row-major M x K (rows 16-byte aligned,
+// K % 4 == 0), B row-major K x N.  Eight waves split K into equal slices of
+// NCH 16-k chunks; a wave issues all of its slice's loads at once (NCH x 8
+// registers a lane) so it waits for one round trip, not one per chunk, then
+// runs 4 * NCH 16x16x4 MFMAs; the wave sums are added in LDS in wave order.
+// (Four waves a workgroup measured slower, sixteen no faster.)
+// Lane l (r = l % 16, q = l / 16) loads A[m0 + r][kb + 4q .. 4q+3] and
+// B[kb + 4q + i][n0 + r]; MFMA i of a chunk then sums k = kb + 4q + i over
+// q.  Loads past the matrix are clamped to it and their values zeroed.
+typedef float f32x4t __attribute__((ext_vector_type(4)));
+constexpr int T16W = 8;  // waves per workgroup
+template <int NCH>
+__global__ void __launch_bounds__(64 * T16W)
+gemm_t16_epi_kernel(int M, int N, int K, const float *__restrict__ A,
+                    const float *__restrict__ B, SmallOut out, int kc) {
+  __shared__ float red[(T16W - 1) * 4 * 64];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, q = lane >> 4;
+  const int m0 = blockIdx.y * 16, n0 = blockIdx.x * 16;
+  const int mr = min(m0 + r, M - 1), nr = min(n0 + r, N - 1);
+  const int k0 = w * kc, k1 = min(K, k0 + kc);
+  const float *__restrict__ ap = A + (long)mr * K;
+  const float *__restrict__ bp = B + nr;
+  float4 av[NCH];
+  float bv[NCH][4];
+#pragma unroll
+  for (int c = 0; c < NCH; c++) {
+    const int kq = k0 + 16 * c + 4 * q;
+    av[c] = *reinterpret_cast<const float4 *>(ap + min(kq, K - 4));
+#pragma unroll
+    for (int i = 0; i < 4; i++) bv[c][i] = bp[(long)min(kq + i, K - 1) * N];
+  }
+  f32x4t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int c = 0; c < NCH; c++) {
+    const int kq = k0 + 16 * c + 4 * q;
+    const float a4[4] = {av[c].x, av[c].y, av[c].z, av[c].w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const bool in = kq + i < k1;
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(in ? a4[i] : 0.0f, in ? bv[c][i] : 0.0f, acc, 0,
+                                                 0, 0);
+    }
+  }
+  if (w > 0) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) red[((w - 1) * 4 + i) * 64 + lane] = acc[i];
+  }
+  __syncthreads();
+  if (w > 0) return;
+#pragma unroll
+  for (int o = 0; o < T16W - 1; o++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[i] += red[(o * 4 + i) * 64 + lane];
+  const int n = n0 + r;
+  if (n >= N) return;
+  const float bn = out.bias[n];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int m = m0 + 4 * q + i;
+    if (m < M) {
+      const float v = acc[i] + bn;
+      out.C[(long)m * out.ldc + n] = v;
+      const float o = v > 0.0f ? v : 0.0f;
+      if (out.relu) out.relu[(long)m * N + n] = o;
+      if (out.pad) {
+        float *pr = out.pad + (long)m * (N + 1);
+        pr[n] = o;
+        if (n == N - 1) pr[N] = 1.0f;
+      }
+    }
+  }
+}
+
+// The 16x16-tile forward when it applies: 0 launched, 1 not covered, < 0
+// launch error.  Taken for at least 256 tiles (one a CU) and at most 1024,
+// K <= 1024.
+int run_t16(int M, int N, int K, const float *A, const float *B, const SmallOut &out) {
+  const long tiles = (long)((M + 15) / 16) * ((N + 15) / 16);
+  if (!g_t16 || K < 16 || K % 4 || !aligned16(A) || tiles < 256 || tiles > 1024 ||
+      K > 1024 || (M + 15) / 16 > 65535)
+    return 1;
+  const int nch = (K + 16 * T16W - 1) / (16 * T16W);  // 16-k chunks a wave
+  const int kc = 16 * nch;
+  const dim3 grid((unsigned)((N + 15) / 16), (unsigned)((M + 15) / 16));
+#define TT_T16(NCH_)                                                                          \
+  hipLaunchKernelGGL((gemm_t16_epi_kernel<NCH_>), grid, dim3(64 * T16W), 0, stream(), M, N, K, A, B, \
+                     out, kc)
+  switch (nch) {
+    case 1: TT_T16(1); break;
+    case 2: TT_T16(2); break;
+    case 3: TT_T16(3); break;
+    case 4: TT_T16(4); break;
+    case 5: TT_T16(5); break;
+    case 6: TT_T16(6); break;
+    case 7: TT_T16(7); break;
+    case 8: TT_T16(8); break;
+    case 9: TT_T16(9); break;
+    case 10: TT_T16(10); break;
+    case 11: TT_T16(11); break;
+    case 12: TT_T16(12); break;
+    case 13: TT_T16(13); break;
+    case 14: TT_T16(14); break;
+    case 15: TT_T16(15); break;
+    default: TT_T16(16); break;
+  }
+#undef TT_T16
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
 // Both gradients of a matmul C = A * B in one launch of small-GEMM tiles:
 // dA = G * B^T (the tiles of tt_k_gemm(M, K, N, G, N, 0, B, N, 1, ...)) in
 // workgroups [0, nba), dB = A^T * G (tt_k_gemm(K, N, M, A, K, 1, G, N, 0, ...))
@@ -1942,6 +2056,11 @@ extern "C" int tth_gemm_small(int on) {
   return 0;
 }
 
+extern "C" int tth_gemm_t16(int on) {
+  g_t16 = on ? 1 : 0;
+  return 0;
+}
+
 extern "C" int tth_gemm_config(int tile, int splits) {
   if (tile >= NTILE || splits > 1024) return -1;
   g_force_tile = tile;
@@ -2082,6 +2201,14 @@ extern "C" int tt_k_gemm_bias_relu_pad(int M, int N, int K, const float *A, cons
   if (g_force_tile < 0) {  // skinny outputs (a classifier): a workgroup per row
     const int rr = ttk_gemm_rows(A, B, bias, C, R, P, M, N, K, nullptr);
     if (rr != 1) return rr;
+  }
+  if (g_force_tile < 0) {  // 16x16 tiles below a full grid of 32x32 ones
+    SmallOut out{C, N, nullptr, nullptr, nullptr};
+    out.bias = bias;
+    out.relu = R;
+    out.pad = P;
+    const int rt = run_t16(M, N, K, A, B, out);
+    if (rt != 1) return rt;
   }
   const Opnd a{A, K, 0, 1}, b{B, N, 0, 1};
   auto big = [](const Plan &p) {
