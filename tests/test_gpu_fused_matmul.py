@@ -126,10 +126,13 @@ def test_matmul_bwd_small_shapes_taken(tlib):
                                       DevBuf(256 * 513).ptr, None, None, None) == 0
 
 
-# (the first two and the last three take the 16x16-tile kernel: ragged M and
-# N, K not a multiple of a wave's slice, waves with no k at all)
+# (the first two and (250, 780, 500) .. (1000, 64, 250) take the 16x16-tile
+# kernel: ragged M and N, K not a multiple of a wave's slice, waves with no
+# k at all; (128, 4096, 10) and the last three its split-K form for skinny
+# outputs: ragged rows, K not a multiple of a slice, 1 to 63 row tiles)
 BIAS_SHAPES = [(256, 784, 512), (256, 512, 256), (256, 256, 10), (128, 4096, 10), (7, 9, 5),
-               (300, 1000, 96), (64, 3, 40), (250, 780, 500), (256, 20, 300), (1000, 64, 250)]
+               (300, 1000, 96), (64, 3, 40), (250, 780, 500), (256, 20, 300), (1000, 64, 250),
+               (100, 2048, 7), (1000, 3000, 3), (16, 4100, 16)]
 
 
 @pytest.mark.parametrize("M,K,N", BIAS_SHAPES)
@@ -232,7 +235,8 @@ def test_autograd_padones_input_unpadded(tlib, read_first):
 
 # (M, N, K): the CNN classifier (128 x 4096 -> 10), the MLP's last layer
 # (256 x 256 -> 10), wider rows, and a shape whose GEMM takes no split-K path
-CE_SHAPES = [(128, 10, 4096), (256, 10, 256), (100, 32, 2000), (7, 3, 4100), (512, 10, 64)]
+CE_SHAPES = [(128, 10, 4096), (256, 10, 256), (100, 32, 2000), (7, 3, 4100), (512, 10, 64),
+             (33, 10, 8192), (200, 16, 2052)]
 
 
 @pytest.mark.parametrize("M,N,K", CE_SHAPES)

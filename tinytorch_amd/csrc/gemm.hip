@@ -1782,6 +1782,68 @@ gemm_t16_epi_kernel(int M, int N, int K, const float *__restrict__ A,
   }
 }
 
+// Partial products of a skinny GEMM (N <= 16 columns, a long K: the CNN
+// classifier's 128 x 4096 -> 10) for split-K: workgroup (tile_n, tile_m, z)
+// multiplies its 16x16 tile over k slice z on the same eight-wave scheme and
+// stores the tile's valid part to ws[z] (M x N), for reduce_splits.  A
+// row-major (lda, rows 16-byte aligned, lda % 4 == 0, K % 4 == 0), B
+// row-major (ldb).
+template <int NCH>
+__global__ void __launch_bounds__(64 * T16W)
+gemm_t16_split_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
+                      const float *__restrict__ B, long ldb, float *__restrict__ ws,
+                      int kslice) {
+  __shared__ float red[(T16W - 1) * 4 * 64];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, q = lane >> 4;
+  const int m0 = blockIdx.y * 16, n0 = blockIdx.x * 16;
+  const int mr = min(m0 + r, M - 1), nr = min(n0 + r, N - 1);
+  const int ks = blockIdx.z * kslice, ke = min(K, ks + kslice);
+  const int k0 = ks + w * 16 * NCH, k1 = min(ke, k0 + 16 * NCH);
+  const float *__restrict__ ap = A + (long)mr * lda;
+  const float *__restrict__ bp = B + nr;
+  float4 av[NCH];
+  float bv[NCH][4];
+#pragma unroll
+  for (int c = 0; c < NCH; c++) {
+    const int kq = k0 + 16 * c + 4 * q;
+    av[c] = *reinterpret_cast<const float4 *>(ap + min(kq, K - 4));
+#pragma unroll
+    for (int i = 0; i < 4; i++) bv[c][i] = bp[(long)min(kq + i, K - 1) * ldb];
+  }
+  f32x4t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int c = 0; c < NCH; c++) {
+    const int kq = k0 + 16 * c + 4 * q;
+    const float a4[4] = {av[c].x, av[c].y, av[c].z, av[c].w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const bool in = kq + i < k1;
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(in ? a4[i] : 0.0f, in ? bv[c][i] : 0.0f, acc, 0,
+                                                 0, 0);
+    }
+  }
+  if (w > 0) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) red[((w - 1) * 4 + i) * 64 + lane] = acc[i];
+  }
+  __syncthreads();
+  if (w > 0) return;
+#pragma unroll
+  for (int o = 0; o < T16W - 1; o++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[i] += red[(o * 4 + i) * 64 + lane];
+  const int n = n0 + r;
+  if (n >= N) return;
+  float *wz = ws + (long)blockIdx.z * M * N;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int m = m0 + 4 * q + i;
+    if (m < M) wz[(long)m * N + n] = acc[i];
+  }
+}
+
 // The 16x16-tile forward when it applies: 0 launched, 1 not covered, < 0
 // launch error.  Taken for at least 256 tiles (one a CU) and at most 1024,
 // K <= 1024.
@@ -1968,6 +2030,41 @@ int run(int M, int N, int K, Opnd A, Opnd B, float *C, long ldc, const float *bi
       // K % 4 != 0 with k-contiguous rows): the same kernel with 4-byte loads
       if (g_mid && 2.0 * M * N * K >= 1e9 && A.ld <= (1L << 22) && B.ld <= (1L << 22))
         return run_mid<A_KC, B_NC, true>(M, N, K, A, B, C, ldc);
+    }
+  }
+  if constexpr (A_KC && B_NC && !A_PERM && !B_PERM && !B_I2C) {
+    // skinny outputs over a long K: 16x16 tiles split over K (partials of
+    // eight-wave workgroups), then the usual reduction and epilogue
+    const long tiles = (long)((M + 15) / 16) * ((N + 15) / 16);
+    if (g_t16 && g_force_tile < 0 && N <= 16 && K >= 2048 && K % 4 == 0 && A.ld % 4 == 0 &&
+        aligned16(A.p) && tiles <= 128 && (M + 15) / 16 <= 65535) {
+      int S = (int)(256 / tiles);
+      if (S > (K + 127) / 128) S = (K + 127) / 128;
+      const int kslice = ((K + S - 1) / S + 127) / 128 * 128;
+      S = (K + kslice - 1) / kslice;
+      const int nch = kslice / 128;
+      if (nch <= 16) {
+        float *ws = ws_alloc(sizeof(float) * (size_t)M * N * S);
+        if (!ws) return -2;
+        const dim3 grid((unsigned)((N + 15) / 16), (unsigned)((M + 15) / 16), (unsigned)S);
+#define TT_T16S(NCH_)                                                                         \
+  hipLaunchKernelGGL((gemm_t16_split_kernel<NCH_>), grid, dim3(64 * T16W), 0, stream(), M, N, K, \
+                     A.p, A.ld, B.p, B.ld, ws, kslice)
+        switch (nch) {
+          case 1: TT_T16S(1); break;
+          case 2: TT_T16S(2); break;
+          case 3: TT_T16S(3); break;
+          case 4: TT_T16S(4); break;
+          case 5: case 6: TT_T16S(6); break;
+          case 7: case 8: TT_T16S(8); break;
+          default: TT_T16S(16); break;
+        }
+#undef TT_T16S
+        if (hipGetLastError() != hipSuccess) { ws_free(ws); return -3; }
+        const int rc = reduce_splits<EPI>(ws, C, M, N, S, ldc, bias, HW);
+        ws_free(ws);
+        return rc;
+      }
     }
   }
   if constexpr (B_I2C) {
