@@ -89,7 +89,7 @@ int    ttk_gemm_tn_padones_sgd(int rows, int Kx, int N, const float *X, const fl
 /* conv.hip: free a job's partials without reducing them */
 void   ttk_dwt_job_drop(TTDwtJob *job);
 /* elementwise.hip: C = A * B + bias (A M x K, B K x N row-major) for N <= 16,
- * one workgroup per row, with R = relu(C) / P = [relu(C), 1] when given, or
+ * one workgroup per 16 rows (K < 16: per row), with R = relu(C) / P = [relu(C), 1] when given, or
  * with the softmax-CE of each row when ce is given (ce->bias unused).  1:
  * not covered (N > 16, K > 1024; with ce, M > TT_CE_ARG_ROWS), nothing
  * launched. */
