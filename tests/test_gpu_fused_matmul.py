@@ -130,10 +130,12 @@ def test_matmul_bwd_small_shapes_taken(tlib):
 # kernel: ragged M and N, K not a multiple of a wave's slice, waves with no
 # k at all; (128, 4096, 10) and the last three its split-K form for skinny
 # outputs: ragged rows, K not a multiple of a slice, 1 to 63 row tiles;
-# (100, 30, 7) the 16-row classifier tiles with unaligned rows)
+# (100, 30, 7) the 16-row classifier tiles with unaligned rows; (256, 784,
+# 512) and (250, 500, 1000) the 16x32 tiles, the latter with a ragged last
+# column block)
 BIAS_SHAPES = [(256, 784, 512), (256, 512, 256), (256, 256, 10), (128, 4096, 10), (7, 9, 5),
                (300, 1000, 96), (64, 3, 40), (250, 780, 500), (256, 20, 300), (1000, 64, 250),
-               (100, 2048, 7), (1000, 3000, 3), (16, 4100, 16), (100, 30, 7)]
+               (100, 2048, 7), (1000, 3000, 3), (16, 4100, 16), (100, 30, 7), (250, 500, 1000)]
 
 
 @pytest.mark.parametrize("M,K,N", BIAS_SHAPES)

@@ -1712,35 +1712,41 @@ gemm_small_epi_kernel(int M, int N, int K, const float *__restrict__ A, long lda
 // NCH 16-k chunks; a wave issues all of its slice's loads at once (NCH x 8
 // registers a lane) so it waits for one round trip, not one per chunk, then
 // runs 4 * NCH 16x16x4 MFMAs; the wave sums are added in LDS in wave order.
-// (Four waves a workgroup measured slower, sixteen no faster.)
+// (Four waves a workgroup measured slower, sixteen no faster.)  TN column
+// blocks of 16 per workgroup share the A fragments.
 // Lane l (r = l % 16, q = l / 16) loads A[m0 + r][kb + 4q .. 4q+3] and
 // B[kb + 4q + i][n0 + r]; MFMA i of a chunk then sums k = kb + 4q + i over
 // q.  Loads past the matrix are clamped to it and their values zeroed.
 typedef float f32x4t __attribute__((ext_vector_type(4)));
 constexpr int T16W = 8;  // waves per workgroup
-template <int NCH>
+template <int NCH, int TN>
 __global__ void __launch_bounds__(64 * T16W)
 gemm_t16_epi_kernel(int M, int N, int K, const float *__restrict__ A,
                     const float *__restrict__ B, SmallOut out, int kc) {
-  __shared__ float red[(T16W - 1) * 4 * 64];
+  __shared__ float red[(T16W - 1) * 4 * TN * 64];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, q = lane >> 4;
-  const int m0 = blockIdx.y * 16, n0 = blockIdx.x * 16;
-  const int mr = min(m0 + r, M - 1), nr = min(n0 + r, N - 1);
+  const int m0 = blockIdx.y * 16, n0 = blockIdx.x * 16 * TN;
+  const int mr = min(m0 + r, M - 1);
   const int k0 = w * kc, k1 = min(K, k0 + kc);
   const float *__restrict__ ap = A + (long)mr * K;
-  const float *__restrict__ bp = B + nr;
   float4 av[NCH];
-  float bv[NCH][4];
+  float bv[NCH][TN][4];
 #pragma unroll
   for (int c = 0; c < NCH; c++) {
     const int kq = k0 + 16 * c + 4 * q;
     av[c] = *reinterpret_cast<const float4 *>(ap + min(kq, K - 4));
 #pragma unroll
-    for (int i = 0; i < 4; i++) bv[c][i] = bp[(long)min(kq + i, K - 1) * N];
+    for (int t = 0; t < TN; t++) {
+      const float *__restrict__ bp = B + min(n0 + 16 * t + r, N - 1);
+#pragma unroll
+      for (int i = 0; i < 4; i++) bv[c][t][i] = bp[(long)min(kq + i, K - 1) * N];
+    }
   }
-  f32x4t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4t acc[TN];
+#pragma unroll
+  for (int t = 0; t < TN; t++) acc[t] = f32x4t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int c = 0; c < NCH; c++) {
     const int kq = k0 + 16 * c + 4 * q;
@@ -1748,35 +1754,44 @@ gemm_t16_epi_kernel(int M, int N, int K, const float *__restrict__ A,
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const bool in = kq + i < k1;
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(in ? a4[i] : 0.0f, in ? bv[c][i] : 0.0f, acc, 0,
-                                                 0, 0);
+#pragma unroll
+      for (int t = 0; t < TN; t++)
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(in ? a4[i] : 0.0f, in ? bv[c][t][i] : 0.0f,
+                                                      acc[t], 0, 0, 0);
     }
   }
   if (w > 0) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) red[((w - 1) * 4 + i) * 64 + lane] = acc[i];
+    for (int t = 0; t < TN; t++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) red[(((w - 1) * TN + t) * 4 + i) * 64 + lane] = acc[t][i];
   }
   __syncthreads();
   if (w > 0) return;
 #pragma unroll
   for (int o = 0; o < T16W - 1; o++)
 #pragma unroll
-    for (int i = 0; i < 4; i++) acc[i] += red[(o * 4 + i) * 64 + lane];
-  const int n = n0 + r;
-  if (n >= N) return;
-  const float bn = out.bias[n];
+    for (int t = 0; t < TN; t++)
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int m = m0 + 4 * q + i;
-    if (m < M) {
-      const float v = acc[i] + bn;
-      out.C[(long)m * out.ldc + n] = v;
-      const float o = v > 0.0f ? v : 0.0f;
-      if (out.relu) out.relu[(long)m * N + n] = o;
-      if (out.pad) {
-        float *pr = out.pad + (long)m * (N + 1);
-        pr[n] = o;
-        if (n == N - 1) pr[N] = 1.0f;
+      for (int i = 0; i < 4; i++) acc[t][i] += red[((o * TN + t) * 4 + i) * 64 + lane];
+#pragma unroll
+  for (int t = 0; t < TN; t++) {
+    const int n = n0 + 16 * t + r;
+    if (n >= N) continue;
+    const float bn = out.bias[n];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int m = m0 + 4 * q + i;
+      if (m < M) {
+        const float v = acc[t][i] + bn;
+        out.C[(long)m * out.ldc + n] = v;
+        const float o = v > 0.0f ? v : 0.0f;
+        if (out.relu) out.relu[(long)m * N + n] = o;
+        if (out.pad) {
+          float *pr = out.pad + (long)m * (N + 1);
+          pr[n] = o;
+          if (n == N - 1) pr[N] = 1.0f;
+        }
       }
     }
   }
@@ -1854,10 +1869,18 @@ int run_t16(int M, int N, int K, const float *A, const float *B, const SmallOut 
     return 1;
   const int nch = (K + 16 * T16W - 1) / (16 * T16W);  // 16-k chunks a wave
   const int kc = 16 * nch;
-  const dim3 grid((unsigned)((N + 15) / 16), (unsigned)((M + 15) / 16));
+  // two column blocks a workgroup (16x32 tiles, each A fragment feeding two
+  // MFMAs) while that still leaves 256 workgroups: 256x512x784 8.6 -> ~7.5
+  // us; at 256 tiles the halved grid is slower
+  const int tn = tiles >= 512 ? 2 : 1;
+  const dim3 grid((unsigned)((N + 16 * tn - 1) / (16 * tn)), (unsigned)((M + 15) / 16));
 #define TT_T16(NCH_)                                                                          \
-  hipLaunchKernelGGL((gemm_t16_epi_kernel<NCH_>), grid, dim3(64 * T16W), 0, stream(), M, N, K, A, B, \
-                     out, kc)
+  if (tn == 2)                                                                                \
+    hipLaunchKernelGGL((gemm_t16_epi_kernel<NCH_, 2>), grid, dim3(64 * T16W), 0, stream(), M, N, \
+                       K, A, B, out, kc);                                                     \
+  else                                                                                        \
+    hipLaunchKernelGGL((gemm_t16_epi_kernel<NCH_, 1>), grid, dim3(64 * T16W), 0, stream(), M, N, \
+                       K, A, B, out, kc)
   switch (nch) {
     case 1: TT_T16(1); break;
     case 2: TT_T16(2); break;
