@@ -161,6 +161,32 @@ def test_gemm_bias_relu_pad_vs_padded_product(tlib, M, K, N, epi):
         assert bits_equal(P.to_np((M, N + 1)), orc.padones_fwd(orc.relu_fwd(c)))
 
 
+@pytest.mark.parametrize("M,K,N", [(256, 784, 512), (128, 4096, 10), (256, 256, 10)])
+def test_gemm_bias_t16_off_same_bar(tlib, M, K, N):
+    """With the 16x16-tile kernels switched off (tth_gemm_t16(0)) the same
+    shapes take the split-K / row kernels: C within the GEMM bar of the
+    oracle either way."""
+    X = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    W = (rng.standard_normal((K + 1, N)) / np.sqrt(K)).astype(np.float32)
+    dX, dW = DevBuf.from_np(X), DevBuf.from_np(W)
+    bias_ptr = dW.ptr + 4 * K * N
+    ref = orc.sgemm(orc.padones_fwd(X), W)
+    amax = max(1.0, float(np.abs(W).max()))
+    out = []
+    print("gemm_bias t16 on/off", M, K, N, flush=True)
+    try:
+        for on in (1, 0):
+            check(tlib.tth_gemm_t16(on), "t16")
+            C = DevBuf(M * N)
+            check(tlib.tt_k_gemm_bias_relu_pad(M, N, K, dX.ptr, dW.ptr, bias_ptr, C.ptr, None,
+                                               None), "bias")
+            out.append(C.to_np((M, N)))
+    finally:
+        check(tlib.tth_gemm_t16(1), "t16 on")
+    for c in out:
+        assert np.abs(c - ref).max() / (np.sqrt(K + 1) * amax) <= 1e-4
+
+
 # (rows, Kx, N, taken): the MLP's first layer (784 -> 512 at batch 256),
 # ragged widths, and a shape the small-GEMM tiles do not take (too few
 # tiles: -1, nothing launched)
