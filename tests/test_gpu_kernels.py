@@ -50,7 +50,26 @@ def run_gemm(tlib, M, N, K, ta, tb, A, B):
 
 SHAPES = [(1, 1, 1), (3, 4, 5), (17, 13, 5), (5, 300, 3), (9, 33, 256), (64, 16, 512),
           (128, 128, 32), (100, 70, 33), (1000, 1003, 997), (256, 512, 785), (256, 10, 257),
-          (513, 65, 1024), (31, 2000, 7)]
+          (513, 65, 1024), (31, 2000, 7), (100, 7, 3000)]
+
+
+def test_gemm_skinny_split_leading_dims(tlib):
+    """A skinny GEMM over a long K (the 16x16 split-K tiles) with leading
+    dimensions wider than the rows: A (lda = K + 4), B (ldb = N + 3) and C
+    (ldc = N + 1) read and written only where the matrix is; the padding of
+    C stays as it was."""
+    M, N, K = 70, 9, 2500
+    A = u(M, K + 4)
+    B = u(K, N + 3)
+    C0 = np.full((M, N + 1), 7.0, np.float32)
+    dA, dB, dC = DevBuf.from_np(A), DevBuf.from_np(B), DevBuf.from_np(C0)
+    print("gemm skinny split ld", M, N, K, flush=True)
+    check(tlib.tt_k_gemm(M, N, K, dA.ptr, K + 4, 0, dB.ptr, N + 3, 0, dC.ptr, N + 1), "gemm")
+    C = dC.to_np((M, N + 1))
+    ref = orc.sgemm(A[:, :K], B[:, :N])
+    norm, rel = gemm_err(C[:, :N], ref, K, np.abs(A).max(), np.abs(B).max())
+    assert norm <= GEMM_TOL and rel <= GEMM_TOL, (norm, rel)
+    assert np.all(C[:, N] == 7.0)
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)
