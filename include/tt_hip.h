@@ -112,10 +112,11 @@ int tth_gemm_mid(int on);
  * for plain GEMMs below 2^29 flops with at least 128 output tiles whose
  * k-contiguous operands have 16-byte aligned rows. */
 int tth_gemm_small(int on);
-/* Tuning hook: 0 disables, 1 (default) enables the 16x16-tile kernel (K
- * split over eight waves, each loading its whole slice before its MFMAs)
- * that tt_k_gemm_bias_relu_pad uses for 256-1024 output tiles of 16x16,
- * K <= 1024, 16-byte aligned A rows. */
+/* Tuning hook: 0 disables, 1 (default) enables the 16x16-tile kernels (K
+ * split over eight waves, each loading its whole slice before its MFMAs):
+ * tt_k_gemm_bias_relu_pad's for 256-1024 output tiles of 16x16, K <= 1024,
+ * 16-byte aligned A rows; and the split-K partials of GEMMs with N <= 16
+ * and K >= 2048 (at most 128 tiles). */
 int tth_gemm_t16(int on);
 
 /* Convolution GEMMs over the im2col matrix col[(c,kh,kw)][(n,ho,wo)]
