@@ -197,7 +197,9 @@ class CnnStep:
         assert t
         return t
 
-    def step(self, lr=0.0):
+    def step(self, lr=0.0, probe=None):
+        """One step; `probe(L, loss)` (tests only) runs after the SGD update,
+        before the graph is released."""
         L, t = self.L, self.t
         nodes = []
 
@@ -217,6 +219,8 @@ class CnnStep:
         L.ag_backward(loss)
         ws = (ctypes.c_void_p * 5)(w1, b1, w2, b2, wfc)
         assert L.ag_sgd_step_many(ws, 5, ctypes.c_float(lr)) == 0
+        if probe is not None:
+            probe(L, loss)
         for n in nodes:
             L.ag_release(n)
 
@@ -236,7 +240,8 @@ class MlpStep:
             shp = (ctypes.c_long * 2)(*a.shape)
             self.t.append(L.tt_fromdata(np.ascontiguousarray(a).ctypes.data_as(F32P), shp, 2))
 
-    def step(self, lr=0.0):
+    def step(self, lr=0.0, probe=None):
+        """One step; `probe(L, loss)` as in CnnStep.step."""
         L = self.L
         nodes = []
 
@@ -253,6 +258,8 @@ class MlpStep:
         L.ag_backward(loss)
         ws = (ctypes.c_void_p * 3)(*W)
         assert L.ag_sgd_step_many(ws, 3, ctypes.c_float(lr)) == 0
+        if probe is not None:
+            probe(L, loss)
         for n in nodes:
             L.ag_release(n)
 

@@ -620,3 +620,43 @@ def test_sgd_step_runs_pending_reductions(tlib):
     fused, plain = run(False), run(True)
     for a, b in zip(fused, plain):
         assert _bits_equal(a, b)
+
+
+def test_sgd_step_more_pending_reductions_than_one_launch_takes(tlib):
+    """Five convolutions, so five pending weight-gradient reductions at the
+    SGD step: more than the fused reduce + step launch takes (four jobs).
+    The step then runs the reductions in their own launch and steps the
+    plain way; weights and gradients bit for bit those of reading every
+    gradient first."""
+    import ctypes
+    from tinytorch_amd.torch_py import Node
+    r = np.random.default_rng(43)
+    chans = [16, 24, 16, 24, 16, 24]
+    x = r.uniform(-1, 1, (4, chans[0], 8, 8)).astype(np.float32)
+    ps = []
+    for ci, co in zip(chans[:-1], chans[1:]):
+        ps.append(r.uniform(-0.3, 0.3, (co, ci, 3, 3)).astype(np.float32))
+        ps.append(r.uniform(-1, 1, co).astype(np.float32))
+    g = r.standard_normal((4, chans[-1], 8, 8)).astype(np.float32)
+
+    def run(read_first):
+        X = Node.leaf(x, False)
+        P = [Node.leaf(p) for p in ps]
+        hs = [X]
+        for i in range(5):
+            hs.append(hs[-1].conv2d(P[2 * i], P[2 * i + 1], (1, 1), (1, 1)))
+        hs[-1].backward(g)
+        if read_first:
+            for p in P:
+                p.grad()
+        arr = (ctypes.c_void_p * len(P))(*[p.ptr for p in P])
+        assert tlib.ag_sgd_step_many(arr, len(P), ctypes.c_float(0.05)) == 0
+        out = [p.value() for p in P] + [p.grad() for p in P]
+        for nd in hs[::-1] + P:
+            nd.release()
+        return out
+
+    print("sgd step with five pending conv reductions", flush=True)
+    fused, plain = run(False), run(True)
+    for a, b in zip(fused, plain):
+        assert _bits_equal(a, b)

@@ -135,7 +135,11 @@ def test_matmul_bwd_small_shapes_taken(tlib):
 # column block)
 BIAS_SHAPES = [(256, 784, 512), (256, 512, 256), (256, 256, 10), (128, 4096, 10), (7, 9, 5),
                (300, 1000, 96), (64, 3, 40), (250, 780, 500), (256, 20, 300), (1000, 64, 250),
-               (100, 2048, 7), (1000, 3000, 3), (16, 4100, 16), (100, 30, 7), (250, 500, 1000)]
+               (100, 2048, 7), (1000, 3000, 3), (16, 4100, 16), (100, 30, 7), (250, 500, 1000),
+               # the skinny split-K kernel's other chunk counts per wave:
+               # 16, 8, 2, 3, 4, 5 (run as 6) and 7 (run as 8) chunks of 16 k
+               (2048, 4096, 10), (1024, 4096, 16), (512, 2048, 16), (512, 3072, 10),
+               (512, 4096, 10), (1024, 2560, 10), (1024, 3584, 12)]
 
 
 @pytest.mark.parametrize("M,K,N", BIAS_SHAPES)
@@ -161,7 +165,8 @@ def test_gemm_bias_relu_pad_vs_padded_product(tlib, M, K, N, epi):
         assert bits_equal(P.to_np((M, N + 1)), orc.padones_fwd(orc.relu_fwd(c)))
 
 
-@pytest.mark.parametrize("M,K,N", [(256, 784, 512), (128, 4096, 10), (256, 256, 10)])
+@pytest.mark.parametrize("M,K,N", [(256, 784, 512), (128, 4096, 10), (256, 256, 10),
+                                   (2048, 4096, 10), (1024, 4096, 16), (512, 2048, 16)])
 def test_gemm_bias_t16_off_same_bar(tlib, M, K, N):
     """With the 16x16-tile kernels switched off (tth_gemm_t16(0)) the same
     shapes take the split-K / row kernels: C within the GEMM bar of the
@@ -265,7 +270,7 @@ def test_autograd_padones_input_unpadded(tlib, read_first):
 # (M, N, K): the CNN classifier (128 x 4096 -> 10), the MLP's last layer
 # (256 x 256 -> 10), wider rows, and a shape whose GEMM takes no split-K path
 CE_SHAPES = [(128, 10, 4096), (256, 10, 256), (100, 32, 2000), (7, 3, 4100), (512, 10, 64),
-             (33, 10, 8192), (200, 16, 2052)]
+             (33, 10, 8192), (200, 16, 2052), (2048, 10, 4096), (1024, 16, 4096), (512, 16, 2048)]
 
 
 @pytest.mark.parametrize("M,N,K", CE_SHAPES)
@@ -413,3 +418,51 @@ def test_mlp_first_layer_grad_pending_into_sgd(tlib, second_pass):
     want = xp.T @ gh
     e = np.abs(fused[2] - want).max() / np.abs(want).max()
     assert e <= 1e-4, e
+
+
+@pytest.mark.parametrize("read_first", [False, True])
+def test_sgd_step_of_a_tensor_a_pending_gradient_reads(tlib, read_first):
+    """One tensor T is both a trained leaf and, through a no-gradient leaf
+    sharing it (`detach`), the padones input of a matmul whose weight
+    gradient [T, 1]^T G stays pending.  The SGD step that updates T must run
+    that gradient from T's values before the update: the stepped weights
+    equal w - lr * [T, 1]^T G within the GEMM bar of float64, and bit for bit
+    the weights of reading every gradient before the step."""
+    from tinytorch_amd.torch_py import Node
+    r = np.random.default_rng(61)
+    M, K, N = 256, 784, 512
+    t = r.uniform(0, 1, (M, K)).astype(np.float32)
+    w = (r.standard_normal((K + 1, N)) * 0.05).astype(np.float32)
+    v = (r.standard_normal((K, N)) * 0.05).astype(np.float32)
+    g = r.standard_normal((M, N)).astype(np.float32)
+    lr = 0.5
+
+    def run(read):
+        T = Node.leaf(t)
+        X = T.detach(False)
+        Wn, Vn = Node.leaf(w), Node.leaf(v, False)
+        P = X.padones()
+        A, B = P.matmul(Wn), T.matmul(Vn)
+        Y = A + B
+        Y.backward(g)
+        if read:
+            Wn.grad(), T.grad()
+        arr = (ctypes.c_void_p * 2)(Wn.ptr, T.ptr)
+        assert tlib.ag_sgd_step_many(arr, 2, ctypes.c_float(lr)) == 0
+        out = [Wn.value(), T.value()]
+        for nd in (Y, A, B, P, X, Wn, Vn, T):
+            nd.release()
+        return out
+
+    print("sgd step of a tensor a pending gradient reads, read_first", read_first, flush=True)
+    got = run(read_first)
+    if not read_first:
+        for a, e in zip(got, run(True)):
+            assert bits_equal(a, e)
+    tp = orc.padones_fwd(t).astype(np.float64)
+    dw = tp.T @ g.astype(np.float64)
+    dt = g.astype(np.float64) @ v.astype(np.float64).T
+    bar_w = lr * 1e-4 * np.sqrt(M) * np.abs(g).max() + np.spacing(np.abs(w).max())
+    bar_t = lr * 1e-4 * np.sqrt(N) * np.abs(g).max() * np.abs(v).max() + np.spacing(1.0)
+    assert np.abs(got[0] - (w - lr * dw)).max() <= bar_w
+    assert np.abs(got[1] - (t - lr * dt)).max() <= bar_t

@@ -1,0 +1,88 @@
+"""The exact steps `bench.py` times, at config size, with a non-zero learning
+rate: `CnnStep` (config 4) and `MlpStep` (config 2) build the graph through
+the C ABI, run the fused softmax-CE, the backward pass and
+`ag_sgd_step_many` -- the launch that also runs the pending weight-gradient
+reductions (`conv_dwt_reduce_sgd_kernel` for the CNN's convolutions,
+`gemm_tn_padones_sgd_kernel` for the MLP's first layer).  After each step
+every weight must equal w - lr*g_oracle, g_oracle being the gradient the
+oracle (bit-identical to the reference CPU path,
+`/root/reference/src/autograd.c:456` conv backward, the harness step of
+`/root/reference/tests/gate_mnist_mlp.py:119-124`) computes at the same
+weights, and the loss the oracle's loss.
+
+Bar: the gradient recovered from the step is within 1e-4 of max|g_oracle|
+(the hot path's relative bar), plus one float32 spacing of the weight for
+the rounding of the subtraction itself.  Two steps are run so that the
+second starts from weights the first one wrote on the device."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import orc
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+LR = 0.01
+
+
+def tensor_np(L, t, shape):
+    n = int(L.tt_numel(t))
+    p = L.tt_data(t)
+    assert p, "tt_data returned NULL"
+    return np.ctypeslib.as_array(p, shape=(n,)).reshape(shape).copy()
+
+
+def check_step(name, w_before, w_after, g_ref):
+    ref = w_before - np.float32(LR) * g_ref
+    err = float(np.abs(w_after.astype(np.float64) - ref).max())
+    bar = LR * TOL * float(np.abs(g_ref).max()) + float(np.spacing(np.abs(w_before).max()))
+    print(f"{name}: max|w - (w0 - lr g_oracle)| = {err:.3e}  bar {bar:.3e}", flush=True)
+    assert err <= bar, name
+    # the weights moved (a step that did nothing fails here unless g == 0)
+    assert np.abs(w_after - w_before).max() > 0, name
+
+
+def loss_probe(out):
+    def probe(L, loss):
+        v = L.ag_value(loss)
+        out["loss"] = float(tensor_np(L, v, (1,))[0])
+    return probe
+
+
+def test_bench_cnn_step_sgd_config4(tlib):
+    import bench
+    L = tlib
+    st = bench.CnnStep(L)
+    keys = ("w1", "b1", "w2", "b2", "wfc")
+    shapes = {}
+    x, y, P = bench.cnn_inputs(B=st.B)
+    for k in keys:
+        shapes[k] = P[k].shape
+    assert np.array_equal(tensor_np(L, st.t["x"], x.shape), x)
+    for it in range(2):
+        w0 = {k: tensor_np(L, st.t[k], shapes[k]) for k in keys}
+        ref = orc.cnn_step(x, y, **w0)
+        got = {}
+        print("bench CnnStep lr", LR, "step", it, flush=True)
+        st.step(lr=LR, probe=loss_probe(got))
+        assert abs(got["loss"] - ref["loss"]) <= TOL * max(1.0, abs(ref["loss"])), (got, ref["loss"])
+        for k, gk in zip(keys, ("dw1", "db1", "dw2", "db2", "dwfc")):
+            check_step(f"cnn step {it} {k}", w0[k], tensor_np(L, st.t[k], shapes[k]), ref[gk])
+
+
+def test_bench_mlp_step_sgd_config2(tlib):
+    import bench
+    L = tlib
+    st = bench.MlpStep(L)
+    x, y, Ws = bench.mlp_inputs(B=st.B)
+    assert np.array_equal(tensor_np(L, st.t[0], x.shape), x)
+    for it in range(2):
+        w0 = [tensor_np(L, t, w.shape) for t, w in zip(st.t[1:], Ws)]
+        ref = orc.mlp_step(x, y, *w0)
+        got = {}
+        print("bench MlpStep lr", LR, "step", it, flush=True)
+        st.step(lr=LR, probe=loss_probe(got))
+        assert abs(got["loss"] - ref["loss"]) <= TOL * max(1.0, abs(ref["loss"])), (got, ref["loss"])
+        for i, k in enumerate(("dW1", "dW2", "dW3")):
+            check_step(f"mlp step {it} {k}", w0[i], tensor_np(L, st.t[i + 1], Ws[i].shape), ref[k])

@@ -1280,6 +1280,10 @@ int ag_sgd_step_many(AGNode *const *leaves, int count, float lr) {
         Tensor *gt[TT_SGD_MAX];
         long n[TT_SGD_MAX];
         int k = 0;
+        /* pending recipes that read a value about to change (a padded copy
+         * or a weight gradient of this very tensor) run first */
+        for (int i = base; i < count && i < base + TT_SGD_MAX; i++)
+            if (leaves[i] && leaves[i]->grad) tt_lazy_before_write(leaves[i]->val);
         for (int i = base; i < count && i < base + TT_SGD_MAX; i++) {
             AGNode *l = leaves[i];
             if (!l || !l->grad) continue;
@@ -1307,6 +1311,7 @@ int ag_sgd_step_many(AGNode *const *leaves, int count, float lr) {
 
 int ag_sgd_step(AGNode *leaf, float lr) {
     if (!leaf || !leaf->grad) return 0;
+    tt_lazy_before_write(leaf->val);
     float *w = tt_dev(leaf->val);
     const float *g = tt_dev(leaf->grad);
     if (!w || !g) return -1;
@@ -1432,6 +1437,8 @@ int ag_optim_step(AGOptim *o, AGNode *const *params, int count) {
         const float *g[TT_SGD_MAX];
         long n[TT_SGD_MAX];
         int k = 0;
+        for (int i = base; i < count && i < base + TT_SGD_MAX; i++)
+            if (params[i]->grad) tt_lazy_before_write(params[i]->val);
         for (int i = base; i < count && i < base + TT_SGD_MAX; i++) {
             AGNode *l = params[i];
             if (!l->grad) continue;   /* no gradient reached it: state untouched */
