@@ -373,6 +373,23 @@ int tt_k_conv2d_relu_pool_fwd_lds(const float *x, const float *w, const float *b
                                   float *rout, float *pout, float *cout, float *dout,
                                   unsigned char *codes, int N, int C, int H, int W, int F, int HH,
                                   int WW, int sh, int sw, int ph, int pw, int Ho, int Wo);
+/* Two tt_k_conv2d_relu_pool_fwd_lds in one launch, for the CNN feature
+ * extractor's shape (reference src/ops_spatial.c:71-164 twice, each followed
+ * by the relu of src/ops.c:104-106): x (N x C1 x 32 x 32, C1 <= 4) -> 3x3 pad
+ * 1 conv with w1 (32 x C1 x 3 x 3) + b1 -> relu -> 2x2 pool = pool1 (N x 32
+ * x 16 x 16, codes1) -> 3x3 pad 1 conv with w2 (64 x 32 x 3 x 3) + b2 -> relu
+ * -> 2x2 pool = pool2 (N x 64 x 8 x 8, codes2).  The convolutions' outputs
+ * are not written; wsnap (optional; 32*C1*9 + 32 + 18432 + 64 floats) gets
+ * w1, b1, w2, b2 as read (zeros for a NULL bias), from which
+ * tt_k_conv2d_fwd_lds recomputes them.  copy2 (pool2 again) and pad2 (N x
+ * 4097, pool2 flattened then 1) are optional; b1 / b2 may be NULL.  Bit for
+ * bit the two separate launches.  -1: shape or alignment not covered (H, W,
+ * F1, F2 must be 32, 32, 32, 64; x, w2, pool1, pool2, copy2, codes1, codes2
+ * 16-byte aligned), nothing launched. */
+int tt_k_conv2d_chain_fwd(const float *x, const float *w1, const float *b1, const float *w2,
+                          const float *b2, float *pool1, unsigned char *codes1, float *pool2,
+                          float *copy2, float *pad2, unsigned char *codes2, float *wsnap, int N,
+                          int C1, int H, int W, int F1, int F2);
 int tt_k_conv2d_dw_lds(const float *g, const float *x, float *dw, float *db,
                        int N, int C, int H, int W, int F, int HH, int WW,
                        int sh, int sw, int ph, int pw, int Ho, int Wo);

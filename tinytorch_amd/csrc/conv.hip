@@ -1935,6 +1935,342 @@ int launch_dwt_plan(const float *gr, const float *x, float *dw, float *db, const
   return -1;
 }
 
+// ---- two convolutions in one launch ----
+//
+// conv(3x3, pad 1) -> relu -> 2x2 max pool -> conv(3x3, pad 1) -> relu -> 2x2
+// max pool for 32x32 images of C1 <= 4 channels, 32 then 64 filters (the
+// CNN's feature extractor), one workgroup of eight waves per image half: the
+// first convolution's pooled output never leaves the CU between the two.
+//
+//   staging (one wait): the image rows the half needs (20 rows: the 16 rows
+//     of the second convolution's 8 output rows, its one-row halo, and the
+//     first convolution's own halo) as a gapped slab, both filter banks, both
+//     biases, all with direct global->LDS loads.  The first filter bank is
+//     written k-major ([k][f]) by choosing each lane's source; the second
+//     (74 KB) is still in flight while the first convolution runs.
+//   MFMA operands swapped against conv_fwd_k_kernel: A = the image (32
+//     pixels), B = the filters, so lane l (filter l % 32) gets 16 pixels in
+//     its accumulators -- 4 consecutive rows 8(r/4) + 4h + r%4, chosen to be
+//     the top-left, top-right, bottom-left and bottom-right pixels of one
+//     pool window.  Bias, relu, pool and the window's code then need no lane
+//     exchange, and every lane does one pool per window instead of one per
+//     pixel.  Each output is the same k sequence of the same products as in
+//     conv_fwd_k_kernel (lane half h takes channels [h*CH2, (h+1)*CH2), taps
+//     in order), so the values are bit for bit those of that kernel.
+//   phase A: the first convolution's 18 output rows (9 pooled rows: 8 owned
+//     plus one halo row), a row pair (two blocks of 8 windows) a wave, wave 0
+//     also the ninth; the pooled rows go to an LDS slab laid out for the
+//     second convolution, the owned rows' codes to an LDS tile.
+//   phase B: the second convolution on that slab: wave w takes a 4x8 pixel
+//     patch (w % 4, 8 windows) and 32 filters (w / 4).
+//   LDS banks: a half-wave's 32 operand reads hit 32 different banks (slab
+//     rows 48 floats apart for phase A's 2x16 pixels, 24 apart for phase B's
+//     4x8: two or four disjoint runs mod 32); the pooled values are written
+//     with an odd (or 9-dword) stride per filter.
+//   The pooled outputs and codes of both convolutions are gathered in LDS and
+//     written as whole 16-byte runs: pool1 (N x 32 x 16 x 16) and its codes
+//     before phase B (they drain under its MFMAs), pool2 (N x 64 x 8 x 8),
+//     its flattened copy, its padded copy (rows of 4097, last one 1) and its
+//     codes at the end.  The convolutions' own outputs are not written; wsnap
+//     (optional) gets the filters and biases as they were read ([w1 | b1 | w2
+//     | b2]), from which a later launch can recompute them.
+namespace chain {
+constexpr int NTH = 512;
+constexpr int W1 = 32, F1 = 32;                   // first convolution: 32x32 -> 32 filters
+constexpr int W2 = 16, F2 = 64;                   // second: 16x16 (pool1) -> 64 filters
+constexpr int G1 = 16, RS1 = W1 + G1, R1 = 20, CS1 = R1 * RS1 + 4;  // image slab
+constexpr int G2 = 8, RS2 = W2 + G2, R2 = 10, CS2 = R2 * RS2 + 5;   // pool1 slab (odd stride)
+constexpr int KST2 = 292;                         // wrow_stride(F1 * 9)
+constexpr int PT = 33, CT = 36;                   // pool2 tile strides (floats, bytes)
+constexpr int C1T = 132;                          // pool1 codes tile stride (bytes)
+constexpr int O_WS2 = 0;                          // F2 x KST2
+constexpr int O_WS1 = O_WS2 + F2 * KST2;          // [k][f], 36 x 32
+constexpr int O_B = O_WS1 + 36 * 32;              // bias1 (32), bias2 (64)
+constexpr int O_X1 = O_B + 128;                   // image slab, 4 planes (then pool2 tiles)
+constexpr int X1_SZ = 4096;
+constexpr int O_X2 = O_X1 + X1_SZ;                // pool1 slab, F1 planes
+constexpr int O_C1 = O_X2 + F1 * CS2 + 4;         // pool1 codes tile, F1 x C1T bytes
+constexpr int LDS_FLOATS = O_C1 + F1 * C1T / 4;
+static_assert(4 * CS1 <= X1_SZ && F2 * PT + F2 * CT / 4 <= X1_SZ, "image slab area");
+static_assert(O_X1 % 64 == 0 && O_X2 % 4 == 0 && (F1 * CS2) % 4 == 0, "alignment");
+static_assert(LDS_FLOATS * 4 <= LDS_MAX, "LDS");
+}  // namespace chain
+
+template <int CH2>
+__global__ void __launch_bounds__(chain::NTH)
+conv_chain_fwd_kernel(const float *__restrict__ x, const float *__restrict__ w1,
+                      const float *__restrict__ b1, const float *__restrict__ w2,
+                      const float *__restrict__ b2, float *__restrict__ pool1,
+                      unsigned char *__restrict__ codes1, float *__restrict__ pool2,
+                      float *__restrict__ copy2, float *__restrict__ pad2,
+                      unsigned char *__restrict__ codes2, float *__restrict__ wsnap, int C1) {
+  using namespace chain;
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  float *ws2 = smem + O_WS2, *ws1 = smem + O_WS1, *bs = smem + O_B;
+  float *xs1 = smem + O_X1, *xs2 = smem + O_X2;
+  unsigned char *c1t = (unsigned char *)(smem + O_C1);
+  const int n = blockIdx.x >> 1, hf = blockIdx.x & 1;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, half = lane >> 5;
+  const int K1 = C1 * 9;
+  const int qlo = hf ? 7 : 0;           // first pooled row of phase A
+  const int iy0 = 2 * qlo - 1;          // image row of slab row 0
+
+  // ---- staging: image slab, filter bank 1 (k-major), biases, then bank 2 ----
+  {
+    const float *xn = x + (long)n * C1 * 1024;
+    constexpr int T1 = 2 * CH2 * CS1;
+    for (int base = wave * 256; base < T1; base += NTH * 4) {
+      const int i = base + lane * 4;
+      const int c = i / CS1, rem = i - c * CS1;
+      const int slot = rem / RS1, j = rem - slot * RS1;
+      const int row = iy0 + slot;
+      const bool ok = i < T1 && c < C1 && slot < R1 && j >= G1 && row >= 0 && row < 32;
+      dma_dwordx4(ok ? xn + (c * 32 + row) * 32 + (j - G1) : g_zero_src, xs1 + base);
+    }
+    for (int base = wave * 64; base < 2 * CH2 * 9 * 32; base += NTH) {
+      const int d = base + lane, k = d >> 5, f = d & 31;
+      dma_dword(k < K1 ? w1 + f * K1 + k : g_zero_src, ws1 + base);
+    }
+    if (wave < 2) {
+      const int d = wave * 64 + lane;
+      const float *p = d < 32 ? (b1 ? b1 + d : g_zero_src)
+                              : d < 96 ? (b2 ? b2 + d - 32 : g_zero_src) : g_zero_src;
+      dma_dword(p, bs + wave * 64);
+    }
+    stage_blocks<true, NTH>(ws2, w2, F2 * KST2, KST2, F2, F1 * 9, 0, F1 * 9);
+    // zeros under the pool1 slab (its gaps, pads and out-of-image rows)
+    const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = tid; i < F1 * CS2 / 4; i += NTH) reinterpret_cast<f32x4 *>(xs2)[i] = z;
+  }
+  // the filters and biases as read, for a later recomputation of the
+  // convolutions' outputs: a slice per workgroup
+  if (wsnap) {
+    const int T = 32 * K1 + 32 + F2 * F1 * 9 + F2;
+    const int per = (T + gridDim.x - 1) / gridDim.x;
+    for (int i = blockIdx.x * per + tid; i < min(T, (int)(blockIdx.x + 1) * per); i += NTH) {
+      int k = i;
+      float v;
+      if (k < 32 * K1) v = w1[k];
+      else if ((k -= 32 * K1) < 32) v = b1 ? b1[k] : 0.0f;
+      else if ((k -= 32) < F2 * F1 * 9) v = w2[k];
+      else v = b2 ? b2[k - F2 * F1 * 9] : 0.0f;
+      wsnap[i] = v;
+    }
+  }
+  // every wave issued at least 9 loads of bank 2 after the rest
+  asm volatile("s_waitcnt vmcnt(9)" ::: "memory");
+  __syncthreads();
+
+  // ---- phase A: first convolution, bias, relu, pool, codes ----
+  {
+    const float *wa = ws1 + half * CH2 * 9 * 32 + l32;
+    const float bias = bs[l32];
+    const int win = l32 >> 2, dy = (l32 >> 1) & 1, dx = l32 & 1;
+    bool first = true;
+    for (int i = wave; i < 9; i += 8) {
+      int bj[2];
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+        bj[j] = (2 * i + dy) * RS1 + 2 * (8 * j + win) + dx + G1 - 1 + half * CH2 * CS1;
+      f32x16 acc[2];
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+        for (int r = 0; r < 16; r++) acc[j][r] = 0.0f;
+      auto load = [&](int c, float (&a)[9], float (&b)[9][2]) {
+#pragma unroll
+        for (int t = 0; t < 9; t++) a[t] = wa[(c * 9 + t) * 32];
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+          for (int kh = 0; kh < 3; kh++)
+#pragma unroll
+            for (int kw = 0; kw < 3; kw++)
+              b[kh * 3 + kw][j] = xs1[bj[j] + c * CS1 + kh * RS1 + kw];
+      };
+      auto mfmas = [&](const float (&a)[9], const float (&b)[9][2]) {
+#pragma unroll
+        for (int t = 0; t < 9; t++)
+#pragma unroll
+          for (int j = 0; j < 2; j++)
+            acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[t][j], a[t], acc[j], 0, 0, 0);
+      };
+      float a0[9], bb0[9][2], a1[9], bb1[9][2];
+      load(0, a0, bb0);
+      int c = 0;
+      for (; c + 1 < CH2; c += 2) {
+        load(c + 1, a1, bb1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(a0, bb0);
+        __builtin_amdgcn_sched_barrier(0);
+        load(c + 2 < CH2 ? c + 2 : c + 1, a0, bb0);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(a1, bb1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (c < CH2) mfmas(a0, bb0);
+      if (first) dma_wait();  // bank 2 landed (before any store counts against vmcnt)
+      first = false;
+
+      const int q = qlo + i;                  // pooled row
+      const bool own = q >= 8 * hf && q < 8 * hf + 8;
+      const int srow = q - 8 * hf + 1;        // its row in the pool1 slab
+      float *dst = xs2 + l32 * CS2 + srow * RS2 + G2;
+      unsigned char *cdst = c1t + l32 * C1T + (q - 8 * hf) * 16;
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int qq = 0; qq < 4; qq++) {
+          float o[4];
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const float v = acc[j][4 * qq + e] + bias;
+            o[e] = v > 0.0f ? v : 0.0f;
+          }
+          unsigned code;
+          const float m = pool_code(o[0], o[1], o[2], o[3], code);
+          const int pc = 8 * j + 2 * qq + half;
+          dst[pc] = m;
+          if (own) cdst[pc] = (unsigned char)code;
+        }
+    }
+  }
+  __syncthreads();
+
+  // ---- pool1 and its codes (owned rows) from LDS, drained under phase B ----
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int idx = tid + k * NTH, f = idx >> 5, r8 = (idx >> 2) & 7, c4 = idx & 3;
+    const float *s = xs2 + f * CS2 + (r8 + 1) * RS2 + G2 + 4 * c4;
+    const f32x4 v = {s[0], s[1], s[2], s[3]};
+    *reinterpret_cast<f32x4 *>(pool1 + (((long)n * F1 + f) * 16 + 8 * hf + r8) * 16 + 4 * c4) = v;
+  }
+  if (tid < 256) {
+    const int f = tid >> 3, r8 = tid & 7;
+    const unsigned *s = reinterpret_cast<const unsigned *>(c1t + f * C1T + r8 * 16);
+    const uint4 v = {s[0], s[1], s[2], s[3]};
+    *reinterpret_cast<uint4 *>(codes1 + ((long)n * F1 + f) * 256 + 128 * hf + 16 * r8) = v;
+  }
+
+  // ---- phase B: second convolution on the pool1 slab ----
+  const int pb = wave & 3, fb = wave >> 2;
+  f32x16 acc;
+  for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+  {
+    const int win = l32 >> 2, dy = (l32 >> 1) & 1, dx = l32 & 1;
+    const int hol = 4 * (pb >> 1) + 2 * (win >> 2) + dy, wo = 8 * (pb & 1) + 2 * (win & 3) + dx;
+    const int bj = hol * RS2 + wo + G2 - 1 + half * 16 * CS2;
+    const float *wa = ws2 + (32 * fb + l32) * KST2 + half * 16 * 9;
+    auto loadw = [&](int q, f32x4 (&wv)[9]) {
+      const f32x4 *p = (const f32x4 *)(wa + q * 36);
+#pragma unroll
+      for (int i = 0; i < 9; i++) wv[i] = p[i];
+    };
+    auto loadb = [&](int c, float (&b)[9]) {
+#pragma unroll
+      for (int kh = 0; kh < 3; kh++)
+#pragma unroll
+        for (int kw = 0; kw < 3; kw++) b[kh * 3 + kw] = xs2[bj + c * CS2 + kh * RS2 + kw];
+    };
+    auto mfq = [&](const f32x4 (&wv)[9], const int cc, const float (&b)[9]) {
+#pragma unroll
+      for (int t = 0; t < 9; t++) {
+        const int e = cc * 9 + t;
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(b[t], wv[e >> 2][e & 3], acc, 0, 0, 0);
+      }
+    };
+    f32x4 wq0[9], wq1[9];
+    float bb0[9], bb1[9];
+    loadw(0, wq0);
+    loadb(0, bb0);
+    for (int q = 0; q < 4; q += 2) {
+      const int c = 4 * q;
+      loadw(q + 1, wq1);
+      loadb(c + 1, bb1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfq(wq0, 0, bb0);
+      __builtin_amdgcn_sched_barrier(0);
+      loadb(c + 2, bb0);
+      __builtin_amdgcn_sched_barrier(0);
+      mfq(wq0, 1, bb1);
+      __builtin_amdgcn_sched_barrier(0);
+      loadb(c + 3, bb1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfq(wq0, 2, bb0);
+      __builtin_amdgcn_sched_barrier(0);
+      loadb(c + 4, bb0);
+      __builtin_amdgcn_sched_barrier(0);
+      mfq(wq0, 3, bb1);
+      __builtin_amdgcn_sched_barrier(0);
+      loadw(q + 2 < 4 ? q + 2 : q + 1, wq0);
+      loadb(c + 5, bb1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfq(wq1, 0, bb0);
+      __builtin_amdgcn_sched_barrier(0);
+      loadb(c + 6, bb0);
+      __builtin_amdgcn_sched_barrier(0);
+      mfq(wq1, 1, bb1);
+      __builtin_amdgcn_sched_barrier(0);
+      loadb(c + 7, bb1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfq(wq1, 2, bb0);
+      __builtin_amdgcn_sched_barrier(0);
+      loadb(c + 8 < 16 ? c + 8 : 15, bb0);
+      __builtin_amdgcn_sched_barrier(0);
+      mfq(wq1, 3, bb1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  __syncthreads();  // every wave is past phase A's slab: the pool2 tiles reuse it
+
+  // ---- bias, relu, pool, codes of the second convolution ----
+  float *pt = xs1;                                      // F2 x PT pooled values
+  unsigned char *ct = (unsigned char *)(xs1 + F2 * PT);  // F2 x CT codes
+  {
+    const int f = 32 * fb + l32;
+    const float bias = bs[32 + f];
+#pragma unroll
+    for (int qq = 0; qq < 4; qq++) {
+      float o[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float v = acc[4 * qq + e] + bias;
+        o[e] = v > 0.0f ? v : 0.0f;
+      }
+      unsigned code;
+      const float m = pool_code(o[0], o[1], o[2], o[3], code);
+      const int wi = 2 * qq + half;
+      const int po = (2 * (pb >> 1) + (wi >> 2)) * 8 + 4 * (pb & 1) + (wi & 3);
+      pt[f * PT + po] = m;
+      ct[f * CT + po] = (unsigned char)code;
+    }
+  }
+  __syncthreads();
+  {
+    const int f = tid >> 3, k = tid & 7;
+    const float *s = pt + f * PT + 4 * k;
+    const f32x4 v = {s[0], s[1], s[2], s[3]};
+    const long o = ((long)n * F2 + f) * 64 + 32 * hf + 4 * k;
+    *reinterpret_cast<f32x4 *>(pool2 + o) = v;
+    if (copy2) *reinterpret_cast<f32x4 *>(copy2 + o) = v;
+    if (pad2) {
+      float *d = pad2 + (long)n * (F2 * 64 + 1) + f * 64 + 32 * hf + 4 * k;
+      d[0] = v[0];
+      d[1] = v[1];
+      d[2] = v[2];
+      d[3] = v[3];
+      if (hf == 0 && tid == 0) pad2[(long)n * (F2 * 64 + 1) + F2 * 64] = 1.0f;
+    }
+    if (tid < 128) {
+      const unsigned *cs = reinterpret_cast<const unsigned *>(ct + (tid >> 1) * CT + 16 * (tid & 1));
+      const uint4 cv = {cs[0], cs[1], cs[2], cs[3]};
+      *reinterpret_cast<uint4 *>(codes2 + ((long)n * F2 + (tid >> 1)) * 64 + 32 * hf +
+                                 16 * (tid & 1)) = cv;
+    }
+  }
+}
+
 int g_lds_conv = 1;  // tth_conv_lds
 
 }  // namespace
@@ -2220,4 +2556,34 @@ extern "C" void ttk_dwt_job_drop(TTDwtJob *job) {
   if (!job) return;
   ttrt_free(job->part);
   job->part = nullptr;
+}
+
+// The CNN feature extractor's two convolutions in one launch (see
+// conv_chain_fwd_kernel): x (N x C1 x 32 x 32, C1 <= 4), w1 (32 x C1 x 3 x 3),
+// w2 (64 x 32 x 3 x 3), biases optional; pad 1, stride 1, relu, 2x2 / stride-2
+// max pools.  Writes pool1 (N x 32 x 16 x 16) and codes1, pool2 (N x 64 x 8 x
+// 8) and codes2 (one byte per pool window, as tt_k_conv2d_relu_pool_fwd_lds),
+// and, when given, copy2 (pool2 again), pad2 (N x 4097: pool2 flattened, then
+// 1) and wsnap (32*C1*9 + 32 + 18432 + 64 floats: w1, b1, w2, b2 as read,
+// zeros for a NULL bias).  Every value bit for bit that of two
+// tt_k_conv2d_relu_pool_fwd_lds launches.  -1: shape or alignment not covered
+// (nothing launched).
+extern "C" int tt_k_conv2d_chain_fwd(const float *x, const float *w1, const float *b1,
+                                     const float *w2, const float *b2, float *pool1,
+                                     unsigned char *codes1, float *pool2, float *copy2,
+                                     float *pad2, unsigned char *codes2, float *wsnap, int N,
+                                     int C1, int H, int W, int F1, int F2) {
+  if (!x || !w1 || !w2 || !pool1 || !codes1 || !pool2 || !codes2 || N <= 0 || N > 65535 ||
+      C1 < 1 || C1 > 4 || H != 32 || W != 32 || F1 != chain::F1 || F2 != chain::F2)
+    return -1;
+  if (!aligned16(x) || !aligned16(w2) || !aligned16(pool1) || !aligned16(pool2) ||
+      ((uintptr_t)codes1 & 15) || ((uintptr_t)codes2 & 15) || (copy2 && !aligned16(copy2)))
+    return -1;
+  if (fail_direct()) return -3;
+  auto kern = C1 > 2 ? conv_chain_fwd_kernel<2> : conv_chain_fwd_kernel<1>;
+  constexpr size_t lds = sizeof(float) * chain::LDS_FLOATS;
+  if (!allow_big_lds((const void *)kern)) return -1;
+  hipLaunchKernelGGL(kern, dim3((unsigned)(2 * N)), dim3(chain::NTH), lds, stream(), x, w1, b1, w2,
+                     b2, pool1, codes1, pool2, copy2, pad2, codes2, wsnap, C1);
+  return hipGetLastError() == hipSuccess ? 0 : -3;
 }
