@@ -342,6 +342,12 @@ int tth_conv_dwt(int on);
  * reshape and relu launches at once.
  * <0 queries; the previous setting is returned. */
 int tth_conv_relu_fuse(int on);
+/* Tuning hook: 0 disables, 1 (default) enables running a conv -> relu ->
+ * 2x2 pool -> conv -> relu -> 2x2 pool chain of ag_* calls (the
+ * tt_k_conv2d_chain_fwd shape) as one launch; the convolutions' outputs are
+ * then recomputed from a snapshot of their filters on first read.  Returns
+ * the previous setting; -1 only queries. */
+int tth_conv_chain(int on);
 int tt_k_conv2d_lds_plan(int N, int C, int H, int W, int F, int HH, int WW,
                          int sh, int sw, int ph, int pw, int Ho, int Wo);
 int tt_k_conv2d_fwd_lds(const float *x, const float *w, const float *bias, float *out,
@@ -379,17 +385,17 @@ int tt_k_conv2d_relu_pool_fwd_lds(const float *x, const float *w, const float *b
  * 1 conv with w1 (32 x C1 x 3 x 3) + b1 -> relu -> 2x2 pool = pool1 (N x 32
  * x 16 x 16, codes1) -> 3x3 pad 1 conv with w2 (64 x 32 x 3 x 3) + b2 -> relu
  * -> 2x2 pool = pool2 (N x 64 x 8 x 8, codes2).  The convolutions' outputs
- * are not written; wsnap (optional; 32*C1*9 + 32 + 18432 + 64 floats) gets
- * w1, b1, w2, b2 as read (zeros for a NULL bias), from which
- * tt_k_conv2d_fwd_lds recomputes them.  copy2 (pool2 again) and pad2 (N x
+ * are not written; snap1 / snap2 (optional, both or neither; 32*C1*9 + 32
+ * and 18432 + 64 floats) get w1 | b1 and w2 | b2 as read (zeros for a NULL
+ * bias), from which tt_k_conv2d_fwd_lds recomputes them.  copy2 (pool2 again) and pad2 (N x
  * 4097, pool2 flattened then 1) are optional; b1 / b2 may be NULL.  Bit for
  * bit the two separate launches.  -1: shape or alignment not covered (H, W,
  * F1, F2 must be 32, 32, 32, 64; x, w2, pool1, pool2, copy2, codes1, codes2
  * 16-byte aligned), nothing launched. */
 int tt_k_conv2d_chain_fwd(const float *x, const float *w1, const float *b1, const float *w2,
                           const float *b2, float *pool1, unsigned char *codes1, float *pool2,
-                          float *copy2, float *pad2, unsigned char *codes2, float *wsnap, int N,
-                          int C1, int H, int W, int F1, int F2);
+                          float *copy2, float *pad2, unsigned char *codes2, float *snap1,
+                          float *snap2, int N, int C1, int H, int W, int F1, int F2);
 int tt_k_conv2d_dw_lds(const float *g, const float *x, float *dw, float *db,
                        int N, int C, int H, int W, int F, int HH, int WW,
                        int sh, int sw, int ph, int pw, int Ho, int Wo);

@@ -71,9 +71,9 @@ def test_conv_chain_matches_two_launches(tlib, N, C1, bias, nan):
     s1, j1 = DevBuf(p1n), DevBuf(p1n, np.uint8)
     s2, e2, f2, j2 = DevBuf(p2n), DevBuf(p2n), DevBuf(N * 4097), DevBuf(p2n, np.uint8)
     K1 = C1 * 9
-    snap = DevBuf(32 * K1 + 32 + 18432 + 64)
+    sa, sb = DevBuf(32 * K1 + 32), DevBuf(18432 + 64)
     check(tlib.tt_k_conv2d_chain_fwd(dx.ptr, dw1.ptr, bp1, dw2.ptr, bp2, s1.ptr, j1.ptr, s2.ptr,
-                                     e2.ptr, f2.ptr, j2.ptr, snap.ptr, N, C1, 32, 32, 32, 64),
+                                     e2.ptr, f2.ptr, j2.ptr, sa.ptr, sb.ptr, N, C1, 32, 32, 32, 64),
           "chain")
     assert bits_equal(p1.to_np((N, 32, 16, 16)), s1.to_np((N, 32, 16, 16)))
     assert bits_equal(p2.to_np((N, 64, 8, 8)), s2.to_np((N, 64, 8, 8)))
@@ -81,14 +81,22 @@ def test_conv_chain_matches_two_launches(tlib, N, C1, bias, nan):
     assert bits_equal(f2.to_np((N, 4097)), orc.padones_fwd(flat))
     assert bits_equal(j1.to_np((N, 32, 16, 16)), k1)
     assert bits_equal(j2.to_np((N, 64, 8, 8)), k2)
-    sn = snap.to_np((snap.n,))
     zb1 = b1 if bias else np.zeros(32, np.float32)
     zb2 = b2 if bias else np.zeros(64, np.float32)
-    assert bits_equal(sn, np.concatenate([w1.ravel(), zb1, w2.ravel(), zb2]))
+    assert bits_equal(sa.to_np((sa.n,)), np.concatenate([w1.ravel(), zb1]))
+    assert bits_equal(sb.to_np((sb.n,)), np.concatenate([w2.ravel(), zb2]))
+    # the convolution outputs recomputed from the snapshots: the same bits
+    y1, y2 = DevBuf(n1), DevBuf(n2)
+    check(tlib.tt_k_conv2d_fwd_lds(dx.ptr, sa.ptr, sa.ptr + 4 * 32 * K1, y1.ptr, *geo(N, C1, 32, 32)),
+          "recompute 1")
+    check(tlib.tt_k_conv2d_fwd_lds(s1.ptr, sb.ptr, sb.ptr + 4 * 18432, y2.ptr, *geo(N, 32, 16, 64)),
+          "recompute 2")
+    assert bits_equal(y1.to_np((N, 32, 32, 32)), o1.to_np((N, 32, 32, 32)))
+    assert bits_equal(y2.to_np((N, 64, 16, 16)), o2.to_np((N, 64, 16, 16)))
     # optional outputs left out: the rest unchanged
     s1b, j1b, s2b, j2b = DevBuf(p1n), DevBuf(p1n, np.uint8), DevBuf(p2n), DevBuf(p2n, np.uint8)
     check(tlib.tt_k_conv2d_chain_fwd(dx.ptr, dw1.ptr, bp1, dw2.ptr, bp2, s1b.ptr, j1b.ptr, s2b.ptr,
-                                     None, None, j2b.ptr, None, N, C1, 32, 32, 32, 64),
+                                     None, None, j2b.ptr, None, None, N, C1, 32, 32, 32, 64),
           "chain, pools only")
     assert bits_equal(s1b.to_np((N, 32, 16, 16)), s1.to_np((N, 32, 16, 16)))
     assert bits_equal(s2b.to_np((N, 64, 8, 8)), s2.to_np((N, 64, 8, 8)))
@@ -114,6 +122,100 @@ def test_conv_chain_matches_two_launches(tlib, N, C1, bias, nan):
 def test_conv_chain_rejects(tlib):
     d = DevBuf(64)
     assert tlib.tt_k_conv2d_chain_fwd(d.ptr, d.ptr, None, d.ptr, None, d.ptr, d.ptr, d.ptr, None,
-                                      None, d.ptr, None, 2, 5, 32, 32, 32, 64) == -1
+                                      None, d.ptr, None, None, 2, 5, 32, 32, 32, 64) == -1
     assert tlib.tt_k_conv2d_chain_fwd(d.ptr, d.ptr, None, d.ptr, None, d.ptr, d.ptr, d.ptr, None,
-                                      None, d.ptr, None, 2, 3, 16, 16, 32, 64) == -1
+                                      None, d.ptr, None, None, 2, 3, 16, 16, 32, 64) == -1
+
+
+def _cnn(Node, x, P, keep):
+    X = Node.leaf(x, False)
+    w1, b1, w2, b2, wfc = (Node.leaf(P[k]) for k in ("w1", "b1", "w2", "b2", "wfc"))
+    c1 = X.conv2d(w1, b1, stride=1, pad=1)
+    r1 = c1.relu()
+    p1 = r1.maxpool2d(2, 2)
+    c2 = p1.conv2d(w2, b2, stride=1, pad=1)
+    r2 = c2.relu()
+    p2 = r2.maxpool2d(2, 2)
+    f = p2.reshape((x.shape[0], P["wfc"].shape[0] - 1))
+    d = f.padones()
+    logits = d.matmul(wfc)
+    keep.extend([X, w1, b1, w2, b2, wfc, c1, r1, p1, c2, r2, p2, f, d, logits])
+    return logits
+
+
+@pytest.mark.parametrize("read_early", [False, True])
+def test_autograd_chain_on_off_bitexact(tlib, read_early):
+    """The config-4 graph through ag_*: with the two-convolution chain
+    (one launch, convolution outputs recomputed from the filter snapshot on
+    first read) every value and gradient is bit for bit the graph without it,
+    also when the convolution and relu outputs are read after an SGD step has
+    changed the filters in place (the recipes read the snapshot), and when
+    read before the backward pass."""
+    from tinytorch_amd.torch_py import Node
+    x, y, P = orc.cnn_inputs(B=16)
+    names = ("X", "w1", "b1", "w2", "b2", "wfc", "c1", "r1", "p1", "c2", "r2", "p2", "f", "d",
+             "logits")
+
+    def run(chain):
+        prev = tlib.tth_conv_chain(1 if chain else 0)
+        keep = []
+        try:
+            logits = _cnn(Node, x, P, keep)
+            loss = logits.softmax_ce(y)
+            vals = {}
+            if read_early:
+                for k in ("c1", "r1", "c2", "r2"):
+                    vals[k + "_early"] = keep[names.index(k)].value()
+            loss.backward(None)
+            grads = {k: keep[names.index(k)].grad() for k in ("w1", "b1", "w2", "b2", "wfc")}
+            for k in ("w1", "b1", "w2", "b2", "wfc"):
+                keep[names.index(k)].sgd_step(0.5)
+            for k, nd in zip(names, keep):
+                vals[k] = nd.value()
+            vals["loss"] = loss.value()
+            for nd in [loss] + keep[::-1]:
+                nd.release()
+            return vals, grads
+        finally:
+            tlib.tth_conv_chain(prev)
+
+    print("autograd chain on/off, read_early", read_early, flush=True)
+    (v1, g1), (v0, g0) = run(True), run(False)
+    for k in v0:
+        assert bits_equal(v1[k], v0[k]), k
+    for k in g0:
+        assert bits_equal(g1[k], g0[k]), k
+    # the recomputed convolution is the one of the filters before the step
+    ref = orc.conv2d_fwd(x, P["w1"], P["b1"], 1, 1, 1, 1)
+    assert np.abs(v1["c1"] - ref).max() <= 1e-4 * max(1.0, np.abs(ref).max())
+
+
+def test_autograd_chain_second_conv_not_pooled(tlib):
+    """conv -> relu -> pool -> conv -> relu with no second pool: the first
+    convolution is launched by itself when the chain cannot complete, the
+    values bit for bit those without the chain."""
+    from tinytorch_amd.torch_py import Node
+    x, y, P = orc.cnn_inputs(B=4)
+
+    def run(chain):
+        prev = tlib.tth_conv_chain(1 if chain else 0)
+        try:
+            X = Node.leaf(x, False)
+            w1, b1, w2, b2 = (Node.leaf(P[k]) for k in ("w1", "b1", "w2", "b2"))
+            c1 = X.conv2d(w1, b1, stride=1, pad=1)
+            r1 = c1.relu()
+            p1 = r1.maxpool2d(2, 2)
+            c2 = p1.conv2d(w2, b2, stride=1, pad=1)
+            r2 = c2.relu()
+            out = [r2.value(), p1.value(), c1.value()]
+            g = np.ones_like(out[0])
+            r2.backward(g)
+            out += [w1.grad(), w2.grad()]
+            for nd in (r2, c2, p1, r1, c1, X, w1, b1, w2, b2):
+                nd.release()
+            return out
+        finally:
+            tlib.tth_conv_chain(prev)
+
+    for a, b in zip(run(True), run(False)):
+        assert bits_equal(a, b)

@@ -169,13 +169,14 @@ SIGNATURES = [
     ("tt_k_conv2d_dx_implicit", _I, [VP, VP, VP] + [_I] * 13),
     ("tth_conv_lds", _I, [_I]),
     ("tth_conv_relu_fuse", _I, [_I]),
+    ("tth_conv_chain", _I, [_I]),
     ("tth_conv_dwt", _I, [_I]),
     ("tt_k_conv2d_lds_plan", _I, [_I] * 13),
     ("tt_k_conv2d_fwd_lds", _I, [VP, VP, VP, VP] + [_I] * 13),
     ("tt_k_conv2d_relu_fwd_lds", _I, [VP, VP, VP, VP, VP] + [_I] * 13),
     ("tt_k_conv2d_relu_pool_fwd_lds", _I, [VP] * 9 + [_I] * 13),
     ("tt_k_conv2d_dw_lds", _I, [VP, VP, VP, VP] + [_I] * 13),
-    ("tt_k_conv2d_chain_fwd", _I, [VP] * 12 + [_I] * 6),
+    ("tt_k_conv2d_chain_fwd", _I, [VP] * 13 + [_I] * 6),
     ("tt_k_conv2d_dw_lds_pooled", _I, [VP] * 5 + [_I] * 13),
     ("tt_k_conv2d_dx_lds", _I, [VP, VP, VP] + [_I] * 13),
     ("tt_k_gather_u8_norm", _I, [VP, _L, _L, _L, _I, VP, _L, F32P, F32P, VP]),

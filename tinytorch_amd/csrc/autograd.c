@@ -361,6 +361,14 @@ AGNode *ag_padones(AGNode *a) {
     if (!a || a->val->ndim != 2) return NULL;
     const long M = a->val->shape[0], K = a->val->shape[1];
     const long shp[2] = {M, K + 1};
+    if (tt_pend1.active && tt_pend.active == TT_PEND_CONV_RELU_POOL_COPY && tt_pend.c == a->val) {
+        /* both convolutions of a conv -> relu -> pool chain, the second's
+         * flattening copy and this padones in one launch */
+        Tensor *v = tt_empty_dev(shp, 2);
+        if (v && tt_chain_launch(v) == 0) return make_node(v, &OP_PADONES, a, NULL, NULL);
+        tt_release(v);
+        tt_flush_first();  /* the first by itself; the second and this padones below */
+    }
     if (tt_pend.active == TT_PEND_CONV_RELU_POOL_COPY && tt_pend.c == a->val) {
         /* convolution, relu, pool, flattening copy and this padones in one
          * launch */
@@ -1480,8 +1488,10 @@ void ag_release(AGNode *n) {
     while (dead) {
         AGNode *d = dead;
         dead = d->next;
-        if (tt_pend.active && (tt_pend.out == d->val || tt_pend.r == d->val ||
-                               tt_pend.p == d->val || tt_pend.c == d->val))
+        if ((tt_pend.active && (tt_pend.out == d->val || tt_pend.r == d->val ||
+                                tt_pend.p == d->val || tt_pend.c == d->val)) ||
+            (tt_pend1.active && (tt_pend1.out == d->val || tt_pend1.r == d->val ||
+                                 tt_pend1.p == d->val)))
             tt_flush_pending();  /* the launch writes into d's tensors */
         tt_release(d->val);
         tt_release(d->grad);

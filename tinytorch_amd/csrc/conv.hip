@@ -1971,9 +1971,9 @@ int launch_dwt_plan(const float *gr, const float *x, float *dw, float *db, const
 //     written as whole 16-byte runs: pool1 (N x 32 x 16 x 16) and its codes
 //     before phase B (they drain under its MFMAs), pool2 (N x 64 x 8 x 8),
 //     its flattened copy, its padded copy (rows of 4097, last one 1) and its
-//     codes at the end.  The convolutions' own outputs are not written; wsnap
-//     (optional) gets the filters and biases as they were read ([w1 | b1 | w2
-//     | b2]), from which a later launch can recompute them.
+//     codes at the end.  The convolutions' own outputs are not written; snap1
+//     / snap2 (optional) get the filters and biases as they were read (w1 |
+//     b1, w2 | b2), from which a later launch can recompute them.
 namespace chain {
 constexpr int NTH = 512;
 constexpr int W1 = 32, F1 = 32;                   // first convolution: 32x32 -> 32 filters
@@ -2003,7 +2003,8 @@ conv_chain_fwd_kernel(const float *__restrict__ x, const float *__restrict__ w1,
                       const float *__restrict__ b2, float *__restrict__ pool1,
                       unsigned char *__restrict__ codes1, float *__restrict__ pool2,
                       float *__restrict__ copy2, float *__restrict__ pad2,
-                      unsigned char *__restrict__ codes2, float *__restrict__ wsnap, int C1) {
+                      unsigned char *__restrict__ codes2, float *__restrict__ snap1,
+                      float *__restrict__ snap2, int C1) {
   using namespace chain;
   extern __shared__ __attribute__((aligned(16))) float smem[];
   float *ws2 = smem + O_WS2, *ws1 = smem + O_WS1, *bs = smem + O_B;
@@ -2045,18 +2046,17 @@ conv_chain_fwd_kernel(const float *__restrict__ x, const float *__restrict__ w1,
     for (int i = tid; i < F1 * CS2 / 4; i += NTH) reinterpret_cast<f32x4 *>(xs2)[i] = z;
   }
   // the filters and biases as read, for a later recomputation of the
-  // convolutions' outputs: a slice per workgroup
-  if (wsnap) {
-    const int T = 32 * K1 + 32 + F2 * F1 * 9 + F2;
+  // convolutions' outputs (snap1 = w1 | b1, snap2 = w2 | b2): a slice per
+  // workgroup
+  if (snap1) {
+    const int T1s = 32 * K1 + 32, T = T1s + F2 * F1 * 9 + F2;
     const int per = (T + gridDim.x - 1) / gridDim.x;
-    for (int i = blockIdx.x * per + tid; i < min(T, (int)(blockIdx.x + 1) * per); i += NTH) {
-      int k = i;
-      float v;
-      if (k < 32 * K1) v = w1[k];
-      else if ((k -= 32 * K1) < 32) v = b1 ? b1[k] : 0.0f;
-      else if ((k -= 32) < F2 * F1 * 9) v = w2[k];
-      else v = b2 ? b2[k - F2 * F1 * 9] : 0.0f;
-      wsnap[i] = v;
+    const int end = min(T, (int)(blockIdx.x + 1) * per);
+    for (int i = blockIdx.x * per + tid; i < end; i += NTH) {
+      if (i < 32 * K1) snap1[i] = w1[i];
+      else if (i < T1s) snap1[i] = b1 ? b1[i - 32 * K1] : 0.0f;
+      else if (i < T1s + F2 * F1 * 9) snap2[i - T1s] = w2[i - T1s];
+      else snap2[i - T1s] = b2 ? b2[i - T1s - F2 * F1 * 9] : 0.0f;
     }
   }
   // every wave issued at least 9 loads of bank 2 after the rest
@@ -2564,17 +2564,18 @@ extern "C" void ttk_dwt_job_drop(TTDwtJob *job) {
 // max pools.  Writes pool1 (N x 32 x 16 x 16) and codes1, pool2 (N x 64 x 8 x
 // 8) and codes2 (one byte per pool window, as tt_k_conv2d_relu_pool_fwd_lds),
 // and, when given, copy2 (pool2 again), pad2 (N x 4097: pool2 flattened, then
-// 1) and wsnap (32*C1*9 + 32 + 18432 + 64 floats: w1, b1, w2, b2 as read,
-// zeros for a NULL bias).  Every value bit for bit that of two
-// tt_k_conv2d_relu_pool_fwd_lds launches.  -1: shape or alignment not covered
-// (nothing launched).
+// 1) and snap1 / snap2 (both or neither: 32*C1*9 + 32 and 18432 + 64 floats,
+// w1 | b1 and w2 | b2 as read, zeros for a NULL bias).  Every value bit for
+// bit that of two tt_k_conv2d_relu_pool_fwd_lds launches.  -1: shape or
+// alignment not covered (nothing launched).
 extern "C" int tt_k_conv2d_chain_fwd(const float *x, const float *w1, const float *b1,
                                      const float *w2, const float *b2, float *pool1,
                                      unsigned char *codes1, float *pool2, float *copy2,
-                                     float *pad2, unsigned char *codes2, float *wsnap, int N,
-                                     int C1, int H, int W, int F1, int F2) {
+                                     float *pad2, unsigned char *codes2, float *snap1,
+                                     float *snap2, int N, int C1, int H, int W, int F1, int F2) {
   if (!x || !w1 || !w2 || !pool1 || !codes1 || !pool2 || !codes2 || N <= 0 || N > 65535 ||
-      C1 < 1 || C1 > 4 || H != 32 || W != 32 || F1 != chain::F1 || F2 != chain::F2)
+      C1 < 1 || C1 > 4 || H != 32 || W != 32 || F1 != chain::F1 || F2 != chain::F2 ||
+      !snap1 != !snap2)
     return -1;
   if (!aligned16(x) || !aligned16(w2) || !aligned16(pool1) || !aligned16(pool2) ||
       ((uintptr_t)codes1 & 15) || ((uintptr_t)codes2 & 15) || (copy2 && !aligned16(copy2)))
@@ -2584,6 +2585,6 @@ extern "C" int tt_k_conv2d_chain_fwd(const float *x, const float *w1, const floa
   constexpr size_t lds = sizeof(float) * chain::LDS_FLOATS;
   if (!allow_big_lds((const void *)kern)) return -1;
   hipLaunchKernelGGL(kern, dim3((unsigned)(2 * N)), dim3(chain::NTH), lds, stream(), x, w1, b1, w2,
-                     b2, pool1, codes1, pool2, copy2, pad2, codes2, wsnap, C1);
+                     b2, pool1, codes1, pool2, copy2, pad2, codes2, snap1, snap2, C1);
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }

@@ -158,8 +158,20 @@ static int valid_pool_params(int ph, int pw, int sh, int sw) {
 }
 
 TTPendConv tt_pend;
+TTPendConv tt_pend1;
 /* defer ag_conv2d / ag_reshape launches so a relu / padones can fuse */
 static int g_conv_relu = 1;
+/* a conv -> relu -> pool -> conv -> relu -> pool chain as one launch */
+static int g_conv_chain = 1;
+
+int tth_conv_chain(int on) {
+    const int prev = g_conv_chain;
+    if (on >= 0) {
+        tt_flush_pending();
+        g_conv_chain = on ? 1 : 0;
+    }
+    return prev;
+}
 
 int tt_defer_enabled(void) { return g_conv_relu; }
 
@@ -234,12 +246,107 @@ static int conv_fwd_gemm(const float *x, const float *wd, const float *bd, float
     return rc ? -3 : 0;
 }
 
+int tt_conv_fwd_any(const float *x, const float *w, const float *b, float *out, const int *q) {
+    if (tt_k_conv2d_fwd_lds(x, w, b, out, q[0], q[1], q[2], q[3], q[4], q[5], q[6], q[7], q[8],
+                            q[9], q[10], q[11], q[12]) == 0)
+        return 0;
+    return conv_fwd_gemm(x, w, b, out, q);
+}
+
+/* The geometry tt_k_conv2d_chain_fwd takes: q1 the first convolution (C1 <=
+ * 4 channels of 32x32 -> 32 filters, 3x3, stride 1, pad 1), q2 the second
+ * (its pool output -> 64 filters, the same kernel). */
+static int chain_geometry(const int *q1, const int *q2) {
+    static const int k[8] = {3, 3, 1, 1, 1, 1};
+    for (int i = 0; i < 6; i++)
+        if (q1[5 + i] != k[i] || q2[5 + i] != k[i]) return 0;
+    return q1[1] >= 1 && q1[1] <= 4 && q1[2] == 32 && q1[3] == 32 && q1[4] == 32 &&
+           q1[11] == 32 && q1[12] == 32 && q2[0] == q1[0] && q2[1] == 32 && q2[2] == 16 &&
+           q2[3] == 16 && q2[4] == 64 && q2[11] == 16 && q2[12] == 16;
+}
+
+/* The convolution outputs of a launched chain were not written: each becomes
+ * a recipe recomputing it from the chain's snapshot of its filters and bias
+ * (or, without memory for the recipe, is computed now), and its relu a
+ * recipe of it. */
+static int chain_outputs(const TTPendConv *p, float *snap) {
+    int rc = 0;
+    if (tt_lazy_conv(p->out, p->xt, snap, p->geo) != 0) {
+        rc = tt_conv_fwd_any(p->x, snap, snap + (long)p->geo[4] * p->geo[1] * 9, p->out->dev,
+                             p->geo);
+        ttrt_free(snap);
+    }
+    if (rc == 0 && tt_lazy_relu(p->r, p->out) != 0)
+        rc = tt_k_relu_fwd(p->out->dev, p->r->dev, p->r->numel);
+    if (rc != 0) {
+        p->out->valid = 0;
+        p->r->valid = 0;
+    }
+    return rc;
+}
+
+int tt_chain_launch(Tensor *pad) {
+    if (!tt_pend1.active || tt_pend1.active != TT_PEND_CONV_RELU_POOL ||
+        (tt_pend.active != TT_PEND_CONV_RELU_POOL && tt_pend.active != TT_PEND_CONV_RELU_POOL_COPY) ||
+        !tt_pend1.codes || !tt_pend.codes || !tt_pend1.xt || tt_pend.xt != tt_pend1.p ||
+        !chain_geometry(tt_pend1.geo, tt_pend.geo))
+        return 1;
+    const TTPendConv a = tt_pend1, b = tt_pend;
+    Tensor *c = b.active == TT_PEND_CONV_RELU_POOL_COPY ? b.c : NULL;
+    const long n1 = 32L * a.geo[1] * 9 + 32, n2 = 64L * 32 * 9 + 64;
+    float *s1 = (float *)ttrt_alloc(sizeof(float) * (size_t)n1);
+    float *s2 = s1 ? (float *)ttrt_alloc(sizeof(float) * (size_t)n2) : NULL;
+    if (!s2 || tt_k_conv2d_chain_fwd(a.x, a.w, a.b, b.w, b.b, a.p->dev,
+                                     (unsigned char *)a.codes->dev, b.p->dev,
+                                     c ? c->dev : NULL, pad ? pad->dev : NULL,
+                                     (unsigned char *)b.codes->dev, s1, s2, a.geo[0], a.geo[1],
+                                     32, 32, 32, 64) != 0) {
+        ttrt_free(s1);
+        ttrt_free(s2);
+        return 1;
+    }
+    tt_pend1.active = 0;
+    tt_pend.active = 0;
+    *a.codes_dst = a.codes;  /* the pool nodes own them now */
+    *b.codes_dst = b.codes;
+    const int rc1 = chain_outputs(&a, s1), rc2 = chain_outputs(&b, s2);
+    if (rc1 || rc2) ttrt_set_error(-3);
+    return 0;
+}
+
 /* Launch the pending kernel.  A convolution whose direct kernel cannot be
  * launched after all runs through conv_fwd_gemm instead.  When nothing can
  * produce the output, the output tensor is marked as holding no valid data,
  * so tt_dev / tt_data on it return NULL (and every op reading it returns
  * NULL), as an op failing at its call would have. */
+static int flush_one(void);
+
+int tt_flush_first(void) {
+    if (!tt_pend1.active) return 0;
+    const TTPendConv second = tt_pend;
+    tt_pend = tt_pend1;
+    tt_pend1.active = 0;
+    const int rc = flush_one();
+    tt_pend = second;
+    return rc;
+}
+
 int tt_flush_pending(void) {
+    if (tt_pend1.active) {
+        if (tt_chain_launch(NULL) == 0) return 0;
+        /* the first convolution by itself, then the second as it stands */
+        const TTPendConv second = tt_pend;
+        tt_pend = tt_pend1;
+        tt_pend1.active = 0;
+        const int rc1 = flush_one();
+        tt_pend = second;
+        const int rc2 = flush_one();
+        return rc1 ? rc1 : rc2;
+    }
+    return flush_one();
+}
+
+static int flush_one(void) {
     if (!tt_pend.active) return 0;
     const int kind = tt_pend.active;
     tt_pend.active = 0;
@@ -332,28 +439,47 @@ Tensor *tt_conv2d_keepcol_ex(const Tensor *a, const Tensor *w, const Tensor *b, 
     const int Wo = (W + 2 * pw - WW) / sw + 1;
     if (Ho <= 0 || Wo <= 0) return NULL;
 
-    const float *x = tt_dev((Tensor *)a), *wd = tt_dev((Tensor *)w);
+    /* the input is the pool output of a pending conv -> relu -> pool: that
+     * launch stays pending (stashed here) so both convolutions can run as
+     * one chain; it is put back (and flushed first) if this one is not
+     * deferred after all */
+    const int q[13] = {N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo};
+    TTPendConv first;
+    first.active = 0;
+    if (defer && g_conv_relu && g_conv_chain && tt_pend.active == TT_PEND_CONV_RELU_POOL &&
+        tt_pend.p == a && !tt_pend1.active && chain_geometry(tt_pend.geo, q)) {
+        first = tt_pend;
+        tt_pend.active = 0;
+    }
+    const float *x = first.active ? a->dev : tt_dev((Tensor *)a), *wd = tt_dev((Tensor *)w);
     const float *bd = b ? tt_dev((Tensor *)b) : NULL;
-    if (!x || !wd || (b && !bd)) return NULL;
-
     const long shp[4] = {N, F, Ho, Wo};
-    Tensor *out = tt_empty_dev(shp, 4);
-    if (!out) return NULL;
+    Tensor *out = x && wd && (!b || bd) ? tt_empty_dev(shp, 4) : NULL;
+    if (!out) {
+        if (first.active) tt_pend = first;
+        return NULL;
+    }
     const int Kc = C * HH * WW;
     const long Ncol = (long)N * Ho * Wo;
     /* LDS-staged direct convolution: taken when it also covers the weight
      * gradient the caller will ask for (that reads x, so no col is kept) */
     const int lds = tt_k_conv2d_lds_plan(N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo);
-    if ((lds & 1) && (!col_out || (lds & 2))) {
-        if (defer && g_conv_relu) {
-            tt_flush_pending();
-            const int q[13] = {N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo};
-            tt_pend.out = out;
-            tt_pend.x = x; tt_pend.w = wd; tt_pend.b = bd;
-            for (int i = 0; i < 13; i++) tt_pend.geo[i] = q[i];
-            tt_pend.active = TT_PEND_CONV;
-            return out;
-        }
+    const int direct = (lds & 1) && (!col_out || (lds & 2));
+    if (direct && defer && g_conv_relu) {
+        tt_flush_pending();
+        tt_pend.out = out;
+        tt_pend.x = x; tt_pend.w = wd; tt_pend.b = bd;
+        tt_pend.xt = (Tensor *)a;
+        for (int i = 0; i < 13; i++) tt_pend.geo[i] = q[i];
+        tt_pend.active = TT_PEND_CONV;
+        if (first.active) tt_pend1 = first;
+        return out;
+    }
+    if (first.active) {  /* not deferred: the first convolution runs now */
+        tt_pend = first;
+        if (!(x = tt_dev((Tensor *)a))) return fail(out);
+    }
+    if (direct) {
         if (tt_k_conv2d_fwd_lds(x, wd, bd, out->dev, N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho,
                                 Wo) == 0)
             return out;

@@ -119,10 +119,14 @@ typedef struct TTLazyVal {
                                   3: the reduction `dwt` (every pending one runs
                                   in the same launch); 4: [src, 1]^T src2, the
                                   weight gradient of a matmul of padones(src)
-                                  (tt_k_gemm_tn_padones, dims rows Kx N) */
+                                  (tt_k_gemm_tn_padones, dims rows Kx N); 5:
+                                  conv(src, buf) -- a convolution output the
+                                  two-convolution chain did not store */
     TTDwtShared *dwt;
     Tensor *src2;
     int dims[3];
+    float *buf;                /* kind 5: the filters | bias snapshot (owned) */
+    int q[13];                 /* kind 5: N C H W F HH WW sh sw ph pw Ho Wo */
     struct TTLazyVal *next;
 } TTLazyVal;
 static TTLazyVal *g_lazy_vals;
@@ -135,6 +139,7 @@ static int lazy_add(Tensor *t, Tensor *src, int kind) {
     l->kind = kind;
     l->dwt = NULL;
     l->src2 = NULL;
+    l->buf = NULL;
     l->next = g_lazy_vals;
     g_lazy_vals = l;
     return 0;
@@ -150,6 +155,13 @@ int tt_lazy_gemm_tn_padones(Tensor *dw, Tensor *x, Tensor *g, int rows, int Kx, 
     g_lazy_vals->dims[0] = rows;
     g_lazy_vals->dims[1] = Kx;
     g_lazy_vals->dims[2] = N;
+    return 0;
+}
+
+int tt_lazy_conv(Tensor *t, Tensor *x, float *snap, const int *q) {
+    if (lazy_add(t, x, 5) != 0) return -1;
+    g_lazy_vals->buf = snap;
+    memcpy(g_lazy_vals->q, q, sizeof(g_lazy_vals->q));
     return 0;
 }
 
@@ -358,12 +370,17 @@ restart:
                            : l->kind == 2 ? tt_k_ce_mean_rows(x, l->t->dev, (int)l->src->numel)
                            : l->kind == 4 ? tt_k_gemm_tn_padones(l->dims[0], l->dims[1],
                                                                  l->dims[2], x, x2, l->t->dev)
+                           : l->kind == 5 ? tt_conv_fwd_any(x, l->buf,
+                                                            l->buf + (long)l->q[4] * l->q[1] *
+                                                                         l->q[5] * l->q[6],
+                                                            l->t->dev, l->q)
                                           : tt_k_relu_fwd(x, l->t->dev, l->t->numel);
             if (rc != 0) l->t->valid = 0;
             else tt_mark_dev_written(l->t);
         }
         tt_release(l->src);
         tt_release(l->src2);
+        ttrt_free(l->buf);  /* stream-ordered: after the recomputation read it */
         free(l);
         goto restart;
     }
@@ -382,7 +399,7 @@ void tt_release(Tensor *t) {
 }
 
 float *tt_dev(Tensor *t) {
-    if (tt_pend.active) tt_flush_pending();
+    if (tt_pend.active || tt_pend1.active) tt_flush_pending();
     if (g_lazy_vals && t) lazy_take(t, 0, 0);
     if (!t || !t->dev || !t->valid) return NULL;
     if (!(t->valid & TT_V_DEV)) {
@@ -397,7 +414,7 @@ float *tt_dev(Tensor *t) {
  * the device copy is re-uploaded before its next use. */
 float *tt_data(const Tensor *ct) {
     Tensor *t = (Tensor *)ct;
-    if (tt_pend.active) tt_flush_pending();
+    if (tt_pend.active || tt_pend1.active) tt_flush_pending();
     if (g_lazy_vals && t) {
         lazy_take(t, 0, 0);
         lazy_take(t, 1, 0);  /* the host may write t: recipes reading it run now */

@@ -46,13 +46,31 @@ typedef struct {
     Tensor *p, *c;            /* the pool output, the reshape's copy (owned by their nodes) */
     const float *x, *w, *b;   /* device operands, retained by the node's parents (matmul: b is
                                  the weights' last row when x is a padones input) */
+    Tensor *xt;               /* conv kinds: the input tensor x belongs to */
     int geo[13];              /* conv: N C H W F HH WW sh sw ph pw Ho Wo; matmul: M N K */
     Tensor *codes;            /* *_POOL* kinds: the pool windows' codes (bytes in a float */
     Tensor **codes_dst;       /* tensor, or NULL), handed to the pool node's field here
                                  once written */
 } TTPendConv;
 extern TTPendConv tt_pend;
+/* The first convolution of a chain conv -> relu -> pool -> conv (kind
+ * TT_PEND_CONV_RELU_POOL, its pool output the input of the convolution
+ * pending in tt_pend): when the second one has its relu and pool too, one
+ * launch runs both (tt_k_conv2d_chain_fwd); otherwise it is flushed first. */
+extern TTPendConv tt_pend1;
 int tt_flush_pending(void);   /* 0 ok; <0 the pending output is invalid */
+/* the chain tt_pend1 + tt_pend (pooled) in one launch, pad: the padded copy
+ * of the second pool's flattened output (or NULL); 0 launched (both cleared),
+ * 1 not possible here (nothing done) */
+int tt_chain_launch(Tensor *pad);
+int tt_flush_first(void);     /* launch tt_pend1 by itself (tt_pend stays pending) */
+/* out = conv(x, w) + b by the direct kernel, else the GEMM path; q holds
+ * N C H W F HH WW sh sw ph pw Ho Wo.  0 ok */
+int tt_conv_fwd_any(const float *x, const float *w, const float *b, float *out, const int *q);
+/* t (allocated, unwritten) = conv(x, w) + b with w | b the F*K + F floats of
+ * snap (device memory the recipe then owns and frees), q as above; written on
+ * first use.  0 ok, -1 no memory (snap is not taken) */
+int tt_lazy_conv(Tensor *t, Tensor *x, float *snap, const int *q);
 /* t (allocated, unwritten) = relu(src), written on first use (tensor.c) */
 int tt_lazy_relu(Tensor *t, Tensor *src);
 int tt_lazy_padones(Tensor *t, Tensor *src);  /* t (M x K+1) = padones(src (M x K)) */
