@@ -345,7 +345,9 @@ int tth_conv_relu_fuse(int on);
 /* Tuning hook: 0 disables, 1 (default) enables running a conv -> relu ->
  * 2x2 pool -> conv -> relu -> 2x2 pool chain of ag_* calls (the
  * tt_k_conv2d_chain_fwd shape) as one launch; the convolutions' outputs are
- * then recomputed from a snapshot of their filters on first read.  Returns
+ * then recomputed from a snapshot of their filters on first read.  The
+ * backward then runs the second convolution's input gradient and the first
+ * one's weight gradient as one launch too (tt_k_conv2d_chain_bwd).  Returns
  * the previous setting; -1 only queries. */
 int tth_conv_chain(int on);
 int tt_k_conv2d_lds_plan(int N, int C, int H, int W, int F, int HH, int WW,
@@ -396,6 +398,17 @@ int tt_k_conv2d_chain_fwd(const float *x, const float *w1, const float *b1, cons
                           const float *b2, float *pool1, unsigned char *codes1, float *pool2,
                           float *copy2, float *pad2, unsigned char *codes2, float *snap1,
                           float *snap2, int N, int C1, int H, int W, int F1, int F2);
+/* The backward between the chain's two convolutions in one launch (plus the
+ * weight-gradient reduction): dx2 (N x 32 x 16 x 16) = the input gradient of
+ * the second convolution (w2 64 x 32 x 3 x 3, pad 1) from its output
+ * gradient dc2 (N x 64 x 16 x 16) -- the reference's src/autograd.c:515-539
+ * + col2im :406-434, bit for bit tt_k_conv2d_dx_lds -- then, through the 2x2
+ * pool + relu backward of the pool codes codes1 (src/autograd.c:555-594,
+ * :318-327), dw1 / db1 of the first convolution (x N x C1 x 32 x 32, C1 <=
+ * 3, 32 filters, 3x3, pad 1; src/autograd.c:456-513), bit for bit
+ * tt_k_conv2d_dw_lds_pooled of dx2.  -1: not covered (nothing launched). */
+int tt_k_conv2d_chain_bwd(const float *dc2, const float *w2, const unsigned char *codes1,
+                          const float *x, float *dx2, float *dw1, float *db1, int N, int C1);
 int tt_k_conv2d_dw_lds(const float *g, const float *x, float *dw, float *db,
                        int N, int C, int H, int W, int F, int HH, int WW,
                        int sh, int sw, int ph, int pw, int Ho, int Wo);

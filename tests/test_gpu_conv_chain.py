@@ -143,16 +143,18 @@ def _cnn(Node, x, P, keep):
     return logits
 
 
-@pytest.mark.parametrize("read_early", [False, True])
-def test_autograd_chain_on_off_bitexact(tlib, read_early):
+@pytest.mark.parametrize("B,read_early", [(16, False), (16, True), (128, False), (128, True)])
+def test_autograd_chain_on_off_bitexact(tlib, B, read_early):
     """The config-4 graph through ag_*: with the two-convolution chain
     (one launch, convolution outputs recomputed from the filter snapshot on
     first read) every value and gradient is bit for bit the graph without it,
     also when the convolution and relu outputs are read after an SGD step has
     changed the filters in place (the recipes read the snapshot), and when
-    read before the backward pass."""
+    read before the backward pass.  At B = 128 the backward also takes the
+    one-launch middle (the second convolution's input gradient and the first
+    one's weight gradient: tt_k_conv2d_chain_bwd)."""
     from tinytorch_amd.torch_py import Node
-    x, y, P = orc.cnn_inputs(B=16)
+    x, y, P = orc.cnn_inputs(B=B)
     names = ("X", "w1", "b1", "w2", "b2", "wfc", "c1", "r1", "p1", "c2", "r2", "p2", "f", "d",
              "logits")
 
@@ -179,15 +181,15 @@ def test_autograd_chain_on_off_bitexact(tlib, read_early):
         finally:
             tlib.tth_conv_chain(prev)
 
-    print("autograd chain on/off, read_early", read_early, flush=True)
+    print("autograd chain on/off, B", B, "read_early", read_early, flush=True)
     (v1, g1), (v0, g0) = run(True), run(False)
     for k in v0:
         assert bits_equal(v1[k], v0[k]), k
     for k in g0:
         assert bits_equal(g1[k], g0[k]), k
     # the recomputed convolution is the one of the filters before the step
-    ref = orc.conv2d_fwd(x, P["w1"], P["b1"], 1, 1, 1, 1)
-    assert np.abs(v1["c1"] - ref).max() <= 1e-4 * max(1.0, np.abs(ref).max())
+    ref = orc.conv2d_fwd(x[:8], P["w1"], P["b1"], 1, 1, 1, 1)
+    assert np.abs(v1["c1"][:8] - ref).max() <= 1e-4 * max(1.0, np.abs(ref).max())
 
 
 def test_autograd_chain_second_conv_not_pooled(tlib):
@@ -219,3 +221,66 @@ def test_autograd_chain_second_conv_not_pooled(tlib):
 
     for a, b in zip(run(True), run(False)):
         assert bits_equal(a, b)
+
+
+# (N, C1): the config-4 batch, other channel counts; the kernel covers the
+# batches whose pooled weight gradient takes units of 8 rows (128 <= N < 256),
+# the others return -1 (the separate kernels run instead)
+BWD_CASES = [(128, 3), (130, 1), (200, 2), (5, 3), (256, 3)]
+
+
+@pytest.mark.parametrize("N,C1", BWD_CASES)
+def test_conv_chain_bwd_matches_separate(tlib, N, C1):
+    """tt_k_conv2d_chain_bwd: dx2 bit for bit tt_k_conv2d_dx_lds, and dw1 /
+    db1 bit for bit tt_k_conv2d_dw_lds_pooled of that dx2 with the pool
+    codes; dx2 and dw1 within the bar of the oracle's conv backward and
+    pool + relu backward (reference src/autograd.c:456-594)."""
+    r = np.random.default_rng(200 + N + C1)
+    x = r.uniform(0, 1, (N, C1, 32, 32)).astype(np.float32)
+    w1 = (r.standard_normal((32, C1, 3, 3)) * np.sqrt(2.0 / (9 * C1))).astype(np.float32)
+    b1 = (r.standard_normal(32) * 0.1).astype(np.float32)
+    w2 = (r.standard_normal((64, 32, 3, 3)) * np.sqrt(2.0 / 288)).astype(np.float32)
+    g = r.standard_normal((N, 64, 16, 16)).astype(np.float32)
+    g.flat[::11] = 0.0
+    dx, dw1_, db1_, dw2_, dg = (DevBuf.from_np(a) for a in (x, w1, b1, w2, g))
+    # the first pool's codes and output from the forward kernels
+    o1, p1 = DevBuf(N * 32 * 1024), DevBuf(N * 32 * 256)
+    codes = DevBuf(N * 32 * 256, np.uint8)
+    r1 = DevBuf(N * 32 * 1024)
+    check(tlib.tt_k_conv2d_relu_fwd_lds(dx.ptr, dw1_.ptr, db1_.ptr, o1.ptr, r1.ptr,
+                                        *geo(N, C1, 32, 32)), "conv1")
+    rv = r1.to_np((N, 32, 32, 32))
+    win = np.stack([rv[:, :, 0::2, 0::2], rv[:, :, 0::2, 1::2], rv[:, :, 1::2, 0::2],
+                    rv[:, :, 1::2, 1::2]])
+    cv = np.argmax(win, axis=0).astype(np.uint8)
+    for k in range(4):
+        cv |= ((win[k] > 0).astype(np.uint8) << (2 + k))
+    codes = DevBuf.from_np(cv)
+    print("conv chain bwd", N, C1, flush=True)
+    # separate kernels
+    ex, ew, eb = DevBuf(N * 32 * 256), DevBuf(w1.size), DevBuf(32)
+    check(tlib.tt_k_conv2d_dx_lds(dg.ptr, dw2_.ptr, ex.ptr, *geo(N, 32, 16, 64)), "dx2")
+    check(tlib.tt_k_conv2d_dw_lds_pooled(ex.ptr, codes.ptr, dx.ptr, ew.ptr, eb.ptr,
+                                         *geo(N, C1, 32, 32)), "dw1 pooled")
+    # one launch
+    fx, fw, fb = DevBuf(N * 32 * 256), DevBuf(w1.size), DevBuf(32)
+    rc = tlib.tt_k_conv2d_chain_bwd(dg.ptr, dw2_.ptr, codes.ptr, dx.ptr, fx.ptr, fw.ptr, fb.ptr,
+                                    N, C1)
+    if not 128 <= N < 256:
+        assert rc == -1
+        return
+    check(rc, "chain bwd")
+    assert bits_equal(fx.to_np((N, 32, 16, 16)), ex.to_np((N, 32, 16, 16)))
+    assert bits_equal(fw.to_np(w1.shape), ew.to_np(w1.shape))
+    assert bits_equal(fb.to_np((32,)), eb.to_np((32,)))
+    if N != 130:
+        return
+    # oracle: dx2, then the pool + relu backward and conv1's dw / db
+    pool1 = orc.maxpool_fwd(rv, 2, 2, 2, 2)
+    rdx = orc.conv2d_bwd(pool1, w2, g, 1, 1, 1, 1, need_dw=False, need_db=False)[0]
+    dx2 = fx.to_np((N, 32, 16, 16))
+    assert np.abs(dx2 - rdx).max() <= 1e-4 * max(1.0, np.abs(rdx).max())
+    gr = orc.relu_bwd(rv, orc.maxpool_bwd(rv, dx2, 2, 2, 2, 2))
+    _, rdw, rdb = orc.conv2d_bwd(x, w1, gr, 1, 1, 1, 1, need_dx=False)
+    assert np.abs(fw.to_np(w1.shape) - rdw).max() <= 1e-4 * max(1.0, np.abs(rdw).max())
+    assert np.abs(fb.to_np((32,)) - rdb).max() <= 1e-4 * max(1.0, np.abs(rdb).max())

@@ -877,6 +877,60 @@ static void backward_reshape(AGNode *n) {
     accum_move(a, tt_reshape(n->grad, a->val->shape, a->val->ndim));
 }
 
+static int conv_takes_pooled(const AGNode *c);
+static void conv_geo(const AGNode *c, int q[13]);
+
+/* The second convolution of a conv -> relu -> 2x2 pool -> conv chain (the
+ * tt_k_conv2d_chain_fwd shape): its input gradient (the pool's gradient,
+ * complete here: the pool feeds only this convolution) and, through the pool
+ * codes, the first convolution's weight gradient in one launch
+ * (ttk_conv2d_chain_bwd, its reduction deferred like conv_dw_deferred's).
+ * The first convolution's rule then has nothing left to do (its input needs
+ * no gradient; its own gradient stays the recipe the pool's rule leaves).
+ * 0: not taken, nothing launched. */
+static int conv_chain_bwd(AGNode *n, const float *gd) {
+    AGNode *p = n->in[0];
+    if (!tt_chain_enabled() || !needs(p) || p->op != &OP_MAXPOOL2D || !p->at.win.codes ||
+        p->fanin != 1 || p->grad || p->lazy_g || p->at.win.kh != 2 || p->at.win.kw != 2 ||
+        p->at.win.sh != 2 || p->at.win.sw != 2)
+        return 0;
+    AGNode *r = p->in[0];
+    if (!relu_fusable(r)) return 0;
+    AGNode *c = r->in[0];
+    if (!conv_takes_pooled(c)) return 0;
+    int q1[13], q2[13];
+    conv_geo(c, q1);
+    conv_geo(n, q2);
+    static const int k[6] = {3, 3, 1, 1, 1, 1};
+    for (int i = 0; i < 6; i++)
+        if (q1[5 + i] != k[i] || q2[5 + i] != k[i]) return 0;
+    if (q1[2] != 32 || q1[3] != 32 || q1[4] != 32 || q2[0] != q1[0] || q2[1] != 32 ||
+        q2[2] != 16 || q2[3] != 16 || q2[4] != 64)
+        return 0;
+    AGNode *w1 = c->in[1], *b1 = c->n_in > 2 ? c->in[2] : NULL;
+    const long bshp[1] = {32};
+    const float *w2 = tt_dev(n->in[1]->val), *x = tt_dev(c->in[0]->val);
+    const unsigned char *codes = (const unsigned char *)tt_dev(p->at.win.codes);
+    Tensor *ga = w2 && x && codes ? tt_empty_like(p->val) : NULL;
+    Tensor *gw = ga ? tt_empty_like(w1->val) : NULL;
+    Tensor *gb = gw && needs(b1) ? tt_empty_dev(bshp, 1) : NULL;
+    TTDwtJob job;
+    if (!gw || (needs(b1) && !gb) ||
+        ttk_conv2d_chain_bwd(gd, w2, codes, x, ga->dev, gw->dev, gb ? gb->dev : NULL, q1[0],
+                             q1[1], &job) != 0) {
+        tt_release(ga);
+        tt_release(gw);
+        tt_release(gb);
+        return 0;
+    }
+    if (tt_lazy_dwt(gw, gb, &job) != 0) ttk_dwt_reduce_jobs(&job, 1);
+    accum_move(p, ga);
+    if (gb) accum_move(b1, gb);
+    accum_move(w1, gw);
+    c->fused = 1;
+    return 1;
+}
+
 static void backward_conv2d(AGNode *n) {
     if (n->lazy_codes) {
         if (conv_pooled_dw(n)) return;
@@ -968,6 +1022,7 @@ static void backward_conv2d(AGNode *n) {
             if (own) ttrt_free(col);
         }
     }
+    if (conv_chain_bwd(n, gd)) return;
     if (needs(a) && (lds & 4)) {
         const float *wd = tt_dev(w->val);
         Tensor *ga = wd ? tt_empty_like(a->val) : NULL;

@@ -2271,6 +2271,250 @@ conv_chain_fwd_kernel(const float *__restrict__ x, const float *__restrict__ w1,
   }
 }
 
+// ---- the middle of the two-convolution chain's backward in one launch ----
+//
+// For the chain of conv_chain_fwd_kernel: from the second convolution's
+// output gradient dc2 (N x 64 x 16 x 16), its input gradient dx2 (the first
+// pool's gradient, N x 32 x 16 x 16), then -- without writing or re-reading
+// it -- the first pool + relu backward decoded from the pool codes and the
+// first convolution's weight gradient partials (dw1 | db1 per unit of 8
+// output rows, exactly the partial blocks conv_dwt_kernel<1, 1, true> writes,
+// for the same deferred reduction).  One workgroup of eight waves per image
+// half:
+//   staging: dc2's rows (the half and a one-row halo each side, gapped rows
+//     of 24 floats), the second filter bank in its own order (the FLIP
+//     layout of conv_fwd_k_kernel), the image rows of the half plus halo and
+//     the first pool's codes, all with direct loads and one wait;
+//   phase 1: dx2 as conv_fwd_k_kernel<1, FLIP, VEC, 3, 3, 2> computes it
+//     (waves 4-7 take the upper half of the channel steps and their sums are
+//     added to waves 0-3's in LDS), on 4x8 pixel patches (a half-wave's
+//     operand reads on 32 different banks); the same MFMA sequence per
+//     output, so the same bits;
+//   phase 2: waves 0-3 store dx2 and write the first convolution's output
+//     gradient into LDS from each pool window's code (the pool + relu
+//     backward: the window's gradient at its first argmax when that relu
+//     value is > 0, else zero);
+//   phase 3: the weight gradient of two units of 8 rows, four waves a unit,
+//     as conv_dwt_kernel<1, 1, true> (the same items, MFMA order, LDS sum
+//     (0 + 2) + (1 + 3) and bias sum), one partial block a unit.
+namespace chainb {
+constexpr int NTH = 512;
+constexpr int G2 = 8, RS2 = 16 + G2, R2 = 10, CS2 = R2 * RS2 + 4;   // dc2 slab
+constexpr int GX = 4, RWX = 32 + GX, RX = 18, CSX = RX * RWX + 4;   // image slab
+constexpr int GS = 260;                  // g1 tile: per filter, 8 rows x 32 + 4
+constexpr int SLOT = 1024 + 64;          // one wave's dW accumulators and bias sum
+constexpr int O_W = 0;                   // filter bank 2, then the g1 tiles of both units
+constexpr int W_SZ = 64 * 32 * 9;
+constexpr int O_D = O_W + W_SZ;          // dc2 slab, then the partial sums
+constexpr int O_X = O_D + 64 * CS2;      // image slab (4 planes)
+constexpr int X_SZ = 2816;
+constexpr int O_C = O_X + X_SZ;          // pool codes, 32 x 128 bytes
+constexpr int LDS_FLOATS = O_C + 1024;
+static_assert(2 * 32 * GS <= W_SZ && 4 * CSX <= X_SZ && X_SZ % 256 == 0, "regions");
+static_assert((64 * CS2) % 256 == 0 && 2 * 2 * SLOT <= 64 * CS2, "dc2 slab");
+static_assert(LDS_FLOATS * 4 <= LDS_MAX, "LDS");
+}  // namespace chainb
+
+__global__ void __launch_bounds__(chainb::NTH)
+conv_chain_bwd_kernel(const float *__restrict__ dc2, const float *__restrict__ w2,
+                      const unsigned char *__restrict__ codes1, const float *__restrict__ x,
+                      float *__restrict__ dx2, float *__restrict__ part, int C1) {
+  using namespace chainb;
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  float *ws = smem + O_W, *ds = smem + O_D, *xs = smem + O_X;
+  const unsigned char *c1t = (const unsigned char *)(smem + O_C);
+  const int n = blockIdx.x >> 1, hf = blockIdx.x & 1;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, half = lane >> 5;
+
+  // ---- staging ----
+  {
+    const float *gn = dc2 + (long)n * 64 * 256;
+    for (int base = wave * 256; base < 64 * CS2; base += NTH * 4) {
+      const int i = base + lane * 4;
+      const int c = i / CS2, rem = i - c * CS2;
+      const int slot = rem / RS2, j = rem - slot * RS2;
+      const int row = 8 * hf - 1 + slot;
+      const bool ok = slot < R2 && j >= G2 && row >= 0 && row < 16;
+      dma_dwordx4(ok ? gn + (c * 16 + row) * 16 + (j - G2) : g_zero_src, ds + base);
+    }
+    for (int base = wave * 256; base < W_SZ; base += NTH * 4)
+      dma_dwordx4(w2 + base + lane * 4, ws + base);
+    const float *xn = x + (long)n * C1 * 1024;
+    for (int base = wave * 256; base < X_SZ; base += NTH * 4) {
+      const int i = base + lane * 4;
+      const int c = i / CSX, rem = i - c * CSX;
+      const int slot = rem / RWX, j = rem - slot * RWX;
+      const int row = 16 * hf - 1 + slot;
+      const bool ok = c < C1 && slot < RX && j >= GX && row >= 0 && row < 32;
+      dma_dwordx4(ok ? xn + (c * 32 + row) * 32 + (j - GX) : g_zero_src, xs + base);
+    }
+    if (wave < 4) {
+      const int i = wave * 1024 + lane * 16;  // byte of the 32 x 128 tile
+      dma_dwordx4((const float *)(codes1 + ((long)n * 32 + (i >> 7)) * 256 + 128 * hf + (i & 127)),
+                  smem + O_C + wave * 256);
+    }
+  }
+  dma_wait();
+  __syncthreads();
+
+  // ---- phase 1: dx2 (the flipped-kernel convolution of dc2) ----
+  const int pb = wave & 3, grp = wave >> 2;
+  const int r4 = l32 >> 3, c8 = l32 & 7;
+  const int hol = 4 * (pb >> 1) + r4, wo = 8 * (pb & 1) + c8;  // pixel in the half
+  f32x16 acc;
+  for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+  {
+    const int bj = hol * RS2 + wo + G2 - 1 + half * 32 * CS2;
+    const float *wa = ws + l32 * 9 + half * 32 * 32 * 9;
+    auto load = [&](int c, float (&a)[9], float (&b)[9]) {
+      const float *wc = wa + c * 32 * 9;
+#pragma unroll
+      for (int t = 0; t < 9; t++) a[t] = wc[8 - t];
+#pragma unroll
+      for (int kh = 0; kh < 3; kh++)
+#pragma unroll
+        for (int kw = 0; kw < 3; kw++) b[kh * 3 + kw] = ds[bj + c * CS2 + kh * RS2 + kw];
+    };
+    auto mfmas = [&](const float (&a)[9], const float (&b)[9]) {
+#pragma unroll
+      for (int t = 0; t < 9; t++)
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t], b[t], acc, 0, 0, 0);
+    };
+    const int cs0 = grp * 16, cs1 = cs0 + 16;
+    float a0[9], b0[9], a1[9], b1[9];
+    load(cs0, a0, b0);
+    for (int c = cs0; c < cs1; c += 2) {
+      load(c + 1, a1, b1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(a0, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      load(c + 2 < cs1 ? c + 2 : c + 1, a0, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(a1, b1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // the upper channel group's sums through LDS, added in a fixed order
+  {
+    float *red = ds + pb * 1024 + lane;
+    __syncthreads();
+    if (grp == 1) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) red[r * 64] = acc[r];
+    }
+    __syncthreads();
+    if (grp == 0) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[r] += red[r * 64];
+    }
+  }
+
+  // ---- phase 2: dx2, and the first convolution's output gradient in LDS ----
+  if (grp == 0) {
+    const int pr = 8 * hf + hol;
+    float *g1 = ws + (hol >> 2) * 32 * GS + ((2 * hol) & 7) * 32 + 2 * wo;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int c = 8 * (r >> 2) + 4 * half + (r & 3);
+      const float v = acc[r] + 0.0f;  // the dX kernel's (zero) bias
+      dx2[(((long)n * 32 + c) * 16 + pr) * 16 + wo] = v;
+      const unsigned code = c1t[c * 128 + hol * 16 + wo];
+      const float gv = 0.0f + v;
+      auto at = [&](unsigned kq) {
+        return ((code & 3) == kq && ((code >> (2 + kq)) & 1)) ? gv : 0.0f;
+      };
+      float *d = g1 + c * GS;
+      *reinterpret_cast<float2 *>(d) = make_float2(at(0), at(1));
+      *reinterpret_cast<float2 *>(d + 32) = make_float2(at(2), at(3));
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 3: the first convolution's weight gradient, two units ----
+  {
+    const int uu = wave >> 2, pq = wave & 3;
+    const int K1 = C1 * 9;
+    int bb = C1 * CSX;  // taps past K: the zero plane
+    if (l32 < K1) {
+      const int c = l32 / 9, t = l32 - c * 9, kh = t / 3, kw = t - kh * 3;
+      bb = c * CSX + kh * RWX + GX + kw - 1;
+    }
+    f32x16 dacc;
+    for (int r = 0; r < 16; r++) dacc[r] = 0.0f;
+    float bsum = 0.0f;
+    const float *ga = ws + uu * 32 * GS + l32 * GS + half * 16;
+    constexpr int quads = 4;
+    constexpr int xstep = 4 * RWX - quads * 4, gstep = 4 * 32 - quads * 4;
+    int go = pq * 32, xo = pq * RWX + half * 16 + uu * 8 * RWX;
+    int qd = 0, left = 8;
+    auto advance = [&]() {
+      if (--left <= 0) return;
+      if (++qd == quads) {
+        qd = 0;
+        go += gstep + 4;
+        xo += xstep + 4;
+      } else {
+        go += 4;
+        xo += 4;
+      }
+    };
+    auto load = [&](f32x4 &a4, float (&bv)[4]) {
+      a4 = *(const f32x4 *)(ga + go);
+#pragma unroll
+      for (int e = 0; e < 4; e++) bv[e] = xs[bb + xo + e];
+    };
+    auto mfmas = [&](const f32x4 &a4, const float (&bv)[4]) {
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        dacc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[e], bv[e], dacc, 0, 0, 0);
+      bsum += (a4[0] + a4[1]) + (a4[2] + a4[3]);
+    };
+    f32x4 a0, a1;
+    float b0[4], b1[4];
+    load(a0, b0);
+#pragma unroll 1
+    for (int it = 0; it < 8; it += 2) {
+      advance();
+      load(a1, b1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(a0, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      advance();
+      load(a0, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(a1, b1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    bsum += __shfl_xor(bsum, 32, 64);  // both halves of filter l32
+    // the four waves of a unit: (0 + 2) + (1 + 3), through LDS
+#pragma unroll
+    for (int s = 2; s >= 1; s >>= 1) {
+      __syncthreads();
+      if (pq >= s && pq < 2 * s) {
+        float *d = ds + (uu * 2 + pq - s) * SLOT;
+#pragma unroll
+        for (int r = 0; r < 16; r++) d[r * 64 + lane] = dacc[r];
+        d[1024 + lane] = bsum;
+      }
+      __syncthreads();
+      if (pq < s) {
+        const float *d = ds + (uu * 2 + pq) * SLOT;
+#pragma unroll
+        for (int r = 0; r < 16; r++) dacc[r] += d[r * 64 + lane];
+        bsum += d[1024 + lane];
+      }
+    }
+    if (pq == 0) {
+      float *pz = part + ((long)n * 4 + 2 * hf + uu) * (1024 + 32);
+#pragma unroll
+      for (int r = 0; r < 16; r++) pz[r * 64 + lane] = dacc[r];
+      if (lane < 32) pz[1024 + lane] = bsum;
+    }
+  }
+}
+
 int g_lds_conv = 1;  // tth_conv_lds
 
 }  // namespace
@@ -2587,4 +2831,54 @@ extern "C" int tt_k_conv2d_chain_fwd(const float *x, const float *w1, const floa
   hipLaunchKernelGGL(kern, dim3((unsigned)(2 * N)), dim3(chain::NTH), lds, stream(), x, w1, b1, w2,
                      b2, pool1, codes1, pool2, copy2, pad2, codes2, snap1, snap2, C1);
   return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+// The middle of the two-convolution chain's backward (conv_chain_bwd_kernel):
+// dx2 (N x 32 x 16 x 16) = the input gradient of the second convolution (w2
+// 64 x 32 x 3 x 3, pad 1) from its output gradient dc2 (N x 64 x 16 x 16),
+// bit for bit tt_k_conv2d_dx_lds; then the first convolution's (x N x C1 x
+// 32 x 32, C1 <= 3, 32 filters, 3x3, pad 1) weight and bias gradient from
+// dx2 through the 2x2 pool + relu backward of codes1, as the deferred
+// reduction *job (the partials tt_k_conv2d_dw_lds_pooled would reduce, the
+// same values).  -1: not covered (nothing launched); < -1: error.
+extern "C" int ttk_conv2d_chain_bwd(const float *dc2, const float *w2, const unsigned char *codes1,
+                                    const float *x, float *dx2, float *dw1, float *db1, int N,
+                                    int C1, TTDwtJob *job) {
+  if (!dc2 || !w2 || !codes1 || !x || !dx2 || !dw1 || !job || !g_dwt || N <= 0 ||
+      N > 16383 || C1 < 1 || C1 > 3)
+    return -1;
+  if (!aligned16(dc2) || !aligned16(w2) || !aligned16(x) || ((uintptr_t)codes1 & 15)) return -1;
+  // the partials must be those of the plan tt_k_conv2d_dw_lds_pooled takes
+  const Geo g1{C1, 32, 32, 3, 3, 1, 1, 1, 1, 32, 32, 32, C1 * 9};
+  const DwtPlan tp = plan_dwt(g1, N);
+  if (tp.tg != 1 || tp.ntgw != 1 || tp.nts != 1 || tp.nfb != 1 || tp.rc != 8 || tp.jbp != 1)
+    return -1;
+  if (fail_direct()) return -3;
+  constexpr size_t lds = sizeof(float) * chainb::LDS_FLOATS;
+  if (!allow_big_lds((const void *)conv_chain_bwd_kernel)) return -1;
+  const long S = 1024 + 32;
+  float *part = (float *)ttrt_alloc(sizeof(float) * (size_t)(S * tp.units));
+  if (!part) return -2;
+  hipLaunchKernelGGL(conv_chain_bwd_kernel, dim3((unsigned)(2 * N)), dim3(chainb::NTH), lds,
+                     stream(), dc2, w2, codes1, x, dx2, part, C1);
+  if (hipGetLastError() != hipSuccess) {
+    ttrt_free(part);
+    return -3;
+  }
+  const long cols = S / 4;
+  int zl = 1;
+  while (zl < 64 && zl * 16 < tp.units) zl *= 2;
+  *job = TTDwtJob{part, dw1, db1, tp.units, 1, 1, 32, C1 * 9, zl,
+                  (int)((cols + NT / zl - 1) / (NT / zl))};
+  return 0;
+}
+
+// ttk_conv2d_chain_bwd with the reduction run at once: dw1 / db1 written.
+extern "C" int tt_k_conv2d_chain_bwd(const float *dc2, const float *w2,
+                                     const unsigned char *codes1, const float *x, float *dx2,
+                                     float *dw1, float *db1, int N, int C1) {
+  TTDwtJob job;
+  const int rc = ttk_conv2d_chain_bwd(dc2, w2, codes1, x, dx2, dw1, db1, N, C1, &job);
+  if (rc != 0) return rc;
+  return ttk_dwt_reduce_jobs(&job, 1);
 }

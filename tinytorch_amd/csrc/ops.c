@@ -164,6 +164,8 @@ static int g_conv_relu = 1;
 /* a conv -> relu -> pool -> conv -> relu -> pool chain as one launch */
 static int g_conv_chain = 1;
 
+int tt_chain_enabled(void) { return g_conv_relu && g_conv_chain; }
+
 int tth_conv_chain(int on) {
     const int prev = g_conv_chain;
     if (on >= 0) {

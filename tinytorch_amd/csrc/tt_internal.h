@@ -63,7 +63,8 @@ int tt_flush_pending(void);   /* 0 ok; <0 the pending output is invalid */
  * of the second pool's flattened output (or NULL); 0 launched (both cleared),
  * 1 not possible here (nothing done) */
 int tt_chain_launch(Tensor *pad);
-int tt_flush_first(void);     /* launch tt_pend1 by itself (tt_pend stays pending) */
+int tt_flush_first(void);
+int tt_chain_enabled(void);   /* tth_conv_chain on (and deferral on) */     /* launch tt_pend1 by itself (tt_pend stays pending) */
 /* out = conv(x, w) + b by the direct kernel, else the GEMM path; q holds
  * N C H W F HH WW sh sw ph pw Ho Wo.  0 ok */
 int tt_conv_fwd_any(const float *x, const float *w, const float *b, float *out, const int *q);
