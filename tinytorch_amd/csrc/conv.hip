@@ -1958,9 +1958,10 @@ int launch_dwt_plan(const float *gr, const float *x, float *dw, float *db, const
 //     conv_fwd_k_kernel (lane half h takes channels [h*CH2, (h+1)*CH2), taps
 //     in order), so the values are bit for bit those of that kernel.
 //   phase A: the first convolution's 18 output rows (9 pooled rows: 8 owned
-//     plus one halo row), a row pair (two blocks of 8 windows) a wave, wave 0
-//     also the ninth; the pooled rows go to an LDS slab laid out for the
-//     second convolution, the owned rows' codes to an LDS tile.
+//     plus one halo row) as 18 blocks of 8 windows (a row pair's left or
+//     right half) dealt round robin to the waves; the pooled rows go to an
+//     LDS slab laid out for the second convolution, the owned rows' codes to
+//     an LDS tile.
 //   phase B: the second convolution on that slab: wave w takes a 4x8 pixel
 //     patch (w % 4, 8 windows) and 32 filters (w / 4).
 //   LDS banks: a half-wave's 32 operand reads hit 32 different banks (slab
@@ -2069,34 +2070,26 @@ conv_chain_fwd_kernel(const float *__restrict__ x, const float *__restrict__ w1,
     const float bias = bs[l32];
     const int win = l32 >> 2, dy = (l32 >> 1) & 1, dx = l32 & 1;
     bool first = true;
-    for (int i = wave; i < 9; i += 8) {
-      int bj[2];
-#pragma unroll
-      for (int j = 0; j < 2; j++)
-        bj[j] = (2 * i + dy) * RS1 + 2 * (8 * j + win) + dx + G1 - 1 + half * CH2 * CS1;
-      f32x16 acc[2];
-#pragma unroll
-      for (int j = 0; j < 2; j++)
-        for (int r = 0; r < 16; r++) acc[j][r] = 0.0f;
-      auto load = [&](int c, float (&a)[9], float (&b)[9][2]) {
+    // 18 blocks (9 row pairs x 2 column halves of 8 windows), round robin
+    for (int blk = wave; blk < 18; blk += 8) {
+      const int i = blk >> 1, j = blk & 1;
+      const int bj = (2 * i + dy) * RS1 + 2 * (8 * j + win) + dx + G1 - 1 + half * CH2 * CS1;
+      f32x16 acc;
+      for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+      auto load = [&](int c, float (&a)[9], float (&b)[9]) {
 #pragma unroll
         for (int t = 0; t < 9; t++) a[t] = wa[(c * 9 + t) * 32];
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int kh = 0; kh < 3; kh++)
 #pragma unroll
-          for (int kh = 0; kh < 3; kh++)
-#pragma unroll
-            for (int kw = 0; kw < 3; kw++)
-              b[kh * 3 + kw][j] = xs1[bj[j] + c * CS1 + kh * RS1 + kw];
+          for (int kw = 0; kw < 3; kw++) b[kh * 3 + kw] = xs1[bj + c * CS1 + kh * RS1 + kw];
       };
-      auto mfmas = [&](const float (&a)[9], const float (&b)[9][2]) {
+      auto mfmas = [&](const float (&a)[9], const float (&b)[9]) {
 #pragma unroll
         for (int t = 0; t < 9; t++)
-#pragma unroll
-          for (int j = 0; j < 2; j++)
-            acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[t][j], a[t], acc[j], 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_32x32x2f32(b[t], a[t], acc, 0, 0, 0);
       };
-      float a0[9], bb0[9][2], a1[9], bb1[9][2];
+      float a0[9], bb0[9], a1[9], bb1[9];
       load(0, a0, bb0);
       int c = 0;
       for (; c + 1 < CH2; c += 2) {
@@ -2119,21 +2112,19 @@ conv_chain_fwd_kernel(const float *__restrict__ x, const float *__restrict__ w1,
       float *dst = xs2 + l32 * CS2 + srow * RS2 + G2;
       unsigned char *cdst = c1t + l32 * C1T + (q - 8 * hf) * 16;
 #pragma unroll
-      for (int j = 0; j < 2; j++)
+      for (int qq = 0; qq < 4; qq++) {
+        float o[4];
 #pragma unroll
-        for (int qq = 0; qq < 4; qq++) {
-          float o[4];
-#pragma unroll
-          for (int e = 0; e < 4; e++) {
-            const float v = acc[j][4 * qq + e] + bias;
-            o[e] = v > 0.0f ? v : 0.0f;
-          }
-          unsigned code;
-          const float m = pool_code(o[0], o[1], o[2], o[3], code);
-          const int pc = 8 * j + 2 * qq + half;
-          dst[pc] = m;
-          if (own) cdst[pc] = (unsigned char)code;
+        for (int e = 0; e < 4; e++) {
+          const float v = acc[4 * qq + e] + bias;
+          o[e] = v > 0.0f ? v : 0.0f;
         }
+        unsigned code;
+        const float m = pool_code(o[0], o[1], o[2], o[3], code);
+        const int pc = 8 * j + 2 * qq + half;
+        dst[pc] = m;
+        if (own) cdst[pc] = (unsigned char)code;
+      }
     }
   }
   __syncthreads();
