@@ -391,13 +391,18 @@ int tt_k_conv2d_relu_pool_fwd_lds(const float *x, const float *w, const float *b
  * and 18432 + 64 floats) get w1 | b1 and w2 | b2 as read (zeros for a NULL
  * bias), from which tt_k_conv2d_fwd_lds recomputes them.  copy2 (pool2 again) and pad2 (N x
  * 4097, pool2 flattened then 1) are optional; b1 / b2 may be NULL.  Bit for
- * bit the two separate launches.  -1: shape or alignment not covered (H, W,
+ * bit the two separate launches.  fcpart (optional, fcn == 10 classes): a
+ * classifier's partial logits, fcpart[h][n][j] = sum over the 2048 features
+ * of image n's half h (flattened pool2, h * 32 + (0..31) of each channel's
+ * 64) of feature * fcw[feature][j] (fcw: 4096 x 10 rows, row-major; bias not
+ * included) -- the matmul of the flattened pool2 split over the halves.  -1: shape or alignment not covered (H, W,
  * F1, F2 must be 32, 32, 32, 64; x, w2, pool1, pool2, copy2, codes1, codes2
  * 16-byte aligned), nothing launched. */
 int tt_k_conv2d_chain_fwd(const float *x, const float *w1, const float *b1, const float *w2,
                           const float *b2, float *pool1, unsigned char *codes1, float *pool2,
                           float *copy2, float *pad2, unsigned char *codes2, float *snap1,
-                          float *snap2, int N, int C1, int H, int W, int F1, int F2);
+                          float *snap2, const float *fcw, int fcn, float *fcpart, int N,
+                          int C1, int H, int W, int F1, int F2);
 /* The backward between the chain's two convolutions in one launch (plus the
  * weight-gradient reduction): dx2 (N x 32 x 16 x 16) = the input gradient of
  * the second convolution (w2 64 x 32 x 3 x 3, pad 1) from its output

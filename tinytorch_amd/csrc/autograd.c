@@ -271,6 +271,26 @@ static const Tensor *padones_input(const AGNode *a) {
 AGNode *ag_matmul(AGNode *a, AGNode *b) {
     if (!a || !b) return NULL;
     const Tensor *av = a->val, *bv = b->val;
+    if (tt_pend.active == TT_PEND_CHAIN_PAD && tt_pend.d == av && bv->ndim == 2 &&
+        bv->shape[0] == av->shape[1] && bv->shape[1] == 10 && padones_input(a) == tt_pend.c) {
+        /* the classifier of a pending conv chain (10 classes): it waits too;
+         * a softmax-CE of it takes its partial sums from the chain's launch,
+         * anything else runs the chain and then this GEMM */
+        const TTPendConv s1 = tt_pend1, s2 = tt_pend;
+        tt_pend1.active = tt_pend.active = 0;  /* the weights' device copy, nothing flushed */
+        const float *wd = tt_dev(b->val);
+        tt_pend1 = s1;
+        tt_pend = s2;
+        const long shp[2] = {av->shape[0], 10};
+        Tensor *out = wd ? tt_empty_dev(shp, 2) : NULL;
+        AGNode *n = out ? make_node(out, &OP_MATMUL, a, b, NULL) : NULL;
+        if (!n) return NULL;
+        tt_pend.fco = out;
+        tt_pend.fcw = wd;
+        tt_pend.fcn = 10;
+        tt_pend.active = TT_PEND_CHAIN_FC;
+        return n;
+    }
     if (av->ndim == 2 && bv->ndim == 2 && av->shape[1] == bv->shape[0] && av->shape[0] > 0 &&
         av->shape[1] > 0 && bv->shape[1] > 0 && av->shape[0] <= 0x7fffffffL &&
         av->shape[1] <= 0x7fffffffL && bv->shape[1] <= 0x7fffffffL) {
@@ -363,10 +383,18 @@ AGNode *ag_padones(AGNode *a) {
     const long shp[2] = {M, K + 1};
     if (tt_pend1.active && tt_pend.active == TT_PEND_CONV_RELU_POOL_COPY && tt_pend.c == a->val) {
         /* both convolutions of a conv -> relu -> pool chain, the second's
-         * flattening copy and this padones in one launch */
-        Tensor *v = tt_empty_dev(shp, 2);
-        if (v && tt_chain_launch(v) == 0) return make_node(v, &OP_PADONES, a, NULL, NULL);
-        tt_release(v);
+         * flattening copy and this padones in one launch -- left pending
+         * too, so that a classifier matmul of this padones and its
+         * softmax-CE can join it */
+        Tensor *v = tt_chain_ready() ? tt_empty_dev(shp, 2) : NULL;
+        if (v) {
+            AGNode *n = make_node(v, &OP_PADONES, a, NULL, NULL);
+            if (n) {
+                tt_pend.d = v;
+                tt_pend.active = TT_PEND_CHAIN_PAD;
+            }
+            return n;
+        }
         tt_flush_first();  /* the first by itself; the second and this padones below */
     }
     if (tt_pend.active == TT_PEND_CONV_RELU_POOL_COPY && tt_pend.c == a->val) {
@@ -549,6 +577,41 @@ AGNode *ag_softmax_ce(AGNode *logits, const int *labels, long rows) {
     int32_t *hlab = (int32_t *)malloc(sizeof(int32_t) * (size_t)rows);
     if (hlab)
         for (long r = 0; r < rows; r++) hlab[r] = (int32_t)labels[r];
+    if (tt_pend.active == TT_PEND_CHAIN_FC && tt_pend.fco == logits->val && probs && seed &&
+        loss && hlab && rows <= TT_CE_ARG_ROWS) {
+        /* the conv chain, its classifier and this softmax-CE pending: the
+         * chain's launch leaves the classifier's two partial sums per row
+         * (the halves of each image), and one reduction adds them, the bias
+         * and runs the softmax-CE (the mean loss a recipe, as below) */
+        const TTPendConv p = tt_pend;
+        const int K = (int)p.c->shape[1];
+        const float *bias = p.fcw + (long)K * cols;
+        Tensor *rl = tt_empty_dev(&rows, 1);
+        float *ws = rl ? (float *)ttrt_alloc(sizeof(float) * 2 * (size_t)rows * cols) : NULL;
+        if (ws && tt_chain_launch(ws) == 0) {
+            const TTCeHook hk = {bias, hlab, probs->dev, seed->dev, rl->dev, 1.0f / (float)rows};
+            int rc = ttk_reduce_ce(ws, logits->val->dev, (int)rows, cols, 2, 1, &hk);
+            ttrt_free(ws);
+            if (rc == 0 && (tt_lazy_ce_mean(loss, rl) == 0 ||
+                            tt_k_ce_mean_rows(rl->dev, loss->dev, (int)rows) == 0)) {
+                tt_release(rl);
+                AGNode *n = make_node(loss, &OP_SOFTMAX_CE, logits, NULL, NULL);
+                if (!n) { tt_release(probs); tt_release(seed); free(hlab); return NULL; }
+                n->at.ce.probs = probs;
+                n->at.ce.seed = seed;
+                n->at.ce.labels = hlab;
+                return n;
+            }
+            /* the reduction did not run: the logits from the GEMM (the
+             * softmax-CE runs below) */
+            if (rc != 0 && tt_k_gemm_bias_relu_pad((int)rows, cols, K, p.c->dev, p.fcw, bias,
+                                                   logits->val->dev, NULL, NULL) != 0)
+                logits->val->valid = 0;
+        } else {
+            ttrt_free(ws);
+        }
+        tt_release(rl);
+    }
     if (tt_pend.active == TT_PEND_MATMUL && tt_pend.out == logits->val && tt_pend.b && probs &&
         seed && loss && hlab && rows <= TT_CE_ARG_ROWS && cols <= 32) {
         /* the classifier's GEMM is still pending: the softmax-CE runs in its
@@ -1544,7 +1607,9 @@ void ag_release(AGNode *n) {
         AGNode *d = dead;
         dead = d->next;
         if ((tt_pend.active && (tt_pend.out == d->val || tt_pend.r == d->val ||
-                                tt_pend.p == d->val || tt_pend.c == d->val)) ||
+                                tt_pend.p == d->val || tt_pend.c == d->val ||
+                                (tt_pend.active >= TT_PEND_CHAIN_PAD && tt_pend.d == d->val) ||
+                                (tt_pend.active == TT_PEND_CHAIN_FC && tt_pend.fco == d->val))) ||
             (tt_pend1.active && (tt_pend1.out == d->val || tt_pend1.r == d->val ||
                                  tt_pend1.p == d->val)))
             tt_flush_pending();  /* the launch writes into d's tensors */

@@ -1997,7 +1997,7 @@ static_assert(O_X1 % 64 == 0 && O_X2 % 4 == 0 && (F1 * CS2) % 4 == 0, "alignment
 static_assert(LDS_FLOATS * 4 <= LDS_MAX, "LDS");
 }  // namespace chain
 
-template <int CH2>
+template <int CH2, int FCN>
 __global__ void __launch_bounds__(chain::NTH)
 conv_chain_fwd_kernel(const float *__restrict__ x, const float *__restrict__ w1,
                       const float *__restrict__ b1, const float *__restrict__ w2,
@@ -2005,7 +2005,8 @@ conv_chain_fwd_kernel(const float *__restrict__ x, const float *__restrict__ w1,
                       unsigned char *__restrict__ codes1, float *__restrict__ pool2,
                       float *__restrict__ copy2, float *__restrict__ pad2,
                       unsigned char *__restrict__ codes2, float *__restrict__ snap1,
-                      float *__restrict__ snap2, int C1) {
+                      float *__restrict__ snap2, const float *__restrict__ fcw,
+                      float *__restrict__ fcpart, int C1) {
   using namespace chain;
   extern __shared__ __attribute__((aligned(16))) float smem[];
   float *ws2 = smem + O_WS2, *ws1 = smem + O_WS1, *bs = smem + O_B;
@@ -2144,6 +2145,15 @@ conv_chain_fwd_kernel(const float *__restrict__ x, const float *__restrict__ w1,
     *reinterpret_cast<uint4 *>(codes1 + ((long)n * F1 + f) * 256 + 128 * hf + 16 * r8) = v;
   }
 
+  // the classifier rows of this thread's four pool2 features (FCN classes
+  // each), loaded now and used after phase B
+  float fw[FCN > 0 ? 4 * FCN : 1];
+  if constexpr (FCN > 0) {
+    const float *wr = fcw + (long)((tid >> 3) * 64 + 32 * hf + 4 * (tid & 7)) * FCN;
+#pragma unroll
+    for (int i = 0; i < 4 * FCN; i++) fw[i] = wr[i];
+  }
+
   // ---- phase B: second convolution on the pool1 slab ----
   const int pb = wave & 3, fb = wave >> 2;
   f32x16 acc;
@@ -2258,6 +2268,32 @@ conv_chain_fwd_kernel(const float *__restrict__ x, const float *__restrict__ w1,
       const uint4 cv = {cs[0], cs[1], cs[2], cs[3]};
       *reinterpret_cast<uint4 *>(codes2 + ((long)n * F2 + (tid >> 1)) * 64 + 32 * hf +
                                  16 * (tid & 1)) = cv;
+    }
+    if constexpr (FCN > 0) {
+      // the classifier's partial logits over this half's 2048 features
+      // (the flattened pool2 row times the weights' rows, the bias left to
+      // the reduction): fused multiply-adds over the thread's 4 features,
+      // then the 512 threads' pieces of class j added in a fixed order --
+      // 32 threads a class, 16 pieces each in thread order, then a tree
+      float *red = ws2;  // the second filter bank is no longer read
+#pragma unroll
+      for (int j = 0; j < FCN; j++) {
+        float a = v[0] * fw[j];
+        a = __builtin_fmaf(v[1], fw[FCN + j], a);
+        a = __builtin_fmaf(v[2], fw[2 * FCN + j], a);
+        a = __builtin_fmaf(v[3], fw[3 * FCN + j], a);
+        red[j * NTH + tid] = a;
+      }
+      __syncthreads();
+      const int j = tid >> 5, l = tid & 31;
+      float a = 0.0f;
+      if (j < FCN) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) a += red[j * NTH + l * 16 + i];
+      }
+#pragma unroll
+      for (int m = 16; m >= 1; m >>= 1) a += __shfl_xor(a, m, 32);
+      if (j < FCN && l == 0) fcpart[((long)hf * gridDim.x / 2 + n) * FCN + j] = a;
     }
   }
 }
@@ -2801,13 +2837,16 @@ extern "C" void ttk_dwt_job_drop(TTDwtJob *job) {
 // and, when given, copy2 (pool2 again), pad2 (N x 4097: pool2 flattened, then
 // 1) and snap1 / snap2 (both or neither: 32*C1*9 + 32 and 18432 + 64 floats,
 // w1 | b1 and w2 | b2 as read, zeros for a NULL bias).  Every value bit for
-// bit that of two tt_k_conv2d_relu_pool_fwd_lds launches.  -1: shape or
-// alignment not covered (nothing launched).
+// bit that of two tt_k_conv2d_relu_pool_fwd_lds launches.  fcpart (optional,
+// fcn == 10): the partial logits of a classifier fcw (4096 x 10 rows, bias
+// not included) over each image half's 2048 pool2 features, fcpart[h][n][j]
+// for h = 0, 1.  -1: shape or alignment not covered (nothing launched).
 extern "C" int tt_k_conv2d_chain_fwd(const float *x, const float *w1, const float *b1,
                                      const float *w2, const float *b2, float *pool1,
                                      unsigned char *codes1, float *pool2, float *copy2,
                                      float *pad2, unsigned char *codes2, float *snap1,
-                                     float *snap2, int N, int C1, int H, int W, int F1, int F2) {
+                                     float *snap2, const float *fcw, int fcn, float *fcpart,
+                                     int N, int C1, int H, int W, int F1, int F2) {
   if (!x || !w1 || !w2 || !pool1 || !codes1 || !pool2 || !codes2 || N <= 0 || N > 65535 ||
       C1 < 1 || C1 > 4 || H != 32 || W != 32 || F1 != chain::F1 || F2 != chain::F2 ||
       !snap1 != !snap2)
@@ -2816,11 +2855,13 @@ extern "C" int tt_k_conv2d_chain_fwd(const float *x, const float *w1, const floa
       ((uintptr_t)codes1 & 15) || ((uintptr_t)codes2 & 15) || (copy2 && !aligned16(copy2)))
     return -1;
   if (fail_direct()) return -3;
-  auto kern = C1 > 2 ? conv_chain_fwd_kernel<2> : conv_chain_fwd_kernel<1>;
+  if (fcpart && (fcn != 10 || !fcw)) return -1;
+  auto kern = fcpart ? (C1 > 2 ? conv_chain_fwd_kernel<2, 10> : conv_chain_fwd_kernel<1, 10>)
+                     : (C1 > 2 ? conv_chain_fwd_kernel<2, 0> : conv_chain_fwd_kernel<1, 0>);
   constexpr size_t lds = sizeof(float) * chain::LDS_FLOATS;
   if (!allow_big_lds((const void *)kern)) return -1;
   hipLaunchKernelGGL(kern, dim3((unsigned)(2 * N)), dim3(chain::NTH), lds, stream(), x, w1, b1, w2,
-                     b2, pool1, codes1, pool2, copy2, pad2, codes2, snap1, snap2, C1);
+                     b2, pool1, codes1, pool2, copy2, pad2, codes2, snap1, snap2, fcw, fcpart, C1);
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 

@@ -287,22 +287,37 @@ static int chain_outputs(const TTPendConv *p, float *snap) {
     return rc;
 }
 
-int tt_chain_launch(Tensor *pad) {
-    if (!tt_pend1.active || tt_pend1.active != TT_PEND_CONV_RELU_POOL ||
-        (tt_pend.active != TT_PEND_CONV_RELU_POOL && tt_pend.active != TT_PEND_CONV_RELU_POOL_COPY) ||
-        !tt_pend1.codes || !tt_pend.codes || !tt_pend1.xt || tt_pend.xt != tt_pend1.p ||
-        !chain_geometry(tt_pend1.geo, tt_pend.geo))
-        return 1;
+int tt_chain_ready(void) {
+    const int k = tt_pend.active;
+    return tt_pend1.active == TT_PEND_CONV_RELU_POOL &&
+           (k == TT_PEND_CONV_RELU_POOL || k == TT_PEND_CONV_RELU_POOL_COPY ||
+            k == TT_PEND_CHAIN_PAD || k == TT_PEND_CHAIN_FC) &&
+           tt_pend1.codes && tt_pend.codes && tt_pend1.xt && tt_pend.xt == tt_pend1.p &&
+           chain_geometry(tt_pend1.geo, tt_pend.geo);
+}
+
+/* the classifier of a TT_PEND_CHAIN_FC (the matmul of the padded copy): its
+ * GEMM from the flattened copy, the weights' last row added as the bias */
+static int chain_fc_gemm(const TTPendConv *b) {
+    const int M = (int)b->c->shape[0], K = (int)b->c->shape[1];
+    return tt_k_gemm_bias_relu_pad(M, b->fcn, K, b->c->dev, b->fcw, b->fcw + (long)K * b->fcn,
+                                   b->fco->dev, NULL, NULL);
+}
+
+int tt_chain_launch(float *fcpart) {
+    if (!tt_chain_ready() || (fcpart && tt_pend.active != TT_PEND_CHAIN_FC)) return 1;
     const TTPendConv a = tt_pend1, b = tt_pend;
-    Tensor *c = b.active == TT_PEND_CONV_RELU_POOL_COPY ? b.c : NULL;
+    Tensor *c = b.active != TT_PEND_CONV_RELU_POOL ? b.c : NULL;
+    Tensor *pad = b.active >= TT_PEND_CHAIN_PAD ? b.d : NULL;
     const long n1 = 32L * a.geo[1] * 9 + 32, n2 = 64L * 32 * 9 + 64;
     float *s1 = (float *)ttrt_alloc(sizeof(float) * (size_t)n1);
     float *s2 = s1 ? (float *)ttrt_alloc(sizeof(float) * (size_t)n2) : NULL;
     if (!s2 || tt_k_conv2d_chain_fwd(a.x, a.w, a.b, b.w, b.b, a.p->dev,
                                      (unsigned char *)a.codes->dev, b.p->dev,
                                      c ? c->dev : NULL, pad ? pad->dev : NULL,
-                                     (unsigned char *)b.codes->dev, s1, s2, a.geo[0], a.geo[1],
-                                     32, 32, 32, 64) != 0) {
+                                     (unsigned char *)b.codes->dev, s1, s2,
+                                     fcpart ? b.fcw : NULL, fcpart ? b.fcn : 0, fcpart,
+                                     a.geo[0], a.geo[1], 32, 32, 32, 64) != 0) {
         ttrt_free(s1);
         ttrt_free(s2);
         return 1;
@@ -312,7 +327,10 @@ int tt_chain_launch(Tensor *pad) {
     *a.codes_dst = a.codes;  /* the pool nodes own them now */
     *b.codes_dst = b.codes;
     const int rc1 = chain_outputs(&a, s1), rc2 = chain_outputs(&b, s2);
-    if (rc1 || rc2) ttrt_set_error(-3);
+    int rc3 = 0;
+    if (b.active == TT_PEND_CHAIN_FC && !fcpart && (rc3 = chain_fc_gemm(&b)) != 0)
+        b.fco->valid = 0;
+    if (rc1 || rc2 || rc3) ttrt_set_error(-3);
     return 0;
 }
 
@@ -366,15 +384,17 @@ static int flush_one(void) {
             if (rc != 0) tt_pend.r->valid = 0;
         }
     } else if (kind == TT_PEND_CONV_RELU || kind == TT_PEND_CONV_RELU_POOL ||
-               kind == TT_PEND_CONV_RELU_POOL_COPY) {
+               kind == TT_PEND_CONV_RELU_POOL_COPY || kind == TT_PEND_CHAIN_PAD ||
+               kind == TT_PEND_CHAIN_FC) {
         const int *q = tt_pend.geo;
         Tensor *p = kind != TT_PEND_CONV_RELU ? tt_pend.p : NULL;
-        Tensor *c = kind == TT_PEND_CONV_RELU_POOL_COPY ? tt_pend.c : NULL;
+        Tensor *c = kind >= TT_PEND_CONV_RELU_POOL_COPY ? tt_pend.c : NULL;
+        Tensor *d = kind >= TT_PEND_CHAIN_PAD ? tt_pend.d : NULL;
         /* with the pool, the relu output is not stored: it becomes a recipe
          * (relu of the convolution output) run on first use */
         Tensor *codes = p ? tt_pend.codes : NULL;
         rc = p ? tt_k_conv2d_relu_pool_fwd_lds(tt_pend.x, tt_pend.w, tt_pend.b, tt_pend.out->dev,
-                                               NULL, p->dev, c ? c->dev : NULL, NULL,
+                                               NULL, p->dev, c ? c->dev : NULL, d ? d->dev : NULL,
                                                codes ? (unsigned char *)codes->dev : NULL,
                                                q[0], q[1], q[2], q[3], q[4], q[5], q[6], q[7],
                                                q[8], q[9], q[10], q[11], q[12])
@@ -399,11 +419,18 @@ static int flush_one(void) {
                 rc = tt_k_maxpool_fwd(tt_pend.r->dev, p->dev, q[0], q[4], q[11], q[12], 2, 2, 2,
                                       2, q[11] / 2, q[12] / 2);
             if (rc == 0 && c) rc = tt_k_copy(c->dev, p->dev, c->numel);
+            if (rc == 0 && d) rc = tt_k_padones_fwd(c->dev, d->dev, c->shape[0], c->shape[1]);
+        }
+        if (rc == 0 && kind == TT_PEND_CHAIN_FC && chain_fc_gemm(&tt_pend) != 0) {
+            tt_pend.fco->valid = 0;
+            ttrt_set_error(-3);
         }
         if (rc != 0) {
             tt_pend.r->valid = 0;
             if (p) p->valid = 0;
             if (c) c->valid = 0;
+            if (d) d->valid = 0;
+            if (kind == TT_PEND_CHAIN_FC) tt_pend.fco->valid = 0;
         }
     } else {
         const int *q = tt_pend.geo;

@@ -39,6 +39,12 @@ Tensor *tt_conv2d_keepcol(const Tensor *a, const Tensor *w, const Tensor *b,
 #define TT_PEND_CONV_RELU 6   /* ag_conv2d and ag_relu of it (r); a 2x2 ag_maxpool2d of r waits too */
 #define TT_PEND_CONV_RELU_POOL 7  /* ... and the 2x2 max pool of r (p); ag_reshape of p waits too */
 #define TT_PEND_CONV_RELU_POOL_COPY 8  /* ... and that reshape's copy (c); ag_padones of c fuses */
+/* with tt_pend1 (a two-convolution chain): ... and the padones of c (d) */
+#define TT_PEND_CHAIN_PAD 9
+/* ... and the matmul of d (fco = c * fcw[:K] + fcw[K], fcn columns): an
+ * ag_softmax_ce of fco takes the classifier's partial sums from the chain's
+ * own launch */
+#define TT_PEND_CHAIN_FC 10
 typedef struct {
     int active;               /* 0 or one of TT_PEND_* */
     Tensor *out;              /* the pending output (owned by its node) */
@@ -47,6 +53,10 @@ typedef struct {
     const float *x, *w, *b;   /* device operands, retained by the node's parents (matmul: b is
                                  the weights' last row when x is a padones input) */
     Tensor *xt;               /* conv kinds: the input tensor x belongs to */
+    Tensor *d;                /* TT_PEND_CHAIN_*: the padded copy */
+    Tensor *fco;              /* TT_PEND_CHAIN_FC: the classifier's output, */
+    const float *fcw;         /* its weights (K + 1 rows of fcn, the last the bias) */
+    int fcn;
     int geo[13];              /* conv: N C H W F HH WW sh sw ph pw Ho Wo; matmul: M N K */
     Tensor *codes;            /* *_POOL* kinds: the pool windows' codes (bytes in a float */
     Tensor **codes_dst;       /* tensor, or NULL), handed to the pool node's field here
@@ -59,10 +69,14 @@ extern TTPendConv tt_pend;
  * launch runs both (tt_k_conv2d_chain_fwd); otherwise it is flushed first. */
 extern TTPendConv tt_pend1;
 int tt_flush_pending(void);   /* 0 ok; <0 the pending output is invalid */
-/* the chain tt_pend1 + tt_pend (pooled) in one launch, pad: the padded copy
- * of the second pool's flattened output (or NULL); 0 launched (both cleared),
- * 1 not possible here (nothing done) */
-int tt_chain_launch(Tensor *pad);
+/* whether the pending chain (tt_pend1 + tt_pend) can run as one launch */
+int tt_chain_ready(void);
+/* the chain tt_pend1 + tt_pend (pooled) in one launch, with the padded copy
+ * and the classifier of the TT_PEND_CHAIN_* kinds; fcpart (TT_PEND_CHAIN_FC
+ * only): the classifier's partial sums go there (2 x rows x fcn) and its
+ * output is left to the caller, else the classifier's GEMM runs after the
+ * chain.  0 launched (both cleared), 1 not possible here (nothing done) */
+int tt_chain_launch(float *fcpart);
 int tt_flush_first(void);
 int tt_chain_enabled(void);   /* tth_conv_chain on (and deferral on) */     /* launch tt_pend1 by itself (tt_pend stays pending) */
 /* out = conv(x, w) + b by the direct kernel, else the GEMM path; q holds
