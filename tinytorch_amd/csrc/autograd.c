@@ -589,11 +589,20 @@ AGNode *ag_softmax_ce(AGNode *logits, const int *labels, long rows) {
         Tensor *rl = tt_empty_dev(&rows, 1);
         float *ws = rl ? (float *)ttrt_alloc(sizeof(float) * 2 * (size_t)rows * cols) : NULL;
         if (ws && tt_chain_launch(ws) == 0) {
-            const TTCeHook hk = {bias, hlab, probs->dev, seed->dev, rl->dev, 1.0f / (float)rows};
-            int rc = ttk_reduce_ce(ws, logits->val->dev, (int)rows, cols, 2, 1, &hk);
-            ttrt_free(ws);
+            /* the reduction is a recipe of all four outputs: the classifier's
+             * backward forms the seed itself and writes them, any earlier
+             * read runs it (ttk_reduce_ce) */
+            Tensor *const out4[4] = {logits->val, probs, seed, rl};
+            int rc = tt_lazy_ce_job(out4, logits->in[1]->val, ws, bias, hlab, (int)rows, cols,
+                                    1.0f / (float)rows);
+            if (rc != 0) {
+                const TTCeHook hk = {bias, hlab, probs->dev, seed->dev, rl->dev,
+                                     1.0f / (float)rows};
+                rc = ttk_reduce_ce(ws, logits->val->dev, (int)rows, cols, 2, 1, &hk);
+                ttrt_free(ws);
+            }
             if (rc == 0 && (tt_lazy_ce_mean(loss, rl) == 0 ||
-                            tt_k_ce_mean_rows(rl->dev, loss->dev, (int)rows) == 0)) {
+                            tt_k_ce_mean_rows(tt_dev(rl), loss->dev, (int)rows) == 0)) {
                 tt_release(rl);
                 AGNode *n = make_node(loss, &OP_SOFTMAX_CE, logits, NULL, NULL);
                 if (!n) { tt_release(probs); tt_release(seed); free(hlab); return NULL; }
@@ -739,11 +748,12 @@ static int relu_fusable(const AGNode *r);
  * (tt_k_matmul_bwd_small, which needs both gradients).  The nodes whose
  * rules this covers are marked `fused`.  0 when done; -1: not taken,
  * nothing launched. */
-static int backward_matmul_fused(AGNode *n, const float *g) {
+static int backward_matmul_fused(AGNode *n, const float *g, const TTHeadCeArgs *ce) {
     AGNode *a = n->in[0], *b = n->in[1];
     const int M = (int)a->val->shape[0], K = (int)a->val->shape[1], N = (int)b->val->shape[1];
     const int head = N <= HEAD_MAX_N;
     if (!head && !(needs(a) && needs(b))) return -1;
+    if (ce && !head) return -1;
     const float *ad = needs(b) ? tt_dev(a->val) : NULL;
     const float *bd = needs(a) ? tt_dev(b->val) : NULL;
     if ((needs(b) && !ad) || (needs(a) && !bd)) return -1;
@@ -784,15 +794,19 @@ static int backward_matmul_fused(AGNode *n, const float *g) {
         float *dB = gb ? gb->dev : NULL, *dA = ga ? ga->dev : NULL;
         float *d1 = tx ? tx->dev : NULL, *d2 = ty ? ty->dev : NULL;
         if (pr)
-            rc = tt_k_head_bwd_pool(ad, M, K, bd, N, g, dB, dA, d1, d2, codes, tc->dev,
-                                    (int)y->val->shape[1], (int)y->val->shape[2],
-                                    (int)y->val->shape[3]);
+            rc = ce ? ttk_head_bwd_ce(ad, M, K, bd, N, ce, dB, dA, d1, d2, NULL, codes, tc->dev,
+                                      (int)y->val->shape[1], (int)y->val->shape[2],
+                                      (int)y->val->shape[3])
+                    : tt_k_head_bwd_pool(ad, M, K, bd, N, g, dB, dA, d1, d2, codes, tc->dev,
+                                         (int)y->val->shape[1], (int)y->val->shape[2],
+                                         (int)y->val->shape[3]);
         if (rc != 0) {
             tt_release(tc);
             tc = NULL;
             pr = NULL;
-            rc = head ? tt_k_head_bwd(ad, M, K, bd, N, g, dB, dA, d1, d2, R)
-                      : tt_k_matmul_bwd_small(ad, M, K, bd, N, g, dB, dA, d1, d2, R);
+            rc = ce ? ttk_head_bwd_ce(ad, M, K, bd, N, ce, dB, dA, d1, d2, R, NULL, NULL, 0, 0, 0)
+                 : head ? tt_k_head_bwd(ad, M, K, bd, N, g, dB, dA, d1, d2, R)
+                        : tt_k_matmul_bwd_small(ad, M, K, bd, N, g, dB, dA, d1, d2, R);
         }
     }
     if (rc != 0) {
@@ -815,9 +829,19 @@ static int backward_matmul_fused(AGNode *n, const float *g) {
 static void backward_matmul(AGNode *n) {
     AGNode *a = n->in[0], *b = n->in[1];
     const int M = (int)a->val->shape[0], K = (int)a->val->shape[1], N = (int)b->val->shape[1];
+    /* the output gradient is a softmax-CE seed still to be reduced from the
+     * logits' partial sums: the classifier kernel forms it itself (and
+     * writes the softmax-CE's outputs) */
+    TTHeadCeArgs ce;
+    void *job = NULL;
+    if (tt_defer_enabled() && tt_lazy_ce_args(n->grad, &ce, &job) == 0 &&
+        backward_matmul_fused(n, NULL, &ce) == 0) {
+        tt_lazy_ce_done(job);
+        return;
+    }
     const float *g = tt_dev(n->grad);
     if (!g) return;
-    if (tt_defer_enabled() && backward_matmul_fused(n, g) == 0) return;
+    if (tt_defer_enabled() && backward_matmul_fused(n, g, NULL) == 0) return;
     if (needs(b) && !needs(a) && a->op == &OP_PADONES && K > 1) {
         /* dB from the padones input: the padded copy is not read; with the
          * deferral, dB is a recipe that the optimizer's step runs in its own

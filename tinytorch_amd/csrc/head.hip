@@ -21,7 +21,12 @@
 //   dA blocks: 64 columns k x 32 rows m, each lane's 8 outputs summed over j
 //     ascending -- the reference matmul_nt order.
 // Both are bit-identical to the reference's loops (this file is compiled
-// without contraction).  dh is written whole (the padones node's gradient)
+// without contraction).  With `gpart` the output gradient is not read: every
+// workgroup forms it first, in LDS, from two partial sums of the logits per
+// row, the bias and the labels -- the seed of the softmax-CE exactly as
+// splitk_reduce_ce_kernel computes it ((0 + p0) + p1 + bias, then ce_row) --
+// and workgroup 0 also writes the logits, probabilities, seed and row
+// losses that reduction would have written.  dh is written whole (the padones node's gradient)
 // and, without its last column, once or twice more: the gradient of the
 // padones' input and, when that input is a reshape (a copy) or a relu used
 // only here, the gradient of the node before it (for a relu, masked by
@@ -31,6 +36,7 @@
 #include <math.h>
 #include <stdint.h>
 #include "tt_rt.h"
+#include "ce_rows.h"
 
 namespace {
 
@@ -39,6 +45,16 @@ inline int launched() { return hipGetLastError() == hipSuccess ? 0 : -3; }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int NT = 256;
+
+// The softmax-CE whose seed the kernel forms itself (kernel argument):
+// part = 2 x M x N partial sums of the logits, bias, labels, scale; the
+// outputs workgroup 0 writes (each may be NULL).
+struct TTHeadCe {
+  const float *part, *bias;
+  LabU8 lab;
+  float scale;
+  float *logits, *probs, *seed, *rowloss;
+};
 
 
 // Every padding element of a staged block is loaded from here.
@@ -49,7 +65,7 @@ __device__ float g_head_zero[4];
 // for r < rows.  Lane t takes column t % COLS of rows t / COLS + (NT/COLS) u;
 // U loads per lane per batch, all issued before the first LDS store.
 template <int COLS, int U>
-__device__ __forceinline__ void stage_load(float (&v)[U], const float *__restrict__ src,
+__device__ __forceinline__ void stage_load(float (&v)[U], const float *src,
                                            long sstride, int base, int nr, int nc) {
   constexpr int RPB = NT / COLS;  // rows per pass of the workgroup
   const int c = threadIdx.x % COLS, r0 = threadIdx.x / COLS;
@@ -78,7 +94,7 @@ __device__ __forceinline__ void stage_store(const float (&v)[U], float *dst, int
 // batch).  (NT / CA) * UA == (NT / CB) * UB rows per batch.
 template <int CA, int UA, int CB, int UB>
 __device__ __forceinline__ void stage_pair(float *da, const float *__restrict__ sa, long lda,
-                                           int nca, float *db, const float *__restrict__ sb,
+                                           int nca, float *db, const float *sb,
                                            long ldb, int ncb, int M) {
   static_assert((NT / CA) * UA == (NT / CB) * UB, "batches of the two blocks differ");
   for (int base = 0; base < M; base += (NT / CA) * UA) {
@@ -94,17 +110,33 @@ __device__ __forceinline__ void stage_pair(float *da, const float *__restrict__ 
 // takes k = k0 + t % KW, j = j0 + t / KW and sums over m ascending from LDS
 // (As: M x KW, Gs: M x JW; the strides are constants, so every LDS read of
 // the loop carries its offset in the instruction).
-template <int KW>
+template <int KW, int NC = 16>
 __device__ __forceinline__ void head_dw_block(const float *__restrict__ A, int M, int K,
-                                              const float *__restrict__ G, int N,
+                                              const float *G, int N,
                                               float *__restrict__ dW, int k0, int j0,
-                                              float *lds) {
+                                              float *lds, const TTHeadCe &ce, bool use_ce,
+                                              float *gl) {
   constexpr int JW = NT / KW;
   const int tid = threadIdx.x;
   float *As = lds, *Gs = lds + M * KW;
-  // batches of 32 * NT / KW rows (128 or 256)
-  stage_pair<KW, 32, JW, 32 * JW / KW>(As, A + k0, K, min(KW, K - k0), Gs, G + j0, N,
-                                       min(JW, N - j0), M);
+  if (use_ce) {
+    // the block of A (M <= 32 * NT / KW rows: one batch) in flight while the
+    // seed of every row is formed (workgroup 0 stores the softmax-CE's
+    // outputs), then the block's columns of it
+    float va[32];
+    stage_load<KW, 32>(va, A + k0, K, 0, M, min(KW, K - k0));
+    head_ce_seed<NC>(ce, 0, M, M, N, gl, N, blockIdx.x == 0);
+    stage_store<KW, 32>(va, As, KW, 0, M);
+    __syncthreads();
+    for (int i = tid; i < M * JW; i += NT) {
+      const int m = i / JW, j = j0 + i % JW;
+      Gs[i] = j < N ? gl[m * N + j] : 0.0f;
+    }
+  } else {
+    // batches of 32 * NT / KW rows (128 or 256)
+    stage_pair<KW, 32, JW, 32 * JW / KW>(As, A + k0, K, min(KW, K - k0), Gs, G + j0, N,
+                                         min(JW, N - j0), M);
+  }
   __syncthreads();
   const int kl = tid % KW, jl = tid / KW;
   const int k = k0 + kl, j = j0 + jl;
@@ -126,23 +158,60 @@ __device__ __forceinline__ void head_dw_block(const float *__restrict__ A, int M
 
 // ---- backward ----
 constexpr int DA_M = 32;  // rows m per dA workgroup (8 per lane)
+// The output gradient of the classifier for rows [r0, r1) from the partial
+// sums of its logits (see above) into gl (row r at gl[(r - r0) * gs]); `out`:
+// also store the softmax-CE's outputs of those rows.  No barrier.
+template <int NC>
+__device__ __forceinline__ void head_ce_seed(const TTHeadCe &ce, int r0, int r1, int M, int N,
+                                             float *gl, int gs, bool out) {
+  for (int r = r0 + (int)threadIdx.x; r < r1; r += NT) {
+    const long total = (long)M * N;
+    float lv[NC], pr[NC], sr[NC];
+#pragma unroll
+    for (int j = 0; j < NC; j++) {
+      lv[j] = 0.0f;
+      if (j < N) {
+        float s = 0.0f;
+        s += ce.part[(long)r * N + j];
+        s += ce.part[total + (long)r * N + j];
+        lv[j] = s + ce.bias[j];
+      }
+    }
+    const float loss = ce_row<NC>(lv, ce.lab[r], pr, sr, N, ce.scale);
+#pragma unroll
+    for (int j = 0; j < NC; j++)
+      if (j < N) gl[(r - r0) * gs + j] = sr[j];
+    if (out) {
+#pragma unroll
+      for (int j = 0; j < NC; j++)
+        if (j < N) {
+          if (ce.logits) ce.logits[(long)r * N + j] = lv[j];
+          if (ce.probs) ce.probs[(long)r * N + j] = pr[j];
+          if (ce.seed) ce.seed[(long)r * N + j] = sr[j];
+        }
+      if (ce.rowloss) ce.rowloss[r] = loss;
+    }
+  }
+}
+
 template <int NC>
 __global__ void __launch_bounds__(NT)
 head_bwd_kernel(const float *__restrict__ A, int M, int K, const float *__restrict__ W, int N,
-                const float *__restrict__ G, float *__restrict__ dW, float *__restrict__ dA,
+                const float *G, float *__restrict__ dW, float *__restrict__ dA,
                 float *__restrict__ d1, float *__restrict__ d2, const float *__restrict__ R,
                 int nbw, int KW, int nkw, const unsigned char *__restrict__ codes,
-                float *__restrict__ dc, int P2, int Wo2) {
+                float *__restrict__ dc, int P2, int Wo2, TTHeadCe ce, int gl_off) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nkb = (K + 63) / 64;
+  const bool cp = ce.part != nullptr;
   if ((int)blockIdx.x < nbw) {
     // dW blocks: KW rows k x NT / KW columns j
     const int JW = NT / KW;
     const int kb = blockIdx.x % nkw, jb = blockIdx.x / nkw;
-    if (KW == 64) head_dw_block<64>(A, M, K, G, N, dW, kb * 64, jb * JW, lds);
-    else head_dw_block<32>(A, M, K, G, N, dW, kb * 32, jb * JW, lds);
+    if (KW == 64) head_dw_block<64, NC>(A, M, K, G, N, dW, kb * 64, jb * JW, lds, ce, cp, lds + gl_off);
+    else head_dw_block<32, NC>(A, M, K, G, N, dW, kb * 32, jb * JW, lds, ce, cp, lds + gl_off);
     return;
   }
   // dA block: columns [k0, k0 + 64) x rows [m0, m0 + DA_M); Ws, Gs (64 / DA_M x NC)
@@ -153,9 +222,17 @@ head_bwd_kernel(const float *__restrict__ A, int M, int K, const float *__restri
     constexpr int UW = 64 / (NT / NC), UG = DA_M / (NT / NC);
     float vw[UW], vg[UG];
     stage_load<NC, UW>(vw, W + (long)k0 * N, N, 0, min(64, K - k0), N);
-    stage_load<NC, UG>(vg, G + (long)m0 * N, N, 0, min(DA_M, M - m0), N);
-    stage_store<NC, UW>(vw, Ws, NC, 0, 64);
-    stage_store<NC, UG>(vg, Gs, NC, 0, DA_M);
+    if (cp) {
+      // the block's rows of the seed, formed here while W is in flight (the
+      // first column block stores their softmax-CE outputs when no dW
+      // workgroup does)
+      head_ce_seed<NC>(ce, m0, min(m0 + DA_M, M), M, N, Gs, NC, nbw == 0 && blk % nkb == 0);
+      stage_store<NC, UW>(vw, Ws, NC, 0, 64);
+    } else {
+      stage_load<NC, UG>(vg, G + (long)m0 * N, N, 0, min(DA_M, M - m0), N);
+      stage_store<NC, UW>(vw, Ws, NC, 0, 64);
+      stage_store<NC, UG>(vg, Gs, NC, 0, DA_M);
+    }
   }
   const int kl = lane, mg = wave;
   const int k = k0 + kl;
@@ -220,16 +297,23 @@ extern "C" {
 
 static int head_bwd(const float *A, int M, int K, const float *W, int N, const float *G,
                     float *dW, float *dA, float *d1, float *d2, const float *R,
-                    const unsigned char *codes, float *dc, int P2, int Wo2) {
-  if (M <= 0 || K <= 0 || N <= 0 || N > 32 || !G || (!dW && !dA) || (dW && !A) ||
+                    const unsigned char *codes, float *dc, int P2, int Wo2,
+                    const TTHeadCe *ce = nullptr) {
+  if (M <= 0 || K <= 0 || N <= 0 || N > 32 || (!G && !ce) || (!dW && !dA) || (dW && !A) ||
       (dA && !W) || ((d1 || d2) && (!dA || K < 2)))
     return -1;
+  if (ce && (!ce->part || !ce->bias || M > TT_CE_ARG_ROWS || N > 16)) return -1;
   const int NC = N <= 16 ? 16 : 32;
   const int KW = (size_t)M * (64 + 4) * sizeof(float) <= 64 * 1024 ? 64 : 32;
   const size_t lds_w = dW ? sizeof(float) * (size_t)M * (KW + NT / KW) : 0;
   const size_t lds_a = dA ? sizeof(float) * (size_t)(64 + DA_M) * NC : 0;
-  const size_t lds = lds_w > lds_a ? lds_w : lds_a;
+  if (ce && dW && M > 32 * (NT / KW)) return -1;  // one batch of A rows (head_dw_block)
+  size_t lds = lds_w > lds_a ? lds_w : lds_a;
+  const int gl_off = (int)(lds / sizeof(float));
+  if (ce) lds += sizeof(float) * (size_t)M * N;  // the output gradient formed in LDS
   if (lds > 64 * 1024) return -1;
+  const TTHeadCe none{};
+  const TTHeadCe &hc = ce ? *ce : none;
   const long nkb = (K + 63) / 64, nkw = (K + KW - 1) / KW;
   const long nbw = dW ? nkw * ((N + NT / KW - 1) / (NT / KW)) : 0;
   const long nba = dA ? nkb * ((M + DA_M - 1) / DA_M) : 0;
@@ -237,10 +321,10 @@ static int head_bwd(const float *A, int M, int K, const float *W, int N, const f
   const dim3 grid((unsigned)(nbw + nba));
   if (NC == 16)
     hipLaunchKernelGGL(head_bwd_kernel<16>, grid, dim3(NT), lds, stream(), A, M, K, W, N, G, dW,
-                       dA, d1, d2, R, (int)nbw, KW, (int)nkw, codes, dc, P2, Wo2);
+                       dA, d1, d2, R, (int)nbw, KW, (int)nkw, codes, dc, P2, Wo2, hc, gl_off);
   else
     hipLaunchKernelGGL(head_bwd_kernel<32>, grid, dim3(NT), lds, stream(), A, M, K, W, N, G, dW,
-                       dA, d1, d2, R, (int)nbw, KW, (int)nkw, codes, dc, P2, Wo2);
+                       dA, d1, d2, R, (int)nbw, KW, (int)nkw, codes, dc, P2, Wo2, hc, gl_off);
   return launched();
 }
 
@@ -259,3 +343,25 @@ int tt_k_head_bwd_pool(const float *A, int M, int K, const float *W, int N, cons
 }
 
 }  // extern "C"
+
+int ttk_head_bwd_ce(const float *A, int M, int K, const float *W, int N, const TTHeadCeArgs *a,
+                    float *dW, float *dA, float *d1, float *d2, const float *R,
+                    const unsigned char *codes, float *dc, int F, int Ho2, int Wo2) {
+  if (!a || !a->labels) return -1;
+  if (codes && (!dc || !d2 || F <= 0 || Ho2 <= 0 || Wo2 <= 0 ||
+                (long)F * Ho2 * Wo2 != (long)K - 1 || ((uintptr_t)dc & 7)))
+    return -1;
+  TTHeadCe ce{};
+  ce.part = a->part;
+  ce.bias = a->bias;
+  ce.scale = a->scale;
+  ce.logits = a->logits;
+  ce.probs = a->probs;
+  ce.seed = a->seed;
+  ce.rowloss = a->rowloss;
+  if (M > TT_CE_ARG_ROWS) return -1;
+  lab_u8_fill(ce.lab, a->labels, M, N);
+  return codes ? head_bwd(A, M, K, W, N, nullptr, dW, dA, d1, d2, nullptr, codes, dc, Ho2 * Wo2,
+                          Wo2, &ce)
+               : head_bwd(A, M, K, W, N, nullptr, dW, dA, d1, d2, R, nullptr, nullptr, 1, 1, &ce);
+}

@@ -113,6 +113,19 @@ typedef struct {
     int refs;
 } TTDwtShared;
 
+/* a softmax-CE whose reduction (two partial sums per logit -> logits,
+ * probabilities, seed, row losses: ttk_reduce_ce) has not run, shared by the
+ * entries of its four outputs */
+typedef struct {
+    float *ws;                 /* 2 x M x N partial sums (owned) */
+    const float *bias;         /* the classifier weights' last row */
+    int32_t *labels;           /* M labels (owned) */
+    int M, N;
+    float scale;
+    Tensor *out[4];            /* logits, probs, seed, row losses; NULL once released */
+    int refs;
+} TTCeJob;
+
 typedef struct TTLazyVal {
     Tensor *t, *src;
     int kind;                  /* 0: relu(src); 1: padones(src); 2: mean of src;
@@ -121,11 +134,14 @@ typedef struct TTLazyVal {
                                   weight gradient of a matmul of padones(src)
                                   (tt_k_gemm_tn_padones, dims rows Kx N); 5:
                                   conv(src, buf) -- a convolution output the
-                                  two-convolution chain did not store */
+                                  two-convolution chain did not store; 6: see
+                                  ce (every output is written at once) */
     TTDwtShared *dwt;
     Tensor *src2;
     int dims[3];
     float *buf;                /* kind 5: the filters | bias snapshot (owned) */
+    TTCeJob *ce;               /* kind 6: one output of the softmax-CE job `ce` (src:
+                                  the classifier weights the bias belongs to) */
     int q[13];                 /* kind 5: N C H W F HH WW sh sw ph pw Ho Wo */
     struct TTLazyVal *next;
 } TTLazyVal;
@@ -140,6 +156,7 @@ static int lazy_add(Tensor *t, Tensor *src, int kind) {
     l->dwt = NULL;
     l->src2 = NULL;
     l->buf = NULL;
+    l->ce = NULL;
     l->next = g_lazy_vals;
     g_lazy_vals = l;
     return 0;
@@ -182,10 +199,12 @@ int tt_lazy_dwt(Tensor *dw, Tensor *db, const TTDwtJob *job) {
     sh->job = *job;
     sh->refs = db ? 2 : 1;
     a->t = dw; a->src = NULL; a->kind = 3; a->dwt = sh; a->src2 = NULL;
+    a->buf = NULL; a->ce = NULL;
     a->next = g_lazy_vals;
     g_lazy_vals = a;
     if (b) {
         b->t = db; b->src = NULL; b->kind = 3; b->dwt = sh; b->src2 = NULL;
+        b->buf = NULL; b->ce = NULL;
         b->next = g_lazy_vals;
         g_lazy_vals = b;
     }
@@ -347,6 +366,110 @@ static void dwt_drop_entry(TTLazyVal **pp) {
     free(l);
 }
 
+int tt_lazy_ce_job(Tensor *const out[4], Tensor *w, float *ws, const float *bias,
+                   const int32_t *labels, int M, int N, float scale) {
+    TTCeJob *j = (TTCeJob *)calloc(1, sizeof(TTCeJob));
+    int32_t *lab = (int32_t *)malloc(sizeof(int32_t) * (size_t)M);
+    TTLazyVal *e[4] = {NULL, NULL, NULL, NULL};
+    int ok = j && lab;
+    for (int i = 0; i < 4 && ok; i++) ok = (e[i] = (TTLazyVal *)malloc(sizeof(TTLazyVal))) != NULL;
+    if (!ok) {
+        for (int i = 0; i < 4; i++) free(e[i]);
+        free(j);
+        free(lab);
+        return -1;
+    }
+    memcpy(lab, labels, sizeof(int32_t) * (size_t)M);
+    j->ws = ws;
+    j->bias = bias;
+    j->labels = lab;
+    j->M = M;
+    j->N = N;
+    j->scale = scale;
+    j->refs = 4;
+    for (int i = 0; i < 4; i++) {
+        j->out[i] = out[i];
+        e[i]->t = out[i];
+        e[i]->src = tt_retain(w);
+        e[i]->src2 = NULL;
+        e[i]->kind = 6;
+        e[i]->dwt = NULL;
+        e[i]->buf = NULL;
+        e[i]->ce = j;
+        e[i]->next = g_lazy_vals;
+        g_lazy_vals = e[i];
+    }
+    return 0;
+}
+
+/* the job's entries leave the registry (outputs written, or not: invalid) */
+static void ce_job_finish(TTCeJob *j, int written) {
+    TTLazyVal **pp = &g_lazy_vals;
+    while (*pp) {
+        TTLazyVal *l = *pp;
+        if (l->kind != 6 || l->ce != j) { pp = &l->next; continue; }
+        *pp = l->next;
+        if (written) tt_mark_dev_written(l->t);
+        else l->t->valid = 0;
+        tt_release(l->src);
+        free(l);
+    }
+    ttrt_free(j->ws);  /* stream-ordered: after the kernel that read it */
+    free(j->labels);
+    free(j);
+}
+
+static void ce_job_run(TTCeJob *j) {
+    float *tmp[4] = {NULL, NULL, NULL, NULL}, *dst[4];
+    int ok = 1;
+    for (int i = 0; i < 4; i++) {
+        if (j->out[i]) { dst[i] = j->out[i]->dev; continue; }
+        const size_t n = i == 3 ? (size_t)j->M : (size_t)j->M * j->N;
+        ok &= (dst[i] = tmp[i] = (float *)ttrt_alloc(sizeof(float) * n)) != NULL;
+    }
+    if (ok) {
+        const TTCeHook hk = {j->bias, j->labels, dst[1], dst[2], dst[3], j->scale};
+        ok = ttk_reduce_ce(j->ws, dst[0], j->M, j->N, 2, 1, &hk) == 0;
+    }
+    for (int i = 0; i < 4; i++) ttrt_free(tmp[i]);
+    ce_job_finish(j, ok);
+}
+
+static void ce_drop_entry(TTLazyVal **pp) {
+    TTLazyVal *l = *pp;
+    TTCeJob *j = l->ce;
+    *pp = l->next;
+    for (int i = 0; i < 4; i++)
+        if (j->out[i] == l->t) j->out[i] = NULL;
+    tt_release(l->src);
+    free(l);
+    if (--j->refs == 0) {
+        ttrt_free(j->ws);
+        free(j->labels);
+        free(j);
+    }
+}
+
+int tt_lazy_ce_args(const Tensor *t, TTHeadCeArgs *a, void **job) {
+    for (TTLazyVal *l = g_lazy_vals; l; l = l->next) {
+        if (l->kind != 6 || l->t != t) continue;
+        TTCeJob *j = l->ce;
+        a->part = j->ws;
+        a->bias = j->bias;
+        a->labels = j->labels;
+        a->scale = j->scale;
+        a->logits = j->out[0] ? j->out[0]->dev : NULL;
+        a->probs = j->out[1] ? j->out[1]->dev : NULL;
+        a->seed = j->out[2] ? j->out[2]->dev : NULL;
+        a->rowloss = j->out[3] ? j->out[3]->dev : NULL;
+        *job = j;
+        return 0;
+    }
+    return -1;
+}
+
+void tt_lazy_ce_done(void *job) { ce_job_finish((TTCeJob *)job, 1); }
+
 /* unlink the entries of t (as the recipe's output, or every entry computed
  * from t when `from`), running their recipes unless `drop`; a recipe's run
  * may change the list, so the walk restarts after each */
@@ -358,6 +481,11 @@ restart:
         if (l->kind == 3) {
             if (drop) dwt_drop_entry(pp);
             else dwt_flush_all();
+            goto restart;
+        }
+        if (l->kind == 6) {
+            if (drop && !from) ce_drop_entry(pp);
+            else ce_job_run(l->ce);
             goto restart;
         }
         *pp = l->next;

@@ -103,6 +103,17 @@ int tt_lazy_gemm_tn_padones(Tensor *dw, Tensor *x, Tensor *g, int rows, int Kx, 
 /* as tt_lazy_dwt_sgd, for one pending tt_lazy_gemm_tn_padones gradient: the
  * GEMM (stepping its weights) and the other tensors' steps in one launch */
 int tt_lazy_gemm_sgd(float *const *w, Tensor *const *g, const long *n, int count, float lr);
+/* out = logits, probs, seed, row losses of a softmax-CE (allocated,
+ * unwritten): one ttk_reduce_ce of ws (2 x M x N partial sums, then owned by
+ * the recipe), the bias (the last row of the classifier weights w, which the
+ * recipe retains) and the labels (copied), run on the first use of any of
+ * them.  0 ok, -1 no memory (nothing registered) */
+int tt_lazy_ce_job(Tensor *const out[4], Tensor *w, float *ws, const float *bias,
+                   const int32_t *labels, int M, int N, float scale);
+/* t pending in such a job: its arguments for ttk_head_bwd_ce (*job set); -1
+ * otherwise.  tt_lazy_ce_done(job): a kernel wrote the job's outputs */
+int tt_lazy_ce_args(const Tensor *t, TTHeadCeArgs *a, void **job);
+void tt_lazy_ce_done(void *job);
 /* t is about to be changed in place: run the recipes that read it */
 void tt_lazy_before_write(Tensor *t);
 Tensor *tt_lazy_relu_src(const Tensor *t);  /* src while t is still unwritten */

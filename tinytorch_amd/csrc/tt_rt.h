@@ -56,6 +56,21 @@ typedef struct {
     float scale;
 } TTCeHook;
 int    ttk_reduce_ce(const float *ws, float *C, int M, int N, int S, int zl, const TTCeHook *h);
+/* head.hip: tt_k_head_bwd / tt_k_head_bwd_pool (codes non-NULL) whose
+ * output gradient is the seed of a softmax-CE of the logits formed by the
+ * kernel itself from two partial sums per logit (part: 2 x M x N), the bias
+ * and the labels -- the values splitk_reduce_ce would give -- and whose
+ * workgroup 0 also writes that reduction's outputs (logits, probs, seed,
+ * rowloss; each may be NULL).  -1: not covered (nothing launched). */
+typedef struct {
+    const float *part, *bias;
+    const int32_t *labels;
+    float scale;
+    float *logits, *probs, *seed, *rowloss;
+} TTHeadCeArgs;
+int    ttk_head_bwd_ce(const float *A, int M, int K, const float *W, int N, const TTHeadCeArgs *a,
+                       float *dW, float *dA, float *d1, float *d2, const float *R,
+                       const unsigned char *codes, float *dc, int F, int Ho2, int Wo2);
 /* conv.hip: a weight gradient whose tiled kernel ran but whose reduction is
  * still to run: the partial sums (owned), the outputs (dw, db; either may
  * be NULL: not written) and the reduction's shape */
