@@ -310,3 +310,49 @@ def test_conv_chain_bwd_matches_separate(tlib, N, C1):
     _, rdw, rdb = orc.conv2d_bwd(x, w1, gr, 1, 1, 1, 1, need_dx=False)
     assert np.abs(fw.to_np(w1.shape) - rdw).max() <= 1e-4 * max(1.0, np.abs(rdw).max())
     assert np.abs(fb.to_np((32,)) - rdb).max() <= 1e-4 * max(1.0, np.abs(rdb).max())
+
+
+@pytest.mark.parametrize("when", ["before", "never", "after"])
+def test_autograd_chain_softmax_ce_recipe(tlib, when):
+    """The config-4 graph with the chain's classifier partial sums: the
+    softmax-CE's outputs are formed by the classifier backward (when the
+    backward runs first) or by their own reduction on a first read before
+    it; read before, after, or never (the graph released unread, then a full
+    step run again), the loss, probabilities and gradients match the graph
+    without the chain to the fp32 bar and the oracle's loss."""
+    from tinytorch_amd.torch_py import Node
+    x, y, P = orc.cnn_inputs(B=128)
+    ref = orc.cnn_step(x, y, **P)
+
+    def run(chain, when):
+        prev = tlib.tth_conv_chain(1 if chain else 0)
+        keep = []
+        try:
+            logits = _cnn(Node, x, P, keep)
+            loss = logits.softmax_ce(y)
+            out = {}
+            if when == "before":
+                out["loss"] = loss.value()
+                out["probs"] = loss.probs()
+            if when != "never":
+                loss.backward(None)
+                out["dwfc"] = keep[5].grad()
+                out["dw2"] = keep[3].grad()
+                if when == "after":
+                    out["loss"] = loss.value()
+                    out["probs"] = loss.probs()
+            for nd in [loss] + keep[::-1]:
+                nd.release()
+            return out
+        finally:
+            tlib.tth_conv_chain(prev)
+
+    print("chain softmax-CE recipe, read", when, flush=True)
+    got = run(True, when)
+    if when == "never":
+        got = run(True, "after")  # the next step after a graph released unread
+    want = run(False, "after")
+    for k in got:
+        assert np.abs(got[k] - want[k]).max() <= 1e-4 * max(1e-30, np.abs(want[k]).max()), k
+    assert abs(float(got["loss"][0]) - ref["loss"]) <= 1e-4 * max(1.0, abs(ref["loss"]))
+    assert np.abs(got["probs"] - ref["probs"]).max() <= 1e-4
