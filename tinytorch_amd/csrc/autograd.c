@@ -971,10 +971,12 @@ static void conv_geo(const AGNode *c, int q[13]);
  * tt_k_conv2d_chain_fwd shape): its input gradient (the pool's gradient,
  * complete here: the pool feeds only this convolution) and, through the pool
  * codes, the first convolution's weight gradient in one launch
- * (ttk_conv2d_chain_bwd, its reduction deferred like conv_dw_deferred's).
- * The first convolution's rule then has nothing left to do (its input needs
- * no gradient; its own gradient stays the recipe the pool's rule leaves).
- * 0: not taken, nothing launched. */
+ * (ttk_conv2d_chain_bwd, its reduction deferred like conv_dw_deferred's),
+ * and in the same grid this convolution's own weight gradient.  The first
+ * convolution's rule then has nothing left to do (its input needs no
+ * gradient; its own gradient stays the recipe the pool's rule leaves).
+ * 0: not taken, nothing launched; 1: done without this convolution's weight
+ * gradient; 2: with it. */
 static int conv_chain_bwd(AGNode *n, const float *gd) {
     AGNode *p = n->in[0];
     if (!tt_chain_enabled() || !needs(p) || p->op != &OP_MAXPOOL2D || !p->at.win.codes ||
@@ -1001,21 +1003,52 @@ static int conv_chain_bwd(AGNode *n, const float *gd) {
     Tensor *ga = w2 && x && codes ? tt_empty_like(p->val) : NULL;
     Tensor *gw = ga ? tt_empty_like(w1->val) : NULL;
     Tensor *gb = gw && needs(b1) ? tt_empty_dev(bshp, 1) : NULL;
-    TTDwtJob job;
-    if (!gw || (needs(b1) && !gb) ||
-        ttk_conv2d_chain_bwd(gd, w2, codes, x, ga->dev, gw->dev, gb ? gb->dev : NULL, q1[0],
-                             q1[1], &job) != 0) {
+    if (!gw || (needs(b1) && !gb)) {
         tt_release(ga);
         tt_release(gw);
         tt_release(gb);
         return 0;
+    }
+    /* this convolution's own weight gradient (and bias) in the same grid,
+     * when its LDS path would compute it (the forward kept no col) */
+    AGNode *w2n = n->in[1], *b2n = n->n_in > 2 ? n->in[2] : NULL;
+    const long b2shp[1] = {64};
+    const float *x2 = needs(w2n) && !n->at.conv.col ? tt_dev(p->val) : NULL;
+    Tensor *gw2 = x2 ? tt_empty_like(w2n->val) : NULL;
+    Tensor *gb2 = gw2 && needs(b2n) ? tt_empty_dev(b2shp, 1) : NULL;
+    if (gw2 && needs(b2n) && !gb2) {
+        tt_release(gw2);
+        gw2 = NULL;
+    }
+    TTDwtJob job, job2;
+    int rc = gw2 ? ttk_conv2d_chain_bwd(gd, w2, codes, x, ga->dev, gw->dev, gb ? gb->dev : NULL,
+                                        q1[0], q1[1], &job, x2, gw2->dev, gb2 ? gb2->dev : NULL,
+                                        &job2)
+                 : -1;
+    if (rc != 0) {
+        tt_release(gw2);
+        tt_release(gb2);
+        gw2 = gb2 = NULL;
+        rc = ttk_conv2d_chain_bwd(gd, w2, codes, x, ga->dev, gw->dev, gb ? gb->dev : NULL, q1[0],
+                                  q1[1], &job, NULL, NULL, NULL, NULL);
+    }
+    if (rc != 0) {
+        tt_release(ga);
+        tt_release(gw);
+        tt_release(gb);
+        return 0;
+    }
+    if (gw2) {
+        if (tt_lazy_dwt(gw2, gb2, &job2) != 0) ttk_dwt_reduce_jobs(&job2, 1);
+        if (gb2) accum_move(b2n, gb2);
+        accum_move(w2n, gw2);
     }
     if (tt_lazy_dwt(gw, gb, &job) != 0) ttk_dwt_reduce_jobs(&job, 1);
     accum_move(p, ga);
     if (gb) accum_move(b1, gb);
     accum_move(w1, gw);
     c->fused = 1;
-    return 1;
+    return gw2 ? 2 : 1;
 }
 
 static void backward_conv2d(AGNode *n) {
@@ -1038,6 +1071,10 @@ static void backward_conv2d(AGNode *n) {
     const float *gd = tt_dev(n->grad);
     if (!gd) return;
 
+    /* the second convolution of a chain: its input gradient, the first
+     * convolution's weight gradient and, in the same launch, its own */
+    const int chained = conv_chain_bwd(n, gd);
+    if (chained == 2) return;
     const long bshp[1] = {F};
     const int lds = tt_k_conv2d_lds_plan(N, C, H, W, F, HH, WW, sh, sw, ph, pw, Ho, Wo);
     int w_done = 0;
@@ -1109,7 +1146,7 @@ static void backward_conv2d(AGNode *n) {
             if (own) ttrt_free(col);
         }
     }
-    if (conv_chain_bwd(n, gd)) return;
+    if (chained) return;
     if (needs(a) && (lds & 4)) {
         const float *wd = tt_dev(w->val);
         Tensor *ga = wd ? tt_empty_like(a->val) : NULL;

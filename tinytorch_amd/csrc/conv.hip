@@ -1176,15 +1176,18 @@ constexpr int DWT_UB = 8;   // pooled-gradient items a lane decodes per batch
 // relu backward would have written them (maxpool2x2_code_bwd_kernel), so
 // that gradient is never stored.  Needs even RC (or one unit per image),
 // even Ho and Wo % 8 == 0.
+// The workgroup (u, ts, fb) of nu units; every thread of a workgroup of
+// 64 * DWT_NPQ * NTGW calls it.
 template <int TG, int NTGW, bool CODE = false>
-__global__ void __launch_bounds__(64 * DWT_NPQ * NTGW)
-conv_dwt_kernel(const float *__restrict__ gr, const float *__restrict__ x,
-                float *__restrict__ part, Geo g, int RC, int nch, int GS, int CS, int jbp,
-                const unsigned char *__restrict__ codes) {
+__device__ __forceinline__ void conv_dwt_block(const float *__restrict__ gr,
+                                               const float *__restrict__ x,
+                                               float *__restrict__ part, const Geo &g, int RC,
+                                               int nch, int GS, int CS, int jbp,
+                                               const unsigned char *__restrict__ codes, int u,
+                                               int ts, int fb, int nu) {
   constexpr int NTH = 64 * DWT_NPQ * NTGW;
   constexpr int SLOT = TG * 1024 + 64;  // one wave's accumulators and bias in LDS
   extern __shared__ __attribute__((aligned(16))) float smem[];
-  const int u = blockIdx.x, ts = blockIdx.y, fb = blockIdx.z;
   const int n = u / nch, ho0 = (u - n * nch) * RC;
   const int rows = min(g.Ho, ho0 + RC) - ho0;
   const int P = g.Ho * g.Wo;
@@ -1378,13 +1381,22 @@ conv_dwt_kernel(const float *__restrict__ gr, const float *__restrict__ x,
     }
   }
   if (pq != 0) return;
-  float *pz = part + ((long)fb * gridDim.x + u) * ((long)jbp * 1024 + 32);
+  float *pz = part + ((long)fb * nu + u) * ((long)jbp * 1024 + 32);
   const int jb0 = (ts * NTGW + tgw) * TG;
 #pragma unroll
   for (int jw = 0; jw < TG; jw++)
 #pragma unroll
     for (int r = 0; r < 16; r++) pz[((jb0 + jw) * 16 + r) * 64 + lane] = acc[jw][r];
   if (ts == 0 && tgw == 0 && lane < 32) pz[jbp * 1024 + lane] = bsum;
+}
+
+template <int TG, int NTGW, bool CODE = false>
+__global__ void __launch_bounds__(64 * DWT_NPQ * NTGW)
+conv_dwt_kernel(const float *__restrict__ gr, const float *__restrict__ x,
+                float *__restrict__ part, Geo g, int RC, int nch, int GS, int CS, int jbp,
+                const unsigned char *__restrict__ codes) {
+  conv_dwt_block<TG, NTGW, CODE>(gr, x, part, g, RC, nch, GS, CS, jbp, codes, blockIdx.x,
+                                 blockIdx.y, blockIdx.z, gridDim.x);
 }
 
 // dW / db from the dwt partials: each lane owns 4 consecutive elements of a
@@ -2342,15 +2354,18 @@ static_assert((64 * CS2) % 256 == 0 && 2 * 2 * SLOT <= 64 * CS2, "dc2 slab");
 static_assert(LDS_FLOATS * 4 <= LDS_MAX, "LDS");
 }  // namespace chainb
 
-__global__ void __launch_bounds__(chainb::NTH)
-conv_chain_bwd_kernel(const float *__restrict__ dc2, const float *__restrict__ w2,
-                      const unsigned char *__restrict__ codes1, const float *__restrict__ x,
-                      float *__restrict__ dx2, float *__restrict__ part, int C1) {
+// Workgroup blk (image blk / 2, half blk % 2); the first 512 threads.
+__device__ __forceinline__ void conv_chain_bwd_block(const float *__restrict__ dc2,
+                                                     const float *__restrict__ w2,
+                                                     const unsigned char *__restrict__ codes1,
+                                                     const float *__restrict__ x,
+                                                     float *__restrict__ dx2,
+                                                     float *__restrict__ part, int C1, int blk) {
   using namespace chainb;
   extern __shared__ __attribute__((aligned(16))) float smem[];
   float *ws = smem + O_W, *ds = smem + O_D, *xs = smem + O_X;
   const unsigned char *c1t = (const unsigned char *)(smem + O_C);
-  const int n = blockIdx.x >> 1, hf = blockIdx.x & 1;
+  const int n = blk >> 1, hf = blk & 1;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, half = lane >> 5;
@@ -2540,6 +2555,35 @@ conv_chain_bwd_kernel(const float *__restrict__ dc2, const float *__restrict__ w
       if (lane < 32) pz[1024 + lane] = bsum;
     }
   }
+}
+
+__global__ void __launch_bounds__(chainb::NTH)
+conv_chain_bwd_kernel(const float *__restrict__ dc2, const float *__restrict__ w2,
+                      const unsigned char *__restrict__ codes1, const float *__restrict__ x,
+                      float *__restrict__ dx2, float *__restrict__ part, int C1) {
+  conv_chain_bwd_block(dc2, w2, codes1, x, dx2, part, C1, blockIdx.x);
+}
+
+// The same and the second convolution's weight gradient (conv_dwt_kernel<3,
+// 3>, independent of it) in one grid: workgroups [0, 2N) the chain's
+// backward middle, the rest the weight-gradient workgroups (unit, filter
+// block), so the second set starts on each CU as the first one leaves it --
+// no launch boundary between them.  768 threads (the weight gradient's 12
+// waves); the chain's workgroups use the first 512.
+__global__ void __launch_bounds__(64 * DWT_NPQ * 3)
+conv_chain_bwd_dw2_kernel(const float *__restrict__ dc2, const float *__restrict__ w2,
+                          const unsigned char *__restrict__ codes1, const float *__restrict__ x,
+                          float *__restrict__ dx2, float *__restrict__ part1, int C1,
+                          const float *__restrict__ x2, float *__restrict__ part2, Geo g2,
+                          int RC, int nch, int GS, int CS, int jbp, int nu2, int nchain) {
+  if ((int)blockIdx.x < nchain) {
+    if (threadIdx.x >= chainb::NTH) return;
+    conv_chain_bwd_block(dc2, w2, codes1, x, dx2, part1, C1, blockIdx.x);
+    return;
+  }
+  const int b = blockIdx.x - nchain;
+  conv_dwt_block<3, 3, false>(dc2, x2, part2, g2, RC, nch, GS, CS, jbp, nullptr, b % nu2, 0,
+                              b / nu2, nu2);
 }
 
 int g_lds_conv = 1;  // tth_conv_lds
@@ -2875,7 +2919,8 @@ extern "C" int tt_k_conv2d_chain_fwd(const float *x, const float *w1, const floa
 // same values).  -1: not covered (nothing launched); < -1: error.
 extern "C" int ttk_conv2d_chain_bwd(const float *dc2, const float *w2, const unsigned char *codes1,
                                     const float *x, float *dx2, float *dw1, float *db1, int N,
-                                    int C1, TTDwtJob *job) {
+                                    int C1, TTDwtJob *job, const float *x2, float *dw2,
+                                    float *db2, TTDwtJob *job2) {
   if (!dc2 || !w2 || !codes1 || !x || !dx2 || !dw1 || !job || !g_dwt || N <= 0 ||
       N > 16383 || C1 < 1 || C1 > 3)
     return -1;
@@ -2885,17 +2930,47 @@ extern "C" int ttk_conv2d_chain_bwd(const float *dc2, const float *w2, const uns
   const DwtPlan tp = plan_dwt(g1, N);
   if (tp.tg != 1 || tp.ntgw != 1 || tp.nts != 1 || tp.nfb != 1 || tp.rc != 8 || tp.jbp != 1)
     return -1;
+  // the second convolution's weight gradient in the same grid: its plan must
+  // be the 3 x 3 tap-group kernel over whole images
+  const Geo g2{32, 16, 16, 3, 3, 1, 1, 1, 1, 16, 16, 64, 288};
+  DwtPlan t2;
+  if (dw2) {
+    if (!x2 || !job2 || !aligned16(x2)) return -1;
+    t2 = plan_dwt(g2, N);
+    if (t2.tg != 3 || t2.ntgw != 3 || t2.nts != 1 || t2.lds > sizeof(float) * chainb::LDS_FLOATS)
+      return -1;
+  }
   if (fail_direct()) return -3;
   constexpr size_t lds = sizeof(float) * chainb::LDS_FLOATS;
-  if (!allow_big_lds((const void *)conv_chain_bwd_kernel)) return -1;
+  const void *kern = dw2 ? (const void *)conv_chain_bwd_dw2_kernel : (const void *)conv_chain_bwd_kernel;
+  if (!allow_big_lds(kern)) return -1;
   const long S = 1024 + 32;
   float *part = (float *)ttrt_alloc(sizeof(float) * (size_t)(S * tp.units));
   if (!part) return -2;
-  hipLaunchKernelGGL(conv_chain_bwd_kernel, dim3((unsigned)(2 * N)), dim3(chainb::NTH), lds,
-                     stream(), dc2, w2, codes1, x, dx2, part, C1);
+  float *part2 = nullptr;
+  const long S2 = dw2 ? (long)t2.jbp * 1024 + 32 : 0;
+  if (dw2 && !(part2 = (float *)ttrt_alloc(sizeof(float) * (size_t)(S2 * t2.units * t2.nfb)))) {
+    ttrt_free(part);
+    return -2;
+  }
+  if (dw2)
+    hipLaunchKernelGGL(conv_chain_bwd_dw2_kernel, dim3((unsigned)(2 * N + t2.units * t2.nfb)),
+                       dim3(64 * DWT_NPQ * 3), lds, stream(), dc2, w2, codes1, x, dx2, part, C1,
+                       x2, part2, g2, t2.rc, t2.nch, t2.gs, t2.cs, t2.jbp, t2.units, 2 * N);
+  else
+    hipLaunchKernelGGL(conv_chain_bwd_kernel, dim3((unsigned)(2 * N)), dim3(chainb::NTH), lds,
+                       stream(), dc2, w2, codes1, x, dx2, part, C1);
   if (hipGetLastError() != hipSuccess) {
     ttrt_free(part);
+    ttrt_free(part2);
     return -3;
+  }
+  if (dw2) {
+    const long cols2 = (long)t2.nfb * (S2 / 4);
+    int zl2 = 1;
+    while (zl2 < 64 && zl2 * 16 < t2.units) zl2 *= 2;
+    *job2 = TTDwtJob{part2, dw2, db2, t2.units, t2.nfb, t2.jbp, 64, 288, zl2,
+                     (int)((cols2 + NT / zl2 - 1) / (NT / zl2))};
   }
   const long cols = S / 4;
   int zl = 1;
@@ -2910,7 +2985,8 @@ extern "C" int tt_k_conv2d_chain_bwd(const float *dc2, const float *w2,
                                      const unsigned char *codes1, const float *x, float *dx2,
                                      float *dw1, float *db1, int N, int C1) {
   TTDwtJob job;
-  const int rc = ttk_conv2d_chain_bwd(dc2, w2, codes1, x, dx2, dw1, db1, N, C1, &job);
+  const int rc = ttk_conv2d_chain_bwd(dc2, w2, codes1, x, dx2, dw1, db1, N, C1, &job, nullptr,
+                                      nullptr, nullptr, nullptr);
   if (rc != 0) return rc;
   return ttk_dwt_reduce_jobs(&job, 1);
 }

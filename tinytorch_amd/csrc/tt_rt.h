@@ -87,10 +87,13 @@ int    ttk_conv2d_dwt_defer(const float *gr, const unsigned char *codes, const f
 /* conv.hip: the CNN chain's middle backward in one launch: dx2 = the input
  * gradient of the second convolution (tt_k_conv2d_dx_lds bits) and the first
  * convolution's weight gradient through the pool codes1 (the job
- * tt_k_conv2d_dw_lds_pooled would defer).  -1: not covered. */
+ * tt_k_conv2d_dw_lds_pooled would defer); with dw2 (db2 optional), the
+ * second convolution's weight gradient from dc2 and its input x2 in the same
+ * grid (the job tt_k_conv2d_dw_lds would defer, *job2).  -1: not covered. */
 int    ttk_conv2d_chain_bwd(const float *dc2, const float *w2, const unsigned char *codes1,
                             const float *x, float *dx2, float *dw1, float *db1, int N, int C1,
-                            TTDwtJob *job);
+                            TTDwtJob *job, const float *x2, float *dw2, float *db2,
+                            TTDwtJob *job2);
 /* conv.hip: the reductions of n jobs in one launch (the same values as
  * each job's own reduction), then their partials freed; 0 ok */
 int    ttk_dwt_reduce_jobs(const TTDwtJob *jobs, int n);
