@@ -411,9 +411,13 @@ int tt_k_conv2d_chain_fwd(const float *x, const float *w1, const float *b1, cons
  * pool + relu backward of the pool codes codes1 (src/autograd.c:555-594,
  * :318-327), dw1 / db1 of the first convolution (x N x C1 x 32 x 32, C1 <=
  * 3, 32 filters, 3x3, pad 1; src/autograd.c:456-513), bit for bit
- * tt_k_conv2d_dw_lds_pooled of dx2.  -1: not covered (nothing launched). */
+ * tt_k_conv2d_dw_lds_pooled of dx2; with dw2 (db2 optional), in the same
+ * grid, the second convolution's weight gradient from dc2 and its input x2
+ * (N x 32 x 16 x 16), bit for bit tt_k_conv2d_dw_lds.  -1: not covered
+ * (nothing launched). */
 int tt_k_conv2d_chain_bwd(const float *dc2, const float *w2, const unsigned char *codes1,
-                          const float *x, float *dx2, float *dw1, float *db1, int N, int C1);
+                          const float *x, float *dx2, float *dw1, float *db1, const float *x2,
+                          float *dw2, float *db2, int N, int C1);
 int tt_k_conv2d_dw_lds(const float *g, const float *x, float *dw, float *db,
                        int N, int C, int H, int W, int F, int HH, int WW,
                        int sh, int sw, int ph, int pw, int Ho, int Wo);

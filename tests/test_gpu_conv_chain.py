@@ -291,7 +291,7 @@ def test_conv_chain_bwd_matches_separate(tlib, N, C1):
     # one launch
     fx, fw, fb = DevBuf(N * 32 * 256), DevBuf(w1.size), DevBuf(32)
     rc = tlib.tt_k_conv2d_chain_bwd(dg.ptr, dw2_.ptr, codes.ptr, dx.ptr, fx.ptr, fw.ptr, fb.ptr,
-                                    N, C1)
+                                    None, None, None, N, C1)
     if not 128 <= N < 256:
         assert rc == -1
         return
@@ -299,6 +299,19 @@ def test_conv_chain_bwd_matches_separate(tlib, N, C1):
     assert bits_equal(fx.to_np((N, 32, 16, 16)), ex.to_np((N, 32, 16, 16)))
     assert bits_equal(fw.to_np(w1.shape), ew.to_np(w1.shape))
     assert bits_equal(fb.to_np((32,)), eb.to_np((32,)))
+    # with the second convolution's weight gradient in the same grid: bit for
+    # bit tt_k_conv2d_dw_lds of dc2 and the pool (its input)
+    p1 = DevBuf.from_np(orc.maxpool_fwd(rv, 2, 2, 2, 2))
+    e2w, e2b = DevBuf(w2.size), DevBuf(64)
+    check(tlib.tt_k_conv2d_dw_lds(dg.ptr, p1.ptr, e2w.ptr, e2b.ptr, *geo(N, 32, 16, 64)), "dw2")
+    gx, gw, gb, g2w, g2b = DevBuf(N * 32 * 256), DevBuf(w1.size), DevBuf(32), DevBuf(w2.size), DevBuf(64)
+    check(tlib.tt_k_conv2d_chain_bwd(dg.ptr, dw2_.ptr, codes.ptr, dx.ptr, gx.ptr, gw.ptr, gb.ptr,
+                                     p1.ptr, g2w.ptr, g2b.ptr, N, C1), "chain bwd + dw2")
+    assert bits_equal(gx.to_np((N, 32, 16, 16)), ex.to_np((N, 32, 16, 16)))
+    assert bits_equal(gw.to_np(w1.shape), ew.to_np(w1.shape))
+    assert bits_equal(gb.to_np((32,)), eb.to_np((32,)))
+    assert bits_equal(g2w.to_np(w2.shape), e2w.to_np(w2.shape))
+    assert bits_equal(g2b.to_np((64,)), e2b.to_np((64,)))
     if N != 130:
         return
     # oracle: dx2, then the pool + relu backward and conv1's dw / db

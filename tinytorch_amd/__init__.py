@@ -177,7 +177,7 @@ SIGNATURES = [
     ("tt_k_conv2d_relu_pool_fwd_lds", _I, [VP] * 9 + [_I] * 13),
     ("tt_k_conv2d_dw_lds", _I, [VP, VP, VP, VP] + [_I] * 13),
     ("tt_k_conv2d_chain_fwd", _I, [VP] * 14 + [_I] + [VP] + [_I] * 6),
-    ("tt_k_conv2d_chain_bwd", _I, [VP] * 7 + [_I] * 2),
+    ("tt_k_conv2d_chain_bwd", _I, [VP] * 10 + [_I] * 2),
     ("tt_k_conv2d_dw_lds_pooled", _I, [VP] * 5 + [_I] * 13),
     ("tt_k_conv2d_dx_lds", _I, [VP, VP, VP] + [_I] * 13),
     ("tt_k_gather_u8_norm", _I, [VP, _L, _L, _L, _I, VP, _L, F32P, F32P, VP]),

@@ -2980,13 +2980,15 @@ extern "C" int ttk_conv2d_chain_bwd(const float *dc2, const float *w2, const uns
   return 0;
 }
 
-// ttk_conv2d_chain_bwd with the reduction run at once: dw1 / db1 written.
+// ttk_conv2d_chain_bwd with the reductions run at once: dw1 / db1 (and dw2 /
+// db2) written.
 extern "C" int tt_k_conv2d_chain_bwd(const float *dc2, const float *w2,
                                      const unsigned char *codes1, const float *x, float *dx2,
-                                     float *dw1, float *db1, int N, int C1) {
-  TTDwtJob job;
-  const int rc = ttk_conv2d_chain_bwd(dc2, w2, codes1, x, dx2, dw1, db1, N, C1, &job, nullptr,
-                                      nullptr, nullptr, nullptr);
+                                     float *dw1, float *db1, const float *x2, float *dw2,
+                                     float *db2, int N, int C1) {
+  TTDwtJob job[2];
+  const int rc = ttk_conv2d_chain_bwd(dc2, w2, codes1, x, dx2, dw1, db1, N, C1, &job[0], x2, dw2,
+                                      db2, &job[1]);
   if (rc != 0) return rc;
-  return ttk_dwt_reduce_jobs(&job, 1);
+  return ttk_dwt_reduce_jobs(job, dw2 ? 2 : 1);
 }
