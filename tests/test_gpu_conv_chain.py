@@ -369,3 +369,38 @@ def test_autograd_chain_softmax_ce_recipe(tlib, when):
         assert np.abs(got[k] - want[k]).max() <= 1e-4 * max(1e-30, np.abs(want[k]).max()), k
     assert abs(float(got["loss"][0]) - ref["loss"]) <= 1e-4 * max(1.0, abs(ref["loss"]))
     assert np.abs(got["probs"] - ref["probs"]).max() <= 1e-4
+
+
+def test_autograd_chain_ce_in_head_bitexact(tlib):
+    """The softmax-CE the classifier backward forms itself (two lanes a row,
+    ce_row_pair) gives the bits the reduction kernel (ce_row, one lane a row)
+    gives: the loss, probabilities and every gradient with the recipe read
+    before the backward (the reduction runs) and after it (the head forms
+    them) are equal bit for bit."""
+    from tinytorch_amd.torch_py import Node
+    x, y, P = orc.cnn_inputs(B=128)
+    y = y.copy()
+    y[::17] = 12  # labels outside [0, 10): the loss of ce_row's rule
+
+    def run(read_first):
+        keep = []
+        logits = _cnn(Node, x, P, keep)
+        loss = logits.softmax_ce(y)
+        out = {}
+        if read_first:
+            out["probs"] = loss.probs()
+        loss.backward(None)
+        out["loss"] = loss.value()
+        out["probs2"] = loss.probs()
+        out["logits"] = logits.value()
+        for k, i in (("dwfc", 5), ("dw2", 3), ("db2", 4), ("dw1", 1), ("db1", 2)):
+            out[k] = keep[i].grad()
+        for nd in [loss] + keep[::-1]:
+            nd.release()
+        return out
+
+    print("chain CE in head vs reduction", flush=True)
+    a, b = run(True), run(False)
+    for k in b:
+        assert bits_equal(a[k], b[k]), k
+    assert bits_equal(a["probs"], b["probs2"])

@@ -59,6 +59,66 @@ __device__ __forceinline__ float ce_row(const float *__restrict__ xr, int y,
   return -logf(fmaxf(py, 1e-12f));
 }
 
+// ce_row by a pair of lanes (this lane and lane ^ 1, both active): lane
+// half q = lane & 1 takes columns [j0, j1) = [q h, q ? cols : h), h = (cols +
+// 1) / 2, whose logits it holds in vh[0 .. j1 - j0); pr / sr get those
+// columns.  The same operations in the same order as ce_row -- the maximum
+// (order-free), each expf, the sum of the exponentials in column order (the
+// upper lane continues the lower lane's running sum), each division -- so
+// the same bits; returns the row's loss in both lanes.
+template <int HC>
+__device__ __forceinline__ float ce_row_pair(float (&vh)[HC], int y, float (&pr)[HC],
+                                             float (&sr)[HC], int cols, float scale) {
+  const int q = threadIdx.x & 1, h = (cols + 1) / 2;
+  const int j0 = q * h, nh = (q ? cols : h) - j0;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < HC; i++) if (i < nh && vh[i] > mx) mx = vh[i];
+  const float om = __shfl_xor(mx, 1, 64);
+  if (om > mx) mx = om;
+  if (mx == -INFINITY) {
+#pragma unroll
+    for (int i = 0; i < HC; i++) vh[i] = 1.0f / (float)cols;
+  } else {
+#pragma unroll
+    for (int i = 0; i < HC; i++)
+      if (i < nh) vh[i] = expf(vh[i] - mx);
+    float sum = 0.0f;
+    if (q == 0) {
+#pragma unroll
+      for (int i = 0; i < HC; i++)
+        if (i < nh) sum += vh[i];
+    }
+    const float s0 = __shfl_xor(sum, 1, 64);  // the upper lane continues the lower's sum
+    if (q == 1) {
+      sum = s0;
+#pragma unroll
+      for (int i = 0; i < HC; i++)
+        if (i < nh) sum += vh[i];
+    }
+    const float s1 = __shfl_xor(sum, 1, 64);
+    if (q == 0) sum = s1;
+#pragma unroll
+    for (int i = 0; i < HC; i++) vh[i] = vh[i] / sum;
+  }
+  float py = 0.0f;
+  int own = 0;
+#pragma unroll
+  for (int i = 0; i < HC; i++)
+    if (i < nh) {
+      const int j = j0 + i;
+      pr[i] = vh[i];
+      sr[i] = (vh[i] - (j == y ? 1.0f : 0.0f)) * scale;
+      if (j == y) { py = vh[i]; own = 1; }
+    }
+  // the loss from the lane holding the label's column (neither, for a label
+  // outside [0, cols): -log(1e-12), as ce_row)
+  const float l = -logf(fmaxf(py, 1e-12f));
+  const float lo = __shfl_xor(l, 1, 64);
+  const int oo = __shfl_xor(own, 1, 64);
+  return own || !oo ? l : lo;
+}
+
 // loss_mean[0] = (sum of the 256 per-thread sums acc, added through `part`
 // (256 floats of LDS) in a fixed tree) / rows.  Every thread of the
 // workgroup calls it; threads 256 and up only take part in the barriers.

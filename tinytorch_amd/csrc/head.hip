@@ -125,7 +125,7 @@ __device__ __forceinline__ void head_dw_block(const float *__restrict__ A, int M
     // outputs), then the block's columns of it
     float va[32];
     stage_load<KW, 32>(va, A + k0, K, 0, M, min(KW, K - k0));
-    head_ce_seed<NC>(ce, 0, M, M, N, gl, N, blockIdx.x == 0);
+    head_ce_seed<NC>(ce, 0, M, M, N, gl, N, blockIdx.x == 0, gl + M * N);
     stage_store<KW, 32>(va, As, KW, 0, M);
     __syncthreads();
     for (int i = tid; i < M * JW; i += NT) {
@@ -160,36 +160,54 @@ __device__ __forceinline__ void head_dw_block(const float *__restrict__ A, int M
 constexpr int DA_M = 32;  // rows m per dA workgroup (8 per lane)
 // The output gradient of the classifier for rows [r0, r1) from the partial
 // sums of its logits (see above) into gl (row r at gl[(r - r0) * gs]); `out`:
-// also store the softmax-CE's outputs of those rows.  No barrier.
+// also store the softmax-CE's outputs of those rows.  The rows' partial sums
+// are first loaded whole-workgroup (coalesced) into pp (2 (r1 - r0) N floats
+// of LDS); one thread a row then forms its softmax-CE.  Every thread calls
+// it (barriers inside).
 template <int NC>
 __device__ __forceinline__ void head_ce_seed(const TTHeadCe &ce, int r0, int r1, int M, int N,
-                                             float *gl, int gs, bool out) {
-  for (int r = r0 + (int)threadIdx.x; r < r1; r += NT) {
-    const long total = (long)M * N;
-    float lv[NC], pr[NC], sr[NC];
+                                             float *gl, int gs, bool out, float *pp) {
+  const int n = (r1 - r0) * N;
+  const long total = (long)M * N;
+  for (int i = threadIdx.x; i < n; i += NT) {
+    pp[i] = ce.part[(long)r0 * N + i];
+    pp[n + i] = ce.part[total + (long)r0 * N + i];
+  }
+  __syncthreads();
+  // two lanes a row (ce_row_pair): lane half q takes columns [j0, j0 + nh)
+  constexpr int HC = (NC + 1) / 2;
+  const int q = threadIdx.x & 1, h = (N + 1) / 2;
+  const int j0 = q * h, nh = (q ? N : h) - j0;
+  for (int r = r0 + (int)(threadIdx.x >> 1); r < r1; r += NT / 2) {
+    float lv[HC], pr[HC], sr[HC];
+    const float *p0 = pp + (r - r0) * N + j0;
 #pragma unroll
-    for (int j = 0; j < NC; j++) {
-      lv[j] = 0.0f;
-      if (j < N) {
+    for (int i = 0; i < HC; i++) {
+      lv[i] = 0.0f;
+      if (i < nh) {
         float s = 0.0f;
-        s += ce.part[(long)r * N + j];
-        s += ce.part[total + (long)r * N + j];
-        lv[j] = s + ce.bias[j];
+        s += p0[i];
+        s += p0[n + i];
+        lv[i] = s + ce.bias[j0 + i];
       }
     }
-    const float loss = ce_row<NC>(lv, ce.lab[r], pr, sr, N, ce.scale);
+    float lg[HC];
 #pragma unroll
-    for (int j = 0; j < NC; j++)
-      if (j < N) gl[(r - r0) * gs + j] = sr[j];
+    for (int i = 0; i < HC; i++) lg[i] = lv[i];
+    const float loss = ce_row_pair<HC>(lv, ce.lab[r], pr, sr, N, ce.scale);
+#pragma unroll
+    for (int i = 0; i < HC; i++)
+      if (i < nh) gl[(r - r0) * gs + j0 + i] = sr[i];
     if (out) {
 #pragma unroll
-      for (int j = 0; j < NC; j++)
-        if (j < N) {
-          if (ce.logits) ce.logits[(long)r * N + j] = lv[j];
-          if (ce.probs) ce.probs[(long)r * N + j] = pr[j];
-          if (ce.seed) ce.seed[(long)r * N + j] = sr[j];
+      for (int i = 0; i < HC; i++)
+        if (i < nh) {
+          const long o = (long)r * N + j0 + i;
+          if (ce.logits) ce.logits[o] = lg[i];
+          if (ce.probs) ce.probs[o] = pr[i];
+          if (ce.seed) ce.seed[o] = sr[i];
         }
-      if (ce.rowloss) ce.rowloss[r] = loss;
+      if (ce.rowloss && q == 0) ce.rowloss[r] = loss;
     }
   }
 }
@@ -226,7 +244,8 @@ head_bwd_kernel(const float *__restrict__ A, int M, int K, const float *__restri
       // the block's rows of the seed, formed here while W is in flight (the
       // first column block stores their softmax-CE outputs when no dW
       // workgroup does)
-      head_ce_seed<NC>(ce, m0, min(m0 + DA_M, M), M, N, Gs, NC, nbw == 0 && blk % nkb == 0);
+      head_ce_seed<NC>(ce, m0, min(m0 + DA_M, M), M, N, Gs, NC, nbw == 0 && blk % nkb == 0,
+                       lds + gl_off);
       stage_store<NC, UW>(vw, Ws, NC, 0, 64);
     } else {
       stage_load<NC, UG>(vg, G + (long)m0 * N, N, 0, min(DA_M, M - m0), N);
@@ -310,7 +329,7 @@ static int head_bwd(const float *A, int M, int K, const float *W, int N, const f
   if (ce && dW && M > 32 * (NT / KW)) return -1;  // one batch of A rows (head_dw_block)
   size_t lds = lds_w > lds_a ? lds_w : lds_a;
   const int gl_off = (int)(lds / sizeof(float));
-  if (ce) lds += sizeof(float) * (size_t)M * N;  // the output gradient formed in LDS
+  if (ce) lds += sizeof(float) * (size_t)3 * M * N;  // the output gradient and partials in LDS
   if (lds > 64 * 1024) return -1;
   const TTHeadCe none{};
   const TTHeadCe &hc = ce ? *ce : none;
