@@ -1169,6 +1169,7 @@ conv_dw32_reduce_kernel(const float *__restrict__ part, float *__restrict__ dw,
 // on the VALU from the same A operands (first group of the first tap set).
 constexpr int DWT_NPQ = 4;  // waves sharing a tap group (pixel quarters)
 constexpr int DWT_UB = 8;   // pooled-gradient items a lane decodes per batch
+constexpr int DWT_UPL = 16;  // units of partials a reduction lane adds (at most; 4, 8 slower)
 
 // CODE: gr is the gradient of a 2x2 / stride-2 max pool of the relu of this
 // convolution's output (N x F x Ho/2 x Wo/2) and codes its windows' codes
@@ -1909,7 +1910,7 @@ int launch_dwt(const float *gr, const float *x, float *dw, float *db, const Geo 
     const long cols = (long)pl.nfb * (S / 4);
     // lanes per element: about 16 units each
     int zl = 1;
-    while (zl < 64 && zl * 16 < pl.units) zl *= 2;
+    while (zl < 64 && zl * DWT_UPL < pl.units) zl *= 2;
     if (defer) {
       *defer = TTDwtJob{part, dw, db, pl.units, pl.nfb, pl.jbp, g.F, g.K, zl,
                         (int)((cols + NT / zl - 1) / (NT / zl))};
@@ -2968,13 +2969,13 @@ extern "C" int ttk_conv2d_chain_bwd(const float *dc2, const float *w2, const uns
   if (dw2) {
     const long cols2 = (long)t2.nfb * (S2 / 4);
     int zl2 = 1;
-    while (zl2 < 64 && zl2 * 16 < t2.units) zl2 *= 2;
+    while (zl2 < 64 && zl2 * DWT_UPL < t2.units) zl2 *= 2;
     *job2 = TTDwtJob{part2, dw2, db2, t2.units, t2.nfb, t2.jbp, 64, 288, zl2,
                      (int)((cols2 + NT / zl2 - 1) / (NT / zl2))};
   }
   const long cols = S / 4;
   int zl = 1;
-  while (zl < 64 && zl * 16 < tp.units) zl *= 2;
+  while (zl < 64 && zl * DWT_UPL < tp.units) zl *= 2;
   *job = TTDwtJob{part, dw1, db1, tp.units, 1, 1, 32, C1 * 9, zl,
                   (int)((cols + NT / zl - 1) / (NT / zl))};
   return 0;
