@@ -1183,7 +1183,7 @@ template <int TG, int NTGW, bool CODE = false>
 __device__ __forceinline__ void conv_dwt_block(const float *__restrict__ gr,
                                                const float *__restrict__ x,
                                                float *__restrict__ part, const Geo &g, int RC,
-                                               int nch, int GS, int CS, int jbp,
+                                               int nch, int GS, int CS, int RW, int jbp,
                                                const unsigned char *__restrict__ codes, int u,
                                                int ts, int fb, int nu) {
   constexpr int NTH = 64 * DWT_NPQ * NTGW;
@@ -1199,7 +1199,7 @@ __device__ __forceinline__ void conv_dwt_block(const float *__restrict__ gr,
   const int c0 = kts / taps;
   const int c1 = min(g.C, (min(g.K, kts + NTGW * TG * 32) + taps - 1) / taps);
   const int nc = c1 - c0;
-  const int G = gslab_gap(g), RW = g.W + G;
+  const int G = RW - g.W;  // zeros before each row's W floats (rows of RW)
   const int R = (rows - 1) * g.sh + g.HH;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1214,14 +1214,25 @@ __device__ __forceinline__ void conv_dwt_block(const float *__restrict__ gr,
     const int T = (nc + 1) * CS;
     const float rcpC = 1.0f / (float)CS, rcpR = 1.0f / (float)RW;
     const float *xn = x + ((long)n * g.C + c0) * g.H * g.W;
-    for (int base = wave * 256; base < T; base += NTH * 4) {
-      const int i = base + lane * 4;
-      const int c = fdiv(i, CS, rcpC), rem = i - c * CS;
-      const int slot = fdiv(rem, RW, rcpR), j = rem - slot * RW;
-      const int row = hs + slot;
-      const bool ok = i < T && c < nc && slot < R && j >= G && row >= 0 && row < g.H;
-      dma_dwordx4(ok ? xn + ((long)c * g.H + row) * g.W + (j - G) : g_zero_src,
-                  xs + base);
+    if (((RW | CS | G) & 3) == 0) {  // whole 16-byte runs
+      for (int base = wave * 256; base < T; base += NTH * 4) {
+        const int i = base + lane * 4;
+        const int c = fdiv(i, CS, rcpC), rem = i - c * CS;
+        const int slot = fdiv(rem, RW, rcpR), j = rem - slot * RW;
+        const int row = hs + slot;
+        const bool ok = i < T && c < nc && slot < R && j >= G && row >= 0 && row < g.H;
+        dma_dwordx4(ok ? xn + ((long)c * g.H + row) * g.W + (j - G) : g_zero_src,
+                    xs + base);
+      }
+    } else {  // a layout of odd strides: element by element
+      for (int base = wave * 64; base < T; base += NTH) {
+        const int i = base + lane;
+        const int c = fdiv(i, CS, rcpC), rem = i - c * CS;
+        const int slot = fdiv(rem, RW, rcpR), j = rem - slot * RW;
+        const int row = hs + slot;
+        const bool ok = i < T && c < nc && slot < R && j >= G && row >= 0 && row < g.H;
+        dma_dword(ok ? xn + ((long)c * g.H + row) * g.W + (j - G) : g_zero_src, xs + base);
+      }
     }
   }
   // stage g rows (32 x GS) -- after the slab's DMA is issued, so a decode
@@ -1394,9 +1405,9 @@ __device__ __forceinline__ void conv_dwt_block(const float *__restrict__ gr,
 template <int TG, int NTGW, bool CODE = false>
 __global__ void __launch_bounds__(64 * DWT_NPQ * NTGW)
 conv_dwt_kernel(const float *__restrict__ gr, const float *__restrict__ x,
-                float *__restrict__ part, Geo g, int RC, int nch, int GS, int CS, int jbp,
-                const unsigned char *__restrict__ codes) {
-  conv_dwt_block<TG, NTGW, CODE>(gr, x, part, g, RC, nch, GS, CS, jbp, codes, blockIdx.x,
+                float *__restrict__ part, Geo g, int RC, int nch, int GS, int CS, int RW,
+                int jbp, const unsigned char *__restrict__ codes) {
+  conv_dwt_block<TG, NTGW, CODE>(gr, x, part, g, RC, nch, GS, CS, RW, jbp, codes, blockIdx.x,
                                  blockIdx.y, blockIdx.z, gridDim.x);
 }
 
@@ -1815,33 +1826,81 @@ int g_dwt = 1;  // tiled weight gradient enabled (tth_conv_dwt)
 
 // ---- dwt planning ----
 struct DwtPlan {
-  int tg = 0, ntgw = 0, nts = 0, nfb = 0, rc = 0, nch = 0, units = 0, gs = 0, cs = 0, jbp = 0;
+  int tg = 0, ntgw = 0, nts = 0, nfb = 0, rc = 0, nch = 0, units = 0, gs = 0, cs = 0, rw = 0,
+      jbp = 0;
   size_t lds = 0;
 };
 
-// Channel stride of the dwt slab: R rows of gslab_rw floats plus a pad (a
-// multiple of 4 below 32) chosen so that the 32 taps of an MFMA operand read
-// fall on as few shared banks as possible (32 banks of 4 bytes).
-int dwt_channel_stride(const Geo &g, int R, int TG) {
-  const int RW = gslab_rw(g), taps = g.HH * g.WW;
-  int best = R * RW, best_worst = 1 << 30;
-  for (int pad = 0; pad < 32; pad += 4) {
-    const int cs = R * RW + pad;
-    int worst = 0;
-    for (int jb = 0; jb < (g.K + 31) / 32 && jb < 64; jb++) {
-      const int k0 = (jb / TG) * TG * 32, c0 = k0 / taps;
-      int cnt[32] = {0};
-      for (int l = 0; l < 32; l++) {
-        const int k = jb * 32 + l;
-        if (k >= g.K) break;
-        const int c = k / taps - c0, t = k % taps, kh = t / g.WW, kw = t % g.WW;
-        const int b = ((c * cs + kh * RW + kw) % 32 + 32) % 32;
-        if (++cnt[b] > worst) worst = cnt[b];
+// Layout of the dwt slab: rows of rw floats (the row's W floats behind rw - W
+// zeros, at least the padding and the widest tap's overhang), channels cs
+// floats apart, chosen so that the 32 taps of an MFMA operand read fall on
+// as few shared banks as possible (32 banks of 4 bytes, a half-wave at a
+// time) among the layouts 16-byte loads can stage (rows, gap and channel
+// stride multiples of 4); only if none exists, element-by-element staging.
+// With 3x3 taps a conflict-free layout exists only with rows of 3 mod 32
+// floats (a channel's 9 taps on 9 consecutive banks) and channels 9-11 or
+// 21-23 mod 32 apart, which 16-byte loads cannot fill: the best staged by
+// them reads 2-way.
+void dwt_layout_search(const Geo &g, int R, int TG, int &rw_out, int &cs_out) {
+  const int taps = g.HH * g.WW;
+  const int ro = (g.Wo - 1) * g.sw - g.pw + g.WW - g.W;  // right overhang
+  int need = g.pw > ro ? g.pw : ro;
+  if (need < 1) need = 1;
+  long best_key = 1L << 50;
+  for (int rw = g.W + need; rw < g.W + need + 32; rw++) {
+    for (int pad = 0; pad < 32; pad++) {
+      const int cs = R * rw + pad;
+      const bool vec = ((rw | cs | (rw - g.W)) & 3) == 0;
+      int worst = 0;
+      for (int jb = 0; jb < (g.K + 31) / 32 && jb < 64; jb++) {
+        const int k0 = (jb / TG) * TG * 32, c0 = k0 / taps;
+        int cnt[32] = {0};
+        for (int l = 0; l < 32; l++) {
+          const int k = jb * 32 + l;
+          if (k >= g.K) break;
+          const int c = k / taps - c0, t = k % taps, kh = t / g.WW, kw = t % g.WW;
+          const int b = ((c * cs + kh * rw + kw) % 32 + 32) % 32;
+          if (++cnt[b] > worst) worst = cnt[b];
+        }
+      }
+      // 16-byte staging first (element-by-element staging measured slower
+      // than the 2-way conflicts it removes: conv2's weight gradient 17 ->
+      // 23 us), then the fewest conflicts, then the smaller slab
+      const long key = (vec ? 0 : (1L << 40)) + ((long)worst << 32) + cs;
+      if (key < best_key) {
+        best_key = key;
+        rw_out = rw;
+        cs_out = cs;
       }
     }
-    if (worst < best_worst) { best_worst = worst; best = cs; }
   }
-  return best;
+}
+
+// dwt_layout_search, remembered per geometry (the plan is made on every
+// backward pass; the search takes about a millisecond)
+void dwt_layout(const Geo &g, int R, int TG, int &rw, int &cs) {
+  struct Entry {
+    int key[10], rw, cs;
+  };
+  static Entry cache[32];
+  static int n = 0, next = 0;  // entries held, the one to replace next
+  const int key[10] = {g.W, g.Wo, g.WW, g.HH, g.sw, g.pw, g.K, g.C, R, TG};
+  for (int i = 0; i < n; i++) {
+    bool same = true;
+    for (int k = 0; k < 10; k++) same &= cache[i].key[k] == key[k];
+    if (same) {
+      rw = cache[i].rw;
+      cs = cache[i].cs;
+      return;
+    }
+  }
+  dwt_layout_search(g, R, TG, rw, cs);
+  Entry &e = cache[next];
+  next = (next + 1) % 32;
+  if (n < 32) n++;
+  for (int k = 0; k < 10; k++) e.key[k] = key[k];
+  e.rw = rw;
+  e.cs = cs;
 }
 
 // The tiled weight gradient covers 16-byte staged (W % 4 == 0) convolutions
@@ -1863,7 +1922,8 @@ DwtPlan plan_dwt(const Geo &g, int N) {
   const long red = 4L * ntgw * (DWT_NPQ / 2) * (TG * 1024 + 64);
   for (int rc = g.Ho;; rc = (rc + 1) / 2) {
     const int R = (rc - 1) * g.sh + g.HH;
-    const int cs = dwt_channel_stride(g, R, TG);
+    int rw = 0, cs = 0;
+    dwt_layout(g, R, TG, rw, cs);
     const int gs = ((rc * g.Wo + 31) & ~31) + 4;
     const long stage = 4L * (round_up(32 * gs, 256) + round_up((ncmax + 1) * cs, 256));
     const long lds = stage > red ? stage : red;
@@ -1883,6 +1943,7 @@ DwtPlan plan_dwt(const Geo &g, int N) {
     pl.units = N * nch;
     pl.gs = gs;
     pl.cs = cs;
+    pl.rw = rw;
     pl.jbp = nts * ntgw * TG;
     pl.lds = (size_t)lds;
     return pl;
@@ -1904,7 +1965,7 @@ int launch_dwt(const float *gr, const float *x, float *dw, float *db, const Geo 
   if (!part) return -2;
   hipLaunchKernelGGL(kern, dim3((unsigned)pl.units, (unsigned)pl.nts, (unsigned)pl.nfb),
                      dim3(64 * DWT_NPQ * NTGW), pl.lds, stream(), gr, x, part, g, pl.rc, pl.nch,
-                     pl.gs, pl.cs, pl.jbp, codes);
+                     pl.gs, pl.cs, pl.rw, pl.jbp, codes);
   int rc = hipGetLastError() == hipSuccess ? 0 : -3;
   if (rc == 0) {
     const long cols = (long)pl.nfb * (S / 4);
@@ -2287,7 +2348,8 @@ conv_chain_fwd_kernel(const float *__restrict__ x, const float *__restrict__ w1,
       // (the flattened pool2 row times the weights' rows, the bias left to
       // the reduction): fused multiply-adds over the thread's 4 features,
       // then the 512 threads' pieces of class j added in a fixed order --
-      // 32 threads a class, 16 pieces each in thread order, then a tree
+      // 32 threads a class, thread l the pieces l, l + 32, ... in order (on
+      // 32 banks), then a tree
       float *red = ws2;  // the second filter bank is no longer read
 #pragma unroll
       for (int j = 0; j < FCN; j++) {
@@ -2302,7 +2364,7 @@ conv_chain_fwd_kernel(const float *__restrict__ x, const float *__restrict__ w1,
       float a = 0.0f;
       if (j < FCN) {
 #pragma unroll
-        for (int i = 0; i < 16; i++) a += red[j * NTH + l * 16 + i];
+        for (int i = 0; i < 16; i++) a += red[j * NTH + i * 32 + l];
       }
 #pragma unroll
       for (int m = 16; m >= 1; m >>= 1) a += __shfl_xor(a, m, 32);
@@ -2340,7 +2402,11 @@ conv_chain_fwd_kernel(const float *__restrict__ x, const float *__restrict__ w1,
 namespace chainb {
 constexpr int NTH = 512;
 constexpr int G2 = 8, RS2 = 16 + G2, R2 = 10, CS2 = R2 * RS2 + 4;   // dc2 slab
-constexpr int GX = 4, RWX = 32 + GX, RX = 18, CSX = RX * RWX + 4;   // image slab
+// image slab: rows of 35 floats (3 zeros, 32 values), channels 630 floats
+// apart: the 27 taps of a weight-gradient operand read on 27 different banks
+// (a channel's 9 taps on 9 consecutive banks, channels 22 mod 32 apart);
+// staged element by element
+constexpr int GX = 3, RWX = 32 + GX, RX = 18, CSX = RX * RWX;
 constexpr int GS = 260;                  // g1 tile: per filter, 8 rows x 32 + 4
 constexpr int SLOT = 1024 + 64;          // one wave's dW accumulators and bias sum
 constexpr int O_W = 0;                   // filter bank 2, then the g1 tiles of both units
@@ -2350,7 +2416,7 @@ constexpr int O_X = O_D + 64 * CS2;      // image slab (4 planes)
 constexpr int X_SZ = 2816;
 constexpr int O_C = O_X + X_SZ;          // pool codes, 32 x 128 bytes
 constexpr int LDS_FLOATS = O_C + 1024;
-static_assert(2 * 32 * GS <= W_SZ && 4 * CSX <= X_SZ && X_SZ % 256 == 0, "regions");
+static_assert(2 * 32 * GS <= W_SZ && 4 * CSX + 64 <= X_SZ && X_SZ % 256 == 0, "regions");
 static_assert((64 * CS2) % 256 == 0 && 2 * 2 * SLOT <= 64 * CS2, "dc2 slab");
 static_assert(LDS_FLOATS * 4 <= LDS_MAX, "LDS");
 }  // namespace chainb
@@ -2385,13 +2451,13 @@ __device__ __forceinline__ void conv_chain_bwd_block(const float *__restrict__ d
     for (int base = wave * 256; base < W_SZ; base += NTH * 4)
       dma_dwordx4(w2 + base + lane * 4, ws + base);
     const float *xn = x + (long)n * C1 * 1024;
-    for (int base = wave * 256; base < X_SZ; base += NTH * 4) {
-      const int i = base + lane * 4;
+    for (int base = wave * 64; base < 4 * CSX; base += NTH) {
+      const int i = base + lane;
       const int c = i / CSX, rem = i - c * CSX;
       const int slot = rem / RWX, j = rem - slot * RWX;
       const int row = 16 * hf - 1 + slot;
       const bool ok = c < C1 && slot < RX && j >= GX && row >= 0 && row < 32;
-      dma_dwordx4(ok ? xn + (c * 32 + row) * 32 + (j - GX) : g_zero_src, xs + base);
+      dma_dword(ok ? xn + (c * 32 + row) * 32 + (j - GX) : g_zero_src, xs + base);
     }
     if (wave < 4) {
       const int i = wave * 1024 + lane * 16;  // byte of the 32 x 128 tile
@@ -2576,15 +2642,16 @@ conv_chain_bwd_dw2_kernel(const float *__restrict__ dc2, const float *__restrict
                           const unsigned char *__restrict__ codes1, const float *__restrict__ x,
                           float *__restrict__ dx2, float *__restrict__ part1, int C1,
                           const float *__restrict__ x2, float *__restrict__ part2, Geo g2,
-                          int RC, int nch, int GS, int CS, int jbp, int nu2, int nchain) {
+                          int RC, int nch, int GS, int CS, int RW, int jbp, int nu2,
+                          int nchain) {
   if ((int)blockIdx.x < nchain) {
     if (threadIdx.x >= chainb::NTH) return;
     conv_chain_bwd_block(dc2, w2, codes1, x, dx2, part1, C1, blockIdx.x);
     return;
   }
   const int b = blockIdx.x - nchain;
-  conv_dwt_block<3, 3, false>(dc2, x2, part2, g2, RC, nch, GS, CS, jbp, nullptr, b % nu2, 0,
-                              b / nu2, nu2);
+  conv_dwt_block<3, 3, false>(dc2, x2, part2, g2, RC, nch, GS, CS, RW, jbp, nullptr, b % nu2,
+                              0, b / nu2, nu2);
 }
 
 int g_lds_conv = 1;  // tth_conv_lds
@@ -2957,7 +3024,8 @@ extern "C" int ttk_conv2d_chain_bwd(const float *dc2, const float *w2, const uns
   if (dw2)
     hipLaunchKernelGGL(conv_chain_bwd_dw2_kernel, dim3((unsigned)(2 * N + t2.units * t2.nfb)),
                        dim3(64 * DWT_NPQ * 3), lds, stream(), dc2, w2, codes1, x, dx2, part, C1,
-                       x2, part2, g2, t2.rc, t2.nch, t2.gs, t2.cs, t2.jbp, t2.units, 2 * N);
+                       x2, part2, g2, t2.rc, t2.nch, t2.gs, t2.cs, t2.rw, t2.jbp, t2.units,
+                       2 * N);
   else
     hipLaunchKernelGGL(conv_chain_bwd_kernel, dim3((unsigned)(2 * N)), dim3(chainb::NTH), lds,
                        stream(), dc2, w2, codes1, x, dx2, part, C1);
