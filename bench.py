@@ -365,9 +365,10 @@ def bandwidth_kernels(L, reps=50):
 
 
 def conv_kernels(L, reps=50):
-    """The direct (LDS-staged) convolution kernels of the CNN step at config-4
-    shapes, each timed with HIP events over `reps` calls (a call of dW includes
-    its partial reduction).  Algorithmic work: 2*F*C*HH*WW*N*Ho*Wo flops; bytes:
+    """The direct (LDS-staged) convolution kernels at config-4 shapes (the
+    separate kernels the graph takes outside the two-convolution chain) and
+    the chain's two kernels the CNN step runs, each timed with HIP events over
+    `reps` calls (a call of dW includes its partial reduction).  Algorithmic work: 2*F*C*HH*WW*N*Ho*Wo flops; bytes:
     every input element read once + every output element written once."""
     from tinytorch_amd.hip import DevBuf, StreamTimer, check, sync
     rng = np.random.default_rng(9)
@@ -403,6 +404,49 @@ def conv_kernels(L, reps=50):
                              bytes=int(nbytes), gb_s=round(nbytes / (ms * 1e-3) / 1e9, 1))
         for bb in (x, w, b, g, y, dx, dw, db):
             bb.free()
+    # the step's own kernels: both convolutions (+ relus, pools, codes, the
+    # flattened and padded copies and the classifier's partial sums) in one
+    # launch, and the backward grid (conv2 dX, conv1 dW through the pool
+    # codes, conv2 dW; with their two weight-gradient reductions)
+    x = DevBuf.from_np(rng.uniform(0, 1, B * 3 * 1024).astype(np.float32))
+    w1 = DevBuf.from_np((rng.standard_normal(32 * 27) * 0.27).astype(np.float32))
+    w2 = DevBuf.from_np((rng.standard_normal(64 * 288) * 0.083).astype(np.float32))
+    b1, b2 = DevBuf.from_np(np.zeros(32, np.float32)), DevBuf.from_np(np.zeros(64, np.float32))
+    fcw = DevBuf.from_np((rng.standard_normal(4097 * 10) / 64).astype(np.float32))
+    p1, k1 = DevBuf(B * 32 * 256), DevBuf(B * 32 * 256, np.uint8)
+    p2, c2, d2, k2 = DevBuf(B * 4096), DevBuf(B * 4096), DevBuf(B * 4097), DevBuf(B * 4096, np.uint8)
+    s1, s2, part = DevBuf(32 * 27 + 32), DevBuf(18432 + 64), DevBuf(2 * B * 10)
+    g2 = DevBuf.from_np(rng.standard_normal(B * 64 * 256).astype(np.float32))
+    dx2, dw1, db1, dw2, db2 = DevBuf(B * 32 * 256), DevBuf(32 * 27), DevBuf(32), DevBuf(64 * 288), DevBuf(64)
+    f1, f2 = 2.0 * 32 * 27 * B * 1024, 2.0 * 64 * 288 * B * 256
+    ops = {"chain_fwd": (lambda: L.tt_k_conv2d_chain_fwd(
+                             x.ptr, w1.ptr, b1.ptr, w2.ptr, b2.ptr, p1.ptr, k1.ptr, p2.ptr, c2.ptr,
+                             d2.ptr, k2.ptr, s1.ptr, s2.ptr, fcw.ptr, 10, part.ptr, B, 3, 32, 32,
+                             32, 64),
+                         f1 + f2 + 2.0 * B * 4096 * 10,
+                         4 * (B * 3 * 1024 + 32 * 27 + 64 * 288 + 4097 * 10 + B * 32 * 256 +
+                              3 * B * 4096 + B * 4097 + 2 * B * 10) + B * 32 * 256 + B * 4096),
+           "chain_bwd": (lambda: L.tt_k_conv2d_chain_bwd(
+                             g2.ptr, w2.ptr, k1.ptr, x.ptr, dx2.ptr, dw1.ptr, db1.ptr, p1.ptr,
+                             dw2.ptr, db2.ptr, B, 3),
+                         f1 + 2 * f2,
+                         4 * (B * 64 * 256 + 64 * 288 + B * 3 * 1024 + 2 * B * 32 * 256 + 32 * 27 +
+                              32 + 64 * 288 + 64) + B * 32 * 256)}
+    for name, (fn, flops, nbytes) in ops.items():
+        check(fn(), name)
+        prewarm(fn, 0.05)
+        tm = StreamTimer()
+        tm.start()
+        for _ in range(reps):
+            fn()
+        ms = tm.stop_ms() / reps
+        tf = flops / (ms * 1e-3) / 1e12
+        out[name] = dict(us=round(ms * 1e3, 2), gflop=round(flops / 1e9, 3), tflops=round(tf, 1),
+                         frac_of_mfma_peak=round(tf / PEAK_FP32_MFMA_TFLOPS, 3), bytes=int(nbytes),
+                         gb_s=round(nbytes / (ms * 1e-3) / 1e9, 1))
+    for bb in (x, w1, w2, b1, b2, fcw, p1, k1, p2, c2, d2, k2, s1, s2, part, g2, dx2, dw1, db1,
+               dw2, db2):
+        bb.free()
     sync()
     return out
 
