@@ -70,6 +70,9 @@ def parse():
                          "traces of them)")
     ap.add_argument("--gemm-shape", choices=None, default=None,
                     help="only time one secondary GEMM shape, by its extra.* name")
+    ap.add_argument("--conv-kernels", action="store_true",
+                    help="only time the convolution kernels alone (extra.conv_kernels; for kernel "
+                         "traces of them)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 1 GiB device copy kernel 5 times (the known-size "
                          "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -573,6 +576,9 @@ def main():
     if args.mlp_only:
         ms = time_steps(MlpStep(L), args.steps, args.warmup)
         print(json.dumps({"mlp_step_ms": round(ms, 4), "steps": args.steps, "warmup": args.warmup}))
+        return
+    if args.conv_kernels:
+        print(json.dumps(conv_kernels(L)))
         return
     if args.gemm_shapes or args.gemm_shape:
         if args.gemm_shape and args.gemm_shape not in GEMM_SHAPES:
