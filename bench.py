@@ -73,6 +73,9 @@ def parse():
     ap.add_argument("--conv-kernels", action="store_true",
                     help="only time the convolution kernels alone (extra.conv_kernels; for kernel "
                          "traces of them)")
+    ap.add_argument("--hbm-kernels", action="store_true",
+                    help="only time the bandwidth kernels alone (extra.hbm_kernels; for kernel "
+                         "traces and HBM counters of them)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 1 GiB device copy kernel 5 times (the known-size "
                          "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -363,6 +366,8 @@ def bandwidth_kernels(L, reps=50):
     h = DevBuf.from_np(rng.standard_normal(B * D).astype(np.float32))
     hp = DevBuf(B * (D + 1))
     run("padones_fwd_fc", lambda: L.tt_k_padones_fwd(h.ptr, hp.ptr, B, D), 4 * (B * D + B * (D + 1)))
+    # the launch floor of this timing: a one-element fill, timed the same way
+    run("launch_floor_fill1", lambda: L.tt_k_fill(hp.ptr, 1, 0.0), 4)
     sync()
     return out
 
@@ -579,6 +584,9 @@ def main():
         return
     if args.conv_kernels:
         print(json.dumps(conv_kernels(L)))
+        return
+    if args.hbm_kernels:
+        print(json.dumps(bandwidth_kernels(L)))
         return
     if args.gemm_shapes or args.gemm_shape:
         if args.gemm_shape and args.gemm_shape not in GEMM_SHAPES:

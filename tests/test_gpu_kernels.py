@@ -128,6 +128,8 @@ CONV_CASES = [  # (N, C, H, W, F, HH, WW, sh, sw, ph, pw)
     (3, 4, 9, 8, 5, 3, 2, 2, 1, 2, 1), (1, 1, 5, 5, 1, 1, 1, 1, 1, 0, 0),
     (4, 32, 16, 16, 64, 3, 3, 1, 1, 1, 1), (8, 3, 32, 32, 32, 3, 3, 1, 1, 1, 1),
     (2, 5, 6, 6, 3, 5, 5, 1, 1, 2, 2),
+    # strided planes that fit the LDS-staged col2im (Ho*Wo % 4 == 0), 4-pixel and 1-pixel lanes
+    (2, 3, 8, 8, 4, 3, 3, 2, 2, 1, 1), (2, 2, 8, 14, 3, 2, 2, 2, 2, 0, 0),
 ]
 
 
@@ -349,11 +351,17 @@ def test_padones_relu_fused_bitexact(tlib, M, K):
     assert bits_equal(ddx.to_np((M, K)), orc.relu_bwd(x, dr_ref))
 
 
-@pytest.mark.parametrize("N,F,HW", [(1, 1, 1), (2, 4, 49), (128, 32, 1024), (128, 64, 256)])
+@pytest.mark.parametrize("N,F,HW", [(1, 1, 1), (2, 4, 49), (128, 32, 1024), (128, 64, 256),
+                                    (64, 5000, 3), (128, 3, 100)])
 def test_bias_grad(tlib, N, F, HW):
+    """Two deterministic stages (partials, then their in-order sum): a second
+    call gives the same bits; F beyond one partial a filter, tiny HW."""
     g = rng.standard_normal((N, F, HW)).astype(np.float32)
     dg, db = DevBuf.from_np(g), DevBuf(F)
     check(tlib.tt_k_bias_grad(dg.ptr, db.ptr, N, F, HW), "bias_grad")
+    first = db.to_np()
+    check(tlib.tt_k_bias_grad(dg.ptr, db.ptr, N, F, HW), "bias_grad again")
+    assert bits_equal(db.to_np(), first)
     ref = orc.bias_grad(g)
     exact = g.astype(np.float64).sum(axis=(0, 2))
     got = db.to_np()

@@ -120,6 +120,68 @@ col2im_px_kernel(const float *__restrict__ col, float *__restrict__ x, int N, in
   }
 }
 
+// col2im staged through LDS, one workgroup per (image n, channel ci) plane:
+// the plane's taps*Ho*Wo column entries (row c = ci*taps + t, columns
+// n*Ho*Wo ..) are read once with 16-byte loads, then each lane gathers its
+// pixels from LDS in the same order as col2im_px_kernel (kh then kw
+// ascending from +0.0f), so the two are bit-identical.  VEC: a lane owns 4
+// consecutive pixels of a row (W % 4 == 0) and stores them with one 16-byte
+// store.  Requires Ho*Wo % 4 == 0 and a 16-byte aligned column matrix.
+template <bool S1, bool VEC>
+__global__ void __launch_bounds__(256)
+col2im_lds_kernel(const float *__restrict__ col, float *__restrict__ x, int N, int C, int H, int W,
+                  int HH, int WW, int sh, int sw, int ph, int pw, int Ho, int Wo) {
+  extern __shared__ float cs[];
+  const int n = blockIdx.x / C, ci = blockIdx.x - n * C;
+  const int HoWo = Ho * Wo, taps = HH * WW;
+  const long Ncol = (long)N * HoWo;
+  const float *src = col + (long)ci * taps * Ncol + (long)n * HoWo;
+  const int q4 = HoWo / 4;
+  for (int i = threadIdx.x; i < taps * q4; i += 256) {
+    const int t = i / q4, q = i - t * q4;
+    *reinterpret_cast<float4 *>(cs + t * HoWo + 4 * q) =
+        *reinterpret_cast<const float4 *>(src + (long)t * Ncol + 4 * q);
+  }
+  __syncthreads();
+  float *dst = x + (long)blockIdx.x * H * W;
+  constexpr int PX = VEC ? 4 : 1;
+  for (int i = threadIdx.x * PX; i < H * W; i += 256 * PX) {
+    const int h = i / W, w0 = i - h * W;
+    float acc[PX];
+#pragma unroll
+    for (int j = 0; j < PX; j++) acc[j] = 0.0f;
+    for (int kh = 0; kh < HH; kh++) {
+      int ho = h + ph - kh;
+      if constexpr (S1) {
+        if (ho < 0 || ho >= Ho) continue;
+      } else {
+        if (ho < 0 || ho % sh) continue;
+        ho /= sh;
+        if (ho >= Ho) continue;
+      }
+      const float *rowp = cs + kh * WW * HoWo + ho * Wo;
+      for (int kw = 0; kw < WW; kw++) {
+#pragma unroll
+        for (int j = 0; j < PX; j++) {
+          int wo = w0 + j + pw - kw;
+          if constexpr (S1) {
+            if (wo < 0 || wo >= Wo) continue;
+          } else {
+            if (wo < 0 || wo % sw) continue;
+            wo /= sw;
+            if (wo >= Wo) continue;
+          }
+          acc[j] += rowp[kw * HoWo + wo];
+        }
+      }
+    }
+    if constexpr (VEC)
+      *reinterpret_cast<float4 *>(dst + i) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    else
+      dst[i] = acc[0];
+  }
+}
+
 // im2col with one workgroup per (kernel tap c, 1024 consecutive columns p):
 // row c of the column matrix is contiguous in p, each lane writes 4 columns
 // with one 16-byte store, c comes from the grid and a lane divides only by
@@ -558,6 +620,17 @@ int tt_k_col2im(const float *col, float *x, int N, int C, int H, int W, int HH, 
   const long total = (long)N * C * H * W;
   if (total <= 0) return 0;
   const bool s1 = sh == 1 && sw == 1;
+  const long HoWo = (long)Ho * Wo;
+  const size_t lds = sizeof(float) * (size_t)HH * WW * HoWo;
+  if (HoWo % 4 == 0 && lds <= 65536 && (long)N * C < (1L << 31) && ((uintptr_t)col & 15) == 0) {
+    const dim3 g((unsigned)((long)N * C)), b(256);
+    const bool vec = W % 4 == 0 && ((uintptr_t)x & 15) == 0;
+    if (s1 && vec) hipLaunchKernelGGL((col2im_lds_kernel<true, true>), g, b, lds, stream(), col, x, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo);
+    else if (s1)   hipLaunchKernelGGL((col2im_lds_kernel<true, false>), g, b, lds, stream(), col, x, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo);
+    else if (vec)  hipLaunchKernelGGL((col2im_lds_kernel<false, true>), g, b, lds, stream(), col, x, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo);
+    else           hipLaunchKernelGGL((col2im_lds_kernel<false, false>), g, b, lds, stream(), col, x, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo);
+    return launched();
+  }
   const dim3 g(blocks_for(total)), b(256);
   if (total < (1L << 31)) {
     if (s1) hipLaunchKernelGGL((col2im_px_kernel<unsigned, true>), g, b, 0, stream(), col, x, N, C, H, W, HH, WW, sh, sw, ph, pw, Ho, Wo);
