@@ -148,3 +148,43 @@ __device__ __forceinline__ void ce_rows_block(const float *__restrict__ x, const
                         seed + (long)r * cols, cols, scale);
   ce_mean_tree(acc, part, loss_mean, rows);
 }
+
+// ce_row by a group of W lanes (W a power of two, cols <= W, the group's
+// lanes consecutive and all active): lane j = threadIdx.x % W holds column
+// j's logit x (ignored for j >= cols) and gets that column's probability pj
+// and seed sj; every lane of the group returns the row's loss.  The same
+// operations in the same order as ce_row, so the same bits: the maximum
+// (order-free; NaN never wins, as with the serial strict compare), one expf
+// a lane, the sum of the exponentials in column order (each lane adds the
+// group's values one by one from 0), one division a lane.
+template <int W>
+__device__ __forceinline__ float ce_row_group(float x, int y, int cols, float scale, float &pj,
+                                              float &sj) {
+  const int j = threadIdx.x & (W - 1);
+  float mx = (j < cols && x > -INFINITY) ? x : -INFINITY;
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) {
+    const float t = __shfl_xor(mx, o, W);
+    if (t > mx) mx = t;
+  }
+  float v;
+  if (mx == -INFINITY) {
+    v = 1.0f / (float)cols;
+  } else {
+    const float e = j < cols ? expf(x - mx) : 0.0f;
+    float sum = 0.0f;
+    for (int c = 0; c < cols; c++) sum += __shfl(e, c, W);
+    v = e / sum;
+  }
+  pj = v;
+  sj = (v - (j == y ? 1.0f : 0.0f)) * scale;
+  const bool has = y >= 0 && y < cols;
+  const float py = __shfl(v, has ? y : 0, W);
+  // opaque to the optimiser: with a label out of range the argument is the
+  // constant 1e-12, and a logf folded at compile time (correctly rounded)
+  // can differ in the last bit from the device logf that ce_row runs
+  float a = fmaxf(has ? py : 0.0f, 1e-12f);
+  asm volatile("" : "+v"(a));
+  return -logf(a);
+}
+

@@ -547,9 +547,10 @@ add_outside_kernel(float *__restrict__ c, const float *__restrict__ cin, int M, 
 // (the classifier): each element summed exactly as gemm.hip's reduce_one
 // (lanes ty = 0..ZL-1 add partials z = ty, ty + ZL, ... in order, then lane
 // 0 adds the lanes' sums in lane order) plus bias, stored to C; a workgroup
-// holds rpb whole rows (ZL x rpb*N threads), so after a barrier thread r
-// runs ce_row on row r from LDS.  The same bits as the reduction followed by
-// softmax_ce_mean_kernel (whose per-row losses ttk_ce_mean_rows adds).
+// holds rpb whole rows (ZL x rpb*N threads), so after a barrier groups of
+// MAXC lanes run each row's softmax-CE from LDS (ce_row_group).  The same
+// bits as the reduction followed by softmax_ce_mean_kernel (whose per-row
+// losses ttk_ce_mean_rows adds).
 template <int ZL, int MAXC>
 __global__ void __launch_bounds__(1024)
 splitk_reduce_ce_kernel(const float *__restrict__ ws, float *__restrict__ C, int M, int N, int S,
@@ -578,11 +579,29 @@ splitk_reduce_ce_kernel(const float *__restrict__ ws, float *__restrict__ C, int
     }
   }
   __syncthreads();
-  const int r = threadIdx.x;
-  const long row = (long)blockIdx.x * rpb + r;
-  if (r < rpb && row < M)
-    rowloss[row] = ce_row<MAXC>(lv + r * N, lab[(int)row], probs + row * N, seed + row * N, N,
-                                scale);
+  const int ng = blockDim.x / MAXC;  // groups of MAXC lanes, a row each (ce_row_group)
+  if (ng == 0) {
+    const int r = threadIdx.x;
+    const long row = (long)blockIdx.x * rpb + r;
+    if (r < rpb && row < M)
+      rowloss[row] = ce_row<MAXC>(lv + r * N, lab[(int)row], probs + row * N, seed + row * N, N,
+                                  scale);
+    return;
+  }
+  const int gi = threadIdx.x / MAXC, j = threadIdx.x % MAXC;
+  if (gi >= ng) return;
+  for (int r = gi; r < rpb; r += ng) {
+    const long row = (long)blockIdx.x * rpb + r;
+    if (row >= M) break;
+    float pj, sj;
+    const float loss = ce_row_group<MAXC>(j < N ? lv[r * N + j] : 0.0f, lab[(int)row], N, scale,
+                                          pj, sj);
+    if (j < N) {
+      probs[row * N + j] = pj;
+      seed[row * N + j] = sj;
+    }
+    if (j == 0) rowloss[row] = loss;
+  }
 }
 
 // loss[0] = the mean of rowloss as softmax_ce_mean_kernel forms it (thread t
@@ -658,7 +677,7 @@ gemm_rows_kernel(const float *__restrict__ A, const float *__restrict__ B,
 // loading its whole slice (NCH 16-k chunks, 8 registers a chunk) before its
 // 16x16x4 MFMAs, so a wave waits for one round trip; the wave sums are added
 // in LDS in wave order, then the epilogue of gemm_rows_kernel for the tile's
-// rows (the softmax-CE by one lane a row).  Lane l (r = l % 16, q = l / 16)
+// rows (the softmax-CE by 16 lanes a row).  Lane l (r = l % 16, q = l / 16)
 // feeds A[m0 + r][k] and B[k][r] for k = kb + 4q + i in MFMA i of a chunk;
 // loads past the matrix are clamped to it and their values zeroed.  VA:
 // 16-byte loads of A's rows (aligned, K % 4 == 0).  MLP step 0.0472 ->
@@ -735,10 +754,18 @@ gemm_rows16_kernel(const float *__restrict__ A, const float *__restrict__ B,
     }
   }
   if constexpr (CE) {
+    // the tile's 16 rows, 16 lanes a row (ce_row_group: the bits of ce_row)
     __syncthreads();
-    const int t = threadIdx.x, m = m0 + t;
-    if (t < 16 && m < M)
-      rowloss[m] = ce_row<16>(lv[t], lab[m], probs + (long)m * N, seed + (long)m * N, N, scale);
+    const int t = threadIdx.x, row = t >> 4, j = t & 15, m = m0 + row;
+    if (t < 256 && m < M) {
+      float pj, sj;
+      const float loss = ce_row_group<16>(lv[row][j], lab[m], N, scale, pj, sj);
+      if (j < N) {
+        probs[(long)m * N + j] = pj;
+        seed[(long)m * N + j] = sj;
+      }
+      if (j == 0) rowloss[m] = loss;
+    }
   }
 }
 
