@@ -59,66 +59,6 @@ __device__ __forceinline__ float ce_row(const float *__restrict__ xr, int y,
   return -logf(fmaxf(py, 1e-12f));
 }
 
-// ce_row by a pair of lanes (this lane and lane ^ 1, both active): lane
-// half q = lane & 1 takes columns [j0, j1) = [q h, q ? cols : h), h = (cols +
-// 1) / 2, whose logits it holds in vh[0 .. j1 - j0); pr / sr get those
-// columns.  The same operations in the same order as ce_row -- the maximum
-// (order-free), each expf, the sum of the exponentials in column order (the
-// upper lane continues the lower lane's running sum), each division -- so
-// the same bits; returns the row's loss in both lanes.
-template <int HC>
-__device__ __forceinline__ float ce_row_pair(float (&vh)[HC], int y, float (&pr)[HC],
-                                             float (&sr)[HC], int cols, float scale) {
-  const int q = threadIdx.x & 1, h = (cols + 1) / 2;
-  const int j0 = q * h, nh = (q ? cols : h) - j0;
-  float mx = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < HC; i++) if (i < nh && vh[i] > mx) mx = vh[i];
-  const float om = __shfl_xor(mx, 1, 64);
-  if (om > mx) mx = om;
-  if (mx == -INFINITY) {
-#pragma unroll
-    for (int i = 0; i < HC; i++) vh[i] = 1.0f / (float)cols;
-  } else {
-#pragma unroll
-    for (int i = 0; i < HC; i++)
-      if (i < nh) vh[i] = expf(vh[i] - mx);
-    float sum = 0.0f;
-    if (q == 0) {
-#pragma unroll
-      for (int i = 0; i < HC; i++)
-        if (i < nh) sum += vh[i];
-    }
-    const float s0 = __shfl_xor(sum, 1, 64);  // the upper lane continues the lower's sum
-    if (q == 1) {
-      sum = s0;
-#pragma unroll
-      for (int i = 0; i < HC; i++)
-        if (i < nh) sum += vh[i];
-    }
-    const float s1 = __shfl_xor(sum, 1, 64);
-    if (q == 0) sum = s1;
-#pragma unroll
-    for (int i = 0; i < HC; i++) vh[i] = vh[i] / sum;
-  }
-  float py = 0.0f;
-  int own = 0;
-#pragma unroll
-  for (int i = 0; i < HC; i++)
-    if (i < nh) {
-      const int j = j0 + i;
-      pr[i] = vh[i];
-      sr[i] = (vh[i] - (j == y ? 1.0f : 0.0f)) * scale;
-      if (j == y) { py = vh[i]; own = 1; }
-    }
-  // the loss from the lane holding the label's column (neither, for a label
-  // outside [0, cols): -log(1e-12), as ce_row)
-  const float l = -logf(fmaxf(py, 1e-12f));
-  const float lo = __shfl_xor(l, 1, 64);
-  const int oo = __shfl_xor(own, 1, 64);
-  return own || !oo ? l : lo;
-}
-
 // loss_mean[0] = (sum of the 256 per-thread sums acc, added through `part`
 // (256 floats of LDS) in a fixed tree) / rows.  Every thread of the
 // workgroup calls it; threads 256 and up only take part in the barriers.
@@ -149,42 +89,61 @@ __device__ __forceinline__ void ce_rows_block(const float *__restrict__ x, const
   ce_mean_tree(acc, part, loss_mean, rows);
 }
 
-// ce_row by a group of W lanes (W a power of two, cols <= W, the group's
-// lanes consecutive and all active): lane j = threadIdx.x % W holds column
-// j's logit x (ignored for j >= cols) and gets that column's probability pj
-// and seed sj; every lane of the group returns the row's loss.  The same
-// operations in the same order as ce_row, so the same bits: the maximum
-// (order-free; NaN never wins, as with the serial strict compare), one expf
-// a lane, the sum of the exponentials in column order (each lane adds the
-// group's values one by one from 0), one division a lane.
-template <int W>
-__device__ __forceinline__ float ce_row_group(float x, int y, int cols, float scale, float &pj,
-                                              float &sj) {
-  const int j = threadIdx.x & (W - 1);
-  float mx = (j < cols && x > -INFINITY) ? x : -INFINITY;
+// ce_row by a group of W lanes (W a power of two, the group's lanes
+// consecutive and all active), CPL columns a lane (cols <= W * CPL): lane q =
+// threadIdx.x % W holds the logits of columns q * CPL + u in x[u] (ignored
+// past cols) and gets those columns' probabilities pj[u] and seeds sj[u];
+// every lane of the group returns the row's loss.  The same operations in the
+// same order as ce_row, so the same bits: the maximum (order-free; NaN never
+// wins, as with the serial strict compare), one expf a column, the sum of the
+// exponentials in column order (each lane adds the group's values one by one
+// from 0), one division a column.
+template <int W, int CPL>
+__device__ __forceinline__ float ce_row_group(const float (&x)[CPL], int y, int cols, float scale,
+                                              float (&pj)[CPL], float (&sj)[CPL]) {
+  const int q = threadIdx.x & (W - 1);
+  float mx = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < CPL; u++)
+    if (q * CPL + u < cols && x[u] > mx) mx = x[u];
 #pragma unroll
   for (int o = W / 2; o > 0; o >>= 1) {
     const float t = __shfl_xor(mx, o, W);
     if (t > mx) mx = t;
   }
-  float v;
+  float v[CPL];
   if (mx == -INFINITY) {
-    v = 1.0f / (float)cols;
+#pragma unroll
+    for (int u = 0; u < CPL; u++) v[u] = 1.0f / (float)cols;
   } else {
-    const float e = j < cols ? expf(x - mx) : 0.0f;
+    float e[CPL];
+#pragma unroll
+    for (int u = 0; u < CPL; u++) e[u] = q * CPL + u < cols ? expf(x[u] - mx) : 0.0f;
     float sum = 0.0f;
-    for (int c = 0; c < cols; c++) sum += __shfl(e, c, W);
-    v = e / sum;
+#pragma unroll
+    for (int c = 0; c < W * CPL; c++) {
+      const float t = __shfl(e[c % CPL], c / CPL, W);
+      if (c < cols) sum += t;
+    }
+#pragma unroll
+    for (int u = 0; u < CPL; u++) v[u] = e[u] / sum;
   }
-  pj = v;
-  sj = (v - (j == y ? 1.0f : 0.0f)) * scale;
-  const bool has = y >= 0 && y < cols;
-  const float py = __shfl(v, has ? y : 0, W);
+  float py = 0.0f;
+#pragma unroll
+  for (int u = 0; u < CPL; u++) {
+    const int j = q * CPL + u;
+    pj[u] = v[u];
+    sj[u] = (v[u] - (j == y ? 1.0f : 0.0f)) * scale;
+    if (j == y) py = v[u];
+  }
+  // the lane that holds column y has its probability, the others 0 (and all
+  // 0 for a label out of range): the largest over the group is p_y
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) py = fmaxf(py, __shfl_xor(py, o, W));
   // opaque to the optimiser: with a label out of range the argument is the
   // constant 1e-12, and a logf folded at compile time (correctly rounded)
   // can differ in the last bit from the device logf that ce_row runs
-  float a = fmaxf(has ? py : 0.0f, 1e-12f);
+  float a = fmaxf(py, 1e-12f);
   asm volatile("" : "+v"(a));
   return -logf(a);
 }
-

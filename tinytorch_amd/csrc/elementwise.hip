@@ -593,12 +593,11 @@ splitk_reduce_ce_kernel(const float *__restrict__ ws, float *__restrict__ C, int
   for (int r = gi; r < rpb; r += ng) {
     const long row = (long)blockIdx.x * rpb + r;
     if (row >= M) break;
-    float pj, sj;
-    const float loss = ce_row_group<MAXC>(j < N ? lv[r * N + j] : 0.0f, lab[(int)row], N, scale,
-                                          pj, sj);
+    float xj[1] = {j < N ? lv[r * N + j] : 0.0f}, pj[1], sj[1];
+    const float loss = ce_row_group<MAXC, 1>(xj, lab[(int)row], N, scale, pj, sj);
     if (j < N) {
-      probs[row * N + j] = pj;
-      seed[row * N + j] = sj;
+      probs[row * N + j] = pj[0];
+      seed[row * N + j] = sj[0];
     }
     if (j == 0) rowloss[row] = loss;
   }
@@ -758,11 +757,11 @@ gemm_rows16_kernel(const float *__restrict__ A, const float *__restrict__ B,
     __syncthreads();
     const int t = threadIdx.x, row = t >> 4, j = t & 15, m = m0 + row;
     if (t < 256 && m < M) {
-      float pj, sj;
-      const float loss = ce_row_group<16>(lv[row][j], lab[m], N, scale, pj, sj);
+      float xj[1] = {lv[row][j]}, pj[1], sj[1];
+      const float loss = ce_row_group<16, 1>(xj, lab[m], N, scale, pj, sj);
       if (j < N) {
-        probs[(long)m * N + j] = pj;
-        seed[(long)m * N + j] = sj;
+        probs[(long)m * N + j] = pj[0];
+        seed[(long)m * N + j] = sj[0];
       }
       if (j == 0) rowloss[m] = loss;
     }

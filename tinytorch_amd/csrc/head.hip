@@ -162,7 +162,7 @@ constexpr int DA_M = 32;  // rows m per dA workgroup (8 per lane)
 // sums of its logits (see above) into gl (row r at gl[(r - r0) * gs]); `out`:
 // also store the softmax-CE's outputs of those rows.  The rows' partial sums
 // are first loaded whole-workgroup (coalesced) into pp (2 (r1 - r0) N floats
-// of LDS); one thread a row then forms its softmax-CE.  Every thread calls
+// of LDS); four lanes a row then form its softmax-CE.  Every thread calls
 // it (barriers inside).
 template <int NC>
 __device__ __forceinline__ void head_ce_seed(const TTHeadCe &ce, int r0, int r1, int M, int N,
@@ -174,38 +174,38 @@ __device__ __forceinline__ void head_ce_seed(const TTHeadCe &ce, int r0, int r1,
     pp[n + i] = ce.part[total + (long)r0 * N + i];
   }
   __syncthreads();
-  // two lanes a row (ce_row_pair): lane half q takes columns [j0, j0 + nh)
-  constexpr int HC = (NC + 1) / 2;
-  const int q = threadIdx.x & 1, h = (N + 1) / 2;
-  const int j0 = q * h, nh = (q ? N : h) - j0;
-  for (int r = r0 + (int)(threadIdx.x >> 1); r < r1; r += NT / 2) {
-    float lv[HC], pr[HC], sr[HC];
-    const float *p0 = pp + (r - r0) * N + j0;
+  // four lanes a row (ce_row_group): lane q takes columns [q CPL, q CPL + CPL)
+  constexpr int GW = 4, CPL = (NC + GW - 1) / GW;
+  const int q = threadIdx.x & (GW - 1);
+  for (int r = r0 + (int)(threadIdx.x / GW); r < r1; r += NT / GW) {
+    float lv[CPL], pr[CPL], sr[CPL];
+    const float *p0 = pp + (r - r0) * N;
 #pragma unroll
-    for (int i = 0; i < HC; i++) {
-      lv[i] = 0.0f;
-      if (i < nh) {
+    for (int u = 0; u < CPL; u++) {
+      const int j = q * CPL + u;
+      lv[u] = 0.0f;
+      if (j < N) {
         float s = 0.0f;
-        s += p0[i];
-        s += p0[n + i];
-        lv[i] = s + ce.bias[j0 + i];
+        s += p0[j];
+        s += p0[n + j];
+        lv[u] = s + ce.bias[j];
       }
     }
-    float lg[HC];
+    float lg[CPL];
 #pragma unroll
-    for (int i = 0; i < HC; i++) lg[i] = lv[i];
-    const float loss = ce_row_pair<HC>(lv, ce.lab[r], pr, sr, N, ce.scale);
+    for (int u = 0; u < CPL; u++) lg[u] = lv[u];
+    const float loss = ce_row_group<GW, CPL>(lv, ce.lab[r], N, ce.scale, pr, sr);
 #pragma unroll
-    for (int i = 0; i < HC; i++)
-      if (i < nh) gl[(r - r0) * gs + j0 + i] = sr[i];
+    for (int u = 0; u < CPL; u++)
+      if (q * CPL + u < N) gl[(r - r0) * gs + q * CPL + u] = sr[u];
     if (out) {
 #pragma unroll
-      for (int i = 0; i < HC; i++)
-        if (i < nh) {
-          const long o = (long)r * N + j0 + i;
-          if (ce.logits) ce.logits[o] = lg[i];
-          if (ce.probs) ce.probs[o] = pr[i];
-          if (ce.seed) ce.seed[o] = sr[i];
+      for (int u = 0; u < CPL; u++)
+        if (q * CPL + u < N) {
+          const long o = (long)r * N + q * CPL + u;
+          if (ce.logits) ce.logits[o] = lg[u];
+          if (ce.probs) ce.probs[o] = pr[u];
+          if (ce.seed) ce.seed[o] = sr[u];
         }
       if (ce.rowloss && q == 0) ce.rowloss[r] = loss;
     }
