@@ -118,6 +118,10 @@ int tth_gemm_small(int on);
  * 16-byte aligned A rows; and the split-K partials of GEMMs with N <= 16
  * and K >= 2048 (at most 128 tiles). */
 int tth_gemm_t16(int on);
+/* Diagnostics: how many classifier backward rules took the input gradients
+   that the classifier's softmax-CE launch formed with the seed (instead of a
+   classifier backward kernel).  No counterpart in the reference. */
+long tth_ce_spec_count(void);
 
 /* Convolution GEMMs over the im2col matrix col[(c,kh,kw)][(n,ho,wo)]
  * (Kc = C*HH*WW rows, Ncol = N*Ho*Wo columns, HW = Ho*Wo):

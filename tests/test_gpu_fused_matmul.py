@@ -466,3 +466,112 @@ def test_sgd_step_of_a_tensor_a_pending_gradient_reads(tlib, read_first):
     bar_t = lr * 1e-4 * np.sqrt(N) * np.abs(g).max() * np.abs(v).max() + np.spacing(1.0)
     assert np.abs(got[0] - (w - lr * dw)).max() <= bar_w
     assert np.abs(got[1] - (t - lr * dt)).max() <= bar_t
+
+
+@pytest.mark.parametrize("case", ["default", "seed2", "twice", "frozen_w2"])
+def test_classifier_input_grads_formed_with_the_seed(tlib, case):
+    """relu -> padones -> matmul -> softmax_ce (the MLP's last layer): the
+    classifier's launch also forms, from each row's seed, the gradients of
+    the padones node, the relu and its input (the classifier backward's dA,
+    bit for bit); the backward takes them when it starts from this loss with
+    the default seed, the weights' gradient then being a recipe of the
+    optimizer's launch.  Every node gradient is compared with the same graph
+    whose logits are read before the softmax-CE (no such launch: the
+    classifier backward kernel): bit for bit, except the classifier weights'
+    gradient (MFMA tiles against the backward kernel's serial sums: within
+    1e-5 of its scale).  A seed of 2, a second backward (accumulating) and
+    frozen classifier weights leave the backward its own kernel."""
+    from tinytorch_amd.torch_py import Node
+    r = np.random.default_rng(21)
+    x = r.uniform(0, 1, (256, 100)).astype(np.float32)
+    w1 = (r.standard_normal((101, 64)) * 0.1).astype(np.float32)
+    w2 = (r.standard_normal((65, 10)) * 0.2).astype(np.float32)
+    y = r.integers(0, 10, 256)
+
+    def run(read_logits, seed=None, twice=False, w2_grad=True):
+        X, W1, W2 = Node.leaf(x, False), Node.leaf(w1), Node.leaf(w2, w2_grad)
+        P1 = X.padones()
+        H = P1.matmul(W1)
+        R = H.relu()
+        P2 = R.padones()
+        Z = P2.matmul(W2)
+        if read_logits:
+            Z.value()
+        L = Z.softmax_ce(y)
+        L.backward(seed)
+        if twice:
+            L.backward(seed)
+        out = dict(loss=L.value(), z=Z.value(), w1=W1.grad(), h=H.grad(), r=R.grad(),
+                   p2=P2.grad(), w2=W2.grad())
+        for nd in (L, Z, P2, R, H, P1, X, W1, W2):
+            nd.release()
+        return out
+
+    print("classifier input grads with the seed:", case, flush=True)
+    kw = dict(default={}, seed2=dict(seed=np.array([2.0], np.float32)), twice=dict(twice=True),
+              frozen_w2=dict(w2_grad=False))[case]
+    n0 = tlib.tth_ce_spec_count()
+    got = run(False, **kw)
+    taken = tlib.tth_ce_spec_count() - n0
+    assert taken == (1 if case in ("default", "twice") else 0), taken
+    ref = run(True, **kw)
+    assert tlib.tth_ce_spec_count() - n0 == taken
+    assert bits_equal(got["loss"], ref["loss"]) and bits_equal(got["z"], ref["z"])
+    for name in ("w1", "h", "r", "p2"):
+        assert bits_equal(got[name], ref[name]), name
+    if case == "frozen_w2":
+        assert got["w2"] is None
+    elif case == "seed2":
+        # not taken: the same kernel on both sides
+        assert bits_equal(got["w2"], ref["w2"])
+    else:
+        assert np.abs(got["w2"] - ref["w2"]).max() <= 1e-5 * np.abs(ref["w2"]).max()
+
+
+def test_classifier_and_first_layer_grads_in_one_sgd_launch(tlib):
+    """The MLP's two pending padones weight gradients (first layer and
+    classifier) and the plain step of the middle layer in one optimizer
+    launch: every weight equals w - lr * g, g the gradient of the same graph
+    read before stepping (each pending gradient formed by its own launch)."""
+    from tinytorch_amd.torch_py import Node
+    r = np.random.default_rng(22)
+    x = r.uniform(0, 1, (256, 784)).astype(np.float32)
+    ws = [(r.standard_normal(s) * 0.05).astype(np.float32) for s in ((785, 128), (129, 64), (65, 10))]
+    y = r.integers(0, 10, 256)
+    lr = 0.05
+
+    def run(read_grads):
+        X = Node.leaf(x, False)
+        W = [Node.leaf(w) for w in ws]
+        h = X.padones().matmul(W[0]).relu().padones().matmul(W[1]).relu().padones()
+        L = h.matmul(W[2]).softmax_ce(y)
+        L.backward(None)
+        g = [w.grad() for w in W] if read_grads else None
+        arr = (ctypes.c_void_p * 3)(*[w.ptr for w in W])
+        check(tlib.ag_sgd_step_many(arr, 3, ctypes.c_float(lr)), "sgd many")
+        out = [w.value() for w in W], g
+        L.release()
+        X.release()
+        for w in W:
+            w.release()
+        return out
+
+    print("sgd launch with two pending padones gradients", flush=True)
+    stepped, _ = run(False)
+    ref_w, g = run(True)
+    for i in range(3):
+        assert bits_equal(ref_w[i], ws[i] - np.float32(lr) * g[i]), i
+        assert bits_equal(stepped[i], ref_w[i]), i
+
+
+
+def test_classifier_input_grads_taken_in_the_mlp_step(tlib):
+    """The bench's config-2 step (and the test graph above) take the
+    classifier's input gradients formed with the seed: the library's count of
+    such backward rules goes up by one a step."""
+    import bench
+    st = bench.MlpStep(tlib)
+    n0 = tlib.tth_ce_spec_count()
+    st.step()
+    st.step(lr=0.01)
+    assert tlib.tth_ce_spec_count() == n0 + 2

@@ -164,6 +164,7 @@ SIGNATURES = [
     ("tth_gemm_mid", _I, [_I]),
     ("tth_gemm_small", _I, [_I]),
     ("tth_gemm_t16", _I, [_I]),
+    ("tth_ce_spec_count", _L, []),
     ("tt_k_conv2d_fwd_implicit", _I, [VP, VP, VP, VP] + [_I] * 13),
     ("tt_k_conv2d_dw_implicit", _I, [VP, VP, VP, VP] + [_I] * 13),
     ("tt_k_conv2d_dx_implicit", _I, [VP, VP, VP] + [_I] * 13),

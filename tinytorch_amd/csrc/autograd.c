@@ -52,7 +52,10 @@ struct AGNode {
         struct { int kh, kw, sh, sw; Tensor *codes; } win;  /* pools (codes: one byte a
                                                       2x2 window, or NULL) */
         struct { int sh, sw, ph, pw; float *col; int col_ones; } conv;
-        struct { Tensor *probs, *seed; int32_t *labels; } ce;  /* softmax-CE */
+        /* softmax-CE; sda: the input gradients of its classifier (see
+         * ce_spec), computed with the seed and not yet handed over */
+        struct { Tensor *probs, *seed; int32_t *labels; Tensor *sda[3]; } ce;
+        struct { Tensor *sda[3]; } mm;  /* matmul: sda handed over by its softmax-CE */
     } at;
     unsigned long long pass;     /* backward pass that scheduled the node */
     int     walk;                /* depth-first walk: next input to enter */
@@ -96,13 +99,17 @@ static void drop_ce(AGNode *n) {
     tt_release(n->at.ce.probs);
     tt_release(n->at.ce.seed);
     free(n->at.ce.labels);
+    for (int i = 0; i < 3; i++) tt_release(n->at.ce.sda[i]);
+}
+static void drop_mm(AGNode *n) {
+    for (int i = 0; i < 3; i++) tt_release(n->at.mm.sda[i]);
 }
 
 static const AGOp OP_ADD = {"add", backward_add, NULL};
 static const AGOp OP_MUL = {"mul", backward_mul, NULL};
 static const AGOp OP_ADDSCALAR = {"addscalar", backward_addscalar, NULL};
 static const AGOp OP_MULSCALAR = {"mulscalar", backward_mulscalar, NULL};
-static const AGOp OP_MATMUL = {"matmul", backward_matmul, NULL};
+static const AGOp OP_MATMUL = {"matmul", backward_matmul, drop_mm};
 static const AGOp OP_RELU = {"relu", backward_relu, NULL};
 static const AGOp OP_SOFTMAX = {"softmax", backward_softmax, NULL};
 static const AGOp OP_PADONES = {"padones", backward_padones, NULL};
@@ -565,6 +572,41 @@ AGNode *ag_avgpool2d(AGNode *a, int ph, int pw, int sh, int sw) {
 
 /* Fused softmax + mean cross-entropy (no reference counterpart: the
  * reference harness does this in NumPy, tests/gate_cifar_cnn.py:175-181). */
+/* The classifier logits = padones(relu(h)) x W pending, its softmax-CE
+ * about to run in the GEMM's launch: the same launch also forms, from each
+ * row's seed, the gradients the classifier's backward would give the
+ * padones node, the relu node and h (dA = seed [W]^T, d1, d2; the
+ * classifier backward kernel's values bit for bit), in sda.  They are the
+ * backward's when it starts from this loss with the default seed and the
+ * three nodes have no other consumer (backward_matmul checks); otherwise
+ * they are dropped.  0: launched (logits, probs, seed, row losses and sda
+ * written); else nothing launched, sda empty. */
+static int ce_spec(AGNode *logits, const TTPendConv *p, const int32_t *hlab, Tensor *probs,
+                   Tensor *seed, Tensor *rl, Tensor *sda[3]) {
+    if (!tt_defer_enabled() || logits->op != &OP_MATMUL) return -1;
+    AGNode *a = logits->in[0];
+    if (!a || a->op != &OP_PADONES || !needs(a)) return -1;
+    AGNode *x = a->in[0];
+    if (!x || x->op != &OP_RELU || !needs(x->in[0]) || !x->val || p->x != x->val->dev ||
+        !p->b || p->b != p->w + (long)p->geo[2] * p->geo[1])
+        return -1;
+    sda[0] = tt_empty_like(a->val);
+    sda[1] = sda[0] ? tt_empty_like(x->val) : NULL;
+    sda[2] = sda[1] ? tt_empty_like(x->in[0]->val) : NULL;
+    const TTCeHook hk = {p->b, hlab, probs->dev, seed->dev, rl->dev,
+                         1.0f / (float)p->geo[0]};
+    const int rc = sda[2] ? ttk_gemm_rows_da(p->x, p->w, p->b, p->out->dev, NULL, NULL,
+                                             p->geo[0], p->geo[1], p->geo[2], &hk, sda[0]->dev,
+                                             sda[1]->dev, sda[2]->dev)
+                          : -1;
+    if (rc != 0) {
+        for (int i = 0; i < 3; i++) { tt_release(sda[i]); sda[i] = NULL; }
+        return -1;
+    }
+    for (int i = 0; i < 3; i++) tt_mark_dev_written(sda[i]);
+    return 0;
+}
+
 AGNode *ag_softmax_ce(AGNode *logits, const int *labels, long rows) {
     if (!logits || !labels || logits->val->ndim != 2 || logits->val->shape[0] != rows ||
         rows <= 0 || logits->val->shape[1] > 0x7fffffffL)
@@ -629,20 +671,28 @@ AGNode *ag_softmax_ce(AGNode *logits, const int *labels, long rows) {
         Tensor *rl = tt_empty_dev(&rows, 1);
         const TTPendConv p = tt_pend;
         tt_pend.active = 0;
-        const int rc = rl ? tt_k_gemm_bias_ce(p.geo[0], p.geo[1], p.geo[2], p.x, p.w, p.b,
-                                              p.out->dev, hlab, probs->dev, seed->dev, rl->dev,
-                                              1.0f / (float)rows)
-                          : -1;
+        Tensor *sda[3] = {NULL, NULL, NULL};
+        int rc = rl ? ce_spec(logits, &p, hlab, probs, seed, rl, sda) : -1;
+        if (rc != 0)
+            rc = rl ? tt_k_gemm_bias_ce(p.geo[0], p.geo[1], p.geo[2], p.x, p.w, p.b, p.out->dev,
+                                        hlab, probs->dev, seed->dev, rl->dev, 1.0f / (float)rows)
+                    : -1;
         if (rc == 0 && (tt_lazy_ce_mean(loss, rl) == 0 ||
                         tt_k_ce_mean_rows(rl->dev, loss->dev, (int)rows) == 0)) {
             tt_release(rl);
             AGNode *n = make_node(loss, &OP_SOFTMAX_CE, logits, NULL, NULL);
-            if (!n) { tt_release(probs); tt_release(seed); free(hlab); return NULL; }
+            if (!n) {
+                tt_release(probs); tt_release(seed); free(hlab);
+                for (int i = 0; i < 3; i++) tt_release(sda[i]);
+                return NULL;
+            }
             n->at.ce.probs = probs;
             n->at.ce.seed = seed;
             n->at.ce.labels = hlab;
+            for (int i = 0; i < 3; i++) n->at.ce.sda[i] = sda[i];
             return n;
         }
+        for (int i = 0; i < 3; i++) tt_release(sda[i]);
         tt_release(rl);
         if (rc < 0) tt_pend = p;  /* not run: the pending GEMM is launched below */
         /* else the GEMM wrote the logits: the softmax-CE runs below */
@@ -826,9 +876,43 @@ static int backward_matmul_fused(AGNode *n, const float *g, const TTHeadCeArgs *
     return 0;
 }
 
+/* The input gradients its softmax-CE formed with the seed (ce_spec), when
+ * they are this pass's: the node's gradient is still exactly that seed (the
+ * loss its only consumer) and the padones and relu feed only this node, as
+ * backward_matmul_fused requires for the same outputs.  Then only dB is left:
+ * a recipe the optimizer's step runs in its own launch.  0 when taken. */
+static long g_spec_taken;  /* backward rules that took them (tth_ce_spec_count) */
+long tth_ce_spec_count(void) { return g_spec_taken; }
+
+static int backward_matmul_spec(AGNode *n) {
+    Tensor *sda[3] = {n->at.mm.sda[0], n->at.mm.sda[1], n->at.mm.sda[2]};
+    for (int i = 0; i < 3; i++) n->at.mm.sda[i] = NULL;
+    AGNode *a = n->in[0], *b = n->in[1];
+    AGNode *x = a->in[0];
+    const int M = (int)a->val->shape[0], K = (int)a->val->shape[1], N = (int)b->val->shape[1];
+    const int ok = n->fanin == 1 && a->op == &OP_PADONES && a->fanin == 1 && !a->grad &&
+                   relu_fusable(x) && !x->grad && needs(b) && tt_defer_enabled() &&
+                   ttk_gemm_tn_padones_any(M, K - 1, N, NULL, NULL, NULL) == 0;
+    Tensor *gb = ok ? tt_empty_like(b->val) : NULL;
+    if (!gb || tt_lazy_gemm_tn_padones(gb, x->val, n->grad, M, K - 1, N) != 0) {
+        tt_release(gb);
+        for (int i = 0; i < 3; i++) tt_release(sda[i]);
+        return -1;
+    }
+    accum_move(b, gb);
+    accum_move(a, sda[0]);
+    accum_move(x, sda[1]);
+    a->fused = 1;
+    accum_move(x->in[0], sda[2]);
+    x->fused = 1;
+    g_spec_taken++;
+    return 0;
+}
+
 static void backward_matmul(AGNode *n) {
     AGNode *a = n->in[0], *b = n->in[1];
     const int M = (int)a->val->shape[0], K = (int)a->val->shape[1], N = (int)b->val->shape[1];
+    if (n->at.mm.sda[0] && backward_matmul_spec(n) == 0) return;
     /* the output gradient is a softmax-CE seed still to be reduced from the
      * logits' partial sums: the classifier kernel forms it itself (and
      * writes the softmax-CE's outputs) */
@@ -1341,6 +1425,14 @@ static void backward_softmax_ce(AGNode *n) {
         if (n->at.ce.labels && !a->grad) {
             a->grad = n->at.ce.seed;
             n->at.ce.seed = NULL;
+            if (n->at.ce.sda[0] && a->op == &OP_MATMUL && !a->at.mm.sda[0]) {
+                /* the seed is the logits' gradient as it stands: the
+                 * classifier's input gradients formed with it go along */
+                for (int i = 0; i < 3; i++) {
+                    a->at.mm.sda[i] = n->at.ce.sda[i];
+                    n->at.ce.sda[i] = NULL;
+                }
+            }
         } else {
             accum_copy(a, n->at.ce.seed);
         }

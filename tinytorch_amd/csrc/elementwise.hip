@@ -683,15 +683,33 @@ gemm_rows_kernel(const float *__restrict__ A, const float *__restrict__ B,
 // 0.0463 ms against a workgroup per row.
 typedef float f32x4r __attribute__((ext_vector_type(4)));
 constexpr int R16W = 8;  // waves per workgroup (sixteen: no faster)
-template <int NCH, bool VA, bool CE>
+struct R16Da {
+  float *dA, *d1, *d2;
+};
+template <int NCH, bool VA, bool CE, bool DA = false>
 __global__ void __launch_bounds__(64 * R16W)
 gemm_rows16_kernel(const float *__restrict__ A, const float *__restrict__ B,
                    const float *__restrict__ bias, float *__restrict__ C, float *__restrict__ R,
                    float *__restrict__ P, int M, int N, int K, int kc, LabU8 lab,
                    float *__restrict__ probs, float *__restrict__ seed,
-                   float *__restrict__ rowloss, float scale) {
+                   float *__restrict__ rowloss, float scale, R16Da da) {
   __shared__ float red[(R16W - 1) * 4 * 64];
   __shared__ float lv[16][17];
+  __shared__ __attribute__((aligned(16))) float gsd[DA ? 16 * 16 : 4];
+  // dA epilogue: lane k (k <= K < 64 * R16W) takes column k of [B; bias]
+  // ((K + 1) x N contiguous) and column k of the tile's rows of A (for the
+  // relu mask), both loaded here, in flight with the GEMM's operands (a load
+  // issued where its row is used costs a memory round trip per row)
+  float wk[DA ? 16 : 1], ak[DA ? 16 : 1];
+  if constexpr (DA) {
+    const int k = min((int)threadIdx.x, K);
+    const int rows = min(16, M - (int)blockIdx.x * 16);
+#pragma unroll
+    for (int jj = 0; jj < 16; jj++) wk[jj] = B[(long)k * N + min(jj, N - 1)];
+    const int ka = min(k, K - 1);
+#pragma unroll
+    for (int mr = 0; mr < 16; mr++) ak[mr] = A[(long)(blockIdx.x * 16 + min(mr, rows - 1)) * K + ka];
+  }
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, q = lane >> 4;
@@ -764,6 +782,54 @@ gemm_rows16_kernel(const float *__restrict__ A, const float *__restrict__ B,
         seed[(long)m * N + j] = sj[0];
       }
       if (j == 0) rowloss[m] = loss;
+      if constexpr (DA) gsd[row * 16 + j] = sj[0];
+    }
+    if constexpr (DA) {
+      // the backward of the layer's input for the tile's rows from the seed
+      // (the logits' gradient when the loss is the only consumer): dA =
+      // seed * [B; bias]^T (M x (K + 1), the padones node's gradient), d1 =
+      // dA without its last column, d2 = d1 where R > 0 (R = A, the relu
+      // output), each sum over j ascending from +0 -- the classifier
+      // backward kernel's (head.hip) dA, bit for bit
+      __syncthreads();
+      const int K1 = K + 1, k = threadIdx.x;
+      const int rows = min(16, M - m0);
+      unsigned pos = 0;  // bit mr: A[m0 + mr][k] > 0
+#pragma unroll
+      for (int mr = 0; mr < 16; mr++) pos |= (ak[mr] > 0.0f ? 1u : 0u) << mr;
+      // four rows at a time: their seeds read from LDS as 16-byte vectors
+      // (one wait for the group, not one a multiply-add)
+      if (k < K1) {
+#pragma unroll
+        for (int m4 = 0; m4 < 16; m4 += 4) {
+          float4 gv[4][4];
+#pragma unroll
+          for (int u = 0; u < 4; u++)
+#pragma unroll
+            for (int v = 0; v < 4; v++)
+              gv[u][v] = *reinterpret_cast<const float4 *>(gsd + (m4 + u) * 16 + 4 * v);
+#pragma unroll
+          for (int u = 0; u < 4; u++) {
+            const int mr = m4 + u;
+            const float g[16] = {gv[u][0].x, gv[u][0].y, gv[u][0].z, gv[u][0].w,
+                                 gv[u][1].x, gv[u][1].y, gv[u][1].z, gv[u][1].w,
+                                 gv[u][2].x, gv[u][2].y, gv[u][2].z, gv[u][2].w,
+                                 gv[u][3].x, gv[u][3].y, gv[u][3].z, gv[u][3].w};
+            float acc = 0.0f;
+#pragma unroll
+            for (int jj = 0; jj < 16; jj++)
+              if (jj < N) acc = acc + g[jj] * wk[jj];
+            if (mr < rows) {
+              const long mm = m0 + mr;
+              da.dA[mm * K1 + k] = acc;
+              if (k < K) {
+                if (da.d1) da.d1[mm * K + k] = acc;
+                if (da.d2) da.d2[mm * K + k] = (pos >> mr) & 1u ? acc : 0.0f;
+              }
+            }
+          }
+        }
+      }
     }
   }
 }
@@ -940,6 +1006,15 @@ extern "C" int ttk_bias_relu_pad(float *c, const float *bias, float *r, float *p
 
 extern "C" int ttk_gemm_rows(const float *A, const float *B, const float *bias, float *C,
                              float *R, float *P, int M, int N, int K, const TTCeHook *ce) {
+  return ttk_gemm_rows_da(A, B, bias, C, R, P, M, N, K, ce, nullptr, nullptr, nullptr);
+}
+
+extern "C" int ttk_gemm_rows_da(const float *A, const float *B, const float *bias, float *C,
+                                float *R, float *P, int M, int N, int K, const TTCeHook *ce,
+                                float *dA, float *d1, float *d2) {
+  if (dA && (!ce || K < 16 || K >= 64 * R16W || bias != B + (long)K * N || N > 16 || M <= 0 ||
+             M > TT_CE_ARG_ROWS || !ce->host_labels))
+    return 1;
   // K <= 1024: four k a thread at most (at the CNN classifier's K = 4096
   // with 128 rows, one workgroup a row measured slower than split-K)
   if (M <= 0 || N <= 0 || N > 16 || K < 0 || K > 1024 || !bias || (ce && (M > TT_CE_ARG_ROWS ||
@@ -953,13 +1028,18 @@ extern "C" int ttk_gemm_rows(const float *A, const float *B, const float *bias, 
     const bool va = ((uintptr_t)A & 15) == 0 && K % 4 == 0;
     const dim3 grid((unsigned)((M + 15) / 16));
 #define TT_R16(NCH_, VA_)                                                                     \
-  if (ce)                                                                                     \
+  if (dA)                                                                                     \
+    hipLaunchKernelGGL((gemm_rows16_kernel<NCH_, VA_, true, true>), grid, dim3(64 * R16W), 0,   \
+                       stream(), A, B, bias, C, R, P, M, N, K, kc, lu, ce->probs, ce->seed,   \
+                       ce->rowloss, ce->scale, R16Da{dA, d1, d2});                            \
+  else if (ce)                                                                                \
     hipLaunchKernelGGL((gemm_rows16_kernel<NCH_, VA_, true>), grid, dim3(64 * R16W), 0, stream(), A, \
                        B, bias, C, R, P, M, N, K, kc, lu, ce->probs, ce->seed, ce->rowloss,   \
-                       ce->scale);                                                            \
+                       ce->scale, R16Da{});                                                   \
   else                                                                                        \
     hipLaunchKernelGGL((gemm_rows16_kernel<NCH_, VA_, false>), grid, dim3(64 * R16W), 0, stream(),   \
-                       A, B, bias, C, R, P, M, N, K, kc, lu, nullptr, nullptr, nullptr, 0.0f)
+                       A, B, bias, C, R, P, M, N, K, kc, lu, nullptr, nullptr, nullptr, 0.0f, \
+                       R16Da{})
 #define TT_R16V(NCH_) \
   if (va) { TT_R16(NCH_, true); } else { TT_R16(NCH_, false); }
     switch (nch) {

@@ -1662,10 +1662,11 @@ gemm_small_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
   small_tile<A_KC, B_NC, VA, VB>(M, N, K, A, lda, B, ldb, out, kc, blockIdx.x, blockIdx.y, red);
 }
 
-// The weight gradient [X, 1]^T G of tt_k_gemm_tn_padones and an SGD step in
-// one launch: workgroups [0, gblocks) are the GEMM's tiles (gx across),
-// each also stepping its tile of wsgd; the rest step the plain tensors of
-// P, a thread an element (sgd_sub, as sgd_multi_kernel).
+// The weight gradients [X, 1]^T G of up to two tt_k_gemm_tn_padones jobs and
+// an SGD step in one launch: workgroups [0, J.j[0].gblocks) are job 0's
+// tiles (gx across), the next J.j[1].gblocks job 1's, each also stepping its
+// tile of the job's wsgd; the rest step the plain tensors of P, a thread an
+// element (sgd_sub, as sgd_multi_kernel).
 struct SgdPlain {
   float *w[TT_SGD_MAX];
   const float *g[TT_SGD_MAX];
@@ -1674,26 +1675,36 @@ struct SgdPlain {
   int np;
   float lr;
 };
+struct TnJob {
+  int M, N, K, kc, ones_m, gx, gblocks;
+  const float *A, *B;
+  float *C, *wsgd;
+};
+struct TnJobs {
+  TnJob j[2];
+  int nj;
+};
 __global__ void __launch_bounds__(64 * SW)
-gemm_tn_padones_sgd_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
-                           const float *__restrict__ B, long ldb, float *__restrict__ C,
-                           long ldc, int kc, int ones_m, float *__restrict__ wsgd, int gx,
-                           int gblocks, SgdPlain P) {
+gemm_tn_padones_sgd_kernel(TnJobs J, SgdPlain P) {
   __shared__ float red[(SW - 1) * 16 * 64];
-  if ((int)blockIdx.x >= gblocks) {
-    const long b = blockIdx.x - gblocks;
-    int t = 0;
-    while (t + 1 < P.np && b >= P.start[t + 1]) t++;
-    const long i = (b - P.start[t]) * (64 * SW) + threadIdx.x;
-    if (i < P.n[t]) P.w[t][i] = sgd_sub(P.w[t][i], P.lr, P.g[t][i]);
-    return;
+  int b = blockIdx.x;
+  for (int q = 0; q < J.nj; q++) {
+    const TnJob &t = J.j[q];
+    if (b < t.gblocks) {
+      SmallOut out{t.C, t.N, nullptr, nullptr, nullptr};
+      out.ones_m = t.ones_m;
+      out.wsgd = t.wsgd;
+      out.lr = P.lr;
+      small_tile<false, true, false, false>(t.M, t.N, t.K, t.A, t.ones_m, t.B, t.N, out, t.kc,
+                                            b % t.gx, b / t.gx, red);
+      return;
+    }
+    b -= t.gblocks;
   }
-  SmallOut out{C, ldc, nullptr, nullptr, nullptr};
-  out.ones_m = ones_m;
-  out.wsgd = wsgd;
-  out.lr = P.lr;
-  small_tile<false, true, false, false>(M, N, K, A, lda, B, ldb, out, kc, blockIdx.x % gx,
-                                        blockIdx.x / gx, red);
+  int k = 0;
+  while (k + 1 < P.np && b >= P.start[k + 1]) k++;
+  const long i = (b - P.start[k]) * (64 * SW) + threadIdx.x;
+  if (i < P.n[k]) P.w[k][i] = sgd_sub(P.w[k][i], P.lr, P.g[k][i]);
 }
 
 // The same tiles with a forward epilogue (SmallOut::bias / relu / pad).
@@ -2270,18 +2281,52 @@ extern "C" int tt_k_gemm_tn_padones(int rows, int Kx, int N, const float *X, con
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
-// tt_k_gemm_tn_padones and the SGD step wsgd -= lr * dW plus the plain
-// steps pw -= lr * pg, in one launch.  1: not covered, nothing launched.
-extern "C" int ttk_gemm_tn_padones_sgd(int rows, int Kx, int N, const float *X, const float *G,
-                                       float *dW, float *wsgd, float lr, float *const *pw,
-                                       const float *const *pg, const long *pn, int np) {
-  if (!X || !G || !dW || !wsgd || np < 0 || np > TT_SGD_MAX ||
-      tt_k_gemm_tn_padones(rows, Kx, N, nullptr, nullptr, nullptr) != 0)
-    return 1;
+// tt_k_gemm_tn_padones on any shape its tiles can index, also where the
+// planner would pick another kernel (few tiles: a classifier's 257 x 10
+// weight gradient) -- for a gradient computed inside another launch or
+// materialised on its own after all.  NULL dW: only asks.
+extern "C" int ttk_gemm_tn_padones_any(int rows, int Kx, int N, const float *X, const float *G,
+                                       float *dW) {
+  if (rows <= 0 || Kx <= 0 || N <= 0 || (Kx + 1 + 31) / 32 > 65535) return -1;
+  if (!dW) return 0;
+  if (!X || !G) return -1;
   const int M = Kx + 1;
   const int kc = ((rows + SW - 1) / SW + 7) / 8 * 8;
-  const int gx = (N + 31) / 32, gy = (M + 31) / 32;
-  const long gblocks = (long)gx * gy;
+  const dim3 grid((unsigned)((N + 31) / 32), (unsigned)((M + 31) / 32));
+  hipLaunchKernelGGL((gemm_small_kernel<false, true, false, false>), grid, dim3(64 * SW), 0,
+                     stream(), M, N, rows, X, (long)Kx, G, (long)N, dW, (long)N, kc, Kx);
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+// Up to two tt_k_gemm_tn_padones jobs, each with the SGD step wsgd -= lr *
+// dW, plus the plain steps pw -= lr * pg, in one launch.  1: not covered,
+// nothing launched.
+extern "C" int ttk_gemm_tn_padones_sgd_jobs(const TTTnSgdJob *jobs, int nj, float lr,
+                                            float *const *pw, const float *const *pg,
+                                            const long *pn, int np) {
+  if (nj < 1 || nj > 2 || np < 0 || np > TT_SGD_MAX) return 1;
+  TnJobs J{};
+  J.nj = nj;
+  long gtot = 0;
+  for (int q = 0; q < nj; q++) {
+    const TTTnSgdJob &a = jobs[q];
+    if (!a.X || !a.G || !a.dW || !a.wsgd ||
+        ttk_gemm_tn_padones_any(a.rows, a.Kx, a.N, nullptr, nullptr, nullptr) != 0)
+      return 1;
+    TnJob &t = J.j[q];
+    t.M = a.Kx + 1;
+    t.N = a.N;
+    t.K = a.rows;
+    t.kc = ((a.rows + SW - 1) / SW + 7) / 8 * 8;
+    t.ones_m = a.Kx;
+    t.gx = (a.N + 31) / 32;
+    t.gblocks = t.gx * ((t.M + 31) / 32);
+    t.A = a.X;
+    t.B = a.G;
+    t.C = a.dW;
+    t.wsgd = a.wsgd;
+    gtot += t.gblocks;
+  }
   SgdPlain P{};
   P.np = np;
   P.lr = lr;
@@ -2294,11 +2339,17 @@ extern "C" int ttk_gemm_tn_padones_sgd(int rows, int Kx, int N, const float *X, 
     tot += (pn[t] + 64 * SW - 1) / (64 * SW);
   }
   P.start[np] = tot;
-  if (gblocks + tot > 0x7fffffffL) return 1;
-  hipLaunchKernelGGL(gemm_tn_padones_sgd_kernel, dim3((unsigned)(gblocks + tot)), dim3(64 * SW),
-                     0, stream(), M, N, rows, X, (long)Kx, G, (long)N, dW, (long)N, kc, Kx, wsgd,
-                     gx, (int)gblocks, P);
+  if (gtot + tot > 0x7fffffffL) return 1;
+  hipLaunchKernelGGL(gemm_tn_padones_sgd_kernel, dim3((unsigned)(gtot + tot)), dim3(64 * SW), 0,
+                     stream(), J, P);
   return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+extern "C" int ttk_gemm_tn_padones_sgd(int rows, int Kx, int N, const float *X, const float *G,
+                                       float *dW, float *wsgd, float lr, float *const *pw,
+                                       const float *const *pg, const long *pn, int np) {
+  const TTTnSgdJob j{rows, Kx, N, X, G, dW, wsgd};
+  return ttk_gemm_tn_padones_sgd_jobs(&j, 1, lr, pw, pg, pn, np);
 }
 
 // C = A * B + bias (A M x K, B K x N row-major and contiguous; bias a row of

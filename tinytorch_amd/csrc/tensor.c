@@ -312,42 +312,53 @@ int tt_lazy_dwt_sgd(float *const *w, Tensor *const *g, const long *n, int count,
 
 int tt_lazy_gemm_sgd(float *const *w, Tensor *const *g, const long *n, int count, float lr) {
     if (count <= 0 || count > TT_SGD_MAX || !g_lazy_vals) return 1;
-    TTLazyVal *pend = NULL;
-    int at = -1;
+    TTLazyVal *pend[2] = {NULL, NULL};
+    int at[2] = {-1, -1}, nj = 0;
     for (int i = 0; i < count; i++) {
         for (TTLazyVal *l = g_lazy_vals; l; l = l->next)
             if (l->kind == 4 && l->t == g[i]) {
-                if (pend) return 1;  /* one such gradient a launch */
-                pend = l;
-                at = i;
+                if (nj == 2) return 1;  /* two such gradients a launch */
+                pend[nj] = l;
+                at[nj++] = i;
             }
         for (int k = 0; k < i; k++)
             if (g[k] == g[i] || w[k] == w[i]) return 1;
     }
-    if (!pend) return 1;
-    const float *x = tt_dev(pend->src), *gg = tt_dev(pend->src2);
-    if (!x || !gg) return -1;
+    if (!nj) return 1;
+    TTTnSgdJob jobs[2];
+    for (int q = 0; q < nj; q++) {
+        const float *x = tt_dev(pend[q]->src), *gg = tt_dev(pend[q]->src2);
+        if (!x || !gg) return -1;
+        jobs[q].rows = pend[q]->dims[0];
+        jobs[q].Kx = pend[q]->dims[1];
+        jobs[q].N = pend[q]->dims[2];
+        jobs[q].X = x;
+        jobs[q].G = gg;
+        jobs[q].dW = pend[q]->t->dev;
+        jobs[q].wsgd = w[at[q]];
+    }
     float *pw[TT_SGD_MAX];
     const float *pg[TT_SGD_MAX];
     long pn[TT_SGD_MAX];
     int np = 0;
     for (int i = 0; i < count; i++) {
-        if (i == at) continue;
+        if (i == at[0] || i == at[1]) continue;
         pw[np] = w[i];
         pn[np] = n[i];
         if (!(pg[np] = tt_dev(g[i]))) return -1;
         np++;
     }
-    const int rc = ttk_gemm_tn_padones_sgd(pend->dims[0], pend->dims[1], pend->dims[2], x, gg,
-                                           pend->t->dev, w[at], lr, pw, pg, pn, np);
+    const int rc = ttk_gemm_tn_padones_sgd_jobs(jobs, nj, lr, pw, pg, pn, np);
     if (rc == 1) return 1;
-    for (TTLazyVal **pp = &g_lazy_vals; *pp; pp = &(*pp)->next)
-        if (*pp == pend) { *pp = pend->next; break; }
-    if (rc != 0) pend->t->valid = 0;
-    else tt_mark_dev_written(pend->t);
-    tt_release(pend->src);
-    tt_release(pend->src2);
-    free(pend);
+    for (int q = 0; q < nj; q++) {
+        for (TTLazyVal **pp = &g_lazy_vals; *pp; pp = &(*pp)->next)
+            if (*pp == pend[q]) { *pp = pend[q]->next; break; }
+        if (rc != 0) pend[q]->t->valid = 0;
+        else tt_mark_dev_written(pend[q]->t);
+        tt_release(pend[q]->src);
+        tt_release(pend[q]->src2);
+        free(pend[q]);
+    }
     return rc;
 }
 
@@ -496,8 +507,8 @@ restart:
                            : l->kind == 1 ? tt_k_padones_fwd(x, l->t->dev, l->t->shape[0],
                                                              l->t->shape[1] - 1)
                            : l->kind == 2 ? tt_k_ce_mean_rows(x, l->t->dev, (int)l->src->numel)
-                           : l->kind == 4 ? tt_k_gemm_tn_padones(l->dims[0], l->dims[1],
-                                                                 l->dims[2], x, x2, l->t->dev)
+                           : l->kind == 4 ? ttk_gemm_tn_padones_any(l->dims[0], l->dims[1],
+                                                                    l->dims[2], x, x2, l->t->dev)
                            : l->kind == 5 ? tt_conv_fwd_any(x, l->buf,
                                                             l->buf + (long)l->q[4] * l->q[1] *
                                                                          l->q[5] * l->q[6],

@@ -100,8 +100,9 @@ int tt_lazy_dwt_sgd(float *const *w, Tensor *const *g, const long *n, int count,
 /* dw (Kx+1 x N) = [x, 1]^T g, the weight gradient of a matmul of padones(x)
  * (x rows x Kx, g rows x N), written on first use; 0 ok, -1 no memory */
 int tt_lazy_gemm_tn_padones(Tensor *dw, Tensor *x, Tensor *g, int rows, int Kx, int N);
-/* as tt_lazy_dwt_sgd, for one pending tt_lazy_gemm_tn_padones gradient: the
- * GEMM (stepping its weights) and the other tensors' steps in one launch */
+/* as tt_lazy_dwt_sgd, for one or two pending tt_lazy_gemm_tn_padones
+ * gradients: the GEMMs (stepping their weights) and the other tensors' steps
+ * in one launch */
 int tt_lazy_gemm_sgd(float *const *w, Tensor *const *g, const long *n, int count, float lr);
 /* out = logits, probs, seed, row losses of a softmax-CE (allocated,
  * unwritten): one ttk_reduce_ce of ws (2 x M x N partial sums, then owned by

@@ -111,6 +111,18 @@ int    ttk_dwt_reduce_sgd(const TTDwtJob *jobs, float *const *wdw, float *const 
 int    ttk_gemm_tn_padones_sgd(int rows, int Kx, int N, const float *X, const float *G,
                                float *dW, float *wsgd, float lr, float *const *pw,
                                const float *const *pg, const long *pn, int np);
+/* gemm.hip: tt_k_gemm_tn_padones on every shape its tiles index (not only
+ * where the planner picks them); NULL dW only asks.  0 ok, -1 not covered */
+int    ttk_gemm_tn_padones_any(int rows, int Kx, int N, const float *X, const float *G,
+                               float *dW);
+/* the same for up to two jobs (dW = [X, 1]^T G, wsgd -= lr * dW each) */
+typedef struct {
+    int rows, Kx, N;
+    const float *X, *G;
+    float *dW, *wsgd;
+} TTTnSgdJob;
+int    ttk_gemm_tn_padones_sgd_jobs(const TTTnSgdJob *jobs, int nj, float lr, float *const *pw,
+                                    const float *const *pg, const long *pn, int np);
 /* conv.hip: free a job's partials without reducing them */
 void   ttk_dwt_job_drop(TTDwtJob *job);
 /* elementwise.hip: C = A * B + bias (A M x K, B K x N row-major) for N <= 16,
@@ -120,6 +132,15 @@ void   ttk_dwt_job_drop(TTDwtJob *job);
  * launched. */
 int    ttk_gemm_rows(const float *A, const float *B, const float *bias, float *C, float *R,
                      float *P, int M, int N, int K, const TTCeHook *ce);
+/* ttk_gemm_rows with ce and, for the rows' softmax-CE seed g, the backward
+ * of the layer's input [A, 1] (B's rows followed by the bias row, bias == B +
+ * K * N): dA = g [B; bias]^T (M x (K + 1)), d1 = dA without its last column
+ * and d2 = d1 where A > 0 (d1, d2 may be NULL) -- the classifier backward
+ * kernel's dA outputs, bit for bit.  1: not covered (the 16-row kernel only:
+ * 16 <= K < 512, N <= 16), nothing launched. */
+int    ttk_gemm_rows_da(const float *A, const float *B, const float *bias, float *C, float *R,
+                        float *P, int M, int N, int K, const TTCeHook *ce, float *dA, float *d1,
+                        float *d2);
 
 /* gemm.hip: look up, on the current device, the device address of the
  * static scratch array behind tt_k_gemm_noalloc; 0 ok */
