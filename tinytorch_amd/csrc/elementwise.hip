@@ -696,20 +696,33 @@ gemm_rows16_kernel(const float *__restrict__ A, const float *__restrict__ B,
   __shared__ float red[(R16W - 1) * 4 * 64];
   __shared__ float lv[16][17];
   __shared__ __attribute__((aligned(16))) float gsd[DA ? 16 * 16 : 4];
-  // dA epilogue: lane k (k <= K < 64 * R16W) takes column k of [B; bias]
-  // ((K + 1) x N contiguous) and column k of the tile's rows of A (for the
-  // relu mask), both loaded here, in flight with the GEMM's operands (a load
-  // issued where its row is used costs a memory round trip per row)
-  float wk[DA ? 16 : 1], ak[DA ? 16 : 1];
-  if constexpr (DA) {
-    const int k = min((int)threadIdx.x, K);
+  __shared__ float bsd[16];
+  __shared__ float wsd[DA ? 4096 : 1];
+  // dA epilogue: lane t takes columns k = t % 256 (+ 256 ...) of [B; bias]
+  // and of A for rows 8 (t / 256) .. + 7 of the tile.  Loaded here, in flight
+  // with the GEMM's operands (a load issued where its row is used costs a
+  // memory round trip per row): the A values of the first column (for the
+  // relu mask) and [B; bias] itself, coalesced, for LDS (each lane then
+  // reads its column's N weights from there).
+  constexpr int WPT = 4096 / (64 * R16W);  // [B; bias] floats a thread stages
+  float ak[DA ? 8 : 1], wv[DA ? WPT : 1];
+  auto da_load_a = [&](int k) {
+    const int kk = min(k, K - 1), h = threadIdx.x >> 8;
     const int rows = min(16, M - (int)blockIdx.x * 16);
 #pragma unroll
-    for (int jj = 0; jj < 16; jj++) wk[jj] = B[(long)k * N + min(jj, N - 1)];
-    const int ka = min(k, K - 1);
+    for (int u = 0; u < 8; u++)
+      ak[u] = A[(long)(blockIdx.x * 16 + min(8 * h + u, rows - 1)) * K + kk];
+  };
+  if constexpr (DA) {
+    da_load_a(threadIdx.x & 255);
 #pragma unroll
-    for (int mr = 0; mr < 16; mr++) ak[mr] = A[(long)(blockIdx.x * 16 + min(mr, rows - 1)) * K + ka];
+    for (int u = 0; u < WPT; u++)
+      wv[u] = B[min((int)threadIdx.x + 64 * R16W * u, (K + 1) * N - 1)];
   }
+  // the epilogue's bias and label, loaded with the operands (a load issued
+  // after the reduction is one more memory round trip before the stores)
+  const float bnr = bias[min((int)(threadIdx.x & 15), N - 1)];
+  const int ylab = CE ? lab[min((int)blockIdx.x * 16 + (int)(threadIdx.x >> 4), M - 1)] : 0;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, q = lane >> 4;
@@ -758,7 +771,7 @@ gemm_rows16_kernel(const float *__restrict__ A, const float *__restrict__ B,
     for (int i = 0; i < 4; i++) {
       const int m = m0 + 4 * q + i;
       if (m < M && n < N) {
-        const float v = acc[i] + bias[n];
+        const float v = acc[i] + bnr;
         C[(long)m * N + n] = v;
         const float o = v > 0.0f ? v : 0.0f;
         if (R) R[(long)m * N + n] = o;
@@ -769,6 +782,7 @@ gemm_rows16_kernel(const float *__restrict__ A, const float *__restrict__ B,
         lv[4 * q + i][n] = v;
       }
     }
+    if (DA && q == 0 && n < N) bsd[n] = bnr;
   }
   if constexpr (CE) {
     // the tile's 16 rows, 16 lanes a row (ce_row_group: the bits of ce_row)
@@ -776,7 +790,7 @@ gemm_rows16_kernel(const float *__restrict__ A, const float *__restrict__ B,
     const int t = threadIdx.x, row = t >> 4, j = t & 15, m = m0 + row;
     if (t < 256 && m < M) {
       float xj[1] = {lv[row][j]}, pj[1], sj[1];
-      const float loss = ce_row_group<16, 1>(xj, lab[m], N, scale, pj, sj);
+      const float loss = ce_row_group<16, 1>(xj, ylab, N, scale, pj, sj);
       if (j < N) {
         probs[(long)m * N + j] = pj[0];
         seed[(long)m * N + j] = sj[0];
@@ -791,26 +805,32 @@ gemm_rows16_kernel(const float *__restrict__ A, const float *__restrict__ B,
       // dA without its last column, d2 = d1 where R > 0 (R = A, the relu
       // output), each sum over j ascending from +0 -- the classifier
       // backward kernel's (head.hip) dA, bit for bit
+#pragma unroll
+      for (int u = 0; u < WPT; u++) wsd[threadIdx.x + 64 * R16W * u] = wv[u];
       __syncthreads();
-      const int K1 = K + 1, k = threadIdx.x;
+      const int K1 = K + 1, h = threadIdx.x >> 8;
       const int rows = min(16, M - m0);
-      unsigned pos = 0;  // bit mr: A[m0 + mr][k] > 0
+      for (int k = threadIdx.x & 255; k < K; k += 256) {
+        if (k >= 256) da_load_a(k);
+        float wk[16];
 #pragma unroll
-      for (int mr = 0; mr < 16; mr++) pos |= (ak[mr] > 0.0f ? 1u : 0u) << mr;
-      // four rows at a time: their seeds read from LDS as 16-byte vectors
-      // (one wait for the group, not one a multiply-add)
-      if (k < K1) {
+        for (int jj = 0; jj < 16; jj++) wk[jj] = wsd[k * N + min(jj, N - 1)];
+        unsigned pos = 0;  // bit u: A[m0 + 8 h + u][k] > 0
 #pragma unroll
-        for (int m4 = 0; m4 < 16; m4 += 4) {
+        for (int u = 0; u < 8; u++) pos |= (ak[u] > 0.0f ? 1u : 0u) << u;
+        // four rows at a time: their seeds read from LDS as 16-byte vectors
+        // (one wait for the group, not one a multiply-add)
+#pragma unroll
+        for (int m4 = 0; m4 < 8; m4 += 4) {
           float4 gv[4][4];
 #pragma unroll
           for (int u = 0; u < 4; u++)
 #pragma unroll
             for (int v = 0; v < 4; v++)
-              gv[u][v] = *reinterpret_cast<const float4 *>(gsd + (m4 + u) * 16 + 4 * v);
+              gv[u][v] = *reinterpret_cast<const float4 *>(gsd + (8 * h + m4 + u) * 16 + 4 * v);
 #pragma unroll
           for (int u = 0; u < 4; u++) {
-            const int mr = m4 + u;
+            const int mr = 8 * h + m4 + u;
             const float g[16] = {gv[u][0].x, gv[u][0].y, gv[u][0].z, gv[u][0].w,
                                  gv[u][1].x, gv[u][1].y, gv[u][1].z, gv[u][1].w,
                                  gv[u][2].x, gv[u][2].y, gv[u][2].z, gv[u][2].w,
@@ -822,13 +842,18 @@ gemm_rows16_kernel(const float *__restrict__ A, const float *__restrict__ B,
             if (mr < rows) {
               const long mm = m0 + mr;
               da.dA[mm * K1 + k] = acc;
-              if (k < K) {
-                if (da.d1) da.d1[mm * K + k] = acc;
-                if (da.d2) da.d2[mm * K + k] = (pos >> mr) & 1u ? acc : 0.0f;
-              }
+              if (da.d1) da.d1[mm * K + k] = acc;
+              if (da.d2) da.d2[mm * K + k] = (pos >> (m4 + u)) & 1u ? acc : 0.0f;
             }
           }
         }
+      }
+      // the ones column of dA (the bias row of B): a lane a row
+      if ((int)threadIdx.x < rows) {
+        const float *g = gsd + threadIdx.x * 16, *bw = bsd;
+        float acc = 0.0f;
+        for (int jj = 0; jj < N; jj++) acc = acc + g[jj] * bw[jj];
+        da.dA[(long)(m0 + threadIdx.x) * K1 + K] = acc;
       }
     }
   }
@@ -1012,8 +1037,8 @@ extern "C" int ttk_gemm_rows(const float *A, const float *B, const float *bias, 
 extern "C" int ttk_gemm_rows_da(const float *A, const float *B, const float *bias, float *C,
                                 float *R, float *P, int M, int N, int K, const TTCeHook *ce,
                                 float *dA, float *d1, float *d2) {
-  if (dA && (!ce || K < 16 || K >= 64 * R16W || bias != B + (long)K * N || N > 16 || M <= 0 ||
-             M > TT_CE_ARG_ROWS || !ce->host_labels))
+  if (dA && (!ce || K < 16 || K >= 64 * R16W || bias != B + (long)K * N || N > 16 ||
+             (long)(K + 1) * N > 4096 || M <= 0 || M > TT_CE_ARG_ROWS || !ce->host_labels))
     return 1;
   // K <= 1024: four k a thread at most (at the CNN classifier's K = 4096
   // with 128 rows, one workgroup a row measured slower than split-K)

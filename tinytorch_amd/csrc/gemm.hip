@@ -1574,6 +1574,28 @@ __device__ __forceinline__ void small_tile(int M, int N, int K, const float *__r
 #pragma unroll
       for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[g][i], b[g][i], acc, 0, 0, 0);
   };
+  // wave 0's epilogue operands -- the relu outputs and the weights to step of
+  // its 16 elements -- loaded before the K loop, clamped to the matrix, so
+  // that they arrive with the first operands (loaded after the wave sums,
+  // they cost one more memory round trip before the stores)
+  const int ne = min(n0 + l32, N - 1);
+  float rv[16], wv[16];
+  if (w == 0 && out.R) {
+    const int nc = ne < N - 1 ? ne : (N > 1 ? N - 2 : 0);
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int m = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
+      rv[r] = out.R[(long)(m < M ? m : M - 1) * (N - 1) + nc];
+    }
+  }
+  if (w == 0 && out.wsgd) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int m = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
+      wv[r] = out.wsgd[(long)(m < M ? m : M - 1) * out.ldc + ne];
+    }
+  }
+  const float bn = w == 0 && out.bias ? out.bias[ne] : 0.0f;
   constexpr int CK = 8 * SG;  // k per chunk
   float a0[SG][4], b0[SG][4], a1[SG][4], b1[SG][4];
   if (k0 < k1) load(k0, a0, b0);
@@ -1597,20 +1619,7 @@ __device__ __forceinline__ void small_tile(int M, int N, int K, const float *__r
   const int n = n0 + l32;
   if (n >= N) return;
   const bool pad = out.d1 || out.d2;
-  // the relu outputs of this lane's 16 elements, loaded up front and
-  // unconditionally (clamped to the matrix): a load under the store's
-  // branches would wait for its own round trip
-  float rv[16];
-  if (out.R) {
-    const int nc = n < N - 1 ? n : (N > 1 ? N - 2 : 0);
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int m = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
-      rv[r] = out.R[(long)(m < M ? m : M - 1) * (N - 1) + nc];
-    }
-  }
   if (out.bias) {  // forward: C = acc + bias[n], and its relu / padded relu
-    const float bn = out.bias[n];
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       const int m = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
@@ -1627,14 +1636,6 @@ __device__ __forceinline__ void small_tile(int M, int N, int K, const float *__r
       }
     }
     return;
-  }
-  float wv[16];
-  if (out.wsgd) {  // loaded up front, clamped, as rv
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int m = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
-      wv[r] = out.wsgd[(long)(m < M ? m : M - 1) * out.ldc + n];
-    }
   }
 #pragma unroll
   for (int r = 0; r < 16; r++) {
@@ -1742,6 +1743,11 @@ gemm_t16_epi_kernel(int M, int N, int K, const float *__restrict__ A,
   const int mr = min(m0 + r, M - 1);
   const int k0 = w * kc, k1 = min(K, k0 + kc);
   const float *__restrict__ ap = A + (long)mr * K;
+  // the epilogue's bias, loaded with the operands (a load issued after the
+  // wave sums is one more memory round trip before the stores)
+  float bnv[TN];
+#pragma unroll
+  for (int t = 0; t < TN; t++) bnv[t] = out.bias[min(n0 + 16 * t + r, N - 1)];
   float4 av[NCH];
   float bv[NCH][TN][4];
 #pragma unroll
@@ -1789,7 +1795,7 @@ gemm_t16_epi_kernel(int M, int N, int K, const float *__restrict__ A,
   for (int t = 0; t < TN; t++) {
     const int n = n0 + 16 * t + r;
     if (n >= N) continue;
-    const float bn = out.bias[n];
+    const float bn = bnv[t];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int m = m0 + 4 * q + i;

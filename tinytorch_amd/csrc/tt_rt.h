@@ -137,7 +137,7 @@ int    ttk_gemm_rows(const float *A, const float *B, const float *bias, float *C
  * K * N): dA = g [B; bias]^T (M x (K + 1)), d1 = dA without its last column
  * and d2 = d1 where A > 0 (d1, d2 may be NULL) -- the classifier backward
  * kernel's dA outputs, bit for bit.  1: not covered (the 16-row kernel only:
- * 16 <= K < 512, N <= 16), nothing launched. */
+ * 16 <= K < 512, N <= 16, (K + 1) * N <= 4096), nothing launched. */
 int    ttk_gemm_rows_da(const float *A, const float *B, const float *bias, float *C, float *R,
                         float *P, int M, int N, int K, const TTCeHook *ce, float *dA, float *d1,
                         float *d2);
