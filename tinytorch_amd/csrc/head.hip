@@ -162,21 +162,27 @@ constexpr int DA_M = 32;  // rows m per dA workgroup (8 per lane)
 // sums of its logits (see above) into gl (row r at gl[(r - r0) * gs]); `out`:
 // also store the softmax-CE's outputs of those rows.  The rows' partial sums
 // are first loaded whole-workgroup (coalesced) into pp (2 (r1 - r0) N floats
-// of LDS); four lanes a row then form its softmax-CE.  Every thread calls
-// it (barriers inside).
+// of LDS) with the rows' labels; four lanes a row then form its softmax-CE.
+// Every thread calls it (barriers inside).
 template <int NC>
 __device__ __forceinline__ void head_ce_seed(const TTHeadCe &ce, int r0, int r1, int M, int N,
                                              float *gl, int gs, bool out, float *pp) {
   const int n = (r1 - r0) * N;
   const long total = (long)M * N;
+  // four lanes a row (ce_row_group): lane q takes columns [q CPL, q CPL + CPL)
+  constexpr int GW = 4, CPL = (NC + GW - 1) / GW;
+  const int q = threadIdx.x & (GW - 1);
+  float bq[CPL];  // this lane's bias values, loaded with the partial sums
+#pragma unroll
+  for (int u = 0; u < CPL; u++) bq[u] = ce.bias[min(q * CPL + u, N - 1)];
   for (int i = threadIdx.x; i < n; i += NT) {
     pp[i] = ce.part[(long)r0 * N + i];
     pp[n + i] = ce.part[total + (long)r0 * N + i];
   }
+  // the rows' labels too (read in the loop below, each was a round trip)
+  int *yl = reinterpret_cast<int *>(pp + 2 * n);
+  for (int i = threadIdx.x; i < r1 - r0; i += NT) yl[i] = ce.lab[r0 + i];
   __syncthreads();
-  // four lanes a row (ce_row_group): lane q takes columns [q CPL, q CPL + CPL)
-  constexpr int GW = 4, CPL = (NC + GW - 1) / GW;
-  const int q = threadIdx.x & (GW - 1);
   for (int r = r0 + (int)(threadIdx.x / GW); r < r1; r += NT / GW) {
     float lv[CPL], pr[CPL], sr[CPL];
     const float *p0 = pp + (r - r0) * N;
@@ -188,13 +194,13 @@ __device__ __forceinline__ void head_ce_seed(const TTHeadCe &ce, int r0, int r1,
         float s = 0.0f;
         s += p0[j];
         s += p0[n + j];
-        lv[u] = s + ce.bias[j];
+        lv[u] = s + bq[u];
       }
     }
     float lg[CPL];
 #pragma unroll
     for (int u = 0; u < CPL; u++) lg[u] = lv[u];
-    const float loss = ce_row_group<GW, CPL>(lv, ce.lab[r], N, ce.scale, pr, sr);
+    const float loss = ce_row_group<GW, CPL>(lv, yl[r - r0], N, ce.scale, pr, sr);
 #pragma unroll
     for (int u = 0; u < CPL; u++)
       if (q * CPL + u < N) gl[(r - r0) * gs + q * CPL + u] = sr[u];
@@ -257,13 +263,26 @@ head_bwd_kernel(const float *__restrict__ A, int M, int K, const float *__restri
   const int k = k0 + kl;
   const int K1 = K - 1;
   constexpr int MI = DA_M / 4;  // rows per lane: m0 + mg + 4 i
+  // the relu outputs and pool codes of this lane's outputs, loaded before
+  // the barrier, clamped to the matrix (a load issued at its store costs a
+  // memory round trip per row)
   float rv[MI];
-  if (R && d2) {
+  unsigned char cv[MI];
+  {
     const int kc = k < K1 ? k : K1 - 1;
+    if (R && d2) {
 #pragma unroll
-    for (int i = 0; i < MI; i++) {
-      const int m = m0 + mg + 4 * i;
-      rv[i] = R[(long)(m < M ? m : M - 1) * K1 + kc];
+      for (int i = 0; i < MI; i++) {
+        const int m = m0 + mg + 4 * i;
+        rv[i] = R[(long)(m < M ? m : M - 1) * K1 + kc];
+      }
+    }
+    if (dc) {
+#pragma unroll
+      for (int i = 0; i < MI; i++) {
+        const int m = m0 + mg + 4 * i;
+        cv[i] = codes[(long)(m < M ? m : M - 1) * K1 + kc];
+      }
     }
   }
   __syncthreads();
@@ -297,7 +316,7 @@ head_bwd_kernel(const float *__restrict__ A, int M, int K, const float *__restri
           // window's code (bits 0-1 argmax, 2-5 relu mask), as
           // maxpool2x2_code_bwd_kernel writes it
           const int fc = k / P2, rem = k - fc * P2, h2 = rem / Wo2, w2 = rem - h2 * Wo2;
-          const unsigned c = codes[o];
+          const unsigned c = cv[i];
           const float g0 = 0.0f + s;
           auto at = [&](unsigned q) { return ((c & 3) == q && ((c >> (2 + q)) & 1)) ? g0 : 0.0f; };
           float *dr = dc + ((long)(m * (K1 / P2) + fc) * (2 * (P2 / Wo2)) + 2 * h2) * (2 * Wo2) +
@@ -329,7 +348,7 @@ static int head_bwd(const float *A, int M, int K, const float *W, int N, const f
   if (ce && dW && M > 32 * (NT / KW)) return -1;  // one batch of A rows (head_dw_block)
   size_t lds = lds_w > lds_a ? lds_w : lds_a;
   const int gl_off = (int)(lds / sizeof(float));
-  if (ce) lds += sizeof(float) * (size_t)3 * M * N;  // the output gradient and partials in LDS
+  if (ce) lds += sizeof(float) * (size_t)(3 * M * N + M);  // output gradient, partials, labels
   if (lds > 64 * 1024) return -1;
   const TTHeadCe none{};
   const TTHeadCe &hc = ce ? *ce : none;
