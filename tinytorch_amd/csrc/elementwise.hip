@@ -686,6 +686,7 @@ constexpr int R16W = 8;  // waves per workgroup (sixteen: no faster)
 struct R16Da {
   float *dA, *d1, *d2;
 };
+constexpr int R16_DA_COLS = 64;  // columns of dA a workgroup
 template <int NCH, bool VA, bool CE, bool DA = false>
 __global__ void __launch_bounds__(64 * R16W)
 gemm_rows16_kernel(const float *__restrict__ A, const float *__restrict__ B,
@@ -697,27 +698,28 @@ gemm_rows16_kernel(const float *__restrict__ A, const float *__restrict__ B,
   __shared__ float lv[16][17];
   __shared__ __attribute__((aligned(16))) float gsd[DA ? 16 * 16 : 4];
   __shared__ float bsd[16];
-  __shared__ float wsd[DA ? 4096 : 1];
-  // dA epilogue: lane t takes columns k = t % 256 (+ 256 ...) of [B; bias]
-  // and of A for rows 8 (t / 256) .. + 7 of the tile.  Loaded here, in flight
-  // with the GEMM's operands (a load issued where its row is used costs a
-  // memory round trip per row): the A values of the first column (for the
-  // relu mask) and [B; bias] itself, coalesced, for LDS (each lane then
-  // reads its column's N weights from there).
-  constexpr int WPT = 4096 / (64 * R16W);  // [B; bias] floats a thread stages
-  float ak[DA ? 8 : 1], wv[DA ? WPT : 1];
-  auto da_load_a = [&](int k) {
-    const int kk = min(k, K - 1), h = threadIdx.x >> 8;
-    const int rows = min(16, M - (int)blockIdx.x * 16);
-#pragma unroll
-    for (int u = 0; u < 8; u++)
-      ak[u] = A[(long)(blockIdx.x * 16 + min(8 * h + u, rows - 1)) * K + kk];
-  };
+  __shared__ float wsd[DA ? R16_DA_COLS * 16 : 1];
+  // dA epilogue: workgroup (tile, blockIdx.y) takes columns [ks0, ks0 +
+  // R16_DA_COLS) of [B; bias] and of the tile's rows of A (every workgroup of
+  // a tile repeats the tile's GEMM and softmax-CE, which cost little; only the
+  // first writes them); lane t takes column ks0 + t % R16_DA_COLS for rows
+  // 2 (t / R16_DA_COLS) and the next.  Loaded here, in flight with the GEMM's
+  // operands (a load issued where its row is used costs a memory round trip
+  // per row): the two A values (for the relu mask) and the slice's rows of B,
+  // coalesced, for LDS (each lane then reads its column's N weights there).
+  constexpr int DC = R16_DA_COLS;
+  const int ks0 = blockIdx.y * DC;
+  float ak[2], wv[DA ? (DC * 16 + 64 * R16W - 1) / (64 * R16W) : 1];
   if constexpr (DA) {
-    da_load_a(threadIdx.x & 255);
+    const int rows = min(16, M - (int)blockIdx.x * 16);
+    const int kk = min(ks0 + (int)(threadIdx.x % DC), K - 1), r2 = 2 * (threadIdx.x / DC);
 #pragma unroll
-    for (int u = 0; u < WPT; u++)
-      wv[u] = B[min((int)threadIdx.x + 64 * R16W * u, (K + 1) * N - 1)];
+    for (int u = 0; u < 2; u++)
+      ak[u] = A[(long)(blockIdx.x * 16 + min(r2 + u, rows - 1)) * K + kk];
+    const int nw = min(DC, K - ks0) * N;  // the slice's floats of B
+#pragma unroll
+    for (int u = 0; u < (DC * 16 + 64 * R16W - 1) / (64 * R16W); u++)
+      wv[u] = B[(long)ks0 * N + min((int)threadIdx.x + 64 * R16W * u, nw - 1)];
   }
   // the epilogue's bias and label, loaded with the operands (a load issued
   // after the reduction is one more memory round trip before the stores)
@@ -772,12 +774,14 @@ gemm_rows16_kernel(const float *__restrict__ A, const float *__restrict__ B,
       const int m = m0 + 4 * q + i;
       if (m < M && n < N) {
         const float v = acc[i] + bnr;
-        C[(long)m * N + n] = v;
-        const float o = v > 0.0f ? v : 0.0f;
-        if (R) R[(long)m * N + n] = o;
-        if (P) {
-          P[(long)m * (N + 1) + n] = o;
-          if (n == N - 1) P[(long)m * (N + 1) + N] = 1.0f;
+        if (blockIdx.y == 0) {
+          C[(long)m * N + n] = v;
+          const float o = v > 0.0f ? v : 0.0f;
+          if (R) R[(long)m * N + n] = o;
+          if (P) {
+            P[(long)m * (N + 1) + n] = o;
+            if (n == N - 1) P[(long)m * (N + 1) + N] = 1.0f;
+          }
         }
         lv[4 * q + i][n] = v;
       }
@@ -791,11 +795,13 @@ gemm_rows16_kernel(const float *__restrict__ A, const float *__restrict__ B,
     if (t < 256 && m < M) {
       float xj[1] = {lv[row][j]}, pj[1], sj[1];
       const float loss = ce_row_group<16, 1>(xj, ylab, N, scale, pj, sj);
-      if (j < N) {
-        probs[(long)m * N + j] = pj[0];
-        seed[(long)m * N + j] = sj[0];
+      if (blockIdx.y == 0) {
+        if (j < N) {
+          probs[(long)m * N + j] = pj[0];
+          seed[(long)m * N + j] = sj[0];
+        }
+        if (j == 0) rowloss[m] = loss;
       }
-      if (j == 0) rowloss[m] = loss;
       if constexpr (DA) gsd[row * 16 + j] = sj[0];
     }
     if constexpr (DA) {
@@ -806,53 +812,48 @@ gemm_rows16_kernel(const float *__restrict__ A, const float *__restrict__ B,
       // output), each sum over j ascending from +0 -- the classifier
       // backward kernel's (head.hip) dA, bit for bit
 #pragma unroll
-      for (int u = 0; u < WPT; u++) wsd[threadIdx.x + 64 * R16W * u] = wv[u];
+      for (int u = 0; u < (DC * 16 + 64 * R16W - 1) / (64 * R16W); u++) {
+        const int i = threadIdx.x + 64 * R16W * u;
+        if (i < DC * 16) wsd[i] = wv[u];
+      }
       __syncthreads();
-      const int K1 = K + 1, h = threadIdx.x >> 8;
-      const int rows = min(16, M - m0);
-      for (int k = threadIdx.x & 255; k < K; k += 256) {
-        if (k >= 256) da_load_a(k);
+      const int K1 = K + 1, rows = min(16, M - m0);
+      const int k = ks0 + (int)(threadIdx.x % DC), r2 = 2 * (threadIdx.x / DC);
+      if (k < K && r2 < rows) {
         float wk[16];
 #pragma unroll
-        for (int jj = 0; jj < 16; jj++) wk[jj] = wsd[k * N + min(jj, N - 1)];
-        unsigned pos = 0;  // bit u: A[m0 + 8 h + u][k] > 0
+        for (int jj = 0; jj < 16; jj++) wk[jj] = wsd[(k - ks0) * N + min(jj, N - 1)];
+        // both rows' seeds read from LDS as 16-byte vectors (one wait, not
+        // one a multiply-add)
+        float4 gv[2][4];
 #pragma unroll
-        for (int u = 0; u < 8; u++) pos |= (ak[u] > 0.0f ? 1u : 0u) << u;
-        // four rows at a time: their seeds read from LDS as 16-byte vectors
-        // (one wait for the group, not one a multiply-add)
+        for (int u = 0; u < 2; u++)
 #pragma unroll
-        for (int m4 = 0; m4 < 8; m4 += 4) {
-          float4 gv[4][4];
+          for (int v = 0; v < 4; v++)
+            gv[u][v] = *reinterpret_cast<const float4 *>(gsd + (r2 + u) * 16 + 4 * v);
 #pragma unroll
-          for (int u = 0; u < 4; u++)
+        for (int u = 0; u < 2; u++) {
+          const float g[16] = {gv[u][0].x, gv[u][0].y, gv[u][0].z, gv[u][0].w,
+                               gv[u][1].x, gv[u][1].y, gv[u][1].z, gv[u][1].w,
+                               gv[u][2].x, gv[u][2].y, gv[u][2].z, gv[u][2].w,
+                               gv[u][3].x, gv[u][3].y, gv[u][3].z, gv[u][3].w};
+          float acc = 0.0f;
 #pragma unroll
-            for (int v = 0; v < 4; v++)
-              gv[u][v] = *reinterpret_cast<const float4 *>(gsd + (8 * h + m4 + u) * 16 + 4 * v);
-#pragma unroll
-          for (int u = 0; u < 4; u++) {
-            const int mr = 8 * h + m4 + u;
-            const float g[16] = {gv[u][0].x, gv[u][0].y, gv[u][0].z, gv[u][0].w,
-                                 gv[u][1].x, gv[u][1].y, gv[u][1].z, gv[u][1].w,
-                                 gv[u][2].x, gv[u][2].y, gv[u][2].z, gv[u][2].w,
-                                 gv[u][3].x, gv[u][3].y, gv[u][3].z, gv[u][3].w};
-            float acc = 0.0f;
-#pragma unroll
-            for (int jj = 0; jj < 16; jj++)
-              if (jj < N) acc = acc + g[jj] * wk[jj];
-            if (mr < rows) {
-              const long mm = m0 + mr;
-              da.dA[mm * K1 + k] = acc;
-              if (da.d1) da.d1[mm * K + k] = acc;
-              if (da.d2) da.d2[mm * K + k] = (pos >> (m4 + u)) & 1u ? acc : 0.0f;
-            }
+          for (int jj = 0; jj < 16; jj++)
+            if (jj < N) acc = acc + g[jj] * wk[jj];
+          if (r2 + u < rows) {
+            const long mm = m0 + r2 + u;
+            da.dA[mm * K1 + k] = acc;
+            if (da.d1) da.d1[mm * K + k] = acc;
+            if (da.d2) da.d2[mm * K + k] = ak[u] > 0.0f ? acc : 0.0f;
           }
         }
       }
-      // the ones column of dA (the bias row of B): a lane a row
-      if ((int)threadIdx.x < rows) {
-        const float *g = gsd + threadIdx.x * 16, *bw = bsd;
+      // the ones column of dA (the bias row of B): a lane a row, first slice
+      if (blockIdx.y == 0 && (int)threadIdx.x < rows) {
+        const float *g = gsd + threadIdx.x * 16;
         float acc = 0.0f;
-        for (int jj = 0; jj < N; jj++) acc = acc + g[jj] * bw[jj];
+        for (int jj = 0; jj < N; jj++) acc = acc + g[jj] * bsd[jj];
         da.dA[(long)(m0 + threadIdx.x) * K1 + K] = acc;
       }
     }
@@ -1052,9 +1053,10 @@ extern "C" int ttk_gemm_rows_da(const float *A, const float *B, const float *bia
     const int kc = 16 * nch;
     const bool va = ((uintptr_t)A & 15) == 0 && K % 4 == 0;
     const dim3 grid((unsigned)((M + 15) / 16));
+    const dim3 grid_da((unsigned)((M + 15) / 16), (unsigned)((K + R16_DA_COLS - 1) / R16_DA_COLS));
 #define TT_R16(NCH_, VA_)                                                                     \
   if (dA)                                                                                     \
-    hipLaunchKernelGGL((gemm_rows16_kernel<NCH_, VA_, true, true>), grid, dim3(64 * R16W), 0,   \
+    hipLaunchKernelGGL((gemm_rows16_kernel<NCH_, VA_, true, true>), grid_da, dim3(64 * R16W), 0, \
                        stream(), A, B, bias, C, R, P, M, N, K, kc, lu, ce->probs, ce->seed,   \
                        ce->rowloss, ce->scale, R16Da{dA, d1, d2});                            \
   else if (ce)                                                                                \
