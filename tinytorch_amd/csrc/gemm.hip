@@ -1574,28 +1574,27 @@ __device__ __forceinline__ void small_tile(int M, int N, int K, const float *__r
 #pragma unroll
       for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[g][i], b[g][i], acc, 0, 0, 0);
   };
-  // wave 0's epilogue operands -- the relu outputs and the weights to step of
-  // its 16 elements -- loaded before the K loop, clamped to the matrix, so
-  // that they arrive with the first operands (loaded after the wave sums,
-  // they cost one more memory round trip before the stores)
-  const int ne = min(n0 + l32, N - 1);
-  float rv[16], wv[16];
-  if (w == 0 && out.R) {
+  // the epilogue: thread e (of 64 SW) takes outputs e + 64 SW j of the tile
+  // (row / 32, column % 32: stores of consecutive columns); their relu
+  // outputs, weights to step and bias are loaded before the K loop, clamped
+  // to the matrix, so that they arrive with the first operands (loaded after
+  // the wave sums, they cost one more memory round trip before the stores)
+  constexpr int EPT = 32 * 32 / (64 * SW);  // outputs a thread
+  const int ecol = threadIdx.x & 31, erow0 = threadIdx.x >> 5;
+  const int ne = min(n0 + ecol, N - 1);
+  float rv[EPT], wv[EPT];
+  if (out.R) {
     const int nc = ne < N - 1 ? ne : (N > 1 ? N - 2 : 0);
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int m = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
-      rv[r] = out.R[(long)(m < M ? m : M - 1) * (N - 1) + nc];
-    }
+    for (int j = 0; j < EPT; j++)
+      rv[j] = out.R[(long)min(m0 + erow0 + 8 * j, M - 1) * (N - 1) + nc];
   }
-  if (w == 0 && out.wsgd) {
+  if (out.wsgd) {
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int m = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
-      wv[r] = out.wsgd[(long)(m < M ? m : M - 1) * out.ldc + ne];
-    }
+    for (int j = 0; j < EPT; j++)
+      wv[j] = out.wsgd[(long)min(m0 + erow0 + 8 * j, M - 1) * out.ldc + ne];
   }
-  const float bn = w == 0 && out.bias ? out.bias[ne] : 0.0f;
+  const float bn = out.bias ? out.bias[ne] : 0.0f;
   constexpr int CK = 8 * SG;  // k per chunk
   float a0[SG][4], b0[SG][4], a1[SG][4], b1[SG][4];
   if (k0 < k1) load(k0, a0, b0);
@@ -1607,47 +1606,41 @@ __device__ __forceinline__ void small_tile(int M, int N, int K, const float *__r
     if (kb + 2 * CK < k1) load(kb + 2 * CK, a0, b0);
     mfmas(a1, b1);
   }
-  if (w > 0) {
+  // every wave's sums to LDS (acc r of lane (l32, h): row 8 (r / 4) + 4 h +
+  // r % 4, column l32); each thread then adds the SW wave sums of its
+  // outputs in wave order
 #pragma unroll
-    for (int r = 0; r < 16; r++) red[((w - 1) * 16 + r) * 64 + lane] = acc[r];
-  }
+  for (int r = 0; r < 16; r++) red[(w * 16 + r) * 64 + lane] = acc[r];
   __syncthreads();
-  if (w > 0) return;
-  for (int o = 0; o < SW - 1; o++)
-#pragma unroll
-    for (int r = 0; r < 16; r++) acc[r] += red[(o * 16 + r) * 64 + lane];
-  const int n = n0 + l32;
-  if (n >= N) return;
   const bool pad = out.d1 || out.d2;
-  if (out.bias) {  // forward: C = acc + bias[n], and its relu / padded relu
+  const int n = n0 + ecol;
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int m = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
-      if (m < M) {
-        const float v = acc[r] + bn;
-        out.C[(long)m * out.ldc + n] = v;
-        const float o = v > 0.0f ? v : 0.0f;
-        if (out.relu) out.relu[(long)m * N + n] = o;
-        if (out.pad) {
-          float *pr = out.pad + (long)m * (N + 1);
-          pr[n] = o;
-          if (n == N - 1) pr[N] = 1.0f;
-        }
+  for (int j = 0; j < EPT; j++) {
+    const int row = erow0 + 8 * j;
+    const int src = (4 * (row >> 3) + (row & 3)) * 64 + 32 * ((row >> 2) & 1) + ecol;
+    float v = red[src];
+#pragma unroll
+    for (int o = 1; o < SW; o++) v += red[o * 16 * 64 + src];
+    const int m = m0 + row;
+    if (m >= M || n >= N) continue;
+    if (out.bias) {  // forward: C = acc + bias[n], and its relu / padded relu
+      v = v + bn;
+      out.C[(long)m * out.ldc + n] = v;
+      const float o = v > 0.0f ? v : 0.0f;
+      if (out.relu) out.relu[(long)m * N + n] = o;
+      if (out.pad) {
+        float *pr = out.pad + (long)m * (N + 1);
+        pr[n] = o;
+        if (n == N - 1) pr[N] = 1.0f;
       }
+      continue;
     }
-    return;
-  }
-#pragma unroll
-  for (int r = 0; r < 16; r++) {
-    const int m = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
-    if (m < M) {
-      out.C[(long)m * out.ldc + n] = acc[r];
-      if (out.wsgd) out.wsgd[(long)m * out.ldc + n] = sgd_sub(wv[r], out.lr, acc[r]);
-      if (pad && n < N - 1) {
-        const long o = (long)m * (N - 1) + n;
-        if (out.d1) out.d1[o] = acc[r];
-        if (out.d2) out.d2[o] = out.R ? (rv[r] > 0.0f ? acc[r] : 0.0f) : acc[r];
-      }
+    out.C[(long)m * out.ldc + n] = v;
+    if (out.wsgd) out.wsgd[(long)m * out.ldc + n] = sgd_sub(wv[j], out.lr, v);
+    if (pad && n < N - 1) {
+      const long o = (long)m * (N - 1) + n;
+      if (out.d1) out.d1[o] = v;
+      if (out.d2) out.d2[o] = out.R ? (rv[j] > 0.0f ? v : 0.0f) : v;
     }
   }
 }
@@ -1657,7 +1650,7 @@ __global__ void __launch_bounds__(64 * SW)
 gemm_small_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
                   const float *__restrict__ B, long ldb, float *__restrict__ C, long ldc, int kc,
                   int ones_m) {
-  __shared__ float red[(SW - 1) * 16 * 64];
+  __shared__ float red[SW * 16 * 64];
   SmallOut out{C, ldc, nullptr, nullptr, nullptr};
   out.ones_m = ones_m;
   small_tile<A_KC, B_NC, VA, VB>(M, N, K, A, lda, B, ldb, out, kc, blockIdx.x, blockIdx.y, red);
@@ -1687,7 +1680,7 @@ struct TnJobs {
 };
 __global__ void __launch_bounds__(64 * SW)
 gemm_tn_padones_sgd_kernel(TnJobs J, SgdPlain P) {
-  __shared__ float red[(SW - 1) * 16 * 64];
+  __shared__ float red[SW * 16 * 64];
   int b = blockIdx.x;
   for (int q = 0; q < J.nj; q++) {
     const TnJob &t = J.j[q];
@@ -1713,7 +1706,7 @@ template <bool VA, bool VB>
 __global__ void __launch_bounds__(64 * SW)
 gemm_small_epi_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
                       const float *__restrict__ B, long ldb, SmallOut out, int kc) {
-  __shared__ float red[(SW - 1) * 16 * 64];
+  __shared__ float red[SW * 16 * 64];
   small_tile<true, true, VA, VB>(M, N, K, A, lda, B, ldb, out, kc, blockIdx.x, blockIdx.y, red);
 }
 
@@ -1735,7 +1728,7 @@ template <int NCH, int TN>
 __global__ void __launch_bounds__(64 * T16W)
 gemm_t16_epi_kernel(int M, int N, int K, const float *__restrict__ A,
                     const float *__restrict__ B, SmallOut out, int kc) {
-  __shared__ float red[(T16W - 1) * 4 * TN * 64];
+  __shared__ float red[T16W * 4 * TN * 64];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, q = lane >> 4;
@@ -1743,11 +1736,11 @@ gemm_t16_epi_kernel(int M, int N, int K, const float *__restrict__ A,
   const int mr = min(m0 + r, M - 1);
   const int k0 = w * kc, k1 = min(K, k0 + kc);
   const float *__restrict__ ap = A + (long)mr * K;
-  // the epilogue's bias, loaded with the operands (a load issued after the
-  // wave sums is one more memory round trip before the stores)
-  float bnv[TN];
-#pragma unroll
-  for (int t = 0; t < TN; t++) bnv[t] = out.bias[min(n0 + 16 * t + r, N - 1)];
+  // the epilogue: thread e < 256 TN takes output row e / (16 TN), column e %
+  // (16 TN) of the tile; its bias is loaded with the operands (a load issued
+  // after the wave sums is one more memory round trip before the stores)
+  const int erow = threadIdx.x / (16 * TN), ecol = threadIdx.x % (16 * TN);
+  const float bn = out.bias[min(n0 + ecol, N - 1)];
   float4 av[NCH];
   float bv[NCH][TN][4];
 #pragma unroll
@@ -1777,40 +1770,30 @@ gemm_t16_epi_kernel(int M, int N, int K, const float *__restrict__ A,
                                                       acc[t], 0, 0, 0);
     }
   }
-  if (w > 0) {
+  // every wave's sums to LDS; then each thread adds the eight wave sums of
+  // its output in wave order and stores it (the stores spread over the
+  // workgroup instead of one wave)
 #pragma unroll
-    for (int t = 0; t < TN; t++)
+  for (int t = 0; t < TN; t++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) red[(((w - 1) * TN + t) * 4 + i) * 64 + lane] = acc[t][i];
-  }
+    for (int i = 0; i < 4; i++) red[((w * TN + t) * 4 + i) * 64 + lane] = acc[t][i];
   __syncthreads();
-  if (w > 0) return;
+  if (threadIdx.x >= 256 * TN) return;
+  const int t = ecol >> 4, i = erow & 3;
+  const int src = (t * 4 + i) * 64 + 16 * (erow >> 2) + (ecol & 15);
+  float v = red[src];
 #pragma unroll
-  for (int o = 0; o < T16W - 1; o++)
-#pragma unroll
-    for (int t = 0; t < TN; t++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) acc[t][i] += red[((o * TN + t) * 4 + i) * 64 + lane];
-#pragma unroll
-  for (int t = 0; t < TN; t++) {
-    const int n = n0 + 16 * t + r;
-    if (n >= N) continue;
-    const float bn = bnv[t];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int m = m0 + 4 * q + i;
-      if (m < M) {
-        const float v = acc[t][i] + bn;
-        out.C[(long)m * out.ldc + n] = v;
-        const float o = v > 0.0f ? v : 0.0f;
-        if (out.relu) out.relu[(long)m * N + n] = o;
-        if (out.pad) {
-          float *pr = out.pad + (long)m * (N + 1);
-          pr[n] = o;
-          if (n == N - 1) pr[N] = 1.0f;
-        }
-      }
-    }
+  for (int o = 1; o < T16W; o++) v += red[o * TN * 4 * 64 + src];
+  const int m = m0 + erow, n = n0 + ecol;
+  if (m >= M || n >= N) return;
+  v += bn;
+  out.C[(long)m * out.ldc + n] = v;
+  const float o = v > 0.0f ? v : 0.0f;
+  if (out.relu) out.relu[(long)m * N + n] = o;
+  if (out.pad) {
+    float *pr = out.pad + (long)m * (N + 1);
+    pr[n] = o;
+    if (n == N - 1) pr[N] = 1.0f;
   }
 }
 
@@ -1930,7 +1913,7 @@ struct SmallJob {
 template <bool VDA>
 __global__ void __launch_bounds__(64 * SW)
 gemm_small_pair_kernel(SmallJob da, SmallJob db, int nba) {
-  __shared__ float red[(SW - 1) * 16 * 64];
+  __shared__ float red[SW * 16 * 64];
   const int i = blockIdx.x;
   if (i < nba)
     small_tile<true, false, VDA, VDA>(da.M, da.N, da.K, da.A, da.lda, da.B, da.ldb, da.out, da.kc,
