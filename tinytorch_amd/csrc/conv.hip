@@ -1436,6 +1436,27 @@ __device__ __forceinline__ void dwt_reduce_block(int blk, f32x4 *sums,
   const long ec = in ? e4 : 0;
   const int fb = (int)(ec / S4), i4 = (int)(ec - (long)fb * S4);
   const f32x4 *p = (const f32x4 *)part + (long)fb * nu * S4 + i4;
+  // the weights the step changes, loaded before the partials (loaded after
+  // the sum, they cost one more memory round trip before the stores)
+  const int i = i4 * 4;
+  const bool isb = i >= jbp * 1024;
+  const int jb = i >> 10, r = (i >> 6) & 15, l = i & 63;
+  const int f = fb * 32 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+  const int k = jb * 32 + (l & 31);
+  float wpre[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (ty == 0 && in) {
+    if (isb) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int fe = fb * 32 + (i + e - jbp * 1024);
+        if (wdb && fe < F) wpre[e] = wdb[fe];
+      }
+    } else if (wdw && f < F) {
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        if (k + e < K) wpre[e] = wdw[(long)f * K + k + e];
+    }
+  }
   f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int q0 = ty; q0 < nu; q0 += 8 * ZL) {
     f32x4 t[8];
@@ -1449,25 +1470,21 @@ __device__ __forceinline__ void dwt_reduce_block(int blk, f32x4 *sums,
   __syncthreads();
   if (ty != 0 || !in) return;
   for (int z = 1; z < ZL; z++) v += sums[z * XL + tx];
-  const int i = i4 * 4;
-  if (i >= jbp * 1024) {
+  if (isb) {
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-      const int f = fb * 32 + (i + e - jbp * 1024);
-      if (db && f < F) db[f] = v[e];
-      if (wdb && f < F) wdb[f] -= lr * v[e];
+      const int fe = fb * 32 + (i + e - jbp * 1024);
+      if (db && fe < F) db[fe] = v[e];
+      if (wdb && fe < F) wdb[fe] = wpre[e] - lr * v[e];
     }
     return;
   }
-  const int jb = i >> 10, r = (i >> 6) & 15, l = i & 63;
-  const int f = fb * 32 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-  const int k = jb * 32 + (l & 31);
   if (f >= F || !dw) return;
 #pragma unroll
   for (int e = 0; e < 4; e++)
     if (k + e < K) {
       dw[(long)f * K + k + e] = v[e];
-      if (wdw) wdw[(long)f * K + k + e] -= lr * v[e];
+      if (wdw) wdw[(long)f * K + k + e] = wpre[e] - lr * v[e];
     }
 }
 
