@@ -192,7 +192,8 @@ int tt_k_head_bwd(const float *A, int M, int K, const float *W, int N, const flo
  * windows' codes are given (tt_k_conv2d_relu_pool_fwd_lds): dc (N x F x
  * 2Ho2 x 2Wo2) gets the pool + relu backward of d2 in the same launch (the
  * reference's src/autograd.c:555-594 then :318-327), bit for bit
- * tt_k_maxpool2x2_code_relu_bwd of d2.  -1: shapes or alignment outside it. */
+ * tt_k_maxpool2x2_code_relu_bwd of d2 (d1 and d2 themselves may be NULL;
+ * dA is required).  -1: shapes or alignment outside it. */
 int tt_k_head_bwd_pool(const float *A, int M, int K, const float *W, int N, const float *G,
                        float *dW, float *dA, float *d1, float *d2, const unsigned char *codes,
                        float *dc, int F, int Ho2, int Wo2);

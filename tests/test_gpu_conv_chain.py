@@ -186,7 +186,8 @@ def test_autograd_chain_on_off_bitexact(tlib, B, read_early):
                 for k in ("c1", "r1", "c2", "r2"):
                     vals[k + "_early"] = keep[names.index(k)].value()
             loss.backward(None)
-            grads = {k: keep[names.index(k)].grad() for k in ("w1", "b1", "w2", "b2", "wfc")}
+            grads = {k: keep[names.index(k)].grad()
+                     for k in ("w1", "b1", "w2", "b2", "wfc", "d", "f", "p2", "c2")}
             for k in ("w1", "b1", "w2", "b2", "wfc"):
                 keep[names.index(k)].sgd_step(0.5)
             for k, nd in zip(names, keep):
@@ -404,3 +405,42 @@ def test_autograd_chain_ce_in_head_bitexact(tlib):
     for k in b:
         assert bits_equal(a[k], b[k]), k
     assert bits_equal(a["probs"], b["probs2"])
+
+
+@pytest.mark.parametrize("deferral", [True, False])
+def test_classifier_backward_input_gradients_recipes(tlib, deferral):
+    """The classifier backward with the second pool's backward in its launch
+    leaves the reshape's and the pool's own gradients (dA without its ones
+    column) as recipes of dA: read after the backward (and after the
+    convolution's gradient was consumed), each equals dA[:, :-1] bit for bit;
+    with every deferral off (tth_conv_relu_fuse(0)) the same gradients come
+    from the unfused rules, within the fp32 bar of the fused ones."""
+    from tinytorch_amd.torch_py import Node
+    x, y, P = orc.cnn_inputs(B=128)
+
+    def run(defer):
+        prev = tlib.tth_conv_relu_fuse(1 if defer else 0)
+        keep = []
+        try:
+            logits = _cnn(Node, x, P, keep)
+            loss = logits.softmax_ce(y)
+            loss.backward(None)
+            names = ("X", "w1", "b1", "w2", "b2", "wfc", "c1", "r1", "p1", "c2", "r2", "p2", "f",
+                     "d", "logits")
+            g = {k: keep[names.index(k)].grad() for k in ("w2", "d", "f", "p2", "c2")}
+            for nd in [loss] + keep[::-1]:
+                nd.release()
+            return g
+        finally:
+            tlib.tth_conv_relu_fuse(prev)
+
+    print("classifier backward input gradient recipes, deferral", deferral, flush=True)
+    g = run(deferral)
+    dA = g["d"]
+    assert bits_equal(g["f"], dA[:, :-1])
+    assert bits_equal(g["p2"].reshape(128, -1), dA[:, :-1])
+    if not deferral:
+        return
+    ref = run(False)
+    for k in ("d", "f", "p2", "c2", "w2"):
+        assert np.abs(g[k] - ref[k]).max() <= 1e-4 * max(1e-30, np.abs(ref[k]).max()), k

@@ -843,13 +843,25 @@ static int backward_matmul_fused(AGNode *n, const float *g, const TTHeadCeArgs *
     if ((!needs(b) || gb) && (!needs(a) || ga) && (!x || tx) && (!y || ty) && (!pr || tc)) {
         float *dB = gb ? gb->dev : NULL, *dA = ga ? ga->dev : NULL;
         float *d1 = tx ? tx->dev : NULL, *d2 = ty ? ty->dev : NULL;
+        /* with the pool's backward in the launch (the convolution's output
+         * gradient written), the reshape's and the pool's own gradients --
+         * dA without its ones column -- are recipes of dA (written if read) */
+        const int lazy12 = pr && dA && tt_defer_enabled();
         if (pr)
-            rc = ce ? ttk_head_bwd_ce(ad, M, K, bd, N, ce, dB, dA, d1, d2, NULL, codes, tc->dev,
+            rc = ce ? ttk_head_bwd_ce(ad, M, K, bd, N, ce, dB, dA, lazy12 ? NULL : d1,
+                                      lazy12 ? NULL : d2, NULL, codes, tc->dev,
                                       (int)y->val->shape[1], (int)y->val->shape[2],
                                       (int)y->val->shape[3])
-                    : tt_k_head_bwd_pool(ad, M, K, bd, N, g, dB, dA, d1, d2, codes, tc->dev,
+                    : tt_k_head_bwd_pool(ad, M, K, bd, N, g, dB, dA, lazy12 ? NULL : d1,
+                                         lazy12 ? NULL : d2, codes, tc->dev,
                                          (int)y->val->shape[1], (int)y->val->shape[2],
                                          (int)y->val->shape[3]);
+        if (rc == 0 && pr && lazy12) {
+            if (tx && tt_lazy_padones_bwd(tx, ga, M, K - 1) != 0)
+                rc = tt_k_padones_bwd(dA, d1, M, K - 1);
+            if (rc == 0 && ty && tt_lazy_padones_bwd(ty, ga, M, K - 1) != 0)
+                rc = tt_k_padones_bwd(dA, d2, M, K - 1);
+        }
         if (rc != 0) {
             tt_release(tc);
             tc = NULL;

@@ -374,7 +374,7 @@ int tt_k_head_bwd(const float *A, int M, int K, const float *W, int N, const flo
 int tt_k_head_bwd_pool(const float *A, int M, int K, const float *W, int N, const float *G,
                        float *dW, float *dA, float *d1, float *d2, const unsigned char *codes,
                        float *dc, int F, int Ho2, int Wo2) {
-  if (!codes || !dc || !d2 || F <= 0 || Ho2 <= 0 || Wo2 <= 0 ||
+  if (!codes || !dc || !dA || F <= 0 || Ho2 <= 0 || Wo2 <= 0 ||
       (long)F * Ho2 * Wo2 != (long)K - 1 || ((uintptr_t)dc & 7))
     return -1;
   return head_bwd(A, M, K, W, N, G, dW, dA, d1, d2, nullptr, codes, dc, Ho2 * Wo2, Wo2);
@@ -386,7 +386,7 @@ int ttk_head_bwd_ce(const float *A, int M, int K, const float *W, int N, const T
                     float *dW, float *dA, float *d1, float *d2, const float *R,
                     const unsigned char *codes, float *dc, int F, int Ho2, int Wo2) {
   if (!a || !a->labels) return -1;
-  if (codes && (!dc || !d2 || F <= 0 || Ho2 <= 0 || Wo2 <= 0 ||
+  if (codes && (!dc || !dA || F <= 0 || Ho2 <= 0 || Wo2 <= 0 ||
                 (long)F * Ho2 * Wo2 != (long)K - 1 || ((uintptr_t)dc & 7)))
     return -1;
   TTHeadCe ce{};

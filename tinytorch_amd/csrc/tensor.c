@@ -135,7 +135,9 @@ typedef struct TTLazyVal {
                                   (tt_k_gemm_tn_padones, dims rows Kx N); 5:
                                   conv(src, buf) -- a convolution output the
                                   two-convolution chain did not store; 6: see
-                                  ce (every output is written at once) */
+                                  ce (every output is written at once); 7:
+                                  src without its last column (padones
+                                  backward, dims M K) */
     TTDwtShared *dwt;
     Tensor *src2;
     int dims[3];
@@ -165,6 +167,12 @@ static int lazy_add(Tensor *t, Tensor *src, int kind) {
 int tt_lazy_relu(Tensor *t, Tensor *src) { return lazy_add(t, src, 0); }
 int tt_lazy_padones(Tensor *t, Tensor *src) { return lazy_add(t, src, 1); }
 int tt_lazy_ce_mean(Tensor *t, Tensor *src) { return lazy_add(t, src, 2); }
+int tt_lazy_padones_bwd(Tensor *t, Tensor *src, long M, long K) {
+    if (M > 0x7fffffffL || K > 0x7fffffffL || lazy_add(t, src, 7) != 0) return -1;
+    g_lazy_vals->dims[0] = (int)M;
+    g_lazy_vals->dims[1] = (int)K;
+    return 0;
+}
 
 int tt_lazy_gemm_tn_padones(Tensor *dw, Tensor *x, Tensor *g, int rows, int Kx, int N) {
     if (lazy_add(dw, x, 4) != 0) return -1;
@@ -509,6 +517,7 @@ restart:
                            : l->kind == 2 ? tt_k_ce_mean_rows(x, l->t->dev, (int)l->src->numel)
                            : l->kind == 4 ? ttk_gemm_tn_padones_any(l->dims[0], l->dims[1],
                                                                     l->dims[2], x, x2, l->t->dev)
+                           : l->kind == 7 ? tt_k_padones_bwd(x, l->t->dev, l->dims[0], l->dims[1])
                            : l->kind == 5 ? tt_conv_fwd_any(x, l->buf,
                                                             l->buf + (long)l->q[4] * l->q[1] *
                                                                          l->q[5] * l->q[6],

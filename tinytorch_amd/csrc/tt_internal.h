@@ -100,6 +100,9 @@ int tt_lazy_dwt_sgd(float *const *w, Tensor *const *g, const long *n, int count,
 /* dw (Kx+1 x N) = [x, 1]^T g, the weight gradient of a matmul of padones(x)
  * (x rows x Kx, g rows x N), written on first use; 0 ok, -1 no memory */
 int tt_lazy_gemm_tn_padones(Tensor *dw, Tensor *x, Tensor *g, int rows, int Kx, int N);
+/* t (M x K elements) = src (M x (K + 1)) without its last column -- the
+ * padones backward -- written on first use; 0 ok, -1 no memory */
+int tt_lazy_padones_bwd(Tensor *t, Tensor *src, long M, long K);
 /* as tt_lazy_dwt_sgd, for one or two pending tt_lazy_gemm_tn_padones
  * gradients: the GEMMs (stepping their weights) and the other tensors' steps
  * in one launch */
