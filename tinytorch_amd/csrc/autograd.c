@@ -595,15 +595,17 @@ static int ce_spec(AGNode *logits, const TTPendConv *p, const int32_t *hlab, Ten
     sda[2] = sda[1] ? tt_empty_like(x->in[0]->val) : NULL;
     const TTCeHook hk = {p->b, hlab, probs->dev, seed->dev, rl->dev,
                          1.0f / (float)p->geo[0]};
+    /* sda[1] (dA without its ones column) is left to a recipe of sda[0] */
     const int rc = sda[2] ? ttk_gemm_rows_da(p->x, p->w, p->b, p->out->dev, NULL, NULL,
                                              p->geo[0], p->geo[1], p->geo[2], &hk, sda[0]->dev,
-                                             sda[1]->dev, sda[2]->dev)
+                                             NULL, sda[2]->dev)
                           : -1;
     if (rc != 0) {
         for (int i = 0; i < 3; i++) { tt_release(sda[i]); sda[i] = NULL; }
         return -1;
     }
-    for (int i = 0; i < 3; i++) tt_mark_dev_written(sda[i]);
+    tt_mark_dev_written(sda[0]);
+    tt_mark_dev_written(sda[2]);
     return 0;
 }
 
@@ -907,6 +909,12 @@ static int backward_matmul_spec(AGNode *n) {
                    ttk_gemm_tn_padones_any(M, K - 1, N, NULL, NULL, NULL) == 0;
     Tensor *gb = ok ? tt_empty_like(b->val) : NULL;
     if (!gb || tt_lazy_gemm_tn_padones(gb, x->val, n->grad, M, K - 1, N) != 0) {
+        tt_release(gb);
+        for (int i = 0; i < 3; i++) tt_release(sda[i]);
+        return -1;
+    }
+    if (tt_lazy_padones_bwd(sda[1], sda[0], M, K - 1) != 0 &&
+        tt_k_padones_bwd(sda[0]->dev, sda[1]->dev, M, K - 1) != 0) {
         tt_release(gb);
         for (int i = 0; i < 3; i++) tt_release(sda[i]);
         return -1;
