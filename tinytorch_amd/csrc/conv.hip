@@ -46,6 +46,9 @@
 #include <stdlib.h>
 #include "tt_rt.h"
 
+#include "probe.h"
+TT_PROBE_DEFINE(conv)
+
 namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -1304,6 +1307,7 @@ __device__ __forceinline__ void conv_dwt_block(const float *__restrict__ gr,
   float bsum = 0.0f;
   dma_wait();
   __syncthreads();
+  TT_PROBE(1, 5);
 
   // items (row, quad): rows pq, pq+4, ... of the unit; lane half h takes
   // the pixels [h*Wo/2, h*Wo/2 + Wo/2) of a row, four at a time: one 16-byte
@@ -1369,6 +1373,7 @@ __device__ __forceinline__ void conv_dwt_block(const float *__restrict__ gr,
     }
   }
   bsum += __shfl_xor(bsum, 32, 64);  // both halves of filter l32
+  TT_PROBE(1, 6);
 
   // add the DWT_NPQ waves of each tap group: (0 + 2) + (1 + 3), through LDS
 #pragma unroll
@@ -2110,6 +2115,7 @@ conv_chain_fwd_kernel(const float *__restrict__ x, const float *__restrict__ w1,
   const int K1 = C1 * 9;
   const int qlo = hf ? 7 : 0;           // first pooled row of phase A
   const int iy0 = 2 * qlo - 1;          // image row of slab row 0
+  TT_PROBE(0, 0);
 
   // ---- staging: image slab, filter bank 1 (k-major), biases, then bank 2 ----
   {
@@ -2155,6 +2161,7 @@ conv_chain_fwd_kernel(const float *__restrict__ x, const float *__restrict__ w1,
   // every wave issued at least 9 loads of bank 2 after the rest
   asm volatile("s_waitcnt vmcnt(9)" ::: "memory");
   __syncthreads();
+  TT_PROBE(0, 1);
 
   // ---- phase A: first convolution, bias, relu, pool, codes ----
   {
@@ -2220,6 +2227,7 @@ conv_chain_fwd_kernel(const float *__restrict__ x, const float *__restrict__ w1,
     }
   }
   __syncthreads();
+  TT_PROBE(0, 2);
 
   // ---- pool1 and its codes (owned rows) from LDS, drained under phase B ----
 #pragma unroll
@@ -2315,6 +2323,7 @@ conv_chain_fwd_kernel(const float *__restrict__ x, const float *__restrict__ w1,
     }
   }
   __syncthreads();  // every wave is past phase A's slab: the pool2 tiles reuse it
+  TT_PROBE(0, 3);
 
   // ---- bias, relu, pool, codes of the second convolution ----
   float *pt = xs1;                                      // F2 x PT pooled values
@@ -2388,6 +2397,7 @@ conv_chain_fwd_kernel(const float *__restrict__ x, const float *__restrict__ w1,
       if (j < FCN && l == 0) fcpart[((long)hf * gridDim.x / 2 + n) * FCN + j] = a;
     }
   }
+  TT_PROBE(0, 4);
 }
 
 // ---- the middle of the two-convolution chain's backward in one launch ----
@@ -2484,6 +2494,7 @@ __device__ __forceinline__ void conv_chain_bwd_block(const float *__restrict__ d
   }
   dma_wait();
   __syncthreads();
+  TT_PROBE(1, 1);
 
   // ---- phase 1: dx2 (the flipped-kernel convolution of dc2) ----
   const int pb = wave & 3, grp = wave >> 2;
@@ -2537,6 +2548,7 @@ __device__ __forceinline__ void conv_chain_bwd_block(const float *__restrict__ d
     }
   }
 
+  TT_PROBE(1, 2);
   // ---- phase 2: dx2, and the first convolution's output gradient in LDS ----
   if (grp == 0) {
     const int pr = 8 * hf + hol;
@@ -2558,6 +2570,7 @@ __device__ __forceinline__ void conv_chain_bwd_block(const float *__restrict__ d
   }
   __syncthreads();
 
+  TT_PROBE(1, 3);
   // ---- phase 3: the first convolution's weight gradient, two units ----
   {
     const int uu = wave >> 2, pq = wave & 3;
@@ -2661,14 +2674,17 @@ conv_chain_bwd_dw2_kernel(const float *__restrict__ dc2, const float *__restrict
                           const float *__restrict__ x2, float *__restrict__ part2, Geo g2,
                           int RC, int nch, int GS, int CS, int RW, int jbp, int nu2,
                           int nchain) {
+  TT_PROBE(1, 0);
   if ((int)blockIdx.x < nchain) {
     if (threadIdx.x >= chainb::NTH) return;
     conv_chain_bwd_block(dc2, w2, codes1, x, dx2, part1, C1, blockIdx.x);
+    TT_PROBE(1, 15);
     return;
   }
   const int b = blockIdx.x - nchain;
   conv_dwt_block<3, 3, false>(dc2, x2, part2, g2, RC, nch, GS, CS, RW, jbp, nullptr, b % nu2,
                               0, b / nu2, nu2);
+  TT_PROBE(1, 15);
 }
 
 int g_lds_conv = 1;  // tth_conv_lds

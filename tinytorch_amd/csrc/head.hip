@@ -37,6 +37,8 @@
 #include <stdint.h>
 #include "tt_rt.h"
 #include "ce_rows.h"
+#include "probe.h"
+TT_PROBE_DEFINE(head)
 
 namespace {
 
@@ -125,7 +127,7 @@ __device__ __forceinline__ void head_dw_block(const float *__restrict__ A, int M
     // outputs), then the block's columns of it
     float va[32];
     stage_load<KW, 32>(va, A + k0, K, 0, M, min(KW, K - k0));
-    head_ce_seed<NC>(ce, 0, M, M, N, gl, N, blockIdx.x == 0, gl + M * N);
+    head_ce_seed<NC, 2>(ce, 0, M, M, N, gl, N, blockIdx.x == 0, gl + M * N);
     stage_store<KW, 32>(va, As, KW, 0, M);
     __syncthreads();
     for (int i = tid; i < M * JW; i += NT) {
@@ -138,6 +140,7 @@ __device__ __forceinline__ void head_dw_block(const float *__restrict__ A, int M
                                          min(JW, N - j0), M);
   }
   __syncthreads();
+  TT_PROBE(0, 1);
   const int kl = tid % KW, jl = tid / KW;
   const int k = k0 + kl, j = j0 + jl;
   if (j >= N || k >= K) return;
@@ -162,27 +165,44 @@ constexpr int DA_M = 32;  // rows m per dA workgroup (8 per lane)
 // sums of its logits (see above) into gl (row r at gl[(r - r0) * gs]); `out`:
 // also store the softmax-CE's outputs of those rows.  The rows' partial sums
 // are first loaded whole-workgroup (coalesced) into pp (2 (r1 - r0) N floats
-// of LDS) with the rows' labels; four lanes a row then form its softmax-CE.
+// of LDS) with the rows' labels; GW lanes a row then form its softmax-CE (one
+// round for the rows of a block: 2 lanes a row for 128 rows, 8 for 32).
 // Every thread calls it (barriers inside).
-template <int NC>
+template <int NC, int GW>
 __device__ __forceinline__ void head_ce_seed(const TTHeadCe &ce, int r0, int r1, int M, int N,
                                              float *gl, int gs, bool out, float *pp) {
   const int n = (r1 - r0) * N;
   const long total = (long)M * N;
-  // four lanes a row (ce_row_group): lane q takes columns [q CPL, q CPL + CPL)
-  constexpr int GW = 4, CPL = (NC + GW - 1) / GW;
+  // GW lanes a row (ce_row_group): lane q takes columns [q CPL, q CPL + CPL)
+  constexpr int CPL = (NC + GW - 1) / GW;
   const int q = threadIdx.x & (GW - 1);
   float bq[CPL];  // this lane's bias values, loaded with the partial sums
 #pragma unroll
   for (int u = 0; u < CPL; u++) bq[u] = ce.bias[min(q * CPL + u, N - 1)];
-  for (int i = threadIdx.x; i < n; i += NT) {
-    pp[i] = ce.part[(long)r0 * N + i];
-    pp[n + i] = ce.part[total + (long)r0 * N + i];
-  }
   // the rows' labels too (read in the loop below, each was a round trip)
   int *yl = reinterpret_cast<int *>(pp + 2 * n);
   for (int i = threadIdx.x; i < r1 - r0; i += NT) yl[i] = ce.lab[r0 + i];
+  // eight elements a thread in flight before their LDS stores (a loop that
+  // stores each load waits a memory round trip per element)
+  for (int b = 0; b < n; b += 8 * NT) {
+    float v0[8], v1[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int i = min(b + (int)threadIdx.x + u * NT, n - 1);
+      v0[u] = ce.part[(long)r0 * N + i];
+      v1[u] = ce.part[total + (long)r0 * N + i];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int i = b + (int)threadIdx.x + u * NT;
+      if (i < n) {
+        pp[i] = v0[u];
+        pp[n + i] = v1[u];
+      }
+    }
+  }
   __syncthreads();
+  TT_PROBE(0, 6);
   for (int r = r0 + (int)(threadIdx.x / GW); r < r1; r += NT / GW) {
     float lv[CPL], pr[CPL], sr[CPL];
     const float *p0 = pp + (r - r0) * N;
@@ -216,6 +236,7 @@ __device__ __forceinline__ void head_ce_seed(const TTHeadCe &ce, int r0, int r1,
       if (ce.rowloss && q == 0) ce.rowloss[r] = loss;
     }
   }
+  TT_PROBE(0, 7);
 }
 
 template <int NC>
@@ -225,6 +246,7 @@ head_bwd_kernel(const float *__restrict__ A, int M, int K, const float *__restri
                 float *__restrict__ d1, float *__restrict__ d2, const float *__restrict__ R,
                 int nbw, int KW, int nkw, const unsigned char *__restrict__ codes,
                 float *__restrict__ dc, int P2, int Wo2, TTHeadCe ce, int gl_off) {
+  TT_PROBE(0, 0);
   extern __shared__ __attribute__((aligned(16))) float lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -236,6 +258,7 @@ head_bwd_kernel(const float *__restrict__ A, int M, int K, const float *__restri
     const int kb = blockIdx.x % nkw, jb = blockIdx.x / nkw;
     if (KW == 64) head_dw_block<64, NC>(A, M, K, G, N, dW, kb * 64, jb * JW, lds, ce, cp, lds + gl_off);
     else head_dw_block<32, NC>(A, M, K, G, N, dW, kb * 32, jb * JW, lds, ce, cp, lds + gl_off);
+    TT_PROBE(0, 2);
     return;
   }
   // dA block: columns [k0, k0 + 64) x rows [m0, m0 + DA_M); Ws, Gs (64 / DA_M x NC)
@@ -250,7 +273,7 @@ head_bwd_kernel(const float *__restrict__ A, int M, int K, const float *__restri
       // the block's rows of the seed, formed here while W is in flight (the
       // first column block stores their softmax-CE outputs when no dW
       // workgroup does)
-      head_ce_seed<NC>(ce, m0, min(m0 + DA_M, M), M, N, Gs, NC, nbw == 0 && blk % nkb == 0,
+      head_ce_seed<NC, NT / DA_M>(ce, m0, min(m0 + DA_M, M), M, N, Gs, NC, nbw == 0 && blk % nkb == 0,
                        lds + gl_off);
       stage_store<NC, UW>(vw, Ws, NC, 0, 64);
     } else {
@@ -286,13 +309,24 @@ head_bwd_kernel(const float *__restrict__ A, int M, int K, const float *__restri
     }
   }
   __syncthreads();
+  TT_PROBE(0, 4);
   if (k >= K) return;
   f32x4 w4[NC / 4];
 #pragma unroll
   for (int v = 0; v < NC / 4; v++) w4[v] = *(const f32x4 *)(Ws + kl * NC + 4 * v);
+  TT_PROBE(0, 8);
+  // this lane's window of the pool backward: dc row m starts at 4 m K1 (2Ho2
+  // x 2Wo2 per feature map); the divisions once per lane, not per row
+  long dco = 0;
+  if (dc) {
+    const int kq = k < K1 ? k : 0;
+    const int fc = kq / P2, rem = kq - fc * P2, h2 = rem / Wo2, w2 = rem - h2 * Wo2;
+    dco = ((long)fc * (2 * (P2 / Wo2)) + 2 * h2) * (2 * Wo2) + 2 * w2;
+  }
 #pragma unroll
   for (int i = 0; i < MI; i++) {
     const int m = m0 + mg + 4 * i;
+    if (i == 1) TT_PROBE(0, 9);
     if (m < M) {
       const f32x4 *gr = (const f32x4 *)(Gs + (mg + 4 * i) * NC);
       float s = 0.0f;
@@ -315,18 +349,17 @@ head_bwd_kernel(const float *__restrict__ A, int M, int K, const float *__restri
           // row) whose input was a relu: its pool + relu backward from the
           // window's code (bits 0-1 argmax, 2-5 relu mask), as
           // maxpool2x2_code_bwd_kernel writes it
-          const int fc = k / P2, rem = k - fc * P2, h2 = rem / Wo2, w2 = rem - h2 * Wo2;
           const unsigned c = cv[i];
           const float g0 = 0.0f + s;
           auto at = [&](unsigned q) { return ((c & 3) == q && ((c >> (2 + q)) & 1)) ? g0 : 0.0f; };
-          float *dr = dc + ((long)(m * (K1 / P2) + fc) * (2 * (P2 / Wo2)) + 2 * h2) * (2 * Wo2) +
-                      2 * w2;
+          float *dr = dc + (long)m * 4 * K1 + dco;
           *reinterpret_cast<float2 *>(dr) = make_float2(at(0), at(1));
           *reinterpret_cast<float2 *>(dr + 2 * Wo2) = make_float2(at(2), at(3));
         }
       }
     }
   }
+  TT_PROBE(0, 5);
 }
 
 }  // namespace
