@@ -60,6 +60,11 @@ $(BUILD)/obj:
 	mkdir -p $@
 
 lib: $(BUILD)/libtinytorch.so
+
+# the library with phase timestamps compiled in (TT_PHASE_PROBE, probe.h) for
+# `bench.py --phases`; a separate build tree, never loaded by the tests
+probe:
+	$(MAKE) BUILD=$(BUILD)/probe HIPFLAGS="$(HIPFLAGS) -DTT_PHASE_PROBE" lib
 pybind: $(BUILD)/tinytorch_pybind$(EXT_SUFFIX)
 
 oracle:
@@ -71,4 +76,4 @@ ref:
 clean:
 	rm -rf $(BUILD)
 
-.PHONY: all lib pybind oracle ref clean
+.PHONY: all lib pybind oracle ref clean probe

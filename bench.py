@@ -76,6 +76,9 @@ def parse():
     ap.add_argument("--hbm-kernels", action="store_true",
                     help="only time the bandwidth kernels alone (extra.hbm_kernels; for kernel "
                          "traces and HBM counters of them)")
+    ap.add_argument("--phases", action="store_true",
+                    help="per-phase kernel timestamps of the CNN step's kernels and the 64x64 "
+                         "GEMM (needs `make probe`: build/probe/libtinytorch.so)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 1 GiB device copy kernel 5 times (the known-size "
                          "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -563,6 +566,77 @@ def gemm_shapes(L, only=None):
     return out
 
 
+PROBE_LIB = os.path.join(ROOT, "build", "probe", "libtinytorch.so")
+
+
+def phase_split(ts, kid, blocks, points, names):
+    """Per-phase durations (us) of kernel `kid`'s workgroups `blocks` from the
+    probe timestamps (100 MHz): the median over the workgroups of each span
+    between consecutive points, and the span of the whole set."""
+    t = ts[kid][blocks].astype(np.int64)
+    out = {"workgroups": int(t.shape[0]),
+           "span_us": round(float(t[:, points[-1]].max() - t[:, points[0]].min()) * 0.01, 2)}
+    for (a, b), nm in zip(zip(points[:-1], points[1:]), names):
+        out[nm] = round(float(np.median(t[:, b] - t[:, a])) * 0.01, 2)
+    return out
+
+
+def phases(L):
+    """Phase timestamps (probe.h) of thread 0 of every workgroup: the config-4
+    CNN step's convolution kernels and classifier backward (the last of 30
+    steps) and gemm_mid_kernel at 1024^3 and 1000x1003x997 (the last of 50
+    launches)."""
+    from tinytorch_amd.hip import sync
+    def read(name):
+        f = getattr(L, "tt_probe_read_" + name)
+        f.restype = ctypes.c_int
+        f.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        buf = np.zeros(4 * 1024 * 16, np.uint64)
+        if f(buf.ctypes.data, buf.size) != 0:
+            raise RuntimeError("tt_probe_read_" + name)
+        return buf.reshape(4, 1024, 16)
+    st = CnnStep(L)
+    for _ in range(30):
+        st.step()
+    sync()
+    conv, head = read("conv"), read("head")
+    nchain = 2 * st.B
+    out = {
+        "conv_chain_fwd_kernel": phase_split(conv, 0, slice(0, nchain), [0, 1, 2, 3, 4],
+                                             ["staging", "conv1_relu_pool", "conv2",
+                                              "relu_pool_fc_epilogue"]),
+        "conv_chain_bwd_dw2_kernel/chain": phase_split(conv, 1, slice(0, nchain),
+                                                       [0, 1, 2, 3, 15],
+                                                       ["staging", "conv2_dx", "pool1_relu_bwd",
+                                                        "conv1_dw_partials"]),
+        "conv_chain_bwd_dw2_kernel/conv2_dw": phase_split(conv, 1, slice(nchain, 2 * nchain),
+                                                          [0, 5, 6, 15],
+                                                          ["staging", "mfma_issue",
+                                                           "wave_sums_partials"]),
+    }
+    t1 = conv[1][:2 * nchain].astype(np.int64)
+    out["conv_chain_bwd_dw2_kernel/grid_span_us"] = round(float(t1[:, 15].max() - t1[:, 0].min()) * 0.01, 2)
+    nbw = int(np.count_nonzero(head[0, :, 2]))
+    out["head_bwd_kernel/dw"] = phase_split(head, 0, slice(0, nbw), [0, 6, 7, 1, 2],
+                                            ["partials_load", "softmax_ce", "stage_a", "dw_sums"])
+    nda = int(np.count_nonzero(head[0, :, 5]))
+    out["head_bwd_kernel/da_pool"] = phase_split(head, 0, slice(nbw, nbw + nda), [0, 6, 7, 4, 5],
+                                                 ["partials_load", "softmax_ce", "stage_w",
+                                                  "da_pool_bwd_stores"])
+    for (M, N, K) in ((1024, 1024, 1024), (1000, 1003, 997)):
+        g = Gemm(L, M, N, K)
+        prewarm(g.launch, 0.2)
+        for _ in range(50):
+            g.launch()
+        sync()
+        gm = read("gemm")
+        out[f"gemm_mid_kernel/{M}x{N}x{K}"] = phase_split(
+            gm, 0, slice(0, 256), [0, 1, 2, 3, 4, 5],
+            ["first_tiles", "k_loop", "barrier", "wave_sums_to_lds", "sum_and_store"])
+        g.free()
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -571,8 +645,15 @@ def main():
               "images, and one all-reduce of the weight gradients per step)", file=sys.stderr)
         sys.exit(2)
     import tinytorch_amd
+    if args.phases:
+        if not os.path.exists(PROBE_LIB):
+            sys.exit(f"bench.py: {PROBE_LIB} is not built; run `make probe`")
+        tinytorch_amd.LIB_PATH = PROBE_LIB
     tinytorch_amd.require_gpu()
     L = tinytorch_amd.lib()
+    if args.phases:
+        print(json.dumps(phases(L)))
+        return
     log("device", tinytorch_amd.device_name())
     if args.cnn_only:
         ms = time_steps(CnnStep(L), args.steps, args.warmup)

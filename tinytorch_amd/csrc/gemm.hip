@@ -37,6 +37,8 @@
 #include <stdint.h>
 #include <stdlib.h>
 #include "tt_rt.h"
+#include "probe.h"
+TT_PROBE_DEFINE(gemm)
 
 namespace {
 
@@ -1089,6 +1091,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
 gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
                 const float *__restrict__ B, long ldb, float *__restrict__ C, long ldc,
                 long split_stride, int kchunk, bool cvec, int alim, int blim) {
+  TT_PROBE(0, 0);
   static_assert(S >= 3, "the pipeline needs three stages");
   constexpr int NTH = 64 * NW;
   static_assert(ROWS % M_T == 0 && NW == (ROWS / M_T) * NWK, "waves = row blocks x k slices");
@@ -1210,6 +1213,7 @@ gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
     if (nk >= S - 1) wait_vm<NL *(S - 2)>();
     else wait_vm<0>();
     __syncthreads();
+    TT_PROBE(0, 1);
     float a0[KSUB][2][4], b0[KSUB][2][4], a1[KSUB][2][4], b1[KSUB][2][4];
     frags(0, a0, b0);
     for (int kt = 0; kt < nk; kt += 2) {
@@ -1221,7 +1225,9 @@ gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
   // wave sums -> LDS (acc r of block (x, y): row 8*(r/4) + 4g + r%4 of the
   // block), then each thread adds the NWK k-slice sums of its outputs in
   // order
+  TT_PROBE(0, 2);
   __syncthreads();
+  TT_PROBE(0, 3);
   float *red = smem + wave * (M_T * M_RLD);
 #pragma unroll
   for (int x = 0; x < 2; x++)
@@ -1237,6 +1243,7 @@ gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
       }
     }
   __syncthreads();
+  TT_PROBE(0, 4);
 #pragma unroll
   for (int f0 = 0; f0 < ROWS * M_T / 4; f0 += NTH) {
     const int f = f0 + tid;  // float4 index: row f / 16, columns 4 * (f % 16) ..
@@ -1262,6 +1269,7 @@ gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
       if (col + 3 < N) crow[col + 3] = v.w;
     }
   }
+  TT_PROBE(0, 5);
 }
 
 inline hipStream_t stream() { return (hipStream_t)ttrt_stream(); }
