@@ -1536,6 +1536,7 @@ __device__ __forceinline__ void small_tile(int M, int N, int K, const float *__r
                                            long lda, const float *__restrict__ B, long ldb,
                                            const SmallOut &out, int kc, int bx, int by,
                                            float *red) {
+  TT_PROBE(1, 0);
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l32 = lane & 31, h = lane >> 5;
@@ -1617,9 +1618,11 @@ __device__ __forceinline__ void small_tile(int M, int N, int K, const float *__r
   // every wave's sums to LDS (acc r of lane (l32, h): row 8 (r / 4) + 4 h +
   // r % 4, column l32); each thread then adds the SW wave sums of its
   // outputs in wave order
+  TT_PROBE(1, 1);
 #pragma unroll
   for (int r = 0; r < 16; r++) red[(w * 16 + r) * 64 + lane] = acc[r];
   __syncthreads();
+  TT_PROBE(1, 2);
   const bool pad = out.d1 || out.d2;
   const int n = n0 + ecol;
 #pragma unroll
@@ -1651,6 +1654,7 @@ __device__ __forceinline__ void small_tile(int M, int N, int K, const float *__r
       if (out.d2) out.d2[o] = out.R ? (rv[j] > 0.0f ? v : 0.0f) : v;
     }
   }
+  TT_PROBE(1, 3);
 }
 
 template <bool A_KC, bool B_NC, bool VA, bool VB>
