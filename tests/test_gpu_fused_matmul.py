@@ -468,7 +468,7 @@ def test_sgd_step_of_a_tensor_a_pending_gradient_reads(tlib, read_first):
     assert np.abs(got[1] - (t - lr * dt)).max() <= bar_t
 
 
-@pytest.mark.parametrize("case", ["default", "seed2", "twice", "frozen_w2"])
+@pytest.mark.parametrize("case", ["default", "seed2", "twice", "frozen_w2", "w2_written"])
 def test_classifier_input_grads_formed_with_the_seed(tlib, case):
     """relu -> padones -> matmul -> softmax_ce (the MLP's last layer): the
     classifier's launch also forms, from each row's seed, the gradients of
@@ -480,7 +480,8 @@ def test_classifier_input_grads_formed_with_the_seed(tlib, case):
     classifier backward kernel): bit for bit, except the classifier weights'
     gradient (MFMA tiles against the backward kernel's serial sums: within
     1e-5 of its scale).  A seed of 2, a second backward (accumulating) and
-    frozen classifier weights leave the backward its own kernel."""
+    frozen classifier weights, or weights written between the passes, leave
+    the backward its own kernel."""
     from tinytorch_amd.torch_py import Node
     r = np.random.default_rng(21)
     x = r.uniform(0, 1, (256, 100)).astype(np.float32)
@@ -488,7 +489,7 @@ def test_classifier_input_grads_formed_with_the_seed(tlib, case):
     w2 = (r.standard_normal((65, 10)) * 0.2).astype(np.float32)
     y = r.integers(0, 10, 256)
 
-    def run(read_logits, seed=None, twice=False, w2_grad=True):
+    def run(read_logits, seed=None, twice=False, w2_grad=True, write_w2=False):
         X, W1, W2 = Node.leaf(x, False), Node.leaf(w1), Node.leaf(w2, w2_grad)
         P1 = X.padones()
         H = P1.matmul(W1)
@@ -498,6 +499,12 @@ def test_classifier_input_grads_formed_with_the_seed(tlib, case):
         if read_logits:
             Z.value()
         L = Z.softmax_ce(y)
+        if write_w2:
+            # the classifier weights changed through their host copy between
+            # the forward and the backward pass
+            t = tlib.ag_value(W2.ptr)
+            hp = tlib.tt_data(t)
+            np.ctypeslib.as_array(hp, shape=(w2.size,))[:] *= np.float32(0.5)
         L.backward(seed)
         if twice:
             L.backward(seed)
@@ -509,7 +516,7 @@ def test_classifier_input_grads_formed_with_the_seed(tlib, case):
 
     print("classifier input grads with the seed:", case, flush=True)
     kw = dict(default={}, seed2=dict(seed=np.array([2.0], np.float32)), twice=dict(twice=True),
-              frozen_w2=dict(w2_grad=False))[case]
+              frozen_w2=dict(w2_grad=False), w2_written=dict(write_w2=True))[case]
     n0 = tlib.tth_ce_spec_count()
     got = run(False, **kw)
     taken = tlib.tth_ce_spec_count() - n0
@@ -521,7 +528,7 @@ def test_classifier_input_grads_formed_with_the_seed(tlib, case):
         assert bits_equal(got[name], ref[name]), name
     if case == "frozen_w2":
         assert got["w2"] is None
-    elif case == "seed2":
+    elif case in ("seed2", "w2_written"):
         # not taken: the same kernel on both sides
         assert bits_equal(got["w2"], ref["w2"])
     else:

@@ -54,8 +54,10 @@ struct AGNode {
         struct { int sh, sw, ph, pw; float *col; int col_ones; } conv;
         /* softmax-CE; sda: the input gradients of its classifier (see
          * ce_spec), computed with the seed and not yet handed over */
-        struct { Tensor *probs, *seed; int32_t *labels; Tensor *sda[3]; } ce;
-        struct { Tensor *sda[3]; } mm;  /* matmul: sda handed over by its softmax-CE */
+        struct { Tensor *probs, *seed; int32_t *labels; Tensor *sda[3]; int *stale; } ce;
+        /* matmul: sda handed over by its softmax-CE; *stale set when the
+         * weights they were formed with are about to change */
+        struct { Tensor *sda[3]; int *stale; } mm;
     } at;
     unsigned long long pass;     /* backward pass that scheduled the node */
     int     walk;                /* depth-first walk: next input to enter */
@@ -95,15 +97,21 @@ static void backward_softmax_ce(AGNode *n);
 
 static void drop_conv(AGNode *n) { ttrt_free(n->at.conv.col); }
 static void drop_pool(AGNode *n) { tt_release(n->at.win.codes); }
+static void spec_drop(Tensor *sda[3], int **stale) {
+    for (int i = 0; i < 3; i++) { tt_release(sda[i]); sda[i] = NULL; }
+    if (*stale) {
+        tt_lazy_guard_drop(*stale);
+        free(*stale);
+        *stale = NULL;
+    }
+}
 static void drop_ce(AGNode *n) {
     tt_release(n->at.ce.probs);
     tt_release(n->at.ce.seed);
     free(n->at.ce.labels);
-    for (int i = 0; i < 3; i++) tt_release(n->at.ce.sda[i]);
+    spec_drop(n->at.ce.sda, &n->at.ce.stale);
 }
-static void drop_mm(AGNode *n) {
-    for (int i = 0; i < 3; i++) tt_release(n->at.mm.sda[i]);
-}
+static void drop_mm(AGNode *n) { spec_drop(n->at.mm.sda, &n->at.mm.stale); }
 
 static const AGOp OP_ADD = {"add", backward_add, NULL};
 static const AGOp OP_MUL = {"mul", backward_mul, NULL};
@@ -582,7 +590,7 @@ AGNode *ag_avgpool2d(AGNode *a, int ph, int pw, int sh, int sw) {
  * they are dropped.  0: launched (logits, probs, seed, row losses and sda
  * written); else nothing launched, sda empty. */
 static int ce_spec(AGNode *logits, const TTPendConv *p, const int32_t *hlab, Tensor *probs,
-                   Tensor *seed, Tensor *rl, Tensor *sda[3]) {
+                   Tensor *seed, Tensor *rl, Tensor *sda[3], int **stale) {
     if (!tt_defer_enabled() || logits->op != &OP_MATMUL) return -1;
     AGNode *a = logits->in[0];
     if (!a || a->op != &OP_PADONES || !needs(a)) return -1;
@@ -606,6 +614,10 @@ static int ce_spec(AGNode *logits, const TTPendConv *p, const int32_t *hlab, Ten
     }
     tt_mark_dev_written(sda[0]);
     tt_mark_dev_written(sda[2]);
+    /* formed with W as it is now: a write to W before the backward makes
+     * them stale (the backward then computes its own) */
+    *stale = (int *)calloc(1, sizeof(int));
+    if (!*stale || tt_lazy_guard(logits->in[1]->val, *stale) != 0) **stale = 1;
     return 0;
 }
 
@@ -674,7 +686,8 @@ AGNode *ag_softmax_ce(AGNode *logits, const int *labels, long rows) {
         const TTPendConv p = tt_pend;
         tt_pend.active = 0;
         Tensor *sda[3] = {NULL, NULL, NULL};
-        int rc = rl ? ce_spec(logits, &p, hlab, probs, seed, rl, sda) : -1;
+        int *stale = NULL;
+        int rc = rl ? ce_spec(logits, &p, hlab, probs, seed, rl, sda, &stale) : -1;
         if (rc != 0)
             rc = rl ? tt_k_gemm_bias_ce(p.geo[0], p.geo[1], p.geo[2], p.x, p.w, p.b, p.out->dev,
                                         hlab, probs->dev, seed->dev, rl->dev, 1.0f / (float)rows)
@@ -685,16 +698,17 @@ AGNode *ag_softmax_ce(AGNode *logits, const int *labels, long rows) {
             AGNode *n = make_node(loss, &OP_SOFTMAX_CE, logits, NULL, NULL);
             if (!n) {
                 tt_release(probs); tt_release(seed); free(hlab);
-                for (int i = 0; i < 3; i++) tt_release(sda[i]);
+                spec_drop(sda, &stale);
                 return NULL;
             }
             n->at.ce.probs = probs;
             n->at.ce.seed = seed;
             n->at.ce.labels = hlab;
             for (int i = 0; i < 3; i++) n->at.ce.sda[i] = sda[i];
+            n->at.ce.stale = stale;
             return n;
         }
-        for (int i = 0; i < 3; i++) tt_release(sda[i]);
+        spec_drop(sda, &stale);
         tt_release(rl);
         if (rc < 0) tt_pend = p;  /* not run: the pending GEMM is launched below */
         /* else the GEMM wrote the logits: the softmax-CE runs below */
@@ -892,8 +906,9 @@ static int backward_matmul_fused(AGNode *n, const float *g, const TTHeadCeArgs *
 
 /* The input gradients its softmax-CE formed with the seed (ce_spec), when
  * they are this pass's: the node's gradient is still exactly that seed (the
- * loss its only consumer) and the padones and relu feed only this node, as
- * backward_matmul_fused requires for the same outputs.  Then only dB is left:
+ * loss its only consumer), the weights have not been written since (no
+ * optimizer step, no host access), and the padones and relu feed only this
+ * node, as backward_matmul_fused requires for the same outputs.  Then only dB is left:
  * a recipe the optimizer's step runs in its own launch.  0 when taken. */
 static long g_spec_taken;  /* backward rules that took them (tth_ce_spec_count) */
 long tth_ce_spec_count(void) { return g_spec_taken; }
@@ -901,10 +916,16 @@ long tth_ce_spec_count(void) { return g_spec_taken; }
 static int backward_matmul_spec(AGNode *n) {
     Tensor *sda[3] = {n->at.mm.sda[0], n->at.mm.sda[1], n->at.mm.sda[2]};
     for (int i = 0; i < 3; i++) n->at.mm.sda[i] = NULL;
+    const int stale = !n->at.mm.stale || *n->at.mm.stale;
+    if (n->at.mm.stale) {
+        tt_lazy_guard_drop(n->at.mm.stale);
+        free(n->at.mm.stale);
+        n->at.mm.stale = NULL;
+    }
     AGNode *a = n->in[0], *b = n->in[1];
     AGNode *x = a->in[0];
     const int M = (int)a->val->shape[0], K = (int)a->val->shape[1], N = (int)b->val->shape[1];
-    const int ok = n->fanin == 1 && a->op == &OP_PADONES && a->fanin == 1 && !a->grad &&
+    const int ok = !stale && n->fanin == 1 && a->op == &OP_PADONES && a->fanin == 1 && !a->grad &&
                    relu_fusable(x) && !x->grad && needs(b) && tt_defer_enabled() &&
                    ttk_gemm_tn_padones_any(M, K - 1, N, NULL, NULL, NULL) == 0;
     Tensor *gb = ok ? tt_empty_like(b->val) : NULL;
@@ -1452,6 +1473,8 @@ static void backward_softmax_ce(AGNode *n) {
                     a->at.mm.sda[i] = n->at.ce.sda[i];
                     n->at.ce.sda[i] = NULL;
                 }
+                a->at.mm.stale = n->at.ce.stale;
+                n->at.ce.stale = NULL;
             }
         } else {
             accum_copy(a, n->at.ce.seed);

@@ -137,7 +137,7 @@ typedef struct TTLazyVal {
                                   two-convolution chain did not store; 6: see
                                   ce (every output is written at once); 7:
                                   src without its last column (padones
-                                  backward, dims M K) */
+                                  backward, dims M K); 8: a guard (flag) */
     TTDwtShared *dwt;
     Tensor *src2;
     int dims[3];
@@ -145,6 +145,8 @@ typedef struct TTLazyVal {
     TTCeJob *ce;               /* kind 6: one output of the softmax-CE job `ce` (src:
                                   the classifier weights the bias belongs to) */
     int q[13];                 /* kind 5: N C H W F HH WW sh sw ph pw Ho Wo */
+    int *flag;                 /* kind 8 (a guard, t NULL): set to 1 when src is about
+                                  to be written */
     struct TTLazyVal *next;
 } TTLazyVal;
 static TTLazyVal *g_lazy_vals;
@@ -159,6 +161,7 @@ static int lazy_add(Tensor *t, Tensor *src, int kind) {
     l->src2 = NULL;
     l->buf = NULL;
     l->ce = NULL;
+    l->flag = NULL;
     l->next = g_lazy_vals;
     g_lazy_vals = l;
     return 0;
@@ -167,6 +170,25 @@ static int lazy_add(Tensor *t, Tensor *src, int kind) {
 int tt_lazy_relu(Tensor *t, Tensor *src) { return lazy_add(t, src, 0); }
 int tt_lazy_padones(Tensor *t, Tensor *src) { return lazy_add(t, src, 1); }
 int tt_lazy_ce_mean(Tensor *t, Tensor *src) { return lazy_add(t, src, 2); }
+int tt_lazy_guard(Tensor *src, int *flag) {
+    if (lazy_add(NULL, src, 8) != 0) return -1;
+    g_lazy_vals->flag = flag;
+    return 0;
+}
+
+void tt_lazy_guard_drop(int *flag) {
+    for (TTLazyVal **pp = &g_lazy_vals; *pp;) {
+        TTLazyVal *l = *pp;
+        if (l->kind == 8 && l->flag == flag) {
+            *pp = l->next;
+            tt_release(l->src);
+            free(l);
+        } else {
+            pp = &l->next;
+        }
+    }
+}
+
 int tt_lazy_padones_bwd(Tensor *t, Tensor *src, long M, long K) {
     if (M > 0x7fffffffL || K > 0x7fffffffL || lazy_add(t, src, 7) != 0) return -1;
     g_lazy_vals->dims[0] = (int)M;
@@ -505,6 +527,13 @@ restart:
         if (l->kind == 6) {
             if (drop && !from) ce_drop_entry(pp);
             else ce_job_run(l->ce);
+            goto restart;
+        }
+        if (l->kind == 8) {  /* a guard: its source is about to change */
+            *pp = l->next;
+            *l->flag = 1;
+            tt_release(l->src);
+            free(l);
             goto restart;
         }
         *pp = l->next;

@@ -103,6 +103,11 @@ int tt_lazy_gemm_tn_padones(Tensor *dw, Tensor *x, Tensor *g, int rows, int Kx, 
 /* t (M x K elements) = src (M x (K + 1)) without its last column -- the
  * padones backward -- written on first use; 0 ok, -1 no memory */
 int tt_lazy_padones_bwd(Tensor *t, Tensor *src, long M, long K);
+/* *flag = 1 when src is about to be written in place or through its host
+ * copy (the accesses that run recipes reading src); tt_lazy_guard_drop
+ * removes the guards of flag.  0 ok, -1 no memory */
+int tt_lazy_guard(Tensor *src, int *flag);
+void tt_lazy_guard_drop(int *flag);
 /* as tt_lazy_dwt_sgd, for one or two pending tt_lazy_gemm_tn_padones
  * gradients: the GEMMs (stepping their weights) and the other tensors' steps
  * in one launch */
