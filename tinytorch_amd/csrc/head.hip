@@ -123,11 +123,12 @@ __device__ __forceinline__ void head_dw_block(const float *__restrict__ A, int M
   float *As = lds, *Gs = lds + M * KW;
   if (use_ce) {
     // the block of A (M <= 32 * NT / KW rows: one batch) in flight while the
-    // seed of every row is formed (workgroup 0 stores the softmax-CE's
+    // seed of every row is formed (its loads issued after the partial sums',
+    // which the softmax-CE waits for; workgroup 0 stores the softmax-CE's
     // outputs), then the block's columns of it
     float va[32];
-    stage_load<KW, 32>(va, A + k0, K, 0, M, min(KW, K - k0));
-    head_ce_seed<NC, 2>(ce, 0, M, M, N, gl, N, blockIdx.x == 0, gl + M * N);
+    head_ce_seed<NC, 2>(ce, 0, M, M, N, gl, N, blockIdx.x == 0, gl + M * N,
+                        [&]() { stage_load<KW, 32>(va, A + k0, K, 0, M, min(KW, K - k0)); });
     stage_store<KW, 32>(va, As, KW, 0, M);
     __syncthreads();
     for (int i = tid; i < M * JW; i += NT) {
@@ -168,9 +169,15 @@ constexpr int DA_M = 32;  // rows m per dA workgroup (8 per lane)
 // of LDS) with the rows' labels; GW lanes a row then form its softmax-CE (one
 // round for the rows of a block: 2 lanes a row for 128 rows, 8 for 32).
 // Every thread calls it (barriers inside).
-template <int NC, int GW>
+struct NoLoads {
+  __device__ void operator()() const {}
+};
+// issue(): called once the first partial sums' loads are issued, before the
+// wait for them -- loads it issues stay in flight through the softmax-CE
+template <int NC, int GW, class Issue = NoLoads>
 __device__ __forceinline__ void head_ce_seed(const TTHeadCe &ce, int r0, int r1, int M, int N,
-                                             float *gl, int gs, bool out, float *pp) {
+                                             float *gl, int gs, bool out, float *pp,
+                                             Issue issue = Issue()) {
   const int n = (r1 - r0) * N;
   const long total = (long)M * N;
   // GW lanes a row (ce_row_group): lane q takes columns [q CPL, q CPL + CPL)
@@ -192,6 +199,7 @@ __device__ __forceinline__ void head_ce_seed(const TTHeadCe &ce, int r0, int r1,
       v0[u] = ce.part[(long)r0 * N + i];
       v1[u] = ce.part[total + (long)r0 * N + i];
     }
+    if (b == 0) issue();
 #pragma unroll
     for (int u = 0; u < 8; u++) {
       const int i = b + (int)threadIdx.x + u * NT;
