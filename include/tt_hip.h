@@ -105,7 +105,9 @@ int tth_gemm_config(int tile, int splits);
 int tth_gemm_direct(int on);
 /* Tuning hook: 0 disables, 1 (default) enables the 64x64 direct-load kernel
  * used for plain GEMMs too small for 128x128 tiles on every CU (and for
- * ragged or unaligned operands); a forced tile (tth_gemm_config) bypasses it. */
+ * ragged or unaligned operands); 2 enables it with the k tiles shared by the
+ * workgroup's waves (a barrier a tile) instead of a load ring per wave (same
+ * results); a forced tile (tth_gemm_config) bypasses it. */
 int tth_gemm_mid(int on);
 /* Tuning hook: 0 disables, 1 (default) enables the 32x32-tile register
  * kernel (K split over the waves of a workgroup, no split-K workspace) used

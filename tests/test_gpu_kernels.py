@@ -565,6 +565,29 @@ def test_gemm_mid_kernel(tlib, M, N, K, ta, tb):
     assert norm2 <= GEMM_TOL, norm2
 
 
+# The 8-wave kernel gives each wave a load ring of its own (its 8-k slice of
+# every tile, no barrier in the K loop); the variant that shares each tile
+# between the waves sums the same products in the same order: same bits,
+# aligned (16-byte loads) and ragged (4-byte loads) operands, split-K too.
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+@pytest.mark.parametrize("M,N,K", [(1024, 1024, 1024), (1000, 1003, 997), (200, 64, 4100),
+                                   (130, 196, 2600), (515, 1025, 1023)])
+def test_gemm_mid_private_ring_bits(tlib, M, N, K, ta, tb):
+    A = u(K, M) if ta else u(M, K)
+    B = u(N, K) if tb else u(K, N)
+    print("gemm mid rings", M, N, K, ta, tb, flush=True)
+    C = run_gemm(tlib, M, N, K, ta, tb, A, B)
+    check(tlib.tth_gemm_mid(2), "mid shared ring")
+    try:
+        C2 = run_gemm(tlib, M, N, K, ta, tb, A, B)
+    finally:
+        check(tlib.tth_gemm_mid(1), "mid on")
+    assert bits_equal(C, C2)
+    ref = (A.T if ta else A).astype(np.float64) @ (B.T if tb else B).astype(np.float64)
+    norm, rel = gemm_err(C, ref, K, 1.0, 1.0)
+    assert norm <= GEMM_TOL and rel <= GEMM_TOL, (norm, rel)
+
+
 # Small GEMMs (2MNK < 2^29, >= 128 tiles of 32x32) run the register kernel
 # that splits K over the waves of one workgroup: edges in M / N, K not a
 # multiple of 8 or below 8, every layout (k-contiguous operands with aligned

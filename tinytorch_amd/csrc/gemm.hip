@@ -985,7 +985,9 @@ struct MidOperand {
   static constexpr int LF = DW ? 64 : 256;         // floats of LDS per load
   static constexpr int NL = T * BK / (LF * NW);    // loads per wave per tile
   static_assert(NL >= 1 && NL * LF * NW == T * BK, "tile too small for the waves");
-  __device__ __forceinline__ static int swz(int R) { return BK == 32 ? (R >> 1) & 7 : R & 15; }
+  __device__ __forceinline__ static int swz(int R) {
+    return BK == 8 ? 0 : BK == 32 ? (R >> 1) & 7 : R & 15;
+  }
   unsigned voff[NL];
   const float *p;
   long ld, r0;
@@ -1084,9 +1086,13 @@ struct MidOperand {
 
 // ROWS: rows of A per tile (64, or 256 for tall operands with few columns:
 // four 64-row blocks share each tile of B); NWK: waves per K tile.  Wave w
-// owns row block w / NWK and k slice w % NWK.
+// owns row block w / NWK and k slice w % NWK.  PRIV (one row block, BK = 8 NW):
+// each wave loads only its own 8-k slice of every tile into a ring of its own,
+// so no wave reads what another loaded and the K loop has no barrier (each
+// wave waits only for its own loads); the same products summed in the same
+// order as the shared ring.
 template <bool A_KC, bool B_NC, int BK, int S, int NW, int ROWS = M_T, int NWK = NW,
-          bool DW = false>
+          bool DW = false, bool PRIV = false>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4, 2)))
 gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
                 const float *__restrict__ B, long ldb, float *__restrict__ C, long ldc,
@@ -1095,14 +1101,17 @@ gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
   static_assert(S >= 3, "the pipeline needs three stages");
   constexpr int NTH = 64 * NW;
   static_assert(ROWS % M_T == 0 && NW == (ROWS / M_T) * NWK, "waves = row blocks x k slices");
-  constexpr int OPA = ROWS * BK, OPB = M_T * BK;  // floats per operand per stage
+  static_assert(!PRIV || (ROWS == M_T && NWK == NW && BK == 8 * NW), "private slices: 8 k a wave");
+  // private ring: one wave's operands of BK = 8, LW = 1, KSL = 1
+  constexpr int OBK = PRIV ? 8 : BK, OW = PRIV ? 1 : NW, OKS = PRIV ? 1 : NWK;
+  constexpr int OPA = ROWS * OBK, OPB = M_T * OBK;  // floats per operand per stage
   constexpr int STAGE = OPA + OPB;
-  constexpr int PIPE = S * STAGE, RED = NW * M_T * M_RLD;
-  constexpr int KSUB = BK / (8 * NWK);  // 8-k sub-slices per wave per tile
+  constexpr int PIPE = S * STAGE * (PRIV ? NW : 1), RED = NW * M_T * M_RLD;
+  constexpr int KSUB = OBK / (8 * OKS);  // 8-k sub-slices per wave per tile
   static_assert(KSUB >= 1, "tile too shallow for the waves");
   __shared__ __attribute__((aligned(16))) float smem[PIPE > RED ? PIPE : RED];
-  using OA = MidOperand<A_KC, BK, NW, ROWS, NWK, DW>;
-  using OB = MidOperand<!B_NC, BK, NW, M_T, NWK, DW>;
+  using OA = MidOperand<A_KC, OBK, OW, ROWS, OKS, DW>;
+  using OB = MidOperand<!B_NC, OBK, OW, M_T, OKS, DW>;
   constexpr int NL = OA::NL + OB::NL;  // loads per wave per tile
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1132,9 +1141,16 @@ gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
   // A k-contiguous: rows m of A (M x K); else rows k of A (K x M), columns m.
   // B m/n-contiguous: rows k of B (K x N); else rows n of B (N x K).
   // (alim / blim: the rows of a KC operand, the readable columns of an NC one)
-  opa.init(A, lda, m0, alim, wave, lane);
-  opb.init(B, ldb, n0, blim, wave, lane);
+  opa.init(A, lda, m0, alim, PRIV ? 0 : wave, lane);
+  opb.init(B, ldb, n0, blim, PRIV ? 0 : wave, lane);
+  // the wave's ring and the k of its slice in a tile (private ring)
+  float *const ring = PRIV ? smem + wave * (S * STAGE) : smem;
+  const int kw = PRIV ? 8 * wave : 0;
+  const int fks = PRIV ? 0 : ks;
 
+#ifdef TT_PHASE_PROBE
+  long long waited = 0;
+#endif
   f32x16 acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; i++)
@@ -1145,10 +1161,10 @@ gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
 
   // loads J0 .. J0+NJ-1 of the NL of tile kt (A's first, then B's)
   auto issue_part = [&](int kt, int j0, int nj) {
-    float *st = smem + (kt % S) * STAGE;
-    const int k0 = kbeg + kt * BK;
+    float *st = ring + (kt % S) * STAGE;
+    const int k0 = kbeg + kt * BK + kw;
     const float *oa = opa.origin(k0), *ob = opb.origin(k0);
-    if (k0 + BK <= kend) {
+    if (k0 + OBK <= kend) {
 #pragma unroll
       for (int j = 0; j < NL; j++) {
         if (j < j0 || j >= j0 + nj) continue;
@@ -1165,11 +1181,11 @@ gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
     }
   };
   auto frags = [&](int kt, float (*a)[2][4], float (*b)[2][4]) {
-    const float *st = smem + (kt % S) * STAGE;
+    const float *st = ring + (kt % S) * STAGE;
 #pragma unroll
     for (int h = 0; h < KSUB; h++) {
-      OA::frag(st, ks, rb * M_T, h, l32, g, a[h]);
-      OB::frag(st + OPA, ks, 0, h, l32, g, b[h]);
+      OA::frag(st, fks, rb * M_T, h, l32, g, a[h]);
+      OB::frag(st + OPA, fks, 0, h, l32, g, b[h]);
     }
   };
   auto mfma4 = [&](float (*ca)[2][4], float (*cb)[2][4], int h, int s) {
@@ -1190,9 +1206,16 @@ gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
   // wait for the new reads instead of only for the previous tile's.
   auto step = [&](int kt, float (*ca)[2][4], float (*cb)[2][4], float (*na)[2][4],
                   float (*nb)[2][4]) {
+#ifdef TT_PHASE_PROBE
+    const long long tw0 = __builtin_amdgcn_s_memtime();
+#endif
     if (kt + S - 2 < nk) wait_vm<NL *(S - 3)>();
     else wait_vm<0>();
-    __syncthreads();
+#ifdef TT_PHASE_PROBE
+    asm volatile("s_nop 0" ::: "memory");
+    waited += __builtin_amdgcn_s_memtime() - tw0;
+#endif
+    if constexpr (!PRIV) __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
     frags(kt + 1, na, nb);
     __builtin_amdgcn_sched_barrier(0);
@@ -1212,20 +1235,31 @@ gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
     for (int t = 0; t < S - 1 && t < nk; t++) issue_part(t, 0, NL);
     if (nk >= S - 1) wait_vm<NL *(S - 2)>();
     else wait_vm<0>();
-    __syncthreads();
+    if constexpr (!PRIV) __syncthreads();
     TT_PROBE(0, 1);
     float a0[KSUB][2][4], b0[KSUB][2][4], a1[KSUB][2][4], b1[KSUB][2][4];
     frags(0, a0, b0);
+#ifdef TT_PHASE_PROBE
+    const long long tl0 = __builtin_amdgcn_s_memtime();
+#endif
     for (int kt = 0; kt < nk; kt += 2) {
       step(kt, a0, b0, a1, b1);
       if (kt + 1 < nk) step(kt + 1, a1, b1, a0, b0);
     }
+#ifdef TT_PHASE_PROBE
+    if ((tid & 63) == 0 && blockIdx.x < 1024 && wave < 8) {
+      // kernel slots 2 and 3: each wave's cycles waiting for its loads, and in its K loop
+      tt_probe_ts[(2 * 1024 + blockIdx.x) * 16 + wave] = waited;
+      tt_probe_ts[(3 * 1024 + blockIdx.x) * 16 + wave] = __builtin_amdgcn_s_memtime() - tl0;
+    }
+#endif
   }
 
   // wave sums -> LDS (acc r of block (x, y): row 8*(r/4) + 4g + r%4 of the
   // block), then each thread adds the NWK k-slice sums of its outputs in
   // order
   TT_PROBE(0, 2);
+  if (wave < 8) TT_PROBE_WAVE(0, 6 + wave);
   __syncthreads();
   TT_PROBE(0, 3);
   float *red = smem + wave * (M_T * M_RLD);
@@ -1313,7 +1347,7 @@ constexpr int TILE_BK[NTILE] = {32, 32, 32, 32, 32, 32, 32, 32, 32, 64, 64};
 // tuning override (tth_gemm_config): -1 = automatic
 int g_force_tile = -1, g_force_splits = -1;
 int g_direct = 1;  // direct-to-LDS 256x256 kernel enabled (tth_gemm_direct)
-int g_mid = 1;     // 64x64 direct-load kernel for plain GEMMs (tth_gemm_mid)
+int g_mid = 1;     // 64x64 direct-load kernel for plain GEMMs (tth_gemm_mid; 2: shared k tiles)
 int g_small = 1;   // 32x32 register kernel for small plain GEMMs (tth_gemm_small)
 int g_t16 = 1;     // 16x16 forward kernel for GEMMs below a full 32x32 grid (tth_gemm_t16)
 
@@ -2026,6 +2060,10 @@ int run_mid(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ld
     hipLaunchKernelGGL((gemm_mid_kernel<A_KC, B_NC, 32, 4, 8, 256, 2, DW>),
                        dim3((unsigned)tiles256), dim3(512), 0, stream(), M, N, K, A.p, A.ld, B.p,
                        B.ld, target, tld, sstride, kc, cvec, alim, blim);
+  else if (tiles * splits <= CUS && g_mid == 1)
+    hipLaunchKernelGGL((gemm_mid_kernel<A_KC, B_NC, 64, 4, 8, M_T, 8, DW, true>), grid, dim3(512),
+                       0, stream(), M, N, K, A.p, A.ld, B.p, B.ld, target, tld, sstride, kc, cvec,
+                       alim, blim);
   else if (tiles * splits <= CUS)
     hipLaunchKernelGGL((gemm_mid_kernel<A_KC, B_NC, 64, 4, 8, M_T, 8, DW>), grid, dim3(512), 0,
                        stream(), M, N, K, A.p, A.ld, B.p, B.ld, target, tld, sstride, kc, cvec,
@@ -2172,7 +2210,7 @@ extern "C" int tth_gemm_direct(int on) {
 }
 
 extern "C" int tth_gemm_mid(int on) {
-  g_mid = on ? 1 : 0;
+  g_mid = on == 2 ? 2 : on ? 1 : 0;
   return 0;
 }
 

@@ -2,7 +2,8 @@
 // says TT_PROBE_DEFINE(name) gets its own device array and an exported
 // tt_probe_read_<name>(host, n) that copies it back, and TT_PROBE(kid, i)
 // records thread 0's s_memrealtime (100 MHz) at point i (< 16) of workgroup
-// blockIdx.x (< 1024) of kernel kid (< 4) of that file.  Without the define
+// blockIdx.x (< 1024) of kernel kid (< 4) of that file (TT_PROBE_WAVE: lane
+// 0 of each wave).  Without the define
 // both expand to nothing.
 #pragma once
 #include <hip/hip_runtime.h>
@@ -23,9 +24,18 @@
     if (threadIdx.x == 0 && blockIdx.x < 1024)                                          \
       tt_probe_ts[((kid) * 1024 + blockIdx.x) * 16 + (i)] = __builtin_amdgcn_s_memrealtime(); \
   } while (0)
+// the same from lane 0 of every wave (point i chosen per wave by the caller)
+#define TT_PROBE_WAVE(kid, i)                                                           \
+  do {                                                                                  \
+    if ((threadIdx.x & 63) == 0 && blockIdx.x < 1024)                                   \
+      tt_probe_ts[((kid) * 1024 + blockIdx.x) * 16 + (i)] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
 #else
 #define TT_PROBE_DEFINE(name)
 #define TT_PROBE(kid, i) \
   do {                   \
+  } while (0)
+#define TT_PROBE_WAVE(kid, i) \
+  do {                        \
   } while (0)
 #endif
