@@ -632,7 +632,7 @@ def phases(L):
         gm = read("gemm")
         out[f"gemm_mid_kernel/{M}x{N}x{K}"] = phase_split(
             gm, 0, slice(0, 256), [0, 1, 2, 3, 4, 5],
-            ["first_tiles", "k_loop", "barrier", "wave_sums_to_lds", "sum_and_store"])
+            ["first_tiles", "k_loop_wave0", "wave0_sums_to_lds", "other_waves", "sum_and_store"])
         g.free()
     return out
 

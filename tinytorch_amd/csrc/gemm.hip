@@ -924,7 +924,6 @@ gemm_direct_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
 //   m/n-contiguous operand: BK rows k of 64 floats; fragments are read as
 //     float2, so block x of a wave holds m/n = 2*l32 + x (interleaved).
 constexpr int M_T = 64;
-constexpr int M_RLD = M_T + 4;  // row stride of the wave-sum area
 
 __device__ __attribute__((aligned(16))) float g_gemm_zero[4];
 
@@ -1106,7 +1105,8 @@ gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
   constexpr int OBK = PRIV ? 8 : BK, OW = PRIV ? 1 : NW, OKS = PRIV ? 1 : NWK;
   constexpr int OPA = ROWS * OBK, OPB = M_T * OBK;  // floats per operand per stage
   constexpr int STAGE = OPA + OPB;
-  constexpr int PIPE = S * STAGE * (PRIV ? NW : 1), RED = NW * M_T * M_RLD;
+  constexpr int PIPE = S * STAGE * (PRIV ? NW : 1), RED = NW * M_T * M_T;
+  static_assert(!PRIV || S * STAGE == M_T * M_T, "a wave's sums fill its own ring");
   constexpr int KSUB = OBK / (8 * OKS);  // 8-k sub-slices per wave per tile
   static_assert(KSUB >= 1, "tile too shallow for the waves");
   __shared__ __attribute__((aligned(16))) float smem[PIPE > RED ? PIPE : RED];
@@ -1255,14 +1255,20 @@ gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
 #endif
   }
 
-  // wave sums -> LDS (acc r of block (x, y): row 8*(r/4) + 4g + r%4 of the
-  // block), then each thread adds the NWK k-slice sums of its outputs in
-  // order
+  // wave sums -> LDS, 64x64 floats a wave (acc r of block (x, y): row
+  // 8*(r/4) + 4g + r%4 of the block), then each thread adds the NWK k-slice
+  // sums of its outputs in order.  A private ring takes its own wave's sums
+  // as soon as that wave's K loop ends (its loads have all landed), so the
+  // waves that finish first write theirs while the others still compute;
+  // the shared ring is free once every wave is past its K loop.  With B
+  // k-contiguous a lane's two stores are 32 columns apart and the two
+  // half-waves write rows 4 (8) apart: the row's 32-column halves swap on
+  // those rows so the 64 lanes hit 64 banks.
   TT_PROBE(0, 2);
   if (wave < 8) TT_PROBE_WAVE(0, 6 + wave);
-  __syncthreads();
-  TT_PROBE(0, 3);
-  float *red = smem + wave * (M_T * M_RLD);
+  if constexpr (!PRIV) __syncthreads();
+  auto swz = [](int m) { return B_NC ? 0 : 32 * ((A_KC ? m >> 2 : m >> 3) & 1); };
+  float *red = smem + wave * (M_T * M_T);
 #pragma unroll
   for (int x = 0; x < 2; x++)
 #pragma unroll
@@ -1270,12 +1276,13 @@ gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
       const int i = 8 * (r >> 2) + 4 * g + (r & 3);
       const int m = A_KC ? 32 * x + i : 2 * i + x;
       if constexpr (B_NC) {
-        *reinterpret_cast<float2 *>(red + m * M_RLD + 2 * l32) = make_float2(acc[x][0][r], acc[x][1][r]);
+        *reinterpret_cast<float2 *>(red + m * M_T + 2 * l32) = make_float2(acc[x][0][r], acc[x][1][r]);
       } else {
-        red[m * M_RLD + l32] = acc[x][0][r];
-        red[m * M_RLD + 32 + l32] = acc[x][1][r];
+        red[m * M_T + (l32 ^ swz(m))] = acc[x][0][r];
+        red[m * M_T + ((32 + l32) ^ swz(m))] = acc[x][1][r];
       }
     }
+  TT_PROBE(0, 3);
   __syncthreads();
   TT_PROBE(0, 4);
 #pragma unroll
@@ -1285,11 +1292,11 @@ gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
     const int fb = mr / M_T, m = mr - fb * M_T;  // row block, row in it
     const long row = m0 + mr;
     if (row >= M) continue;
-    const float *rb0 = smem + (fb * NWK) * (M_T * M_RLD) + m * M_RLD + n;
+    const float *rb0 = smem + (fb * NWK) * (M_T * M_T) + m * M_T + (n ^ swz(m));
     float4 v = *reinterpret_cast<const float4 *>(rb0);
 #pragma unroll
     for (int w = 1; w < NWK; w++) {
-      const float4 t = *reinterpret_cast<const float4 *>(rb0 + w * (M_T * M_RLD));
+      const float4 t = *reinterpret_cast<const float4 *>(rb0 + w * (M_T * M_T));
       v.x += t.x; v.y += t.y; v.z += t.z; v.w += t.w;
     }
     float *crow = C + row * ldc;
