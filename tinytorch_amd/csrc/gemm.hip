@@ -984,8 +984,11 @@ struct MidOperand {
   static constexpr int LF = DW ? 64 : 256;         // floats of LDS per load
   static constexpr int NL = T * BK / (LF * NW);    // loads per wave per tile
   static_assert(NL >= 1 && NL * LF * NW == T * BK, "tile too small for the waves");
+  // 16-byte chunk swizzle of KC rows: a fragment read of 16 lanes (rows R..
+  // R+15 of one chunk) touches every bank once (8-k rows: rows 8 apart would
+  // share banks, so their two chunks swap)
   __device__ __forceinline__ static int swz(int R) {
-    return BK == 8 ? 0 : BK == 32 ? (R >> 1) & 7 : R & 15;
+    return BK == 8 ? (R >> 3) & 1 : BK == 32 ? (R >> 1) & 7 : R & 15;
   }
   unsigned voff[NL];
   const float *p;
