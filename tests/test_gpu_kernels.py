@@ -565,13 +565,15 @@ def test_gemm_mid_kernel(tlib, M, N, K, ta, tb):
     assert norm2 <= GEMM_TOL, norm2
 
 
-# The 8-wave kernel gives each wave a load ring of its own (its 8-k slice of
-# every tile, no barrier in the K loop); the variant that shares each tile
-# between the waves sums the same products in the same order: same bits,
-# aligned (16-byte loads) and ragged (4-byte loads) operands, split-K too.
+# The 8- and 4-wave kernels give each wave a load ring of its own (its 8-k
+# slice of every tile, no barrier in the K loop); the variants that share
+# each tile between the waves sum the same products in the same order: same
+# bits, aligned (16-byte loads) and ragged (4-byte loads) operands, split-K
+# and grids of more tiles than CUs (the 4-wave kernel) too.
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
 @pytest.mark.parametrize("M,N,K", [(1024, 1024, 1024), (1000, 1003, 997), (200, 64, 4100),
-                                   (130, 196, 2600), (515, 1025, 1023)])
+                                   (130, 196, 2600), (515, 1025, 1023), (2052, 1024, 132),
+                                   (1100, 2000, 262)])
 def test_gemm_mid_private_ring_bits(tlib, M, N, K, ta, tb):
     A = u(K, M) if ta else u(M, K)
     B = u(N, K) if tb else u(K, N)

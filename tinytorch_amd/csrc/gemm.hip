@@ -2060,9 +2060,10 @@ int run_mid(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ld
   const bool cvec = aligned16(target) && tld % 4 == 0;
   const dim3 grid((unsigned)tiles, 1, splits);
   const long sstride = (long)M * N;
-  // at most one workgroup per CU: 8 waves (two per SIMD) over 4 stages of
-  // 64 k (139 KB of LDS); more: 4 waves over 5 stages of 32 k (80 KB), two
-  // workgroups per CU
+  // at most one workgroup per CU: 8 waves (two per SIMD), a ring of 4
+  // stages of 8 k per wave (128 KB of LDS); more: 4 waves, 4 stages of 8 k
+  // per wave (64 KB), two workgroups per CU.  g_mid 2: the rings shared by
+  // the waves (64-k stages, 4 of them, and 32-k stages, 5 of them)
   const int alim = M, blim = N;
   const long tiles256 = (long)((M + 255) / 256) * ((N + M_T - 1) / M_T);
   if (N <= M_T && splits == 1 && tiles256 >= CUS)
@@ -2077,6 +2078,10 @@ int run_mid(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ld
   else if (tiles * splits <= CUS)
     hipLaunchKernelGGL((gemm_mid_kernel<A_KC, B_NC, 64, 4, 8, M_T, 8, DW>), grid, dim3(512), 0,
                        stream(), M, N, K, A.p, A.ld, B.p, B.ld, target, tld, sstride, kc, cvec,
+                       alim, blim);
+  else if (g_mid == 1)
+    hipLaunchKernelGGL((gemm_mid_kernel<A_KC, B_NC, 32, 4, 4, M_T, 4, DW, true>), grid, dim3(256),
+                       0, stream(), M, N, K, A.p, A.ld, B.p, B.ld, target, tld, sstride, kc, cvec,
                        alim, blim);
   else
     hipLaunchKernelGGL((gemm_mid_kernel<A_KC, B_NC, 32, 5, 4, M_T, 4, DW>), grid, dim3(256), 0,
