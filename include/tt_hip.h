@@ -109,6 +109,10 @@ int tth_gemm_direct(int on);
  * workgroup's waves (a barrier a tile) instead of a load ring per wave (same
  * results); a forced tile (tth_gemm_config) bypasses it. */
 int tth_gemm_mid(int on);
+/* Tuning hook for tests: 1 sends every plain GEMM that the 64x64
+ * direct-load kernel covers to it whatever its size (below the sizes where
+ * it pays off, and ahead of the 32x32 register kernel); 0 (default) off. */
+int tth_gemm_mid_force(int on);
 /* Tuning hook: 0 disables, 1 (default) enables the 32x32-tile register
  * kernel (K split over the waves of a workgroup, no split-K workspace) used
  * for plain GEMMs below 2^29 flops with at least 128 output tiles whose

@@ -590,6 +590,35 @@ def test_gemm_mid_private_ring_bits(tlib, M, N, K, ta, tb):
     assert norm <= GEMM_TOL and rel <= GEMM_TOL, (norm, rel)
 
 
+# Edges of the 64x64 kernel's rings at sizes where it does not run by itself
+# (tth_gemm_mid_force): K tails where most waves' 8-k slices lie past K (K =
+# 4, 12, 36), partial edge tiles in M and N, split-K over short K chunks,
+# 16-byte loads (aligned) and 4-byte loads (K, M or N ragged), both rings
+# against each other (same bits) and against float64.
+MID_EDGE_SHAPES = [(4, 4, 4), (64, 64, 64), (100, 68, 36), (60, 4, 1028), (130, 196, 260),
+                   (68, 132, 12), (17, 13, 5), (33, 70, 99), (5, 300, 3), (300, 260, 1001)]
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", MID_EDGE_SHAPES)
+def test_gemm_mid_forced_edges(tlib, M, N, K, ta, tb):
+    A = u(K, M) if ta else u(M, K)
+    B = u(N, K) if tb else u(K, N)
+    print("gemm mid forced", M, N, K, ta, tb, flush=True)
+    check(tlib.tth_gemm_mid_force(1), "mid force")
+    try:
+        C = run_gemm(tlib, M, N, K, ta, tb, A, B)
+        check(tlib.tth_gemm_mid(2), "mid shared ring")
+        C2 = run_gemm(tlib, M, N, K, ta, tb, A, B)
+    finally:
+        check(tlib.tth_gemm_mid(1), "mid on")
+        check(tlib.tth_gemm_mid_force(0), "mid force off")
+    assert bits_equal(C, C2)
+    ref = (A.T if ta else A).astype(np.float64) @ (B.T if tb else B).astype(np.float64)
+    norm, rel = gemm_err(C, ref, K, 1.0, 1.0)
+    assert norm <= GEMM_TOL and rel <= GEMM_TOL, (norm, rel)
+
+
 # Small GEMMs (2MNK < 2^29, >= 128 tiles of 32x32) run the register kernel
 # that splits K over the waves of one workgroup: edges in M / N, K not a
 # multiple of 8 or below 8, every layout (k-contiguous operands with aligned

@@ -162,6 +162,7 @@ SIGNATURES = [
     ("tth_conv_config", _I, [_L]),
     ("tth_gemm_direct", _I, [_I]),
     ("tth_gemm_mid", _I, [_I]),
+    ("tth_gemm_mid_force", _I, [_I]),
     ("tth_gemm_small", _I, [_I]),
     ("tth_gemm_t16", _I, [_I]),
     ("tth_ce_spec_count", _L, []),

@@ -1358,6 +1358,7 @@ constexpr int TILE_BK[NTILE] = {32, 32, 32, 32, 32, 32, 32, 32, 32, 64, 64};
 int g_force_tile = -1, g_force_splits = -1;
 int g_direct = 1;  // direct-to-LDS 256x256 kernel enabled (tth_gemm_direct)
 int g_mid = 1;     // 64x64 direct-load kernel for plain GEMMs (tth_gemm_mid; 2: shared k tiles)
+int g_mid_force = 0;  // every plain GEMM of small size takes it too (tth_gemm_mid_force)
 int g_small = 1;   // 32x32 register kernel for small plain GEMMs (tth_gemm_small)
 int g_t16 = 1;     // 16x16 forward kernel for GEMMs below a full 32x32 grid (tth_gemm_t16)
 
@@ -1575,12 +1576,13 @@ struct SmallOut {
   float lr = 0.0f;
 };
 
-template <bool A_KC, bool B_NC, bool VA, bool VB>
+// PK: the probe slot set of the calling kernel (phase-probe builds only)
+template <bool A_KC, bool B_NC, bool VA, bool VB, int PK = 1>
 __device__ __forceinline__ void small_tile(int M, int N, int K, const float *__restrict__ A,
                                            long lda, const float *__restrict__ B, long ldb,
                                            const SmallOut &out, int kc, int bx, int by,
                                            float *red) {
-  TT_PROBE(1, 0);
+  TT_PROBE(PK, 0);
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l32 = lane & 31, h = lane >> 5;
@@ -1662,11 +1664,11 @@ __device__ __forceinline__ void small_tile(int M, int N, int K, const float *__r
   // every wave's sums to LDS (acc r of lane (l32, h): row 8 (r / 4) + 4 h +
   // r % 4, column l32); each thread then adds the SW wave sums of its
   // outputs in wave order
-  TT_PROBE(1, 1);
+  TT_PROBE(PK, 1);
 #pragma unroll
   for (int r = 0; r < 16; r++) red[(w * 16 + r) * 64 + lane] = acc[r];
   __syncthreads();
-  TT_PROBE(1, 2);
+  TT_PROBE(PK, 2);
   const bool pad = out.d1 || out.d2;
   const int n = n0 + ecol;
 #pragma unroll
@@ -1698,7 +1700,7 @@ __device__ __forceinline__ void small_tile(int M, int N, int K, const float *__r
       if (out.d2) out.d2[o] = out.R ? (rv[j] > 0.0f ? v : 0.0f) : v;
     }
   }
-  TT_PROBE(1, 3);
+  TT_PROBE(PK, 3);
 }
 
 template <bool A_KC, bool B_NC, bool VA, bool VB>
@@ -1972,11 +1974,11 @@ gemm_small_pair_kernel(SmallJob da, SmallJob db, int nba) {
   __shared__ float red[SW * 16 * 64];
   const int i = blockIdx.x;
   if (i < nba)
-    small_tile<true, false, VDA, VDA>(da.M, da.N, da.K, da.A, da.lda, da.B, da.ldb, da.out, da.kc,
-                                      i % da.nbx, i / da.nbx, red);
+    small_tile<true, false, VDA, VDA, 2>(da.M, da.N, da.K, da.A, da.lda, da.B, da.ldb, da.out,
+                                         da.kc, i % da.nbx, i / da.nbx, red);
   else
-    small_tile<false, true, false, false>(db.M, db.N, db.K, db.A, db.lda, db.B, db.ldb, db.out,
-                                          db.kc, (i - nba) % db.nbx, (i - nba) / db.nbx, red);
+    small_tile<false, true, false, false, 2>(db.M, db.N, db.K, db.A, db.lda, db.B, db.ldb, db.out,
+                                             db.kc, (i - nba) % db.nbx, (i - nba) / db.nbx, red);
 }
 
 // small_ok: below the 64x64 kernel's range (2MNK < 2^29) with at least 128
@@ -2022,7 +2024,8 @@ bool mid_ok(int M, int N, int K, const Opnd &A, const Opnd &B, bool vec) {
   // below ~0.5 GFLOP the per-launch cost of the deep pipeline and the wave
   // sums outweighs its faster K loop (measured: 512^3 and the MLP GEMMs are
   // faster on the register-staged 64x64 kernel)
-  return g_mid && vec && 2.0 * M * N * K >= (double)(1L << 29) && A.ld <= (1L << 22) && B.ld <= (1L << 22) && (!kc_ops || K % 4 == 0) &&
+  return g_mid && vec && (g_mid_force || 2.0 * M * N * K >= (double)(1L << 29)) &&
+         A.ld <= (1L << 22) && B.ld <= (1L << 22) && (!kc_ops || K % 4 == 0) &&
          (A_KC || M % 4 == 0) && (!B_NC || N % 4 == 0);
 }
 
@@ -2071,7 +2074,7 @@ int run_mid(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ld
     hipLaunchKernelGGL((gemm_mid_kernel<A_KC, B_NC, 32, 4, 8, 256, 2, DW>),
                        dim3((unsigned)tiles256), dim3(512), 0, stream(), M, N, K, A.p, A.ld, B.p,
                        B.ld, target, tld, sstride, kc, cvec, alim, blim);
-  else if (tiles * splits <= CUS && g_mid == 1)
+  else if (tiles * splits <= CUS && g_mid != 2)
     hipLaunchKernelGGL((gemm_mid_kernel<A_KC, B_NC, 64, 4, 8, M_T, 8, DW, true>), grid, dim3(512),
                        0, stream(), M, N, K, A.p, A.ld, B.p, B.ld, target, tld, sstride, kc, cvec,
                        alim, blim);
@@ -2079,7 +2082,7 @@ int run_mid(int M, int N, int K, const Opnd &A, const Opnd &B, float *C, long ld
     hipLaunchKernelGGL((gemm_mid_kernel<A_KC, B_NC, 64, 4, 8, M_T, 8, DW>), grid, dim3(512), 0,
                        stream(), M, N, K, A.p, A.ld, B.p, B.ld, target, tld, sstride, kc, cvec,
                        alim, blim);
-  else if (g_mid == 1)
+  else if (g_mid != 2)
     hipLaunchKernelGGL((gemm_mid_kernel<A_KC, B_NC, 32, 4, 4, M_T, 4, DW, true>), grid, dim3(256),
                        0, stream(), M, N, K, A.p, A.ld, B.p, B.ld, target, tld, sstride, kc, cvec,
                        alim, blim);
@@ -2105,11 +2108,13 @@ int run(int M, int N, int K, Opnd A, Opnd B, float *C, long ldc, const float *bi
   Plan p = plan(M, N, K > 0 ? K : 1);
   if constexpr (!A_PERM && !B_PERM && !B_I2C && EPI == EPI_STORE) {
     if (p.tile != T256x256 && p.tile != T256x128 && p.tile != T128x128 && g_force_tile < 0) {
-      if (small_ok<A_KC, B_NC>(M, N, K, A, B)) return run_small<A_KC, B_NC>(M, N, K, A, B, C, ldc);
+      if (!g_mid_force && small_ok<A_KC, B_NC>(M, N, K, A, B))
+        return run_small<A_KC, B_NC>(M, N, K, A, B, C, ldc);
       if (mid_ok<A_KC, B_NC>(M, N, K, A, B, vec)) return run_mid<A_KC, B_NC>(M, N, K, A, B, C, ldc);
       // operands that are not 16-byte aligned (ragged leading dimensions,
       // K % 4 != 0 with k-contiguous rows): the same kernel with 4-byte loads
-      if (g_mid && 2.0 * M * N * K >= 1e9 && A.ld <= (1L << 22) && B.ld <= (1L << 22))
+      if (g_mid && (g_mid_force || 2.0 * M * N * K >= 1e9) && A.ld <= (1L << 22) &&
+          B.ld <= (1L << 22))
         return run_mid<A_KC, B_NC, true>(M, N, K, A, B, C, ldc);
     }
   }
@@ -2226,6 +2231,11 @@ extern "C" int tth_gemm_direct(int on) {
 
 extern "C" int tth_gemm_mid(int on) {
   g_mid = on == 2 ? 2 : on ? 1 : 0;
+  return 0;
+}
+
+extern "C" int tth_gemm_mid_force(int on) {
+  g_mid_force = on ? 1 : 0;
   return 0;
 }
 
