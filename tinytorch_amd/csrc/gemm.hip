@@ -1104,7 +1104,7 @@ gemm_mid_kernel(int M, int N, int K, const float *__restrict__ A, long lda,
   constexpr int NTH = 64 * NW;
   static_assert(ROWS % M_T == 0 && NW == (ROWS / M_T) * NWK, "waves = row blocks x k slices");
   static_assert(!PRIV || (ROWS == M_T && NWK == NW && BK == 8 * NW), "private slices: 8 k a wave");
-  // private ring: one wave's operands of BK = 8, LW = 1, KSL = 1
+  // a private ring holds one wave's operands: tiles of 8 k, loaded by that wave alone
   constexpr int OBK = PRIV ? 8 : BK, OW = PRIV ? 1 : NW, OKS = PRIV ? 1 : NWK;
   constexpr int OPA = ROWS * OBK, OPB = M_T * OBK;  // floats per operand per stage
   constexpr int STAGE = OPA + OPB;
