@@ -186,9 +186,13 @@ __device__ __forceinline__ void head_ce_seed(const TTHeadCe &ce, int r0, int r1,
   float bq[CPL];  // this lane's bias values, loaded with the partial sums
 #pragma unroll
   for (int u = 0; u < CPL; u++) bq[u] = ce.bias[min(q * CPL + u, N - 1)];
-  // the rows' labels too (read in the loop below, each was a round trip)
+  // the rows' labels too (read in the loop below, each was a round trip):
+  // the first NT loaded into a register here and stored to LDS after the
+  // partial sums' loads are issued (stored at once, their round trip would
+  // come before those loads)
   int *yl = reinterpret_cast<int *>(pp + 2 * n);
-  for (int i = threadIdx.x; i < r1 - r0; i += NT) yl[i] = ce.lab[r0 + i];
+  const int nr = r1 - r0;
+  const int y0 = (int)threadIdx.x < nr ? ce.lab[r0 + threadIdx.x] : 0;
   // eight elements a thread in flight before their LDS stores (a loop that
   // stores each load waits a memory round trip per element)
   for (int b = 0; b < n; b += 8 * NT) {
@@ -209,6 +213,8 @@ __device__ __forceinline__ void head_ce_seed(const TTHeadCe &ce, int r0, int r1,
       }
     }
   }
+  if ((int)threadIdx.x < nr) yl[threadIdx.x] = y0;
+  for (int i = threadIdx.x + NT; i < nr; i += NT) yl[i] = ce.lab[r0 + i];
   __syncthreads();
   TT_PROBE(0, 6);
   for (int r = r0 + (int)(threadIdx.x / GW); r < r1; r += NT / GW) {
